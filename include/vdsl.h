@@ -1,0 +1,329 @@
+/*
+ * vdsl.h - C ABI of the MI355X (gfx950) HIP device for VernonDSL's tensor-op hot path.
+ *
+ * The reference (morphling666/VernonDSL) has no C ABI, FFI or runtime: its only backend
+ * seam is the MLIR pass plugin
+ *     std::unique_ptr<mlir::Pass> mlir::vernon::createVernonToSPIRVPass();   VernonToSpirv.h:7-9
+ *     void mlir::vernon::registerVernonToSPIRVPass();                        VernonToSpirv.cpp:71-75
+ * and its only executing program is the Taichi kernel `paint` in fractal.py:16-25, which runs
+ * inside third-party Taichi 1.7.4 (`ti.init(arch=...)`, fractal.py:5, selects the backend).
+ * This header is the boundary that replaces both: a front end (the Python package
+ * `vernondsl_amd`, or any ctypes/cffi/C++ caller) lowers a DSL program to the op classes below
+ * and drives them through opaque handles.  Each declaration names the reference item it stands
+ * in for.
+ *
+ * Conventions
+ *  - Every function returns int: 0 (VDSL_OK) or a negative vdsl_status.  On failure
+ *    vdsl_last_error() returns a thread-local message.  Nothing aborts the process.
+ *  - Handles are opaque and owned by the caller; each is released by its *_destroy/_free/_close.
+ *    A buffer belongs to the device it was allocated on.
+ *  - Op calls are asynchronous: they enqueue work on the queue (one hipStream_t) and return.
+ *    vdsl_buffer_read and vdsl_queue_sync block.
+ *  - A queue is used by one host thread at a time; different queues may be used concurrently.
+ *  - Between vdsl_graph_begin(q) and vdsl_graph_end(q, &g) op calls on q are recorded, not run;
+ *    vdsl_graph_launch replays the whole recording as one hipGraph.  Host<->device transfers
+ *    (vdsl_buffer_write/read) are rejected while a queue is capturing.
+ *  - Tensors are dense and row-major.  "rows x cols" means cols is the contiguous axis.
+ *  - bf16 is stored as uint16 (the upper half of an IEEE binary32); conversions round to
+ *    nearest-even.
+ */
+#ifndef VDSL_H
+#define VDSL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VDSL_ABI_VERSION 1
+
+typedef enum vdsl_status {
+  VDSL_OK = 0,
+  VDSL_ERR_INVALID_ARG = -1,     /* bad enum, null pointer, negative size, ... */
+  VDSL_ERR_INVALID_HANDLE = -2,  /* null or already-released handle */
+  VDSL_ERR_OUT_OF_MEMORY = -3,   /* device allocation failed (real or injected) */
+  VDSL_ERR_DEVICE = -4,          /* a HIP runtime call failed; message has the HIP error */
+  VDSL_ERR_UNSUPPORTED = -5,     /* valid request this build does not implement */
+  VDSL_ERR_CAPTURE = -6,         /* graph-capture misuse (nested begin, end without begin, ...) */
+  VDSL_ERR_SHAPE = -7,           /* operand shape / buffer size mismatch */
+  VDSL_ERR_NO_DEVICE = -8        /* no HIP device with that ordinal */
+} vdsl_status;
+
+typedef enum vdsl_device_kind {
+  /* `arch=ti.hip` in the front end; ti.init(arch=...) at fractal.py:5 is the reference's
+   * backend switch.  The CPU executor is test infrastructure (oracle/) and is not a device of
+   * this library. */
+  VDSL_DEVICE_HIP = 1
+} vdsl_device_kind;
+
+/* Buffer binding kinds: the vocabulary of the `vernon.semantic` argument attribute that
+ * VernonToSPIRVPass maps to SPIR-V storage classes (VernonToSpirv.cpp:43-56; used in
+ * color.mlir:4-9,43-45).  Ops may read any kind; UNIFORM_CONSTANT buffers are read-only on the
+ * device, and an op that would write one fails with VDSL_ERR_INVALID_ARG. */
+typedef enum vdsl_binding {
+  VDSL_BIND_STORAGE_BUFFER = 0,  /* "storage_buffer": read-write (default) */
+  VDSL_BIND_INPUT = 1,           /* "input" */
+  VDSL_BIND_OUTPUT = 2,          /* "output" */
+  VDSL_BIND_UNIFORM = 3,         /* "uniform" */
+  VDSL_BIND_UNIFORM_CONSTANT = 4,/* "uniform_constant": device read-only */
+  VDSL_BIND_IMAGE = 5,           /* "image" (the pass maps it to the Input class) */
+  VDSL_BIND_VARYING = 6          /* "varying" (color.mlir:9,44; unmapped by the pass) */
+} vdsl_binding;
+
+typedef enum vdsl_dtype {
+  VDSL_F32 = 0,
+  VDSL_BF16 = 1,
+  VDSL_I8 = 2,
+  VDSL_I32 = 3
+} vdsl_dtype;
+
+typedef struct vdsl_device_s* vdsl_device;
+typedef struct vdsl_buffer_s* vdsl_buffer;
+typedef struct vdsl_queue_s* vdsl_queue;
+typedef struct vdsl_graph_s* vdsl_graph;
+typedef struct vdsl_event_s* vdsl_event;
+
+typedef struct vdsl_device_info {
+  char name[64];          /* marketing name, e.g. "AMD Instinct MI355X" */
+  char arch[32];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int32_t compute_units;
+  int32_t clock_khz;
+  int32_t wavefront_size;
+  int32_t lds_bytes_per_block;
+  uint64_t hbm_bytes;
+} vdsl_device_info;
+
+/* ---- errors / version -------------------------------------------------------------------- */
+const char* vdsl_last_error(void);
+int vdsl_abi_version(void);
+
+/* ---- device (replaces ti.init(arch=...), fractal.py:5) ------------------------------------ */
+int vdsl_device_count(int kind, int* count);
+int vdsl_device_open(int kind, int ordinal, vdsl_device* out);
+int vdsl_device_close(vdsl_device dev);
+int vdsl_device_get_info(vdsl_device dev, vdsl_device_info* info);
+
+/* ---- buffers (replaces ti.field storage, fractal.py:8; binding kinds VernonToSpirv.cpp:43-56) */
+int vdsl_buffer_alloc(vdsl_device dev, size_t bytes, int binding, vdsl_buffer* out);
+int vdsl_buffer_free(vdsl_buffer buf);
+int vdsl_buffer_size(vdsl_buffer buf, size_t* bytes);
+int vdsl_buffer_binding(vdsl_buffer buf, int* binding);
+/* Device address of the allocation, for interop with other HIP code in the same process. */
+int vdsl_buffer_device_address(vdsl_buffer buf, uint64_t* address);
+/* Host -> device.  Returns once `src` may be reused. */
+int vdsl_buffer_write(vdsl_queue q, vdsl_buffer buf, size_t offset, const void* src, size_t bytes);
+/* Device -> host.  Blocks until `dst` holds the data (replaces gui.set_image's read-back,
+ * fractal.py:32). */
+int vdsl_buffer_read(vdsl_queue q, vdsl_buffer buf, size_t offset, void* dst, size_t bytes);
+/* Fill with a repeated 32-bit pattern using a kernel (safe to record into a graph).
+ * offset and bytes must be multiples of 4. */
+int vdsl_buffer_fill_u32(vdsl_queue q, vdsl_buffer buf, size_t offset, size_t bytes, uint32_t pattern);
+int vdsl_buffer_copy(vdsl_queue q, vdsl_buffer dst, size_t dst_offset, vdsl_buffer src,
+                     size_t src_offset, size_t bytes);
+
+/* ---- queues ------------------------------------------------------------------------------ */
+int vdsl_queue_create(vdsl_device dev, vdsl_queue* out);
+int vdsl_queue_destroy(vdsl_queue q);
+int vdsl_queue_sync(vdsl_queue q);
+
+/* ---- execution-graph replay (one hipGraph per recorded op sequence) ------------------------ */
+int vdsl_graph_begin(vdsl_queue q);
+int vdsl_graph_end(vdsl_queue q, vdsl_graph* out);
+int vdsl_graph_launch(vdsl_graph g, vdsl_queue q);
+int vdsl_graph_destroy(vdsl_graph g);
+
+/* ---- timing (hipEvents on the queue's own stream) ----------------------------------------- */
+int vdsl_event_create(vdsl_device dev, vdsl_event* out);
+int vdsl_event_record(vdsl_event ev, vdsl_queue q);
+/* Waits for `end`, then returns the elapsed milliseconds between the two records. */
+int vdsl_event_elapsed_ms(vdsl_event start, vdsl_event end, float* ms);
+int vdsl_event_destroy(vdsl_event ev);
+
+/* ========================================================================================== */
+/* Op class 1: per-pixel escape-time iterative map.                                           */
+/* Replaces the body of `paint(t)` (fractal.py:16-25): struct-for over the field (:18), the   */
+/* pixel -> complex map (:20), the check-then-update loop (:22-24) built on complex_sqr        */
+/* (:11-13), and the store (:25).                                                             */
+/* ========================================================================================== */
+typedef enum vdsl_escape_family {
+  VDSL_ESC_MANDELBROT = 0,  /* z0 = 0, c = pixel coordinate */
+  VDSL_ESC_JULIA = 1        /* z0 = pixel coordinate, c = (c_re, c_im)  (fractal.py:19-20) */
+} vdsl_escape_family;
+
+typedef enum vdsl_escape_test {
+  VDSL_ESC_MAG2_GT = 0,     /* stop when zr*zr + zi*zi > bound  (config-1 form, bound = 4) */
+  VDSL_ESC_NORM_GE = 1      /* continue while sqrt(zr*zr + zi*zi) < bound (fractal.py:22) */
+} vdsl_escape_test;
+
+typedef enum vdsl_escape_rounding {
+  /* every product and sum rounded separately, in the order of complex_sqr (fractal.py:13):
+   *   m = zr*zr + zi*zi;  zr' = (zr*zr - zi*zi) + cr;  zi' = ((zi*zr)*2) + ci               */
+  VDSL_ESC_ROUND_SEPARATE = 0,
+  /* fused multiply-add form (one rounding per fma):
+   *   q = zi*zi;  m = fma(zr,zr,q);  zr' = fma(zr,zr,-q) + cr;  zi' = fma(zr+zr, zi, ci)      */
+  VDSL_ESC_ROUND_FMA = 1
+} vdsl_escape_rounding;
+
+typedef enum vdsl_escape_output {
+  VDSL_ESC_OUT_I32_COUNT = 0,   /* int32 iteration count */
+  VDSL_ESC_OUT_F32_AFFINE = 1   /* f32 out_base + float(count) * out_scale (fractal.py:25) */
+} vdsl_escape_output;
+
+typedef struct vdsl_escape_time_params {
+  int32_t ni;          /* extent of the outer axis i (real part); rows of the output */
+  int32_t nj;          /* extent of the inner axis j (imaginary part); contiguous */
+  int32_t family;      /* vdsl_escape_family */
+  int32_t escape_test; /* vdsl_escape_test */
+  int32_t rounding;    /* vdsl_escape_rounding */
+  int32_t out_kind;    /* vdsl_escape_output */
+  int32_t max_iter;    /* >= 0 */
+  float bound;
+  /* coordinate map, every step rounded in f32:  re = ((float(i) / re_den) + re_off) * re_scale + re_post
+   * fractal.py:20 is (i/n - 1) * 2; the config-1 window is (i/1024) * 3 + (-2). */
+  float re_den, re_off, re_scale, re_post;
+  float im_den, im_off, im_scale, im_post;
+  float c_re, c_im;    /* Julia constant (fractal.py:19) */
+  float out_base, out_scale;
+} vdsl_escape_time_params;
+
+/* out: int32 or f32 [ni][nj] per out_kind. */
+int vdsl_op_escape_time(vdsl_queue q, const vdsl_escape_time_params* p, vdsl_buffer out);
+
+/* ========================================================================================== */
+/* Op class 2: fused elementwise / broadcast map chain (no reference code; north-star op      */
+/* class).  A chain is a straight-line register program evaluated per output element.         */
+/* ========================================================================================== */
+#define VDSL_MAP_MAX_INSTR 32
+#define VDSL_MAP_MAX_REGS 8
+#define VDSL_MAP_MAX_INPUTS 4
+
+typedef enum vdsl_map_opcode {
+  VDSL_MAP_LOAD = 1,    /* r[dst] = input[a] at this element (per the input's broadcast) */
+  VDSL_MAP_CONST = 2,   /* r[dst] = imm */
+  VDSL_MAP_MOV = 3,     /* r[dst] = r[a] */
+  VDSL_MAP_NEG = 4,
+  VDSL_MAP_ABS = 5,
+  VDSL_MAP_SQUARE = 6,  /* r[a] * r[a] */
+  VDSL_MAP_EXP = 7,
+  VDSL_MAP_LOG = 8,
+  VDSL_MAP_TANH = 9,
+  VDSL_MAP_SIGMOID = 10,/* 1 / (1 + exp(-r[a])) */
+  VDSL_MAP_RELU = 11,   /* max(r[a], 0) */
+  VDSL_MAP_SQRT = 12,
+  VDSL_MAP_RECIP = 13,  /* 1 / r[a] */
+  VDSL_MAP_ADD = 14,    /* r[a] + r[b] */
+  VDSL_MAP_SUB = 15,
+  VDSL_MAP_MUL = 16,
+  VDSL_MAP_DIV = 17,
+  VDSL_MAP_MAX = 18,
+  VDSL_MAP_MIN = 19,
+  VDSL_MAP_FMA = 20,    /* fma(r[a], r[b], r[c]), one rounding */
+  VDSL_MAP_MUL_IMM = 21,/* r[a] * imm */
+  VDSL_MAP_ADD_IMM = 22 /* r[a] + imm */
+} vdsl_map_opcode;
+
+typedef struct vdsl_map_instr {
+  uint8_t op, dst, a, b, c;
+  uint8_t pad[3];
+  float imm;
+} vdsl_map_instr;
+
+typedef enum vdsl_broadcast {
+  VDSL_BCAST_FULL = 0,   /* [rows][cols] */
+  VDSL_BCAST_ROW = 1,    /* [cols]: one value per column, shared by every row (a row bias) */
+  VDSL_BCAST_COL = 2,    /* [rows]: one value per row */
+  VDSL_BCAST_SCALAR = 3  /* [1] */
+} vdsl_broadcast;
+
+typedef struct vdsl_map_input {
+  vdsl_buffer buf;
+  int32_t bcast;        /* vdsl_broadcast */
+  int32_t dtype;        /* VDSL_F32 */
+} vdsl_map_input;
+
+/* out (f32 [rows][cols]) = r[out_reg] after running `code` for each element. */
+int vdsl_op_map_chain(vdsl_queue q, int64_t rows, int64_t cols, const vdsl_map_instr* code,
+                      int32_t n_instr, const vdsl_map_input* inputs, int32_t n_inputs,
+                      int32_t out_reg, vdsl_buffer out);
+
+/* ========================================================================================== */
+/* Op class 3: row reductions + softmax (no reference code; north-star op class).             */
+/* ========================================================================================== */
+/* x: dtype [rows][cols] (F32 or BF16).  Any output may be NULL.
+ * row_sum, row_max: f32 [rows];  softmax: dtype [rows][cols] = exp(x - max) / sum(exp(x - max)). */
+int vdsl_op_row_reduce_softmax(vdsl_queue q, int64_t rows, int64_t cols, int32_t dtype,
+                               vdsl_buffer x, vdsl_buffer row_sum, vdsl_buffer row_max,
+                               vdsl_buffer softmax);
+/* Column reductions of an f32/bf16 [rows][cols] tensor: col_sum, col_max f32 [cols] (either NULL). */
+int vdsl_op_col_reduce(vdsl_queue q, int64_t rows, int64_t cols, int32_t dtype, vdsl_buffer x,
+                       vdsl_buffer col_sum, vdsl_buffer col_max);
+
+/* ========================================================================================== */
+/* Op class 4: dense bf16 matmul on MFMA, fp32 accumulate (no reference code; north star).    */
+/* ========================================================================================== */
+typedef enum vdsl_epilogue {
+  VDSL_EPI_NONE = 0,
+  VDSL_EPI_GELU = 1,    /* exact-erf GELU: 0.5 * v * (1 + erf(v / sqrt(2))) */
+  VDSL_EPI_RELU = 2
+} vdsl_epilogue;
+
+/* C (c_dtype [M][N]) = epilogue(op(A) . op(B)).
+ *   trans_a = 0: A is [M][K];  trans_a = 1: A is stored [K][M].
+ *   trans_b = 0: B is [K][N];  trans_b = 1: B is stored [N][K].
+ * pre_act: if not NULL, receives the f32 [M][N] accumulator before the epilogue (for autodiff).
+ * workspace: device scratch for operand re-layout; vdsl_gemm_bf16_workspace_bytes() says how
+ * much (0 for trans_a = 0, trans_b = 1), and it may be NULL when that is 0. */
+int vdsl_gemm_bf16_workspace_bytes(int32_t trans_a, int32_t trans_b, int64_t M, int64_t N,
+                                   int64_t K, size_t* bytes);
+int vdsl_op_gemm_bf16(vdsl_queue q, int32_t trans_a, int32_t trans_b, int64_t M, int64_t N,
+                      int64_t K, vdsl_buffer A, vdsl_buffer B, vdsl_buffer C, int32_t c_dtype,
+                      int32_t epilogue, vdsl_buffer pre_act, vdsl_buffer workspace);
+
+/* 2-D transpose: dst [cols][rows] = src [rows][cols]^T, dtype F32 or BF16. */
+int vdsl_op_transpose(vdsl_queue q, int64_t rows, int64_t cols, int32_t dtype, vdsl_buffer src,
+                      vdsl_buffer dst);
+/* Elementwise conversion of n elements (F32 <-> BF16). */
+int vdsl_op_cast(vdsl_queue q, int64_t n, int32_t src_dtype, vdsl_buffer src, int32_t dst_dtype,
+                 vdsl_buffer dst);
+
+/* Autodiff building blocks for the MLP graph (no reference code; north star). */
+/* GELU backward: da (bf16 [rows][cols]) = dh (f32) * GELU'(pre) (f32);  da_t (optional, bf16
+ * [cols][rows]) receives the transpose of da. */
+int vdsl_op_gelu_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer dh, vdsl_buffer pre,
+                     vdsl_buffer da, vdsl_buffer da_t);
+/* MSE: loss (f32 [1]) = mean((y - t)^2);  dy (bf16 [rows][cols]) = 2 (y - t) / (rows*cols);
+ * dy_t (optional) = dy^T.  y, t: f32 [rows][cols].  partials: f32 scratch of
+ * vdsl_mse_partials_count(rows, cols) elements (deterministic two-stage reduction). */
+int64_t vdsl_mse_partials_count(int64_t rows, int64_t cols);
+int vdsl_op_mse_fwd_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer y, vdsl_buffer t,
+                        vdsl_buffer loss, vdsl_buffer dy, vdsl_buffer dy_t, vdsl_buffer partials);
+
+/* ========================================================================================== */
+/* Op class 5: int8 W8A8 GEMM with fused dequant (no reference code; north star).             */
+/* ========================================================================================== */
+/* Per-row symmetric activation quantisation:  s = max|x_row| / 127 (f32);
+ * q = clamp(rne(x / s), -127, 127) (int8), q = 0 for an all-zero row.
+ * x: F32 or BF16 [rows][cols];  q: int8 [rows][cols];  scale: f32 [rows]. */
+int vdsl_op_quantize_rows_i8(vdsl_queue q, int64_t rows, int64_t cols, int32_t x_dtype,
+                             vdsl_buffer x, vdsl_buffer qx, vdsl_buffer scale);
+/* y (out_dtype [M][N]) = relu?( (float(acc) * x_scale[m]) * w_scale[n] ),
+ * acc = sum_k xq[m][k] * w[n][k] in int32 (exact).  xq int8 [M][K]; w int8 [N][K] (out x in,
+ * per-output-channel scales w_scale f32 [N]).  acc_out (optional) receives int32 [M][N].
+ * workspace: int32 split-K partials, vdsl_gemm_w8a8_workspace_bytes() bytes (may be 0). */
+int vdsl_gemm_w8a8_workspace_bytes(int64_t M, int64_t N, int64_t K, size_t* bytes);
+int vdsl_op_gemm_w8a8(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer xq,
+                      vdsl_buffer x_scale, vdsl_buffer w, vdsl_buffer w_scale, vdsl_buffer y,
+                      int32_t out_dtype, int32_t relu, vdsl_buffer acc_out, vdsl_buffer workspace);
+
+/* ---- failure injection (tests of error paths, host-side only) ----------------------------- */
+/* After `n` more successful buffer allocations, the next one fails with VDSL_ERR_OUT_OF_MEMORY
+ * (n < 0 disables).  Also settable with the environment variable VDSL_FAIL_ALLOC_AFTER. */
+int vdsl_debug_fail_alloc_after(int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VDSL_H */

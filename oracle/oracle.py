@@ -1,0 +1,221 @@
+"""ctypes wrapper of liboracle.so (vdsl_oracle.c): numpy arrays in, numpy arrays out.
+
+TEST INFRASTRUCTURE: the parity checker and the timed CPU baseline.  Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg may use it.  It never touches the GPU.
+Each wrapper names the C function (and through it the reference lines) it calls.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+F32, BF16, I8, I32 = 0, 1, 2, 3
+# vdsl_map_opcode values (include/vdsl.h)
+MAP_OPS = {
+    "load": 1, "const": 2, "mov": 3, "neg": 4, "abs": 5, "square": 6, "exp": 7, "log": 8,
+    "tanh": 9, "sigmoid": 10, "relu": 11, "sqrt": 12, "recip": 13, "add": 14, "sub": 15,
+    "mul": 16, "div": 17, "max": 18, "min": 19, "fma": 20, "mul_imm": 21, "add_imm": 22,
+}
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        build()
+    return C.CDLL(LIB_PATH)
+
+
+_lib = _load()
+_vp = C.c_void_p
+_i64 = C.c_int64
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class EscapeTimeParams(C.Structure):
+    # Same layout as vdsl_escape_time_params (include/vdsl.h).
+    _fields_ = [
+        ("ni", C.c_int32), ("nj", C.c_int32), ("family", C.c_int32), ("escape_test", C.c_int32),
+        ("rounding", C.c_int32), ("out_kind", C.c_int32), ("max_iter", C.c_int32), ("bound", C.c_float),
+        ("re_den", C.c_float), ("re_off", C.c_float), ("re_scale", C.c_float), ("re_post", C.c_float),
+        ("im_den", C.c_float), ("im_off", C.c_float), ("im_scale", C.c_float), ("im_post", C.c_float),
+        ("c_re", C.c_float), ("c_im", C.c_float), ("out_base", C.c_float), ("out_scale", C.c_float),
+    ]
+
+
+class MapInstr(C.Structure):
+    _fields_ = [
+        ("op", C.c_uint8), ("dst", C.c_uint8), ("a", C.c_uint8), ("b", C.c_uint8), ("c", C.c_uint8),
+        ("pad", C.c_uint8 * 3), ("imm", C.c_float),
+    ]
+
+
+_lib.orc_escape_time_rows.argtypes = [C.POINTER(EscapeTimeParams), _vp, C.c_int, C.c_int]
+_lib.orc_map_chain_rows.argtypes = [_i64, _i64, C.POINTER(MapInstr), C.c_int, C.POINTER(_vp), C.POINTER(C.c_int),
+                                    C.c_int, C.c_int, _vp, _i64, _i64]
+_lib.orc_row_reduce_softmax_rows.argtypes = [_i64, _i64, C.c_int, _vp, _vp, _vp, _vp, _i64, _i64]
+_lib.orc_col_reduce.argtypes = [_i64, _i64, C.c_int, _vp, _vp, _vp]
+_lib.orc_gemm_bf16_rows.argtypes = [C.c_int, C.c_int, _i64, _i64, _i64, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _i64, _i64]
+_lib.orc_transpose.argtypes = [_i64, _i64, C.c_int, _vp, _vp]
+_lib.orc_cast.argtypes = [_i64, C.c_int, _vp, C.c_int, _vp]
+_lib.orc_gelu_bwd.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp]
+_lib.orc_mse_fwd_bwd.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp, _vp]
+_lib.orc_quantize_rows_i8.argtypes = [_i64, _i64, C.c_int, _vp, _vp, _vp]
+_lib.orc_gemm_w8a8_rows.argtypes = [_i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _i64, _i64]
+_lib.orc_num_threads.restype = C.c_int
+_lib.orc_set_num_threads.argtypes = [C.c_int]
+
+
+def num_threads() -> int:
+    return _lib.orc_num_threads()
+
+
+def set_num_threads(n: int):
+    _lib.orc_set_num_threads(int(n))
+
+
+def _dt(a: np.ndarray) -> int:
+    return BF16 if a.dtype == np.uint16 else F32
+
+
+# ---- escape time: orc_escape_time (fractal.py:11-25) ----------------------------------------
+def escape_time(params: dict, rows=None) -> np.ndarray:
+    """Full grid, or only rows [r0, r1) when rows=(r0, r1) (the result then has r1 - r0 rows)."""
+    p = EscapeTimeParams(**params)
+    r0, r1 = rows if rows else (0, p.ni)
+    dt = np.int32 if p.out_kind == 0 else np.float32
+    out = np.zeros((p.ni, p.nj), dtype=dt)
+    _lib.orc_escape_time_rows(C.byref(p), _p(out), r0, r1)
+    return out[r0:r1]
+
+
+# ---- map chain: orc_map_chain -------------------------------------------------------------------
+def map_chain(prog, inputs, rows: int, cols: int, row_range=None) -> np.ndarray:
+    """prog: vernondsl_amd.mapchain.Program (its code list and broadcasts)."""
+    code = (MapInstr * max(1, len(prog.code)))()
+    for i, (op, dst, a, b, c, imm) in enumerate(prog.code):
+        code[i].op, code[i].dst, code[i].a, code[i].b, code[i].c, code[i].imm = MAP_OPS[op], dst, a, b, c, imm
+    arrs = [np.ascontiguousarray(x, dtype=np.float32) for x in inputs]
+    ptrs = (_vp * max(1, len(arrs)))(*[a.ctypes.data for a in arrs])
+    bc = (C.c_int * max(1, len(arrs)))(*[prog.bcast[k] for k in range(len(arrs))])
+    r0, r1 = row_range if row_range else (0, rows)
+    out = np.zeros((r1 - r0, cols), dtype=np.float32)
+    # The C routine indexes output rows absolutely; shift the base pointer by -r0 rows.
+    base = out.ctypes.data - r0 * cols * 4
+    _lib.orc_map_chain_rows(rows, cols, code, len(prog.code), ptrs, bc, len(arrs), prog.out_reg, _vp(base), r0, r1)
+    return out
+
+
+# ---- row reduce + softmax: orc_row_reduce_softmax ----------------------------------------------
+def row_reduce_softmax(x: np.ndarray, row_range=None):
+    """Returns (row_sum f32, row_max f32, softmax in x's dtype) for rows [r0, r1)."""
+    x = np.ascontiguousarray(x)
+    rows, cols = x.shape
+    r0, r1 = row_range if row_range else (0, rows)
+    n = r1 - r0
+    s = np.zeros(n, np.float32)
+    m = np.zeros(n, np.float32)
+    sm = np.zeros((n, cols), x.dtype)
+    _lib.orc_row_reduce_softmax_rows(rows, cols, _dt(x), _p(x), _vp(s.ctypes.data - r0 * 4),
+                                     _vp(m.ctypes.data - r0 * 4), _vp(sm.ctypes.data - r0 * cols * x.itemsize), r0, r1)
+    return s, m, sm
+
+
+def col_reduce(x: np.ndarray):
+    x = np.ascontiguousarray(x)
+    rows, cols = x.shape
+    s = np.zeros(cols, np.float32)
+    m = np.zeros(cols, np.float32)
+    _lib.orc_col_reduce(rows, cols, _dt(x), _p(x), _p(s), _p(m))
+    return s, m
+
+
+# ---- bf16 GEMM and friends: orc_gemm_bf16 etc. -----------------------------------------------------
+def gemm_bf16(A: np.ndarray, B: np.ndarray, trans_a=False, trans_b=False, c_dtype=F32, epilogue=0,
+              want_pre=False, row_range=None):
+    A = np.ascontiguousarray(A, dtype=np.uint16)
+    B = np.ascontiguousarray(B, dtype=np.uint16)
+    if trans_a:
+        K, M = A.shape
+    else:
+        M, K = A.shape
+    N = B.shape[0] if trans_b else B.shape[1]
+    r0, r1 = row_range if row_range else (0, M)
+    Cm = np.zeros((r1 - r0, N), np.uint16 if c_dtype == BF16 else np.float32)
+    pre = np.zeros((r1 - r0, N), np.float32) if want_pre else None
+    es = Cm.itemsize
+    _lib.orc_gemm_bf16_rows(int(trans_a), int(trans_b), M, N, K, _p(A), _p(B), _vp(Cm.ctypes.data - r0 * N * es),
+                            c_dtype, epilogue, None if pre is None else _vp(pre.ctypes.data - r0 * N * 4), r0, r1)
+    return (Cm, pre) if want_pre else Cm
+
+
+def transpose(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    rows, cols = x.shape
+    out = np.zeros((cols, rows), x.dtype)
+    _lib.orc_transpose(rows, cols, _dt(x), _p(x), _p(out))
+    return out
+
+
+def cast(x: np.ndarray, dst_dtype: int) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    out = np.zeros(x.shape, np.uint16 if dst_dtype == BF16 else np.float32)
+    _lib.orc_cast(x.size, _dt(x), _p(x), dst_dtype, _p(out))
+    return out
+
+
+def gelu_bwd(dh: np.ndarray, pre: np.ndarray):
+    dh = np.ascontiguousarray(dh, np.float32)
+    pre = np.ascontiguousarray(pre, np.float32)
+    rows, cols = dh.shape
+    da = np.zeros((rows, cols), np.uint16)
+    da_t = np.zeros((cols, rows), np.uint16)
+    _lib.orc_gelu_bwd(rows, cols, _p(dh), _p(pre), _p(da), _p(da_t))
+    return da, da_t
+
+
+def mse_fwd_bwd(y: np.ndarray, t: np.ndarray):
+    y = np.ascontiguousarray(y, np.float32)
+    t = np.ascontiguousarray(t, np.float32)
+    rows, cols = y.shape
+    loss = np.zeros(1, np.float32)
+    dy = np.zeros((rows, cols), np.uint16)
+    dy_t = np.zeros((cols, rows), np.uint16)
+    _lib.orc_mse_fwd_bwd(rows, cols, _p(y), _p(t), _p(loss), _p(dy), _p(dy_t))
+    return float(loss[0]), dy, dy_t
+
+
+# ---- int8 W8A8: orc_quantize_rows_i8 / orc_gemm_w8a8 -----------------------------------------------
+def quantize_rows_i8(x: np.ndarray):
+    x = np.ascontiguousarray(x)
+    rows, cols = x.shape
+    q = np.zeros((rows, cols), np.int8)
+    s = np.zeros(rows, np.float32)
+    _lib.orc_quantize_rows_i8(rows, cols, _dt(x), _p(x), _p(q), _p(s))
+    return q, s
+
+
+def gemm_w8a8(xq, xs, w, ws, out_dtype=BF16, relu=False, want_acc=False, row_range=None):
+    xq = np.ascontiguousarray(xq, np.int8)
+    w = np.ascontiguousarray(w, np.int8)
+    xs = np.ascontiguousarray(xs, np.float32)
+    ws = np.ascontiguousarray(ws, np.float32)
+    M, K = xq.shape
+    N = w.shape[0]
+    r0, r1 = row_range if row_range else (0, M)
+    y = np.zeros((r1 - r0, N), np.uint16 if out_dtype == BF16 else np.float32)
+    acc = np.zeros((r1 - r0, N), np.int32) if want_acc else None
+    _lib.orc_gemm_w8a8_rows(M, N, K, _p(xq), _p(xs), _p(w), _p(ws), _vp(y.ctypes.data - r0 * N * y.itemsize), out_dtype,
+                            int(relu), None if acc is None else _vp(acc.ctypes.data - r0 * N * 4), r0, r1)
+    return (y, acc) if want_acc else y

@@ -1,0 +1,405 @@
+/*
+ * vdsl_oracle.c - CPU restatement of every op class of include/vdsl.h.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker and the timed CPU baseline.  Only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load liboracle.so, and
+ * only to check or time it beside the HIP device; the product (libvdsl.so and the
+ * vernondsl_amd package) never calls it and has no CPU fallback.
+ *
+ * Built with -ffp-contract=off: every f32 operation below rounds exactly where it is written;
+ * fmaf() is used only where the spec asks for a single rounding.
+ *
+ * What pins each function (the checks live in tests/):
+ *   orc_escape_time      fractal.py:11-25.  Pinned by an independent numpy evaluation (exactly
+ *                        rounded; fma emulated by round-to-odd in f64), the known answers
+ *                        sum = 49,860,131 and sha256 prefix 747b980a873b342e of the 1024^2
+ *                        separately-rounded grid, the main-cardioid / period-2-bulb closed
+ *                        forms, conjugate symmetry, and f64 brute force away from the boundary.
+ *   orc_map_chain        no reference code.  Pinned against f64 numpy evaluation and the
+ *                        special values x = 0 and |x| large.
+ *   orc_row_reduce_softmax / orc_col_reduce
+ *                        no reference code.  Pinned by f64 sums, exact max, rows summing to 1,
+ *                        constant row -> 1/cols, shift invariance, injected outlier argmax.
+ *   orc_gemm_bf16        no reference code.  Pinned by exact integer-valued products (bf16
+ *                        small integers), brute force in Python integers, and numpy f64.
+ *   orc_gelu_bwd / orc_mse_fwd_bwd
+ *                        no reference code.  Pinned by central finite differences in f64.
+ *   orc_quantize_rows_i8 / orc_gemm_w8a8
+ *                        no reference code.  Pinned by int64 numpy dot products (exact) and a
+ *                        numpy restatement of the f32 dequant sequence.
+ *   orc_transpose / orc_cast
+ *                        pinned by numpy transpose / bit-level RNE.
+ * The reference's own program (fractal.py) runs on third-party Taichi 1.7.4, which is not
+ * importable here; its exact Taichi floating-point behaviour is parity unpinned.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../include/vdsl.h"
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static inline float bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static inline uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+int orc_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+void orc_set_num_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}
+
+/* ---- escape time: fractal.py:16-25 ------------------------------------------------------- */
+
+static float pixel_coord(int idx, float den, float off, float scale, float post) {
+  float v = (float)idx / den; /* fractal.py:20 `i / n` (true division in f32) */
+  v = v + off;                /* `- 1` / `- 0.5` */
+  v = v * scale;              /* `* 2` */
+  return v + post;
+}
+
+/* Rows [i0, i1) of the grid.  Each pixel follows the check-then-update loop of
+ * fractal.py:22-24 with complex_sqr (fractal.py:11-13). */
+void orc_escape_time_rows(const vdsl_escape_time_params* p, void* out, int i0, int i1) {
+#pragma omp parallel for schedule(dynamic, 4)
+  for (int i = i0; i < i1; ++i) {
+    for (int j = 0; j < p->nj; ++j) {
+      const float re = pixel_coord(i, p->re_den, p->re_off, p->re_scale, p->re_post);
+      const float im = pixel_coord(j, p->im_den, p->im_off, p->im_scale, p->im_post);
+      float zr, zi, cr, ci;
+      if (p->family == VDSL_ESC_MANDELBROT) {
+        zr = 0.0f; zi = 0.0f; cr = re; ci = im;
+      } else {
+        zr = re; zi = im; cr = p->c_re; ci = p->c_im;
+      }
+      int it = 0;
+      while (it < p->max_iter) {
+        float mag, nzr, nzi;
+        if (p->rounding == VDSL_ESC_ROUND_SEPARATE) {
+          const float zr2 = zr * zr; /* z[0]**2 */
+          const float zi2 = zi * zi; /* z[1]**2 */
+          mag = zr2 + zi2;
+          nzr = (zr2 - zi2) + cr;        /* z[0]**2 - z[1]**2, then + c */
+          nzi = ((zi * zr) * 2.0f) + ci; /* z[1] * z[0] * 2, then + c */
+        } else {
+          const float q = zi * zi;
+          mag = fmaf(zr, zr, q);
+          nzr = fmaf(zr, zr, -q) + cr;
+          nzi = fmaf(zr + zr, zi, ci);
+        }
+        int go_on = (p->escape_test == VDSL_ESC_MAG2_GT) ? !(mag > p->bound) : (sqrtf(mag) < p->bound);
+        if (!go_on) break;
+        zr = nzr;
+        zi = nzi;
+        ++it;
+      }
+      const size_t o = (size_t)i * (size_t)p->nj + (size_t)j;
+      if (p->out_kind == VDSL_ESC_OUT_I32_COUNT) {
+        ((int32_t*)out)[o] = it;
+      } else {
+        const float f = (float)it * p->out_scale; /* `iterations * 0.02` */
+        ((float*)out)[o] = p->out_base + f;       /* `1 - ...` as 1 + (-0.02 * it) */
+      }
+    }
+  }
+}
+
+void orc_escape_time(const vdsl_escape_time_params* p, void* out) { orc_escape_time_rows(p, out, 0, p->ni); }
+
+/* ---- map chain --------------------------------------------------------------------------- */
+
+static float map_apply(int op, float a, float b, float c, float imm) {
+  switch (op) {
+    case VDSL_MAP_CONST: return imm;
+    case VDSL_MAP_MOV: return a;
+    case VDSL_MAP_NEG: return -a;
+    case VDSL_MAP_ABS: return fabsf(a);
+    case VDSL_MAP_SQUARE: return a * a;
+    case VDSL_MAP_EXP: return expf(a);
+    case VDSL_MAP_LOG: return logf(a);
+    case VDSL_MAP_TANH: return tanhf(a);
+    case VDSL_MAP_SIGMOID: return 1.0f / (1.0f + expf(-a));
+    case VDSL_MAP_RELU: return a > 0.0f ? a : 0.0f;
+    case VDSL_MAP_SQRT: return sqrtf(a);
+    case VDSL_MAP_RECIP: return 1.0f / a;
+    case VDSL_MAP_ADD: return a + b;
+    case VDSL_MAP_SUB: return a - b;
+    case VDSL_MAP_MUL: return a * b;
+    case VDSL_MAP_DIV: return a / b;
+    case VDSL_MAP_MAX: return fmaxf(a, b);
+    case VDSL_MAP_MIN: return fminf(a, b);
+    case VDSL_MAP_FMA: return fmaf(a, b, c);
+    case VDSL_MAP_MUL_IMM: return a * imm;
+    case VDSL_MAP_ADD_IMM: return a + imm;
+    default: return 0.0f;
+  }
+}
+
+/* Rows [r0, r1). in_ptrs[k] holds input k per bcast[k] (vdsl_broadcast). */
+void orc_map_chain_rows(int64_t rows, int64_t cols, const vdsl_map_instr* code, int n_instr,
+                        const float* const* in_ptrs, const int* bcast, int n_inputs, int out_reg, float* out,
+                        int64_t r0, int64_t r1) {
+  (void)rows;
+  (void)n_inputs;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = r0; r < r1; ++r) {
+    for (int64_t c = 0; c < cols; ++c) {
+      float reg[VDSL_MAP_MAX_REGS] = {0};
+      for (int pc = 0; pc < n_instr; ++pc) {
+        const vdsl_map_instr* s = &code[pc];
+        if (s->op == VDSL_MAP_LOAD) {
+          const float* p = in_ptrs[s->a];
+          const int bc = bcast[s->a];
+          reg[s->dst] = bc == VDSL_BCAST_FULL ? p[r * cols + c] : bc == VDSL_BCAST_ROW ? p[c] : bc == VDSL_BCAST_COL ? p[r] : p[0];
+        } else {
+          reg[s->dst] = map_apply(s->op, reg[s->a], reg[s->b], reg[s->c], s->imm);
+        }
+      }
+      out[r * cols + c] = reg[out_reg];
+    }
+  }
+}
+
+void orc_map_chain(int64_t rows, int64_t cols, const vdsl_map_instr* code, int n_instr, const float* const* in_ptrs,
+                   const int* bcast, int n_inputs, int out_reg, float* out) {
+  orc_map_chain_rows(rows, cols, code, n_instr, in_ptrs, bcast, n_inputs, out_reg, out, 0, rows);
+}
+
+/* ---- row reduce + softmax ---------------------------------------------------------------- */
+
+static inline float load_elem(const void* x, int dtype, int64_t idx) {
+  return dtype == VDSL_BF16 ? bf16_to_f32(((const uint16_t*)x)[idx]) : ((const float*)x)[idx];
+}
+
+/* Rows [r0, r1).  sum: f64 accumulation rounded once to f32.  max: exact.  softmax:
+ * e = expf(x - max) in f32, s = f64 sum of e rounded to f32, out = e / s (f32), then RNE to bf16
+ * for bf16 tensors. */
+void orc_row_reduce_softmax_rows(int64_t rows, int64_t cols, int dtype, const void* x, float* row_sum,
+                                 float* row_max, void* softmax, int64_t r0, int64_t r1) {
+  (void)rows;
+#pragma omp parallel
+  {
+    float* e = (float*)malloc(sizeof(float) * (size_t)(cols > 0 ? cols : 1));
+#pragma omp for schedule(static)
+    for (int64_t r = r0; r < r1; ++r) {
+      const int64_t base = r * cols;
+      double s = 0.0;
+      float m = -INFINITY;
+      for (int64_t c = 0; c < cols; ++c) {
+        const float v = load_elem(x, dtype, base + c);
+        s += v;
+        m = fmaxf(m, v);
+      }
+      if (row_sum) row_sum[r] = (float)s;
+      if (row_max) row_max[r] = m;
+      if (softmax) {
+        double es = 0.0;
+        for (int64_t c = 0; c < cols; ++c) {
+          e[c] = expf(load_elem(x, dtype, base + c) - m);
+          es += e[c];
+        }
+        const float esf = (float)es;
+        for (int64_t c = 0; c < cols; ++c) {
+          const float v = e[c] / esf;
+          if (dtype == VDSL_BF16) ((uint16_t*)softmax)[base + c] = f32_to_bf16(v);
+          else ((float*)softmax)[base + c] = v;
+        }
+      }
+    }
+    free(e);
+  }
+}
+
+void orc_row_reduce_softmax(int64_t rows, int64_t cols, int dtype, const void* x, float* row_sum, float* row_max,
+                            void* softmax) {
+  orc_row_reduce_softmax_rows(rows, cols, dtype, x, row_sum, row_max, softmax, 0, rows);
+}
+
+void orc_col_reduce(int64_t rows, int64_t cols, int dtype, const void* x, float* col_sum, float* col_max) {
+#pragma omp parallel for schedule(static)
+  for (int64_t c = 0; c < cols; ++c) {
+    double s = 0.0;
+    float m = -INFINITY;
+    for (int64_t r = 0; r < rows; ++r) {
+      const float v = load_elem(x, dtype, r * cols + c);
+      s += v;
+      m = fmaxf(m, v);
+    }
+    if (col_sum) col_sum[c] = (float)s;
+    if (col_max) col_max[c] = m;
+  }
+}
+
+/* ---- bf16 GEMM, transpose, cast ---------------------------------------------------------- */
+
+static double gelu_d(double v) { return 0.5 * v * (1.0 + erf(v * 0.70710678118654752440)); }
+
+static void store_out(void* C, int c_dtype, int64_t idx, float v) {
+  if (c_dtype == VDSL_BF16) ((uint16_t*)C)[idx] = f32_to_bf16(v);
+  else ((float*)C)[idx] = v;
+}
+
+/* Rows [m0, m1) of C = epilogue(op(A) op(B)); products and sums in f64 (exact products of bf16
+ * values; the f64 sum is then rounded once to f32). */
+void orc_gemm_bf16_rows(int ta, int tb, int64_t M, int64_t N, int64_t K, const uint16_t* A, const uint16_t* B,
+                        void* C, int c_dtype, int epilogue, float* pre_act, int64_t m0, int64_t m1) {
+#pragma omp parallel
+  {
+    double* acc = (double*)malloc(sizeof(double) * (size_t)(N > 0 ? N : 1));
+#pragma omp for schedule(static)
+    for (int64_t m = m0; m < m1; ++m) {
+      for (int64_t n = 0; n < N; ++n) acc[n] = 0.0;
+      for (int64_t k = 0; k < K; ++k) {
+        const double a = bf16_to_f32(ta ? A[k * M + m] : A[m * K + k]);
+        if (a == 0.0) continue;
+        if (!tb) {
+          const uint16_t* brow = B + k * N;
+          for (int64_t n = 0; n < N; ++n) acc[n] += a * (double)bf16_to_f32(brow[n]);
+        } else {
+          for (int64_t n = 0; n < N; ++n) acc[n] += a * (double)bf16_to_f32(B[n * K + k]);
+        }
+      }
+      for (int64_t n = 0; n < N; ++n) {
+        const float v = (float)acc[n];
+        if (pre_act) pre_act[m * N + n] = v;
+        float o = v;
+        if (epilogue == VDSL_EPI_GELU) o = (float)gelu_d((double)v);
+        else if (epilogue == VDSL_EPI_RELU) o = v > 0.0f ? v : 0.0f;
+        store_out(C, c_dtype, m * N + n, o);
+      }
+    }
+    free(acc);
+  }
+  (void)M;
+}
+
+void orc_gemm_bf16(int ta, int tb, int64_t M, int64_t N, int64_t K, const uint16_t* A, const uint16_t* B, void* C,
+                   int c_dtype, int epilogue, float* pre_act) {
+  orc_gemm_bf16_rows(ta, tb, M, N, K, A, B, C, c_dtype, epilogue, pre_act, 0, M);
+}
+
+void orc_transpose(int64_t rows, int64_t cols, int dtype, const void* src, void* dst) {
+  const size_t es = dtype == VDSL_BF16 ? 2 : 4;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < cols; ++c)
+      memcpy((char*)dst + ((size_t)c * (size_t)rows + (size_t)r) * es, (const char*)src + ((size_t)r * (size_t)cols + (size_t)c) * es, es);
+}
+
+void orc_cast(int64_t n, int src_dtype, const void* src, int dst_dtype, void* dst) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) store_out(dst, dst_dtype, i, load_elem(src, src_dtype, i));
+}
+
+/* ---- autodiff blocks --------------------------------------------------------------------- */
+
+/* d/dv GELU(v) = 0.5 (1 + erf(v/sqrt2)) + v exp(-v^2/2) / sqrt(2 pi), evaluated in f64. */
+static double gelu_grad_d(double v) {
+  return 0.5 * (1.0 + erf(v * 0.70710678118654752440)) + v * exp(-0.5 * v * v) * 0.39894228040143267794;
+}
+
+void orc_gelu_bwd(int64_t rows, int64_t cols, const float* dh, const float* pre, uint16_t* da, uint16_t* da_t) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < cols; ++c) {
+      const float g = (float)((double)dh[r * cols + c] * gelu_grad_d((double)pre[r * cols + c]));
+      const uint16_t h = f32_to_bf16(g);
+      if (da) da[r * cols + c] = h;
+      if (da_t) da_t[c * rows + r] = h;
+    }
+}
+
+/* loss = mean((y - t)^2) (f64 sum, rounded once); dy = (y - t) * (2 / n) in f32, RNE to bf16. */
+void orc_mse_fwd_bwd(int64_t rows, int64_t cols, const float* y, const float* t, float* loss, uint16_t* dy,
+                     uint16_t* dy_t) {
+  const int64_t n = rows * cols;
+  const float scale = 2.0f / (float)n;
+  double s = 0.0;
+#pragma omp parallel for schedule(static) reduction(+ : s)
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t c = 0; c < cols; ++c) {
+      const float d = y[r * cols + c] - t[r * cols + c];
+      s += (double)d * (double)d;
+      const uint16_t h = f32_to_bf16(d * scale);
+      if (dy) dy[r * cols + c] = h;
+      if (dy_t) dy_t[c * rows + r] = h;
+    }
+  }
+  if (loss) *loss = (float)(s / (double)n);
+}
+
+/* ---- int8 W8A8 --------------------------------------------------------------------------- */
+
+/* s = max|x| / 127; q = clamp(rint(x / s), -127, 127); an all-zero (or underflowing) row gives
+ * s = 0 and q = 0. */
+void orc_quantize_rows_i8(int64_t rows, int64_t cols, int x_dtype, const void* x, int8_t* q, float* scale) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    float amax = 0.0f;
+    for (int64_t c = 0; c < cols; ++c) amax = fmaxf(amax, fabsf(load_elem(x, x_dtype, r * cols + c)));
+    const float s = amax / 127.0f;
+    scale[r] = s;
+    for (int64_t c = 0; c < cols; ++c) {
+      int v = 0;
+      if (s > 0.0f) {
+        float t = rintf(load_elem(x, x_dtype, r * cols + c) / s);
+        if (t > 127.0f) t = 127.0f;
+        if (t < -127.0f) t = -127.0f;
+        v = (int)t;
+      }
+      q[r * cols + c] = (int8_t)v;
+    }
+  }
+}
+
+/* Rows [m0, m1): acc = sum_k xq[m][k] w[n][k] (exact, int64 then int32);
+ * y = relu?((float(acc) * xs[m]) * ws[n]) in f32, stored as out_dtype. */
+void orc_gemm_w8a8_rows(int64_t M, int64_t N, int64_t K, const int8_t* xq, const float* xs, const int8_t* w,
+                        const float* ws, void* y, int out_dtype, int relu, int32_t* acc_out, int64_t m0, int64_t m1) {
+  (void)M;
+#pragma omp parallel for schedule(static)
+  for (int64_t m = m0; m < m1; ++m) {
+    const int8_t* xr = xq + m * K;
+    for (int64_t n = 0; n < N; ++n) {
+      const int8_t* wr = w + n * K;
+      int64_t acc = 0;
+      for (int64_t k = 0; k < K; ++k) acc += (int64_t)xr[k] * (int64_t)wr[k];
+      const int32_t a32 = (int32_t)acc;
+      if (acc_out) acc_out[m * N + n] = a32;
+      float v = (float)a32 * xs[m];
+      v = v * ws[n];
+      if (relu && !(v > 0.0f)) v = 0.0f;
+      store_out(y, out_dtype, m * N + n, v);
+    }
+  }
+}
+
+void orc_gemm_w8a8(int64_t M, int64_t N, int64_t K, const int8_t* xq, const float* xs, const int8_t* w,
+                   const float* ws, void* y, int out_dtype, int relu, int32_t* acc_out) {
+  orc_gemm_w8a8_rows(M, N, K, xq, xs, w, ws, y, out_dtype, relu, acc_out, 0, M);
+}

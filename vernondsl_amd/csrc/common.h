@@ -1,0 +1,116 @@
+// Internal definitions shared by the runtime and the gfx950 kernels of libvdsl.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <atomic>
+#include <string>
+
+#include "vdsl.h"
+
+// ---- handle objects ------------------------------------------------------------------------
+enum : uint32_t {
+  kMagicDevice = 0x56444556u,  // "VDEV"
+  kMagicBuffer = 0x56425546u,  // "VBUF"
+  kMagicQueue = 0x56515545u,   // "VQUE"
+  kMagicGraph = 0x56475250u,   // "VGRP"
+  kMagicEvent = 0x56455654u,   // "VEVT"
+};
+
+struct vdsl_device_s {
+  uint32_t magic;
+  int ordinal;
+  hipDeviceProp_t props;
+  std::atomic<int> live;  // buffers, queues, graphs and events that belong to this device
+};
+
+struct vdsl_buffer_s {
+  uint32_t magic;
+  vdsl_device dev;
+  void* ptr;
+  size_t bytes;
+  int binding;
+};
+
+struct vdsl_queue_s {
+  uint32_t magic;
+  vdsl_device dev;
+  hipStream_t stream;
+  bool capturing;
+};
+
+struct vdsl_graph_s {
+  uint32_t magic;
+  vdsl_device dev;
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+};
+
+struct vdsl_event_s {
+  uint32_t magic;
+  vdsl_device dev;
+  hipEvent_t ev;
+};
+
+namespace vdsl {
+
+// Records `msg` as this thread's last error and returns `status`.
+int fail(int status, const std::string& msg);
+// Fails with VDSL_ERR_DEVICE and the HIP error string if `e` is not hipSuccess.
+int check_hip(hipError_t e, const char* what);
+// Checks the launch that was just enqueued.
+int check_launch(const char* kernel);
+
+bool valid_device(vdsl_device d);
+bool valid_buffer(vdsl_buffer b);
+bool valid_queue(vdsl_queue q);
+
+// Validates a queue and makes its device current.  Returns VDSL_OK or an error status.
+int enter_queue(vdsl_queue q);
+// Validates `b` (on the queue's device) and that it holds at least `bytes`.  `name` is used in
+// the error message.  If `writable`, rejects UNIFORM_CONSTANT buffers.
+int check_buffer(vdsl_queue q, vdsl_buffer b, size_t bytes, const char* name, bool writable);
+
+size_t dtype_size(int dtype);
+
+}  // namespace vdsl
+
+#define VDSL_TRY(expr)              \
+  do {                              \
+    int _st = (expr);               \
+    if (_st != VDSL_OK) return _st; \
+  } while (0)
+
+// ---- device-side helpers -------------------------------------------------------------------
+namespace vdsl {
+
+// Clang vector types (what the nontemporal and MFMA builtins accept).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even f32 -> bf16; NaN maps to the canonical quiet NaN 0x7FC0.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Butterfly reductions across one 64-lane wavefront (every lane gets the result).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+}  // namespace vdsl

@@ -1,0 +1,309 @@
+// Op class 2: fused elementwise / broadcast map chains on gfx950.
+//
+// The reference has no elementwise code (the only compute is fractal.py:16-25); this op class
+// comes from the north-star spec.  A chain is a straight-line register program
+// (vdsl_map_instr, include/vdsl.h) evaluated once per output element, so a whole expression
+// such as tanh(a*x + b) * exp(-x^2) + bias[col] costs one HBM read of each operand and one
+// write of the result.
+//
+// Mapping: the tensor is [rows][cols] row-major.  A block of 256 lanes spans 256 float4 column
+// slots (1024 columns) of R consecutive rows, so every wave reads 1 KiB contiguous per row with
+// 16-byte loads, a row-broadcast operand (VDSL_BCAST_ROW, e.g. a bias) is loaded once per lane
+// and reused for all R rows, and all R rows' loads are issued before any arithmetic.
+//
+// One interpreter serves two instantiations:
+//   - generic: the program is a kernel argument, executed with a uniform (scalar-branch)
+//     dispatch and uniform register indices;
+//   - fixed: the program is a compile-time table (ProgTanhExpBias below); the same interpreter is
+//     fully unrolled and constant-folded into straight-line code.  A runtime chain whose opcodes,
+//     register indices and input broadcasts equal a table entry runs this version; its
+//     immediates still come from the runtime program.
+
+#include <type_traits>
+#include <utility>
+
+#include "common.h"
+
+namespace vdsl {
+namespace {
+
+struct MapProg {
+  vdsl_map_instr code[VDSL_MAP_MAX_INSTR];
+  int32_t n;
+  int32_t out_reg;
+};
+
+struct MapIn {
+  const float* p[VDSL_MAP_MAX_INPUTS];
+  int32_t bcast[VDSL_MAP_MAX_INPUTS];
+  int32_t n;
+};
+
+__device__ __forceinline__ float apply_op(int op, float a, float b, float c, float imm) {
+  switch (op) {
+    case VDSL_MAP_CONST: return imm;
+    case VDSL_MAP_MOV: return a;
+    case VDSL_MAP_NEG: return -a;
+    case VDSL_MAP_ABS: return fabsf(a);
+    case VDSL_MAP_SQUARE: return a * a;
+    case VDSL_MAP_EXP: return expf(a);
+    case VDSL_MAP_LOG: return logf(a);
+    case VDSL_MAP_TANH: return tanhf(a);
+    case VDSL_MAP_SIGMOID: return 1.0f / (1.0f + expf(-a));
+    case VDSL_MAP_RELU: return a > 0.0f ? a : 0.0f;
+    case VDSL_MAP_SQRT: return sqrtf(a);
+    case VDSL_MAP_RECIP: return 1.0f / a;
+    case VDSL_MAP_ADD: return a + b;
+    case VDSL_MAP_SUB: return a - b;
+    case VDSL_MAP_MUL: return a * b;
+    case VDSL_MAP_DIV: return a / b;
+    case VDSL_MAP_MAX: return fmaxf(a, b);
+    case VDSL_MAP_MIN: return fminf(a, b);
+    case VDSL_MAP_FMA: return __builtin_fmaf(a, b, c);
+    case VDSL_MAP_MUL_IMM: return a * imm;
+    case VDSL_MAP_ADD_IMM: return a + imm;
+    default: return 0.0f;
+  }
+}
+
+// Compile-time programs.  Each lists its opcodes/registers, input broadcasts and output register.
+struct ProgTanhExpBias {
+  // y = tanh(x * a + b) * exp(-(x * x)) + bias[col]   (input 0 = x: FULL, input 1 = bias: ROW),
+  // register-allocated exactly as vernondsl_amd.mapchain.compile emits it.
+  static constexpr int n = 10;
+  static constexpr int n_inputs = 2;
+  static constexpr int out_reg = 0;
+  __host__ __device__ static constexpr int bcast_of(int k) { return k == 1 ? VDSL_BCAST_ROW : VDSL_BCAST_FULL; }
+  static constexpr vdsl_map_instr code[VDSL_MAP_MAX_INSTR] = {
+      {VDSL_MAP_LOAD, 0, 0, 0, 0, {0, 0, 0}, 0.f},     // r0 = x
+      {VDSL_MAP_MUL_IMM, 1, 0, 0, 0, {0, 0, 0}, 0.f},  // r1 = r0 * a
+      {VDSL_MAP_ADD_IMM, 1, 1, 0, 0, {0, 0, 0}, 0.f},  // r1 = r1 + b
+      {VDSL_MAP_TANH, 1, 1, 0, 0, {0, 0, 0}, 0.f},     // r1 = tanh(r1)
+      {VDSL_MAP_SQUARE, 0, 0, 0, 0, {0, 0, 0}, 0.f},   // r0 = r0 * r0
+      {VDSL_MAP_NEG, 0, 0, 0, 0, {0, 0, 0}, 0.f},      // r0 = -r0
+      {VDSL_MAP_EXP, 0, 0, 0, 0, {0, 0, 0}, 0.f},      // r0 = exp(r0)
+      {VDSL_MAP_MUL, 0, 1, 0, 0, {0, 0, 0}, 0.f},      // r0 = r1 * r0
+      {VDSL_MAP_LOAD, 1, 1, 0, 0, {0, 0, 0}, 0.f},     // r1 = bias[col]
+      {VDSL_MAP_ADD, 0, 0, 1, 0, {0, 0, 0}, 0.f},      // r0 = r0 + r1
+  };
+};
+
+struct GenericProgram {};  // marker: program comes from the kernel argument
+
+template <int VEC>
+struct Vec;
+template <>
+struct Vec<4> {
+  using T = float4;
+  __device__ static __forceinline__ void to(const T& v, float (&o)[4]) { o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w; }
+  __device__ static __forceinline__ T from(const float (&o)[4]) { return make_float4(o[0], o[1], o[2], o[3]); }
+};
+template <>
+struct Vec<1> {
+  using T = float;
+  __device__ static __forceinline__ void to(const T& v, float (&o)[1]) { o[0] = v; }
+  __device__ static __forceinline__ T from(const float (&o)[1]) { return o[0]; }
+};
+
+// Loads input k for a VEC-wide element group at (row, col).
+template <int VEC>
+__device__ __forceinline__ void load_input(const float* __restrict__ p, int bcast, int64_t row, int64_t col,
+                                           int64_t cols, float (&o)[VEC]) {
+  using V = Vec<VEC>;
+  if (bcast == VDSL_BCAST_FULL) {
+    V::to(*reinterpret_cast<const typename V::T*>(p + row * cols + col), o);
+  } else if (bcast == VDSL_BCAST_ROW) {
+    V::to(*reinterpret_cast<const typename V::T*>(p + col), o);
+  } else {
+    const float s = (bcast == VDSL_BCAST_COL) ? p[row] : p[0];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o[k] = s;
+  }
+}
+
+template <class P, int VEC, int PC>
+__device__ __forceinline__ void fixed_step(const MapProg& rt, const float (&in)[VDSL_MAP_MAX_INPUTS][VEC],
+                                           float (&r)[VDSL_MAP_MAX_REGS][VEC]) {
+  constexpr vdsl_map_instr s = P::code[PC];
+  if constexpr (s.op == VDSL_MAP_LOAD) {
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) r[s.dst][k] = in[s.a][k];
+  } else {
+    const float imm = rt.code[PC].imm;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) r[s.dst][k] = apply_op(s.op, r[s.a][k], r[s.b][k], r[s.c][k], imm);
+  }
+}
+
+template <class P, int VEC, int... PC>
+__device__ __forceinline__ void run_fixed(const MapProg& rt, const float (&in)[VDSL_MAP_MAX_INPUTS][VEC],
+                                          float (&r)[VDSL_MAP_MAX_REGS][VEC], std::integer_sequence<int, PC...>) {
+  (fixed_step<P, VEC, PC>(rt, in, r), ...);
+}
+
+template <class P, int VEC>
+__device__ __forceinline__ void run_program(const MapProg& rt, const float (&in)[VDSL_MAP_MAX_INPUTS][VEC],
+                                            float (&r)[VDSL_MAP_MAX_REGS][VEC]) {
+  if constexpr (!std::is_same<P, GenericProgram>::value) {
+    run_fixed<P, VEC>(rt, in, r, std::make_integer_sequence<int, P::n>{});
+  } else {
+#pragma unroll 1
+    for (int pc = 0; pc < rt.n; ++pc) {
+      const vdsl_map_instr s = rt.code[pc];
+      if (s.op == VDSL_MAP_LOAD) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) r[s.dst][k] = in[s.a][k];
+      } else {
+        float t[VEC];
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) t[k] = apply_op(s.op, r[s.a][k], r[s.b][k], r[s.c][k], s.imm);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) r[s.dst][k] = t[k];
+      }
+    }
+  }
+}
+
+// Broadcast mode of input k: a compile-time constant for fixed programs.
+template <class P>
+__device__ __forceinline__ int input_bcast(const MapIn& in, int k) {
+  if constexpr (std::is_same<P, GenericProgram>::value) return in.bcast[k];
+  else return P::bcast_of(k);
+}
+
+template <class P, int VEC, int R>
+__global__ __launch_bounds__(256) void map_chain_kernel(MapProg rt, MapIn in, float* __restrict__ out, int64_t rows,
+                                                        int64_t cols) {
+  using V = Vec<VEC>;
+  const int64_t col = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * VEC;
+  if (col >= cols) return;
+  int n_in, out_reg;
+  if constexpr (std::is_same<P, GenericProgram>::value) {
+    n_in = in.n;
+    out_reg = rt.out_reg;
+  } else {
+    n_in = P::n_inputs;
+    out_reg = P::out_reg;
+  }
+
+  for (int64_t row0 = static_cast<int64_t>(blockIdx.y) * R; row0 < rows; row0 += static_cast<int64_t>(gridDim.y) * R) {
+    float vin[R][VDSL_MAP_MAX_INPUTS][VEC];
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      const int64_t row = row0 + u;
+      if (row < rows) {
+#pragma unroll
+        for (int k = 0; k < VDSL_MAP_MAX_INPUTS; ++k) {
+          if (k < n_in) {
+            const int bc = input_bcast<P>(in, k);
+            load_input<VEC>(in.p[k], bc, row, col, cols, vin[u][k]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      const int64_t row = row0 + u;
+      if (row < rows) {
+        float r[VDSL_MAP_MAX_REGS][VEC];
+#pragma unroll
+        for (int g = 0; g < VDSL_MAP_MAX_REGS; ++g)
+#pragma unroll
+          for (int k = 0; k < VEC; ++k) r[g][k] = 0.0f;
+        run_program<P, VEC>(rt, vin[u], r);
+        *reinterpret_cast<typename V::T*>(out + row * cols + col) = V::from(r[out_reg]);
+      }
+    }
+  }
+}
+
+template <class P>
+bool matches(const MapProg& rt, const MapIn& in) {
+  if (rt.n != P::n || in.n != P::n_inputs || rt.out_reg != P::out_reg) return false;
+  for (int k = 0; k < P::n_inputs; ++k)
+    if (in.bcast[k] != P::bcast_of(k)) return false;
+  for (int pc = 0; pc < P::n; ++pc) {
+    const vdsl_map_instr& a = rt.code[pc];
+    const vdsl_map_instr& b = P::code[pc];
+    if (a.op != b.op || a.dst != b.dst) return false;
+    // Compare only the operand fields the opcode reads.
+    switch (a.op) {
+      case VDSL_MAP_CONST: break;
+      case VDSL_MAP_LOAD:
+      case VDSL_MAP_MOV: case VDSL_MAP_NEG: case VDSL_MAP_ABS: case VDSL_MAP_SQUARE: case VDSL_MAP_EXP:
+      case VDSL_MAP_LOG: case VDSL_MAP_TANH: case VDSL_MAP_SIGMOID: case VDSL_MAP_RELU: case VDSL_MAP_SQRT:
+      case VDSL_MAP_RECIP: case VDSL_MAP_MUL_IMM: case VDSL_MAP_ADD_IMM:
+        if (a.a != b.a) return false;
+        break;
+      case VDSL_MAP_FMA:
+        if (a.a != b.a || a.b != b.b || a.c != b.c) return false;
+        break;
+      default:
+        if (a.a != b.a || a.b != b.b) return false;
+    }
+  }
+  return true;
+}
+
+template <class P, int VEC, int R>
+int launch(const MapProg& rt, const MapIn& in, float* out, int64_t rows, int64_t cols, hipStream_t s) {
+  const int64_t slots = (cols + VEC - 1) / VEC;
+  const int64_t gx = (slots + 255) / 256;
+  int64_t gy = (rows + R - 1) / R;
+  if (gy > 65535) gy = 65535;
+  if (gx > 0x7fffffff) return fail(VDSL_ERR_UNSUPPORTED, "map chain: cols too large");
+  hipLaunchKernelGGL((map_chain_kernel<P, VEC, R>), dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)), dim3(256),
+                     0, s, rt, in, out, rows, cols);
+  return check_launch("map_chain_kernel");
+}
+
+}  // namespace
+}  // namespace vdsl
+
+using namespace vdsl;
+
+extern "C" int vdsl_op_map_chain(vdsl_queue q, int64_t rows, int64_t cols, const vdsl_map_instr* code, int32_t n_instr,
+                                 const vdsl_map_input* inputs, int32_t n_inputs, int32_t out_reg, vdsl_buffer out) {
+  VDSL_TRY(enter_queue(q));
+  if (rows < 0 || cols < 0) return fail(VDSL_ERR_INVALID_ARG, "negative shape");
+  if (n_instr < 0 || n_instr > VDSL_MAP_MAX_INSTR) return fail(VDSL_ERR_INVALID_ARG, "n_instr out of range [0, 32]");
+  if (n_inputs < 0 || n_inputs > VDSL_MAP_MAX_INPUTS) return fail(VDSL_ERR_INVALID_ARG, "n_inputs out of range [0, 4]");
+  if (out_reg < 0 || out_reg >= VDSL_MAP_MAX_REGS) return fail(VDSL_ERR_INVALID_ARG, "out_reg out of range");
+  if (n_instr && !code) return fail(VDSL_ERR_INVALID_ARG, "code is null");
+  if (n_inputs && !inputs) return fail(VDSL_ERR_INVALID_ARG, "inputs is null");
+  const int64_t n = rows * cols;
+  VDSL_TRY(check_buffer(q, out, static_cast<size_t>(n) * 4u, "out", true));
+
+  MapProg rt{};
+  rt.n = n_instr;
+  rt.out_reg = out_reg;
+  for (int pc = 0; pc < n_instr; ++pc) {
+    const vdsl_map_instr& s = code[pc];
+    if (s.op < VDSL_MAP_LOAD || s.op > VDSL_MAP_ADD_IMM)
+      return fail(VDSL_ERR_INVALID_ARG, "instruction " + std::to_string(pc) + ": unknown opcode " + std::to_string(s.op));
+    if (s.dst >= VDSL_MAP_MAX_REGS || s.b >= VDSL_MAP_MAX_REGS || s.c >= VDSL_MAP_MAX_REGS)
+      return fail(VDSL_ERR_INVALID_ARG, "instruction " + std::to_string(pc) + ": register out of range");
+    if (s.op == VDSL_MAP_LOAD ? s.a >= n_inputs : s.a >= VDSL_MAP_MAX_REGS)
+      return fail(VDSL_ERR_INVALID_ARG, "instruction " + std::to_string(pc) + ": operand out of range");
+    rt.code[pc] = s;
+  }
+  MapIn in{};
+  in.n = n_inputs;
+  for (int k = 0; k < n_inputs; ++k) {
+    const vdsl_map_input& d = inputs[k];
+    if (d.dtype != VDSL_F32) return fail(VDSL_ERR_UNSUPPORTED, "map chain inputs must be f32");
+    if (d.bcast < VDSL_BCAST_FULL || d.bcast > VDSL_BCAST_SCALAR) return fail(VDSL_ERR_INVALID_ARG, "unknown broadcast");
+    const int64_t need = d.bcast == VDSL_BCAST_FULL ? n : d.bcast == VDSL_BCAST_ROW ? cols : d.bcast == VDSL_BCAST_COL ? rows : 1;
+    std::string name = "input" + std::to_string(k);
+    VDSL_TRY(check_buffer(q, d.buf, static_cast<size_t>(need) * 4u, name.c_str(), false));
+    in.p[k] = static_cast<const float*>(d.buf->ptr);
+    in.bcast[k] = d.bcast;
+  }
+  if (n == 0) return VDSL_OK;
+  float* o = static_cast<float*>(out->ptr);
+  // 16-byte vectors need cols % 4 == 0 and 16-byte aligned bases (hipMalloc gives 256).
+  const bool vec4 = (cols % 4) == 0;
+  if (vec4 && matches<ProgTanhExpBias>(rt, in)) return launch<ProgTanhExpBias, 4, 4>(rt, in, o, rows, cols, q->stream);
+  if (vec4) return launch<GenericProgram, 4, 1>(rt, in, o, rows, cols, q->stream);
+  return launch<GenericProgram, 1, 1>(rt, in, o, rows, cols, q->stream);
+}

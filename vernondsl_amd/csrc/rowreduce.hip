@@ -1,0 +1,252 @@
+// Op class 3: row reductions (sum, max) + softmax, and column reductions, on gfx950.
+//
+// No reference code (the north-star op class).  Semantics, shared with the CPU oracle:
+//   row_sum = sum_j x[j] accumulated in f64, rounded once to f32;
+//   row_max = max_j x[j] (exact);
+//   softmax[j] = e[j] / s,  e[j] = expf(x[j] - row_max) in f32,  s = f64 sum of e rounded to f32.
+//
+// Mapping: one 64-lane wavefront owns one row and keeps it in VGPRs, so x is read from HBM once
+// and softmax written once (the HBM roofline's minimum traffic).  Lane l holds the 16-byte
+// vectors v*64 + l, v < NV, so every load/store instruction of a wave covers 1 KiB contiguous.
+// Reductions stay inside the wave (xor butterflies), so a 256-thread block is 4 independent
+// rows and needs no LDS and no barrier.  Widths that are not one of the register-resident
+// shapes use a 3-pass streaming kernel (max/sum, exp-sum, write) with the same arithmetic.
+
+#include "common.h"
+
+namespace vdsl {
+namespace {
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+template <int DT>
+struct Elem;
+template <>
+struct Elem<VDSL_F32> {
+  static constexpr int kPerVec = 4;  // elements per 16-byte vector
+  __device__ static __forceinline__ void unpack(const uint4& v, float (&o)[4]) {
+    o[0] = __uint_as_float(v.x); o[1] = __uint_as_float(v.y); o[2] = __uint_as_float(v.z); o[3] = __uint_as_float(v.w);
+  }
+  __device__ static __forceinline__ uint4 pack(const float (&o)[4]) {
+    return make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3]));
+  }
+  __device__ static __forceinline__ float load1(const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }
+  __device__ static __forceinline__ void store1(void* p, int64_t i, float v) { static_cast<float*>(p)[i] = v; }
+};
+template <>
+struct Elem<VDSL_BF16> {
+  static constexpr int kPerVec = 8;
+  __device__ static __forceinline__ void unpack(const uint4& v, float (&o)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      o[2 * k] = __uint_as_float(w[k] << 16);
+      o[2 * k + 1] = __uint_as_float(w[k] & 0xFFFF0000u);
+    }
+  }
+  __device__ static __forceinline__ uint4 pack(const float (&o)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      w[k] = static_cast<uint32_t>(f32_to_bf16(o[2 * k])) | (static_cast<uint32_t>(f32_to_bf16(o[2 * k + 1])) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  __device__ static __forceinline__ float load1(const void* p, int64_t i) {
+    return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  }
+  __device__ static __forceinline__ void store1(void* p, int64_t i, float v) { static_cast<uint16_t*>(p)[i] = f32_to_bf16(v); }
+};
+
+// Register-resident row: NV 16-byte vectors per lane, cols = 64 * NV * E::kPerVec.
+template <int DT, int NV>
+__global__ __launch_bounds__(256) void row_softmax_resident(const void* __restrict__ x, float* __restrict__ row_sum,
+                                                            float* __restrict__ row_max, void* __restrict__ sm,
+                                                            int64_t rows) {
+  using E = Elem<DT>;
+  constexpr int PV = E::kPerVec;
+  constexpr int64_t cols = 64 * NV * PV;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint4* src = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + row * cols * (DT == VDSL_F32 ? 4 : 2));
+
+  float v[NV][PV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + k * 64 + lane));
+    E::unpack(make_uint4(r[0], r[1], r[2], r[3]), v[k]);
+  }
+  double s = 0.0;
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+#pragma unroll
+    for (int e = 0; e < PV; ++e) {
+      s += static_cast<double>(v[k][e]);
+      m = fmaxf(m, v[k][e]);
+    }
+  s = wave_sum_f64(s);
+  m = wave_max(m);
+  if (lane == 0) {
+    if (row_sum) row_sum[row] = static_cast<float>(s);
+    if (row_max) row_max[row] = m;
+  }
+  if (!sm) return;
+  double es = 0.0;
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+#pragma unroll
+    for (int e = 0; e < PV; ++e) {
+      v[k][e] = expf(v[k][e] - m);
+      es += static_cast<double>(v[k][e]);
+    }
+  const float esf = static_cast<float>(wave_sum_f64(es));
+  uint4* dst = reinterpret_cast<uint4*>(static_cast<char*>(sm) + row * cols * (DT == VDSL_F32 ? 4 : 2));
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+#pragma unroll
+    for (int e = 0; e < PV; ++e) v[k][e] = v[k][e] / esf;
+    const uint4 w = E::pack(v[k]);
+    const u32x4 wv = {w.x, w.y, w.z, w.w};
+    __builtin_nontemporal_store(wv, reinterpret_cast<u32x4*>(dst + k * 64 + lane));
+  }
+}
+
+// Any width: three streaming passes over the row with the same arithmetic.
+template <int DT>
+__global__ __launch_bounds__(256) void row_softmax_generic(const void* __restrict__ x, float* __restrict__ row_sum,
+                                                           float* __restrict__ row_max, void* __restrict__ sm,
+                                                           int64_t rows, int64_t cols) {
+  using E = Elem<DT>;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  double s = 0.0;
+  float m = -INFINITY;
+  for (int64_t c = lane; c < cols; c += 64) {
+    const float v = E::load1(x, base + c);
+    s += static_cast<double>(v);
+    m = fmaxf(m, v);
+  }
+  s = wave_sum_f64(s);
+  m = wave_max(m);
+  if (lane == 0) {
+    if (row_sum) row_sum[row] = static_cast<float>(s);
+    if (row_max) row_max[row] = m;
+  }
+  if (!sm) return;
+  double es = 0.0;
+  for (int64_t c = lane; c < cols; c += 64) es += static_cast<double>(expf(E::load1(x, base + c) - m));
+  const float esf = static_cast<float>(wave_sum_f64(es));
+  for (int64_t c = lane; c < cols; c += 64) E::store1(sm, base + c, expf(E::load1(x, base + c) - m) / esf);
+}
+
+// Column reductions: a block owns 64 columns; 4 row groups accumulate in f64 and are combined in
+// a fixed order, so results do not depend on scheduling.
+template <int DT>
+__global__ __launch_bounds__(256) void col_reduce_kernel(const void* __restrict__ x, float* __restrict__ col_sum,
+                                                         float* __restrict__ col_max, int64_t rows, int64_t cols) {
+  using E = Elem<DT>;
+  __shared__ double ssum[4][64];
+  __shared__ float smax[4][64];
+  const int c_local = threadIdx.x & 63;
+  const int g = threadIdx.x >> 6;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + c_local;
+  double s = 0.0;
+  float m = -INFINITY;
+  if (c < cols)
+    for (int64_t r = g; r < rows; r += 4) {
+      const float v = E::load1(x, r * cols + c);
+      s += static_cast<double>(v);
+      m = fmaxf(m, v);
+    }
+  ssum[g][c_local] = s;
+  smax[g][c_local] = m;
+  __syncthreads();
+  if (g == 0 && c < cols) {
+    const double t = ((ssum[0][c_local] + ssum[1][c_local]) + ssum[2][c_local]) + ssum[3][c_local];
+    const float mm = fmaxf(fmaxf(smax[0][c_local], smax[1][c_local]), fmaxf(smax[2][c_local], smax[3][c_local]));
+    if (col_sum) col_sum[c] = static_cast<float>(t);
+    if (col_max) col_max[c] = mm;
+  }
+}
+
+template <int DT>
+int launch_rows(const void* x, float* rs, float* rm, void* sm, int64_t rows, int64_t cols, hipStream_t st) {
+  const int64_t blocks = (rows + 3) / 4;
+  if (blocks > 0x7fffffff) return fail(VDSL_ERR_UNSUPPORTED, "too many rows");
+  const dim3 grid(static_cast<unsigned>(blocks)), block(256);
+  constexpr int PV = Elem<DT>::kPerVec;
+  switch (cols) {
+#define VDSL_ROW_CASE(NV) \
+  case 64 * NV * PV: hipLaunchKernelGGL((row_softmax_resident<DT, NV>), grid, block, 0, st, x, rs, rm, sm, rows); break;
+    VDSL_ROW_CASE(1)
+    VDSL_ROW_CASE(2)
+    VDSL_ROW_CASE(4)
+    VDSL_ROW_CASE(8)
+    VDSL_ROW_CASE(16)
+#undef VDSL_ROW_CASE
+    default:
+      if (DT == VDSL_F32 && cols == 64 * 32 * 4) {
+        hipLaunchKernelGGL((row_softmax_resident<DT, 32>), grid, block, 0, st, x, rs, rm, sm, rows);
+      } else {
+        hipLaunchKernelGGL((row_softmax_generic<DT>), grid, block, 0, st, x, rs, rm, sm, rows, cols);
+      }
+  }
+  return check_launch("row_softmax");
+}
+
+}  // namespace
+}  // namespace vdsl
+
+using namespace vdsl;
+
+extern "C" int vdsl_op_row_reduce_softmax(vdsl_queue q, int64_t rows, int64_t cols, int32_t dtype, vdsl_buffer x,
+                                          vdsl_buffer row_sum, vdsl_buffer row_max, vdsl_buffer softmax) {
+  VDSL_TRY(enter_queue(q));
+  if (rows < 0 || cols < 0) return fail(VDSL_ERR_INVALID_ARG, "negative shape");
+  if (dtype != VDSL_F32 && dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "softmax dtype must be f32 or bf16");
+  const size_t es = dtype_size(dtype);
+  const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols);
+  VDSL_TRY(check_buffer(q, x, n * es, "x", false));
+  if (row_sum) VDSL_TRY(check_buffer(q, row_sum, static_cast<size_t>(rows) * 4, "row_sum", true));
+  if (row_max) VDSL_TRY(check_buffer(q, row_max, static_cast<size_t>(rows) * 4, "row_max", true));
+  if (softmax) VDSL_TRY(check_buffer(q, softmax, n * es, "softmax", true));
+  if (rows == 0) return VDSL_OK;
+  if (cols == 0) {
+    // sum of an empty row is 0 and its max is -inf; nothing else to write
+    if (row_sum) VDSL_TRY(vdsl_buffer_fill_u32(q, row_sum, 0, static_cast<size_t>(rows) * 4, 0u));
+    if (row_max) VDSL_TRY(vdsl_buffer_fill_u32(q, row_max, 0, static_cast<size_t>(rows) * 4, 0xFF800000u));
+    return VDSL_OK;
+  }
+  float* rs = row_sum ? static_cast<float*>(row_sum->ptr) : nullptr;
+  float* rm = row_max ? static_cast<float*>(row_max->ptr) : nullptr;
+  void* sm = softmax ? softmax->ptr : nullptr;
+  if (dtype == VDSL_F32) return launch_rows<VDSL_F32>(x->ptr, rs, rm, sm, rows, cols, q->stream);
+  return launch_rows<VDSL_BF16>(x->ptr, rs, rm, sm, rows, cols, q->stream);
+}
+
+extern "C" int vdsl_op_col_reduce(vdsl_queue q, int64_t rows, int64_t cols, int32_t dtype, vdsl_buffer x,
+                                  vdsl_buffer col_sum, vdsl_buffer col_max) {
+  VDSL_TRY(enter_queue(q));
+  if (rows < 0 || cols < 0) return fail(VDSL_ERR_INVALID_ARG, "negative shape");
+  if (dtype != VDSL_F32 && dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "col_reduce dtype must be f32 or bf16");
+  const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols);
+  VDSL_TRY(check_buffer(q, x, n * dtype_size(dtype), "x", false));
+  if (col_sum) VDSL_TRY(check_buffer(q, col_sum, static_cast<size_t>(cols) * 4, "col_sum", true));
+  if (col_max) VDSL_TRY(check_buffer(q, col_max, static_cast<size_t>(cols) * 4, "col_max", true));
+  if (cols == 0) return VDSL_OK;
+  const int64_t blocks = (cols + 63) / 64;
+  float* cs = col_sum ? static_cast<float*>(col_sum->ptr) : nullptr;
+  float* cm = col_max ? static_cast<float*>(col_max->ptr) : nullptr;
+  if (dtype == VDSL_F32)
+    hipLaunchKernelGGL((col_reduce_kernel<VDSL_F32>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, q->stream, x->ptr, cs, cm, rows, cols);
+  else
+    hipLaunchKernelGGL((col_reduce_kernel<VDSL_BF16>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, q->stream, x->ptr, cs, cm, rows, cols);
+  return check_launch("col_reduce_kernel");
+}

@@ -1,0 +1,173 @@
+"""Op-class calls on the HIP device, one function per `vdsl_op_*` entry point of include/vdsl.h.
+
+Each function checks operand shapes and dtypes on the host before anything is enqueued (the C
+ABI checks buffer sizes again), then enqueues the op on `q` and returns without waiting.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+from . import _lib
+from ._lib import call
+from .mapchain import Program
+from .rhi import Queue, Tensor, dtype_code
+
+
+def _h(t):
+    return None if t is None else t.handle
+
+
+def _expect(t: Tensor, shape, dtype, name):
+    if t is None:
+        return
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: shape {t.shape}, expected {tuple(shape)}")
+    if t.dtype != dtype_code(dtype):
+        raise ValueError(f"{name}: dtype {t.dtype}, expected {dtype}")
+
+
+# ---- op class 1: escape-time iterative map (fractal.py:16-25) -------------------------------
+def escape_time_params(**kw) -> _lib.EscapeTimeParams:
+    p = _lib.EscapeTimeParams()
+    defaults = dict(family=_lib.ESC_MANDELBROT, escape_test=_lib.ESC_MAG2_GT, rounding=_lib.ESC_ROUND_FMA,
+                    out_kind=_lib.ESC_OUT_I32_COUNT, max_iter=256, bound=4.0,
+                    re_den=1.0, re_off=0.0, re_scale=1.0, re_post=0.0,
+                    im_den=1.0, im_off=0.0, im_scale=1.0, im_post=0.0,
+                    c_re=0.0, c_im=0.0, out_base=0.0, out_scale=1.0)
+    defaults.update(kw)
+    for k, v in defaults.items():
+        setattr(p, k, v)
+    return p
+
+
+def escape_time(q: Queue, p: _lib.EscapeTimeParams, out: Tensor):
+    dt = "i32" if p.out_kind == _lib.ESC_OUT_I32_COUNT else "f32"
+    _expect(out, (p.ni, p.nj), dt, "out")
+    call("vdsl_op_escape_time", q.handle, C.byref(p), out.handle)
+
+
+# ---- op class 2: fused map chain --------------------------------------------------------------
+def map_chain(q: Queue, prog: Program, inputs, out: Tensor):
+    """inputs[k] is the Tensor for Input(k); its broadcast comes from the program."""
+    rows, cols = out.shape
+    if len(inputs) != prog.n_inputs:
+        raise ValueError(f"program reads {prog.n_inputs} inputs, {len(inputs)} given")
+    arr = (_lib.MapInput * max(1, len(inputs)))()
+    for k, t in enumerate(inputs):
+        bc = prog.bcast[k]
+        want = {_lib.BCAST_FULL: (rows, cols), _lib.BCAST_ROW: (cols,), _lib.BCAST_COL: (rows,), _lib.BCAST_SCALAR: (1,)}[bc]
+        _expect(t, want, "f32", f"input{k}")
+        arr[k].buf, arr[k].bcast, arr[k].dtype = t.handle.value, bc, _lib.F32
+    _expect(out, (rows, cols), "f32", "out")
+    code = prog.instr_array()
+    call("vdsl_op_map_chain", q.handle, rows, cols, code, len(prog.code), arr, len(inputs), prog.out_reg, out.handle)
+
+
+# ---- op class 3: row reductions + softmax ------------------------------------------------------
+def row_reduce_softmax(q: Queue, x: Tensor, row_sum=None, row_max=None, softmax=None):
+    rows, cols = x.shape
+    _expect(row_sum, (rows,), "f32", "row_sum")
+    _expect(row_max, (rows,), "f32", "row_max")
+    _expect(softmax, (rows, cols), x.dtype, "softmax")
+    call("vdsl_op_row_reduce_softmax", q.handle, rows, cols, x.dtype, x.handle, _h(row_sum), _h(row_max), _h(softmax))
+
+
+def col_reduce(q: Queue, x: Tensor, col_sum=None, col_max=None):
+    rows, cols = x.shape
+    _expect(col_sum, (cols,), "f32", "col_sum")
+    _expect(col_max, (cols,), "f32", "col_max")
+    call("vdsl_op_col_reduce", q.handle, rows, cols, x.dtype, x.handle, _h(col_sum), _h(col_max))
+
+
+# ---- op class 4: bf16 GEMM + layout + autodiff blocks ------------------------------------------
+def gemm_bf16_workspace_bytes(trans_a, trans_b, M, N, K) -> int:
+    n = C.c_size_t()
+    call("vdsl_gemm_bf16_workspace_bytes", int(trans_a), int(trans_b), M, N, K, C.byref(n))
+    return n.value
+
+
+def gemm_bf16(q: Queue, A: Tensor, B: Tensor, Cout: Tensor, trans_a=False, trans_b=False,
+              epilogue=_lib.EPI_NONE, pre_act=None, workspace=None):
+    if trans_a:
+        K, M = A.shape
+    else:
+        M, K = A.shape
+    if trans_b:
+        N, K2 = B.shape
+    else:
+        K2, N = B.shape
+    if K != K2:
+        raise ValueError(f"inner dimensions differ: {K} vs {K2}")
+    _expect(A, A.shape, "bf16", "A")
+    _expect(B, B.shape, "bf16", "B")
+    if Cout.shape != (M, N):
+        raise ValueError(f"C: shape {Cout.shape}, expected {(M, N)}")
+    _expect(pre_act, (M, N), "f32", "pre_act")
+    call("vdsl_op_gemm_bf16", q.handle, int(trans_a), int(trans_b), M, N, K, A.handle, B.handle, Cout.handle,
+         Cout.dtype, int(epilogue), _h(pre_act), _h(workspace))
+
+
+def transpose(q: Queue, src: Tensor, dst: Tensor):
+    rows, cols = src.shape
+    _expect(dst, (cols, rows), src.dtype, "dst")
+    call("vdsl_op_transpose", q.handle, rows, cols, src.dtype, src.handle, dst.handle)
+
+
+def cast(q: Queue, src: Tensor, dst: Tensor):
+    if src.numel != dst.numel:
+        raise ValueError("cast: element counts differ")
+    call("vdsl_op_cast", q.handle, src.numel, src.dtype, src.handle, dst.dtype, dst.handle)
+
+
+def gelu_bwd(q: Queue, dh: Tensor, pre: Tensor, da: Tensor, da_t=None):
+    rows, cols = dh.shape
+    _expect(dh, (rows, cols), "f32", "dh")
+    _expect(pre, (rows, cols), "f32", "pre")
+    _expect(da, (rows, cols), "bf16", "da")
+    _expect(da_t, (cols, rows), "bf16", "da_t")
+    call("vdsl_op_gelu_bwd", q.handle, rows, cols, dh.handle, pre.handle, da.handle, _h(da_t))
+
+
+def mse_partials_count(rows, cols) -> int:
+    return int(_lib.lib.vdsl_mse_partials_count(rows, cols))
+
+
+def mse_fwd_bwd(q: Queue, y: Tensor, t: Tensor, loss: Tensor, dy: Tensor, dy_t, partials: Tensor):
+    rows, cols = y.shape
+    _expect(t, (rows, cols), "f32", "t")
+    _expect(loss, (1,), "f32", "loss")
+    _expect(dy, (rows, cols), "bf16", "dy")
+    _expect(dy_t, (cols, rows), "bf16", "dy_t")
+    call("vdsl_op_mse_fwd_bwd", q.handle, rows, cols, y.handle, t.handle, loss.handle, dy.handle, _h(dy_t),
+         partials.handle)
+
+
+# ---- op class 5: int8 W8A8 -----------------------------------------------------------------------
+def quantize_rows_i8(q: Queue, x: Tensor, qx: Tensor, scale: Tensor):
+    rows, cols = x.shape
+    _expect(qx, (rows, cols), "i8", "qx")
+    _expect(scale, (rows,), "f32", "scale")
+    call("vdsl_op_quantize_rows_i8", q.handle, rows, cols, x.dtype, x.handle, qx.handle, scale.handle)
+
+
+def gemm_w8a8_workspace_bytes(M, N, K) -> int:
+    n = C.c_size_t()
+    call("vdsl_gemm_w8a8_workspace_bytes", M, N, K, C.byref(n))
+    return n.value
+
+
+def gemm_w8a8(q: Queue, xq: Tensor, x_scale: Tensor, w: Tensor, w_scale: Tensor, y: Tensor, relu=False,
+              acc_out=None, workspace=None):
+    M, K = xq.shape
+    N, K2 = w.shape
+    if K != K2:
+        raise ValueError(f"inner dimensions differ: {K} vs {K2}")
+    _expect(xq, (M, K), "i8", "xq")
+    _expect(w, (N, K), "i8", "w")
+    _expect(x_scale, (M,), "f32", "x_scale")
+    _expect(w_scale, (N,), "f32", "w_scale")
+    if y.shape != (M, N):
+        raise ValueError(f"y: shape {y.shape}, expected {(M, N)}")
+    _expect(acc_out, (M, N), "i32", "acc_out")
+    call("vdsl_op_gemm_w8a8", q.handle, M, N, K, xq.handle, x_scale.handle, w.handle, w_scale.handle, y.handle,
+         y.dtype, int(bool(relu)), _h(acc_out), _h(workspace))
