@@ -176,6 +176,116 @@ def bench_softmax(dev, q, steps, warmup, do_cpu):
     return out
 
 
+# ---- config 4 ------------------------------------------------------------------------------------
+def bench_mlp(dev, q, steps, warmup, do_cpu):
+    from oracle import oracle
+    from vernondsl_amd import _lib, graph, kernels, spec
+    from vernondsl_amd.rhi import Event, Tensor
+    B, D, Hd, O = 2048, 4096, 4096, 4096
+    x, w1, w2, t = spec.mlp_inputs(B, D, Hd, O)
+    g, _ = graph.mlp_train_graph(B, D, Hd, O)
+    exe = g.compile(dev)
+    for name, arr in (("X", x), ("W1", w1), ("W2", w2), ("T", t)):
+        exe.write(q, name, arr)
+    step = exe.capture(q)
+    for _ in range(max(1, warmup // 5)):
+        step.launch(q)
+    q.sync()
+    n = max(5, steps // 5)
+    e0, e1 = Event(dev), Event(dev)
+    e0.record(q)
+    for _ in range(n):
+        step.launch(q)
+    e1.record(q)
+    ms = e0.elapsed_ms(e1) / n
+    flops = spec.mlp_flops(B, D, Hd, O)
+    tflops = flops / (ms * 1e-3) / 1e12
+    loss = float(exe.read(q, "loss")[0])
+    step.destroy()
+    exe.free()
+    # dominant kernel: the forward GEMM (NT, 2048x4096x4096, GELU epilogue) timed alone
+    tx, tw = Tensor.from_numpy(dev, q, x, "bf16"), Tensor.from_numpy(dev, q, w1, "bf16")
+    th, tp = Tensor(dev, (B, Hd), "bf16"), Tensor(dev, (B, Hd), "f32")
+    gms, _ = time_replays(q, dev, lambda: kernels.gemm_bf16(q, tx, tw, th, False, True, _lib.EPI_GELU, tp),
+                          max(2, steps // 10), 1, per_graph=10)
+    gflop = 2 * B * D * Hd
+    gt = gflop / (gms * 1e-3) / 1e12
+    for t_ in (tx, tw, th, tp):
+        t_.free()
+    res = {"config": 4, "workload": "2-layer MLP 4096-4096-4096, GELU, MSE, batch 2048, bf16 MFMA, fwd+bwd as one hipGraph",
+           "metric": "MFMA TFLOPS (GEMM)", "value": tflops, "unit": "TFLOP/s", "ms_per_step": ms,
+           "flop_per_step": flops, "loss": loss,
+           "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                        "frac": gt / PEAK_BF16_TFLOPS, "kernel": "gemm_bf16_nt<GELU,bf16,pre> 2048x4096x4096",
+                        "kernel_ms": gms},
+           "whole_graph_frac_of_peak": tflops / PEAK_BF16_TFLOPS}
+    if do_cpu:
+        b = 64
+        xs, ts_ = x[:b], t[:b]
+        tc = time_cpu(lambda: oracle.mlp_train_step(xs, w1, w2, ts_), min_s=1.0, max_reps=2)
+        res["cpu_baseline"] = {"value": spec.mlp_flops(b, D, Hd, O) / tc / 1e12, "unit": "TFLOP/s",
+                               "cores": oracle.num_threads(), "kind": "port",
+                               "sample": f"the same step at batch {b} (of {B}), f64-accumulating oracle"}
+    return res
+
+
+# ---- config 5 ------------------------------------------------------------------------------------
+def bench_w8a8(dev, q, steps, warmup, do_cpu):
+    from oracle import oracle
+    from vernondsl_amd import graph, kernels, spec
+    from vernondsl_amd.rhi import Event, Tensor
+    B, widths = 512, spec.W8A8_WIDTHS
+    x, layers = spec.w8a8_inputs(B, widths)
+    g = graph.w8a8_infer_graph(B, widths)
+    exe = g.compile(dev)
+    exe.write(q, "X", x)
+    for li, (w, sc) in enumerate(layers):
+        exe.write(q, f"W{li}", w)
+        exe.write(q, f"S{li}", sc)
+    step = exe.capture(q)
+    for _ in range(max(1, warmup // 5)):
+        step.launch(q)
+    q.sync()
+    n = max(5, steps // 2)
+    e0, e1 = Event(dev), Event(dev)
+    e0.record(q)
+    for _ in range(n):
+        step.launch(q)
+    e1.record(q)
+    ms = e0.elapsed_ms(e1) / n
+    ops = spec.w8a8_ops(B, widths)
+    tops = ops / (ms * 1e-3) / 1e12
+    got = exe.read(q, "Y")
+    rows = np.array([0, 511])
+    parity = "ok" if np.array_equal(got[rows], oracle.w8a8_forward(x[rows], layers)) else "FAIL"
+    step.destroy()
+    exe.free()
+    # dominant kernel: one 512x8192x8192 layer GEMM timed alone
+    K = N = 8192
+    txq = Tensor.from_numpy(dev, q, np.zeros((B, K), np.int8))
+    txs = Tensor.from_numpy(dev, q, np.ones(B, np.float32))
+    tw, tws = Tensor.from_numpy(dev, q, layers[0][0]), Tensor.from_numpy(dev, q, layers[0][1])
+    ty = Tensor(dev, (B, N), "bf16")
+    gms, _ = time_replays(q, dev, lambda: kernels.gemm_w8a8(q, txq, txs, tw, tws, ty, True), max(2, steps // 10), 1,
+                          per_graph=10)
+    gt = 2 * B * K * N / (gms * 1e-3) / 1e12
+    for t_ in (txq, txs, tw, tws, ty):
+        t_.free()
+    res = {"config": 5, "workload": "int8 W8A8 MLP 8192-8192-8192-8192-1024, batch 512, dequant+ReLU fused, one hipGraph",
+           "metric": "MFMA TOPS (int8 GEMM)", "value": tops, "unit": "TOP/s", "ms_per_step": ms, "ops_per_step": ops,
+           "parity": parity,
+           "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+                        "frac": gt / PEAK_INT8_TOPS, "kernel": "gemm_w8a8_nt 512x8192x8192", "kernel_ms": gms},
+           "whole_graph_frac_of_peak": tops / PEAK_INT8_TOPS}
+    if do_cpu:
+        r = 8
+        tc = time_cpu(lambda: oracle.w8a8_forward(x[:r], layers), min_s=1.0, max_reps=2)
+        res["cpu_baseline"] = {"value": spec.w8a8_ops(r, widths) / tc / 1e12, "unit": "TOP/s",
+                               "cores": oracle.num_threads(), "kind": "port",
+                               "sample": f"{r} of {B} rows through all 4 layers (rows are independent)"}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -202,7 +312,7 @@ def main():
     head = bench_map_chain(dev, q, args.steps, args.warmup, do_cpu)
     log("bench: config 2", {k: v for k, v in head.items() if k != "cpu"})
     per_config = []
-    for fn, cid in ((bench_fractal, 1), (bench_softmax, 3)):
+    for fn, cid in ((bench_fractal, 1), (bench_softmax, 3), (bench_mlp, 4), (bench_w8a8, 5)):
         if args.only and args.only != cid:
             continue
         r = fn(dev, q, args.steps, args.warmup, do_cpu)

@@ -219,3 +219,30 @@ def gemm_w8a8(xq, xs, w, ws, out_dtype=BF16, relu=False, want_acc=False, row_ran
     _lib.orc_gemm_w8a8_rows(M, N, K, _p(xq), _p(xs), _p(w), _p(ws), _vp(y.ctypes.data - r0 * N * y.itemsize), out_dtype,
                             int(relu), None if acc is None else _vp(acc.ctypes.data - r0 * N * 4), r0, r1)
     return (y, acc) if want_acc else y
+
+
+# ---- composite programs of configs 4 and 5 (built from the routines above) --------------------
+GELU = 1
+
+
+def mlp_train_step(x, w1, w2, t, batch_rows=None):
+    """Config 4 forward + backward with the same roundings as the HIP graph:
+    H = bf16(GELU(X W1^T)) (pre-activation kept in f32), Y = H W2^T (f32), loss = mean((Y - T)^2),
+    dY = bf16((Y - T) 2/n), dW2 = dY^T H, dH = dY W2 (f32), dA = bf16(dH GELU'(pre)), dW1 = dA^T X."""
+    h, pre = gemm_bf16(x, w1, False, True, c_dtype=BF16, epilogue=GELU, want_pre=True)
+    y = gemm_bf16(h, w2, False, True)
+    loss, dy, dy_t = mse_fwd_bwd(y, t)
+    dw2 = gemm_bf16(dy_t, h, False, False)
+    dh = gemm_bf16(dy, w2, False, False)
+    da, da_t = gelu_bwd(dh, pre)
+    dw1 = gemm_bf16(da_t, x, False, False)
+    return {"H": h, "pre": pre, "Y": y, "loss": loss, "dY": dy, "dW2": dw2, "dH": dh, "dA": da, "dW1": dw1}
+
+
+def w8a8_forward(x, layers):
+    """Config 5 forward: per layer quantise rows, int8 GEMM, dequant, ReLU except after the last."""
+    h = x
+    for li, (w, s) in enumerate(layers):
+        xq, xs = quantize_rows_i8(h)
+        h = gemm_w8a8(xq, xs, w, s, out_dtype=BF16, relu=li < len(layers) - 1)
+    return h

@@ -257,7 +257,8 @@ void orc_col_reduce(int64_t rows, int64_t cols, int dtype, const void* x, float*
 
 /* ---- bf16 GEMM, transpose, cast ---------------------------------------------------------- */
 
-static double gelu_d(double v) { return 0.5 * v * (1.0 + erf(v * 0.70710678118654752440)); }
+/* 0.5 v (1 + erf(v / sqrt2)) = 0.5 v erfc(-v / sqrt2) (no cancellation for v < 0). */
+static double gelu_d(double v) { return 0.5 * v * erfc(-v * 0.70710678118654752440); }
 
 static void store_out(void* C, int c_dtype, int64_t idx, float v) {
   if (c_dtype == VDSL_BF16) ((uint16_t*)C)[idx] = f32_to_bf16(v);
@@ -318,9 +319,9 @@ void orc_cast(int64_t n, int src_dtype, const void* src, int dst_dtype, void* ds
 
 /* ---- autodiff blocks --------------------------------------------------------------------- */
 
-/* d/dv GELU(v) = 0.5 (1 + erf(v/sqrt2)) + v exp(-v^2/2) / sqrt(2 pi), evaluated in f64. */
+/* d/dv GELU(v) = Phi(v) + v phi(v) = 0.5 erfc(-v/sqrt2) + v exp(-v^2/2) / sqrt(2 pi), in f64. */
 static double gelu_grad_d(double v) {
-  return 0.5 * (1.0 + erf(v * 0.70710678118654752440)) + v * exp(-0.5 * v * v) * 0.39894228040143267794;
+  return 0.5 * erfc(-v * 0.70710678118654752440) + v * exp(-0.5 * v * v) * 0.39894228040143267794;
 }
 
 void orc_gelu_bwd(int64_t rows, int64_t cols, const float* dh, const float* pre, uint16_t* da, uint16_t* da_t) {

@@ -1,0 +1,208 @@
+"""GPU parity of the MFMA GEMMs, layout ops and autodiff blocks against the CPU oracle.
+
+Tolerances: bf16 GEMM (f32 accumulate) - Frobenius-relative error <= 1e-2 and elementwise
+|gpu - oracle| <= 1e-2 * (|A| |B|)[m][n] (the magnitude the sum was formed from); bf16 outputs
+are compared after converting both sides to f32 with a one-bf16-ulp allowance.  int8: the int32
+accumulators and the dequantised outputs are bit-exact.  Layout ops: bit-exact.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle
+from vernondsl_amd import _lib, kernels, rng
+from vernondsl_amd.rhi import Tensor
+
+pytestmark = pytest.mark.gpu
+F32, BF16 = 0, 1
+
+
+def bf16_rand(shape, seed, lo=-1.0, hi=1.0):
+    return rng.f32_to_bf16(rng.uniform(seed, int(np.prod(shape)), lo, hi)).reshape(shape)
+
+
+def gemm_gpu(dev, q, A, B, ta, tb, c_dtype="f32", epi=_lib.EPI_NONE, want_pre=False):
+    K, M = A.shape if ta else A.shape[::-1]
+    N = B.shape[0] if tb else B.shape[1]
+    tA, tB = Tensor.from_numpy(dev, q, A, "bf16"), Tensor.from_numpy(dev, q, B, "bf16")
+    tC = Tensor(dev, (M, N), c_dtype)
+    tC.buffer.fill_u32(q, 0x7FC07FC0)
+    pre = Tensor(dev, (M, N), "f32") if want_pre else None
+    wsb = kernels.gemm_bf16_workspace_bytes(ta, tb, M, N, K)
+    ws = Tensor(dev, (max(1, wsb),), "i8") if wsb else None
+    kernels.gemm_bf16(q, tA, tB, tC, ta, tb, epi, pre, ws)
+    out = tC.numpy(q)
+    p = pre.numpy(q) if want_pre else None
+    for t in (tA, tB, tC, pre, ws):
+        if t is not None:
+            t.free()
+    return (out, p) if want_pre else out
+
+
+def magnitude(A, B, ta, tb):
+    Af = np.abs(rng.bf16_to_f32(A).astype(np.float64))
+    Bf = np.abs(rng.bf16_to_f32(B).astype(np.float64))
+    return (Af.T if ta else Af) @ (Bf.T if tb else Bf)
+
+
+def assert_gemm_close(got, ref, mag):
+    got = got.astype(np.float64)
+    ref = ref.astype(np.float64)
+    fro = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+    assert fro <= 1e-2, fro
+    assert np.all(np.abs(got - ref) <= 1e-2 * mag + 1e-30), float(np.max(np.abs(got - ref) / (mag + 1e-30)))
+
+
+def test_mfma_single_tile_layout(dev, q):
+    # one 32x32x16 MFMA worth of work: checks the operand/accumulator lane layout exactly
+    r = np.random.default_rng(0)
+    A = rng.f32_to_bf16(r.integers(-4, 5, (32, 16)).astype(np.float32))
+    B = rng.f32_to_bf16(r.integers(-4, 5, (32, 16)).astype(np.float32))
+    got = gemm_gpu(dev, q, A, B, 0, 1)
+    ref = rng.bf16_to_f32(A).astype(np.int64) @ rng.bf16_to_f32(B).astype(np.int64).T
+    assert np.array_equal(got, ref.astype(np.float32))
+
+
+def test_exact_small_integers_large_tile(dev, q):
+    r = np.random.default_rng(1)
+    A = rng.f32_to_bf16(r.integers(-8, 9, (256, 512)).astype(np.float32))
+    B = rng.f32_to_bf16(r.integers(-8, 9, (384, 512)).astype(np.float32))
+    got = gemm_gpu(dev, q, A, B, 0, 1)
+    ref = rng.bf16_to_f32(A).astype(np.int64) @ rng.bf16_to_f32(B).astype(np.int64).T
+    assert np.array_equal(got, ref.astype(np.float32))  # |sums| < 2^24: exact in f32
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 1), (0, 0), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(256, 384, 192), (130, 70, 72), (1, 1, 8), (300, 129, 1000), (64, 64, 13)])
+def test_layouts_and_edges(dev, q, ta, tb, M, N, K):
+    A = bf16_rand((K, M) if ta else (M, K), M * 7 + K)
+    B = bf16_rand((N, K) if tb else (K, N), N * 3 + K)
+    got = gemm_gpu(dev, q, A, B, ta, tb)
+    ref = oracle.gemm_bf16(A, B, ta, tb)
+    assert_gemm_close(got, ref, magnitude(A, B, ta, tb))
+
+
+@pytest.mark.parametrize("epi", [_lib.EPI_GELU, _lib.EPI_RELU])
+def test_epilogues_bf16_out_and_pre(dev, q, epi):
+    A, B = bf16_rand((256, 256), 11, -2, 2), bf16_rand((128, 256), 12, -2, 2)
+    out, pre = gemm_gpu(dev, q, A, B, 0, 1, "bf16", epi, want_pre=True)
+    rout, rpre = oracle.gemm_bf16(A, B, 0, 1, c_dtype=BF16, epilogue=epi, want_pre=True)
+    mag = magnitude(A, B, 0, 1)
+    assert_gemm_close(pre, rpre, mag)
+    a, b = rng.bf16_to_f32(out).astype(np.float64), rng.bf16_to_f32(rout).astype(np.float64)
+    assert np.all(np.abs(a - b) <= 1e-2 * np.maximum(np.abs(b), mag * 1e-2) + 1e-30)
+
+
+def test_config4_shape_gemm(dev, q):
+    """One forward GEMM of config 4 at full size, checked on sampled rows."""
+    from vernondsl_amd import spec
+    x, w1, _, _ = spec.mlp_inputs()
+    out, pre = gemm_gpu(dev, q, x, w1, 0, 1, "bf16", _lib.EPI_GELU, want_pre=True)
+    for r in (0, 1000, 2047):
+        rout, rpre = oracle.gemm_bf16(x, w1, 0, 1, c_dtype=BF16, epilogue=_lib.EPI_GELU, want_pre=True,
+                                      row_range=(r, r + 1))
+        mag = magnitude(x[r:r + 1], w1, 0, 1)
+        assert_gemm_close(pre[r:r + 1], rpre, mag)
+
+
+def test_transpose_and_cast(dev, q):
+    for shape in ((64, 64), (37, 1000), (1, 5), (513, 129)):
+        x = rng.normal(3, int(np.prod(shape))).reshape(shape)
+        for dt, h in (("f32", x), ("bf16", rng.f32_to_bf16(x))):
+            ts = Tensor.from_numpy(dev, q, h, dt)
+            td = Tensor(dev, shape[::-1], dt)
+            kernels.transpose(q, ts, td)
+            assert np.array_equal(td.numpy(q), h.T)
+            ts.free()
+            td.free()
+    x = rng.normal(4, 10001)
+    tx = Tensor.from_numpy(dev, q, x)
+    tb = Tensor(dev, (10001,), "bf16")
+    tf = Tensor(dev, (10001,), "f32")
+    kernels.cast(q, tx, tb)
+    kernels.cast(q, tb, tf)
+    assert np.array_equal(tb.numpy(q), rng.f32_to_bf16(x))
+    assert np.array_equal(tf.numpy(q), rng.bf16_to_f32(rng.f32_to_bf16(x)))
+    for t in (tx, tb, tf):
+        t.free()
+
+
+@pytest.mark.parametrize("rows,cols", [(128, 192), (70, 33), (2048, 4096)])
+def test_gelu_bwd(dev, q, rows, cols):
+    dh = rng.normal(21, rows * cols).reshape(rows, cols) * np.float32(1e-3)
+    pre = rng.normal(22, rows * cols, 0, 2).reshape(rows, cols)
+    tdh, tpre = Tensor.from_numpy(dev, q, dh), Tensor.from_numpy(dev, q, pre)
+    tda, tdat = Tensor(dev, (rows, cols), "bf16"), Tensor(dev, (cols, rows), "bf16")
+    kernels.gelu_bwd(q, tdh, tpre, tda, tdat)
+    da, dat = tda.numpy(q), tdat.numpy(q)
+    rda, _ = oracle.gelu_bwd(dh, pre)
+    a, b = rng.bf16_to_f32(da).astype(np.float64), rng.bf16_to_f32(rda).astype(np.float64)
+    # 1e-2 relative, with a floor of |dh| * 2^-20: GELU' is O(1) and its f32 evaluation carries an
+    # absolute error of a few 2^-24, which dominates where GELU'(pre) itself underflows (pre << 0)
+    assert np.all(np.abs(a - b) <= 1e-2 * np.abs(b) + np.abs(dh.astype(np.float64)) * 2.0 ** -20)
+    assert np.array_equal(dat, da.T)
+    for t in (tdh, tpre, tda, tdat):
+        t.free()
+
+
+@pytest.mark.parametrize("rows,cols", [(128, 192), (70, 33), (2048, 4096)])
+def test_mse(dev, q, rows, cols):
+    y = rng.normal(31, rows * cols).reshape(rows, cols)
+    t = rng.normal(32, rows * cols).reshape(rows, cols)
+    ty, tt = Tensor.from_numpy(dev, q, y), Tensor.from_numpy(dev, q, t)
+    loss = Tensor(dev, (1,), "f32")
+    dy, dyt = Tensor(dev, (rows, cols), "bf16"), Tensor(dev, (cols, rows), "bf16")
+    part = Tensor(dev, (kernels.mse_partials_count(rows, cols),), "f32")
+    kernels.mse_fwd_bwd(q, ty, tt, loss, dy, dyt, part)
+    rl, rdy, _ = oracle.mse_fwd_bwd(y, t)
+    assert abs(float(loss.numpy(q)[0]) - rl) <= 1e-6 * abs(rl)
+    g = dy.numpy(q)
+    assert np.array_equal(g, rdy)  # dy = (y - t) * 2^-k exactly, then RNE: bit-exact
+    assert np.array_equal(dyt.numpy(q), g.T)
+    for x in (ty, tt, loss, dy, dyt, part):
+        x.free()
+
+
+@pytest.mark.parametrize("rows,cols,dt", [(512, 8192, "bf16"), (37, 100, "f32"), (5, 16, "bf16")])
+def test_quantize_rows(dev, q, rows, cols, dt):
+    x = rng.normal(41, rows * cols).reshape(rows, cols)
+    if rows > 3:
+        x[3] = 0
+    xh = rng.f32_to_bf16(x) if dt == "bf16" else x
+    tx = Tensor.from_numpy(dev, q, xh, dt)
+    tq, ts = Tensor(dev, (rows, cols), "i8"), Tensor(dev, (rows,), "f32")
+    kernels.quantize_rows_i8(q, tx, tq, ts)
+    rq, rs = oracle.quantize_rows_i8(xh)
+    assert np.array_equal(ts.numpy(q), rs)
+    assert np.array_equal(tq.numpy(q), rq)
+    for t in (tx, tq, ts):
+        t.free()
+
+
+@pytest.mark.parametrize("M,N,K,relu,dt", [(512, 8192, 8192, True, "bf16"), (512, 1024, 8192, False, "bf16"),
+                                           (100, 70, 48, True, "f32"), (128, 128, 4096, False, "f32"),
+                                           (33, 257, 272, True, "bf16")])
+def test_w8a8_bit_exact(dev, q, M, N, K, relu, dt):
+    r = np.random.default_rng(M + N + K)
+    xq = r.integers(-127, 128, (M, K)).astype(np.int8)
+    w = r.integers(-127, 128, (N, K)).astype(np.int8)
+    xs = r.uniform(0.001, 0.01, M).astype(np.float32)
+    ws = r.uniform(0.005, 0.02, N).astype(np.float32)
+    txq, tw = Tensor.from_numpy(dev, q, xq), Tensor.from_numpy(dev, q, w)
+    txs, tws = Tensor.from_numpy(dev, q, xs), Tensor.from_numpy(dev, q, ws)
+    ty, tacc = Tensor(dev, (M, N), dt), Tensor(dev, (M, N), "i32")
+    wsb = kernels.gemm_w8a8_workspace_bytes(M, N, K)
+    twk = Tensor(dev, (max(1, wsb),), "i8")
+    kernels.gemm_w8a8(q, txq, txs, tw, tws, ty, relu, tacc, twk if wsb else None)
+    acc = tacc.numpy(q)
+    y = ty.numpy(q)
+    sample = slice(None) if M * N <= 1 << 20 else slice(0, 16)
+    ry, racc = oracle.gemm_w8a8(xq[sample], xs[sample], w, ws, out_dtype=BF16 if dt == "bf16" else F32, relu=relu,
+                                want_acc=True)
+    assert np.array_equal(acc[sample], racc)
+    assert np.array_equal(y[sample], ry)
+    if M * N > 1 << 20:  # every row's accumulators against an exact int64 product of a column slice
+        cols = slice(0, 64)
+        ref = xq.astype(np.int64) @ w[cols].astype(np.int64).T
+        assert np.array_equal(acc[:, cols], ref.astype(np.int32))
+    for t in (txq, tw, txs, tws, ty, tacc, twk):
+        t.free()

@@ -1,0 +1,135 @@
+"""GPU execution graphs of configs 4 and 5, replayed as one hipGraph, against the CPU oracle.
+
+Config 4 (bf16 MLP train step): small shapes are compared end to end with the oracle composite;
+the full shape is checked op by op on sampled rows, each op fed the GPU's own inputs.
+Config 5 (int8 inference): bit-exact.  Quantisation is per row, so every output row depends on
+its input row only, and sampled rows of the full-size network are checked exactly.
+Every graph test replays the graph several times, with eager work and synchronisation between
+replays, and compares each replay with the eager run bit for bit.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle
+from vernondsl_amd import graph, rng, spec
+
+pytestmark = pytest.mark.gpu
+BF16 = 1
+
+
+def gemm_close(got, ref, mag, rel=1e-2):
+    got, ref = got.astype(np.float64), ref.astype(np.float64)
+    assert np.linalg.norm(got - ref) <= rel * max(np.linalg.norm(ref), 1e-30)
+    assert np.all(np.abs(got - ref) <= rel * mag + 1e-30)
+
+
+def bf16_close(a, b, floor=0.0):
+    a, b = rng.bf16_to_f32(a).astype(np.float64), rng.bf16_to_f32(b).astype(np.float64)
+    assert np.all(np.abs(a - b) <= 1e-2 * np.abs(b) + floor)
+
+
+def absmm(a, b):
+    return np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64))
+
+
+def run_mlp(dev, q, x, w1, w2, t, replays=3):
+    B, D = x.shape
+    Hd, O = w1.shape[0], w2.shape[0]
+    g, grads = graph.mlp_train_graph(B, D, Hd, O)
+    exe = g.compile(dev)
+    for name, arr in (("X", x), ("W1", w1), ("W2", w2), ("T", t)):
+        exe.write(q, name, arr)
+    names = ["H", "Y", "loss", "grad_W1", "grad_W2"]
+    exe.run(q)
+    eager = {n: exe.read(q, n) for n in names}
+    step = exe.capture(q)
+    for _ in range(replays):
+        for n in names:  # poison the outputs, then replay
+            exe.t[n].buffer.fill_u32(q, 0x7FC07FC0)
+        q.sync()
+        step.launch(q)
+        q.sync()
+        for n in names:
+            assert np.array_equal(exe.read(q, n), eager[n]), f"replay differs from eager run in {n}"
+    step.destroy()
+    out = dict(eager)
+    out["pre"] = exe.read(q, g.ops[0].attrs["pre"].name)
+    exe.free()
+    return out
+
+
+def test_mlp_small_end_to_end(dev, q):
+    x, w1, w2, t = spec.mlp_inputs(batch=256, d_in=384, hidden=512, d_out=256)
+    got = run_mlp(dev, q, x, w1, w2, t)
+    ref = oracle.mlp_train_step(x, w1, w2, t)
+    X, W1 = rng.bf16_to_f32(x), rng.bf16_to_f32(w1)
+    gemm_close(got["pre"], ref["pre"], absmm(X, W1.T))
+    assert abs(float(got["loss"][0]) - ref["loss"]) <= 1e-2 * ref["loss"]
+    for n in ("grad_W1", "grad_W2"):
+        r = ref["d" + n[5:]]
+        a = got[n].astype(np.float64)
+        assert np.linalg.norm(a - r) <= 1e-2 * np.linalg.norm(r), n
+
+
+def test_mlp_config4_full_size(dev, q):
+    x, w1, w2, t = spec.mlp_inputs()
+    got = run_mlp(dev, q, x, w1, w2, t, replays=2)
+    B = x.shape[0]
+    rows = [0, 777, B - 1]
+    X, W1, W2 = rng.bf16_to_f32(x), rng.bf16_to_f32(w1), rng.bf16_to_f32(w2)
+    # forward, sampled rows
+    for r in rows:
+        h, pre = oracle.gemm_bf16(x, w1, 0, 1, c_dtype=BF16, epilogue=1, want_pre=True, row_range=(r, r + 1))
+        gemm_close(got["pre"][r:r + 1], pre, absmm(X[r:r + 1], W1.T))
+        y = oracle.gemm_bf16(got["H"], w2, 0, 1, row_range=(r, r + 1))
+        gemm_close(got["Y"][r:r + 1], y, absmm(rng.bf16_to_f32(got["H"][r:r + 1]), W2.T))
+    # loss and dY from the GPU's Y: dY is exact, the loss within f64-sum rounding
+    loss, dy, dy_t = oracle.mse_fwd_bwd(got["Y"], t)
+    assert abs(float(got["loss"][0]) - loss) <= 1e-6 * loss
+    # weight gradients, sampled output rows, from the GPU's own intermediates
+    for o in (0, 2048, 4095):
+        dw2 = oracle.gemm_bf16(dy_t, got["H"], 0, 0, row_range=(o, o + 1))
+        gemm_close(got["grad_W2"][o:o + 1], dw2, absmm(rng.bf16_to_f32(dy_t[o:o + 1]), rng.bf16_to_f32(got["H"])))
+    dh = oracle.gemm_bf16(dy, w2, 0, 0)
+    da, da_t = oracle.gelu_bwd(dh, got["pre"])
+    for o in (0, 1234, 4095):
+        dw1 = oracle.gemm_bf16(da_t, x, 0, 0, row_range=(o, o + 1))
+        gemm_close(got["grad_W1"][o:o + 1], dw1, absmm(rng.bf16_to_f32(da_t[o:o + 1]), X), rel=2e-2)
+
+
+def run_w8a8(dev, q, x, layers, replays=3):
+    widths = (x.shape[1],) + tuple(w.shape[0] for w, _ in layers)
+    g = graph.w8a8_infer_graph(x.shape[0], widths)
+    exe = g.compile(dev)
+    exe.write(q, "X", x)
+    for li, (w, s) in enumerate(layers):
+        exe.write(q, f"W{li}", w)
+        exe.write(q, f"S{li}", s)
+    exe.run(q)
+    eager = exe.read(q, "Y")
+    step = exe.capture(q)
+    for _ in range(replays):
+        exe.t["Y"].buffer.fill_u32(q, 0x7FC07FC0)
+        q.sync()
+        step.launch(q)
+        q.sync()
+        assert np.array_equal(exe.read(q, "Y"), eager)
+    step.destroy()
+    exe.free()
+    return eager
+
+
+def test_w8a8_small_bit_exact(dev, q):
+    x, layers = spec.w8a8_inputs(batch=64, widths=(512, 384, 256, 128))
+    got = run_w8a8(dev, q, x, layers)
+    assert np.array_equal(got, oracle.w8a8_forward(x, layers))
+
+
+def test_w8a8_config5_full_size_sampled_rows(dev, q):
+    x, layers = spec.w8a8_inputs()
+    got = run_w8a8(dev, q, x, layers, replays=2)
+    assert got.shape == (512, 1024)
+    rows = np.array([0, 1, 255, 256, 511])
+    ref = oracle.w8a8_forward(x[rows], layers)
+    assert np.array_equal(got[rows], ref)
+    assert np.isfinite(rng.bf16_to_f32(got)).all()

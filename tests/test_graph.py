@@ -1,0 +1,87 @@
+"""Execution-graph construction and autodiff on the CPU (no device): the op sequence the
+backward pass emits, shapes and layouts, and an f64 finite-difference pin of the composite
+oracle (oracle.mlp_train_step) that the GPU graph is compared with."""
+import numpy as np
+import pytest
+from scipy.special import erf
+
+from oracle import oracle
+from vernondsl_amd import graph, rng
+
+
+def test_mlp_backward_op_sequence():
+    g, grads = graph.mlp_train_graph(batch=64, d_in=32, hidden=48, d_out=16)
+    kinds = [op.kind for op in g.ops]
+    assert kinds == ["linear", "linear", "mse", "gemm", "gemm", "gelu_bwd", "gemm"]
+    assert sorted(grads) == ["W1", "W2"]
+    assert grads["W1"].shape == (48, 32) and grads["W2"].shape == (16, 48)
+    assert grads["W1"].dtype == "f32"
+    mse = g.ops[2]
+    assert [v.shape for v in mse.outputs] == [(1,), (64, 16), (16, 64), mse.outputs[3].shape]
+    dW2, dH, gb, dW1 = g.ops[3], g.ops[4], g.ops[5], g.ops[6]
+    assert dW2.inputs[0].shape == (16, 64) and dW2.inputs[1].name == "H"   # dY^T [out][B], H [B][hid]
+    assert dH.inputs[1].name == "W2" and dH.outputs[0].dtype == "f32"
+    assert gb.inputs[1] is g.ops[0].attrs["pre"]
+    assert dW1.inputs[1].name == "X" and dW1.outputs[0].name == "grad_W1"
+
+
+def test_inference_graph_has_no_backward():
+    g = graph.w8a8_infer_graph(batch=8, widths=(64, 64, 32))
+    assert [op.kind for op in g.ops] == ["quantize", "w8a8", "quantize", "w8a8"]
+    assert [op.attrs.get("relu") for op in g.ops if op.kind == "w8a8"] == [True, False]
+
+
+def test_graph_rejects_bad_programs():
+    g = graph.Graph()
+    x = g.input("X", (4, 8), "bf16")
+    w = g.param("W", (6, 9), "bf16")
+    with pytest.raises(ValueError):
+        g.linear(x, w)
+    with pytest.raises(ValueError):
+        g.input("X", (1,), "f32")
+    y = g.linear(x, g.param("W2", (6, 8), "bf16"), out_dtype="f32")
+    with pytest.raises(ValueError):
+        g.backward(y)  # not a loss
+
+
+def _mlp_f64(x, w1, w2, t):
+    a = x @ w1.T
+    h = 0.5 * a * (1 + erf(a / np.sqrt(2)))
+    y = h @ w2.T
+    return np.mean((y - t) ** 2)
+
+
+def test_oracle_mlp_gradients_match_finite_differences():
+    """Small MLP: the oracle composite's dW1/dW2 (bf16 roundings included) against central
+    differences of the f64 loss; the tolerance covers the bf16 roundings of H, dY and dA."""
+    B, D, Hd, O = 16, 8, 12, 6
+    x = rng.f32_to_bf16(rng.normal(1, B * D)).reshape(B, D)
+    w1 = rng.f32_to_bf16(rng.uniform(2, Hd * D, -0.5, 0.5)).reshape(Hd, D)
+    w2 = rng.f32_to_bf16(rng.uniform(3, O * Hd, -0.5, 0.5)).reshape(O, Hd)
+    t = rng.normal(4, B * O).reshape(B, O)
+    r = oracle.mlp_train_step(x, w1, w2, t)
+    X, W1, W2 = (rng.bf16_to_f32(a).astype(np.float64) for a in (x, w1, w2))
+    T = t.astype(np.float64)
+    assert abs(r["loss"] - _mlp_f64(X, W1, W2, T)) <= 1e-2 * _mlp_f64(X, W1, W2, T)
+    eps = 1e-5
+    for name, W in (("dW1", W1), ("dW2", W2)):
+        fd = np.zeros_like(W)
+        for idx in np.ndindex(W.shape):
+            Wp, Wm = W.copy(), W.copy()
+            Wp[idx] += eps
+            Wm[idx] -= eps
+            if name == "dW1":
+                fd[idx] = (_mlp_f64(X, Wp, W2, T) - _mlp_f64(X, Wm, W2, T)) / (2 * eps)
+            else:
+                fd[idx] = (_mlp_f64(X, W1, Wp, T) - _mlp_f64(X, W1, Wm, T)) / (2 * eps)
+        got = r[name].astype(np.float64)
+        assert np.linalg.norm(got - fd) <= 2e-2 * np.linalg.norm(fd), name
+
+
+def test_oracle_w8a8_forward_rows_independent():
+    x = rng.f32_to_bf16(rng.normal(5, 6 * 64)).reshape(6, 64)
+    layers = [(rng.int_uniform(6, 64 * 64, -127, 127).astype(np.int8).reshape(64, 64), rng.uniform(7, 64, 0.005, 0.02)),
+              (rng.int_uniform(8, 32 * 64, -127, 127).astype(np.int8).reshape(32, 64), rng.uniform(9, 32, 0.005, 0.02))]
+    full = oracle.w8a8_forward(x, layers)
+    part = oracle.w8a8_forward(x[2:4], layers)
+    assert np.array_equal(full[2:4], part)

@@ -1,0 +1,151 @@
+// Autodiff building blocks of the MLP graph on gfx950: GELU backward and MSE forward+backward.
+//
+// No reference code (north-star op class: "compiler-generated backward").  Both kernels are
+// elementwise over [rows][cols] and also emit the transposed gradient, because the weight
+// gradients dW = G^T X need G K-contiguous along the batch: a 256-lane block reads a 64x64 tile
+// (coalesced), writes the row-major result directly and the transposed result through an LDS
+// tile (coalesced along the transposed rows), so the transpose costs no extra HBM pass.
+//
+// MSE: loss = mean((y - t)^2) as a deterministic two-stage reduction - each tile writes one f64
+// partial sum, then one block adds the partials in tile order - and dy = (y - t) * (2 / n) in
+// f32, rounded to bf16.
+
+#include "common.h"
+
+namespace vdsl {
+namespace {
+
+__device__ __forceinline__ float gelu_grad_f(float v) {
+  // d/dv [0.5 v (1 + erf(v / sqrt2))] = Phi(v) + v phi(v), with Phi(v) = 0.5 erfc(-v / sqrt2)
+  // (erfc keeps full relative accuracy where 1 + erf(.) would cancel, v < 0).
+  return 0.5f * erfcf(-v * 0.7071067811865476f) + v * expf(-0.5f * v * v) * 0.3989422804014327f;
+}
+
+__global__ __launch_bounds__(256) void gelu_bwd_kernel(const float* __restrict__ dh, const float* __restrict__ pre,
+                                                       uint16_t* __restrict__ da, uint16_t* __restrict__ da_t,
+                                                       int64_t rows, int64_t cols) {
+  __shared__ uint16_t tile[64][66];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+#pragma unroll 4
+  for (int p = 0; p < 16; ++p) {
+    const int64_t r = r0 + ty + 4 * p, c = c0 + tx;
+    if (r < rows && c < cols) {
+      const int64_t o = r * cols + c;
+      const uint16_t h = f32_to_bf16(dh[o] * gelu_grad_f(pre[o]));
+      da[o] = h;
+      tile[ty + 4 * p][tx] = h;
+    }
+  }
+  if (!da_t) return;  // uniform across the block
+  __syncthreads();
+#pragma unroll 4
+  for (int p = 0; p < 16; ++p) {
+    const int64_t c = c0 + ty + 4 * p, r = r0 + tx;
+    if (r < rows && c < cols) da_t[c * rows + r] = tile[tx][ty + 4 * p];
+  }
+}
+
+__global__ __launch_bounds__(256) void mse_tile_kernel(const float* __restrict__ y, const float* __restrict__ t,
+                                                       uint16_t* __restrict__ dy, uint16_t* __restrict__ dy_t,
+                                                       double* __restrict__ partials, int64_t rows, int64_t cols,
+                                                       float scale) {
+  __shared__ uint16_t tile[64][66];
+  __shared__ double wsum[4];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  double s = 0.0;
+#pragma unroll 4
+  for (int p = 0; p < 16; ++p) {
+    const int64_t r = r0 + ty + 4 * p, c = c0 + tx;
+    if (r < rows && c < cols) {
+      const int64_t o = r * cols + c;
+      const float d = y[o] - t[o];
+      s += static_cast<double>(d) * static_cast<double>(d);
+      const uint16_t h = f32_to_bf16(d * scale);
+      if (dy) dy[o] = h;
+      tile[ty + 4 * p][tx] = h;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+  if (tx == 0) wsum[ty] = s;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    partials[static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x] = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+  if (!dy_t) return;
+#pragma unroll 4
+  for (int p = 0; p < 16; ++p) {
+    const int64_t c = c0 + ty + 4 * p, r = r0 + tx;
+    if (r < rows && c < cols) dy_t[c * rows + r] = tile[tx][ty + 4 * p];
+  }
+}
+
+// One block: lane-strided f64 sums of the partials, then a fixed-order combine.
+__global__ __launch_bounds__(256) void mse_finish_kernel(const double* __restrict__ partials, int64_t n_partials,
+                                                         float* __restrict__ loss, double inv_n) {
+  __shared__ double wsum[4];
+  double s = 0.0;
+  for (int64_t i = threadIdx.x; i < n_partials; i += 256) s += partials[i];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+  if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) loss[0] = static_cast<float>((((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]) * inv_n);
+}
+
+int64_t tiles_of(int64_t rows, int64_t cols) { return ((rows + 63) / 64) * ((cols + 63) / 64); }
+
+}  // namespace
+}  // namespace vdsl
+
+using namespace vdsl;
+
+extern "C" int vdsl_op_gelu_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer dh, vdsl_buffer pre, vdsl_buffer da,
+                                vdsl_buffer da_t) {
+  VDSL_TRY(enter_queue(q));
+  if (rows < 0 || cols < 0) return fail(VDSL_ERR_INVALID_ARG, "negative shape");
+  const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols);
+  VDSL_TRY(check_buffer(q, dh, n * 4, "dh", false));
+  VDSL_TRY(check_buffer(q, pre, n * 4, "pre", false));
+  VDSL_TRY(check_buffer(q, da, n * 2, "da", true));
+  if (da_t) VDSL_TRY(check_buffer(q, da_t, n * 2, "da_t", true));
+  if (n == 0) return VDSL_OK;
+  const int64_t gx = (cols + 63) / 64, gy = (rows + 63) / 64;
+  if (gy > 65535 || gx > 0x7fffffff) return fail(VDSL_ERR_UNSUPPORTED, "gelu_bwd: tensor too large");
+  hipLaunchKernelGGL(gelu_bwd_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)), dim3(256), 0, q->stream,
+                     static_cast<const float*>(dh->ptr), static_cast<const float*>(pre->ptr), static_cast<uint16_t*>(da->ptr),
+                     da_t ? static_cast<uint16_t*>(da_t->ptr) : nullptr, rows, cols);
+  return check_launch("gelu_bwd_kernel");
+}
+
+extern "C" int64_t vdsl_mse_partials_count(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return 2 * tiles_of(rows, cols);  // one f64 (two f32 slots) per 64x64 tile
+}
+
+extern "C" int vdsl_op_mse_fwd_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer y, vdsl_buffer t, vdsl_buffer loss,
+                                   vdsl_buffer dy, vdsl_buffer dy_t, vdsl_buffer partials) {
+  VDSL_TRY(enter_queue(q));
+  if (rows <= 0 || cols <= 0) return fail(VDSL_ERR_INVALID_ARG, "MSE needs a non-empty tensor");
+  const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols);
+  VDSL_TRY(check_buffer(q, y, n * 4, "y", false));
+  VDSL_TRY(check_buffer(q, t, n * 4, "t", false));
+  VDSL_TRY(check_buffer(q, loss, 4, "loss", true));
+  if (dy) VDSL_TRY(check_buffer(q, dy, n * 2, "dy", true));
+  if (dy_t) VDSL_TRY(check_buffer(q, dy_t, n * 2, "dy_t", true));
+  const int64_t np = tiles_of(rows, cols);
+  VDSL_TRY(check_buffer(q, partials, static_cast<size_t>(np) * 8, "partials", true));
+  const int64_t gx = (cols + 63) / 64, gy = (rows + 63) / 64;
+  if (gy > 65535 || gx > 0x7fffffff) return fail(VDSL_ERR_UNSUPPORTED, "mse: tensor too large");
+  const float scale = 2.0f / static_cast<float>(n);
+  double* part = static_cast<double*>(partials->ptr);
+  hipLaunchKernelGGL(mse_tile_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)), dim3(256), 0, q->stream,
+                     static_cast<const float*>(y->ptr), static_cast<const float*>(t->ptr),
+                     dy ? static_cast<uint16_t*>(dy->ptr) : nullptr, dy_t ? static_cast<uint16_t*>(dy_t->ptr) : nullptr, part,
+                     rows, cols, scale);
+  VDSL_TRY(check_launch("mse_tile_kernel"));
+  hipLaunchKernelGGL(mse_finish_kernel, dim3(1), dim3(256), 0, q->stream, part, np, static_cast<float*>(loss->ptr),
+                     1.0 / static_cast<double>(n));
+  return check_launch("mse_finish_kernel");
+}

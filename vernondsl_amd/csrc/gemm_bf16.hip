@@ -33,7 +33,8 @@ namespace {
 
 constexpr int BM = 128, BN = 128, BK = 64, LDK = BK + 8;
 
-__device__ __forceinline__ float gelu_f(float v) { return 0.5f * v * (1.0f + erff(v * 0.7071067811865476f)); }
+// 0.5 v (1 + erf(v / sqrt2)) written as 0.5 v erfc(-v / sqrt2): no cancellation for v < 0.
+__device__ __forceinline__ float gelu_f(float v) { return 0.5f * v * erfcf(-v * 0.7071067811865476f); }
 
 __device__ __forceinline__ int remap_xcd(int b, int nb) {
   // Hardware dispatches block b to XCD b % 8.  Give the blocks of one XCD a contiguous range of

@@ -1,0 +1,92 @@
+// Layout ops: 2-D transpose (f32 / bf16) and f32 <-> bf16 conversion, on gfx950.
+//
+// No reference code.  The GEMMs of op class 4 consume K-contiguous operands; the transpose
+// re-lays a K-strided operand, and the execution graph uses it for weight transposes.
+//
+// Transpose mapping: a 256-lane block moves one 64x64 tile through LDS.  Reads are coalesced
+// along the source row, writes along the destination row; the tile's LDS rows are padded by one
+// element so the column-wise LDS reads of the write phase fall in different banks.
+
+#include "common.h"
+
+namespace vdsl {
+
+namespace {
+
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t rows,
+                                                        int64_t cols) {
+  __shared__ T tile[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+#pragma unroll
+  for (int p = 0; p < 16; ++p) {
+    const int64_t r = r0 + ty + 4 * p, c = c0 + tx;
+    if (r < rows && c < cols) tile[ty + 4 * p][tx] = src[r * cols + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < 16; ++p) {
+    const int64_t c = c0 + ty + 4 * p, r = r0 + tx;  // dst row c, column r
+    if (r < rows && c < cols) dst[c * rows + r] = tile[tx][ty + 4 * p];
+  }
+}
+
+__global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* __restrict__ s, uint16_t* __restrict__ d, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+    d[i] = f32_to_bf16(s[i]);
+}
+
+__global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __restrict__ s, float* __restrict__ d, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+    d[i] = bf16_to_f32(s[i]);
+}
+
+}  // namespace
+
+int launch_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int dtype, hipStream_t s) {
+  if (rows == 0 || cols == 0) return VDSL_OK;
+  const int64_t gx = (cols + 63) / 64, gy = (rows + 63) / 64;
+  if (gx > 0x7fffffff || gy > 65535) return fail(VDSL_ERR_UNSUPPORTED, "transpose: tensor too large");
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+  if (dtype == VDSL_F32)
+    hipLaunchKernelGGL(transpose_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(src), static_cast<float*>(dst), rows, cols);
+  else
+    hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), rows, cols);
+  return check_launch("transpose_kernel");
+}
+
+}  // namespace vdsl
+
+using namespace vdsl;
+
+extern "C" int vdsl_op_transpose(vdsl_queue q, int64_t rows, int64_t cols, int32_t dtype, vdsl_buffer src, vdsl_buffer dst) {
+  VDSL_TRY(enter_queue(q));
+  if (rows < 0 || cols < 0) return fail(VDSL_ERR_INVALID_ARG, "negative shape");
+  if (dtype != VDSL_F32 && dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "transpose dtype must be f32 or bf16");
+  const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols) * dtype_size(dtype);
+  VDSL_TRY(check_buffer(q, src, n, "src", false));
+  VDSL_TRY(check_buffer(q, dst, n, "dst", true));
+  if (src == dst && n) return fail(VDSL_ERR_INVALID_ARG, "in-place transpose is not supported");
+  return launch_transpose(src->ptr, dst->ptr, rows, cols, dtype, q->stream);
+}
+
+extern "C" int vdsl_op_cast(vdsl_queue q, int64_t n, int32_t src_dtype, vdsl_buffer src, int32_t dst_dtype, vdsl_buffer dst) {
+  VDSL_TRY(enter_queue(q));
+  if (n < 0) return fail(VDSL_ERR_INVALID_ARG, "negative element count");
+  const bool ok = (src_dtype == VDSL_F32 || src_dtype == VDSL_BF16) && (dst_dtype == VDSL_F32 || dst_dtype == VDSL_BF16);
+  if (!ok) return fail(VDSL_ERR_UNSUPPORTED, "cast supports f32 <-> bf16");
+  VDSL_TRY(check_buffer(q, src, static_cast<size_t>(n) * dtype_size(src_dtype), "src", false));
+  VDSL_TRY(check_buffer(q, dst, static_cast<size_t>(n) * dtype_size(dst_dtype), "dst", true));
+  if (n == 0) return VDSL_OK;
+  if (src_dtype == dst_dtype) return vdsl_buffer_copy(q, dst, 0, src, 0, static_cast<size_t>(n) * dtype_size(src_dtype));
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 16384) blocks = 16384;
+  if (src_dtype == VDSL_F32)
+    hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, q->stream,
+                       static_cast<const float*>(src->ptr), static_cast<uint16_t*>(dst->ptr), n);
+  else
+    hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, q->stream,
+                       static_cast<const uint16_t*>(src->ptr), static_cast<float*>(dst->ptr), n);
+  return check_launch("cast_kernel");
+}

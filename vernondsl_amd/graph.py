@@ -1,0 +1,299 @@
+"""Execution graph with reverse-mode autodiff, replayed as one hipGraph.
+
+The reference has no execution graph or autodiff (it has no runtime at all); this module is the
+front end the north star asks for: a program of tensor ops is built once, the autodiff pass
+appends the backward ops, every tensor gets a static device buffer, and the whole step is
+recorded on one queue and replayed as a single hipGraph (no host work or allocation per step).
+
+    g = Graph()
+    x = g.input("X", (2048, 4096), "bf16")
+    w1 = g.param("W1", (4096, 4096), "bf16")         # [out][in]
+    h = g.linear(x, w1, act="gelu")                  # bf16, GELU fused into the GEMM epilogue
+    y = g.linear(h, g.param("W2", (4096, 4096), "bf16"), out_dtype="f32")
+    loss = g.mse_loss(y, g.input("T", (2048, 4096), "f32"))
+    grads = g.backward(loss)                         # {param name: gradient Value (f32)}
+    exe = g.compile(dev)
+    exe.write(q, "X", x_host) ...; step = exe.capture(q); step.launch(q)
+
+Backward rules (y = act(x W^T), W stored [out][in]):
+    g    = dL/dy (+ its transpose g^T), bf16; for act = gelu: g = gelu_bwd(dL/dh, pre)
+    dW   = g^T x        -> vdsl_op_gemm_bf16(A = g^T [out][B], B = x [B][in], trans_b = 0)
+    dx   = g W          -> vdsl_op_gemm_bf16(A = g [B][out], B = W [out][in], trans_b = 0)
+    MSE: loss and dL/dy = 2 (y - t) / n (bf16, plus transpose) from one fused op.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+from . import _lib, kernels
+from .rhi import Device, Queue, Tensor
+
+
+@dataclass
+class Value:
+    name: str
+    shape: tuple
+    dtype: str
+    kind: str = "activation"   # input | param | activation | grad | scratch
+    producer: "Op | None" = None
+    requires_grad: bool = False
+
+
+@dataclass
+class Op:
+    kind: str
+    inputs: list
+    outputs: list
+    attrs: dict = field(default_factory=dict)
+
+
+class Graph:
+    def __init__(self):
+        self.values: dict[str, Value] = {}
+        self.ops: list[Op] = []
+        self._n = 0
+
+    # ---- construction -------------------------------------------------------------------------
+    def _value(self, name, shape, dtype, kind="activation", requires_grad=False) -> Value:
+        if name in self.values:
+            raise ValueError(f"duplicate tensor name {name!r}")
+        v = Value(name, tuple(int(s) for s in shape), dtype, kind, None, requires_grad)
+        self.values[name] = v
+        return v
+
+    def _fresh(self, base):
+        self._n += 1
+        return f"{base}#{self._n}"
+
+    def _op(self, kind, inputs, outputs, **attrs) -> Op:
+        op = Op(kind, list(inputs), list(outputs), attrs)
+        for o in outputs:
+            o.producer = op
+        self.ops.append(op)
+        return op
+
+    def input(self, name, shape, dtype) -> Value:
+        return self._value(name, shape, dtype, "input")
+
+    def param(self, name, shape, dtype, requires_grad=True) -> Value:
+        return self._value(name, shape, dtype, "param", requires_grad)
+
+    def linear(self, x: Value, w: Value, act: str = "none", out_dtype: str | None = None, name=None) -> Value:
+        """y = act(x W^T); x [B][in] bf16, W [out][in] bf16 (K-contiguous: the native MFMA layout)."""
+        if x.dtype != "bf16" or w.dtype != "bf16":
+            raise TypeError("linear takes bf16 activations and weights")
+        if x.shape[1] != w.shape[1]:
+            raise ValueError(f"linear: x {x.shape} and W {w.shape} disagree on the input width")
+        if act not in ("none", "gelu", "relu"):
+            raise ValueError(f"unknown activation {act!r}")
+        out_dtype = out_dtype or ("bf16" if act != "none" else "f32")
+        y = self._value(name or self._fresh("linear"), (x.shape[0], w.shape[0]), out_dtype,
+                        requires_grad=x.requires_grad or w.requires_grad)
+        pre = None
+        if act != "none":
+            pre = self._value(self._fresh("pre"), y.shape, "f32")  # kept for the backward pass
+        self._op("linear", [x, w], [y] + ([pre] if pre else []), act=act, pre=pre)
+        return y
+
+    def mse_loss(self, y: Value, t: Value, name="loss") -> Value:
+        if y.dtype != "f32" or t.dtype != "f32" or y.shape != t.shape:
+            raise TypeError("mse_loss takes two f32 tensors of one shape")
+        loss = self._value(name, (1,), "f32", requires_grad=y.requires_grad)
+        self._op("mse", [y, t], [loss])
+        return loss
+
+    def quant_linear(self, x: Value, wq: Value, w_scale: Value, relu: bool, out_dtype="bf16", name=None) -> Value:
+        """y = relu?(dequant(q(x) wq^T)): per-row dynamic int8 activations, int8 weights [out][in]
+        with per-output-channel f32 scales; int32 accumulation on MFMA."""
+        if wq.dtype != "i8" or w_scale.dtype != "f32":
+            raise TypeError("quant_linear takes int8 weights and f32 scales")
+        rows, k = x.shape
+        xq = self._value(self._fresh("xq"), (rows, k), "i8")
+        xs = self._value(self._fresh("xscale"), (rows,), "f32")
+        self._op("quantize", [x], [xq, xs])
+        y = self._value(name or self._fresh("qlinear"), (rows, wq.shape[0]), out_dtype)
+        self._op("w8a8", [xq, xs, wq, w_scale], [y], relu=bool(relu))
+        return y
+
+    # ---- autodiff --------------------------------------------------------------------------------
+    def backward(self, loss: Value) -> dict:
+        """Appends the backward ops of `loss` and returns {param name: f32 gradient Value}."""
+        if loss.producer is None or loss.producer.kind != "mse":
+            raise ValueError("backward() starts from an mse_loss value")
+        fwd_ops = list(self.ops)
+        # gradient of each activation: ("bf16", g, g_t) or ("f32", g)
+        grad: dict[str, tuple] = {}
+        y, _ = loss.producer.inputs
+        dy = self._value(self._fresh("d_" + y.name), y.shape, "bf16", "grad")
+        dy_t = self._value(self._fresh("dT_" + y.name), y.shape[::-1], "bf16", "grad")
+        part = self._value(self._fresh("mse_partials"), (max(1, kernels.mse_partials_count(*y.shape)),), "f32", "scratch")
+        loss.producer.outputs += [dy, dy_t, part]  # the forward MSE op also emits dL/dy
+        grad[y.name] = ("bf16", dy, dy_t)
+        param_grads = {}
+        for op in reversed(fwd_ops):
+            if op.kind == "mse":
+                continue
+            if op.kind != "linear":
+                raise NotImplementedError(f"no backward rule for {op.kind}")
+            y = op.outputs[0]
+            if y.name not in grad:
+                continue
+            x, w = op.inputs
+            g = grad[y.name]
+            act = op.attrs["act"]
+            if act == "gelu":
+                if g[0] != "f32":
+                    g = self._to_f32(g[1])
+                da = self._value(self._fresh("d_pre"), y.shape, "bf16", "grad")
+                da_t = self._value(self._fresh("dT_pre"), y.shape[::-1], "bf16", "grad")
+                self._op("gelu_bwd", [g[1], op.attrs["pre"]], [da, da_t])
+                gb, gt = da, da_t
+            elif act == "none":
+                if g[0] == "f32":
+                    gb, gt = self._to_bf16_pair(g[1])
+                else:
+                    gb, gt = g[1], g[2]
+            else:
+                raise NotImplementedError("backward through relu is not implemented (training graphs use gelu)")
+            if w.requires_grad:
+                dw = self._value("grad_" + w.name, w.shape, "f32", "grad")
+                # dW[out][in] = sum_b g[b][out] x[b][in]: A = g^T [out][B] (K = B contiguous), B = x [B][in]
+                self._op("gemm", [gt, x], [dw], trans_a=False, trans_b=False, epi=_lib.EPI_NONE)
+                param_grads[w.name] = dw
+            if x.requires_grad or (x.producer is not None and x.kind == "activation" and _needs(x, self)):
+                dx = self._value(self._fresh("d_" + x.name), x.shape, "f32", "grad")
+                # dx[B][in] = sum_o g[b][o] W[o][in]: A = g [B][out], B = W stored [out][in] = [K][N]
+                self._op("gemm", [gb, w], [dx], trans_a=False, trans_b=False, epi=_lib.EPI_NONE)
+                grad[x.name] = ("f32", dx)
+        return param_grads
+
+    def _to_f32(self, v: Value) -> Value:
+        o = self._value(self._fresh(v.name + "_f32"), v.shape, "f32", "grad")
+        self._op("cast", [v], [o])
+        return o
+
+    def _to_bf16_pair(self, v: Value):
+        b = self._value(self._fresh(v.name + "_bf16"), v.shape, "bf16", "grad")
+        bt = self._value(self._fresh(v.name + "_bf16T"), v.shape[::-1], "bf16", "grad")
+        self._op("cast", [v], [b])
+        self._op("transpose", [b], [bt])
+        return b, bt
+
+    # ---- compile ---------------------------------------------------------------------------------
+    def compile(self, dev: Device) -> "Executable":
+        return Executable(self, dev)
+
+
+def _needs(x: Value, g: Graph) -> bool:
+    """An activation needs a gradient if some parameter upstream of it requires one."""
+    seen, stack = set(), [x]
+    while stack:
+        v = stack.pop()
+        if v.name in seen:
+            continue
+        seen.add(v.name)
+        if v.kind == "param" and v.requires_grad:
+            return True
+        if v.producer is not None:
+            stack.extend(v.producer.inputs)
+    return False
+
+
+class Executable:
+    """Static buffers for every value, the op sequence bound to them, and hipGraph capture."""
+
+    def __init__(self, g: Graph, dev: Device):
+        self.graph = g
+        self.dev = dev
+        self.t: dict[str, Tensor] = {}
+        for v in g.values.values():
+            self.t[v.name] = Tensor(dev, v.shape, v.dtype)
+        ws = 0
+        for op in g.ops:
+            if op.kind == "gemm":
+                a, b = op.inputs
+                M, K = (a.shape[1], a.shape[0]) if op.attrs["trans_a"] else a.shape
+                N = b.shape[0] if op.attrs["trans_b"] else b.shape[1]
+                ws = max(ws, kernels.gemm_bf16_workspace_bytes(op.attrs["trans_a"], op.attrs["trans_b"], M, N, K))
+            if op.kind == "w8a8":
+                xq, _, wq, _ = op.inputs
+                ws = max(ws, kernels.gemm_w8a8_workspace_bytes(xq.shape[0], wq.shape[0], xq.shape[1]))
+        # One workspace shared by all ops: they run in order on one queue.
+        self.workspace = Tensor(dev, (max(ws, 4),), "i8") if ws else None
+
+    def write(self, q: Queue, name: str, host):
+        self.t[name].buffer.write(q, host)
+
+    def read(self, q: Queue, name: str):
+        return self.t[name].numpy(q)
+
+    def run(self, q: Queue):
+        """Enqueues every op of the graph, in order, on q."""
+        T = self.t
+        for op in self.graph.ops:
+            ins = [T[v.name] for v in op.inputs]
+            outs = [T[v.name] for v in op.outputs]
+            if op.kind == "linear":
+                pre = T[op.attrs["pre"].name] if op.attrs["pre"] is not None else None
+                epi = {"none": _lib.EPI_NONE, "gelu": _lib.EPI_GELU, "relu": _lib.EPI_RELU}[op.attrs["act"]]
+                kernels.gemm_bf16(q, ins[0], ins[1], outs[0], trans_a=False, trans_b=True, epilogue=epi, pre_act=pre)
+            elif op.kind == "gemm":
+                kernels.gemm_bf16(q, ins[0], ins[1], outs[0], op.attrs["trans_a"], op.attrs["trans_b"], op.attrs["epi"],
+                                  None, self.workspace)
+            elif op.kind == "mse":
+                loss = outs[0]
+                if len(outs) == 4:
+                    kernels.mse_fwd_bwd(q, ins[0], ins[1], loss, outs[1], outs[2], outs[3])
+                else:
+                    raise RuntimeError("mse without backward: call Graph.backward() or use the loss op's fused form")
+            elif op.kind == "gelu_bwd":
+                kernels.gelu_bwd(q, ins[0], ins[1], outs[0], outs[1])
+            elif op.kind == "cast":
+                kernels.cast(q, ins[0], outs[0])
+            elif op.kind == "transpose":
+                kernels.transpose(q, ins[0], outs[0])
+            elif op.kind == "quantize":
+                kernels.quantize_rows_i8(q, ins[0], outs[0], outs[1])
+            elif op.kind == "w8a8":
+                kernels.gemm_w8a8(q, ins[0], ins[1], ins[2], ins[3], outs[0], op.attrs["relu"], None, self.workspace)
+            else:
+                raise NotImplementedError(op.kind)
+
+    def capture(self, q: Queue):
+        """Records one run() into a hipGraph and returns it (rhi.Graph: .launch(q), .destroy())."""
+        with q.capture() as rec:
+            self.run(q)
+        return rec.graph
+
+    def free(self):
+        for t in self.t.values():
+            t.free()
+        if self.workspace is not None:
+            self.workspace.free()
+
+
+# ---- the two workload graphs ------------------------------------------------------------------------
+def mlp_train_graph(batch=2048, d_in=4096, hidden=4096, d_out=4096):
+    """Config 4: X -> GELU(X W1^T) -> (.) W2^T -> MSE(., T), with backward for W1 and W2."""
+    g = Graph()
+    x = g.input("X", (batch, d_in), "bf16")
+    w1 = g.param("W1", (hidden, d_in), "bf16")
+    w2 = g.param("W2", (d_out, hidden), "bf16")
+    t = g.input("T", (batch, d_out), "f32")
+    h = g.linear(x, w1, act="gelu", name="H")
+    y = g.linear(h, w2, out_dtype="f32", name="Y")
+    loss = g.mse_loss(y, t)
+    grads = g.backward(loss)
+    return g, grads
+
+
+def w8a8_infer_graph(batch=512, widths=(8192, 8192, 8192, 8192, 1024)):
+    """Config 5: int8 MLP, ReLU between layers, bf16 activations."""
+    g = Graph()
+    h = g.input("X", (batch, widths[0]), "bf16")
+    for li in range(len(widths) - 1):
+        wq = g.param(f"W{li}", (widths[li + 1], widths[li]), "i8", requires_grad=False)
+        ws = g.param(f"S{li}", (widths[li + 1],), "f32", requires_grad=False)
+        last = li == len(widths) - 2
+        h = g.quant_linear(h, wq, ws, relu=not last, name="Y" if last else f"H{li}")
+    return g
