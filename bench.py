@@ -198,6 +198,8 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
         step.launch(q)
     e1.record(q)
     ms = e0.elapsed_ms(e1) / n
+    e0.destroy()
+    e1.destroy()
     flops = spec.mlp_flops(B, D, Hd, O)
     tflops = flops / (ms * 1e-3) / 1e12
     loss = float(exe.read(q, "loss")[0])
@@ -253,6 +255,8 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
         step.launch(q)
     e1.record(q)
     ms = e0.elapsed_ms(e1) / n
+    e0.destroy()
+    e1.destroy()
     ops = spec.w8a8_ops(B, widths)
     tops = ops / (ms * 1e-3) / 1e12
     got = exe.read(q, "Y")
