@@ -290,6 +290,55 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
     return res
 
 
+# ---- single-kernel mode (for rocprofv3 counter passes) ---------------------------------------------
+def run_kernel_only(dev, q, name, reps):
+    """Runs one kernel `reps` times on the config's shape and nothing else (no parity, no CPU):
+    the program a `rocprofv3 --pmc` pass profiles.  `copy` is a 512 MiB device-to-device copy
+    (known traffic: 512 MiB read + 512 MiB written) used to calibrate FETCH_SIZE / WRITE_SIZE."""
+    from vernondsl_amd import _lib, kernels, mapchain as mc, spec
+    from vernondsl_amd.rhi import Tensor
+    ts = []
+    if name == "map_chain":
+        x, bias = spec.map_chain_inputs(8192, 8192)
+        tx, tb, ty = Tensor.from_numpy(dev, q, x), Tensor.from_numpy(dev, q, bias), Tensor(dev, (8192, 8192), "f32")
+        prog = mc.compile(spec.map_chain_expr())
+        fn, ts = (lambda: kernels.map_chain(q, prog, [tx, tb], ty)), [tx, tb, ty]
+    elif name in ("softmax_f32", "softmax_bf16"):
+        dt = name.split("_")[1]
+        tx = Tensor(dev, (16384, 4096), dt)
+        tx.buffer.fill_u32(q, 0x3F803F80)
+        outs = [Tensor(dev, (16384,), "f32"), Tensor(dev, (16384,), "f32"), Tensor(dev, (16384, 4096), dt)]
+        fn, ts = (lambda: kernels.row_reduce_softmax(q, tx, *outs)), [tx] + outs
+    elif name == "gemm_bf16":
+        A, B = Tensor(dev, (2048, 4096), "bf16"), Tensor(dev, (4096, 4096), "bf16")
+        H, P = Tensor(dev, (2048, 4096), "bf16"), Tensor(dev, (2048, 4096), "f32")
+        A.buffer.fill_u32(q, 0x3F803F80)
+        B.buffer.fill_u32(q, 0x3C003C00)
+        fn, ts = (lambda: kernels.gemm_bf16(q, A, B, H, False, True, _lib.EPI_GELU, P)), [A, B, H, P]
+    elif name == "gemm_w8a8":
+        A, B = Tensor(dev, (512, 8192), "i8"), Tensor(dev, (8192, 8192), "i8")
+        xs, ws, Y = Tensor(dev, (512,), "f32"), Tensor(dev, (8192,), "f32"), Tensor(dev, (512, 8192), "bf16")
+        for t_ in (A, B, xs, ws):
+            t_.buffer.fill_u32(q, 0x01010101)
+        fn, ts = (lambda: kernels.gemm_w8a8(q, A, xs, B, ws, Y, True)), [A, B, xs, ws, Y]
+    elif name == "escape_time":
+        p = kernels.escape_time_params(**spec.mandelbrot_params())
+        out = Tensor(dev, (1024, 1024), "i32")
+        fn, ts = (lambda: kernels.escape_time(q, p, out)), [out]
+    elif name == "copy":
+        n = 512 << 20
+        a, b = Tensor(dev, (n,), "i8"), Tensor(dev, (n,), "i8")
+        fn, ts = (lambda: _lib.call("vdsl_buffer_copy", q.handle, b.handle, 0, a.handle, 0, n)), [a, b]
+    else:
+        raise SystemExit(f"unknown kernel {name!r}")
+    for _ in range(reps):
+        fn()
+    q.sync()
+    for t_ in ts:
+        t_.free()
+    print(json.dumps({"kernel": name, "reps": reps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -297,6 +346,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline timings")
     ap.add_argument("--only", type=int, default=0, help="run only the headline (2) or one extra config")
+    ap.add_argument("--kernel", default="", help="run one kernel --reps times and exit (for rocprofv3 --pmc): "
+                    "map_chain, softmax_f32, softmax_bf16, gemm_bf16, gemm_w8a8, escape_time, copy")
+    ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -309,6 +361,11 @@ def main():
     from vernondsl_amd.rhi import Device, Queue
     dev = Device(0)
     q = Queue(dev)
+    if args.kernel:
+        run_kernel_only(dev, q, args.kernel, args.reps)
+        q.destroy()
+        dev.close()
+        return
     info = dev.info()
     log("bench: device", info)
     do_cpu = not args.no_cpu

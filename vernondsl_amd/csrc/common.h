@@ -93,12 +93,17 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// Round-to-nearest-even f32 -> bf16; NaN maps to the canonical quiet NaN 0x7FC0.
+// Round-to-nearest-even f32 -> bf16 with gfx950's v_cvt_pk_bf16_f32 (identical to the
+// bit-level RNE of the CPU oracle for every non-NaN input; a NaN stays a quiet NaN).
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+// Two values converted by one v_cvt_pk_bf16_f32: lo in bits 0-15, hi in bits 16-31.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 // Butterfly reductions across one 64-lane wavefront (every lane gets the result).

@@ -6,31 +6,36 @@
 //   GEMM:     acc = sum_k xq[m][k] * w[n][k] in int32 (exact: |acc| <= K * 127 * 127 < 2^31
 //             for K < 133,000), y = relu?((float(acc) * xs[m]) * ws[n]), RNE to bf16.
 //
-// Tiling mirrors the bf16 kernel byte for byte: a 256-lane block computes a 128x128 tile; K
-// advances 128 int8 (128 bytes) per LDS tile, so A/B tiles are [128][128+16] bytes.  Each wave
-// owns 64x64 as 2x2 v_mfma_i32_32x32x32_i8 accumulators; lane l supplies A[row = l%32][k =
-// 16*(l/32) .. +15] (one 16-byte fragment) and B likewise; accumulator element r of lane l is
-// C[8*(r/4) + 4*(l/32) + r%4][l%32].
+// The main loop is gemm_mfma.h's, shared byte for byte with the bf16 GEMM: the
+// v_mfma_i32_32x32x32_i8 fragment is 16 int8 per lane (A[row = l%32][k = 16*(l/32) .. +15]) and
+// the accumulator layout is the f32 one.  This file adds the dequant epilogue and the split-K path.
 //
 // Narrow outputs (too few tiles to fill 256 CUs, e.g. the 1024-wide last layer at batch 512)
 // split K across blocks: each block adds its int32 partial tile into a zeroed int32 workspace
 // with atomics - integer addition is exact and order-independent, so the result is still
 // deterministic - and a second kernel applies the dequant epilogue.
 
-#include "common.h"
+#include "gemm_mfma.h"
 
 namespace vdsl {
 namespace {
 
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef int i32x16 __attribute__((ext_vector_type(16)));
-
-constexpr int BM = 128, BN = 128, BKB = 128, LDB = BKB + 16;  // BKB: K bytes per tile
-
-__device__ __forceinline__ int remap_xcd(int b, int nb) {
-  if (nb % 8) return b;
-  return (b % 8) * (nb / 8) + (b / 8);
-}
+// Tile configurations (block M x N, K bytes per stage, wave grid); K bytes = K int8 elements.
+using I0 = GemmConfig<MfmaI8, 128, 128, 128, 2, 2>;
+using I1 = GemmConfig<MfmaI8, 256, 128, 128, 2, 2>;
+using I2 = GemmConfig<MfmaI8, 128, 256, 128, 2, 2>;
+using I3 = GemmConfig<MfmaI8, 256, 256, 128, 2, 2>;
+using I4 = GemmConfig<MfmaI8, 256, 256, 128, 2, 4>;
+using I5 = GemmConfig<MfmaI8, 256, 128, 128, 4, 2>;
+using I6 = GemmConfig<MfmaI8, 128, 128, 256, 2, 2>;
+using I7 = GemmConfig<MfmaI8, 128, 64, 128, 2, 2>;   // wave tile 64x32: twice the blocks of 128x128
+using I8 = GemmConfig<MfmaI8, 64, 128, 128, 2, 2>;   // wave tile 32x64
+using I9 = GemmConfig<MfmaI8, 128, 128, 64, 2, 2>;   // 64 K bytes per stage: 3 blocks per CU fit in LDS
+using I10 = GemmConfig<MfmaI8, 256, 128, 64, 2, 2>;  // wave tile 128x64, 2 blocks per CU
+using I11 = GemmConfig<MfmaI8, 128, 256, 64, 2, 2>;  // wave tile 64x128, 2 blocks per CU
+using I12 = GemmConfig<MfmaI8, 256, 256, 64, 2, 4>;  // 8 waves, wave tile 128x64
+using I13 = GemmConfig<MfmaI8, 256, 128, 64, 4, 2>;  // 8 waves, wave tile 64x64, 2 blocks per CU
+constexpr int kNumConfigs = 14;
 
 __device__ __forceinline__ void store_y(void* y, int out_dtype, size_t o, float v) {
   if (out_dtype == VDSL_F32) static_cast<float*>(y)[o] = v;
@@ -44,102 +49,30 @@ __device__ __forceinline__ float dequant(int32_t acc, float xs, float ws, int re
   return v;
 }
 
-// SPLIT: this block covers K range [kz*k_per, (kz+1)*k_per) and adds into ws_acc.
-template <bool SPLIT>
-__global__ __launch_bounds__(256, 2) void gemm_w8a8_nt(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
-                                                       const float* __restrict__ xs, const float* __restrict__ wsc,
-                                                       void* __restrict__ y, int out_dtype, int relu,
-                                                       int32_t* __restrict__ acc_out, int32_t* __restrict__ ws_acc, int M,
-                                                       int N, int K, int k_per) {
-  __shared__ __attribute__((aligned(16))) int8_t As[BM * LDB];
-  __shared__ __attribute__((aligned(16))) int8_t Bs[BN * LDB];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  const int t = remap_xcd(blockIdx.x, gridDim.x);
-  constexpr int G = 8;
-  const int group = t / (G * tiles_n);
-  const int first_m = group * G;
-  const int gsize = min(G, tiles_m - first_m);
-  const int in_group = t - group * G * tiles_n;
-  const int tile_m = first_m + in_group % gsize;
-  const int tile_n = in_group / gsize;
-  const int m0 = tile_m * BM, n0 = tile_n * BN;
+// SPLIT: block (x, z) covers K range [z*k_per, (z+1)*k_per) and adds its int32 tile into ws_acc.
+template <class Cfg, bool SPLIT, bool EDGE>
+__global__ __launch_bounds__(Cfg::NT, 2) void gemm_w8a8_nt(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
+                                                        const float* __restrict__ xs, const float* __restrict__ wsc,
+                                                        void* __restrict__ y, int out_dtype, int relu,
+                                                        int32_t* __restrict__ acc_out, int32_t* __restrict__ ws_acc, int M,
+                                                        int N, int K, int k_per) {
+  __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS_BYTES];
+  const int tiles_m = (M + Cfg::BM - 1) / Cfg::BM, tiles_n = (N + Cfg::BN - 1) / Cfg::BN;
+  int tm, tn;
+  tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * Cfg::BM, n0 = tn * Cfg::BN;
   const int k_begin = SPLIT ? blockIdx.y * k_per : 0;
   const int k_end = SPLIT ? min(K, k_begin + k_per) : K;
-
-  i32x16 acc[2][2];
+  i32x16 acc[Cfg::FM][Cfg::FN];
+  gemm_mainloop<MfmaI8, Cfg, EDGE>(reinterpret_cast<const char*>(A), reinterpret_cast<const char*>(B), M, N, K, k_begin, k_end,
+                             m0, n0, smem, acc);
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < Cfg::FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-
-  uint4 ra[4], rb[4];
-  auto load_tiles = [&](int kb) {  // kb: first K index of the tile
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c >> 3;
-      const int k = kb + (c & 7) * 16;
-      const int gm = m0 + row, gn = n0 + row;
-      ra[i] = (gm < M && k < k_end) ? *reinterpret_cast<const uint4*>(A + static_cast<size_t>(gm) * K + k) : make_uint4(0, 0, 0, 0);
-      rb[i] = (gn < N && k < k_end) ? *reinterpret_cast<const uint4*>(B + static_cast<size_t>(gn) * K + k) : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto store_tiles = [&]() {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c >> 3;
-      const int kc = (c & 7) * 16;
-      *reinterpret_cast<uint4*>(&As[row * LDB + kc]) = ra[i];
-      *reinterpret_cast<uint4*>(&Bs[row * LDB + kc]) = rb[i];
-    }
-  };
-
-  const int nk = (k_end - k_begin + BKB - 1) / BKB;
-  if (nk > 0) {
-    load_tiles(k_begin);
-    store_tiles();
-  }
-  __syncthreads();
-  const int frag_row = lane & 31;
-  const int frag_k = (lane >> 5) * 16;
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) load_tiles(k_begin + (kt + 1) * BKB);
-#pragma unroll
-    for (int kk = 0; kk < BKB; kk += 32) {
-      i32x4 a[2], b[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        a[i] = *reinterpret_cast<const i32x4*>(&As[(wm * 64 + i * 32 + frag_row) * LDB + kk + frag_k]);
-        b[i] = *reinterpret_cast<const i32x4*>(&Bs[(wn * 64 + i * 32 + frag_row) * LDB + kk + frag_k]);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
-    __syncthreads();
-    if (kt + 1 < nk) {
-      store_tiles();
-      __syncthreads();
-    }
-  }
-
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < Cfg::FN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+        const int row = acc_row<Cfg>(m0, i, r), col = acc_col<Cfg>(n0, j);
         if (row < M && col < N) {
           const size_t o = static_cast<size_t>(row) * N + col;
           const int32_t a = acc[i][j][r];
@@ -165,7 +98,65 @@ __global__ __launch_bounds__(256) void w8a8_epilogue(const int32_t* __restrict__
   }
 }
 
-// One wave per row: pass 1 finds max|x|, pass 2 quantises.
+// One 256-lane block per row; 16-byte vectors (PV elements) per lane; pass 1 finds max|x| (lane
+// max, wave butterfly, 4-wave combine in LDS), pass 2 re-reads the row (from L2) and quantises.
+template <int DT>
+__global__ __launch_bounds__(256) void quantize_rows_vec(const void* __restrict__ x, int8_t* __restrict__ q,
+                                                         float* __restrict__ scale, int64_t cols) {
+  constexpr int PV = DT == VDSL_F32 ? 4 : 8;
+  __shared__ float wmax[4];
+  const int64_t row = blockIdx.x;
+  const int64_t nvec = cols / PV;
+  const uint4* src = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + row * cols * (DT == VDSL_F32 ? 4 : 2));
+  auto unpack = [](const uint4& v, float (&o)[PV]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    if (DT == VDSL_F32) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o[k] = __uint_as_float(w[k]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        o[2 * k] = __uint_as_float(w[k] << 16);
+        o[2 * k + 1] = __uint_as_float(w[k] & 0xFFFF0000u);
+      }
+    }
+  };
+  float amax = 0.0f;
+  for (int64_t v = threadIdx.x; v < nvec; v += 256) {
+    float e[PV];
+    unpack(src[v], e);
+#pragma unroll
+    for (int k = 0; k < PV; ++k) amax = fmaxf(amax, fabsf(e[k]));
+  }
+  amax = wave_max(amax);
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float s = amax / 127.0f;
+  if (threadIdx.x == 0) scale[row] = s;
+  int8_t* dst = q + row * cols;
+  for (int64_t v = threadIdx.x; v < nvec; v += 256) {
+    float e[PV];
+    unpack(src[v], e);
+    uint32_t packed[PV / 4];
+#pragma unroll
+    for (int w = 0; w < PV / 4; ++w) packed[w] = 0;
+#pragma unroll
+    for (int k = 0; k < PV; ++k) {
+      int iv = 0;
+      if (s > 0.0f) {
+        float t = rintf(e[k] / s);
+        t = fminf(fmaxf(t, -127.0f), 127.0f);
+        iv = static_cast<int>(t);
+      }
+      packed[k / 4] |= (static_cast<uint32_t>(iv) & 0xFFu) << (8 * (k % 4));
+    }
+    if (PV == 4) *reinterpret_cast<uint32_t*>(dst + v * PV) = packed[0];
+    else *reinterpret_cast<uint2*>(dst + v * PV) = make_uint2(packed[0], packed[PV / 4 - 1]);
+  }
+}
+
+// Any width: one wave per row, element at a time, same arithmetic.
 template <int DT>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restrict__ x, int8_t* __restrict__ q,
                                                             float* __restrict__ scale, int64_t rows, int64_t cols) {
@@ -193,13 +184,79 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restri
   }
 }
 
+int64_t tiles_for(int bm, int bn, int64_t M, int64_t N) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
+
+// Measured on MI355X over every configuration above (config-5 shapes 512x8192x8192 and the split-K
+// 512x1024x8192): 128x64 tiles (twice the blocks of 128x128 at batch 512) are fastest.
+int choose_config(int64_t M, int64_t N) {
+  const int o = gemm_config_override();
+  if (o >= 0 && o < kNumConfigs) return o;
+  (void)M;
+  (void)N;
+  return 7;
+}
+
+void config_tile(int c, int& bm, int& bn) {
+  static const int t[kNumConfigs][2] = {{128, 128}, {256, 128}, {128, 256}, {256, 256}, {256, 256},
+                                          {256, 128}, {128, 128}, {128, 64},  {64, 128},  {128, 128},
+                                          {256, 128}, {128, 256}, {256, 256}, {256, 128}};
+  bm = t[c][0];
+  bn = t[c][1];
+}
+
+// K splits for outputs with too few tiles to fill the 256 CUs (the split-K path).
 int split_of(int64_t M, int64_t N, int64_t K) {
-  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  if (tiles >= 128 || K < 2 * BKB) return 1;
+  int bm, bn;
+  config_tile(choose_config(M, N), bm, bn);
+  const int64_t tiles = tiles_for(bm, bn, M, N);
+  if (tiles >= 128 || K < 256) return 1;
   int64_t s = 256 / tiles;
-  const int64_t kt = (K + BKB - 1) / BKB;
+  const int64_t kt = (K + 127) / 128;
   if (s > kt) s = kt;
   return static_cast<int>(s < 1 ? 1 : s);
+}
+
+template <class Cfg>
+int launch_cfg(const int8_t* a, const int8_t* b, const float* xs, const float* wsc, void* y, int out_dtype, int relu,
+               int32_t* ao, int32_t* wacc, int m, int n, int k, int split, hipStream_t s) {
+  const int64_t tiles = tiles_for(Cfg::BM, Cfg::BN, m, n);
+  if (split == 1) {
+    if (gemm_needs_edge<Cfg>(m, n, k))
+      hipLaunchKernelGGL((gemm_w8a8_nt<Cfg, false, true>), dim3(static_cast<unsigned>(tiles), 1), dim3(Cfg::NT), 0, s, a, b, xs,
+                         wsc, y, out_dtype, relu, ao, nullptr, m, n, k, k);
+    else
+      hipLaunchKernelGGL((gemm_w8a8_nt<Cfg, false, false>), dim3(static_cast<unsigned>(tiles), 1), dim3(Cfg::NT), 0, s, a, b, xs,
+                         wsc, y, out_dtype, relu, ao, nullptr, m, n, k, k);
+    return check_launch("gemm_w8a8_nt");
+  }
+  // k_per: a multiple of the K stage so every split starts on a stage boundary
+  const int kt = (k + Cfg::BKB - 1) / Cfg::BKB;
+  const int k_per = ((kt + split - 1) / split) * Cfg::BKB;
+  const int nsplit = (k + k_per - 1) / k_per;
+  // the last split may be shorter than k_per: it takes the edge path
+  hipLaunchKernelGGL((gemm_w8a8_nt<Cfg, true, true>), dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(nsplit)), dim3(Cfg::NT),
+                     0, s, a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, k_per);
+  return check_launch("gemm_w8a8_nt<split>");
+}
+
+int launch_w8a8(const int8_t* a, const int8_t* b, const float* xs, const float* wsc, void* y, int out_dtype, int relu,
+                int32_t* ao, int32_t* wacc, int m, int n, int k, int split, hipStream_t s) {
+  switch (choose_config(m, n)) {
+    case 1: return launch_cfg<I1>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 2: return launch_cfg<I2>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 3: return launch_cfg<I3>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 4: return launch_cfg<I4>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 5: return launch_cfg<I5>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 6: return launch_cfg<I6>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 7: return launch_cfg<I7>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 8: return launch_cfg<I8>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 9: return launch_cfg<I9>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 10: return launch_cfg<I10>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 11: return launch_cfg<I11>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 12: return launch_cfg<I12>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 13: return launch_cfg<I13>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    default: return launch_cfg<I0>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+  }
 }
 
 }  // namespace
@@ -217,6 +274,16 @@ extern "C" int vdsl_op_quantize_rows_i8(vdsl_queue q, int64_t rows, int64_t cols
   VDSL_TRY(check_buffer(q, qx, n, "qx", true));
   VDSL_TRY(check_buffer(q, scale, static_cast<size_t>(rows) * 4, "scale", true));
   if (rows == 0) return VDSL_OK;
+  const int pv = x_dtype == VDSL_F32 ? 4 : 8;
+  if (cols % pv == 0 && rows <= 0x7fffffff) {  // rows of whole 16-byte vectors (hipMalloc bases are aligned)
+    if (x_dtype == VDSL_F32)
+      hipLaunchKernelGGL(quantize_rows_vec<VDSL_F32>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, q->stream, x->ptr,
+                         static_cast<int8_t*>(qx->ptr), static_cast<float*>(scale->ptr), cols);
+    else
+      hipLaunchKernelGGL(quantize_rows_vec<VDSL_BF16>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, q->stream, x->ptr,
+                         static_cast<int8_t*>(qx->ptr), static_cast<float*>(scale->ptr), cols);
+    return check_launch("quantize_rows_vec");
+  }
   const int64_t blocks = (rows + 3) / 4;
   if (x_dtype == VDSL_F32)
     hipLaunchKernelGGL(quantize_rows_kernel<VDSL_F32>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, q->stream, x->ptr,
@@ -252,26 +319,15 @@ extern "C" int vdsl_op_gemm_w8a8(vdsl_queue q, int64_t M, int64_t N, int64_t K, 
   if (split > 1) VDSL_TRY(check_buffer(q, workspace, static_cast<size_t>(M) * N * 4, "workspace", true));
   if (M == 0 || N == 0) return VDSL_OK;
   const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
-  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   int32_t* ao = acc_out ? static_cast<int32_t*>(acc_out->ptr) : nullptr;
   const auto* a = static_cast<const int8_t*>(xq->ptr);
   const auto* b = static_cast<const int8_t*>(w->ptr);
   const auto* xs = static_cast<const float*>(x_scale->ptr);
   const auto* wsc = static_cast<const float*>(w_scale->ptr);
-  if (split == 1) {
-    hipLaunchKernelGGL(gemm_w8a8_nt<false>, dim3(static_cast<unsigned>(tiles), 1), dim3(256), 0, q->stream, a, b, xs, wsc,
-                       y->ptr, out_dtype, relu, ao, nullptr, m, n, k, k);
-    return check_launch("gemm_w8a8_nt");
-  }
-  // k_per: a multiple of the K tile so every split starts on a tile boundary
-  const int kt = (k + BKB - 1) / BKB;
-  const int k_per = ((kt + split - 1) / split) * BKB;
-  const int nsplit = (k + k_per - 1) / k_per;
+  if (split == 1) return launch_w8a8(a, b, xs, wsc, y->ptr, out_dtype, relu, ao, nullptr, m, n, k, 1, q->stream);
   VDSL_TRY(vdsl_buffer_fill_u32(q, workspace, 0, static_cast<size_t>(M) * N * 4, 0u));
   int32_t* wacc = static_cast<int32_t*>(workspace->ptr);
-  hipLaunchKernelGGL(gemm_w8a8_nt<true>, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(nsplit)), dim3(256), 0,
-                     q->stream, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, wacc, m, n, k, k_per);
-  VDSL_TRY(check_launch("gemm_w8a8_nt<split>"));
+  VDSL_TRY(launch_w8a8(a, b, xs, wsc, y->ptr, out_dtype, relu, ao, wacc, m, n, k, split, q->stream));
   int64_t blocks = (static_cast<int64_t>(M) * N + 255) / 256;
   if (blocks > 8192) blocks = 8192;
   hipLaunchKernelGGL(w8a8_epilogue, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, q->stream, wacc, xs, wsc, y->ptr,

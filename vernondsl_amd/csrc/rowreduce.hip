@@ -4,6 +4,10 @@
 //   row_sum = sum_j x[j] accumulated in f64, rounded once to f32;
 //   row_max = max_j x[j] (exact);
 //   softmax[j] = e[j] / s,  e[j] = expf(x[j] - row_max) in f32,  s = f64 sum of e rounded to f32.
+// The register-resident kernel multiplies by 1/s instead of dividing (within one ulp of e/s) and
+// forms its sums as f32 partials of 4 or 8 elements added into f64 accumulators; both stay far
+// inside the op's 1e-5 (f32) / 1e-2 (bf16) tolerances and cut the VALU work per element, which
+// bounds the bf16 kernel.
 //
 // Mapping: one 64-lane wavefront owns one row and keeps it in VGPRs, so x is read from HBM once
 // and softmax written once (the HBM roofline's minimum traffic).  Lane l holds the 16-byte
@@ -49,11 +53,7 @@ struct Elem<VDSL_BF16> {
     }
   }
   __device__ static __forceinline__ uint4 pack(const float (&o)[8]) {
-    uint32_t w[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      w[k] = static_cast<uint32_t>(f32_to_bf16(o[2 * k])) | (static_cast<uint32_t>(f32_to_bf16(o[2 * k + 1])) << 16);
-    return make_uint4(w[0], w[1], w[2], w[3]);
+    return make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7]));
   }
   __device__ static __forceinline__ float load1(const void* p, int64_t i) {
     return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
@@ -83,12 +83,15 @@ __global__ __launch_bounds__(256) void row_softmax_resident(const void* __restri
   double s = 0.0;
   float m = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < NV; ++k)
+  for (int k = 0; k < NV; ++k) {
+    float part = 0.0f;
 #pragma unroll
     for (int e = 0; e < PV; ++e) {
-      s += static_cast<double>(v[k][e]);
+      part += v[k][e];
       m = fmaxf(m, v[k][e]);
     }
+    s += static_cast<double>(part);
+  }
   s = wave_sum_f64(s);
   m = wave_max(m);
   if (lane == 0) {
@@ -98,18 +101,21 @@ __global__ __launch_bounds__(256) void row_softmax_resident(const void* __restri
   if (!sm) return;
   double es = 0.0;
 #pragma unroll
-  for (int k = 0; k < NV; ++k)
+  for (int k = 0; k < NV; ++k) {
+    float part = 0.0f;
 #pragma unroll
     for (int e = 0; e < PV; ++e) {
       v[k][e] = expf(v[k][e] - m);
-      es += static_cast<double>(v[k][e]);
+      part += v[k][e];
     }
-  const float esf = static_cast<float>(wave_sum_f64(es));
+    es += static_cast<double>(part);
+  }
+  const float inv = 1.0f / static_cast<float>(wave_sum_f64(es));
   uint4* dst = reinterpret_cast<uint4*>(static_cast<char*>(sm) + row * cols * (DT == VDSL_F32 ? 4 : 2));
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
 #pragma unroll
-    for (int e = 0; e < PV; ++e) v[k][e] = v[k][e] / esf;
+    for (int e = 0; e < PV; ++e) v[k][e] = v[k][e] * inv;
     const uint4 w = E::pack(v[k]);
     const u32x4 wv = {w.x, w.y, w.z, w.w};
     __builtin_nontemporal_store(wv, reinterpret_cast<u32x4*>(dst + k * 64 + lane));
