@@ -33,6 +33,17 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    (profiles/traffic.json, written from the counter runs described in profiles/traffic_counters.md,
+    each counter scaled by what it reads for a 512 MiB copy); None if not measured."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            return json.load(f)["kernels"][kernel]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def time_replays(q, dev, fn, steps, warmup, per_graph=1):
     """Records `per_graph` consecutive calls of fn() into one hipGraph, replays it `warmup` then
     `steps` times; returns (ms per call from HIP events on q's stream, wall ms per call)."""
@@ -163,7 +174,8 @@ def bench_softmax(dev, q, steps, warmup, do_cpu):
         res = {"config": 3, "workload": f"row sum/max/softmax [{rows}][{cols}] {dt}", "metric": "achieved HBM GB/s",
                "value": gbs, "unit": "GB/s", "ms_per_launch": ms, "parity": "ok" if ok else "FAIL",
                "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                            "frac": gbs / PEAK_HBM_GBS, "bytes_per_launch": nbytes}}
+                            "frac": gbs / PEAK_HBM_GBS, "bytes_per_launch": nbytes,
+                            "traffic": measured_traffic("softmax_" + dt)}}
         if do_cpu:
             n_rows = 2048
             t = time_cpu(lambda: oracle.row_reduce_softmax(xh, row_range=(0, n_rows)), min_s=1.0, max_reps=3)
@@ -219,7 +231,7 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
            "flop_per_step": flops, "loss": loss,
            "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                         "frac": gt / PEAK_BF16_TFLOPS, "kernel": "gemm_bf16_nt<GELU,bf16,pre> 2048x4096x4096",
-                        "kernel_ms": gms},
+                        "kernel_ms": gms, "traffic": measured_traffic("gemm_bf16")},
            "whole_graph_frac_of_peak": tflops / PEAK_BF16_TFLOPS}
     if do_cpu:
         b = 64
@@ -279,7 +291,8 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
            "metric": "MFMA TOPS (int8 GEMM)", "value": tops, "unit": "TOP/s", "ms_per_step": ms, "ops_per_step": ops,
            "parity": parity,
            "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                        "frac": gt / PEAK_INT8_TOPS, "kernel": "gemm_w8a8_nt 512x8192x8192", "kernel_ms": gms},
+                        "frac": gt / PEAK_INT8_TOPS, "kernel": "gemm_w8a8_nt 512x8192x8192", "kernel_ms": gms,
+                        "traffic": measured_traffic("gemm_w8a8")},
            "whole_graph_frac_of_peak": tops / PEAK_INT8_TOPS}
     if do_cpu:
         r = 8
@@ -397,7 +410,7 @@ def main():
                    "rows": 8192, "cols": 8192, "dtype": "f32", "bytes_per_step": head["bytes"]},
         "parity": head["parity"],
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(head["gbs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(head["gbs"] / PEAK_HBM_GBS, 4), "traffic": measured_traffic("map_chain"),
                      "kernel": "map_chain_kernel<ProgTanhExpBias,4,4>"},
         "cpu_baseline": head.get("cpu"),
         "device": {"name": info["name"], "arch": info["arch"], "compute_units": info["compute_units"]},
