@@ -33,3 +33,26 @@ def test_julia_program_frames_match_oracle(dev, q):
     assert res["frames"] == 3
     _, p = tc.lower_source(open(os.path.join(EX, "julia_orbit.py")).read(), "frame", {"phase": 2 * 0.05})
     assert np.array_equal(img, oracle.escape_time(p))
+
+
+def test_bindings_allocate_device_buffers(dev, q):
+    import ctypes
+
+    from vernondsl_amd import bindings, kernels, mapchain as mc
+    from vernondsl_amd.rhi import Tensor
+    text = ('func.func @k(%a: tensor<16x4xf32> {vernon.semantic = "input"}, '
+            '%c: tensor<4xf32> {vernon.semantic = "uniform_constant"}) -> (tensor<16x4xf32> {vernon.semantic = "output"})')
+    ts = bindings.allocate(dev, bindings.read_bindings(text, "k"))
+    assert ts["%a"].shape == (16, 4) and ts["result0"].buffer.nbytes == 256
+    b = ctypes.c_int()
+    _lib.call("vdsl_buffer_binding", ts["%c"].handle, ctypes.byref(b))
+    assert b.value == _lib.BIND_UNIFORM_CONSTANT
+    # ops write "output" buffers; a uniform_constant buffer is device read-only and is refused
+    prog = mc.compile(mc.Input(0) * 2.0)
+    kernels.map_chain(q, prog, [ts["%a"]], ts["result0"])
+    ro = Tensor(dev, (16, 4), "f32", binding="uniform_constant")
+    with pytest.raises(_lib.VdslError) as ei:
+        kernels.map_chain(q, prog, [ts["%a"]], ro)
+    assert ei.value.status == -1 and "read-only" in ei.value.message
+    for t in list(ts.values()) + [ro]:
+        t.free()
