@@ -44,6 +44,27 @@ def measured_traffic(kernel):
         return None
 
 
+def time_launches(q, dev, fn, reps, warmup=30):
+    """Mean duration of one fn() call from HIP events on q's stream around `reps` back-to-back
+    stream launches, after `warmup` untimed calls (enough GPU time for the clocks to ramp up after
+    host-side setup).  This is the per-kernel figure; graph replays (time_replays) add the graph's
+    launch latency to the first node."""
+    from vernondsl_amd.rhi import Event
+    for _ in range(warmup):
+        fn()
+    q.sync()
+    e0, e1 = Event(dev), Event(dev)
+    e0.record(q)
+    for _ in range(reps):
+        fn()
+    e1.record(q)
+    q.sync()
+    ms = e0.elapsed_ms(e1) / reps
+    e0.destroy()
+    e1.destroy()
+    return ms
+
+
 def time_replays(q, dev, fn, steps, warmup, per_graph=1):
     """Records `per_graph` consecutive calls of fn() into one hipGraph, replays it `warmup` then
     `steps` times; returns (ms per call from HIP events on q's stream, wall ms per call)."""
@@ -210,6 +231,8 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
         step.launch(q)
     e1.record(q)
     ms = e0.elapsed_ms(e1) / n
+    # the same step issued op by op on the stream (no graph), for comparison
+    eager_ms = time_launches(q, dev, lambda: exe.run(q), n, warmup=2)
     e0.destroy()
     e1.destroy()
     flops = spec.mlp_flops(B, D, Hd, O)
@@ -220,17 +243,16 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
     # dominant kernel: the forward GEMM (NT, 2048x4096x4096, GELU epilogue) timed alone
     tx, tw = Tensor.from_numpy(dev, q, x, "bf16"), Tensor.from_numpy(dev, q, w1, "bf16")
     th, tp = Tensor(dev, (B, Hd), "bf16"), Tensor(dev, (B, Hd), "f32")
-    gms, _ = time_replays(q, dev, lambda: kernels.gemm_bf16(q, tx, tw, th, False, True, _lib.EPI_GELU, tp),
-                          max(2, steps // 10), 1, per_graph=10)
+    gms = time_launches(q, dev, lambda: kernels.gemm_bf16(q, tx, tw, th, False, True, _lib.EPI_GELU, tp), max(20, steps))
     gflop = 2 * B * D * Hd
     gt = gflop / (gms * 1e-3) / 1e12
     for t_ in (tx, tw, th, tp):
         t_.free()
     res = {"config": 4, "workload": "2-layer MLP 4096-4096-4096, GELU, MSE, batch 2048, bf16 MFMA, fwd+bwd as one hipGraph",
            "metric": "MFMA TFLOPS (GEMM)", "value": tflops, "unit": "TFLOP/s", "ms_per_step": ms,
-           "flop_per_step": flops, "loss": loss,
+           "eager_ms_per_step": eager_ms, "flop_per_step": flops, "loss": loss,
            "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                        "frac": gt / PEAK_BF16_TFLOPS, "kernel": "gemm_bf16_nt<GELU,bf16,pre> 2048x4096x4096",
+                        "frac": gt / PEAK_BF16_TFLOPS, "kernel": "gemm_bf16_dma<128x256> (GELU, bf16 out, f32 pre) 2048x4096x4096",
                         "kernel_ms": gms, "traffic": measured_traffic("gemm_bf16")},
            "whole_graph_frac_of_peak": tflops / PEAK_BF16_TFLOPS}
     if do_cpu:
@@ -267,6 +289,7 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
         step.launch(q)
     e1.record(q)
     ms = e0.elapsed_ms(e1) / n
+    eager_ms = time_launches(q, dev, lambda: exe.run(q), n, warmup=2)
     e0.destroy()
     e1.destroy()
     ops = spec.w8a8_ops(B, widths)
@@ -278,20 +301,23 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
     exe.free()
     # dominant kernel: one 512x8192x8192 layer GEMM timed alone
     K = N = 8192
-    txq = Tensor.from_numpy(dev, q, np.zeros((B, K), np.int8))
+    # activations: int8 rows of the same uniform distribution as the weights (layer 1's first rows)
+    txq = Tensor.from_numpy(dev, q, np.ascontiguousarray(layers[1][0][:B]))
     txs = Tensor.from_numpy(dev, q, np.ones(B, np.float32))
     tw, tws = Tensor.from_numpy(dev, q, layers[0][0]), Tensor.from_numpy(dev, q, layers[0][1])
     ty = Tensor(dev, (B, N), "bf16")
-    gms, _ = time_replays(q, dev, lambda: kernels.gemm_w8a8(q, txq, txs, tw, tws, ty, True), max(2, steps // 10), 1,
-                          per_graph=10)
+    wsb = kernels.gemm_w8a8_workspace_bytes(B, N, K)
+    tws_acc = Tensor(dev, (wsb,), "i8") if wsb else None
+    gms = time_launches(q, dev, lambda: kernels.gemm_w8a8(q, txq, txs, tw, tws, ty, True, None, tws_acc), max(20, steps))
     gt = 2 * B * K * N / (gms * 1e-3) / 1e12
-    for t_ in (txq, txs, tw, tws, ty):
+    for t_ in (txq, txs, tw, tws, ty) + ((tws_acc,) if tws_acc else ()):
         t_.free()
     res = {"config": 5, "workload": "int8 W8A8 MLP 8192-8192-8192-8192-1024, batch 512, dequant+ReLU fused, one hipGraph",
-           "metric": "MFMA TOPS (int8 GEMM)", "value": tops, "unit": "TOP/s", "ms_per_step": ms, "ops_per_step": ops,
+           "metric": "MFMA TOPS (int8 GEMM)", "value": tops, "unit": "TOP/s", "ms_per_step": ms,
+           "eager_ms_per_step": eager_ms, "ops_per_step": ops,
            "parity": parity,
            "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                        "frac": gt / PEAK_INT8_TOPS, "kernel": "gemm_w8a8_nt 512x8192x8192", "kernel_ms": gms,
+                        "frac": gt / PEAK_INT8_TOPS, "kernel": "gemm_w8a8_dma<128x128> (dequant+ReLU) 512x8192x8192", "kernel_ms": gms,
                         "traffic": measured_traffic("gemm_w8a8")},
            "whole_graph_frac_of_peak": tops / PEAK_INT8_TOPS}
     if do_cpu:
@@ -323,17 +349,19 @@ def run_kernel_only(dev, q, name, reps):
         outs = [Tensor(dev, (16384,), "f32"), Tensor(dev, (16384,), "f32"), Tensor(dev, (16384, 4096), dt)]
         fn, ts = (lambda: kernels.row_reduce_softmax(q, tx, *outs)), [tx] + outs
     elif name == "gemm_bf16":
-        A, B = Tensor(dev, (2048, 4096), "bf16"), Tensor(dev, (4096, 4096), "bf16")
+        x, w1, _, _ = spec.mlp_inputs()
+        A, B = Tensor.from_numpy(dev, q, x, "bf16"), Tensor.from_numpy(dev, q, w1, "bf16")
         H, P = Tensor(dev, (2048, 4096), "bf16"), Tensor(dev, (2048, 4096), "f32")
-        A.buffer.fill_u32(q, 0x3F803F80)
-        B.buffer.fill_u32(q, 0x3C003C00)
         fn, ts = (lambda: kernels.gemm_bf16(q, A, B, H, False, True, _lib.EPI_GELU, P)), [A, B, H, P]
     elif name == "gemm_w8a8":
-        A, B = Tensor(dev, (512, 8192), "i8"), Tensor(dev, (8192, 8192), "i8")
-        xs, ws, Y = Tensor(dev, (512,), "f32"), Tensor(dev, (8192,), "f32"), Tensor(dev, (512, 8192), "bf16")
-        for t_ in (A, B, xs, ws):
-            t_.buffer.fill_u32(q, 0x01010101)
-        fn, ts = (lambda: kernels.gemm_w8a8(q, A, xs, B, ws, Y, True)), [A, B, xs, ws, Y]
+        _, layers = spec.w8a8_inputs()
+        A = Tensor.from_numpy(dev, q, np.ascontiguousarray(layers[1][0][:512]))
+        B = Tensor.from_numpy(dev, q, layers[0][0])
+        xs, ws, Y = Tensor(dev, (512,), "f32"), Tensor.from_numpy(dev, q, layers[0][1]), Tensor(dev, (512, 8192), "bf16")
+        xs.buffer.fill_u32(q, 0x3F800000)
+        wsb = kernels.gemm_w8a8_workspace_bytes(512, 8192, 8192)
+        W = Tensor(dev, (wsb,), "i8") if wsb else None
+        fn, ts = (lambda: kernels.gemm_w8a8(q, A, xs, B, ws, Y, True, None, W)), [A, B, xs, ws, Y] + ([W] if W else [])
     elif name == "escape_time":
         p = kernels.escape_time_params(**spec.mandelbrot_params())
         out = Tensor(dev, (1024, 1024), "i32")

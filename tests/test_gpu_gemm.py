@@ -81,9 +81,13 @@ def test_layouts_and_edges(dev, q, ta, tb, M, N, K):
     assert_gemm_close(got, ref, magnitude(A, B, ta, tb))
 
 
+@pytest.mark.parametrize("shape", [(256, 128, 256), (200, 100, 96), (64, 48, 40)])
 @pytest.mark.parametrize("epi", [_lib.EPI_GELU, _lib.EPI_RELU])
-def test_epilogues_bf16_out_and_pre(dev, q, epi):
-    A, B = bf16_rand((256, 256), 11, -2, 2), bf16_rand((128, 256), 12, -2, 2)
+def test_epilogues_bf16_out_and_pre(dev, q, epi, shape):
+    """Whole tiles (the fixed-variant epilogue), ragged tiles on the direct-to-LDS loop and a K that
+    takes the register-staged loop (both through the per-element epilogue)."""
+    M, N, K = shape
+    A, B = bf16_rand((M, K), 11, -2, 2), bf16_rand((N, K), 12, -2, 2)
     out, pre = gemm_gpu(dev, q, A, B, 0, 1, "bf16", epi, want_pre=True)
     rout, rpre = oracle.gemm_bf16(A, B, 0, 1, c_dtype=BF16, epilogue=epi, want_pre=True)
     mag = magnitude(A, B, 0, 1)

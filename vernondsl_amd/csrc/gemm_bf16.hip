@@ -13,6 +13,7 @@
 #include <cstdlib>
 
 #include "gemm_mfma.h"
+#include "gemm_dma.h"
 
 namespace vdsl {
 
@@ -29,8 +30,30 @@ int gemm_config_override() {
 
 namespace {
 
+// erfc(x) by the Chebyshev-fitted form of Numerical Recipes (Press et al., 2nd ed., sec. 6.2,
+// "erfcc"): erfc(|x|) = t exp(-x^2 + P(t)), t = 1 / (1 + |x|/2), P a degree-9 polynomial, with
+// fractional error below 1.2e-7 for every x; erfc(-x) = 2 - erfc(x).  Branch-free (the library
+// erfcf picks among argument ranges per lane), which matters in a GEMM epilogue that evaluates it
+// on every output element.
+__device__ __forceinline__ float erfc_cheb(float x) {
+  const float z = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = __builtin_fmaf(p, t, -0.82215223f);
+  p = __builtin_fmaf(p, t, 1.48851587f);
+  p = __builtin_fmaf(p, t, -1.13520398f);
+  p = __builtin_fmaf(p, t, 0.27886807f);
+  p = __builtin_fmaf(p, t, -0.18628806f);
+  p = __builtin_fmaf(p, t, 0.09678418f);
+  p = __builtin_fmaf(p, t, 0.37409196f);
+  p = __builtin_fmaf(p, t, 1.00002368f);
+  p = __builtin_fmaf(p, t, -1.26551223f);
+  const float r = t * __expf(__builtin_fmaf(-z, z, p));
+  return x >= 0.0f ? r : 2.0f - r;
+}
+
 // 0.5 v (1 + erf(v / sqrt2)) written as 0.5 v erfc(-v / sqrt2): no cancellation for v < 0.
-__device__ __forceinline__ float gelu_f(float v) { return 0.5f * v * erfcf(-v * 0.7071067811865476f); }
+__device__ __forceinline__ float gelu_f(float v) { return 0.5f * v * erfc_cheb(-v * 0.7071067811865476f); }
 
 // Tile configurations (block M x N, K bytes per stage, wave grid).
 using Bf0 = GemmConfig<MfmaBf16, 128, 128, 128, 2, 2>;  // wave tile 64x64
@@ -47,7 +70,73 @@ using Bf10 = GemmConfig<MfmaBf16, 256, 128, 64, 2, 2>;  // wave tile 128x64, 2 b
 using Bf11 = GemmConfig<MfmaBf16, 128, 256, 64, 2, 2>;  // wave tile 64x128, 2 blocks per CU
 using Bf12 = GemmConfig<MfmaBf16, 256, 256, 64, 2, 4>;  // 8 waves, wave tile 128x64
 using Bf13 = GemmConfig<MfmaBf16, 256, 128, 64, 4, 2>;  // 8 waves, wave tile 64x64, 2 blocks per CU
-constexpr int kNumConfigs = 14;
+// Direct-to-LDS loop (gemm_dma.h), configurations 14..: <BM, BN, WGM, WGN, LDS stages>
+using Dm14 = DmaConfig<MfmaBf16, 128, 256, 2, 4, 4>;  // 8 waves of 64x64
+using Dm15 = DmaConfig<MfmaBf16, 256, 256, 2, 4, 3>;  // 8 waves of 128x64
+using Dm16 = DmaConfig<MfmaBf16, 256, 128, 4, 2, 4>;  // 8 waves of 64x64
+using Dm17 = DmaConfig<MfmaBf16, 128, 128, 2, 2, 4>;  // 4 waves of 64x64, 2 blocks per CU
+using Dm18 = DmaConfig<MfmaBf16, 128, 256, 2, 2, 4>;  // 4 waves of 64x128
+using Dm19 = DmaConfig<MfmaBf16, 256, 128, 2, 2, 4>;  // 4 waves of 128x64
+constexpr int kNumConfigs = 20;
+
+// Epilogue of one accumulator element at (row, col), shared by both main loops.
+__device__ __forceinline__ void bf16_epilogue(float v, int row, int col, int M, int N, void* __restrict__ C,
+                                              float* __restrict__ pre, int epi, int c_dtype) {
+  if (row < M && col < N) {
+    const size_t o = static_cast<size_t>(row) * N + col;
+    if (pre) pre[o] = v;
+    float y = v;
+    if (epi == VDSL_EPI_GELU) y = gelu_f(v);
+    else if (epi == VDSL_EPI_RELU) y = v > 0.0f ? v : 0.0f;
+    if (c_dtype == VDSL_F32) static_cast<float*>(C)[o] = y;
+    else static_cast<uint16_t*>(C)[o] = f32_to_bf16(y);
+  }
+}
+
+// Whole-tile epilogue with the variant fixed at compile time: no bounds checks and no per-element
+// branches (the generic per-element form costs ~6000 instructions of branchy code per tile).
+// Variants: 0 = f32 C, no activation, no pre-activation; 1 = bf16 C = GELU(v) with f32 pre-activation.
+template <class Cfg, int VARIANT>
+__device__ __forceinline__ void bf16_epilogue_tile(const f32x16 (&acc)[Cfg::FM][Cfg::FN], int m0, int n0, int N,
+                                                   void* __restrict__ C, float* __restrict__ pre) {
+#pragma unroll
+  for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < Cfg::FN; ++j) {
+      const int col = acc_col<Cfg>(n0, j);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const size_t o = static_cast<size_t>(acc_row<Cfg>(m0, i, r)) * N + col;
+        const float v = acc[i][j][r];
+        if (VARIANT == 0) {
+          static_cast<float*>(C)[o] = v;
+        } else {
+          pre[o] = v;
+          static_cast<uint16_t*>(C)[o] = f32_to_bf16(gelu_f(v));
+        }
+      }
+    }
+}
+
+// Picks the whole-tile variant when one applies, else the generic per-element epilogue.
+template <class Cfg>
+__device__ __forceinline__ void bf16_store_tile(const f32x16 (&acc)[Cfg::FM][Cfg::FN], int m0, int n0, int M, int N,
+                                                void* __restrict__ C, float* __restrict__ pre, int epi, int c_dtype) {
+  const bool whole = m0 + Cfg::BM <= M && n0 + Cfg::BN <= N;
+  if (whole && epi == VDSL_EPI_NONE && c_dtype == VDSL_F32 && !pre) {
+    bf16_epilogue_tile<Cfg, 0>(acc, m0, n0, N, C, pre);
+  } else if (whole && epi == VDSL_EPI_GELU && c_dtype == VDSL_BF16 && pre) {
+    bf16_epilogue_tile<Cfg, 1>(acc, m0, n0, N, C, pre);
+  } else {
+#pragma unroll
+    for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          bf16_epilogue(acc[i][j][r], acc_row<Cfg>(m0, i, r), acc_col<Cfg>(n0, j), M, N, C, pre, epi, c_dtype);
+  }
+}
 
 template <class Cfg, bool EDGE>
 __global__ __launch_bounds__(Cfg::NT, 2) void gemm_bf16_nt(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
@@ -61,24 +150,25 @@ __global__ __launch_bounds__(Cfg::NT, 2) void gemm_bf16_nt(const uint16_t* __res
   f32x16 acc[Cfg::FM][Cfg::FN];
   gemm_mainloop<MfmaBf16, Cfg, EDGE>(reinterpret_cast<const char*>(A), reinterpret_cast<const char*>(B), M, N, K * 2, 0, K * 2,
                                m0, n0, smem, acc);
-#pragma unroll
-  for (int i = 0; i < Cfg::FM; ++i)
-#pragma unroll
-    for (int j = 0; j < Cfg::FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = acc_row<Cfg>(m0, i, r), col = acc_col<Cfg>(n0, j);
-        if (row < M && col < N) {
-          const float v = acc[i][j][r];
-          const size_t o = static_cast<size_t>(row) * N + col;
-          if (pre) pre[o] = v;
-          float y = v;
-          if (epi == VDSL_EPI_GELU) y = gelu_f(v);
-          else if (epi == VDSL_EPI_RELU) y = v > 0.0f ? v : 0.0f;
-          if (c_dtype == VDSL_F32) static_cast<float*>(C)[o] = y;
-          else static_cast<uint16_t*>(C)[o] = f32_to_bf16(y);
-        }
-      }
+  bf16_store_tile<Cfg>(acc, m0, n0, M, N, C, pre, epi, c_dtype);
+}
+
+// Direct-to-LDS kernel (gemm_dma.h).  Blocks of 8 waves are sized for one block per CU, blocks
+// of 4 waves for two.
+template <class Cfg>
+__global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_bf16_dma(const uint16_t* __restrict__ A,
+                                                                               const uint16_t* __restrict__ B,
+                                                                               void* __restrict__ C, float* __restrict__ pre,
+                                                                               int M, int N, int K, int epi, int c_dtype) {
+  __shared__ __attribute__((aligned(1024))) char smem[Cfg::LDS_BYTES];
+  const int tiles_m = (M + Cfg::BM - 1) / Cfg::BM, tiles_n = (N + Cfg::BN - 1) / Cfg::BN;
+  int tm, tn;
+  tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * Cfg::BM, n0 = tn * Cfg::BN;
+  f32x16 acc[Cfg::FM][Cfg::FN];
+  dma_mainloop<MfmaBf16, Cfg>(reinterpret_cast<const char*>(A), reinterpret_cast<const char*>(B), M, N, K * 2, 0, K * 2, m0,
+                              n0, smem, acc);
+  bf16_store_tile<Cfg>(acc, m0, n0, M, N, C, pre, epi, c_dtype);
 }
 
 // Any K (including K % 8 != 0): one lane per output, f32 accumulate in k order.
@@ -109,12 +199,31 @@ int launch_cfg(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M,
   return check_launch("gemm_bf16_nt");
 }
 
-// Measured on MI355X over every configuration above (config-4 shapes): 128x128 tiles are fastest
-// for 2048x4096 outputs (512 blocks, 2 per CU); 256x128 blocks of 8 waves are fastest once they
-// still give every CU two blocks (4096x4096 outputs).  Throughput follows resident waves per CU.
-int choose_config(int64_t M, int64_t N) {
+template <class Cfg>
+int launch_dma(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, int N, int K, int epi, int ct, hipStream_t s) {
+  const int64_t tiles = static_cast<int64_t>((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN);
+  hipLaunchKernelGGL((gemm_bf16_dma<Cfg>), dim3(static_cast<unsigned>(tiles)), dim3(Cfg::NT), 0, s, A, B, C, pre, M, N, K, epi, ct);
+  return check_launch("gemm_bf16_dma");
+}
+
+// Configuration for a shape.  The direct-to-LDS loop (14..) runs whenever K is a whole number of
+// its 64-byte stages (K % 32 == 0); measured on MI355X with random operands (bf16, f32 out):
+// 128x256 blocks of 8 waves are fastest while they still give every CU a block (2048x4096x4096:
+// 950 TFLOP/s against 794 for the best register-staged configuration), 256x256 blocks once those
+// do (4096x4096x2048: 973 against 870).  Smaller launches take 128x128 blocks, two per CU.  Other
+// K use the register-staged loop (0..13), where 128x128 tiles are fastest below 512 tiles of
+// 256x128 and 256x128 tiles of 8 waves above.
+int choose_config(int64_t M, int64_t N, int64_t K) {
+  const bool dma = dma_k_ok(0, K * 2);
   const int o = gemm_config_override();
-  if (o >= 0 && o < kNumConfigs) return o;
+  if (o >= 0 && o < kNumConfigs && (o < 14 || dma)) return o;
+  if (dma) {
+    const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+    const int64_t t128x256 = ((M + 127) / 128) * ((N + 255) / 256);
+    if (t256 >= 240) return 15;
+    if (t128x256 >= 128) return 14;
+    return 17;
+  }
   const int64_t tiles_256x128 = ((M + 255) / 256) * ((N + 127) / 128);
   return tiles_256x128 >= 512 ? 13 : 0;
 }
@@ -125,7 +234,7 @@ int launch_nt(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, 
     hipLaunchKernelGGL(gemm_bf16_nt_simple, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, A, B, C, pre, M, N, K, epi, ct);
     return check_launch("gemm_bf16_nt_simple");
   }
-  switch (choose_config(M, N)) {
+  switch (choose_config(M, N, K)) {
     case 1: return launch_cfg<Bf1>(A, B, C, pre, M, N, K, epi, ct, s);
     case 2: return launch_cfg<Bf2>(A, B, C, pre, M, N, K, epi, ct, s);
     case 3: return launch_cfg<Bf3>(A, B, C, pre, M, N, K, epi, ct, s);
@@ -139,6 +248,12 @@ int launch_nt(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, 
     case 11: return launch_cfg<Bf11>(A, B, C, pre, M, N, K, epi, ct, s);
     case 12: return launch_cfg<Bf12>(A, B, C, pre, M, N, K, epi, ct, s);
     case 13: return launch_cfg<Bf13>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 14: return launch_dma<Dm14>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 15: return launch_dma<Dm15>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 16: return launch_dma<Dm16>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 17: return launch_dma<Dm17>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 18: return launch_dma<Dm18>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 19: return launch_dma<Dm19>(A, B, C, pre, M, N, K, epi, ct, s);
     default: return launch_cfg<Bf0>(A, B, C, pre, M, N, K, epi, ct, s);
   }
 }

@@ -1,0 +1,187 @@
+// Direct-to-LDS MFMA main loop for gfx950: C[m][n] = sum_k A[m][k] B[n][k], both operands
+// K-contiguous, for launches whose K range is a whole number of 64-byte stages.
+//
+// Global -> LDS copies use global_load_lds_dwordx4: each lane's 16 bytes go straight into LDS at
+// (wave-uniform base + 16 * lane), with no VGPR round trip and no ds_write.  Freed of prefetch
+// registers, the loop keeps NS stages of LDS in flight (NS-1 stages of global latency hidden).
+//
+// LDS layout, per operand and stage: 64 K bytes (4 chunks of 16 B) of each row, in 1 KiB blocks
+// of 16 rows.  Within a block row r occupies 64 bytes at 64 * (r % 16) and its chunk c sits in
+// slot c ^ ((r >> 2) & 3).  Both sides of that choice are measured constraints of the hardware:
+//   - the address unit coalesces 4 consecutive lanes; the copy gives lanes 4q..4q+3 one row's 4
+//     chunks (a whole 64-byte sector, in swizzled order), so a copy instruction touches 16 sectors;
+//   - an MFMA fragment read has lane l take row l % 32, chunk 2 * kk + l / 32; the 16 lanes read
+//     together land in 16 distinct 16-byte bank groups (rows 4 apart share a 64-byte bank window
+//     and the XOR gives them distinct slots), so fragment reads are free of bank conflicts.
+//
+// Pipeline per stage t (ring of NS LDS stages): issue the copy of stage t+NS-1 (into the slot
+// stage t-1 used), read fragments k-step by k-step one step ahead of the MFMAs, then before the
+// MFMAs of the last k-step wait for this wave's copy of stage t+1 (vmcnt = copies issued after
+// it) and meet the block barrier, so stage t+1's first fragment reads overlap those MFMAs.  The
+// barrier also orders every wave's reads of stage t before the copy that overwrites it (issued
+// at stage t+1).  Rows past M or N are clamped to the last row (their products only reach
+// outputs that are not stored).
+#pragma once
+
+#include "gemm_mfma.h"
+
+namespace vdsl {
+
+template <class T, int BM_, int BN_, int WGM_, int WGN_, int NS_>
+struct DmaConfig {
+  static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, NS = NS_;
+  static constexpr int BKB = 64;                     // K bytes per stage
+  static constexpr int RPB = 16;                     // rows per 1 KiB LDS block
+  static constexpr int NT = WGM * WGN * 64, NW = WGM * WGN;
+  static constexpr int WTM = BM / WGM, WTN = BN / WGN;
+  static constexpr int FM = WTM / 32, FN = WTN / 32;
+  static constexpr int STAGE = (BM + BN) * BKB;
+  static constexpr int LDS_BYTES = NS * STAGE;
+  static constexpr int NBLK = (BM + BN) / RPB;       // 1 KiB copy blocks per stage
+  static constexpr int BPW = NBLK / NW;              // copy instructions per wave per stage
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 MFMA tiles");
+  static_assert(BM % RPB == 0 && BN % RPB == 0 && NBLK % NW == 0, "copy blocks must split evenly over waves");
+  static_assert(NS >= 3, "the loop keeps two stages in flight beyond the one being read");
+  static_assert(LDS_BYTES <= 160 * 1024, "gfx950 workgroup LDS limit");
+};
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// LDS offset (within a stage's operand area) of chunk c of row r.
+__device__ __forceinline__ int dma_slot(int r, int c) {
+  return (r >> 4) * 1024 + (r & 15) * 64 + ((c ^ ((r >> 2) & 3)) << 4);
+}
+
+// The gfx950-only builtins sit in plain (non-template) device functions: inside a function
+// template, clang's host pass marks the specialization invalid on first instantiation and then
+// rejects every later call to it.
+__device__ __forceinline__ void lds_copy16(const char* g, char* l) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void_t*)l, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4 left at
+// its no-wait value 7, lgkmcnt 11:8 = 0).  The count must be a constant.
+#define VDSL_WAIT_VM_LGKM0(n) dma_wait<(n)>()
+template <int N>
+__device__ __forceinline__ void dma_wait();
+#define VDSL_DMA_WAIT_CASE(n) \
+  template <> __device__ __forceinline__ void dma_wait<n>() { __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4)); }
+VDSL_DMA_WAIT_CASE(0)
+VDSL_DMA_WAIT_CASE(3)
+VDSL_DMA_WAIT_CASE(4)
+VDSL_DMA_WAIT_CASE(6)
+VDSL_DMA_WAIT_CASE(8)
+VDSL_DMA_WAIT_CASE(12)
+#undef VDSL_DMA_WAIT_CASE
+
+// Block barrier without the full memory fence of __syncthreads (which would also wait for the
+// copies still meant to be in flight); the empty asm statements stop the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void dma_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// K loop over bytes [kb_begin, kb_end) for the tile at (m0, n0).  Requires kb_begin % 16 == 0 and
+// (kb_end - kb_begin) % 64 == 0; Kb = row stride of A and B in bytes.
+template <class T, class Cfg, class AccT, int FM_, int FN_>
+__device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const char* __restrict__ B, int M, int N, int Kb,
+                                             int kb_begin, int kb_end, int m0, int n0, char* smem, AccT (&acc)[FM_][FN_]) {
+  static_assert(FM_ == Cfg::FM && FN_ == Cfg::FN, "accumulator array must match the configuration");
+  using Frag = typename T::Frag;
+  constexpr int FM = Cfg::FM, FN = Cfg::FN, NS = Cfg::NS, BPW = Cfg::BPW, STAGE = Cfg::STAGE;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = T::zero();
+
+  // Copy block b = wave * BPW + u of a stage: blocks [0, BM/16) are A rows 16b.., the rest B.
+  // Lane l copies row 16 * (b') + l / 4, LDS slot l % 4, i.e. global chunk (l % 4) ^ swizzle.
+  const char* src[BPW];
+#pragma unroll
+  for (int u = 0; u < BPW; ++u) {
+    const int b = wave * BPW + u;
+    const bool is_a = b < Cfg::BM / Cfg::RPB;
+    const int r = Cfg::RPB * (is_a ? b : b - Cfg::BM / Cfg::RPB) + (lane >> 2);
+    const int c = (lane & 3) ^ ((r >> 2) & 3);
+    const size_t row = is_a ? static_cast<size_t>(min(m0 + r, M - 1)) : static_cast<size_t>(min(n0 + r, N - 1));
+    src[u] = (is_a ? A : B) + row * Kb + kb_begin + c * 16;
+  }
+  char* const dst = smem + wave * BPW * 1024;
+  // This lane's fragment rows (within the stage's A and B areas).
+  const int ra = wm * Cfg::WTM + (lane & 31);
+  const int rb = wn * Cfg::WTN + (lane & 31);
+  const int hk = lane >> 5;
+  const char* const fa = smem;
+  const char* const fb = smem + Cfg::BM * Cfg::BKB;
+
+#define VDSL_DMA_COPY(ST, KB)                                                                     \
+  do {                                                                                            \
+    _Pragma("unroll") for (int u = 0; u < BPW; ++u)                                               \
+      lds_copy16(src[u] + (KB), dst + (ST) * STAGE + u * 1024);                                   \
+  } while (0)
+#define VDSL_DMA_READ(A_, B_, ST, KK)                                                             \
+  do {                                                                                            \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                \
+      A_[i] = *reinterpret_cast<const Frag*>(fa + (ST) * STAGE + dma_slot(ra + 32 * i, 2 * (KK) + hk)); \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j)                                                \
+      B_[j] = *reinterpret_cast<const Frag*>(fb + (ST) * STAGE + dma_slot(rb + 32 * j, 2 * (KK) + hk)); \
+  } while (0)
+#define VDSL_DMA_MMA(A_, B_)                                                                      \
+  do {                                                                                            \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = T::mma(A_[i], B_[j], acc[i][j]); \
+  } while (0)
+// Reads of the next k-step first, then the MFMAs (sched_group_barrier masks: 0x100 DS read,
+// 0x008 MFMA); the scheduling barrier keeps each k-step's instructions together.
+#define VDSL_DMA_ORDER()                                                                          \
+  do {                                                                                            \
+    __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);                                      \
+    __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);                                      \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+  } while (0)
+
+  const int nk = (kb_end - kb_begin) / Cfg::BKB;
+  if (nk <= 0) return;
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) VDSL_DMA_COPY(s, min(s, nk - 1) * Cfg::BKB);
+  VDSL_WAIT_VM_LGKM0((NS - 2) * BPW);
+  dma_barrier();
+  Frag a0[FM], b0[FN], a1[FM], b1[FN];
+  VDSL_DMA_READ(a0, b0, 0, 0);
+  int st = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int nst = st + 1 == NS ? 0 : st + 1;
+    const int cst = st == 0 ? NS - 1 : st - 1;  // = (kt + NS - 1) % NS
+    // Past the last stage the copy repeats it (never read): the copy count per stage stays fixed,
+    // which is what the vmcnt in the wait below counts on.
+    VDSL_DMA_COPY(cst, min(kt + NS - 1, nk - 1) * Cfg::BKB);
+    __builtin_amdgcn_sched_barrier(0);
+    VDSL_DMA_READ(a1, b1, st, 1);
+    VDSL_DMA_MMA(a0, b0);
+    VDSL_DMA_ORDER();
+    VDSL_WAIT_VM_LGKM0((NS - 2) * BPW);
+    dma_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    VDSL_DMA_READ(a0, b0, nst, 0);
+    VDSL_DMA_MMA(a1, b1);
+    VDSL_DMA_ORDER();
+    st = nst;
+  }
+  // Drain the copies of the stages past the end before the block's LDS can be reused or freed.
+  VDSL_WAIT_VM_LGKM0(0);
+#undef VDSL_DMA_ORDER
+#undef VDSL_DMA_MMA
+#undef VDSL_DMA_READ
+#undef VDSL_DMA_COPY
+}
+
+// True when the direct-to-LDS loop can run this K range.
+inline bool dma_k_ok(int64_t kb_begin, int64_t kbytes) { return kb_begin % 16 == 0 && kbytes % 64 == 0 && kbytes > 0; }
+
+}  // namespace vdsl

@@ -122,21 +122,48 @@ __device__ __forceinline__ void gemm_store_tile(const u32x4 (&r)[ROWS * Cfg::CPR
   }
 }
 
-// MFMAs of one LDS stage for this wave.
+// MFMAs of one LDS stage for this wave.  The fragments of k-step kk+1 are read before the MFMAs
+// of k-step kk (two fragment sets in turn), so LDS latency hides behind FM*FN MFMAs; scheduling
+// barriers keep that order (left alone, the compiler moves each read next to its first use).
+// sched_group_barrier masks: 0x008 MFMA, 0x100 DS read.
 template <class T, class Cfg>
 __device__ __forceinline__ void gemm_compute_stage(const char* sa, const char* sb, typename T::Acc (&acc)[Cfg::FM][Cfg::FN]) {
+  using Frag = typename T::Frag;
+  constexpr int FM = Cfg::FM, FN = Cfg::FN, KS = Cfg::BKB / 32;
+  Frag a0[FM], b0[FN], a1[FM], b1[FN];
+#define VDSL_GEMM_READ(A_, B_, KK)                                                              \
+  do {                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i)                                              \
+      A_[i] = *reinterpret_cast<const Frag*>(sa + i * 32 * Cfg::ROW + (KK) * 32);               \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j)                                              \
+      B_[j] = *reinterpret_cast<const Frag*>(sb + j * 32 * Cfg::ROW + (KK) * 32);               \
+  } while (0)
+#define VDSL_GEMM_MMA(A_, B_)                                                                   \
+  do {                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i)                                              \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = T::mma(A_[i], B_[j], acc[i][j]); \
+  } while (0)
+#define VDSL_GEMM_ORDER()                                                                       \
+  do {                                                                                          \
+    __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);                                    \
+    __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);                                    \
+    __builtin_amdgcn_sched_barrier(0);                                                          \
+  } while (0)
+  VDSL_GEMM_READ(a0, b0, 0);
 #pragma unroll
-  for (int kk = 0; kk < Cfg::BKB; kk += 32) {
-    typename T::Frag a[Cfg::FM], b[Cfg::FN];
-#pragma unroll
-    for (int i = 0; i < Cfg::FM; ++i) a[i] = *reinterpret_cast<const typename T::Frag*>(sa + i * 32 * Cfg::ROW + kk);
-#pragma unroll
-    for (int j = 0; j < Cfg::FN; ++j) b[j] = *reinterpret_cast<const typename T::Frag*>(sb + j * 32 * Cfg::ROW + kk);
-#pragma unroll
-    for (int i = 0; i < Cfg::FM; ++i)
-#pragma unroll
-      for (int j = 0; j < Cfg::FN; ++j) acc[i][j] = T::mma(a[i], b[j], acc[i][j]);
+  for (int kk = 0; kk < KS; kk += 2) {
+    if (kk + 1 < KS) VDSL_GEMM_READ(a1, b1, kk + 1);
+    VDSL_GEMM_MMA(a0, b0);
+    VDSL_GEMM_ORDER();
+    if (kk + 1 < KS) {
+      if (kk + 2 < KS) VDSL_GEMM_READ(a0, b0, kk + 2);
+      VDSL_GEMM_MMA(a1, b1);
+      VDSL_GEMM_ORDER();
+    }
   }
+#undef VDSL_GEMM_ORDER
+#undef VDSL_GEMM_MMA
+#undef VDSL_GEMM_READ
 }
 
 // Runs the K loop over bytes [kb_begin, kb_end) of rows m0.. and n0.. and leaves the wave's
@@ -186,25 +213,37 @@ __device__ __forceinline__ void gemm_mainloop(const char* __restrict__ A, const 
     gemm_store_tile<Cfg, Cfg::BN>(RB, smem + (ST) * Cfg::STAGE + Cfg::BM * Cfg::ROW, tid);      \
   } while (0)
 // Stage kt computed from LDS stage CUR; RA/RB_L receive tile kt+2; RA/RB_S (tile kt+1) go to
-// LDS stage CUR ^ 1.
+// LDS stage CUR ^ 1.  The loads and the store are unconditional: past the last tile they repeat
+// it (kb clamped to kb_last) and that copy is never read.  A branch around them would make the
+// compiler's wait counts conservative at the join: it then waits for every outstanding load at
+// the top of each stage, which leaves one stage of prefetch instead of two.
+// The scheduling barrier after the loads keeps the compiler from sinking them below the store
+// of the previous tile (it does so otherwise, and the store then waits for every load).
 #define VDSL_GEMM_STEP(KT, CUR, RA_L, RB_L, RA_S, RB_S)                                         \
   do {                                                                                          \
-    if ((KT) + 2 < nk) VDSL_GEMM_LOAD(RA_L, RB_L, kb_begin + ((KT) + 2) * Cfg::BKB);           \
+    VDSL_GEMM_LOAD(RA_L, RB_L, min(kb_begin + ((KT) + 2) * Cfg::BKB, kb_last));                \
+    __builtin_amdgcn_sched_barrier(0);                                                          \
     gemm_compute_stage<T, Cfg>(fa + (CUR) * Cfg::STAGE, fb + (CUR) * Cfg::STAGE, acc);          \
-    if ((KT) + 1 < nk) VDSL_GEMM_STORE(RA_S, RB_S, (CUR) ^ 1);                                  \
+    VDSL_GEMM_STORE(RA_S, RB_S, (CUR) ^ 1);                                                     \
     __syncthreads();                                                                            \
+    __builtin_amdgcn_sched_barrier(0);                                                          \
   } while (0)
 
   const int nk = (kb_end - kb_begin + Cfg::BKB - 1) / Cfg::BKB;
   if (nk <= 0) return;
+  const int kb_last = kb_begin + (nk - 1) * Cfg::BKB;
   VDSL_GEMM_LOAD(ra0, rb0, kb_begin);
-  if (nk > 1) VDSL_GEMM_LOAD(ra1, rb1, kb_begin + Cfg::BKB);
+  VDSL_GEMM_LOAD(ra1, rb1, min(kb_begin + Cfg::BKB, kb_last));
   VDSL_GEMM_STORE(ra0, rb0, 0);
   __syncthreads();
-  for (int kt = 0; kt < nk; kt += 2) {
+  // Unrolled by two so every register set index is a constant; no early exit inside the loop
+  // (the accumulators then stay in one register class across the back edge).
+  int kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
     VDSL_GEMM_STEP(kt, 0, ra0, rb0, ra1, rb1);
-    if (kt + 1 < nk) VDSL_GEMM_STEP(kt + 1, 1, ra1, rb1, ra0, rb0);
+    VDSL_GEMM_STEP(kt + 1, 1, ra1, rb1, ra0, rb0);
   }
+  if (kt < nk) VDSL_GEMM_STEP(kt, 0, ra0, rb0, ra1, rb1);
 #undef VDSL_GEMM_STEP
 #undef VDSL_GEMM_STORE
 #undef VDSL_GEMM_LOAD

@@ -15,6 +15,7 @@
 // with atomics - integer addition is exact and order-independent, so the result is still
 // deterministic - and a second kernel applies the dequant epilogue.
 
+#include "gemm_dma.h"
 #include "gemm_mfma.h"
 
 namespace vdsl {
@@ -35,7 +36,14 @@ using I10 = GemmConfig<MfmaI8, 256, 128, 64, 2, 2>;  // wave tile 128x64, 2 bloc
 using I11 = GemmConfig<MfmaI8, 128, 256, 64, 2, 2>;  // wave tile 64x128, 2 blocks per CU
 using I12 = GemmConfig<MfmaI8, 256, 256, 64, 2, 4>;  // 8 waves, wave tile 128x64
 using I13 = GemmConfig<MfmaI8, 256, 128, 64, 4, 2>;  // 8 waves, wave tile 64x64, 2 blocks per CU
-constexpr int kNumConfigs = 14;
+// Direct-to-LDS loop (gemm_dma.h), configurations 14..: <BM, BN, WGM, WGN, LDS stages>
+using Di14 = DmaConfig<MfmaI8, 128, 256, 2, 4, 4>;  // 8 waves of 64x64
+using Di15 = DmaConfig<MfmaI8, 256, 256, 2, 4, 3>;  // 8 waves of 128x64
+using Di16 = DmaConfig<MfmaI8, 256, 128, 4, 2, 4>;  // 8 waves of 64x64
+using Di17 = DmaConfig<MfmaI8, 128, 128, 2, 2, 4>;  // 4 waves of 64x64, 2 blocks per CU
+using Di18 = DmaConfig<MfmaI8, 128, 256, 2, 2, 4>;  // 4 waves of 64x128
+using Di19 = DmaConfig<MfmaI8, 128, 64, 2, 2, 4>;   // 4 waves of 64x32
+constexpr int kNumConfigs = 20;
 
 __device__ __forceinline__ void store_y(void* y, int out_dtype, size_t o, float v) {
   if (out_dtype == VDSL_F32) static_cast<float*>(y)[o] = v;
@@ -66,6 +74,42 @@ __global__ __launch_bounds__(Cfg::NT, 2) void gemm_w8a8_nt(const int8_t* __restr
   i32x16 acc[Cfg::FM][Cfg::FN];
   gemm_mainloop<MfmaI8, Cfg, EDGE>(reinterpret_cast<const char*>(A), reinterpret_cast<const char*>(B), M, N, K, k_begin, k_end,
                              m0, n0, smem, acc);
+#pragma unroll
+  for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = acc_row<Cfg>(m0, i, r), col = acc_col<Cfg>(n0, j);
+        if (row < M && col < N) {
+          const size_t o = static_cast<size_t>(row) * N + col;
+          const int32_t a = acc[i][j][r];
+          if (SPLIT) {
+            atomicAdd(ws_acc + o, a);
+          } else {
+            if (acc_out) acc_out[o] = a;
+            store_y(y, out_dtype, o, dequant(a, xs[row], wsc[col], relu));
+          }
+        }
+      }
+}
+
+// Direct-to-LDS variant (gemm_dma.h); same epilogue and split-K contract as gemm_w8a8_nt.
+template <class Cfg, bool SPLIT>
+__global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_w8a8_dma(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ B, const float* __restrict__ xs, const float* __restrict__ wsc,
+    void* __restrict__ y, int out_dtype, int relu, int32_t* __restrict__ acc_out, int32_t* __restrict__ ws_acc, int M, int N,
+    int K, int k_per) {
+  __shared__ __attribute__((aligned(1024))) char smem[Cfg::LDS_BYTES];
+  const int tiles_m = (M + Cfg::BM - 1) / Cfg::BM, tiles_n = (N + Cfg::BN - 1) / Cfg::BN;
+  int tm, tn;
+  tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * Cfg::BM, n0 = tn * Cfg::BN;
+  const int k_begin = SPLIT ? static_cast<int>(blockIdx.y) * k_per : 0;
+  const int k_end = SPLIT ? (K < k_begin + k_per ? K : k_begin + k_per) : K;
+  i32x16 acc[Cfg::FM][Cfg::FN];
+  dma_mainloop<MfmaI8, Cfg>(reinterpret_cast<const char*>(A), reinterpret_cast<const char*>(B), M, N, K, k_begin, k_end, m0,
+                            n0, smem, acc);
 #pragma unroll
   for (int i = 0; i < Cfg::FM; ++i)
 #pragma unroll
@@ -186,30 +230,33 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restri
 
 int64_t tiles_for(int bm, int bn, int64_t M, int64_t N) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
-// Measured on MI355X over every configuration above (config-5 shapes 512x8192x8192 and the split-K
-// 512x1024x8192): 128x64 tiles (twice the blocks of 128x128 at batch 512) are fastest.
-int choose_config(int64_t M, int64_t N) {
+// Configuration for a shape.  The direct-to-LDS loop (14..) runs when K is a multiple of its
+// 64-byte stage.  Measured on MI355X with random int8 (config-5 shapes): 128x128 blocks of 4
+// waves when they give every CU a block (512x8192x8192: 1030 TOP/s against 1005 for the best
+// register-staged configuration), else 128x64 blocks with split-K (512x1024x8192: 398 against
+// 345).  Other K use the register-staged loop, where 128x64 tiles measured fastest.
+int choose_config(int64_t M, int64_t N, int64_t K) {
+  const bool dma = K % 64 == 0 && K > 0;
   const int o = gemm_config_override();
-  if (o >= 0 && o < kNumConfigs) return o;
-  (void)M;
-  (void)N;
-  return 7;
+  if (o >= 0 && o < kNumConfigs && (o < 14 || dma)) return o;
+  if (!dma) return 7;
+  return ((M + 127) / 128) * ((N + 127) / 128) >= 256 ? 17 : 19;
 }
 
 void config_tile(int c, int& bm, int& bn) {
-  static const int t[kNumConfigs][2] = {{128, 128}, {256, 128}, {128, 256}, {256, 256}, {256, 256},
-                                          {256, 128}, {128, 128}, {128, 64},  {64, 128},  {128, 128},
-                                          {256, 128}, {128, 256}, {256, 256}, {256, 128}};
+  static const int t[kNumConfigs][2] = {{128, 128}, {256, 128}, {128, 256}, {256, 256}, {256, 256}, {256, 128}, {128, 128},
+                                          {128, 64},  {64, 128},  {128, 128}, {256, 128}, {128, 256}, {256, 256}, {256, 128},
+                                          {128, 256}, {256, 256}, {256, 128}, {128, 128}, {128, 256}, {128, 64}};
   bm = t[c][0];
   bn = t[c][1];
 }
 
-// K splits for outputs with too few tiles to fill the 256 CUs (the split-K path).
+// K splits for outputs with fewer tiles than the 256 CUs (the split-K path).
 int split_of(int64_t M, int64_t N, int64_t K) {
   int bm, bn;
-  config_tile(choose_config(M, N), bm, bn);
+  config_tile(choose_config(M, N, K), bm, bn);
   const int64_t tiles = tiles_for(bm, bn, M, N);
-  if (tiles >= 128 || K < 256) return 1;
+  if (tiles >= 256 || K < 256) return 1;
   int64_t s = 256 / tiles;
   const int64_t kt = (K + 127) / 128;
   if (s > kt) s = kt;
@@ -239,9 +286,33 @@ int launch_cfg(const int8_t* a, const int8_t* b, const float* xs, const float* w
   return check_launch("gemm_w8a8_nt<split>");
 }
 
+template <class Cfg>
+int launch_dma(const int8_t* a, const int8_t* b, const float* xs, const float* wsc, void* y, int out_dtype, int relu,
+               int32_t* ao, int32_t* wacc, int m, int n, int k, int split, hipStream_t s) {
+  const int64_t tiles = tiles_for(Cfg::BM, Cfg::BN, m, n);
+  if (split == 1) {
+    hipLaunchKernelGGL((gemm_w8a8_dma<Cfg, false>), dim3(static_cast<unsigned>(tiles), 1), dim3(Cfg::NT), 0, s, a, b, xs, wsc, y,
+                       out_dtype, relu, ao, nullptr, m, n, k, k);
+    return check_launch("gemm_w8a8_dma");
+  }
+  // k_per: a multiple of the 64-byte stage, so with K % 64 == 0 every split is whole stages
+  const int kt = (k + Cfg::BKB - 1) / Cfg::BKB;
+  const int k_per = ((kt + split - 1) / split) * Cfg::BKB;
+  const int nsplit = (k + k_per - 1) / k_per;
+  hipLaunchKernelGGL((gemm_w8a8_dma<Cfg, true>), dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(nsplit)), dim3(Cfg::NT),
+                     0, s, a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, k_per);
+  return check_launch("gemm_w8a8_dma<split>");
+}
+
 int launch_w8a8(const int8_t* a, const int8_t* b, const float* xs, const float* wsc, void* y, int out_dtype, int relu,
                 int32_t* ao, int32_t* wacc, int m, int n, int k, int split, hipStream_t s) {
-  switch (choose_config(m, n)) {
+  switch (choose_config(m, n, k)) {
+    case 14: return launch_dma<Di14>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 15: return launch_dma<Di15>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 16: return launch_dma<Di16>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 17: return launch_dma<Di17>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 18: return launch_dma<Di18>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 19: return launch_dma<Di19>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
     case 1: return launch_cfg<I1>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
     case 2: return launch_cfg<I2>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
     case 3: return launch_cfg<I3>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
