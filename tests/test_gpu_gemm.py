@@ -109,7 +109,9 @@ def test_config4_shape_gemm(dev, q):
 
 
 def test_transpose_and_cast(dev, q):
-    for shape in ((64, 64), (37, 1000), (1, 5), (513, 129)):
+    # odd extents take the element-wise kernel; even bf16 extents the 2x2-pair kernel (one partial
+    # 128x128 tile in each direction for the last two)
+    for shape in ((64, 64), (37, 1000), (1, 5), (513, 129), (2, 2), (130, 258), (256, 2050)):
         x = rng.normal(3, int(np.prod(shape))).reshape(shape)
         for dt, h in (("f32", x), ("bf16", rng.f32_to_bf16(x))):
             ts = Tensor.from_numpy(dev, q, h, dt)

@@ -102,6 +102,31 @@ def test_every_opcode(dev, q):
         np.testing.assert_allclose(got, ref, rtol=REL, atol=1e-30, err_msg=str(prog.code))
 
 
+@pytest.mark.parametrize("cols_pad", [0, 1])
+def test_transcendentals_ranges_and_specials(dev, q, cols_pad):
+    """exp / tanh / sigmoid over their whole f32 range, across the tanh series-to-exponential switch
+    at |u| = 0.4, and at +-inf, NaN, +-0 and results in the subnormal range; cols_pad = 1 makes the
+    row width odd (the one-element path)."""
+    vals = np.concatenate([np.linspace(-110, 95, 4096), np.linspace(-1, 1, 4097), np.linspace(0.39, 0.41, 512),
+                           -np.linspace(0.39, 0.41, 512), np.logspace(-38, 1, 1024), -np.logspace(-38, 1, 1024),
+                           [np.inf, -np.inf, np.nan, 0.0, -0.0, 88.7, 88.8, 89.0, -87.3, -103.0, -104.0]])
+    cols = len(vals) + (len(vals) + cols_pad) % 2  # even or odd row width
+    a = np.zeros((2, cols), np.float32)
+    a[0, :len(vals)] = vals
+    a[1, :len(vals)] = vals[::-1]
+    A = mc.Input(0)
+    for e in (mc.exp(A), mc.tanh(A), mc.sigmoid(A)):
+        prog = mc.compile(e)
+        got = run_chain(dev, q, prog, [a], 2, cols).astype(np.float64)
+        ref = oracle.map_chain(prog, [a], 2, cols).astype(np.float64)
+        assert np.array_equal(np.isnan(got), np.isnan(ref)), str(prog.code)
+        inf = np.isinf(ref)
+        assert np.array_equal(got[inf], ref[inf]), str(prog.code)
+        fin = np.isfinite(ref)
+        # results below the smallest normal f32 may be flushed by the hardware exp2
+        assert np.all(np.abs(got[fin] - ref[fin]) <= REL * np.abs(ref[fin]) + 1.2e-38), str(prog.code)
+
+
 def test_invalid_program_rejected(dev, q):
     prog = mc.compile(spec.map_chain_expr())
     prog.code[1] = ("mul_imm", 9, 0, 0, 0, 1.0)  # register 9 does not exist

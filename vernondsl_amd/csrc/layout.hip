@@ -6,6 +6,11 @@
 // Transpose mapping: a 256-lane block moves one 64x64 tile through LDS.  Reads are coalesced
 // along the source row, writes along the destination row; the tile's LDS rows are padded by one
 // element so the column-wise LDS reads of the write phase fall in different banks.
+//
+// bf16 with even extents takes a 128x128 tile of 2x2 element blocks instead: a lane loads two
+// 4-byte pairs (rows r, r+1 at columns c, c+1), swaps them into the two destination pairs in
+// registers, and the 32-bit pairs go through LDS as a 64x64 tile; every global access is then
+// 4 bytes per lane (the 2-byte form runs at about a quarter of the copy bandwidth).
 
 #include "common.h"
 
@@ -32,6 +37,33 @@ __global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ sr
   }
 }
 
+// bf16, rows and cols even: block (bx, by) covers source rows 128*by.., cols 128*bx...
+__global__ __launch_bounds__(256) void transpose_bf16_pairs(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst,
+                                                            int64_t rows, int64_t cols) {
+  __shared__ uint32_t tile[128][65];  // [dst row within tile][dst column pair]
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 128, c0 = static_cast<int64_t>(blockIdx.x) * 128;
+  const int64_t cp = cols / 2, rp = rows / 2;  // pairs per source row, per destination row
+#pragma unroll 4
+  for (int p = 0; p < 16; ++p) {
+    const int q = ty + 4 * p;  // source row pair within the tile
+    const int64_t r = r0 + 2 * q, c = c0 + 2 * tx;
+    if (r < rows && c < cols) {
+      const uint32_t a = src[r * cp + c / 2];        // (x[r][c], x[r][c+1])
+      const uint32_t b = src[(r + 1) * cp + c / 2];  // (x[r+1][c], x[r+1][c+1])
+      tile[2 * tx][q] = (a & 0xFFFFu) | (b << 16);            // dst row c:   (x[r][c], x[r+1][c])
+      tile[2 * tx + 1][q] = (a >> 16) | (b & 0xFFFF0000u);    // dst row c+1: (x[r][c+1], x[r+1][c+1])
+    }
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int p = 0; p < 32; ++p) {
+    const int row = ty + 4 * p;  // destination row within the tile
+    const int64_t c = c0 + row, r = r0 + 2 * tx;
+    if (c < cols && r < rows) dst[c * rp + r / 2] = tile[row][tx];
+  }
+}
+
 __global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* __restrict__ s, uint16_t* __restrict__ d, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
     d[i] = f32_to_bf16(s[i]);
@@ -46,6 +78,13 @@ __global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __rest
 
 int launch_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int dtype, hipStream_t s) {
   if (rows == 0 || cols == 0) return VDSL_OK;
+  if (dtype == VDSL_BF16 && rows % 2 == 0 && cols % 2 == 0) {
+    const int64_t bx = (cols + 127) / 128, by = (rows + 127) / 128;
+    if (bx > 0x7fffffff || by > 65535) return fail(VDSL_ERR_UNSUPPORTED, "transpose: tensor too large");
+    hipLaunchKernelGGL(transpose_bf16_pairs, dim3(static_cast<unsigned>(bx), static_cast<unsigned>(by)), dim3(256), 0, s,
+                       static_cast<const uint32_t*>(src), static_cast<uint32_t*>(dst), rows, cols);
+    return check_launch("transpose_bf16_pairs");
+  }
   const int64_t gx = (cols + 63) / 64, gy = (rows + 63) / 64;
   if (gx > 0x7fffffff || gy > 65535) return fail(VDSL_ERR_UNSUPPORTED, "transpose: tensor too large");
   const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
