@@ -329,6 +329,57 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
     return res
 
 
+# ---- HBM traffic from counter passes ----------------------------------------------------------------
+# name in --kernel mode -> (substring of the profiled kernel's name, algorithmic bytes per launch)
+def _traffic_kernels():
+    from vernondsl_amd import _lib, spec
+    return {
+        "copy": ("copyBuffer", 2 * (512 << 20)),
+        "map_chain": ("map_chain_kernel", spec.map_chain_bytes(8192, 8192)),
+        "softmax_f32": ("row_softmax_resident<0", spec.softmax_bytes(16384, 4096, _lib.F32)),
+        "softmax_bf16": ("row_softmax_resident<1", spec.softmax_bytes(16384, 4096, _lib.BF16)),
+        # A, B read once; bf16 H and f32 pre-activation written once
+        "gemm_bf16": ("gemm_bf16_", 2 * (2048 * 4096 + 4096 * 4096 + 2048 * 4096) + 4 * 2048 * 4096),
+        # int8 A, B and the two scale vectors read once; bf16 Y written once
+        "gemm_w8a8": ("gemm_w8a8_", 512 * 8192 + 8192 * 8192 + 4 * (512 + 8192) + 2 * 512 * 8192),
+    }
+
+
+def traffic_summary(run_dir):
+    """Builds profiles/traffic.json from the rocprofv3 counter runs in run_dir (one directory per
+    kernel and counter, traffic_<kernel>_<FETCH_SIZE|WRITE_SIZE>/run_counter_collection.csv, as the
+    commands in profiles/traffic_counters.md write them) and prints the summary table.  Each
+    counter is scaled so that it reads the known traffic of the 512 MiB copy."""
+    import csv
+    def per_dispatch(kernel, counter, name_part):
+        path = os.path.join(run_dir, f"traffic_{kernel}_{counter}", "run_counter_collection.csv")
+        vals = [float(r["Counter_Value"]) for r in csv.DictReader(open(path))
+                if name_part in r["Kernel_Name"] and r["Counter_Name"] == counter]
+        if not vals:
+            raise SystemExit(f"{path}: no dispatch of a kernel named *{name_part}*")
+        return sum(vals) / len(vals)
+    ks = _traffic_kernels()
+    cf = per_dispatch("copy", "FETCH_SIZE", ks["copy"][0])
+    cw = per_dispatch("copy", "WRITE_SIZE", ks["copy"][0])
+    half = (512 << 20) / 1024  # KiB read and KiB written by the copy
+    ff, wf = half / cf, half / cw
+    out = {"fetch_factor": round(ff, 4), "write_factor": round(wf, 4), "kernels": {}}
+    rows = []
+    for k, (part, alg) in ks.items():
+        if k == "copy":
+            continue
+        f, w = per_dispatch(k, "FETCH_SIZE", part), per_dispatch(k, "WRITE_SIZE", part)
+        t = (f * ff + w * wf) * 1024
+        out["kernels"][k] = {"traffic_bytes": int(round(t)), "algorithmic_bytes": alg, "fetch_kib": f, "write_kib": w}
+        rows.append(f"| {k} | {f:.0f} | {w:.0f} | {int(round(t)):,} | {alg:,} | {t / alg:.3f} |")
+    with open(os.path.join(ROOT, "profiles", "traffic.json"), "w") as fh:
+        json.dump(out, fh, indent=1)
+    print(f"copy: FETCH_SIZE {cf:.0f} KiB, WRITE_SIZE {cw:.0f} KiB per dispatch -> factors {ff:.4f}, {wf:.4f}")
+    print("| Kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | Traffic (scaled) B | Algorithmic B | Traffic / algorithmic |")
+    print("|---|---|---|---|---|---|")
+    print("\n".join(rows))
+
+
 # ---- single-kernel mode (for rocprofv3 counter passes) ---------------------------------------------
 def run_kernel_only(dev, q, name, reps):
     """Runs one kernel `reps` times on the config's shape and nothing else (no parity, no CPU):
@@ -390,8 +441,13 @@ def main():
     ap.add_argument("--kernel", default="", help="run one kernel --reps times and exit (for rocprofv3 --pmc): "
                     "map_chain, softmax_f32, softmax_bf16, gemm_bf16, gemm_w8a8, escape_time, copy")
     ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--traffic-summary", default="", metavar="DIR",
+                    help="write profiles/traffic.json from the counter runs in DIR and exit (no GPU needed)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.traffic_summary:
+        traffic_summary(args.traffic_summary)
+        return
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each config would shard rows or "
               "batch across GPUs with no exchange except config 4's gradient all-reduce; not built). "

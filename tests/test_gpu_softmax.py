@@ -42,8 +42,10 @@ def check(xh, got, ref, bf16):
 
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("cols", [4096, 256, 512, 1000, 8192, 3])
-def test_softmax_shapes(dev, q, cols, bf16):
-    x, _, _ = spec.softmax_inputs(rows=130, cols=cols)
+@pytest.mark.parametrize("rows", [130, 160])
+def test_softmax_shapes(dev, q, cols, bf16, rows):
+    """Row counts that fill the last 4-row block partially (130) and exactly (160)."""
+    x, _, _ = spec.softmax_inputs(rows=rows, cols=cols)
     xh = rng.f32_to_bf16(x) if bf16 else x
     got = run(dev, q, xh, "bf16" if bf16 else "f32")
     check(xh, got, oracle.row_reduce_softmax(xh), bf16)
@@ -70,10 +72,11 @@ def test_config3_full_size(dev, q, bf16):
     assert np.array_equal(gm, xf.max(axis=1))
 
 
-def test_only_some_outputs_and_empty(dev, q):
-    x = np.random.default_rng(4).standard_normal((8, 4096)).astype(np.float32)
+@pytest.mark.parametrize("nrows", [8, 16])
+def test_only_some_outputs_and_empty(dev, q, nrows):
+    x = np.random.default_rng(4).standard_normal((nrows, 4096)).astype(np.float32)
     tx = Tensor.from_numpy(dev, q, x)
-    m = Tensor(dev, (8,), "f32")
+    m = Tensor(dev, (nrows,), "f32")
     kernels.row_reduce_softmax(q, tx, row_max=m)
     assert np.array_equal(m.numpy(q), x.max(axis=1))
     e = Tensor(dev, (0, 16), "f32")
