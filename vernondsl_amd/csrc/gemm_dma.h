@@ -145,6 +145,16 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
     __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);                                      \
     __builtin_amdgcn_sched_barrier(0);                                                            \
   } while (0)
+// First k-step of a stage: one MFMA ahead of the reads.  At the loop top the compiler waits for
+// every outstanding LDS read before the first MFMA (lgkmcnt(0)); issuing the next k-step's reads
+// after that MFMA keeps them out of that wait.
+#define VDSL_DMA_ORDER_LATE()                                                                     \
+  do {                                                                                            \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                            \
+    __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);                                      \
+    __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - 1, 0);                                  \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+  } while (0)
 
   const int nk = (kb_end - kb_begin) / Cfg::BKB;
   if (nk <= 0) return;
@@ -164,7 +174,7 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
     __builtin_amdgcn_sched_barrier(0);
     VDSL_DMA_READ(a1, b1, st, 1);
     VDSL_DMA_MMA(a0, b0);
-    VDSL_DMA_ORDER();
+    VDSL_DMA_ORDER_LATE();
     VDSL_WAIT_VM_LGKM0((NS - 2) * BPW);
     dma_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -175,6 +185,7 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
   }
   // Drain the copies of the stages past the end before the block's LDS can be reused or freed.
   VDSL_WAIT_VM_LGKM0(0);
+#undef VDSL_DMA_ORDER_LATE
 #undef VDSL_DMA_ORDER
 #undef VDSL_DMA_MMA
 #undef VDSL_DMA_READ

@@ -39,9 +39,9 @@ using I13 = GemmConfig<MfmaI8, 256, 128, 64, 4, 2>;  // 8 waves, wave tile 64x64
 // Direct-to-LDS loop (gemm_dma.h), configurations 14..: <BM, BN, WGM, WGN, LDS stages>
 using Di14 = DmaConfig<MfmaI8, 128, 256, 2, 4, 4>;  // 8 waves of 64x64
 using Di15 = DmaConfig<MfmaI8, 256, 256, 2, 4, 3>;  // 8 waves of 128x64
-using Di16 = DmaConfig<MfmaI8, 256, 128, 4, 2, 4>;  // 8 waves of 64x64
+using Di16 = DmaConfig<MfmaI8, 64, 128, 2, 2, 4>;   // 4 waves of 32x64, two blocks per CU
 using Di17 = DmaConfig<MfmaI8, 128, 128, 2, 2, 4>;  // 4 waves of 64x64, 2 blocks per CU
-using Di18 = DmaConfig<MfmaI8, 128, 256, 2, 2, 4>;  // 4 waves of 64x128
+using Di18 = DmaConfig<MfmaI8, 128, 128, 2, 4, 4>;  // 8 waves of 64x32
 using Di19 = DmaConfig<MfmaI8, 128, 64, 2, 2, 4>;   // 4 waves of 64x32
 constexpr int kNumConfigs = 20;
 
@@ -231,22 +231,22 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restri
 int64_t tiles_for(int bm, int bn, int64_t M, int64_t N) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
 // Configuration for a shape.  The direct-to-LDS loop (14..) runs when K is a multiple of its
-// 64-byte stage.  Measured on MI355X with random int8 (config-5 shapes): 128x128 blocks of 4
-// waves when they give every CU a block (512x8192x8192: 1030 TOP/s against 1005 for the best
-// register-staged configuration), else 128x64 blocks with split-K (512x1024x8192: 398 against
-// 345).  Other K use the register-staged loop, where 128x64 tiles measured fastest.
+// 64-byte stage.  Measured on MI355X with random int8 (config-5 shapes): 128x128 blocks of 8
+// waves when they give every CU a block (512x8192x8192: 1198 TOP/s; 4 waves: 1154; the best
+// register-staged configuration: 1005), else 64x128 blocks with split-K (512x1024x8192: 450
+// against 345).  Other K use the register-staged loop, where 128x64 tiles measured fastest.
 int choose_config(int64_t M, int64_t N, int64_t K) {
   const bool dma = K % 64 == 0 && K > 0;
   const int o = gemm_config_override();
   if (o >= 0 && o < kNumConfigs && (o < 14 || dma)) return o;
   if (!dma) return 7;
-  return ((M + 127) / 128) * ((N + 127) / 128) >= 256 ? 17 : 19;
+  return ((M + 127) / 128) * ((N + 127) / 128) >= 256 ? 18 : 16;
 }
 
 void config_tile(int c, int& bm, int& bn) {
   static const int t[kNumConfigs][2] = {{128, 128}, {256, 128}, {128, 256}, {256, 256}, {256, 256}, {256, 128}, {128, 128},
                                           {128, 64},  {64, 128},  {128, 128}, {256, 128}, {128, 256}, {256, 256}, {256, 128},
-                                          {128, 256}, {256, 256}, {256, 128}, {128, 128}, {128, 256}, {128, 64}};
+                                          {128, 256}, {256, 256}, {64, 128},  {128, 128}, {128, 128}, {128, 64}};
   bm = t[c][0];
   bn = t[c][1];
 }
