@@ -112,6 +112,21 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
   return v;
 }
+// exp in f32, Cody-Waite style: n log2(e) = t + r with t = fl(n * log2e) and r its rounding
+// residual (exact through an fma, plus the low part of log2 e), then e^n = 2^t (1 + r ln 2) with
+// the hardware exp2.  Where t is not finite (n = +-inf, NaN) or 2^t overflows, 2^t itself is the
+// answer (inf, 0 or NaN) and the correction, which would form inf * 0, is skipped.  Relative
+// error below 2e-7 in an f32 emulation of these steps (against exp in f64 over [-87, 88]), plus
+// the hardware exp2's 1 ulp.
+__device__ __forceinline__ float exp_fast(float n) {
+  const float t = n * 1.4426950408889634f;
+  float r = __builtin_fmaf(n, 1.4426950408889634f, -t);
+  r = __builtin_fmaf(n, 1.92596299e-08f, r);  // log2(e) - fl(log2(e))
+  const float e = __builtin_amdgcn_exp2f(t);
+  const float c = __builtin_fmaf(e, r * 0.6931471805599453f, e);
+  return (__builtin_isfinite(t) && e != __builtin_inff()) ? c : e;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));

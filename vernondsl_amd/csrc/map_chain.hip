@@ -39,21 +39,6 @@ struct MapIn {
   int32_t n;
 };
 
-// exp in f32, Cody-Waite style: n log2(e) = t + r with t = fl(n * log2e) and r its rounding
-// residual (exact through an fma, plus the low part of log2 e), then e^n = 2^t (1 + r ln 2) with
-// the hardware exp2.  Where t is not finite (n = +-inf, NaN) or 2^t overflows, 2^t itself is the
-// answer (inf, 0 or NaN) and the correction, which would form inf * 0, is skipped.  Relative
-// error below 2e-7 in an f32 emulation of these steps (against exp in f64 over [-87, 88]), plus
-// the hardware exp2's 1 ulp.
-__device__ __forceinline__ float exp_fast(float n) {
-  const float t = n * 1.4426950408889634f;
-  float r = __builtin_fmaf(n, 1.4426950408889634f, -t);
-  r = __builtin_fmaf(n, 1.92596299e-08f, r);  // log2(e) - fl(log2(e))
-  const float e = __builtin_amdgcn_exp2f(t);
-  const float c = __builtin_fmaf(e, r * 0.6931471805599453f, e);
-  return (__builtin_isfinite(t) && e != __builtin_inff()) ? c : e;
-}
-
 // tanh in f32 without the argument-range branches of the library tanhf (which diverge per lane):
 //   |u| < 0.4:  Taylor series u (1 + z (c1 + z (c2 + ... + z c5))), z = u^2, with the exact
 //               coefficients c_k of tanh's expansion (-1/3, 2/15, -17/315, 62/2835, -1382/155925);

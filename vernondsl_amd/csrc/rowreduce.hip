@@ -3,7 +3,9 @@
 // No reference code (the north-star op class).  Semantics, shared with the CPU oracle:
 //   row_sum = sum_j x[j] accumulated in f64, rounded once to f32;
 //   row_max = max_j x[j] (exact);
-//   softmax[j] = e[j] / s,  e[j] = expf(x[j] - row_max) in f32,  s = f64 sum of e rounded to f32.
+//   softmax[j] = e[j] / s,  e[j] = exp(x[j] - row_max) in f32,  s = f64 sum of e rounded to f32.
+// (The register-resident kernel evaluates exp with the branch-free exp_fast of common.h, within
+// a few ulp of the library expf that the generic kernel and the oracle use.)
 // The register-resident kernel multiplies by 1/s instead of dividing (within one ulp of e/s) and
 // forms its sums as f32 partials of 4 or 8 elements added into f64 accumulators; both stay far
 // inside the op's 1e-5 (f32) / 1e-2 (bf16) tolerances and cut the VALU work per element, which
@@ -105,7 +107,7 @@ __global__ __launch_bounds__(256) void row_softmax_resident(const void* __restri
     float part = 0.0f;
 #pragma unroll
     for (int e = 0; e < PV; ++e) {
-      v[k][e] = expf(v[k][e] - m);
+      v[k][e] = exp_fast(v[k][e] - m);
       part += v[k][e];
     }
     es += static_cast<double>(part);
