@@ -288,6 +288,11 @@ int vdsl_op_transpose(vdsl_queue q, int64_t rows, int64_t cols, int32_t dtype, v
 int vdsl_op_cast(vdsl_queue q, int64_t n, int32_t src_dtype, vdsl_buffer src, int32_t dst_dtype,
                  vdsl_buffer dst);
 
+/* Elementwise GELU, y = 0.5 x (1 + erf(x / sqrt 2)) (the exact-erf form; no reference code, north
+ * star op class 4, which fuses it into the GEMM epilogue; this is the standalone op).  x: F32 or
+ * BF16 [n];  y: F32 or BF16 [n];  in-place (x == y, same dtype) is allowed. */
+int vdsl_op_gelu_fwd(vdsl_queue q, int64_t n, int32_t x_dtype, vdsl_buffer x, int32_t y_dtype, vdsl_buffer y);
+
 /* Autodiff building blocks for the MLP graph (no reference code; north star). */
 /* GELU backward: da (bf16 [rows][cols]) = dh (f32) * GELU'(pre) (f32);  da_t (optional, bf16
  * [cols][rows]) receives the transpose of da. */

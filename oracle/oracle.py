@@ -69,6 +69,7 @@ _lib.orc_col_reduce.argtypes = [_i64, _i64, C.c_int, _vp, _vp, _vp]
 _lib.orc_gemm_bf16_rows.argtypes = [C.c_int, C.c_int, _i64, _i64, _i64, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _i64, _i64]
 _lib.orc_transpose.argtypes = [_i64, _i64, C.c_int, _vp, _vp]
 _lib.orc_cast.argtypes = [_i64, C.c_int, _vp, C.c_int, _vp]
+_lib.orc_gelu_fwd.argtypes = [_i64, C.c_int, _vp, C.c_int, _vp]
 _lib.orc_gelu_bwd.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp]
 _lib.orc_mse_fwd_bwd.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp, _vp]
 _lib.orc_quantize_rows_i8.argtypes = [_i64, _i64, C.c_int, _vp, _vp, _vp]
@@ -173,6 +174,17 @@ def cast(x: np.ndarray, dst_dtype: int) -> np.ndarray:
     out = np.zeros(x.shape, np.uint16 if dst_dtype == BF16 else np.float32)
     _lib.orc_cast(x.size, _dt(x), _p(x), dst_dtype, _p(out))
     return out
+
+
+def gelu_fwd(x: np.ndarray, y_bf16: bool = False):
+    """GELU(x) elementwise; x f32, or uint16 holding bf16; returns f32 or (y_bf16) uint16 bf16."""
+    x = np.ascontiguousarray(x)
+    xd = 1 if x.dtype == np.uint16 else 0
+    if xd == 0:
+        x = x.astype(np.float32, copy=False)
+    y = np.zeros(x.shape, np.uint16 if y_bf16 else np.float32)
+    _lib.orc_gelu_fwd(x.size, xd, _p(x), 1 if y_bf16 else 0, _p(y))
+    return y
 
 
 def gelu_bwd(dh: np.ndarray, pre: np.ndarray):

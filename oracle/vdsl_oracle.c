@@ -22,7 +22,7 @@
  *                        constant row -> 1/cols, shift invariance, injected outlier argmax.
  *   orc_gemm_bf16        no reference code.  Pinned by exact integer-valued products (bf16
  *                        small integers), brute force in Python integers, and numpy f64.
- *   orc_gelu_bwd / orc_mse_fwd_bwd
+ *   orc_gelu_fwd / orc_gelu_bwd / orc_mse_fwd_bwd
  *                        no reference code.  Pinned by central finite differences in f64.
  *   orc_quantize_rows_i8 / orc_gemm_w8a8
  *                        no reference code.  Pinned by int64 numpy dot products (exact) and a
@@ -318,6 +318,18 @@ void orc_cast(int64_t n, int src_dtype, const void* src, int dst_dtype, void* ds
 }
 
 /* ---- autodiff blocks --------------------------------------------------------------------- */
+
+/* Elementwise GELU (x_dtype, y_dtype: 0 = f32, 1 = bf16): f64 evaluation of the exact-erf form,
+ * rounded once to f32 (then RNE to bf16 when y is bf16). */
+void orc_gelu_fwd(int64_t n, int x_dtype, const void* x, int y_dtype, void* y) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    const float v = x_dtype == 0 ? ((const float*)x)[i] : bf16_to_f32(((const uint16_t*)x)[i]);
+    const float g = (float)gelu_d((double)v);
+    if (y_dtype == 0) ((float*)y)[i] = g;
+    else ((uint16_t*)y)[i] = f32_to_bf16(g);
+  }
+}
 
 /* d/dv GELU(v) = Phi(v) + v phi(v) = 0.5 erfc(-v/sqrt2) + v exp(-v^2/2) / sqrt(2 pi), in f64. */
 static double gelu_grad_d(double v) {

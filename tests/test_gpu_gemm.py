@@ -108,6 +108,31 @@ def test_config4_shape_gemm(dev, q):
         assert_gemm_close(pre[r:r + 1], rpre, mag)
 
 
+@pytest.mark.parametrize("xdt,ydt", [("f32", "f32"), ("f32", "bf16"), ("bf16", "f32"), ("bf16", "bf16")])
+def test_gelu_fwd(dev, q, xdt, ydt):
+    x = np.concatenate([np.random.default_rng(7).normal(0, 3, 10000), np.linspace(-12, 12, 2001),
+                        [0.0, -0.0, np.inf, -np.inf, np.nan, 1e-30, -1e-30, 30.0, -30.0]]).astype(np.float32)
+    xh = rng.f32_to_bf16(x) if xdt == "bf16" else x
+    tx = Tensor.from_numpy(dev, q, xh, xdt)
+    ty = Tensor(dev, x.shape, ydt)
+    kernels.gelu_fwd(q, tx, ty)
+    got = ty.numpy(q)
+    ref = oracle.gelu_fwd(xh, y_bf16=(ydt == "bf16"))
+    g = (rng.bf16_to_f32(got) if ydt == "bf16" else got).astype(np.float64)
+    r = (rng.bf16_to_f32(ref) if ydt == "bf16" else ref).astype(np.float64)
+    assert np.array_equal(np.isnan(g), np.isnan(r))
+    fin = ~np.isnan(r)
+    tol = 1e-2 if ydt == "bf16" else 1e-5
+    bad = np.abs(g[fin] - r[fin]) > tol * np.abs(r[fin]) + 1e-37
+    xf = (rng.bf16_to_f32(xh) if xdt == "bf16" else xh)[fin]
+    assert not bad.any(), list(zip(xf[bad][:5].tolist(), g[fin][bad][:5].tolist(), r[fin][bad][:5].tolist()))
+    if xdt == ydt:  # in place
+        kernels.gelu_fwd(q, tx, tx)
+        assert np.array_equal(tx.numpy(q), got, equal_nan=True) if ydt == "f32" else np.array_equal(tx.numpy(q), got)
+    tx.free()
+    ty.free()
+
+
 def test_transpose_and_cast(dev, q):
     # odd extents take the element-wise kernel; even bf16 extents the 2x2-pair kernel (one partial
     # 128x128 tile in each direction for the last two)

@@ -70,6 +70,24 @@ def test_bf16_rounding_is_nearest_even():
     assert np.array_equal(got, rng.f32_to_bf16(vals))
 
 
+def test_gelu_fwd_known_values_and_odd_part_identity():
+    """GELU(x) - GELU(-x) = x (Phi(x) + Phi(-x) = 1): a dropped term, a wrong sign or erf in
+    place of erfc breaks it; plus closed-form values and bf16 in/out rounding."""
+    x = np.linspace(-8, 8, 4001).astype(np.float32)
+    g = oracle.gelu_fwd(x).astype(np.float64)
+    gm = oracle.gelu_fwd(-x).astype(np.float64)
+    assert np.all(np.abs((g - gm) - x.astype(np.float64)) <= 2 * np.spacing(np.abs(x).astype(np.float32)) + 1e-30)
+    # scipy's erfc (an implementation independent of the C library's) in the cancellation-free form
+    ref = 0.5 * x.astype(np.float64) * erfc(-x.astype(np.float64) / np.sqrt(2))
+    assert np.all(np.abs(g - ref) <= 1e-6 * np.abs(ref) + 1e-30)
+    assert oracle.gelu_fwd(np.array([0.0, 1.0, -1.0], np.float32)).tolist() == [
+        0.0, np.float32(0.8413447460685429), np.float32(-0.15865525393145707)]
+    # bf16 input is widened exactly; bf16 output is the RNE of the f32 result
+    xb = rng.f32_to_bf16(x)
+    assert np.array_equal(oracle.gelu_fwd(xb), oracle.gelu_fwd(rng.bf16_to_f32(xb)))
+    assert np.array_equal(oracle.gelu_fwd(x, y_bf16=True), rng.f32_to_bf16(oracle.gelu_fwd(x)))
+
+
 def test_gelu_bwd_matches_finite_differences():
     pre = np.linspace(-4, 4, 64 * 48).astype(np.float32).reshape(64, 48)
     dh = np.ones_like(pre)

@@ -10,6 +10,8 @@
 // partial sum, then one block adds the partials in tile order - and dy = (y - t) * (2 / n) in
 // f32, rounded to bf16.
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace vdsl {
@@ -122,6 +124,40 @@ extern "C" int vdsl_op_gelu_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_b
 extern "C" int64_t vdsl_mse_partials_count(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
   return 2 * tiles_of(rows, cols);  // one f64 (two f32 slots) per 64x64 tile
+}
+
+namespace vdsl {
+namespace {
+// Grid-stride elementwise GELU (erfc form, branch-free; the accurate variant, since f32 results
+// are held to 1e-5 relative).
+template <int XT, int YT>
+__global__ __launch_bounds__(256) void gelu_fwd_kernel(const void* __restrict__ x, void* __restrict__ y, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256) {
+    const float v = XT == VDSL_F32 ? static_cast<const float*>(x)[i] : bf16_to_f32(static_cast<const uint16_t*>(x)[i]);
+    const float g = gelu_f_acc(v);
+    if (YT == VDSL_F32) static_cast<float*>(y)[i] = g;
+    else static_cast<uint16_t*>(y)[i] = f32_to_bf16(g);
+  }
+}
+}  // namespace
+}  // namespace vdsl
+
+extern "C" int vdsl_op_gelu_fwd(vdsl_queue q, int64_t n, int32_t x_dtype, vdsl_buffer x, int32_t y_dtype, vdsl_buffer y) {
+  VDSL_TRY(enter_queue(q));
+  if (n < 0) return fail(VDSL_ERR_INVALID_ARG, "negative element count");
+  const bool ok = (x_dtype == VDSL_F32 || x_dtype == VDSL_BF16) && (y_dtype == VDSL_F32 || y_dtype == VDSL_BF16);
+  if (!ok) return fail(VDSL_ERR_UNSUPPORTED, "gelu_fwd supports f32 and bf16");
+  VDSL_TRY(check_buffer(q, x, static_cast<size_t>(n) * dtype_size(x_dtype), "x", false));
+  VDSL_TRY(check_buffer(q, y, static_cast<size_t>(n) * dtype_size(y_dtype), "y", true));
+  if (x == y && x_dtype != y_dtype) return fail(VDSL_ERR_INVALID_ARG, "in-place gelu_fwd needs one dtype");
+  if (n == 0) return VDSL_OK;
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256, 256 * 32);
+  const dim3 g(static_cast<unsigned>(blocks)), b(256);
+  if (x_dtype == VDSL_F32 && y_dtype == VDSL_F32) hipLaunchKernelGGL((gelu_fwd_kernel<VDSL_F32, VDSL_F32>), g, b, 0, q->stream, x->ptr, y->ptr, n);
+  else if (x_dtype == VDSL_F32) hipLaunchKernelGGL((gelu_fwd_kernel<VDSL_F32, VDSL_BF16>), g, b, 0, q->stream, x->ptr, y->ptr, n);
+  else if (y_dtype == VDSL_F32) hipLaunchKernelGGL((gelu_fwd_kernel<VDSL_BF16, VDSL_F32>), g, b, 0, q->stream, x->ptr, y->ptr, n);
+  else hipLaunchKernelGGL((gelu_fwd_kernel<VDSL_BF16, VDSL_BF16>), g, b, 0, q->stream, x->ptr, y->ptr, n);
+  return check_launch("gelu_fwd_kernel");
 }
 
 extern "C" int vdsl_op_mse_fwd_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer y, vdsl_buffer t, vdsl_buffer loss,

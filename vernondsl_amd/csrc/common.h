@@ -127,6 +127,61 @@ __device__ __forceinline__ float exp_fast(float n) {
   return (__builtin_isfinite(t) && e != __builtin_inff()) ? c : e;
 }
 
+// erfc(x) by the Chebyshev-fitted form of Numerical Recipes (Press et al., 2nd ed., sec. 6.2,
+// "erfcc"): erfc(|x|) = t exp(-x^2 + P(t)), t = 1 / (1 + |x|/2), P a degree-9 polynomial, with
+// fractional error below 1.2e-7 for every x; erfc(-x) = 2 - erfc(x).  Branch-free (the library
+// erfcf picks among argument ranges per lane), which matters in a GEMM epilogue that evaluates it
+// on every output element.
+__device__ __forceinline__ float erfc_cheb(float x) {
+  const float z = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = __builtin_fmaf(p, t, -0.82215223f);
+  p = __builtin_fmaf(p, t, 1.48851587f);
+  p = __builtin_fmaf(p, t, -1.13520398f);
+  p = __builtin_fmaf(p, t, 0.27886807f);
+  p = __builtin_fmaf(p, t, -0.18628806f);
+  p = __builtin_fmaf(p, t, 0.09678418f);
+  p = __builtin_fmaf(p, t, 0.37409196f);
+  p = __builtin_fmaf(p, t, 1.00002368f);
+  p = __builtin_fmaf(p, t, -1.26551223f);
+  const float r = t * __expf(__builtin_fmaf(-z, z, p));
+  return x >= 0.0f ? r : 2.0f - r;
+}
+
+// 0.5 v (1 + erf(v / sqrt2)) written as 0.5 v erfc(-v / sqrt2): no cancellation for v < 0.
+// Used where the result is rounded to bf16 (the GEMM epilogue): erfc_cheb rounds its exponent
+// -x^2 + P once, an absolute error of up to ulp(x^2)/2, i.e. a relative error growing like
+// x^2 2^-24 (4e-6 at |x| = 8.5), far below bf16 resolution.
+__device__ __forceinline__ float gelu_f(float v) { return 0.5f * v * erfc_cheb(-v * 0.7071067811865476f); }
+
+// GELU for f32 results (the standalone elementwise op), relative accuracy ~1e-6 over the f32
+// range.  With z = |v|/sqrt2 and erfc(z) = t exp(-z^2 + P(t)) as above, the exponent is the
+// sensitive part (erfc's condition number is ~2 z^2), so it is never formed from a rounded z:
+// z^2 = v^2 / 2 = (h + l) / 2 with h = fl(v v) and l = v v - h exact (one fma), and
+// exp(-z^2 + P) = exp(-h/2) exp(P) (1 - l/2), both exponentials by exp_fast.  Only t, where
+// the sensitivity is small, uses the rounded z.
+__device__ __forceinline__ float gelu_f_acc(float v) {
+  const float a = fabsf(v);
+  const float z = a * 0.7071067811865476f;
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = __builtin_fmaf(p, t, -0.82215223f);
+  p = __builtin_fmaf(p, t, 1.48851587f);
+  p = __builtin_fmaf(p, t, -1.13520398f);
+  p = __builtin_fmaf(p, t, 0.27886807f);
+  p = __builtin_fmaf(p, t, -0.18628806f);
+  p = __builtin_fmaf(p, t, 0.09678418f);
+  p = __builtin_fmaf(p, t, 0.37409196f);
+  p = __builtin_fmaf(p, t, 1.00002368f);
+  p = __builtin_fmaf(p, t, -1.26551223f);
+  const float h = a * a;
+  const float l = __builtin_isfinite(h) ? __builtin_fmaf(a, a, -h) : 0.0f;  // inf - inf would be NaN
+  const float c = (exp_fast(-0.5f * h) * exp_fast(p)) * t;
+  const float e = __builtin_fmaf(c, -0.5f * l, c);  // erfc(|v| / sqrt2)
+  return 0.5f * v * (v <= 0.0f ? e : 2.0f - e);     // erfc(-v / sqrt2)
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));

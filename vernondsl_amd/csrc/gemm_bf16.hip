@@ -30,30 +30,6 @@ int gemm_config_override() {
 
 namespace {
 
-// erfc(x) by the Chebyshev-fitted form of Numerical Recipes (Press et al., 2nd ed., sec. 6.2,
-// "erfcc"): erfc(|x|) = t exp(-x^2 + P(t)), t = 1 / (1 + |x|/2), P a degree-9 polynomial, with
-// fractional error below 1.2e-7 for every x; erfc(-x) = 2 - erfc(x).  Branch-free (the library
-// erfcf picks among argument ranges per lane), which matters in a GEMM epilogue that evaluates it
-// on every output element.
-__device__ __forceinline__ float erfc_cheb(float x) {
-  const float z = fabsf(x);
-  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, z, 1.0f));
-  float p = 0.17087277f;
-  p = __builtin_fmaf(p, t, -0.82215223f);
-  p = __builtin_fmaf(p, t, 1.48851587f);
-  p = __builtin_fmaf(p, t, -1.13520398f);
-  p = __builtin_fmaf(p, t, 0.27886807f);
-  p = __builtin_fmaf(p, t, -0.18628806f);
-  p = __builtin_fmaf(p, t, 0.09678418f);
-  p = __builtin_fmaf(p, t, 0.37409196f);
-  p = __builtin_fmaf(p, t, 1.00002368f);
-  p = __builtin_fmaf(p, t, -1.26551223f);
-  const float r = t * __expf(__builtin_fmaf(-z, z, p));
-  return x >= 0.0f ? r : 2.0f - r;
-}
-
-// 0.5 v (1 + erf(v / sqrt2)) written as 0.5 v erfc(-v / sqrt2): no cancellation for v < 0.
-__device__ __forceinline__ float gelu_f(float v) { return 0.5f * v * erfc_cheb(-v * 0.7071067811865476f); }
 
 // Tile configurations (block M x N, K bytes per stage, wave grid).
 using Bf0 = GemmConfig<MfmaBf16, 128, 128, 128, 2, 2>;  // wave tile 64x64
@@ -73,9 +49,9 @@ using Bf13 = GemmConfig<MfmaBf16, 256, 128, 64, 4, 2>;  // 8 waves, wave tile 64
 // Direct-to-LDS loop (gemm_dma.h), configurations 14..: <BM, BN, WGM, WGN, LDS stages>
 using Dm14 = DmaConfig<MfmaBf16, 128, 256, 2, 4, 4>;  // 8 waves of 64x64
 using Dm15 = DmaConfig<MfmaBf16, 256, 256, 2, 4, 3>;  // 8 waves of 128x64
-using Dm16 = DmaConfig<MfmaBf16, 256, 128, 4, 2, 4>;  // 8 waves of 64x64
+using Dm16 = DmaConfig<MfmaBf16, 128, 256, 2, 4, 3>;  // 8 waves of 64x64, 3 LDS stages
 using Dm17 = DmaConfig<MfmaBf16, 128, 128, 2, 2, 4>;  // 4 waves of 64x64, 2 blocks per CU
-using Dm18 = DmaConfig<MfmaBf16, 128, 256, 2, 2, 4>;  // 4 waves of 64x128
+using Dm18 = DmaConfig<MfmaBf16, 128, 256, 2, 4, 5>;  // 8 waves of 64x64, 5 LDS stages
 using Dm19 = DmaConfig<MfmaBf16, 256, 128, 2, 2, 4>;  // 4 waves of 128x64
 constexpr int kNumConfigs = 20;
 

@@ -71,6 +71,7 @@ VDSL_DMA_WAIT_CASE(3)
 VDSL_DMA_WAIT_CASE(4)
 VDSL_DMA_WAIT_CASE(6)
 VDSL_DMA_WAIT_CASE(8)
+VDSL_DMA_WAIT_CASE(9)
 VDSL_DMA_WAIT_CASE(12)
 #undef VDSL_DMA_WAIT_CASE
 

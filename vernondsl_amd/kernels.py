@@ -119,6 +119,13 @@ def cast(q: Queue, src: Tensor, dst: Tensor):
     call("vdsl_op_cast", q.handle, src.numel, src.dtype, src.handle, dst.dtype, dst.handle)
 
 
+def gelu_fwd(q: Queue, x: Tensor, y: Tensor):
+    """y = GELU(x) elementwise (exact-erf form); x, y f32 or bf16 of one element count."""
+    if x.numel != y.numel:
+        raise ValueError(f"gelu_fwd: x has {x.numel} elements, y {y.numel}")
+    call("vdsl_op_gelu_fwd", q.handle, x.numel, x.dtype, x.handle, y.dtype, y.handle)
+
+
 def gelu_bwd(q: Queue, dh: Tensor, pre: Tensor, da: Tensor, da_t=None):
     rows, cols = dh.shape
     _expect(dh, (rows, cols), "f32", "dh")
