@@ -434,8 +434,10 @@ def run_kernel_only(dev, q, name, reps):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    # 100 untimed steps (~9 ms of GPU work for config 2): the clocks ramp up during the first
+    # milliseconds after host-side setup, and a shorter warm-up reads the kernel up to 5% low
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline timings")
     ap.add_argument("--only", type=int, default=0, help="run only the headline (2) or one extra config")
     ap.add_argument("--kernel", default="", help="run one kernel --reps times and exit (for rocprofv3 --pmc): "
