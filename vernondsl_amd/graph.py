@@ -206,8 +206,7 @@ class Executable:
         self.graph = g
         self.dev = dev
         self.t: dict[str, Tensor] = {}
-        for v in g.values.values():
-            self.t[v.name] = Tensor(dev, v.shape, v.dtype)
+        self.workspace = None
         ws = 0
         for op in g.ops:
             if op.kind == "gemm":
@@ -218,8 +217,14 @@ class Executable:
             if op.kind == "w8a8":
                 xq, _, wq, _ = op.inputs
                 ws = max(ws, kernels.gemm_w8a8_workspace_bytes(xq.shape[0], wq.shape[0], xq.shape[1]))
-        # One workspace shared by all ops: they run in order on one queue.
-        self.workspace = Tensor(dev, (max(ws, 4),), "i8") if ws else None
+        try:
+            for v in g.values.values():
+                self.t[v.name] = Tensor(dev, v.shape, v.dtype)
+            # One workspace shared by all ops: they run in order on one queue.
+            self.workspace = Tensor(dev, (max(ws, 4),), "i8") if ws else None
+        except BaseException:
+            self.free()  # an allocation failed: release what was allocated before re-raising
+            raise
 
     def write(self, q: Queue, name: str, host):
         self.t[name].buffer.write(q, host)
@@ -268,8 +273,10 @@ class Executable:
     def free(self):
         for t in self.t.values():
             t.free()
+        self.t = {}
         if self.workspace is not None:
             self.workspace.free()
+            self.workspace = None
 
 
 # ---- the two workload graphs ------------------------------------------------------------------------

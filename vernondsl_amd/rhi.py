@@ -123,10 +123,14 @@ class Tensor:
         if dtype is None:
             inv = {v: k for k, v in _NP_DTYPES.items()}
             dtype = inv[np.dtype(host.dtype)]
+        if host.dtype != np_dtype(dtype):
+            raise TypeError(f"host dtype {host.dtype} does not match device dtype {dtype}")
         t = cls(device, host.shape, dtype, binding)
-        if host.dtype != np_dtype(t.dtype):
-            raise TypeError(f"host dtype {host.dtype} does not match device dtype {t.dtype}")
-        t.buffer.write(queue, host)
+        try:
+            t.buffer.write(queue, host)
+        except BaseException:
+            t.free()
+            raise
         return t
 
     def numpy(self, queue: "Queue") -> np.ndarray:
