@@ -135,8 +135,10 @@ def test_gelu_fwd(dev, q, xdt, ydt):
 
 def test_transpose_and_cast(dev, q):
     # odd extents take the element-wise kernel; even bf16 extents the 2x2-pair kernel (one partial
-    # 128x128 tile in each direction for the last two)
-    for shape in ((64, 64), (37, 1000), (1, 5), (513, 129), (2, 2), (130, 258), (256, 2050)):
+    # 128x128 tile in each direction for (130, 258), (256, 2050)); bf16 extents that are multiples
+    # of 8 the 16-byte kernel (partial 64x64 tiles for (72, 200), a single 8x8 corner for (8, 8))
+    for shape in ((64, 64), (37, 1000), (1, 5), (513, 129), (2, 2), (130, 258), (256, 2050), (72, 200), (8, 8),
+                  (2048, 4096)):
         x = rng.normal(3, int(np.prod(shape))).reshape(shape)
         for dt, h in (("f32", x), ("bf16", rng.f32_to_bf16(x))):
             ts = Tensor.from_numpy(dev, q, h, dt)
@@ -157,7 +159,9 @@ def test_transpose_and_cast(dev, q):
         t.free()
 
 
-@pytest.mark.parametrize("rows,cols", [(128, 192), (70, 33), (2048, 4096)])
+# (70, 33): the element-wise kernel; the others the 16-byte kernel (rows % 8 == 0, cols % 4 == 0),
+# (72, 100) and (8, 4) with partial tiles
+@pytest.mark.parametrize("rows,cols", [(128, 192), (70, 33), (72, 100), (8, 4), (2048, 4096)])
 def test_gelu_bwd(dev, q, rows, cols):
     dh = rng.normal(21, rows * cols).reshape(rows, cols) * np.float32(1e-3)
     pre = rng.normal(22, rows * cols, 0, 2).reshape(rows, cols)
@@ -175,7 +179,7 @@ def test_gelu_bwd(dev, q, rows, cols):
         t.free()
 
 
-@pytest.mark.parametrize("rows,cols", [(128, 192), (70, 33), (2048, 4096)])
+@pytest.mark.parametrize("rows,cols", [(128, 192), (70, 33), (72, 100), (8, 4), (2048, 4096)])
 def test_mse(dev, q, rows, cols):
     y = rng.normal(31, rows * cols).reshape(rows, cols)
     t = rng.normal(32, rows * cols).reshape(rows, cols)
@@ -191,6 +195,32 @@ def test_mse(dev, q, rows, cols):
     assert np.array_equal(dyt.numpy(q), g.T)
     for x in (ty, tt, loss, dy, dyt, part):
         x.free()
+
+
+@pytest.mark.parametrize("rows,cols", [(72, 100), (70, 33)])
+def test_optional_outputs_absent(dev, q, rows, cols):
+    """gelu_bwd without da_t, MSE without dy or without dy_t: the outputs that are given match the
+    full call, the loss is the same."""
+    dh = rng.normal(51, rows * cols).reshape(rows, cols)
+    pre = rng.normal(52, rows * cols).reshape(rows, cols)
+    tdh, tpre = Tensor.from_numpy(dev, q, dh), Tensor.from_numpy(dev, q, pre)
+    da1, da2, dat = Tensor(dev, (rows, cols), "bf16"), Tensor(dev, (rows, cols), "bf16"), Tensor(dev, (cols, rows), "bf16")
+    kernels.gelu_bwd(q, tdh, tpre, da1, dat)
+    kernels.gelu_bwd(q, tdh, tpre, da2, None)
+    assert np.array_equal(da1.numpy(q), da2.numpy(q))
+    part = Tensor(dev, (kernels.mse_partials_count(rows, cols),), "f32")
+    l1, l2, l3 = (Tensor(dev, (1,), "f32") for _ in range(3))
+    dy1, dyt1 = Tensor(dev, (rows, cols), "bf16"), Tensor(dev, (cols, rows), "bf16")
+    dy2, dyt3 = Tensor(dev, (rows, cols), "bf16"), Tensor(dev, (cols, rows), "bf16")
+    kernels.mse_fwd_bwd(q, tdh, tpre, l1, dy1, dyt1, part)
+    kernels.mse_fwd_bwd(q, tdh, tpre, l2, dy2, None, part)
+    call = _lib.call
+    call("vdsl_op_mse_fwd_bwd", q.handle, rows, cols, tdh.handle, tpre.handle, l3.handle, None, dyt3.handle, part.handle)
+    assert l1.numpy(q)[0] == l2.numpy(q)[0] == l3.numpy(q)[0]
+    assert np.array_equal(dy1.numpy(q), dy2.numpy(q))
+    assert np.array_equal(dyt1.numpy(q), dyt3.numpy(q))
+    for t in (tdh, tpre, da1, da2, dat, part, l1, l2, l3, dy1, dyt1, dy2, dyt3):
+        t.free()
 
 
 @pytest.mark.parametrize("rows,cols,dt", [(512, 8192, "bf16"), (37, 100, "f32"), (5, 16, "bf16")])

@@ -19,8 +19,149 @@ namespace {
 
 __device__ __forceinline__ float gelu_grad_f(float v) {
   // d/dv [0.5 v (1 + erf(v / sqrt2))] = Phi(v) + v phi(v), with Phi(v) = 0.5 erfc(-v / sqrt2)
-  // (erfc keeps full relative accuracy where 1 + erf(.) would cancel, v < 0).
-  return 0.5f * erfcf(-v * 0.7071067811865476f) + v * expf(-0.5f * v * v) * 0.3989422804014327f;
+  // (erfc keeps full relative accuracy where 1 + erf(.) would cancel, v < 0).  Branch-free:
+  // erfc_cheb (fractional error < 1.2e-7) and exp_fast (< 2e-7 + 1 ulp); the result is rounded
+  // to bf16, and near the zero of GELU' (v = -0.75) the absolute error stays below 1e-7.
+  return 0.5f * erfc_cheb(-v * 0.7071067811865476f) + v * exp_fast(-0.5f * v * v) * 0.3989422804014327f;
+}
+
+// Vector forms of the two kernels below, for rows % 8 == 0 and cols % 4 == 0 (every base is a
+// whole hipMalloc buffer, 256-byte aligned): a 64x64 tile per 256-lane block, each lane loads two
+// units of 2 rows x 4 columns with 16-byte loads (all loads issued before any arithmetic), stores
+// the row-major result as 8-byte runs and hands the transposed result to LDS as row pairs, which
+// go out as 16-byte runs of the transposed rows (store_pair_tile_transposed).
+
+// Unit k of this lane: source rows r0 + 2q, r0 + 2q + 1, columns c0 + 4t .. c0 + 4t + 3.
+__device__ __forceinline__ void unit_of(int k, int& q, int& t) {
+  const int u = static_cast<int>(threadIdx.x) + 256 * k;
+  q = u >> 4;
+  t = u & 15;
+}
+
+// Packs the bf16 results of one unit: row-major words (2 per row) and the 4 column pairs.
+__device__ __forceinline__ void pack_unit(const float (&v)[2][4], uint32_t (&row)[2][2], uint32_t (&pair)[4]) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    row[i][0] = pack_bf16x2(v[i][0], v[i][1]);
+    row[i][1] = pack_bf16x2(v[i][2], v[i][3]);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    pair[2 * h] = (row[0][h] & 0xFFFFu) | (row[1][h] << 16);
+    pair[2 * h + 1] = (row[0][h] >> 16) | (row[1][h] & 0xFFFF0000u);
+  }
+}
+
+__global__ __launch_bounds__(256) void gelu_bwd_vec(const float* __restrict__ dh, const float* __restrict__ pre,
+                                                    uint16_t* __restrict__ da, uint16_t* __restrict__ da_t,
+                                                    int64_t rows, int64_t cols) {
+  __shared__ __align__(16) uint32_t tile[kPairTileWords];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  f32x4 g[2][2], x[2][2];
+  bool ok[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    int q, t;
+    unit_of(k, q, t);
+    ok[k] = r0 + 2 * q < rows && c0 + 4 * t < cols;
+    const int64_t o = (r0 + 2 * q) * cols + c0 + 4 * t;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (ok[k]) {
+        g[k][i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(dh + o + i * cols));
+        x[k][i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(pre + o + i * cols));
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if (!ok[k]) continue;
+    int q, t;
+    unit_of(k, q, t);
+    float v[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[i][j] = g[k][i][j] * gelu_grad_f(x[k][i][j]);
+    uint32_t row[2][2], pair[4];
+    pack_unit(v, row, pair);
+    const int64_t o = (r0 + 2 * q) * cols + c0 + 4 * t;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      uint2 w;
+      w.x = row[i][0];
+      w.y = row[i][1];
+      *reinterpret_cast<uint2*>(da + o + i * cols) = w;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tile[pair_slot(4 * t + j, q)] = pair[j];
+  }
+  if (!da_t) return;  // uniform across the block
+  __syncthreads();
+  store_pair_tile_transposed(tile, da_t, rows, cols, r0, c0);
+}
+
+__global__ __launch_bounds__(256) void mse_tile_vec(const float* __restrict__ y, const float* __restrict__ t_in,
+                                                    uint16_t* __restrict__ dy, uint16_t* __restrict__ dy_t,
+                                                    double* __restrict__ partials, int64_t rows, int64_t cols,
+                                                    float scale) {
+  __shared__ __align__(16) uint32_t tile[kPairTileWords];
+  __shared__ double wsum[4];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  f32x4 a[2][2], b[2][2];
+  bool ok[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    int q, t;
+    unit_of(k, q, t);
+    ok[k] = r0 + 2 * q < rows && c0 + 4 * t < cols;
+    const int64_t o = (r0 + 2 * q) * cols + c0 + 4 * t;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (ok[k]) {
+        a[k][i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(y + o + i * cols));
+        b[k][i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(t_in + o + i * cols));
+      }
+    }
+  }
+  double s = 0.0;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if (!ok[k]) continue;
+    int q, t;
+    unit_of(k, q, t);
+    float v[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float d = a[k][i][j] - b[k][i][j];
+        s += static_cast<double>(d) * static_cast<double>(d);
+        v[i][j] = d * scale;
+      }
+    uint32_t row[2][2], pair[4];
+    pack_unit(v, row, pair);
+    const int64_t o = (r0 + 2 * q) * cols + c0 + 4 * t;
+    if (dy) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        uint2 w;
+        w.x = row[i][0];
+        w.y = row[i][1];
+        *reinterpret_cast<uint2*>(dy + o + i * cols) = w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tile[pair_slot(4 * t + j, q)] = pair[j];
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+  if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    partials[static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x] = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+  if (!dy_t) return;
+  store_pair_tile_transposed(tile, dy_t, rows, cols, r0, c0);
 }
 
 __global__ __launch_bounds__(256) void gelu_bwd_kernel(const float* __restrict__ dh, const float* __restrict__ pre,
@@ -115,7 +256,14 @@ extern "C" int vdsl_op_gelu_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_b
   if (n == 0) return VDSL_OK;
   const int64_t gx = (cols + 63) / 64, gy = (rows + 63) / 64;
   if (gy > 65535 || gx > 0x7fffffff) return fail(VDSL_ERR_UNSUPPORTED, "gelu_bwd: tensor too large");
-  hipLaunchKernelGGL(gelu_bwd_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)), dim3(256), 0, q->stream,
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+  if (rows % 8 == 0 && cols % 4 == 0) {
+    hipLaunchKernelGGL(gelu_bwd_vec, grid, dim3(256), 0, q->stream, static_cast<const float*>(dh->ptr),
+                       static_cast<const float*>(pre->ptr), static_cast<uint16_t*>(da->ptr),
+                       da_t ? static_cast<uint16_t*>(da_t->ptr) : nullptr, rows, cols);
+    return check_launch("gelu_bwd_vec");
+  }
+  hipLaunchKernelGGL(gelu_bwd_kernel, grid, dim3(256), 0, q->stream,
                      static_cast<const float*>(dh->ptr), static_cast<const float*>(pre->ptr), static_cast<uint16_t*>(da->ptr),
                      da_t ? static_cast<uint16_t*>(da_t->ptr) : nullptr, rows, cols);
   return check_launch("gelu_bwd_kernel");
@@ -176,10 +324,16 @@ extern "C" int vdsl_op_mse_fwd_bwd(vdsl_queue q, int64_t rows, int64_t cols, vds
   if (gy > 65535 || gx > 0x7fffffff) return fail(VDSL_ERR_UNSUPPORTED, "mse: tensor too large");
   const float scale = 2.0f / static_cast<float>(n);
   double* part = static_cast<double*>(partials->ptr);
-  hipLaunchKernelGGL(mse_tile_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)), dim3(256), 0, q->stream,
-                     static_cast<const float*>(y->ptr), static_cast<const float*>(t->ptr),
-                     dy ? static_cast<uint16_t*>(dy->ptr) : nullptr, dy_t ? static_cast<uint16_t*>(dy_t->ptr) : nullptr, part,
-                     rows, cols, scale);
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+  if (rows % 8 == 0 && cols % 4 == 0)
+    hipLaunchKernelGGL(mse_tile_vec, grid, dim3(256), 0, q->stream, static_cast<const float*>(y->ptr),
+                       static_cast<const float*>(t->ptr), dy ? static_cast<uint16_t*>(dy->ptr) : nullptr,
+                       dy_t ? static_cast<uint16_t*>(dy_t->ptr) : nullptr, part, rows, cols, scale);
+  else
+    hipLaunchKernelGGL(mse_tile_kernel, grid, dim3(256), 0, q->stream,
+                       static_cast<const float*>(y->ptr), static_cast<const float*>(t->ptr),
+                       dy ? static_cast<uint16_t*>(dy->ptr) : nullptr, dy_t ? static_cast<uint16_t*>(dy_t->ptr) : nullptr, part,
+                       rows, cols, scale);
   VDSL_TRY(check_launch("mse_tile_kernel"));
   hipLaunchKernelGGL(mse_finish_kernel, dim3(1), dim3(256), 0, q->stream, part, np, static_cast<float*>(loss->ptr),
                      1.0 / static_cast<double>(n));

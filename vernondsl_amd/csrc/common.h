@@ -188,4 +188,32 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// ---- transposed bf16 tiles through LDS as row pairs ------------------------------------------
+// A 64x64 bf16 tile is held transposed in LDS as 32-bit pairs: the pair at (column c, p) holds
+// the tile's elements (2p, c) and (2p + 1, c), i.e. two consecutive elements of transposed row c.
+// A transposed row is 32 pairs (128 bytes); its groups of 4 pairs are XOR-swizzled by
+// (c >> 2) & 7, which spreads the pair writes of lanes on neighbouring columns over the banks and
+// keeps each group contiguous for one 16-byte read.
+constexpr int kPairTileWords = 64 * 32;
+
+__device__ __forceinline__ int pair_slot(int c, int p) { return c * 32 + (p ^ (((c >> 2) & 7) << 2)); }
+
+// Writes the transposed tile (tile rows r0.., columns c0.. of a rows x cols source) to dst, whose
+// row c0 + c holds source column c0 + c: 512 16-byte units (8 source rows of one column), two per
+// lane of a 256-lane block, 8 lanes per transposed row.  Needs rows % 8 == 0 (16-byte aligned
+// units, each wholly inside or outside the tensor); the caller has written every in-bounds pair
+// and synchronised the block.
+__device__ __forceinline__ void store_pair_tile_transposed(const uint32_t* __restrict__ tile, uint16_t* __restrict__ dst,
+                                                           int64_t rows, int64_t cols, int64_t r0, int64_t c0) {
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int u = static_cast<int>(threadIdx.x) + 256 * k;
+    const int c = u >> 3, g = u & 7;
+    if (c0 + c < cols && r0 + 8 * g < rows) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(tile + pair_slot(c, 4 * g));
+      *reinterpret_cast<u32x4*>(dst + (c0 + c) * rows + r0 + 8 * g) = v;
+    }
+  }
+}
+
 }  // namespace vdsl

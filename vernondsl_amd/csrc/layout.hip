@@ -10,7 +10,9 @@
 // bf16 with even extents takes a 128x128 tile of 2x2 element blocks instead: a lane loads two
 // 4-byte pairs (rows r, r+1 at columns c, c+1), swaps them into the two destination pairs in
 // registers, and the 32-bit pairs go through LDS as a 64x64 tile; every global access is then
-// 4 bytes per lane (the 2-byte form runs at about a quarter of the copy bandwidth).
+// 4 bytes per lane (the 2-byte form runs at about a quarter of the copy bandwidth).  With
+// extents that are multiples of 8 the same pairing runs on 16-byte loads and stores
+// (transpose_bf16_vec).
 
 #include "common.h"
 
@@ -64,6 +66,29 @@ __global__ __launch_bounds__(256) void transpose_bf16_pairs(const uint32_t* __re
   }
 }
 
+// bf16, rows % 8 == 0 and cols % 8 == 0: a 64x64 tile per block; lane u loads source rows
+// r0 + 2q, r0 + 2q + 1 (q = u / 8) at columns c0 + 8t .. + 7 (t = u % 8) with two 16-byte loads,
+// forms the 8 column pairs in registers and the tile leaves as 16-byte runs of the destination
+// rows (store_pair_tile_transposed).
+__global__ __launch_bounds__(256) void transpose_bf16_vec(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                          int64_t rows, int64_t cols) {
+  __shared__ __align__(16) uint32_t tile[kPairTileWords];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int q = static_cast<int>(threadIdx.x) >> 3, t = static_cast<int>(threadIdx.x) & 7;
+  if (r0 + 2 * q < rows && c0 + 8 * t < cols) {
+    const int64_t o = (r0 + 2 * q) * cols + c0 + 8 * t;
+    const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + o));
+    const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + o + cols));
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      tile[pair_slot(8 * t + 2 * h, q)] = (a[h] & 0xFFFFu) | (b[h] << 16);
+      tile[pair_slot(8 * t + 2 * h + 1, q)] = (a[h] >> 16) | (b[h] & 0xFFFF0000u);
+    }
+  }
+  __syncthreads();
+  store_pair_tile_transposed(tile, dst, rows, cols, r0, c0);
+}
+
 __global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* __restrict__ s, uint16_t* __restrict__ d, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
     d[i] = f32_to_bf16(s[i]);
@@ -78,6 +103,13 @@ __global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __rest
 
 int launch_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int dtype, hipStream_t s) {
   if (rows == 0 || cols == 0) return VDSL_OK;
+  if (dtype == VDSL_BF16 && rows % 8 == 0 && cols % 8 == 0) {
+    const int64_t bx = (cols + 63) / 64, by = (rows + 63) / 64;
+    if (bx > 0x7fffffff || by > 65535) return fail(VDSL_ERR_UNSUPPORTED, "transpose: tensor too large");
+    hipLaunchKernelGGL(transpose_bf16_vec, dim3(static_cast<unsigned>(bx), static_cast<unsigned>(by)), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), rows, cols);
+    return check_launch("transpose_bf16_vec");
+  }
   if (dtype == VDSL_BF16 && rows % 2 == 0 && cols % 2 == 0) {
     const int64_t bx = (cols + 127) / 128, by = (rows + 127) / 128;
     if (bx > 0x7fffffff || by > 65535) return fail(VDSL_ERR_UNSUPPORTED, "transpose: tensor too large");
