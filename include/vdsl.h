@@ -327,6 +327,16 @@ int vdsl_op_gemm_w8a8(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer
  * (n < 0 disables).  Also settable with the environment variable VDSL_FAIL_ALLOC_AFTER. */
 int vdsl_debug_fail_alloc_after(int64_t n);
 
+/* ---- tuning hook (tests and sweeps, host-side only) ----------------------------------------- */
+/* Forces the GEMM tile configuration `config` (an index into the library's table for both
+ * vdsl_op_gemm_bf16 and vdsl_op_gemm_w8a8) for later calls on every thread; config < 0 restores
+ * the per-shape choice.  A configuration that cannot run a given shape (an index past the table,
+ * a direct-to-LDS configuration whose stage does not divide K) is ignored for that call.  Also
+ * settable with the environment variable VDSL_GEMM_CONFIG.  Query workspace sizes after setting
+ * it: the int8 split-K workspace depends on the configuration.  No counterpart in the reference
+ * (which has no kernels); callers are tuning sweeps and the tests that cover every configuration. */
+int vdsl_debug_gemm_config(int32_t config);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,95 @@
+"""Every GEMM tile configuration of the library, forced one at a time with vdsl_debug_gemm_config.
+
+The per-shape choice runs only a few configurations in the other tests; this file runs all of them
+on shapes with ragged edge tiles in both directions (rows and columns past M and N are clamped in
+the direct-to-LDS loops, masked in the register-staged ones) and a K that every configuration
+accepts.  bf16: every configuration accumulates the same k-steps in the same order with the same
+MFMA, so each output must equal the per-shape choice's bit for bit, and that one is checked
+against the oracle at the bf16 GEMM tolerance.  int8 (including the split-K configurations, which
+these small outputs select): accumulators and outputs bit-exact against the oracle.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle
+from vernondsl_amd import _lib, kernels, rng
+from vernondsl_amd._lib import call
+from vernondsl_amd.rhi import Tensor
+
+pytestmark = pytest.mark.gpu
+BF16 = 1
+N_BF16_CONFIGS = 27  # gemm_bf16.hip: register-staged 0..13, direct-to-LDS 14..22, 128-byte stages 23..26
+N_W8A8_CONFIGS = 23  # gemm_w8a8.hip: register-staged 0..13, direct-to-LDS 14..19, 128-byte stages 20..22
+
+
+@pytest.fixture
+def forced_config():
+    yield lambda c: call("vdsl_debug_gemm_config", c)
+    call("vdsl_debug_gemm_config", -1)
+
+
+def run_bf16(dev, q, tA, tB, M, N, K, gelu):
+    out = Tensor(dev, (M, N), "bf16" if gelu else "f32")
+    out.buffer.fill_u32(q, 0x7FC07FC0)
+    pre = Tensor(dev, (M, N), "f32") if gelu else None
+    if pre is not None:
+        pre.buffer.fill_u32(q, 0x7FC07FC0)
+    kernels.gemm_bf16(q, tA, tB, out, False, True, _lib.EPI_GELU if gelu else _lib.EPI_NONE, pre)
+    res = (out.numpy(q), pre.numpy(q) if pre is not None else None)
+    out.free()
+    if pre is not None:
+        pre.free()
+    return res
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 520, 256), (129, 258, 128)])
+def test_every_bf16_config_matches(dev, q, forced_config, M, N, K):
+    A = rng.f32_to_bf16(rng.uniform(71, M * K, -1, 1)).reshape(M, K)
+    B = rng.f32_to_bf16(rng.uniform(72, N * K, -1, 1)).reshape(N, K)
+    tA, tB = Tensor.from_numpy(dev, q, A, "bf16"), Tensor.from_numpy(dev, q, B, "bf16")
+    try:
+        forced_config(-1)
+        base = {g: run_bf16(dev, q, tA, tB, M, N, K, g) for g in (False, True)}
+        ref_f32 = oracle.gemm_bf16(A, B, False, True)
+        got = base[False][0].astype(np.float64)
+        mag = np.abs(rng.bf16_to_f32(A).astype(np.float64)) @ np.abs(rng.bf16_to_f32(B).astype(np.float64)).T
+        assert np.all(np.abs(got - ref_f32) <= 1e-2 * mag + 1e-30)
+        assert np.array_equal(base[True][1], base[False][0])  # pre-activation == plain product
+        for c in range(N_BF16_CONFIGS):
+            forced_config(c)
+            for g in (False, True):
+                out, pre = run_bf16(dev, q, tA, tB, M, N, K, g)
+                assert np.array_equal(out, base[g][0]), f"config {c} gelu={g}: output differs"
+                if g:
+                    assert np.array_equal(pre, base[g][1]), f"config {c}: pre-activation differs"
+    finally:
+        tA.free()
+        tB.free()
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 520, 1024), (64, 1000, 512)])
+def test_every_w8a8_config_bit_exact(dev, q, forced_config, M, N, K):
+    r = np.random.default_rng(M * 7 + N + K)
+    xq = r.integers(-127, 128, (M, K)).astype(np.int8)
+    w = r.integers(-127, 128, (N, K)).astype(np.int8)
+    xs = r.uniform(0.001, 0.01, M).astype(np.float32)
+    ws = r.uniform(0.005, 0.02, N).astype(np.float32)
+    ry, racc = oracle.gemm_w8a8(xq, xs, w, ws, out_dtype=BF16, relu=True, want_acc=True)
+    ts = [Tensor.from_numpy(dev, q, a) for a in (xq, w, xs, ws)]
+    txq, tw, txs, tws = ts
+    try:
+        for c in [-1] + list(range(N_W8A8_CONFIGS)):
+            forced_config(c)
+            wsb = kernels.gemm_w8a8_workspace_bytes(M, N, K)  # depends on the configuration
+            ty, tacc = Tensor(dev, (M, N), "bf16"), Tensor(dev, (M, N), "i32")
+            twk = Tensor(dev, (max(1, wsb),), "i8") if wsb else None
+            tacc.buffer.fill_u32(q, 0xDEADBEEF)
+            kernels.gemm_w8a8(q, txq, txs, tw, tws, ty, True, tacc, twk)
+            assert np.array_equal(tacc.numpy(q), racc), f"config {c}: int32 accumulators differ"
+            assert np.array_equal(ty.numpy(q), ry), f"config {c}: outputs differ"
+            for t in (ty, tacc, twk):
+                if t is not None:
+                    t.free()
+    finally:
+        for t in ts:
+            t.free()

@@ -10,6 +10,7 @@
 // adds the epilogue (GELU / ReLU, optional f32 pre-activation, f32 or bf16 C) and the choice of
 // tile configuration per shape.
 
+#include <atomic>
 #include <cstdlib>
 
 #include "gemm_mfma.h"
@@ -20,11 +21,17 @@ namespace vdsl {
 // Defined in layout.hip.
 int launch_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int dtype, hipStream_t s);
 
+namespace {
+std::atomic<int> g_gemm_config{-2};  // -2: not yet read from the environment
+}  // namespace
+
 int gemm_config_override() {
-  static const int v = [] {
+  int v = g_gemm_config.load(std::memory_order_relaxed);
+  if (v == -2) {
     const char* e = std::getenv("VDSL_GEMM_CONFIG");
-    return e ? std::atoi(e) : -1;
-  }();
+    g_gemm_config.compare_exchange_strong(v, e ? std::atoi(e) : -1);
+    v = g_gemm_config.load(std::memory_order_relaxed);
+  }
   return v;
 }
 
@@ -53,7 +60,16 @@ using Dm16 = DmaConfig<MfmaBf16, 128, 256, 2, 4, 3>;  // 8 waves of 64x64, 3 LDS
 using Dm17 = DmaConfig<MfmaBf16, 128, 128, 2, 2, 4>;  // 4 waves of 64x64, 2 blocks per CU
 using Dm18 = DmaConfig<MfmaBf16, 128, 256, 2, 4, 5>;  // 8 waves of 64x64, 5 LDS stages
 using Dm19 = DmaConfig<MfmaBf16, 256, 128, 2, 2, 4>;  // 4 waves of 128x64
-constexpr int kNumConfigs = 20;
+using Dm20 = DmaConfig<MfmaBf16, 128, 256, 2, 2, 4>;  // 4 waves of 64x128
+using Dm21 = DmaConfig<MfmaBf16, 128, 256, 2, 2, 3>;  // 4 waves of 64x128, 3 LDS stages
+using Dm22 = DmaConfig<MfmaBf16, 128, 256, 2, 2, 5>;  // 4 waves of 64x128, 5 LDS stages
+// 128-byte stages (one barrier per 64 bf16 of K); need K % 64 == 0
+using Dm23 = DmaConfig<MfmaBf16, 128, 256, 2, 4, 3, 128>;  // 8 waves of 64x64
+using Dm24 = DmaConfig<MfmaBf16, 128, 256, 2, 2, 3, 128>;  // 4 waves of 64x128
+using Dm25 = DmaConfig<MfmaBf16, 128, 128, 2, 2, 4, 128>;  // 4 waves of 64x64
+using Dm26 = DmaConfig<MfmaBf16, 256, 128, 2, 2, 3, 128>;  // 4 waves of 128x64
+constexpr int kNumConfigs = 27;
+constexpr int kFirstDma = 14, kFirstDma128 = 23;
 
 // Epilogue of one accumulator element at (row, col), shared by both main loops.
 __device__ __forceinline__ void bf16_epilogue(float v, int row, int col, int M, int N, void* __restrict__ C,
@@ -114,6 +130,49 @@ __device__ __forceinline__ void bf16_store_tile(const f32x16 (&acc)[Cfg::FM][Cfg
   }
 }
 
+// Whole-tile epilogue staged through LDS (after the main loop, when the block's LDS is free):
+// each wave writes one 32-row block of its accumulators to a private LDS area (row stride WTN + 8
+// floats: the lanes of one accumulator store, 32 columns x rows 4 apart, hit 64 distinct banks),
+// reads it back as 4 consecutive columns per lane and stores 16-byte runs of the f32 output (or
+// of the pre-activation) and 8-byte runs of the bf16 output, instead of one 4- or 2-byte store
+// per accumulator element.  Needs N % 4 == 0 (aligned runs) and NW * 32 * (WTN + 8) floats of
+// LDS; the caller has synchronised the block after the main loop.
+template <class Cfg>
+constexpr bool kLdsEpilogue = Cfg::NW * 32 * (Cfg::WTN + 8) * 4 <= Cfg::LDS_BYTES;
+
+template <class Cfg, int VARIANT>
+__device__ __forceinline__ void bf16_epilogue_tile_lds(const f32x16 (&acc)[Cfg::FM][Cfg::FN], int m0, int n0, int N,
+                                                       void* __restrict__ C, float* __restrict__ pre, char* smem) {
+  constexpr int WTN = Cfg::WTN, LD = WTN + 8;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
+  float* const area = reinterpret_cast<float*>(smem) + wave * 32 * LD;
+  const int row0 = m0 + wm * Cfg::WTM, col0 = n0 + wn * WTN;
+#pragma unroll
+  for (int i = 0; i < Cfg::FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) area[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * LD + 32 * j + (lane & 31)] = acc[i][j][r];
+    constexpr int Q = WTN / 4;  // 16-byte units per row
+#pragma unroll
+    for (int k = 0; k < 32 * Q / 64; ++k) {
+      const int u = lane + 64 * k, row = u / Q, c4 = u % Q;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(area + row * LD + 4 * c4);
+      const size_t o = static_cast<size_t>(row0 + 32 * i + row) * N + col0 + 4 * c4;
+      if (VARIANT == 0) {
+        *reinterpret_cast<f32x4*>(static_cast<float*>(C) + o) = v;
+      } else {
+        *reinterpret_cast<f32x4*>(pre + o) = v;
+        uint2 h;
+        h.x = pack_bf16x2(gelu_f(v[0]), gelu_f(v[1]));
+        h.y = pack_bf16x2(gelu_f(v[2]), gelu_f(v[3]));
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(C) + o) = h;
+      }
+    }
+  }
+}
+
 template <class Cfg, bool EDGE>
 __global__ __launch_bounds__(Cfg::NT, 2) void gemm_bf16_nt(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                         void* __restrict__ C, float* __restrict__ pre, int M, int N, int K,
@@ -144,6 +203,18 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_bf16_dma
   f32x16 acc[Cfg::FM][Cfg::FN];
   dma_mainloop<MfmaBf16, Cfg>(reinterpret_cast<const char*>(A), reinterpret_cast<const char*>(B), M, N, K * 2, 0, K * 2, m0,
                               n0, smem, acc);
+  if constexpr (kLdsEpilogue<Cfg>) {
+    // Block-uniform: the tile is whole, N allows aligned runs, and the variant is one of the two.
+    const bool whole = m0 + Cfg::BM <= M && n0 + Cfg::BN <= N && N % 4 == 0;
+    const bool v0 = epi == VDSL_EPI_NONE && c_dtype == VDSL_F32 && !pre;
+    const bool v1 = epi == VDSL_EPI_GELU && c_dtype == VDSL_BF16 && pre;
+    if (whole && (v0 || v1)) {
+      dma_barrier();  // every wave's last fragment reads of the main loop are done
+      if (v0) bf16_epilogue_tile_lds<Cfg, 0>(acc, m0, n0, N, C, pre, smem);
+      else bf16_epilogue_tile_lds<Cfg, 1>(acc, m0, n0, N, C, pre, smem);
+      return;
+    }
+  }
   bf16_store_tile<Cfg>(acc, m0, n0, M, N, C, pre, epi, c_dtype);
 }
 
@@ -184,20 +255,21 @@ int launch_dma(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M,
 
 // Configuration for a shape.  The direct-to-LDS loop (14..) runs whenever K is a whole number of
 // its 64-byte stages (K % 32 == 0); measured on MI355X with random operands (bf16, f32 out):
-// 128x256 blocks of 8 waves are fastest while they still give every CU a block (2048x4096x4096:
-// 950 TFLOP/s against 794 for the best register-staged configuration), 256x256 blocks once those
-// do (4096x4096x2048: 973 against 870).  Smaller launches take 128x128 blocks, two per CU.  Other
-// K use the register-staged loop (0..13), where 128x128 tiles are fastest below 512 tiles of
-// 256x128 and 256x128 tiles of 8 waves above.
+// 128x256 blocks of 8 waves are fastest while they still give every CU a block, with 128-byte
+// stages and fragments read two k-steps ahead when K % 64 == 0 (2048x4096x4096: 890-915 TFLOP/s
+// against 845-860 with 64-byte stages), 256x256 blocks once those do (4096x4096x2048: 955 against
+// 870).  Smaller launches take 128x128 blocks, two per CU.  Other K use the register-staged loop
+// (0..13), where 128x128 tiles are fastest below 512 tiles of 256x128 and 256x128 tiles of 8
+// waves above.
 int choose_config(int64_t M, int64_t N, int64_t K) {
-  const bool dma = dma_k_ok(0, K * 2);
+  const bool dma = dma_k_ok(0, K * 2), dma128 = dma_k_ok(0, K * 2, 128);
   const int o = gemm_config_override();
-  if (o >= 0 && o < kNumConfigs && (o < 14 || dma)) return o;
+  if (o >= 0 && o < kNumConfigs && (o < kFirstDma || (o < kFirstDma128 ? dma : dma128))) return o;
   if (dma) {
     const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
     const int64_t t128x256 = ((M + 127) / 128) * ((N + 255) / 256);
     if (t256 >= 240) return 15;
-    if (t128x256 >= 128) return 14;
+    if (t128x256 >= 128) return dma128 ? 23 : 14;
     return 17;
   }
   const int64_t tiles_256x128 = ((M + 255) / 256) * ((N + 127) / 128);
@@ -230,6 +302,13 @@ int launch_nt(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, 
     case 17: return launch_dma<Dm17>(A, B, C, pre, M, N, K, epi, ct, s);
     case 18: return launch_dma<Dm18>(A, B, C, pre, M, N, K, epi, ct, s);
     case 19: return launch_dma<Dm19>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 20: return launch_dma<Dm20>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 21: return launch_dma<Dm21>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 22: return launch_dma<Dm22>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 23: return launch_dma<Dm23>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 24: return launch_dma<Dm24>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 25: return launch_dma<Dm25>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 26: return launch_dma<Dm26>(A, B, C, pre, M, N, K, epi, ct, s);
     default: return launch_cfg<Bf0>(A, B, C, pre, M, N, K, epi, ct, s);
   }
 }
@@ -286,4 +365,10 @@ extern "C" int vdsl_op_gemm_bf16(vdsl_queue q, int32_t trans_a, int32_t trans_b,
   float* pre = pre_act ? static_cast<float*>(pre_act->ptr) : nullptr;
   return launch_nt(a, b, C->ptr, pre, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), epilogue, c_dtype,
                    q->stream);
+}
+
+extern "C" int vdsl_debug_gemm_config(int32_t config) {
+  vdsl::gemm_config_override();  // consume the environment value first, so it cannot override this
+  vdsl::g_gemm_config.store(config < 0 ? -1 : config, std::memory_order_relaxed);
+  return VDSL_OK;
 }

@@ -14,10 +14,12 @@
 //     together land in 16 distinct 16-byte bank groups (rows 4 apart share a 64-byte bank window
 //     and the XOR gives them distinct slots), so fragment reads are free of bank conflicts.
 //
+// A stage is BKB = 64 or 128 K bytes: one or two 64-byte sub-stages, each laid out as above.
 // Pipeline per stage t (ring of NS LDS stages): issue the copy of stage t+NS-1 (into the slot
 // stage t-1 used), read fragments k-step by k-step one step ahead of the MFMAs, then before the
 // MFMAs of the last k-step wait for this wave's copy of stage t+1 (vmcnt = copies issued after
-// it) and meet the block barrier, so stage t+1's first fragment reads overlap those MFMAs.  The
+// it) and meet the block barrier, so stage t+1's first fragment reads overlap those MFMAs.  A
+// 128-byte stage halves the barriers per MFMA.  The
 // barrier also orders every wave's reads of stage t before the copy that overwrites it (issued
 // at stage t+1).  Rows past M or N are clamped to the last row (their products only reach
 // outputs that are not stored).
@@ -27,18 +29,23 @@
 
 namespace vdsl {
 
-template <class T, int BM_, int BN_, int WGM_, int WGN_, int NS_>
+template <class T, int BM_, int BN_, int WGM_, int WGN_, int NS_, int BKB_ = 64>
 struct DmaConfig {
   static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, NS = NS_;
-  static constexpr int BKB = 64;                     // K bytes per stage
+  static constexpr int BKB = BKB_;                   // K bytes per stage (one barrier per stage)
+  static constexpr int KSUB = BKB / 64;              // 64-byte sub-stages per stage
+  static constexpr int KS = BKB / 32;                // MFMA k-steps per stage
   static constexpr int RPB = 16;                     // rows per 1 KiB LDS block
   static constexpr int NT = WGM * WGN * 64, NW = WGM * WGN;
   static constexpr int WTM = BM / WGM, WTN = BN / WGN;
   static constexpr int FM = WTM / 32, FN = WTN / 32;
-  static constexpr int STAGE = (BM + BN) * BKB;
+  static constexpr int SUB = (BM + BN) * 64;         // bytes of one sub-stage
+  static constexpr int STAGE = KSUB * SUB;
   static constexpr int LDS_BYTES = NS * STAGE;
-  static constexpr int NBLK = (BM + BN) / RPB;       // 1 KiB copy blocks per stage
-  static constexpr int BPW = NBLK / NW;              // copy instructions per wave per stage
+  static constexpr int NBLK = (BM + BN) / RPB;       // 1 KiB copy blocks per sub-stage
+  static constexpr int BPW = NBLK / NW;              // copy instructions per wave per sub-stage
+  static constexpr int CPW = KSUB * BPW;             // copy instructions per wave per stage
+  static_assert(BKB % 64 == 0 && BKB > 0, "a stage is a whole number of 64-byte sub-stages");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 MFMA tiles");
   static_assert(BM % RPB == 0 && BN % RPB == 0 && NBLK % NW == 0, "copy blocks must split evenly over waves");
   static_assert(NS >= 3, "the loop keeps two stages in flight beyond the one being read");
@@ -73,6 +80,9 @@ VDSL_DMA_WAIT_CASE(6)
 VDSL_DMA_WAIT_CASE(8)
 VDSL_DMA_WAIT_CASE(9)
 VDSL_DMA_WAIT_CASE(12)
+VDSL_DMA_WAIT_CASE(16)
+VDSL_DMA_WAIT_CASE(18)
+VDSL_DMA_WAIT_CASE(24)
 #undef VDSL_DMA_WAIT_CASE
 
 // Block barrier without the full memory fence of __syncthreads (which would also wait for the
@@ -85,13 +95,14 @@ __device__ __forceinline__ void dma_barrier() {
 }
 
 // K loop over bytes [kb_begin, kb_end) for the tile at (m0, n0).  Requires kb_begin % 16 == 0 and
-// (kb_end - kb_begin) % 64 == 0; Kb = row stride of A and B in bytes.
+// (kb_end - kb_begin) % BKB == 0; Kb = row stride of A and B in bytes.
 template <class T, class Cfg, class AccT, int FM_, int FN_>
 __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const char* __restrict__ B, int M, int N, int Kb,
                                              int kb_begin, int kb_end, int m0, int n0, char* smem, AccT (&acc)[FM_][FN_]) {
   static_assert(FM_ == Cfg::FM && FN_ == Cfg::FN, "accumulator array must match the configuration");
   using Frag = typename T::Frag;
-  constexpr int FM = Cfg::FM, FN = Cfg::FN, NS = Cfg::NS, BPW = Cfg::BPW, STAGE = Cfg::STAGE;
+  constexpr int FM = Cfg::FM, FN = Cfg::FN, NS = Cfg::NS, BPW = Cfg::BPW, STAGE = Cfg::STAGE, SUB = Cfg::SUB;
+  constexpr int KS = Cfg::KS, KSUB = Cfg::KSUB, CPW = Cfg::CPW;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -101,7 +112,7 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = T::zero();
 
-  // Copy block b = wave * BPW + u of a stage: blocks [0, BM/16) are A rows 16b.., the rest B.
+  // Copy block b = wave * BPW + u of a sub-stage: blocks [0, BM/16) are A rows 16b.., the rest B.
   // Lane l copies row 16 * (b') + l / 4, LDS slot l % 4, i.e. global chunk (l % 4) ^ swizzle.
   const char* src[BPW];
 #pragma unroll
@@ -114,24 +125,35 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
     src[u] = (is_a ? A : B) + row * Kb + kb_begin + c * 16;
   }
   char* const dst = smem + wave * BPW * 1024;
-  // This lane's fragment rows (within the stage's A and B areas).
+  // This lane's fragment rows (within a sub-stage's A and B areas).
   const int ra = wm * Cfg::WTM + (lane & 31);
   const int rb = wn * Cfg::WTN + (lane & 31);
   const int hk = lane >> 5;
   const char* const fa = smem;
-  const char* const fb = smem + Cfg::BM * Cfg::BKB;
+  const char* const fb = smem + Cfg::BM * 64;
 
 #define VDSL_DMA_COPY(ST, KB)                                                                     \
   do {                                                                                            \
-    _Pragma("unroll") for (int u = 0; u < BPW; ++u)                                               \
-      lds_copy16(src[u] + (KB), dst + (ST) * STAGE + u * 1024);                                   \
+    _Pragma("unroll") for (int sb = 0; sb < KSUB; ++sb)                                           \
+      _Pragma("unroll") for (int u = 0; u < BPW; ++u)                                             \
+        lds_copy16(src[u] + (KB) + 64 * sb, dst + (ST) * STAGE + sb * SUB + u * 1024);            \
   } while (0)
+// Copies [I0, I1) of a stage's CPW copies (copy i = sub-stage i / BPW, block i % BPW).
+#define VDSL_DMA_COPY_PART(ST, KB, I0, I1)                                                        \
+  do {                                                                                            \
+    _Pragma("unroll") for (int i = (I0); i < (I1); ++i)                                           \
+      lds_copy16(src[i % BPW] + (KB) + 64 * (i / BPW), dst + (ST) * STAGE + (i / BPW) * SUB +     \
+                 (i % BPW) * 1024);                                                               \
+  } while (0)
+// Fragments of k-step KK (32 K bytes) of stage ST: sub-stage KK / 2, chunks 2 (KK % 2) + hk.
 #define VDSL_DMA_READ(A_, B_, ST, KK)                                                             \
   do {                                                                                            \
     _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                \
-      A_[i] = *reinterpret_cast<const Frag*>(fa + (ST) * STAGE + dma_slot(ra + 32 * i, 2 * (KK) + hk)); \
+      A_[i] = *reinterpret_cast<const Frag*>(fa + (ST) * STAGE + ((KK) >> 1) * SUB +              \
+                                             dma_slot(ra + 32 * i, 2 * ((KK) & 1) + hk));          \
     _Pragma("unroll") for (int j = 0; j < FN; ++j)                                                \
-      B_[j] = *reinterpret_cast<const Frag*>(fb + (ST) * STAGE + dma_slot(rb + 32 * j, 2 * (KK) + hk)); \
+      B_[j] = *reinterpret_cast<const Frag*>(fb + (ST) * STAGE + ((KK) >> 1) * SUB +              \
+                                             dma_slot(rb + 32 * j, 2 * ((KK) & 1) + hk));          \
   } while (0)
 #define VDSL_DMA_MMA(A_, B_)                                                                      \
   do {                                                                                            \
@@ -156,6 +178,20 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
     __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - 1, 0);                                  \
     __builtin_amdgcn_sched_barrier(0);                                                            \
   } while (0)
+// A k-step that also issues NC copies (VMEM, mask 0x020): reads first (after one MFMA when
+// LATE), then each copy between MFMAs, so the copies of all waves do not reach the address unit
+// in one burst while no MFMA issues.
+#define VDSL_DMA_ORDER_COPIES(LATE, NC)                                                           \
+  do {                                                                                            \
+    if (LATE) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                  \
+    __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);                                      \
+    _Pragma("unroll") for (int c = 0; c < (NC); ++c) {                                            \
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                          \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                          \
+    }                                                                                             \
+    __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);                                      \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+  } while (0)
 
 // Wave priority (s_setprio, the issue arbiter's per-wave priority) is raised while a wave issues
 // its fragment reads and MFMAs and dropped for its copies, waits and barrier, so of the two waves
@@ -171,29 +207,80 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
   if (nk <= 0) return;
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s) VDSL_DMA_COPY(s, min(s, nk - 1) * Cfg::BKB);
-  VDSL_WAIT_VM_LGKM0((NS - 2) * BPW);
+  VDSL_WAIT_VM_LGKM0((NS - 2) * CPW);
   dma_barrier();
-  Frag a0[FM], b0[FN], a1[FM], b1[FN];
-  VDSL_DMA_READ(a0, b0, 0, 0);
+  if constexpr (KS == 4) {
+    // 128-byte stages: fragments are read two k-steps ahead (four register sets, k-step kk in set
+    // kk), so an LDS read has two k-steps of MFMAs to land.  The barrier moves one k-step earlier:
+    // it precedes the first read of stage kt+1 (k-step 2's group).
+    Frag af[4][FM], bf[4][FN];
+    VDSL_DMA_READ(af[0], bf[0], 0, 0);
+    VDSL_DMA_READ(af[1], bf[1], 0, 1);
+    int st = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+      const int nst = st + 1 == NS ? 0 : st + 1;
+      const int cst = st == 0 ? NS - 1 : st - 1;
+      const int kb_copy = min(kt + NS - 1, nk - 1) * Cfg::BKB;
+      __builtin_amdgcn_sched_barrier(0);
+      VDSL_DMA_PRIO(1);
+      VDSL_DMA_READ(af[2], bf[2], st, 2);
+      VDSL_DMA_MMA(af[0], bf[0]);
+      VDSL_DMA_COPY_PART(cst, kb_copy, 0, CPW / 2);
+      VDSL_DMA_ORDER_COPIES(true, CPW / 2);
+      VDSL_DMA_READ(af[3], bf[3], st, 3);
+      VDSL_DMA_MMA(af[1], bf[1]);
+      VDSL_DMA_COPY_PART(cst, kb_copy, CPW / 2, CPW);
+      VDSL_DMA_ORDER_COPIES(true, CPW - CPW / 2);
+      VDSL_DMA_PRIO(0);
+      VDSL_WAIT_VM_LGKM0((NS - 2) * CPW);
+      dma_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      VDSL_DMA_PRIO(1);
+      VDSL_DMA_READ(af[0], bf[0], nst, 0);
+      VDSL_DMA_MMA(af[2], bf[2]);
+      VDSL_DMA_ORDER_LATE();
+      VDSL_DMA_READ(af[1], bf[1], nst, 1);
+      VDSL_DMA_MMA(af[3], bf[3]);
+      VDSL_DMA_ORDER_LATE();
+      VDSL_DMA_PRIO(0);
+      st = nst;
+    }
+    VDSL_WAIT_VM_LGKM0(0);
+    return;
+  }
+  // Fragment double buffer: k-step kk of a stage computes from set kk % 2 while set (kk + 1) % 2
+  // is read (KS is even, so every stage starts on set 0).
+  Frag af[2][FM], bf[2][FN];
+  VDSL_DMA_READ(af[0], bf[0], 0, 0);
   int st = 0;
   for (int kt = 0; kt < nk; ++kt) {
     const int nst = st + 1 == NS ? 0 : st + 1;
     const int cst = st == 0 ? NS - 1 : st - 1;  // = (kt + NS - 1) % NS
-    // Past the last stage the copy repeats it (never read): the copy count per stage stays fixed,
-    // which is what the vmcnt in the wait below counts on.
-    VDSL_DMA_COPY(cst, min(kt + NS - 1, nk - 1) * Cfg::BKB);
+    // The copy of stage kt+NS-1 (into the slot stage kt-1 used, whose reads all ended before the
+    // last barrier) is spread over the k-steps before the last, between MFMAs.  Past the last
+    // stage it repeats that stage (never read): the copy count per stage stays fixed, which is
+    // what the vmcnt in the wait below counts on.
+    const int kb_copy = min(kt + NS - 1, nk - 1) * Cfg::BKB;
     __builtin_amdgcn_sched_barrier(0);
-    VDSL_DMA_PRIO(1);
-    VDSL_DMA_READ(a1, b1, st, 1);
-    VDSL_DMA_MMA(a0, b0);
-    VDSL_DMA_ORDER_LATE();
-    VDSL_DMA_PRIO(0);
-    VDSL_WAIT_VM_LGKM0((NS - 2) * BPW);
+#pragma unroll
+    for (int kk = 0; kk < KS - 1; ++kk) {
+      constexpr int kParts = KS - 1;
+      const int c0 = kk * CPW / kParts, c1 = (kk + 1) * CPW / kParts;
+      VDSL_DMA_PRIO(1);
+      VDSL_DMA_READ(af[(kk + 1) & 1], bf[(kk + 1) & 1], st, kk + 1);
+      VDSL_DMA_MMA(af[kk & 1], bf[kk & 1]);
+      VDSL_DMA_COPY_PART(cst, kb_copy, c0, c1);
+      VDSL_DMA_ORDER_COPIES(kk == 0, c1 - c0);
+      VDSL_DMA_PRIO(0);
+    }
+    // Before the last k-step: this wave's copy of stage kt+1 has landed, and every wave's has
+    // once all meet the barrier (which also ends all reads of the slot the next copy overwrites).
+    VDSL_WAIT_VM_LGKM0((NS - 2) * CPW);
     dma_barrier();
     __builtin_amdgcn_sched_barrier(0);
     VDSL_DMA_PRIO(1);
-    VDSL_DMA_READ(a0, b0, nst, 0);
-    VDSL_DMA_MMA(a1, b1);
+    VDSL_DMA_READ(af[0], bf[0], nst, 0);
+    VDSL_DMA_MMA(af[1], bf[1]);
     VDSL_DMA_ORDER();
     VDSL_DMA_PRIO(0);
     st = nst;
@@ -201,14 +288,18 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
   // Drain the copies of the stages past the end before the block's LDS can be reused or freed.
   VDSL_WAIT_VM_LGKM0(0);
 #undef VDSL_DMA_PRIO
+#undef VDSL_DMA_ORDER_COPIES
 #undef VDSL_DMA_ORDER_LATE
 #undef VDSL_DMA_ORDER
 #undef VDSL_DMA_MMA
 #undef VDSL_DMA_READ
+#undef VDSL_DMA_COPY_PART
 #undef VDSL_DMA_COPY
 }
 
-// True when the direct-to-LDS loop can run this K range.
-inline bool dma_k_ok(int64_t kb_begin, int64_t kbytes) { return kb_begin % 16 == 0 && kbytes % 64 == 0 && kbytes > 0; }
+// True when the direct-to-LDS loop with `bkb` K bytes per stage can run this K range.
+inline bool dma_k_ok(int64_t kb_begin, int64_t kbytes, int64_t bkb = 64) {
+  return kb_begin % 16 == 0 && kbytes % bkb == 0 && kbytes > 0;
+}
 
 }  // namespace vdsl

@@ -43,7 +43,12 @@ using Di16 = DmaConfig<MfmaI8, 64, 128, 2, 2, 4>;   // 4 waves of 32x64, two blo
 using Di17 = DmaConfig<MfmaI8, 128, 128, 2, 2, 4>;  // 4 waves of 64x64, 2 blocks per CU
 using Di18 = DmaConfig<MfmaI8, 128, 128, 2, 4, 4>;  // 8 waves of 64x32
 using Di19 = DmaConfig<MfmaI8, 128, 64, 2, 2, 4>;   // 4 waves of 64x32
-constexpr int kNumConfigs = 20;
+// 128-byte stages (one barrier per 128 int8 of K); need K % 128 == 0
+using Di20 = DmaConfig<MfmaI8, 128, 128, 2, 4, 4, 128>;  // 8 waves of 64x32
+using Di21 = DmaConfig<MfmaI8, 128, 128, 2, 2, 4, 128>;  // 4 waves of 64x64
+using Di22 = DmaConfig<MfmaI8, 64, 128, 2, 2, 4, 128>;   // 4 waves of 32x64
+constexpr int kNumConfigs = 23;
+constexpr int kFirstDma = 14, kFirstDma128 = 20;
 
 __device__ __forceinline__ void store_y(void* y, int out_dtype, size_t o, float v) {
   if (out_dtype == VDSL_F32) static_cast<float*>(y)[o] = v;
@@ -236,9 +241,9 @@ int64_t tiles_for(int bm, int bn, int64_t M, int64_t N) { return ((M + bm - 1) /
 // register-staged configuration: 1005), else 64x128 blocks with split-K (512x1024x8192: 450
 // against 345).  Other K use the register-staged loop, where 128x64 tiles measured fastest.
 int choose_config(int64_t M, int64_t N, int64_t K) {
-  const bool dma = K % 64 == 0 && K > 0;
+  const bool dma = K % 64 == 0 && K > 0, dma128 = K % 128 == 0 && K > 0;
   const int o = gemm_config_override();
-  if (o >= 0 && o < kNumConfigs && (o < 14 || dma)) return o;
+  if (o >= 0 && o < kNumConfigs && (o < kFirstDma || (o < kFirstDma128 ? dma : dma128))) return o;
   if (!dma) return 7;
   return ((M + 127) / 128) * ((N + 127) / 128) >= 256 ? 18 : 16;
 }
@@ -246,7 +251,8 @@ int choose_config(int64_t M, int64_t N, int64_t K) {
 void config_tile(int c, int& bm, int& bn) {
   static const int t[kNumConfigs][2] = {{128, 128}, {256, 128}, {128, 256}, {256, 256}, {256, 256}, {256, 128}, {128, 128},
                                           {128, 64},  {64, 128},  {128, 128}, {256, 128}, {128, 256}, {256, 256}, {256, 128},
-                                          {128, 256}, {256, 256}, {64, 128},  {128, 128}, {128, 128}, {128, 64}};
+                                          {128, 256}, {256, 256}, {64, 128},  {128, 128}, {128, 128}, {128, 64},
+                                          {128, 128}, {128, 128}, {64, 128}};
   bm = t[c][0];
   bn = t[c][1];
 }
@@ -295,7 +301,7 @@ int launch_dma(const int8_t* a, const int8_t* b, const float* xs, const float* w
                        out_dtype, relu, ao, nullptr, m, n, k, k);
     return check_launch("gemm_w8a8_dma");
   }
-  // k_per: a multiple of the 64-byte stage, so with K % 64 == 0 every split is whole stages
+  // k_per: a multiple of the stage (BKB bytes), so with K % BKB == 0 every split is whole stages
   const int kt = (k + Cfg::BKB - 1) / Cfg::BKB;
   const int k_per = ((kt + split - 1) / split) * Cfg::BKB;
   const int nsplit = (k + k_per - 1) / k_per;
@@ -313,6 +319,9 @@ int launch_w8a8(const int8_t* a, const int8_t* b, const float* xs, const float* 
     case 17: return launch_dma<Di17>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
     case 18: return launch_dma<Di18>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
     case 19: return launch_dma<Di19>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 20: return launch_dma<Di20>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 21: return launch_dma<Di21>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
+    case 22: return launch_dma<Di22>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
     case 1: return launch_cfg<I1>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
     case 2: return launch_cfg<I2>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
     case 3: return launch_cfg<I3>(a, b, xs, wsc, y, out_dtype, relu, ao, wacc, m, n, k, split, s);
