@@ -44,14 +44,20 @@ def measured_traffic(kernel):
         return None
 
 
-def time_launches(q, dev, fn, reps, warmup=30):
+def time_launches(q, dev, fn, reps, warmup=30, warmup_ms=25.0):
     """Mean duration of one fn() call from HIP events on q's stream around `reps` back-to-back
-    stream launches, after `warmup` untimed calls (enough GPU time for the clocks to ramp up after
-    host-side setup).  This is the per-kernel figure; graph replays (time_replays) add the graph's
-    launch latency to the first node."""
+    stream launches, after at least `warmup` untimed calls and at least `warmup_ms` of wall time
+    spent in them (the clocks take milliseconds of GPU work to ramp up after host-side setup: a
+    GEMM timed after 30 launches, ~2 ms, reads 7-10% low).  This is the per-kernel figure; graph
+    replays (time_replays) add the graph's launch latency to the first node."""
     from vernondsl_amd.rhi import Event
-    for _ in range(warmup):
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or (time.perf_counter() - t0) * 1e3 < warmup_ms:
         fn()
+        n += 1
+        if n % 8 == 0:
+            q.sync()
     q.sync()
     e0, e1 = Event(dev), Event(dev)
     e0.record(q)
@@ -65,16 +71,22 @@ def time_launches(q, dev, fn, reps, warmup=30):
     return ms
 
 
-def time_replays(q, dev, fn, steps, warmup, per_graph=1):
-    """Records `per_graph` consecutive calls of fn() into one hipGraph, replays it `warmup` then
-    `steps` times; returns (ms per call from HIP events on q's stream, wall ms per call)."""
+def time_replays(q, dev, fn, steps, warmup, per_graph=1, warmup_ms=25.0):
+    """Records `per_graph` consecutive calls of fn() into one hipGraph, replays it at least `warmup`
+    times and for at least `warmup_ms` of wall time, then `steps` times; returns (ms per call from
+    HIP events on q's stream, wall ms per call)."""
     from vernondsl_amd.rhi import Event
     with q.capture() as rec:
         for _ in range(per_graph):
             fn()
     g = rec.graph
-    for _ in range(warmup):
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or (time.perf_counter() - t0) * 1e3 < warmup_ms:
         g.launch(q)
+        n += 1
+        if n % 4 == 0:
+            q.sync()
     q.sync()
     e0, e1 = Event(dev), Event(dev)
     t0 = time.perf_counter()
@@ -252,7 +264,7 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
            "metric": "MFMA TFLOPS (GEMM)", "value": tflops, "unit": "TFLOP/s", "ms_per_step": ms,
            "eager_ms_per_step": eager_ms, "flop_per_step": flops, "loss": loss,
            "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                        "frac": gt / PEAK_BF16_TFLOPS, "kernel": "gemm_bf16_dma<128x256> (GELU, bf16 out, f32 pre) 2048x4096x4096",
+                        "frac": gt / PEAK_BF16_TFLOPS, "kernel": "gemm_bf16_dma<128x256, 8 waves, 128-byte stages> (GELU, bf16 out, f32 pre) 2048x4096x4096",
                         "kernel_ms": gms, "traffic": measured_traffic("gemm_bf16")},
            "whole_graph_frac_of_peak": tflops / PEAK_BF16_TFLOPS}
     if do_cpu:
@@ -317,7 +329,7 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
            "eager_ms_per_step": eager_ms, "ops_per_step": ops,
            "parity": parity,
            "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                        "frac": gt / PEAK_INT8_TOPS, "kernel": "gemm_w8a8_dma<128x128, 8 waves> (dequant+ReLU) 512x8192x8192", "kernel_ms": gms,
+                        "frac": gt / PEAK_INT8_TOPS, "kernel": "gemm_w8a8_dma<128x128, 8 waves, 128-byte stages> (dequant+ReLU) 512x8192x8192", "kernel_ms": gms,
                         "traffic": measured_traffic("gemm_w8a8")},
            "whole_graph_frac_of_peak": tops / PEAK_INT8_TOPS}
     if do_cpu:

@@ -236,16 +236,18 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restri
 int64_t tiles_for(int bm, int bn, int64_t M, int64_t N) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
 // Configuration for a shape.  The direct-to-LDS loop (14..) runs when K is a multiple of its
-// 64-byte stage.  Measured on MI355X with random int8 (config-5 shapes): 128x128 blocks of 8
-// waves when they give every CU a block (512x8192x8192: 1198 TOP/s; 4 waves: 1154; the best
-// register-staged configuration: 1005), else 64x128 blocks with split-K (512x1024x8192: 450
-// against 345).  Other K use the register-staged loop, where 128x64 tiles measured fastest.
+// 64-byte stage (128-byte stages, 20..: K % 128 == 0).  Measured on MI355X with random int8
+// (config-5 shapes, clocks warm): 128x128 blocks of 8 waves when they give every CU a block
+// (512x8192x8192: 1438-1460 TOP/s with 128-byte stages, 1424-1426 with 64-byte ones, 1366 with 4
+// waves), else 64x128 blocks with split-K (512x1024x8192: 460, the same with 128-byte stages).
+// Other K use the register-staged loop, where 128x64 tiles measured fastest.
 int choose_config(int64_t M, int64_t N, int64_t K) {
   const bool dma = K % 64 == 0 && K > 0, dma128 = K % 128 == 0 && K > 0;
   const int o = gemm_config_override();
   if (o >= 0 && o < kNumConfigs && (o < kFirstDma || (o < kFirstDma128 ? dma : dma128))) return o;
   if (!dma) return 7;
-  return ((M + 127) / 128) * ((N + 127) / 128) >= 256 ? 18 : 16;
+  if (((M + 127) / 128) * ((N + 127) / 128) >= 256) return dma128 ? 20 : 18;
+  return 16;
 }
 
 void config_tile(int c, int& bm, int& bn) {
