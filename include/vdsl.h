@@ -321,6 +321,21 @@ int vdsl_gemm_w8a8_workspace_bytes(int64_t M, int64_t N, int64_t K, size_t* byte
 int vdsl_op_gemm_w8a8(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer xq,
                       vdsl_buffer x_scale, vdsl_buffer w, vdsl_buffer w_scale, vdsl_buffer y,
                       int32_t out_dtype, int32_t relu, vdsl_buffer acc_out, vdsl_buffer workspace);
+/* Weights in MFMA fragment order, for vdsl_op_gemm_w8a8_packed (a layout transform done once when
+ * weights are loaded, not per call).  w: int8 [N][K] (out x in); wp: int8, N*K bytes, receives
+ * 1 KiB units u = (nb, kb), nb = n / 32, kb = k / 32, at byte (nb * (K/32) + kb) * 1024, lane l's
+ * 16 bytes at 16 l = w[32 nb + l % 32][32 kb + 16 (l / 32) .. +15].  N % 32 == 0, K % 32 == 0.
+ * Same role as ti.field storage (fractal.py:8) for a weight operand: no reference counterpart. */
+int vdsl_op_pack_w8a8_weights(vdsl_queue q, int64_t N, int64_t K, vdsl_buffer w, vdsl_buffer wp);
+/* vdsl_op_gemm_w8a8 with packed weights wp (vdsl_op_pack_w8a8_weights): same arithmetic, bit for
+ * bit.  N % 32 == 0, K % 512 == 0.  workspace: int32 split-K partials,
+ * vdsl_gemm_w8a8_packed_workspace_bytes() bytes (0 when the launch does not split K; any
+ * contents).  Two calls that overlap in time need two workspaces. */
+int vdsl_gemm_w8a8_packed_workspace_bytes(int64_t M, int64_t N, int64_t K, size_t* bytes);
+int vdsl_op_gemm_w8a8_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer xq,
+                             vdsl_buffer x_scale, vdsl_buffer wp, vdsl_buffer w_scale, vdsl_buffer y,
+                             int32_t out_dtype, int32_t relu, vdsl_buffer acc_out,
+                             vdsl_buffer workspace);
 
 /* ---- failure injection (tests of error paths, host-side only) ----------------------------- */
 /* After `n` more successful buffer allocations, the next one fails with VDSL_ERR_OUT_OF_MEMORY

@@ -223,7 +223,8 @@ def test_optional_outputs_absent(dev, q, rows, cols):
         t.free()
 
 
-@pytest.mark.parametrize("rows,cols,dt", [(512, 8192, "bf16"), (37, 100, "f32"), (5, 16, "bf16")])
+@pytest.mark.parametrize("rows,cols,dt", [(512, 8192, "bf16"), (37, 100, "f32"), (5, 16, "bf16"), (64, 8192, "f32"),
+                                          (3, 16384, "bf16"), (7, 4096, "f32"), (9, 4104, "f32")])
 def test_quantize_rows(dev, q, rows, cols, dt):
     x = rng.normal(41, rows * cols).reshape(rows, cols)
     if rows > 3:

@@ -133,3 +133,29 @@ def test_w8a8_config5_full_size_sampled_rows(dev, q):
     ref = oracle.w8a8_forward(x[rows], layers)
     assert np.array_equal(got[rows], ref)
     assert np.isfinite(rng.bf16_to_f32(got)).all()
+
+
+def test_w8a8_rewritten_weights_are_repacked(dev, q):
+    """A weight written after a run is packed again before the next run, and before a capture."""
+    x, layers = spec.w8a8_inputs(batch=32, widths=(1024, 512, 256))
+    g = graph.w8a8_infer_graph(32, (1024, 512, 256))
+    assert [op.kind for op in g.ops].count("w8a8_packed") == 2
+    exe = g.compile(dev)
+    exe.write(q, "X", x)
+    for li, (w, s) in enumerate(layers):
+        exe.write(q, f"W{li}", w)
+        exe.write(q, f"S{li}", s)
+    exe.run(q)
+    assert np.array_equal(exe.read(q, "Y"), oracle.w8a8_forward(x, layers))
+    w0 = np.ascontiguousarray(layers[0][0][::-1])  # other weights, same shape
+    layers2 = [(w0, layers[0][1])] + layers[1:]
+    exe.write(q, "W0", w0)
+    exe.run(q)
+    assert np.array_equal(exe.read(q, "Y"), oracle.w8a8_forward(x, layers2))
+    exe.write(q, "W0", layers[0][0])
+    step = exe.capture(q)
+    step.launch(q)
+    q.sync()
+    assert np.array_equal(exe.read(q, "Y"), oracle.w8a8_forward(x, layers))
+    step.destroy()
+    exe.free()

@@ -31,6 +31,22 @@ def test_inference_graph_has_no_backward():
     assert [op.attrs.get("relu") for op in g.ops if op.kind == "w8a8"] == [True, False]
 
 
+def test_inference_graph_packs_weights():
+    """Layers whose shape the packed int8 GEMM takes (in % 512, out % 32) read packed weights made
+    by prepare ops, which are not part of the replayed step; others keep the row-major GEMM."""
+    g = graph.w8a8_infer_graph(batch=8, widths=(512, 1024, 96, 64))
+    assert [op.kind for op in g.ops] == ["quantize", "w8a8_packed", "quantize", "w8a8_packed", "quantize", "w8a8"]
+    assert [op.kind for op in g.prepare_ops] == ["pack_w8a8", "pack_w8a8"]
+    assert [op.inputs[0].name for op in g.prepare_ops] == ["W0", "W1"]
+    for op, pre in zip([o for o in g.ops if o.kind == "w8a8_packed"], g.prepare_ops):
+        assert op.inputs[2] is pre.outputs[0] and op.inputs[2].shape == pre.inputs[0].shape
+    g2 = graph.Graph()
+    x = g2.input("X", (8, 512), "bf16")
+    g2.quant_linear(x, g2.param("W", (64, 512), "i8", False), g2.param("S", (64,), "f32", False), relu=True,
+                    packed=False)
+    assert [op.kind for op in g2.ops] == ["quantize", "w8a8"] and not g2.prepare_ops
+
+
 def test_graph_rejects_bad_programs():
     g = graph.Graph()
     x = g.input("X", (4, 8), "bf16")

@@ -138,6 +138,9 @@ PROTOTYPES = {
     "vdsl_op_quantize_rows_i8": (C.c_int, [_vp, _i64, _i64, _i32, _vp, _vp, _vp]),
     "vdsl_gemm_w8a8_workspace_bytes": (C.c_int, [_i64, _i64, _i64, C.POINTER(_sz)]),
     "vdsl_op_gemm_w8a8": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
+    "vdsl_op_pack_w8a8_weights": (C.c_int, [_vp, _i64, _i64, _vp, _vp]),
+    "vdsl_gemm_w8a8_packed_workspace_bytes": (C.c_int, [_i64, _i64, _i64, C.POINTER(_sz)]),
+    "vdsl_op_gemm_w8a8_packed": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "vdsl_debug_fail_alloc_after": (C.c_int, [_i64]),
     "vdsl_debug_gemm_config": (C.c_int, [_i32]),
 }

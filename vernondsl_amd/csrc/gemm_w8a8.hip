@@ -15,6 +15,7 @@
 // with atomics - integer addition is exact and order-independent, so the result is still
 // deterministic - and a second kernel applies the dequant epilogue.
 
+#include "gemm_bpk.h"
 #include "gemm_dma.h"
 #include "gemm_mfma.h"
 
@@ -205,6 +206,57 @@ __global__ __launch_bounds__(256) void quantize_rows_vec(const void* __restrict_
   }
 }
 
+// Rows of exactly NV 16-byte vectors per lane (256 lanes): the row is read once and held in
+// registers across the block max, so it is never fetched twice (bf16 [512][8192]: NV = 4).
+template <int DT, int NV>
+__global__ __launch_bounds__(256) void quantize_rows_resident(const void* __restrict__ x, int8_t* __restrict__ q,
+                                                              float* __restrict__ scale) {
+  constexpr int PV = DT == VDSL_F32 ? 4 : 8;
+  constexpr int64_t COLS = static_cast<int64_t>(NV) * 256 * PV;
+  __shared__ float wmax[4];
+  const int64_t row = blockIdx.x;
+  const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const char*>(x) + row * COLS * (DT == VDSL_F32 ? 4 : 2));
+  u32x4 v[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) v[k] = __builtin_nontemporal_load(src + threadIdx.x + 256 * k);
+  auto elem = [&](int k, int e) -> float {
+    const uint32_t w = v[k][DT == VDSL_F32 ? e : e >> 1];
+    if (DT == VDSL_F32) return __uint_as_float(w);
+    return __uint_as_float((e & 1) ? (w & 0xFFFF0000u) : (w << 16));
+  };
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+#pragma unroll
+    for (int e = 0; e < PV; ++e) amax = fmaxf(amax, fabsf(elem(k, e)));
+  amax = wave_max(amax);
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float s = amax / 127.0f;
+  if (threadIdx.x == 0) scale[row] = s;
+  int8_t* dst = q + row * COLS;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    uint32_t packed[PV / 4];
+#pragma unroll
+    for (int w = 0; w < PV / 4; ++w) packed[w] = 0;
+#pragma unroll
+    for (int e = 0; e < PV; ++e) {
+      int iv = 0;
+      if (s > 0.0f) {
+        float t = rintf(elem(k, e) / s);
+        t = fminf(fmaxf(t, -127.0f), 127.0f);
+        iv = static_cast<int>(t);
+      }
+      packed[e / 4] |= (static_cast<uint32_t>(iv) & 0xFFu) << (8 * (e % 4));
+    }
+    const int64_t vi = threadIdx.x + 256 * k;
+    if (PV == 4) *reinterpret_cast<uint32_t*>(dst + vi * PV) = packed[0];
+    else *reinterpret_cast<uint2*>(dst + vi * PV) = make_uint2(packed[0], packed[PV / 4 - 1]);
+  }
+}
+
 // Any width: one wave per row, element at a time, same arithmetic.
 template <int DT>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restrict__ x, int8_t* __restrict__ q,
@@ -341,6 +393,193 @@ int launch_w8a8(const int8_t* a, const int8_t* b, const float* xs, const float* 
   }
 }
 
+
+// ---- packed-weight GEMM (gemm_bpk.h main loop) ------------------------------------------------
+// Weights in fragment order (bpk_pack_kernel), activations row-major through LDS.  A launch of
+// tiles * S blocks: block (tile, z) covers K bytes [z K/S, (z+1) K/S) of its tile.  With S == 1 the
+// block runs the dequant epilogue itself; with S > 1 it stores its int32 partial tile to the
+// workspace in accumulator order (each wave's fragments as 16-byte runs: 1 KiB per store
+// instruction) and w8a8_bpk_reduce adds the S partials and runs the epilogue.  Integer addition
+// is exact and order-free, so the result is the unsplit one, bit for bit.
+//
+// Measured on MI355X, 512x8192x8192, clocks warm.  The MFMA rate depends on the operand bits:
+// the main loop alone ran 41.1 us on random full-range int8, 38.3 us on bytes 0..127 and 33.4 us
+// on bytes 0..15.  On bytes 0..127: 64 x 256 blocks, no split, 35.8 us; 128 x 256 blocks split in
+// two with the partials exchanged inside the kernel (counters, last block adds) 46.3 us; 128 x
+// 256 unsplit on 128 CUs 47.0 us.  The 1024-wide last layer (32 tiles of 64 x 256): the last
+// block of each tile adding S - 1 partials alone took 18.5 us (S = 4) to 28.6 us on full-range
+// data; the separate reduce spreads that work over the whole GPU.
+using P0 = BpkConfig<MfmaI8, 4, 2, 4, 3>;  // 128 x 256 blocks, 4 waves of 128 x 64
+using P1 = BpkConfig<MfmaI8, 2, 2, 4, 3>;  // 64 x 256 blocks, 4 waves of 64 x 64
+using P2 = BpkConfig<MfmaI8, 2, 2, 4, 7>;  // P1 with loads 7 stages ahead (stages % 8 == 0)
+
+// Whole-tile bf16 epilogue through LDS: each wave writes its dequantised fragments as bf16 into a
+// [BM][EPI_ROW] staging tile (2-byte writes; the row stride 528 = 512 + 16 puts the rows r and
+// r + 4 that one store instruction covers into disjoint 16-bank windows), then every thread
+// stores 16-byte runs of whole rows.
+constexpr int kEpiRow = 528;
+template <class Cfg>
+constexpr int bpk_smem_bytes() {
+  return Cfg::LDS_BYTES > Cfg::BM * kEpiRow ? Cfg::LDS_BYTES : Cfg::BM * kEpiRow;
+}
+
+template <class Cfg>
+__global__ __launch_bounds__(Cfg::NT, 1) void gemm_w8a8_bpk(const int8_t* __restrict__ A, const int8_t* __restrict__ Bp,
+                                                         const float* __restrict__ xs, const float* __restrict__ wsc,
+                                                         void* __restrict__ y, int out_dtype, int relu,
+                                                         int32_t* __restrict__ acc_out, char* __restrict__ part, int M,
+                                                         int N, int K, int S) {
+  constexpr int FM = Cfg::FM, FN = Cfg::FN, W = Cfg::W;
+  constexpr size_t WAVE_BYTES = static_cast<size_t>(FM) * FN * 4096;
+  // The only __shared__ variable (see gemm_bpk.h); after the main loop it stages the epilogue.
+  __shared__ __attribute__((aligned(1024))) char smem[bpk_smem_bytes<Cfg>()];
+  const int tiles_m = (M + Cfg::BM - 1) / Cfg::BM;
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = w / S, z = w % S;
+  const int m0 = (tile % tiles_m) * Cfg::BM, n0 = (tile / tiles_m) * Cfg::BN;
+  const int kper = K / S;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  i32x16 acc[FM][FN];
+  bpk_mainloop<MfmaI8, Cfg>(reinterpret_cast<const char*>(A), reinterpret_cast<const char*>(Bp), M, N / 32, K, z * kper,
+                            (z + 1) * kper, m0, n0, smem, acc);
+  if (S > 1) {
+    char* const mine = part + ((static_cast<size_t>(tile) * S + z) * W + wave) * WAVE_BYTES + lane * 16;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const i32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          *reinterpret_cast<i32x4*>(mine + ((i * FN + j) * 4 + q) * 1024) = v;
+        }
+    return;
+  }
+  if (out_dtype == VDSL_BF16 && !acc_out && m0 + Cfg::BM <= M && n0 + Cfg::BN <= N) {
+    __syncthreads();  // every wave is past its last read of the main loop's LDS
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int c = 64 * wave + 32 * j + (lane & 31);
+        const float wcol = wsc[n0 + c];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rr = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          *reinterpret_cast<uint16_t*>(smem + rr * kEpiRow + 2 * c) = f32_to_bf16(dequant(acc[i][j][r], xs[m0 + rr], wcol, relu));
+        }
+      }
+    __syncthreads();
+    constexpr int CHUNKS = Cfg::BM * (Cfg::BN * 2 / 16);  // 16-byte runs of the tile
+    char* const yb = static_cast<char*>(y);
+#pragma unroll
+    for (int k = 0; k < CHUNKS / Cfg::NT; ++k) {
+      const int idx = threadIdx.x + Cfg::NT * k;
+      const int rr = idx / (Cfg::BN * 2 / 16), ch = idx % (Cfg::BN * 2 / 16);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(smem + rr * kEpiRow + ch * 16);
+      *reinterpret_cast<u32x4*>(yb + (static_cast<size_t>(m0 + rr) * N + n0) * 2 + ch * 16) = v;
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = n0 + 64 * wave + 32 * j + (lane & 31);
+      if (col >= N) continue;
+      const float wcol = wsc[col];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row < M) {
+          const size_t o = static_cast<size_t>(row) * N + col;
+          const int32_t a = acc[i][j][r];
+          if (acc_out) acc_out[o] = a;
+          store_y(y, out_dtype, o, dequant(a, xs[row], wcol, relu));
+        }
+      }
+    }
+}
+
+// Sum of the S partial tiles of a split launch, then the dequant epilogue.  Thread u takes 16-byte
+// chunk u of one partial (tile, wave, fragment, quarter q, lane): accumulators 4q .. 4q+3 of
+// that lane, i.e. rows 8q + 4 (lane / 32) + 0..3 of column lane % 32 of the fragment.
+template <class Cfg>
+__global__ __launch_bounds__(256) void w8a8_bpk_reduce(const char* __restrict__ part, const float* __restrict__ xs,
+                                                       const float* __restrict__ wsc, void* __restrict__ y, int out_dtype,
+                                                       int relu, int32_t* __restrict__ acc_out, int M, int N, int S,
+                                                       int64_t tiles) {
+  constexpr int FM = Cfg::FM, FN = Cfg::FN, W = Cfg::W;
+  constexpr int64_t WAVE_CHUNKS = static_cast<int64_t>(FM) * FN * 4 * 64;  // 16-byte chunks per wave
+  const int tiles_m = (M + Cfg::BM - 1) / Cfg::BM;
+  const int64_t total = tiles * W * WAVE_CHUNKS;
+  for (int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; u < total; u += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t tw = u / WAVE_CHUNKS;  // tile * W + wave
+    const int rem = static_cast<int>(u % WAVE_CHUNKS);
+    const int tile = static_cast<int>(tw / W), wave = static_cast<int>(tw % W);
+    const int lane = rem & 63, fq = rem >> 6;  // fq = (i * FN + j) * 4 + q
+    const int q = fq & 3, f = fq >> 2, i = f / FN, j = f % FN;
+    const char* p = part + (static_cast<size_t>(tile) * S * W + wave) * (WAVE_CHUNKS * 16) + static_cast<size_t>(rem) * 16;
+    i32x4 sum = *reinterpret_cast<const i32x4*>(p);
+    for (int z = 1; z < S; ++z) sum += *reinterpret_cast<const i32x4*>(p + static_cast<size_t>(z) * W * WAVE_CHUNKS * 16);
+    const int m0 = (tile % tiles_m) * Cfg::BM, n0 = (tile / tiles_m) * Cfg::BN;
+    const int col = n0 + 64 * wave + 32 * j + (lane & 31);
+    if (col >= N) continue;
+    const float wcol = wsc[col];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = m0 + 32 * i + 8 * q + 4 * (lane >> 5) + e;
+      if (row < M) {
+        const size_t o = static_cast<size_t>(row) * N + col;
+        if (acc_out) acc_out[o] = sum[e];
+        store_y(y, out_dtype, o, dequant(sum[e], xs[row], wcol, relu));
+      }
+    }
+  }
+}
+
+// Launch plan of the packed GEMM for a shape: configuration (0 = P0, 1 = P1), K split S, tiles.
+// 128 x 256 tiles when they alone give every CU a block; else 64 x 256; K is split only when
+// those are fewer than 256, into about 256 blocks, each a whole number of loop trips (NR stages
+// of 128 bytes).
+struct BpkPlan {
+  int cfg, split;  // cfg: 0 = P0, 1 = P1, 2 = P2
+  int64_t tiles;
+};
+BpkPlan bpk_plan(int64_t M, int64_t N, int64_t K) {
+  BpkPlan p;
+  const int64_t t0 = ((M + P0::BM - 1) / P0::BM) * ((N + P0::BN - 1) / P0::BN);
+  p.cfg = t0 >= 256 ? 0 : 1;
+  p.tiles = p.cfg == 0 ? t0 : ((M + P1::BM - 1) / P1::BM) * ((N + P1::BN - 1) / P1::BN);
+  const int64_t trips = K / (128 * P0::NR);
+  int64_t s = p.tiles >= 256 ? 1 : (256 + p.tiles - 1) / p.tiles;
+  if (s > trips) s = trips;
+  while (s > 1 && trips % s) --s;
+  p.split = static_cast<int>(s < 1 ? 1 : s);
+  if (p.cfg == 1 && (K / p.split / 128) % P2::NR == 0) p.cfg = 2;
+  return p;
+}
+size_t bpk_workspace_bytes(const BpkPlan& p) {
+  if (p.split == 1) return 0;
+  const size_t tile_bytes = p.cfg == 0 ? static_cast<size_t>(P0::BM) * P0::BN * 4 : static_cast<size_t>(P1::BM) * P1::BN * 4;
+  return static_cast<size_t>(p.tiles) * p.split * tile_bytes;
+}
+
+template <class Cfg>
+int launch_bpk(const BpkPlan& p, const int8_t* a, const int8_t* b, const float* xs, const float* wsc, void* y, int out_dtype,
+               int relu, int32_t* ao, char* part, int m, int n, int k, hipStream_t s) {
+  hipLaunchKernelGGL(gemm_w8a8_bpk<Cfg>, dim3(static_cast<unsigned>(p.tiles * p.split)), dim3(Cfg::NT), 0, s, a, b, xs, wsc, y,
+                     out_dtype, relu, p.split > 1 ? nullptr : ao, part, m, n, k, p.split);
+  VDSL_TRY(check_launch("gemm_w8a8_bpk"));
+  if (p.split == 1) return VDSL_OK;
+  const int64_t chunks = p.tiles * Cfg::W * Cfg::FM * Cfg::FN * 4 * 64;
+  int64_t blocks = (chunks + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(w8a8_bpk_reduce<Cfg>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, part, xs, wsc, y, out_dtype,
+                     relu, ao, m, n, p.split, p.tiles);
+  return check_launch("w8a8_bpk_reduce");
+}
+
 }  // namespace
 }  // namespace vdsl
 
@@ -357,6 +596,20 @@ extern "C" int vdsl_op_quantize_rows_i8(vdsl_queue q, int64_t rows, int64_t cols
   VDSL_TRY(check_buffer(q, scale, static_cast<size_t>(rows) * 4, "scale", true));
   if (rows == 0) return VDSL_OK;
   const int pv = x_dtype == VDSL_F32 ? 4 : 8;
+  if (rows <= 0x7fffffff && (cols == 256 * pv * 4 || cols == 256 * pv * 8)) {  // register-resident rows
+    const dim3 g(static_cast<unsigned>(rows)), b(256);
+    auto* qp = static_cast<int8_t*>(qx->ptr);
+    auto* sp = static_cast<float*>(scale->ptr);
+    const bool nv4 = cols == 256 * pv * 4;
+    if (x_dtype == VDSL_F32) {
+      if (nv4) hipLaunchKernelGGL((quantize_rows_resident<VDSL_F32, 4>), g, b, 0, q->stream, x->ptr, qp, sp);
+      else hipLaunchKernelGGL((quantize_rows_resident<VDSL_F32, 8>), g, b, 0, q->stream, x->ptr, qp, sp);
+    } else {
+      if (nv4) hipLaunchKernelGGL((quantize_rows_resident<VDSL_BF16, 4>), g, b, 0, q->stream, x->ptr, qp, sp);
+      else hipLaunchKernelGGL((quantize_rows_resident<VDSL_BF16, 8>), g, b, 0, q->stream, x->ptr, qp, sp);
+    }
+    return check_launch("quantize_rows_resident");
+  }
   if (cols % pv == 0 && rows <= 0x7fffffff) {  // rows of whole 16-byte vectors (hipMalloc bases are aligned)
     if (x_dtype == VDSL_F32)
       hipLaunchKernelGGL(quantize_rows_vec<VDSL_F32>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, q->stream, x->ptr,
@@ -415,4 +668,67 @@ extern "C" int vdsl_op_gemm_w8a8(vdsl_queue q, int64_t M, int64_t N, int64_t K, 
   hipLaunchKernelGGL(w8a8_epilogue, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, q->stream, wacc, xs, wsc, y->ptr,
                      out_dtype, relu, ao, m, n);
   return check_launch("w8a8_epilogue");
+}
+
+
+extern "C" int vdsl_op_pack_w8a8_weights(vdsl_queue q, int64_t N, int64_t K, vdsl_buffer w, vdsl_buffer wp) {
+  VDSL_TRY(enter_queue(q));
+  if (N < 0 || K < 0) return fail(VDSL_ERR_INVALID_ARG, "negative weight extent");
+  if (N % 32 || K % 32) return fail(VDSL_ERR_UNSUPPORTED, "packed weights need N % 32 == 0 and K % 32 == 0");
+  const size_t n = static_cast<size_t>(N) * static_cast<size_t>(K);
+  VDSL_TRY(check_buffer(q, w, n, "w", false));
+  VDSL_TRY(check_buffer(q, wp, n, "wp", true));
+  if (w == wp) return fail(VDSL_ERR_INVALID_ARG, "w and wp must be different buffers");
+  if (n == 0) return VDSL_OK;
+  const int64_t chunks = static_cast<int64_t>(n / 16);
+  int64_t blocks = (chunks + 255) / 256;
+  if (blocks > 16384) blocks = 16384;
+  hipLaunchKernelGGL(bpk_pack_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, q->stream,
+                     static_cast<const char*>(w->ptr), static_cast<char*>(wp->ptr), N / 32, K / 32, K);
+  return check_launch("bpk_pack_kernel");
+}
+
+static int packed_shape_ok(int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N < 0 || K < 0) return fail(VDSL_ERR_INVALID_ARG, "negative GEMM extent");
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 133000)
+    return fail(VDSL_ERR_UNSUPPORTED, "extent too large (K <= 133000 keeps int32 exact)");
+  if (N % 32) return fail(VDSL_ERR_UNSUPPORTED, "packed GEMM needs N % 32 == 0");
+  if (K % (128 * P0::NR)) return fail(VDSL_ERR_UNSUPPORTED, "packed GEMM needs K % 512 == 0");
+  return VDSL_OK;
+}
+
+extern "C" int vdsl_gemm_w8a8_packed_workspace_bytes(int64_t M, int64_t N, int64_t K, size_t* bytes) {
+  if (!bytes) return fail(VDSL_ERR_INVALID_ARG, "bytes is null");
+  VDSL_TRY(packed_shape_ok(M, N, K));
+  *bytes = (M == 0 || N == 0 || K == 0) ? 0 : bpk_workspace_bytes(bpk_plan(M, N, K));
+  return VDSL_OK;
+}
+
+extern "C" int vdsl_op_gemm_w8a8_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer xq, vdsl_buffer x_scale,
+                                        vdsl_buffer wp, vdsl_buffer w_scale, vdsl_buffer y, int32_t out_dtype, int32_t relu,
+                                        vdsl_buffer acc_out, vdsl_buffer workspace) {
+  VDSL_TRY(enter_queue(q));
+  VDSL_TRY(packed_shape_ok(M, N, K));
+  if (out_dtype != VDSL_F32 && out_dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "y must be f32 or bf16");
+  VDSL_TRY(check_buffer(q, xq, static_cast<size_t>(M) * K, "xq", false));
+  VDSL_TRY(check_buffer(q, x_scale, static_cast<size_t>(M) * 4, "x_scale", false));
+  VDSL_TRY(check_buffer(q, wp, static_cast<size_t>(N) * K, "wp", false));
+  VDSL_TRY(check_buffer(q, w_scale, static_cast<size_t>(N) * 4, "w_scale", false));
+  VDSL_TRY(check_buffer(q, y, static_cast<size_t>(M) * N * dtype_size(out_dtype), "y", true));
+  if (acc_out) VDSL_TRY(check_buffer(q, acc_out, static_cast<size_t>(M) * N * 4, "acc_out", true));
+  if (M == 0 || N == 0) return VDSL_OK;
+  if (K == 0) return fail(VDSL_ERR_UNSUPPORTED, "packed GEMM needs K > 0");
+  const BpkPlan p = bpk_plan(M, N, K);
+  const size_t wsb = bpk_workspace_bytes(p);
+  if (wsb) VDSL_TRY(check_buffer(q, workspace, wsb, "workspace", true));
+  char* part = wsb ? static_cast<char*>(workspace->ptr) : nullptr;
+  int32_t* ao = acc_out ? static_cast<int32_t*>(acc_out->ptr) : nullptr;
+  const auto* a = static_cast<const int8_t*>(xq->ptr);
+  const auto* b = static_cast<const int8_t*>(wp->ptr);
+  const auto* xs = static_cast<const float*>(x_scale->ptr);
+  const auto* wsc = static_cast<const float*>(w_scale->ptr);
+  const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+  if (p.cfg == 0) return launch_bpk<P0>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
+  if (p.cfg == 2) return launch_bpk<P2>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
+  return launch_bpk<P1>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
 }

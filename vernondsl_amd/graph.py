@@ -51,6 +51,9 @@ class Graph:
     def __init__(self):
         self.values: dict[str, Value] = {}
         self.ops: list[Op] = []
+        # Ops that derive constant operands from params (weight packing): run by
+        # Executable.prepare() after the params are written, never inside the replayed step.
+        self.prepare_ops: list[Op] = []
         self._n = 0
 
     # ---- construction -------------------------------------------------------------------------
@@ -102,17 +105,32 @@ class Graph:
         self._op("mse", [y, t], [loss])
         return loss
 
-    def quant_linear(self, x: Value, wq: Value, w_scale: Value, relu: bool, out_dtype="bf16", name=None) -> Value:
+    def quant_linear(self, x: Value, wq: Value, w_scale: Value, relu: bool, out_dtype="bf16", name=None,
+                     packed: bool | None = None) -> Value:
         """y = relu?(dequant(q(x) wq^T)): per-row dynamic int8 activations, int8 weights [out][in]
-        with per-output-channel f32 scales; int32 accumulation on MFMA."""
+        with per-output-channel f32 scales; int32 accumulation on MFMA.
+
+        packed (default: whenever the shape allows it, out % 32 == 0 and in % 512 == 0): the
+        step reads a copy of wq in MFMA fragment order, made by a prepare op (once per write of
+        wq, outside the replayed step); same results bit for bit."""
         if wq.dtype != "i8" or w_scale.dtype != "f32":
             raise TypeError("quant_linear takes int8 weights and f32 scales")
         rows, k = x.shape
+        n = wq.shape[0]
+        if packed is None:
+            packed = n % 32 == 0 and k % 512 == 0 and k > 0
         xq = self._value(self._fresh("xq"), (rows, k), "i8")
         xs = self._value(self._fresh("xscale"), (rows,), "f32")
         self._op("quantize", [x], [xq, xs])
-        y = self._value(name or self._fresh("qlinear"), (rows, wq.shape[0]), out_dtype)
-        self._op("w8a8", [xq, xs, wq, w_scale], [y], relu=bool(relu))
+        y = self._value(name or self._fresh("qlinear"), (rows, n), out_dtype)
+        if packed:
+            wp = self._value(self._fresh(f"{wq.name}.packed"), wq.shape, "i8", "param")
+            op = Op("pack_w8a8", [wq], [wp])
+            wp.producer = op
+            self.prepare_ops.append(op)
+            self._op("w8a8_packed", [xq, xs, wp, w_scale], [y], relu=bool(relu))
+        else:
+            self._op("w8a8", [xq, xs, wq, w_scale], [y], relu=bool(relu))
         return y
 
     # ---- autodiff --------------------------------------------------------------------------------
@@ -207,6 +225,7 @@ class Executable:
         self.dev = dev
         self.t: dict[str, Tensor] = {}
         self.workspace = None
+        self._stale: set[str] = {v.name for op in g.prepare_ops for v in op.inputs}
         ws = 0
         for op in g.ops:
             if op.kind == "gemm":
@@ -217,6 +236,9 @@ class Executable:
             if op.kind == "w8a8":
                 xq, _, wq, _ = op.inputs
                 ws = max(ws, kernels.gemm_w8a8_workspace_bytes(xq.shape[0], wq.shape[0], xq.shape[1]))
+            if op.kind == "w8a8_packed":
+                xq, _, wp, _ = op.inputs
+                ws = max(ws, kernels.gemm_w8a8_packed_workspace_bytes(xq.shape[0], wp.shape[0], xq.shape[1]))
         try:
             for v in g.values.values():
                 self.t[v.name] = Tensor(dev, v.shape, v.dtype)
@@ -228,13 +250,28 @@ class Executable:
 
     def write(self, q: Queue, name: str, host):
         self.t[name].buffer.write(q, host)
+        if any(v.name == name for op in self.graph.prepare_ops for v in op.inputs):
+            self._stale.add(name)
+
+    def prepare(self, q: Queue):
+        """Runs the prepare ops (weight packing) whose params were written since they last ran.
+        run() and capture() call it first, so a replayed step never reads stale packed weights
+        unless a param is written after capture (then call prepare() before the next launch)."""
+        T = self.t
+        for op in self.graph.prepare_ops:
+            if op.kind == "pack_w8a8" and op.inputs[0].name in self._stale:
+                kernels.pack_w8a8_weights(q, T[op.inputs[0].name], T[op.outputs[0].name])
+        self._stale.clear()
 
     def read(self, q: Queue, name: str):
         return self.t[name].numpy(q)
 
     def run(self, q: Queue):
-        """Enqueues every op of the graph, in order, on q."""
+        """Enqueues every op of the graph, in order, on q (after any pending prepare ops, unless q
+        is recording a capture)."""
         T = self.t
+        if self._stale and not q.capturing:
+            self.prepare(q)
         for op in self.graph.ops:
             ins = [T[v.name] for v in op.inputs]
             outs = [T[v.name] for v in op.outputs]
@@ -261,11 +298,17 @@ class Executable:
                 kernels.quantize_rows_i8(q, ins[0], outs[0], outs[1])
             elif op.kind == "w8a8":
                 kernels.gemm_w8a8(q, ins[0], ins[1], ins[2], ins[3], outs[0], op.attrs["relu"], None, self.workspace)
+            elif op.kind == "w8a8_packed":
+                kernels.gemm_w8a8_packed(q, ins[0], ins[1], ins[2], ins[3], outs[0], op.attrs["relu"], None,
+                                         self.workspace)
             else:
                 raise NotImplementedError(op.kind)
 
     def capture(self, q: Queue):
-        """Records one run() into a hipGraph and returns it (rhi.Graph: .launch(q), .destroy())."""
+        """Records one run() into a hipGraph and returns it (rhi.Graph: .launch(q), .destroy()).
+        Pending prepare ops run first, eagerly, outside the recording."""
+        if self._stale:
+            self.prepare(q)
         with q.capture() as rec:
             self.run(q)
         return rec.graph

@@ -178,3 +178,36 @@ def gemm_w8a8(q: Queue, xq: Tensor, x_scale: Tensor, w: Tensor, w_scale: Tensor,
     _expect(acc_out, (M, N), "i32", "acc_out")
     call("vdsl_op_gemm_w8a8", q.handle, M, N, K, xq.handle, x_scale.handle, w.handle, w_scale.handle, y.handle,
          y.dtype, int(bool(relu)), _h(acc_out), _h(workspace))
+
+
+def pack_w8a8_weights(q: Queue, w: Tensor, wp: Tensor):
+    """Writes w (int8 [N][K]) into wp in the MFMA fragment order gemm_w8a8_packed reads."""
+    N, K = w.shape
+    _expect(w, (N, K), "i8", "w")
+    _expect(wp, (N, K), "i8", "wp")
+    call("vdsl_op_pack_w8a8_weights", q.handle, N, K, w.handle, wp.handle)
+
+
+def gemm_w8a8_packed_workspace_bytes(M, N, K) -> int:
+    n = C.c_size_t()
+    call("vdsl_gemm_w8a8_packed_workspace_bytes", M, N, K, C.byref(n))
+    return n.value
+
+
+def gemm_w8a8_packed(q: Queue, xq: Tensor, x_scale: Tensor, wp: Tensor, w_scale: Tensor, y: Tensor, relu=False,
+                     acc_out=None, workspace=None):
+    """gemm_w8a8 with weights packed by pack_w8a8_weights (wp keeps the logical shape [N][K]).
+    workspace: gemm_w8a8_packed_workspace_bytes(M, N, K) bytes (split-K partials)."""
+    M, K = xq.shape
+    N, K2 = wp.shape
+    if K != K2:
+        raise ValueError(f"inner dimensions differ: {K} vs {K2}")
+    _expect(xq, (M, K), "i8", "xq")
+    _expect(wp, (N, K), "i8", "wp")
+    _expect(x_scale, (M,), "f32", "x_scale")
+    _expect(w_scale, (N,), "f32", "w_scale")
+    if y.shape != (M, N):
+        raise ValueError(f"y: shape {y.shape}, expected {(M, N)}")
+    _expect(acc_out, (M, N), "i32", "acc_out")
+    call("vdsl_op_gemm_w8a8_packed", q.handle, M, N, K, xq.handle, x_scale.handle, wp.handle, w_scale.handle,
+         y.handle, y.dtype, int(bool(relu)), _h(acc_out), _h(workspace))

@@ -166,15 +166,18 @@ class Queue:
         call("vdsl_queue_create", device.handle, C.byref(h))
         self.handle = h
         self.device = device
+        self.capturing = False  # between begin_graph() and end_graph()
 
     def sync(self):
         call("vdsl_queue_sync", self.handle)
 
     def begin_graph(self):
         call("vdsl_graph_begin", self.handle)
+        self.capturing = True
 
     def end_graph(self) -> Graph:
         h = C.c_void_p()
+        self.capturing = False
         call("vdsl_graph_end", self.handle, C.byref(h))
         return Graph(h)
 
