@@ -23,10 +23,11 @@ namespace {
 
 constexpr int kTile = 8;          // wave tile edge (8x8 = 64 lanes)
 constexpr int kBlockEdge = 16;    // block patch edge: 2x2 wave tiles
-#ifndef VDSL_ESC_PPL
-#define VDSL_ESC_PPL 1
+// Trips per block of the deferred count (measured on the config-1 image: 8 -> 21.8 us, 16 -> 20.0,
+// 32 -> 19.8; a block also bounds the trips a wave makes after its last lane escaped).
+#ifndef VDSL_ESC_UNROLL
+#define VDSL_ESC_UNROLL 16
 #endif
-constexpr int kPixelsPerLane = VDSL_ESC_PPL;  // independent pixels per lane (rows 8 apart)
 
 __device__ __forceinline__ float pixel_coord(int idx, float den, float off, float scale, float post) {
   float v = static_cast<float>(idx) / den;  // correctly rounded f32 division
@@ -37,29 +38,21 @@ __device__ __forceinline__ float pixel_coord(int idx, float den, float off, floa
 
 template <int FAMILY, int TEST, int ROUNDING, int OUT>
 __global__ __launch_bounds__(256) void escape_time_kernel(vdsl_escape_time_params p, void* __restrict__ out) {
-  // PPL pixels per lane: lane (r, c) of the wave's 8x8 tile also owns the pixel kTile rows below,
-  // so each lane carries PPL independent dependency chains (the wave tile is (8*PPL) x 8).
-  constexpr int PPL = kPixelsPerLane;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int i0 = blockIdx.y * (kBlockEdge * PPL) + (wave >> 1) * (kTile * PPL) + (lane >> 3);
+  const int i = blockIdx.y * kBlockEdge + (wave >> 1) * kTile + (lane >> 3);
   const int j = blockIdx.x * kBlockEdge + (wave & 1) * kTile + (lane & 7);
-  if (j >= p.nj || i0 >= p.ni) return;
+  if (j >= p.nj || i >= p.ni) return;
 
-  float zr[PPL], zi[PPL], cr[PPL], ci[PPL];
-  int it[PPL], live[PPL];
-  const float im = pixel_coord(j, p.im_den, p.im_off, p.im_scale, p.im_post);
-#pragma unroll
-  for (int q = 0; q < PPL; ++q) {
-    const int i = i0 + q * kTile;
+  float zr, zi, cr, ci;
+  {
+    const float im = pixel_coord(j, p.im_den, p.im_off, p.im_scale, p.im_post);
     const float re = pixel_coord(i, p.re_den, p.re_off, p.re_scale, p.re_post);
     if (FAMILY == VDSL_ESC_MANDELBROT) {
-      zr[q] = 0.0f; zi[q] = 0.0f; cr[q] = re; ci[q] = im;
+      zr = 0.0f; zi = 0.0f; cr = re; ci = im;
     } else {
-      zr[q] = re; zi[q] = im; cr[q] = p.c_re; ci[q] = p.c_im;
+      zr = re; zi = im; cr = p.c_re; ci = p.c_im;
     }
-    it[q] = 0;
-    live[q] = i < p.ni ? 1 : 0;  // a pixel past the last row never counts
   }
   // Escape test of this pixel's current z (mag = |z|^2): MAG2_GT continues while !(mag > bound);
   // NORM_GE continues while sqrtf(mag) < b, evaluated as mag < bound: for NORM_GE the launcher
@@ -67,66 +60,72 @@ __global__ __launch_bounds__(256) void escape_time_kernel(vdsl_escape_time_param
   const float bound = p.bound;
   const int max_iter = p.max_iter;
 
-  // Wave-uniform loop: every pixel steps z each trip; `live` (sticky, 1 until the first failed
-  // escape test) counts the trips made while live, which is the number of updates of the
-  // check-then-update loop.  An escaped pixel keeps stepping z but its count is frozen.  `live` is
-  // a vector value updated with VALU selects, so a trip needs no exec-mask or scalar-mask work; full
-  // blocks of kUnroll trips run without a max_iter check (the tail block checks it), and the wave
-  // stops once no pixel is live (tested once per block).
-#ifndef VDSL_ESC_UNROLL
-#define VDSL_ESC_UNROLL 8
-#endif
+  // Wave-uniform loop: every pixel steps z each trip; `live` (sticky: true until the first failed
+  // escape test) marks the trips made while live, whose number is the count of updates of the
+  // check-then-update loop.  An escaped pixel keeps stepping z but is no longer counted.  `live` is
+  // a lane mask in scalar registers (the test writes one, s_and keeps it sticky), so a trip costs
+  // the six rounded operations of the update, one compare and one scalar op.  Counting is
+  // deferred to the end of each block of kUnroll trips: when no lane of the wave died in the
+  // block, every live lane adds kUnroll (one select and one add per block); otherwise each lane
+  // adds the trips it was live for, from the per-trip masks.  The max_iter check is made once per
+  // block (the tail block checks each trip), and the wave stops once no lane is live.
   constexpr int kUnroll = VDSL_ESC_UNROLL;
-  auto trip = [&]() {
-#pragma unroll
-    for (int q = 0; q < PPL; ++q) {
-      float nzr, nzi, mag;
-      if (ROUNDING == VDSL_ESC_ROUND_SEPARATE) {
-        const float zr2 = zr[q] * zr[q];
-        const float zi2 = zi[q] * zi[q];
-        mag = zr2 + zi2;
-        nzr = (zr2 - zi2) + cr[q];
-        nzi = ((zi[q] * zr[q]) * 2.0f) + ci[q];
-      } else {
-        const float qq = zi[q] * zi[q];
-        mag = __builtin_fmaf(zr[q], zr[q], qq);
-        nzr = __builtin_fmaf(zr[q], zr[q], -qq) + cr[q];
-        nzi = __builtin_fmaf(zr[q] + zr[q], zi[q], ci[q]);
-      }
-      const bool pass = (TEST == VDSL_ESC_MAG2_GT) ? !(mag > bound) : (mag < bound);
-      live[q] = pass ? live[q] : 0;
-      it[q] += live[q];
-      zr[q] = nzr;
-      zi[q] = nzi;
+  auto step = [&](bool lv) -> bool {
+    float nzr, nzi, mag;
+    if (ROUNDING == VDSL_ESC_ROUND_SEPARATE) {
+      const float zr2 = zr * zr;
+      const float zi2 = zi * zi;
+      mag = zr2 + zi2;
+      nzr = (zr2 - zi2) + cr;
+      nzi = ((zi * zr) * 2.0f) + ci;
+    } else {
+      const float qq = zi * zi;
+      mag = __builtin_fmaf(zr, zr, qq);
+      nzr = __builtin_fmaf(zr, zr, -qq) + cr;
+      nzi = __builtin_fmaf(zr + zr, zi, ci);
     }
+    const bool pass = (TEST == VDSL_ESC_MAG2_GT) ? !(mag > bound) : (mag < bound);
+    zr = nzr;
+    zi = nzi;
+    return lv && pass;
   };
-  auto any_live = [&]() {
-    int a = 0;
-#pragma unroll
-    for (int q = 0; q < PPL; ++q) a |= live[q];
-    return __any(a);
-  };
+  bool live = true;
+  int it = 0;
   int k = 0;
   for (; k + kUnroll <= max_iter; k += kUnroll) {
+    bool d[kUnroll];
+    bool lk = live;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) trip();
-    if (!any_live()) break;
+    for (int u = 0; u < kUnroll; ++u) {
+      lk = step(lk);
+      d[u] = lk;
+    }
+    if (__builtin_amdgcn_ballot_w64(lk) == __builtin_amdgcn_ballot_w64(live)) {
+      it += live ? kUnroll : 0;
+    } else {
+      // The increment comes from a volatile asm, so the selects below cannot be computed before
+      // the branch (the compiler otherwise speculates this path into every block).
+      int one;
+      asm volatile("v_mov_b32 %0, 1" : "=v"(one));
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) it += d[u] ? one : 0;
+    }
+    live = lk;
+    if (__builtin_amdgcn_ballot_w64(live) == 0) break;
   }
-  if (k + kUnroll > max_iter && any_live()) {
-    for (; k < max_iter; ++k) trip();
+  if (k + kUnroll > max_iter && __builtin_amdgcn_ballot_w64(live) != 0) {
+    for (; k < max_iter; ++k) {
+      live = step(live);
+      it += live ? 1 : 0;
+    }
   }
 
-#pragma unroll
-  for (int q = 0; q < PPL; ++q) {
-    const int i = i0 + q * kTile;
-    if (i >= p.ni) continue;
-    const size_t o = static_cast<size_t>(i) * static_cast<size_t>(p.nj) + static_cast<size_t>(j);
-    if (OUT == VDSL_ESC_OUT_I32_COUNT) {
-      static_cast<int32_t*>(out)[o] = it[q];
-    } else {
-      const float f = static_cast<float>(it[q]) * p.out_scale;
-      static_cast<float*>(out)[o] = p.out_base + f;
-    }
+  const size_t o = static_cast<size_t>(i) * static_cast<size_t>(p.nj) + static_cast<size_t>(j);
+  if (OUT == VDSL_ESC_OUT_I32_COUNT) {
+    static_cast<int32_t*>(out)[o] = it;
+  } else {
+    const float f = static_cast<float>(it) * p.out_scale;
+    static_cast<float*>(out)[o] = p.out_base + f;
   }
 }
 
@@ -188,8 +187,7 @@ extern "C" int vdsl_op_escape_time(vdsl_queue q, const vdsl_escape_time_params* 
   const size_t bytes = static_cast<size_t>(p->ni) * static_cast<size_t>(p->nj) * 4u;
   VDSL_TRY(check_buffer(q, out, bytes, "out", true));
   if (bytes == 0) return VDSL_OK;
-  const dim3 grid((p->nj + kBlockEdge - 1) / kBlockEdge,
-                  (p->ni + kBlockEdge * kPixelsPerLane - 1) / (kBlockEdge * kPixelsPerLane));
+  const dim3 grid((p->nj + kBlockEdge - 1) / kBlockEdge, (p->ni + kBlockEdge - 1) / kBlockEdge);
   if (grid.y > 65535u) return fail(VDSL_ERR_UNSUPPORTED, "ni too large");
   vdsl_escape_time_params kp = *p;
   if (kp.escape_test == VDSL_ESC_NORM_GE) kp.bound = norm_threshold(p->bound);
