@@ -298,6 +298,13 @@ int vdsl_op_gelu_fwd(vdsl_queue q, int64_t n, int32_t x_dtype, vdsl_buffer x, in
  * [cols][rows]) receives the transpose of da. */
 int vdsl_op_gelu_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer dh, vdsl_buffer pre,
                      vdsl_buffer da, vdsl_buffer da_t);
+/* The backward of y = GELU(pre) through the GEMM that forms dL/dy, fused: dh = A B^T (f32
+ * accumulate, never written), da (bf16 [M][N]) = dh * GELU'(pre), da_t (optional, bf16 [N][M]) =
+ * da^T.  A: bf16 [M][K]; B: bf16 [N][K] (the NT form); pre: f32 [M][N].  Bit-identical to
+ * vdsl_op_gemm_bf16(trans_a = 0, trans_b = 1, f32 C) followed by vdsl_op_gelu_bwd.  No reference
+ * counterpart (north-star op class: compiler-generated backward GEMMs). */
+int vdsl_op_gemm_bf16_gelu_bwd(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer A,
+                               vdsl_buffer B, vdsl_buffer pre, vdsl_buffer da, vdsl_buffer da_t);
 /* MSE: loss (f32 [1]) = mean((y - t)^2);  dy (bf16 [rows][cols]) = 2 (y - t) / (rows*cols);
  * dy_t (optional) = dy^T.  y, t: f32 [rows][cols].  partials: f32 scratch of
  * vdsl_mse_partials_count(rows, cols) elements (deterministic two-stage reduction). */

@@ -223,6 +223,34 @@ def test_optional_outputs_absent(dev, q, rows, cols):
         t.free()
 
 
+def test_gemm_gelu_bwd_fused_config4(dev, q):
+    """Config 4's dL/dpre at full size (2048x4096, K 4096): the fused op equals the plain GEMM +
+    GELU backward bit for bit, and the values match the oracle's GELU backward of the oracle GEMM
+    on sampled rows (bf16 tolerance)."""
+    M, N, K = 2048, 4096, 4096
+    A = bf16_rand((M, K), 91)
+    B = bf16_rand((N, K), 92)
+    pre = (rng.normal(93, M * N) * 2.0).astype(np.float32).reshape(M, N)
+    tA, tB, tpre = Tensor.from_numpy(dev, q, A, "bf16"), Tensor.from_numpy(dev, q, B, "bf16"), Tensor.from_numpy(dev, q, pre)
+    da, da_t, dh = Tensor(dev, (M, N), "bf16"), Tensor(dev, (N, M), "bf16"), Tensor(dev, (M, N), "f32")
+    da2, da2_t = Tensor(dev, (M, N), "bf16"), Tensor(dev, (N, M), "bf16")
+    kernels.gemm_bf16_gelu_bwd(q, tA, tB, tpre, da, da_t)
+    kernels.gemm_bf16(q, tA, tB, dh, False, True, _lib.EPI_NONE)
+    kernels.gelu_bwd(q, dh, tpre, da2, da2_t)
+    g, gt = da.numpy(q), da_t.numpy(q)
+    assert np.array_equal(g, da2.numpy(q))
+    assert np.array_equal(gt, da2_t.numpy(q))
+    assert np.array_equal(gt, g.T)
+    rows = [0, 777, 2047]
+    dh_ref = oracle.gemm_bf16(A[rows], B, False, True)
+    ref, _ = oracle.gelu_bwd(dh_ref.astype(np.float32), pre[rows])
+    got = rng.bf16_to_f32(g[rows]).astype(np.float64)
+    mag = (np.abs(rng.bf16_to_f32(A[rows]).astype(np.float64)) @ np.abs(rng.bf16_to_f32(B).astype(np.float64)).T) * 1.2
+    assert np.all(np.abs(got - rng.bf16_to_f32(ref).astype(np.float64)) <= 1e-2 * mag + 1e-30)
+    for t in (tA, tB, tpre, da, da_t, dh, da2, da2_t):
+        t.free()
+
+
 @pytest.mark.parametrize("rows,cols,dt", [(512, 8192, "bf16"), (37, 100, "f32"), (5, 16, "bf16"), (64, 8192, "f32"),
                                           (3, 16384, "bf16"), (7, 4096, "f32"), (9, 4104, "f32")])
 def test_quantize_rows(dev, q, rows, cols, dt):

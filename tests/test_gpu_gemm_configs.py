@@ -67,6 +67,48 @@ def test_every_bf16_config_matches(dev, q, forced_config, M, N, K):
         tB.free()
 
 
+def gelu_bwd_pair(dev, q, tA, tB, tpre, M, N, fused):
+    """(da, da_t) from the fused GEMM + GELU backward, or from the plain GEMM (f32) followed by
+    the GELU backward op."""
+    da, da_t = Tensor(dev, (M, N), "bf16"), Tensor(dev, (N, M), "bf16")
+    for t in (da, da_t):
+        t.buffer.fill_u32(q, 0x7FC07FC0)
+    if fused:
+        kernels.gemm_bf16_gelu_bwd(q, tA, tB, tpre, da, da_t)
+    else:
+        dh = Tensor(dev, (M, N), "f32")
+        kernels.gemm_bf16(q, tA, tB, dh, False, True, _lib.EPI_NONE)
+        kernels.gelu_bwd(q, dh, tpre, da, da_t)
+        dh.free()
+    res = (da.numpy(q), da_t.numpy(q))
+    da.free()
+    da_t.free()
+    return res
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 512, 256), (300, 520, 256), (129, 258, 128)])
+def test_every_bf16_config_gelu_bwd_fused(dev, q, forced_config, M, N, K):
+    """The fused dL/dpre = (A B^T) * GELU'(pre) equals the GEMM followed by the GELU backward op,
+    bit for bit, under every tile configuration (whole tiles with M % 8 == 0 take the LDS-staged
+    epilogue with the transposed store, the others the per-element one)."""
+    A = rng.f32_to_bf16(rng.uniform(81, M * K, -1, 1)).reshape(M, K)
+    B = rng.f32_to_bf16(rng.uniform(82, N * K, -1, 1)).reshape(N, K)
+    pre = (rng.normal(83, M * N) * 2.0).astype(np.float32).reshape(M, N)
+    tA, tB, tpre = Tensor.from_numpy(dev, q, A, "bf16"), Tensor.from_numpy(dev, q, B, "bf16"), Tensor.from_numpy(dev, q, pre)
+    try:
+        forced_config(-1)
+        base = gelu_bwd_pair(dev, q, tA, tB, tpre, M, N, fused=False)
+        assert np.array_equal(base[1], base[0].T)
+        for c in [-1] + list(range(N_BF16_CONFIGS)):
+            forced_config(c)
+            got = gelu_bwd_pair(dev, q, tA, tB, tpre, M, N, fused=True)
+            assert np.array_equal(got[0], base[0]), f"config {c}: da differs"
+            assert np.array_equal(got[1], base[1]), f"config {c}: da_t differs"
+    finally:
+        for t in (tA, tB, tpre):
+            t.free()
+
+
 @pytest.mark.parametrize("M,N,K", [(300, 520, 1024), (64, 1000, 512)])
 def test_every_w8a8_config_bit_exact(dev, q, forced_config, M, N, K):
     r = np.random.default_rng(M * 7 + N + K)

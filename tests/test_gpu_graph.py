@@ -32,10 +32,10 @@ def absmm(a, b):
     return np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64))
 
 
-def run_mlp(dev, q, x, w1, w2, t, replays=3):
+def run_mlp(dev, q, x, w1, w2, t, replays=3, **variant):
     B, D = x.shape
     Hd, O = w1.shape[0], w2.shape[0]
-    g, grads = graph.mlp_train_graph(B, D, Hd, O)
+    g, grads = graph.mlp_train_graph(B, D, Hd, O, **variant)
     exe = g.compile(dev)
     for name, arr in (("X", x), ("W1", w1), ("W2", w2), ("T", t)):
         exe.write(q, name, arr)
@@ -69,6 +69,18 @@ def test_mlp_small_end_to_end(dev, q):
         r = ref["d" + n[5:]]
         a = got[n].astype(np.float64)
         assert np.linalg.norm(a - r) <= 1e-2 * np.linalg.norm(r), n
+
+
+def test_mlp_graph_variants_identical(dev, q):
+    """The prepared-transpose and fused-GELU-backward forms of the training step run the same
+    products in the same order: every output equals the default graph's bit for bit (each graph
+    also replays equal to its eager run)."""
+    x, w1, w2, t = spec.mlp_inputs(batch=256, d_in=384, hidden=512, d_out=256)
+    base = run_mlp(dev, q, x, w1, w2, t, replays=2)
+    for variant in ({"prepare_transposes": True}, {"prepare_transposes": True, "fuse_gelu_backward": True}):
+        got = run_mlp(dev, q, x, w1, w2, t, replays=2, **variant)
+        for n in ("H", "Y", "loss", "grad_W1", "grad_W2", "pre"):
+            assert np.array_equal(got[n], base[n]), f"{variant}: {n} differs"
 
 
 def test_mlp_config4_full_size(dev, q):

@@ -20,9 +20,27 @@ def test_mlp_backward_op_sequence():
     assert [v.shape for v in mse.outputs] == [(1,), (64, 16), (16, 64), mse.outputs[3].shape]
     dW2, dH, gb, dW1 = g.ops[3], g.ops[4], g.ops[5], g.ops[6]
     assert dW2.inputs[0].shape == (16, 64) and dW2.inputs[1].name == "H"   # dY^T [out][B], H [B][hid]
-    assert dH.inputs[1].name == "W2" and dH.outputs[0].dtype == "f32"
+    assert dH.inputs[1].name == "W2" and dH.outputs[0].dtype == "f32" and not dH.attrs["trans_b"]
     assert gb.inputs[1] is g.ops[0].attrs["pre"]
     assert dW1.inputs[1].name == "X" and dW1.outputs[0].name == "grad_W1"
+    assert not g.prepare_ops
+
+
+def test_mlp_backward_prepared_transpose_and_fused_gelu():
+    g, _ = graph.mlp_train_graph(batch=64, d_in=32, hidden=48, d_out=16, prepare_transposes=True)
+    assert [op.kind for op in g.ops] == ["linear", "linear", "mse", "gemm", "gemm", "gelu_bwd", "gemm"]
+    # dH = dY W2 in the NT form on W2^T [hid][out], made by a prepare op (not on every step)
+    dH = g.ops[4]
+    assert dH.inputs[1].name == "W2.T" and dH.inputs[1].shape == (48, 16) and dH.attrs["trans_b"]
+    assert [(op.kind, op.inputs[0].name, op.outputs[0].name) for op in g.prepare_ops] == [("transpose", "W2", "W2.T")]
+    g, _ = graph.mlp_train_graph(batch=64, d_in=32, hidden=48, d_out=16, prepare_transposes=True,
+                                 fuse_gelu_backward=True)
+    assert [op.kind for op in g.ops] == ["linear", "linear", "mse", "gemm", "gemm_gelu_bwd", "gemm"]
+    dA, dW1 = g.ops[4], g.ops[5]
+    # dL/dpre = (dY W2) * GELU'(pre) in one op
+    assert dA.inputs[1].name == "W2.T" and dA.inputs[2] is g.ops[0].attrs["pre"]
+    assert [v.shape for v in dA.outputs] == [(64, 48), (48, 64)] and dA.outputs[0].dtype == "bf16"
+    assert dW1.inputs[0] is dA.outputs[1]
 
 
 def test_inference_graph_has_no_backward():

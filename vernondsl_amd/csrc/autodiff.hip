@@ -17,13 +17,6 @@
 namespace vdsl {
 namespace {
 
-__device__ __forceinline__ float gelu_grad_f(float v) {
-  // d/dv [0.5 v (1 + erf(v / sqrt2))] = Phi(v) + v phi(v), with Phi(v) = 0.5 erfc(-v / sqrt2)
-  // (erfc keeps full relative accuracy where 1 + erf(.) would cancel, v < 0).  Branch-free:
-  // erfc_cheb (fractional error < 1.2e-7) and exp_fast (< 2e-7 + 1 ulp); the result is rounded
-  // to bf16, and near the zero of GELU' (v = -0.75) the absolute error stays below 1e-7.
-  return 0.5f * erfc_cheb(-v * 0.7071067811865476f) + v * exp_fast(-0.5f * v * v) * 0.3989422804014327f;
-}
 
 // Vector forms of the two kernels below, for rows % 8 == 0 and cols % 4 == 0 (every base is a
 // whole hipMalloc buffer, 256-byte aligned): a 64x64 tile per 256-lane block, each lane loads two

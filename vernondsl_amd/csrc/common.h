@@ -155,6 +155,16 @@ __device__ __forceinline__ float erfc_cheb(float x) {
 // x^2 2^-24 (4e-6 at |x| = 8.5), far below bf16 resolution.
 __device__ __forceinline__ float gelu_f(float v) { return 0.5f * v * erfc_cheb(-v * 0.7071067811865476f); }
 
+// GELU'(v), shared by the GELU backward kernels and the fused GEMM epilogue (one definition, so
+// the fused and unfused paths agree bit for bit).
+__device__ __forceinline__ float gelu_grad_f(float v) {
+  // d/dv [0.5 v (1 + erf(v / sqrt2))] = Phi(v) + v phi(v), with Phi(v) = 0.5 erfc(-v / sqrt2)
+  // (erfc keeps full relative accuracy where 1 + erf(.) would cancel, v < 0).  Branch-free:
+  // erfc_cheb (fractional error < 1.2e-7) and exp_fast (< 2e-7 + 1 ulp); the result is rounded
+  // to bf16, and near the zero of GELU' (v = -0.75) the absolute error stays below 1e-7.
+  return 0.5f * erfc_cheb(-v * 0.7071067811865476f) + v * exp_fast(-0.5f * v * v) * 0.3989422804014327f;
+}
+
 // GELU for f32 results (the standalone elementwise op), relative accuracy ~1e-6 over the f32
 // range.  With z = |v|/sqrt2 and erfc(z) = t exp(-z^2 + P(t)) as above, the exponent is the
 // sensitive part (erfc's condition number is ~2 z^2), so it is never formed from a rounded z:

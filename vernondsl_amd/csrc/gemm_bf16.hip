@@ -71,11 +71,22 @@ using Dm26 = DmaConfig<MfmaBf16, 256, 128, 2, 2, 3, 128>;  // 4 waves of 128x64
 constexpr int kNumConfigs = 27;
 constexpr int kFirstDma = 14, kFirstDma128 = 23;
 
+// Internal epilogue code of vdsl_op_gemm_bf16_gelu_bwd: C (bf16) = v * GELU'(pre) with `pre` an
+// input, and the same values transposed into `ctr` ([N][M], optional).
+constexpr int kEpiGeluBwd = 3;
+
 // Epilogue of one accumulator element at (row, col), shared by both main loops.
+template <bool BWD>
 __device__ __forceinline__ void bf16_epilogue(float v, int row, int col, int M, int N, void* __restrict__ C,
-                                              float* __restrict__ pre, int epi, int c_dtype) {
+                                              float* __restrict__ pre, int epi, int c_dtype, uint16_t* __restrict__ ctr) {
   if (row < M && col < N) {
     const size_t o = static_cast<size_t>(row) * N + col;
+    if constexpr (BWD) {
+      const uint16_t h = f32_to_bf16(v * gelu_grad_f(pre[o]));
+      static_cast<uint16_t*>(C)[o] = h;
+      if (ctr) ctr[static_cast<size_t>(col) * M + row] = h;
+      return;
+    }
     if (pre) pre[o] = v;
     float y = v;
     if (epi == VDSL_EPI_GELU) y = gelu_f(v);
@@ -111,11 +122,20 @@ __device__ __forceinline__ void bf16_epilogue_tile(const f32x16 (&acc)[Cfg::FM][
 }
 
 // Picks the whole-tile variant when one applies, else the generic per-element epilogue.
-template <class Cfg>
+template <class Cfg, bool BWD>
 __device__ __forceinline__ void bf16_store_tile(const f32x16 (&acc)[Cfg::FM][Cfg::FN], int m0, int n0, int M, int N,
-                                                void* __restrict__ C, float* __restrict__ pre, int epi, int c_dtype) {
+                                                void* __restrict__ C, float* __restrict__ pre, int epi, int c_dtype,
+                                                uint16_t* __restrict__ ctr) {
   const bool whole = m0 + Cfg::BM <= M && n0 + Cfg::BN <= N;
-  if (whole && epi == VDSL_EPI_NONE && c_dtype == VDSL_F32 && !pre) {
+  if (BWD) {
+#pragma unroll
+    for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          bf16_epilogue<true>(acc[i][j][r], acc_row<Cfg>(m0, i, r), acc_col<Cfg>(n0, j), M, N, C, pre, epi, c_dtype, ctr);
+  } else if (whole && epi == VDSL_EPI_NONE && c_dtype == VDSL_F32 && !pre) {
     bf16_epilogue_tile<Cfg, 0>(acc, m0, n0, N, C, pre);
   } else if (whole && epi == VDSL_EPI_GELU && c_dtype == VDSL_BF16 && pre) {
     bf16_epilogue_tile<Cfg, 1>(acc, m0, n0, N, C, pre);
@@ -126,7 +146,7 @@ __device__ __forceinline__ void bf16_store_tile(const f32x16 (&acc)[Cfg::FM][Cfg
       for (int j = 0; j < Cfg::FN; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          bf16_epilogue(acc[i][j][r], acc_row<Cfg>(m0, i, r), acc_col<Cfg>(n0, j), M, N, C, pre, epi, c_dtype);
+          bf16_epilogue<false>(acc[i][j][r], acc_row<Cfg>(m0, i, r), acc_col<Cfg>(n0, j), M, N, C, pre, epi, c_dtype, ctr);
   }
 }
 
@@ -139,6 +159,7 @@ __device__ __forceinline__ void bf16_store_tile(const f32x16 (&acc)[Cfg::FM][Cfg
 // LDS; the caller has synchronised the block after the main loop.
 template <class Cfg>
 constexpr bool kLdsEpilogue = Cfg::NW * 32 * (Cfg::WTN + 8) * 4 <= Cfg::LDS_BYTES;
+
 
 template <class Cfg, int VARIANT>
 __device__ __forceinline__ void bf16_epilogue_tile_lds(const f32x16 (&acc)[Cfg::FM][Cfg::FN], int m0, int n0, int N,
@@ -173,10 +194,83 @@ __device__ __forceinline__ void bf16_epilogue_tile_lds(const f32x16 (&acc)[Cfg::
   }
 }
 
-template <class Cfg, bool EDGE>
+// Whole-tile GELU-backward epilogue (vdsl_op_gemm_bf16_gelu_bwd), also through each wave's LDS
+// area: C = bf16(v * GELU'(pre)) stored as 8-byte runs; the f32 products go back into the area and,
+// if `ctr` is set, each lane then reads one column of the 32-row block (64 lanes, 64 consecutive
+// floats per read: no bank conflict) and writes it as a 64-byte run of the transposed output
+// ctr[N][M] (needs M % 8 == 0 and WTN % 64 == 0).  `pre` is usually cold (written by the forward
+// pass long before): every load of it for the wave's whole tile is issued first, before the block
+// barrier that ends the main loop, so the tile pays one memory latency instead of one per unit
+// (in a training step the per-unit form made this GEMM 38 us slower than without the epilogue).
+template <class Cfg>
+__device__ __forceinline__ void bf16_epilogue_bwd_lds(const f32x16 (&acc)[Cfg::FM][Cfg::FN], int m0, int n0, int M,
+                                                      int N, void* __restrict__ C, const float* __restrict__ pre,
+                                                      char* smem, uint16_t* __restrict__ ctr) {
+  constexpr int WTN = Cfg::WTN, LD = WTN + 8, Q = WTN / 4, UPL = 32 * Q / 64;  // 16-byte units per lane per row block
+  // Rows of the wave's area: the whole wave tile when it fits in the block's LDS (then each lane's
+  // transposed run is WTM * 2 bytes, a whole 128-byte line for 64-row wave tiles), else 32.
+  constexpr int AR = Cfg::NW * Cfg::WTM * LD * 4 <= Cfg::LDS_BYTES ? Cfg::WTM : 32;
+  static_assert(WTN % 64 == 0, "the transposed store takes whole columns per lane");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
+  float* const area = reinterpret_cast<float*>(smem) + wave * AR * LD;
+  const int row0 = m0 + wm * Cfg::WTM, col0 = n0 + wn * WTN;
+  f32x4 x[Cfg::FM][UPL];
+#pragma unroll
+  for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+    for (int k = 0; k < UPL; ++k) {
+      const int u = lane + 64 * k, row = u / Q, c4 = u % Q;
+      x[i][k] = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4*>(pre + static_cast<size_t>(row0 + 32 * i + row) * N + col0 + 4 * c4));
+    }
+  dma_barrier();  // every wave's last fragment reads of the main loop are done
+  // The transposed output of rows [r0, r0 + AR) of the wave tile: lane c takes column c and writes
+  // AR bf16 (AR * 2 bytes) of ctr row col0 + c.
+  auto store_transposed = [&](int r0) {
+#pragma unroll
+    for (int cc = 0; cc < WTN / 64; ++cc) {
+      const int c = lane + 64 * cc;
+      u32x4* dst = reinterpret_cast<u32x4*>(ctr + static_cast<size_t>(col0 + c) * M + row0 + r0);
+#pragma unroll
+      for (int q4 = 0; q4 < AR / 8; ++q4) {
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(area[(8 * q4 + 2 * e) * LD + c], area[(8 * q4 + 2 * e + 1) * LD + c]);
+        dst[q4] = w;
+      }
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < Cfg::FM; ++i) {
+    float* const blk = area + (AR == 32 ? 0 : 32 * i) * LD;  // this 32-row block's rows of the area
+#pragma unroll
+    for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) blk[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * LD + 32 * j + (lane & 31)] = acc[i][j][r];
+#pragma unroll
+    for (int k = 0; k < UPL; ++k) {
+      const int u = lane + 64 * k, row = u / Q, c4 = u % Q;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(blk + row * LD + 4 * c4);
+      const size_t o = static_cast<size_t>(row0 + 32 * i + row) * N + col0 + 4 * c4;
+      f32x4 d;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d[e] = v[e] * gelu_grad_f(x[i][k][e]);
+      uint2 h;
+      h.x = pack_bf16x2(d[0], d[1]);
+      h.y = pack_bf16x2(d[2], d[3]);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(C) + o) = h;
+      if (ctr) *reinterpret_cast<f32x4*>(blk + row * LD + 4 * c4) = d;
+    }
+    if (AR == 32 && ctr) store_transposed(32 * i);
+  }
+  if (AR != 32 && ctr) store_transposed(0);
+}
+
+template <class Cfg, bool EDGE, bool BWD>
 __global__ __launch_bounds__(Cfg::NT, 2) void gemm_bf16_nt(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                         void* __restrict__ C, float* __restrict__ pre, int M, int N, int K,
-                                                        int epi, int c_dtype) {
+                                                        int epi, int c_dtype, uint16_t* __restrict__ ctr) {
   __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS_BYTES];
   const int tiles_m = (M + Cfg::BM - 1) / Cfg::BM, tiles_n = (N + Cfg::BN - 1) / Cfg::BN;
   int tm, tn;
@@ -185,16 +279,17 @@ __global__ __launch_bounds__(Cfg::NT, 2) void gemm_bf16_nt(const uint16_t* __res
   f32x16 acc[Cfg::FM][Cfg::FN];
   gemm_mainloop<MfmaBf16, Cfg, EDGE>(reinterpret_cast<const char*>(A), reinterpret_cast<const char*>(B), M, N, K * 2, 0, K * 2,
                                m0, n0, smem, acc);
-  bf16_store_tile<Cfg>(acc, m0, n0, M, N, C, pre, epi, c_dtype);
+  bf16_store_tile<Cfg, BWD>(acc, m0, n0, M, N, C, pre, epi, c_dtype, ctr);
 }
 
 // Direct-to-LDS kernel (gemm_dma.h).  Blocks of 8 waves are sized for one block per CU, blocks
 // of 4 waves for two.
-template <class Cfg>
+template <class Cfg, bool BWD>
 __global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_bf16_dma(const uint16_t* __restrict__ A,
                                                                                const uint16_t* __restrict__ B,
                                                                                void* __restrict__ C, float* __restrict__ pre,
-                                                                               int M, int N, int K, int epi, int c_dtype) {
+                                                                               int M, int N, int K, int epi, int c_dtype,
+                                                                               uint16_t* __restrict__ ctr) {
   __shared__ __attribute__((aligned(1024))) char smem[Cfg::LDS_BYTES];
   const int tiles_m = (M + Cfg::BM - 1) / Cfg::BM, tiles_n = (N + Cfg::BN - 1) / Cfg::BN;
   int tm, tn;
@@ -206,28 +301,43 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_bf16_dma
   if constexpr (kLdsEpilogue<Cfg>) {
     // Block-uniform: the tile is whole, N allows aligned runs, and the variant is one of the two.
     const bool whole = m0 + Cfg::BM <= M && n0 + Cfg::BN <= N && N % 4 == 0;
-    const bool v0 = epi == VDSL_EPI_NONE && c_dtype == VDSL_F32 && !pre;
-    const bool v1 = epi == VDSL_EPI_GELU && c_dtype == VDSL_BF16 && pre;
-    if (whole && (v0 || v1)) {
-      dma_barrier();  // every wave's last fragment reads of the main loop are done
-      if (v0) bf16_epilogue_tile_lds<Cfg, 0>(acc, m0, n0, N, C, pre, smem);
-      else bf16_epilogue_tile_lds<Cfg, 1>(acc, m0, n0, N, C, pre, smem);
-      return;
+    if constexpr (BWD) {
+      if constexpr (Cfg::WTN % 64 == 0 && Cfg::FM * Cfg::WTN / 2 <= 64) {  // pre prefetch: FM * WTN / 2 VGPRs
+        if (whole && (!ctr || M % 8 == 0)) {
+          bf16_epilogue_bwd_lds<Cfg>(acc, m0, n0, M, N, C, pre, smem, ctr);
+          return;
+        }
+      }
+    } else {
+      const bool v0 = epi == VDSL_EPI_NONE && c_dtype == VDSL_F32 && !pre;
+      const bool v1 = epi == VDSL_EPI_GELU && c_dtype == VDSL_BF16 && pre;
+      if (whole && (v0 || v1)) {
+        dma_barrier();  // every wave's last fragment reads of the main loop are done
+        if (v0) bf16_epilogue_tile_lds<Cfg, 0>(acc, m0, n0, N, C, pre, smem);
+        else bf16_epilogue_tile_lds<Cfg, 1>(acc, m0, n0, N, C, pre, smem);
+        return;
+      }
     }
   }
-  bf16_store_tile<Cfg>(acc, m0, n0, M, N, C, pre, epi, c_dtype);
+  bf16_store_tile<Cfg, BWD>(acc, m0, n0, M, N, C, pre, epi, c_dtype, ctr);
 }
 
 // Any K (including K % 8 != 0): one lane per output, f32 accumulate in k order.
 __global__ __launch_bounds__(256) void gemm_bf16_nt_simple(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                            void* __restrict__ C, float* __restrict__ pre, int M, int N,
-                                                           int K, int epi, int c_dtype) {
+                                                           int K, int epi, int c_dtype, uint16_t* __restrict__ ctr) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (idx >= static_cast<int64_t>(M) * N) return;
   const int row = static_cast<int>(idx / N), col = static_cast<int>(idx % N);
   float v = 0.0f;
   for (int k = 0; k < K; ++k)
     v = __builtin_fmaf(bf16_to_f32(A[static_cast<size_t>(row) * K + k]), bf16_to_f32(B[static_cast<size_t>(col) * K + k]), v);
+  if (epi == kEpiGeluBwd) {
+    const uint16_t h = f32_to_bf16(v * gelu_grad_f(pre[idx]));
+    static_cast<uint16_t*>(C)[idx] = h;
+    if (ctr) ctr[static_cast<size_t>(col) * M + row] = h;
+    return;
+  }
   if (pre) pre[idx] = v;
   float y = v;
   if (epi == VDSL_EPI_GELU) y = gelu_f(v);
@@ -237,19 +347,31 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_simple(const uint16_t* __res
 }
 
 template <class Cfg>
-int launch_cfg(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, int N, int K, int epi, int ct, hipStream_t s) {
+int launch_cfg(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, int N, int K, int epi, int ct, hipStream_t s,
+               uint16_t* ctr) {
   const int64_t tiles = static_cast<int64_t>((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN);
-  if (gemm_needs_edge<Cfg>(M, N, static_cast<int64_t>(K) * 2))
-    hipLaunchKernelGGL((gemm_bf16_nt<Cfg, true>), dim3(static_cast<unsigned>(tiles)), dim3(Cfg::NT), 0, s, A, B, C, pre, M, N, K, epi, ct);
-  else
-    hipLaunchKernelGGL((gemm_bf16_nt<Cfg, false>), dim3(static_cast<unsigned>(tiles)), dim3(Cfg::NT), 0, s, A, B, C, pre, M, N, K, epi, ct);
+  const dim3 g(static_cast<unsigned>(tiles)), b(Cfg::NT);
+  const bool edge = gemm_needs_edge<Cfg>(M, N, static_cast<int64_t>(K) * 2);
+  if (epi == kEpiGeluBwd) {
+    if (edge) hipLaunchKernelGGL((gemm_bf16_nt<Cfg, true, true>), g, b, 0, s, A, B, C, pre, M, N, K, epi, ct, ctr);
+    else hipLaunchKernelGGL((gemm_bf16_nt<Cfg, false, true>), g, b, 0, s, A, B, C, pre, M, N, K, epi, ct, ctr);
+  } else {
+    if (edge) hipLaunchKernelGGL((gemm_bf16_nt<Cfg, true, false>), g, b, 0, s, A, B, C, pre, M, N, K, epi, ct, ctr);
+    else hipLaunchKernelGGL((gemm_bf16_nt<Cfg, false, false>), g, b, 0, s, A, B, C, pre, M, N, K, epi, ct, ctr);
+  }
   return check_launch("gemm_bf16_nt");
 }
 
 template <class Cfg>
-int launch_dma(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, int N, int K, int epi, int ct, hipStream_t s) {
+int launch_dma(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, int N, int K, int epi, int ct, hipStream_t s,
+               uint16_t* ctr) {
   const int64_t tiles = static_cast<int64_t>((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN);
-  hipLaunchKernelGGL((gemm_bf16_dma<Cfg>), dim3(static_cast<unsigned>(tiles)), dim3(Cfg::NT), 0, s, A, B, C, pre, M, N, K, epi, ct);
+  if (epi == kEpiGeluBwd)
+    hipLaunchKernelGGL((gemm_bf16_dma<Cfg, true>), dim3(static_cast<unsigned>(tiles)), dim3(Cfg::NT), 0, s, A, B, C, pre, M, N, K, epi,
+                       ct, ctr);
+  else
+    hipLaunchKernelGGL((gemm_bf16_dma<Cfg, false>), dim3(static_cast<unsigned>(tiles)), dim3(Cfg::NT), 0, s, A, B, C, pre, M, N, K,
+                       epi, ct, ctr);
   return check_launch("gemm_bf16_dma");
 }
 
@@ -276,40 +398,41 @@ int choose_config(int64_t M, int64_t N, int64_t K) {
   return tiles_256x128 >= 512 ? 13 : 0;
 }
 
-int launch_nt(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, int N, int K, int epi, int ct, hipStream_t s) {
+int launch_nt(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, int N, int K, int epi, int ct, hipStream_t s,
+              uint16_t* ctr = nullptr) {
   if (K % 8 != 0) {
     const int64_t blocks = (static_cast<int64_t>(M) * N + 255) / 256;
-    hipLaunchKernelGGL(gemm_bf16_nt_simple, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, A, B, C, pre, M, N, K, epi, ct);
+    hipLaunchKernelGGL(gemm_bf16_nt_simple, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, A, B, C, pre, M, N, K, epi, ct, ctr);
     return check_launch("gemm_bf16_nt_simple");
   }
   switch (choose_config(M, N, K)) {
-    case 1: return launch_cfg<Bf1>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 2: return launch_cfg<Bf2>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 3: return launch_cfg<Bf3>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 4: return launch_cfg<Bf4>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 5: return launch_cfg<Bf5>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 6: return launch_cfg<Bf6>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 7: return launch_cfg<Bf7>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 8: return launch_cfg<Bf8>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 9: return launch_cfg<Bf9>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 10: return launch_cfg<Bf10>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 11: return launch_cfg<Bf11>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 12: return launch_cfg<Bf12>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 13: return launch_cfg<Bf13>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 14: return launch_dma<Dm14>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 15: return launch_dma<Dm15>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 16: return launch_dma<Dm16>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 17: return launch_dma<Dm17>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 18: return launch_dma<Dm18>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 19: return launch_dma<Dm19>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 20: return launch_dma<Dm20>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 21: return launch_dma<Dm21>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 22: return launch_dma<Dm22>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 23: return launch_dma<Dm23>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 24: return launch_dma<Dm24>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 25: return launch_dma<Dm25>(A, B, C, pre, M, N, K, epi, ct, s);
-    case 26: return launch_dma<Dm26>(A, B, C, pre, M, N, K, epi, ct, s);
-    default: return launch_cfg<Bf0>(A, B, C, pre, M, N, K, epi, ct, s);
+    case 1: return launch_cfg<Bf1>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 2: return launch_cfg<Bf2>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 3: return launch_cfg<Bf3>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 4: return launch_cfg<Bf4>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 5: return launch_cfg<Bf5>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 6: return launch_cfg<Bf6>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 7: return launch_cfg<Bf7>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 8: return launch_cfg<Bf8>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 9: return launch_cfg<Bf9>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 10: return launch_cfg<Bf10>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 11: return launch_cfg<Bf11>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 12: return launch_cfg<Bf12>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 13: return launch_cfg<Bf13>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 14: return launch_dma<Dm14>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 15: return launch_dma<Dm15>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 16: return launch_dma<Dm16>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 17: return launch_dma<Dm17>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 18: return launch_dma<Dm18>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 19: return launch_dma<Dm19>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 20: return launch_dma<Dm20>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 21: return launch_dma<Dm21>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 22: return launch_dma<Dm22>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 23: return launch_dma<Dm23>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 24: return launch_dma<Dm24>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 25: return launch_dma<Dm25>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    case 26: return launch_dma<Dm26>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
+    default: return launch_cfg<Bf0>(A, B, C, pre, M, N, K, epi, ct, s, ctr);
   }
 }
 
@@ -371,4 +494,20 @@ extern "C" int vdsl_debug_gemm_config(int32_t config) {
   vdsl::gemm_config_override();  // consume the environment value first, so it cannot override this
   vdsl::g_gemm_config.store(config < 0 ? -1 : config, std::memory_order_relaxed);
   return VDSL_OK;
+}
+
+extern "C" int vdsl_op_gemm_bf16_gelu_bwd(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer A, vdsl_buffer B,
+                                          vdsl_buffer pre, vdsl_buffer da, vdsl_buffer da_t) {
+  VDSL_TRY(enter_queue(q));
+  if (M < 0 || N < 0 || K < 0) return fail(VDSL_ERR_INVALID_ARG, "negative GEMM extent");
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x3fffffff) return fail(VDSL_ERR_UNSUPPORTED, "GEMM extent too large");
+  VDSL_TRY(check_buffer(q, A, static_cast<size_t>(M) * K * 2, "A", false));
+  VDSL_TRY(check_buffer(q, B, static_cast<size_t>(N) * K * 2, "B", false));
+  VDSL_TRY(check_buffer(q, pre, static_cast<size_t>(M) * N * 4, "pre", false));
+  VDSL_TRY(check_buffer(q, da, static_cast<size_t>(M) * N * 2, "da", true));
+  if (da_t) VDSL_TRY(check_buffer(q, da_t, static_cast<size_t>(M) * N * 2, "da_t", true));
+  if (M == 0 || N == 0) return VDSL_OK;
+  return launch_nt(static_cast<const uint16_t*>(A->ptr), static_cast<const uint16_t*>(B->ptr), da->ptr,
+                   static_cast<float*>(pre->ptr), static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), kEpiGeluBwd,
+                   VDSL_BF16, q->stream, da_t ? static_cast<uint16_t*>(da_t->ptr) : nullptr);
 }

@@ -48,7 +48,18 @@ class Op:
 
 
 class Graph:
-    def __init__(self):
+    def __init__(self, prepare_transposes: bool = False, fuse_gelu_backward: bool = False):
+        # prepare_transposes: backward() takes a param's transpose (the NT form's B of dL/dx) from a
+        # prepare op instead of transposing the param inside every step's GEMM.
+        # fuse_gelu_backward (needs prepare_transposes): GELU' is applied in the epilogue of the GEMM
+        # that forms dL/dy of a GELU output (vdsl_op_gemm_bf16_gelu_bwd) instead of by a separate op.
+        # Both off by default: measured on config 4 in one process, the step took 445.6 us as is,
+        # 462 us with the transpose prepared (the transpose's 11.6 us gone, yet the back-to-back
+        # GEMMs slower: they are power-bound and a memory-bound kernel between them lets the clock
+        # recover) and 450 us with both (the fused GEMM 94 us against 100 us for GEMM + transpose +
+        # GELU backward, the next forward GEMM 13 us slower).
+        self.prepare_transposes = prepare_transposes
+        self.fuse_gelu_backward = fuse_gelu_backward
         self.values: dict[str, Value] = {}
         self.ops: list[Op] = []
         # Ops that derive constant operands from params (weight packing): run by
@@ -160,12 +171,15 @@ class Graph:
             g = grad[y.name]
             act = op.attrs["act"]
             if act == "gelu":
-                if g[0] != "f32":
-                    g = self._to_f32(g[1])
-                da = self._value(self._fresh("d_pre"), y.shape, "bf16", "grad")
-                da_t = self._value(self._fresh("dT_pre"), y.shape[::-1], "bf16", "grad")
-                self._op("gelu_bwd", [g[1], op.attrs["pre"]], [da, da_t])
-                gb, gt = da, da_t
+                if g[0] == "gelu_da":  # the GEMM that formed dL/dy already applied GELU'
+                    gb, gt = g[1], g[2]
+                else:
+                    if g[0] != "f32":
+                        g = self._to_f32(g[1])
+                    da = self._value(self._fresh("d_pre"), y.shape, "bf16", "grad")
+                    da_t = self._value(self._fresh("dT_pre"), y.shape[::-1], "bf16", "grad")
+                    self._op("gelu_bwd", [g[1], op.attrs["pre"]], [da, da_t])
+                    gb, gt = da, da_t
             elif act == "none":
                 if g[0] == "f32":
                     gb, gt = self._to_bf16_pair(g[1])
@@ -179,11 +193,38 @@ class Graph:
                 self._op("gemm", [gt, x], [dw], trans_a=False, trans_b=False, epi=_lib.EPI_NONE)
                 param_grads[w.name] = dw
             if x.requires_grad or (x.producer is not None and x.kind == "activation" and _needs(x, self)):
-                dx = self._value(self._fresh("d_" + x.name), x.shape, "f32", "grad")
-                # dx[B][in] = sum_o g[b][o] W[o][in]: A = g [B][out], B = W stored [out][in] = [K][N]
-                self._op("gemm", [gb, w], [dx], trans_a=False, trans_b=False, epi=_lib.EPI_NONE)
-                grad[x.name] = ("f32", dx)
+                # dx[B][in] = sum_o g[b][o] W[o][in]: A = g [B][out], B = W stored [out][in] = [K][N].
+                # A param's transpose W^T [in][out] (the NT form's B) is made once by a prepare op
+                # instead of by the GEMM on every step.
+                wt = self._param_transpose(w) if self.prepare_transposes and w.kind == "param" else None
+                xp = x.producer
+                if (self.fuse_gelu_backward and wt is not None and xp is not None and xp.kind == "linear"
+                        and xp.attrs["act"] == "gelu"):
+                    # x = GELU(pre): the GEMM's epilogue applies GELU'(pre) and emits dL/dpre (bf16,
+                    # plus its transpose) without writing dL/dx
+                    da = self._value(self._fresh("d_pre"), x.shape, "bf16", "grad")
+                    da_t = self._value(self._fresh("dT_pre"), x.shape[::-1], "bf16", "grad")
+                    self._op("gemm_gelu_bwd", [gb, wt, xp.attrs["pre"]], [da, da_t])
+                    grad[x.name] = ("gelu_da", da, da_t)
+                else:
+                    dx = self._value(self._fresh("d_" + x.name), x.shape, "f32", "grad")
+                    if wt is not None:
+                        self._op("gemm", [gb, wt], [dx], trans_a=False, trans_b=True, epi=_lib.EPI_NONE)
+                    else:
+                        self._op("gemm", [gb, w], [dx], trans_a=False, trans_b=False, epi=_lib.EPI_NONE)
+                    grad[x.name] = ("f32", dx)
         return param_grads
+
+    def _param_transpose(self, w: Value) -> Value:
+        """W^T of a param, made by a prepare op (once per write of W, outside the replayed step)."""
+        name = w.name + ".T"
+        if name in self.values:
+            return self.values[name]
+        wt = self._value(name, w.shape[::-1], w.dtype, "param")
+        op = Op("transpose", [w], [wt])
+        wt.producer = op
+        self.prepare_ops.append(op)
+        return wt
 
     def _to_f32(self, v: Value) -> Value:
         o = self._value(self._fresh(v.name + "_f32"), v.shape, "f32", "grad")
@@ -259,8 +300,14 @@ class Executable:
         unless a param is written after capture (then call prepare() before the next launch)."""
         T = self.t
         for op in self.graph.prepare_ops:
-            if op.kind == "pack_w8a8" and op.inputs[0].name in self._stale:
+            if op.inputs[0].name not in self._stale:
+                continue
+            if op.kind == "pack_w8a8":
                 kernels.pack_w8a8_weights(q, T[op.inputs[0].name], T[op.outputs[0].name])
+            elif op.kind == "transpose":
+                kernels.transpose(q, T[op.inputs[0].name], T[op.outputs[0].name])
+            else:
+                raise NotImplementedError(op.kind)
         self._stale.clear()
 
     def read(self, q: Queue, name: str):
@@ -290,6 +337,8 @@ class Executable:
                     raise RuntimeError("mse without backward: call Graph.backward() or use the loss op's fused form")
             elif op.kind == "gelu_bwd":
                 kernels.gelu_bwd(q, ins[0], ins[1], outs[0], outs[1])
+            elif op.kind == "gemm_gelu_bwd":
+                kernels.gemm_bf16_gelu_bwd(q, ins[0], ins[1], ins[2], outs[0], outs[1])
             elif op.kind == "cast":
                 kernels.cast(q, ins[0], outs[0])
             elif op.kind == "transpose":
@@ -323,9 +372,10 @@ class Executable:
 
 
 # ---- the two workload graphs ------------------------------------------------------------------------
-def mlp_train_graph(batch=2048, d_in=4096, hidden=4096, d_out=4096):
+def mlp_train_graph(batch=2048, d_in=4096, hidden=4096, d_out=4096, prepare_transposes=False,
+                    fuse_gelu_backward=False):
     """Config 4: X -> GELU(X W1^T) -> (.) W2^T -> MSE(., T), with backward for W1 and W2."""
-    g = Graph()
+    g = Graph(prepare_transposes, fuse_gelu_backward)
     x = g.input("X", (batch, d_in), "bf16")
     w1 = g.param("W1", (hidden, d_in), "bf16")
     w2 = g.param("W2", (d_out, hidden), "bf16")
