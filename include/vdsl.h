@@ -280,6 +280,15 @@ int vdsl_gemm_bf16_workspace_bytes(int32_t trans_a, int32_t trans_b, int64_t M, 
 int vdsl_op_gemm_bf16(vdsl_queue q, int32_t trans_a, int32_t trans_b, int64_t M, int64_t N,
                       int64_t K, vdsl_buffer A, vdsl_buffer B, vdsl_buffer C, int32_t c_dtype,
                       int32_t epilogue, vdsl_buffer pre_act, vdsl_buffer workspace);
+/* Weights in MFMA fragment order, for vdsl_op_gemm_bf16_packed (packed once when the weights are
+ * written, not per call): w bf16 [N][K] (out x in) -> wp, same bytes, in the layout of
+ * vdsl_op_pack_w8a8_weights on the K*2-byte rows.  N % 32 == 0, K % 16 == 0. */
+int vdsl_op_pack_bf16_weights(vdsl_queue q, int64_t N, int64_t K, vdsl_buffer w, vdsl_buffer wp);
+/* vdsl_op_gemm_bf16(trans_a = 0, trans_b = 1) with B packed by vdsl_op_pack_bf16_weights: the
+ * same products in the same order, bit for bit.  N % 32 == 0, K % 256 == 0.  No workspace. */
+int vdsl_op_gemm_bf16_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer A,
+                             vdsl_buffer Bp, vdsl_buffer C, int32_t c_dtype, int32_t epilogue,
+                             vdsl_buffer pre_act);
 
 /* 2-D transpose: dst [cols][rows] = src [rows][cols]^T, dtype F32 or BF16. */
 int vdsl_op_transpose(vdsl_queue q, int64_t rows, int64_t cols, int32_t dtype, vdsl_buffer src,

@@ -223,6 +223,37 @@ def test_optional_outputs_absent(dev, q, rows, cols):
         t.free()
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 4096), (300, 544, 256), (129, 96, 512)])
+def test_gemm_bf16_packed_bit_identical(dev, q, M, N, K):
+    """The packed-weight GEMM equals the row-major NT GEMM bit for bit (same k-steps, same order),
+    with f32 output and with the GELU epilogue (bf16 out + f32 pre-activation), whole and ragged
+    tiles; the packed weights hold the same bytes."""
+    A = bf16_rand((M, K), 101)
+    B = bf16_rand((N, K), 102)
+    tA, tB = Tensor.from_numpy(dev, q, A, "bf16"), Tensor.from_numpy(dev, q, B, "bf16")
+    tBp = Tensor(dev, (N, K), "bf16")
+    kernels.pack_bf16_weights(q, tB, tBp)
+    assert np.array_equal(np.sort(tBp.numpy(q).reshape(-1)), np.sort(B.reshape(-1)))
+    outs = []
+    for packed in (False, True):
+        c32, h, pre = Tensor(dev, (M, N), "f32"), Tensor(dev, (M, N), "bf16"), Tensor(dev, (M, N), "f32")
+        for t in (c32, h, pre):
+            t.buffer.fill_u32(q, 0x7FC07FC0)
+        if packed:
+            kernels.gemm_bf16_packed(q, tA, tBp, c32)
+            kernels.gemm_bf16_packed(q, tA, tBp, h, _lib.EPI_GELU, pre)
+        else:
+            kernels.gemm_bf16(q, tA, tB, c32, False, True)
+            kernels.gemm_bf16(q, tA, tB, h, False, True, _lib.EPI_GELU, pre)
+        outs.append([t.numpy(q) for t in (c32, h, pre)])
+        for t in (c32, h, pre):
+            t.free()
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+    for t in (tA, tB, tBp):
+        t.free()
+
+
 def test_gemm_gelu_bwd_fused_config4(dev, q):
     """Config 4's dL/dpre at full size (2048x4096, K 4096): the fused op equals the plain GEMM +
     GELU backward bit for bit, and the values match the oracle's GELU backward of the oracle GEMM

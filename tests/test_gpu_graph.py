@@ -72,12 +72,15 @@ def test_mlp_small_end_to_end(dev, q):
 
 
 def test_mlp_graph_variants_identical(dev, q):
-    """The prepared-transpose and fused-GELU-backward forms of the training step run the same
-    products in the same order: every output equals the default graph's bit for bit (each graph
-    also replays equal to its eager run)."""
-    x, w1, w2, t = spec.mlp_inputs(batch=256, d_in=384, hidden=512, d_out=256)
-    base = run_mlp(dev, q, x, w1, w2, t, replays=2)
-    for variant in ({"prepare_transposes": True}, {"prepare_transposes": True, "fuse_gelu_backward": True}):
+    """The prepared-transpose, fused-GELU-backward and packed-weight forms of the training step (and
+    mlp_train_graph's default, all three) run the same products in the same order: every output
+    equals the plain graph's bit for bit (each graph also replays equal to its eager run)."""
+    x, w1, w2, t = spec.mlp_inputs(batch=256, d_in=512, hidden=512, d_out=256)
+    plain = {"prepare_transposes": False, "fuse_gelu_backward": False, "pack_weights": False}
+    base = run_mlp(dev, q, x, w1, w2, t, replays=2, **plain)
+    for variant in ({"prepare_transposes": True}, {"prepare_transposes": True, "fuse_gelu_backward": True},
+                    {"pack_weights": True}, {}):
+        variant = {**plain, **variant} if variant else {}
         got = run_mlp(dev, q, x, w1, w2, t, replays=2, **variant)
         for n in ("H", "Y", "loss", "grad_W1", "grad_W2", "pre"):
             assert np.array_equal(got[n], base[n]), f"{variant}: {n} differs"

@@ -10,7 +10,8 @@ from vernondsl_amd import graph, rng
 
 
 def test_mlp_backward_op_sequence():
-    g, grads = graph.mlp_train_graph(batch=64, d_in=32, hidden=48, d_out=16)
+    g, grads = graph.mlp_train_graph(batch=64, d_in=32, hidden=48, d_out=16, prepare_transposes=False,
+                                     fuse_gelu_backward=False)
     kinds = [op.kind for op in g.ops]
     assert kinds == ["linear", "linear", "mse", "gemm", "gemm", "gelu_bwd", "gemm"]
     assert sorted(grads) == ["W1", "W2"]
@@ -27,7 +28,8 @@ def test_mlp_backward_op_sequence():
 
 
 def test_mlp_backward_prepared_transpose_and_fused_gelu():
-    g, _ = graph.mlp_train_graph(batch=64, d_in=32, hidden=48, d_out=16, prepare_transposes=True)
+    g, _ = graph.mlp_train_graph(batch=64, d_in=32, hidden=48, d_out=16, prepare_transposes=True,
+                                 fuse_gelu_backward=False)
     assert [op.kind for op in g.ops] == ["linear", "linear", "mse", "gemm", "gemm", "gelu_bwd", "gemm"]
     # dH = dY W2 in the NT form on W2^T [hid][out], made by a prepare op (not on every step)
     dH = g.ops[4]
@@ -41,6 +43,22 @@ def test_mlp_backward_prepared_transpose_and_fused_gelu():
     assert dA.inputs[1].name == "W2.T" and dA.inputs[2] is g.ops[0].attrs["pre"]
     assert [v.shape for v in dA.outputs] == [(64, 48), (48, 64)] and dA.outputs[0].dtype == "bf16"
     assert dW1.inputs[0] is dA.outputs[1]
+
+
+def test_mlp_packed_weights():
+    """pack_weights: each forward linear op on a param reads a packed copy made by a prepare op;
+    the backward ops still read the row-major weight."""
+    g, _ = graph.mlp_train_graph(batch=64, d_in=512, hidden=512, d_out=256, pack_weights=True,
+                                 prepare_transposes=False, fuse_gelu_backward=False)
+    assert [(op.kind, op.inputs[0].name, op.outputs[0].name) for op in g.prepare_ops] == [
+        ("pack_bf16", "W1", "W1.packed"), ("pack_bf16", "W2", "W2.packed")]
+    lin = [op for op in g.ops if op.kind == "linear"]
+    assert [op.attrs["packed"].name for op in lin] == ["W1.packed", "W2.packed"]
+    assert [op.inputs[1].name for op in lin] == ["W1", "W2"]
+    assert g.ops[4].inputs[1].name == "W2"  # dH = dY W2 uses the row-major weight
+    g2, _ = graph.mlp_train_graph(batch=64, d_in=32, hidden=48, d_out=16, pack_weights=True,
+                                  prepare_transposes=False)
+    assert not g2.prepare_ops  # widths the packed GEMM does not take (K % 256) stay row-major
 
 
 def test_inference_graph_has_no_backward():

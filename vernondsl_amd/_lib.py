@@ -129,6 +129,8 @@ PROTOTYPES = {
     "vdsl_op_col_reduce": (C.c_int, [_vp, _i64, _i64, _i32, _vp, _vp, _vp]),
     "vdsl_gemm_bf16_workspace_bytes": (C.c_int, [_i32, _i32, _i64, _i64, _i64, C.POINTER(_sz)]),
     "vdsl_op_gemm_bf16": (C.c_int, [_vp, _i32, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
+    "vdsl_op_pack_bf16_weights": (C.c_int, [_vp, _i64, _i64, _vp, _vp]),
+    "vdsl_op_gemm_bf16_packed": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _vp]),
     "vdsl_op_transpose": (C.c_int, [_vp, _i64, _i64, _i32, _vp, _vp]),
     "vdsl_op_cast": (C.c_int, [_vp, _i64, _i32, _vp, _i32, _vp]),
     "vdsl_op_gelu_fwd": (C.c_int, [_vp, _i64, _i32, _vp, _i32, _vp]),

@@ -35,6 +35,8 @@ template <class T, int FM_, int FN_, int W_, int PD_>
 struct BpkConfig {
   static constexpr int FM = FM_, FN = FN_, W = W_, PD = PD_;
   static constexpr int BM = 32 * FM, BN = 32 * FN * W, NT = 64 * W;
+  // The wave grid in the terms the shared epilogues use (1 x W waves, each BM x 32 FN).
+  static constexpr int WGM = 1, WGN = W, NW = W, WTM = BM, WTN = 32 * FN;
   static constexpr int BKB = 128, KS = 4;   // K bytes and MFMA k-steps per stage
   static constexpr int NR = PD + 1;         // LDS slots = B register sets = stages per loop trip
   static constexpr int SUB = BM * 64;       // one 64-byte sub-stage of A
@@ -207,8 +209,9 @@ __device__ __forceinline__ void bpk_mainloop(const char* __restrict__ A, const c
 }
 
 // Packs B [N][K] (row-major, Kb bytes per row; N % 32 == 0, Kb % 32 == 0) into fragment order:
-// thread u writes 16-byte chunk u of the packed array.
-__global__ __launch_bounds__(256) void bpk_pack_kernel(const char* __restrict__ B, char* __restrict__ Bp, int64_t nblk,
+// thread u writes 16-byte chunk u of the packed array.  Internal linkage: each source file that
+// includes this header launches its own copy.
+static __global__ __launch_bounds__(256) void bpk_pack_kernel(const char* __restrict__ B, char* __restrict__ Bp, int64_t nblk,
                                                        int64_t kblk, int64_t Kb) {
   const int64_t chunks = nblk * kblk * 64;
   for (int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; u < chunks;

@@ -107,6 +107,30 @@ def gemm_bf16(q: Queue, A: Tensor, B: Tensor, Cout: Tensor, trans_a=False, trans
          Cout.dtype, int(epilogue), _h(pre_act), _h(workspace))
 
 
+def pack_bf16_weights(q: Queue, w: Tensor, wp: Tensor):
+    """Writes w (bf16 [N][K]) into wp in the MFMA fragment order gemm_bf16_packed reads."""
+    N, K = w.shape
+    _expect(w, (N, K), "bf16", "w")
+    _expect(wp, (N, K), "bf16", "wp")
+    call("vdsl_op_pack_bf16_weights", q.handle, N, K, w.handle, wp.handle)
+
+
+def gemm_bf16_packed(q: Queue, A: Tensor, Bp: Tensor, Cout: Tensor, epilogue=_lib.EPI_NONE, pre_act=None):
+    """gemm_bf16(A, B, trans_b=True) with B packed by pack_bf16_weights (Bp keeps the logical
+    shape [N][K]); bit-identical results."""
+    M, K = A.shape
+    N, K2 = Bp.shape
+    if K != K2:
+        raise ValueError(f"inner dimensions differ: {K} vs {K2}")
+    _expect(A, (M, K), "bf16", "A")
+    _expect(Bp, (N, K), "bf16", "Bp")
+    if Cout.shape != (M, N):
+        raise ValueError(f"C: shape {Cout.shape}, expected {(M, N)}")
+    _expect(pre_act, (M, N), "f32", "pre_act")
+    call("vdsl_op_gemm_bf16_packed", q.handle, M, N, K, A.handle, Bp.handle, Cout.handle, Cout.dtype, int(epilogue),
+         _h(pre_act))
+
+
 def transpose(q: Queue, src: Tensor, dst: Tensor):
     rows, cols = src.shape
     _expect(dst, (cols, rows), src.dtype, "dst")
