@@ -314,6 +314,10 @@ int vdsl_op_gelu_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer dh, v
  * counterpart (north-star op class: compiler-generated backward GEMMs). */
 int vdsl_op_gemm_bf16_gelu_bwd(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer A,
                                vdsl_buffer B, vdsl_buffer pre, vdsl_buffer da, vdsl_buffer da_t);
+/* vdsl_op_gemm_bf16_gelu_bwd with B packed by vdsl_op_pack_bf16_weights (for a constant B, e.g. the
+ * transposed weight of the layer above): same results bit for bit.  N % 32 == 0, K % 256 == 0. */
+int vdsl_op_gemm_bf16_gelu_bwd_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer A,
+                                      vdsl_buffer Bp, vdsl_buffer pre, vdsl_buffer da, vdsl_buffer da_t);
 /* MSE: loss (f32 [1]) = mean((y - t)^2);  dy (bf16 [rows][cols]) = 2 (y - t) / (rows*cols);
  * dy_t (optional) = dy^T.  y, t: f32 [rows][cols].  partials: f32 scratch of
  * vdsl_mse_partials_count(rows, cols) elements (deterministic two-stage reduction). */

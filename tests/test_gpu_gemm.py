@@ -254,6 +254,35 @@ def test_gemm_bf16_packed_bit_identical(dev, q, M, N, K):
         t.free()
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 544, 256), (256, 512, 512), (129, 96, 512)])
+def test_gemm_gelu_bwd_packed_small(dev, q, M, N, K):
+    """Packed fused GELU backward = plain GEMM + GELU backward, bit for bit, whole and ragged tiles
+    (M % 8 != 0 takes the per-element transposed store)."""
+    A, B = bf16_rand((M, K), 111), bf16_rand((N, K), 112)
+    pre = (rng.normal(113, M * N) * 2.0).astype(np.float32).reshape(M, N)
+    tA, tB, tpre = Tensor.from_numpy(dev, q, A, "bf16"), Tensor.from_numpy(dev, q, B, "bf16"), Tensor.from_numpy(dev, q, pre)
+    tBp = Tensor(dev, (N, K), "bf16")
+    kernels.pack_bf16_weights(q, tB, tBp)
+    res = []
+    for fused in (False, True):
+        da, da_t = Tensor(dev, (M, N), "bf16"), Tensor(dev, (N, M), "bf16")
+        for t in (da, da_t):
+            t.buffer.fill_u32(q, 0x7FC07FC0)
+        if fused:
+            kernels.gemm_bf16_gelu_bwd(q, tA, tBp, tpre, da, da_t, packed=True)
+        else:
+            dh = Tensor(dev, (M, N), "f32")
+            kernels.gemm_bf16(q, tA, tB, dh, False, True)
+            kernels.gelu_bwd(q, dh, tpre, da, da_t)
+            dh.free()
+        res.append((da.numpy(q), da_t.numpy(q)))
+        da.free()
+        da_t.free()
+    assert np.array_equal(res[0][0], res[1][0]) and np.array_equal(res[0][1], res[1][1])
+    for t in (tA, tB, tBp, tpre):
+        t.free()
+
+
 def test_gemm_gelu_bwd_fused_config4(dev, q):
     """Config 4's dL/dpre at full size (2048x4096, K 4096): the fused op equals the plain GEMM +
     GELU backward bit for bit, and the values match the oracle's GELU backward of the oracle GEMM
@@ -272,6 +301,14 @@ def test_gemm_gelu_bwd_fused_config4(dev, q):
     assert np.array_equal(g, da2.numpy(q))
     assert np.array_equal(gt, da2_t.numpy(q))
     assert np.array_equal(gt, g.T)
+    tBp = Tensor(dev, (N, K), "bf16")  # the packed-weight form: same bits
+    kernels.pack_bf16_weights(q, tB, tBp)
+    for t in (da2, da2_t):
+        t.buffer.fill_u32(q, 0x7FC07FC0)
+    kernels.gemm_bf16_gelu_bwd(q, tA, tBp, tpre, da2, da2_t, packed=True)
+    assert np.array_equal(g, da2.numpy(q))
+    assert np.array_equal(gt, da2_t.numpy(q))
+    tBp.free()
     rows = [0, 777, 2047]
     dh_ref = oracle.gemm_bf16(A[rows], B, False, True)
     ref, _ = oracle.gelu_bwd(dh_ref.astype(np.float32), pre[rows])

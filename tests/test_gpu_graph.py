@@ -86,6 +86,29 @@ def test_mlp_graph_variants_identical(dev, q):
             assert np.array_equal(got[n], base[n]), f"{variant}: {n} differs"
 
 
+def test_mlp_rewritten_weights_reprepared(dev, q):
+    """Writing W2 after a run re-runs the prepare chain that derives from it (W2 packed; W2^T, then
+    W2^T packed): the next step equals the plain graph's step with the new W2, bit for bit."""
+    x, w1, w2, t = spec.mlp_inputs(batch=256, d_in=512, hidden=512, d_out=256)
+    w2b = np.ascontiguousarray(w2[::-1])
+    plain = {"prepare_transposes": False, "fuse_gelu_backward": False, "pack_weights": False}
+    ref = run_mlp(dev, q, x, w1, w2b, t, replays=1, **plain)
+    g, _ = graph.mlp_train_graph(256, 512, 512, 256)
+    assert len(g.prepare_ops) == 4
+    exe = g.compile(dev)
+    for name, arr in (("X", x), ("W1", w1), ("W2", w2), ("T", t)):
+        exe.write(q, name, arr)
+    exe.run(q)
+    exe.write(q, "W2", w2b)
+    step = exe.capture(q)
+    step.launch(q)
+    q.sync()
+    for n in ("Y", "loss", "grad_W1", "grad_W2"):
+        assert np.array_equal(exe.read(q, n), ref[n]), n
+    step.destroy()
+    exe.free()
+
+
 def test_mlp_config4_full_size(dev, q):
     x, w1, w2, t = spec.mlp_inputs()
     got = run_mlp(dev, q, x, w1, w2, t, replays=2)

@@ -61,6 +61,18 @@ def test_mlp_packed_weights():
     assert not g2.prepare_ops  # widths the packed GEMM does not take (K % 256) stay row-major
 
 
+def test_mlp_default_graph_prepare_chain():
+    """mlp_train_graph's default: packed forward weights, and the fused GELU-backward GEMM on W2^T
+    packed (transpose, then pack: two prepare ops run in order)."""
+    g, _ = graph.mlp_train_graph(batch=64, d_in=512, hidden=512, d_out=256)
+    assert [op.kind for op in g.ops] == ["linear", "linear", "mse", "gemm", "gemm_gelu_bwd", "gemm"]
+    assert [(op.kind, op.inputs[0].name, op.outputs[0].name) for op in g.prepare_ops] == [
+        ("pack_bf16", "W1", "W1.packed"), ("pack_bf16", "W2", "W2.packed"), ("transpose", "W2", "W2.T"),
+        ("pack_bf16", "W2.T", "W2.T.packed")]
+    dA = g.ops[4]
+    assert dA.inputs[1].name == "W2.T.packed" and dA.attrs["packed"]
+
+
 def test_inference_graph_has_no_backward():
     g = graph.w8a8_infer_graph(batch=8, widths=(64, 64, 32))
     assert [op.kind for op in g.ops] == ["quantize", "w8a8", "quantize", "w8a8"]

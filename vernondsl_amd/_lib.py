@@ -136,6 +136,7 @@ PROTOTYPES = {
     "vdsl_op_gelu_fwd": (C.c_int, [_vp, _i64, _i32, _vp, _i32, _vp]),
     "vdsl_op_gelu_bwd": (C.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "vdsl_op_gemm_bf16_gelu_bwd": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "vdsl_op_gemm_bf16_gelu_bwd_packed": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
     "vdsl_mse_partials_count": (C.c_int64, [_i64, _i64]),
     "vdsl_op_mse_fwd_bwd": (C.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vdsl_op_quantize_rows_i8": (C.c_int, [_vp, _i64, _i64, _i32, _vp, _vp, _vp]),

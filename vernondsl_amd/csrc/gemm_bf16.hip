@@ -203,14 +203,14 @@ __device__ __forceinline__ void bf16_epilogue_tile_lds(const f32x16 (&acc)[Cfg::
 // pass long before): every load of it for the wave's whole tile is issued first, before the block
 // barrier that ends the main loop, so the tile pays one memory latency instead of one per unit
 // (in a training step the per-unit form made this GEMM 38 us slower than without the epilogue).
-template <class Cfg>
+template <class Cfg, int LDS_AVAIL = Cfg::LDS_BYTES>
 __device__ __forceinline__ void bf16_epilogue_bwd_lds(const f32x16 (&acc)[Cfg::FM][Cfg::FN], int m0, int n0, int M,
                                                       int N, void* __restrict__ C, const float* __restrict__ pre,
                                                       char* smem, uint16_t* __restrict__ ctr) {
   constexpr int WTN = Cfg::WTN, LD = WTN + 8, Q = WTN / 4, UPL = 32 * Q / 64;  // 16-byte units per lane per row block
-  // Rows of the wave's area: the whole wave tile when it fits in the block's LDS (then each lane's
-  // transposed run is WTM * 2 bytes, a whole 128-byte line for 64-row wave tiles), else 32.
-  constexpr int AR = Cfg::NW * Cfg::WTM * LD * 4 <= Cfg::LDS_BYTES ? Cfg::WTM : 32;
+  // Rows of the wave's area: the whole wave tile when it fits in the block's LDS (LDS_AVAIL bytes;
+  // then each lane's transposed run is WTM * 2 bytes, whole 128-byte lines), else 32.
+  constexpr int AR = Cfg::NW * Cfg::WTM * LD * 4 <= LDS_AVAIL ? Cfg::WTM : 32;
   static_assert(WTN % 64 == 0, "the transposed store takes whole columns per lane");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
@@ -354,12 +354,20 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_simple(const uint16_t* __res
 // 2048x4096x4096 (random bf16, f32 out): 61-63 us against 66-68 us for the direct-to-LDS kernel.
 using Pb0 = BpkConfig<MfmaBf16, 4, 2, 4, 3>;  // 128 x 256 blocks, 4 waves of 128 x 64
 
-template <class Cfg>
+// BWD: the GELU-backward epilogue of vdsl_op_gemm_bf16_gelu_bwd_packed (C = da, pre an input, ctr =
+// da^T); its LDS is enlarged so the whole wave tile stages at once (whole-line transposed stores).
+template <class Cfg, bool BWD>
+constexpr int bpk_bf16_smem() {
+  return BWD && Cfg::NW * Cfg::WTM * (Cfg::WTN + 8) * 4 > Cfg::LDS_BYTES ? Cfg::NW * Cfg::WTM * (Cfg::WTN + 8) * 4
+                                                                          : Cfg::LDS_BYTES;
+}
+
+template <class Cfg, bool BWD>
 __global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_bpk(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bp,
                                                          void* __restrict__ C, float* __restrict__ pre, int M, int N, int K,
-                                                         int epi, int c_dtype) {
+                                                         int epi, int c_dtype, uint16_t* __restrict__ ctr) {
   // The only __shared__ variable (see gemm_bpk.h); after the main loop it stages the epilogue.
-  __shared__ __attribute__((aligned(1024))) char smem[Cfg::LDS_BYTES];
+  __shared__ __attribute__((aligned(1024))) char smem[bpk_bf16_smem<Cfg, BWD>()];
   const int tiles_m = (M + Cfg::BM - 1) / Cfg::BM;
   const int tile = xcd_remap(blockIdx.x, gridDim.x);
   const int m0 = (tile % tiles_m) * Cfg::BM, n0 = (tile / tiles_m) * Cfg::BN;
@@ -368,15 +376,22 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_bpk(const uint16_t* __re
                               m0, n0, smem, acc);
   static_assert(kLdsEpilogue<Cfg>, "the LDS-staged epilogue must fit the main loop's LDS");
   const bool whole = m0 + Cfg::BM <= M && n0 + Cfg::BN <= N && N % 4 == 0;
-  const bool v0 = epi == VDSL_EPI_NONE && c_dtype == VDSL_F32 && !pre;
-  const bool v1 = epi == VDSL_EPI_GELU && c_dtype == VDSL_BF16 && pre;
-  if (whole && (v0 || v1)) {
-    __syncthreads();  // every wave is past its last read of the main loop's LDS
-    if (v0) bf16_epilogue_tile_lds<Cfg, 0>(acc, m0, n0, N, C, pre, smem);
-    else bf16_epilogue_tile_lds<Cfg, 1>(acc, m0, n0, N, C, pre, smem);
-    return;
+  if constexpr (BWD) {
+    if (whole && (!ctr || M % 8 == 0)) {
+      bf16_epilogue_bwd_lds<Cfg, bpk_bf16_smem<Cfg, true>()>(acc, m0, n0, M, N, C, pre, smem, ctr);
+      return;
+    }
+  } else {
+    const bool v0 = epi == VDSL_EPI_NONE && c_dtype == VDSL_F32 && !pre;
+    const bool v1 = epi == VDSL_EPI_GELU && c_dtype == VDSL_BF16 && pre;
+    if (whole && (v0 || v1)) {
+      __syncthreads();  // every wave is past its last read of the main loop's LDS
+      if (v0) bf16_epilogue_tile_lds<Cfg, 0>(acc, m0, n0, N, C, pre, smem);
+      else bf16_epilogue_tile_lds<Cfg, 1>(acc, m0, n0, N, C, pre, smem);
+      return;
+    }
   }
-  bf16_store_tile<Cfg, false>(acc, m0, n0, M, N, C, pre, epi, c_dtype, nullptr);
+  bf16_store_tile<Cfg, BWD>(acc, m0, n0, M, N, C, pre, epi, c_dtype, ctr);
 }
 
 template <class Cfg>
@@ -576,9 +591,30 @@ extern "C" int vdsl_op_gemm_bf16_packed(vdsl_queue q, int64_t M, int64_t N, int6
   if (pre_act) VDSL_TRY(check_buffer(q, pre_act, static_cast<size_t>(M) * N * 4, "pre_act", true));
   if (M == 0 || N == 0) return VDSL_OK;
   const int64_t tiles = ((M + Pb0::BM - 1) / Pb0::BM) * ((N + Pb0::BN - 1) / Pb0::BN);
-  hipLaunchKernelGGL(gemm_bf16_bpk<Pb0>, dim3(static_cast<unsigned>(tiles)), dim3(Pb0::NT), 0, q->stream,
+  hipLaunchKernelGGL((gemm_bf16_bpk<Pb0, false>), dim3(static_cast<unsigned>(tiles)), dim3(Pb0::NT), 0, q->stream,
                      static_cast<const uint16_t*>(A->ptr), static_cast<const uint16_t*>(Bp->ptr), C->ptr,
                      pre_act ? static_cast<float*>(pre_act->ptr) : nullptr, static_cast<int>(M), static_cast<int>(N),
-                     static_cast<int>(K), epilogue, c_dtype);
+                     static_cast<int>(K), epilogue, c_dtype, nullptr);
   return check_launch("gemm_bf16_bpk");
+}
+
+extern "C" int vdsl_op_gemm_bf16_gelu_bwd_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer A,
+                                                 vdsl_buffer Bp, vdsl_buffer pre, vdsl_buffer da, vdsl_buffer da_t) {
+  VDSL_TRY(enter_queue(q));
+  if (M < 0 || N < 0 || K < 0) return fail(VDSL_ERR_INVALID_ARG, "negative GEMM extent");
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x3fffffff) return fail(VDSL_ERR_UNSUPPORTED, "GEMM extent too large");
+  if (N % 32) return fail(VDSL_ERR_UNSUPPORTED, "packed GEMM needs N % 32 == 0");
+  if ((2 * K) % (128 * Pb0::NR) || K == 0) return fail(VDSL_ERR_UNSUPPORTED, "packed bf16 GEMM needs K % 256 == 0 and K > 0");
+  VDSL_TRY(check_buffer(q, A, static_cast<size_t>(M) * K * 2, "A", false));
+  VDSL_TRY(check_buffer(q, Bp, static_cast<size_t>(N) * K * 2, "Bp", false));
+  VDSL_TRY(check_buffer(q, pre, static_cast<size_t>(M) * N * 4, "pre", false));
+  VDSL_TRY(check_buffer(q, da, static_cast<size_t>(M) * N * 2, "da", true));
+  if (da_t) VDSL_TRY(check_buffer(q, da_t, static_cast<size_t>(M) * N * 2, "da_t", true));
+  if (M == 0 || N == 0) return VDSL_OK;
+  const int64_t tiles = ((M + Pb0::BM - 1) / Pb0::BM) * ((N + Pb0::BN - 1) / Pb0::BN);
+  hipLaunchKernelGGL((gemm_bf16_bpk<Pb0, true>), dim3(static_cast<unsigned>(tiles)), dim3(Pb0::NT), 0, q->stream,
+                     static_cast<const uint16_t*>(A->ptr), static_cast<const uint16_t*>(Bp->ptr), da->ptr,
+                     static_cast<float*>(pre->ptr), static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
+                     kEpiGeluBwd, VDSL_BF16, da_t ? static_cast<uint16_t*>(da_t->ptr) : nullptr);
+  return check_launch("gemm_bf16_bpk<gelu_bwd>");
 }

@@ -223,7 +223,10 @@ class Graph:
                     # plus its transpose) without writing dL/dx
                     da = self._value(self._fresh("d_pre"), x.shape, "bf16", "grad")
                     da_t = self._value(self._fresh("dT_pre"), x.shape[::-1], "bf16", "grad")
-                    self._op("gemm_gelu_bwd", [gb, wt, xp.attrs["pre"]], [da, da_t])
+                    packed = self.pack_weights and wt.shape[0] % 32 == 0 and wt.shape[1] % 256 == 0
+                    if packed:  # W^T packed into MFMA fragment order (a second prepare op)
+                        wt = self._prepared(wt, "packed", wt.shape, "pack_bf16")
+                    self._op("gemm_gelu_bwd", [gb, wt, xp.attrs["pre"]], [da, da_t], packed=packed)
                     grad[x.name] = ("gelu_da", da, da_t)
                 else:
                     dx = self._value(self._fresh("d_" + x.name), x.shape, "f32", "grad")
@@ -311,9 +314,10 @@ class Executable:
         run() and capture() call it first, so a replayed step never reads stale packed weights
         unless a param is written after capture (then call prepare() before the next launch)."""
         T = self.t
-        for op in self.graph.prepare_ops:
+        for op in self.graph.prepare_ops:  # in order: an op may read what an earlier one made
             if op.inputs[0].name not in self._stale:
                 continue
+            self._stale.update(v.name for v in op.outputs)
             if op.kind == "pack_w8a8":
                 kernels.pack_w8a8_weights(q, T[op.inputs[0].name], T[op.outputs[0].name])
             elif op.kind == "transpose":
@@ -356,7 +360,7 @@ class Executable:
             elif op.kind == "gelu_bwd":
                 kernels.gelu_bwd(q, ins[0], ins[1], outs[0], outs[1])
             elif op.kind == "gemm_gelu_bwd":
-                kernels.gemm_bf16_gelu_bwd(q, ins[0], ins[1], ins[2], outs[0], outs[1])
+                kernels.gemm_bf16_gelu_bwd(q, ins[0], ins[1], ins[2], outs[0], outs[1], op.attrs.get("packed", False))
             elif op.kind == "cast":
                 kernels.cast(q, ins[0], outs[0])
             elif op.kind == "transpose":

@@ -159,9 +159,10 @@ def gelu_bwd(q: Queue, dh: Tensor, pre: Tensor, da: Tensor, da_t=None):
     call("vdsl_op_gelu_bwd", q.handle, rows, cols, dh.handle, pre.handle, da.handle, _h(da_t))
 
 
-def gemm_bf16_gelu_bwd(q: Queue, A: Tensor, B: Tensor, pre: Tensor, da: Tensor, da_t=None):
+def gemm_bf16_gelu_bwd(q: Queue, A: Tensor, B: Tensor, pre: Tensor, da: Tensor, da_t=None, packed=False):
     """da = (A B^T) * GELU'(pre) as bf16 (and da_t = da^T): the GEMM forming dL/dy fused with the
-    GELU backward (A bf16 [M][K], B bf16 [N][K], pre f32 [M][N])."""
+    GELU backward (A bf16 [M][K], B bf16 [N][K] - packed by pack_bf16_weights if `packed` -, pre
+    f32 [M][N])."""
     M, K = A.shape
     N, K2 = B.shape
     if K != K2:
@@ -171,7 +172,8 @@ def gemm_bf16_gelu_bwd(q: Queue, A: Tensor, B: Tensor, pre: Tensor, da: Tensor, 
     _expect(pre, (M, N), "f32", "pre")
     _expect(da, (M, N), "bf16", "da")
     _expect(da_t, (N, M), "bf16", "da_t")
-    call("vdsl_op_gemm_bf16_gelu_bwd", q.handle, M, N, K, A.handle, B.handle, pre.handle, da.handle, _h(da_t))
+    call("vdsl_op_gemm_bf16_gelu_bwd_packed" if packed else "vdsl_op_gemm_bf16_gelu_bwd", q.handle, M, N, K, A.handle,
+         B.handle, pre.handle, da.handle, _h(da_t))
 
 
 def mse_partials_count(rows, cols) -> int:
