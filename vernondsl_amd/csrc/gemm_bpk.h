@@ -15,10 +15,14 @@
 // the copies of both operands when both go through LDS.
 //
 // Pipeline, per 128-byte K stage t (ring of NS = PD+1 LDS slots for A and PD+1 register sets for
-// B): the wave issues its B loads and A copies for stage t+PD, reads A fragments two k-steps ahead
-// of the MFMAs, and before the MFMAs of k-step 2 waits (vmcnt) for its own loads of stage t+1 and
-// meets the block barrier.  The loop body is unrolled over the PD+1 stages of the ring so every
-// register-set index is a constant; the stage count of a launch must be a multiple of PD+1.
+// B): the wave reads A fragments two k-steps ahead of the MFMAs, issues its B loads for stage t+PD
+// during k-steps 0-1 and its A copies for stage t+PD during k-steps 2-3, each spread evenly between
+// MFMAs, and before the MFMAs of k-step 2 waits (vmcnt) for its own loads of stage t+1 and meets
+// the block barrier.  Spreading matters: with the stage's 12 loads and copies issued back to back
+// the address unit backs up and stalls the wave's MFMA issue (2048x4096x4096 bf16: 60-62 us
+// against 56-57 spread over the four k-steps).  The loop body is unrolled over the PD+1 stages of
+// the ring so every register-set index is a constant; the stage count of a launch must be a
+// multiple of PD+1.
 // Rows of A past M are clamped to the last row and fragments of B past N to the last unit (their
 // products only reach outputs that are not stored).
 //
@@ -58,6 +62,24 @@ template <int N>
 __device__ __forceinline__ void bpk_wait_vm() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
+// Orders one k-step's instructions: one MFMA, the D fragment reads (LDS), then the other NM - 1
+// MFMAs with V vector-memory instructions spread evenly between them (sched_group_barrier masks:
+// 0x008 MFMA, 0x100 DS read, 0x020 VMEM read).  The MFMA ahead of the reads works on fragments
+// read earlier, so the wait the compiler puts before it covers only those older reads.
+template <int NM, int D, int V>
+__device__ __forceinline__ void bpk_sched_kstep() {
+  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  if constexpr (D > 0) __builtin_amdgcn_sched_group_barrier(0x100, D, 0);
+#pragma unroll
+  for (int i = 0; i < NM - 1; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+    for (int v = i * V / (NM - 1); v < (i + 1) * V / (NM - 1); ++v) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+  }
+  if constexpr (NM == 1 && V > 0) __builtin_amdgcn_sched_group_barrier(0x020, V, 0);
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // K loop over bytes [kb_begin, kb_end) of the tile at (m0, n0): ((kb_end - kb_begin) / 128) must
@@ -104,15 +126,16 @@ __device__ __forceinline__ void bpk_mainloop(const char* __restrict__ A, const c
   Frag af[4][FM];
   const int nk = (kb_end - kb_begin) / Cfg::BKB;
 
-#define VDSL_BPK_LOAD_B(SET, ST)                                                                 \
+  // B fragment loads of k-steps [K0, K1) and A copies [U0, U1) of stage ST.
+#define VDSL_BPK_LOAD_B(SET, ST, K0, K1)                                                         \
   do {                                                                                           \
-    _Pragma("unroll") for (int kk = 0; kk < KS; ++kk)                                            \
+    _Pragma("unroll") for (int kk = (K0); kk < (K1); ++kk)                                       \
       _Pragma("unroll") for (int j = 0; j < FN; ++j)                                             \
         bq[SET][kk][j] = *reinterpret_cast<const Frag*>(bsrc[j] + static_cast<size_t>((ST) * KS + kk) * 1024); \
   } while (0)
-#define VDSL_BPK_COPY_A(SLOT, ST)                                                                \
+#define VDSL_BPK_COPY_A(SLOT, ST, U0, U1)                                                        \
   do {                                                                                           \
-    _Pragma("unroll") for (int u = 0; u < CPW; ++u)                                              \
+    _Pragma("unroll") for (int u = (U0); u < (U1); ++u)                                          \
       lds_copy16(asrc[u] + (ST) * Cfg::BKB, smem + (SLOT) * STAGE + adst[u]);                    \
   } while (0)
 #define VDSL_BPK_READ_A(DST, SLOT, KK)                                                           \
@@ -135,8 +158,8 @@ __device__ __forceinline__ void bpk_mainloop(const char* __restrict__ A, const c
 #pragma unroll
   for (int s = 0; s < PD; ++s) {
     const int st = min(s, nk - 1);
-    VDSL_BPK_LOAD_B(s, st);
-    VDSL_BPK_COPY_A(s, st);
+    VDSL_BPK_LOAD_B(s, st, 0, KS);
+    VDSL_BPK_COPY_A(s, st, 0, CPW);
   }
   __builtin_amdgcn_sched_barrier(0);
   bpk_wait_vm<(PD - 1) * Cfg::VPS>();
@@ -146,6 +169,7 @@ __device__ __forceinline__ void bpk_mainloop(const char* __restrict__ A, const c
 
   // do-while: the launch guarantees nk >= NR, and a loop guard here would let the compiler sink
   // the prologue's B loads below the barrier into the guarded block.
+  constexpr int NM = FM * FN, HB = KS / 2, HC = CPW / 2;
   int kt = 0;
   do {
 #pragma unroll
@@ -156,47 +180,26 @@ __device__ __forceinline__ void bpk_mainloop(const char* __restrict__ A, const c
       __builtin_amdgcn_sched_barrier(0);
       VDSL_BPK_READ_A(af[2], s, 2);
       VDSL_BPK_MMA(af[0], s, 0);
-      VDSL_BPK_LOAD_B(pslot, pst);
-      VDSL_BPK_COPY_A(pslot, pst);
-      // k-step 0: the reads of k-step 2, then the stage's loads and copies spread between MFMAs
-      // (sched_group_barrier masks: 0x100 DS read, 0x008 MFMA, 0x020 VMEM).
-      {
-        // One MFMA (on fragments read in the previous stage) ahead of the reads: the wait the
-        // compiler puts before it then covers only those older reads, not the new ones.
-        constexpr int pairs = Cfg::VPS < FM * FN - 1 ? Cfg::VPS : FM * FN - 1;
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);
-#pragma unroll
-        for (int v = 0; v < pairs; ++v) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        }
-        if constexpr (Cfg::VPS > pairs) __builtin_amdgcn_sched_group_barrier(0x020, Cfg::VPS - pairs, 0);
-        if constexpr (FM * FN - 1 > pairs) __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - 1 - pairs, 0);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      VDSL_BPK_LOAD_B(pslot, pst, 0, HB);
+      bpk_sched_kstep<NM, FM, HB * FN>();
       VDSL_BPK_READ_A(af[3], s, 3);
       VDSL_BPK_MMA(af[1], s, 1);
-      __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      // This wave's loads of stage kt+s+1 have landed once at most (PD-1) stages' worth of later
-      // loads are outstanding; after the barrier every wave's A copies of that stage have.
-      bpk_wait_vm<(PD - 1) * Cfg::VPS>();
+      VDSL_BPK_LOAD_B(pslot, pst, HB, KS);
+      bpk_sched_kstep<NM, FM, (KS - HB) * FN>();
+      // This wave's loads of stage kt+s+1 have landed once only later ones are outstanding: the
+      // B loads and A copies of stages kt+s+2 .. kt+s+PD-1 and the B loads of stage kt+s+PD (its
+      // A copies follow below).  After the barrier every wave's A copies of that stage have too.
+      bpk_wait_vm<(PD - 2) * Cfg::VPS + Cfg::BPW>();
       dma_barrier();
       __builtin_amdgcn_sched_barrier(0);
       VDSL_BPK_READ_A(af[0], nslot, 0);
       VDSL_BPK_MMA(af[2], s, 2);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - 1, 0);
-      __builtin_amdgcn_sched_barrier(0);
+      VDSL_BPK_COPY_A(pslot, pst, 0, HC);
+      bpk_sched_kstep<NM, FM, HC>();
       VDSL_BPK_READ_A(af[1], nslot, 1);
       VDSL_BPK_MMA(af[3], s, 3);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - 1, 0);
-      __builtin_amdgcn_sched_barrier(0);
+      VDSL_BPK_COPY_A(pslot, pst, HC, CPW);
+      bpk_sched_kstep<NM, FM, CPW - HC>();
     }
     kt += NR;
   } while (kt < nk);
