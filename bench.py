@@ -533,7 +533,7 @@ def main():
         "parity": head["parity"],
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(head["gbs"] / PEAK_HBM_GBS, 4), "traffic": measured_traffic("map_chain"),
-                     "kernel": "map_chain_kernel<ProgTanhExpBias,4,4>"},
+                     "kernel": "map_chain_kernel<ProgTanhExpBias,4,2,int32_t>"},
         "cpu_baseline": head.get("cpu"),
         "device": {"name": info["name"], "arch": info["arch"], "compute_units": info["compute_units"]},
         "per_config": per_config,

@@ -127,10 +127,11 @@ struct Vec<1> {
   __device__ static __forceinline__ T from(const float (&o)[1]) { return o[0]; }
 };
 
-// Loads input k for a VEC-wide element group at (row, col).
-template <int VEC>
-__device__ __forceinline__ void load_input(const float* __restrict__ p, int bcast, int64_t row, int64_t col,
-                                           int64_t cols, float (&o)[VEC]) {
+// Loads input k for a VEC-wide element group at (row, col).  IDX is the index type of the launch
+// (32-bit whenever every element offset fits, which saves the 64-bit address arithmetic).
+template <int VEC, class IDX>
+__device__ __forceinline__ void load_input(const float* __restrict__ p, int bcast, IDX row, IDX col, IDX cols,
+                                           float (&o)[VEC]) {
   using V = Vec<VEC>;
   if (bcast == VDSL_BCAST_FULL) {
     // Streamed once: a nontemporal load keeps it from displacing reused data (the broadcast
@@ -149,6 +150,9 @@ __device__ __forceinline__ void load_input(const float* __restrict__ p, int bcas
     for (int k = 0; k < VEC; ++k) o[k] = s;
   }
 }
+
+// Inputs whose value does not depend on the row (broadcast along rows, or a scalar).
+__device__ __forceinline__ bool row_invariant(int bcast) { return bcast == VDSL_BCAST_ROW || bcast == VDSL_BCAST_SCALAR; }
 
 template <class P, int VEC, int PC>
 __device__ __forceinline__ void fixed_step(const MapProg& rt, const float (&in)[VDSL_MAP_MAX_INPUTS][VEC],
@@ -200,11 +204,57 @@ __device__ __forceinline__ int input_bcast(const MapIn& in, int k) {
   else return P::bcast_of(k);
 }
 
-template <class P, int VEC, int R>
-__global__ __launch_bounds__(256) void map_chain_kernel(MapProg rt, MapIn in, float* __restrict__ out, int64_t rows,
-                                                        int64_t cols) {
-  using V = Vec<VEC>;
-  const int64_t col = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * VEC;
+// R rows of one thread's column group: every row's loads, then each row's program and store.
+// GUARD: rows past `rows` are skipped (the last, partial group of a launch).
+template <class P, int VEC, int R, bool GUARD, class IDX>
+__device__ __forceinline__ void map_chain_rows(const MapProg& rt, const MapIn& in, float* __restrict__ out, IDX rows, IDX cols,
+                                               IDX row0, IDX col, int n_in, int out_reg,
+                                               const float (&vfix)[VDSL_MAP_MAX_INPUTS][VEC]) {
+  float vin[R][VDSL_MAP_MAX_INPUTS][VEC];
+#pragma unroll
+  for (int u = 0; u < R; ++u) {
+    const IDX row = row0 + u;
+    if (!GUARD || row < rows) {
+#pragma unroll
+      for (int k = 0; k < VDSL_MAP_MAX_INPUTS; ++k) {
+        if (k < n_in) {
+          const int bc = input_bcast<P>(in, k);
+          if (row_invariant(bc)) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) vin[u][k][e] = vfix[k][e];
+          } else {
+            load_input<VEC, IDX>(in.p[k], bc, row, col, cols, vin[u][k]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < R; ++u) {
+    const IDX row = row0 + u;
+    if (!GUARD || row < rows) {
+      float r[VDSL_MAP_MAX_REGS][VEC];
+#pragma unroll
+      for (int g = 0; g < VDSL_MAP_MAX_REGS; ++g)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) r[g][k] = 0.0f;
+      run_program<P, VEC>(rt, vin[u], r);
+      if constexpr (VEC == 4) {
+        const f32x4 v = {r[out_reg][0], r[out_reg][1], r[out_reg][2], r[out_reg][3]};
+        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(out + row * cols + col));
+      } else {
+        __builtin_nontemporal_store(r[out_reg][0], out + row * cols + col);
+      }
+    }
+  }
+}
+
+// One thread per VEC-wide column group; the block's threads cover 256 VEC columns and step over R
+// rows at a time (all R rows' loads issued before any compute).  Row-invariant inputs are loaded
+// once per thread, not once per row.
+template <class P, int VEC, int R, class IDX>
+__global__ __launch_bounds__(256) void map_chain_kernel(MapProg rt, MapIn in, float* __restrict__ out, IDX rows, IDX cols) {
+  const IDX col = (static_cast<IDX>(blockIdx.x) * 256 + static_cast<IDX>(threadIdx.x)) * VEC;
   if (col >= cols) return;
   int n_in, out_reg;
   if constexpr (std::is_same<P, GenericProgram>::value) {
@@ -214,40 +264,20 @@ __global__ __launch_bounds__(256) void map_chain_kernel(MapProg rt, MapIn in, fl
     n_in = P::n_inputs;
     out_reg = P::out_reg;
   }
+  float vfix[VDSL_MAP_MAX_INPUTS][VEC];
+#pragma unroll
+  for (int k = 0; k < VDSL_MAP_MAX_INPUTS; ++k) {
+    if (k < n_in) {
+      const int bc = input_bcast<P>(in, k);
+      if (row_invariant(bc)) load_input<VEC, IDX>(in.p[k], bc, IDX(0), col, cols, vfix[k]);
+    }
+  }
 
-  for (int64_t row0 = static_cast<int64_t>(blockIdx.y) * R; row0 < rows; row0 += static_cast<int64_t>(gridDim.y) * R) {
-    float vin[R][VDSL_MAP_MAX_INPUTS][VEC];
-#pragma unroll
-    for (int u = 0; u < R; ++u) {
-      const int64_t row = row0 + u;
-      if (row < rows) {
-#pragma unroll
-        for (int k = 0; k < VDSL_MAP_MAX_INPUTS; ++k) {
-          if (k < n_in) {
-            const int bc = input_bcast<P>(in, k);
-            load_input<VEC>(in.p[k], bc, row, col, cols, vin[u][k]);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < R; ++u) {
-      const int64_t row = row0 + u;
-      if (row < rows) {
-        float r[VDSL_MAP_MAX_REGS][VEC];
-#pragma unroll
-        for (int g = 0; g < VDSL_MAP_MAX_REGS; ++g)
-#pragma unroll
-          for (int k = 0; k < VEC; ++k) r[g][k] = 0.0f;
-        run_program<P, VEC>(rt, vin[u], r);
-        if constexpr (VEC == 4) {
-          const f32x4 v = {r[out_reg][0], r[out_reg][1], r[out_reg][2], r[out_reg][3]};
-          __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(out + row * cols + col));
-        } else {
-          __builtin_nontemporal_store(r[out_reg][0], out + row * cols + col);
-        }
-      }
-    }
+  for (IDX row0 = static_cast<IDX>(blockIdx.y) * R; row0 < rows; row0 += static_cast<IDX>(gridDim.y) * R) {
+    // A whole group of R rows takes the path without per-row guards: with them the compiler
+    // waits for every row's loads before computing the first row.
+    if (row0 + R <= rows) map_chain_rows<P, VEC, R, false>(rt, in, out, rows, cols, row0, col, n_in, out_reg, vfix);
+    else map_chain_rows<P, VEC, R, true>(rt, in, out, rows, cols, row0, col, n_in, out_reg, vfix);
   }
 }
 
@@ -279,6 +309,8 @@ bool matches(const MapProg& rt, const MapIn& in) {
   return true;
 }
 
+// 32-bit indices when every offset the kernel forms (row * cols + col, and row0 plus a grid's
+// worth of rows) stays far below 2^31.
 template <class P, int VEC, int R>
 int launch(const MapProg& rt, const MapIn& in, float* out, int64_t rows, int64_t cols, hipStream_t s) {
   const int64_t slots = (cols + VEC - 1) / VEC;
@@ -286,8 +318,12 @@ int launch(const MapProg& rt, const MapIn& in, float* out, int64_t rows, int64_t
   int64_t gy = (rows + R - 1) / R;
   if (gy > 65535) gy = 65535;
   if (gx > 0x7fffffff) return fail(VDSL_ERR_UNSUPPORTED, "map chain: cols too large");
-  hipLaunchKernelGGL((map_chain_kernel<P, VEC, R>), dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)), dim3(256),
-                     0, s, rt, in, out, rows, cols);
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+  if (rows * (cols + 256 * VEC) <= (int64_t{1} << 30) && rows <= (int64_t{1} << 30))
+    hipLaunchKernelGGL((map_chain_kernel<P, VEC, R, int32_t>), grid, dim3(256), 0, s, rt, in, out, static_cast<int32_t>(rows),
+                       static_cast<int32_t>(cols));
+  else
+    hipLaunchKernelGGL((map_chain_kernel<P, VEC, R, int64_t>), grid, dim3(256), 0, s, rt, in, out, rows, cols);
   return check_launch("map_chain_kernel");
 }
 
@@ -337,7 +373,7 @@ extern "C" int vdsl_op_map_chain(vdsl_queue q, int64_t rows, int64_t cols, const
   float* o = static_cast<float*>(out->ptr);
   // 16-byte vectors need cols % 4 == 0 and 16-byte aligned bases (hipMalloc gives 256).
   const bool vec4 = (cols % 4) == 0;
-  if (vec4 && matches<ProgTanhExpBias>(rt, in)) return launch<ProgTanhExpBias, 4, 4>(rt, in, o, rows, cols, q->stream);
+  if (vec4 && matches<ProgTanhExpBias>(rt, in)) return launch<ProgTanhExpBias, 4, 2>(rt, in, o, rows, cols, q->stream);
   if (vec4) return launch<GenericProgram, 4, 1>(rt, in, o, rows, cols, q->stream);
   return launch<GenericProgram, 1, 1>(rt, in, o, rows, cols, q->stream);
 }
