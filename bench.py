@@ -366,8 +366,8 @@ def _traffic_kernels():
     return {
         "copy": ("copyBuffer", 2 * (512 << 20)),
         "map_chain": ("map_chain_kernel", spec.map_chain_bytes(8192, 8192)),
-        "softmax_f32": ("row_softmax_resident<0", spec.softmax_bytes(16384, 4096, _lib.F32)),
-        "softmax_bf16": ("row_softmax_resident<1", spec.softmax_bytes(16384, 4096, _lib.BF16)),
+        "softmax_f32": ("row_softmax_split<0", spec.softmax_bytes(16384, 4096, _lib.F32)),
+        "softmax_bf16": ("row_softmax_split<1", spec.softmax_bytes(16384, 4096, _lib.BF16)),
         # A, B read once; bf16 H and f32 pre-activation written once
         "gemm_bf16": ("gemm_bf16_", 2 * (2048 * 4096 + 4096 * 4096 + 2048 * 4096) + 4 * 2048 * 4096),
         # int8 A, B and the two scale vectors read once; bf16 Y written once

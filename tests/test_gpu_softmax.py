@@ -41,10 +41,12 @@ def check(xh, got, ref, bf16):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
-@pytest.mark.parametrize("cols", [4096, 256, 512, 1000, 8192, 3])
+@pytest.mark.parametrize("cols", [4096, 256, 512, 1000, 2048, 8192, 16384, 3])
 @pytest.mark.parametrize("rows", [130, 160])
 def test_softmax_shapes(dev, q, cols, bf16, rows):
-    """Row counts that fill the last 4-row block partially (130) and exactly (160)."""
+    """Row counts that fill the last 4-row block partially (130) and exactly (160); widths that take
+    the one-wave-per-row kernel (256, 512), the one-block-per-row kernel with 1, 2 and 4 vectors per
+    lane (2048 f32, 4096, 8192, 16384 bf16) and the streaming kernel (1000, 3)."""
     x, _, _ = spec.softmax_inputs(rows=rows, cols=cols)
     xh = rng.f32_to_bf16(x) if bf16 else x
     got = run(dev, q, xh, "bf16" if bf16 else "f32")
