@@ -347,7 +347,7 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
            "eager_ms_per_step": eager_ms, "ops_per_step": ops,
            "parity": parity,
            "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                        "frac": gt / PEAK_INT8_TOPS, "kernel": "gemm_w8a8_bpk<64x256, 4 waves of 64x64, weights from packed fragments, loads 7 stages ahead> (dequant+ReLU) 512x8192x8192, weights cycling through the 3 layers", "kernel_ms": gms,
+                        "frac": gt / PEAK_INT8_TOPS, "kernel": "gemm_w8a8_bpk<128x128, 4 waves of 128x32, weights from packed fragments> (dequant+ReLU) 512x8192x8192, weights cycling through the 3 layers", "kernel_ms": gms,
                         "traffic": measured_traffic("gemm_w8a8")},
            "whole_graph_frac_of_peak": tops / PEAK_INT8_TOPS}
     if do_cpu:

@@ -2,8 +2,8 @@
 
 Bar: bit-exact.  The int32 accumulators and the dequantised outputs must equal the CPU oracle's
 (orc_gemm_w8a8 on the unpacked weights) and the row-major GPU kernel's, for shapes that take
-every launch plan: 128 x 256 blocks (large M), 64 x 256 blocks (config-5 layers), 64 x 256 blocks
-with K split eight ways (the 1024-wide last layer) and in other counts, and ragged M and N.  Calls
+every launch plan: 128 x 256 blocks (large M), 128 x 128 blocks (config-5 layers), 64 x 256
+blocks with K split eight ways (the 1024-wide last layer) and in other counts, and ragged M and N.  Calls
 in a row on one workspace (left holding the previous call's partials) must not depend on its
 contents.
 """
@@ -79,7 +79,9 @@ def test_pack_layout(dev, q):
                                            (130, 320, 2048, True, "bf16"),  # ragged M and N, split 4
                                            (256, 512, 1024, False, "f32"),  # split 2
                                            (1024, 8192, 512, True, "bf16"),  # 128x256 blocks
-                                           (1000, 8224, 512, False, "f32")])  # 128x256, ragged
+                                           (1000, 8224, 512, False, "f32"),  # 128x256, ragged
+                                           (500, 8224, 512, True, "bf16"),    # 128x128, ragged M and N
+                                           (512, 4096, 1024, False, "bf16")])  # 128x128, whole tiles
 def test_packed_vs_oracle(dev, q, M, N, K, relu, dt):
     xq, w, xs, ws = _operands(M, N, K, M * 7 + N + K)
     p = Packed(dev, q, M, N, K)
