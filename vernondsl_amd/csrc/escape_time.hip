@@ -145,12 +145,19 @@ float norm_threshold(float b) {
   return t;
 }
 
+// Unused dynamic LDS reserved per block to cap residency at 6 blocks (24 waves) per CU: 160 KiB
+// of LDS / 24 KiB.  Left at the register limit (8 blocks per CU) the waves of set-interior tiles
+// (256 trips) pile up to 8 deep on the SIMDs that took them first and finish last, at a fraction
+// of the issue rate; fewer than ~4 waves per SIMD cannot hide the z update's dependence chain.
+// Config 1: 6 blocks 18.6 us, 7 blocks 19.3, 8 (no cap) 19.9, 5 blocks 19.7, 3 or fewer 26.7.
+constexpr unsigned kEscLdsBytes = 24u << 10;
+
 template <int FAMILY, int TEST, int ROUNDING>
 int launch_out(const vdsl_escape_time_params& p, void* out, hipStream_t s, dim3 grid) {
   if (p.out_kind == VDSL_ESC_OUT_I32_COUNT)
-    hipLaunchKernelGGL((escape_time_kernel<FAMILY, TEST, ROUNDING, VDSL_ESC_OUT_I32_COUNT>), grid, dim3(256), 0, s, p, out);
+    hipLaunchKernelGGL((escape_time_kernel<FAMILY, TEST, ROUNDING, VDSL_ESC_OUT_I32_COUNT>), grid, dim3(256), kEscLdsBytes, s, p, out);
   else
-    hipLaunchKernelGGL((escape_time_kernel<FAMILY, TEST, ROUNDING, VDSL_ESC_OUT_F32_AFFINE>), grid, dim3(256), 0, s, p, out);
+    hipLaunchKernelGGL((escape_time_kernel<FAMILY, TEST, ROUNDING, VDSL_ESC_OUT_F32_AFFINE>), grid, dim3(256), kEscLdsBytes, s, p, out);
   return check_launch("escape_time_kernel");
 }
 
