@@ -104,6 +104,9 @@ def time_replays(q, dev, fn, steps, warmup, per_graph=1, warmup_ms=25.0):
     return ms / n, wall / n
 
 
+NOT_CHECKED = "not checked (--no-cpu: the oracle runs only in the CPU-baseline leg)"
+
+
 def time_cpu(fn, min_s=2.0, max_reps=5):
     fn()  # warm-up
     reps, t_total = 0, 0.0
@@ -131,18 +134,19 @@ def bench_map_chain(dev, q, steps, warmup, do_cpu):
                                max(1, warmup // per), per_graph=per)
     nbytes = spec.map_chain_bytes(rows, cols)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    # parity spot check of the benchmarked output
-    got = ty.numpy(q)
-    from oracle import oracle
-    parity = "ok"
-    for r in (0, 4097, rows - 1):
-        ref = oracle.map_chain(prog, [x, bias], rows, cols, row_range=(r, r + 1))[0]
-        u = ((np.float32(spec.MAP_A) * x[r]) + np.float32(spec.MAP_B)).astype(np.float64)
-        sc = np.abs(np.tanh(u) * np.exp(-(x[r].astype(np.float64) ** 2))) + np.abs(bias.astype(np.float64))
-        if not np.all(np.abs(got[r].astype(np.float64) - ref) <= 1e-5 * sc):
-            parity = f"FAIL row {r}"
-    res = {"ms": ms, "wall_ms": wall_ms, "gbs": gbs, "bytes": nbytes, "parity": parity}
+    res = {"ms": ms, "wall_ms": wall_ms, "gbs": gbs, "bytes": nbytes, "parity": NOT_CHECKED}
     if do_cpu:
+        # CPU-baseline leg: the oracle is timed on the full workload and, as the checker, its output
+        # on three rows is compared with the benchmarked GPU output.
+        from oracle import oracle
+        got = ty.numpy(q)
+        res["parity"] = "ok"
+        for r in (0, 4097, rows - 1):
+            ref = oracle.map_chain(prog, [x, bias], rows, cols, row_range=(r, r + 1))[0]
+            u = ((np.float32(spec.MAP_A) * x[r]) + np.float32(spec.MAP_B)).astype(np.float64)
+            sc = np.abs(np.tanh(u) * np.exp(-(x[r].astype(np.float64) ** 2))) + np.abs(bias.astype(np.float64))
+            if not np.all(np.abs(got[r].astype(np.float64) - ref) <= 1e-5 * sc):
+                res["parity"] = f"FAIL row {r}"
         t = time_cpu(lambda: oracle.map_chain(prog, [x, bias], rows, cols))
         res["cpu"] = {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": oracle.num_threads(), "kind": "port",
                       "sample": f"the full workload ([{rows}][{cols}] f32), {t:.3f} s per pass, oracle orc_map_chain"}
@@ -153,7 +157,6 @@ def bench_map_chain(dev, q, steps, warmup, do_cpu):
 
 # ---- config 1 ------------------------------------------------------------------------------------
 def bench_fractal(dev, q, steps, warmup, do_cpu):
-    from oracle import oracle
     from vernondsl_amd import kernels, spec
     from vernondsl_amd.rhi import Tensor
     params = spec.mandelbrot_params()
@@ -162,8 +165,11 @@ def bench_fractal(dev, q, steps, warmup, do_cpu):
     ms, wall_ms = time_replays(q, dev, lambda: kernels.escape_time(q, p, out), max(10, steps // 5), warmup, per_graph=20)
     got = out.numpy(q)
     total = int(got.sum(dtype=np.int64))
-    ref = oracle.escape_time(params)
-    parity = "ok" if np.array_equal(got, ref) else f"FAIL {int((got != ref).sum())} px"
+    parity = NOT_CHECKED
+    if do_cpu:  # CPU-baseline leg (timed below); its output is the checker
+        from oracle import oracle
+        ref = oracle.escape_time(params)
+        parity = "ok" if np.array_equal(got, ref) else f"FAIL {int((got != ref).sum())} px"
     gpix = total / (ms * 1e-3) / 1e9
     tflops = 8 * total / (ms * 1e-3) / 1e12
     res = {"config": 1, "workload": "Mandelbrot 1024x1024, max_iter 256, |z|^2>4, int32 counts (fma rounding form)",
@@ -181,7 +187,6 @@ def bench_fractal(dev, q, steps, warmup, do_cpu):
 
 # ---- config 3 ------------------------------------------------------------------------------------
 def bench_softmax(dev, q, steps, warmup, do_cpu):
-    from oracle import oracle
     from vernondsl_amd import kernels, rng, spec
     from vernondsl_amd.rhi import Tensor
     rows, cols = 16384, 4096
@@ -197,15 +202,18 @@ def bench_softmax(dev, q, steps, warmup, do_cpu):
         gbs = nbytes / (ms * 1e-3) / 1e9
         gm = tm.numpy(q)
         xf = x if dt == "f32" else rng.bf16_to_f32(xh)
-        ok = np.array_equal(gm, xf.max(axis=1))
-        r = 4097
-        rs, rm, rsm = oracle.row_reduce_softmax(xh, row_range=(r, r + 1))
-        got = tsm.numpy(q)[r]
-        a = got.astype(np.float64) if dt == "f32" else rng.bf16_to_f32(got).astype(np.float64)
-        b = rsm[0].astype(np.float64) if dt == "f32" else rng.bf16_to_f32(rsm[0]).astype(np.float64)
-        ok = ok and np.all(np.abs(a - b) <= (1e-5 if dt == "f32" else 1e-2) * np.abs(b) + 1e-38)
+        ok = np.array_equal(gm, xf.max(axis=1))  # row max is exact
+        if do_cpu:  # CPU-baseline leg (timed below): the oracle's softmax row as the checker
+            from oracle import oracle
+            r = 4097
+            rs, rm, rsm = oracle.row_reduce_softmax(xh, row_range=(r, r + 1))
+            got = tsm.numpy(q)[r]
+            a = got.astype(np.float64) if dt == "f32" else rng.bf16_to_f32(got).astype(np.float64)
+            b = rsm[0].astype(np.float64) if dt == "f32" else rng.bf16_to_f32(rsm[0]).astype(np.float64)
+            ok = ok and np.all(np.abs(a - b) <= (1e-5 if dt == "f32" else 1e-2) * np.abs(b) + 1e-38)
         res = {"config": 3, "workload": f"row sum/max/softmax [{rows}][{cols}] {dt}", "metric": "achieved HBM GB/s",
-               "value": gbs, "unit": "GB/s", "ms_per_launch": ms, "parity": "ok" if ok else "FAIL",
+               "value": gbs, "unit": "GB/s", "ms_per_launch": ms,
+               "parity": ("ok" if ok else "FAIL") if do_cpu else ("row max exact; softmax " + NOT_CHECKED if ok else "FAIL"),
                "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                             "frac": gbs / PEAK_HBM_GBS, "bytes_per_launch": nbytes,
                             "traffic": measured_traffic("softmax_" + dt)}}
@@ -223,7 +231,6 @@ def bench_softmax(dev, q, steps, warmup, do_cpu):
 
 # ---- config 4 ------------------------------------------------------------------------------------
 def bench_mlp(dev, q, steps, warmup, do_cpu):
-    from oracle import oracle
     from vernondsl_amd import _lib, graph, kernels, spec
     from vernondsl_amd.rhi import Event, Tensor
     B, D, Hd, O = 2048, 4096, 4096, 4096
@@ -270,7 +277,8 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
                         "frac": gt / PEAK_BF16_TFLOPS, "kernel": "gemm_bf16_bpk<128x256, 4 waves of 128x64, weights from packed fragments> (GELU, bf16 out, f32 pre) 2048x4096x4096",
                         "kernel_ms": gms, "traffic": measured_traffic("gemm_bf16")},
            "whole_graph_frac_of_peak": tflops / PEAK_BF16_TFLOPS}
-    if do_cpu:
+    if do_cpu:  # CPU-baseline leg
+        from oracle import oracle
         b = 64
         xs, ts_ = x[:b], t[:b]
         tc = time_cpu(lambda: oracle.mlp_train_step(xs, w1, w2, ts_), min_s=1.0, max_reps=2)
@@ -282,7 +290,6 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
 
 # ---- config 5 ------------------------------------------------------------------------------------
 def bench_w8a8(dev, q, steps, warmup, do_cpu):
-    from oracle import oracle
     from vernondsl_amd import graph, kernels, spec
     from vernondsl_amd.rhi import Event, Tensor
     B, widths = 512, spec.W8A8_WIDTHS
@@ -311,7 +318,10 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
     tops = ops / (ms * 1e-3) / 1e12
     got = exe.read(q, "Y")
     rows = np.array([0, 511])
-    parity = "ok" if np.array_equal(got[rows], oracle.w8a8_forward(x[rows], layers)) else "FAIL"
+    parity = NOT_CHECKED
+    if do_cpu:  # CPU-baseline leg (timed below): the oracle's forward of two rows as the checker
+        from oracle import oracle
+        parity = "ok" if np.array_equal(got[rows], oracle.w8a8_forward(x[rows], layers)) else "FAIL"
     step.destroy()
     exe.free()
     # dominant kernel: the 512x8192x8192 layer GEMM alone, on the config's input quantised as
@@ -492,7 +502,6 @@ def main():
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
-    from oracle import oracle
     from vernondsl_amd.rhi import Device, Queue
     dev = Device(0)
     q = Queue(dev)
