@@ -66,27 +66,42 @@ __global__ __launch_bounds__(256) void transpose_bf16_pairs(const uint32_t* __re
   }
 }
 
-// bf16, rows % 8 == 0 and cols % 8 == 0: a 64x64 tile per block; lane u loads source rows
+// bf16, rows % 8 == 0 and cols % 8 == 0: TPB 64x64 tiles per block; per tile lane u loads source rows
 // r0 + 2q, r0 + 2q + 1 (q = u / 8) at columns c0 + 8t .. + 7 (t = u % 8) with two 16-byte loads,
 // forms the 8 column pairs in registers and the tile leaves as 16-byte runs of the destination
 // rows (store_pair_tile_transposed).
+template <int TPB>
 __global__ __launch_bounds__(256) void transpose_bf16_vec(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
                                                           int64_t rows, int64_t cols) {
-  __shared__ __align__(16) uint32_t tile[kPairTileWords];
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  // TPB 64x64 tiles stacked along the source rows per block: every tile's loads are issued before
+  // any LDS write, so a thread has 2 TPB 16-byte loads in flight.
+  __shared__ __align__(16) uint32_t tile[TPB][kPairTileWords];
+  const int64_t rb = static_cast<int64_t>(blockIdx.y) * 64 * TPB, c0 = static_cast<int64_t>(blockIdx.x) * 64;
   const int q = static_cast<int>(threadIdx.x) >> 3, t = static_cast<int>(threadIdx.x) & 7;
-  if (r0 + 2 * q < rows && c0 + 8 * t < cols) {
-    const int64_t o = (r0 + 2 * q) * cols + c0 + 8 * t;
-    const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + o));
-    const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + o + cols));
+  u32x4 a[TPB], b[TPB];
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      tile[pair_slot(8 * t + 2 * h, q)] = (a[h] & 0xFFFFu) | (b[h] << 16);
-      tile[pair_slot(8 * t + 2 * h + 1, q)] = (a[h] >> 16) | (b[h] & 0xFFFF0000u);
+  for (int h = 0; h < TPB; ++h) {
+    const int64_t r0 = rb + 64 * h;
+    if (r0 + 2 * q < rows && c0 + 8 * t < cols) {
+      const int64_t o = (r0 + 2 * q) * cols + c0 + 8 * t;
+      a[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + o));
+      b[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + o + cols));
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < TPB; ++h) {
+    if (rb + 64 * h + 2 * q < rows && c0 + 8 * t < cols) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        tile[h][pair_slot(8 * t + 2 * e, q)] = (a[h][e] & 0xFFFFu) | (b[h][e] << 16);
+        tile[h][pair_slot(8 * t + 2 * e + 1, q)] = (a[h][e] >> 16) | (b[h][e] & 0xFFFF0000u);
+      }
     }
   }
   __syncthreads();
-  store_pair_tile_transposed(tile, dst, rows, cols, r0, c0);
+#pragma unroll
+  for (int h = 0; h < TPB; ++h)
+    if (rb + 64 * h < rows) store_pair_tile_transposed(tile[h], dst, rows, cols, rb + 64 * h, c0);
 }
 
 __global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* __restrict__ s, uint16_t* __restrict__ d, int64_t n) {
@@ -104,9 +119,9 @@ __global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __rest
 int launch_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int dtype, hipStream_t s) {
   if (rows == 0 || cols == 0) return VDSL_OK;
   if (dtype == VDSL_BF16 && rows % 8 == 0 && cols % 8 == 0) {
-    const int64_t bx = (cols + 63) / 64, by = (rows + 63) / 64;
+    const int64_t bx = (cols + 63) / 64, by = (rows + 127) / 128;
     if (bx > 0x7fffffff || by > 65535) return fail(VDSL_ERR_UNSUPPORTED, "transpose: tensor too large");
-    hipLaunchKernelGGL(transpose_bf16_vec, dim3(static_cast<unsigned>(bx), static_cast<unsigned>(by)), dim3(256), 0, s,
+    hipLaunchKernelGGL(transpose_bf16_vec<2>, dim3(static_cast<unsigned>(bx), static_cast<unsigned>(by)), dim3(256), 0, s,
                        static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), rows, cols);
     return check_launch("transpose_bf16_vec");
   }
