@@ -206,19 +206,21 @@ __global__ __launch_bounds__(256) void quantize_rows_vec(const void* __restrict_
   }
 }
 
-// Rows of exactly NV 16-byte vectors per lane (256 lanes): the row is read once and held in
-// registers across the block max, so it is never fetched twice (bf16 [512][8192]: NV = 4).
-template <int DT, int NV>
-__global__ __launch_bounds__(256) void quantize_rows_resident(const void* __restrict__ x, int8_t* __restrict__ q,
+// Rows of exactly NV 16-byte vectors per lane (BT lanes, one block per row): the row is read once
+// and held in registers across the block max, so it is never fetched twice.  With few rows (512
+// in config 5) the kernel is one load-reduce-store chain per block: 1024 lanes of one vector each
+// (bf16 [512][8192]: NV = 1) shorten it against 256 lanes of four (config-5 step ~1 us faster).
+template <int DT, int NV, int BT>
+__global__ __launch_bounds__(BT) void quantize_rows_resident(const void* __restrict__ x, int8_t* __restrict__ q,
                                                               float* __restrict__ scale) {
   constexpr int PV = DT == VDSL_F32 ? 4 : 8;
-  constexpr int64_t COLS = static_cast<int64_t>(NV) * 256 * PV;
-  __shared__ float wmax[4];
+  constexpr int64_t COLS = static_cast<int64_t>(NV) * BT * PV;
+  __shared__ float wmax[BT / 64];
   const int64_t row = blockIdx.x;
   const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const char*>(x) + row * COLS * (DT == VDSL_F32 ? 4 : 2));
   u32x4 v[NV];
 #pragma unroll
-  for (int k = 0; k < NV; ++k) v[k] = __builtin_nontemporal_load(src + threadIdx.x + 256 * k);
+  for (int k = 0; k < NV; ++k) v[k] = __builtin_nontemporal_load(src + threadIdx.x + BT * k);
   auto elem = [&](int k, int e) -> float {
     const uint32_t w = v[k][DT == VDSL_F32 ? e : e >> 1];
     if (DT == VDSL_F32) return __uint_as_float(w);
@@ -232,7 +234,9 @@ __global__ __launch_bounds__(256) void quantize_rows_resident(const void* __rest
   amax = wave_max(amax);
   if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
   __syncthreads();
-  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  amax = wmax[0];
+#pragma unroll
+  for (int w = 1; w < BT / 64; ++w) amax = fmaxf(amax, wmax[w]);
   const float s = amax / 127.0f;
   if (threadIdx.x == 0) scale[row] = s;
   int8_t* dst = q + row * COLS;
@@ -251,7 +255,7 @@ __global__ __launch_bounds__(256) void quantize_rows_resident(const void* __rest
       }
       packed[e / 4] |= (static_cast<uint32_t>(iv) & 0xFFu) << (8 * (e % 4));
     }
-    const int64_t vi = threadIdx.x + 256 * k;
+    const int64_t vi = threadIdx.x + BT * k;
     if (PV == 4) *reinterpret_cast<uint32_t*>(dst + vi * PV) = packed[0];
     else *reinterpret_cast<uint2*>(dst + vi * PV) = make_uint2(packed[0], packed[PV / 4 - 1]);
   }
@@ -609,16 +613,17 @@ extern "C" int vdsl_op_quantize_rows_i8(vdsl_queue q, int64_t rows, int64_t cols
   if (rows == 0) return VDSL_OK;
   const int pv = x_dtype == VDSL_F32 ? 4 : 8;
   if (rows <= 0x7fffffff && (cols == 256 * pv * 4 || cols == 256 * pv * 8)) {  // register-resident rows
-    const dim3 g(static_cast<unsigned>(rows)), b(256);
+    const dim3 g(static_cast<unsigned>(rows));
     auto* qp = static_cast<int8_t*>(qx->ptr);
     auto* sp = static_cast<float*>(scale->ptr);
     const bool nv4 = cols == 256 * pv * 4;
+    const dim3 b4(1024);
     if (x_dtype == VDSL_F32) {
-      if (nv4) hipLaunchKernelGGL((quantize_rows_resident<VDSL_F32, 4>), g, b, 0, q->stream, x->ptr, qp, sp);
-      else hipLaunchKernelGGL((quantize_rows_resident<VDSL_F32, 8>), g, b, 0, q->stream, x->ptr, qp, sp);
+      if (nv4) hipLaunchKernelGGL((quantize_rows_resident<VDSL_F32, 1, 1024>), g, b4, 0, q->stream, x->ptr, qp, sp);
+      else hipLaunchKernelGGL((quantize_rows_resident<VDSL_F32, 2, 1024>), g, b4, 0, q->stream, x->ptr, qp, sp);
     } else {
-      if (nv4) hipLaunchKernelGGL((quantize_rows_resident<VDSL_BF16, 4>), g, b, 0, q->stream, x->ptr, qp, sp);
-      else hipLaunchKernelGGL((quantize_rows_resident<VDSL_BF16, 8>), g, b, 0, q->stream, x->ptr, qp, sp);
+      if (nv4) hipLaunchKernelGGL((quantize_rows_resident<VDSL_BF16, 1, 1024>), g, b4, 0, q->stream, x->ptr, qp, sp);
+      else hipLaunchKernelGGL((quantize_rows_resident<VDSL_BF16, 2, 1024>), g, b4, 0, q->stream, x->ptr, qp, sp);
     }
     return check_launch("quantize_rows_resident");
   }
