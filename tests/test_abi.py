@@ -91,6 +91,12 @@ def test_workspace_queries_are_pure_host():
     assert n.value == (256 * 128 + 512 * 128) * 2
     assert L.vdsl_gemm_bf16_workspace_bytes(0, 1, -1, 2, 2, C.byref(n)) == -1
     assert L.vdsl_mse_partials_count(2048, 4096) > 0
+    # sizes that wrap size_t are errors, not small numbers
+    n.value = 123
+    assert L.vdsl_gemm_bf16_workspace_bytes(1, 0, 1 << 40, 1 << 40, 1 << 40, C.byref(n)) == -7
+    assert b"overflows" in L.vdsl_last_error() and n.value == 123
+    # a narrow output splits K into M x N int32 partials
+    assert L.vdsl_gemm_w8a8_workspace_bytes(64, 64, 4096, C.byref(n)) == 0 and n.value == 64 * 64 * 4
 
 
 def test_last_error_is_thread_local():

@@ -109,6 +109,38 @@ def test_mlp_rewritten_weights_reprepared(dev, q):
     exe.free()
 
 
+def test_mlp_weights_written_after_capture_reach_the_replay(dev, q):
+    """A param written after capture (a training loop's weight update): the captured step's next
+    launch re-derives the packed W1, W2, W2^T and packed W2^T first, so the replay equals the plain
+    graph's step on the new weights bit for bit; then again with the old weights restored."""
+    x, w1, w2, t = spec.mlp_inputs(batch=256, d_in=512, hidden=512, d_out=256)
+    w1b, w2b = np.ascontiguousarray(w1[:, ::-1]), np.ascontiguousarray(w2[::-1])
+    plain = {"prepare_transposes": False, "fuse_gelu_backward": False, "pack_weights": False}
+    ref_new = run_mlp(dev, q, x, w1b, w2b, t, replays=1, **plain)
+    ref_old = run_mlp(dev, q, x, w1, w2, t, replays=1, **plain)
+    g, _ = graph.mlp_train_graph(256, 512, 512, 256)
+    exe = g.compile(dev)
+    for name, arr in (("X", x), ("W1", w1), ("W2", w2), ("T", t)):
+        exe.write(q, name, arr)
+    step = exe.capture(q)
+    step.launch(q)
+    q.sync()
+    names = ("H", "Y", "loss", "grad_W1", "grad_W2")
+    for n in names:
+        assert np.array_equal(exe.read(q, n), ref_old[n]), n
+    for (a1, a2), ref in (((w1b, w2b), ref_new), ((w1, w2), ref_old)):
+        exe.write(q, "W1", a1)
+        exe.write(q, "W2", a2)
+        for n in names:
+            exe.t[n].buffer.fill_u32(q, 0x7FC07FC0)
+        step.launch(q)
+        q.sync()
+        for n in names:
+            assert np.array_equal(exe.read(q, n), ref[n]), n
+    step.destroy()
+    exe.free()
+
+
 def test_mlp_config4_full_size(dev, q):
     x, w1, w2, t = spec.mlp_inputs()
     got = run_mlp(dev, q, x, w1, w2, t, replays=2)

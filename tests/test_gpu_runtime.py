@@ -166,6 +166,38 @@ def test_op_output_too_small_is_a_shape_error(dev, q):
         out.free()
 
 
+def test_overflowing_extents_are_shape_errors_before_any_launch(dev, q):
+    """Extents whose byte size wraps size_t (rows * cols * element size >= 2^64) must be refused
+    by the host-side size check; a wrapped size would pass a small buffer and the kernel would
+    read past it.  Every call below returns before it enqueues anything."""
+    b = Buffer(dev, 4096)
+    try:
+        h = b.handle
+        big = 1 << 62                      # x 4 bytes = 2^64
+        cases = [
+            ("vdsl_op_row_reduce_softmax", q.handle, 1, big, _lib.F32, h, None, None, None),
+            ("vdsl_op_col_reduce", q.handle, big, 1, _lib.F32, h, None, None),
+            ("vdsl_op_transpose", q.handle, big, 2, _lib.BF16, h, b.handle),
+            ("vdsl_op_cast", q.handle, big, _lib.F32, h, _lib.BF16, h),
+            ("vdsl_op_gelu_fwd", q.handle, big, _lib.F32, h, _lib.F32, h),
+            ("vdsl_op_gelu_bwd", q.handle, 1 << 40, 1 << 40, h, h, h, None),
+            ("vdsl_op_mse_fwd_bwd", q.handle, 1 << 40, 1 << 40, h, h, h, None, None, h),
+            ("vdsl_op_quantize_rows_i8", q.handle, 1, big, _lib.F32, h, h, h),
+        ]
+        for fn, *args in cases:
+            st, msg = status(fn, *args)
+            assert st == SHAPE and "overflows" in msg, (fn, st, msg)
+        # the map chain sizes its output from rows * cols
+        prog = (_lib.MapInstr * 1)()
+        prog[0].op, prog[0].dst = _lib.MAP_OPS["const"], 0
+        st, msg = status("vdsl_op_map_chain", q.handle, 1 << 40, 1 << 40, prog, 1, None, 0, 0, h)
+        assert st == SHAPE and "overflows" in msg, msg
+        st, msg = status("vdsl_op_map_chain", q.handle, -1, 4, prog, 1, None, 0, 0, h)
+        assert st == INVALID_ARG
+    finally:
+        b.free()
+
+
 def test_stale_and_double_freed_handles(dev, q):
     b = Buffer(dev, 64)
     h = C.c_void_p(b.handle.value)

@@ -29,10 +29,16 @@ def test_mandelbrot_program_equals_known_answers(dev, q):
 
 
 def test_julia_program_frames_match_oracle(dev, q):
-    res, img = run_program(os.path.join(EX, "julia_orbit.py"), 3)
-    assert res["frames"] == 3
-    _, p = tc.lower_source(open(os.path.join(EX, "julia_orbit.py")).read(), "frame", {"phase": 2 * 0.05})
+    res, img = run_program(os.path.join(EX, "rabbit_drift.py"), 3)
+    assert res["frames"] == 3 and img.shape == (512, 512) and img.dtype == np.float32
+    angle = 0.0
+    for _ in range(2):  # the program's own accumulation: the third frame is drawn at 0.0 + 0.1 + 0.1
+        angle += 0.1
+    _, p = tc.lower_source(open(os.path.join(EX, "rabbit_drift.py")).read(), "draw", {"angle": angle})
     assert np.array_equal(img, oracle.escape_time(p))
+    # every shade is 1 - k/128 for a count k in [0, 128]
+    k = (1.0 - img.astype(np.float64)) * 128
+    assert np.array_equal(k, np.round(k)) and k.min() >= 1 and k.max() == 128
 
 
 def test_bindings_allocate_device_buffers(dev, q):

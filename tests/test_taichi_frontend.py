@@ -38,13 +38,17 @@ def test_mandelbrot_example_lowers_to_config1_separate_form():
 
 
 def test_julia_example_lowering():
-    fld, p = tc.lower_source(open(os.path.join(EX, "julia_orbit.py")).read(), "frame", {"phase": 0.5})
-    assert fld.shape == (400, 300)
-    assert p["family"] == _lib.ESC_JULIA and p["escape_test"] == _lib.ESC_NORM_GE and p["bound"] == 8.0
-    assert p["max_iter"] == 96 and p["out_kind"] == _lib.ESC_OUT_F32_AFFINE
-    assert np.float32(p["c_im"]) == np.float32(np.sin(np.float32(0.5), dtype=np.float32) * np.float32(0.3842))
-    assert np.float32(p["re_off"]) == -np.float32(0.6667) and p["re_den"] == 300.0 and p["re_scale"] == 3.0
-    assert np.float32(p["out_base"]) == np.float32(0.05) and np.float32(p["out_scale"]) == np.float32(0.01)
+    fld, p = tc.lower_source(open(os.path.join(EX, "rabbit_drift.py")).read(), "draw", {"angle": 0.5})
+    assert fld.shape == (512, 512) and fld.dtype == "f32"
+    assert p["family"] == _lib.ESC_JULIA and p["escape_test"] == _lib.ESC_MAG2_GT and p["bound"] == 16.0
+    assert p["max_iter"] == 128 and p["out_kind"] == _lib.ESC_OUT_F32_AFFINE
+    a = np.float32(0.5)
+    assert np.float32(p["c_re"]) == np.float32(-0.1226) + np.float32(0.05) * np.cos(a, dtype=np.float32)
+    assert np.float32(p["c_im"]) == np.float32(0.7449) + np.float32(0.05) * np.sin(a, dtype=np.float32)
+    for ax in ("re", "im"):
+        assert p[f"{ax}_den"] == 512.0 and p[f"{ax}_off"] == 0.0
+        assert np.float32(p[f"{ax}_scale"]) == np.float32(3.2) and np.float32(p[f"{ax}_post"]) == -np.float32(1.6)
+    assert p["out_base"] == 1.0 and p["out_scale"] == -1.0 / 128
 
 
 PROG = '''

@@ -241,11 +241,11 @@ extern "C" int vdsl_op_gelu_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_b
                                 vdsl_buffer da_t) {
   VDSL_TRY(enter_queue(q));
   if (rows < 0 || cols < 0) return fail(VDSL_ERR_INVALID_ARG, "negative shape");
-  const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols);
-  VDSL_TRY(check_buffer(q, dh, n * 4, "dh", false));
-  VDSL_TRY(check_buffer(q, pre, n * 4, "pre", false));
-  VDSL_TRY(check_buffer(q, da, n * 2, "da", true));
-  if (da_t) VDSL_TRY(check_buffer(q, da_t, n * 2, "da_t", true));
+  VDSL_TRY(check_buffer(q, dh, nbytes(rows, cols, 4), "dh", false));
+  VDSL_TRY(check_buffer(q, pre, nbytes(rows, cols, 4), "pre", false));
+  VDSL_TRY(check_buffer(q, da, nbytes(rows, cols, 2), "da", true));
+  if (da_t) VDSL_TRY(check_buffer(q, da_t, nbytes(rows, cols, 2), "da_t", true));
+  const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols);  // fits: checked above
   if (n == 0) return VDSL_OK;
   const int64_t gx = (cols + 63) / 64, gy = (rows + 63) / 64;
   if (gy > 65535 || gx > 0x7fffffff) return fail(VDSL_ERR_UNSUPPORTED, "gelu_bwd: tensor too large");
@@ -288,8 +288,8 @@ extern "C" int vdsl_op_gelu_fwd(vdsl_queue q, int64_t n, int32_t x_dtype, vdsl_b
   if (n < 0) return fail(VDSL_ERR_INVALID_ARG, "negative element count");
   const bool ok = (x_dtype == VDSL_F32 || x_dtype == VDSL_BF16) && (y_dtype == VDSL_F32 || y_dtype == VDSL_BF16);
   if (!ok) return fail(VDSL_ERR_UNSUPPORTED, "gelu_fwd supports f32 and bf16");
-  VDSL_TRY(check_buffer(q, x, static_cast<size_t>(n) * dtype_size(x_dtype), "x", false));
-  VDSL_TRY(check_buffer(q, y, static_cast<size_t>(n) * dtype_size(y_dtype), "y", true));
+  VDSL_TRY(check_buffer(q, x, nbytes(n, dtype_size(x_dtype)), "x", false));
+  VDSL_TRY(check_buffer(q, y, nbytes(n, dtype_size(y_dtype)), "y", true));
   if (x == y && x_dtype != y_dtype) return fail(VDSL_ERR_INVALID_ARG, "in-place gelu_fwd needs one dtype");
   if (n == 0) return VDSL_OK;
   const int64_t blocks = std::min<int64_t>((n + 255) / 256, 256 * 32);
@@ -305,14 +305,14 @@ extern "C" int vdsl_op_mse_fwd_bwd(vdsl_queue q, int64_t rows, int64_t cols, vds
                                    vdsl_buffer dy, vdsl_buffer dy_t, vdsl_buffer partials) {
   VDSL_TRY(enter_queue(q));
   if (rows <= 0 || cols <= 0) return fail(VDSL_ERR_INVALID_ARG, "MSE needs a non-empty tensor");
-  const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols);
-  VDSL_TRY(check_buffer(q, y, n * 4, "y", false));
-  VDSL_TRY(check_buffer(q, t, n * 4, "t", false));
+  VDSL_TRY(check_buffer(q, y, nbytes(rows, cols, 4), "y", false));
+  VDSL_TRY(check_buffer(q, t, nbytes(rows, cols, 4), "t", false));
   VDSL_TRY(check_buffer(q, loss, 4, "loss", true));
-  if (dy) VDSL_TRY(check_buffer(q, dy, n * 2, "dy", true));
-  if (dy_t) VDSL_TRY(check_buffer(q, dy_t, n * 2, "dy_t", true));
+  if (dy) VDSL_TRY(check_buffer(q, dy, nbytes(rows, cols, 2), "dy", true));
+  if (dy_t) VDSL_TRY(check_buffer(q, dy_t, nbytes(rows, cols, 2), "dy_t", true));
+  const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols);  // fits: checked above
   const int64_t np = tiles_of(rows, cols);
-  VDSL_TRY(check_buffer(q, partials, static_cast<size_t>(np) * 8, "partials", true));
+  VDSL_TRY(check_buffer(q, partials, nbytes(np, 8), "partials", true));
   const int64_t gx = (cols + 63) / 64, gy = (rows + 63) / 64;
   if (gy > 65535 || gx > 0x7fffffff) return fail(VDSL_ERR_UNSUPPORTED, "mse: tensor too large");
   const float scale = 2.0f / static_cast<float>(n);

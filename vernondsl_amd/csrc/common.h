@@ -74,6 +74,20 @@ int check_buffer(vdsl_queue q, vdsl_buffer b, size_t bytes, const char* name, bo
 
 size_t dtype_size(int dtype);
 
+// Byte size a * b * c of a dense operand, or kSizeOverflow when a factor is negative or the
+// product does not fit in size_t.  check_buffer rejects kSizeOverflow with VDSL_ERR_SHAPE, so an
+// entry point that sizes every operand with nbytes() fails before it enqueues anything instead of
+// accepting a wrapped (small) size and reading past an allocation.
+constexpr size_t kSizeOverflow = ~static_cast<size_t>(0);
+inline size_t nbytes(int64_t a, int64_t b, int64_t c = 1) {
+  if (a < 0 || b < 0 || c < 0) return kSizeOverflow;
+  size_t ab = 0, abc = 0;
+  if (__builtin_mul_overflow(static_cast<size_t>(a), static_cast<size_t>(b), &ab) ||
+      __builtin_mul_overflow(ab, static_cast<size_t>(c), &abc) || abc == kSizeOverflow)
+    return kSizeOverflow;
+  return abc;
+}
+
 }  // namespace vdsl
 
 #define VDSL_TRY(expr)              \

@@ -489,11 +489,11 @@ int launch_nt(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, 
   }
 }
 
+// kSizeOverflow when the re-layout copies' size does not fit size_t.
 size_t workspace_bytes(int ta, int tb, int64_t M, int64_t N, int64_t K) {
-  size_t b = 0;
-  if (ta) b += static_cast<size_t>(M) * K * 2;
-  if (!tb) b += static_cast<size_t>(N) * K * 2;
-  return b;
+  const size_t a = ta ? nbytes(M, K, 2) : 0, b = tb ? 0 : nbytes(N, K, 2);
+  if (a == kSizeOverflow || b == kSizeOverflow || a > kSizeOverflow - 1 - b) return kSizeOverflow;
+  return a + b;
 }
 
 }  // namespace
@@ -505,7 +505,9 @@ extern "C" int vdsl_gemm_bf16_workspace_bytes(int32_t trans_a, int32_t trans_b, 
                                               size_t* bytes) {
   if (!bytes) return fail(VDSL_ERR_INVALID_ARG, "bytes is null");
   if (M < 0 || N < 0 || K < 0) return fail(VDSL_ERR_INVALID_ARG, "negative GEMM extent");
-  *bytes = workspace_bytes(trans_a != 0, trans_b != 0, M, N, K);
+  const size_t ws = workspace_bytes(trans_a != 0, trans_b != 0, M, N, K);
+  if (ws == kSizeOverflow) return fail(VDSL_ERR_SHAPE, "GEMM workspace size overflows (extents too large)");
+  *bytes = ws;
   return VDSL_OK;
 }
 
@@ -518,10 +520,10 @@ extern "C" int vdsl_op_gemm_bf16(vdsl_queue q, int32_t trans_a, int32_t trans_b,
   if (c_dtype != VDSL_F32 && c_dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "C must be f32 or bf16");
   if (epilogue < VDSL_EPI_NONE || epilogue > VDSL_EPI_RELU) return fail(VDSL_ERR_INVALID_ARG, "unknown epilogue");
   const bool ta = trans_a != 0, tb = trans_b != 0;
-  VDSL_TRY(check_buffer(q, A, static_cast<size_t>(M) * K * 2, "A", false));
-  VDSL_TRY(check_buffer(q, B, static_cast<size_t>(N) * K * 2, "B", false));
-  VDSL_TRY(check_buffer(q, C, static_cast<size_t>(M) * N * dtype_size(c_dtype), "C", true));
-  if (pre_act) VDSL_TRY(check_buffer(q, pre_act, static_cast<size_t>(M) * N * 4, "pre_act", true));
+  VDSL_TRY(check_buffer(q, A, nbytes(M, K, 2), "A", false));
+  VDSL_TRY(check_buffer(q, B, nbytes(N, K, 2), "B", false));
+  VDSL_TRY(check_buffer(q, C, nbytes(M, N, dtype_size(c_dtype)), "C", true));
+  if (pre_act) VDSL_TRY(check_buffer(q, pre_act, nbytes(M, N, 4), "pre_act", true));
   const size_t ws = workspace_bytes(ta, tb, M, N, K);
   if (ws) VDSL_TRY(check_buffer(q, workspace, ws, "workspace", true));
   if (M == 0 || N == 0) return VDSL_OK;
@@ -554,11 +556,11 @@ extern "C" int vdsl_op_gemm_bf16_gelu_bwd(vdsl_queue q, int64_t M, int64_t N, in
   VDSL_TRY(enter_queue(q));
   if (M < 0 || N < 0 || K < 0) return fail(VDSL_ERR_INVALID_ARG, "negative GEMM extent");
   if (M > 0x7fffffff || N > 0x7fffffff || K > 0x3fffffff) return fail(VDSL_ERR_UNSUPPORTED, "GEMM extent too large");
-  VDSL_TRY(check_buffer(q, A, static_cast<size_t>(M) * K * 2, "A", false));
-  VDSL_TRY(check_buffer(q, B, static_cast<size_t>(N) * K * 2, "B", false));
-  VDSL_TRY(check_buffer(q, pre, static_cast<size_t>(M) * N * 4, "pre", false));
-  VDSL_TRY(check_buffer(q, da, static_cast<size_t>(M) * N * 2, "da", true));
-  if (da_t) VDSL_TRY(check_buffer(q, da_t, static_cast<size_t>(M) * N * 2, "da_t", true));
+  VDSL_TRY(check_buffer(q, A, nbytes(M, K, 2), "A", false));
+  VDSL_TRY(check_buffer(q, B, nbytes(N, K, 2), "B", false));
+  VDSL_TRY(check_buffer(q, pre, nbytes(M, N, 4), "pre", false));
+  VDSL_TRY(check_buffer(q, da, nbytes(M, N, 2), "da", true));
+  if (da_t) VDSL_TRY(check_buffer(q, da_t, nbytes(M, N, 2), "da_t", true));
   if (M == 0 || N == 0) return VDSL_OK;
   return launch_nt(static_cast<const uint16_t*>(A->ptr), static_cast<const uint16_t*>(B->ptr), da->ptr,
                    static_cast<float*>(pre->ptr), static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), kEpiGeluBwd,
@@ -569,7 +571,7 @@ extern "C" int vdsl_op_pack_bf16_weights(vdsl_queue q, int64_t N, int64_t K, vds
   VDSL_TRY(enter_queue(q));
   if (N < 0 || K < 0) return fail(VDSL_ERR_INVALID_ARG, "negative weight extent");
   if (N % 32 || K % 16) return fail(VDSL_ERR_UNSUPPORTED, "packed bf16 weights need N % 32 == 0 and K % 16 == 0");
-  const size_t n = static_cast<size_t>(N) * static_cast<size_t>(K) * 2;
+  const size_t n = nbytes(N, K, 2);
   VDSL_TRY(check_buffer(q, w, n, "w", false));
   VDSL_TRY(check_buffer(q, wp, n, "wp", true));
   if (w == wp) return fail(VDSL_ERR_INVALID_ARG, "w and wp must be different buffers");
@@ -590,10 +592,10 @@ extern "C" int vdsl_op_gemm_bf16_packed(vdsl_queue q, int64_t M, int64_t N, int6
   if ((2 * K) % (128 * Pb0::NR) || K == 0) return fail(VDSL_ERR_UNSUPPORTED, "packed bf16 GEMM needs K % 256 == 0 and K > 0");
   if (c_dtype != VDSL_F32 && c_dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "C must be f32 or bf16");
   if (epilogue < VDSL_EPI_NONE || epilogue > VDSL_EPI_RELU) return fail(VDSL_ERR_INVALID_ARG, "unknown epilogue");
-  VDSL_TRY(check_buffer(q, A, static_cast<size_t>(M) * K * 2, "A", false));
-  VDSL_TRY(check_buffer(q, Bp, static_cast<size_t>(N) * K * 2, "Bp", false));
-  VDSL_TRY(check_buffer(q, C, static_cast<size_t>(M) * N * dtype_size(c_dtype), "C", true));
-  if (pre_act) VDSL_TRY(check_buffer(q, pre_act, static_cast<size_t>(M) * N * 4, "pre_act", true));
+  VDSL_TRY(check_buffer(q, A, nbytes(M, K, 2), "A", false));
+  VDSL_TRY(check_buffer(q, Bp, nbytes(N, K, 2), "Bp", false));
+  VDSL_TRY(check_buffer(q, C, nbytes(M, N, dtype_size(c_dtype)), "C", true));
+  if (pre_act) VDSL_TRY(check_buffer(q, pre_act, nbytes(M, N, 4), "pre_act", true));
   if (M == 0 || N == 0) return VDSL_OK;
   const int64_t tiles = ((M + Pb0::BM - 1) / Pb0::BM) * ((N + Pb0::BN - 1) / Pb0::BN);
   hipLaunchKernelGGL((gemm_bf16_bpk<Pb0, false>), dim3(static_cast<unsigned>(tiles)), dim3(Pb0::NT), 0, q->stream,
@@ -610,11 +612,11 @@ extern "C" int vdsl_op_gemm_bf16_gelu_bwd_packed(vdsl_queue q, int64_t M, int64_
   if (M > 0x7fffffff || N > 0x7fffffff || K > 0x3fffffff) return fail(VDSL_ERR_UNSUPPORTED, "GEMM extent too large");
   if (N % 32) return fail(VDSL_ERR_UNSUPPORTED, "packed GEMM needs N % 32 == 0");
   if ((2 * K) % (128 * Pb0::NR) || K == 0) return fail(VDSL_ERR_UNSUPPORTED, "packed bf16 GEMM needs K % 256 == 0 and K > 0");
-  VDSL_TRY(check_buffer(q, A, static_cast<size_t>(M) * K * 2, "A", false));
-  VDSL_TRY(check_buffer(q, Bp, static_cast<size_t>(N) * K * 2, "Bp", false));
-  VDSL_TRY(check_buffer(q, pre, static_cast<size_t>(M) * N * 4, "pre", false));
-  VDSL_TRY(check_buffer(q, da, static_cast<size_t>(M) * N * 2, "da", true));
-  if (da_t) VDSL_TRY(check_buffer(q, da_t, static_cast<size_t>(M) * N * 2, "da_t", true));
+  VDSL_TRY(check_buffer(q, A, nbytes(M, K, 2), "A", false));
+  VDSL_TRY(check_buffer(q, Bp, nbytes(N, K, 2), "Bp", false));
+  VDSL_TRY(check_buffer(q, pre, nbytes(M, N, 4), "pre", false));
+  VDSL_TRY(check_buffer(q, da, nbytes(M, N, 2), "da", true));
+  if (da_t) VDSL_TRY(check_buffer(q, da_t, nbytes(M, N, 2), "da_t", true));
   if (M == 0 || N == 0) return VDSL_OK;
   const int64_t tiles = ((M + Pb0::BM - 1) / Pb0::BM) * ((N + Pb0::BN - 1) / Pb0::BN);
   hipLaunchKernelGGL((gemm_bf16_bpk<Pb0, true>), dim3(static_cast<unsigned>(tiles)), dim3(Pb0::NT), 0, q->stream,

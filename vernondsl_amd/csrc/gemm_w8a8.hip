@@ -606,10 +606,9 @@ extern "C" int vdsl_op_quantize_rows_i8(vdsl_queue q, int64_t rows, int64_t cols
   VDSL_TRY(enter_queue(q));
   if (rows < 0 || cols < 0) return fail(VDSL_ERR_INVALID_ARG, "negative shape");
   if (x_dtype != VDSL_F32 && x_dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "quantize input must be f32 or bf16");
-  const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols);
-  VDSL_TRY(check_buffer(q, x, n * dtype_size(x_dtype), "x", false));
-  VDSL_TRY(check_buffer(q, qx, n, "qx", true));
-  VDSL_TRY(check_buffer(q, scale, static_cast<size_t>(rows) * 4, "scale", true));
+  VDSL_TRY(check_buffer(q, x, nbytes(rows, cols, dtype_size(x_dtype)), "x", false));
+  VDSL_TRY(check_buffer(q, qx, nbytes(rows, cols), "qx", true));
+  VDSL_TRY(check_buffer(q, scale, nbytes(rows, 4), "scale", true));
   if (rows == 0) return VDSL_OK;
   const int pv = x_dtype == VDSL_F32 ? 4 : 8;
   if (rows <= 0x7fffffff && (cols == 256 * pv * 4 || cols == 256 * pv * 8)) {  // register-resident rows
@@ -649,7 +648,9 @@ extern "C" int vdsl_op_quantize_rows_i8(vdsl_queue q, int64_t rows, int64_t cols
 extern "C" int vdsl_gemm_w8a8_workspace_bytes(int64_t M, int64_t N, int64_t K, size_t* bytes) {
   if (!bytes) return fail(VDSL_ERR_INVALID_ARG, "bytes is null");
   if (M < 0 || N < 0 || K < 0) return fail(VDSL_ERR_INVALID_ARG, "negative GEMM extent");
-  *bytes = split_of(M, N, K) > 1 ? static_cast<size_t>(M) * static_cast<size_t>(N) * 4 : 0;
+  const size_t ws = split_of(M, N, K) > 1 ? nbytes(M, N, 4) : 0;
+  if (ws == kSizeOverflow) return fail(VDSL_ERR_SHAPE, "GEMM workspace size overflows (extents too large)");
+  *bytes = ws;
   return VDSL_OK;
 }
 
@@ -661,14 +662,14 @@ extern "C" int vdsl_op_gemm_w8a8(vdsl_queue q, int64_t M, int64_t N, int64_t K, 
   if (M > 0x7fffffff || N > 0x7fffffff || K > 133000) return fail(VDSL_ERR_UNSUPPORTED, "extent too large (K <= 133000 keeps int32 exact)");
   if (out_dtype != VDSL_F32 && out_dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "y must be f32 or bf16");
   if (K % 16) return fail(VDSL_ERR_UNSUPPORTED, "K must be a multiple of 16 (16-byte int8 rows)");
-  VDSL_TRY(check_buffer(q, xq, static_cast<size_t>(M) * K, "xq", false));
-  VDSL_TRY(check_buffer(q, x_scale, static_cast<size_t>(M) * 4, "x_scale", false));
-  VDSL_TRY(check_buffer(q, w, static_cast<size_t>(N) * K, "w", false));
-  VDSL_TRY(check_buffer(q, w_scale, static_cast<size_t>(N) * 4, "w_scale", false));
-  VDSL_TRY(check_buffer(q, y, static_cast<size_t>(M) * N * dtype_size(out_dtype), "y", true));
-  if (acc_out) VDSL_TRY(check_buffer(q, acc_out, static_cast<size_t>(M) * N * 4, "acc_out", true));
+  VDSL_TRY(check_buffer(q, xq, nbytes(M, K), "xq", false));
+  VDSL_TRY(check_buffer(q, x_scale, nbytes(M, 4), "x_scale", false));
+  VDSL_TRY(check_buffer(q, w, nbytes(N, K), "w", false));
+  VDSL_TRY(check_buffer(q, w_scale, nbytes(N, 4), "w_scale", false));
+  VDSL_TRY(check_buffer(q, y, nbytes(M, N, dtype_size(out_dtype)), "y", true));
+  if (acc_out) VDSL_TRY(check_buffer(q, acc_out, nbytes(M, N, 4), "acc_out", true));
   const int split = split_of(M, N, K);
-  if (split > 1) VDSL_TRY(check_buffer(q, workspace, static_cast<size_t>(M) * N * 4, "workspace", true));
+  if (split > 1) VDSL_TRY(check_buffer(q, workspace, nbytes(M, N, 4), "workspace", true));
   if (M == 0 || N == 0) return VDSL_OK;
   const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
   int32_t* ao = acc_out ? static_cast<int32_t*>(acc_out->ptr) : nullptr;
@@ -692,7 +693,7 @@ extern "C" int vdsl_op_pack_w8a8_weights(vdsl_queue q, int64_t N, int64_t K, vds
   VDSL_TRY(enter_queue(q));
   if (N < 0 || K < 0) return fail(VDSL_ERR_INVALID_ARG, "negative weight extent");
   if (N % 32 || K % 32) return fail(VDSL_ERR_UNSUPPORTED, "packed weights need N % 32 == 0 and K % 32 == 0");
-  const size_t n = static_cast<size_t>(N) * static_cast<size_t>(K);
+  const size_t n = nbytes(N, K);
   VDSL_TRY(check_buffer(q, w, n, "w", false));
   VDSL_TRY(check_buffer(q, wp, n, "wp", true));
   if (w == wp) return fail(VDSL_ERR_INVALID_ARG, "w and wp must be different buffers");
@@ -727,12 +728,12 @@ extern "C" int vdsl_op_gemm_w8a8_packed(vdsl_queue q, int64_t M, int64_t N, int6
   VDSL_TRY(enter_queue(q));
   VDSL_TRY(packed_shape_ok(M, N, K));
   if (out_dtype != VDSL_F32 && out_dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "y must be f32 or bf16");
-  VDSL_TRY(check_buffer(q, xq, static_cast<size_t>(M) * K, "xq", false));
-  VDSL_TRY(check_buffer(q, x_scale, static_cast<size_t>(M) * 4, "x_scale", false));
-  VDSL_TRY(check_buffer(q, wp, static_cast<size_t>(N) * K, "wp", false));
-  VDSL_TRY(check_buffer(q, w_scale, static_cast<size_t>(N) * 4, "w_scale", false));
-  VDSL_TRY(check_buffer(q, y, static_cast<size_t>(M) * N * dtype_size(out_dtype), "y", true));
-  if (acc_out) VDSL_TRY(check_buffer(q, acc_out, static_cast<size_t>(M) * N * 4, "acc_out", true));
+  VDSL_TRY(check_buffer(q, xq, nbytes(M, K), "xq", false));
+  VDSL_TRY(check_buffer(q, x_scale, nbytes(M, 4), "x_scale", false));
+  VDSL_TRY(check_buffer(q, wp, nbytes(N, K), "wp", false));
+  VDSL_TRY(check_buffer(q, w_scale, nbytes(N, 4), "w_scale", false));
+  VDSL_TRY(check_buffer(q, y, nbytes(M, N, dtype_size(out_dtype)), "y", true));
+  if (acc_out) VDSL_TRY(check_buffer(q, acc_out, nbytes(M, N, 4), "acc_out", true));
   if (M == 0 || N == 0) return VDSL_OK;
   if (K == 0) return fail(VDSL_ERR_UNSUPPORTED, "packed GEMM needs K > 0");
   const BpkPlan p = bpk_plan(M, N, K);

@@ -150,7 +150,7 @@ extern "C" int vdsl_op_transpose(vdsl_queue q, int64_t rows, int64_t cols, int32
   VDSL_TRY(enter_queue(q));
   if (rows < 0 || cols < 0) return fail(VDSL_ERR_INVALID_ARG, "negative shape");
   if (dtype != VDSL_F32 && dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "transpose dtype must be f32 or bf16");
-  const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols) * dtype_size(dtype);
+  const size_t n = nbytes(rows, cols, dtype_size(dtype));
   VDSL_TRY(check_buffer(q, src, n, "src", false));
   VDSL_TRY(check_buffer(q, dst, n, "dst", true));
   if (src == dst && n) return fail(VDSL_ERR_INVALID_ARG, "in-place transpose is not supported");
@@ -162,8 +162,8 @@ extern "C" int vdsl_op_cast(vdsl_queue q, int64_t n, int32_t src_dtype, vdsl_buf
   if (n < 0) return fail(VDSL_ERR_INVALID_ARG, "negative element count");
   const bool ok = (src_dtype == VDSL_F32 || src_dtype == VDSL_BF16) && (dst_dtype == VDSL_F32 || dst_dtype == VDSL_BF16);
   if (!ok) return fail(VDSL_ERR_UNSUPPORTED, "cast supports f32 <-> bf16");
-  VDSL_TRY(check_buffer(q, src, static_cast<size_t>(n) * dtype_size(src_dtype), "src", false));
-  VDSL_TRY(check_buffer(q, dst, static_cast<size_t>(n) * dtype_size(dst_dtype), "dst", true));
+  VDSL_TRY(check_buffer(q, src, nbytes(n, dtype_size(src_dtype)), "src", false));
+  VDSL_TRY(check_buffer(q, dst, nbytes(n, dtype_size(dst_dtype)), "dst", true));
   if (n == 0) return VDSL_OK;
   if (src_dtype == dst_dtype) return vdsl_buffer_copy(q, dst, 0, src, 0, static_cast<size_t>(n) * dtype_size(src_dtype));
   int64_t blocks = (n + 255) / 256;

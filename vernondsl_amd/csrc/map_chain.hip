@@ -341,8 +341,8 @@ extern "C" int vdsl_op_map_chain(vdsl_queue q, int64_t rows, int64_t cols, const
   if (out_reg < 0 || out_reg >= VDSL_MAP_MAX_REGS) return fail(VDSL_ERR_INVALID_ARG, "out_reg out of range");
   if (n_instr && !code) return fail(VDSL_ERR_INVALID_ARG, "code is null");
   if (n_inputs && !inputs) return fail(VDSL_ERR_INVALID_ARG, "inputs is null");
-  const int64_t n = rows * cols;
-  VDSL_TRY(check_buffer(q, out, static_cast<size_t>(n) * 4u, "out", true));
+  VDSL_TRY(check_buffer(q, out, nbytes(rows, cols, 4), "out", true));
+  const int64_t n = rows * cols;  // no overflow: rows * cols * 4 fits size_t (checked above)
 
   MapProg rt{};
   rt.n = n_instr;
@@ -365,7 +365,7 @@ extern "C" int vdsl_op_map_chain(vdsl_queue q, int64_t rows, int64_t cols, const
     if (d.bcast < VDSL_BCAST_FULL || d.bcast > VDSL_BCAST_SCALAR) return fail(VDSL_ERR_INVALID_ARG, "unknown broadcast");
     const int64_t need = d.bcast == VDSL_BCAST_FULL ? n : d.bcast == VDSL_BCAST_ROW ? cols : d.bcast == VDSL_BCAST_COL ? rows : 1;
     std::string name = "input" + std::to_string(k);
-    VDSL_TRY(check_buffer(q, d.buf, static_cast<size_t>(need) * 4u, name.c_str(), false));
+    VDSL_TRY(check_buffer(q, d.buf, nbytes(need, 4), name.c_str(), false));
     in.p[k] = static_cast<const float*>(d.buf->ptr);
     in.bcast[k] = d.bcast;
   }

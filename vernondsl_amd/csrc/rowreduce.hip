@@ -311,11 +311,10 @@ extern "C" int vdsl_op_row_reduce_softmax(vdsl_queue q, int64_t rows, int64_t co
   if (rows < 0 || cols < 0) return fail(VDSL_ERR_INVALID_ARG, "negative shape");
   if (dtype != VDSL_F32 && dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "softmax dtype must be f32 or bf16");
   const size_t es = dtype_size(dtype);
-  const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols);
-  VDSL_TRY(check_buffer(q, x, n * es, "x", false));
-  if (row_sum) VDSL_TRY(check_buffer(q, row_sum, static_cast<size_t>(rows) * 4, "row_sum", true));
-  if (row_max) VDSL_TRY(check_buffer(q, row_max, static_cast<size_t>(rows) * 4, "row_max", true));
-  if (softmax) VDSL_TRY(check_buffer(q, softmax, n * es, "softmax", true));
+  VDSL_TRY(check_buffer(q, x, nbytes(rows, cols, es), "x", false));
+  if (row_sum) VDSL_TRY(check_buffer(q, row_sum, nbytes(rows, 4), "row_sum", true));
+  if (row_max) VDSL_TRY(check_buffer(q, row_max, nbytes(rows, 4), "row_max", true));
+  if (softmax) VDSL_TRY(check_buffer(q, softmax, nbytes(rows, cols, es), "softmax", true));
   if (rows == 0) return VDSL_OK;
   if (cols == 0) {
     // sum of an empty row is 0 and its max is -inf; nothing else to write
@@ -335,10 +334,9 @@ extern "C" int vdsl_op_col_reduce(vdsl_queue q, int64_t rows, int64_t cols, int3
   VDSL_TRY(enter_queue(q));
   if (rows < 0 || cols < 0) return fail(VDSL_ERR_INVALID_ARG, "negative shape");
   if (dtype != VDSL_F32 && dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "col_reduce dtype must be f32 or bf16");
-  const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols);
-  VDSL_TRY(check_buffer(q, x, n * dtype_size(dtype), "x", false));
-  if (col_sum) VDSL_TRY(check_buffer(q, col_sum, static_cast<size_t>(cols) * 4, "col_sum", true));
-  if (col_max) VDSL_TRY(check_buffer(q, col_max, static_cast<size_t>(cols) * 4, "col_max", true));
+  VDSL_TRY(check_buffer(q, x, nbytes(rows, cols, dtype_size(dtype)), "x", false));
+  if (col_sum) VDSL_TRY(check_buffer(q, col_sum, nbytes(cols, 4), "col_sum", true));
+  if (col_max) VDSL_TRY(check_buffer(q, col_max, nbytes(cols, 4), "col_max", true));
   if (cols == 0) return VDSL_OK;
   const int64_t blocks = (cols + 63) / 64;
   float* cs = col_sum ? static_cast<float*>(col_sum->ptr) : nullptr;

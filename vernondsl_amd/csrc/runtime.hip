@@ -93,6 +93,8 @@ int check_buffer(vdsl_queue q, vdsl_buffer b, size_t bytes, const char* name, bo
   if (!valid_buffer(b)) return fail(VDSL_ERR_INVALID_HANDLE, std::string("invalid buffer handle: ") + name);
   if (b->dev != q->dev)
     return fail(VDSL_ERR_INVALID_ARG, std::string("buffer ") + name + " belongs to another device");
+  if (bytes == kSizeOverflow)
+    return fail(VDSL_ERR_SHAPE, std::string("operand ") + name + ": its byte size overflows (extents too large)");
   if (b->bytes < bytes)
     return fail(VDSL_ERR_SHAPE, std::string("buffer ") + name + " holds " + std::to_string(b->bytes) +
                                     " bytes, op needs " + std::to_string(bytes));

@@ -14,6 +14,7 @@ recorded on one queue and replayed as a single hipGraph (no host work or allocat
     grads = g.backward(loss)                         # {param name: gradient Value (f32)}
     exe = g.compile(dev)
     exe.write(q, "X", x_host) ...; step = exe.capture(q); step.launch(q)
+    exe.write(q, "W1", w1_new); step.launch(q)       # re-packs W1 first, then replays
 
 Backward rules (y = act(x W^T), W stored [out][in]):
     g    = dL/dy (+ its transpose g^T), bf16; for act = gelu: g = gelu_bwd(dL/dh, pre)
@@ -310,9 +311,9 @@ class Executable:
             self._stale.add(name)
 
     def prepare(self, q: Queue):
-        """Runs the prepare ops (weight packing) whose params were written since they last ran.
-        run() and capture() call it first, so a replayed step never reads stale packed weights
-        unless a param is written after capture (then call prepare() before the next launch)."""
+        """Runs the prepare ops (weight packing, param transposes) whose params were written since
+        they last ran.  run(), capture() and every Step.launch() call it first, so no step reads
+        packed or transposed weights older than the params they derive from."""
         T = self.t
         for op in self.graph.prepare_ops:  # in order: an op may read what an earlier one made
             if op.inputs[0].name not in self._stale:
@@ -375,14 +376,14 @@ class Executable:
             else:
                 raise NotImplementedError(op.kind)
 
-    def capture(self, q: Queue):
-        """Records one run() into a hipGraph and returns it (rhi.Graph: .launch(q), .destroy()).
+    def capture(self, q: Queue) -> "Step":
+        """Records one run() into a hipGraph and returns it as a Step (.launch(q), .destroy()).
         Pending prepare ops run first, eagerly, outside the recording."""
         if self._stale:
             self.prepare(q)
         with q.capture() as rec:
             self.run(q)
-        return rec.graph
+        return Step(self, rec.graph)
 
     def free(self):
         for t in self.t.values():
@@ -391,6 +392,29 @@ class Executable:
         if self.workspace is not None:
             self.workspace.free()
             self.workspace = None
+
+
+class Step:
+    """One captured step of an Executable.  The recording reads the prepared operands (packed
+    weights, param transposes) from their static buffers, so launch() first re-runs, eagerly on
+    the same queue and outside the recording, the prepare ops of any param written with
+    Executable.write() since the last launch; the replay then reads the new weights."""
+
+    def __init__(self, exe: Executable, g):
+        self.exe = exe
+        self.graph = g
+
+    @property
+    def handle(self):
+        return self.graph.handle
+
+    def launch(self, q: Queue):
+        if self.exe._stale:
+            self.exe.prepare(q)
+        self.graph.launch(q)
+
+    def destroy(self):
+        self.graph.destroy()
 
 
 # ---- the two workload graphs ------------------------------------------------------------------------
