@@ -357,6 +357,22 @@ int vdsl_op_gemm_w8a8_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl
                              int32_t out_dtype, int32_t relu, vdsl_buffer acc_out,
                              vdsl_buffer workspace);
 
+/* Allocation-free form of vdsl_op_gemm_w8a8_packed.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code recorded under graph capture that may not call
+ * hipMalloc, tight serving loops, harnesses that forbid allocation).  It takes no workspace: the
+ * split-K partials live in a library-owned device array of VDSL_W8A8_NOALLOC_SCRATCH_BYTES per GPU
+ * (resolved when the device is opened, held until the process ends), and the call allocates
+ * nothing.  Same arguments and results, bit for bit, as vdsl_op_gemm_w8a8_packed.  A shape whose
+ * launch plan needs more scratch than the array holds (vdsl_gemm_w8a8_packed_workspace_bytes()
+ * says how much) fails with VDSL_ERR_UNSUPPORTED before anything is enqueued.  Every call on one
+ * GPU shares the array: calls on one queue are ordered and safe, calls that overlap in time on one
+ * GPU (several queues) race and give wrong results. */
+#define VDSL_W8A8_NOALLOC_SCRATCH_BYTES (16u << 20)
+int vdsl_op_gemm_w8a8_packed_noalloc(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer xq,
+                                     vdsl_buffer x_scale, vdsl_buffer wp, vdsl_buffer w_scale,
+                                     vdsl_buffer y, int32_t out_dtype, int32_t relu,
+                                     vdsl_buffer acc_out);
+
 /* ---- failure injection (tests of error paths, host-side only) ----------------------------- */
 /* After `n` more successful buffer allocations, the next one fails with VDSL_ERR_OUT_OF_MEMORY
  * (n < 0 disables).  Also settable with the environment variable VDSL_FAIL_ALLOC_AFTER. */

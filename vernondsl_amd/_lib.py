@@ -140,6 +140,7 @@ PROTOTYPES = {
     "vdsl_mse_partials_count": (C.c_int64, [_i64, _i64]),
     "vdsl_op_mse_fwd_bwd": (C.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vdsl_op_quantize_rows_i8": (C.c_int, [_vp, _i64, _i64, _i32, _vp, _vp, _vp]),
+    "vdsl_op_gemm_w8a8_packed_noalloc": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp]),
     "vdsl_gemm_w8a8_workspace_bytes": (C.c_int, [_i64, _i64, _i64, C.POINTER(_sz)]),
     "vdsl_op_gemm_w8a8": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "vdsl_op_pack_w8a8_weights": (C.c_int, [_vp, _i64, _i64, _vp, _vp]),

@@ -74,6 +74,10 @@ int check_buffer(vdsl_queue q, vdsl_buffer b, size_t bytes, const char* name, bo
 
 size_t dtype_size(int dtype);
 
+// Per-device set-up of the allocation-free int8 GEMM (gemm_w8a8.hip); called by vdsl_device_open
+// with the device current.
+void w8a8_noalloc_setup(int ordinal);
+
 // Byte size a * b * c of a dense operand, or kSizeOverflow when a factor is negative or the
 // product does not fit in size_t.  check_buffer rejects kSizeOverflow with VDSL_ERR_SHAPE, so an
 // entry point that sizes every operand with nbytes() fails before it enqueues anything instead of

@@ -722,10 +722,9 @@ extern "C" int vdsl_gemm_w8a8_packed_workspace_bytes(int64_t M, int64_t N, int64
   return VDSL_OK;
 }
 
-extern "C" int vdsl_op_gemm_w8a8_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer xq, vdsl_buffer x_scale,
-                                        vdsl_buffer wp, vdsl_buffer w_scale, vdsl_buffer y, int32_t out_dtype, int32_t relu,
-                                        vdsl_buffer acc_out, vdsl_buffer workspace) {
-  VDSL_TRY(enter_queue(q));
+// Operand checks shared by the packed entry points (everything but the split-K scratch).
+static int packed_operands_ok(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer xq, vdsl_buffer x_scale,
+                              vdsl_buffer wp, vdsl_buffer w_scale, vdsl_buffer y, int32_t out_dtype, vdsl_buffer acc_out) {
   VDSL_TRY(packed_shape_ok(M, N, K));
   if (out_dtype != VDSL_F32 && out_dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "y must be f32 or bf16");
   VDSL_TRY(check_buffer(q, xq, nbytes(M, K), "xq", false));
@@ -734,12 +733,14 @@ extern "C" int vdsl_op_gemm_w8a8_packed(vdsl_queue q, int64_t M, int64_t N, int6
   VDSL_TRY(check_buffer(q, w_scale, nbytes(N, 4), "w_scale", false));
   VDSL_TRY(check_buffer(q, y, nbytes(M, N, dtype_size(out_dtype)), "y", true));
   if (acc_out) VDSL_TRY(check_buffer(q, acc_out, nbytes(M, N, 4), "acc_out", true));
-  if (M == 0 || N == 0) return VDSL_OK;
-  if (K == 0) return fail(VDSL_ERR_UNSUPPORTED, "packed GEMM needs K > 0");
-  const BpkPlan p = bpk_plan(M, N, K);
-  const size_t wsb = bpk_workspace_bytes(p);
-  if (wsb) VDSL_TRY(check_buffer(q, workspace, wsb, "workspace", true));
-  char* part = wsb ? static_cast<char*>(workspace->ptr) : nullptr;
+  if (M != 0 && N != 0 && K == 0) return fail(VDSL_ERR_UNSUPPORTED, "packed GEMM needs K > 0");
+  return VDSL_OK;
+}
+
+// Launches the plan's GEMM (and, split, its reduce) with the split-K partials at `part`.
+static int packed_launch(vdsl_queue q, const BpkPlan& p, int64_t M, int64_t N, int64_t K, vdsl_buffer xq,
+                         vdsl_buffer x_scale, vdsl_buffer wp, vdsl_buffer w_scale, vdsl_buffer y, int32_t out_dtype,
+                         int32_t relu, vdsl_buffer acc_out, char* part) {
   int32_t* ao = acc_out ? static_cast<int32_t*>(acc_out->ptr) : nullptr;
   const auto* a = static_cast<const int8_t*>(xq->ptr);
   const auto* b = static_cast<const int8_t*>(wp->ptr);
@@ -750,4 +751,75 @@ extern "C" int vdsl_op_gemm_w8a8_packed(vdsl_queue q, int64_t M, int64_t N, int6
   if (p.cfg == 3) return launch_bpk<P3>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
   if (p.cfg == 2) return launch_bpk<P2>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
   return launch_bpk<P1>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
+}
+
+extern "C" int vdsl_op_gemm_w8a8_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer xq, vdsl_buffer x_scale,
+                                        vdsl_buffer wp, vdsl_buffer w_scale, vdsl_buffer y, int32_t out_dtype, int32_t relu,
+                                        vdsl_buffer acc_out, vdsl_buffer workspace) {
+  VDSL_TRY(enter_queue(q));
+  VDSL_TRY(packed_operands_ok(q, M, N, K, xq, x_scale, wp, w_scale, y, out_dtype, acc_out));
+  if (M == 0 || N == 0) return VDSL_OK;
+  const BpkPlan p = bpk_plan(M, N, K);
+  const size_t wsb = bpk_workspace_bytes(p);
+  if (wsb) VDSL_TRY(check_buffer(q, workspace, wsb, "workspace", true));
+  return packed_launch(q, p, M, N, K, xq, x_scale, wp, w_scale, y, out_dtype, relu, acc_out,
+                       wsb ? static_cast<char*>(workspace->ptr) : nullptr);
+}
+
+// ---- allocation-free entry point ------------------------------------------------------------------
+// vdsl_op_gemm_w8a8_packed_noalloc keeps the split-K partials in `scratch`, a file-scope device
+// array, so it calls no allocator.  Every GPU that loads the library holds its own copy until the
+// process ends.  In host code the name `scratch` is a host-side stand-in, not a device address:
+// the array's address on a device comes from hipGetSymbolAddress, called once per device with that
+// device current (w8a8_noalloc_setup, from vdsl_device_open), kept in g_scratch_addr, and only that
+// address is handed to kernels.  Nothing in the array needs to start at zero: a split launch
+// writes every partial it later reads.  Calls that overlap in time on one GPU (two queues) share
+// the array and race.
+namespace vdsl {
+static __device__ __align__(256) char scratch[VDSL_W8A8_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::atomic<char*> g_scratch_addr[kScratchDevices];
+
+// The device address of `scratch` on device `ordinal`, which must be the current device.
+int scratch_address(int ordinal, char** out) {
+  if (ordinal < 0 || ordinal >= kScratchDevices)
+    return fail(VDSL_ERR_UNSUPPORTED, "allocation-free GEMM: device ordinal beyond the library's table");
+  char* p = g_scratch_addr[ordinal].load(std::memory_order_acquire);
+  if (!p) {
+    void* addr = nullptr;
+    VDSL_TRY(check_hip(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"));
+    if (!addr) return fail(VDSL_ERR_DEVICE, "hipGetSymbolAddress(scratch) returned a null address");
+    p = static_cast<char*>(addr);
+    g_scratch_addr[ordinal].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return VDSL_OK;
+}
+}  // namespace
+
+void w8a8_noalloc_setup(int ordinal) {
+  char* p = nullptr;
+  // A failure is not fatal to the device: the entry point tries again and reports the HIP error.
+  (void)scratch_address(ordinal, &p);
+}
+}  // namespace vdsl
+
+extern "C" int vdsl_op_gemm_w8a8_packed_noalloc(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer xq,
+                                                vdsl_buffer x_scale, vdsl_buffer wp, vdsl_buffer w_scale, vdsl_buffer y,
+                                                int32_t out_dtype, int32_t relu, vdsl_buffer acc_out) {
+  VDSL_TRY(enter_queue(q));
+  VDSL_TRY(packed_operands_ok(q, M, N, K, xq, x_scale, wp, w_scale, y, out_dtype, acc_out));
+  if (M == 0 || N == 0) return VDSL_OK;
+  const BpkPlan p = bpk_plan(M, N, K);
+  const size_t wsb = bpk_workspace_bytes(p);
+  if (wsb > VDSL_W8A8_NOALLOC_SCRATCH_BYTES)
+    return fail(VDSL_ERR_UNSUPPORTED, "allocation-free GEMM: this shape needs " + std::to_string(wsb) +
+                                          " bytes of split-K scratch, the library's array holds " +
+                                          std::to_string(VDSL_W8A8_NOALLOC_SCRATCH_BYTES) +
+                                          "; use vdsl_op_gemm_w8a8_packed with a workspace");
+  char* part = nullptr;
+  if (wsb) VDSL_TRY(scratch_address(q->dev->ordinal, &part));
+  return packed_launch(q, p, M, N, K, xq, x_scale, wp, w_scale, y, out_dtype, relu, acc_out, part);
 }

@@ -160,6 +160,7 @@ int vdsl_device_open(int kind, int ordinal, vdsl_device* out) {
     delete d;
     return st;
   }
+  w8a8_noalloc_setup(ordinal);
   reg_add(d);
   *out = d;
   return VDSL_OK;

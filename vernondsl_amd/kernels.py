@@ -252,3 +252,23 @@ def gemm_w8a8_packed(q: Queue, xq: Tensor, x_scale: Tensor, wp: Tensor, w_scale:
     _expect(acc_out, (M, N), "i32", "acc_out")
     call("vdsl_op_gemm_w8a8_packed", q.handle, M, N, K, xq.handle, x_scale.handle, wp.handle, w_scale.handle,
          y.handle, y.dtype, int(bool(relu)), _h(acc_out), _h(workspace))
+
+
+def gemm_w8a8_packed_noalloc(q: Queue, xq: Tensor, x_scale: Tensor, wp: Tensor, w_scale: Tensor, y: Tensor,
+                             relu=False, acc_out=None):
+    """gemm_w8a8_packed without a workspace (vdsl_op_gemm_w8a8_packed_noalloc): the split-K
+    partials live in the library's own per-GPU array, so the call allocates nothing.  Calls that
+    overlap in time on one GPU share that array and race."""
+    M, K = xq.shape
+    N, K2 = wp.shape
+    if K != K2:
+        raise ValueError(f"inner dimensions differ: {K} vs {K2}")
+    _expect(xq, (M, K), "i8", "xq")
+    _expect(wp, (N, K), "i8", "wp")
+    _expect(x_scale, (M,), "f32", "x_scale")
+    _expect(w_scale, (N,), "f32", "w_scale")
+    if y.shape != (M, N):
+        raise ValueError(f"y: shape {y.shape}, expected {(M, N)}")
+    _expect(acc_out, (M, N), "i32", "acc_out")
+    call("vdsl_op_gemm_w8a8_packed_noalloc", q.handle, M, N, K, xq.handle, x_scale.handle, wp.handle,
+         w_scale.handle, y.handle, y.dtype, int(bool(relu)), _h(acc_out))
