@@ -104,6 +104,51 @@ def time_replays(q, dev, fn, steps, warmup, per_graph=1, warmup_ms=25.0):
     return ms / n, wall / n
 
 
+def time_ops_in_step(q, dev, exe, reps, warmup_ms=25.0):
+    """In-step duration of every op of an Executable's step: `reps` steps are issued op by op on q,
+    back to back on their real buffers, with a HIP event recorded on q after each op; the mean over
+    the steps of the time between consecutive events.  An untimed lead step ahead of them keeps the
+    queue busy, so no event waits on a launch from the host (after at least `warmup_ms` of wall time
+    in untimed steps).  Returns (per-op ms list, mean ms of the whole evented step)."""
+    from vernondsl_amd.rhi import Event
+    ops = exe.graph.ops
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < warmup_ms:
+        exe.run(q)
+        q.sync()
+    evs = [[Event(dev) for _ in range(len(ops) + 1)] for _ in range(reps)]
+    exe.run(q)  # the lead step
+    for r in range(reps):
+        evs[r][0].record(q)
+        exe.run(q, events=evs[r][1:])
+    q.sync()
+    tot = [0.0] * len(ops)
+    whole = 0.0
+    for ev in evs:
+        for i in range(len(ops)):
+            tot[i] += ev[i].elapsed_ms(ev[i + 1])
+        whole += ev[0].elapsed_ms(ev[-1])
+    for ev in evs:
+        for e in ev:
+            e.destroy()
+    return [t / reps for t in tot], whole / reps
+
+
+def in_step_report(exe, op_ms, peak, unit_scale=1e12):
+    """Per-op in-step rows and the dominant GEMM op (the one with the most in-step time)."""
+    rows, dom = [], None
+    for op, ms in zip(exe.graph.ops, op_ms):
+        fl = exe.op_flops(op)
+        row = {"op": exe.op_label(op), "ms": round(ms, 5)}
+        if fl:
+            rate = fl / (ms * 1e-3) / unit_scale
+            row.update(rate=round(rate, 1), frac=round(rate / peak, 4))
+            if dom is None or ms > dom[1]:
+                dom = (row["op"], ms, fl)
+        rows.append(row)
+    return rows, dom
+
+
 NOT_CHECKED = "not checked (--no-cpu: the oracle runs only in the CPU-baseline leg)"
 
 
@@ -231,8 +276,7 @@ def bench_softmax(dev, q, steps, warmup, do_cpu):
 
 # ---- config 4 ------------------------------------------------------------------------------------
 def bench_mlp(dev, q, steps, warmup, do_cpu):
-    from vernondsl_amd import _lib, graph, kernels, spec
-    from vernondsl_amd.rhi import Event, Tensor
+    from vernondsl_amd import graph, spec
     B, D, Hd, O = 2048, 4096, 4096, 4096
     x, w1, w2, t = spec.mlp_inputs(B, D, Hd, O)
     g, _ = graph.mlp_train_graph(B, D, Hd, O)
@@ -240,42 +284,30 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
     for name, arr in (("X", x), ("W1", w1), ("W2", w2), ("T", t)):
         exe.write(q, name, arr)
     step = exe.capture(q)
-    for _ in range(max(1, warmup // 5)):
-        step.launch(q)
-    q.sync()
     n = max(5, steps // 5)
-    e0, e1 = Event(dev), Event(dev)
-    e0.record(q)
-    for _ in range(n):
-        step.launch(q)
-    e1.record(q)
-    ms = e0.elapsed_ms(e1) / n
+    # graph replays, after the same >= 25 ms warm-up as every other timing
+    ms = time_launches(q, dev, lambda: step.launch(q), n, warmup=max(1, warmup // 5))
     # the same step issued op by op on the stream (no graph), for comparison
     eager_ms = time_launches(q, dev, lambda: exe.run(q), n, warmup=2)
-    e0.destroy()
-    e1.destroy()
+    # every op's in-step duration: events between the ops of eagerly issued steps
+    op_ms, ev_step_ms = time_ops_in_step(q, dev, exe, n)
+    rows, (dom_op, dom_ms, dom_flop) = in_step_report(exe, op_ms, PEAK_BF16_TFLOPS)
     flops = spec.mlp_flops(B, D, Hd, O)
     tflops = flops / (ms * 1e-3) / 1e12
+    gemm_ms = sum(r["ms"] for r in rows if "rate" in r)
     loss = float(exe.read(q, "loss")[0])
     step.destroy()
     exe.free()
-    # dominant kernel: the forward GEMM (2048x4096x4096, GELU epilogue) timed alone, on W1 packed as
-    # the graph's prepare step packs it
-    tx, tw = Tensor.from_numpy(dev, q, x, "bf16"), Tensor.from_numpy(dev, q, w1, "bf16")
-    twp = Tensor(dev, (Hd, D), "bf16")
-    kernels.pack_bf16_weights(q, tw, twp)
-    th, tp = Tensor(dev, (B, Hd), "bf16"), Tensor(dev, (B, Hd), "f32")
-    gms = time_launches(q, dev, lambda: kernels.gemm_bf16_packed(q, tx, twp, th, _lib.EPI_GELU, tp), max(20, steps))
-    gflop = 2 * B * D * Hd
-    gt = gflop / (gms * 1e-3) / 1e12
-    for t_ in (tx, tw, twp, th, tp):
-        t_.free()
+    gt = dom_flop / (dom_ms * 1e-3) / 1e12
     res = {"config": 4, "workload": "2-layer MLP 4096-4096-4096, GELU, MSE, batch 2048, bf16 MFMA, fwd+bwd as one hipGraph",
            "metric": "MFMA TFLOPS (GEMM)", "value": tflops, "unit": "TFLOP/s", "ms_per_step": ms,
            "eager_ms_per_step": eager_ms, "flop_per_step": flops, "loss": loss,
+           "in_step": {"ops": rows, "gemm_ms": gemm_ms, "gemm_frac": flops / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                       "evented_step_ms": ev_step_ms,
+                       "method": "HIP events after every op of eagerly issued steps on the real buffers"},
            "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                        "frac": gt / PEAK_BF16_TFLOPS, "kernel": "gemm_bf16_bpk<128x256, 4 waves of 128x64, weights from packed fragments> (GELU, bf16 out, f32 pre) 2048x4096x4096",
-                        "kernel_ms": gms, "traffic": measured_traffic("gemm_bf16")},
+                        "frac": gt / PEAK_BF16_TFLOPS, "kernel": f"dominant in-step op: {dom_op}",
+                        "kernel_ms": dom_ms, "traffic": measured_traffic("gemm_bf16")},
            "whole_graph_frac_of_peak": tflops / PEAK_BF16_TFLOPS}
     if do_cpu:  # CPU-baseline leg
         from oracle import oracle
@@ -290,8 +322,7 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
 
 # ---- config 5 ------------------------------------------------------------------------------------
 def bench_w8a8(dev, q, steps, warmup, do_cpu):
-    from vernondsl_amd import graph, kernels, spec
-    from vernondsl_amd.rhi import Event, Tensor
+    from vernondsl_amd import graph, spec
     B, widths = 512, spec.W8A8_WIDTHS
     x, layers = spec.w8a8_inputs(B, widths)
     g = graph.w8a8_infer_graph(B, widths)
@@ -301,64 +332,38 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
         exe.write(q, f"W{li}", w)
         exe.write(q, f"S{li}", sc)
     step = exe.capture(q)
-    for _ in range(max(1, warmup // 5)):
-        step.launch(q)
-    q.sync()
     n = max(5, steps // 2)
-    e0, e1 = Event(dev), Event(dev)
-    e0.record(q)
-    for _ in range(n):
-        step.launch(q)
-    e1.record(q)
-    ms = e0.elapsed_ms(e1) / n
+    ms = time_launches(q, dev, lambda: step.launch(q), n, warmup=max(1, warmup // 5))
     eager_ms = time_launches(q, dev, lambda: exe.run(q), n, warmup=2)
-    e0.destroy()
-    e1.destroy()
+    op_ms, ev_step_ms = time_ops_in_step(q, dev, exe, n)
+    rows, _ = in_step_report(exe, op_ms, PEAK_INT8_TOPS)
     ops = spec.w8a8_ops(B, widths)
     tops = ops / (ms * 1e-3) / 1e12
     got = exe.read(q, "Y")
-    rows = np.array([0, 511])
     parity = NOT_CHECKED
     if do_cpu:  # CPU-baseline leg (timed below): the oracle's forward of two rows as the checker
         from oracle import oracle
-        parity = "ok" if np.array_equal(got[rows], oracle.w8a8_forward(x[rows], layers)) else "FAIL"
+        rows_chk = np.array([0, 511])
+        parity = "ok" if np.array_equal(got[rows_chk], oracle.w8a8_forward(x[rows_chk], layers)) else "FAIL"
     step.destroy()
     exe.free()
-    # dominant kernel: the 512x8192x8192 layer GEMM alone, on the config's input quantised as
-    # layer 0 sees it, launches cycling through the three 8192x8192 layers' packed weights as the
-    # graph does (192 MB: one matrix reused launch after launch would be served from the 256 MB
-    # last-level cache and time ~20% faster than the step ever sees)
-    K = N = 8192
-    tx = Tensor.from_numpy(dev, q, x, "bf16")
-    txq, txs = Tensor(dev, (B, K), "i8"), Tensor(dev, (B,), "f32")
-    kernels.quantize_rows_i8(q, tx, txq, txs)
-    tx.free()
-    packs = []
-    for li in range(3):
-        tw = Tensor.from_numpy(dev, q, layers[li][0])
-        twp = Tensor(dev, (N, K), "i8")
-        kernels.pack_w8a8_weights(q, tw, twp)  # once, as the graph's prepare step does
-        tw.free()
-        packs.append((twp, Tensor.from_numpy(dev, q, layers[li][1])))
-    ty = Tensor(dev, (B, N), "bf16")
-    assert kernels.gemm_w8a8_packed_workspace_bytes(B, N, K) == 0
-    nxt = {"i": 0}
-
-    def layer_gemm():
-        twp, tsc = packs[nxt["i"]]
-        nxt["i"] = (nxt["i"] + 1) % 3
-        kernels.gemm_w8a8_packed(q, txq, txs, twp, tsc, ty, True, None, None)
-    gms = time_launches(q, dev, layer_gemm, max(21, steps // 3 * 3))
-    gt = 2 * B * K * N / (gms * 1e-3) / 1e12
-    for t_ in (txq, txs, ty) + tuple(t for pk in packs for t in pk):
-        t_.free()
+    # dominant kernel: the three 512x8192x8192 layer GEMMs, each timed inside the step (their
+    # weights stream from HBM there: 192 MB rotate through the 256 MB last-level cache)
+    big = [r for r in rows if r["op"].startswith("w8a8_packed") and r["op"].endswith("512x8192x8192")]
+    kms = sum(r["ms"] for r in big) / len(big)
+    gt = 2 * B * 8192 * 8192 / (kms * 1e-3) / 1e12
+    gemm_ms = sum(r["ms"] for r in rows if "rate" in r)
     res = {"config": 5, "workload": "int8 W8A8 MLP 8192-8192-8192-8192-1024, batch 512, dequant+ReLU fused, one hipGraph",
            "metric": "MFMA TOPS (int8 GEMM)", "value": tops, "unit": "TOP/s", "ms_per_step": ms,
            "eager_ms_per_step": eager_ms, "ops_per_step": ops,
            "parity": parity,
+           "in_step": {"ops": rows, "gemm_ms": gemm_ms, "gemm_frac": ops / (gemm_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS,
+                       "evented_step_ms": ev_step_ms,
+                       "method": "HIP events after every op of eagerly issued steps on the real buffers"},
            "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                        "frac": gt / PEAK_INT8_TOPS, "kernel": "gemm_w8a8_bpk<128x128, 4 waves of 128x32, weights from packed fragments> (dequant+ReLU) 512x8192x8192, weights cycling through the 3 layers", "kernel_ms": gms,
-                        "traffic": measured_traffic("gemm_w8a8")},
+                        "frac": gt / PEAK_INT8_TOPS,
+                        "kernel": "gemm_w8a8_bpk 512x8192x8192 (dequant+ReLU), mean of the three layers as timed inside the step",
+                        "kernel_ms": kms, "traffic": measured_traffic("gemm_w8a8")},
            "whole_graph_frac_of_peak": tops / PEAK_INT8_TOPS}
     if do_cpu:
         r = 8
@@ -459,6 +464,24 @@ def run_kernel_only(dev, q, name, reps):
         if W is not None:
             W.buffer.fill_u32(q, 0)
         fn, ts = (lambda: kernels.gemm_w8a8_packed(q, A, xs, B, ws, Y, True, None, W)), [A, B0, B, xs, ws, Y] + ([W] if W else [])
+    elif name == "c4_step":  # one eager config-4 training step per rep (every kernel of the step)
+        from vernondsl_amd import graph
+        x, w1, w2, t = spec.mlp_inputs()
+        g, _ = graph.mlp_train_graph()
+        exe = g.compile(dev)
+        for nm, arr in (("X", x), ("W1", w1), ("W2", w2), ("T", t)):
+            exe.write(q, nm, arr)
+        fn, ts = (lambda: exe.run(q)), [exe]
+    elif name == "c5_step":  # one eager config-5 forward per rep
+        from vernondsl_amd import graph
+        x, layers = spec.w8a8_inputs()
+        g = graph.w8a8_infer_graph()
+        exe = g.compile(dev)
+        exe.write(q, "X", x)
+        for li, (w, sc) in enumerate(layers):
+            exe.write(q, f"W{li}", w)
+            exe.write(q, f"S{li}", sc)
+        fn, ts = (lambda: exe.run(q)), [exe]
     elif name == "escape_time":
         p = kernels.escape_time_params(**spec.mandelbrot_params())
         out = Tensor(dev, (1024, 1024), "i32")
@@ -487,7 +510,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline timings")
     ap.add_argument("--only", type=int, default=0, help="run only the headline (2) or one extra config")
     ap.add_argument("--kernel", default="", help="run one kernel --reps times and exit (for rocprofv3 --pmc): "
-                    "map_chain, softmax_f32, softmax_bf16, gemm_bf16, gemm_w8a8, escape_time, copy")
+                    "map_chain, softmax_f32, softmax_bf16, gemm_bf16, gemm_w8a8, escape_time, copy, c4_step, c5_step")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--traffic-summary", default="", metavar="DIR",
                     help="write profiles/traffic.json from the counter runs in DIR and exit (no GPU needed)")

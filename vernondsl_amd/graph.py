@@ -332,49 +332,91 @@ class Executable:
     def read(self, q: Queue, name: str):
         return self.t[name].numpy(q)
 
-    def run(self, q: Queue):
+    def run(self, q: Queue, events=None):
         """Enqueues every op of the graph, in order, on q (after any pending prepare ops, unless q
-        is recording a capture)."""
-        T = self.t
+        is recording a capture).  events: optional rhi.Events, one per op, each recorded on q right
+        after its op (per-op timing of the step as it runs)."""
         if self._stale and not q.capturing:
             self.prepare(q)
-        for op in self.graph.ops:
-            ins = [T[v.name] for v in op.inputs]
-            outs = [T[v.name] for v in op.outputs]
-            if op.kind == "linear":
-                pre = T[op.attrs["pre"].name] if op.attrs["pre"] is not None else None
-                epi = {"none": _lib.EPI_NONE, "gelu": _lib.EPI_GELU, "relu": _lib.EPI_RELU}[op.attrs["act"]]
-                if op.attrs.get("packed") is not None:
-                    kernels.gemm_bf16_packed(q, ins[0], T[op.attrs["packed"].name], outs[0], epi, pre)
-                else:
-                    kernels.gemm_bf16(q, ins[0], ins[1], outs[0], trans_a=False, trans_b=True, epilogue=epi,
-                                      pre_act=pre)
-            elif op.kind == "gemm":
-                kernels.gemm_bf16(q, ins[0], ins[1], outs[0], op.attrs["trans_a"], op.attrs["trans_b"], op.attrs["epi"],
-                                  None, self.workspace)
-            elif op.kind == "mse":
-                loss = outs[0]
-                if len(outs) == 4:
-                    kernels.mse_fwd_bwd(q, ins[0], ins[1], loss, outs[1], outs[2], outs[3])
-                else:
-                    raise RuntimeError("mse without backward: call Graph.backward() or use the loss op's fused form")
-            elif op.kind == "gelu_bwd":
-                kernels.gelu_bwd(q, ins[0], ins[1], outs[0], outs[1])
-            elif op.kind == "gemm_gelu_bwd":
-                kernels.gemm_bf16_gelu_bwd(q, ins[0], ins[1], ins[2], outs[0], outs[1], op.attrs.get("packed", False))
-            elif op.kind == "cast":
-                kernels.cast(q, ins[0], outs[0])
-            elif op.kind == "transpose":
-                kernels.transpose(q, ins[0], outs[0])
-            elif op.kind == "quantize":
-                kernels.quantize_rows_i8(q, ins[0], outs[0], outs[1])
-            elif op.kind == "w8a8":
-                kernels.gemm_w8a8(q, ins[0], ins[1], ins[2], ins[3], outs[0], op.attrs["relu"], None, self.workspace)
-            elif op.kind == "w8a8_packed":
-                kernels.gemm_w8a8_packed(q, ins[0], ins[1], ins[2], ins[3], outs[0], op.attrs["relu"], None,
-                                         self.workspace)
+        if events is not None and len(events) != len(self.graph.ops):
+            raise ValueError(f"{len(events)} events for {len(self.graph.ops)} ops")
+        for i, op in enumerate(self.graph.ops):
+            self._run_op(q, op)
+            if events is not None:
+                events[i].record(q)
+
+    def op_label(self, op: Op) -> str:
+        """A short description of one op: its kind, form and extents (M x N x K for GEMMs)."""
+        ins, outs = op.inputs, op.outputs
+        if op.kind == "linear":
+            (M, K), N = ins[0].shape, ins[1].shape[0]
+            form = "packed" if op.attrs.get("packed") is not None else "row-major"
+            return f"linear {op.attrs['act']} ({form} weights, {outs[0].dtype} out) {M}x{N}x{K}"
+        if op.kind == "gemm":
+            a, b = ins
+            M, K = (a.shape[1], a.shape[0]) if op.attrs["trans_a"] else a.shape
+            N = b.shape[0] if op.attrs["trans_b"] else b.shape[1]
+            return f"gemm {'T' if op.attrs['trans_a'] else 'N'}{'T' if op.attrs['trans_b'] else 'N'} {M}x{N}x{K}"
+        if op.kind == "gemm_gelu_bwd":
+            (M, K), N = ins[0].shape, ins[1].shape[0]
+            return f"gemm + GELU backward ({'packed' if op.attrs.get('packed') else 'row-major'} B) {M}x{N}x{K}"
+        if op.kind in ("w8a8", "w8a8_packed"):
+            (M, K), N = ins[0].shape, ins[2].shape[0]
+            return f"{op.kind} {'relu' if op.attrs['relu'] else 'no relu'} {M}x{N}x{K}"
+        return f"{op.kind} {'x'.join(map(str, ins[0].shape))}"
+
+    def op_flops(self, op: Op) -> int:
+        """2 M N K for a GEMM op (multiply-adds of its main loop), 0 otherwise."""
+        ins = op.inputs
+        if op.kind in ("linear", "gemm_gelu_bwd"):
+            return 2 * ins[0].shape[0] * ins[0].shape[1] * ins[1].shape[0]
+        if op.kind == "gemm":
+            a, b = ins
+            M, K = (a.shape[1], a.shape[0]) if op.attrs["trans_a"] else a.shape
+            N = b.shape[0] if op.attrs["trans_b"] else b.shape[1]
+            return 2 * M * N * K
+        if op.kind in ("w8a8", "w8a8_packed"):
+            return 2 * ins[0].shape[0] * ins[0].shape[1] * ins[2].shape[0]
+        return 0
+
+    def _run_op(self, q: Queue, op: Op):
+        T = self.t
+        ins = [T[v.name] for v in op.inputs]
+        outs = [T[v.name] for v in op.outputs]
+        if op.kind == "linear":
+            pre = T[op.attrs["pre"].name] if op.attrs["pre"] is not None else None
+            epi = {"none": _lib.EPI_NONE, "gelu": _lib.EPI_GELU, "relu": _lib.EPI_RELU}[op.attrs["act"]]
+            if op.attrs.get("packed") is not None:
+                kernels.gemm_bf16_packed(q, ins[0], T[op.attrs["packed"].name], outs[0], epi, pre)
             else:
-                raise NotImplementedError(op.kind)
+                kernels.gemm_bf16(q, ins[0], ins[1], outs[0], trans_a=False, trans_b=True, epilogue=epi,
+                                  pre_act=pre)
+        elif op.kind == "gemm":
+            kernels.gemm_bf16(q, ins[0], ins[1], outs[0], op.attrs["trans_a"], op.attrs["trans_b"], op.attrs["epi"],
+                              None, self.workspace)
+        elif op.kind == "mse":
+            loss = outs[0]
+            if len(outs) == 4:
+                kernels.mse_fwd_bwd(q, ins[0], ins[1], loss, outs[1], outs[2], outs[3])
+            else:
+                raise RuntimeError("mse without backward: call Graph.backward() or use the loss op's fused form")
+        elif op.kind == "gelu_bwd":
+            kernels.gelu_bwd(q, ins[0], ins[1], outs[0], outs[1])
+        elif op.kind == "gemm_gelu_bwd":
+            kernels.gemm_bf16_gelu_bwd(q, ins[0], ins[1], ins[2], outs[0], outs[1], op.attrs.get("packed", False))
+        elif op.kind == "cast":
+            kernels.cast(q, ins[0], outs[0])
+        elif op.kind == "transpose":
+            kernels.transpose(q, ins[0], outs[0])
+        elif op.kind == "quantize":
+            kernels.quantize_rows_i8(q, ins[0], outs[0], outs[1])
+        elif op.kind == "w8a8":
+            kernels.gemm_w8a8(q, ins[0], ins[1], ins[2], ins[3], outs[0], op.attrs["relu"], None, self.workspace)
+        elif op.kind == "w8a8_packed":
+            kernels.gemm_w8a8_packed(q, ins[0], ins[1], ins[2], ins[3], outs[0], op.attrs["relu"], None,
+                                     self.workspace)
+        else:
+            raise NotImplementedError(op.kind)
 
     def capture(self, q: Queue) -> "Step":
         """Records one run() into a hipGraph and returns it as a Step (.launch(q), .destroy()).
