@@ -74,8 +74,11 @@ def time_launches(q, dev, fn, reps, warmup=30, warmup_ms=25.0):
 def time_replays(q, dev, fn, steps, warmup, per_graph=1, warmup_ms=25.0):
     """Records `per_graph` consecutive calls of fn() into one hipGraph, replays it at least `warmup`
     times and for at least `warmup_ms` of wall time, then `steps` times; returns (ms per call from
-    HIP events on q's stream, wall ms per call)."""
+    HIP events on q's stream, wall ms per call).  fn() runs once eagerly first: a map chain the
+    library compiles at run time is compiled there (nothing is compiled while recording)."""
     from vernondsl_amd.rhi import Event
+    fn()
+    q.sync()
     with q.capture() as rec:
         for _ in range(per_graph):
             fn()
@@ -198,6 +201,121 @@ def bench_map_chain(dev, q, steps, warmup, do_cpu):
     for t_ in (tx, tb, ty):
         t_.free()
     return res
+
+
+def bench_map_chain_generic(dev, q, steps, warmup, do_cpu):
+    """The map chain as an op class: config 2's chain (which the library runs as a built-in
+    specialisation by default) in the generic interpreter and compiled at run time, and a second
+    chain of another shape, sigmoid(x) * colvec[row] + x^2 with a per-row operand, which has no
+    built-in specialisation, in both forms.  All on [8192][8192] f32, HBM GB/s from algorithmic
+    bytes."""
+    from vernondsl_amd import _lib, kernels, mapchain as mc, spec
+    from vernondsl_amd.rhi import Tensor
+    rows = cols = 8192
+    x, bias = spec.map_chain_inputs(rows, cols)
+    colv = np.ascontiguousarray(bias[:rows])
+    tx, tb, tc = Tensor.from_numpy(dev, q, x), Tensor.from_numpy(dev, q, bias), Tensor.from_numpy(dev, q, colv)
+    ty = Tensor(dev, (rows, cols), "f32")
+    q.sync()
+    out = []
+    p1 = mc.compile(spec.map_chain_expr())
+    p2 = mc.compile(mc.sigmoid(mc.Input(0)) * mc.Input(1, "col") + mc.Input(0) * mc.Input(0))
+    b1, b2 = spec.map_chain_bytes(rows, cols), 8 * rows * cols + 4 * rows
+    c2 = "sigmoid(x) * colvec[row] + x^2"
+    cases = (("config-2 chain, generic interpreter", p1, [tx, tb], 1, b1),
+             ("config-2 chain, compiled at run time (instead of the built-in specialisation)", p1, [tx, tb], 2, b1),
+             (c2 + ", generic interpreter", p2, [tx, tc], 1, b2),
+             (c2 + ", compiled at run time (the default for it)", p2, [tx, tc], 0, b2))
+    for name, prog, ins, mode, nbytes in cases:
+        _lib.call("vdsl_debug_map_chain_mode", mode)
+        per = 10
+        try:
+            ms, _ = time_replays(q, dev, lambda: kernels.map_chain(q, prog, ins, ty), max(1, steps // per),
+                                 max(1, warmup // per), per_graph=per)
+        finally:
+            _lib.call("vdsl_debug_map_chain_mode", 0)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res = {"config": "2-generic", "workload": f"map chain {name}, [{rows}][{cols}] f32", "metric": "achieved HBM GB/s",
+               "value": gbs, "unit": "GB/s", "ms_per_launch": ms, "parity": NOT_CHECKED,
+               "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                            "frac": gbs / PEAK_HBM_GBS, "bytes_per_launch": nbytes}}
+        if do_cpu:
+            from oracle import oracle
+            hx = [x, bias] if prog is p1 else [x, colv]
+            got = ty.numpy(q)
+            r = 4097
+            ref = oracle.map_chain(prog, hx, rows, cols, row_range=(r, r + 1))[0].astype(np.float64)
+            ok = np.all(np.abs(got[r].astype(np.float64) - ref) <= 1e-5 * (np.abs(ref) + 1.0))
+            res["parity"] = "ok (row 4097 against the oracle)" if ok else "FAIL"
+            sample = 512
+            t = time_cpu(lambda: oracle.map_chain(prog, hx, rows, cols, row_range=(0, sample)), min_s=1.0, max_reps=3)
+            res["cpu_baseline"] = {"value": nbytes * sample / rows / t / 1e9, "unit": "GB/s",
+                                   "cores": oracle.num_threads(), "kind": "port",
+                                   "sample": f"first {sample} of {rows} rows, oracle orc_map_chain"}
+        out.append(res)
+    for t_ in (tx, tb, tc, ty):
+        t_.free()
+    return out
+
+
+# ---- the vector vocabulary: MVP vertex transform and a swizzle (color.mlir, README.md:23-55) -------
+def bench_vecmat(dev, q, steps, warmup, do_cpu):
+    from vernondsl_amd import kernels, mapchain as mc
+    from vernondsl_amd.rhi import Tensor
+    out = []
+    r = np.random.default_rng(0x5EED0008)
+    # the vertex shader of color.mlir:10-39 over 2^24 vertices: vec3 in, 3 mat4 uniforms, vec4 out + varying
+    n = 1 << 24
+    pos = r.standard_normal((n, 3)).astype(np.float32)
+    mats = r.standard_normal((3, 4, 4)).astype(np.float32)
+    tp, tm = Tensor.from_numpy(dev, q, pos), Tensor.from_numpy(dev, q, mats)
+    to, tv = Tensor(dev, (n, 4), "f32"), Tensor(dev, (n, 3), "f32")
+    per = 10
+    ms, _ = time_replays(q, dev, lambda: kernels.vec_transform(q, tp, tm, to, tv), max(1, steps // per),
+                         max(1, warmup // per), per_graph=per)
+    nbytes = n * (12 + 16 + 12)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    res = {"config": "vec_transform", "workload": f"MVP vertex transform (color.mlir vertex_main) of {n} vec3 vertices, "
+           "3 mat4 uniforms, vec4 gl_Position + vec3 varying out", "metric": "achieved HBM GB/s", "value": gbs,
+           "unit": "GB/s", "ms_per_launch": ms, "parity": NOT_CHECKED,
+           "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                        "bytes_per_launch": nbytes, "traffic": measured_traffic("vec_transform")}}
+    if do_cpu:
+        from oracle import oracle
+        idx = np.array([0, 1, n // 2, n - 1])
+        got = to.numpy(q)
+        res["parity"] = "ok" if np.array_equal(got[idx], oracle.vec_transform(pos[idx], mats)) else "FAIL"
+        s = 1 << 22
+        t = time_cpu(lambda: oracle.vec_transform(pos[:s], mats), min_s=1.0, max_reps=3)
+        res["cpu_baseline"] = {"value": s * 40 / t / 1e9, "unit": "GB/s", "cores": oracle.num_threads(), "kind": "port",
+                               "sample": f"first {s} of {n} vertices, oracle orc_vec_transform"}
+    out.append(res)
+    for t_ in (tp, tm, to, tv):
+        t_.free()
+    # a swizzle: vec4 [4096][4096] -> .bgra
+    rows = cols = 4096
+    x = r.standard_normal((rows, cols, 4)).astype(np.float32)
+    prog = mc.compile(mc.VecInput(0, 4).bgra)
+    tx, ty = Tensor.from_numpy(dev, q, x), Tensor(dev, (rows, cols, 4), "f32")
+    ms, _ = time_replays(q, dev, lambda: kernels.map_chain_v(q, prog, [tx], ty), max(1, steps // per),
+                         max(1, warmup // per), per_graph=per)
+    nbytes = 2 * rows * cols * 16
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    res = {"config": "swizzle", "workload": f"swizzle .bgra of vec4 [{rows}][{cols}] (vdsl_op_map_chain_v)",
+           "metric": "achieved HBM GB/s", "value": gbs, "unit": "GB/s", "ms_per_launch": ms,
+           "parity": "ok" if np.array_equal(ty.numpy(q)[::511], x[::511][..., [2, 1, 0, 3]]) else "FAIL",
+           "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                        "bytes_per_launch": nbytes, "traffic": measured_traffic("swizzle")}}
+    if do_cpu:
+        from oracle import oracle
+        s = 512
+        t = time_cpu(lambda: oracle.map_chain_v(prog, [x], rows, cols, row_range=(0, s)), min_s=1.0, max_reps=3)
+        res["cpu_baseline"] = {"value": nbytes * s / rows / t / 1e9, "unit": "GB/s", "cores": oracle.num_threads(),
+                               "kind": "port", "sample": f"first {s} of {rows} rows, oracle orc_map_chain_v_rows"}
+    out.append(res)
+    tx.free()
+    ty.free()
+    return out
 
 
 # ---- config 1 ------------------------------------------------------------------------------------
@@ -387,6 +505,10 @@ def _traffic_kernels():
         "gemm_bf16": ("gemm_bf16_", 2 * (2048 * 4096 + 4096 * 4096 + 2048 * 4096) + 4 * 2048 * 4096),
         # int8 A, B and the two scale vectors read once; bf16 Y written once
         "gemm_w8a8": ("gemm_w8a8_", 512 * 8192 + 8192 * 8192 + 4 * (512 + 8192) + 2 * 512 * 8192),
+        # vec3 positions read, vec4 positions and vec3 varyings written (2^24 vertices)
+        "vec_transform": ("vec_transform_kernel", (1 << 24) * 40),
+        # vec4 [4096][4096] read and written
+        "swizzle": ("map_chain_v_kernel", 2 * 4096 * 4096 * 16),
     }
 
 
@@ -482,6 +604,18 @@ def run_kernel_only(dev, q, name, reps):
             exe.write(q, f"W{li}", w)
             exe.write(q, f"S{li}", sc)
         fn, ts = (lambda: exe.run(q)), [exe]
+    elif name == "vec_transform":
+        n = 1 << 24
+        tp, tm = Tensor(dev, (n, 3), "f32"), Tensor(dev, (3, 4, 4), "f32")
+        tp.buffer.fill_u32(q, 0x3F800000)
+        tm.buffer.fill_u32(q, 0x3F000000)
+        to, tv = Tensor(dev, (n, 4), "f32"), Tensor(dev, (n, 3), "f32")
+        fn, ts = (lambda: kernels.vec_transform(q, tp, tm, to, tv)), [tp, tm, to, tv]
+    elif name == "swizzle":
+        tx, ty = Tensor(dev, (4096, 4096, 4), "f32"), Tensor(dev, (4096, 4096, 4), "f32")
+        tx.buffer.fill_u32(q, 0x3F800000)
+        prog = mc.compile(mc.VecInput(0, 4).bgra)
+        fn, ts = (lambda: kernels.map_chain_v(q, prog, [tx], ty)), [tx, ty]
     elif name == "escape_time":
         p = kernels.escape_time_params(**spec.mandelbrot_params())
         out = Tensor(dev, (1024, 1024), "i32")
@@ -508,7 +642,8 @@ def main():
     # milliseconds after host-side setup, and a shorter warm-up reads the kernel up to 5% low
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline timings")
-    ap.add_argument("--only", type=int, default=0, help="run only the headline (2) or one extra config")
+    ap.add_argument("--only", type=int, default=0, help="run only the headline and one extra config "
+                    "(1, 3, 4, 5; 2: the generic map chains; 6: the vector ops)")
     ap.add_argument("--kernel", default="", help="run one kernel --reps times and exit (for rocprofv3 --pmc): "
                     "map_chain, softmax_f32, softmax_bf16, gemm_bf16, gemm_w8a8, escape_time, copy, c4_step, c5_step")
     ap.add_argument("--reps", type=int, default=20)
@@ -540,7 +675,8 @@ def main():
     head = bench_map_chain(dev, q, args.steps, args.warmup, do_cpu)
     log("bench: config 2", {k: v for k, v in head.items() if k != "cpu"})
     per_config = []
-    for fn, cid in ((bench_fractal, 1), (bench_softmax, 3), (bench_mlp, 4), (bench_w8a8, 5)):
+    for fn, cid in ((bench_map_chain_generic, 2), (bench_fractal, 1), (bench_softmax, 3), (bench_mlp, 4),
+                    (bench_w8a8, 5), (bench_vecmat, 6)):
         if args.only and args.only != cid:
             continue
         r = fn(dev, q, args.steps, args.warmup, do_cpu)

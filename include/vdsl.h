@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define VDSL_ABI_VERSION 1
+#define VDSL_ABI_VERSION 2
 
 typedef enum vdsl_status {
   VDSL_OK = 0,
@@ -243,10 +243,46 @@ typedef struct vdsl_map_input {
   int32_t dtype;        /* VDSL_F32 */
 } vdsl_map_input;
 
-/* out (f32 [rows][cols]) = r[out_reg] after running `code` for each element. */
+/* out (f32 [rows][cols]) = r[out_reg] after running `code` for each element.  A LOAD's `c` field
+ * must be 0 here (scalar inputs). */
 int vdsl_op_map_chain(vdsl_queue q, int64_t rows, int64_t cols, const vdsl_map_instr* code,
                       int32_t n_instr, const vdsl_map_input* inputs, int32_t n_inputs,
                       int32_t out_reg, vdsl_buffer out);
+
+/* ---- vector operands: the vernon dialect's vec2-4 vocabulary (source/README.md:23-55) ------- */
+/* A map-chain input whose elements are f32 vectors of `width` (1..4) components stored AoS
+ * (!vernon.vec2-4 element types): element e of a FULL input is the floats [e*width, e*width+width);
+ * a ROW input holds [cols][width], a COL input [rows][width], a SCALAR input [width]. */
+typedef struct vdsl_map_vinput {
+  vdsl_buffer buf;
+  int32_t bcast;        /* vdsl_broadcast (a vector counts as one element) */
+  int32_t dtype;        /* VDSL_F32 */
+  int32_t width;        /* components per element, 1..4 */
+  int32_t pad;
+} vdsl_map_vinput;
+
+/* The map chain over vector operands.  A LOAD (op = VDSL_MAP_LOAD, a = input, c = component)
+ * reads one component of its input's element: ExtractComponentOp (README.md:41-45) fused into the
+ * load; a swizzle (SwizzleOp, README.md:47-52) is several such loads, or the order of out_regs.
+ * out: f32 [rows][cols][out_width] (AoS, out_width 1..4); component k of each element is
+ * r[out_regs[k]] (tensor.from_elements of color.mlir:21,55).  Components are moved, never
+ * rounded: a chain of loads and stores only is an exact permutation. */
+int vdsl_op_map_chain_v(vdsl_queue q, int64_t rows, int64_t cols, const vdsl_map_instr* code,
+                        int32_t n_instr, const vdsl_map_vinput* inputs, int32_t n_inputs,
+                        const int32_t* out_regs, int32_t out_width, vdsl_buffer out);
+
+/* Batched vertex transform: the MVP chain of the reference's test shader (color.mlir:10-39:
+ * vec4(pos, 1.0), then linalg.matvec by model, view and proj) over n vertices.
+ *   pos:  f32 [n][in_width]; in_width 3 (extended to vec4(pos, 1.0), color.mlir:15-21) or 4;
+ *   mats: f32 [n_mats][4][4] row-major mat4 uniforms (!vernon.mat4<f32>), n_mats 1..3, applied in
+ *         order (model, view, proj): v <- M v with
+ *         out[i] = (((0 + M[i][0] v[0]) + M[i][1] v[1]) + M[i][2] v[2]) + M[i][3] v[3],
+ *         every product and sum rounded to f32 (linalg.matvec's mulf/addf accumulation into a
+ *         zero-initialised output, no contraction);
+ *   out:  f32 [n][4] (gl_Position);
+ *   varying (optional): f32 [n][in_width] = pos (the pass-through result of color.mlir:39). */
+int vdsl_op_vec_transform(vdsl_queue q, int64_t n, int32_t in_width, vdsl_buffer pos, int32_t n_mats,
+                          vdsl_buffer mats, vdsl_buffer out, vdsl_buffer varying);
 
 /* ========================================================================================== */
 /* Op class 3: row reductions + softmax (no reference code; north-star op class).             */
@@ -387,6 +423,22 @@ int vdsl_debug_fail_alloc_after(int64_t n);
  * it: the int8 split-K workspace depends on the configuration.  No counterpart in the reference
  * (which has no kernels); callers are tuning sweeps and the tests that cover every configuration. */
 int vdsl_debug_gemm_config(int32_t config);
+
+/* ---- map-chain forms (benchmarks and tests, host-side only) ---------------------------------- */
+/* A map chain (vdsl_op_map_chain, vdsl_op_map_chain_v) runs as a specialisation built into the
+ * library, as a kernel compiled at run time for the chain (cached per chain and device; the
+ * chain's immediates stay arguments), or in the generic interpreter; all three give the same
+ * bits.  mode 0 (default): built-in specialisation if one matches, else the compiled form for
+ * launches of at least 2^20 elements, else the interpreter; 1: the interpreter for every chain;
+ * 2: the compiled form for every chain (built-in specialisations skipped).  A chain not compiled
+ * before a queue starts recording a graph is recorded in the interpreter (nothing is compiled
+ * while recording); a chain whose compilation fails runs in the interpreter.  Also settable with
+ * the environment variable VDSL_MAP_MODE.  No counterpart in the reference; callers are
+ * benchmarks and the tests that compare the forms. */
+int vdsl_debug_map_chain_mode(int32_t mode);
+/* Counters since the library was loaded: launches in compiled form, compilations, failed
+ * compilations (any pointer may be NULL). */
+int vdsl_debug_map_chain_stats(int64_t* compiled_launches, int64_t* compiles, int64_t* failures);
 
 #ifdef __cplusplus
 }

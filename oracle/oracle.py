@@ -64,6 +64,9 @@ class MapInstr(C.Structure):
 _lib.orc_escape_time_rows.argtypes = [C.POINTER(EscapeTimeParams), _vp, C.c_int, C.c_int]
 _lib.orc_map_chain_rows.argtypes = [_i64, _i64, C.POINTER(MapInstr), C.c_int, C.POINTER(_vp), C.POINTER(C.c_int),
                                     C.c_int, C.c_int, _vp, _i64, _i64]
+_lib.orc_map_chain_v_rows.argtypes = [_i64, _i64, C.POINTER(MapInstr), C.c_int, C.POINTER(_vp), C.POINTER(C.c_int),
+                                      C.POINTER(C.c_int), C.c_int, C.POINTER(C.c_int), C.c_int, _vp, _i64, _i64]
+_lib.orc_vec_transform.argtypes = [_i64, C.c_int, _vp, C.c_int, _vp, _vp]
 _lib.orc_row_reduce_softmax_rows.argtypes = [_i64, _i64, C.c_int, _vp, _vp, _vp, _vp, _i64, _i64]
 _lib.orc_col_reduce.argtypes = [_i64, _i64, C.c_int, _vp, _vp, _vp]
 _lib.orc_gemm_bf16_rows.argtypes = [C.c_int, C.c_int, _i64, _i64, _i64, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _i64, _i64]
@@ -115,6 +118,36 @@ def map_chain(prog, inputs, rows: int, cols: int, row_range=None) -> np.ndarray:
     # The C routine indexes output rows absolutely; shift the base pointer by -r0 rows.
     base = out.ctypes.data - r0 * cols * 4
     _lib.orc_map_chain_rows(rows, cols, code, len(prog.code), ptrs, bc, len(arrs), prog.out_reg, _vp(base), r0, r1)
+    return out
+
+
+def map_chain_v(prog, inputs, rows: int, cols: int, row_range=None) -> np.ndarray:
+    """Vector-operand chain (orc_map_chain_v_rows): prog carries widths and out_regs; returns
+    [rows][cols][len(out_regs)] (or [rows][cols] for one output component) for rows [r0, r1)."""
+    code = (MapInstr * max(1, len(prog.code)))()
+    for i, (op, dst, a, b, c, imm) in enumerate(prog.code):
+        code[i].op, code[i].dst, code[i].a, code[i].b, code[i].c, code[i].imm = MAP_OPS[op], dst, a, b, c, imm
+    arrs = [np.ascontiguousarray(x, dtype=np.float32) for x in inputs]
+    n = max(1, len(arrs))
+    ptrs = (_vp * n)(*[a.ctypes.data for a in arrs])
+    bc = (C.c_int * n)(*[prog.bcast[k] for k in range(len(arrs))])
+    wd = (C.c_int * n)(*[prog.widths[k] for k in range(len(arrs))])
+    ow = len(prog.out_regs)
+    regs = (C.c_int * 4)(*(list(prog.out_regs) + [0] * (4 - ow)))
+    r0, r1 = row_range if row_range else (0, rows)
+    out = np.zeros((r1 - r0, cols, ow), dtype=np.float32)
+    base = out.ctypes.data - r0 * cols * ow * 4
+    _lib.orc_map_chain_v_rows(rows, cols, code, len(prog.code), ptrs, bc, wd, len(arrs), regs, ow, _vp(base), r0, r1)
+    return out if ow > 1 else out[:, :, 0]
+
+
+def vec_transform(pos: np.ndarray, mats: np.ndarray) -> np.ndarray:
+    """orc_vec_transform: pos f32 [n][3|4], mats f32 [k][4][4] -> f32 [n][4]."""
+    pos = np.ascontiguousarray(pos, np.float32)
+    mats = np.ascontiguousarray(mats, np.float32)
+    n, w = pos.shape
+    out = np.empty((n, 4), np.float32)
+    _lib.orc_vec_transform(n, w, _p(pos), mats.shape[0], _p(mats), _p(out))
     return out
 
 

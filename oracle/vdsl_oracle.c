@@ -17,6 +17,15 @@
  *                        forms, conjugate symmetry, and f64 brute force away from the boundary.
  *   orc_map_chain        no reference code.  Pinned against f64 numpy evaluation and the
  *                        special values x = 0 and |x| large.
+ *   orc_map_chain_v_rows vector operands (the vec2-4 / extract_component / swizzle vocabulary of
+ *                        source/README.md:23-55).  Pinned by permutation closed forms: a swizzle
+ *                        program equals numpy fancy indexing of the components, swizzles compose
+ *                        as permutations, extract_component after a swizzle picks the permuted
+ *                        component, and with width-1 operands it equals orc_map_chain.
+ *   orc_vec_transform    the MVP chain of color.mlir:10-39 (vec4(pos, 1) then three linalg.matvec).
+ *                        Pinned by identity, permutation, power-of-two scaling and translation
+ *                        matrices (exact in f32), small-integer matrices and positions (exact
+ *                        integer arithmetic), and numpy f64 within a rounding bound.
  *   orc_row_reduce_softmax / orc_col_reduce
  *                        no reference code.  Pinned by f64 sums, exact max, rows summing to 1,
  *                        constant row -> 1/cols, shift invariance, injected outlier argmax.
@@ -188,6 +197,59 @@ void orc_map_chain_rows(int64_t rows, int64_t cols, const vdsl_map_instr* code, 
 void orc_map_chain(int64_t rows, int64_t cols, const vdsl_map_instr* code, int n_instr, const float* const* in_ptrs,
                    const int* bcast, int n_inputs, int out_reg, float* out) {
   orc_map_chain_rows(rows, cols, code, n_instr, in_ptrs, bcast, n_inputs, out_reg, out, 0, rows);
+}
+
+/* Vector operands (vdsl_op_map_chain_v): input k holds elements of widths[k] components (AoS);
+ * a LOAD reads component `c` of its input's element; output element (r, c) is the out_width
+ * registers out_regs[0..out_width) in that order. */
+void orc_map_chain_v_rows(int64_t rows, int64_t cols, const vdsl_map_instr* code, int n_instr,
+                          const float* const* in_ptrs, const int* bcast, const int* widths, int n_inputs,
+                          const int* out_regs, int out_width, float* out, int64_t r0, int64_t r1) {
+  (void)rows;
+  (void)n_inputs;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = r0; r < r1; ++r) {
+    for (int64_t c = 0; c < cols; ++c) {
+      float reg[VDSL_MAP_MAX_REGS] = {0};
+      for (int pc = 0; pc < n_instr; ++pc) {
+        const vdsl_map_instr* s = &code[pc];
+        if (s->op == VDSL_MAP_LOAD) {
+          const int bc = bcast[s->a], w = widths[s->a];
+          const int64_t e = bc == VDSL_BCAST_FULL ? r * cols + c : bc == VDSL_BCAST_ROW ? c : bc == VDSL_BCAST_COL ? r : 0;
+          reg[s->dst] = in_ptrs[s->a][e * w + s->c];
+        } else {
+          reg[s->dst] = map_apply(s->op, reg[s->a], reg[s->b], reg[s->c], s->imm);
+        }
+      }
+      for (int k = 0; k < out_width; ++k) out[(r * cols + c) * out_width + k] = reg[out_regs[k]];
+    }
+  }
+}
+
+/* The MVP chain of color.mlir:10-39 over n vertices: v = vec4(pos, 1) (or pos for in_width 4),
+ * then for each of the n_mats row-major mat4s in order, v <- M v with
+ * out[i] = (((0 + M[i][0] v0) + M[i][1] v1) + M[i][2] v2) + M[i][3] v3 (f32 products and sums, the
+ * mulf/addf accumulation of linalg.matvec into a zero-initialised output). */
+void orc_vec_transform(int64_t n, int in_width, const float* pos, int n_mats, const float* mats, float* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t e = 0; e < n; ++e) {
+    float v[4] = {pos[e * in_width], pos[e * in_width + 1], pos[e * in_width + 2], 1.0f};
+    if (in_width == 4) v[3] = pos[e * in_width + 3];
+    for (int t = 0; t < n_mats; ++t) {
+      const float* m = mats + 16 * t;
+      float o[4];
+      for (int i = 0; i < 4; ++i) {
+        float acc = 0.0f;
+        for (int j = 0; j < 4; ++j) {
+          const float prod = m[4 * i + j] * v[j];
+          acc = acc + prod;
+        }
+        o[i] = acc;
+      }
+      for (int i = 0; i < 4; ++i) v[i] = o[i];
+    }
+    for (int i = 0; i < 4; ++i) out[e * 4 + i] = v[i];
+  }
 }
 
 /* ---- row reduce + softmax ---------------------------------------------------------------- */

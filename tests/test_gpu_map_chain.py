@@ -301,3 +301,119 @@ def test_random_exact_programs_end_to_end(dev, q, seed):
         assert np.array_equal(np.isnan(got), np.isnan(ref)), prog.code
         fin = ~np.isnan(ref)
         assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32)), prog.code
+
+
+# ---- the three forms of a chain: built-in specialisation, compiled at run time, interpreter ----------
+def _stats():
+    import ctypes
+    v = [ctypes.c_int64() for _ in range(3)]
+    _lib.call("vdsl_debug_map_chain_stats", *[ctypes.byref(x) for x in v])
+    return [x.value for x in v]
+
+
+def _in_mode(mode, fn):
+    _lib.call("vdsl_debug_map_chain_mode", mode)
+    try:
+        return fn()
+    finally:
+        _lib.call("vdsl_debug_map_chain_mode", 0)
+
+
+def test_config2_chain_same_bits_in_every_form(dev, q):
+    rows, cols = 96, 2048
+    x, bias = spec.map_chain_inputs(rows, cols)
+    prog = mc.compile(spec.map_chain_expr())
+    launches0, compiles0, failures0 = _stats()
+    forms = {m: _in_mode(m, lambda: run_chain(dev, q, prog, [x, bias], rows, cols)) for m in (0, 1, 2)}
+    launches1, compiles1, failures1 = _stats()
+    assert launches1 == launches0 + 1 and failures1 == failures0   # mode 2 ran the compiled kernel
+    for m in (1, 2):
+        assert np.array_equal(forms[m].view(np.uint32), forms[0].view(np.uint32)), f"mode {m}"
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_random_programs_compiled_equal_interpreted(dev, q, seed):
+    """Every random program (all opcodes, broadcasts, specials in the inputs) gives the same bits
+    compiled at run time as in the interpreter, NaN payloads included."""
+    rng = np.random.default_rng(3000 + seed)
+    for _ in range(5):
+        prog = _random_program(rng)
+        rows, cols = int(rng.integers(1, 40)), int(rng.choice([4, 64, 1028]))
+        inputs = _random_inputs(rng, prog, rows, cols)
+        a = _in_mode(1, lambda: run_chain(dev, q, prog, inputs, rows, cols))
+        before = _stats()[0]
+        b = _in_mode(2, lambda: run_chain(dev, q, prog, inputs, rows, cols))
+        assert _stats()[0] == before + 1
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), prog.code
+
+
+def run_v(dev, q, prog, inputs, rows, cols):
+    ts = [Tensor.from_numpy(dev, q, np.ascontiguousarray(a, np.float32)) for a in inputs]
+    ow = len(prog.out_regs)
+    out = Tensor(dev, (rows, cols, ow) if ow > 1 else (rows, cols), "f32")
+    out.buffer.fill_u32(q, 0x7FC00001)
+    kernels.map_chain_v(q, prog, ts, out)
+    got = out.numpy(q)
+    for t in ts + [out]:
+        t.free()
+    return got
+
+
+def test_vector_chains_compiled_equal_interpreted(dev, q):
+    rng = np.random.default_rng(3100)
+    rows, cols = 45, 777
+    full = rng.standard_normal((rows, cols, 3)).astype(np.float32)
+    rowb = rng.standard_normal((cols, 4)).astype(np.float32)
+    a, b = mc.VecInput(0, 3), mc.VecInput(1, 4, "row")
+    for out in (mc.vec(a.zyx, 1.0), b.bgra, mc.vec(mc.tanh(a.xy * b.ba), a.z - b.r), a.y):
+        prog = mc.compile(out)
+        ins = []
+        for k in range(prog.n_inputs):   # an input the program never reads is declared width 1, full
+            if (prog.bcast[k], prog.widths[k]) == (_lib.BCAST_FULL, 3):
+                ins.append(full)
+            elif (prog.bcast[k], prog.widths[k]) == (_lib.BCAST_ROW, 4):
+                ins.append(rowb)
+            else:
+                ins.append(np.zeros((rows, cols), np.float32))
+        i = _in_mode(1, lambda: run_v(dev, q, prog, ins, rows, cols))
+        before = _stats()[0]
+        c = _in_mode(2, lambda: run_v(dev, q, prog, ins, rows, cols))
+        assert _stats()[0] == before + 1
+        assert np.array_equal(i.view(np.uint32), c.view(np.uint32))
+        assert np.array_equal(i, oracle.map_chain_v(prog, ins, rows, cols)) or "tanh" in str(prog.code)
+
+
+def test_recording_uses_compiled_chains_only_if_compiled_before(dev, q):
+    """While a queue records a graph nothing is compiled: a chain first seen there is recorded in
+    the interpreter; one compiled earlier is recorded in compiled form.  Replays equal eager runs."""
+    rows, cols = 64, 1024
+    x = np.random.default_rng(3200).standard_normal((rows, cols)).astype(np.float32)
+    tx, ty = Tensor.from_numpy(dev, q, x), Tensor(dev, (rows, cols), "f32")
+    fresh = mc.compile(mc.sigmoid(mc.Input(0)) * 0.375 + mc.Input(0) * mc.Input(0) * 0.125)
+    seen = mc.compile(mc.relu(mc.Input(0)) * 1.25 - mc.Input(0) * 0.0625)
+    try:
+        _lib.call("vdsl_debug_map_chain_mode", 2)
+        kernels.map_chain(q, seen, [tx], ty)      # compiled eagerly
+        eager_seen = ty.numpy(q)
+        launches0, compiles0, _ = _stats()
+        with q.capture() as rec:
+            kernels.map_chain(q, fresh, [tx], ty)
+        g1 = rec.graph
+        assert _stats()[:2] == [launches0, compiles0]   # interpreter, nothing compiled
+        with q.capture() as rec:
+            kernels.map_chain(q, seen, [tx], ty)
+        g2 = rec.graph
+        assert _stats()[:2] == [launches0 + 1, compiles0]
+    finally:
+        _lib.call("vdsl_debug_map_chain_mode", 0)
+    for _ in range(3):
+        ty.buffer.fill_u32(q, 0x7FC00000)
+        g1.launch(q)
+        q.sync()
+        assert np.array_equal(ty.numpy(q), _in_mode(1, lambda: run_chain(dev, q, fresh, [x], rows, cols)))
+        ty.buffer.fill_u32(q, 0x7FC00000)
+        g2.launch(q)
+        q.sync()
+        assert np.array_equal(ty.numpy(q), eager_seen)
+    for t in (g1, g2, tx, ty):
+        t.destroy() if hasattr(t, "launch") else t.free()

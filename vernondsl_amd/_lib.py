@@ -90,6 +90,11 @@ class MapInput(C.Structure):
     _fields_ = [("buf", C.c_void_p), ("bcast", C.c_int32), ("dtype", C.c_int32)]
 
 
+class MapVInput(C.Structure):
+    _fields_ = [("buf", C.c_void_p), ("bcast", C.c_int32), ("dtype", C.c_int32), ("width", C.c_int32),
+                ("pad", C.c_int32)]
+
+
 _vp = C.c_void_p
 _i32 = C.c_int32
 _i64 = C.c_int64
@@ -125,6 +130,11 @@ PROTOTYPES = {
     "vdsl_event_destroy": (C.c_int, [_vp]),
     "vdsl_op_escape_time": (C.c_int, [_vp, C.POINTER(EscapeTimeParams), _vp]),
     "vdsl_op_map_chain": (C.c_int, [_vp, _i64, _i64, C.POINTER(MapInstr), _i32, C.POINTER(MapInput), _i32, _i32, _vp]),
+    "vdsl_op_map_chain_v": (C.c_int, [_vp, _i64, _i64, C.POINTER(MapInstr), _i32, C.POINTER(MapVInput), _i32,
+                                      C.POINTER(_i32), _i32, _vp]),
+    "vdsl_op_vec_transform": (C.c_int, [_vp, _i64, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "vdsl_debug_map_chain_mode": (C.c_int, [_i32]),
+    "vdsl_debug_map_chain_stats": (C.c_int, [C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i64)]),
     "vdsl_op_row_reduce_softmax": (C.c_int, [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp]),
     "vdsl_op_col_reduce": (C.c_int, [_vp, _i64, _i64, _i32, _vp, _vp, _vp]),
     "vdsl_gemm_bf16_workspace_bytes": (C.c_int, [_i32, _i32, _i64, _i64, _i64, C.POINTER(_sz)]),

@@ -7,6 +7,7 @@
 #include <atomic>
 #include <string>
 
+#include "fmath.h"
 #include "vdsl.h"
 
 // ---- handle objects ------------------------------------------------------------------------
@@ -103,9 +104,6 @@ inline size_t nbytes(int64_t a, int64_t b, int64_t c = 1) {
 // ---- device-side helpers -------------------------------------------------------------------
 namespace vdsl {
 
-// Clang vector types (what the nontemporal and MFMA builtins accept).
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
@@ -118,7 +116,6 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 }
 // Two values converted by one v_cvt_pk_bf16_f32: lo in bits 0-15, hi in bits 16-31.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const f32x2_t v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
@@ -130,21 +127,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
   return v;
 }
-// exp in f32, Cody-Waite style: n log2(e) = t + r with t = fl(n * log2e) and r its rounding
-// residual (exact through an fma, plus the low part of log2 e), then e^n = 2^t (1 + r ln 2) with
-// the hardware exp2.  Where t is not finite (n = +-inf, NaN) or 2^t overflows, 2^t itself is the
-// answer (inf, 0 or NaN) and the correction, which would form inf * 0, is skipped.  Relative
-// error below 2e-7 in an f32 emulation of these steps (against exp in f64 over [-87, 88]), plus
-// the hardware exp2's 1 ulp.
-__device__ __forceinline__ float exp_fast(float n) {
-  const float t = n * 1.4426950408889634f;
-  float r = __builtin_fmaf(n, 1.4426950408889634f, -t);
-  r = __builtin_fmaf(n, 1.92596299e-08f, r);  // log2(e) - fl(log2(e))
-  const float e = __builtin_amdgcn_exp2f(t);
-  const float c = __builtin_fmaf(e, r * 0.6931471805599453f, e);
-  return (__builtin_isfinite(t) && e != __builtin_inff()) ? c : e;
-}
-
 // erfc(x) by the Chebyshev-fitted form of Numerical Recipes (Press et al., 2nd ed., sec. 6.2,
 // "erfcc"): erfc(|x|) = t exp(-x^2 + P(t)), t = 1 / (1 + |x|/2), P a degree-9 polynomial, with
 // fractional error below 1.2e-7 for every x; erfc(-x) = 2 - erfc(x).  Branch-free (the library

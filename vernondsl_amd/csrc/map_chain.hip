@@ -1,92 +1,36 @@
-// Op class 2: fused elementwise / broadcast map chains on gfx950.
+// Op class 2: fused elementwise / broadcast map chains on gfx950 (host side).
 //
 // The reference has no elementwise code (the only compute is fractal.py:16-25); this op class
 // comes from the north-star spec.  A chain is a straight-line register program
 // (vdsl_map_instr, include/vdsl.h) evaluated once per output element, so a whole expression
 // such as tanh(a*x + b) * exp(-x^2) + bias[col] costs one HBM read of each operand and one
-// write of the result.
+// write of the result.  The device code is mapchain_kern.h.
 //
-// Mapping: the tensor is [rows][cols] row-major.  A block of 256 lanes spans 256 float4 column
-// slots (1024 columns) of R consecutive rows, so every wave reads 1 KiB contiguous per row with
-// 16-byte loads, a row-broadcast operand (VDSL_BCAST_ROW, e.g. a bias) is loaded once per lane
-// and reused for all R rows, and all R rows' loads are issued before any arithmetic.
-//
-// One interpreter serves two instantiations:
-//   - generic: the program is a kernel argument, executed with a uniform (scalar-branch)
-//     dispatch and uniform register indices;
-//   - fixed: the program is a compile-time table (ProgTanhExpBias below); the same interpreter is
-//     fully unrolled and constant-folded into straight-line code.  A runtime chain whose opcodes,
-//     register indices and input broadcasts equal a table entry runs this version; its
-//     immediates still come from the runtime program.
+// A chain runs in one of three forms, all from the same source and bit-identical:
+//   - a compile-time specialisation built into the library (ProgTanhExpBias, config 2's chain),
+//     chosen when a runtime chain's opcodes, registers and broadcasts equal its table;
+//   - a kernel compiled at run time for the chain (hiprtc, for the device's architecture, with the
+//     library's own compile flags): the chain becomes a compile-time table and the interpreter
+//     unrolls into straight-line code.  Compiled once per distinct chain and device (the
+//     immediates are kernel arguments, not part of the compiled code), for launches of at least
+//     kCompileMinElements elements, never while the queue is recording a graph;
+//   - the generic interpreter, a kernel argument program with uniform dispatch: small launches,
+//     chains first seen while recording, and the fallback if run-time compilation fails.
+// vdsl_debug_map_chain_mode selects the interpreter or the compiled form for every chain.
 
-#include <type_traits>
-#include <utility>
+#include <hip/hiprtc.h>
+
+#include <cstdlib>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
 
 #include "common.h"
+#include "mapchain_kern.h"
 
 namespace vdsl {
 namespace {
-
-struct MapProg {
-  vdsl_map_instr code[VDSL_MAP_MAX_INSTR];
-  int32_t n;
-  int32_t out_reg;
-};
-
-struct MapIn {
-  const float* p[VDSL_MAP_MAX_INPUTS];
-  int32_t bcast[VDSL_MAP_MAX_INPUTS];
-  int32_t n;
-};
-
-// tanh in f32 without the argument-range branches of the library tanhf (which diverge per lane):
-//   |u| < 0.4:  Taylor series u (1 + z (c1 + z (c2 + ... + z c5))), z = u^2, with the exact
-//               coefficients c_k of tanh's expansion (-1/3, 2/15, -17/315, 62/2835, -1382/155925);
-//               the first omitted term is below 1e-7 of the result there;
-//   otherwise:  sign(u) (1 - 2 / (e^(2|u|) + 1)), whose cancellation costs at most a few ulp once
-//               tanh(|u|) >= 0.38 (e^(2|u|) overflows to inf for large |u|, giving exactly 1).
-// Both branches are evaluated and selected.  Relative error against tanh in f64: below 1.8e-7 in
-// an f32 emulation of the same steps, plus the hardware exp2 / reciprocal (1 ulp each).
-__device__ __forceinline__ float tanh_fast(float u) {
-  const float a = fabsf(u);
-  const float z = u * u;
-  float p = -0.0088632358238101f;                  // -1382/155925
-  p = __builtin_fmaf(p, z, 0.021869488060474396f);   // 62/2835
-  p = __builtin_fmaf(p, z, -0.05396825447678566f);   // -17/315
-  p = __builtin_fmaf(p, z, 0.13333334028720856f);    // 2/15
-  p = __builtin_fmaf(p, z, -0.3333333432674408f);    // -1/3
-  const float small = __builtin_fmaf(u * z, p, u);
-  const float e = __builtin_amdgcn_exp2f(a * 2.8853900817779268f);  // e^(2|u|) = 2^(2|u| log2 e)
-  const float big = __builtin_copysignf(__builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f), u);
-  return a < 0.4f ? small : big;
-}
-
-__device__ __forceinline__ float apply_op(int op, float a, float b, float c, float imm) {
-  switch (op) {
-    case VDSL_MAP_CONST: return imm;
-    case VDSL_MAP_MOV: return a;
-    case VDSL_MAP_NEG: return -a;
-    case VDSL_MAP_ABS: return fabsf(a);
-    case VDSL_MAP_SQUARE: return a * a;
-    case VDSL_MAP_EXP: return exp_fast(a);
-    case VDSL_MAP_LOG: return logf(a);
-    case VDSL_MAP_TANH: return tanh_fast(a);
-    case VDSL_MAP_SIGMOID: return 1.0f / (1.0f + exp_fast(-a));
-    case VDSL_MAP_RELU: return a > 0.0f ? a : 0.0f;
-    case VDSL_MAP_SQRT: return sqrtf(a);
-    case VDSL_MAP_RECIP: return 1.0f / a;
-    case VDSL_MAP_ADD: return a + b;
-    case VDSL_MAP_SUB: return a - b;
-    case VDSL_MAP_MUL: return a * b;
-    case VDSL_MAP_DIV: return a / b;
-    case VDSL_MAP_MAX: return fmaxf(a, b);
-    case VDSL_MAP_MIN: return fminf(a, b);
-    case VDSL_MAP_FMA: return __builtin_fmaf(a, b, c);
-    case VDSL_MAP_MUL_IMM: return a * imm;
-    case VDSL_MAP_ADD_IMM: return a + imm;
-    default: return 0.0f;
-  }
-}
 
 // Compile-time programs.  Each lists its opcodes/registers, input broadcasts and output register.
 struct ProgTanhExpBias {
@@ -110,175 +54,16 @@ struct ProgTanhExpBias {
   };
 };
 
-struct GenericProgram {};  // marker: program comes from the kernel argument
-
-template <int VEC>
-struct Vec;
-template <>
-struct Vec<4> {
-  using T = float4;
-  __device__ static __forceinline__ void to(const T& v, float (&o)[4]) { o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w; }
-  __device__ static __forceinline__ T from(const float (&o)[4]) { return make_float4(o[0], o[1], o[2], o[3]); }
-};
-template <>
-struct Vec<1> {
-  using T = float;
-  __device__ static __forceinline__ void to(const T& v, float (&o)[1]) { o[0] = v; }
-  __device__ static __forceinline__ T from(const float (&o)[1]) { return o[0]; }
-};
-
-// Loads input k for a VEC-wide element group at (row, col).  IDX is the index type of the launch
-// (32-bit whenever every element offset fits, which saves the 64-bit address arithmetic).
-template <int VEC, class IDX>
-__device__ __forceinline__ void load_input(const float* __restrict__ p, int bcast, IDX row, IDX col, IDX cols,
-                                           float (&o)[VEC]) {
-  using V = Vec<VEC>;
-  if (bcast == VDSL_BCAST_FULL) {
-    // Streamed once: a nontemporal load keeps it from displacing reused data (the broadcast
-    // operands) in the caches.
-    if constexpr (VEC == 4) {
-      const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + row * cols + col));
-      o[0] = v[0]; o[1] = v[1]; o[2] = v[2]; o[3] = v[3];
-    } else {
-      o[0] = __builtin_nontemporal_load(p + row * cols + col);
-    }
-  } else if (bcast == VDSL_BCAST_ROW) {
-    V::to(*reinterpret_cast<const typename V::T*>(p + col), o);
-  } else {
-    const float s = (bcast == VDSL_BCAST_COL) ? p[row] : p[0];
-#pragma unroll
-    for (int k = 0; k < VEC; ++k) o[k] = s;
-  }
-}
-
-// Inputs whose value does not depend on the row (broadcast along rows, or a scalar).
-__device__ __forceinline__ bool row_invariant(int bcast) { return bcast == VDSL_BCAST_ROW || bcast == VDSL_BCAST_SCALAR; }
-
-template <class P, int VEC, int PC>
-__device__ __forceinline__ void fixed_step(const MapProg& rt, const float (&in)[VDSL_MAP_MAX_INPUTS][VEC],
-                                           float (&r)[VDSL_MAP_MAX_REGS][VEC]) {
-  constexpr vdsl_map_instr s = P::code[PC];
-  if constexpr (s.op == VDSL_MAP_LOAD) {
-#pragma unroll
-    for (int k = 0; k < VEC; ++k) r[s.dst][k] = in[s.a][k];
-  } else {
-    const float imm = rt.code[PC].imm;
-#pragma unroll
-    for (int k = 0; k < VEC; ++k) r[s.dst][k] = apply_op(s.op, r[s.a][k], r[s.b][k], r[s.c][k], imm);
-  }
-}
-
-template <class P, int VEC, int... PC>
-__device__ __forceinline__ void run_fixed(const MapProg& rt, const float (&in)[VDSL_MAP_MAX_INPUTS][VEC],
-                                          float (&r)[VDSL_MAP_MAX_REGS][VEC], std::integer_sequence<int, PC...>) {
-  (fixed_step<P, VEC, PC>(rt, in, r), ...);
-}
-
-template <class P, int VEC>
-__device__ __forceinline__ void run_program(const MapProg& rt, const float (&in)[VDSL_MAP_MAX_INPUTS][VEC],
-                                            float (&r)[VDSL_MAP_MAX_REGS][VEC]) {
-  if constexpr (!std::is_same<P, GenericProgram>::value) {
-    run_fixed<P, VEC>(rt, in, r, std::make_integer_sequence<int, P::n>{});
-  } else {
-#pragma unroll 1
-    for (int pc = 0; pc < rt.n; ++pc) {
-      const vdsl_map_instr s = rt.code[pc];
-      if (s.op == VDSL_MAP_LOAD) {
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) r[s.dst][k] = in[s.a][k];
-      } else {
-        float t[VEC];
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) t[k] = apply_op(s.op, r[s.a][k], r[s.b][k], r[s.c][k], s.imm);
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) r[s.dst][k] = t[k];
-      }
-    }
-  }
-}
-
-// Broadcast mode of input k: a compile-time constant for fixed programs.
-template <class P>
-__device__ __forceinline__ int input_bcast(const MapIn& in, int k) {
-  if constexpr (std::is_same<P, GenericProgram>::value) return in.bcast[k];
-  else return P::bcast_of(k);
-}
-
-// R rows of one thread's column group: every row's loads, then each row's program and store.
-// GUARD: rows past `rows` are skipped (the last, partial group of a launch).
-template <class P, int VEC, int R, bool GUARD, class IDX>
-__device__ __forceinline__ void map_chain_rows(const MapProg& rt, const MapIn& in, float* __restrict__ out, IDX rows, IDX cols,
-                                               IDX row0, IDX col, int n_in, int out_reg,
-                                               const float (&vfix)[VDSL_MAP_MAX_INPUTS][VEC]) {
-  float vin[R][VDSL_MAP_MAX_INPUTS][VEC];
-#pragma unroll
-  for (int u = 0; u < R; ++u) {
-    const IDX row = row0 + u;
-    if (!GUARD || row < rows) {
-#pragma unroll
-      for (int k = 0; k < VDSL_MAP_MAX_INPUTS; ++k) {
-        if (k < n_in) {
-          const int bc = input_bcast<P>(in, k);
-          if (row_invariant(bc)) {
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) vin[u][k][e] = vfix[k][e];
-          } else {
-            load_input<VEC, IDX>(in.p[k], bc, row, col, cols, vin[u][k]);
-          }
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < R; ++u) {
-    const IDX row = row0 + u;
-    if (!GUARD || row < rows) {
-      float r[VDSL_MAP_MAX_REGS][VEC];
-#pragma unroll
-      for (int g = 0; g < VDSL_MAP_MAX_REGS; ++g)
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) r[g][k] = 0.0f;
-      run_program<P, VEC>(rt, vin[u], r);
-      if constexpr (VEC == 4) {
-        const f32x4 v = {r[out_reg][0], r[out_reg][1], r[out_reg][2], r[out_reg][3]};
-        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(out + row * cols + col));
-      } else {
-        __builtin_nontemporal_store(r[out_reg][0], out + row * cols + col);
-      }
-    }
-  }
-}
-
-// One thread per VEC-wide column group; the block's threads cover 256 VEC columns and step over R
-// rows at a time (all R rows' loads issued before any compute).  Row-invariant inputs are loaded
-// once per thread, not once per row.
+// The kernels built into the library: thin wrappers around the shared bodies.
 template <class P, int VEC, int R, class IDX>
 __global__ __launch_bounds__(256) void map_chain_kernel(MapProg rt, MapIn in, float* __restrict__ out, IDX rows, IDX cols) {
-  const IDX col = (static_cast<IDX>(blockIdx.x) * 256 + static_cast<IDX>(threadIdx.x)) * VEC;
-  if (col >= cols) return;
-  int n_in, out_reg;
-  if constexpr (std::is_same<P, GenericProgram>::value) {
-    n_in = in.n;
-    out_reg = rt.out_reg;
-  } else {
-    n_in = P::n_inputs;
-    out_reg = P::out_reg;
-  }
-  float vfix[VDSL_MAP_MAX_INPUTS][VEC];
-#pragma unroll
-  for (int k = 0; k < VDSL_MAP_MAX_INPUTS; ++k) {
-    if (k < n_in) {
-      const int bc = input_bcast<P>(in, k);
-      if (row_invariant(bc)) load_input<VEC, IDX>(in.p[k], bc, IDX(0), col, cols, vfix[k]);
-    }
-  }
+  map_chain_body<P, VEC, R, IDX>(rt, in, out, rows, cols);
+}
 
-  for (IDX row0 = static_cast<IDX>(blockIdx.y) * R; row0 < rows; row0 += static_cast<IDX>(gridDim.y) * R) {
-    // A whole group of R rows takes the path without per-row guards: with them the compiler
-    // waits for every row's loads before computing the first row.
-    if (row0 + R <= rows) map_chain_rows<P, VEC, R, false>(rt, in, out, rows, cols, row0, col, n_in, out_reg, vfix);
-    else map_chain_rows<P, VEC, R, true>(rt, in, out, rows, cols, row0, col, n_in, out_reg, vfix);
-  }
+template <class P, int R, class IDX>
+__global__ __launch_bounds__(256) void map_chain_v_kernel(MapProg rt, MapVIn in, MapVOut vo, float* __restrict__ out,
+                                                          IDX rows, IDX cols) {
+  map_chain_v_body<P, R, IDX>(rt, in, vo, out, rows, cols);
 }
 
 template <class P>
@@ -309,22 +94,248 @@ bool matches(const MapProg& rt, const MapIn& in) {
   return true;
 }
 
-// 32-bit indices when every offset the kernel forms (row * cols + col, and row0 plus a grid's
-// worth of rows) stays far below 2^31.
-template <class P, int VEC, int R>
-int launch(const MapProg& rt, const MapIn& in, float* out, int64_t rows, int64_t cols, hipStream_t s) {
-  const int64_t slots = (cols + VEC - 1) / VEC;
+// Launch geometry: VEC columns per lane, 256 lanes per block, R rows per step, at most 65535
+// blocks along the rows (the kernels stride over the rest).  32-bit indices when every offset the
+// kernel forms (row * cols + col, and row0 plus a grid's worth of rows) stays far below 2^31.
+struct Geometry {
+  dim3 grid;
+  bool idx32;
+};
+
+int geometry(int vec, int r, int comps, int64_t rows, int64_t cols, Geometry& g) {
+  const int64_t slots = (cols + vec - 1) / vec;
   const int64_t gx = (slots + 255) / 256;
-  int64_t gy = (rows + R - 1) / R;
+  int64_t gy = (rows + r - 1) / r;
   if (gy > 65535) gy = 65535;
   if (gx > 0x7fffffff) return fail(VDSL_ERR_UNSUPPORTED, "map chain: cols too large");
-  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
-  if (rows * (cols + 256 * VEC) <= (int64_t{1} << 30) && rows <= (int64_t{1} << 30))
-    hipLaunchKernelGGL((map_chain_kernel<P, VEC, R, int32_t>), grid, dim3(256), 0, s, rt, in, out, static_cast<int32_t>(rows),
+  g.grid = dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+  g.idx32 = rows * (cols + 256 * vec) * comps <= (int64_t{1} << 30) && rows <= (int64_t{1} << 28);
+  return VDSL_OK;
+}
+
+template <class P, int VEC, int R>
+int launch(const MapProg& rt, const MapIn& in, float* out, int64_t rows, int64_t cols, hipStream_t s) {
+  Geometry g;
+  VDSL_TRY(geometry(VEC, R, 1, rows, cols, g));
+  if (g.idx32)
+    hipLaunchKernelGGL((map_chain_kernel<P, VEC, R, int32_t>), g.grid, dim3(256), 0, s, rt, in, out, static_cast<int32_t>(rows),
                        static_cast<int32_t>(cols));
   else
-    hipLaunchKernelGGL((map_chain_kernel<P, VEC, R, int64_t>), grid, dim3(256), 0, s, rt, in, out, rows, cols);
+    hipLaunchKernelGGL((map_chain_kernel<P, VEC, R, int64_t>), g.grid, dim3(256), 0, s, rt, in, out, rows, cols);
   return check_launch("map_chain_kernel");
+}
+
+constexpr int kRowsV = 4;  // rows per lane step of the vector kernels
+
+int launch_v(const MapProg& rt, const MapVIn& in, const MapVOut& vo, float* out, int64_t rows, int64_t cols, hipStream_t s) {
+  Geometry g;
+  VDSL_TRY(geometry(1, kRowsV, 4, rows, cols, g));
+  if (g.idx32)
+    hipLaunchKernelGGL((map_chain_v_kernel<GenericProgram, kRowsV, int32_t>), g.grid, dim3(256), 0, s, rt, in, vo, out,
+                       static_cast<int32_t>(rows), static_cast<int32_t>(cols));
+  else
+    hipLaunchKernelGGL((map_chain_v_kernel<GenericProgram, kRowsV, int64_t>), g.grid, dim3(256), 0, s, rt, in, vo, out, rows,
+                       cols);
+  return check_launch("map_chain_v_kernel");
+}
+
+// ---- mode switch -------------------------------------------------------------------------------------
+enum { kModeAuto = 0, kModeInterpret = 1, kModeCompile = 2 };
+std::atomic<int> g_mode{-1};  // -1: not yet read from VDSL_MAP_MODE
+
+int map_mode() {
+  int v = g_mode.load();
+  if (v < 0) {
+    const char* e = std::getenv("VDSL_MAP_MODE");
+    int init = e ? std::atoi(e) : kModeAuto;
+    if (init < kModeAuto || init > kModeCompile) init = kModeAuto;
+    g_mode.compare_exchange_strong(v, init);
+    v = g_mode.load();
+  }
+  return v;
+}
+
+// ---- chains compiled at run time --------------------------------------------------------------------
+// Launches of fewer elements run the interpreter: they are over in microseconds, and compiling
+// costs a fraction of a second once per chain.
+constexpr int64_t kCompileMinElements = int64_t{1} << 20;
+constexpr int kMaxCompiledPerDevice = 512;
+constexpr int kMaxDevices = 64;
+
+// The text of vdsl.h, fmath.h and mapchain_kern.h (generated by the Makefile), handed to hiprtc as
+// in-memory headers together with minimal stddef.h / stdint.h (hiprtc has no C library headers).
+#include "embedded_src.inc"
+const char kStubStddef[] = "typedef decltype(sizeof(0)) size_t;\n";
+const char kStubStdint[] =
+    "typedef signed char int8_t; typedef unsigned char uint8_t; typedef short int16_t;\n"
+    "typedef unsigned short uint16_t; typedef int int32_t; typedef unsigned int uint32_t;\n"
+    "typedef long long int64_t; typedef unsigned long long uint64_t;\n";
+
+struct Compiled {
+  hipModule_t mod = nullptr;
+  hipFunction_t f32 = nullptr, f64 = nullptr;  // entries with 32- and 64-bit indices
+  bool failed = false;
+};
+
+std::mutex g_jit_mu;
+std::unordered_map<std::string, Compiled> g_jit[kMaxDevices];
+std::atomic<int64_t> g_jit_launches{0}, g_jit_compiles{0}, g_jit_failures{0};
+
+// The fixed-program table of a chain, as C++ source; it names the kernel completely (with the entry
+// points), so it is also the cache key.
+std::string program_source(const MapProg& rt, int n_inputs, const int32_t* bcast, const int32_t* widths,
+                           const int32_t* out_regs, int out_width, bool vector) {
+  std::string s = "#include \"mapchain_kern.h\"\nnamespace vdsl {\nstruct JitProg {\n";
+  s += "  static constexpr int n = " + std::to_string(rt.n) + ";\n";
+  s += "  static constexpr int n_inputs = " + std::to_string(n_inputs) + ";\n";
+  s += "  static constexpr int out_reg = " + std::to_string(rt.out_reg) + ";\n";
+  s += "  static constexpr int out_width = " + std::to_string(out_width) + ";\n";
+  auto table = [&](const char* name, const int32_t* v, int cnt) {
+    s += std::string("  static constexpr int ") + name + "[4] = {";
+    for (int k = 0; k < 4; ++k) s += std::to_string(k < cnt ? v[k] : 0) + (k < 3 ? ", " : "};\n");
+  };
+  table("bcast_tab", bcast, n_inputs);
+  table("width_tab", widths, n_inputs);
+  table("out_regs", out_regs, out_width);
+  s += "  __host__ __device__ static constexpr int bcast_of(int k) { return bcast_tab[k]; }\n";
+  s += "  __host__ __device__ static constexpr int width_of(int k) { return width_tab[k]; }\n";
+  s += "  static constexpr vdsl_map_instr code[VDSL_MAP_MAX_INSTR] = {\n";
+  for (int pc = 0; pc < rt.n; ++pc) {
+    const vdsl_map_instr& c = rt.code[pc];
+    s += "    {" + std::to_string(c.op) + ", " + std::to_string(c.dst) + ", " + std::to_string(c.a) + ", " +
+         std::to_string(c.b) + ", " + std::to_string(c.c) + ", {0, 0, 0}, 0.f},\n";
+  }
+  s += "  };\n};\n}  // namespace vdsl\n";
+  if (!vector) {
+    s += "extern \"C\" __global__ __launch_bounds__(256) void vdsl_map_jit32(vdsl::MapProg rt, vdsl::MapIn in, "
+         "float* __restrict__ out, int rows, int cols) {\n"
+         "  vdsl::map_chain_body<vdsl::JitProg, 4, 2, int>(rt, in, out, rows, cols);\n}\n";
+    s += "extern \"C\" __global__ __launch_bounds__(256) void vdsl_map_jit64(vdsl::MapProg rt, vdsl::MapIn in, "
+         "float* __restrict__ out, long long rows, long long cols) {\n"
+         "  vdsl::map_chain_body<vdsl::JitProg, 4, 2, long long>(rt, in, out, rows, cols);\n}\n";
+  } else {
+    const std::string R = std::to_string(kRowsV);
+    s += "extern \"C\" __global__ __launch_bounds__(256) void vdsl_map_jit32(vdsl::MapProg rt, vdsl::MapVIn in, "
+         "vdsl::MapVOut vo, float* __restrict__ out, int rows, int cols) {\n"
+         "  vdsl::map_chain_v_body<vdsl::JitProg, " + R + ", int>(rt, in, vo, out, rows, cols);\n}\n";
+    s += "extern \"C\" __global__ __launch_bounds__(256) void vdsl_map_jit64(vdsl::MapProg rt, vdsl::MapVIn in, "
+         "vdsl::MapVOut vo, float* __restrict__ out, long long rows, long long cols) {\n"
+         "  vdsl::map_chain_v_body<vdsl::JitProg, " + R + ", long long>(rt, in, vo, out, rows, cols);\n}\n";
+  }
+  return s;
+}
+
+// Compiles (once per device and source) and loads the chain's kernels on the current device.
+// Returns VDSL_OK with *out set, or an error (also remembered, so a failing chain is not retried).
+int compiled_kernels(int ordinal, const std::string& src, const Compiled** out) {
+  if (ordinal < 0 || ordinal >= kMaxDevices) return fail(VDSL_ERR_UNSUPPORTED, "map chain: device ordinal beyond the table");
+  std::lock_guard<std::mutex> lk(g_jit_mu);
+  auto& cache = g_jit[ordinal];
+  auto it = cache.find(src);
+  if (it != cache.end()) {
+    if (it->second.failed) return fail(VDSL_ERR_DEVICE, "map chain: run-time compilation failed earlier for this chain");
+    *out = &it->second;
+    return VDSL_OK;
+  }
+  if (static_cast<int>(cache.size()) >= kMaxCompiledPerDevice)
+    return fail(VDSL_ERR_UNSUPPORTED, "map chain: compiled-chain cache is full");
+  Compiled& c = cache[src];
+  c.failed = true;  // until every step below succeeds
+  ++g_jit_compiles;
+  hiprtcProgram prog = nullptr;
+  const char* hdrs[] = {kSrc_vdsl_h, kSrc_fmath_h, kSrc_mapchain_kern_h, kStubStddef, kStubStdint};
+  const char* names[] = {"vdsl.h", "fmath.h", "mapchain_kern.h", "stddef.h", "stdint.h"};
+  if (hiprtcCreateProgram(&prog, src.c_str(), "vdsl_map_chain_program.hip", 5, hdrs, names) != HIPRTC_SUCCESS) {
+    ++g_jit_failures;
+    return fail(VDSL_ERR_DEVICE, "map chain: hiprtcCreateProgram failed");
+  }
+  // The library's own device flags (Makefile HIPFLAGS): same code generation as the built-in kernels.
+  const char* opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  const hiprtcResult cr = hiprtcCompileProgram(prog, 8, opts);
+  if (cr != HIPRTC_SUCCESS) {
+    size_t ls = 0;
+    hiprtcGetProgramLogSize(prog, &ls);
+    std::string log(ls, '\0');
+    if (ls) hiprtcGetProgramLog(prog, &log[0]);
+    hiprtcDestroyProgram(&prog);
+    ++g_jit_failures;
+    return fail(VDSL_ERR_DEVICE, "map chain: run-time compilation failed: " + log.substr(0, 1500));
+  }
+  size_t cs = 0;
+  hiprtcGetCodeSize(prog, &cs);
+  std::vector<char> code(cs);
+  hiprtcGetCode(prog, code.data());
+  hiprtcDestroyProgram(&prog);
+  int st = check_hip(hipModuleLoadData(&c.mod, code.data()), "hipModuleLoadData");
+  if (st == VDSL_OK) st = check_hip(hipModuleGetFunction(&c.f32, c.mod, "vdsl_map_jit32"), "hipModuleGetFunction");
+  if (st == VDSL_OK) st = check_hip(hipModuleGetFunction(&c.f64, c.mod, "vdsl_map_jit64"), "hipModuleGetFunction");
+  if (st != VDSL_OK) {
+    ++g_jit_failures;
+    return st;
+  }
+  c.failed = false;
+  *out = &c;
+  return VDSL_OK;
+}
+
+// Whether a launch of `elements` should use (and, if needed, compile) the chain's own kernel.
+bool want_compiled(vdsl_queue q, int64_t elements) {
+  const int m = map_mode();
+  if (m == kModeInterpret) return false;
+  if (q->capturing) return true;  // only a chain compiled earlier (checked by the caller)
+  return m == kModeCompile || elements >= kCompileMinElements;
+}
+
+// Runs a chain in its compiled form.  VDSL_OK: launched.  VDSL_ERR_UNSUPPORTED with nothing
+// enqueued: not available (not compiled yet while recording a graph, or compilation failed) - the
+// caller runs the interpreter instead.
+int launch_compiled(vdsl_queue q, const std::string& src, bool vector, void* prog_arg, void* in_arg, void* vo_arg, float* out,
+                    int64_t rows, int64_t cols) {
+  const Compiled* c = nullptr;
+  if (q->capturing) {
+    std::lock_guard<std::mutex> lk(g_jit_mu);
+    auto& cache = g_jit[q->dev->ordinal];
+    auto it = cache.find(src);
+    if (it == cache.end() || it->second.failed) return VDSL_ERR_UNSUPPORTED;
+    c = &it->second;
+  } else if (compiled_kernels(q->dev->ordinal, src, &c) != VDSL_OK) {
+    return VDSL_ERR_UNSUPPORTED;
+  }
+  Geometry g;
+  VDSL_TRY(geometry(vector ? 1 : 4, vector ? kRowsV : 2, vector ? 4 : 1, rows, cols, g));
+  int32_t r32 = static_cast<int32_t>(rows), c32 = static_cast<int32_t>(cols);
+  int64_t r64 = rows, c64 = cols;
+  void* a32v[] = {prog_arg, in_arg, vo_arg, &out, &r32, &c32};
+  void* a64v[] = {prog_arg, in_arg, vo_arg, &out, &r64, &c64};
+  void* a32s[] = {prog_arg, in_arg, &out, &r32, &c32};
+  void* a64s[] = {prog_arg, in_arg, &out, &r64, &c64};
+  void** args = vector ? (g.idx32 ? a32v : a64v) : (g.idx32 ? a32s : a64s);
+  VDSL_TRY(check_hip(hipModuleLaunchKernel(g.idx32 ? c->f32 : c->f64, g.grid.x, g.grid.y, 1, 256, 1, 1, 0, q->stream, args,
+                                           nullptr),
+                     "hipModuleLaunchKernel(map chain)"));
+  ++g_jit_launches;
+  return VDSL_OK;
+}
+
+// Shared validation of a chain's instructions.  widths[k]: the component count of input k (1 for
+// the scalar entry point), which bounds a LOAD's component field.
+int load_program(const vdsl_map_instr* code, int32_t n_instr, int32_t n_inputs, const int32_t* widths, MapProg& rt) {
+  if (n_instr < 0 || n_instr > VDSL_MAP_MAX_INSTR) return fail(VDSL_ERR_INVALID_ARG, "n_instr out of range [0, 32]");
+  if (n_instr && !code) return fail(VDSL_ERR_INVALID_ARG, "code is null");
+  rt = MapProg{};
+  rt.n = n_instr;
+  for (int pc = 0; pc < n_instr; ++pc) {
+    const vdsl_map_instr& s = code[pc];
+    if (s.op < VDSL_MAP_LOAD || s.op > VDSL_MAP_ADD_IMM)
+      return fail(VDSL_ERR_INVALID_ARG, "instruction " + std::to_string(pc) + ": unknown opcode " + std::to_string(s.op));
+    if (s.dst >= VDSL_MAP_MAX_REGS || s.b >= VDSL_MAP_MAX_REGS || s.c >= VDSL_MAP_MAX_REGS)
+      return fail(VDSL_ERR_INVALID_ARG, "instruction " + std::to_string(pc) + ": register out of range");
+    if (s.op == VDSL_MAP_LOAD ? (s.a >= n_inputs || s.c >= widths[s.a]) : s.a >= VDSL_MAP_MAX_REGS)
+      return fail(VDSL_ERR_INVALID_ARG, "instruction " + std::to_string(pc) + ": operand out of range");
+    rt.code[pc] = s;
+  }
+  return VDSL_OK;
 }
 
 }  // namespace
@@ -336,27 +347,15 @@ extern "C" int vdsl_op_map_chain(vdsl_queue q, int64_t rows, int64_t cols, const
                                  const vdsl_map_input* inputs, int32_t n_inputs, int32_t out_reg, vdsl_buffer out) {
   VDSL_TRY(enter_queue(q));
   if (rows < 0 || cols < 0) return fail(VDSL_ERR_INVALID_ARG, "negative shape");
-  if (n_instr < 0 || n_instr > VDSL_MAP_MAX_INSTR) return fail(VDSL_ERR_INVALID_ARG, "n_instr out of range [0, 32]");
   if (n_inputs < 0 || n_inputs > VDSL_MAP_MAX_INPUTS) return fail(VDSL_ERR_INVALID_ARG, "n_inputs out of range [0, 4]");
   if (out_reg < 0 || out_reg >= VDSL_MAP_MAX_REGS) return fail(VDSL_ERR_INVALID_ARG, "out_reg out of range");
-  if (n_instr && !code) return fail(VDSL_ERR_INVALID_ARG, "code is null");
   if (n_inputs && !inputs) return fail(VDSL_ERR_INVALID_ARG, "inputs is null");
   VDSL_TRY(check_buffer(q, out, nbytes(rows, cols, 4), "out", true));
   const int64_t n = rows * cols;  // no overflow: rows * cols * 4 fits size_t (checked above)
-
-  MapProg rt{};
-  rt.n = n_instr;
+  const int32_t ones[VDSL_MAP_MAX_INPUTS] = {1, 1, 1, 1};
+  MapProg rt;
+  VDSL_TRY(load_program(code, n_instr, n_inputs, ones, rt));
   rt.out_reg = out_reg;
-  for (int pc = 0; pc < n_instr; ++pc) {
-    const vdsl_map_instr& s = code[pc];
-    if (s.op < VDSL_MAP_LOAD || s.op > VDSL_MAP_ADD_IMM)
-      return fail(VDSL_ERR_INVALID_ARG, "instruction " + std::to_string(pc) + ": unknown opcode " + std::to_string(s.op));
-    if (s.dst >= VDSL_MAP_MAX_REGS || s.b >= VDSL_MAP_MAX_REGS || s.c >= VDSL_MAP_MAX_REGS)
-      return fail(VDSL_ERR_INVALID_ARG, "instruction " + std::to_string(pc) + ": register out of range");
-    if (s.op == VDSL_MAP_LOAD ? s.a >= n_inputs : s.a >= VDSL_MAP_MAX_REGS)
-      return fail(VDSL_ERR_INVALID_ARG, "instruction " + std::to_string(pc) + ": operand out of range");
-    rt.code[pc] = s;
-  }
   MapIn in{};
   in.n = n_inputs;
   for (int k = 0; k < n_inputs; ++k) {
@@ -373,7 +372,79 @@ extern "C" int vdsl_op_map_chain(vdsl_queue q, int64_t rows, int64_t cols, const
   float* o = static_cast<float*>(out->ptr);
   // 16-byte vectors need cols % 4 == 0 and 16-byte aligned bases (hipMalloc gives 256).
   const bool vec4 = (cols % 4) == 0;
-  if (vec4 && matches<ProgTanhExpBias>(rt, in)) return launch<ProgTanhExpBias, 4, 2>(rt, in, o, rows, cols, q->stream);
+  const int mode = map_mode();
+  if (vec4 && mode == kModeAuto && matches<ProgTanhExpBias>(rt, in))
+    return launch<ProgTanhExpBias, 4, 2>(rt, in, o, rows, cols, q->stream);
+  if (vec4 && want_compiled(q, n)) {
+    const int32_t regs[4] = {out_reg, 0, 0, 0};
+    const std::string src = program_source(rt, n_inputs, in.bcast, ones, regs, 1, false);
+    const int st = launch_compiled(q, src, false, &rt, &in, nullptr, o, rows, cols);
+    if (st != VDSL_ERR_UNSUPPORTED) return st;
+  }
   if (vec4) return launch<GenericProgram, 4, 1>(rt, in, o, rows, cols, q->stream);
   return launch<GenericProgram, 1, 1>(rt, in, o, rows, cols, q->stream);
+}
+
+extern "C" int vdsl_debug_map_chain_mode(int32_t mode) {
+  if (mode < kModeAuto || mode > kModeCompile) return fail(VDSL_ERR_INVALID_ARG, "map chain mode must be 0, 1 or 2");
+  map_mode();
+  g_mode.store(mode);
+  return VDSL_OK;
+}
+
+extern "C" int vdsl_debug_map_chain_stats(int64_t* compiled_launches, int64_t* compiles, int64_t* failures) {
+  if (compiled_launches) *compiled_launches = g_jit_launches.load();
+  if (compiles) *compiles = g_jit_compiles.load();
+  if (failures) *failures = g_jit_failures.load();
+  return VDSL_OK;
+}
+
+extern "C" int vdsl_op_map_chain_v(vdsl_queue q, int64_t rows, int64_t cols, const vdsl_map_instr* code, int32_t n_instr,
+                                   const vdsl_map_vinput* inputs, int32_t n_inputs, const int32_t* out_regs, int32_t out_width,
+                                   vdsl_buffer out) {
+  VDSL_TRY(enter_queue(q));
+  if (rows < 0 || cols < 0) return fail(VDSL_ERR_INVALID_ARG, "negative shape");
+  if (n_inputs < 0 || n_inputs > VDSL_MAP_MAX_INPUTS) return fail(VDSL_ERR_INVALID_ARG, "n_inputs out of range [0, 4]");
+  if (n_inputs && !inputs) return fail(VDSL_ERR_INVALID_ARG, "inputs is null");
+  if (out_width < 1 || out_width > 4) return fail(VDSL_ERR_INVALID_ARG, "out_width out of range [1, 4]");
+  if (!out_regs) return fail(VDSL_ERR_INVALID_ARG, "out_regs is null");
+  MapVOut vo{};
+  vo.width = out_width;
+  for (int k = 0; k < out_width; ++k) {
+    if (out_regs[k] < 0 || out_regs[k] >= VDSL_MAP_MAX_REGS) return fail(VDSL_ERR_INVALID_ARG, "out_regs entry out of range");
+    vo.regs[k] = out_regs[k];
+  }
+  VDSL_TRY(check_buffer(q, out, nbytes(rows, cols, 4 * static_cast<int64_t>(out_width)), "out", true));
+  MapVIn in{};
+  in.n = n_inputs;
+  int32_t widths[VDSL_MAP_MAX_INPUTS] = {1, 1, 1, 1};
+  for (int k = 0; k < n_inputs; ++k) {
+    const vdsl_map_vinput& d = inputs[k];
+    if (d.dtype != VDSL_F32) return fail(VDSL_ERR_UNSUPPORTED, "map chain inputs must be f32");
+    if (d.bcast < VDSL_BCAST_FULL || d.bcast > VDSL_BCAST_SCALAR) return fail(VDSL_ERR_INVALID_ARG, "unknown broadcast");
+    if (d.width < 1 || d.width > 4) return fail(VDSL_ERR_INVALID_ARG, "input width out of range [1, 4]");
+    const size_t need = d.bcast == VDSL_BCAST_FULL ? nbytes(rows, cols, 4 * static_cast<int64_t>(d.width))
+                        : d.bcast == VDSL_BCAST_ROW ? nbytes(cols, 4 * static_cast<int64_t>(d.width))
+                        : d.bcast == VDSL_BCAST_COL ? nbytes(rows, 4 * static_cast<int64_t>(d.width))
+                                                    : nbytes(1, 4 * static_cast<int64_t>(d.width));
+    std::string name = "input" + std::to_string(k);
+    VDSL_TRY(check_buffer(q, d.buf, need, name.c_str(), false));
+    // 8- and 16-byte records need their alignment (hipMalloc bases are 256-byte aligned)
+    if ((d.width == 2 || d.width == 4) && (reinterpret_cast<uintptr_t>(d.buf->ptr) % (4 * d.width)))
+      return fail(VDSL_ERR_INVALID_ARG, name + ": base not aligned to its record size");
+    in.p[k] = static_cast<const float*>(d.buf->ptr);
+    in.bcast[k] = d.bcast;
+    in.width[k] = d.width;
+    widths[k] = d.width;
+  }
+  MapProg rt;
+  VDSL_TRY(load_program(code, n_instr, n_inputs, widths, rt));
+  if (rows == 0 || cols == 0) return VDSL_OK;
+  float* o = static_cast<float*>(out->ptr);
+  if (want_compiled(q, rows * cols)) {
+    const std::string src = program_source(rt, n_inputs, in.bcast, widths, vo.regs, out_width, true);
+    const int st = launch_compiled(q, src, true, &rt, &in, &vo, o, rows, cols);
+    if (st != VDSL_ERR_UNSUPPORTED) return st;
+  }
+  return launch_v(rt, in, vo, o, rows, cols, q->stream);
 }

@@ -63,6 +63,40 @@ def map_chain(q: Queue, prog: Program, inputs, out: Tensor):
     call("vdsl_op_map_chain", q.handle, rows, cols, code, len(prog.code), arr, len(inputs), prog.out_reg, out.handle)
 
 
+def map_chain_v(q: Queue, prog: Program, inputs, out: Tensor):
+    """A chain over vector operands (vdsl_op_map_chain_v).  inputs[k] is the Tensor of input k:
+    [rows][cols][w] for a full input of width w > 1 ([rows][cols] when w = 1), [cols][w] / [rows][w]
+    / [w] when broadcast.  out: [rows][cols][len(prog.out_regs)] ([rows][cols] for one component)."""
+    rows, cols = out.shape[:2]
+    ow = len(prog.out_regs)
+    _expect(out, (rows, cols, ow) if ow > 1 else (rows, cols), "f32", "out")
+    if len(inputs) != prog.n_inputs:
+        raise ValueError(f"program reads {prog.n_inputs} inputs, {len(inputs)} given")
+    arr = (_lib.MapVInput * max(1, len(inputs)))()
+    for k, t in enumerate(inputs):
+        bc, w = prog.bcast[k], prog.widths[k]
+        want = {_lib.BCAST_FULL: (rows, cols), _lib.BCAST_ROW: (cols,), _lib.BCAST_COL: (rows,), _lib.BCAST_SCALAR: ()}[bc]
+        want = want + (w,) if (w > 1 or bc == _lib.BCAST_SCALAR) else want
+        _expect(t, want, "f32", f"input{k}")
+        arr[k].buf, arr[k].bcast, arr[k].dtype, arr[k].width = t.handle.value, bc, _lib.F32, w
+    regs = (C.c_int32 * 4)(*(prog.out_regs + [0] * (4 - ow)))
+    call("vdsl_op_map_chain_v", q.handle, rows, cols, prog.instr_array(), len(prog.code), arr, len(inputs), regs, ow,
+         out.handle)
+
+
+# ---- vertex transform (color.mlir:10-39) ----------------------------------------------------------
+def vec_transform(q: Queue, pos: Tensor, mats: Tensor, out: Tensor, varying: Tensor | None = None):
+    """out [n][4] = M_k ... M_1 vec4(pos, 1) for pos [n][3] (or M... pos for [n][4]); mats [k][4][4]
+    row-major (model, view, proj order), k = 1..3; varying (optional) [n][3|4] = pos."""
+    n, w = pos.shape
+    nm = mats.shape[0]
+    _expect(pos, (n, w), "f32", "pos")
+    _expect(mats, (nm, 4, 4), "f32", "mats")
+    _expect(out, (n, 4), "f32", "out")
+    _expect(varying, (n, w), "f32", "varying")
+    call("vdsl_op_vec_transform", q.handle, n, w, pos.handle, nm, mats.handle, out.handle, _h(varying))
+
+
 # ---- op class 3: row reductions + softmax ------------------------------------------------------
 def row_reduce_softmax(q: Queue, x: Tensor, row_sum=None, row_max=None, softmax=None):
     rows, cols = x.shape
