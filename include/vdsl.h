@@ -361,6 +361,18 @@ int64_t vdsl_mse_partials_count(int64_t rows, int64_t cols);
 int vdsl_op_mse_fwd_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer y, vdsl_buffer t,
                         vdsl_buffer loss, vdsl_buffer dy, vdsl_buffer dy_t, vdsl_buffer partials);
 
+/* The output layer of a regression head fused with its MSE loss (no reference counterpart;
+ * north-star op class: compiler-generated backward): y = A Bp^T (f32 accumulate, Bp packed by
+ * vdsl_op_pack_bf16_weights), d = y - t, and in the GEMM's epilogue loss = mean(d^2) (per-wave f64
+ * partial sums, added by a one-block kernel in a fixed order), dy = bf16(d * 2 / (M N)),
+ * dy_t = dy^T (optional), y itself (optional; the gradient does not need it).  dy and dy_t equal
+ * vdsl_op_gemm_bf16_packed (f32 C) followed by vdsl_op_mse_fwd_bwd bit for bit; the loss is the
+ * same f64 sum taken in another order.  M % 128 == 0, N % 256 == 0, K % 256 == 0.  partials: f32
+ * scratch of vdsl_mse_partials_count(M, N) elements, as for vdsl_op_mse_fwd_bwd. */
+int vdsl_op_gemm_bf16_mse_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer A,
+                                 vdsl_buffer Bp, vdsl_buffer t, vdsl_buffer y, vdsl_buffer loss,
+                                 vdsl_buffer dy, vdsl_buffer dy_t, vdsl_buffer partials);
+
 /* ========================================================================================== */
 /* Op class 5: int8 W8A8 GEMM with fused dequant (no reference code; north star).             */
 /* ========================================================================================== */

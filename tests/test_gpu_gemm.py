@@ -319,6 +319,55 @@ def test_gemm_gelu_bwd_fused_config4(dev, q):
         t.free()
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 4096), (128, 256, 256), (384, 768, 512)])
+def test_gemm_mse_fused_equals_gemm_then_mse(dev, q, M, N, K):
+    """vdsl_op_gemm_bf16_mse_packed against the packed GEMM (f32 out) followed by the MSE op on its
+    output: y, dy and dy^T bit for bit, the loss (the same f64 sum in another order) to 1e-6; with
+    y not requested the y buffer is left untouched; the loss also against the oracle's f64 MSE of
+    the GPU's own y, and dy against the oracle's dy of it bit for bit."""
+    A = bf16_rand((M, K), 95)
+    B = bf16_rand((N, K), 96)
+    T = rng.normal(97, M * N).reshape(M, N)
+    tA, tB, tT = Tensor.from_numpy(dev, q, A, "bf16"), Tensor.from_numpy(dev, q, B, "bf16"), Tensor.from_numpy(dev, q, T)
+    tBp = Tensor(dev, (N, K), "bf16")
+    kernels.pack_bf16_weights(q, tB, tBp)
+    part = Tensor(dev, (kernels.mse_partials_count(M, N),), "f32")
+    y1, y2 = Tensor(dev, (M, N), "f32"), Tensor(dev, (M, N), "f32")
+    l1, l2 = Tensor(dev, (1,), "f32"), Tensor(dev, (1,), "f32")
+    d1, d2 = Tensor(dev, (M, N), "bf16"), Tensor(dev, (M, N), "bf16")
+    t1, t2 = Tensor(dev, (N, M), "bf16"), Tensor(dev, (N, M), "bf16")
+    for t in (y1, d1, t1, l1):
+        t.buffer.fill_u32(q, 0x7FC07FC0)
+    kernels.gemm_bf16_mse_packed(q, tA, tBp, tT, y1, l1, d1, t1, part)
+    kernels.gemm_bf16_packed(q, tA, tBp, y2, _lib.EPI_NONE, None)
+    kernels.mse_fwd_bwd(q, y2, tT, l2, d2, t2, part)
+    y, d, dt_ = y1.numpy(q), d1.numpy(q), t1.numpy(q)
+    assert np.array_equal(y, y2.numpy(q))
+    assert np.array_equal(d, d2.numpy(q)) and np.array_equal(dt_, t2.numpy(q)) and np.array_equal(dt_, d.T)
+    la, lb = float(l1.numpy(q)[0]), float(l2.numpy(q)[0])
+    assert abs(la - lb) <= 1e-6 * abs(lb)
+    rl, rdy, _ = oracle.mse_fwd_bwd(y, T)
+    assert abs(la - rl) <= 1e-6 * abs(rl) and np.array_equal(d, rdy)
+    # y not requested: same loss and gradients, y's buffer untouched
+    y1.buffer.fill_u32(q, 0x7FC07FC1)
+    kernels.gemm_bf16_mse_packed(q, tA, tBp, tT, None, l1, d1, None, part)
+    assert float(l1.numpy(q)[0]) == la and np.array_equal(d1.numpy(q), d)
+    assert np.all(y1.numpy(q).view(np.uint32) == 0x7FC07FC1)
+    for t in (tA, tB, tT, tBp, part, y1, y2, l1, l2, d1, d2, t1, t2):
+        t.free()
+
+
+def test_gemm_mse_fused_shape_errors(dev, q):
+    import ctypes
+    tA, tBp, tT = Tensor(dev, (100, 256), "bf16"), Tensor(dev, (256, 256), "bf16"), Tensor(dev, (100, 256), "f32")
+    loss, dy, part = Tensor(dev, (1,), "f32"), Tensor(dev, (100, 256), "bf16"), Tensor(dev, (4096,), "f32")
+    st = _lib.lib.vdsl_op_gemm_bf16_mse_packed(q.handle, 100, 256, 256, tA.handle, tBp.handle, tT.handle, None,
+                                               loss.handle, dy.handle, None, part.handle)
+    assert st == -5 and b"M % 128" in _lib.lib.vdsl_last_error()
+    for t in (tA, tBp, tT, loss, dy, part):
+        t.free()
+
+
 @pytest.mark.parametrize("rows,cols,dt", [(512, 8192, "bf16"), (37, 100, "f32"), (5, 16, "bf16"), (64, 8192, "f32"),
                                           (3, 16384, "bf16"), (7, 4096, "f32"), (9, 4104, "f32")])
 def test_quantize_rows(dev, q, rows, cols, dt):

@@ -133,6 +133,7 @@ PROTOTYPES = {
     "vdsl_op_map_chain_v": (C.c_int, [_vp, _i64, _i64, C.POINTER(MapInstr), _i32, C.POINTER(MapVInput), _i32,
                                       C.POINTER(_i32), _i32, _vp]),
     "vdsl_op_vec_transform": (C.c_int, [_vp, _i64, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "vdsl_op_gemm_bf16_mse_packed": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vdsl_debug_map_chain_mode": (C.c_int, [_i32]),
     "vdsl_debug_map_chain_stats": (C.c_int, [C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i64)]),
     "vdsl_op_row_reduce_softmax": (C.c_int, [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp]),

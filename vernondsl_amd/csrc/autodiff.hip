@@ -233,6 +233,12 @@ __global__ __launch_bounds__(256) void mse_finish_kernel(const double* __restric
 int64_t tiles_of(int64_t rows, int64_t cols) { return ((rows + 63) / 64) * ((cols + 63) / 64); }
 
 }  // namespace
+
+int launch_mse_finish(const double* partials, int64_t n_partials, float* loss, double inv_n, hipStream_t s) {
+  hipLaunchKernelGGL(mse_finish_kernel, dim3(1), dim3(256), 0, s, partials, n_partials, loss, inv_n);
+  return check_launch("mse_finish_kernel");
+}
+
 }  // namespace vdsl
 
 using namespace vdsl;

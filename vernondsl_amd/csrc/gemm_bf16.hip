@@ -21,6 +21,8 @@ namespace vdsl {
 
 // Defined in layout.hip.
 int launch_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int dtype, hipStream_t s);
+// Defined in autodiff.hip: the one-block, fixed-order sum of MSE partials into the loss.
+int launch_mse_finish(const double* partials, int64_t n_partials, float* loss, double inv_n, hipStream_t s);
 
 namespace {
 std::atomic<int> g_gemm_config{-2};  // -2: not yet read from the environment
@@ -268,6 +270,84 @@ __device__ __forceinline__ void bf16_epilogue_bwd_lds(const f32x16 (&acc)[Cfg::F
   if (AR != 32 && ctr) store_transposed(0);
 }
 
+// Whole-tile MSE epilogue (vdsl_op_gemm_bf16_mse_packed), through each wave's LDS area like the
+// GELU-backward one: with y the accumulator and d = y - t, dy = bf16(d * scale) as 8-byte runs, y
+// as 16-byte runs (if wanted), dy^T through the area (each lane one column, AR * 2-byte runs of
+// dy_t[N][M]), and the wave's sum of d^2 in f64 (lane order: 32-row block, unit, component; then a
+// butterfly over the wave) into *part.  t, like `pre` there, is cold: every load of the wave's
+// tile is issued before the block barrier that ends the main loop.  The arithmetic of d, dy and
+// its rounding is that of mse_tile_vec (autodiff.hip), so dy and dy_t equal the unfused op's.
+template <class Cfg, int LDS_AVAIL>
+__device__ __forceinline__ void bf16_epilogue_mse_lds(const f32x16 (&acc)[Cfg::FM][Cfg::FN], int m0, int n0, int M, int N,
+                                                      const float* __restrict__ t, float scale, float* __restrict__ y,
+                                                      uint16_t* __restrict__ dy, uint16_t* __restrict__ dyt,
+                                                      double* __restrict__ part, char* smem) {
+  constexpr int WTN = Cfg::WTN, LD = WTN + 8, Q = WTN / 4, UPL = 32 * Q / 64;
+  constexpr int AR = Cfg::NW * Cfg::WTM * LD * 4 <= LDS_AVAIL ? Cfg::WTM : 32;
+  static_assert(WTN % 64 == 0, "the transposed store takes whole columns per lane");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
+  float* const area = reinterpret_cast<float*>(smem) + wave * AR * LD;
+  const int row0 = m0 + wm * Cfg::WTM, col0 = n0 + wn * WTN;
+  f32x4 x[Cfg::FM][UPL];
+#pragma unroll
+  for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+    for (int k = 0; k < UPL; ++k) {
+      const int u = lane + 64 * k, row = u / Q, c4 = u % Q;
+      x[i][k] = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4*>(t + static_cast<size_t>(row0 + 32 * i + row) * N + col0 + 4 * c4));
+    }
+  dma_barrier();  // every wave's last fragment reads of the main loop are done
+  auto store_transposed = [&](int r0) {
+#pragma unroll
+    for (int cc = 0; cc < WTN / 64; ++cc) {
+      const int c = lane + 64 * cc;
+      u32x4* dst = reinterpret_cast<u32x4*>(dyt + static_cast<size_t>(col0 + c) * M + row0 + r0);
+#pragma unroll
+      for (int q4 = 0; q4 < AR / 8; ++q4) {
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(area[(8 * q4 + 2 * e) * LD + c], area[(8 * q4 + 2 * e + 1) * LD + c]);
+        dst[q4] = w;
+      }
+    }
+  };
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < Cfg::FM; ++i) {
+    float* const blk = area + (AR == 32 ? 0 : 32 * i) * LD;
+#pragma unroll
+    for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) blk[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * LD + 32 * j + (lane & 31)] = acc[i][j][r];
+#pragma unroll
+    for (int k = 0; k < UPL; ++k) {
+      const int u = lane + 64 * k, row = u / Q, c4 = u % Q;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(blk + row * LD + 4 * c4);
+      const size_t o = static_cast<size_t>(row0 + 32 * i + row) * N + col0 + 4 * c4;
+      f32x4 g;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = v[e] - x[i][k][e];
+        s += static_cast<double>(d) * static_cast<double>(d);
+        g[e] = d * scale;
+      }
+      uint2 h;
+      h.x = pack_bf16x2(g[0], g[1]);
+      h.y = pack_bf16x2(g[2], g[3]);
+      *reinterpret_cast<uint2*>(dy + o) = h;
+      if (y) *reinterpret_cast<f32x4*>(y + o) = v;
+      if (dyt) *reinterpret_cast<f32x4*>(blk + row * LD + 4 * c4) = g;
+    }
+    if (AR == 32 && dyt) store_transposed(32 * i);
+  }
+  if (AR != 32 && dyt) store_transposed(0);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+  if (lane == 0) *part = s;
+}
+
 template <class Cfg, bool EDGE, bool BWD>
 __global__ __launch_bounds__(Cfg::NT, 2) void gemm_bf16_nt(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                         void* __restrict__ C, float* __restrict__ pre, int M, int N, int K,
@@ -397,6 +477,25 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_bpk(const uint16_t* __re
     }
   }
   bf16_store_tile<Cfg, BWD>(acc, m0, n0, M, N, C, pre, epi, c_dtype, ctr);
+}
+
+// The packed GEMM fused with the MSE loss of its f32 output (vdsl_op_gemm_bf16_mse_packed): whole
+// tiles only; partials[tile * W + wave] receives each wave's sum of squared differences.
+template <class Cfg>
+__global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_bpk_mse(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bp,
+                                                             const float* __restrict__ t, float* __restrict__ y,
+                                                             uint16_t* __restrict__ dy, uint16_t* __restrict__ dyt,
+                                                             double* __restrict__ partials, int M, int N, int K, float scale) {
+  __shared__ __attribute__((aligned(1024))) char smem[bpk_bf16_smem<Cfg, true>()];
+  const int tiles_m = M / Cfg::BM, tiles_n = N / Cfg::BN;
+  int tm, tn;
+  tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * Cfg::BM, n0 = tn * Cfg::BN;
+  f32x16 acc[Cfg::FM][Cfg::FN];
+  bpk_mainloop<MfmaBf16, Cfg>(reinterpret_cast<const char*>(A), reinterpret_cast<const char*>(Bp), M, N / 32, K * 2, 0, K * 2,
+                              m0, n0, smem, acc);
+  double* const part = partials + (static_cast<size_t>(tm) * tiles_n + tn) * Cfg::W + (threadIdx.x >> 6);
+  bf16_epilogue_mse_lds<Cfg, bpk_bf16_smem<Cfg, true>()>(acc, m0, n0, M, N, t, scale, y, dy, dyt, part, smem);
 }
 
 template <class Cfg>
@@ -624,4 +723,35 @@ extern "C" int vdsl_op_gemm_bf16_gelu_bwd_packed(vdsl_queue q, int64_t M, int64_
                      static_cast<float*>(pre->ptr), static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
                      kEpiGeluBwd, VDSL_BF16, da_t ? static_cast<uint16_t*>(da_t->ptr) : nullptr);
   return check_launch("gemm_bf16_bpk<gelu_bwd>");
+}
+
+extern "C" int vdsl_op_gemm_bf16_mse_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer A, vdsl_buffer Bp,
+                                            vdsl_buffer t, vdsl_buffer y, vdsl_buffer loss, vdsl_buffer dy, vdsl_buffer dy_t,
+                                            vdsl_buffer partials) {
+  VDSL_TRY(enter_queue(q));
+  if (M <= 0 || N <= 0 || K <= 0) return fail(VDSL_ERR_INVALID_ARG, "GEMM + MSE needs positive extents");
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x3fffffff) return fail(VDSL_ERR_UNSUPPORTED, "GEMM extent too large");
+  if (M % Pb0::BM || N % Pb0::BN) return fail(VDSL_ERR_UNSUPPORTED, "GEMM + MSE needs M % 128 == 0 and N % 256 == 0");
+  if ((2 * K) % (128 * Pb0::NR)) return fail(VDSL_ERR_UNSUPPORTED, "packed bf16 GEMM needs K % 256 == 0");
+  VDSL_TRY(check_buffer(q, A, nbytes(M, K, 2), "A", false));
+  VDSL_TRY(check_buffer(q, Bp, nbytes(N, K, 2), "Bp", false));
+  VDSL_TRY(check_buffer(q, t, nbytes(M, N, 4), "t", false));
+  if (y) VDSL_TRY(check_buffer(q, y, nbytes(M, N, 4), "y", true));
+  VDSL_TRY(check_buffer(q, loss, 4, "loss", true));
+  VDSL_TRY(check_buffer(q, dy, nbytes(M, N, 2), "dy", true));
+  if (dy_t) VDSL_TRY(check_buffer(q, dy_t, nbytes(M, N, 2), "dy_t", true));
+  const int64_t tiles = (M / Pb0::BM) * (N / Pb0::BN), n_part = tiles * Pb0::W;
+  VDSL_TRY(check_buffer(q, partials, nbytes(vdsl_mse_partials_count(M, N), 4), "partials", true));
+  if (static_cast<int64_t>(n_part * 2) > vdsl_mse_partials_count(M, N))
+    return fail(VDSL_ERR_UNSUPPORTED, "GEMM + MSE: partial sums exceed the MSE scratch size");
+  const size_t n = static_cast<size_t>(M) * static_cast<size_t>(N);
+  const float scale = 2.0f / static_cast<float>(n);  // as vdsl_op_mse_fwd_bwd
+  double* part = static_cast<double*>(partials->ptr);
+  hipLaunchKernelGGL((gemm_bf16_bpk_mse<Pb0>), dim3(static_cast<unsigned>(tiles)), dim3(Pb0::NT), 0, q->stream,
+                     static_cast<const uint16_t*>(A->ptr), static_cast<const uint16_t*>(Bp->ptr),
+                     static_cast<const float*>(t->ptr), y ? static_cast<float*>(y->ptr) : nullptr,
+                     static_cast<uint16_t*>(dy->ptr), dy_t ? static_cast<uint16_t*>(dy_t->ptr) : nullptr, part,
+                     static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), scale);
+  VDSL_TRY(check_launch("gemm_bf16_bpk_mse"));
+  return launch_mse_finish(part, n_part, static_cast<float*>(loss->ptr), 1.0 / static_cast<double>(n), q->stream);
 }

@@ -50,7 +50,7 @@ class Op:
 
 class Graph:
     def __init__(self, prepare_transposes: bool = False, fuse_gelu_backward: bool = False,
-                 pack_weights: bool = False):
+                 pack_weights: bool = False, fuse_mse: bool = False, keep_y: bool = True):
         # prepare_transposes: backward() takes a param's transpose (the NT form's B of dL/dx) from a
         # prepare op instead of transposing the param inside every step's GEMM.
         # fuse_gelu_backward (needs prepare_transposes): GELU' is applied in the epilogue of the GEMM
@@ -65,6 +65,11 @@ class Graph:
         # pack_weights: linear ops on a param weight read a copy packed into MFMA fragment order
         # (vdsl_op_gemm_bf16_packed), made by a prepare op; same results bit for bit.
         self.pack_weights = pack_weights
+        # fuse_mse: backward() merges an MSE loss with the packed, activation-free linear op that
+        # produces its input (vdsl_op_gemm_bf16_mse_packed), so y never makes a round trip through
+        # memory before the loss; keep_y: that op still stores y (the gradient does not need it).
+        self.fuse_mse = fuse_mse
+        self.keep_y = keep_y
         self.values: dict[str, Value] = {}
         self.ops: list[Op] = []
         # Ops that derive constant operands from params (weight packing): run by
@@ -178,16 +183,28 @@ class Graph:
         part = self._value(self._fresh("mse_partials"), (max(1, kernels.mse_partials_count(*y.shape)),), "f32", "scratch")
         loss.producer.outputs += [dy, dy_t, part]  # the forward MSE op also emits dL/dy
         grad[y.name] = ("bf16", dy, dy_t)
+        lin = y.producer
+        if (self.fuse_mse and lin is not None and lin.kind == "linear" and lin.attrs["act"] == "none"
+                and lin.attrs.get("packed") is not None and y.dtype == "f32"
+                and y.shape[0] % 128 == 0 and y.shape[1] % 256 == 0):
+            # the linear op and the loss become one op: the GEMM's epilogue forms the loss and dL/dy
+            mse_op = loss.producer
+            self.ops.remove(mse_op)
+            lin.kind = "linear_mse"
+            lin.inputs.append(mse_op.inputs[1])
+            lin.outputs += [loss, dy, dy_t, part]
+            for v in (loss, dy, dy_t, part):
+                v.producer = lin
         param_grads = {}
         for op in reversed(fwd_ops):
             if op.kind == "mse":
                 continue
-            if op.kind != "linear":
+            if op.kind not in ("linear", "linear_mse"):
                 raise NotImplementedError(f"no backward rule for {op.kind}")
             y = op.outputs[0]
             if y.name not in grad:
                 continue
-            x, w = op.inputs
+            x, w = op.inputs[:2]
             g = grad[y.name]
             act = op.attrs["act"]
             if act == "gelu":
@@ -352,6 +369,9 @@ class Executable:
             (M, K), N = ins[0].shape, ins[1].shape[0]
             form = "packed" if op.attrs.get("packed") is not None else "row-major"
             return f"linear {op.attrs['act']} ({form} weights, {outs[0].dtype} out) {M}x{N}x{K}"
+        if op.kind == "linear_mse":
+            (M, K), N = ins[0].shape, ins[1].shape[0]
+            return f"linear + MSE loss and dL/dy (packed weights) {M}x{N}x{K}"
         if op.kind == "gemm":
             a, b = ins
             M, K = (a.shape[1], a.shape[0]) if op.attrs["trans_a"] else a.shape
@@ -368,7 +388,7 @@ class Executable:
     def op_flops(self, op: Op) -> int:
         """2 M N K for a GEMM op (multiply-adds of its main loop), 0 otherwise."""
         ins = op.inputs
-        if op.kind in ("linear", "gemm_gelu_bwd"):
+        if op.kind in ("linear", "gemm_gelu_bwd", "linear_mse"):
             return 2 * ins[0].shape[0] * ins[0].shape[1] * ins[1].shape[0]
         if op.kind == "gemm":
             a, b = ins
@@ -394,6 +414,10 @@ class Executable:
         elif op.kind == "gemm":
             kernels.gemm_bf16(q, ins[0], ins[1], outs[0], op.attrs["trans_a"], op.attrs["trans_b"], op.attrs["epi"],
                               None, self.workspace)
+        elif op.kind == "linear_mse":
+            y, loss, dy, dy_t, part = outs
+            kernels.gemm_bf16_mse_packed(q, ins[0], T[op.attrs["packed"].name], ins[2], y if self.graph.keep_y else None,
+                                         loss, dy, dy_t, part)
         elif op.kind == "mse":
             loss = outs[0]
             if len(outs) == 4:
@@ -461,13 +485,13 @@ class Step:
 
 # ---- the two workload graphs ------------------------------------------------------------------------
 def mlp_train_graph(batch=2048, d_in=4096, hidden=4096, d_out=4096, prepare_transposes=True,
-                    fuse_gelu_backward=True, pack_weights=True):
+                    fuse_gelu_backward=True, pack_weights=True, fuse_mse=True, keep_y=True):
     """Config 4: X -> GELU(X W1^T) -> (.) W2^T -> MSE(., T), with backward for W1 and W2.
 
     The defaults are the fastest form measured on MI355X (one process, graph replays, same
     gradients bit for bit): 400 us per step, against 415 us with packed weights alone and 438 us
     with none of the three options."""
-    g = Graph(prepare_transposes, fuse_gelu_backward, pack_weights)
+    g = Graph(prepare_transposes, fuse_gelu_backward, pack_weights, fuse_mse, keep_y)
     x = g.input("X", (batch, d_in), "bf16")
     w1 = g.param("W1", (hidden, d_in), "bf16")
     w2 = g.param("W2", (d_out, hidden), "bf16")

@@ -141,6 +141,23 @@ def gemm_bf16(q: Queue, A: Tensor, B: Tensor, Cout: Tensor, trans_a=False, trans
          Cout.dtype, int(epilogue), _h(pre_act), _h(workspace))
 
 
+def gemm_bf16_mse_packed(q: Queue, A: Tensor, Bp: Tensor, T: Tensor, Y, loss: Tensor, dy: Tensor, dy_t=None,
+                         partials: Tensor = None):
+    """Y = A Bp^T fused with loss = mean((Y - T)^2), dy = bf16(2 (Y - T) / n), dy_t = dy^T
+    (vdsl_op_gemm_bf16_mse_packed); Y (f32) and dy_t may be None.  Bp: packed [N][K] weights."""
+    M, K = A.shape
+    N = Bp.shape[0]
+    _expect(A, (M, K), "bf16", "A")
+    _expect(Bp, (N, K), "bf16", "Bp")
+    _expect(T, (M, N), "f32", "T")
+    _expect(Y, (M, N), "f32", "Y")
+    _expect(loss, (1,), "f32", "loss")
+    _expect(dy, (M, N), "bf16", "dy")
+    _expect(dy_t, (N, M), "bf16", "dy_t")
+    call("vdsl_op_gemm_bf16_mse_packed", q.handle, M, N, K, A.handle, Bp.handle, T.handle, _h(Y), loss.handle, dy.handle,
+         _h(dy_t), partials.handle)
+
+
 def pack_bf16_weights(q: Queue, w: Tensor, wp: Tensor):
     """Writes w (bf16 [N][K]) into wp in the MFMA fragment order gemm_bf16_packed reads."""
     N, K = w.shape
