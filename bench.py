@@ -155,15 +155,45 @@ def in_step_report(exe, op_ms, peak, unit_scale=1e12):
 NOT_CHECKED = "not checked (--no-cpu: the oracle runs only in the CPU-baseline leg)"
 
 
-def time_cpu(fn, min_s=2.0, max_reps=5):
+def time_cpu(fn, reps=5):
+    """Median wall time of `reps` runs of fn() after one untimed run."""
     fn()  # warm-up
-    reps, t_total = 0, 0.0
-    while reps < max_reps and (reps == 0 or t_total < min_s):
+    ts = []
+    for _ in range(reps):
         t0 = time.perf_counter()
         fn()
-        t_total += time.perf_counter() - t0
-        reps += 1
-    return t_total / reps
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(run, work, unit, sample, run_1=None, work_1=None, sample_1=None, reps=5):
+    """The oracle (the CPU restatement of the path: kind "port") on the host's cores.  run() does
+    `work` units of the workload (a bounded sample, described by `sample`), timed as the median of
+    `reps` runs with every OpenMP thread, then run_1() (a smaller sample, default the same) with one
+    thread.  value = work / seconds in `unit`."""
+    from oracle import oracle
+    threads = oracle.num_threads()
+    t = time_cpu(run, reps)
+    run_1, work_1, sample_1 = run_1 or run, work_1 or work, sample_1 or sample
+    oracle.set_num_threads(1)
+    try:
+        t1 = time_cpu(run_1, reps)
+    finally:
+        oracle.set_num_threads(threads)
+    return {"value": work / t, "unit": unit, "cores": threads, "kind": "port", "sample": sample,
+            "seconds_median": t, "single_core_value": work_1 / t1, "single_core_sample": sample_1,
+            "single_core_seconds_median": t1, "median_of": reps, "model": cpu_model()}
 
 
 # ---- config 2 (headline) -------------------------------------------------------------------------
@@ -195,9 +225,11 @@ def bench_map_chain(dev, q, steps, warmup, do_cpu):
             sc = np.abs(np.tanh(u) * np.exp(-(x[r].astype(np.float64) ** 2))) + np.abs(bias.astype(np.float64))
             if not np.all(np.abs(got[r].astype(np.float64) - ref) <= 1e-5 * sc):
                 res["parity"] = f"FAIL row {r}"
-        t = time_cpu(lambda: oracle.map_chain(prog, [x, bias], rows, cols))
-        res["cpu"] = {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": oracle.num_threads(), "kind": "port",
-                      "sample": f"the full workload ([{rows}][{cols}] f32), {t:.3f} s per pass, oracle orc_map_chain"}
+        r1 = 1024
+        res["cpu"] = cpu_baseline(lambda: oracle.map_chain(prog, [x, bias], rows, cols), nbytes / 1e9, "GB/s",
+                                  f"the full workload ([{rows}][{cols}] f32), oracle orc_map_chain",
+                                  lambda: oracle.map_chain(prog, [x, bias], rows, cols, row_range=(0, r1)),
+                                  nbytes * r1 / rows / 1e9, f"first {r1} of {rows} rows")
     for t_ in (tx, tb, ty):
         t_.free()
     return res
@@ -247,11 +279,12 @@ def bench_map_chain_generic(dev, q, steps, warmup, do_cpu):
             ref = oracle.map_chain(prog, hx, rows, cols, row_range=(r, r + 1))[0].astype(np.float64)
             ok = np.all(np.abs(got[r].astype(np.float64) - ref) <= 1e-5 * (np.abs(ref) + 1.0))
             res["parity"] = "ok (row 4097 against the oracle)" if ok else "FAIL"
-            sample = 512
-            t = time_cpu(lambda: oracle.map_chain(prog, hx, rows, cols, row_range=(0, sample)), min_s=1.0, max_reps=3)
-            res["cpu_baseline"] = {"value": nbytes * sample / rows / t / 1e9, "unit": "GB/s",
-                                   "cores": oracle.num_threads(), "kind": "port",
-                                   "sample": f"first {sample} of {rows} rows, oracle orc_map_chain"}
+            sample, s1 = 2048, 256
+            res["cpu_baseline"] = cpu_baseline(
+                lambda: oracle.map_chain(prog, hx, rows, cols, row_range=(0, sample)), nbytes * sample / rows / 1e9, "GB/s",
+                f"first {sample} of {rows} rows, oracle orc_map_chain",
+                lambda: oracle.map_chain(prog, hx, rows, cols, row_range=(0, s1)), nbytes * s1 / rows / 1e9,
+                f"first {s1} of {rows} rows", reps=3)
         out.append(res)
     for t_ in (tx, tb, tc, ty):
         t_.free()
@@ -285,10 +318,11 @@ def bench_vecmat(dev, q, steps, warmup, do_cpu):
         idx = np.array([0, 1, n // 2, n - 1])
         got = to.numpy(q)
         res["parity"] = "ok" if np.array_equal(got[idx], oracle.vec_transform(pos[idx], mats)) else "FAIL"
-        s = 1 << 22
-        t = time_cpu(lambda: oracle.vec_transform(pos[:s], mats), min_s=1.0, max_reps=3)
-        res["cpu_baseline"] = {"value": s * 40 / t / 1e9, "unit": "GB/s", "cores": oracle.num_threads(), "kind": "port",
-                               "sample": f"first {s} of {n} vertices, oracle orc_vec_transform"}
+        s, s1 = 1 << 22, 1 << 19
+        res["cpu_baseline"] = cpu_baseline(
+            lambda: oracle.vec_transform(pos[:s], mats), s * 40 / 1e9, "GB/s",
+            f"first {s} of {n} vertices, oracle orc_vec_transform", lambda: oracle.vec_transform(pos[:s1], mats),
+            s1 * 40 / 1e9, f"first {s1} of {n} vertices", reps=3)
     out.append(res)
     for t_ in (tp, tm, to, tv):
         t_.free()
@@ -308,10 +342,12 @@ def bench_vecmat(dev, q, steps, warmup, do_cpu):
                         "bytes_per_launch": nbytes, "traffic": measured_traffic("swizzle")}}
     if do_cpu:
         from oracle import oracle
-        s = 512
-        t = time_cpu(lambda: oracle.map_chain_v(prog, [x], rows, cols, row_range=(0, s)), min_s=1.0, max_reps=3)
-        res["cpu_baseline"] = {"value": nbytes * s / rows / t / 1e9, "unit": "GB/s", "cores": oracle.num_threads(),
-                               "kind": "port", "sample": f"first {s} of {rows} rows, oracle orc_map_chain_v_rows"}
+        s, s1 = 1024, 128
+        res["cpu_baseline"] = cpu_baseline(
+            lambda: oracle.map_chain_v(prog, [x], rows, cols, row_range=(0, s)), nbytes * s / rows / 1e9, "GB/s",
+            f"first {s} of {rows} rows, oracle orc_map_chain_v_rows",
+            lambda: oracle.map_chain_v(prog, [x], rows, cols, row_range=(0, s1)), nbytes * s1 / rows / 1e9,
+            f"first {s1} of {rows} rows", reps=3)
     out.append(res)
     tx.free()
     ty.free()
@@ -341,9 +377,8 @@ def bench_fractal(dev, q, steps, warmup, do_cpu):
            "roofline": {"bound": "valu", "achieved": tflops, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
                         "frac": tflops / PEAK_FP32_TFLOPS, "flop_per_pixel_iteration": 8}}
     if do_cpu:
-        t = time_cpu(lambda: oracle.escape_time(params), min_s=1.0, max_reps=3)
-        res["cpu_baseline"] = {"value": total / t / 1e9, "unit": "Gpix-iter/s", "cores": oracle.num_threads(),
-                               "kind": "port", "sample": "the full 1024x1024 grid"}
+        res["cpu_baseline"] = cpu_baseline(lambda: oracle.escape_time(params), total / 1e9, "Gpix-iter/s",
+                                           "the full 1024x1024 grid")
     out.free()
     return res
 
@@ -381,11 +416,12 @@ def bench_softmax(dev, q, steps, warmup, do_cpu):
                             "frac": gbs / PEAK_HBM_GBS, "bytes_per_launch": nbytes,
                             "traffic": measured_traffic("softmax_" + dt)}}
         if do_cpu:
-            n_rows = 2048
-            t = time_cpu(lambda: oracle.row_reduce_softmax(xh, row_range=(0, n_rows)), min_s=1.0, max_reps=3)
-            res["cpu_baseline"] = {"value": spec.softmax_bytes(n_rows, cols, tx.dtype) / t / 1e9, "unit": "GB/s",
-                                   "cores": oracle.num_threads(), "kind": "port",
-                                   "sample": f"first {n_rows} of {rows} rows"}
+            n_rows, n1 = 4096, 512
+            res["cpu_baseline"] = cpu_baseline(
+                lambda: oracle.row_reduce_softmax(xh, row_range=(0, n_rows)), spec.softmax_bytes(n_rows, cols, tx.dtype) / 1e9,
+                "GB/s", f"first {n_rows} of {rows} rows (rows are independent)",
+                lambda: oracle.row_reduce_softmax(xh, row_range=(0, n1)), spec.softmax_bytes(n1, cols, tx.dtype) / 1e9,
+                f"first {n1} of {rows} rows")
         out.append(res)
         for t_ in (tx, ts, tm, tsm):
             t_.free()
@@ -429,12 +465,12 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
            "whole_graph_frac_of_peak": tflops / PEAK_BF16_TFLOPS}
     if do_cpu:  # CPU-baseline leg
         from oracle import oracle
-        b = 64
-        xs, ts_ = x[:b], t[:b]
-        tc = time_cpu(lambda: oracle.mlp_train_step(xs, w1, w2, ts_), min_s=1.0, max_reps=2)
-        res["cpu_baseline"] = {"value": spec.mlp_flops(b, D, Hd, O) / tc / 1e12, "unit": "TFLOP/s",
-                               "cores": oracle.num_threads(), "kind": "port",
-                               "sample": f"the same step at batch {b} (of {B}), f64-accumulating oracle"}
+        b, b1 = 64, 8
+        res["cpu_baseline"] = cpu_baseline(
+            lambda: oracle.mlp_train_step(x[:b], w1, w2, t[:b]), spec.mlp_flops(b, D, Hd, O) / 1e12, "TFLOP/s",
+            f"the same step at batch {b} of {B} (every GEMM keeps its 4096x4096 weight shape), f64-accumulating oracle",
+            lambda: oracle.mlp_train_step(x[:b1], w1, w2, t[:b1]), spec.mlp_flops(b1, D, Hd, O) / 1e12,
+            f"the same step at batch {b1} of {B}", reps=3)
     return res
 
 
@@ -484,11 +520,12 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
                         "kernel_ms": kms, "traffic": measured_traffic("gemm_w8a8")},
            "whole_graph_frac_of_peak": tops / PEAK_INT8_TOPS}
     if do_cpu:
-        r = 8
-        tc = time_cpu(lambda: oracle.w8a8_forward(x[:r], layers), min_s=1.0, max_reps=2)
-        res["cpu_baseline"] = {"value": spec.w8a8_ops(r, widths) / tc / 1e12, "unit": "TOP/s",
-                               "cores": oracle.num_threads(), "kind": "port",
-                               "sample": f"{r} of {B} rows through all 4 layers (rows are independent)"}
+        r, r1 = 16, 2
+        res["cpu_baseline"] = cpu_baseline(
+            lambda: oracle.w8a8_forward(x[:r], layers), spec.w8a8_ops(r, widths) / 1e12, "TOP/s",
+            f"{r} of {B} rows through all 4 layers (rows are independent)",
+            lambda: oracle.w8a8_forward(x[:r1], layers), spec.w8a8_ops(r1, widths) / 1e12,
+            f"{r1} of {B} rows through all 4 layers", reps=3)
     return res
 
 
