@@ -177,12 +177,12 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(run, work, unit, sample, run_1=None, work_1=None, sample_1=None, reps=5):
-    """The oracle (the CPU restatement of the path: kind "port") on the host's cores.  run() does
+def cpu_baseline(oracle, run, work, unit, sample, run_1=None, work_1=None, sample_1=None, reps=5):
+    """The oracle module (the CPU restatement of the path: kind "port", imported by the caller's
+    CPU-baseline leg) timed on the host's cores.  run() does
     `work` units of the workload (a bounded sample, described by `sample`), timed as the median of
     `reps` runs with every OpenMP thread, then run_1() (a smaller sample, default the same) with one
     thread.  value = work / seconds in `unit`."""
-    from oracle import oracle
     threads = oracle.num_threads()
     t = time_cpu(run, reps)
     run_1, work_1, sample_1 = run_1 or run, work_1 or work, sample_1 or sample
@@ -226,7 +226,7 @@ def bench_map_chain(dev, q, steps, warmup, do_cpu):
             if not np.all(np.abs(got[r].astype(np.float64) - ref) <= 1e-5 * sc):
                 res["parity"] = f"FAIL row {r}"
         r1 = 1024
-        res["cpu"] = cpu_baseline(lambda: oracle.map_chain(prog, [x, bias], rows, cols), nbytes / 1e9, "GB/s",
+        res["cpu"] = cpu_baseline(oracle, lambda: oracle.map_chain(prog, [x, bias], rows, cols), nbytes / 1e9, "GB/s",
                                   f"the full workload ([{rows}][{cols}] f32), oracle orc_map_chain",
                                   lambda: oracle.map_chain(prog, [x, bias], rows, cols, row_range=(0, r1)),
                                   nbytes * r1 / rows / 1e9, f"first {r1} of {rows} rows")
@@ -281,7 +281,7 @@ def bench_map_chain_generic(dev, q, steps, warmup, do_cpu):
             res["parity"] = "ok (row 4097 against the oracle)" if ok else "FAIL"
             sample, s1 = 2048, 256
             res["cpu_baseline"] = cpu_baseline(
-                lambda: oracle.map_chain(prog, hx, rows, cols, row_range=(0, sample)), nbytes * sample / rows / 1e9, "GB/s",
+                oracle, lambda: oracle.map_chain(prog, hx, rows, cols, row_range=(0, sample)), nbytes * sample / rows / 1e9, "GB/s",
                 f"first {sample} of {rows} rows, oracle orc_map_chain",
                 lambda: oracle.map_chain(prog, hx, rows, cols, row_range=(0, s1)), nbytes * s1 / rows / 1e9,
                 f"first {s1} of {rows} rows", reps=3)
@@ -320,7 +320,7 @@ def bench_vecmat(dev, q, steps, warmup, do_cpu):
         res["parity"] = "ok" if np.array_equal(got[idx], oracle.vec_transform(pos[idx], mats)) else "FAIL"
         s, s1 = 1 << 22, 1 << 19
         res["cpu_baseline"] = cpu_baseline(
-            lambda: oracle.vec_transform(pos[:s], mats), s * 40 / 1e9, "GB/s",
+            oracle, lambda: oracle.vec_transform(pos[:s], mats), s * 40 / 1e9, "GB/s",
             f"first {s} of {n} vertices, oracle orc_vec_transform", lambda: oracle.vec_transform(pos[:s1], mats),
             s1 * 40 / 1e9, f"first {s1} of {n} vertices", reps=3)
     out.append(res)
@@ -344,7 +344,7 @@ def bench_vecmat(dev, q, steps, warmup, do_cpu):
         from oracle import oracle
         s, s1 = 1024, 128
         res["cpu_baseline"] = cpu_baseline(
-            lambda: oracle.map_chain_v(prog, [x], rows, cols, row_range=(0, s)), nbytes * s / rows / 1e9, "GB/s",
+            oracle, lambda: oracle.map_chain_v(prog, [x], rows, cols, row_range=(0, s)), nbytes * s / rows / 1e9, "GB/s",
             f"first {s} of {rows} rows, oracle orc_map_chain_v_rows",
             lambda: oracle.map_chain_v(prog, [x], rows, cols, row_range=(0, s1)), nbytes * s1 / rows / 1e9,
             f"first {s1} of {rows} rows", reps=3)
@@ -377,7 +377,7 @@ def bench_fractal(dev, q, steps, warmup, do_cpu):
            "roofline": {"bound": "valu", "achieved": tflops, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
                         "frac": tflops / PEAK_FP32_TFLOPS, "flop_per_pixel_iteration": 8}}
     if do_cpu:
-        res["cpu_baseline"] = cpu_baseline(lambda: oracle.escape_time(params), total / 1e9, "Gpix-iter/s",
+        res["cpu_baseline"] = cpu_baseline(oracle, lambda: oracle.escape_time(params), total / 1e9, "Gpix-iter/s",
                                            "the full 1024x1024 grid")
     out.free()
     return res
@@ -418,7 +418,7 @@ def bench_softmax(dev, q, steps, warmup, do_cpu):
         if do_cpu:
             n_rows, n1 = 4096, 512
             res["cpu_baseline"] = cpu_baseline(
-                lambda: oracle.row_reduce_softmax(xh, row_range=(0, n_rows)), spec.softmax_bytes(n_rows, cols, tx.dtype) / 1e9,
+                oracle, lambda: oracle.row_reduce_softmax(xh, row_range=(0, n_rows)), spec.softmax_bytes(n_rows, cols, tx.dtype) / 1e9,
                 "GB/s", f"first {n_rows} of {rows} rows (rows are independent)",
                 lambda: oracle.row_reduce_softmax(xh, row_range=(0, n1)), spec.softmax_bytes(n1, cols, tx.dtype) / 1e9,
                 f"first {n1} of {rows} rows")
@@ -467,7 +467,7 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
         from oracle import oracle
         b, b1 = 64, 8
         res["cpu_baseline"] = cpu_baseline(
-            lambda: oracle.mlp_train_step(x[:b], w1, w2, t[:b]), spec.mlp_flops(b, D, Hd, O) / 1e12, "TFLOP/s",
+            oracle, lambda: oracle.mlp_train_step(x[:b], w1, w2, t[:b]), spec.mlp_flops(b, D, Hd, O) / 1e12, "TFLOP/s",
             f"the same step at batch {b} of {B} (every GEMM keeps its 4096x4096 weight shape), f64-accumulating oracle",
             lambda: oracle.mlp_train_step(x[:b1], w1, w2, t[:b1]), spec.mlp_flops(b1, D, Hd, O) / 1e12,
             f"the same step at batch {b1} of {B}", reps=3)
@@ -522,7 +522,7 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
     if do_cpu:
         r, r1 = 16, 2
         res["cpu_baseline"] = cpu_baseline(
-            lambda: oracle.w8a8_forward(x[:r], layers), spec.w8a8_ops(r, widths) / 1e12, "TOP/s",
+            oracle, lambda: oracle.w8a8_forward(x[:r], layers), spec.w8a8_ops(r, widths) / 1e12, "TOP/s",
             f"{r} of {B} rows through all 4 layers (rows are independent)",
             lambda: oracle.w8a8_forward(x[:r1], layers), spec.w8a8_ops(r1, widths) / 1e12,
             f"{r1} of {B} rows through all 4 layers", reps=3)
