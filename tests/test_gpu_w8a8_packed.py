@@ -2,8 +2,9 @@
 
 Bar: bit-exact.  The int32 accumulators and the dequantised outputs must equal the CPU oracle's
 (orc_gemm_w8a8 on the unpacked weights) and the row-major GPU kernel's, for shapes that take
-every launch plan: 128 x 256 blocks (large M), 128 x 128 blocks (config-5 layers), 64 x 256
-blocks with K split eight ways (the 1024-wide last layer) and in other counts, and ragged M and N.  Calls
+every launch plan: 128 x 256 blocks (large M), 128 x 128 blocks (config-5 layers), 128 x 128
+blocks with K split four ways (the 1024-wide last layer), 64 x 256 blocks with K split (M < 128),
+and ragged M and N; and every plan forced on one ragged shape.  Calls
 in a row on one workspace (left holding the previous call's partials) must not depend on its
 contents.
 """
@@ -143,3 +144,22 @@ def test_packed_shape_errors(dev, q):
         kernels.pack_w8a8_weights(q, tw, twp)  # N % 32
     tw.free()
     twp.free()
+
+
+@pytest.mark.parametrize("cfg,split", [(0, 1), (0, 2), (1, 1), (1, 4), (2, 1), (2, 2), (3, 1), (3, 3), (3, 8)])
+def test_every_forced_plan(dev, q, cfg, split):
+    """Each tile configuration and K split, forced with vdsl_debug_w8a8_packed_plan on a shape
+    ragged in M and N: bit-exact against the oracle (a split whose stages do not divide K is
+    ignored by the library; K = 6144 divides by every split here)."""
+    M, N, K = 200, 352, 6144
+    xq, w, xs, ws = _operands(M, N, K, 31 * cfg + split)
+    _lib.call("vdsl_debug_w8a8_packed_plan", cfg, split)
+    try:
+        p = Packed(dev, q, M, N, K)
+        y, acc = p.run(xq, w, xs, ws, True, "bf16")
+        p.free()
+    finally:
+        _lib.call("vdsl_debug_w8a8_packed_plan", -1, 0)
+    ry, racc = oracle.gemm_w8a8(xq, xs, w, ws, out_dtype=BF16, relu=True, want_acc=True)
+    assert np.array_equal(acc, racc)
+    assert np.array_equal(y, ry)

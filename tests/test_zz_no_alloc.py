@@ -3,10 +3,11 @@ against vdsl_op_gemm_w8a8_packed with a caller-provided workspace: bit for bit (
 accumulators and dequantised outputs).
 
 Two calls in a row that both split K, so both run through the library's scratch array: config 5's
-last layer (512 x 1024 x 8192, K split 8 ways: the full 16 MiB), then a smaller input
-(256 x 512 x 4096, 4 MiB) that leaves most of the first call's partials in place; then the first
-shape again, and an unsplit shape that needs no scratch.  A shape whose launch plan needs more
-scratch than the array holds is refused before anything is enqueued."""
+last layer (512 x 1024 x 8192) with its K split 8 ways (forced with vdsl_debug_w8a8_packed_plan:
+the full 16 MiB), then a smaller input (256 x 512 x 4096, 4 MiB) that leaves most of the first
+call's partials in place; then the first shape in its own plan (8 MiB), and an unsplit shape that
+needs no scratch.  A launch plan that needs more scratch than the array holds is refused before
+anything is enqueued."""
 import ctypes as C
 
 import numpy as np
@@ -21,7 +22,13 @@ SCRATCH = 16 << 20  # VDSL_W8A8_NOALLOC_SCRATCH_BYTES
 UNSUPPORTED = -5
 
 
-def _case(dev, q, M, N, K, seed, relu, dt):
+def _case(dev, q, M, N, K, seed, relu, dt, plan=None):
+    if plan is not None:
+        call("vdsl_debug_w8a8_packed_plan", *plan)
+        try:
+            return _case(dev, q, M, N, K, seed, relu, dt)
+        finally:
+            call("vdsl_debug_w8a8_packed_plan", -1, 0)
     r = np.random.default_rng(seed)
     xq = r.integers(-127, 128, (M, K)).astype(np.int8)
     w = r.integers(-127, 128, (N, K)).astype(np.int8)
@@ -57,23 +64,25 @@ def _case(dev, q, M, N, K, seed, relu, dt):
 
 
 def test_noalloc_matches_workspace_entry_point(dev, q):
-    assert _case(dev, q, 512, 1024, 8192, 1, relu=False, dt="bf16") == SCRATCH
+    assert _case(dev, q, 512, 1024, 8192, 1, relu=False, dt="bf16", plan=(3, 8)) == SCRATCH
     assert _case(dev, q, 256, 512, 4096, 2, relu=True, dt="f32") == 4 << 20
-    assert _case(dev, q, 512, 1024, 8192, 3, relu=True, dt="bf16") == SCRATCH
+    assert _case(dev, q, 512, 1024, 8192, 3, relu=True, dt="bf16") == 8 << 20
     assert _case(dev, q, 2048, 2048, 512, 4, relu=True, dt="bf16") == 0
 
 
 def test_noalloc_refuses_plans_beyond_the_scratch_array(dev, q):
-    M, N, K = 8256, 256, 1024  # 129 tiles of 64 x 256, K split 2: 129 * 2 * 64 KiB > 16 MiB
-    need = kernels.gemm_w8a8_packed_workspace_bytes(M, N, K)
-    assert need > SCRATCH
+    M, N, K = 8256, 256, 1024  # forced: 65 tiles of 128 x 256, K split 2: 65 * 2 * 128 KiB > 16 MiB
+    call("vdsl_debug_w8a8_packed_plan", 0, 2)
     txq, twp, ty = Tensor(dev, (M, K), "i8"), Tensor(dev, (N, K), "i8"), Tensor(dev, (M, N), "bf16")
     txs, tws = Tensor(dev, (M,), "f32"), Tensor(dev, (N,), "f32")
     try:
+        need = kernels.gemm_w8a8_packed_workspace_bytes(M, N, K)
+        assert need > SCRATCH
         st = lib.vdsl_op_gemm_w8a8_packed_noalloc(q.handle, M, N, K, txq.handle, txs.handle, twp.handle,
                                                   tws.handle, ty.handle, _lib.BF16, 1, None)
         msg = lib.vdsl_last_error().decode()
         assert st == UNSUPPORTED and str(need) in msg and "16777216" in msg, (st, msg)
     finally:
+        call("vdsl_debug_w8a8_packed_plan", -1, 0)
         for t in (txq, twp, ty, txs, tws):
             t.free()

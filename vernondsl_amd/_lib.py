@@ -159,6 +159,7 @@ PROTOTYPES = {
     "vdsl_op_gemm_w8a8_packed": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "vdsl_debug_fail_alloc_after": (C.c_int, [_i64]),
     "vdsl_debug_gemm_config": (C.c_int, [_i32]),
+    "vdsl_debug_w8a8_packed_plan": (C.c_int, [_i32, _i32]),
 }
 
 

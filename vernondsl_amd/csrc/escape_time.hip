@@ -36,14 +36,31 @@ __device__ __forceinline__ float pixel_coord(int idx, float den, float off, floa
   return v + post;
 }
 
-template <int FAMILY, int TEST, int ROUNDING, int OUT>
-__global__ __launch_bounds__(256) void escape_time_kernel(vdsl_escape_time_params p, void* __restrict__ out) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int i = blockIdx.y * kBlockEdge + (wave >> 1) * kTile + (lane >> 3);
-  const int j = blockIdx.x * kBlockEdge + (wave & 1) * kTile + (lane & 7);
-  if (j >= p.nj || i >= p.ni) return;
+// Per-lane selects on a 64-bit lane mask held in scalar registers (the mask is the select's
+// condition operand, so it is never turned into a vector of 0/1 and back).
+__device__ __forceinline__ int lane_select(uint64_t mask, int if_set, int if_clear) {
+  int r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(if_clear), "v"(if_set), "s"(mask));
+  return r;
+}
+// The same for a count's bit: volatile, so a select meant for a rarely taken branch is not hoisted
+// out of it.
+template <int V>
+__device__ __forceinline__ int lane_bit(uint64_t mask) {
+  int r;
+  asm volatile("v_cndmask_b32_e64 %0, 0, %1, %2" : "=v"(r) : "n"(V), "s"(mask));
+  return r;
+}
+#define lane_select_v(mask, V) lane_bit<V>(mask)
+__device__ __forceinline__ int lane_select_keep(uint64_t mask, int if_set, int keep) {
+  int r;
+  asm volatile("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(keep), "v"(if_set), "s"(mask));
+  return r;
+}
 
+// Iteration count of pixel (i, j), run by one lane of a wave of in-grid pixels.
+template <int FAMILY, int TEST, int ROUNDING>
+__device__ __forceinline__ int escape_count(const vdsl_escape_time_params& p, int i, int j) {
   float zr, zi, cr, ci;
   {
     const float im = pixel_coord(j, p.im_den, p.im_off, p.im_scale, p.im_post);
@@ -60,17 +77,19 @@ __global__ __launch_bounds__(256) void escape_time_kernel(vdsl_escape_time_param
   const float bound = p.bound;
   const int max_iter = p.max_iter;
 
-  // Wave-uniform loop: every pixel steps z each trip; `live` (sticky: true until the first failed
+  // Wave-uniform loop: every pixel steps z each trip; `live` (sticky: set until the first failed
   // escape test) marks the trips made while live, whose number is the count of updates of the
-  // check-then-update loop.  An escaped pixel keeps stepping z but is no longer counted.  `live` is
-  // a lane mask in scalar registers (the test writes one, s_and keeps it sticky), so a trip costs
-  // the six rounded operations of the update, one compare and one scalar op.  Counting is
-  // deferred to the end of each block of kUnroll trips: when no lane of the wave died in the
-  // block, every live lane adds kUnroll (one select and one add per block); otherwise each lane
-  // adds the trips it was live for, from the per-trip masks.  The max_iter check is made once per
-  // block (the tail block checks each trip), and the wave stops once no lane is live.
+  // check-then-update loop.  An escaped pixel keeps stepping z but is no longer counted.  The live
+  // set is a 64-bit lane mask held in scalar registers: each trip's escape test is a ballot (the
+  // compare writes the mask directly) and one scalar AND keeps it sticky, so a trip costs the six
+  // rounded operations of the update and one compare.  Counting is deferred to the end of each
+  // block of kUnroll trips: when no lane died in the block, every live lane adds kUnroll (one
+  // select); otherwise each lane adds the trips it was live for, whose bits follow from a binary
+  // search over the block's sticky masks (scalar ops, then five selects).  The max_iter check is
+  // made once per block (the tail block checks each trip), and the wave stops once no lane is live.
   constexpr int kUnroll = VDSL_ESC_UNROLL;
-  auto step = [&](bool lv) -> bool {
+  static_assert(kUnroll == 16, "the bit-plane count covers 16-trip blocks");
+  auto step = [&]() -> bool {  // one update of z; returns this trip's escape test (true: go on)
     float nzr, nzi, mag;
     if (ROUNDING == VDSL_ESC_ROUND_SEPARATE) {
       const float zr2 = zr * zr;
@@ -87,39 +106,61 @@ __global__ __launch_bounds__(256) void escape_time_kernel(vdsl_escape_time_param
     const bool pass = (TEST == VDSL_ESC_MAG2_GT) ? !(mag > bound) : (mag < bound);
     zr = nzr;
     zi = nzi;
-    return lv && pass;
+    return pass;
   };
-  bool live = true;
+  uint64_t live = __builtin_amdgcn_ballot_w64(true);
   int it = 0;
   int k = 0;
+  // Exact periodicity: z is saved (as bits) at the end of blocks 1, 2, 4, 8, ... and compared with
+  // z at the end of every block.  A live lane whose z equals an earlier z of its own orbit repeats
+  // the escape tests it has passed since then for ever, so its count is max_iter; it leaves the
+  // live set at once instead of stepping on to max_iter.  Bitwise equality, so -0 != +0 and NaN
+  // never matches: only a state that truly recurs is taken.
+  uint32_t save_r = __float_as_uint(zr), save_i = __float_as_uint(zi);
   for (; k + kUnroll <= max_iter; k += kUnroll) {
-    bool d[kUnroll];
-    bool lk = live;
+    uint64_t m[kUnroll];
+    uint64_t lk = live;
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      lk = step(lk);
-      d[u] = lk;
+      lk &= __builtin_amdgcn_ballot_w64(step());
+      m[u] = lk;
     }
-    if (__builtin_amdgcn_ballot_w64(lk) == __builtin_amdgcn_ballot_w64(live)) {
-      it += live ? kUnroll : 0;
+    if (lk == live) {
+      it += lane_select(live, kUnroll, 0);
     } else {
-      // The increment comes from a volatile asm, so the selects below cannot be computed before
-      // the branch (the compiler otherwise speculates this path into every block).
-      int one;
-      asm volatile("v_mov_b32 %0, 1" : "=v"(one));
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) it += d[u] ? one : 0;
+      // c = sum_u m[u] per lane (0..16); the masks are sticky (m[0] >= m[1] >= ...), so c >= 8
+      // iff m[7]; then c >= 4 more iff m[11] (or, below 8, m[3]); and so on; c == 16 adds m[15].
+      const uint64_t b3 = m[7];
+      const uint64_t b2 = (m[7] & m[11]) | (~m[7] & m[3]);
+      const uint64_t c00 = ~b3 & ~b2, c01 = ~b3 & b2, c10 = b3 & ~b2, c11 = b3 & b2;
+      const uint64_t b1 = (c00 & m[1]) | (c01 & m[5]) | (c10 & m[9]) | (c11 & m[13]);
+      const uint64_t b0 = (c00 & ~b1 & m[0]) | (c00 & b1 & m[2]) | (c01 & ~b1 & m[4]) | (c01 & b1 & m[6]) |
+                          (c10 & ~b1 & m[8]) | (c10 & b1 & m[10]) | (c11 & ~b1 & m[12]) | (c11 & b1 & m[14]);
+      it += lane_select_v(b0, 1) + lane_select_v(b1, 2) + lane_select_v(b2, 4) + lane_select_v(b3, 8) +
+            lane_select_v(m[15], 1);
     }
-    live = lk;
-    if (__builtin_amdgcn_ballot_w64(live) == 0) break;
+    const uint32_t br = __float_as_uint(zr), bi = __float_as_uint(zi);
+    const uint64_t per = lk & __builtin_amdgcn_ballot_w64(br == save_r) & __builtin_amdgcn_ballot_w64(bi == save_i);
+    if (per) it = lane_select_keep(per, max_iter, it);
+    live = lk & ~per;
+    const int blocks_done = __builtin_amdgcn_readfirstlane(k) / kUnroll + 1;  // wave-uniform
+    if ((blocks_done & (blocks_done - 1)) == 0) {
+      save_r = br;
+      save_i = bi;
+    }
+    if (live == 0) break;
   }
-  if (k + kUnroll > max_iter && __builtin_amdgcn_ballot_w64(live) != 0) {
+  if (k + kUnroll > max_iter && live != 0) {
     for (; k < max_iter; ++k) {
-      live = step(live);
-      it += live ? 1 : 0;
+      live &= __builtin_amdgcn_ballot_w64(step());
+      it += lane_select(live, 1, 0);
     }
   }
+  return it;
+}
 
+template <int OUT>
+__device__ __forceinline__ void escape_store(const vdsl_escape_time_params& p, void* out, int i, int j, int it) {
   const size_t o = static_cast<size_t>(i) * static_cast<size_t>(p.nj) + static_cast<size_t>(j);
   if (OUT == VDSL_ESC_OUT_I32_COUNT) {
     static_cast<int32_t*>(out)[o] = it;
@@ -127,6 +168,18 @@ __global__ __launch_bounds__(256) void escape_time_kernel(vdsl_escape_time_param
     const float f = static_cast<float>(it) * p.out_scale;
     static_cast<float*>(out)[o] = p.out_base + f;
   }
+}
+
+// One 8x8 tile per wave, 2x2 tiles per block, one block per 16x16 patch.
+template <int FAMILY, int TEST, int ROUNDING, int OUT>
+__global__ __launch_bounds__(256) void escape_time_kernel(vdsl_escape_time_params p, void* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int i = blockIdx.y * kBlockEdge + (wave >> 1) * kTile + (lane >> 3);
+  const int j = blockIdx.x * kBlockEdge + (wave & 1) * kTile + (lane & 7);
+  if (j >= p.nj || i >= p.ni) return;
+  const int it = escape_count<FAMILY, TEST, ROUNDING>(p, i, j);
+  escape_store<OUT>(p, out, i, j, it);
 }
 
 // Smallest f32 m >= 0 with sqrtf(m) >= b, so that for every f32 m (including +inf and NaN)
@@ -172,7 +225,6 @@ int launch_test(const vdsl_escape_time_params& p, void* out, hipStream_t s, dim3
   if (p.escape_test == VDSL_ESC_MAG2_GT) return launch_round<FAMILY, VDSL_ESC_MAG2_GT>(p, out, s, grid);
   return launch_round<FAMILY, VDSL_ESC_NORM_GE>(p, out, s, grid);
 }
-
 }  // namespace
 }  // namespace vdsl
 

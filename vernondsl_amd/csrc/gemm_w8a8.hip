@@ -555,8 +555,26 @@ struct BpkPlan {
   int cfg, split;  // cfg: 0 = P0, 1 = P1, 2 = P2, 3 = P3
   int64_t tiles;
 };
+std::atomic<int> g_bpk_plan{-1};  // debug override: cfg * 256 + split, or -1
+
+template <class Cfg>
+int64_t bpk_tiles(int64_t M, int64_t N) {
+  return ((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN);
+}
+
 BpkPlan bpk_plan(int64_t M, int64_t N, int64_t K) {
   BpkPlan p;
+  const int o = g_bpk_plan.load(std::memory_order_relaxed);
+  if (o >= 0) {  // a forced plan, when its stages split evenly: K % (128 * NR * split) == 0
+    const int cfg = o >> 8, split = o & 255;
+    const int nr = cfg == 2 ? P2::NR : P0::NR;
+    if (cfg >= 0 && cfg <= 3 && split >= 1 && K % (static_cast<int64_t>(128) * nr * split) == 0) {
+      p.cfg = cfg;
+      p.split = split;
+      p.tiles = cfg == 0 ? bpk_tiles<P0>(M, N) : cfg == 3 ? bpk_tiles<P3>(M, N) : bpk_tiles<P1>(M, N);
+      return p;
+    }
+  }
   const int64_t t0 = ((M + P0::BM - 1) / P0::BM) * ((N + P0::BN - 1) / P0::BN);
   const int64_t t3 = ((M + P3::BM - 1) / P3::BM) * ((N + P3::BN - 1) / P3::BN);
   if (t0 < 256 && t3 >= 256) {
@@ -565,9 +583,23 @@ BpkPlan bpk_plan(int64_t M, int64_t N, int64_t K) {
     p.split = 1;
     return p;
   }
+  const int64_t trips = K / (128 * P0::NR);
+  if (t0 < 256 && M >= 128) {
+    // Narrow outputs: 128 x 128 tiles with K split into about 128 blocks.  The partials' round
+    // trip through memory and the reduce cost more than the extra CUs of a larger split gain:
+    // 512x1024x8192 with weights rotating through 16 copies, same box: split 4 (128 blocks)
+    // 14.4 us, split 8 16.5-16.9, split 2 18.4, unsplit 25.6; 64 x 256 tiles split 8 (the plan
+    // before) 17.3-18.4, split 4 15.0.
+    p.cfg = 3;
+    p.tiles = t3;
+    int64_t s = t3 >= 128 ? 1 : 128 / t3;
+    if (s > trips) s = trips;
+    while (s > 1 && trips % s) --s;
+    p.split = static_cast<int>(s < 1 ? 1 : s);
+    return p;
+  }
   p.cfg = t0 >= 256 ? 0 : 1;
   p.tiles = p.cfg == 0 ? t0 : ((M + P1::BM - 1) / P1::BM) * ((N + P1::BN - 1) / P1::BN);
-  const int64_t trips = K / (128 * P0::NR);
   int64_t s = p.tiles >= 256 ? 1 : (256 + p.tiles - 1) / p.tiles;
   if (s > trips) s = trips;
   while (s > 1 && trips % s) --s;
@@ -577,7 +609,9 @@ BpkPlan bpk_plan(int64_t M, int64_t N, int64_t K) {
 }
 size_t bpk_workspace_bytes(const BpkPlan& p) {
   if (p.split == 1) return 0;
-  const size_t tile_bytes = p.cfg == 0 ? static_cast<size_t>(P0::BM) * P0::BN * 4 : static_cast<size_t>(P1::BM) * P1::BN * 4;
+  const size_t tile_bytes = p.cfg == 0   ? static_cast<size_t>(P0::BM) * P0::BN * 4
+                            : p.cfg == 3 ? static_cast<size_t>(P3::BM) * P3::BN * 4
+                                         : static_cast<size_t>(P1::BM) * P1::BN * 4;
   return static_cast<size_t>(p.tiles) * p.split * tile_bytes;
 }
 
@@ -751,6 +785,16 @@ static int packed_launch(vdsl_queue q, const BpkPlan& p, int64_t M, int64_t N, i
   if (p.cfg == 3) return launch_bpk<P3>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
   if (p.cfg == 2) return launch_bpk<P2>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
   return launch_bpk<P1>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
+}
+
+extern "C" int vdsl_debug_w8a8_packed_plan(int32_t cfg, int32_t split) {
+  if (cfg < 0) {
+    g_bpk_plan.store(-1, std::memory_order_relaxed);
+    return VDSL_OK;
+  }
+  if (cfg > 3 || split < 1 || split > 255) return fail(VDSL_ERR_INVALID_ARG, "plan: cfg 0..3, split 1..255");
+  g_bpk_plan.store(cfg * 256 + split, std::memory_order_relaxed);
+  return VDSL_OK;
 }
 
 extern "C" int vdsl_op_gemm_w8a8_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer xq, vdsl_buffer x_scale,
