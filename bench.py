@@ -44,6 +44,19 @@ def measured_traffic(kernel):
         return None
 
 
+def measured_valu_issue():
+    """VALU-issue share of the escape-time kernel's cycles from the committed rocprofv3 counter pass
+    (profiles/escape_time_valu.json: SQ_INSTS_VALU x 4 cycles / 1024 SIMDs over SQ_BUSY_CYCLES per
+    shader engine, as profiles/escape_time_valu_counters.md derives it); None if not measured."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "escape_time_valu.json")) as f:
+            d = json.load(f)
+        return {"valu_issue_frac": d["valu_issue_frac"], "effective_clock_ghz": d["effective_clock_ghz"],
+                "source": d["source"]}
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def time_launches(q, dev, fn, reps, warmup=30, warmup_ms=25.0):
     """Mean duration of one fn() call from HIP events on q's stream around `reps` back-to-back
     stream launches, after at least `warmup` untimed calls and at least `warmup_ms` of wall time
@@ -375,7 +388,10 @@ def bench_fractal(dev, q, steps, warmup, do_cpu):
            "metric": "Gpix-iter/s (fractal)", "value": gpix, "unit": "Gpix-iter/s", "ms_per_launch": ms,
            "pixel_iterations": total, "parity": parity,
            "roofline": {"bound": "valu", "achieved": tflops, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                        "frac": tflops / PEAK_FP32_TFLOPS, "flop_per_pixel_iteration": 8}}
+                        "frac": tflops / PEAK_FP32_TFLOPS, "flop_per_pixel_iteration": 8,
+                        "valu_issue": measured_valu_issue(),
+                        "note": "pixel-iterations counted as the program makes them (sum of counts); lanes whose "
+                                "orbit becomes exactly periodic stop early, so about 17% fewer trips execute"}}
     if do_cpu:
         res["cpu_baseline"] = cpu_baseline(oracle, lambda: oracle.escape_time(params), total / 1e9, "Gpix-iter/s",
                                            "the full 1024x1024 grid")
