@@ -77,6 +77,7 @@ _lib.orc_gelu_bwd.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp]
 _lib.orc_mse_fwd_bwd.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp, _vp]
 _lib.orc_quantize_rows_i8.argtypes = [_i64, _i64, C.c_int, _vp, _vp, _vp]
 _lib.orc_gemm_w8a8_rows.argtypes = [_i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _i64, _i64]
+_lib.orc_w8a8_dequant.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp, C.c_int, C.c_int]
 _lib.orc_num_threads.restype = C.c_int
 _lib.orc_set_num_threads.argtypes = [C.c_int]
 
@@ -264,6 +265,17 @@ def gemm_w8a8(xq, xs, w, ws, out_dtype=BF16, relu=False, want_acc=False, row_ran
     _lib.orc_gemm_w8a8_rows(M, N, K, _p(xq), _p(xs), _p(w), _p(ws), _vp(y.ctypes.data - r0 * N * y.itemsize), out_dtype,
                             int(relu), None if acc is None else _vp(acc.ctypes.data - r0 * N * 4), r0, r1)
     return (y, acc) if want_acc else y
+
+
+def w8a8_dequant(acc, xs, ws, relu=False, out_dtype=BF16):
+    """The dequant epilogue of gemm_w8a8 on given int32 accumulators acc [M][N]."""
+    acc = np.ascontiguousarray(acc, np.int32)
+    xs = np.ascontiguousarray(xs, np.float32)
+    ws = np.ascontiguousarray(ws, np.float32)
+    M, N = acc.shape
+    y = np.zeros((M, N), np.uint16 if out_dtype == BF16 else np.float32)
+    _lib.orc_w8a8_dequant(M, N, _p(acc), _p(xs), _p(ws), _p(y), out_dtype, int(relu))
+    return y
 
 
 # ---- composite programs of configs 4 and 5 (built from the routines above) --------------------

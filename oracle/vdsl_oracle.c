@@ -33,9 +33,10 @@
  *                        small integers), brute force in Python integers, and numpy f64.
  *   orc_gelu_fwd / orc_gelu_bwd / orc_mse_fwd_bwd
  *                        no reference code.  Pinned by central finite differences in f64.
- *   orc_quantize_rows_i8 / orc_gemm_w8a8
+ *   orc_quantize_rows_i8 / orc_gemm_w8a8 / orc_w8a8_dequant
  *                        no reference code.  Pinned by int64 numpy dot products (exact) and a
- *                        numpy restatement of the f32 dequant sequence.
+ *                        numpy restatement of the f32 dequant sequence (orc_w8a8_dequant is the
+ *                        GEMM's own epilogue code, checked against the same restatement).
  *   orc_transpose / orc_cast
  *                        pinned by numpy transpose / bit-level RNE.
  * The reference's own program (fractal.py) runs on third-party Taichi 1.7.4, which is not
@@ -452,6 +453,14 @@ void orc_quantize_rows_i8(int64_t rows, int64_t cols, int x_dtype, const void* x
   }
 }
 
+/* The dequant epilogue of one accumulator: relu?((float(acc) * xs) * ws), each product rounded. */
+static inline float w8a8_dequant_one(int32_t acc, float xs, float ws, int relu) {
+  float v = (float)acc * xs;
+  v = v * ws;
+  if (relu && !(v > 0.0f)) v = 0.0f;
+  return v;
+}
+
 /* Rows [m0, m1): acc = sum_k xq[m][k] w[n][k] (exact, int64 then int32);
  * y = relu?((float(acc) * xs[m]) * ws[n]) in f32, stored as out_dtype. */
 void orc_gemm_w8a8_rows(int64_t M, int64_t N, int64_t K, const int8_t* xq, const float* xs, const int8_t* w,
@@ -466,12 +475,19 @@ void orc_gemm_w8a8_rows(int64_t M, int64_t N, int64_t K, const int8_t* xq, const
       for (int64_t k = 0; k < K; ++k) acc += (int64_t)xr[k] * (int64_t)wr[k];
       const int32_t a32 = (int32_t)acc;
       if (acc_out) acc_out[m * N + n] = a32;
-      float v = (float)a32 * xs[m];
-      v = v * ws[n];
-      if (relu && !(v > 0.0f)) v = 0.0f;
-      store_out(y, out_dtype, m * N + n, v);
+      store_out(y, out_dtype, m * N + n, w8a8_dequant_one(a32, xs[m], ws[n], relu));
     }
   }
+}
+
+/* The epilogue of orc_gemm_w8a8 alone, on given int32 accumulators acc [M][N] (the same code, so
+ * it is pinned with orc_gemm_w8a8): lets a full-size check take exact accumulators from another
+ * source (an f64 matrix product of the int8 operands is exact at these sizes). */
+void orc_w8a8_dequant(int64_t M, int64_t N, const int32_t* acc, const float* xs, const float* ws, void* y, int out_dtype,
+                      int relu) {
+#pragma omp parallel for schedule(static)
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n) store_out(y, out_dtype, m * N + n, w8a8_dequant_one(acc[m * N + n], xs[m], ws[n], relu));
 }
 
 void orc_gemm_w8a8(int64_t M, int64_t N, int64_t K, const int8_t* xq, const float* xs, const int8_t* w,

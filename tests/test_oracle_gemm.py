@@ -153,6 +153,23 @@ def test_w8a8_exact_int_and_dequant_sequence():
     yb = oracle.gemm_w8a8(xq, xs, w, ws, out_dtype=BF16, relu=False)
     v2 = ((acc_ref.astype(np.float32) * xs[:, None]).astype(np.float32) * ws[None, :]).astype(np.float32)
     assert np.array_equal(yb, rng.f32_to_bf16(v2))
+    # the epilogue alone on given accumulators (what the full-size GPU check feeds it)
+    assert np.array_equal(oracle.w8a8_dequant(acc_ref.astype(np.int32), xs, ws, relu=True, out_dtype=F32), y)
+    assert np.array_equal(oracle.w8a8_dequant(acc_ref.astype(np.int32), xs, ws, relu=False), yb)
+
+
+def test_w8a8_dequant_large_accumulators():
+    """Accumulators of a K = 8192 layer reach 8192 * 127^2 > 2^24, where float(acc) rounds (RNE)."""
+    r = np.random.default_rng(2)
+    acc = r.integers(-8192 * 127 * 127, 8192 * 127 * 127 + 1, (16, 32)).astype(np.int32)
+    acc[0, :4] = [2**24 + 1, -(2**24 + 3), 2**27 - 1, 0]
+    xs = r.uniform(1e-4, 1e-2, 16).astype(np.float32)
+    ws = r.uniform(0.005, 0.02, 32).astype(np.float32)
+    a32 = acc.astype(np.float64).astype(np.float32)  # exact int -> f64, then one RNE rounding to f32
+    assert a32[0, 0] == np.float32(2**24) and a32[0, 1] == np.float32(-(2**24 + 4))
+    v = ((a32 * xs[:, None]).astype(np.float32) * ws[None, :]).astype(np.float32)
+    assert np.array_equal(oracle.w8a8_dequant(acc, xs, ws, relu=False, out_dtype=F32), v)
+    assert np.array_equal(oracle.w8a8_dequant(acc, xs, ws, relu=True), rng.f32_to_bf16(np.maximum(v, np.float32(0))))
 
 
 def test_w8a8_config_generators():
