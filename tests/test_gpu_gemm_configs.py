@@ -67,6 +67,53 @@ def test_every_bf16_config_matches(dev, q, forced_config, M, N, K):
         tB.free()
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 512, 256), (256, 768, 192), (129, 258, 128)])
+def test_bf16_nn_k_major_b_matches_nt(dev, q, forced_config, M, N, K):
+    """B stored [K][N] (trans_b = 0): with N % 256 == 0 the 256-wide direct-to-LDS configurations
+    (15, and 23 when K % 64 == 0) read B K-major with transposing LDS reads instead of transposing
+    it first; every output equals the NT product of the host-transposed B under the same
+    configuration, bit for bit (same k-steps, same order).  N = 258 takes the transpose path."""
+    A = rng.f32_to_bf16(rng.uniform(81, M * K, -1, 1)).reshape(M, K)
+    B = rng.f32_to_bf16(rng.uniform(82, K * N, -1, 1)).reshape(K, N)
+    tA, tB = Tensor.from_numpy(dev, q, A, "bf16"), Tensor.from_numpy(dev, q, B, "bf16")
+    tBt = Tensor.from_numpy(dev, q, np.ascontiguousarray(B.T), "bf16")
+    ws = Tensor(dev, (max(1, kernels.gemm_bf16_workspace_bytes(False, False, M, N, K)),), "i8")
+    try:
+        for c in (-1, 15, 23):
+            forced_config(c)
+            for gelu in (False, True):
+                outs = []
+                for tb, src in ((False, tB), (True, tBt)):
+                    ws.buffer.fill_u32(q, 0xA5A5A5A5)
+                    out = Tensor(dev, (M, N), "bf16" if gelu else "f32")
+                    pre = Tensor(dev, (M, N), "f32") if gelu else None
+                    for t in (out, pre):
+                        if t is not None:
+                            t.buffer.fill_u32(q, 0x7FC07FC0)
+                    kernels.gemm_bf16(q, tA, src, out, False, tb, _lib.EPI_GELU if gelu else _lib.EPI_NONE, pre,
+                                      None if tb else ws)
+                    outs.append((out.numpy(q), pre.numpy(q) if pre is not None else None))
+                    if not tb and c in (15, 23) and N % 256 == 0:  # the K-major kernel ran: no transpose into ws
+                        assert np.all(ws.numpy(q).view(np.uint32) == 0xA5A5A5A5), f"config {c}: B was transposed"
+                    out.free()
+                    if pre is not None:
+                        pre.free()
+                (o_nn, p_nn), (o_nt, p_nt) = outs
+                assert np.array_equal(o_nn, o_nt), f"config {c} gelu={gelu}: NN output differs from NT"
+                if gelu:
+                    assert np.array_equal(p_nn, p_nt), f"config {c}: NN pre-activation differs from NT"
+        forced_config(-1)
+        ref = oracle.gemm_bf16(A, B, False, False)
+        out = Tensor(dev, (M, N), "f32")
+        kernels.gemm_bf16(q, tA, tB, out, False, False, _lib.EPI_NONE, None, ws)
+        mag = np.abs(rng.bf16_to_f32(A).astype(np.float64)) @ np.abs(rng.bf16_to_f32(B).astype(np.float64))
+        assert np.all(np.abs(out.numpy(q).astype(np.float64) - ref) <= 1e-2 * mag + 1e-30)
+        out.free()
+    finally:
+        for t in (tA, tB, tBt, ws):
+            t.free()
+
+
 def gelu_bwd_pair(dev, q, tA, tB, tpre, M, N, fused):
     """(da, da_t) from the fused GEMM + GELU backward, or from the plain GEMM (f32) followed by
     the GELU backward op."""

@@ -364,8 +364,8 @@ __global__ __launch_bounds__(Cfg::NT, 2) void gemm_bf16_nt(const uint16_t* __res
 }
 
 // Direct-to-LDS kernel (gemm_dma.h).  Blocks of 8 waves are sized for one block per CU, blocks
-// of 4 waves for two.
-template <class Cfg, bool BWD>
+// of 4 waves for two.  BKN: B stored [K][N] (the "NN" form, no transpose first; N % 256 == 0).
+template <class Cfg, bool BWD, bool BKN = false>
 __global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_bf16_dma(const uint16_t* __restrict__ A,
                                                                                const uint16_t* __restrict__ B,
                                                                                void* __restrict__ C, float* __restrict__ pre,
@@ -377,8 +377,8 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_bf16_dma
   tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
   const int m0 = tm * Cfg::BM, n0 = tn * Cfg::BN;
   f32x16 acc[Cfg::FM][Cfg::FN];
-  dma_mainloop<MfmaBf16, Cfg>(reinterpret_cast<const char*>(A), reinterpret_cast<const char*>(B), M, N, K * 2, 0, K * 2, m0,
-                              n0, smem, acc);
+  dma_mainloop<MfmaBf16, Cfg, f32x16, Cfg::FM, Cfg::FN, BKN>(reinterpret_cast<const char*>(A), reinterpret_cast<const char*>(B),
+                                                             M, N, K * 2, 0, K * 2, m0, n0, smem, acc, N * 2);
   if constexpr (kLdsEpilogue<Cfg>) {
     // Block-uniform: the tile is whole, N allows aligned runs, and the variant is one of the two.
     const bool whole = m0 + Cfg::BM <= M && n0 + Cfg::BN <= N && N % 4 == 0;
@@ -527,6 +527,24 @@ int launch_dma(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M,
   return check_launch("gemm_bf16_dma");
 }
 
+// The "NN" form (B stored [K][N]) without a transpose: the direct-to-LDS configurations with
+// 256-wide tiles read B K-major (gemm_dma.h) when every tile is whole along N.  Returns 1 (never a
+// status) when the shape needs the transpose path instead.
+int launch_dma_kn(int cfg, const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, int N, int K, int epi, int ct,
+                  hipStream_t s) {
+  if (N % 256 != 0) return 1;
+  auto go = [&](auto cfg_tag) {
+    using Cfg = decltype(cfg_tag);
+    const int64_t tiles = static_cast<int64_t>((M + Cfg::BM - 1) / Cfg::BM) * (N / Cfg::BN);
+    hipLaunchKernelGGL((gemm_bf16_dma<Cfg, false, true>), dim3(static_cast<unsigned>(tiles)), dim3(Cfg::NT), 0, s, A, B, C, pre,
+                       M, N, K, epi, ct, nullptr);
+    return check_launch("gemm_bf16_dma<K-major B>");
+  };
+  if (cfg == 15) return go(Dm15{});
+  if (cfg == 23) return go(Dm23{});
+  return 1;
+}
+
 // Configuration for a shape.  The direct-to-LDS loop (14..) runs whenever K is a whole number of
 // its 64-byte stages (K % 32 == 0); measured on MI355X with random operands (bf16, f32 out):
 // 128x256 blocks of 8 waves are fastest while they still give every CU a block, with 128-byte
@@ -629,6 +647,12 @@ extern "C" int vdsl_op_gemm_bf16(vdsl_queue q, int32_t trans_a, int32_t trans_b,
 
   const uint16_t* a = static_cast<const uint16_t*>(A->ptr);
   const uint16_t* b = static_cast<const uint16_t*>(B->ptr);
+  float* pre = pre_act ? static_cast<float*>(pre_act->ptr) : nullptr;
+  if (!ta && !tb && K % 8 == 0) {  // B stored [K][N]: read K-major when a 256-wide configuration runs the shape
+    const int rc = launch_dma_kn(choose_config(M, N, K), a, b, C->ptr, pre, static_cast<int>(M), static_cast<int>(N),
+                                 static_cast<int>(K), epilogue, c_dtype, q->stream);
+    if (rc != 1) return rc;
+  }
   char* w = ws ? static_cast<char*>(workspace->ptr) : nullptr;
   if (ta) {  // A stored [K][M] -> [M][K]
     VDSL_TRY(launch_transpose(a, w, K, M, VDSL_BF16, q->stream));
@@ -639,7 +663,6 @@ extern "C" int vdsl_op_gemm_bf16(vdsl_queue q, int32_t trans_a, int32_t trans_b,
     VDSL_TRY(launch_transpose(b, w, K, N, VDSL_BF16, q->stream));
     b = reinterpret_cast<const uint16_t*>(w);
   }
-  float* pre = pre_act ? static_cast<float*>(pre_act->ptr) : nullptr;
   return launch_nt(a, b, C->ptr, pre, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), epilogue, c_dtype,
                    q->stream);
 }

@@ -23,6 +23,16 @@
 // barrier also orders every wave's reads of stage t before the copy that overwrites it (issued
 // at stage t+1).  Rows past M or N are clamped to the last row (their products only reach
 // outputs that are not stored).
+//
+// K-major B (BKN, bf16 only): B stored [K][N] (N contiguous), the layout of an activation that a
+// weight-gradient GEMM takes as is (dW = g^T x with x [batch][in]), so no transpose kernel runs
+// first.  A sub-stage's B area then holds the 32 K rows of the tile, each 2 BN bytes, with chunk
+// c of row k in slot c ^ kn_swz(k); the copies move whole 64-byte runs of a row, and a B fragment
+// is assembled by two transposing LDS reads (ds_read_b64_tr_b16): within each group of 16 lanes,
+// result lane i, element e is element i % 4 of the 8 bytes addressed by lane 4 e + i / 4, so
+// pointing lane j at row k0 + j / 4, columns 4 (j % 4) .. + 3 hands lane i the 4 K values of
+// column i (measured on gfx950 with an in-bounds lane-layout probe).  Same products in the same
+// order as the NT form of the transposed B, so the same results bit for bit.
 #pragma once
 
 #include "gemm_mfma.h"
@@ -66,6 +76,18 @@ __device__ __forceinline__ void lds_copy16(const char* g, char* l) {
   __builtin_amdgcn_global_load_lds(g, (lds_void_t*)l, 16, 0, 0);
 }
 
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 at an 8-byte aligned LDS address (see the K-major B note above).
+__device__ __forceinline__ i16x4_t lds_read_tr16(const char* l) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(l));
+}
+
+// K-major B: the 16-byte slot XOR of K row k (0..31 within a sub-stage), in chunk units.  It flips
+// bits 2-4 of the chunk index, so a row's 64-byte runs stay whole; the 8 rows one transposing read
+// touches (k0 + 0..3 and k0 + 8..11, k0 % 4 == 0) get 8 distinct 64-byte windows of a 512-byte row.
+__device__ __forceinline__ int kn_swz(int k) { return ((k & 7) ^ ((k >> 1) & 4)) << 2; }
+
 // s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4 left at
 // its no-wait value 7, lgkmcnt 11:8 = 0).  The count must be a constant.
 #define VDSL_WAIT_VM_LGKM0(n) dma_wait<(n)>()
@@ -96,10 +118,14 @@ __device__ __forceinline__ void dma_barrier() {
 
 // K loop over bytes [kb_begin, kb_end) for the tile at (m0, n0).  Requires kb_begin % 16 == 0 and
 // (kb_end - kb_begin) % BKB == 0; Kb = row stride of A and B in bytes.
-template <class T, class Cfg, class AccT, int FM_, int FN_>
+// BKN: B is stored [K][N] with row stride Nb bytes (needs BN == 256, bf16, and the tile's N range
+// inside N: the caller launches it only for N % 256 == 0).
+template <class T, class Cfg, class AccT, int FM_, int FN_, bool BKN = false>
 __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const char* __restrict__ B, int M, int N, int Kb,
-                                             int kb_begin, int kb_end, int m0, int n0, char* smem, AccT (&acc)[FM_][FN_]) {
+                                             int kb_begin, int kb_end, int m0, int n0, char* smem, AccT (&acc)[FM_][FN_],
+                                             int Nb = 0) {
   static_assert(FM_ == Cfg::FM && FN_ == Cfg::FN, "accumulator array must match the configuration");
+  static_assert(!BKN || (Cfg::BN == 256 && std::is_same<T, MfmaBf16>::value), "K-major B: bf16, 256-wide tiles");
   using Frag = typename T::Frag;
   constexpr int FM = Cfg::FM, FN = Cfg::FN, NS = Cfg::NS, BPW = Cfg::BPW, STAGE = Cfg::STAGE, SUB = Cfg::SUB;
   constexpr int KS = Cfg::KS, KSUB = Cfg::KSUB, CPW = Cfg::CPW;
@@ -115,15 +141,27 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
   // Copy block b = wave * BPW + u of a sub-stage: blocks [0, BM/16) are A rows 16b.., the rest B.
   // Lane l copies row 16 * (b') + l / 4, LDS slot l % 4, i.e. global chunk (l % 4) ^ swizzle.
   const char* src[BPW];
+  size_t kmul[BPW];  // K-major B: bytes of source per K byte of the stage offset (1 for row-major rows)
 #pragma unroll
   for (int u = 0; u < BPW; ++u) {
     const int b = wave * BPW + u;
     const bool is_a = b < Cfg::BM / Cfg::RPB;
+    if (BKN && !is_a) {
+      // 1 KiB block j holds K rows 2j, 2j+1 of the sub-stage; lane l fills slot l % 32 of row
+      // 2j + l / 32 with global chunk (l % 32) ^ kn_swz(row) of that row's 512-byte run.
+      const int k = 2 * (b - Cfg::BM / Cfg::RPB) + (lane >> 5);
+      const int c = (lane & 31) ^ kn_swz(k);
+      src[u] = B + static_cast<size_t>(kb_begin / 2 + k) * Nb + static_cast<size_t>(n0) * 2 + c * 16;
+      kmul[u] = static_cast<size_t>(Nb) / 2;
+      continue;
+    }
     const int r = Cfg::RPB * (is_a ? b : b - Cfg::BM / Cfg::RPB) + (lane >> 2);
     const int c = (lane & 3) ^ ((r >> 2) & 3);
     const size_t row = is_a ? static_cast<size_t>(min(m0 + r, M - 1)) : static_cast<size_t>(min(n0 + r, N - 1));
     src[u] = (is_a ? A : B) + row * Kb + kb_begin + c * 16;
+    kmul[u] = 1;
   }
+  (void)kmul;
   char* const dst = smem + wave * BPW * 1024;
   // This lane's fragment rows (within a sub-stage's A and B areas).
   const int ra = wm * Cfg::WTM + (lane & 31);
@@ -131,18 +169,34 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
   const int hk = lane >> 5;
   const char* const fa = smem;
   const char* const fb = smem + Cfg::BM * 64;
+  // K-major B: offsets of this lane's two transposing reads (r = K values 0-3 / 4-7 of its half)
+  // of fragment j in the first k-step of a sub-stage; the second k-step is 16 rows further.
+  int tro[2][FN];
+  if constexpr (BKN) {
+    const int g = lane >> 4, i = lane & 15;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int k = 8 * (g >> 1) + 4 * r + (i >> 2);
+        const int n = wn * Cfg::WTN + 32 * j + 16 * (g & 1) + 4 * (i & 3);
+        tro[r][j] = k * (2 * Cfg::BN) + (((n >> 3) ^ kn_swz(k)) << 4) + ((n >> 2) & 1) * 8;
+      }
+  }
+  constexpr int NRD = FM + (BKN ? 2 : 1) * FN;  // LDS read instructions per k-step
 
+#define VDSL_DMA_SRC(U, KOFF) (BKN ? src[U] + static_cast<size_t>(KOFF) * kmul[U] : src[U] + (KOFF))
 #define VDSL_DMA_COPY(ST, KB)                                                                     \
   do {                                                                                            \
     _Pragma("unroll") for (int sb = 0; sb < KSUB; ++sb)                                           \
       _Pragma("unroll") for (int u = 0; u < BPW; ++u)                                             \
-        lds_copy16(src[u] + (KB) + 64 * sb, dst + (ST) * STAGE + sb * SUB + u * 1024);            \
+        lds_copy16(VDSL_DMA_SRC(u, (KB) + 64 * sb), dst + (ST) * STAGE + sb * SUB + u * 1024);    \
   } while (0)
 // Copies [I0, I1) of a stage's CPW copies (copy i = sub-stage i / BPW, block i % BPW).
 #define VDSL_DMA_COPY_PART(ST, KB, I0, I1)                                                        \
   do {                                                                                            \
     _Pragma("unroll") for (int i = (I0); i < (I1); ++i)                                           \
-      lds_copy16(src[i % BPW] + (KB) + 64 * (i / BPW), dst + (ST) * STAGE + (i / BPW) * SUB +     \
+      lds_copy16(VDSL_DMA_SRC(i % BPW, (KB) + 64 * (i / BPW)), dst + (ST) * STAGE + (i / BPW) * SUB + \
                  (i % BPW) * 1024);                                                               \
   } while (0)
 // Fragments of k-step KK (32 K bytes) of stage ST: sub-stage KK / 2, chunks 2 (KK % 2) + hk.
@@ -151,9 +205,17 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
     _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                \
       A_[i] = *reinterpret_cast<const Frag*>(fa + (ST) * STAGE + ((KK) >> 1) * SUB +              \
                                              dma_slot(ra + 32 * i, 2 * ((KK) & 1) + hk));          \
-    _Pragma("unroll") for (int j = 0; j < FN; ++j)                                                \
-      B_[j] = *reinterpret_cast<const Frag*>(fb + (ST) * STAGE + ((KK) >> 1) * SUB +              \
-                                             dma_slot(rb + 32 * j, 2 * ((KK) & 1) + hk));          \
+    if constexpr (BKN) {                                                                          \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j) {                                            \
+        const char* const kb_ = fb + (ST) * STAGE + ((KK) >> 1) * SUB + ((KK) & 1) * 32 * Cfg::BN; \
+        const i16x4_t lo_ = lds_read_tr16(kb_ + tro[0][j]), hi_ = lds_read_tr16(kb_ + tro[1][j]); \
+        B_[j] = __builtin_bit_cast(Frag, __builtin_shufflevector(lo_, hi_, 0, 1, 2, 3, 4, 5, 6, 7)); \
+      }                                                                                           \
+    } else {                                                                                      \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j)                                              \
+        B_[j] = *reinterpret_cast<const Frag*>(fb + (ST) * STAGE + ((KK) >> 1) * SUB +            \
+                                               dma_slot(rb + 32 * j, 2 * ((KK) & 1) + hk));        \
+    }                                                                                             \
   } while (0)
 #define VDSL_DMA_MMA(A_, B_)                                                                      \
   do {                                                                                            \
@@ -164,7 +226,7 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
 // 0x008 MFMA); the scheduling barrier keeps each k-step's instructions together.
 #define VDSL_DMA_ORDER()                                                                          \
   do {                                                                                            \
-    __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);                                      \
+    __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);                                      \
     __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);                                      \
     __builtin_amdgcn_sched_barrier(0);                                                            \
   } while (0)
@@ -174,7 +236,7 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
 #define VDSL_DMA_ORDER_LATE()                                                                     \
   do {                                                                                            \
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                            \
-    __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);                                      \
+    __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);                                      \
     __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - 1, 0);                                  \
     __builtin_amdgcn_sched_barrier(0);                                                            \
   } while (0)
@@ -184,7 +246,7 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
 #define VDSL_DMA_ORDER_COPIES(LATE, NC)                                                           \
   do {                                                                                            \
     if (LATE) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                  \
-    __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);                                      \
+    __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);                                      \
     _Pragma("unroll") for (int c = 0; c < (NC); ++c) {                                            \
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                          \
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                          \
@@ -295,6 +357,7 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
 #undef VDSL_DMA_READ
 #undef VDSL_DMA_COPY_PART
 #undef VDSL_DMA_COPY
+#undef VDSL_DMA_SRC
 }
 
 // True when the direct-to-LDS loop with `bkb` K bytes per stage can run this K range.
