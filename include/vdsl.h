@@ -302,7 +302,11 @@ int vdsl_op_col_reduce(vdsl_queue q, int64_t rows, int64_t cols, int32_t dtype, 
 typedef enum vdsl_epilogue {
   VDSL_EPI_NONE = 0,
   VDSL_EPI_GELU = 1,    /* exact-erf GELU: 0.5 * v * (1 + erf(v / sqrt(2))) */
-  VDSL_EPI_RELU = 2
+  VDSL_EPI_RELU = 2,
+  /* GELU, with pre_act receiving GELU'(v) (f32) instead of v: what the backward pass multiplies
+   * by (vdsl_op_gemm_bf16_mul_packed), formed while erfc(-v / sqrt 2) is at hand for GELU(v).
+   * vdsl_op_gemm_bf16_packed only. */
+  VDSL_EPI_GELU_DERIV = 3
 } vdsl_epilogue;
 
 /* C (c_dtype [M][N]) = epilogue(op(A) . op(B)).
@@ -354,6 +358,14 @@ int vdsl_op_gemm_bf16_gelu_bwd(vdsl_queue q, int64_t M, int64_t N, int64_t K, vd
  * transposed weight of the layer above): same results bit for bit.  N % 32 == 0, K % 256 == 0. */
 int vdsl_op_gemm_bf16_gelu_bwd_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer A,
                                       vdsl_buffer Bp, vdsl_buffer pre, vdsl_buffer da, vdsl_buffer da_t);
+/* c = bf16((A Bp^T) * g) elementwise, c_t = c^T (optional): the GEMM forming dL/dh fused with the
+ * multiply by a stored local derivative g (f32 [M][N]; for a GELU layer, GELU'(pre) from the
+ * forward epilogue VDSL_EPI_GELU_DERIV), so with that g it equals vdsl_op_gemm_bf16_gelu_bwd_packed
+ * bit for bit without evaluating GELU' in the backward pass.  Bp packed by
+ * vdsl_op_pack_bf16_weights.  N % 32 == 0, K % 256 == 0.  No counterpart in the reference
+ * (north-star op class: compiler-generated backward GEMMs). */
+int vdsl_op_gemm_bf16_mul_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer A,
+                                 vdsl_buffer Bp, vdsl_buffer g, vdsl_buffer c, vdsl_buffer c_t);
 /* MSE: loss (f32 [1]) = mean((y - t)^2);  dy (bf16 [rows][cols]) = 2 (y - t) / (rows*cols);
  * dy_t (optional) = dy^T.  y, t: f32 [rows][cols].  partials: f32 scratch of
  * vdsl_mse_partials_count(rows, cols) elements (deterministic two-stage reduction). */

@@ -74,6 +74,7 @@ _lib.orc_transpose.argtypes = [_i64, _i64, C.c_int, _vp, _vp]
 _lib.orc_cast.argtypes = [_i64, C.c_int, _vp, C.c_int, _vp]
 _lib.orc_gelu_fwd.argtypes = [_i64, C.c_int, _vp, C.c_int, _vp]
 _lib.orc_gelu_bwd.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp]
+_lib.orc_gelu_grad.argtypes = [_i64, _vp, _vp]
 _lib.orc_mse_fwd_bwd.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp, _vp]
 _lib.orc_quantize_rows_i8.argtypes = [_i64, _i64, C.c_int, _vp, _vp, _vp]
 _lib.orc_gemm_w8a8_rows.argtypes = [_i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _i64, _i64]
@@ -229,6 +230,14 @@ def gelu_bwd(dh: np.ndarray, pre: np.ndarray):
     da_t = np.zeros((cols, rows), np.uint16)
     _lib.orc_gelu_bwd(rows, cols, _p(dh), _p(pre), _p(da), _p(da_t))
     return da, da_t
+
+
+def gelu_grad(x: np.ndarray) -> np.ndarray:
+    """GELU'(x) elementwise, f32 in and out."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.zeros(x.shape, np.float32)
+    _lib.orc_gelu_grad(x.size, _p(x), _p(y))
+    return y
 
 
 def mse_fwd_bwd(y: np.ndarray, t: np.ndarray):

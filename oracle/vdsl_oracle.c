@@ -31,7 +31,7 @@
  *                        constant row -> 1/cols, shift invariance, injected outlier argmax.
  *   orc_gemm_bf16        no reference code.  Pinned by exact integer-valued products (bf16
  *                        small integers), brute force in Python integers, and numpy f64.
- *   orc_gelu_fwd / orc_gelu_bwd / orc_mse_fwd_bwd
+ *   orc_gelu_fwd / orc_gelu_bwd / orc_gelu_grad / orc_mse_fwd_bwd
  *                        no reference code.  Pinned by central finite differences in f64.
  *   orc_quantize_rows_i8 / orc_gemm_w8a8 / orc_w8a8_dequant
  *                        no reference code.  Pinned by int64 numpy dot products (exact) and a
@@ -397,6 +397,13 @@ void orc_gelu_fwd(int64_t n, int x_dtype, const void* x, int y_dtype, void* y) {
 /* d/dv GELU(v) = Phi(v) + v phi(v) = 0.5 erfc(-v/sqrt2) + v exp(-v^2/2) / sqrt(2 pi), in f64. */
 static double gelu_grad_d(double v) {
   return 0.5 * erfc(-v * 0.70710678118654752440) + v * exp(-0.5 * v * v) * 0.39894228040143267794;
+}
+
+/* GELU'(x) elementwise in f32 (the f64 formula above, rounded once): the local derivative the
+ * forward epilogue VDSL_EPI_GELU_DERIV stores for the backward pass. */
+void orc_gelu_grad(int64_t n, const float* x, float* y) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) y[i] = (float)gelu_grad_d((double)x[i]);
 }
 
 void orc_gelu_bwd(int64_t rows, int64_t cols, const float* dh, const float* pre, uint16_t* da, uint16_t* da_t) {

@@ -15,7 +15,8 @@ import numpy as np
 import pytest
 
 from oracle import oracle
-from vernondsl_amd import graph, rng, spec
+from vernondsl_amd import _lib, graph, kernels, rng, spec
+from vernondsl_amd.rhi import Tensor
 
 pytestmark = pytest.mark.gpu
 
@@ -80,14 +81,27 @@ def test_mlp_config4_every_element(dev, q):
         by_kind.setdefault(op.kind, []).append(op)
     fwd1 = by_kind["linear"][0]
     mse = by_kind["linear_mse"][0]
-    bwd = by_kind["gemm_gelu_bwd"][0]
+    bwd = by_kind["gemm_mul_bwd"][0]
     rd = lambda v: exe.read(q, v.name)  # noqa: E731
-    pre, h = rd(fwd1.attrs["pre"]), exe.read(q, "H")
+    dgelu, h = rd(fwd1.attrs["dgelu"]), exe.read(q, "H")
     y, loss, dy, dy_t = (rd(v) for v in mse.outputs[:4])
     da, da_t = (rd(v) for v in bwd.outputs[:2])
     X, W1, W2 = _f32(x), _f32(w1), _f32(w2)
-    # forward: pre-activation, GELU (bf16, within one bf16 ulp of the oracle's libm GELU), Y
+    # The step keeps GELU'(pre), not pre: the same forward GEMM with the plain GELU epilogue on the
+    # step's own operands gives pre, and its H must equal the step's bit for bit.
+    tp, th = Tensor(dev, pre_shape := (x.shape[0], w1.shape[0]), "f32"), Tensor(dev, pre_shape, "bf16")
+    kernels.gemm_bf16_packed(q, exe.t["X"], exe.t[fwd1.attrs["packed"].name], th, _lib.EPI_GELU, tp)
+    pre = tp.numpy(q)
+    assert np.array_equal(th.numpy(q), h), "H from the GELU'-storing epilogue differs from the GELU one"
+    tp.free()
+    th.free()
+    # forward: pre-activation, GELU (bf16, within one bf16 ulp of the oracle's libm GELU), GELU'
+    # (within its approximation bound of the oracle's f64 GELU'), Y
     check_gemm(pre, X, W1.T, what="pre = X W1^T")
+    dg_ref = oracle.gelu_grad(pre).astype(np.float64)
+    err = np.abs(dgelu.astype(np.float64) - dg_ref) - (4e-7 * np.abs(dg_ref) + 2e-7)
+    w = np.unravel_index(np.argmax(err), err.shape)
+    assert err[w] <= 0, f"GELU'(pre) at {w}: pre {pre[w]!r} got {dgelu[w]!r} ref {dg_ref[w]!r}, {np.count_nonzero(err > 0)} over"
     h_ref = oracle.gelu_fwd(pre, y_bf16=True)
     ulps = np.abs(h.astype(np.int32) - h_ref.astype(np.int32))
     assert ulps.max() <= 1 and np.count_nonzero(ulps) <= 1e-3 * h.size, "H = GELU(pre)"

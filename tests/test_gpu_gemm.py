@@ -319,6 +319,45 @@ def test_gemm_gelu_bwd_fused_config4(dev, q):
         t.free()
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 4096), (256, 512, 512), (200, 544, 256)])
+def test_gelu_deriv_forward_and_mul_backward(dev, q, M, N, K):
+    """The stored-derivative pair: the forward GEMM with VDSL_EPI_GELU_DERIV gives the same H as
+    VDSL_EPI_GELU bit for bit and GELU'(pre) (against the oracle's f64 GELU' of the same pre: the
+    device GELU' is within 4e-7 relative plus 2e-7 absolute near its zero); the backward GEMM that
+    multiplies by it (vdsl_op_gemm_bf16_mul_packed) equals the GELU-backward GEMM on pre bit for bit,
+    da and da^T.  M = 200 leaves a ragged row tile (the per-element epilogues)."""
+    X, W = bf16_rand((M, K), 101), bf16_rand((N, K), 102)
+    G, W2 = bf16_rand((M, K), 103), bf16_rand((N, K), 104)  # the backward GEMM's dL/dy and W2^T
+    tX, tW, tG, tW2 = (Tensor.from_numpy(dev, q, a, "bf16") for a in (X, W, G, W2))
+    tWp, tW2p = Tensor(dev, (N, K), "bf16"), Tensor(dev, (N, K), "bf16")
+    kernels.pack_bf16_weights(q, tW, tWp)
+    kernels.pack_bf16_weights(q, tW2, tW2p)
+    H1, H2 = Tensor(dev, (M, N), "bf16"), Tensor(dev, (M, N), "bf16")
+    P, D = Tensor(dev, (M, N), "f32"), Tensor(dev, (M, N), "f32")
+    kernels.gemm_bf16_packed(q, tX, tWp, H1, _lib.EPI_GELU, P)
+    kernels.gemm_bf16_packed(q, tX, tWp, H2, _lib.EPI_GELU_DERIV, D)
+    pre, dg = P.numpy(q), D.numpy(q)
+    assert np.array_equal(H1.numpy(q), H2.numpy(q))
+    ref = oracle.gelu_grad(pre).astype(np.float64)
+    assert np.all(np.abs(dg.astype(np.float64) - ref) <= 4e-7 * np.abs(ref) + 2e-7)
+    outs = []
+    for mul in (False, True):
+        da, da_t = Tensor(dev, (M, N), "bf16"), Tensor(dev, (N, M), "bf16")
+        for t in (da, da_t):
+            t.buffer.fill_u32(q, 0x7FC07FC0)
+        if mul:
+            kernels.gemm_bf16_mul_packed(q, tG, tW2p, D, da, da_t)
+        else:
+            kernels.gemm_bf16_gelu_bwd(q, tG, tW2p, P, da, da_t, packed=True)
+        outs.append((da.numpy(q), da_t.numpy(q)))
+        da.free()
+        da_t.free()
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    assert np.array_equal(outs[1][1], outs[1][0].T)
+    for t in (tX, tW, tG, tW2, tWp, tW2p, H1, H2, P, D):
+        t.free()
+
+
 @pytest.mark.parametrize("M,N,K", [(2048, 4096, 4096), (128, 256, 256), (384, 768, 512)])
 def test_gemm_mse_fused_equals_gemm_then_mse(dev, q, M, N, K):
     """vdsl_op_gemm_bf16_mse_packed against the packed GEMM (f32 out) followed by the MSE op on its

@@ -45,6 +45,21 @@ def test_mlp_backward_prepared_transpose_and_fused_gelu():
     assert dW1.inputs[0] is dA.outputs[1]
 
 
+def test_mlp_stored_gelu_derivative():
+    """The config-4 default: the forward GELU GEMM stores GELU'(pre) in place of pre and the fused
+    backward GEMM multiplies by it; no value named pre remains, and the plain form keeps pre."""
+    g, _ = graph.mlp_train_graph(batch=256, d_in=512, hidden=512, d_out=256)
+    kinds = [op.kind for op in g.ops]
+    assert kinds == ["linear", "linear_mse", "gemm", "gemm_mul_bwd", "gemm"]
+    fwd, mul = g.ops[0], g.ops[3]
+    dg = fwd.attrs["dgelu"]
+    assert fwd.attrs["pre"] is None and fwd.outputs == [g.values["H"], dg] and dg.dtype == "f32"
+    assert mul.inputs[1].name == "W2.T.packed" and mul.inputs[2] is dg and mul.outputs[1].shape == (512, 256)
+    assert not any(n.startswith("pre#") for n in g.values)
+    g2, _ = graph.mlp_train_graph(batch=256, d_in=512, hidden=512, d_out=256, store_gelu_deriv=False)
+    assert [op.kind for op in g2.ops][3] == "gemm_gelu_bwd" and g2.ops[0].attrs["pre"] is not None
+
+
 def test_mlp_packed_weights():
     """pack_weights: each forward linear op on a param reads a packed copy made by a prepare op;
     the backward ops still read the row-major weight."""
@@ -64,7 +79,7 @@ def test_mlp_packed_weights():
 def test_mlp_default_graph_prepare_chain():
     """mlp_train_graph's default: packed forward weights, and the fused GELU-backward GEMM on W2^T
     packed (transpose, then pack: two prepare ops run in order)."""
-    g, _ = graph.mlp_train_graph(batch=64, d_in=512, hidden=512, d_out=256)
+    g, _ = graph.mlp_train_graph(batch=64, d_in=512, hidden=512, d_out=256, store_gelu_deriv=False)
     assert [op.kind for op in g.ops] == ["linear", "linear", "mse", "gemm", "gemm_gelu_bwd", "gemm"]
     assert [(op.kind, op.inputs[0].name, op.outputs[0].name) for op in g.prepare_ops] == [
         ("pack_bf16", "W1", "W1.packed"), ("pack_bf16", "W2", "W2.packed"), ("transpose", "W2", "W2.T"),

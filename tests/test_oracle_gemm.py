@@ -101,6 +101,21 @@ def test_gelu_bwd_matches_finite_differences():
     assert np.array_equal(da_t, da.T)
 
 
+def test_gelu_grad_f32_matches_finite_differences():
+    """The f32 GELU' (what the forward epilogue stores for the backward pass) against central
+    differences of the f64 GELU, and equal to the f32 rounding of the backward's factor (dh = 1)."""
+    pre = np.linspace(-6, 6, 4001).astype(np.float32)
+    g = oracle.gelu_grad(pre).astype(np.float64)
+    p = pre.astype(np.float64)
+    h = 1e-5
+    gelu = lambda v: 0.5 * v * (1 + erf(v / np.sqrt(2)))  # noqa: E731
+    fd = (gelu(p + h) - gelu(p - h)) / (2 * h)
+    assert np.all(np.abs(g - fd) <= 1e-7 * np.abs(fd) + 1e-9)
+    da, _ = oracle.gelu_bwd(np.ones((1, pre.size), np.float32), pre.reshape(1, -1))
+    assert np.array_equal(da[0], rng.f32_to_bf16(g.astype(np.float32)))
+    assert oracle.gelu_grad(np.array([0.0], np.float32))[0] == np.float32(0.5)
+
+
 def test_gelu_grad_keeps_relative_accuracy_for_negative_pre():
     pre = np.array([[-3.0, -5.0, -7.0, -9.0]], np.float32)
     da, _ = oracle.gelu_bwd(np.ones_like(pre), pre)

@@ -53,7 +53,7 @@ MAP_OPS = {
 }
 BCAST_FULL, BCAST_ROW, BCAST_COL, BCAST_SCALAR = 0, 1, 2, 3
 
-EPI_NONE, EPI_GELU, EPI_RELU = 0, 1, 2
+EPI_NONE, EPI_GELU, EPI_RELU, EPI_GELU_DERIV = 0, 1, 2, 3
 
 
 # ---- structs -------------------------------------------------------------------------------
@@ -148,6 +148,7 @@ PROTOTYPES = {
     "vdsl_op_gelu_bwd": (C.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "vdsl_op_gemm_bf16_gelu_bwd": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
     "vdsl_op_gemm_bf16_gelu_bwd_packed": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "vdsl_op_gemm_bf16_mul_packed": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
     "vdsl_mse_partials_count": (C.c_int64, [_i64, _i64]),
     "vdsl_op_mse_fwd_bwd": (C.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vdsl_op_quantize_rows_i8": (C.c_int, [_vp, _i64, _i64, _i32, _vp, _vp, _vp]),

@@ -161,7 +161,8 @@ __device__ __forceinline__ float gelu_grad_f(float v) {
   // d/dv [0.5 v (1 + erf(v / sqrt2))] = Phi(v) + v phi(v), with Phi(v) = 0.5 erfc(-v / sqrt2)
   // (erfc keeps full relative accuracy where 1 + erf(.) would cancel, v < 0).  Branch-free:
   // erfc_cheb (fractional error < 1.2e-7) and exp_fast (< 2e-7 + 1 ulp); the result is rounded
-  // to bf16, and near the zero of GELU' (v = -0.75) the absolute error stays below 1e-7.
+  // to bf16, and near the zero of GELU' (v = -0.75) the absolute error stays below 2e-7 (1.2e-7
+  // measured over config 4's 8.4 M pre-activations against the f64 formula).
   return 0.5f * erfc_cheb(-v * 0.7071067811865476f) + v * exp_fast(-0.5f * v * v) * 0.3989422804014327f;
 }
 

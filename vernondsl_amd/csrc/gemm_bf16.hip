@@ -76,18 +76,35 @@ constexpr int kFirstDma = 14, kFirstDma128 = 23;
 
 // Internal epilogue code of vdsl_op_gemm_bf16_gelu_bwd: C (bf16) = v * GELU'(pre) with `pre` an
 // input, and the same values transposed into `ctr` ([N][M], optional).
-constexpr int kEpiGeluBwd = 3;
+constexpr int kEpiGeluBwd = 100;
 
-// Epilogue of one accumulator element at (row, col), shared by both main loops.
-template <bool BWD>
+// Backward epilogue modes (template argument BWD): 0 = forward (epi selects it), 1 = C = v *
+// GELU'(pre) (vdsl_op_gemm_bf16_gelu_bwd), 2 = C = v * g with the factor g given in `pre`
+// (vdsl_op_gemm_bf16_mul_packed).  With g = GELU'(pre) from the forward epilogue
+// VDSL_EPI_GELU_DERIV, modes 1 and 2 compute the same product and round it the same way.
+template <int BWD>
+__device__ __forceinline__ float bwd_factor(float p) {
+  if constexpr (BWD == 2) return p;
+  else return gelu_grad_f(p);
+}
+
+// Epilogue of one accumulator element at (row, col), shared by both main loops.  DERIV: the
+// kernel runs VDSL_EPI_GELU_DERIV only (a separate instantiation: in the shared forward kernels
+// its code made the register allocator spill).
+template <int BWD, bool DERIV = false>
 __device__ __forceinline__ void bf16_epilogue(float v, int row, int col, int M, int N, void* __restrict__ C,
                                               float* __restrict__ pre, int epi, int c_dtype, uint16_t* __restrict__ ctr) {
   if (row < M && col < N) {
     const size_t o = static_cast<size_t>(row) * N + col;
-    if constexpr (BWD) {
-      const uint16_t h = f32_to_bf16(v * gelu_grad_f(pre[o]));
+    if constexpr (BWD != 0) {
+      const uint16_t h = f32_to_bf16(v * bwd_factor<BWD>(pre[o]));
       static_cast<uint16_t*>(C)[o] = h;
       if (ctr) ctr[static_cast<size_t>(col) * M + row] = h;
+      return;
+    }
+    if constexpr (DERIV) {
+      pre[o] = gelu_grad_f(v);
+      static_cast<uint16_t*>(C)[o] = f32_to_bf16(gelu_f(v));
       return;
     }
     if (pre) pre[o] = v;
@@ -125,19 +142,27 @@ __device__ __forceinline__ void bf16_epilogue_tile(const f32x16 (&acc)[Cfg::FM][
 }
 
 // Picks the whole-tile variant when one applies, else the generic per-element epilogue.
-template <class Cfg, bool BWD>
+template <class Cfg, int BWD, bool DERIV = false>
 __device__ __forceinline__ void bf16_store_tile(const f32x16 (&acc)[Cfg::FM][Cfg::FN], int m0, int n0, int M, int N,
                                                 void* __restrict__ C, float* __restrict__ pre, int epi, int c_dtype,
                                                 uint16_t* __restrict__ ctr) {
   const bool whole = m0 + Cfg::BM <= M && n0 + Cfg::BN <= N;
-  if (BWD) {
+  if (DERIV) {
 #pragma unroll
     for (int i = 0; i < Cfg::FM; ++i)
 #pragma unroll
       for (int j = 0; j < Cfg::FN; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          bf16_epilogue<true>(acc[i][j][r], acc_row<Cfg>(m0, i, r), acc_col<Cfg>(n0, j), M, N, C, pre, epi, c_dtype, ctr);
+          bf16_epilogue<0, true>(acc[i][j][r], acc_row<Cfg>(m0, i, r), acc_col<Cfg>(n0, j), M, N, C, pre, epi, c_dtype, ctr);
+  } else if (BWD != 0) {
+#pragma unroll
+    for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          bf16_epilogue<BWD>(acc[i][j][r], acc_row<Cfg>(m0, i, r), acc_col<Cfg>(n0, j), M, N, C, pre, epi, c_dtype, ctr);
   } else if (whole && epi == VDSL_EPI_NONE && c_dtype == VDSL_F32 && !pre) {
     bf16_epilogue_tile<Cfg, 0>(acc, m0, n0, N, C, pre);
   } else if (whole && epi == VDSL_EPI_GELU && c_dtype == VDSL_BF16 && pre) {
@@ -149,7 +174,7 @@ __device__ __forceinline__ void bf16_store_tile(const f32x16 (&acc)[Cfg::FM][Cfg
       for (int j = 0; j < Cfg::FN; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          bf16_epilogue<false>(acc[i][j][r], acc_row<Cfg>(m0, i, r), acc_col<Cfg>(n0, j), M, N, C, pre, epi, c_dtype, ctr);
+          bf16_epilogue<0>(acc[i][j][r], acc_row<Cfg>(m0, i, r), acc_col<Cfg>(n0, j), M, N, C, pre, epi, c_dtype, ctr);
   }
 }
 
@@ -187,7 +212,14 @@ __device__ __forceinline__ void bf16_epilogue_tile_lds(const f32x16 (&acc)[Cfg::
       if (VARIANT == 0) {
         *reinterpret_cast<f32x4*>(static_cast<float*>(C) + o) = v;
       } else {
-        *reinterpret_cast<f32x4*>(pre + o) = v;
+        if (VARIANT == 1) {
+          *reinterpret_cast<f32x4*>(pre + o) = v;
+        } else {  // GELU'(v) for the backward pass; erfc(-v / sqrt2) is shared with GELU(v) below
+          f32x4 d;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) d[e] = gelu_grad_f(v[e]);
+          *reinterpret_cast<f32x4*>(pre + o) = d;
+        }
         uint2 h;
         h.x = pack_bf16x2(gelu_f(v[0]), gelu_f(v[1]));
         h.y = pack_bf16x2(gelu_f(v[2]), gelu_f(v[3]));
@@ -205,7 +237,7 @@ __device__ __forceinline__ void bf16_epilogue_tile_lds(const f32x16 (&acc)[Cfg::
 // pass long before): every load of it for the wave's whole tile is issued first, before the block
 // barrier that ends the main loop, so the tile pays one memory latency instead of one per unit
 // (in a training step the per-unit form made this GEMM 38 us slower than without the epilogue).
-template <class Cfg, int LDS_AVAIL = Cfg::LDS_BYTES>
+template <class Cfg, int LDS_AVAIL = Cfg::LDS_BYTES, int BWD = 1>
 __device__ __forceinline__ void bf16_epilogue_bwd_lds(const f32x16 (&acc)[Cfg::FM][Cfg::FN], int m0, int n0, int M,
                                                       int N, void* __restrict__ C, const float* __restrict__ pre,
                                                       char* smem, uint16_t* __restrict__ ctr) {
@@ -258,7 +290,7 @@ __device__ __forceinline__ void bf16_epilogue_bwd_lds(const f32x16 (&acc)[Cfg::F
       const size_t o = static_cast<size_t>(row0 + 32 * i + row) * N + col0 + 4 * c4;
       f32x4 d;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) d[e] = v[e] * gelu_grad_f(x[i][k][e]);
+      for (int e = 0; e < 4; ++e) d[e] = v[e] * bwd_factor<BWD>(x[i][k][e]);
       uint2 h;
       h.x = pack_bf16x2(d[0], d[1]);
       h.y = pack_bf16x2(d[2], d[3]);
@@ -434,20 +466,22 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_simple(const uint16_t* __res
 // 2048x4096x4096 (random bf16, f32 out): 61-63 us against 66-68 us for the direct-to-LDS kernel.
 using Pb0 = BpkConfig<MfmaBf16, 4, 2, 4, 3>;  // 128 x 256 blocks, 4 waves of 128 x 64
 
-// BWD: the GELU-backward epilogue of vdsl_op_gemm_bf16_gelu_bwd_packed (C = da, pre an input, ctr =
-// da^T); its LDS is enlarged so the whole wave tile stages at once (whole-line transposed stores).
+// BWD: the backward epilogues (1: vdsl_op_gemm_bf16_gelu_bwd_packed, C = da, pre an input, ctr =
+// da^T; 2: vdsl_op_gemm_bf16_mul_packed, the factor given); their LDS is enlarged so the whole wave
+// tile stages at once (whole-line transposed stores).
 template <class Cfg, bool BWD>
 constexpr int bpk_bf16_smem() {
   return BWD && Cfg::NW * Cfg::WTM * (Cfg::WTN + 8) * 4 > Cfg::LDS_BYTES ? Cfg::NW * Cfg::WTM * (Cfg::WTN + 8) * 4
                                                                           : Cfg::LDS_BYTES;
 }
 
-template <class Cfg, bool BWD>
+// BWD: the backward epilogue mode (bf16_epilogue); DERIV: the forward VDSL_EPI_GELU_DERIV kernel.
+template <class Cfg, int BWD, bool DERIV = false>
 __global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_bpk(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bp,
                                                          void* __restrict__ C, float* __restrict__ pre, int M, int N, int K,
                                                          int epi, int c_dtype, uint16_t* __restrict__ ctr) {
   // The only __shared__ variable (see gemm_bpk.h); after the main loop it stages the epilogue.
-  __shared__ __attribute__((aligned(1024))) char smem[bpk_bf16_smem<Cfg, BWD>()];
+  __shared__ __attribute__((aligned(1024))) char smem[bpk_bf16_smem<Cfg, BWD != 0>()];
   // Tiles in groups of 8 tile-rows, walked column-major (tile_coords): the 32 blocks one XCD runs
   // (congruent ids, made consecutive by xcd_remap) then cover 8 row tiles x 4 column panels, so
   // each XCD's L2 fetches 1/2 of A and 1/4 of B (2048x4096x4096: 128 MB fetched in all, against
@@ -461,9 +495,15 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_bpk(const uint16_t* __re
                               m0, n0, smem, acc);
   static_assert(kLdsEpilogue<Cfg>, "the LDS-staged epilogue must fit the main loop's LDS");
   const bool whole = m0 + Cfg::BM <= M && n0 + Cfg::BN <= N && N % 4 == 0;
-  if constexpr (BWD) {
+  if constexpr (BWD != 0) {
     if (whole && (!ctr || M % 8 == 0)) {
-      bf16_epilogue_bwd_lds<Cfg, bpk_bf16_smem<Cfg, true>()>(acc, m0, n0, M, N, C, pre, smem, ctr);
+      bf16_epilogue_bwd_lds<Cfg, bpk_bf16_smem<Cfg, true>(), BWD>(acc, m0, n0, M, N, C, pre, smem, ctr);
+      return;
+    }
+  } else if constexpr (DERIV) {
+    if (whole) {
+      __syncthreads();  // every wave is past its last read of the main loop's LDS
+      bf16_epilogue_tile_lds<Cfg, 2>(acc, m0, n0, N, C, pre, smem);
       return;
     }
   } else {
@@ -476,7 +516,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_bpk(const uint16_t* __re
       return;
     }
   }
-  bf16_store_tile<Cfg, BWD>(acc, m0, n0, M, N, C, pre, epi, c_dtype, ctr);
+  bf16_store_tile<Cfg, BWD, DERIV>(acc, m0, n0, M, N, C, pre, epi, c_dtype, ctr);
 }
 
 // The packed GEMM fused with the MSE loss of its f32 output (vdsl_op_gemm_bf16_mse_packed): whole
@@ -713,14 +753,17 @@ extern "C" int vdsl_op_gemm_bf16_packed(vdsl_queue q, int64_t M, int64_t N, int6
   if (N % 32) return fail(VDSL_ERR_UNSUPPORTED, "packed GEMM needs N % 32 == 0");
   if ((2 * K) % (128 * Pb0::NR) || K == 0) return fail(VDSL_ERR_UNSUPPORTED, "packed bf16 GEMM needs K % 256 == 0 and K > 0");
   if (c_dtype != VDSL_F32 && c_dtype != VDSL_BF16) return fail(VDSL_ERR_UNSUPPORTED, "C must be f32 or bf16");
-  if (epilogue < VDSL_EPI_NONE || epilogue > VDSL_EPI_RELU) return fail(VDSL_ERR_INVALID_ARG, "unknown epilogue");
+  if (epilogue < VDSL_EPI_NONE || epilogue > VDSL_EPI_GELU_DERIV) return fail(VDSL_ERR_INVALID_ARG, "unknown epilogue");
+  if (epilogue == VDSL_EPI_GELU_DERIV && (!pre_act || c_dtype != VDSL_BF16))
+    return fail(VDSL_ERR_INVALID_ARG, "VDSL_EPI_GELU_DERIV needs pre_act and a bf16 C");
   VDSL_TRY(check_buffer(q, A, nbytes(M, K, 2), "A", false));
   VDSL_TRY(check_buffer(q, Bp, nbytes(N, K, 2), "Bp", false));
   VDSL_TRY(check_buffer(q, C, nbytes(M, N, dtype_size(c_dtype)), "C", true));
   if (pre_act) VDSL_TRY(check_buffer(q, pre_act, nbytes(M, N, 4), "pre_act", true));
   if (M == 0 || N == 0) return VDSL_OK;
   const int64_t tiles = ((M + Pb0::BM - 1) / Pb0::BM) * ((N + Pb0::BN - 1) / Pb0::BN);
-  hipLaunchKernelGGL((gemm_bf16_bpk<Pb0, false>), dim3(static_cast<unsigned>(tiles)), dim3(Pb0::NT), 0, q->stream,
+  auto* kern = epilogue == VDSL_EPI_GELU_DERIV ? gemm_bf16_bpk<Pb0, 0, true> : gemm_bf16_bpk<Pb0, 0, false>;
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles)), dim3(Pb0::NT), 0, q->stream,
                      static_cast<const uint16_t*>(A->ptr), static_cast<const uint16_t*>(Bp->ptr), C->ptr,
                      pre_act ? static_cast<float*>(pre_act->ptr) : nullptr, static_cast<int>(M), static_cast<int>(N),
                      static_cast<int>(K), epilogue, c_dtype, nullptr);
@@ -741,11 +784,32 @@ extern "C" int vdsl_op_gemm_bf16_gelu_bwd_packed(vdsl_queue q, int64_t M, int64_
   if (da_t) VDSL_TRY(check_buffer(q, da_t, nbytes(M, N, 2), "da_t", true));
   if (M == 0 || N == 0) return VDSL_OK;
   const int64_t tiles = ((M + Pb0::BM - 1) / Pb0::BM) * ((N + Pb0::BN - 1) / Pb0::BN);
-  hipLaunchKernelGGL((gemm_bf16_bpk<Pb0, true>), dim3(static_cast<unsigned>(tiles)), dim3(Pb0::NT), 0, q->stream,
+  hipLaunchKernelGGL((gemm_bf16_bpk<Pb0, 1>), dim3(static_cast<unsigned>(tiles)), dim3(Pb0::NT), 0, q->stream,
                      static_cast<const uint16_t*>(A->ptr), static_cast<const uint16_t*>(Bp->ptr), da->ptr,
                      static_cast<float*>(pre->ptr), static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
                      kEpiGeluBwd, VDSL_BF16, da_t ? static_cast<uint16_t*>(da_t->ptr) : nullptr);
   return check_launch("gemm_bf16_bpk<gelu_bwd>");
+}
+
+extern "C" int vdsl_op_gemm_bf16_mul_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer A, vdsl_buffer Bp,
+                                            vdsl_buffer g, vdsl_buffer c, vdsl_buffer c_t) {
+  VDSL_TRY(enter_queue(q));
+  if (M < 0 || N < 0 || K < 0) return fail(VDSL_ERR_INVALID_ARG, "negative GEMM extent");
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x3fffffff) return fail(VDSL_ERR_UNSUPPORTED, "GEMM extent too large");
+  if (N % 32) return fail(VDSL_ERR_UNSUPPORTED, "packed GEMM needs N % 32 == 0");
+  if ((2 * K) % (128 * Pb0::NR) || K == 0) return fail(VDSL_ERR_UNSUPPORTED, "packed bf16 GEMM needs K % 256 == 0 and K > 0");
+  VDSL_TRY(check_buffer(q, A, nbytes(M, K, 2), "A", false));
+  VDSL_TRY(check_buffer(q, Bp, nbytes(N, K, 2), "Bp", false));
+  VDSL_TRY(check_buffer(q, g, nbytes(M, N, 4), "g", false));
+  VDSL_TRY(check_buffer(q, c, nbytes(M, N, 2), "c", true));
+  if (c_t) VDSL_TRY(check_buffer(q, c_t, nbytes(M, N, 2), "c_t", true));
+  if (M == 0 || N == 0) return VDSL_OK;
+  const int64_t tiles = ((M + Pb0::BM - 1) / Pb0::BM) * ((N + Pb0::BN - 1) / Pb0::BN);
+  hipLaunchKernelGGL((gemm_bf16_bpk<Pb0, 2>), dim3(static_cast<unsigned>(tiles)), dim3(Pb0::NT), 0, q->stream,
+                     static_cast<const uint16_t*>(A->ptr), static_cast<const uint16_t*>(Bp->ptr), c->ptr,
+                     static_cast<float*>(g->ptr), static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
+                     kEpiGeluBwd, VDSL_BF16, c_t ? static_cast<uint16_t*>(c_t->ptr) : nullptr);
+  return check_launch("gemm_bf16_bpk<mul>");
 }
 
 extern "C" int vdsl_op_gemm_bf16_mse_packed(vdsl_queue q, int64_t M, int64_t N, int64_t K, vdsl_buffer A, vdsl_buffer Bp,

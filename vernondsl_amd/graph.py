@@ -50,7 +50,8 @@ class Op:
 
 class Graph:
     def __init__(self, prepare_transposes: bool = False, fuse_gelu_backward: bool = False,
-                 pack_weights: bool = False, fuse_mse: bool = False, keep_y: bool = True):
+                 pack_weights: bool = False, fuse_mse: bool = False, keep_y: bool = True,
+                 store_gelu_deriv: bool = False):
         # prepare_transposes: backward() takes a param's transpose (the NT form's B of dL/dx) from a
         # prepare op instead of transposing the param inside every step's GEMM.
         # fuse_gelu_backward (needs prepare_transposes): GELU' is applied in the epilogue of the GEMM
@@ -70,6 +71,11 @@ class Graph:
         # memory before the loss; keep_y: that op still stores y (the gradient does not need it).
         self.fuse_mse = fuse_mse
         self.keep_y = keep_y
+        # store_gelu_deriv (with fuse_gelu_backward and packed weights): the forward GELU GEMM stores
+        # GELU'(pre) instead of pre (VDSL_EPI_GELU_DERIV, sharing erfc with GELU), and the fused
+        # backward GEMM multiplies by it (vdsl_op_gemm_bf16_mul_packed) instead of evaluating GELU'
+        # after its main loop; the same products rounded the same way, bit for bit.
+        self.store_gelu_deriv = store_gelu_deriv
         self.values: dict[str, Value] = {}
         self.ops: list[Op] = []
         # Ops that derive constant operands from params (weight packing): run by
@@ -244,7 +250,17 @@ class Graph:
                     packed = self.pack_weights and wt.shape[0] % 32 == 0 and wt.shape[1] % 256 == 0
                     if packed:  # W^T packed into MFMA fragment order (a second prepare op)
                         wt = self._prepared(wt, "packed", wt.shape, "pack_bf16")
-                    self._op("gemm_gelu_bwd", [gb, wt, xp.attrs["pre"]], [da, da_t], packed=packed)
+                    if packed and self.store_gelu_deriv and xp.attrs.get("packed") is not None:
+                        # the forward op keeps GELU'(pre) in place of pre, which nothing else reads
+                        pre = xp.attrs["pre"]
+                        dg = self._value(self._fresh("dgelu"), pre.shape, "f32")
+                        xp.outputs[xp.outputs.index(pre)] = dg
+                        dg.producer = xp
+                        del self.values[pre.name]
+                        xp.attrs["pre"], xp.attrs["dgelu"] = None, dg
+                        self._op("gemm_mul_bwd", [gb, wt, dg], [da, da_t])
+                    else:
+                        self._op("gemm_gelu_bwd", [gb, wt, xp.attrs["pre"]], [da, da_t], packed=packed)
                     grad[x.name] = ("gelu_da", da, da_t)
                 else:
                     dx = self._value(self._fresh("d_" + x.name), x.shape, "f32", "grad")
@@ -380,6 +396,9 @@ class Executable:
         if op.kind == "gemm_gelu_bwd":
             (M, K), N = ins[0].shape, ins[1].shape[0]
             return f"gemm + GELU backward ({'packed' if op.attrs.get('packed') else 'row-major'} B) {M}x{N}x{K}"
+        if op.kind == "gemm_mul_bwd":
+            (M, K), N = ins[0].shape, ins[1].shape[0]
+            return f"gemm x stored GELU' (packed B) {M}x{N}x{K}"
         if op.kind in ("w8a8", "w8a8_packed"):
             (M, K), N = ins[0].shape, ins[2].shape[0]
             return f"{op.kind} {'relu' if op.attrs['relu'] else 'no relu'} {M}x{N}x{K}"
@@ -388,7 +407,7 @@ class Executable:
     def op_flops(self, op: Op) -> int:
         """2 M N K for a GEMM op (multiply-adds of its main loop), 0 otherwise."""
         ins = op.inputs
-        if op.kind in ("linear", "gemm_gelu_bwd", "linear_mse"):
+        if op.kind in ("linear", "gemm_gelu_bwd", "gemm_mul_bwd", "linear_mse"):
             return 2 * ins[0].shape[0] * ins[0].shape[1] * ins[1].shape[0]
         if op.kind == "gemm":
             a, b = ins
@@ -406,6 +425,8 @@ class Executable:
         if op.kind == "linear":
             pre = T[op.attrs["pre"].name] if op.attrs["pre"] is not None else None
             epi = {"none": _lib.EPI_NONE, "gelu": _lib.EPI_GELU, "relu": _lib.EPI_RELU}[op.attrs["act"]]
+            if op.attrs.get("dgelu") is not None:  # GELU'(pre) stored in place of pre
+                epi, pre = _lib.EPI_GELU_DERIV, T[op.attrs["dgelu"].name]
             if op.attrs.get("packed") is not None:
                 kernels.gemm_bf16_packed(q, ins[0], T[op.attrs["packed"].name], outs[0], epi, pre)
             else:
@@ -428,6 +449,8 @@ class Executable:
             kernels.gelu_bwd(q, ins[0], ins[1], outs[0], outs[1])
         elif op.kind == "gemm_gelu_bwd":
             kernels.gemm_bf16_gelu_bwd(q, ins[0], ins[1], ins[2], outs[0], outs[1], op.attrs.get("packed", False))
+        elif op.kind == "gemm_mul_bwd":
+            kernels.gemm_bf16_mul_packed(q, ins[0], ins[1], ins[2], outs[0], outs[1])
         elif op.kind == "cast":
             kernels.cast(q, ins[0], outs[0])
         elif op.kind == "transpose":
@@ -485,13 +508,12 @@ class Step:
 
 # ---- the two workload graphs ------------------------------------------------------------------------
 def mlp_train_graph(batch=2048, d_in=4096, hidden=4096, d_out=4096, prepare_transposes=True,
-                    fuse_gelu_backward=True, pack_weights=True, fuse_mse=True, keep_y=True):
+                    fuse_gelu_backward=True, pack_weights=True, fuse_mse=True, keep_y=True, store_gelu_deriv=True):
     """Config 4: X -> GELU(X W1^T) -> (.) W2^T -> MSE(., T), with backward for W1 and W2.
 
     The defaults are the fastest form measured on MI355X (one process, graph replays, same
-    gradients bit for bit): 400 us per step, against 415 us with packed weights alone and 438 us
-    with none of the three options."""
-    g = Graph(prepare_transposes, fuse_gelu_backward, pack_weights, fuse_mse, keep_y)
+    gradients bit for bit as the plain graph with none of the options)."""
+    g = Graph(prepare_transposes, fuse_gelu_backward, pack_weights, fuse_mse, keep_y, store_gelu_deriv)
     x = g.input("X", (batch, d_in), "bf16")
     w1 = g.param("W1", (hidden, d_in), "bf16")
     w2 = g.param("W2", (d_out, hidden), "bf16")

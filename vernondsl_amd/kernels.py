@@ -227,6 +227,22 @@ def gemm_bf16_gelu_bwd(q: Queue, A: Tensor, B: Tensor, pre: Tensor, da: Tensor, 
          B.handle, pre.handle, da.handle, _h(da_t))
 
 
+def gemm_bf16_mul_packed(q: Queue, A: Tensor, Bp: Tensor, g: Tensor, c: Tensor, c_t=None):
+    """c = bf16((A Bp^T) * g) (and c_t = c^T): the GEMM forming dL/dh fused with the multiply by a
+    stored local derivative g (f32 [M][N], e.g. GELU'(pre) from a forward GEMM with the
+    EPI_GELU_DERIV epilogue).  Bp: packed [N][K] weights."""
+    M, K = A.shape
+    N, K2 = Bp.shape
+    if K != K2:
+        raise ValueError(f"inner dimensions differ: {K} vs {K2}")
+    _expect(A, (M, K), "bf16", "A")
+    _expect(Bp, (N, K), "bf16", "Bp")
+    _expect(g, (M, N), "f32", "g")
+    _expect(c, (M, N), "bf16", "c")
+    _expect(c_t, (N, M), "bf16", "c_t")
+    call("vdsl_op_gemm_bf16_mul_packed", q.handle, M, N, K, A.handle, Bp.handle, g.handle, c.handle, _h(c_t))
+
+
 def mse_partials_count(rows, cols) -> int:
     return int(_lib.lib.vdsl_mse_partials_count(rows, cols))
 
