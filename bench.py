@@ -151,7 +151,8 @@ def time_ops_in_step(q, dev, exe, reps, warmup_ms=25.0):
 
 
 def in_step_report(exe, op_ms, peak, unit_scale=1e12):
-    """Per-op in-step rows and the dominant GEMM op (the one with the most in-step time)."""
+    """Per-op in-step rows and the dominant GEMM op (the one with the most in-step time):
+    (label, ms, flops, op kind)."""
     rows, dom = [], None
     for op, ms in zip(exe.graph.ops, op_ms):
         fl = exe.op_flops(op)
@@ -160,7 +161,7 @@ def in_step_report(exe, op_ms, peak, unit_scale=1e12):
             rate = fl / (ms * 1e-3) / unit_scale
             row.update(rate=round(rate, 1), frac=round(rate / peak, 4))
             if dom is None or ms > dom[1]:
-                dom = (row["op"], ms, fl)
+                dom = (row["op"], ms, fl, op.kind)
         rows.append(row)
     return rows, dom
 
@@ -461,7 +462,7 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
     eager_ms = time_launches(q, dev, lambda: exe.run(q), n, warmup=2)
     # every op's in-step duration: events between the ops of eagerly issued steps
     op_ms, ev_step_ms = time_ops_in_step(q, dev, exe, n)
-    rows, (dom_op, dom_ms, dom_flop) = in_step_report(exe, op_ms, PEAK_BF16_TFLOPS)
+    rows, (dom_op, dom_ms, dom_flop, dom_kind) = in_step_report(exe, op_ms, PEAK_BF16_TFLOPS)
     flops = spec.mlp_flops(B, D, Hd, O)
     tflops = flops / (ms * 1e-3) / 1e12
     gemm_ms = sum(r["ms"] for r in rows if "rate" in r)
@@ -477,7 +478,7 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
                        "method": "HIP events after every op of eagerly issued steps on the real buffers"},
            "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                         "frac": gt / PEAK_BF16_TFLOPS, "kernel": f"dominant in-step op: {dom_op}",
-                        "kernel_ms": dom_ms, "traffic": measured_traffic("gemm_bf16")},
+                        "kernel_ms": dom_ms, "traffic": measured_traffic("c4:" + dom_kind)},
            "whole_graph_frac_of_peak": tflops / PEAK_BF16_TFLOPS}
     if do_cpu:  # CPU-baseline leg
         from oracle import oracle
@@ -533,7 +534,7 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
            "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
                         "frac": gt / PEAK_INT8_TOPS,
                         "kernel": "gemm_w8a8_bpk 512x8192x8192 (dequant+ReLU), mean of the three layers as timed inside the step",
-                        "kernel_ms": kms, "traffic": measured_traffic("gemm_w8a8")},
+                        "kernel_ms": kms, "traffic": measured_traffic("c5:w8a8_packed")},
            "whole_graph_frac_of_peak": tops / PEAK_INT8_TOPS}
     if do_cpu:
         r, r1 = 16, 2
@@ -546,22 +547,38 @@ def bench_w8a8(dev, q, steps, warmup, do_cpu):
 
 
 # ---- HBM traffic from counter passes ----------------------------------------------------------------
-# name in --kernel mode -> (substring of the profiled kernel's name, algorithmic bytes per launch)
+# traffic key -> (--kernel run it is measured in, substring of the profiled kernel's name, grid size
+# in work-items or None, algorithmic bytes per launch).  The c4:/c5: keys are the GEMMs of the
+# config-4 and config-5 steps as they run inside the step (one eager step per rep), keyed by the
+# graph op kind whose in-step time bench.py reports.
+_MB = 1 << 20
+_C4_BPK = "gemm_bf16_bpk<vdsl::BpkConfig<vdsl::MfmaBf16, 4, 2, 4, 3>, "
+
+
 def _traffic_kernels():
     from vernondsl_amd import _lib, spec
     return {
-        "copy": ("copyBuffer", 2 * (512 << 20)),
-        "map_chain": ("map_chain_kernel", spec.map_chain_bytes(8192, 8192)),
-        "softmax_f32": ("row_softmax_split<0", spec.softmax_bytes(16384, 4096, _lib.F32)),
-        "softmax_bf16": ("row_softmax_split<1", spec.softmax_bytes(16384, 4096, _lib.BF16)),
-        # A, B read once; bf16 H and f32 pre-activation written once
-        "gemm_bf16": ("gemm_bf16_", 2 * (2048 * 4096 + 4096 * 4096 + 2048 * 4096) + 4 * 2048 * 4096),
-        # int8 A, B and the two scale vectors read once; bf16 Y written once
-        "gemm_w8a8": ("gemm_w8a8_", 512 * 8192 + 8192 * 8192 + 4 * (512 + 8192) + 2 * 512 * 8192),
+        "copy": ("copy", "copyBuffer", None, 2 * (512 << 20)),
+        "map_chain": ("map_chain", "map_chain_kernel", None, spec.map_chain_bytes(8192, 8192)),
+        "softmax_f32": ("softmax_f32", "row_softmax_split<0", None, spec.softmax_bytes(16384, 4096, _lib.F32)),
+        "softmax_bf16": ("softmax_bf16", "row_softmax_split<1", None, spec.softmax_bytes(16384, 4096, _lib.BF16)),
         # vec3 positions read, vec4 positions and vec3 varyings written (2^24 vertices)
-        "vec_transform": ("vec_transform_kernel", (1 << 24) * 40),
+        "vec_transform": ("vec_transform", "vec_transform_kernel", None, (1 << 24) * 40),
         # vec4 [4096][4096] read and written
-        "swizzle": ("map_chain_v_kernel", 2 * 4096 * 4096 * 16),
+        "swizzle": ("swizzle", "vdsl_map_jit", None, 2 * 4096 * 4096 * 16),  # the chain compiled at run time
+        # config 4 (2048 x 4096 x 4096 and 4096 x 4096 x 2048 bf16): operands read once, outputs written once
+        # X, W1 read; H (bf16) and GELU'(pre) (f32) written
+        "c4:linear": ("c4_step", _C4_BPK + "0, true>", None, (16 + 32 + 16 + 32) * _MB),
+        # H, W2, T read; Y (f32), dL/dY and its transpose (bf16) written
+        "c4:linear_mse": ("c4_step", "gemm_bf16_bpk_mse", None, (16 + 32 + 32 + 32 + 16 + 16) * _MB),
+        # dL/dY^T (or dL/dpre^T) and H (or X) read; the f32 weight gradient written
+        "c4:gemm": ("c4_step", "gemm_bf16_dma<vdsl::DmaConfig<vdsl::MfmaBf16, 256, 256, 2, 4, 3, 64>, false, true>", None,
+                    (16 + 16 + 64) * _MB),
+        # dL/dY, W2^T, GELU'(pre) read; dL/dpre and its transpose written
+        "c4:gemm_mul_bwd": ("c4_step", _C4_BPK + "2, false>", None, (16 + 32 + 32 + 16 + 16) * _MB),
+        # config 5 layer 512 x 8192 x 8192 (256 blocks): int8 A, B and both scale vectors read; bf16 Y written
+        "c5:w8a8_packed": ("c5_step", "gemm_w8a8_bpk<", 256 * 256,
+                           512 * 8192 + 8192 * 8192 + 4 * (512 + 8192) + 2 * 512 * 8192),
     }
 
 
@@ -571,24 +588,25 @@ def traffic_summary(run_dir):
     commands in profiles/traffic_counters.md write them) and prints the summary table.  Each
     counter is scaled so that it reads the known traffic of the 512 MiB copy."""
     import csv
-    def per_dispatch(kernel, counter, name_part):
-        path = os.path.join(run_dir, f"traffic_{kernel}_{counter}", "run_counter_collection.csv")
+    def per_dispatch(run, counter, name_part, grid):
+        path = os.path.join(run_dir, f"traffic_{run}_{counter}", "run_counter_collection.csv")
         vals = [float(r["Counter_Value"]) for r in csv.DictReader(open(path))
-                if name_part in r["Kernel_Name"] and r["Counter_Name"] == counter]
+                if name_part in r["Kernel_Name"] and r["Counter_Name"] == counter
+                and (grid is None or int(r["Grid_Size"]) == grid)]
         if not vals:
             raise SystemExit(f"{path}: no dispatch of a kernel named *{name_part}*")
         return sum(vals) / len(vals)
     ks = _traffic_kernels()
-    cf = per_dispatch("copy", "FETCH_SIZE", ks["copy"][0])
-    cw = per_dispatch("copy", "WRITE_SIZE", ks["copy"][0])
+    cf = per_dispatch("copy", "FETCH_SIZE", ks["copy"][1], None)
+    cw = per_dispatch("copy", "WRITE_SIZE", ks["copy"][1], None)
     half = (512 << 20) / 1024  # KiB read and KiB written by the copy
     ff, wf = half / cf, half / cw
     out = {"fetch_factor": round(ff, 4), "write_factor": round(wf, 4), "kernels": {}}
     rows = []
-    for k, (part, alg) in ks.items():
+    for k, (run, part, grid, alg) in ks.items():
         if k == "copy":
             continue
-        f, w = per_dispatch(k, "FETCH_SIZE", part), per_dispatch(k, "WRITE_SIZE", part)
+        f, w = per_dispatch(run, "FETCH_SIZE", part, grid), per_dispatch(run, "WRITE_SIZE", part, grid)
         t = (f * ff + w * wf) * 1024
         out["kernels"][k] = {"traffic_bytes": int(round(t)), "algorithmic_bytes": alg, "fetch_kib": f, "write_kib": w}
         rows.append(f"| {k} | {f:.0f} | {w:.0f} | {int(round(t)):,} | {alg:,} | {t / alg:.3f} |")
