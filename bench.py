@@ -400,6 +400,55 @@ def bench_fractal(dev, q, steps, warmup, do_cpu):
     return res
 
 
+def bench_pixel_program(dev, q, steps, warmup, do_cpu):
+    """Struct-for bodies by the general path (vdsl_op_pixel_program: the lowered Taichi kernel,
+    compiled at run time): Mandelbrot beside the hand-tuned escape-time kernel in the same
+    rounding form (the cost of generality), and the Burning Ship, which only the general path
+    runs (its update folds |x|, |y| and is not a complex polynomial)."""
+    from vernondsl_amd import _lib, kernels, spec, taichi_compat as tc
+    from vernondsl_amd.rhi import Tensor
+    ex = os.path.join(ROOT, "vernondsl_amd", "examples")
+    mandel = tc.lower_source_kernel(open(os.path.join(ex, "mandelbrot_counts.py")).read(), "render", {"limit": 256},
+                                    general=True)
+    ship = tc.lower_source_kernel(open(os.path.join(ex, "burning_ship.py")).read(), "ship", {"zoom": 3.2})
+    esc = kernels.escape_time_params(**spec.mandelbrot_params(rounding=_lib.ESC_ROUND_SEPARATE))
+    out = Tensor(dev, (1024, 1024), "i32")
+    res = []
+    esc_ms, _ = time_replays(q, dev, lambda: kernels.escape_time(q, esc, out), max(10, steps // 5), warmup, per_graph=20)
+    for name, low, flop, desc in (
+            ("mandelbrot", mandel, 8, "Mandelbrot 1024x1024, max_iter 256, separately rounded (examples/"
+                                      "mandelbrot_counts.py by the general path)"),
+            ("burning_ship", ship, 8, "Burning Ship 1024x1024, max_iter 256 (examples/burning_ship.py)")):
+        prog = low.program
+        ms, _ = time_replays(q, dev, lambda: kernels.pixel_program(q, prog, [], out), max(10, steps // 5), warmup,
+                             per_graph=20)
+        got = out.numpy(q)
+        total = int(got.sum(dtype=np.int64))
+        parity = NOT_CHECKED
+        if do_cpu:  # CPU-baseline leg (timed below); its output is the checker
+            from oracle import oracle
+            ref = oracle.pixel_program(prog, 1024, 1024)
+            parity = "ok" if np.array_equal(got, ref) else f"FAIL {int((got != ref).sum())} px"
+        tflops = flop * total / (ms * 1e-3) / 1e12
+        r = {"config": "1-general", "workload": desc + ", vdsl_op_pixel_program", "metric": "Gpix-iter/s (fractal)",
+             "value": total / (ms * 1e-3) / 1e9, "unit": "Gpix-iter/s", "ms_per_launch": ms,
+             "pixel_iterations": total, "parity": parity,
+             "roofline": {"bound": "valu", "achieved": tflops, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                          "frac": tflops / PEAK_FP32_TFLOPS, "flop_per_pixel_iteration": flop,
+                          "note": "pixel-iterations counted as the program makes them (sum of counts); these "
+                                  "programs store only the count, so lanes whose loop state recurs exactly stop "
+                                  "early, as in the escape-time kernel; Burning Ship's two |.| per trip are not "
+                                  "counted as flops"}}
+        if name == "mandelbrot":
+            r["escape_time_kernel_ms"] = esc_ms  # the same counts from the hand-tuned op
+        if do_cpu:
+            r["cpu_baseline"] = cpu_baseline(oracle, lambda: oracle.pixel_program(prog, 1024, 1024), total / 1e9,
+                                             "Gpix-iter/s", "the full 1024x1024 grid")
+        res.append(r)
+    out.free()
+    return res
+
+
 # ---- config 3 ------------------------------------------------------------------------------------
 def bench_softmax(dev, q, steps, warmup, do_cpu):
     from vernondsl_amd import kernels, rng, spec
@@ -746,7 +795,8 @@ def main():
     head = bench_map_chain(dev, q, args.steps, args.warmup, do_cpu)
     log("bench: config 2", {k: v for k, v in head.items() if k != "cpu"})
     per_config = []
-    for fn, cid in ((bench_map_chain_generic, 2), (bench_fractal, 1), (bench_softmax, 3), (bench_mlp, 4),
+    for fn, cid in ((bench_map_chain_generic, 2), (bench_fractal, 1), (bench_pixel_program, 1), (bench_softmax, 3),
+                    (bench_mlp, 4),
                     (bench_w8a8, 5), (bench_vecmat, 6)):
         if args.only and args.only != cid:
             continue

@@ -271,6 +271,62 @@ int vdsl_op_map_chain_v(vdsl_queue q, int64_t rows, int64_t cols, const vdsl_map
                         int32_t n_instr, const vdsl_map_vinput* inputs, int32_t n_inputs,
                         const int32_t* out_regs, int32_t out_width, vdsl_buffer out);
 
+/* ---- general per-pixel programs: the body of a struct-for over a 2-D field ------------------ */
+/* The general form of op class 1 (fractal.py:16-25): what a Taichi @ti.kernel `for i, j in F:`
+ * body computes per pixel, as a register program of four sections run in order on 16 f32
+ * registers (all 0 at the start):
+ *   pre  (code[0, n_pre)):            per-pixel set-up (index maps, field reads, constants);
+ *   loop (code[n_pre, +n_test) test, code[.., +n_body) body): when `loop` is set, the
+ *        check-then-update loop of fractal.py:22-24: run the test section; stop unless
+ *        r[test_a] <test> r[test_b] holds (VDSL_PIX_TEST_NONE: always holds) and fewer than
+ *        max_iter updates were made; run the body section; count one update; repeat;
+ *   post (the last n_post instructions): the stored value, which may read the count.
+ * out[i][j] = r[out_reg] (an f32 field) or the count (VDSL_PIX_OUT_COUNT: an int32 field).
+ * Instructions are vdsl_map_instr with the map-chain opcodes (VDSL_MAP_LOAD: a = input field,
+ * read at [i][j]) plus the ones below; every operation rounds once, in f32, where it is written
+ * (an fma only for VDSL_MAP_FMA).  Compiled at run time for each program (once per device): a
+ * program first seen while a queue records a graph is refused, so run it once before
+ * recording.  No counterpart in the reference beyond the program surface it runs; the caller is
+ * the Taichi-subset front end for kernel bodies other than the escape-time form of
+ * vdsl_op_escape_time. */
+#define VDSL_PIX_MAX_INSTR 64
+#define VDSL_PIX_MAX_REGS 16
+#define VDSL_PIX_MAX_INPUTS 4
+
+typedef enum vdsl_pix_opcode {
+  VDSL_PIX_INDEX = 32,  /* r[dst] = float(i) (a = 0, the outer axis) or float(j) (a = 1) */
+  VDSL_PIX_COS = 33,    /* cosf(r[a]) */
+  VDSL_PIX_SIN = 34,    /* sinf(r[a]) */
+  VDSL_PIX_COUNT = 35   /* r[dst] = float(count of loop updates); post section only */
+} vdsl_pix_opcode;
+
+typedef enum vdsl_pix_test {
+  VDSL_PIX_TEST_NONE = 0, VDSL_PIX_TEST_LT = 1, VDSL_PIX_TEST_LE = 2, VDSL_PIX_TEST_GT = 3,
+  VDSL_PIX_TEST_GE = 4
+} vdsl_pix_test;
+
+typedef enum vdsl_pix_output {
+  VDSL_PIX_OUT_REG = 0,    /* f32 field: r[out_reg] */
+  VDSL_PIX_OUT_COUNT = 1   /* int32 field: the count of loop updates */
+} vdsl_pix_output;
+
+typedef struct vdsl_pixel_program {
+  int32_t n_pre, n_test, n_body, n_post;   /* section lengths; their sum <= VDSL_PIX_MAX_INSTR */
+  int32_t loop;                            /* 0: no loop (n_test = n_body = 0) */
+  int32_t max_iter;                        /* at most this many loop updates (>= 0) */
+  int32_t test;                            /* vdsl_pix_test */
+  int32_t test_a, test_b;                  /* registers compared by the test */
+  int32_t out_kind;                        /* vdsl_pix_output */
+  int32_t out_reg;
+  int32_t pad;
+  vdsl_map_instr code[VDSL_PIX_MAX_INSTR];
+} vdsl_pixel_program;
+
+/* Runs `prog` for every pixel of an [ni][nj] grid.  inputs: f32 [ni][nj] fields (n_inputs <= 4);
+ * out: f32 (VDSL_PIX_OUT_REG) or int32 (VDSL_PIX_OUT_COUNT) [ni][nj]. */
+int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const vdsl_pixel_program* prog,
+                          const vdsl_buffer* inputs, int32_t n_inputs, vdsl_buffer out);
+
 /* Batched vertex transform: the MVP chain of the reference's test shader (color.mlir:10-39:
  * vec4(pos, 1.0), then linalg.matvec by model, view and proj) over n vertices.
  *   pos:  f32 [n][in_width]; in_width 3 (extended to vec4(pos, 1.0), color.mlir:15-21) or 4;

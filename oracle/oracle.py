@@ -75,6 +75,7 @@ _lib.orc_cast.argtypes = [_i64, C.c_int, _vp, C.c_int, _vp]
 _lib.orc_gelu_fwd.argtypes = [_i64, C.c_int, _vp, C.c_int, _vp]
 _lib.orc_gelu_bwd.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp]
 _lib.orc_gelu_grad.argtypes = [_i64, _vp, _vp]
+_lib.orc_pixel_program_rows.argtypes = [_vp, _i64, _i64, C.POINTER(_vp), _vp, _i64, _i64]
 _lib.orc_mse_fwd_bwd.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp, _vp]
 _lib.orc_quantize_rows_i8.argtypes = [_i64, _i64, C.c_int, _vp, _vp, _vp]
 _lib.orc_gemm_w8a8_rows.argtypes = [_i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _i64, _i64]
@@ -141,6 +142,20 @@ def map_chain_v(prog, inputs, rows: int, cols: int, row_range=None) -> np.ndarra
     base = out.ctypes.data - r0 * cols * ow * 4
     _lib.orc_map_chain_v_rows(rows, cols, code, len(prog.code), ptrs, bc, wd, len(arrs), regs, ow, _vp(base), r0, r1)
     return out if ow > 1 else out[:, :, 0]
+
+
+def pixel_program(prog, ni: int, nj: int, inputs=(), rows=None) -> np.ndarray:
+    """orc_pixel_program_rows: prog is a vernondsl_amd.pixprog.PixelProgram (the C struct);
+    inputs: f32 [ni][nj] arrays; returns f32 or int32 [rows][nj] (rows: (r0, r1), default all)."""
+    ins = [np.ascontiguousarray(a, np.float32) for a in inputs]
+    for a in ins:
+        if a.shape != (ni, nj):
+            raise ValueError(f"input of shape {a.shape}, expected {(ni, nj)}")
+    r0, r1 = rows if rows else (0, ni)
+    out = np.zeros((r1 - r0, nj), np.int32 if prog.out_kind == 1 else np.float32)
+    ptrs = (_vp * max(1, len(ins)))(*[a.ctypes.data for a in ins])
+    _lib.orc_pixel_program_rows(C.addressof(prog), ni, nj, ptrs, _p(out), r0, r1)
+    return out
 
 
 def vec_transform(pos: np.ndarray, mats: np.ndarray) -> np.ndarray:

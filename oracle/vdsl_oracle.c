@@ -17,6 +17,13 @@
  *                        forms, conjugate symmetry, and f64 brute force away from the boundary.
  *   orc_map_chain        no reference code.  Pinned against f64 numpy evaluation and the
  *                        special values x = 0 and |x| large.
+ *   orc_pixel_program_rows
+ *                        the general form of fractal.py:16-25 (a struct-for body with its check-
+ *                        then-update loop).  Pinned by independent numpy restatements of whole
+ *                        programs (Mandelbrot / Burning Ship / cubic maps, plain per-pixel
+ *                        expressions, field reads), by equality with orc_escape_time on the
+ *                        programs both express, and by closed forms (a loop with no test runs
+ *                        max_iter times; identity programs copy their input).
  *   orc_map_chain_v_rows vector operands (the vec2-4 / extract_component / swizzle vocabulary of
  *                        source/README.md:23-55).  Pinned by permutation closed forms: a swizzle
  *                        program equals numpy fancy indexing of the components, swizzles compose
@@ -168,6 +175,60 @@ static float map_apply(int op, float a, float b, float c, float imm) {
     case VDSL_MAP_ADD_IMM: return a + imm;
     default: return 0.0f;
   }
+}
+
+/* ---- general per-pixel programs (vdsl_pixel_program) -------------------------------------- */
+
+static float pix_apply(const vdsl_map_instr* s, const float* reg, const float* const* inputs, int64_t o, int64_t i,
+                       int64_t j, int count) {
+  switch (s->op) {
+    case VDSL_MAP_LOAD: return inputs[s->a][o];
+    case VDSL_PIX_INDEX: return s->a == 0 ? (float)i : (float)j;
+    case VDSL_PIX_COUNT: return (float)count;
+    case VDSL_PIX_COS: return cosf(reg[s->a]);
+    case VDSL_PIX_SIN: return sinf(reg[s->a]);
+    default: return map_apply(s->op, reg[s->a], reg[s->b], reg[s->c], s->imm);
+  }
+}
+
+static int pix_test(int test, float a, float b) {
+  switch (test) {
+    case VDSL_PIX_TEST_LT: return a < b;
+    case VDSL_PIX_TEST_LE: return a <= b;
+    case VDSL_PIX_TEST_GT: return a > b;
+    case VDSL_PIX_TEST_GE: return a >= b;
+    default: return 1;
+  }
+}
+
+/* Rows [r0, r1) of vdsl_op_pixel_program: per pixel, 16 registers at 0, the pre section, the
+ * check-then-update loop (fractal.py:22-24: test, stop unless it holds and fewer than max_iter
+ * updates were made, body, count), the post section, then out[i][j] = r[out_reg] (f32) or the
+ * count (int32).  The program is taken as validated by the caller. */
+void orc_pixel_program_rows(const vdsl_pixel_program* p, int64_t ni, int64_t nj, const float* const* inputs, void* out,
+                            int64_t r0, int64_t r1) {
+  const int t0 = p->n_pre, b0 = t0 + p->n_test, q0 = b0 + p->n_body, end = q0 + p->n_post;
+  (void)ni;
+#pragma omp parallel for schedule(dynamic, 4)
+  for (int64_t i = r0; i < r1; ++i)
+    for (int64_t j = 0; j < nj; ++j) {
+      const int64_t o = i * nj + j;
+      float reg[VDSL_PIX_MAX_REGS];
+      for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) reg[k] = 0.0f;
+      int count = 0;
+      for (int pc = 0; pc < t0; ++pc) reg[p->code[pc].dst] = pix_apply(&p->code[pc], reg, inputs, o, i, j, 0);
+      if (p->loop) {
+        while (count < p->max_iter) {
+          for (int pc = t0; pc < b0; ++pc) reg[p->code[pc].dst] = pix_apply(&p->code[pc], reg, inputs, o, i, j, 0);
+          if (!pix_test(p->test, reg[p->test_a], reg[p->test_b])) break;
+          for (int pc = b0; pc < q0; ++pc) reg[p->code[pc].dst] = pix_apply(&p->code[pc], reg, inputs, o, i, j, 0);
+          ++count;
+        }
+      }
+      for (int pc = q0; pc < end; ++pc) reg[p->code[pc].dst] = pix_apply(&p->code[pc], reg, inputs, o, i, j, count);
+      if (p->out_kind == VDSL_PIX_OUT_COUNT) ((int32_t*)out)[o - r0 * nj] = count;
+      else ((float*)out)[o - r0 * nj] = reg[p->out_reg];
+    }
 }
 
 /* Rows [r0, r1). in_ptrs[k] holds input k per bcast[k] (vdsl_broadcast). */

@@ -1,0 +1,262 @@
+"""vdsl_op_pixel_program on the GPU against the CPU oracle (oracle.pixel_program): bit for bit for
+programs of exactly rounded operations (+ - * / abs min max sqrt, moves, indices, loads, the
+loop count), within stated bounds for the transcendentals (the device's sin/cos/log against the
+C library's, exp and tanh from the map chains' own approximations).  Edge cases: grids that are
+not whole 16x16 blocks, empty grids, loops of zero trips, loops without a test, four input
+fields, the count read after the loop, invalid programs, graph recording."""
+import contextlib
+import io
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from vernondsl_amd import _lib, kernels, pixprog as pp, run, taichi_compat as tc
+from vernondsl_amd.rhi import Tensor
+
+pytestmark = pytest.mark.gpu
+REL = 1e-5  # the map chains' bound for their exp / tanh / sigmoid / log
+EX = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "vernondsl_amd", "examples")
+
+
+def run_prog(dev, q, prog, inputs, ni, nj):
+    ts = [Tensor.from_numpy(dev, q, np.ascontiguousarray(a, np.float32)) for a in inputs]
+    out = Tensor(dev, (ni, nj), "i32" if prog.out_kind == pp.OUT_COUNT else "f32")
+    if ni and nj:
+        out.buffer.fill_u32(q, 0x7FC00000)  # NaN / a large count: every element must be written
+    kernels.pixel_program(q, prog, ts, out)
+    got = out.numpy(q)
+    for t in ts + [out]:
+        t.free()
+    return got
+
+
+def escape_program(c_re=-0.8, c_im=0.156, limit=200, scale=3.0, test="lt"):
+    """Julia set as a plain program: z0 from the pixel, z <- z^2 + c while |z|^2 < 4."""
+    b = pp.Builder()
+    x0 = b.op("add", b.op("mul", b.op("div", b.index(0), 37.0), scale), -1.5)
+    y0 = b.op("add", b.op("mul", b.op("div", b.index(1), 53.0), scale), -1.5)
+    x, y = b.state("x"), b.state("y")
+    r2 = b.op("add", b.op("mul", x, x), b.op("mul", y, y))
+    return pp.compile_program(
+        b, init={"x": x0, "y": y0}, test=(test, r2, 4.0),
+        body={"x": b.op("add", b.op("sub", b.op("mul", x, x), b.op("mul", y, y)), c_re),
+              "y": b.op("add", b.op("mul", b.op("mul", x, y), 2.0), c_im)},
+        max_iter=limit, out=pp.COUNT)
+
+
+@pytest.mark.parametrize("ni,nj", [(37, 53), (1, 1), (16, 16), (17, 15), (300, 129), (1024, 1024)])
+def test_escape_program_counts_bit_exact(dev, q, ni, nj):
+    prog = escape_program()
+    got = run_prog(dev, q, prog, [], ni, nj)
+    ref = oracle.pixel_program(prog, ni, nj)
+    assert np.array_equal(got, ref)
+
+
+def state_program(limit):
+    """Mandelbrot whose stored value reads the loop state after the loop (|z|^2 + count / 1000):
+    lanes keep the state of the trip they left the loop at."""
+    b = pp.Builder()
+    cx = b.op("add", b.op("mul", b.op("div", b.index(0), 300.0), 3.0), -2.0)
+    cy = b.op("add", b.op("mul", b.op("div", b.index(1), 129.0), 3.0), -1.5)
+    x, y = b.state("x"), b.state("y")
+    r2 = b.op("add", b.op("mul", x, x), b.op("mul", y, y))
+    return pp.compile_program(
+        b, init={"x": 0.0, "y": 0.0}, test=("le", r2, 4.0),
+        body={"x": b.op("add", b.op("sub", b.op("mul", x, x), b.op("mul", y, y)), cx),
+              "y": b.op("add", b.op("mul", b.op("mul", x, y), 2.0), cy)},
+        max_iter=limit, out=b.op("add", r2, b.op("mul", b.count(), 0.001)))
+
+
+@pytest.mark.parametrize("limit", [0, 5, 16, 77, 256])
+def test_state_read_after_the_loop_bit_exact(dev, q, limit):
+    prog = state_program(limit)
+    got = run_prog(dev, q, prog, [], 300, 129)
+    assert np.array_equal(got, oracle.pixel_program(prog, 300, 129))
+
+
+@pytest.mark.parametrize("limit", [3, 40, 256])
+def test_test_section_value_read_after_the_loop(dev, q, limit):
+    """A program (built by hand: the compiler recomputes instead) that stores a register the test
+    section writes (and the body reuses as a temporary): a lane whose test failed stores the
+    value of that test, one that made max_iter trips what its last body trip left there."""
+    prog = escape_program(limit=limit)
+    ts = prog.n_pre
+    assert prog.n_test == 3 and prog.code[ts + 2].dst == prog.test_a
+    prog.n_post, prog.out_kind, prog.out_reg = 0, pp.OUT_REG, prog.test_a
+    got = run_prog(dev, q, prog, [], 300, 129)
+    ref = oracle.pixel_program(prog, 300, 129)
+    assert np.array_equal(got, ref)
+    assert np.any(ref > 4.0) and np.any(ref < 4.0)
+
+
+def test_empty_grid_writes_nothing(dev, q):
+    prog = escape_program()
+    for ni, nj in [(0, 5), (5, 0), (0, 0)]:
+        out = Tensor(dev, (max(ni, 1), max(nj, 1)), "i32")
+        out.buffer.fill_u32(q, 7)
+        _lib.call("vdsl_op_pixel_program", q.handle, ni, nj, __import__("ctypes").byref(prog), None, 0, out.handle)
+        q.sync()
+        assert np.all(out.numpy(q) == 7)
+        out.free()
+
+
+def logistic_program(steps, with_count_in_post):
+    """A loop without a test (fixed trip count) over a state read from an input field; the post
+    section reads the count."""
+    b = pp.Builder()
+    r = b.op("add", b.op("mul", b.op("div", b.index(0), 64.0), 1.5), 2.5)
+    x = b.state("x")
+    out = x if not with_count_in_post else b.op("add", x, b.op("mul", b.count(), 0.25))
+    return pp.compile_program(b, init={"x": b.op("add", b.op("mul", b.load(0), 0.5), 0.25)},
+                              body={"x": b.op("mul", b.op("mul", r, x), b.op("sub", 1.0, x))},
+                              max_iter=steps, out=out, loop=True)
+
+
+@pytest.mark.parametrize("steps", [0, 1, 7, 300])
+@pytest.mark.parametrize("post", [False, True])
+def test_fixed_trip_loops_bit_exact(dev, q, steps, post):
+    g = np.random.default_rng(steps).random((64, 200), dtype=np.float32)
+    prog = logistic_program(steps, post)
+    assert np.array_equal(run_prog(dev, q, prog, [g], 64, 200), oracle.pixel_program(prog, 64, 200, [g]))
+
+
+def test_four_inputs_no_loop_bit_exact(dev, q):
+    rng = np.random.default_rng(11)
+    ins = [rng.standard_normal((77, 91)).astype(np.float32) for _ in range(4)]
+    ins[3] = np.abs(ins[3]) + 0.5
+    b = pp.Builder()
+    l0, l1, l2, l3 = (b.load(k) for k in range(4))
+    v = b.op("add", b.op("mul", l0, l1), b.op("div", l2, l3))
+    v = b.op("max", b.op("min", v, b.op("sqrt", b.op("add", b.op("abs", l0), b.index(1)))), b.op("neg", b.index(0)))
+    v = b.op("fma", v, l3, b.op("sub", l2, b.op("square", l1)))
+    prog = pp.compile_program(b, out=v)
+    assert not prog.loop
+    assert np.array_equal(run_prog(dev, q, prog, ins, 77, 91), oracle.pixel_program(prog, 77, 91, ins))
+
+
+def test_transcendentals_within_bounds(dev, q):
+    ni, nj = 96, 160
+    b = pp.Builder()
+    t = b.op("add", b.op("mul", b.index(0), 0.37), b.op("mul", b.index(1), -0.21))  # about [-34, 35]
+    progs = {
+        "sin": b.op("sin", t), "cos": b.op("cos", t), "exp": b.op("exp", b.op("mul", t, 0.5)),
+        "log": b.op("log", b.op("add", b.op("abs", t), 1e-3)), "tanh": b.op("tanh", b.op("mul", t, 0.1)),
+        "sigmoid": b.op("sigmoid", t),
+    }
+    for name, node in progs.items():
+        prog = pp.compile_program(b, out=node)
+        got = run_prog(dev, q, prog, [], ni, nj).astype(np.float64)
+        ref = oracle.pixel_program(prog, ni, nj).astype(np.float64)
+        if name in ("sin", "cos"):  # values in [-1, 1]: absolute bound
+            assert np.max(np.abs(got - ref)) <= 4e-7, name
+        else:
+            assert np.all(np.abs(got - ref) <= REL * np.abs(ref) + 1e-37), name
+
+
+def test_invalid_programs_rejected(dev, q):
+    import ctypes
+    out = Tensor(dev, (8, 8), "f32")
+    good = logistic_program(3, False)
+
+    def call(p, n_inputs=1, ins=None):
+        ins = ins or [Tensor(dev, (8, 8), "f32") for _ in range(n_inputs)]
+        hs = (ctypes.c_void_p * max(1, len(ins)))(*[t.handle for t in ins])
+        try:
+            with pytest.raises(_lib.VdslError) as ei:
+                _lib.call("vdsl_op_pixel_program", q.handle, 8, 8, ctypes.byref(p), hs, n_inputs, out.handle)
+        finally:
+            for t in ins:
+                t.free()
+        return ei.value.message
+
+    def mutate(**kw):
+        p = pp.PixelProgram()
+        ctypes.memmove(ctypes.byref(p), ctypes.byref(good), ctypes.sizeof(p))
+        for k, v in kw.items():
+            setattr(p, k, v)
+        return p
+
+    assert "LOAD" in call(good, n_inputs=0, ins=[])
+    assert "at most 64" in call(mutate(n_post=60))
+    assert "unknown test" in call(mutate(test=9))
+    p = mutate()
+    p.code[0].dst = 16
+    assert "register out of range" in call(p)
+    p = mutate()
+    p.code[0].op = 99
+    assert "unknown opcode" in call(p)
+    assert "count needs a loop" in call(mutate(loop=0, n_body=0, out_kind=1))
+    assert "n_inputs" in call(good, n_inputs=5, ins=[Tensor(dev, (8, 8), "f32") for _ in range(5)])
+    small = Tensor(dev, (4, 8), "f32")
+    hs = (ctypes.c_void_p * 1)(small.handle)
+    with pytest.raises(_lib.VdslError):
+        _lib.call("vdsl_op_pixel_program", q.handle, 8, 8, ctypes.byref(good), hs, 1, out.handle)
+    small.free()
+    out.free()
+
+
+def test_recording_needs_a_compiled_program(dev, q):
+    """A program first seen while a graph records is refused (nothing is compiled during
+    recording); one run eagerly before records, and its replays equal the eager run.  Programs
+    differing only in immediates and max_iter share one compiled kernel (those stay arguments)."""
+    ni, nj = 130, 70
+    fresh = escape_program(test="le")  # a test no earlier program used: a new kernel
+    out = Tensor(dev, (ni, nj), "i32")
+    with pytest.raises(_lib.VdslError) as ei:
+        with q.capture():
+            kernels.pixel_program(q, fresh, [], out)
+    assert ei.value.status == -6  # VDSL_ERR_CAPTURE
+    kernels.pixel_program(q, fresh, [], out)
+    eager = out.numpy(q)
+    assert np.array_equal(eager, oracle.pixel_program(fresh, ni, nj))
+    same_kernel = escape_program(c_re=-0.4, c_im=0.6, limit=77, test="le")
+    with q.capture() as rec:
+        kernels.pixel_program(q, fresh, [], out)
+    with q.capture() as rec2:
+        kernels.pixel_program(q, same_kernel, [], out)
+    other = oracle.pixel_program(same_kernel, ni, nj)
+    assert not np.array_equal(other, eager)
+    for _ in range(3):
+        out.buffer.fill_u32(q, 0xFFFFFFFF)
+        rec.graph.launch(q)
+        q.sync()
+        assert np.array_equal(out.numpy(q), eager)
+        out.buffer.fill_u32(q, 0xFFFFFFFF)
+        rec2.graph.launch(q)
+        q.sync()
+        assert np.array_equal(out.numpy(q), other)
+    rec.graph.destroy()
+    rec2.graph.destroy()
+    out.free()
+
+
+def run_program(path, frames):
+    buf = io.StringIO()
+    with contextlib.redirect_stdout(buf):
+        assert run.main([path, "--frames", str(frames)]) == 0
+    return json.loads(buf.getvalue().strip().splitlines()[-1]), tc._state["last_gui"].last_image
+
+
+def test_burning_ship_example_bit_exact(dev, q):
+    path = os.path.join(EX, "burning_ship.py")
+    res, img = run_program(path, 1)
+    assert res["frames"] == 1 and img.shape == (1024, 1024) and img.dtype == np.int32
+    low = tc.lower_source_kernel(open(path).read(), "ship", {"zoom": 3.2})
+    assert low.kind == "pixel_program"
+    assert np.array_equal(img, oracle.pixel_program(low.program, 1024, 1024))
+    assert int(img.sum()) == 51_201_175
+
+
+def test_interference_example_frames(dev, q):
+    path = os.path.join(EX, "interference.py")
+    res, img = run_program(path, 3)
+    assert res["frames"] == 3 and img.shape == (768, 768) and img.dtype == np.float32
+    text = open(path).read()
+    mask = oracle.pixel_program(tc.lower_source_kernel(text, "make_mask", {}).program, 768, 768)
+    low = tc.lower_source_kernel(text, "waves", {"phase": 1.0})  # the third frame: 0.0 + 0.5 + 0.5
+    ref = oracle.pixel_program(low.program, 768, 768, [mask]).astype(np.float64)
+    # the mask's exp (relative REL) and the two sines (4e-7 each), scaled by 0.25 * |amp| <= 0.5
+    assert np.max(np.abs(img.astype(np.float64) - ref)) <= 0.5 * REL + 2e-7 + 1e-7

@@ -1,0 +1,185 @@
+"""The general path of the Taichi-subset front end on the CPU: struct-for bodies that are not of
+the escape-time form lower to per-pixel register programs (vernondsl_amd.pixprog), which the CPU
+oracle runs (oracle.pixel_program).  The oracle's interpreter is pinned here by independent numpy
+restatements of whole programs (same f32 operations in the same order, so bit for bit where the
+program has only exactly rounded operations) and by agreement with the escape-time oracle on the
+programs both express."""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from vernondsl_amd import _lib, pixprog as pp, spec, taichi_compat as tc
+
+EX = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "vernondsl_amd", "examples")
+REF = "/root/reference/fractal.py"
+f32 = np.float32
+
+
+def ex(name):
+    return open(os.path.join(EX, name)).read()
+
+
+def general(text, kernel, args):
+    """Lowers by the general path even where the escape-time form also applies."""
+    return tc.lower_source_kernel(text, kernel, args, general=True)
+
+
+def test_mandelbrot_by_the_general_path_equals_the_escape_time_oracle():
+    low = general(ex("mandelbrot_counts.py"), "render", {"limit": 256})
+    assert low.kind == "pixel_program" and low.program.out_kind == pp.OUT_COUNT and low.program.max_iter == 256
+    got = oracle.pixel_program(low.program, 1024, 1024)
+    assert int(got.sum()) == 49_860_131  # the separately-rounded grid's known sum
+    assert np.array_equal(got, oracle.escape_time(spec.mandelbrot_params(rounding=_lib.ESC_ROUND_SEPARATE)))
+
+
+def test_julia_by_the_general_path_equals_the_escape_time_oracle():
+    text = ex("rabbit_drift.py")
+    low = general(text, "draw", {"angle": 0.3})
+    _, p = tc.lower_source(text, "draw", {"angle": 0.3})
+    assert np.array_equal(oracle.pixel_program(low.program, 512, 512), oracle.escape_time(p))
+
+
+@pytest.mark.skipif(not os.path.exists(REF), reason="the reference tree is only mounted in the build container")
+def test_reference_fractal_py_keeps_the_escape_time_op():
+    low = tc.lower_source_kernel(open(REF).read(), "paint", {"t": 0.03})
+    assert low.kind == "escape_time"
+
+
+def burning_ship_numpy(n, limit, zoom):
+    i = np.arange(n, dtype=np.float32)[:, None] * np.ones((1, n), np.float32)
+    j = np.ones((n, 1), np.float32) * np.arange(n, dtype=np.float32)[None, :]
+    cx = ((i / f32(n)) + f32(-0.5)) * f32(zoom) + f32(-0.45)
+    cy = ((j / f32(n)) + f32(-0.5)) * f32(zoom) + f32(-0.5)
+    x = np.zeros_like(cx)
+    y = np.zeros_like(cx)
+    cnt = np.zeros(cx.shape, np.int32)
+    live = np.ones(cx.shape, bool)
+    for _ in range(limit):
+        live &= (x * x + y * y) <= f32(4.0)
+        if not live.any():
+            break
+        ax, ay = np.abs(x), np.abs(y)
+        nx = (ax * ax - ay * ay) + cx
+        ny = (f32(2.0) * ax) * ay + cy
+        x = np.where(live, nx, x)
+        y = np.where(live, ny, y)
+        cnt += live
+    return cnt
+
+
+def test_burning_ship_program_against_numpy():
+    low = tc.lower_source_kernel(ex("burning_ship.py"), "ship", {"zoom": 3.2})
+    assert low.kind == "pixel_program" and low.field.dtype == "i32"
+    got = oracle.pixel_program(low.program, 1024, 1024, rows=(0, 256))
+    ref = burning_ship_numpy(1024, 256, 3.2)[:256]
+    assert np.array_equal(got, ref)
+    assert got.max() == 256 and got.min() >= 1
+
+
+def test_interference_programs_against_numpy():
+    text = ex("interference.py")
+    mask_low = tc.lower_source_kernel(text, "make_mask", {})
+    assert mask_low.kind == "pixel_program" and not mask_low.program.loop and mask_low.inputs == []
+    n = 768
+    mask = oracle.pixel_program(mask_low.program, n, n)
+    i = np.arange(n, dtype=np.float64)[:, None]
+    j = np.arange(n, dtype=np.float64)[None, :]
+    mref = np.exp(-((i - 384.0) ** 2 + (j - 384.0) ** 2) * 1e-5)
+    assert np.all(np.abs(mask - mref) <= 2e-6 * mref)
+    low = tc.lower_source_kernel(text, "waves", {"phase": 0.5})
+    assert [f.shape for f in low.inputs] == [(n, n)]
+    got = oracle.pixel_program(low.program, n, n, [mask]).astype(np.float64)
+    d1 = np.sqrt((i - 200.0) ** 2 + (j - 300.0) ** 2)
+    d2 = np.sqrt((i - 560.0) ** 2 + (j - 420.0) ** 2)
+    ref = 0.5 + 0.25 * (np.sin(d1 * 0.08 - 0.5) + np.sin(d2 * 0.08 - 0.5)) * mask
+    assert np.all(np.abs(got - ref) <= 2e-5)
+
+
+LOGISTIC = '''
+import taichi as ti
+n = 96
+f = ti.field(dtype=float, shape=(n, n))
+g = ti.field(dtype=float, shape=(n, n))
+
+@ti.kernel
+def k():
+    for i, j in f:
+        r = 2.5 + i / n * 1.5
+        x = 0.25 + g[i, j] * 0.5
+        for _ in range(STEPS):
+            x = r * x * (1.0 - x)
+        f[i, j] = x
+'''
+
+
+@pytest.mark.parametrize("steps", [0, 1, 37])
+def test_fixed_trip_loop_against_numpy(steps):
+    low = tc.lower_source_kernel(LOGISTIC.replace("STEPS", str(steps)), "k", {})
+    p = low.program
+    assert p.loop == 1 and p.test == 0 and p.max_iter == steps
+    g = np.random.default_rng(5).random((96, 96), dtype=np.float32)
+    got = oracle.pixel_program(p, 96, 96, [g])
+    i = np.arange(96, dtype=np.float32)[:, None] * np.ones((1, 96), np.float32)
+    r = f32(2.5) + (i / f32(96)) * f32(1.5)
+    x = f32(0.25) + g * f32(0.5)
+    for _ in range(steps):
+        x = (r * x) * (f32(1.0) - x)
+    assert np.array_equal(got, x)
+
+
+def test_count_stored_into_f32_and_parallel_swap():
+    text = '''
+import taichi as ti
+f = ti.field(dtype=float, shape=(16, 24))
+
+@ti.kernel
+def k():
+    for i, j in f:
+        a = i * 1.0
+        b = j * 1.0
+        m = 0
+        while a < b and m < 50:
+            a, b = b, a + 1.0
+            m += 1
+        f[i, j] = m * 0.5 + a - b
+'''
+    low = tc.lower_source_kernel(text, "k", {})
+    got = oracle.pixel_program(low.program, 16, 24)
+    ref = np.zeros((16, 24), np.float32)
+    for i in range(16):
+        for j in range(24):
+            a, b, m = f32(i), f32(j), 0
+            while a < b and m < 50:
+                a, b = b, a + f32(1.0)
+                m += 1
+            ref[i, j] = (f32(m) * f32(0.5) + a) - b
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("body,msg", [
+    ("        k = 0\n        while k < 10:\n            k += 1\n            k += 1\n        f[i, j] = k", "counter|loop"),
+    ("        x = 0.0\n        k = 0\n        while k < 10:\n            x = x + k\n            k += 1\n        f[i, j] = x", "counter"),
+    ("        f[i, j] = 1.0\n        x = 2.0", "last statement"),
+    ("        x = 0.0\n        for _ in range(3):\n            for _ in range(2):\n                x = x + 1.0\n        f[i, j] = x", "statement"),
+    ("        f[i, j] = i % 3", "Mod"),
+])
+def test_rejected_general_bodies(body, msg):
+    text = "import taichi as ti\nf = ti.field(dtype=float, shape=(8, 8))\n@ti.kernel\ndef k():\n    for i, j in f:\n" + body + "\n"
+    with pytest.raises(tc.TaichiLoweringError, match=msg):
+        tc.lower_source_kernel(text, "k", {})
+
+
+def test_register_pressure_is_reported():
+    b = pp.Builder()
+    vals = [b.op("sin", b.op("mul", b.index(0), float(k + 1))) for k in range(20)]
+    acc = vals[0]
+    for v in vals[1:]:
+        acc = b.op("add", acc, v)
+    pp.compile_program(b, out=acc)  # a chain: few registers live at once
+    wide = b.op("add", vals[0], vals[1])
+    for k in range(2, 20):
+        wide = b.op("add", wide, b.op("mul", vals[k], vals[(k + 7) % 20]))
+    with pytest.raises(pp.ProgramError, match="registers|instructions"):
+        pp.compile_program(b, out=wide)

@@ -149,6 +149,7 @@ PROTOTYPES = {
     "vdsl_op_gemm_bf16_gelu_bwd": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
     "vdsl_op_gemm_bf16_gelu_bwd_packed": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
     "vdsl_op_gemm_bf16_mul_packed": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "vdsl_op_pixel_program": (C.c_int, [_vp, C.c_int32, C.c_int32, _vp, C.POINTER(_vp), C.c_int32, _vp]),
     "vdsl_mse_partials_count": (C.c_int64, [_i64, _i64]),
     "vdsl_op_mse_fwd_bwd": (C.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vdsl_op_quantize_rows_i8": (C.c_int, [_vp, _i64, _i64, _i32, _vp, _vp, _vp]),

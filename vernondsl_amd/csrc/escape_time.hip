@@ -17,6 +17,7 @@
 #include <cstring>
 
 #include "common.h"
+#include "lanemask.h"
 
 namespace vdsl {
 namespace {
@@ -34,28 +35,6 @@ __device__ __forceinline__ float pixel_coord(int idx, float den, float off, floa
   v = v + off;
   v = v * scale;
   return v + post;
-}
-
-// Per-lane selects on a 64-bit lane mask held in scalar registers (the mask is the select's
-// condition operand, so it is never turned into a vector of 0/1 and back).
-__device__ __forceinline__ int lane_select(uint64_t mask, int if_set, int if_clear) {
-  int r;
-  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(if_clear), "v"(if_set), "s"(mask));
-  return r;
-}
-// The same for a count's bit: volatile, so a select meant for a rarely taken branch is not hoisted
-// out of it.
-template <int V>
-__device__ __forceinline__ int lane_bit(uint64_t mask) {
-  int r;
-  asm volatile("v_cndmask_b32_e64 %0, 0, %1, %2" : "=v"(r) : "n"(V), "s"(mask));
-  return r;
-}
-#define lane_select_v(mask, V) lane_bit<V>(mask)
-__device__ __forceinline__ int lane_select_keep(uint64_t mask, int if_set, int keep) {
-  int r;
-  asm volatile("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(keep), "v"(if_set), "s"(mask));
-  return r;
 }
 
 // Iteration count of pixel (i, j), run by one lane of a wave of in-grid pixels.
@@ -117,7 +96,7 @@ __device__ __forceinline__ int escape_count(const vdsl_escape_time_params& p, in
   // live set at once instead of stepping on to max_iter.  Bitwise equality, so -0 != +0 and NaN
   // never matches: only a state that truly recurs is taken.
   uint32_t save_r = __float_as_uint(zr), save_i = __float_as_uint(zi);
-  for (; k + kUnroll <= max_iter; k += kUnroll) {
+  for (; k <= max_iter - kUnroll; k += kUnroll) {
     uint64_t m[kUnroll];
     uint64_t lk = live;
 #pragma unroll
@@ -125,20 +104,7 @@ __device__ __forceinline__ int escape_count(const vdsl_escape_time_params& p, in
       lk &= __builtin_amdgcn_ballot_w64(step());
       m[u] = lk;
     }
-    if (lk == live) {
-      it += lane_select(live, kUnroll, 0);
-    } else {
-      // c = sum_u m[u] per lane (0..16); the masks are sticky (m[0] >= m[1] >= ...), so c >= 8
-      // iff m[7]; then c >= 4 more iff m[11] (or, below 8, m[3]); and so on; c == 16 adds m[15].
-      const uint64_t b3 = m[7];
-      const uint64_t b2 = (m[7] & m[11]) | (~m[7] & m[3]);
-      const uint64_t c00 = ~b3 & ~b2, c01 = ~b3 & b2, c10 = b3 & ~b2, c11 = b3 & b2;
-      const uint64_t b1 = (c00 & m[1]) | (c01 & m[5]) | (c10 & m[9]) | (c11 & m[13]);
-      const uint64_t b0 = (c00 & ~b1 & m[0]) | (c00 & b1 & m[2]) | (c01 & ~b1 & m[4]) | (c01 & b1 & m[6]) |
-                          (c10 & ~b1 & m[8]) | (c10 & b1 & m[10]) | (c11 & ~b1 & m[12]) | (c11 & b1 & m[14]);
-      it += lane_select_v(b0, 1) + lane_select_v(b1, 2) + lane_select_v(b2, 4) + lane_select_v(b3, 8) +
-            lane_select_v(m[15], 1);
-    }
+    it += block_trips16(m, live);
     const uint32_t br = __float_as_uint(zr), bi = __float_as_uint(zi);
     const uint64_t per = lk & __builtin_amdgcn_ballot_w64(br == save_r) & __builtin_amdgcn_ballot_w64(bi == save_i);
     if (per) it = lane_select_keep(per, max_iter, it);
@@ -150,7 +116,7 @@ __device__ __forceinline__ int escape_count(const vdsl_escape_time_params& p, in
     }
     if (live == 0) break;
   }
-  if (k + kUnroll > max_iter && live != 0) {
+  if (k > max_iter - kUnroll && live != 0) {
     for (; k < max_iter; ++k) {
       live &= __builtin_amdgcn_ballot_w64(step());
       it += lane_select(live, 1, 0);

@@ -18,15 +18,11 @@
 //     chains first seen while recording, and the fallback if run-time compilation fails.
 // vdsl_debug_map_chain_mode selects the interpreter or the compiled form for every chain.
 
-#include <hip/hiprtc.h>
-
 #include <cstdlib>
-#include <mutex>
 #include <string>
-#include <unordered_map>
-#include <vector>
 
 #include "common.h"
+#include "jit.h"
 #include "mapchain_kern.h"
 
 namespace vdsl {
@@ -159,27 +155,9 @@ int map_mode() {
 // Launches of fewer elements run the interpreter: they are over in microseconds, and compiling
 // costs a fraction of a second once per chain.
 constexpr int64_t kCompileMinElements = int64_t{1} << 20;
-constexpr int kMaxCompiledPerDevice = 512;
-constexpr int kMaxDevices = 64;
 
-// The text of vdsl.h, fmath.h and mapchain_kern.h (generated by the Makefile), handed to hiprtc as
-// in-memory headers together with minimal stddef.h / stdint.h (hiprtc has no C library headers).
-#include "embedded_src.inc"
-const char kStubStddef[] = "typedef decltype(sizeof(0)) size_t;\n";
-const char kStubStdint[] =
-    "typedef signed char int8_t; typedef unsigned char uint8_t; typedef short int16_t;\n"
-    "typedef unsigned short uint16_t; typedef int int32_t; typedef unsigned int uint32_t;\n"
-    "typedef long long int64_t; typedef unsigned long long uint64_t;\n";
-
-struct Compiled {
-  hipModule_t mod = nullptr;
-  hipFunction_t f32 = nullptr, f64 = nullptr;  // entries with 32- and 64-bit indices
-  bool failed = false;
-};
-
-std::mutex g_jit_mu;
-std::unordered_map<std::string, Compiled> g_jit[kMaxDevices];
-std::atomic<int64_t> g_jit_launches{0}, g_jit_compiles{0}, g_jit_failures{0};
+JitCounters g_jit;
+std::atomic<int64_t> g_jit_launches{0};
 
 // The fixed-program table of a chain, as C++ source; it names the kernel completely (with the entry
 // points), so it is also the cache key.
@@ -225,60 +203,6 @@ std::string program_source(const MapProg& rt, int n_inputs, const int32_t* bcast
   return s;
 }
 
-// Compiles (once per device and source) and loads the chain's kernels on the current device.
-// Returns VDSL_OK with *out set, or an error (also remembered, so a failing chain is not retried).
-int compiled_kernels(int ordinal, const std::string& src, const Compiled** out) {
-  if (ordinal < 0 || ordinal >= kMaxDevices) return fail(VDSL_ERR_UNSUPPORTED, "map chain: device ordinal beyond the table");
-  std::lock_guard<std::mutex> lk(g_jit_mu);
-  auto& cache = g_jit[ordinal];
-  auto it = cache.find(src);
-  if (it != cache.end()) {
-    if (it->second.failed) return fail(VDSL_ERR_DEVICE, "map chain: run-time compilation failed earlier for this chain");
-    *out = &it->second;
-    return VDSL_OK;
-  }
-  if (static_cast<int>(cache.size()) >= kMaxCompiledPerDevice)
-    return fail(VDSL_ERR_UNSUPPORTED, "map chain: compiled-chain cache is full");
-  Compiled& c = cache[src];
-  c.failed = true;  // until every step below succeeds
-  ++g_jit_compiles;
-  hiprtcProgram prog = nullptr;
-  const char* hdrs[] = {kSrc_vdsl_h, kSrc_fmath_h, kSrc_mapchain_kern_h, kStubStddef, kStubStdint};
-  const char* names[] = {"vdsl.h", "fmath.h", "mapchain_kern.h", "stddef.h", "stdint.h"};
-  if (hiprtcCreateProgram(&prog, src.c_str(), "vdsl_map_chain_program.hip", 5, hdrs, names) != HIPRTC_SUCCESS) {
-    ++g_jit_failures;
-    return fail(VDSL_ERR_DEVICE, "map chain: hiprtcCreateProgram failed");
-  }
-  // The library's own device flags (Makefile HIPFLAGS): same code generation as the built-in kernels.
-  const char* opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
-                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
-  const hiprtcResult cr = hiprtcCompileProgram(prog, 8, opts);
-  if (cr != HIPRTC_SUCCESS) {
-    size_t ls = 0;
-    hiprtcGetProgramLogSize(prog, &ls);
-    std::string log(ls, '\0');
-    if (ls) hiprtcGetProgramLog(prog, &log[0]);
-    hiprtcDestroyProgram(&prog);
-    ++g_jit_failures;
-    return fail(VDSL_ERR_DEVICE, "map chain: run-time compilation failed: " + log.substr(0, 1500));
-  }
-  size_t cs = 0;
-  hiprtcGetCodeSize(prog, &cs);
-  std::vector<char> code(cs);
-  hiprtcGetCode(prog, code.data());
-  hiprtcDestroyProgram(&prog);
-  int st = check_hip(hipModuleLoadData(&c.mod, code.data()), "hipModuleLoadData");
-  if (st == VDSL_OK) st = check_hip(hipModuleGetFunction(&c.f32, c.mod, "vdsl_map_jit32"), "hipModuleGetFunction");
-  if (st == VDSL_OK) st = check_hip(hipModuleGetFunction(&c.f64, c.mod, "vdsl_map_jit64"), "hipModuleGetFunction");
-  if (st != VDSL_OK) {
-    ++g_jit_failures;
-    return st;
-  }
-  c.failed = false;
-  *out = &c;
-  return VDSL_OK;
-}
-
 // Whether a launch of `elements` should use (and, if needed, compile) the chain's own kernel.
 bool want_compiled(vdsl_queue q, int64_t elements) {
   const int m = map_mode();
@@ -292,16 +216,11 @@ bool want_compiled(vdsl_queue q, int64_t elements) {
 // caller runs the interpreter instead.
 int launch_compiled(vdsl_queue q, const std::string& src, bool vector, void* prog_arg, void* in_arg, void* vo_arg, float* out,
                     int64_t rows, int64_t cols) {
-  const Compiled* c = nullptr;
-  if (q->capturing) {
-    std::lock_guard<std::mutex> lk(g_jit_mu);
-    auto& cache = g_jit[q->dev->ordinal];
-    auto it = cache.find(src);
-    if (it == cache.end() || it->second.failed) return VDSL_ERR_UNSUPPORTED;
-    c = &it->second;
-  } else if (compiled_kernels(q->dev->ordinal, src, &c) != VDSL_OK) {
+  // Entries with 32- and 64-bit indices.  While recording, only a chain compiled earlier runs.
+  const char* const entries[] = {"vdsl_map_jit32", "vdsl_map_jit64"};
+  const JitKernels* c = nullptr;
+  if (jit_kernels(q->dev->ordinal, src, entries, 2, q->capturing, g_jit, "map chain", &c) != VDSL_OK)
     return VDSL_ERR_UNSUPPORTED;
-  }
   Geometry g;
   VDSL_TRY(geometry(vector ? 1 : 4, vector ? kRowsV : 2, vector ? 4 : 1, rows, cols, g));
   int32_t r32 = static_cast<int32_t>(rows), c32 = static_cast<int32_t>(cols);
@@ -311,7 +230,7 @@ int launch_compiled(vdsl_queue q, const std::string& src, bool vector, void* pro
   void* a32s[] = {prog_arg, in_arg, &out, &r32, &c32};
   void* a64s[] = {prog_arg, in_arg, &out, &r64, &c64};
   void** args = vector ? (g.idx32 ? a32v : a64v) : (g.idx32 ? a32s : a64s);
-  VDSL_TRY(check_hip(hipModuleLaunchKernel(g.idx32 ? c->f32 : c->f64, g.grid.x, g.grid.y, 1, 256, 1, 1, 0, q->stream, args,
+  VDSL_TRY(check_hip(hipModuleLaunchKernel(g.idx32 ? c->fn[0] : c->fn[1], g.grid.x, g.grid.y, 1, 256, 1, 1, 0, q->stream, args,
                                            nullptr),
                      "hipModuleLaunchKernel(map chain)"));
   ++g_jit_launches;
@@ -394,8 +313,8 @@ extern "C" int vdsl_debug_map_chain_mode(int32_t mode) {
 
 extern "C" int vdsl_debug_map_chain_stats(int64_t* compiled_launches, int64_t* compiles, int64_t* failures) {
   if (compiled_launches) *compiled_launches = g_jit_launches.load();
-  if (compiles) *compiles = g_jit_compiles.load();
-  if (failures) *failures = g_jit_failures.load();
+  if (compiles) *compiles = g_jit.compiles.load();
+  if (failures) *failures = g_jit.failures.load();
   return VDSL_OK;
 }
 

@@ -1,0 +1,124 @@
+// General per-pixel programs (vdsl_op_pixel_program), host side: validation, the program's
+// source for run-time compilation, and the launch.  The device code is pixprog_kern.h.
+//
+// The reference's only computing program is a Taichi struct-for (fractal.py:16-25); its
+// escape-time form has a hand-tuned kernel (escape_time.hip).  Any other body the Taichi-subset
+// front end lowers (other iterated maps, plain per-pixel expressions, reads of other fields) runs
+// here: the body is a register program (include/vdsl.h), compiled once per program and device into
+// straight-line code around the same check-then-update loop.
+
+#include <string>
+
+#include "common.h"
+#include "jit.h"
+#include "pixprog_kern.h"
+
+namespace vdsl {
+namespace {
+
+JitCounters g_pix_jit;
+
+int check_program(const vdsl_pixel_program& p, int n_inputs) {
+  const int64_t total = int64_t{p.n_pre} + p.n_test + p.n_body + p.n_post;
+  if (p.n_pre < 0 || p.n_test < 0 || p.n_body < 0 || p.n_post < 0 || total > VDSL_PIX_MAX_INSTR)
+    return fail(VDSL_ERR_INVALID_ARG, "pixel program: section lengths must be >= 0 and sum to at most 64");
+  if (p.loop != 0 && p.loop != 1) return fail(VDSL_ERR_INVALID_ARG, "pixel program: loop must be 0 or 1");
+  if (!p.loop && (p.n_test || p.n_body)) return fail(VDSL_ERR_INVALID_ARG, "pixel program: test/body sections without a loop");
+  if (p.max_iter < 0) return fail(VDSL_ERR_INVALID_ARG, "pixel program: max_iter < 0");
+  if (p.test < VDSL_PIX_TEST_NONE || p.test > VDSL_PIX_TEST_GE) return fail(VDSL_ERR_INVALID_ARG, "pixel program: unknown test");
+  if (p.test_a < 0 || p.test_a >= VDSL_PIX_MAX_REGS || p.test_b < 0 || p.test_b >= VDSL_PIX_MAX_REGS)
+    return fail(VDSL_ERR_INVALID_ARG, "pixel program: test register out of range");
+  if (p.out_kind != VDSL_PIX_OUT_REG && p.out_kind != VDSL_PIX_OUT_COUNT)
+    return fail(VDSL_ERR_INVALID_ARG, "pixel program: unknown out_kind");
+  if (p.out_reg < 0 || p.out_reg >= VDSL_PIX_MAX_REGS) return fail(VDSL_ERR_INVALID_ARG, "pixel program: out_reg out of range");
+  if (p.out_kind == VDSL_PIX_OUT_COUNT && !p.loop) return fail(VDSL_ERR_INVALID_ARG, "pixel program: a count needs a loop");
+  const int post0 = p.n_pre + p.n_test + p.n_body;
+  for (int pc = 0; pc < total; ++pc) {
+    const vdsl_map_instr& s = p.code[pc];
+    const std::string at = "pixel program: instruction " + std::to_string(pc);
+    const bool map_op = s.op >= VDSL_MAP_LOAD && s.op <= VDSL_MAP_ADD_IMM;
+    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_COUNT;
+    if (!map_op && !pix_op) return fail(VDSL_ERR_INVALID_ARG, at + ": unknown opcode " + std::to_string(s.op));
+    if (s.dst >= VDSL_PIX_MAX_REGS || s.b >= VDSL_PIX_MAX_REGS || s.c >= VDSL_PIX_MAX_REGS)
+      return fail(VDSL_ERR_INVALID_ARG, at + ": register out of range");
+    if (s.op == VDSL_MAP_LOAD) {
+      if (s.a >= n_inputs || s.c != 0) return fail(VDSL_ERR_INVALID_ARG, at + ": LOAD of an input that is not there");
+    } else if (s.op == VDSL_PIX_INDEX) {
+      if (s.a > 1) return fail(VDSL_ERR_INVALID_ARG, at + ": INDEX axis must be 0 (i) or 1 (j)");
+    } else if (s.a >= VDSL_PIX_MAX_REGS) {
+      return fail(VDSL_ERR_INVALID_ARG, at + ": register out of range");
+    }
+    if (s.op == VDSL_PIX_COUNT && pc < post0) return fail(VDSL_ERR_INVALID_ARG, at + ": COUNT outside the post section");
+  }
+  return VDSL_OK;
+}
+
+// The program's table as C++ source (opcodes and registers; immediates stay kernel arguments).
+// It names the kernel completely, so it is also the cache key.
+std::string program_source(const vdsl_pixel_program& p) {
+  std::string s = "#include \"pixprog_kern.h\"\nnamespace vdsl {\nstruct PixJit {\n";
+  auto c = [&](const char* name, int v) { s += std::string("  static constexpr int ") + name + " = " + std::to_string(v) + ";\n"; };
+  c("n_pre", p.n_pre);
+  c("n_test", p.n_test);
+  c("n_body", p.n_body);
+  c("n_post", p.n_post);
+  c("loop", p.loop);
+  c("test", p.test);
+  c("test_a", p.test_a);
+  c("test_b", p.test_b);
+  c("out_kind", p.out_kind);
+  c("out_reg", p.out_reg);
+  s += "  static constexpr vdsl_map_instr code[VDSL_PIX_MAX_INSTR] = {\n";
+  const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
+  for (int pc = 0; pc < total; ++pc) {
+    const vdsl_map_instr& k = p.code[pc];
+    s += "    {" + std::to_string(k.op) + ", " + std::to_string(k.dst) + ", " + std::to_string(k.a) + ", " + std::to_string(k.b) +
+         ", " + std::to_string(k.c) + ", {0, 0, 0}, 0.f},\n";
+  }
+  s += "  };\n};\n}  // namespace vdsl\n";
+  s += "extern \"C\" __global__ __launch_bounds__(256) void vdsl_pix_jit(vdsl::PixRt rt, vdsl::PixIn in, void* out, int ni, "
+       "int nj) {\n  vdsl::pixel_body<vdsl::PixJit>(rt, in, out, ni, nj);\n}\n";
+  return s;
+}
+
+}  // namespace
+}  // namespace vdsl
+
+using namespace vdsl;
+
+extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const vdsl_pixel_program* prog,
+                                     const vdsl_buffer* inputs, int32_t n_inputs, vdsl_buffer out) {
+  VDSL_TRY(enter_queue(q));
+  if (!prog) return fail(VDSL_ERR_INVALID_ARG, "prog is null");
+  if (ni < 0 || nj < 0) return fail(VDSL_ERR_INVALID_ARG, "negative grid extent");
+  if (n_inputs < 0 || n_inputs > VDSL_PIX_MAX_INPUTS) return fail(VDSL_ERR_INVALID_ARG, "n_inputs out of range [0, 4]");
+  if (n_inputs && !inputs) return fail(VDSL_ERR_INVALID_ARG, "inputs is null");
+  const vdsl_pixel_program& p = *prog;
+  VDSL_TRY(check_program(p, n_inputs));
+  const size_t bytes = nbytes(ni, nj, 4);
+  VDSL_TRY(check_buffer(q, out, bytes, "out", true));
+  PixIn in{};
+  for (int k = 0; k < n_inputs; ++k) {
+    const std::string name = "input" + std::to_string(k);
+    VDSL_TRY(check_buffer(q, inputs[k], bytes, name.c_str(), false));
+    in.p[k] = static_cast<const float*>(inputs[k]->ptr);
+  }
+  if (ni == 0 || nj == 0) return VDSL_OK;
+  if ((ni + 15) / 16 > 65535) return fail(VDSL_ERR_UNSUPPORTED, "pixel program: ni too large");
+  PixRt rt{};
+  const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
+  for (int pc = 0; pc < total; ++pc) rt.imm[pc] = p.code[pc].imm;
+  rt.max_iter = p.max_iter;
+  const std::string src = program_source(p);
+  const char* const entries[] = {"vdsl_pix_jit"};
+  const JitKernels* k = nullptr;
+  const int st = jit_kernels(q->dev->ordinal, src, entries, 1, q->capturing, g_pix_jit, "pixel program", &k);
+  if (st == VDSL_ERR_UNSUPPORTED && q->capturing)
+    return fail(VDSL_ERR_CAPTURE, "pixel program: not compiled yet; run it once before recording a graph");
+  VDSL_TRY(st);
+  void* o = out->ptr;
+  void* args[] = {&rt, &in, &o, &ni, &nj};
+  return check_hip(hipModuleLaunchKernel(k->fn[0], static_cast<unsigned>((nj + 15) / 16), static_cast<unsigned>((ni + 15) / 16), 1,
+                                         256, 1, 1, 0, q->stream, args, nullptr),
+                   "hipModuleLaunchKernel(pixel program)");
+}

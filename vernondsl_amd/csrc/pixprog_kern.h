@@ -1,0 +1,227 @@
+// Device side of general per-pixel programs (vdsl_op_pixel_program): the struct-for body of a
+// Taichi kernel over a 2-D field, with the check-then-update loop of fractal.py:22-24.  The host
+// (pixel_prog.hip) compiles this header at run time with one program's opcode table, so the
+// program unrolls into straight-line code; only immediates and max_iter stay kernel arguments.
+// Shares apply_op with the map chains (mapchain_kern.h), so an opcode means the same arithmetic in
+// both op classes.  Uses nothing from the C++ standard library (hiprtc has none).
+//
+// Mapping: one lane per pixel; each wave takes an 8x8 tile (lanes of a tile tend to leave an
+// escape loop at similar trips) and a 256-lane block a 16x16 patch.  The loop is the escape-time
+// kernel's (escape_time.hip) made general: wave-uniform, in blocks of 16 trips, with the live set
+// a sticky 64-bit lane mask (one ballot and one scalar AND per trip) and the count added per
+// block from the block's masks (lanemask.h).  Every lane runs every trip of its wave; what a lane
+// computes after its test failed is discarded, as follows.  The program's register sets are
+// worked out at compile time from the opcode table: only the registers the post section (or the
+// store) reads that the loop also writes need their values from the trip the lane left the loop,
+// and only those are kept, by one select per trip each (none for count-only programs such as an
+// escape count).  When none is needed, a lane whose loop-carried registers return to the bits
+// they held at an earlier block end (saved at the ends of blocks 1, 2, 4, 8, ...) would pass its
+// test for ever: its count is max_iter and it leaves the live set at once (exact periodicity).
+#pragma once
+
+#include "lanemask.h"
+#include "mapchain_kern.h"
+
+namespace vdsl {
+
+struct PixRt {
+  float imm[VDSL_PIX_MAX_INSTR];
+  int32_t max_iter;
+};
+
+struct PixIn {
+  const float* p[VDSL_PIX_MAX_INPUTS];
+};
+
+// One instruction at program counter PC of the table P.
+template <class P, int PC>
+__device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], unsigned long long o,
+                                         float fi, float fj, float fcount) {
+  constexpr vdsl_map_instr s = P::code[PC];
+  if constexpr (s.op == VDSL_MAP_LOAD) {
+    r[s.dst] = in.p[s.a][o];
+  } else if constexpr (s.op == VDSL_PIX_INDEX) {
+    r[s.dst] = s.a == 0 ? fi : fj;
+  } else if constexpr (s.op == VDSL_PIX_COUNT) {
+    r[s.dst] = fcount;
+  } else if constexpr (s.op == VDSL_PIX_COS) {
+    r[s.dst] = cosf(r[s.a]);
+  } else if constexpr (s.op == VDSL_PIX_SIN) {
+    r[s.dst] = sinf(r[s.a]);
+  } else {
+    r[s.dst] = apply_op(s.op, r[s.a], r[s.b], r[s.c], rt.imm[PC]);
+  }
+}
+
+template <class P, int BASE, int... K>
+__device__ __forceinline__ void pix_section(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], unsigned long long o,
+                                            float fi, float fj, float fcount, Seq<K...>) {
+  (pix_step<P, BASE + K>(rt, in, r, o, fi, fj, fcount), ...);
+}
+
+template <int TEST>
+__device__ __forceinline__ bool pix_test(float a, float b) {
+  if constexpr (TEST == VDSL_PIX_TEST_LT) return a < b;
+  else if constexpr (TEST == VDSL_PIX_TEST_LE) return a <= b;
+  else if constexpr (TEST == VDSL_PIX_TEST_GT) return a > b;
+  else if constexpr (TEST == VDSL_PIX_TEST_GE) return a >= b;
+  else return true;
+}
+
+// Registers an instruction reads (a bit per register).
+__device__ constexpr uint32_t pix_reads(const vdsl_map_instr& s) {
+  switch (s.op) {
+    case VDSL_MAP_LOAD: case VDSL_MAP_CONST: case VDSL_PIX_INDEX: case VDSL_PIX_COUNT: return 0u;
+    case VDSL_MAP_ADD: case VDSL_MAP_SUB: case VDSL_MAP_MUL: case VDSL_MAP_DIV: case VDSL_MAP_MAX: case VDSL_MAP_MIN:
+      return (1u << s.a) | (1u << s.b);
+    case VDSL_MAP_FMA: return (1u << s.a) | (1u << s.b) | (1u << s.c);
+    default: return 1u << s.a;
+  }
+}
+
+// Register sets of program P (instructions [lo, hi) of its table): written, and read before
+// written (read-before-write, i.e. the values the range takes from before it).
+template <class P>
+struct PixSets {
+  static constexpr int t0 = P::n_pre, b0 = t0 + P::n_test, q0 = b0 + P::n_body, end = q0 + P::n_post;
+  static constexpr uint32_t writes(int lo, int hi) {
+    uint32_t w = 0u;
+    for (int pc = lo; pc < hi; ++pc) w |= 1u << P::code[pc].dst;
+    return w;
+  }
+  static constexpr uint32_t rbw(int lo, int hi) {
+    uint32_t w = 0u, r = 0u;
+    for (int pc = lo; pc < hi; ++pc) {
+      r |= pix_reads(P::code[pc]) & ~w;
+      w |= 1u << P::code[pc].dst;
+    }
+    return r;
+  }
+  static constexpr uint32_t test_w = writes(t0, b0);
+  static constexpr uint32_t body_w = writes(b0, q0);
+  static constexpr uint32_t loop_w = test_w | body_w;
+  // What the post section and the store take from the loop.
+  static constexpr uint32_t post_r =
+      rbw(q0, end) | ((P::out_kind == VDSL_PIX_OUT_REG && !((writes(q0, end) >> P::out_reg) & 1u)) ? (1u << P::out_reg) : 0u);
+  static constexpr uint32_t keep_t = test_w & post_r;   // kept from the trip a lane's test failed
+  static constexpr uint32_t keep_b = body_w & post_r;   // kept from the lane's last counted trip
+  static constexpr bool free_running = (loop_w & post_r) == 0u;
+  static constexpr uint32_t carried = rbw(t0, q0) & loop_w;  // the loop's state from trip to trip
+};
+
+template <class P, int BASE, int N>
+__device__ __forceinline__ void pix_run(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], unsigned long long o,
+                                        float fi, float fj, float fcount) {
+  pix_section<P, BASE>(rt, in, r, o, fi, fj, fcount, typename MakeSeq<N>::type{});
+}
+
+// r[k] <- r[k] where the lane's bit of `mask` is set, else old[k], for the registers in KEEP.
+template <uint32_t KEEP>
+__device__ __forceinline__ void pix_keep(float (&r)[VDSL_PIX_MAX_REGS], const float (&old)[VDSL_PIX_MAX_REGS], uint64_t mask) {
+#pragma unroll
+  for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k)
+    if constexpr (KEEP != 0u)
+      if ((KEEP >> k) & 1u) r[k] = lane_select_f(mask, r[k], old[k]);
+}
+
+// One trip: the test section, the lane's test into the sticky mask `lk`, the body.  Registers in
+// the keep sets hold their values on lanes that are not live.
+template <class P>
+__device__ __forceinline__ void pix_trip(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], unsigned long long o,
+                                         float fi, float fj, uint64_t& lk) {
+  using S = PixSets<P>;
+  float old[VDSL_PIX_MAX_REGS];
+  if constexpr (S::keep_t != 0u) {
+#pragma unroll
+    for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) old[k] = r[k];
+  }
+  const uint64_t start = lk;
+  pix_run<P, S::t0, P::n_test>(rt, in, r, o, fi, fj, 0.0f);
+  pix_keep<S::keep_t>(r, old, start);
+  lk &= __builtin_amdgcn_ballot_w64(pix_test<P::test>(r[P::test_a], r[P::test_b]));
+  if constexpr (S::keep_b != 0u) {
+#pragma unroll
+    for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) old[k] = r[k];
+  }
+  pix_run<P, S::b0, P::n_body>(rt, in, r, o, fi, fj, 0.0f);
+  pix_keep<S::keep_b>(r, old, lk);
+}
+
+// P: the program table (n_pre, n_test, n_body, n_post, loop, test, test_a, test_b, out_kind,
+// out_reg, code[]).  out: f32 or int32 [ni][nj].
+template <class P>
+__device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, void* __restrict__ out, int ni, int nj) {
+  using S = PixSets<P>;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int i = blockIdx.y * 16 + (wave >> 1) * 8 + (lane >> 3);
+  const int j = blockIdx.x * 16 + (wave & 1) * 8 + (lane & 7);
+  const bool inside = i < ni && j < nj;
+  // Lanes past the grid run the program on pixel (0, 0), are never live, and store nothing.
+  const unsigned long long o = inside ? static_cast<unsigned long long>(i) * static_cast<unsigned>(nj) + j : 0ull;
+  const float fi = static_cast<float>(i), fj = static_cast<float>(j);
+  float r[VDSL_PIX_MAX_REGS];
+#pragma unroll
+  for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) r[k] = 0.0f;
+  pix_run<P, 0, P::n_pre>(rt, in, r, o, fi, fj, 0.0f);
+  int count = 0;
+  if constexpr (P::loop && P::test == VDSL_PIX_TEST_NONE) {
+    // No test: every lane makes max_iter trips; they run only if something after the loop reads
+    // what they compute.
+    const int max_iter = rt.max_iter;
+    if constexpr (!S::free_running) {
+      for (int t = 0; t < max_iter; ++t) {
+        pix_run<P, S::t0, P::n_test>(rt, in, r, o, fi, fj, 0.0f);
+        pix_run<P, S::b0, P::n_body>(rt, in, r, o, fi, fj, 0.0f);
+      }
+    }
+    count = max_iter;
+  } else if constexpr (P::loop) {
+    constexpr int kUnroll = 16;
+    const int max_iter = rt.max_iter;
+    uint64_t live = __builtin_amdgcn_ballot_w64(inside);
+    float save[VDSL_PIX_MAX_REGS];
+#pragma unroll
+    for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) save[k] = r[k];
+    int t = 0;
+    for (; t <= max_iter - kUnroll; t += kUnroll) {
+      uint64_t m[kUnroll];
+      uint64_t lk = live;
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        pix_trip<P>(rt, in, r, o, fi, fj, lk);
+        m[u] = lk;
+      }
+      count += block_trips16(m, live);
+      live = lk;
+      if constexpr (S::free_running && S::carried != 0u) {
+        uint64_t same = live;
+#pragma unroll
+        for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k)
+          if ((S::carried >> k) & 1u) same &= __builtin_amdgcn_ballot_w64(__float_as_uint(r[k]) == __float_as_uint(save[k]));
+        if (same) count = lane_select_keep(same, max_iter, count);
+        live &= ~same;
+        const int blocks_done = __builtin_amdgcn_readfirstlane(t) / kUnroll + 1;  // wave-uniform
+        if ((blocks_done & (blocks_done - 1)) == 0) {
+#pragma unroll
+          for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k)
+            if ((S::carried >> k) & 1u) save[k] = r[k];
+        }
+      }
+      if (live == 0ull) break;
+    }
+    if (t > max_iter - kUnroll && live != 0ull) {
+      for (; t < max_iter; ++t) {  // the last max_iter % 16 trips, counted one by one
+        pix_trip<P>(rt, in, r, o, fi, fj, live);
+        count += lane_select(live, 1, 0);
+      }
+    }
+  }
+  pix_run<P, S::q0, P::n_post>(rt, in, r, o, fi, fj, static_cast<float>(count));
+  if (inside) {
+    if constexpr (P::out_kind == VDSL_PIX_OUT_COUNT) static_cast<int*>(out)[o] = count;
+    else static_cast<float*>(out)[o] = r[P::out_reg];
+  }
+}
+
+}  // namespace vdsl

@@ -243,6 +243,21 @@ def gemm_bf16_mul_packed(q: Queue, A: Tensor, Bp: Tensor, g: Tensor, c: Tensor, 
     call("vdsl_op_gemm_bf16_mul_packed", q.handle, M, N, K, A.handle, Bp.handle, g.handle, c.handle, _h(c_t))
 
 
+def pixel_program(q: Queue, prog, inputs, out: Tensor):
+    """Runs a compiled per-pixel program (vernondsl_amd.pixprog.PixelProgram) over out's [ni][nj]
+    grid: out f32 (the program stores a register) or i32 (it stores its loop count); inputs: f32
+    fields of out's shape, read at each pixel."""
+    if len(out.shape) != 2:
+        raise ValueError("out must be a 2-D field")
+    ni, nj = out.shape
+    want = "i32" if prog.out_kind == 1 else "f32"
+    _expect(out, (ni, nj), want, "out")
+    for k, t in enumerate(inputs):
+        _expect(t, (ni, nj), "f32", f"input{k}")
+    hs = (C.c_void_p * max(1, len(inputs)))(*[t.handle for t in inputs])
+    call("vdsl_op_pixel_program", q.handle, ni, nj, C.byref(prog), hs, len(inputs), out.handle)
+
+
 def mse_partials_count(rows, cols) -> int:
     return int(_lib.lib.vdsl_mse_partials_count(rows, cols))
 

@@ -24,8 +24,13 @@ f32 (Taichi's default float type), and the body must have the escape-time shape
             k += 1
         F[i, j] = <k, or a + k * b / a - k * b>
 
-A body of any other shape raises TaichiLoweringError naming what did not match; there is no CPU
-fallback.  Accepted complex squares are the ones equal bit for bit to (zr*zr - zi*zi, (zi*zr)*2):
+Bodies of any other shape are lowered by the general path to a per-pixel register program
+(vernondsl_amd.pixprog, run by vdsl_op_pixel_program, compiled at run time for the program): any
+expression of the pixel indices, scalar kernel arguments, other 2-D f32 fields read at [i, j]
+and constants, with at most one loop - a `while <test> and <counter> < MAX:` check-then-update
+loop whose body ends with `counter += 1`, or a `for _ in range(N):` loop - and one store
+`F[i, j] = <value>` (an i32 field stores the loop counter).  What neither path lowers raises
+TaichiLoweringError naming what did not match; there is no CPU fallback.  Accepted complex squares are the ones equal bit for bit to (zr*zr - zi*zi, (zi*zr)*2):
 `z[0]**2 - z[1]**2`, `z[0]*z[0] - z[1]*z[1]`, and `z[1]*z[0]*2` / `z[0]*z[1]*2` / `2*(z[0]*z[1])` /
 `z[0]*z[1] + z[0]*z[1]` for the imaginary part (`(2*z[0])*z[1]` is refused: it rounds differently
 when the product is subnormal).
@@ -179,18 +184,20 @@ class Kernel:
         self.arg_names = [a.arg for a in self.fdef.args.args]
         self.arg_types = [_annotation(a.annotation) for a in self.fdef.args.args]
 
-    def lower(self, *args):
+    def lower(self, *args) -> "Lowered":
         env = dict(self.fn.__globals__)
         for name, typ, val in zip(self.arg_names, self.arg_types, args):
             env[name] = _coerce(typ, val)
-        return lower_escape_time(self.fdef, _FuncResolver(env), env)
+        return lower_kernel(self.fdef, _FuncResolver(env), env)
 
     def __call__(self, *args):
-        fld, params = self.lower(*args)
+        low = self.lower(*args)
         from . import kernels
         _, q = _device()
-        p = kernels.escape_time_params(**params)
-        kernels.escape_time(q, p, fld.tensor())
+        if low.kind == "escape_time":
+            kernels.escape_time(q, kernels.escape_time_params(**low.params), low.field.tensor())
+        else:
+            kernels.pixel_program(q, low.program, [f.tensor() for f in low.inputs], low.field.tensor())
 
 
 def _annotation(node):
@@ -561,8 +568,23 @@ def _lower_store(v, fld, params):
 
 # ---- lowering from program text (no execution) -----------------------------------------------------
 def lower_source(text: str, kernel_name: str, args: dict) -> tuple:
-    """Lowers `kernel_name` of a Taichi program given as text, without running it: module-level
-    constants and fields are evaluated statically (literals, arithmetic, ti.field calls)."""
+    """Lowers `kernel_name` of a Taichi program given as text, without running it, to the
+    escape-time op: (field, vdsl_escape_time_params as a dict).  Module-level constants and fields
+    are evaluated statically (literals, arithmetic, ti.field calls)."""
+    kern, funcs, env = _parse_source(text, kernel_name, args)
+    return lower_escape_time(kern, _FuncResolver(env, funcs), env)
+
+
+def lower_source_kernel(text: str, kernel_name: str, args: dict, general: bool = False) -> "Lowered":
+    """As lower_source, by either path (escape-time op, else the general per-pixel program);
+    general=True takes the general path even for bodies of the escape-time form."""
+    kern, funcs, env = _parse_source(text, kernel_name, args)
+    if general:
+        return lower_pixel_program(kern, _FuncResolver(env, funcs), env)
+    return lower_kernel(kern, _FuncResolver(env, funcs), env)
+
+
+def _parse_source(text: str, kernel_name: str, args: dict):
     mod = ast.parse(text)
     env = {"float": float, "int": int}
     tinames = set()
@@ -610,8 +632,434 @@ def lower_source(text: str, kernel_name: str, args: dict) -> tuple:
     for a in kern.args.args:
         if a.arg in args:
             env[a.arg] = _coerce(_annotation(a.annotation), args[a.arg])
-    return lower_escape_time(kern, _FuncResolver(env, funcs), env)
+    return kern, funcs, env
 
 
 # math helpers programs sometimes use at module level
 pi = math.pi
+
+
+# ---- the general path: any struct-for body as a per-pixel register program ---------------------------
+class Lowered:
+    """A lowered kernel: kind "escape_time" (field, params for vdsl_op_escape_time) or
+    "pixel_program" (field, program for vdsl_op_pixel_program, input fields it reads)."""
+
+    def __init__(self, kind, field, params=None, program=None, inputs=()):
+        self.kind, self.field, self.params, self.program, self.inputs = kind, field, params, program, list(inputs)
+
+
+def lower_kernel(fdef: ast.FunctionDef, funcs, env) -> Lowered:
+    """The escape-time op for bodies of that form (its hand-tuned kernel), else the general
+    per-pixel program; TaichiLoweringError when neither lowers the body."""
+    try:
+        fld, params = lower_escape_time(fdef, funcs, env)
+        return Lowered("escape_time", fld, params=params)
+    except TaichiLoweringError as e1:
+        try:
+            return lower_pixel_program(fdef, funcs, env)
+        except TaichiLoweringError as e2:
+            raise TaichiLoweringError(f"{e2} (and not of the escape-time form: {e1})") from None
+
+
+class _PVec:
+    """A small vector (ti.Vector) of per-pixel values: numbers or pixprog Nodes."""
+
+    def __init__(self, comps):
+        self.comps = list(comps)
+
+
+_UNARY_FUNCS = {"sqrt": "sqrt", "exp": "exp", "log": "log", "sin": "sin", "cos": "cos", "tanh": "tanh", "abs": "abs"}
+
+
+class _PixInterp:
+    """Evaluates a struct-for body over numbers (folded in f32 as Taichi's default float, ints
+    kept exact), pixprog Nodes and _PVec vectors."""
+
+    def __init__(self, env, funcs, b, fld, iname, jname):
+        from . import pixprog
+        self.pp = pixprog
+        self.env, self.funcs, self.b = env, funcs, b
+        self.fld, self.iname, self.jname = fld, iname, jname
+        self.inputs = []  # Fields read at [i, j], in LOAD order
+
+    # -- values
+    def node(self, v):
+        if isinstance(v, self.pp.Node):
+            return v
+        if _is_num(v):
+            return self.b.const(_f32(v))
+        raise TaichiLoweringError(f"{v!r} is not a per-pixel scalar")
+
+    def arith(self, op, x, y):
+        if isinstance(x, _PVec) or isinstance(y, _PVec):
+            xs = x.comps if isinstance(x, _PVec) else None
+            ys = y.comps if isinstance(y, _PVec) else None
+            if xs is not None and ys is not None and len(xs) != len(ys):
+                raise TaichiLoweringError("vector length mismatch")
+            n = len(xs if xs is not None else ys)
+            return _PVec([self.arith(op, xs[k] if xs is not None else x, ys[k] if ys is not None else y) for k in range(n)])
+        if _is_num(x) and _is_num(y):
+            if op == "pow":
+                return _binop("pow", x, y)
+            return _binop(op, x, y)
+        if op == "pow":
+            if not (isinstance(y, (int, np.integer)) and 1 <= int(y) <= 8):
+                raise TaichiLoweringError("only small positive integer powers (x ** n, n <= 8) are supported")
+            r = x
+            for _ in range(int(y) - 1):
+                r = self.b.op("mul", self.node(r), self.node(x))
+            return r
+        return self.b.op(op, self.node(x), self.node(y))
+
+    def unary(self, fn, x):
+        if isinstance(x, _PVec):
+            return _PVec([self.unary(fn, c) for c in x.comps])
+        if _is_num(x):
+            v = np.float32(x)
+            with np.errstate(all="ignore"):
+                return {"neg": -v, "abs": np.abs(v), "sqrt": np.sqrt(v), "exp": np.exp(v), "log": np.log(v), "sin": np.sin(v),
+                        "cos": np.cos(v), "tanh": np.tanh(v)}[fn]
+        return self.b.op(fn, x)
+
+    def dot(self, a, c):
+        if not (isinstance(a, _PVec) and isinstance(c, _PVec) and len(a.comps) == len(c.comps)):
+            raise TaichiLoweringError("dot needs two vectors of one length")
+        acc = self.arith("mul", a.comps[0], c.comps[0])
+        for x, y in zip(a.comps[1:], c.comps[1:]):
+            acc = self.arith("add", acc, self.arith("mul", x, y))
+        return acc
+
+    # -- expressions
+    def expr(self, n, local):
+        if isinstance(n, ast.Constant):
+            if isinstance(n.value, bool) or not isinstance(n.value, (int, float)):
+                raise TaichiLoweringError(f"constant {n.value!r} is not a number")
+            return n.value
+        if isinstance(n, ast.Name):
+            if n.id in local:
+                v = local[n.id]
+                if v is _UNREADABLE:
+                    raise TaichiLoweringError(f"{n.id!r} can only be read after the loop (the loop counter)")
+                return v
+            if n.id in self.env:
+                return self.env[n.id]
+            raise TaichiLoweringError(f"unknown name {n.id!r}")
+        if isinstance(n, ast.BinOp):
+            ops = {ast.Add: "add", ast.Sub: "sub", ast.Mult: "mul", ast.Div: "div", ast.Pow: "pow"}
+            if type(n.op) not in ops:
+                raise TaichiLoweringError(f"operator {type(n.op).__name__} is not supported")
+            return self.arith(ops[type(n.op)], self.expr(n.left, local), self.expr(n.right, local))
+        if isinstance(n, ast.UnaryOp):
+            v = self.expr(n.operand, local)
+            if isinstance(n.op, ast.USub):
+                return self.unary("neg", v)
+            if isinstance(n.op, ast.UAdd):
+                return v
+            raise TaichiLoweringError(f"unary {type(n.op).__name__} is not supported")
+        if isinstance(n, ast.Subscript):
+            base = self.expr(n.value, local)
+            if isinstance(base, Field):
+                return self.field_read(base, n.slice)
+            idx = self.expr(n.slice, local)
+            if isinstance(base, _PVec) and isinstance(idx, (int, np.integer)) and -len(base.comps) <= idx < len(base.comps):
+                return base.comps[int(idx)]
+            raise TaichiLoweringError("only constant vector indexing and field[i, j] reads are supported")
+        if isinstance(n, ast.Attribute):
+            base = self.expr(n.value, local)
+            if isinstance(base, _PVec) and n.attr in ("x", "y", "z", "w"):
+                k = "xyzw".index(n.attr)
+                if k >= len(base.comps):
+                    raise TaichiLoweringError(f"vector has no component {n.attr!r}")
+                return base.comps[k]
+            if isinstance(base, (_PVec, self.pp.Node)):
+                return (base, n.attr)
+            return getattr(base, n.attr)
+        if isinstance(n, (ast.List, ast.Tuple)):
+            return [self.expr(e, local) for e in n.elts]
+        if isinstance(n, ast.Call):
+            return self.call(n, local)
+        raise TaichiLoweringError(f"expression {ast.dump(n)[:60]} is not supported")
+
+    def field_read(self, fld, idx):
+        if not (isinstance(idx, ast.Tuple) and [getattr(e, "id", None) for e in idx.elts] == [self.iname, self.jname]):
+            raise TaichiLoweringError("fields are read at [i, j] of the struct-for only")
+        if fld.shape != self.fld.shape or fld.dtype != f32:
+            raise TaichiLoweringError("a field read must be an f32 field of the iterated field's shape")
+        if fld not in self.inputs:
+            if len(self.inputs) == self.pp.MAX_INPUTS:
+                raise TaichiLoweringError(f"at most {self.pp.MAX_INPUTS} fields can be read")
+            self.inputs.append(fld)
+        return self.b.load(self.inputs.index(fld))
+
+    def call(self, n, local):
+        f = n.func
+        if isinstance(f, ast.Attribute):
+            base = self.expr(f.value, local)
+            if isinstance(base, _PVec):
+                if f.attr == "norm":
+                    return self.unary("sqrt", self.dot(base, base))
+                if f.attr == "norm_sqr":
+                    return self.dot(base, base)
+                if f.attr == "dot":
+                    return self.dot(base, self.expr(n.args[0], local))
+                raise TaichiLoweringError(f"vector method {f.attr!r} is not supported")
+            if f.attr == "Vector":
+                comps = self.expr(n.args[0], local)
+                if not isinstance(comps, list) or any(isinstance(c, _PVec) for c in comps):
+                    raise TaichiLoweringError("ti.Vector takes a list of scalars")
+                return _PVec(comps)
+            if f.attr in _UNARY_FUNCS:
+                return self.unary(_UNARY_FUNCS[f.attr], self.expr(n.args[0], local))
+            if f.attr in ("max", "min"):
+                return self.minmax(f.attr, [self.expr(a, local) for a in n.args])
+            raise TaichiLoweringError(f"call {f.attr!r} is not supported")
+        if isinstance(f, ast.Name):
+            fdef = self.funcs.get(f.id)
+            if fdef is None:
+                obj = self.env.get(f.id, _BUILTINS.get(f.id))
+                if obj is abs:
+                    return self.unary("abs", self.expr(n.args[0], local))
+                if obj in (max, min):
+                    return self.minmax(obj.__name__, [self.expr(a, local) for a in n.args])
+                if obj is float:
+                    v = self.expr(n.args[0], local)
+                    return _f32(v) if _is_num(v) else v
+                raise TaichiLoweringError(f"call of {f.id!r}: only @ti.func functions are inlined")
+            args = [self.expr(a, local) for a in n.args]
+            sub = dict(zip([a.arg for a in fdef.args.args], args))
+            for st in fdef.body:
+                if isinstance(st, ast.Return):
+                    return self.expr(st.value, sub)
+                if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Name):
+                    sub[st.targets[0].id] = self.expr(st.value, sub)
+                    continue
+                if isinstance(st, ast.Expr) and isinstance(st.value, ast.Constant):
+                    continue
+                raise TaichiLoweringError(f"statement in @ti.func {f.id!r} is not supported")
+            raise TaichiLoweringError(f"@ti.func {f.id!r} returns nothing")
+        raise TaichiLoweringError("unsupported call")
+
+    def minmax(self, which, vals):
+        if len(vals) < 2:
+            raise TaichiLoweringError(f"{which} needs two or more values")
+        acc = vals[0]
+        for v in vals[1:]:
+            if _is_num(acc) and _is_num(v):
+                acc = (max if which == "max" else min)(_f32(acc), _f32(v))
+            else:
+                acc = self.b.op(which, self.node(acc), self.node(v))
+        return acc
+
+    # -- statements
+    def assign(self, st, local):
+        if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Name):
+            local[st.targets[0].id] = self.expr(st.value, local)
+            return True
+        if (isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Tuple)
+                and all(isinstance(t, ast.Name) for t in st.targets[0].elts)):
+            vals = self.expr(st.value, local)  # every right-hand value first: a parallel assignment
+            names = [t.id for t in st.targets[0].elts]
+            if isinstance(vals, _PVec):
+                vals = vals.comps
+            if not isinstance(vals, list) or len(vals) != len(names):
+                raise TaichiLoweringError("tuple assignment of a different number of values")
+            for nm, v in zip(names, vals):
+                local[nm] = v
+            return True
+        if isinstance(st, ast.AugAssign) and isinstance(st.target, ast.Name):
+            ops = {ast.Add: "add", ast.Sub: "sub", ast.Mult: "mul", ast.Div: "div"}
+            if type(st.op) not in ops:
+                raise TaichiLoweringError(f"augmented {type(st.op).__name__} is not supported")
+            cur = self.expr(st.target, local)
+            local[st.target.id] = self.arith(ops[type(st.op)], cur, self.expr(st.value, local))
+            return True
+        return False
+
+
+_UNREADABLE = object()  # the loop counter inside the loop
+
+
+_BUILTINS = {"abs": abs, "max": max, "min": min, "float": float}
+
+
+def _assigned_names(stmts):
+    out = []
+    for st in stmts:
+        if isinstance(st, ast.Assign):
+            for t in st.targets:
+                for e in (t.elts if isinstance(t, ast.Tuple) else [t]):
+                    if isinstance(e, ast.Name) and e.id not in out:
+                        out.append(e.id)
+        elif isinstance(st, ast.AugAssign) and isinstance(st.target, ast.Name) and st.target.id not in out:
+            out.append(st.target.id)
+    return out
+
+
+def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
+    """Lowers one @ti.kernel struct-for body to a per-pixel program (vernondsl_amd.pixprog)."""
+    from . import pixprog as pp
+    body = [s for s in fdef.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant))]
+    if len(body) != 1 or not isinstance(body[0], ast.For):
+        raise TaichiLoweringError("the kernel body must be one struct-for `for i, j in field:`")
+    loop = body[0]
+    if not (isinstance(loop.target, ast.Tuple) and len(loop.target.elts) == 2):
+        raise TaichiLoweringError("the struct-for must bind two indices (a 2-D field)")
+    iname, jname = (e.id for e in loop.target.elts)
+    b = pp.Builder()
+    it0 = _PixInterp(env, funcs, b, None, iname, jname)
+    fld = it0.expr(loop.iter, {})
+    if not isinstance(fld, Field) or len(fld.shape) != 2:
+        raise TaichiLoweringError("the struct-for must iterate a 2-D ti.field")
+    ip = _PixInterp(env, funcs, b, fld, iname, jname)
+    local = {iname: b.index(0), jname: b.index(1)}
+    stmts = [s for s in loop.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant)) and not isinstance(s, ast.Pass)]
+    init, test, new_state, max_iter, has_loop, out = {}, None, {}, 0, False, None
+    k = 0
+    while k < len(stmts):
+        st = stmts[k]
+        k += 1
+        if ip.assign(st, local):
+            continue
+        if isinstance(st, (ast.While, ast.For)):
+            if has_loop:
+                raise TaichiLoweringError("at most one loop per struct-for body")
+            has_loop = True
+            init, test, new_state, max_iter = _lower_loop(st, ip, local, b)
+            continue
+        if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Subscript):
+            tgt = st.targets[0]
+            if ip.expr(tgt.value, local) is not fld:
+                raise TaichiLoweringError("the store must write the iterated field")
+            idx = tgt.slice
+            if not (isinstance(idx, ast.Tuple) and [getattr(e, "id", None) for e in idx.elts] == [iname, jname]):
+                raise TaichiLoweringError("the store must write field[i, j]")
+            if out is not None or k != len(stmts):
+                raise TaichiLoweringError("the store field[i, j] = ... must be the last statement")
+            v = ip.expr(st.value, local)
+            if isinstance(v, _PVec):
+                raise TaichiLoweringError("a field of scalars stores a scalar")
+            if fld.dtype == i32:
+                if not (isinstance(v, pp.Node) and v.kind == "count"):
+                    raise TaichiLoweringError("an i32 field stores the loop counter")
+                out = pp.COUNT
+            else:
+                out = v if isinstance(v, pp.Node) else float(_f32(v))
+            continue
+        raise TaichiLoweringError(f"statement at line {getattr(st, 'lineno', '?')} is not supported")
+    if out is None:
+        raise TaichiLoweringError("the struct-for body must end with a store field[i, j] = ...")
+    try:
+        prog = pp.compile_program(b, init=init, test=test, body=new_state, max_iter=max_iter, out=out, loop=has_loop)
+    except pp.ProgramError as e:
+        raise TaichiLoweringError(str(e)) from None
+    return Lowered("pixel_program", fld, program=prog, inputs=ip.inputs)
+
+
+def _lower_loop(st, ip: _PixInterp, local: dict, b):
+    """One loop of the body: (initial states, test, new states, max_iter); rebinds `local` to the
+    values after the loop (states, and the counter as the loop's count)."""
+    from . import pixprog as pp
+    counter = None
+    if isinstance(st, ast.For):
+        it = st.iter
+        if not (isinstance(it, ast.Call) and isinstance(it.func, ast.Name) and it.func.id == "range" and len(it.args) == 1):
+            raise TaichiLoweringError("the inner loop must be `for _ in range(N)` or a while loop")
+        max_iter = ip.expr(it.args[0], local)
+        if not isinstance(max_iter, (int, np.integer)) or max_iter < 0:
+            raise TaichiLoweringError("range(N) needs a non-negative integer constant N")
+        loop_var = st.target.id if isinstance(st.target, ast.Name) else None
+        loop_body = list(st.body)
+        test = None
+    else:
+        tests = st.test.values if isinstance(st.test, ast.BoolOp) and isinstance(st.test.op, ast.And) else [st.test]
+        loop_body = list(st.body)
+        inc = loop_body[-1] if loop_body else None
+        if not (isinstance(inc, ast.AugAssign) and isinstance(inc.op, ast.Add) and isinstance(inc.target, ast.Name)
+                and isinstance(inc.value, ast.Constant) and inc.value.value == 1):
+            raise TaichiLoweringError("a while loop must end with `counter += 1`")
+        counter = inc.target.id
+        if not (counter in local and _is_num(local[counter]) and isinstance(local[counter], (int, np.integer))
+                and int(local[counter]) == 0):
+            raise TaichiLoweringError("the loop counter must start at 0")
+        loop_body = loop_body[:-1]
+        max_iter, test_cmp = None, []
+        for t in tests:
+            if not (isinstance(t, ast.Compare) and len(t.ops) == 1):
+                raise TaichiLoweringError("each while test must be one comparison")
+            if isinstance(t.left, ast.Name) and t.left.id == counter:
+                if not isinstance(t.ops[0], (ast.Lt, ast.LtE)):
+                    raise TaichiLoweringError("the counter test must be `counter < MAX` or `counter <= MAX`")
+                m = ip.expr(t.comparators[0], local)
+                if not isinstance(m, (int, np.integer)):
+                    raise TaichiLoweringError("the counter bound must be an integer constant")
+                max_iter = int(m) + (1 if isinstance(t.ops[0], ast.LtE) else 0)
+            else:
+                test_cmp.append(t)
+        if max_iter is None:
+            raise TaichiLoweringError("the while condition needs a bound `counter < MAX`")
+        if len(test_cmp) > 1:
+            raise TaichiLoweringError("at most one test besides the counter bound")
+        test = test_cmp[0] if test_cmp else None
+        loop_var = None
+        max_iter = max(0, max_iter)
+    # loop-carried state: names assigned in the body that exist before the loop
+    assigned = _assigned_names(loop_body)
+    state = [nm for nm in assigned if nm in local and nm != counter]
+    init, names = {}, {}
+    body_local = dict(local)
+    if counter is not None:
+        body_local[counter] = _UNREADABLE
+    if loop_var is not None:
+        body_local[loop_var] = _UNREADABLE
+    for nm in state:
+        v = local[nm]
+        if isinstance(v, _PVec):
+            comps = []
+            for c, cv in enumerate(v.comps):
+                key = f"{nm}.{c}"
+                init[key] = cv if isinstance(cv, pp.Node) else _f32(cv)
+                comps.append(b.state(key))
+            names[nm] = (len(v.comps),)
+            body_local[nm] = _PVec(comps)
+        elif _is_num(v) or isinstance(v, pp.Node):
+            init[nm] = v if isinstance(v, pp.Node) else _f32(v)
+            names[nm] = ()
+            body_local[nm] = b.state(nm)
+        else:
+            raise TaichiLoweringError(f"loop state {nm!r} must be a number or a vector")
+    for nm in assigned:
+        if nm not in state and nm != counter:
+            body_local.pop(nm, None)  # defined inside the loop: read before assignment is an error
+    test_out = None
+    if test is not None:
+        ops = {ast.Lt: "lt", ast.LtE: "le", ast.Gt: "gt", ast.GtE: "ge"}
+        if type(test.ops[0]) not in ops:
+            raise TaichiLoweringError("the loop test must be <, <=, > or >=")
+        lhs, rhs = ip.expr(test.left, body_local), ip.expr(test.comparators[0], body_local)
+        if isinstance(lhs, _PVec) or isinstance(rhs, _PVec):
+            raise TaichiLoweringError("the loop test compares scalars")
+        test_out = (ops[type(test.ops[0])], lhs, rhs)
+    for s2 in loop_body:
+        if not ip.assign(s2, body_local):
+            raise TaichiLoweringError(f"statement at line {getattr(s2, 'lineno', '?')} in the loop is not supported")
+    new_state = {}
+    for nm, shape in names.items():
+        v = body_local[nm]
+        if shape:
+            if not (isinstance(v, _PVec) and len(v.comps) == shape[0]):
+                raise TaichiLoweringError(f"loop state {nm!r} changes its vector length")
+            for c, cv in enumerate(v.comps):
+                new_state[f"{nm}.{c}"] = cv
+        else:
+            if isinstance(v, _PVec):
+                raise TaichiLoweringError(f"loop state {nm!r} changes from a scalar to a vector")
+            new_state[nm] = v
+    # after the loop: states hold their final values, the counter the loop's count
+    for nm, shape in names.items():
+        local[nm] = _PVec([b.state(f"{nm}.{c}") for c in range(shape[0])]) if shape else b.state(nm)
+    if counter is not None:
+        local[counter] = b.count()
+    for nm in assigned:
+        if nm not in state and nm != counter:
+            local.pop(nm, None)
+    return init, test_out, new_state, max_iter
