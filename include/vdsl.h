@@ -297,7 +297,13 @@ typedef enum vdsl_pix_opcode {
   VDSL_PIX_INDEX = 32,  /* r[dst] = float(i) (a = 0, the outer axis) or float(j) (a = 1) */
   VDSL_PIX_COS = 33,    /* cosf(r[a]) */
   VDSL_PIX_SIN = 34,    /* sinf(r[a]) */
-  VDSL_PIX_COUNT = 35   /* r[dst] = float(count of loop updates); post section only */
+  VDSL_PIX_COUNT = 35,  /* r[dst] = float(count of loop updates); post section only */
+  VDSL_PIX_LT = 36,     /* r[dst] = r[a] < r[b] ? 1 : 0 (a NaN operand gives 0) */
+  VDSL_PIX_LE = 37,     /* r[a] <= r[b] ? 1 : 0 */
+  VDSL_PIX_EQ = 38,     /* r[a] == r[b] ? 1 : 0 */
+  VDSL_PIX_NE = 39,     /* r[a] != r[b] ? 1 : 0 (a NaN operand gives 1) */
+  VDSL_PIX_SELECT = 40, /* r[a] != 0 ? r[b] : r[c] (NaN counts as true) */
+  VDSL_PIX_FLOOR = 41   /* floorf(r[a]) */
 } vdsl_pix_opcode;
 
 typedef enum vdsl_pix_test {

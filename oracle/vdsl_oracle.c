@@ -20,10 +20,11 @@
  *   orc_pixel_program_rows
  *                        the general form of fractal.py:16-25 (a struct-for body with its check-
  *                        then-update loop).  Pinned by independent numpy restatements of whole
- *                        programs (Mandelbrot / Burning Ship / cubic maps, plain per-pixel
- *                        expressions, field reads), by equality with orc_escape_time on the
- *                        programs both express, and by closed forms (a loop with no test runs
- *                        max_iter times; identity programs copy their input).
+ *                        programs (Mandelbrot / Burning Ship / logistic maps, plain per-pixel
+ *                        expressions, field reads, if / else and compound loop tests), by
+ *                        equality with orc_escape_time on the programs both express, by closed
+ *                        forms (a loop with no test runs max_iter times), and the comparison,
+ *                        select and floor opcodes by numpy on every pair of special values.
  *   orc_map_chain_v_rows vector operands (the vec2-4 / extract_component / swizzle vocabulary of
  *                        source/README.md:23-55).  Pinned by permutation closed forms: a swizzle
  *                        program equals numpy fancy indexing of the components, swizzles compose
@@ -187,6 +188,12 @@ static float pix_apply(const vdsl_map_instr* s, const float* reg, const float* c
     case VDSL_PIX_COUNT: return (float)count;
     case VDSL_PIX_COS: return cosf(reg[s->a]);
     case VDSL_PIX_SIN: return sinf(reg[s->a]);
+    case VDSL_PIX_LT: return reg[s->a] < reg[s->b] ? 1.0f : 0.0f;
+    case VDSL_PIX_LE: return reg[s->a] <= reg[s->b] ? 1.0f : 0.0f;
+    case VDSL_PIX_EQ: return reg[s->a] == reg[s->b] ? 1.0f : 0.0f;
+    case VDSL_PIX_NE: return reg[s->a] != reg[s->b] ? 1.0f : 0.0f;
+    case VDSL_PIX_SELECT: return reg[s->a] != 0.0f ? reg[s->b] : reg[s->c];
+    case VDSL_PIX_FLOOR: return floorf(reg[s->a]);
     default: return map_apply(s->op, reg[s->a], reg[s->b], reg[s->c], s->imm);
   }
 }

@@ -260,3 +260,68 @@ def test_interference_example_frames(dev, q):
     ref = oracle.pixel_program(low.program, 768, 768, [mask]).astype(np.float64)
     # the mask's exp (relative REL) and the two sines (4e-7 each), scaled by 0.25 * |amp| <= 0.5
     assert np.max(np.abs(img.astype(np.float64) - ref)) <= 0.5 * REL + 2e-7 + 1e-7
+
+
+SPECIALS = np.array([0.0, -0.0, 1.0, -1.0, 0.5, -0.5, 2.5, -2.5, 1e-40, -1e-40, 3.4e38, -3.4e38, np.inf, -np.inf, np.nan,
+                     7.0, -7.25, 123456.75, -0.1], np.float32)
+
+
+def test_compare_select_floor_opcodes_bit_exact(dev, q):
+    n = len(SPECIALS)
+    a = np.ascontiguousarray(np.repeat(SPECIALS[:, None], n, axis=1))
+    c = np.ascontiguousarray(np.repeat(SPECIALS[None, :], n, axis=0))
+    b = pp.Builder()
+    la, lc = b.load(0), b.load(1)
+    for node in (b.op("lt", la, lc), b.op("le", la, lc), b.op("eq", la, lc), b.op("ne", la, lc),
+                 b.op("select", la, lc, b.op("neg", lc)), b.op("floor", la),
+                 b.op("select", b.op("lt", la, lc), b.op("floor", lc), b.op("max", la, lc))):
+        prog = pp.compile_program(b, out=node)
+        got = run_prog(dev, q, prog, [a, c], n, n)
+        ref = oracle.pixel_program(prog, n, n, [a, c])
+        if "max" in pp.describe(prog):  # max / min: equal values (the sign of a zero result may differ)
+            assert np.array_equal(got, ref, equal_nan=True), pp.describe(prog)
+        else:
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), pp.describe(prog)
+
+
+BOUNCE = '''
+import taichi as ti
+n = 40
+f = ti.field(dtype=float, shape=(300, 129))
+
+@ti.kernel
+def k():
+    for i, j in f:
+        x = i / n
+        y = j / n
+        k = 0
+        while k < 100 and x * x + y * y < 4.0 and abs(x - y) < 1.5:
+            if x > y:
+                x = x * x - y + 0.1
+            else:
+                x, y = y * 0.9, x * 1.1 - 0.3
+            k += 1
+        f[i, j] = k + x
+'''
+
+
+def test_compound_test_and_if_in_the_loop_bit_exact(dev, q):
+    low = tc.lower_source_kernel(BOUNCE, "k", {})
+    got = run_prog(dev, q, low.program, [], 300, 129)
+    assert np.array_equal(got, oracle.pixel_program(low.program, 300, 129))
+
+
+def test_tiles_example_frames_bit_exact(dev, q):
+    path = os.path.join(EX, "tiles.py")
+    res, img = run_program(path, 4)
+    assert res["frames"] == 4 and img.shape == (640, 640) and img.dtype == np.float32
+    text = open(path).read()
+    fade = tc.lower_source_kernel(text, "fade", {}).program
+    trail = np.zeros((640, 640), np.float32)  # fields start zeroed
+    t = 0.0
+    for _ in range(4):
+        canvas = oracle.pixel_program(tc.lower_source_kernel(text, "paint", {"t": t}).program, 640, 640)
+        trail = oracle.pixel_program(fade, 640, 640, [canvas, trail])
+        t += 0.25
+    assert np.array_equal(img, trail)
+    assert len(np.unique(img)) > 4

@@ -161,9 +161,12 @@ def k():
 @pytest.mark.parametrize("body,msg", [
     ("        k = 0\n        while k < 10:\n            k += 1\n            k += 1\n        f[i, j] = k", "counter|loop"),
     ("        x = 0.0\n        k = 0\n        while k < 10:\n            x = x + k\n            k += 1\n        f[i, j] = x", "counter"),
-    ("        f[i, j] = 1.0\n        x = 2.0", "last statement"),
+    ("        f[i, j] = 1.0\n        for _ in range(3):\n            x = 2.0", "after the loop"),
     ("        x = 0.0\n        for _ in range(3):\n            for _ in range(2):\n                x = x + 1.0\n        f[i, j] = x", "statement"),
-    ("        f[i, j] = i % 3", "Mod"),
+    ("        x = 0.0\n        for _ in range(3):\n            f[i, j] = x", "store inside the loop"),
+    ("        f[i, j] = i << 3", "LShift"),
+    ("        if i > j:\n            y = 1.0\n        f[i, j] = y", "one branch"),
+    ("        x = 1.0", "must store"),
 ])
 def test_rejected_general_bodies(body, msg):
     text = "import taichi as ti\nf = ti.field(dtype=float, shape=(8, 8))\n@ti.kernel\ndef k():\n    for i, j in f:\n" + body + "\n"
@@ -183,3 +186,106 @@ def test_register_pressure_is_reported():
         wide = b.op("add", wide, b.op("mul", vals[k], vals[(k + 7) % 20]))
     with pytest.raises(pp.ProgramError, match="registers|instructions"):
         pp.compile_program(b, out=wide)
+
+
+def grid(ni, nj):
+    i = np.arange(ni, dtype=np.float32)[:, None] * np.ones((1, nj), np.float32)
+    j = np.ones((ni, 1), np.float32) * np.arange(nj, dtype=np.float32)[None, :]
+    return i, j
+
+
+def body_kernel(body, shape=(40, 56), extra=""):
+    return ("import taichi as ti\nn = 40\nf = ti.field(dtype=float, shape=" + repr(shape) + ")\n" + extra +
+            "@ti.kernel\ndef k():\n    for i, j in f:\n" + body + "\n")
+
+
+def test_if_else_store_with_floor_division_and_mod():
+    body = ("        if (i // 8 + j // 8) % 2 == 0:\n            f[i, j] = 1.0\n"
+            "        else:\n            f[i, j] = 0.25")
+    low = tc.lower_source_kernel(body_kernel(body), "k", {})
+    got = oracle.pixel_program(low.program, 40, 56)
+    i, j = grid(40, 56)
+    ref = np.where(((np.floor(i / f32(8)) + np.floor(j / f32(8))) % 2) == 0, f32(1.0), f32(0.25))
+    assert np.array_equal(got, ref) and set(np.unique(got)) == {0.25, 1.0}
+
+
+def test_store_in_one_branch_keeps_the_field():
+    body = "        if i < j:\n            f[i, j] = f[i, j] * 2.0 + 1.0"
+    low = tc.lower_source_kernel(body_kernel(body), "k", {})
+    assert [fl.shape for fl in low.inputs] == [(40, 56)] and low.inputs[0] is low.field
+    g = np.random.default_rng(2).standard_normal((40, 56)).astype(np.float32)
+    got = oracle.pixel_program(low.program, 40, 56, [g])
+    i, j = grid(40, 56)
+    assert np.array_equal(got, np.where(i < j, g * f32(2.0) + f32(1.0), g))
+
+
+def test_conditions_select_and_reading_back_a_store():
+    body = ("        v = i * 0.1 - j * 0.05\n"
+            "        w = ti.select(v > 0.0 and not (i % 3 == 0), v, -v * 0.5)\n"
+            "        f[i, j] = w if (w < 1.5 or j > 40) else 1.5\n"
+            "        f[i, j] = f[i, j] + (1.0 if i == j else 0.0)")
+    low = tc.lower_source_kernel(body_kernel(body), "k", {})
+    assert low.inputs == []
+    got = oracle.pixel_program(low.program, 40, 56)
+    i, j = grid(40, 56)
+    v = i * f32(0.1) - j * f32(0.05)
+    w = np.where((v > 0) & ~((i - np.floor(i / f32(3)) * f32(3)) == 0), v, (-v) * f32(0.5))
+    st = np.where((w < f32(1.5)) | (j > 40), w, f32(1.5))
+    assert np.array_equal(got, st + np.where(i == j, f32(1.0), f32(0.0)))
+
+
+BOUNCE = '''
+        x = i / n
+        y = j / n
+        k = 0
+        while k < 100 and x * x + y * y < 4.0 and abs(x - y) < 1.5:
+            if x > y:
+                x = x * x - y + 0.1
+            else:
+                x, y = y * 0.9, x * 1.1 - 0.3
+            k += 1
+        f[i, j] = k + x'''
+
+
+def test_compound_loop_test_and_if_inside_the_loop():
+    low = tc.lower_source_kernel(body_kernel(BOUNCE), "k", {})
+    p = low.program
+    assert p.loop and p.test == pp.TESTS["gt"] and p.max_iter == 100
+    got = oracle.pixel_program(p, 40, 56)
+    i, j = grid(40, 56)
+    x, y = i / f32(40), j / f32(40)
+    cnt = np.zeros_like(x)
+    live = np.ones(x.shape, bool)
+    for _ in range(100):
+        live &= ((x * x + y * y) < f32(4.0)) & (np.abs(x - y) < f32(1.5))
+        nx = np.where(x > y, (x * x - y) + f32(0.1), y * f32(0.9))
+        ny = np.where(x > y, y, x * f32(1.1) - f32(0.3))
+        x, y = np.where(live, nx, x), np.where(live, ny, y)
+        cnt += live
+    assert np.array_equal(got, cnt.astype(np.float32) + x)
+    assert 0 < cnt.min() < cnt.max() <= 100
+
+
+SPECIALS = np.array([0.0, -0.0, 1.0, -1.0, 0.5, -0.5, 2.5, -2.5, 1e-40, -1e-40, 3.4e38, -3.4e38, np.inf, -np.inf, np.nan,
+                     7.0, -7.25, 123456.75, -0.1], np.float32)
+
+
+def test_compare_select_floor_opcodes_against_numpy():
+    """The new opcodes on every pair of special values (signed zeros, subnormals, infinities,
+    NaN): comparisons as IEEE predicates, select on `!= 0` (NaN true, -0 false), floor as np.floor."""
+    n = len(SPECIALS)
+    a = np.repeat(SPECIALS[:, None], n, axis=1)
+    c = np.repeat(SPECIALS[None, :], n, axis=0)
+    b = pp.Builder()
+    la, lc = b.load(0), b.load(1)
+    cases = {"lt": a < c, "le": a <= c, "eq": a == c, "ne": a != c}
+    for kind, want in cases.items():
+        prog = pp.compile_program(b, out=b.op(kind, la, lc))
+        assert np.array_equal(oracle.pixel_program(prog, n, n, [a, c]), want.astype(np.float32)), kind
+    prog = pp.compile_program(b, out=b.op("select", la, lc, b.op("neg", lc)))
+    sel = oracle.pixel_program(prog, n, n, [a, c])
+    want = np.where(a != 0, c, -c)
+    assert np.array_equal(sel.view(np.uint32), want.view(np.uint32))
+    prog = pp.compile_program(b, out=b.op("floor", la))
+    fl = oracle.pixel_program(prog, n, n, [a, c])
+    assert np.array_equal(fl.view(np.uint32), np.floor(a).view(np.uint32))

@@ -48,6 +48,18 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
     r[s.dst] = cosf(r[s.a]);
   } else if constexpr (s.op == VDSL_PIX_SIN) {
     r[s.dst] = sinf(r[s.a]);
+  } else if constexpr (s.op == VDSL_PIX_LT) {
+    r[s.dst] = r[s.a] < r[s.b] ? 1.0f : 0.0f;
+  } else if constexpr (s.op == VDSL_PIX_LE) {
+    r[s.dst] = r[s.a] <= r[s.b] ? 1.0f : 0.0f;
+  } else if constexpr (s.op == VDSL_PIX_EQ) {
+    r[s.dst] = r[s.a] == r[s.b] ? 1.0f : 0.0f;
+  } else if constexpr (s.op == VDSL_PIX_NE) {
+    r[s.dst] = r[s.a] != r[s.b] ? 1.0f : 0.0f;
+  } else if constexpr (s.op == VDSL_PIX_SELECT) {
+    r[s.dst] = r[s.a] != 0.0f ? r[s.b] : r[s.c];
+  } else if constexpr (s.op == VDSL_PIX_FLOOR) {
+    r[s.dst] = floorf(r[s.a]);
   } else {
     r[s.dst] = apply_op(s.op, r[s.a], r[s.b], r[s.c], rt.imm[PC]);
   }
@@ -73,8 +85,9 @@ __device__ constexpr uint32_t pix_reads(const vdsl_map_instr& s) {
   switch (s.op) {
     case VDSL_MAP_LOAD: case VDSL_MAP_CONST: case VDSL_PIX_INDEX: case VDSL_PIX_COUNT: return 0u;
     case VDSL_MAP_ADD: case VDSL_MAP_SUB: case VDSL_MAP_MUL: case VDSL_MAP_DIV: case VDSL_MAP_MAX: case VDSL_MAP_MIN:
+    case VDSL_PIX_LT: case VDSL_PIX_LE: case VDSL_PIX_EQ: case VDSL_PIX_NE:
       return (1u << s.a) | (1u << s.b);
-    case VDSL_MAP_FMA: return (1u << s.a) | (1u << s.b) | (1u << s.c);
+    case VDSL_MAP_FMA: case VDSL_PIX_SELECT: return (1u << s.a) | (1u << s.b) | (1u << s.c);
     default: return 1u << s.a;
   }
 }

@@ -25,13 +25,15 @@ from . import _lib
 
 MAX_INSTR, MAX_REGS, MAX_INPUTS = 64, 16, 4
 OP = dict(_lib.MAP_OPS)
-OP.update({"index": 32, "cos": 33, "sin": 34, "count": 35})
+OP.update({"index": 32, "cos": 33, "sin": 34, "count": 35, "lt": 36, "le": 37, "eq": 38, "ne": 39, "select": 40,
+           "floor": 41})
 TESTS = {"none": 0, "lt": 1, "le": 2, "gt": 3, "ge": 4}
 OUT_REG, OUT_COUNT = 0, 1
 COUNT = "count"  # compile_program(out=COUNT): store the loop's update count (an int32 field)
 
-UNARY = ("neg", "abs", "sqrt", "exp", "log", "tanh", "sigmoid", "cos", "sin", "recip", "square")
-BINARY = ("add", "sub", "mul", "div", "max", "min")
+UNARY = ("neg", "abs", "sqrt", "exp", "log", "tanh", "sigmoid", "cos", "sin", "recip", "square", "floor")
+BINARY = ("add", "sub", "mul", "div", "max", "min", "lt", "le", "eq", "ne")  # comparisons give 1.0 / 0.0
+TERNARY = ("fma", "select")  # select(c, a, b): a where c != 0 (NaN included), else b
 
 
 class PixelProgram(C.Structure):
@@ -104,8 +106,8 @@ class Builder:
             assert len(args) == 1, kind
         elif kind in BINARY:
             assert len(args) == 2, kind
-        elif kind == "fma":
-            assert len(args) == 3
+        elif kind in TERNARY:
+            assert len(args) == 3, kind
         else:
             raise ProgramError(f"unknown operation {kind!r}")
         return self._node(kind, args)
@@ -204,8 +206,8 @@ class _Emitter:
             op, a = OP[k], srcs[0]
         elif k in BINARY:
             op, a, b = OP[k], srcs[0], srcs[1]
-        elif k == "fma":
-            op, a, b, c = OP["fma"], srcs[0], srcs[1], srcs[2]
+        elif k in TERNARY:
+            op, a, b, c = OP[k], srcs[0], srcs[1], srcs[2]
         else:
             raise ProgramError(f"cannot emit {k!r}")
         if len(self.code) >= MAX_INSTR:

@@ -85,7 +85,8 @@ def _device():
 
 
 class Field:
-    """A dense 2-D field (fractal.py:8).  Storage is a device tensor, allocated on first use."""
+    """A dense 2-D field (fractal.py:8).  Storage is a device tensor, allocated and zeroed on first
+    use."""
 
     def __init__(self, dtype, shape):
         if dtype in (float, f32, None):
@@ -102,8 +103,10 @@ class Field:
     def tensor(self):
         if self._tensor is None:
             from .rhi import Tensor
-            dev, _ = _device()
-            self._tensor = Tensor(dev, self.shape, self.dtype)
+            dev, q = _device()
+            t = Tensor(dev, self.shape, self.dtype)
+            t.buffer.fill_u32(q, 0)  # a Taichi field starts zeroed
+            self._tensor = t
         return self._tensor
 
     def to_numpy(self):
@@ -668,7 +671,9 @@ class _PVec:
         self.comps = list(comps)
 
 
-_UNARY_FUNCS = {"sqrt": "sqrt", "exp": "exp", "log": "log", "sin": "sin", "cos": "cos", "tanh": "tanh", "abs": "abs"}
+_UNARY_FUNCS = {"sqrt": "sqrt", "exp": "exp", "log": "log", "sin": "sin", "cos": "cos", "tanh": "tanh", "abs": "abs",
+                "floor": "floor"}
+_STORE = "__store__"  # the value the body stores to the iterated field at [i, j]
 
 
 class _PixInterp:
@@ -681,6 +686,8 @@ class _PixInterp:
         self.env, self.funcs, self.b = env, funcs, b
         self.fld, self.iname, self.jname = fld, iname, jname
         self.inputs = []  # Fields read at [i, j], in LOAD order
+        self.bools = set()  # ids of Nodes known to hold 1.0 / 0.0 (comparisons and their logic)
+        self.in_loop = False
 
     # -- values
     def node(self, v):
@@ -718,7 +725,7 @@ class _PixInterp:
             v = np.float32(x)
             with np.errstate(all="ignore"):
                 return {"neg": -v, "abs": np.abs(v), "sqrt": np.sqrt(v), "exp": np.exp(v), "log": np.log(v), "sin": np.sin(v),
-                        "cos": np.cos(v), "tanh": np.tanh(v)}[fn]
+                        "cos": np.cos(v), "tanh": np.tanh(v), "floor": np.floor(v)}[fn]
         return self.b.op(fn, x)
 
     def dot(self, a, c):
@@ -740,26 +747,40 @@ class _PixInterp:
                 v = local[n.id]
                 if v is _UNREADABLE:
                     raise TaichiLoweringError(f"{n.id!r} can only be read after the loop (the loop counter)")
+                if v is _ONE_BRANCH:
+                    raise TaichiLoweringError(f"{n.id!r} is assigned in one branch of an if only")
                 return v
             if n.id in self.env:
                 return self.env[n.id]
             raise TaichiLoweringError(f"unknown name {n.id!r}")
         if isinstance(n, ast.BinOp):
             ops = {ast.Add: "add", ast.Sub: "sub", ast.Mult: "mul", ast.Div: "div", ast.Pow: "pow"}
+            x, y = self.expr(n.left, local), self.expr(n.right, local)
+            if isinstance(n.op, (ast.Mod, ast.FloorDiv)):
+                return self.floor_op(type(n.op) is ast.Mod, x, y)
             if type(n.op) not in ops:
                 raise TaichiLoweringError(f"operator {type(n.op).__name__} is not supported")
-            return self.arith(ops[type(n.op)], self.expr(n.left, local), self.expr(n.right, local))
+            return self.arith(ops[type(n.op)], x, y)
         if isinstance(n, ast.UnaryOp):
             v = self.expr(n.operand, local)
             if isinstance(n.op, ast.USub):
                 return self.unary("neg", v)
             if isinstance(n.op, ast.UAdd):
                 return v
+            if isinstance(n.op, ast.Not):
+                return self.logic_not(v)
             raise TaichiLoweringError(f"unary {type(n.op).__name__} is not supported")
+        if isinstance(n, ast.Compare):
+            return self.compare(n, local)
+        if isinstance(n, ast.BoolOp):
+            vals = [self.expr(v, local) for v in n.values]
+            return self.logic("and" if isinstance(n.op, ast.And) else "or", vals)
+        if isinstance(n, ast.IfExp):
+            return self.select(self.expr(n.test, local), self.expr(n.body, local), self.expr(n.orelse, local))
         if isinstance(n, ast.Subscript):
             base = self.expr(n.value, local)
             if isinstance(base, Field):
-                return self.field_read(base, n.slice)
+                return self.field_read(base, n.slice, local)
             idx = self.expr(n.slice, local)
             if isinstance(base, _PVec) and isinstance(idx, (int, np.integer)) and -len(base.comps) <= idx < len(base.comps):
                 return base.comps[int(idx)]
@@ -780,9 +801,11 @@ class _PixInterp:
             return self.call(n, local)
         raise TaichiLoweringError(f"expression {ast.dump(n)[:60]} is not supported")
 
-    def field_read(self, fld, idx):
+    def field_read(self, fld, idx, local):
         if not (isinstance(idx, ast.Tuple) and [getattr(e, "id", None) for e in idx.elts] == [self.iname, self.jname]):
             raise TaichiLoweringError("fields are read at [i, j] of the struct-for only")
+        if fld is self.fld and _STORE in local:
+            return local[_STORE]  # the value this pixel stored earlier in the body
         if fld.shape != self.fld.shape or fld.dtype != f32:
             raise TaichiLoweringError("a field read must be an f32 field of the iterated field's shape")
         if fld not in self.inputs:
@@ -810,6 +833,12 @@ class _PixInterp:
                 return _PVec(comps)
             if f.attr in _UNARY_FUNCS:
                 return self.unary(_UNARY_FUNCS[f.attr], self.expr(n.args[0], local))
+            if f.attr == "select":
+                if len(n.args) != 3:
+                    raise TaichiLoweringError("ti.select takes (condition, if_true, if_false)")
+                return self.select(*[self.expr(a, local) for a in n.args])
+            if f.attr == "ceil":
+                return self.unary("neg", self.unary("floor", self.unary("neg", self.expr(n.args[0], local))))
             if f.attr in ("max", "min"):
                 return self.minmax(f.attr, [self.expr(a, local) for a in n.args])
             raise TaichiLoweringError(f"call {f.attr!r} is not supported")
@@ -850,8 +879,146 @@ class _PixInterp:
                 acc = self.b.op(which, self.node(acc), self.node(v))
         return acc
 
+    # -- conditions: comparisons give 1.0 / 0.0; a value is true where it is not 0 (NaN is true)
+    def _bool(self, n):
+        self.bools.add(id(n))
+        return n
+
+    def truth(self, v):
+        if isinstance(v, _PVec):
+            raise TaichiLoweringError("a vector is not a condition")
+        if _is_num(v):
+            return 1 if _f32(v) != 0 else 0
+        if id(v) in self.bools:
+            return v
+        return self._bool(self.b.op("ne", v, 0.0))
+
+    def compare(self, n, local):
+        ops = {ast.Lt: ("lt", False), ast.LtE: ("le", False), ast.Gt: ("lt", True), ast.GtE: ("le", True),
+               ast.Eq: ("eq", False), ast.NotEq: ("ne", False)}
+        terms, left = [], self.expr(n.left, local)
+        for op, rhs_n in zip(n.ops, n.comparators):
+            if type(op) not in ops:
+                raise TaichiLoweringError(f"comparison {type(op).__name__} is not supported")
+            right = self.expr(rhs_n, local)
+            if isinstance(left, _PVec) or isinstance(right, _PVec):
+                raise TaichiLoweringError("comparisons are of scalars")
+            kind, swap = ops[type(op)]
+            a, c = (right, left) if swap else (left, right)
+            if _is_num(a) and _is_num(c):
+                fa, fc = _f32(a), _f32(c)
+                terms.append(int({"lt": fa < fc, "le": fa <= fc, "eq": fa == fc, "ne": fa != fc}[kind]))
+            else:
+                terms.append(self._bool(self.b.op(kind, self.node(a), self.node(c))))
+            left = right
+        return self.logic("and", terms)
+
+    def logic(self, which, vals):
+        acc = self.truth(vals[0])
+        for v in vals[1:]:
+            t = self.truth(v)
+            if _is_num(acc) and _is_num(t):
+                acc = (acc and t) if which == "and" else (acc or t)
+            elif _is_num(acc) or _is_num(t):
+                k, other = (acc, t) if _is_num(acc) else (t, acc)
+                if which == "and":
+                    acc = other if k else 0
+                else:
+                    acc = 1 if k else other
+            else:
+                acc = self._bool(self.b.op("mul" if which == "and" else "max", acc, t))
+        return acc
+
+    def logic_not(self, v):
+        t = self.truth(v)
+        if _is_num(t):
+            return 1 - t
+        return self._bool(self.b.op("eq", t, 0.0))
+
+    def select(self, c, x, y):
+        if isinstance(x, _PVec) or isinstance(y, _PVec):
+            if not (isinstance(x, _PVec) and isinstance(y, _PVec) and len(x.comps) == len(y.comps)):
+                raise TaichiLoweringError("a conditional picks between two vectors of one length or two scalars")
+            return _PVec([self.select(c, a, d) for a, d in zip(x.comps, y.comps)])
+        if isinstance(c, _PVec):
+            raise TaichiLoweringError("a vector is not a condition")
+        if _is_num(c):
+            return x if _f32(c) != 0 else y
+        if x is y or (_is_num(x) and _is_num(y) and _f32(x).tobytes() == _f32(y).tobytes()):
+            return x
+        r = self.b.op("select", c, self.node(x), self.node(y))
+        if id(self.node(x)) in self.bools and id(self.node(y)) in self.bools:
+            self.bools.add(id(r))
+        return r
+
+    def floor_op(self, mod, x, y):
+        """x % y (floored, the sign of y) and x // y, as x - floor(x / y) * y and floor(x / y)."""
+        if isinstance(x, _PVec) or isinstance(y, _PVec):
+            raise TaichiLoweringError("% and // are of scalars")
+        if isinstance(x, (int, np.integer)) and isinstance(y, (int, np.integer)) and not isinstance(x, bool):
+            if y == 0:
+                raise TaichiLoweringError("integer division by zero")
+            return x % y if mod else x // y
+        q = self.unary("floor", self.arith("div", x, y))
+        return self.arith("sub", x, self.arith("mul", q, y)) if mod else q
+
     # -- statements
+    def if_stmt(self, st, local):
+        """Both branches are evaluated; each name either assigns afterwards takes the branch's value
+        by a select on the condition (a store in one branch only keeps the field's value in the
+        other)."""
+        c = self.expr(st.test, local)
+        if isinstance(c, _PVec):
+            raise TaichiLoweringError("a vector is not a condition")
+        if _is_num(c):  # a condition known when the kernel is lowered
+            for s2 in (st.body if _f32(c) != 0 else st.orelse):
+                if not self.assign(s2, local):
+                    raise TaichiLoweringError(f"statement at line {getattr(s2, 'lineno', '?')} is not supported")
+            return
+        branches = []
+        for stmts in (st.body, st.orelse):
+            loc = dict(local)
+            for s2 in stmts:
+                if not self.assign(s2, loc):
+                    raise TaichiLoweringError(f"statement at line {getattr(s2, 'lineno', '?')} in an if is not supported")
+            branches.append(loc)
+        lt, lf = branches
+        for nm in list(dict.fromkeys(list(lt) + list(lf))):
+            vt, vf = lt.get(nm, _ONE_BRANCH), lf.get(nm, _ONE_BRANCH)
+            if vt is vf:
+                local[nm] = vt
+                continue
+            if nm == _STORE:  # the field keeps its value where a branch does not store
+                keep = local.get(_STORE)
+                if keep is None:
+                    if self.fld.dtype != f32:
+                        raise TaichiLoweringError("an i32 field must be stored on every path")
+                    keep = self.field_read(self.fld, ast.Tuple(elts=[ast.Name(id=self.iname), ast.Name(id=self.jname)]), {})
+                vt = keep if vt is _ONE_BRANCH else vt
+                vf = keep if vf is _ONE_BRANCH else vf
+            elif vt is _ONE_BRANCH or vf is _ONE_BRANCH or vt is _UNREADABLE or vf is _UNREADABLE:
+                local[nm] = _ONE_BRANCH
+                continue
+            local[nm] = self.select(c, vt, vf)
+
     def assign(self, st, local):
+        if isinstance(st, ast.If):
+            self.if_stmt(st, local)
+            return True
+        if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Subscript):
+            tgt = st.targets[0]
+            if self.expr(tgt.value, local) is not self.fld:
+                raise TaichiLoweringError("the body may only store to the iterated field")
+            idx = tgt.slice
+            if not (isinstance(idx, ast.Tuple) and [getattr(e, "id", None) for e in idx.elts] == [self.iname, self.jname]):
+                raise TaichiLoweringError("the store must write field[i, j]")
+            if self.in_loop:
+                raise TaichiLoweringError("a store inside the loop is not supported (store after it)")
+            v = self.expr(st.value, local)
+            if isinstance(v, _PVec):
+                raise TaichiLoweringError("a field of scalars stores a scalar")
+            local[_STORE] = v
+            return True
         if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Name):
             local[st.targets[0].id] = self.expr(st.value, local)
             return True
@@ -877,6 +1044,7 @@ class _PixInterp:
 
 
 _UNREADABLE = object()  # the loop counter inside the loop
+_ONE_BRANCH = object()  # a name an if statement assigns in one branch only
 
 
 _BUILTINS = {"abs": abs, "max": max, "min": min, "float": float}
@@ -885,7 +1053,11 @@ _BUILTINS = {"abs": abs, "max": max, "min": min, "float": float}
 def _assigned_names(stmts):
     out = []
     for st in stmts:
-        if isinstance(st, ast.Assign):
+        if isinstance(st, ast.If):
+            for nm in _assigned_names(st.body) + _assigned_names(st.orelse):
+                if nm not in out:
+                    out.append(nm)
+        elif isinstance(st, ast.Assign):
             for t in st.targets:
                 for e in (t.elts if isinstance(t, ast.Tuple) else [t]):
                     if isinstance(e, ast.Name) and e.id not in out:
@@ -913,41 +1085,28 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
     ip = _PixInterp(env, funcs, b, fld, iname, jname)
     local = {iname: b.index(0), jname: b.index(1)}
     stmts = [s for s in loop.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant)) and not isinstance(s, ast.Pass)]
-    init, test, new_state, max_iter, has_loop, out = {}, None, {}, 0, False, None
-    k = 0
-    while k < len(stmts):
-        st = stmts[k]
-        k += 1
-        if ip.assign(st, local):
-            continue
+    init, test, new_state, max_iter, has_loop = {}, None, {}, 0, False
+    for st in stmts:
         if isinstance(st, (ast.While, ast.For)):
             if has_loop:
                 raise TaichiLoweringError("at most one loop per struct-for body")
+            if _STORE in local:
+                raise TaichiLoweringError("the store field[i, j] = ... must come after the loop")
             has_loop = True
             init, test, new_state, max_iter = _lower_loop(st, ip, local, b)
             continue
-        if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Subscript):
-            tgt = st.targets[0]
-            if ip.expr(tgt.value, local) is not fld:
-                raise TaichiLoweringError("the store must write the iterated field")
-            idx = tgt.slice
-            if not (isinstance(idx, ast.Tuple) and [getattr(e, "id", None) for e in idx.elts] == [iname, jname]):
-                raise TaichiLoweringError("the store must write field[i, j]")
-            if out is not None or k != len(stmts):
-                raise TaichiLoweringError("the store field[i, j] = ... must be the last statement")
-            v = ip.expr(st.value, local)
-            if isinstance(v, _PVec):
-                raise TaichiLoweringError("a field of scalars stores a scalar")
-            if fld.dtype == i32:
-                if not (isinstance(v, pp.Node) and v.kind == "count"):
-                    raise TaichiLoweringError("an i32 field stores the loop counter")
-                out = pp.COUNT
-            else:
-                out = v if isinstance(v, pp.Node) else float(_f32(v))
+        if ip.assign(st, local):
             continue
         raise TaichiLoweringError(f"statement at line {getattr(st, 'lineno', '?')} is not supported")
-    if out is None:
-        raise TaichiLoweringError("the struct-for body must end with a store field[i, j] = ...")
+    if _STORE not in local:
+        raise TaichiLoweringError("the struct-for body must store field[i, j] = ...")
+    v = local[_STORE]
+    if fld.dtype == i32:
+        if not (isinstance(v, pp.Node) and v.kind == "count"):
+            raise TaichiLoweringError("an i32 field stores the loop counter")
+        out = pp.COUNT
+    else:
+        out = v if isinstance(v, pp.Node) else float(_f32(v))
     try:
         prog = pp.compile_program(b, init=init, test=test, body=new_state, max_iter=max_iter, out=out, loop=has_loop)
     except pp.ProgramError as e:
@@ -984,9 +1143,7 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
         loop_body = loop_body[:-1]
         max_iter, test_cmp = None, []
         for t in tests:
-            if not (isinstance(t, ast.Compare) and len(t.ops) == 1):
-                raise TaichiLoweringError("each while test must be one comparison")
-            if isinstance(t.left, ast.Name) and t.left.id == counter:
+            if isinstance(t, ast.Compare) and len(t.ops) == 1 and isinstance(t.left, ast.Name) and t.left.id == counter:
                 if not isinstance(t.ops[0], (ast.Lt, ast.LtE)):
                     raise TaichiLoweringError("the counter test must be `counter < MAX` or `counter <= MAX`")
                 m = ip.expr(t.comparators[0], local)
@@ -997,9 +1154,7 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
                 test_cmp.append(t)
         if max_iter is None:
             raise TaichiLoweringError("the while condition needs a bound `counter < MAX`")
-        if len(test_cmp) > 1:
-            raise TaichiLoweringError("at most one test besides the counter bound")
-        test = test_cmp[0] if test_cmp else None
+        test = test_cmp or None
         loop_var = None
         max_iter = max(0, max_iter)
     # loop-carried state: names assigned in the body that exist before the loop
@@ -1033,15 +1188,22 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
     test_out = None
     if test is not None:
         ops = {ast.Lt: "lt", ast.LtE: "le", ast.Gt: "gt", ast.GtE: "ge"}
-        if type(test.ops[0]) not in ops:
-            raise TaichiLoweringError("the loop test must be <, <=, > or >=")
-        lhs, rhs = ip.expr(test.left, body_local), ip.expr(test.comparators[0], body_local)
-        if isinstance(lhs, _PVec) or isinstance(rhs, _PVec):
-            raise TaichiLoweringError("the loop test compares scalars")
-        test_out = (ops[type(test.ops[0])], lhs, rhs)
-    for s2 in loop_body:
-        if not ip.assign(s2, body_local):
-            raise TaichiLoweringError(f"statement at line {getattr(s2, 'lineno', '?')} in the loop is not supported")
+        one = test[0]
+        if len(test) == 1 and isinstance(one, ast.Compare) and len(one.ops) == 1 and type(one.ops[0]) in ops:
+            lhs, rhs = ip.expr(one.left, body_local), ip.expr(one.comparators[0], body_local)
+            if isinstance(lhs, _PVec) or isinstance(rhs, _PVec):
+                raise TaichiLoweringError("the loop test compares scalars")
+            test_out = (ops[type(one.ops[0])], lhs, rhs)
+        else:  # any other condition: its truth value (1 / 0) against 0.5
+            t = ip.logic("and", [ip.expr(e, body_local) for e in test])
+            test_out = ("gt", t, 0.5)
+    ip.in_loop = True
+    try:
+        for s2 in loop_body:
+            if not ip.assign(s2, body_local):
+                raise TaichiLoweringError(f"statement at line {getattr(s2, 'lineno', '?')} in the loop is not supported")
+    finally:
+        ip.in_loop = False
     new_state = {}
     for nm, shape in names.items():
         v = body_local[nm]
