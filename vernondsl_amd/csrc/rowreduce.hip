@@ -4,12 +4,14 @@
 //   row_sum = sum_j x[j] accumulated in f64, rounded once to f32;
 //   row_max = max_j x[j] (exact);
 //   softmax[j] = e[j] / s,  e[j] = exp(x[j] - row_max) in f32,  s = f64 sum of e rounded to f32.
-// (The register-resident kernel evaluates exp with the branch-free exp_fast of common.h, within
-// a few ulp of the library expf that the generic kernel and the oracle use.)
-// The register-resident kernel multiplies by 1/s instead of dividing (within one ulp of e/s) and
-// forms its sums as f32 partials of 4 or 8 elements added into f64 accumulators; both stay far
-// inside the op's 1e-5 (f32) / 1e-2 (bf16) tolerances and cut the VALU work per element, which
-// bounds the bf16 kernel.
+// (The register-resident kernels evaluate exp with the branch-free exp_fast of fmath.h, in its
+// form for arguments <= 0, within a few ulp of the library expf that the generic kernel and the
+// oracle use.)
+// The register-resident kernels multiply by 1/s instead of dividing (within one ulp of e/s) and
+// form their sums as f32 partials of 4 or 8 elements added into f64 accumulators (f32 rows) or,
+// for bf16 rows, as f32 sums across the wave (DPP) added in f64 across waves: sums within a few
+// ulp of the f64 accumulation, far inside the op's 1e-5 (f32) / 1e-2 (bf16) tolerances, for less
+// VALU work per element, which bounds the bf16 kernels.
 //
 // Mapping: one 64-lane wavefront owns one row and keeps it in VGPRs, so x is read from HBM once
 // and softmax written once (the HBM roofline's minimum traffic).  Lane l holds the 16-byte
@@ -27,6 +29,55 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
   return v;
+}
+
+// Wave reductions through DPP (no LDS round trip): a butterfly inside each row of 16 lanes
+// (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then the four rows' values read
+// as scalars and combined.  Every lane gets the result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_lane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  v += dpp_f32<0x141>(v);
+  v += dpp_f32<0x140>(v);
+  return (row_lane(v, 0) + row_lane(v, 16)) + (row_lane(v, 32) + row_lane(v, 48));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  return fmaxf(fmaxf(row_lane(v, 0), row_lane(v, 16)), fmaxf(row_lane(v, 32), row_lane(v, 48)));
+}
+
+// exp_fast for n <= 0 (softmax's x - max): 2^t cannot overflow there, so only a non-finite t
+// (n = -inf or NaN) skips the correction.  The same value as exp_fast for every such n.
+__device__ __forceinline__ float exp_nonpos(float n) {
+  const float t = n * 1.4426950408889634f;
+  float r = __builtin_fmaf(n, 1.4426950408889634f, -t);
+  r = __builtin_fmaf(n, 1.92596299e-08f, r);  // log2(e) - fl(log2(e))
+  const float e = __builtin_amdgcn_exp2f(t);
+  const float c = __builtin_fmaf(e, r * 0.6931471805599453f, e);
+  return __builtin_isfinite(t) ? c : e;
+}
+
+// A wave's partial sum: f64 butterflies for f32 rows; for bf16 rows (outputs with 8 significant
+// bits, bound by VALU work rather than HBM) the lanes' f32 partials meet in f32 through DPP.
+template <int DT>
+__device__ __forceinline__ double wave_partial_sum(float lane_part, double lane_part64) {
+  if constexpr (DT == VDSL_BF16) return static_cast<double>(wave_sum_dpp(lane_part));
+  else return wave_sum_f64(lane_part64);
+}
+template <int DT>
+__device__ __forceinline__ float wave_partial_max(float v) {
+  if constexpr (DT == VDSL_BF16) return wave_max_dpp(v);
+  else return wave_max(v);
 }
 
 template <int DT>
@@ -83,6 +134,7 @@ __global__ __launch_bounds__(256) void row_softmax_resident(const void* __restri
     E::unpack(make_uint4(r[0], r[1], r[2], r[3]), v[k]);
   }
   double s = 0.0;
+  float fs = 0.0f;
   float m = -INFINITY;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
@@ -93,26 +145,29 @@ __global__ __launch_bounds__(256) void row_softmax_resident(const void* __restri
       m = fmaxf(m, v[k][e]);
     }
     s += static_cast<double>(part);
+    fs += part;
   }
-  s = wave_sum_f64(s);
-  m = wave_max(m);
+  s = wave_partial_sum<DT>(fs, s);
+  m = wave_partial_max<DT>(m);
   if (lane == 0) {
     if (row_sum) row_sum[row] = static_cast<float>(s);
     if (row_max) row_max[row] = m;
   }
   if (!sm) return;
   double es = 0.0;
+  float fes = 0.0f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     float part = 0.0f;
 #pragma unroll
     for (int e = 0; e < PV; ++e) {
-      v[k][e] = exp_fast(v[k][e] - m);
+      v[k][e] = exp_nonpos(v[k][e] - m);
       part += v[k][e];
     }
     es += static_cast<double>(part);
+    fes += part;
   }
-  const float inv = 1.0f / static_cast<float>(wave_sum_f64(es));
+  const float inv = 1.0f / static_cast<float>(wave_partial_sum<DT>(fes, es));
   uint4* dst = reinterpret_cast<uint4*>(static_cast<char*>(sm) + row * cols * (DT == VDSL_F32 ? 4 : 2));
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
@@ -151,6 +206,7 @@ __global__ __launch_bounds__(64 * WPR) void row_softmax_split(const void* __rest
     E::unpack(make_uint4(r[0], r[1], r[2], r[3]), v[k]);
   }
   double s = 0.0;
+  float fs = 0.0f;
   float m = -INFINITY;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
@@ -161,9 +217,10 @@ __global__ __launch_bounds__(64 * WPR) void row_softmax_split(const void* __rest
       m = fmaxf(m, v[k][e]);
     }
     s += static_cast<double>(part);
+    fs += part;
   }
-  s = wave_sum_f64(s);
-  m = wave_max(m);
+  s = wave_partial_sum<DT>(fs, s);
+  m = wave_partial_max<DT>(m);
   if (lane == 0) {
     part_sum[wave] = s;
     part_max[wave] = m;
@@ -182,17 +239,19 @@ __global__ __launch_bounds__(64 * WPR) void row_softmax_split(const void* __rest
   }
   if (!sm) return;
   double es = 0.0;
+  float fes = 0.0f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     float part = 0.0f;
 #pragma unroll
     for (int e = 0; e < PV; ++e) {
-      v[k][e] = exp_fast(v[k][e] - m);
+      v[k][e] = exp_nonpos(v[k][e] - m);
       part += v[k][e];
     }
     es += static_cast<double>(part);
+    fes += part;
   }
-  es = wave_sum_f64(es);
+  es = wave_partial_sum<DT>(fes, es);
   __syncthreads();  // every wave has read part_sum
   if (lane == 0) part_sum[wave] = es;
   __syncthreads();
@@ -274,14 +333,22 @@ __global__ __launch_bounds__(256) void col_reduce_kernel(const void* __restrict_
 template <int DT>
 int launch_rows(const void* x, float* rs, float* rm, void* sm, int64_t rows, int64_t cols, hipStream_t st) {
   constexpr int PV = Elem<DT>::kPerVec;
-  // Rows of 8, 16 or 32 vectors per 64 lanes: one block per row, 4 waves of 2 vectors per lane
-  // or 8 waves of 2 or 4.
+  // Rows of 8, 16 or 32 vectors per 64 lanes: one block per row.  f32: 4 waves of 2 vectors per
+  // lane or 8 waves of 2 or 4; bf16 (VALU-bound): 4 vectors per lane in 2, 4 or 8 waves, which
+  // halves the reductions per element at 4096 columns (42.9 us against 45.7 for 2 vectors in 4
+  // waves on [16384][4096], with the DPP reductions).
   if (cols == 64 * 8 * PV || cols == 64 * 16 * PV || cols == 64 * 32 * PV) {
     if (rows > 0x7fffffff) return fail(VDSL_ERR_UNSUPPORTED, "too many rows");
     const dim3 g(static_cast<unsigned>(rows));
-    if (cols == 64 * 8 * PV) hipLaunchKernelGGL((row_softmax_split<DT, 2, 4>), g, dim3(256), 0, st, x, rs, rm, sm, rows);
-    else if (cols == 64 * 16 * PV) hipLaunchKernelGGL((row_softmax_split<DT, 2, 8>), g, dim3(512), 0, st, x, rs, rm, sm, rows);
-    else hipLaunchKernelGGL((row_softmax_split<DT, 4, 8>), g, dim3(512), 0, st, x, rs, rm, sm, rows);
+    if constexpr (DT == VDSL_BF16) {
+      if (cols == 64 * 8 * PV) hipLaunchKernelGGL((row_softmax_split<DT, 4, 2>), g, dim3(128), 0, st, x, rs, rm, sm, rows);
+      else if (cols == 64 * 16 * PV) hipLaunchKernelGGL((row_softmax_split<DT, 4, 4>), g, dim3(256), 0, st, x, rs, rm, sm, rows);
+      else hipLaunchKernelGGL((row_softmax_split<DT, 4, 8>), g, dim3(512), 0, st, x, rs, rm, sm, rows);
+    } else {
+      if (cols == 64 * 8 * PV) hipLaunchKernelGGL((row_softmax_split<DT, 2, 4>), g, dim3(256), 0, st, x, rs, rm, sm, rows);
+      else if (cols == 64 * 16 * PV) hipLaunchKernelGGL((row_softmax_split<DT, 2, 8>), g, dim3(512), 0, st, x, rs, rm, sm, rows);
+      else hipLaunchKernelGGL((row_softmax_split<DT, 4, 8>), g, dim3(512), 0, st, x, rs, rm, sm, rows);
+    }
     return check_launch("row_softmax_split");
   }
   const int64_t blocks = (rows + 3) / 4;
