@@ -31,6 +31,8 @@ void orc_gelu_fwd(int64_t n, int x_dtype, const void* x, int y_dtype, void* y);
 void orc_gelu_bwd(int64_t rows, int64_t cols, const float* dh, const float* pre, uint16_t* da, uint16_t* da_t);
 void orc_mse_fwd_bwd(int64_t rows, int64_t cols, const float* y, const float* t, float* loss, uint16_t* dy, uint16_t* dy_t);
 void orc_quantize_rows_i8(int64_t rows, int64_t cols, int x_dtype, const void* x, int8_t* q, float* scale);
+void orc_pixel_program_rows(const vdsl_pixel_program* p, int64_t ni, int64_t nj, const float* const* inputs, void* out,
+                            int64_t r0, int64_t r1);
 void orc_gemm_w8a8_rows(int64_t M, int64_t N, int64_t K, const int8_t* xq, const float* xs, const int8_t* w, const float* ws,
                         void* y, int out_dtype, int relu, int32_t* acc_out, int64_t m0, int64_t m1);
 
@@ -197,8 +199,53 @@ static void elementwise(void) {
   }
 }
 
+/* Per-pixel programs: an escape loop over two input fields with a count and state read after the
+ * loop, every pixel-only opcode, ragged and empty grids, a loop of no trips. */
+static void pixel_programs(void) {
+  static const vdsl_map_instr code[] = {
+      /* pre: r2 = in0, r3 = in1, r4 = 4, r0 = i / 16, r1 = j / 16 */
+      {VDSL_MAP_LOAD, 2, 0, 0, 0, {0}, 0.f}, {VDSL_MAP_LOAD, 3, 1, 0, 0, {0}, 0.f}, {VDSL_MAP_CONST, 4, 0, 0, 0, {0}, 4.f},
+      {VDSL_PIX_INDEX, 0, 0, 0, 0, {0}, 0.f}, {VDSL_MAP_MUL_IMM, 0, 0, 0, 0, {0}, 0.0625f},
+      {VDSL_PIX_INDEX, 1, 1, 0, 0, {0}, 0.f}, {VDSL_MAP_MUL_IMM, 1, 1, 0, 0, {0}, 0.0625f},
+      /* test: r5 = r0^2 + r1^2 < r4 */
+      {VDSL_MAP_SQUARE, 5, 0, 0, 0, {0}, 0.f}, {VDSL_MAP_SQUARE, 6, 1, 0, 0, {0}, 0.f}, {VDSL_MAP_ADD, 5, 5, 6, 0, {0}, 0.f},
+      /* body: (r0, r1) <- (r0^2 - r1^2 + r2, 2 r0 r1 + r3), through selects and floors */
+      {VDSL_MAP_SQUARE, 6, 0, 0, 0, {0}, 0.f}, {VDSL_MAP_SQUARE, 7, 1, 0, 0, {0}, 0.f}, {VDSL_MAP_SUB, 6, 6, 7, 0, {0}, 0.f},
+      {VDSL_MAP_ADD, 6, 6, 2, 0, {0}, 0.f}, {VDSL_MAP_MUL, 7, 0, 1, 0, {0}, 0.f}, {VDSL_MAP_MUL_IMM, 7, 7, 0, 0, {0}, 2.f},
+      {VDSL_MAP_ADD, 7, 7, 3, 0, {0}, 0.f}, {VDSL_PIX_LT, 8, 6, 7, 0, {0}, 0.f},
+      {VDSL_PIX_SELECT, 9, 8, 6, 7, {0}, 0.f}, {VDSL_PIX_FLOOR, 10, 9, 0, 0, {0}, 0.f},
+      {VDSL_MAP_MOV, 0, 6, 0, 0, {0}, 0.f}, {VDSL_MAP_MOV, 1, 7, 0, 0, {0}, 0.f},
+      /* post: r11 = count + cos(r0) + sin(r1) + (r0 == r1) + (r0 != r1) + (r0 <= r1) + r10 */
+      {VDSL_PIX_COUNT, 11, 0, 0, 0, {0}, 0.f}, {VDSL_PIX_COS, 12, 0, 0, 0, {0}, 0.f}, {VDSL_MAP_ADD, 11, 11, 12, 0, {0}, 0.f},
+      {VDSL_PIX_SIN, 12, 1, 0, 0, {0}, 0.f}, {VDSL_MAP_ADD, 11, 11, 12, 0, {0}, 0.f},
+      {VDSL_PIX_EQ, 12, 0, 1, 0, {0}, 0.f}, {VDSL_MAP_ADD, 11, 11, 12, 0, {0}, 0.f},
+      {VDSL_PIX_NE, 12, 0, 1, 0, {0}, 0.f}, {VDSL_MAP_ADD, 11, 11, 12, 0, {0}, 0.f},
+      {VDSL_PIX_LE, 12, 0, 1, 0, {0}, 0.f}, {VDSL_MAP_ADD, 11, 11, 12, 0, {0}, 0.f}, {VDSL_MAP_ADD, 11, 11, 10, 0, {0}, 0.f},
+  };
+  vdsl_pixel_program p;
+  memset(&p, 0, sizeof p);
+  p.n_pre = 7; p.n_test = 3; p.n_body = 12; p.n_post = (int)(sizeof code / sizeof code[0]) - 22;
+  p.loop = 1; p.test = VDSL_PIX_TEST_LT; p.test_a = 5; p.test_b = 4; p.out_reg = 11;
+  memcpy(p.code, code, sizeof code);
+  const int shapes[][2] = {{1, 1}, {7, 13}, {0, 5}, {5, 0}, {33, 17}};
+  for (int s = 0; s < 5; ++s) {
+    const int64_t ni = shapes[s][0], nj = shapes[s][1];
+    for (int variant = 0; variant < 3; ++variant) {
+      p.max_iter = variant == 0 ? 0 : 30;
+      p.out_kind = variant == 2 ? VDSL_PIX_OUT_COUNT : VDSL_PIX_OUT_REG;
+      float* in0 = buf((size_t)(ni * nj) * 4, 1);
+      float* in1 = buf((size_t)(ni * nj) * 4, 1);
+      const float* ins[2] = {in0, in1};
+      void* out = buf((size_t)(ni * nj) * 4, 0);
+      orc_pixel_program_rows(&p, ni, nj, ins, out, 0, ni);
+      free(in0); free(in1); free(out);
+    }
+  }
+}
+
 int main(void) {
   escape_time();
+  pixel_programs();
   map_chains();
   vec_transform();
   reductions();

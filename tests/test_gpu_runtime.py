@@ -280,6 +280,18 @@ def test_allocation_failure_injection_leaves_nothing_behind(dev):
     b.free()
 
 
+def test_real_allocation_failure_does_not_fail_the_next_launch(dev, q):
+    """A hipMalloc that fails leaves HIP's per-thread last error set; the library clears it, so the
+    next op's launch check does not report that failure against its own kernel."""
+    with pytest.raises(VdslError) as ei:
+        Buffer(dev, 1 << 62)
+    assert ei.value.status == OOM
+    t = Tensor.from_numpy(dev, q, np.arange(64, dtype=np.float32))
+    t.buffer.fill_u32(q, 0x3F800000)  # a kernel launch right after the failure
+    assert np.all(t.numpy(q) == 1.0)
+    t.free()
+
+
 def test_capture_misuse_is_rejected_and_capture_survives(dev):
     q2 = Queue(dev)
     buf = Buffer(dev, 1024)

@@ -70,6 +70,9 @@ int fail(int status, const std::string& msg) {
 
 int check_hip(hipError_t e, const char* what) {
   if (e == hipSuccess) return VDSL_OK;
+  // The error is reported here; clear HIP's per-thread last error, or the next launch check
+  // would report it again against an unrelated kernel.
+  (void)hipGetLastError();
   int st = (e == hipErrorOutOfMemory) ? VDSL_ERR_OUT_OF_MEMORY : VDSL_ERR_DEVICE;
   return fail(st, std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")");
 }
@@ -86,6 +89,9 @@ bool valid_queue(vdsl_queue q) { return q && reg_has(q) && q->magic == kMagicQue
 
 int enter_queue(vdsl_queue q) {
   if (!valid_queue(q)) return fail(VDSL_ERR_INVALID_HANDLE, "invalid queue handle");
+  // A launch check reads HIP's per-thread last error: drop one left by a call whose failure was
+  // ignored or reported earlier, so an op's launch check sees its own launches only.
+  (void)hipGetLastError();
   return check_hip(hipSetDevice(q->dev->ordinal), "hipSetDevice");
 }
 
