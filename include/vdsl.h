@@ -281,9 +281,10 @@ int vdsl_op_map_chain_v(vdsl_queue q, int64_t rows, int64_t cols, const vdsl_map
  *        r[test_a] <test> r[test_b] holds (VDSL_PIX_TEST_NONE: always holds) and fewer than
  *        max_iter updates were made; run the body section; count one update; repeat;
  *   post (the last n_post instructions): the stored value, which may read the count.
- * out[i][j] = r[out_reg] (an f32 field) or the count (VDSL_PIX_OUT_COUNT: an int32 field).
+ * out[i][j][k] = r[out_regs[k]] for k < out_width (an f32 field of scalars or vec2-4) or the
+ * count (VDSL_PIX_OUT_COUNT: an int32 field of scalars).
  * Instructions are vdsl_map_instr with the map-chain opcodes (VDSL_MAP_LOAD: a = input field,
- * read at [i][j]) plus the ones below; every operation rounds once, in f32, where it is written
+ * c = component, read at [i][j]) plus the ones below; every operation rounds once, in f32, where it is written
  * (an fma only for VDSL_MAP_FMA).  Compiled at run time for each program (once per device): a
  * program first seen while a queue records a graph is refused, so run it once before
  * recording.  No counterpart in the reference beyond the program surface it runs; the caller is
@@ -312,8 +313,8 @@ typedef enum vdsl_pix_test {
 } vdsl_pix_test;
 
 typedef enum vdsl_pix_output {
-  VDSL_PIX_OUT_REG = 0,    /* f32 field: r[out_reg] */
-  VDSL_PIX_OUT_COUNT = 1   /* int32 field: the count of loop updates */
+  VDSL_PIX_OUT_REG = 0,    /* f32 field: r[out_regs[k]], k < out_width */
+  VDSL_PIX_OUT_COUNT = 1   /* int32 field: the count of loop updates (out_width 1) */
 } vdsl_pix_output;
 
 typedef struct vdsl_pixel_program {
@@ -323,13 +324,15 @@ typedef struct vdsl_pixel_program {
   int32_t test;                            /* vdsl_pix_test */
   int32_t test_a, test_b;                  /* registers compared by the test */
   int32_t out_kind;                        /* vdsl_pix_output */
-  int32_t out_reg;
-  int32_t pad;
+  int32_t out_width;                       /* components stored per pixel, 1..4 (ti.Vector.field) */
+  int32_t out_regs[4];                     /* their registers, in component order */
+  int32_t in_widths[VDSL_PIX_MAX_INPUTS];  /* components per pixel of input k, 1..4 */
   vdsl_map_instr code[VDSL_PIX_MAX_INSTR];
 } vdsl_pixel_program;
 
-/* Runs `prog` for every pixel of an [ni][nj] grid.  inputs: f32 [ni][nj] fields (n_inputs <= 4);
- * out: f32 (VDSL_PIX_OUT_REG) or int32 (VDSL_PIX_OUT_COUNT) [ni][nj]. */
+/* Runs `prog` for every pixel of an [ni][nj] grid.  inputs: f32 [ni][nj][in_widths[k]] fields
+ * (n_inputs <= 4); out: f32 [ni][nj][out_width] (VDSL_PIX_OUT_REG) or int32 [ni][nj]
+ * (VDSL_PIX_OUT_COUNT). */
 int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const vdsl_pixel_program* prog,
                           const vdsl_buffer* inputs, int32_t n_inputs, vdsl_buffer out);
 

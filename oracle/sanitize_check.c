@@ -203,8 +203,8 @@ static void elementwise(void) {
  * loop, every pixel-only opcode, ragged and empty grids, a loop of no trips. */
 static void pixel_programs(void) {
   static const vdsl_map_instr code[] = {
-      /* pre: r2 = in0, r3 = in1, r4 = 4, r0 = i / 16, r1 = j / 16 */
-      {VDSL_MAP_LOAD, 2, 0, 0, 0, {0}, 0.f}, {VDSL_MAP_LOAD, 3, 1, 0, 0, {0}, 0.f}, {VDSL_MAP_CONST, 4, 0, 0, 0, {0}, 4.f},
+      /* pre: r2 = in0 (component 1 of 2), r3 = in1, r4 = 4, r0 = i / 16, r1 = j / 16 */
+      {VDSL_MAP_LOAD, 2, 0, 0, 1, {0}, 0.f}, {VDSL_MAP_LOAD, 3, 1, 0, 0, {0}, 0.f}, {VDSL_MAP_CONST, 4, 0, 0, 0, {0}, 4.f},
       {VDSL_PIX_INDEX, 0, 0, 0, 0, {0}, 0.f}, {VDSL_MAP_MUL_IMM, 0, 0, 0, 0, {0}, 0.0625f},
       {VDSL_PIX_INDEX, 1, 1, 0, 0, {0}, 0.f}, {VDSL_MAP_MUL_IMM, 1, 1, 0, 0, {0}, 0.0625f},
       /* test: r5 = r0^2 + r1^2 < r4 */
@@ -225,7 +225,8 @@ static void pixel_programs(void) {
   vdsl_pixel_program p;
   memset(&p, 0, sizeof p);
   p.n_pre = 7; p.n_test = 3; p.n_body = 12; p.n_post = (int)(sizeof code / sizeof code[0]) - 22;
-  p.loop = 1; p.test = VDSL_PIX_TEST_LT; p.test_a = 5; p.test_b = 4; p.out_reg = 11;
+  p.loop = 1; p.test = VDSL_PIX_TEST_LT; p.test_a = 5; p.test_b = 4;
+  p.in_widths[0] = 2; p.in_widths[1] = 1;
   memcpy(p.code, code, sizeof code);
   const int shapes[][2] = {{1, 1}, {7, 13}, {0, 5}, {5, 0}, {33, 17}};
   for (int s = 0; s < 5; ++s) {
@@ -233,10 +234,12 @@ static void pixel_programs(void) {
     for (int variant = 0; variant < 3; ++variant) {
       p.max_iter = variant == 0 ? 0 : 30;
       p.out_kind = variant == 2 ? VDSL_PIX_OUT_COUNT : VDSL_PIX_OUT_REG;
-      float* in0 = buf((size_t)(ni * nj) * 4, 1);
+      p.out_width = variant == 1 ? 3 : 1; /* a vec3 field, or scalars */
+      p.out_regs[0] = 11; p.out_regs[1] = 0; p.out_regs[2] = 1;
+      float* in0 = buf((size_t)(ni * nj) * 8, 1);
       float* in1 = buf((size_t)(ni * nj) * 4, 1);
       const float* ins[2] = {in0, in1};
-      void* out = buf((size_t)(ni * nj) * 4, 0);
+      void* out = buf((size_t)(ni * nj) * 4 * p.out_width, 0);
       orc_pixel_program_rows(&p, ni, nj, ins, out, 0, ni);
       free(in0); free(in1); free(out);
     }

@@ -180,10 +180,10 @@ static float map_apply(int op, float a, float b, float c, float imm) {
 
 /* ---- general per-pixel programs (vdsl_pixel_program) -------------------------------------- */
 
-static float pix_apply(const vdsl_map_instr* s, const float* reg, const float* const* inputs, int64_t o, int64_t i,
-                       int64_t j, int count) {
+static float pix_apply(const vdsl_pixel_program* p, const vdsl_map_instr* s, const float* reg, const float* const* inputs,
+                       int64_t o, int64_t i, int64_t j, int count) {
   switch (s->op) {
-    case VDSL_MAP_LOAD: return inputs[s->a][o];
+    case VDSL_MAP_LOAD: return inputs[s->a][o * p->in_widths[s->a] + s->c];
     case VDSL_PIX_INDEX: return s->a == 0 ? (float)i : (float)j;
     case VDSL_PIX_COUNT: return (float)count;
     case VDSL_PIX_COS: return cosf(reg[s->a]);
@@ -210,8 +210,9 @@ static int pix_test(int test, float a, float b) {
 
 /* Rows [r0, r1) of vdsl_op_pixel_program: per pixel, 16 registers at 0, the pre section, the
  * check-then-update loop (fractal.py:22-24: test, stop unless it holds and fewer than max_iter
- * updates were made, body, count), the post section, then out[i][j] = r[out_reg] (f32) or the
- * count (int32).  The program is taken as validated by the caller. */
+ * updates were made, body, count), the post section, then out[i][j][k] = r[out_regs[k]] (f32,
+ * out_width components) or the count (int32).  A LOAD reads component c of input a's pixel
+ * (in_widths[a] components each).  The program is taken as validated by the caller. */
 void orc_pixel_program_rows(const vdsl_pixel_program* p, int64_t ni, int64_t nj, const float* const* inputs, void* out,
                             int64_t r0, int64_t r1) {
   const int t0 = p->n_pre, b0 = t0 + p->n_test, q0 = b0 + p->n_body, end = q0 + p->n_post;
@@ -223,18 +224,21 @@ void orc_pixel_program_rows(const vdsl_pixel_program* p, int64_t ni, int64_t nj,
       float reg[VDSL_PIX_MAX_REGS];
       for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) reg[k] = 0.0f;
       int count = 0;
-      for (int pc = 0; pc < t0; ++pc) reg[p->code[pc].dst] = pix_apply(&p->code[pc], reg, inputs, o, i, j, 0);
+      for (int pc = 0; pc < t0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, 0);
       if (p->loop) {
         while (count < p->max_iter) {
-          for (int pc = t0; pc < b0; ++pc) reg[p->code[pc].dst] = pix_apply(&p->code[pc], reg, inputs, o, i, j, 0);
+          for (int pc = t0; pc < b0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, 0);
           if (!pix_test(p->test, reg[p->test_a], reg[p->test_b])) break;
-          for (int pc = b0; pc < q0; ++pc) reg[p->code[pc].dst] = pix_apply(&p->code[pc], reg, inputs, o, i, j, 0);
+          for (int pc = b0; pc < q0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, 0);
           ++count;
         }
       }
-      for (int pc = q0; pc < end; ++pc) reg[p->code[pc].dst] = pix_apply(&p->code[pc], reg, inputs, o, i, j, count);
-      if (p->out_kind == VDSL_PIX_OUT_COUNT) ((int32_t*)out)[o - r0 * nj] = count;
-      else ((float*)out)[o - r0 * nj] = reg[p->out_reg];
+      for (int pc = q0; pc < end; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, count);
+      if (p->out_kind == VDSL_PIX_OUT_COUNT) {
+        ((int32_t*)out)[o - r0 * nj] = count;
+      } else {
+        for (int k = 0; k < p->out_width; ++k) ((float*)out)[(o - r0 * nj) * p->out_width + k] = reg[p->out_regs[k]];
+      }
     }
 }
 

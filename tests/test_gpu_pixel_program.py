@@ -23,7 +23,8 @@ EX = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "
 
 def run_prog(dev, q, prog, inputs, ni, nj):
     ts = [Tensor.from_numpy(dev, q, np.ascontiguousarray(a, np.float32)) for a in inputs]
-    out = Tensor(dev, (ni, nj), "i32" if prog.out_kind == pp.OUT_COUNT else "f32")
+    w = 1 if prog.out_kind == pp.OUT_COUNT else prog.out_width
+    out = Tensor(dev, (ni, nj) if w == 1 else (ni, nj, w), "i32" if prog.out_kind == pp.OUT_COUNT else "f32")
     if ni and nj:
         out.buffer.fill_u32(q, 0x7FC00000)  # NaN / a large count: every element must be written
     kernels.pixel_program(q, prog, ts, out)
@@ -85,7 +86,7 @@ def test_test_section_value_read_after_the_loop(dev, q, limit):
     prog = escape_program(limit=limit)
     ts = prog.n_pre
     assert prog.n_test == 3 and prog.code[ts + 2].dst == prog.test_a
-    prog.n_post, prog.out_kind, prog.out_reg = 0, pp.OUT_REG, prog.test_a
+    prog.n_post, prog.out_kind, prog.out_width, prog.out_regs[0] = 0, pp.OUT_REG, 1, prog.test_a
     got = run_prog(dev, q, prog, [], 300, 129)
     ref = oracle.pixel_program(prog, 300, 129)
     assert np.array_equal(got, ref)
@@ -325,3 +326,33 @@ def test_tiles_example_frames_bit_exact(dev, q):
         t += 0.25
     assert np.array_equal(img, trail)
     assert len(np.unique(img)) > 4
+
+
+def test_vector_inputs_and_outputs_bit_exact(dev, q):
+    """Inputs of 2 and 3 components read by component, a vec4 output in chosen component order."""
+    rng = np.random.default_rng(8)
+    a = rng.standard_normal((45, 70, 2)).astype(np.float32)
+    c3 = rng.standard_normal((45, 70, 3)).astype(np.float32)
+    b = pp.Builder()
+    x, y = b.load(0, 0), b.load(0, 1)
+    r, g, bl = b.load(1, 0), b.load(1, 1), b.load(1, 2)
+    outs = [b.op("add", y, bl), x, b.op("mul", r, g), b.op("select", b.op("lt", x, y), r, bl)]
+    prog = pp.compile_program(b, out=outs, in_widths=[2, 3])
+    assert prog.out_width == 4
+    got = run_prog(dev, q, prog, [a, c3], 45, 70)
+    assert got.shape == (45, 70, 4)
+    ref = oracle.pixel_program(prog, 45, 70, [a, c3])
+    assert np.array_equal(got, ref)
+    assert np.array_equal(ref[..., 1], a[..., 0]) and np.array_equal(ref[..., 2], c3[..., 0] * c3[..., 1])
+
+
+def test_palette_example_vector_fields(dev, q):
+    path = os.path.join(EX, "palette.py")
+    res, img = run_program(path, 2)
+    assert res["frames"] == 2 and img.shape == (800, 600, 3) and img.dtype == np.float32
+    text = open(path).read()
+    rgb = oracle.pixel_program(tc.lower_source_kernel(text, "render", {"shift": 0.05}).program, 800, 600)
+    ref = oracle.pixel_program(tc.lower_source_kernel(text, "vignette", {}).program, 800, 600, [rgb])
+    # cosf on the device against the C library's: at most a few ulp of values in [0, 1]
+    assert np.max(np.abs(img.astype(np.float64) - ref)) <= 5e-7
+    assert np.array_equal(img == 0, ref == 0)  # the same pixels reach the limit (black)

@@ -289,3 +289,67 @@ def test_compare_select_floor_opcodes_against_numpy():
     prog = pp.compile_program(b, out=b.op("floor", la))
     fl = oracle.pixel_program(prog, n, n, [a, c])
     assert np.array_equal(fl.view(np.uint32), np.floor(a).view(np.uint32))
+
+
+def palette_numpy(shift, W=800, H=600, limit=120):
+    x, y = grid(W, H)
+    c0 = (x / f32(W)) * f32(3.0) + f32(-1.5)
+    c1 = (y / f32(H)) * f32(2.4) + f32(-1.2)
+    z0 = np.zeros_like(c0)
+    z1 = np.zeros_like(c0)
+    n = np.zeros(c0.shape, np.int32)
+    live = np.ones(c0.shape, bool)
+    for _ in range(limit):
+        live &= (z0 * z0 + z1 * z1) < f32(16.0)
+        re2 = z0 * z0 - z1 * z1
+        im2 = (f32(2.0) * z0) * z1
+        n0 = (z0 * re2 - z1 * im2) + c0
+        n1 = (z0 * im2 + z1 * re2) + c1
+        z0, z1 = np.where(live, n0, z0), np.where(live, n1, z1)
+        n += live
+    t = n.astype(np.float32) / f32(limit) + f32(shift)
+    col = np.stack([f32(0.5) + f32(0.5) * np.cos(f32(6.2831) * (t + f32(o)), dtype=np.float32)
+                    for o in (0.0, 0.33, 0.67)], axis=-1)
+    col[:, :, 0] = f32(0.5) + f32(0.5) * np.cos(f32(6.2831) * t, dtype=np.float32)
+    return np.where((n == limit)[:, :, None], f32(0.0), col), n
+
+
+def test_vector_fields_palette_example_against_numpy():
+    text = ex("palette.py")
+    low = tc.lower_source_kernel(text, "render", {"shift": 0.05})
+    assert low.kind == "pixel_program" and low.field.width == 3 and low.program.out_width == 3
+    img = oracle.pixel_program(low.program, 800, 600, rows=(300, 500))
+    ref, n = palette_numpy(0.05)
+    ref = ref[300:500]
+    assert img.shape == (200, 600, 3)
+    inside = n[300:500] == 120
+    assert inside.any() and (~inside).any()
+    assert np.array_equal(img[inside], ref[inside])                # exact zeros inside the set
+    assert np.max(np.abs(img - ref)) <= 2e-6                       # cosf against numpy's cos
+    vig = tc.lower_source_kernel(text, "vignette", {})
+    assert [f.width for f in vig.inputs] == [3] and list(vig.program.in_widths)[:1] == [3]
+    full = oracle.pixel_program(low.program, 800, 600)
+    sh = oracle.pixel_program(vig.program, 800, 600, [full])
+    x, y = grid(800, 600)
+    d0, d1 = x / f32(800) + f32(-0.5), y / f32(600) + f32(-0.5)
+    k = f32(1.0) - f32(1.2) * (d0 * d0 + d1 * d1)
+    want = np.stack([full[:, :, 0] * k, full[:, :, 1] * k, np.minimum(full[:, :, 2] * k + f32(0.05), f32(1.0))], -1)
+    assert np.array_equal(sh, want)
+
+
+def test_vector_field_stores_and_errors():
+    text = ('import taichi as ti\nv = ti.Vector.field(2, dtype=float, shape=(8, 8))\n'
+            'w = ti.Vector.field(4, dtype=float, shape=(8, 8))\n'
+            '@ti.kernel\ndef fill():\n    for i, j in v:\n        v[i, j] = i * 0.5\n'
+            '@ti.kernel\ndef swap():\n    for i, j in w:\n        a = v[i, j]\n        w[i, j] = [a.y, a.x, a[0] + a[1], 1.0]\n'
+            '@ti.kernel\ndef bad():\n    for i, j in v:\n        v[i, j] = ti.Vector([1.0, 2.0, 3.0])\n')
+    low = tc.lower_source_kernel(text, "fill", {})
+    vv = oracle.pixel_program(low.program, 8, 8)
+    i, _ = grid(8, 8)
+    assert vv.shape == (8, 8, 2) and np.array_equal(vv, np.stack([i * f32(0.5)] * 2, -1))
+    low = tc.lower_source_kernel(text, "swap", {})
+    g = np.random.default_rng(4).standard_normal((8, 8, 2)).astype(np.float32)
+    ww = oracle.pixel_program(low.program, 8, 8, [g])
+    assert np.array_equal(ww, np.stack([g[..., 1], g[..., 0], g[..., 0] + g[..., 1], np.ones((8, 8), np.float32)], -1))
+    with pytest.raises(tc.TaichiLoweringError, match="2-vectors stores 2"):
+        tc.lower_source_kernel(text, "bad", {})

@@ -120,13 +120,19 @@ int main(void) {
 
   vdsl_pixel_program pp;
   memset(&pp, 0, sizeof pp);
-  pp.n_pre = 2; pp.n_post = 1; pp.out_reg = 2;
+  pp.n_pre = 2; pp.n_post = 1; pp.out_width = 1; pp.out_regs[0] = 2;
   pp.code[0].op = VDSL_PIX_INDEX; pp.code[0].dst = 0; pp.code[0].a = 0;
   pp.code[1].op = VDSL_PIX_INDEX; pp.code[1].dst = 1; pp.code[1].a = 1;
   pp.code[2].op = VDSL_PIX_SELECT; pp.code[2].dst = 2; pp.code[2].a = 0; pp.code[2].b = 1; pp.code[2].c = 0;
   EXPECT_OK(vdsl_op_pixel_program(q, 8, 16, &pp, NULL, 0, a));
   EXPECT_ERR(vdsl_op_pixel_program(q, 64, 64, &pp, NULL, 0, a)); /* out too small */
   EXPECT_ERR(vdsl_op_pixel_program(q, 8, 16, &pp, NULL, 5, a));  /* too many inputs */
+  pp.out_width = 5;
+  EXPECT_ERR(vdsl_op_pixel_program(q, 8, 16, &pp, NULL, 0, a));  /* at most 4 components */
+  pp.out_width = 4;
+  EXPECT_OK(vdsl_op_pixel_program(q, 8, 16, &pp, NULL, 0, a));   /* a vec4 field: 2048 bytes */
+  EXPECT_ERR(vdsl_op_pixel_program(q, 32, 16, &pp, NULL, 0, a)); /* 8192 bytes > 4096 */
+  pp.out_width = 1;
   pp.code[2].c = 16;
   EXPECT_ERR(vdsl_op_pixel_program(q, 8, 16, &pp, NULL, 0, a));  /* register out of range */
 

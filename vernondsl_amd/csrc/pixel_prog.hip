@@ -30,7 +30,13 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
     return fail(VDSL_ERR_INVALID_ARG, "pixel program: test register out of range");
   if (p.out_kind != VDSL_PIX_OUT_REG && p.out_kind != VDSL_PIX_OUT_COUNT)
     return fail(VDSL_ERR_INVALID_ARG, "pixel program: unknown out_kind");
-  if (p.out_reg < 0 || p.out_reg >= VDSL_PIX_MAX_REGS) return fail(VDSL_ERR_INVALID_ARG, "pixel program: out_reg out of range");
+  if (p.out_width < 1 || p.out_width > 4 || (p.out_kind == VDSL_PIX_OUT_COUNT && p.out_width != 1))
+    return fail(VDSL_ERR_INVALID_ARG, "pixel program: out_width must be 1..4 (1 for a count)");
+  for (int k = 0; k < p.out_width; ++k)
+    if (p.out_regs[k] < 0 || p.out_regs[k] >= VDSL_PIX_MAX_REGS)
+      return fail(VDSL_ERR_INVALID_ARG, "pixel program: out_regs out of range");
+  for (int k = 0; k < n_inputs; ++k)
+    if (p.in_widths[k] < 1 || p.in_widths[k] > 4) return fail(VDSL_ERR_INVALID_ARG, "pixel program: in_widths must be 1..4");
   if (p.out_kind == VDSL_PIX_OUT_COUNT && !p.loop) return fail(VDSL_ERR_INVALID_ARG, "pixel program: a count needs a loop");
   const int post0 = p.n_pre + p.n_test + p.n_body;
   for (int pc = 0; pc < total; ++pc) {
@@ -42,7 +48,8 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
     if (s.dst >= VDSL_PIX_MAX_REGS || s.b >= VDSL_PIX_MAX_REGS || s.c >= VDSL_PIX_MAX_REGS)
       return fail(VDSL_ERR_INVALID_ARG, at + ": register out of range");
     if (s.op == VDSL_MAP_LOAD) {
-      if (s.a >= n_inputs || s.c != 0) return fail(VDSL_ERR_INVALID_ARG, at + ": LOAD of an input that is not there");
+      if (s.a >= n_inputs || s.c >= p.in_widths[s.a])
+        return fail(VDSL_ERR_INVALID_ARG, at + ": LOAD of an input or component that is not there");
     } else if (s.op == VDSL_PIX_INDEX) {
       if (s.a > 1) return fail(VDSL_ERR_INVALID_ARG, at + ": INDEX axis must be 0 (i) or 1 (j)");
     } else if (s.a >= VDSL_PIX_MAX_REGS) {
@@ -55,7 +62,7 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
 
 // The program's table as C++ source (opcodes and registers; immediates stay kernel arguments).
 // It names the kernel completely, so it is also the cache key.
-std::string program_source(const vdsl_pixel_program& p) {
+std::string program_source(const vdsl_pixel_program& p, int n_inputs) {
   std::string s = "#include \"pixprog_kern.h\"\nnamespace vdsl {\nstruct PixJit {\n";
   auto c = [&](const char* name, int v) { s += std::string("  static constexpr int ") + name + " = " + std::to_string(v) + ";\n"; };
   c("n_pre", p.n_pre);
@@ -67,7 +74,14 @@ std::string program_source(const vdsl_pixel_program& p) {
   c("test_a", p.test_a);
   c("test_b", p.test_b);
   c("out_kind", p.out_kind);
-  c("out_reg", p.out_reg);
+  c("out_width", p.out_width);
+  // Entries past out_width / n_inputs are not used: written as 0 / 1, so they do not split the cache.
+  auto list = [&](const char* name, const int32_t* v, int n, int fill) {
+    s += std::string("  static constexpr int ") + name + "[4] = {";
+    for (int k = 0; k < 4; ++k) s += std::to_string(k < n ? v[k] : fill) + (k < 3 ? ", " : "};\n");
+  };
+  list("out_regs", p.out_regs, p.out_width, 0);
+  list("in_widths", p.in_widths, n_inputs, 1);
   s += "  static constexpr vdsl_map_instr code[VDSL_PIX_MAX_INSTR] = {\n";
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   for (int pc = 0; pc < total; ++pc) {
@@ -95,12 +109,11 @@ extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const
   if (n_inputs && !inputs) return fail(VDSL_ERR_INVALID_ARG, "inputs is null");
   const vdsl_pixel_program& p = *prog;
   VDSL_TRY(check_program(p, n_inputs));
-  const size_t bytes = nbytes(ni, nj, 4);
-  VDSL_TRY(check_buffer(q, out, bytes, "out", true));
+  VDSL_TRY(check_buffer(q, out, nbytes(ni, nj, 4 * p.out_width), "out", true));
   PixIn in{};
   for (int k = 0; k < n_inputs; ++k) {
     const std::string name = "input" + std::to_string(k);
-    VDSL_TRY(check_buffer(q, inputs[k], bytes, name.c_str(), false));
+    VDSL_TRY(check_buffer(q, inputs[k], nbytes(ni, nj, 4 * p.in_widths[k]), name.c_str(), false));
     in.p[k] = static_cast<const float*>(inputs[k]->ptr);
   }
   if (ni == 0 || nj == 0) return VDSL_OK;
@@ -109,7 +122,7 @@ extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   for (int pc = 0; pc < total; ++pc) rt.imm[pc] = p.code[pc].imm;
   rt.max_iter = p.max_iter;
-  const std::string src = program_source(p);
+  const std::string src = program_source(p, n_inputs);
   const char* const entries[] = {"vdsl_pix_jit"};
   const JitKernels* k = nullptr;
   const int st = jit_kernels(q->dev->ordinal, src, entries, 1, q->capturing, g_pix_jit, "pixel program", &k);

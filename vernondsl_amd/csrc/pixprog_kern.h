@@ -39,7 +39,7 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
                                          float fi, float fj, float fcount) {
   constexpr vdsl_map_instr s = P::code[PC];
   if constexpr (s.op == VDSL_MAP_LOAD) {
-    r[s.dst] = in.p[s.a][o];
+    r[s.dst] = in.p[s.a][o * P::in_widths[s.a] + s.c];
   } else if constexpr (s.op == VDSL_PIX_INDEX) {
     r[s.dst] = s.a == 0 ? fi : fj;
   } else if constexpr (s.op == VDSL_PIX_COUNT) {
@@ -113,9 +113,14 @@ struct PixSets {
   static constexpr uint32_t test_w = writes(t0, b0);
   static constexpr uint32_t body_w = writes(b0, q0);
   static constexpr uint32_t loop_w = test_w | body_w;
+  static constexpr uint32_t stored() {
+    uint32_t m = 0u;
+    if (P::out_kind == VDSL_PIX_OUT_REG)
+      for (int k = 0; k < P::out_width; ++k) m |= 1u << P::out_regs[k];
+    return m;
+  }
   // What the post section and the store take from the loop.
-  static constexpr uint32_t post_r =
-      rbw(q0, end) | ((P::out_kind == VDSL_PIX_OUT_REG && !((writes(q0, end) >> P::out_reg) & 1u)) ? (1u << P::out_reg) : 0u);
+  static constexpr uint32_t post_r = rbw(q0, end) | (stored() & ~writes(q0, end));
   static constexpr uint32_t keep_t = test_w & post_r;   // kept from the trip a lane's test failed
   static constexpr uint32_t keep_b = body_w & post_r;   // kept from the lane's last counted trip
   static constexpr bool free_running = (loop_w & post_r) == 0u;
@@ -161,7 +166,7 @@ __device__ __forceinline__ void pix_trip(const PixRt& rt, const PixIn& in, float
 }
 
 // P: the program table (n_pre, n_test, n_body, n_post, loop, test, test_a, test_b, out_kind,
-// out_reg, code[]).  out: f32 or int32 [ni][nj].
+// out_width, out_regs[], in_widths[], code[]).  out: f32 [ni][nj][out_width] or int32 [ni][nj].
 template <class P>
 __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, void* __restrict__ out, int ni, int nj) {
   using S = PixSets<P>;
@@ -232,8 +237,12 @@ __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, voi
   }
   pix_run<P, S::q0, P::n_post>(rt, in, r, o, fi, fj, static_cast<float>(count));
   if (inside) {
-    if constexpr (P::out_kind == VDSL_PIX_OUT_COUNT) static_cast<int*>(out)[o] = count;
-    else static_cast<float*>(out)[o] = r[P::out_reg];
+    if constexpr (P::out_kind == VDSL_PIX_OUT_COUNT) {
+      static_cast<int*>(out)[o] = count;
+    } else {
+#pragma unroll
+      for (int k = 0; k < P::out_width; ++k) static_cast<float*>(out)[o * P::out_width + k] = r[P::out_regs[k]];
+    }
   }
 }
 

@@ -245,15 +245,22 @@ def gemm_bf16_mul_packed(q: Queue, A: Tensor, Bp: Tensor, g: Tensor, c: Tensor, 
 
 def pixel_program(q: Queue, prog, inputs, out: Tensor):
     """Runs a compiled per-pixel program (vernondsl_amd.pixprog.PixelProgram) over out's [ni][nj]
-    grid: out f32 (the program stores a register) or i32 (it stores its loop count); inputs: f32
-    fields of out's shape, read at each pixel."""
-    if len(out.shape) != 2:
-        raise ValueError("out must be a 2-D field")
-    ni, nj = out.shape
-    want = "i32" if prog.out_kind == 1 else "f32"
-    _expect(out, (ni, nj), want, "out")
+    grid: out f32 [ni][nj] or [ni][nj][out_width] (the program stores registers) or i32 [ni][nj]
+    (it stores its loop count); inputs: f32 fields [ni][nj] or [ni][nj][in_widths[k]], read at
+    each pixel."""
+    if len(out.shape) not in (2, 3):
+        raise ValueError("out must be a 2-D field of scalars or vectors")
+    ni, nj = out.shape[:2]
+
+    def field_shape(w):
+        return (ni, nj) if w == 1 else (ni, nj, w)
+
+    if prog.out_kind == 1:
+        _expect(out, (ni, nj), "i32", "out")
+    else:
+        _expect(out, field_shape(prog.out_width), "f32", "out")
     for k, t in enumerate(inputs):
-        _expect(t, (ni, nj), "f32", f"input{k}")
+        _expect(t, field_shape(prog.in_widths[k]), "f32", f"input{k}")
     hs = (C.c_void_p * max(1, len(inputs)))(*[t.handle for t in inputs])
     call("vdsl_op_pixel_program", q.handle, ni, nj, C.byref(prog), hs, len(inputs), out.handle)
 

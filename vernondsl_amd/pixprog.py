@@ -40,8 +40,8 @@ class PixelProgram(C.Structure):
     # Same layout as vdsl_pixel_program (include/vdsl.h).
     _fields_ = [("n_pre", C.c_int32), ("n_test", C.c_int32), ("n_body", C.c_int32), ("n_post", C.c_int32),
                 ("loop", C.c_int32), ("max_iter", C.c_int32), ("test", C.c_int32), ("test_a", C.c_int32),
-                ("test_b", C.c_int32), ("out_kind", C.c_int32), ("out_reg", C.c_int32), ("pad", C.c_int32),
-                ("code", _lib.MapInstr * MAX_INSTR)]
+                ("test_b", C.c_int32), ("out_kind", C.c_int32), ("out_width", C.c_int32), ("out_regs", C.c_int32 * 4),
+                ("in_widths", C.c_int32 * MAX_INPUTS), ("code", _lib.MapInstr * MAX_INSTR)]
 
 
 class ProgramError(ValueError):
@@ -89,10 +89,13 @@ class Builder:
     def index(self, axis: int) -> Node:
         return self._node("index", val=int(axis))
 
-    def load(self, k: int) -> Node:
+    def load(self, k: int, component: int = 0) -> Node:
+        """Component `component` of input field k at this pixel."""
         if not 0 <= k < MAX_INPUTS:
             raise ProgramError(f"at most {MAX_INPUTS} input fields")
-        return self._node("load", val=int(k))
+        if not 0 <= component < 4:
+            raise ProgramError("a field has at most 4 components")
+        return self._node("load", val=(int(k), int(component)))
 
     def state(self, name: str) -> Node:
         return self._node("state", val=name)
@@ -191,7 +194,7 @@ class _Emitter:
         elif k == "index":
             op, a = OP["index"], n.val
         elif k == "load":
-            op, a = OP["load"], n.val
+            op, a, c = OP["load"], n.val[0], n.val[1]
         elif k == "count":
             op = OP["count"]
         elif k == "state":
@@ -222,12 +225,13 @@ def _node_of(b: Builder, v) -> Node:
 
 
 def compile_program(b: Builder, init: dict | None = None, test=None, body: dict | None = None, max_iter: int = 0,
-                    out=None, loop: bool | None = None) -> PixelProgram:
+                    out=None, loop: bool | None = None, in_widths=()) -> PixelProgram:
     """init: {state name: initial Node or number}; test: (op, lhs, rhs) with op in lt/le/gt/ge (None:
     no test), both sides per-pixel values; body: {state name: new value} (the parallel update of
     one loop trip; names not listed keep their value); max_iter: most updates; out: the stored
-    value (a Node using states, count() and invariants) or COUNT.  loop defaults to whether a body
-    or test is given."""
+    value (a Node using states, count() and invariants; a list or tuple of 1-4 of them for a
+    field of vectors) or COUNT.  loop defaults to whether a body or test is given.  in_widths:
+    components per pixel of each input field (default 1)."""
     init = dict(init or {})
     body = dict(body or {})
     loop = bool(body or test) if loop is None else bool(loop)
@@ -239,7 +243,10 @@ def compile_program(b: Builder, init: dict | None = None, test=None, body: dict 
     state_names = list(init)
     nodes_test = [] if test is None else [_node_of(b, v) for v in test[1:]]
     nodes_body = [_node_of(b, body[nm]) for nm in body]
-    out_node = None if out is COUNT else _node_of(b, out)
+    outs = [] if out is COUNT else [_node_of(b, v) for v in (out if isinstance(out, (list, tuple)) else [out])]
+    if out is not COUNT and not 1 <= len(outs) <= 4:
+        raise ProgramError("a pixel stores 1 to 4 components")
+    out_node = outs[0] if outs else None
     init_nodes = [_node_of(b, init[nm]) for nm in state_names]
     for n in nodes_test + nodes_body:
         if "count" in n.deps:
@@ -247,7 +254,7 @@ def compile_program(b: Builder, init: dict | None = None, test=None, body: dict 
     for n in init_nodes:
         if n.deps:
             raise ProgramError("an initial value reads loop state or the count")
-    if not loop and (out is COUNT or (out_node is not None and "count" in out_node.deps)):
+    if not loop and (out is COUNT or any("count" in n.deps for n in outs)):
         raise ProgramError("the count needs a loop")
     # Registers pinned for the whole program: one per state, then each maximal loop-invariant
     # subexpression the loop reads (computed once, in pre) and each constant the test compares.
@@ -318,17 +325,25 @@ def compile_program(b: Builder, init: dict | None = None, test=None, body: dict 
         for nm, r in staged.items():
             _move(code, r, pinned[b.state(nm)])
         n_body = len(code) - n_pre - n_test
-    out_kind, out_reg = OUT_REG, 0
+    out_kind, out_regs = OUT_REG, [0]
     if out is COUNT:
         out_kind = OUT_COUNT
     else:
-        out_reg = _Emitter(code, pinned, reserved).emit([out_node])[out_node]
+        regs = _Emitter(code, pinned, reserved).emit(outs)
+        out_regs = [regs[n] for n in outs]
     n_post = len(code) - n_pre - n_test - n_body
     p = PixelProgram()
     p.n_pre, p.n_test, p.n_body, p.n_post = n_pre, n_test, n_body, n_post
     p.loop, p.max_iter = int(loop), int(max_iter)
     p.test, p.test_a, p.test_b = test_kind, ta, tb
-    p.out_kind, p.out_reg = out_kind, out_reg
+    p.out_kind, p.out_width = out_kind, len(out_regs)
+    for k, r in enumerate(out_regs):
+        p.out_regs[k] = r
+    widths = list(in_widths) + [1] * (MAX_INPUTS - len(in_widths))
+    for k in range(MAX_INPUTS):
+        if not 1 <= widths[k] <= 4:
+            raise ProgramError("an input field has 1 to 4 components")
+        p.in_widths[k] = widths[k]
     for k, ins in enumerate(code):
         p.code[k] = ins
     return p

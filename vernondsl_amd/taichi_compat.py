@@ -85,10 +85,11 @@ def _device():
 
 
 class Field:
-    """A dense 2-D field (fractal.py:8).  Storage is a device tensor, allocated and zeroed on first
-    use."""
+    """A dense 2-D field (fractal.py:8) of scalars, or of vectors of `width` f32 components
+    (ti.Vector.field).  Storage is a device tensor ([W][H] or [W][H][width]), allocated and zeroed
+    on first use."""
 
-    def __init__(self, dtype, shape):
+    def __init__(self, dtype, shape, width=1):
         if dtype in (float, f32, None):
             self.dtype = f32
         elif dtype in (int, i32):
@@ -98,13 +99,16 @@ class Field:
         if isinstance(shape, int):
             shape = (shape,)
         self.shape = tuple(int(s) for s in shape)
+        self.width = int(width)
+        if not 1 <= self.width <= 4 or (self.width > 1 and self.dtype != f32):
+            raise TaichiLoweringError("vector fields hold 1 to 4 f32 components")
         self._tensor = None
 
     def tensor(self):
         if self._tensor is None:
             from .rhi import Tensor
             dev, q = _device()
-            t = Tensor(dev, self.shape, self.dtype)
+            t = Tensor(dev, self.shape if self.width == 1 else self.shape + (self.width,), self.dtype)
             t.buffer.fill_u32(q, 0)  # a Taichi field starts zeroed
             self._tensor = t
         return self._tensor
@@ -133,6 +137,11 @@ def kernel(fn):
 class Vector:  # only meaningful inside kernels, where the lowering interprets it
     def __init__(self, *_a, **_k):
         raise TaichiLoweringError("ti.Vector is only available inside @ti.kernel / @ti.func code")
+
+    @staticmethod
+    def field(n, dtype=float, shape=None, **_kw):
+        """ti.Vector.field(n, dtype, shape): a 2-D field of n-component f32 vectors."""
+        return Field(dtype, shape, width=n)
 
 
 def cos(x):
@@ -432,6 +441,8 @@ def lower_escape_time(fdef: ast.FunctionDef, funcs, env) -> tuple:
     fld = interp.expr(loop.iter, {})
     if not isinstance(fld, Field) or len(fld.shape) != 2:
         raise TaichiLoweringError("the struct-for must iterate a 2-D ti.field")
+    if fld.width != 1:
+        raise TaichiLoweringError("the escape-time op stores one value per pixel (a field of scalars)")
     local = {iname: Sym("i"), jname: Sym("j")}
     params = dict(ni=fld.shape[0], nj=fld.shape[1])
     state = {}
@@ -620,11 +631,15 @@ def _parse_source(text: str, kernel_name: str, args: dict):
             v = st.value
             if isinstance(v, ast.Call) and isinstance(v.func, ast.Attribute) and v.func.attr == "field":
                 kw = {k.arg: k.value for k in v.keywords}
+                is_vec = isinstance(v.func.value, ast.Attribute) and v.func.value.attr == "Vector"
+                width = 1
+                if is_vec:
+                    width = interp.expr(kw["n"] if "n" in kw else v.args[0], {})
                 shape = interp.expr(kw["shape"], {})
                 dt = kw.get("dtype")
                 dtype = f32 if dt is None or (isinstance(dt, ast.Name) and dt.id == "float") else (
                     i32 if (isinstance(dt, ast.Name) and dt.id == "int") or getattr(dt, "attr", "") in ("i32", "int32") else f32)
-                env[st.targets[0].id] = Field(dtype, shape)
+                env[st.targets[0].id] = Field(dtype, shape, width=int(width))
             else:
                 try:
                     env[st.targets[0].id] = interp.expr(v, {})
@@ -812,7 +827,10 @@ class _PixInterp:
             if len(self.inputs) == self.pp.MAX_INPUTS:
                 raise TaichiLoweringError(f"at most {self.pp.MAX_INPUTS} fields can be read")
             self.inputs.append(fld)
-        return self.b.load(self.inputs.index(fld))
+        k = self.inputs.index(fld)
+        if fld.width == 1:
+            return self.b.load(k)
+        return _PVec([self.b.load(k, c) for c in range(fld.width)])
 
     def call(self, n, local):
         f = n.func
@@ -1015,8 +1033,15 @@ class _PixInterp:
             if self.in_loop:
                 raise TaichiLoweringError("a store inside the loop is not supported (store after it)")
             v = self.expr(st.value, local)
-            if isinstance(v, _PVec):
-                raise TaichiLoweringError("a field of scalars stores a scalar")
+            if isinstance(v, list):
+                v = _PVec(v)
+            if self.fld.width == 1:
+                if isinstance(v, _PVec):
+                    raise TaichiLoweringError("a field of scalars stores a scalar")
+            elif not isinstance(v, _PVec):
+                v = _PVec([v] * self.fld.width)  # a scalar fills every component
+            elif len(v.comps) != self.fld.width:
+                raise TaichiLoweringError(f"a field of {self.fld.width}-vectors stores {self.fld.width} components")
             local[_STORE] = v
             return True
         if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Name):
@@ -1105,10 +1130,13 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
         if not (isinstance(v, pp.Node) and v.kind == "count"):
             raise TaichiLoweringError("an i32 field stores the loop counter")
         out = pp.COUNT
+    elif isinstance(v, _PVec):
+        out = [c if isinstance(c, pp.Node) else float(_f32(c)) for c in v.comps]
     else:
         out = v if isinstance(v, pp.Node) else float(_f32(v))
     try:
-        prog = pp.compile_program(b, init=init, test=test, body=new_state, max_iter=max_iter, out=out, loop=has_loop)
+        prog = pp.compile_program(b, init=init, test=test, body=new_state, max_iter=max_iter, out=out, loop=has_loop,
+                                  in_widths=[f.width for f in ip.inputs])
     except pp.ProgramError as e:
         raise TaichiLoweringError(str(e)) from None
     return Lowered("pixel_program", fld, program=prog, inputs=ip.inputs)
