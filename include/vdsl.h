@@ -273,7 +273,7 @@ int vdsl_op_map_chain_v(vdsl_queue q, int64_t rows, int64_t cols, const vdsl_map
 
 /* ---- general per-pixel programs: the body of a struct-for over a 2-D field ------------------ */
 /* The general form of op class 1 (fractal.py:16-25): what a Taichi @ti.kernel `for i, j in F:`
- * body computes per pixel, as a register program of four sections run in order on 16 f32
+ * body computes per pixel, as a register program of four sections run in order on 32 f32
  * registers (all 0 at the start):
  *   pre  (code[0, n_pre)):            per-pixel set-up (index maps, field reads, constants);
  *   loop (code[n_pre, +n_test) test, code[.., +n_body) body): when `loop` is set, the
@@ -290,8 +290,8 @@ int vdsl_op_map_chain_v(vdsl_queue q, int64_t rows, int64_t cols, const vdsl_map
  * recording.  No counterpart in the reference beyond the program surface it runs; the caller is
  * the Taichi-subset front end for kernel bodies other than the escape-time form of
  * vdsl_op_escape_time. */
-#define VDSL_PIX_MAX_INSTR 64
-#define VDSL_PIX_MAX_REGS 16
+#define VDSL_PIX_MAX_INSTR 128
+#define VDSL_PIX_MAX_REGS 32
 #define VDSL_PIX_MAX_INPUTS 4
 
 typedef enum vdsl_pix_opcode {

@@ -208,7 +208,7 @@ static int pix_test(int test, float a, float b) {
   }
 }
 
-/* Rows [r0, r1) of vdsl_op_pixel_program: per pixel, 16 registers at 0, the pre section, the
+/* Rows [r0, r1) of vdsl_op_pixel_program: per pixel, VDSL_PIX_MAX_REGS registers at 0, the pre section, the
  * check-then-update loop (fractal.py:22-24: test, stop unless it holds and fewer than max_iter
  * updates were made, body, count), the post section, then out[i][j][k] = r[out_regs[k]] (f32,
  * out_width components) or the count (int32).  A LOAD reads component c of input a's pixel

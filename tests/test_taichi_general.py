@@ -176,14 +176,14 @@ def test_rejected_general_bodies(body, msg):
 
 def test_register_pressure_is_reported():
     b = pp.Builder()
-    vals = [b.op("sin", b.op("mul", b.index(0), float(k + 1))) for k in range(20)]
+    vals = [b.op("sin", b.op("mul", b.index(0), float(k + 1))) for k in range(40)]
     acc = vals[0]
     for v in vals[1:]:
         acc = b.op("add", acc, v)
     pp.compile_program(b, out=acc)  # a chain: few registers live at once
     wide = b.op("add", vals[0], vals[1])
-    for k in range(2, 20):
-        wide = b.op("add", wide, b.op("mul", vals[k], vals[(k + 7) % 20]))
+    for k in range(2, 40):
+        wide = b.op("add", wide, b.op("mul", vals[k], vals[(k + 7) % 40]))
     with pytest.raises(pp.ProgramError, match="registers|instructions"):
         pp.compile_program(b, out=wide)
 
@@ -353,3 +353,38 @@ def test_vector_field_stores_and_errors():
     assert np.array_equal(ww, np.stack([g[..., 1], g[..., 0], g[..., 0] + g[..., 1], np.ones((8, 8), np.float32)], -1))
     with pytest.raises(tc.TaichiLoweringError, match="2-vectors stores 2"):
         tc.lower_source_kernel(text, "bad", {})
+
+
+def shading_numpy(t, m, W=480, H=400):
+    """examples/shading.py's draw(t) restated in numpy f32 (Taichi's definitions of the
+    taichi.math functions: normalized = v * (1 / |v|), mix = x (1 - a) + y a, ...)."""
+    x, y = grid(W, H)
+    p0 = (x / f32(W) + f32(-0.5)) * f32(2.0)
+    p1 = (y / f32(H) + f32(-0.5)) * f32(2.0)
+
+    def norm3(a, b, c):
+        inv = f32(1.0) / np.sqrt((a * a + b * b) + c * c)
+        return a * inv, b * inv, c * inv
+
+    l0, l1, l2 = norm3(f32(0.3), f32(0.5), f32(1.0))
+    n0, n1, n2 = norm3(p0, p1, np.ones_like(p0))
+    sh = np.minimum(np.maximum((n0 * l0 + n1 * l1) + n2 * l2, f32(0.0)), f32(1.0))
+    fx = p0 * f32(3.0) + f32(t)
+    length = np.sqrt(p0 * p0 + p1 * p1)
+    tt = np.minimum(np.maximum((length - f32(0.2)) / (f32(0.8) - f32(0.2)), f32(0.0)), f32(1.0))
+    base = [fx - np.floor(fx), (tt * tt) * (f32(3.0) - f32(2.0) * tt), np.where(p1 < f32(0.0), f32(0.0), f32(1.0))]
+    sign = np.where(f32(0.0) < p0, f32(1.0), np.where(p0 < f32(0.0), f32(-1.0), f32(0.0)))
+    acc = [base[k] * sh + (sign * f32(0.1)) * f32(k) for k in range(3)]
+    cz = [acc[1] * f32(1.0) - acc[2] * f32(0.0), acc[2] * f32(0.0) - acc[0] * f32(1.0), acc[0] * f32(0.0) - acc[1] * f32(0.0)]
+    return np.stack([(acc[k] * (f32(1.0) - f32(0.25)) + cz[k] * f32(0.25)) * m for k in range(3)], -1)
+
+
+def test_math_functions_ndrange_and_static_loops():
+    text = ex("shading.py")
+    low = tc.lower_source_kernel(text, "draw", {"t": 0.25})
+    assert low.kind == "pixel_program" and low.field.width == 3 and [f.width for f in low.inputs] == [1]
+    m = np.random.default_rng(3).random((480, 400), dtype=np.float32)
+    got = oracle.pixel_program(low.program, 480, 400, [m])
+    assert np.array_equal(got, shading_numpy(0.25, m))
+    mk = oracle.pixel_program(tc.lower_source_kernel(text, "make_mask", {}).program, 480, 400)
+    assert set(np.unique(mk)) == {0.5, 1.0}

@@ -133,7 +133,7 @@ int main(void) {
   EXPECT_OK(vdsl_op_pixel_program(q, 8, 16, &pp, NULL, 0, a));   /* a vec4 field: 2048 bytes */
   EXPECT_ERR(vdsl_op_pixel_program(q, 32, 16, &pp, NULL, 0, a)); /* 8192 bytes > 4096 */
   pp.out_width = 1;
-  pp.code[2].c = 16;
+  pp.code[2].c = VDSL_PIX_MAX_REGS;
   EXPECT_ERR(vdsl_op_pixel_program(q, 8, 16, &pp, NULL, 0, a));  /* register out of range */
 
   /* ---- op class 2: map chains ---- */

@@ -21,7 +21,7 @@ JitCounters g_pix_jit;
 int check_program(const vdsl_pixel_program& p, int n_inputs) {
   const int64_t total = int64_t{p.n_pre} + p.n_test + p.n_body + p.n_post;
   if (p.n_pre < 0 || p.n_test < 0 || p.n_body < 0 || p.n_post < 0 || total > VDSL_PIX_MAX_INSTR)
-    return fail(VDSL_ERR_INVALID_ARG, "pixel program: section lengths must be >= 0 and sum to at most 64");
+    return fail(VDSL_ERR_INVALID_ARG, "pixel program: section lengths must be >= 0 and sum to at most " + std::to_string(VDSL_PIX_MAX_INSTR));
   if (p.loop != 0 && p.loop != 1) return fail(VDSL_ERR_INVALID_ARG, "pixel program: loop must be 0 or 1");
   if (!p.loop && (p.n_test || p.n_body)) return fail(VDSL_ERR_INVALID_ARG, "pixel program: test/body sections without a loop");
   if (p.max_iter < 0) return fail(VDSL_ERR_INVALID_ARG, "pixel program: max_iter < 0");

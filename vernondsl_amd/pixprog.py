@@ -4,7 +4,7 @@ A per-pixel program is what the body of a Taichi struct-for over a 2-D field com
 (the reference's `paint`, fractal.py:16-25, is one): values are expression DAGs over the pixel
 indices, other fields read at the same pixel, constants and, inside its one check-then-update loop
 (fractal.py:22-24), the loop-carried state.  `compile_program` lowers such a program to the four
-sections the device runs (pre, loop test, loop body, post) on 16 f32 registers:
+sections the device runs (pre, loop test, loop body, post) on 32 f32 registers:
 
     b = Builder()
     c_re = b.op("add", b.op("mul", b.op("div", b.index(0), 1024.0), 3.0), -2.0)   # any DAG
@@ -23,7 +23,7 @@ import numpy as np
 
 from . import _lib
 
-MAX_INSTR, MAX_REGS, MAX_INPUTS = 64, 16, 4
+MAX_INSTR, MAX_REGS, MAX_INPUTS = 128, 32, 4
 OP = dict(_lib.MAP_OPS)
 OP.update({"index": 32, "cos": 33, "sin": 34, "count": 35, "lt": 36, "le": 37, "eq": 38, "ne": 39, "select": 40,
            "floor": 41})

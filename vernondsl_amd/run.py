@@ -23,8 +23,9 @@ def main(argv=None):
     ap.add_argument("program")
     ap.add_argument("--frames", type=int, default=8)
     args = ap.parse_args(argv)
-    saved = sys.modules.get("taichi")
+    saved = {name: sys.modules.get(name) for name in ("taichi", "taichi.math")}
     sys.modules["taichi"] = taichi_compat
+    sys.modules["taichi.math"] = taichi_compat.math
     taichi_compat.GUI.frame_limit = args.frames
     result = {"program": args.program, "frames": 0, "last_image_sha256": None}
     try:
@@ -32,10 +33,11 @@ def main(argv=None):
     except taichi_compat.FrameLimitReached:
         pass
     finally:
-        if saved is None:
-            sys.modules.pop("taichi", None)
-        else:
-            sys.modules["taichi"] = saved
+        for name, mod in saved.items():
+            if mod is None:
+                sys.modules.pop(name, None)
+            else:
+                sys.modules[name] = mod
     gui = taichi_compat._state.get("last_gui")
     if gui is not None and gui.last_image is not None:
         img = np.ascontiguousarray(gui.last_image)

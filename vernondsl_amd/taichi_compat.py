@@ -39,8 +39,9 @@ from __future__ import annotations
 
 import ast
 import inspect
-import math
+import math as _pymath
 import textwrap
+import types
 
 import numpy as np
 
@@ -602,12 +603,14 @@ def _parse_source(text: str, kernel_name: str, args: dict):
     mod = ast.parse(text)
     env = {"float": float, "int": int}
     tinames = set()
+    import sys as _sys
     for st in mod.body:
         if isinstance(st, ast.Import):
             for a in st.names:
                 if a.name == "taichi":
                     tinames.add(a.asname or "taichi")
-    import sys as _sys
+                elif a.name == "taichi.math" and a.asname:
+                    env[a.asname] = math
     for name in tinames:
         env[name] = _sys.modules[__name__]
     funcs, kern = {}, None
@@ -654,7 +657,31 @@ def _parse_source(text: str, kernel_name: str, args: dict):
 
 
 # math helpers programs sometimes use at module level
-pi = math.pi
+pi = _pymath.pi
+
+# ti.math (also importable as taichi.math under the runner): names only; inside kernels the
+# lowering interprets the calls (vec2-4, clamp, mix, smoothstep, length, normalize, dot, cross,
+# fract, sign, step and the scalar functions).
+math = types.ModuleType("taichi.math")
+math.pi = _pymath.pi
+math.e = _pymath.e
+for _name in ("vec2", "vec3", "vec4", "clamp", "mix", "smoothstep", "length", "normalize", "dot", "cross", "fract",
+              "sign", "step", "sqrt", "exp", "log", "sin", "cos", "tanh", "floor", "ceil", "min", "max"):
+    setattr(math, _name, _name)  # placeholders: only meaningful inside kernels
+
+
+def ndrange(*extents):
+    """ti.ndrange(W, H): the index space of a struct-for that is not over a field."""
+    return tuple(int(e) for e in extents)
+
+
+def static(v):
+    """ti.static(range(N)): a loop unrolled when the kernel is lowered."""
+    return v
+
+
+def template():
+    return None
 
 
 # ---- the general path: any struct-for body as a per-pixel register program ---------------------------
@@ -689,6 +716,8 @@ class _PVec:
 _UNARY_FUNCS = {"sqrt": "sqrt", "exp": "exp", "log": "log", "sin": "sin", "cos": "cos", "tanh": "tanh", "abs": "abs",
                 "floor": "floor"}
 _STORE = "__store__"  # the value the body stores to the iterated field at [i, j]
+_MATH_FUNCS = ("vec2", "vec3", "vec4", "clamp", "mix", "smoothstep", "length", "normalize", "dot", "cross", "fract",
+               "step", "sign")
 
 
 class _PixInterp:
@@ -700,6 +729,7 @@ class _PixInterp:
         self.pp = pixprog
         self.env, self.funcs, self.b = env, funcs, b
         self.fld, self.iname, self.jname = fld, iname, jname
+        self.shape = fld.shape if isinstance(fld, Field) else None  # the struct-for's index space
         self.inputs = []  # Fields read at [i, j], in LOAD order
         self.bools = set()  # ids of Nodes known to hold 1.0 / 0.0 (comparisons and their logic)
         self.in_loop = False
@@ -821,7 +851,7 @@ class _PixInterp:
             raise TaichiLoweringError("fields are read at [i, j] of the struct-for only")
         if fld is self.fld and _STORE in local:
             return local[_STORE]  # the value this pixel stored earlier in the body
-        if fld.shape != self.fld.shape or fld.dtype != f32:
+        if fld.shape != self.shape or fld.dtype != f32:
             raise TaichiLoweringError("a field read must be an f32 field of the iterated field's shape")
         if fld not in self.inputs:
             if len(self.inputs) == self.pp.MAX_INPUTS:
@@ -843,6 +873,10 @@ class _PixInterp:
                     return self.dot(base, base)
                 if f.attr == "dot":
                     return self.dot(base, self.expr(n.args[0], local))
+                if f.attr == "normalized":
+                    return self.normalize(base)
+                if f.attr == "cross":
+                    return self.cross(base, self.expr(n.args[0], local))
                 raise TaichiLoweringError(f"vector method {f.attr!r} is not supported")
             if f.attr == "Vector":
                 comps = self.expr(n.args[0], local)
@@ -855,6 +889,8 @@ class _PixInterp:
                 if len(n.args) != 3:
                     raise TaichiLoweringError("ti.select takes (condition, if_true, if_false)")
                 return self.select(*[self.expr(a, local) for a in n.args])
+            if f.attr in _MATH_FUNCS:
+                return self.math_call(f.attr, [self.expr(a, local) for a in n.args])
             if f.attr == "ceil":
                 return self.unary("neg", self.unary("floor", self.unary("neg", self.expr(n.args[0], local))))
             if f.attr in ("max", "min"):
@@ -891,11 +927,84 @@ class _PixInterp:
             raise TaichiLoweringError(f"{which} needs two or more values")
         acc = vals[0]
         for v in vals[1:]:
-            if _is_num(acc) and _is_num(v):
-                acc = (max if which == "max" else min)(_f32(acc), _f32(v))
-            else:
-                acc = self.b.op(which, self.node(acc), self.node(v))
+            acc = self.elementwise(lambda x, y: self._minmax2(which, x, y), acc, v)
         return acc
+
+    def _minmax2(self, which, x, y):
+        if _is_num(x) and _is_num(y):
+            return (max if which == "max" else min)(_f32(x), _f32(y))
+        return self.b.op(which, self.node(x), self.node(y))
+
+    def elementwise(self, fn, *vals):
+        """fn over scalars, or per component where some of vals are vectors (scalars broadcast)."""
+        vecs = [v for v in vals if isinstance(v, _PVec)]
+        if not vecs:
+            return fn(*vals)
+        n = len(vecs[0].comps)
+        if any(len(v.comps) != n for v in vecs):
+            raise TaichiLoweringError("vector length mismatch")
+        return _PVec([fn(*[v.comps[k] if isinstance(v, _PVec) else v for v in vals]) for k in range(n)])
+
+    def normalize(self, v):
+        """v * (1 / |v|), as Taichi's Matrix.normalized forms it."""
+        if not isinstance(v, _PVec):
+            raise TaichiLoweringError("normalize takes a vector")
+        inv = self.arith("div", 1.0, self.unary("sqrt", self.dot(v, v)))
+        return _PVec([self.arith("mul", c, inv) for c in v.comps])
+
+    def cross(self, a, c):
+        if not (isinstance(a, _PVec) and isinstance(c, _PVec) and len(a.comps) == len(c.comps) == 3):
+            raise TaichiLoweringError("cross takes two 3-vectors")
+        x, y = a.comps, c.comps
+        comp = lambda i, j: self.arith("sub", self.arith("mul", x[i], y[j]), self.arith("mul", x[j], y[i]))
+        return _PVec([comp(1, 2), comp(2, 0), comp(0, 1)])
+
+    def math_call(self, name, args):
+        """ti.math's functions, written out in the operations Taichi's definitions use."""
+        if name in ("vec2", "vec3", "vec4"):
+            comps = []
+            for a in args:
+                comps.extend(a.comps if isinstance(a, _PVec) else [a])
+            want = int(name[3])
+            if len(comps) == 1:
+                comps = comps * want
+            if len(comps) != want:
+                raise TaichiLoweringError(f"{name} of {len(comps)} components")
+            return _PVec(comps)
+        if name == "clamp":
+            x, lo, hi = args
+            return self.minmax("min", [self.minmax("max", [x, lo]), hi])
+        if name == "mix":  # x * (1 - a) + y * a
+            x, y, a = args
+            return self.arith("add", self.arith("mul", x, self.arith("sub", 1.0, a)), self.arith("mul", y, a))
+        if name == "smoothstep":  # t = clamp((x - e0) / (e1 - e0), 0, 1); t * t * (3 - 2 t)
+            e0, e1, x = args
+            t = self.math_call("clamp", [self.arith("div", self.arith("sub", x, e0), self.arith("sub", e1, e0)), 0.0, 1.0])
+            return self.arith("mul", self.arith("mul", t, t), self.arith("sub", 3.0, self.arith("mul", 2.0, t)))
+        if name == "length":
+            return self.unary("sqrt", self.dot(args[0], args[0]))
+        if name == "normalize":
+            return self.normalize(args[0])
+        if name == "dot":
+            return self.dot(args[0], args[1])
+        if name == "cross":
+            return self.cross(args[0], args[1])
+        if name == "fract":
+            return self.arith("sub", args[0], self.unary("floor", args[0]))
+        if name == "step":  # 0 where x < edge, else 1
+            edge, x = args
+            return self.elementwise(lambda e, v: self.select(self.cmp_value("lt", v, e), 0.0, 1.0), edge, x)
+        if name == "sign":
+            return self.elementwise(
+                lambda v: self.select(self.cmp_value("lt", 0.0, v), 1.0, self.select(self.cmp_value("lt", v, 0.0), -1.0, 0.0)),
+                args[0])
+        raise TaichiLoweringError(f"ti.math.{name} is not supported")
+
+    def cmp_value(self, kind, a, c):
+        if _is_num(a) and _is_num(c):
+            fa, fc = _f32(a), _f32(c)
+            return int({"lt": fa < fc, "le": fa <= fc, "eq": fa == fc, "ne": fa != fc}[kind])
+        return self._bool(self.b.op(kind, self.node(a), self.node(c)))
 
     # -- conditions: comparisons give 1.0 / 0.0; a value is true where it is not 0 (NaN is true)
     def _bool(self, n):
@@ -1008,6 +1117,8 @@ class _PixInterp:
                 continue
             if nm == _STORE:  # the field keeps its value where a branch does not store
                 keep = local.get(_STORE)
+                if self.fld is None:
+                    raise TaichiLoweringError("no output field")
                 if keep is None:
                     if self.fld.dtype != f32:
                         raise TaichiLoweringError("an i32 field must be stored on every path")
@@ -1019,14 +1130,89 @@ class _PixInterp:
                 continue
             local[nm] = self.select(c, vt, vf)
 
+    def static_values(self, st, local):
+        """The values of `for v in ti.static(...)` (a loop unrolled when the kernel is lowered), or
+        None for any other statement."""
+        if not isinstance(st, ast.For):
+            return None
+        it = st.iter
+        if not (isinstance(it, ast.Call) and len(it.args) == 1 and
+                ((isinstance(it.func, ast.Attribute) and it.func.attr == "static") or
+                 (isinstance(it.func, ast.Name) and it.func.id == "static"))):
+            # `for k in range(N)` whose body reads k (a component index, say): unrolled as well,
+            # which runs the same statements in the same order; N is bounded by the program size
+            if (isinstance(it, ast.Call) and isinstance(it.func, ast.Name) and it.func.id == "range"
+                    and isinstance(st.target, ast.Name)
+                    and any(isinstance(nd, ast.Name) and nd.id == st.target.id and isinstance(nd.ctx, ast.Load)
+                            for s2 in st.body for nd in ast.walk(s2))):
+                bounds = [self.expr(a, local) for a in it.args]
+                if all(isinstance(v, (int, np.integer)) for v in bounds) and len(range(*map(int, bounds))) <= 32:
+                    return list(range(*[int(v) for v in bounds]))
+            return None
+        inner = it.args[0]
+        if isinstance(inner, ast.Call) and isinstance(inner.func, ast.Name) and inner.func.id == "range":
+            bounds = [self.expr(a, local) for a in inner.args]
+            if not all(isinstance(v, (int, np.integer)) for v in bounds):
+                raise TaichiLoweringError("ti.static(range(...)) needs integer constants")
+            return list(range(*[int(v) for v in bounds]))
+        vals = self.expr(inner, local)
+        if isinstance(vals, _PVec):
+            return list(vals.comps)
+        if isinstance(vals, (list, tuple)):
+            return list(vals)
+        raise TaichiLoweringError("ti.static loops over range(...) or a list of values")
+
+    def component_assign(self, st, tgt, local):
+        """v[k] = x, v.x = x, v[k] += x on a local vector: a new vector with component k replaced."""
+        name = tgt.value.id
+        vec = local[name]
+        if isinstance(tgt, ast.Attribute):
+            if tgt.attr not in ("x", "y", "z", "w"):
+                raise TaichiLoweringError(f"vector has no component {tgt.attr!r}")
+            k = "xyzw".index(tgt.attr)
+        else:
+            k = self.expr(tgt.slice, local)
+        if not isinstance(k, (int, np.integer)) or not -len(vec.comps) <= k < len(vec.comps):
+            raise TaichiLoweringError("a vector component is set at a constant index")
+        val = self.expr(st.value, local)
+        if isinstance(st, ast.AugAssign):
+            ops = {ast.Add: "add", ast.Sub: "sub", ast.Mult: "mul", ast.Div: "div"}
+            if type(st.op) not in ops:
+                raise TaichiLoweringError(f"augmented {type(st.op).__name__} is not supported")
+            val = self.arith(ops[type(st.op)], vec.comps[int(k)], val)
+        if isinstance(val, _PVec):
+            raise TaichiLoweringError("a vector component takes a scalar")
+        comps = list(vec.comps)
+        comps[int(k)] = val
+        local[name] = _PVec(comps)
+        return True
+
     def assign(self, st, local):
         if isinstance(st, ast.If):
             self.if_stmt(st, local)
             return True
+        vals = self.static_values(st, local)
+        if vals is not None:
+            if not isinstance(st.target, ast.Name) or st.orelse:
+                raise TaichiLoweringError("a ti.static loop binds one name and has no else")
+            for v in vals:
+                local[st.target.id] = v
+                for s2 in st.body:
+                    if not self.assign(s2, local):
+                        raise TaichiLoweringError(f"statement at line {getattr(s2, 'lineno', '?')} is not supported")
+            return True
+        if (isinstance(st, (ast.Assign, ast.AugAssign)) and isinstance(getattr(st, "target", None) or st.targets[0],
+                                                                       (ast.Subscript, ast.Attribute))):
+            tgt = st.target if isinstance(st, ast.AugAssign) else st.targets[0]
+            if isinstance(tgt.value, ast.Name) and isinstance(local.get(tgt.value.id), _PVec):
+                return self.component_assign(st, tgt, local)
         if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Subscript):
             tgt = st.targets[0]
-            if self.expr(tgt.value, local) is not self.fld:
-                raise TaichiLoweringError("the body may only store to the iterated field")
+            target = self.expr(tgt.value, local)
+            if self.fld is None and isinstance(target, Field) and target.shape == self.shape:
+                self.fld = target  # a loop over ti.ndrange stores to a field of its shape
+            if target is not self.fld:
+                raise TaichiLoweringError("the body may only store to the iterated field (one output field)")
             idx = tgt.slice
             if not (isinstance(idx, ast.Tuple) and [getattr(e, "id", None) for e in idx.elts] == [self.iname, self.jname]):
                 raise TaichiLoweringError("the store must write field[i, j]")
@@ -1078,8 +1264,9 @@ _BUILTINS = {"abs": abs, "max": max, "min": min, "float": float}
 def _assigned_names(stmts):
     out = []
     for st in stmts:
-        if isinstance(st, ast.If):
-            for nm in _assigned_names(st.body) + _assigned_names(st.orelse):
+        if isinstance(st, (ast.If, ast.For)):  # if branches; unrolled loops (their variable too)
+            names = [st.target.id] if isinstance(st, ast.For) and isinstance(st.target, ast.Name) else []
+            for nm in names + _assigned_names(st.body) + _assigned_names(st.orelse):
                 if nm not in out:
                     out.append(nm)
         elif isinstance(st, ast.Assign):
@@ -1104,15 +1291,24 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
     iname, jname = (e.id for e in loop.target.elts)
     b = pp.Builder()
     it0 = _PixInterp(env, funcs, b, None, iname, jname)
-    fld = it0.expr(loop.iter, {})
-    if not isinstance(fld, Field) or len(fld.shape) != 2:
-        raise TaichiLoweringError("the struct-for must iterate a 2-D ti.field")
-    ip = _PixInterp(env, funcs, b, fld, iname, jname)
+    it = loop.iter
+    if (isinstance(it, ast.Call) and ((isinstance(it.func, ast.Attribute) and it.func.attr == "ndrange") or
+                                      (isinstance(it.func, ast.Name) and it.func.id == "ndrange"))):
+        shape = tuple(it0.expr(a, {}) for a in it.args)
+        if len(shape) != 2 or not all(isinstance(v, (int, np.integer)) and v >= 0 for v in shape):
+            raise TaichiLoweringError("ti.ndrange needs two non-negative integer extents")
+        ip = _PixInterp(env, funcs, b, None, iname, jname)
+        ip.shape = tuple(int(v) for v in shape)
+    else:
+        fld = it0.expr(it, {})
+        if not isinstance(fld, Field) or len(fld.shape) != 2:
+            raise TaichiLoweringError("the struct-for must iterate a 2-D ti.field or ti.ndrange(W, H)")
+        ip = _PixInterp(env, funcs, b, fld, iname, jname)
     local = {iname: b.index(0), jname: b.index(1)}
     stmts = [s for s in loop.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant)) and not isinstance(s, ast.Pass)]
     init, test, new_state, max_iter, has_loop = {}, None, {}, 0, False
     for st in stmts:
-        if isinstance(st, (ast.While, ast.For)):
+        if isinstance(st, (ast.While, ast.For)) and ip.static_values(st, local) is None:
             if has_loop:
                 raise TaichiLoweringError("at most one loop per struct-for body")
             if _STORE in local:
@@ -1125,6 +1321,7 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
         raise TaichiLoweringError(f"statement at line {getattr(st, 'lineno', '?')} is not supported")
     if _STORE not in local:
         raise TaichiLoweringError("the struct-for body must store field[i, j] = ...")
+    fld = ip.fld
     v = local[_STORE]
     if fld.dtype == i32:
         if not (isinstance(v, pp.Node) and v.kind == "count"):
