@@ -304,7 +304,11 @@ typedef enum vdsl_pix_opcode {
   VDSL_PIX_EQ = 38,     /* r[a] == r[b] ? 1 : 0 */
   VDSL_PIX_NE = 39,     /* r[a] != r[b] ? 1 : 0 (a NaN operand gives 1) */
   VDSL_PIX_SELECT = 40, /* r[a] != 0 ? r[b] : r[c] (NaN counts as true) */
-  VDSL_PIX_FLOOR = 41   /* floorf(r[a]) */
+  VDSL_PIX_FLOOR = 41,  /* floorf(r[a]) */
+  /* Component (int)imm of input a's pixel [row][col], row = index(r[b], ni), col = index(r[c], nj)
+   * with index(x, n) = 0 if !(x >= 0), n - 1 if x >= n - 1, else (int)x: a stencil or gather read,
+   * clamped to the field (Taichi leaves reads outside a field undefined). */
+  VDSL_PIX_LOAD_AT = 42
 } vdsl_pix_opcode;
 
 typedef enum vdsl_pix_test {
@@ -314,7 +318,10 @@ typedef enum vdsl_pix_test {
 
 typedef enum vdsl_pix_output {
   VDSL_PIX_OUT_REG = 0,    /* f32 field: r[out_regs[k]], k < out_width */
-  VDSL_PIX_OUT_COUNT = 1   /* int32 field: the count of loop updates (out_width 1) */
+  VDSL_PIX_OUT_COUNT = 1,  /* int32 field: the count of loop updates (out_width 1) */
+  /* int32 field: r[out_regs[0]] converted as a Taichi int field assignment does, truncating
+   * toward zero (NaN gives 0, values beyond the int32 range saturate); out_width 1 */
+  VDSL_PIX_OUT_I32 = 2
 } vdsl_pix_output;
 
 typedef struct vdsl_pixel_program {
@@ -327,12 +334,15 @@ typedef struct vdsl_pixel_program {
   int32_t out_width;                       /* components stored per pixel, 1..4 (ti.Vector.field) */
   int32_t out_regs[4];                     /* their registers, in component order */
   int32_t in_widths[VDSL_PIX_MAX_INPUTS];  /* components per pixel of input k, 1..4 */
+  int32_t in_dtypes[VDSL_PIX_MAX_INPUTS];  /* VDSL_F32, or VDSL_I32 (one component, read as float(v)) */
   vdsl_map_instr code[VDSL_PIX_MAX_INSTR];
 } vdsl_pixel_program;
 
-/* Runs `prog` for every pixel of an [ni][nj] grid.  inputs: f32 [ni][nj][in_widths[k]] fields
- * (n_inputs <= 4); out: f32 [ni][nj][out_width] (VDSL_PIX_OUT_REG) or int32 [ni][nj]
- * (VDSL_PIX_OUT_COUNT). */
+/* Runs `prog` for every pixel of an [ni][nj] grid.  inputs: f32 [ni][nj][in_widths[k]] or int32
+ * [ni][nj] fields (n_inputs <= 4); out: f32 [ni][nj][out_width] (VDSL_PIX_OUT_REG) or int32
+ * [ni][nj] (VDSL_PIX_OUT_COUNT, VDSL_PIX_OUT_I32).  A program may read its output buffer as an
+ * input: at [i][j] that is the pixel's value before the store; elsewhere (LOAD_AT) the result
+ * depends on the order pixels run in, as for a Taichi kernel reading the field it writes. */
 int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const vdsl_pixel_program* prog,
                           const vdsl_buffer* inputs, int32_t n_inputs, vdsl_buffer out);
 

@@ -146,16 +146,18 @@ def map_chain_v(prog, inputs, rows: int, cols: int, row_range=None) -> np.ndarra
 
 def pixel_program(prog, ni: int, nj: int, inputs=(), rows=None) -> np.ndarray:
     """orc_pixel_program_rows: prog is a vernondsl_amd.pixprog.PixelProgram (the C struct);
-    inputs: f32 [ni][nj] (one component) or [ni][nj][w] arrays, w = prog.in_widths[k]; returns
-    f32 [rows][nj] or [rows][nj][out_width], or int32 [rows][nj] (rows: (r0, r1), default all)."""
-    ins = [np.ascontiguousarray(a, np.float32) for a in inputs]
+    inputs: f32 [ni][nj] (one component) or [ni][nj][w] arrays, w = prog.in_widths[k], or int32
+    [ni][nj] (prog.in_dtypes[k] = VDSL_I32); returns f32 [rows][nj] or [rows][nj][out_width], or
+    int32 [rows][nj] (the count or an int32 field; rows: (r0, r1), default all)."""
+    ins = [np.ascontiguousarray(a, np.int32 if prog.in_dtypes[k] == 3 else np.float32) for k, a in enumerate(inputs)]
     for k, a in enumerate(ins):
         w = prog.in_widths[k]
         if a.shape != ((ni, nj) if w == 1 else (ni, nj, w)) and a.shape != (ni, nj, w):
             raise ValueError(f"input {k} of shape {a.shape}, expected {(ni, nj, w)}")
     r0, r1 = rows if rows else (0, ni)
-    shape = (r1 - r0, nj) if prog.out_kind == 1 or prog.out_width == 1 else (r1 - r0, nj, prog.out_width)
-    out = np.zeros(shape, np.int32 if prog.out_kind == 1 else np.float32)
+    int_out = prog.out_kind in (1, 2)  # the loop count, or a value stored to an int32 field
+    shape = (r1 - r0, nj) if int_out or prog.out_width == 1 else (r1 - r0, nj, prog.out_width)
+    out = np.zeros(shape, np.int32 if int_out else np.float32)
     ptrs = (_vp * max(1, len(ins)))(*[a.ctypes.data for a in ins])
     _lib.orc_pixel_program_rows(C.addressof(prog), ni, nj, ptrs, _p(out), r0, r1)
     return out

@@ -31,7 +31,7 @@ void orc_gelu_fwd(int64_t n, int x_dtype, const void* x, int y_dtype, void* y);
 void orc_gelu_bwd(int64_t rows, int64_t cols, const float* dh, const float* pre, uint16_t* da, uint16_t* da_t);
 void orc_mse_fwd_bwd(int64_t rows, int64_t cols, const float* y, const float* t, float* loss, uint16_t* dy, uint16_t* dy_t);
 void orc_quantize_rows_i8(int64_t rows, int64_t cols, int x_dtype, const void* x, int8_t* q, float* scale);
-void orc_pixel_program_rows(const vdsl_pixel_program* p, int64_t ni, int64_t nj, const float* const* inputs, void* out,
+void orc_pixel_program_rows(const vdsl_pixel_program* p, int64_t ni, int64_t nj, const void* const* inputs, void* out,
                             int64_t r0, int64_t r1);
 void orc_gemm_w8a8_rows(int64_t M, int64_t N, int64_t K, const int8_t* xq, const float* xs, const int8_t* w, const float* ws,
                         void* y, int out_dtype, int relu, int32_t* acc_out, int64_t m0, int64_t m1);
@@ -238,7 +238,7 @@ static void pixel_programs(void) {
       p.out_regs[0] = 11; p.out_regs[1] = 0; p.out_regs[2] = 1;
       float* in0 = buf((size_t)(ni * nj) * 8, 1);
       float* in1 = buf((size_t)(ni * nj) * 4, 1);
-      const float* ins[2] = {in0, in1};
+      const void* ins[2] = {in0, in1};
       void* out = buf((size_t)(ni * nj) * 4 * p.out_width, 0);
       orc_pixel_program_rows(&p, ni, nj, ins, out, 0, ni);
       free(in0); free(in1); free(out);

@@ -180,10 +180,34 @@ static float map_apply(int op, float a, float b, float c, float imm) {
 
 /* ---- general per-pixel programs (vdsl_pixel_program) -------------------------------------- */
 
-static float pix_apply(const vdsl_pixel_program* p, const vdsl_map_instr* s, const float* reg, const float* const* inputs,
-                       int64_t o, int64_t i, int64_t j, int count) {
+/* Element e (pixel index), component comp of input a: f32 fields of in_widths[a] components, or
+ * int32 fields read as float(v). */
+static float pix_load(const vdsl_pixel_program* p, const void* const* inputs, int a, int64_t e, int comp) {
+  if (p->in_dtypes[a] == VDSL_I32) return (float)((const int32_t*)inputs[a])[e];
+  return ((const float*)inputs[a])[e * p->in_widths[a] + comp];
+}
+
+/* A field index from a register: 0 if !(x >= 0) (NaN included), else min((int)min(x, 2^30), n-1). */
+static int64_t pix_index(float x, int64_t n) {
+  if (!(x >= 0.0f)) return 0;
+  const int64_t v = (int64_t)fminf(x, 1073741824.0f);
+  return v < n - 1 ? v : n - 1;
+}
+
+/* A register stored to an int32 field: truncation toward zero, NaN -> 0, saturating. */
+static int32_t pix_to_i32(float x) {
+  if (x != x) return 0;
+  if (x >= 2147483648.0f) return INT32_MAX;
+  if (x < -2147483648.0f) return INT32_MIN;
+  return (int32_t)x;
+}
+
+static float pix_apply(const vdsl_pixel_program* p, const vdsl_map_instr* s, const float* reg, const void* const* inputs,
+                       int64_t o, int64_t i, int64_t j, int count, int64_t ni, int64_t nj) {
   switch (s->op) {
-    case VDSL_MAP_LOAD: return inputs[s->a][o * p->in_widths[s->a] + s->c];
+    case VDSL_MAP_LOAD: return pix_load(p, inputs, s->a, o, s->c);
+    case VDSL_PIX_LOAD_AT:
+      return pix_load(p, inputs, s->a, pix_index(reg[s->b], ni) * nj + pix_index(reg[s->c], nj), (int)s->imm);
     case VDSL_PIX_INDEX: return s->a == 0 ? (float)i : (float)j;
     case VDSL_PIX_COUNT: return (float)count;
     case VDSL_PIX_COS: return cosf(reg[s->a]);
@@ -213,10 +237,9 @@ static int pix_test(int test, float a, float b) {
  * updates were made, body, count), the post section, then out[i][j][k] = r[out_regs[k]] (f32,
  * out_width components) or the count (int32).  A LOAD reads component c of input a's pixel
  * (in_widths[a] components each).  The program is taken as validated by the caller. */
-void orc_pixel_program_rows(const vdsl_pixel_program* p, int64_t ni, int64_t nj, const float* const* inputs, void* out,
+void orc_pixel_program_rows(const vdsl_pixel_program* p, int64_t ni, int64_t nj, const void* const* inputs, void* out,
                             int64_t r0, int64_t r1) {
   const int t0 = p->n_pre, b0 = t0 + p->n_test, q0 = b0 + p->n_body, end = q0 + p->n_post;
-  (void)ni;
 #pragma omp parallel for schedule(dynamic, 4)
   for (int64_t i = r0; i < r1; ++i)
     for (int64_t j = 0; j < nj; ++j) {
@@ -224,18 +247,20 @@ void orc_pixel_program_rows(const vdsl_pixel_program* p, int64_t ni, int64_t nj,
       float reg[VDSL_PIX_MAX_REGS];
       for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) reg[k] = 0.0f;
       int count = 0;
-      for (int pc = 0; pc < t0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, 0);
+      for (int pc = 0; pc < t0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, 0, ni, nj);
       if (p->loop) {
         while (count < p->max_iter) {
-          for (int pc = t0; pc < b0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, 0);
+          for (int pc = t0; pc < b0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, 0, ni, nj);
           if (!pix_test(p->test, reg[p->test_a], reg[p->test_b])) break;
-          for (int pc = b0; pc < q0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, 0);
+          for (int pc = b0; pc < q0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, 0, ni, nj);
           ++count;
         }
       }
-      for (int pc = q0; pc < end; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, count);
+      for (int pc = q0; pc < end; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, count, ni, nj);
       if (p->out_kind == VDSL_PIX_OUT_COUNT) {
         ((int32_t*)out)[o - r0 * nj] = count;
+      } else if (p->out_kind == VDSL_PIX_OUT_I32) {
+        ((int32_t*)out)[o - r0 * nj] = pix_to_i32(reg[p->out_regs[0]]);
       } else {
         for (int k = 0; k < p->out_width; ++k) ((float*)out)[(o - r0 * nj) * p->out_width + k] = reg[p->out_regs[k]];
       }

@@ -22,9 +22,11 @@ EX = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "
 
 
 def run_prog(dev, q, prog, inputs, ni, nj):
-    ts = [Tensor.from_numpy(dev, q, np.ascontiguousarray(a, np.float32)) for a in inputs]
-    w = 1 if prog.out_kind == pp.OUT_COUNT else prog.out_width
-    out = Tensor(dev, (ni, nj) if w == 1 else (ni, nj, w), "i32" if prog.out_kind == pp.OUT_COUNT else "f32")
+    ts = [Tensor.from_numpy(dev, q, np.ascontiguousarray(a, np.int32 if prog.in_dtypes[k] == pp.I32 else np.float32))
+          for k, a in enumerate(inputs)]
+    int_out = prog.out_kind in (pp.OUT_COUNT, pp.OUT_I32)
+    w = 1 if int_out else prog.out_width
+    out = Tensor(dev, (ni, nj) if w == 1 else (ni, nj, w), "i32" if int_out else "f32")
     if ni and nj:
         out.buffer.fill_u32(q, 0x7FC00000)  # NaN / a large count: every element must be written
     kernels.pixel_program(q, prog, ts, out)
@@ -369,3 +371,50 @@ def test_shading_example_taichi_math_bit_exact(dev, q):
     mask = oracle.pixel_program(tc.lower_source_kernel(text, "make_mask", {}).program, 480, 400)
     ref = oracle.pixel_program(tc.lower_source_kernel(text, "draw", {"t": 0.5}).program, 480, 400, [mask])
     assert np.array_equal(img, ref)
+
+
+def life_numpy(a):
+    c = sum(np.roll(np.roll(a, -di, 0), -dj, 1) for di in (-1, 0, 1) for dj in (-1, 0, 1) if (di, dj) != (0, 0))
+    return ((c == 3) | ((a == 1) & (c == 2))).astype(np.int32)
+
+
+def test_life_example_against_numpy(dev, q):
+    """int32 fields, neighbour reads at wrapped offsets: eight generations on the device equal
+    numpy's game of life (np.roll) and the oracle, cell for cell."""
+    path = os.path.join(EX, "life.py")
+    res, img = run_program(path, 8)
+    assert res["frames"] == 8 and img.shape == (320, 320) and img.dtype == np.int32
+    i, j = np.meshgrid(np.arange(320), np.arange(320), indexing="ij")
+    st = ((i * 37 + j * 91 + i * j) % 7 < 2).astype(np.int32)
+    for _ in range(8):
+        st = life_numpy(st)
+    assert np.array_equal(img, st) and 0 < st.sum() < st.size
+
+
+def test_heat_example_bit_exact(dev, q):
+    path = os.path.join(EX, "heat.py")
+    res, img = run_program(path, 2)
+    text = open(path).read()
+    u0 = oracle.pixel_program(tc.lower_source_kernel(text, "init", {}).program, 384, 256)
+    prog = tc.lower_source_kernel(text, "diffuse", {"k": 0.2}).program
+    u = u0
+    for _ in range(20):  # two frames of ten diffuse + swap each
+        u = oracle.pixel_program(prog, 384, 256, [u])
+    assert np.array_equal(img, u)
+    assert (img > 0).sum() > (u0 > 0).sum() and img.max() <= 1.0  # the heat has spread
+
+
+def test_gather_and_int32_store_bit_exact(dev, q):
+    b = pp.Builder()
+    rowi = b.op("sub", b.op("mul", b.index(0), 3.0), 5.0)
+    prog = pp.compile_program(b, out=b.load_at(0, rowi, b.load(1)), in_widths=[1, 1])
+    rng = np.random.default_rng(6)
+    src = rng.standard_normal((90, 70)).astype(np.float32)
+    cols = np.array(rng.choice([-3.0, 0.0, 2.5, 6.9, 69.0, 100.0, np.nan, 1e30, -np.inf], size=(90, 70)), np.float32)
+    assert np.array_equal(run_prog(dev, q, prog, [src, cols], 90, 70), oracle.pixel_program(prog, 90, 70, [src, cols]))
+    b = pp.Builder()
+    prog = pp.compile_program(b, out=b.op("add", b.load(0), b.load(1)), in_dtypes=[pp.I32, pp.F32], out_i32=True)
+    ints = rng.integers(-1000, 1000, size=(33, 65)).astype(np.int32)
+    fl = np.array(rng.choice([0.25, -0.75, 2.5, np.nan, 3e9, -3e9, 1e-3], size=(33, 65)), np.float32)
+    got = run_prog(dev, q, prog, [ints, fl], 33, 65)
+    assert got.dtype == np.int32 and np.array_equal(got, oracle.pixel_program(prog, 33, 65, [ints, fl]))

@@ -388,3 +388,66 @@ def test_math_functions_ndrange_and_static_loops():
     assert np.array_equal(got, shading_numpy(0.25, m))
     mk = oracle.pixel_program(tc.lower_source_kernel(text, "make_mask", {}).program, 480, 400)
     assert set(np.unique(mk)) == {0.5, 1.0}
+
+
+def life_numpy(a):
+    c = sum(np.roll(np.roll(a, -di, 0), -dj, 1) for di in (-1, 0, 1) for dj in (-1, 0, 1) if (di, dj) != (0, 0))
+    return ((c == 3) | ((a == 1) & (c == 2))).astype(np.int32)
+
+
+def test_life_example_int_fields_and_neighbour_reads():
+    text = ex("life.py")
+    seed = tc.lower_source_kernel(text, "seed", {})
+    assert seed.kind == "pixel_program" and seed.program.out_kind == pp.OUT_I32
+    st = oracle.pixel_program(seed.program, 320, 320)
+    i, j = np.meshgrid(np.arange(320), np.arange(320), indexing="ij")
+    assert np.array_equal(st, ((i * 37 + j * 91 + i * j) % 7 < 2).astype(np.int32))
+    step = tc.lower_source_kernel(text, "step", {})
+    assert [(f.dtype, f.width) for f in step.inputs] == [("i32", 1)]
+    for _ in range(3):
+        nx = oracle.pixel_program(step.program, 320, 320, [st])
+        assert np.array_equal(nx, life_numpy(st))
+        st = nx
+    back = tc.lower_source_kernel(text, "copy_back", {})
+    assert np.array_equal(oracle.pixel_program(back.program, 320, 320, [st]), st)
+
+
+def test_heat_example_clamped_stencil():
+    text = ex("heat.py")
+    u = oracle.pixel_program(tc.lower_source_kernel(text, "init", {}).program, 384, 256)
+    prog = tc.lower_source_kernel(text, "diffuse", {"k": 0.2}).program
+    for _ in range(3):
+        v = oracle.pixel_program(prog, 384, 256, [u])
+        up = np.concatenate([u[:1], u[:-1]], 0)
+        dn = np.concatenate([u[1:], u[-1:]], 0)
+        lf = np.concatenate([u[:, :1], u[:, :-1]], 1)
+        rt = np.concatenate([u[:, 1:], u[:, -1:]], 1)
+        assert np.array_equal(v, u + f32(0.2) * ((((up + dn) + lf) + rt) - f32(4.0) * u))
+        u = v
+
+
+def test_gather_clamps_and_int_store_truncates():
+    """LOAD_AT clamps its indices to the field (NaN and negatives to 0, past the end to the last
+    row / column); an int32 field store truncates toward zero, NaN gives 0, large values
+    saturate."""
+    b = pp.Builder()
+    vals = b.load(0)
+    rowi = b.op("sub", b.op("mul", b.index(0), 3.0), 5.0)  # 3i - 5: below 0 and past the end
+    colv = b.load(1)                                       # arbitrary per-pixel values
+    prog = pp.compile_program(b, out=b.load_at(0, rowi, colv), in_widths=[1, 1])
+    rng = np.random.default_rng(6)
+    src = rng.standard_normal((9, 7)).astype(np.float32)
+    cols = np.array(rng.choice([-3.0, 0.0, 2.5, 6.9, 7.0, 100.0, np.nan, 1e30], size=(9, 7)), np.float32)
+    got = oracle.pixel_program(prog, 9, 7, [src, cols])
+
+    def index(x, n):
+        return 0 if not x >= 0 else min(int(min(x, 2.0 ** 30)), n - 1)
+
+    want = np.array([[src[index(3 * i - 5.0, 9), index(cols[i, j], 7)] for j in range(7)] for i in range(9)], np.float32)
+    assert np.array_equal(got, want)
+    b = pp.Builder()
+    prog = pp.compile_program(b, out=b.load(0), out_i32=True)
+    x = np.array([[2.7, -2.7, 0.5, -0.5, np.nan, 3e9, -3e9, 2147483520.0, -2147483648.0]], np.float32)
+    got = oracle.pixel_program(prog, 1, 9, [x])
+    assert got.dtype == np.int32
+    assert got.tolist() == [[2, -2, 0, 0, 0, 2147483647, -2147483648, 2147483520, -2147483648]]

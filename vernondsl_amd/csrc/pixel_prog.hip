@@ -28,28 +28,35 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
   if (p.test < VDSL_PIX_TEST_NONE || p.test > VDSL_PIX_TEST_GE) return fail(VDSL_ERR_INVALID_ARG, "pixel program: unknown test");
   if (p.test_a < 0 || p.test_a >= VDSL_PIX_MAX_REGS || p.test_b < 0 || p.test_b >= VDSL_PIX_MAX_REGS)
     return fail(VDSL_ERR_INVALID_ARG, "pixel program: test register out of range");
-  if (p.out_kind != VDSL_PIX_OUT_REG && p.out_kind != VDSL_PIX_OUT_COUNT)
+  if (p.out_kind != VDSL_PIX_OUT_REG && p.out_kind != VDSL_PIX_OUT_COUNT && p.out_kind != VDSL_PIX_OUT_I32)
     return fail(VDSL_ERR_INVALID_ARG, "pixel program: unknown out_kind");
-  if (p.out_width < 1 || p.out_width > 4 || (p.out_kind == VDSL_PIX_OUT_COUNT && p.out_width != 1))
-    return fail(VDSL_ERR_INVALID_ARG, "pixel program: out_width must be 1..4 (1 for a count)");
+  if (p.out_width < 1 || p.out_width > 4 || (p.out_kind != VDSL_PIX_OUT_REG && p.out_width != 1))
+    return fail(VDSL_ERR_INVALID_ARG, "pixel program: out_width must be 1..4 (1 for an int32 field)");
   for (int k = 0; k < p.out_width; ++k)
     if (p.out_regs[k] < 0 || p.out_regs[k] >= VDSL_PIX_MAX_REGS)
       return fail(VDSL_ERR_INVALID_ARG, "pixel program: out_regs out of range");
-  for (int k = 0; k < n_inputs; ++k)
+  for (int k = 0; k < n_inputs; ++k) {
     if (p.in_widths[k] < 1 || p.in_widths[k] > 4) return fail(VDSL_ERR_INVALID_ARG, "pixel program: in_widths must be 1..4");
+    if (p.in_dtypes[k] != VDSL_F32 && !(p.in_dtypes[k] == VDSL_I32 && p.in_widths[k] == 1))
+      return fail(VDSL_ERR_INVALID_ARG, "pixel program: in_dtypes must be VDSL_F32 or VDSL_I32 (one component)");
+  }
   if (p.out_kind == VDSL_PIX_OUT_COUNT && !p.loop) return fail(VDSL_ERR_INVALID_ARG, "pixel program: a count needs a loop");
   const int post0 = p.n_pre + p.n_test + p.n_body;
   for (int pc = 0; pc < total; ++pc) {
     const vdsl_map_instr& s = p.code[pc];
     const std::string at = "pixel program: instruction " + std::to_string(pc);
     const bool map_op = s.op >= VDSL_MAP_LOAD && s.op <= VDSL_MAP_ADD_IMM;
-    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_FLOOR;
+    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_LOAD_AT;
     if (!map_op && !pix_op) return fail(VDSL_ERR_INVALID_ARG, at + ": unknown opcode " + std::to_string(s.op));
     if (s.dst >= VDSL_PIX_MAX_REGS || s.b >= VDSL_PIX_MAX_REGS || s.c >= VDSL_PIX_MAX_REGS)
       return fail(VDSL_ERR_INVALID_ARG, at + ": register out of range");
     if (s.op == VDSL_MAP_LOAD) {
       if (s.a >= n_inputs || s.c >= p.in_widths[s.a])
         return fail(VDSL_ERR_INVALID_ARG, at + ": LOAD of an input or component that is not there");
+    } else if (s.op == VDSL_PIX_LOAD_AT) {
+      const bool comp_ok = s.a < n_inputs && s.imm >= 0.0f && s.imm < static_cast<float>(p.in_widths[s.a]) &&
+                           s.imm == static_cast<float>(static_cast<int>(s.imm));
+      if (!comp_ok) return fail(VDSL_ERR_INVALID_ARG, at + ": LOAD_AT of an input or component that is not there");
     } else if (s.op == VDSL_PIX_INDEX) {
       if (s.a > 1) return fail(VDSL_ERR_INVALID_ARG, at + ": INDEX axis must be 0 (i) or 1 (j)");
     } else if (s.a >= VDSL_PIX_MAX_REGS) {
@@ -82,6 +89,7 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs) {
   };
   list("out_regs", p.out_regs, p.out_width, 0);
   list("in_widths", p.in_widths, n_inputs, 1);
+  list("in_dtypes", p.in_dtypes, n_inputs, VDSL_F32);
   s += "  static constexpr vdsl_map_instr code[VDSL_PIX_MAX_INSTR] = {\n";
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   for (int pc = 0; pc < total; ++pc) {

@@ -34,12 +34,38 @@ struct PixIn {
 };
 
 // One instruction at program counter PC of the table P.
+// Element e, component c of input a (an int32 input is read as float(v)).
+template <class P, int A>
+__device__ __forceinline__ float pix_load(const PixIn& in, unsigned long long e, int c) {
+  if constexpr (P::in_dtypes[A] == VDSL_I32) return static_cast<float>(reinterpret_cast<const int*>(in.p[A])[e]);
+  else return in.p[A][e * P::in_widths[A] + c];
+}
+
+// A field index from a register: 0 if !(x >= 0) (NaN included), else min((int)min(x, 2^30), n-1).
+__device__ __forceinline__ unsigned pix_index(float x, int n) {
+  if (!(x >= 0.0f)) return 0u;
+  const int v = static_cast<int>(fminf(x, 1073741824.0f));
+  return static_cast<unsigned>(v < n - 1 ? v : n - 1);
+}
+
+// A register stored to an int32 field: truncation toward zero, NaN -> 0, saturating.
+__device__ __forceinline__ int pix_to_i32(float x) {
+  if (x != x) return 0;
+  if (x >= 2147483648.0f) return 2147483647;
+  if (x < -2147483648.0f) return -2147483647 - 1;
+  return static_cast<int>(x);
+}
+
 template <class P, int PC>
 __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], unsigned long long o,
-                                         float fi, float fj, float fcount) {
+                                         float fi, float fj, float fcount, int ni, int nj) {
   constexpr vdsl_map_instr s = P::code[PC];
   if constexpr (s.op == VDSL_MAP_LOAD) {
-    r[s.dst] = in.p[s.a][o * P::in_widths[s.a] + s.c];
+    r[s.dst] = pix_load<P, s.a>(in, o, s.c);
+  } else if constexpr (s.op == VDSL_PIX_LOAD_AT) {
+    const unsigned long long e = static_cast<unsigned long long>(pix_index(r[s.b], ni)) * static_cast<unsigned>(nj) +
+                                 pix_index(r[s.c], nj);
+    r[s.dst] = pix_load<P, s.a>(in, e, static_cast<int>(rt.imm[PC]));
   } else if constexpr (s.op == VDSL_PIX_INDEX) {
     r[s.dst] = s.a == 0 ? fi : fj;
   } else if constexpr (s.op == VDSL_PIX_COUNT) {
@@ -67,8 +93,8 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
 
 template <class P, int BASE, int... K>
 __device__ __forceinline__ void pix_section(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], unsigned long long o,
-                                            float fi, float fj, float fcount, Seq<K...>) {
-  (pix_step<P, BASE + K>(rt, in, r, o, fi, fj, fcount), ...);
+                                            float fi, float fj, float fcount, int ni, int nj, Seq<K...>) {
+  (pix_step<P, BASE + K>(rt, in, r, o, fi, fj, fcount, ni, nj), ...);
 }
 
 template <int TEST>
@@ -87,6 +113,7 @@ __device__ constexpr uint32_t pix_reads(const vdsl_map_instr& s) {
     case VDSL_MAP_ADD: case VDSL_MAP_SUB: case VDSL_MAP_MUL: case VDSL_MAP_DIV: case VDSL_MAP_MAX: case VDSL_MAP_MIN:
     case VDSL_PIX_LT: case VDSL_PIX_LE: case VDSL_PIX_EQ: case VDSL_PIX_NE:
       return (1u << s.a) | (1u << s.b);
+    case VDSL_PIX_LOAD_AT: return (1u << s.b) | (1u << s.c);
     case VDSL_MAP_FMA: case VDSL_PIX_SELECT: return (1u << s.a) | (1u << s.b) | (1u << s.c);
     default: return 1u << s.a;
   }
@@ -115,7 +142,7 @@ struct PixSets {
   static constexpr uint32_t loop_w = test_w | body_w;
   static constexpr uint32_t stored() {
     uint32_t m = 0u;
-    if (P::out_kind == VDSL_PIX_OUT_REG)
+    if (P::out_kind != VDSL_PIX_OUT_COUNT)
       for (int k = 0; k < P::out_width; ++k) m |= 1u << P::out_regs[k];
     return m;
   }
@@ -129,8 +156,8 @@ struct PixSets {
 
 template <class P, int BASE, int N>
 __device__ __forceinline__ void pix_run(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], unsigned long long o,
-                                        float fi, float fj, float fcount) {
-  pix_section<P, BASE>(rt, in, r, o, fi, fj, fcount, typename MakeSeq<N>::type{});
+                                        float fi, float fj, float fcount, int ni, int nj) {
+  pix_section<P, BASE>(rt, in, r, o, fi, fj, fcount, ni, nj, typename MakeSeq<N>::type{});
 }
 
 // r[k] <- r[k] where the lane's bit of `mask` is set, else old[k], for the registers in KEEP.
@@ -146,7 +173,7 @@ __device__ __forceinline__ void pix_keep(float (&r)[VDSL_PIX_MAX_REGS], const fl
 // the keep sets hold their values on lanes that are not live.
 template <class P>
 __device__ __forceinline__ void pix_trip(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], unsigned long long o,
-                                         float fi, float fj, uint64_t& lk) {
+                                         float fi, float fj, int ni, int nj, uint64_t& lk) {
   using S = PixSets<P>;
   float old[VDSL_PIX_MAX_REGS];
   if constexpr (S::keep_t != 0u) {
@@ -154,14 +181,14 @@ __device__ __forceinline__ void pix_trip(const PixRt& rt, const PixIn& in, float
     for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) old[k] = r[k];
   }
   const uint64_t start = lk;
-  pix_run<P, S::t0, P::n_test>(rt, in, r, o, fi, fj, 0.0f);
+  pix_run<P, S::t0, P::n_test>(rt, in, r, o, fi, fj, 0.0f, ni, nj);
   pix_keep<S::keep_t>(r, old, start);
   lk &= __builtin_amdgcn_ballot_w64(pix_test<P::test>(r[P::test_a], r[P::test_b]));
   if constexpr (S::keep_b != 0u) {
 #pragma unroll
     for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) old[k] = r[k];
   }
-  pix_run<P, S::b0, P::n_body>(rt, in, r, o, fi, fj, 0.0f);
+  pix_run<P, S::b0, P::n_body>(rt, in, r, o, fi, fj, 0.0f, ni, nj);
   pix_keep<S::keep_b>(r, old, lk);
 }
 
@@ -181,7 +208,7 @@ __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, voi
   float r[VDSL_PIX_MAX_REGS];
 #pragma unroll
   for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) r[k] = 0.0f;
-  pix_run<P, 0, P::n_pre>(rt, in, r, o, fi, fj, 0.0f);
+  pix_run<P, 0, P::n_pre>(rt, in, r, o, fi, fj, 0.0f, ni, nj);
   int count = 0;
   if constexpr (P::loop && P::test == VDSL_PIX_TEST_NONE) {
     // No test: every lane makes max_iter trips; they run only if something after the loop reads
@@ -189,8 +216,8 @@ __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, voi
     const int max_iter = rt.max_iter;
     if constexpr (!S::free_running) {
       for (int t = 0; t < max_iter; ++t) {
-        pix_run<P, S::t0, P::n_test>(rt, in, r, o, fi, fj, 0.0f);
-        pix_run<P, S::b0, P::n_body>(rt, in, r, o, fi, fj, 0.0f);
+        pix_run<P, S::t0, P::n_test>(rt, in, r, o, fi, fj, 0.0f, ni, nj);
+        pix_run<P, S::b0, P::n_body>(rt, in, r, o, fi, fj, 0.0f, ni, nj);
       }
     }
     count = max_iter;
@@ -207,7 +234,7 @@ __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, voi
       uint64_t lk = live;
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        pix_trip<P>(rt, in, r, o, fi, fj, lk);
+        pix_trip<P>(rt, in, r, o, fi, fj, ni, nj, lk);
         m[u] = lk;
       }
       count += block_trips16(m, live);
@@ -230,15 +257,17 @@ __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, voi
     }
     if (t > max_iter - kUnroll && live != 0ull) {
       for (; t < max_iter; ++t) {  // the last max_iter % 16 trips, counted one by one
-        pix_trip<P>(rt, in, r, o, fi, fj, live);
+        pix_trip<P>(rt, in, r, o, fi, fj, ni, nj, live);
         count += lane_select(live, 1, 0);
       }
     }
   }
-  pix_run<P, S::q0, P::n_post>(rt, in, r, o, fi, fj, static_cast<float>(count));
+  pix_run<P, S::q0, P::n_post>(rt, in, r, o, fi, fj, static_cast<float>(count), ni, nj);
   if (inside) {
     if constexpr (P::out_kind == VDSL_PIX_OUT_COUNT) {
       static_cast<int*>(out)[o] = count;
+    } else if constexpr (P::out_kind == VDSL_PIX_OUT_I32) {
+      static_cast<int*>(out)[o] = pix_to_i32(r[P::out_regs[0]]);
     } else {
 #pragma unroll
       for (int k = 0; k < P::out_width; ++k) static_cast<float*>(out)[o * P::out_width + k] = r[P::out_regs[k]];

@@ -255,12 +255,12 @@ def pixel_program(q: Queue, prog, inputs, out: Tensor):
     def field_shape(w):
         return (ni, nj) if w == 1 else (ni, nj, w)
 
-    if prog.out_kind == 1:
+    if prog.out_kind in (1, 2):  # the loop count, or an int32 field
         _expect(out, (ni, nj), "i32", "out")
     else:
         _expect(out, field_shape(prog.out_width), "f32", "out")
     for k, t in enumerate(inputs):
-        _expect(t, field_shape(prog.in_widths[k]), "f32", f"input{k}")
+        _expect(t, field_shape(prog.in_widths[k]), "i32" if prog.in_dtypes[k] == _lib.I32 else "f32", f"input{k}")
     hs = (C.c_void_p * max(1, len(inputs)))(*[t.handle for t in inputs])
     call("vdsl_op_pixel_program", q.handle, ni, nj, C.byref(prog), hs, len(inputs), out.handle)
 

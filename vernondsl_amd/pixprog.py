@@ -26,9 +26,10 @@ from . import _lib
 MAX_INSTR, MAX_REGS, MAX_INPUTS = 128, 32, 4
 OP = dict(_lib.MAP_OPS)
 OP.update({"index": 32, "cos": 33, "sin": 34, "count": 35, "lt": 36, "le": 37, "eq": 38, "ne": 39, "select": 40,
-           "floor": 41})
+           "floor": 41, "load_at": 42})
 TESTS = {"none": 0, "lt": 1, "le": 2, "gt": 3, "ge": 4}
-OUT_REG, OUT_COUNT = 0, 1
+OUT_REG, OUT_COUNT, OUT_I32 = 0, 1, 2
+F32, I32 = _lib.F32, _lib.I32  # input dtypes (vdsl_dtype)
 COUNT = "count"  # compile_program(out=COUNT): store the loop's update count (an int32 field)
 
 UNARY = ("neg", "abs", "sqrt", "exp", "log", "tanh", "sigmoid", "cos", "sin", "recip", "square", "floor")
@@ -41,7 +42,8 @@ class PixelProgram(C.Structure):
     _fields_ = [("n_pre", C.c_int32), ("n_test", C.c_int32), ("n_body", C.c_int32), ("n_post", C.c_int32),
                 ("loop", C.c_int32), ("max_iter", C.c_int32), ("test", C.c_int32), ("test_a", C.c_int32),
                 ("test_b", C.c_int32), ("out_kind", C.c_int32), ("out_width", C.c_int32), ("out_regs", C.c_int32 * 4),
-                ("in_widths", C.c_int32 * MAX_INPUTS), ("code", _lib.MapInstr * MAX_INSTR)]
+                ("in_widths", C.c_int32 * MAX_INPUTS), ("in_dtypes", C.c_int32 * MAX_INPUTS),
+                ("code", _lib.MapInstr * MAX_INSTR)]
 
 
 class ProgramError(ValueError):
@@ -96,6 +98,14 @@ class Builder:
         if not 0 <= component < 4:
             raise ProgramError("a field has at most 4 components")
         return self._node("load", val=(int(k), int(component)))
+
+    def load_at(self, k: int, row, col, component: int = 0) -> Node:
+        """Component `component` of input field k at [row][col] (per-pixel values, clamped to the
+        field when the program runs)."""
+        if not 0 <= k < MAX_INPUTS:
+            raise ProgramError(f"at most {MAX_INPUTS} input fields")
+        args = tuple(a if isinstance(a, Node) else self.const(a) for a in (row, col))
+        return self._node("load_at", args, val=(int(k), int(component)))
 
     def state(self, name: str) -> Node:
         return self._node("state", val=name)
@@ -195,6 +205,8 @@ class _Emitter:
             op, a = OP["index"], n.val
         elif k == "load":
             op, a, c = OP["load"], n.val[0], n.val[1]
+        elif k == "load_at":
+            op, a, b, c, imm = OP["load_at"], n.val[0], srcs[0], srcs[1], float(n.val[1])
         elif k == "count":
             op = OP["count"]
         elif k == "state":
@@ -225,13 +237,15 @@ def _node_of(b: Builder, v) -> Node:
 
 
 def compile_program(b: Builder, init: dict | None = None, test=None, body: dict | None = None, max_iter: int = 0,
-                    out=None, loop: bool | None = None, in_widths=()) -> PixelProgram:
+                    out=None, loop: bool | None = None, in_widths=(), in_dtypes=(), out_i32: bool = False) -> PixelProgram:
     """init: {state name: initial Node or number}; test: (op, lhs, rhs) with op in lt/le/gt/ge (None:
     no test), both sides per-pixel values; body: {state name: new value} (the parallel update of
     one loop trip; names not listed keep their value); max_iter: most updates; out: the stored
     value (a Node using states, count() and invariants; a list or tuple of 1-4 of them for a
     field of vectors) or COUNT.  loop defaults to whether a body or test is given.  in_widths:
-    components per pixel of each input field (default 1)."""
+    components per pixel of each input field (default 1); in_dtypes: F32 or I32 per input (an
+    int32 field of one component, read as float); out_i32: store the (single) value into an int32
+    field, truncating as a Taichi int field assignment does."""
     init = dict(init or {})
     body = dict(body or {})
     loop = bool(body or test) if loop is None else bool(loop)
@@ -331,6 +345,10 @@ def compile_program(b: Builder, init: dict | None = None, test=None, body: dict 
     else:
         regs = _Emitter(code, pinned, reserved).emit(outs)
         out_regs = [regs[n] for n in outs]
+        if out_i32:
+            if len(outs) != 1:
+                raise ProgramError("an int32 field stores one value per pixel")
+            out_kind = OUT_I32
     n_post = len(code) - n_pre - n_test - n_body
     p = PixelProgram()
     p.n_pre, p.n_test, p.n_body, p.n_post = n_pre, n_test, n_body, n_post
@@ -340,10 +358,14 @@ def compile_program(b: Builder, init: dict | None = None, test=None, body: dict 
     for k, r in enumerate(out_regs):
         p.out_regs[k] = r
     widths = list(in_widths) + [1] * (MAX_INPUTS - len(in_widths))
+    dtypes = list(in_dtypes) + [F32] * (MAX_INPUTS - len(in_dtypes))
     for k in range(MAX_INPUTS):
         if not 1 <= widths[k] <= 4:
             raise ProgramError("an input field has 1 to 4 components")
+        if dtypes[k] not in (F32, I32) or (dtypes[k] == I32 and widths[k] != 1):
+            raise ProgramError("an input field is f32, or int32 of one component")
         p.in_widths[k] = widths[k]
+        p.in_dtypes[k] = dtypes[k]
     for k, ins in enumerate(code):
         p.code[k] = ins
     return p

@@ -635,9 +635,16 @@ def _parse_source(text: str, kernel_name: str, args: dict):
             if isinstance(v, ast.Call) and isinstance(v.func, ast.Attribute) and v.func.attr == "field":
                 kw = {k.arg: k.value for k in v.keywords}
                 is_vec = isinstance(v.func.value, ast.Attribute) and v.func.value.attr == "Vector"
+                pos = list(v.args)
                 width = 1
-                if is_vec:
-                    width = interp.expr(kw["n"] if "n" in kw else v.args[0], {})
+                if is_vec:  # ti.Vector.field(n, dtype, shape)
+                    width = interp.expr(kw["n"] if "n" in kw else pos.pop(0), {})
+                elif "n" in kw:
+                    raise TaichiLoweringError("ti.field takes no component count")
+                if "dtype" not in kw and pos:  # ti.field(dtype, shape)
+                    kw["dtype"] = pos.pop(0)
+                if "shape" not in kw and pos:
+                    kw["shape"] = pos.pop(0)
                 shape = interp.expr(kw["shape"], {})
                 dt = kw.get("dtype")
                 dtype = f32 if dt is None or (isinstance(dt, ast.Name) and dt.id == "float") else (
@@ -766,6 +773,8 @@ class _PixInterp:
     def unary(self, fn, x):
         if isinstance(x, _PVec):
             return _PVec([self.unary(fn, c) for c in x.comps])
+        if isinstance(x, (int, np.integer)) and not isinstance(x, bool) and fn in ("neg", "abs"):
+            return -int(x) if fn == "neg" else abs(int(x))  # integers stay exact integers
         if _is_num(x):
             v = np.float32(x)
             with np.errstate(all="ignore"):
@@ -847,20 +856,31 @@ class _PixInterp:
         raise TaichiLoweringError(f"expression {ast.dump(n)[:60]} is not supported")
 
     def field_read(self, fld, idx, local):
-        if not (isinstance(idx, ast.Tuple) and [getattr(e, "id", None) for e in idx.elts] == [self.iname, self.jname]):
-            raise TaichiLoweringError("fields are read at [i, j] of the struct-for only")
-        if fld is self.fld and _STORE in local:
+        """fld[i, j] (this pixel), or fld[e1, e2] at per-pixel indices (a stencil or gather read,
+        clamped to the field, whose shape must be the struct-for's)."""
+        if not (isinstance(idx, ast.Tuple) and len(idx.elts) == 2):
+            raise TaichiLoweringError("fields are 2-D: read them as field[i, j]")
+        here = [getattr(e, "id", None) for e in idx.elts] == [self.iname, self.jname]
+        if here and fld is self.fld and _STORE in local:
             return local[_STORE]  # the value this pixel stored earlier in the body
-        if fld.shape != self.shape or fld.dtype != f32:
-            raise TaichiLoweringError("a field read must be an f32 field of the iterated field's shape")
+        if fld.shape != self.shape:
+            raise TaichiLoweringError("a field read must be of a field of the struct-for's shape")
         if fld not in self.inputs:
             if len(self.inputs) == self.pp.MAX_INPUTS:
                 raise TaichiLoweringError(f"at most {self.pp.MAX_INPUTS} fields can be read")
             self.inputs.append(fld)
         k = self.inputs.index(fld)
+        if here:
+            if fld.width == 1:
+                return self.b.load(k)
+            return _PVec([self.b.load(k, c) for c in range(fld.width)])
+        row, col = (self.expr(e, local) for e in idx.elts)
+        if isinstance(row, _PVec) or isinstance(col, _PVec):
+            raise TaichiLoweringError("field indices are scalars")
+        row, col = self.node(row), self.node(col)
         if fld.width == 1:
-            return self.b.load(k)
-        return _PVec([self.b.load(k, c) for c in range(fld.width)])
+            return self.b.load_at(k, row, col)
+        return _PVec([self.b.load_at(k, row, col, c) for c in range(fld.width)])
 
     def call(self, n, local):
         f = n.func
@@ -1120,8 +1140,6 @@ class _PixInterp:
                 if self.fld is None:
                     raise TaichiLoweringError("no output field")
                 if keep is None:
-                    if self.fld.dtype != f32:
-                        raise TaichiLoweringError("an i32 field must be stored on every path")
                     keep = self.field_read(self.fld, ast.Tuple(elts=[ast.Name(id=self.iname), ast.Name(id=self.jname)]), {})
                 vt = keep if vt is _ONE_BRANCH else vt
                 vf = keep if vf is _ONE_BRANCH else vf
@@ -1323,17 +1341,20 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
         raise TaichiLoweringError("the struct-for body must store field[i, j] = ...")
     fld = ip.fld
     v = local[_STORE]
+    out_i32 = False
     if fld.dtype == i32:
-        if not (isinstance(v, pp.Node) and v.kind == "count"):
-            raise TaichiLoweringError("an i32 field stores the loop counter")
-        out = pp.COUNT
+        if isinstance(v, pp.Node) and v.kind == "count":
+            out = pp.COUNT
+        else:  # any value, truncated as Taichi's int field assignment does
+            out, out_i32 = (v if isinstance(v, pp.Node) else float(_f32(v))), True
     elif isinstance(v, _PVec):
         out = [c if isinstance(c, pp.Node) else float(_f32(c)) for c in v.comps]
     else:
         out = v if isinstance(v, pp.Node) else float(_f32(v))
     try:
         prog = pp.compile_program(b, init=init, test=test, body=new_state, max_iter=max_iter, out=out, loop=has_loop,
-                                  in_widths=[f.width for f in ip.inputs])
+                                  in_widths=[f.width for f in ip.inputs],
+                                  in_dtypes=[pp.I32 if f.dtype == i32 else pp.F32 for f in ip.inputs], out_i32=out_i32)
     except pp.ProgramError as e:
         raise TaichiLoweringError(str(e)) from None
     return Lowered("pixel_program", fld, program=prog, inputs=ip.inputs)
