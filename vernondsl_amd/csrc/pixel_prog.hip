@@ -69,7 +69,17 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
 
 // The program's table as C++ source (opcodes and registers; immediates stay kernel arguments).
 // It names the kernel completely, so it is also the cache key.
-std::string program_source(const vdsl_pixel_program& p, int n_inputs) {
+// Blocks of 4 rows x 256 pixels for programs whose pixels all do the same work (no escape loop),
+// while the row count fits the grid's y extent; 16x16 patches otherwise.
+// Rows per block in the row mapping (each thread runs that many pixels of its column): 4 and 8
+// measure alike on memory-bound programs, 2 and 16 lower.
+constexpr int kRowsPerBlock = 4;
+
+bool row_mapping(const vdsl_pixel_program& p, int ni) {
+  return !(p.loop && p.test != VDSL_PIX_TEST_NONE) && (ni + kRowsPerBlock - 1) / kRowsPerBlock <= 65535;
+}
+
+std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni) {
   std::string s = "#include \"pixprog_kern.h\"\nnamespace vdsl {\nstruct PixJit {\n";
   auto c = [&](const char* name, int v) { s += std::string("  static constexpr int ") + name + " = " + std::to_string(v) + ";\n"; };
   c("n_pre", p.n_pre);
@@ -82,6 +92,7 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs) {
   c("test_b", p.test_b);
   c("out_kind", p.out_kind);
   c("out_width", p.out_width);
+  c("rows", row_mapping(p, ni) ? kRowsPerBlock : 0);
   // Entries past out_width / n_inputs are not used: written as 0 / 1, so they do not split the cache.
   auto list = [&](const char* name, const int32_t* v, int n, int fill) {
     s += std::string("  static constexpr int ") + name + "[4] = {";
@@ -130,7 +141,7 @@ extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   for (int pc = 0; pc < total; ++pc) rt.imm[pc] = p.code[pc].imm;
   rt.max_iter = p.max_iter;
-  const std::string src = program_source(p, n_inputs);
+  const std::string src = program_source(p, n_inputs, ni);
   const char* const entries[] = {"vdsl_pix_jit"};
   const JitKernels* k = nullptr;
   const int st = jit_kernels(q->dev->ordinal, src, entries, 1, q->capturing, g_pix_jit, "pixel program", &k);
@@ -139,7 +150,9 @@ extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const
   VDSL_TRY(st);
   void* o = out->ptr;
   void* args[] = {&rt, &in, &o, &ni, &nj};
-  return check_hip(hipModuleLaunchKernel(k->fn[0], static_cast<unsigned>((nj + 15) / 16), static_cast<unsigned>((ni + 15) / 16), 1,
-                                         256, 1, 1, 0, q->stream, args, nullptr),
+  const bool rows = row_mapping(p, ni);
+  const unsigned gx = rows ? static_cast<unsigned>((nj + 255) / 256) : static_cast<unsigned>((nj + 15) / 16);
+  const unsigned gy = rows ? static_cast<unsigned>((ni + kRowsPerBlock - 1) / kRowsPerBlock) : static_cast<unsigned>((ni + 15) / 16);
+  return check_hip(hipModuleLaunchKernel(k->fn[0], gx, gy, 1, 256, 1, 1, 0, q->stream, args, nullptr),
                    "hipModuleLaunchKernel(pixel program)");
 }

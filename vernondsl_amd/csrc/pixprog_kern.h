@@ -5,8 +5,9 @@
 // Shares apply_op with the map chains (mapchain_kern.h), so an opcode means the same arithmetic in
 // both op classes.  Uses nothing from the C++ standard library (hiprtc has none).
 //
-// Mapping: one lane per pixel; each wave takes an 8x8 tile (lanes of a tile tend to leave an
-// escape loop at similar trips) and a 256-lane block a 16x16 patch.  The loop is the escape-time
+// Mapping: one lane per pixel.  For a program with an escape loop each wave takes an 8x8 tile
+// (lanes of a tile tend to leave the loop at similar trips) and a 256-lane block a 16x16 patch;
+// any other program runs 256 consecutive pixels of a row per block (coalesced memory access).  The loop is the escape-time
 // kernel's (escape_time.hip) made general: wave-uniform, in blocks of 16 trips, with the live set
 // a sticky 64-bit lane mask (one ballot and one scalar AND per trip) and the count added per
 // block from the block's masks (lanemask.h).  Every lane runs every trip of its wave; what a lane
@@ -195,12 +196,10 @@ __device__ __forceinline__ void pix_trip(const PixRt& rt, const PixIn& in, float
 // P: the program table (n_pre, n_test, n_body, n_post, loop, test, test_a, test_b, out_kind,
 // out_width, out_regs[], in_widths[], code[]).  out: f32 [ni][nj][out_width] or int32 [ni][nj].
 template <class P>
-__device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, void* __restrict__ out, int ni, int nj) {
+__device__ __forceinline__ void pixel_at(const PixRt& rt, const PixIn& in, void* __restrict__ out, int ni, int nj, int i,
+                                         int j) {
   using S = PixSets<P>;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int i = blockIdx.y * 16 + (wave >> 1) * 8 + (lane >> 3);
-  const int j = blockIdx.x * 16 + (wave & 1) * 8 + (lane & 7);
   const bool inside = i < ni && j < nj;
   // Lanes past the grid run the program on pixel (0, 0), are never live, and store nothing.
   const unsigned long long o = inside ? static_cast<unsigned long long>(i) * static_cast<unsigned>(nj) + j : 0ull;
@@ -272,6 +271,24 @@ __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, voi
 #pragma unroll
       for (int k = 0; k < P::out_width; ++k) static_cast<float*>(out)[o * P::out_width + k] = r[P::out_regs[k]];
     }
+  }
+}
+
+// P::rows > 0: a block takes 256 consecutive pixels of P::rows rows (programs whose pixels all
+// do the same work, where memory access is what counts: every load and store of a wave is 256
+// contiguous bytes, and a thread runs several pixels); otherwise 8x8 tiles per wave and a 16x16
+// patch per block (escape loops, whose lanes leave at different trips).
+template <class P>
+__device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, void* __restrict__ out, int ni, int nj) {
+  if constexpr (P::rows > 0) {
+    const int j = static_cast<int>(blockIdx.x * 256 + threadIdx.x);
+#pragma unroll
+    for (int t = 0; t < P::rows; ++t) pixel_at<P>(rt, in, out, ni, nj, static_cast<int>(blockIdx.y) * P::rows + t, j);
+  } else {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    pixel_at<P>(rt, in, out, ni, nj, static_cast<int>(blockIdx.y * 16 + (wave >> 1) * 8 + (lane >> 3)),
+                static_cast<int>(blockIdx.x * 16 + (wave & 1) * 8 + (lane & 7)));
   }
 }
 
