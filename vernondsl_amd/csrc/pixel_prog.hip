@@ -67,18 +67,27 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
   return VDSL_OK;
 }
 
-// The program's table as C++ source (opcodes and registers; immediates stay kernel arguments).
-// It names the kernel completely, so it is also the cache key.
-// Blocks of 4 rows x 256 pixels for programs whose pixels all do the same work (no escape loop),
-// while the row count fits the grid's y extent; 16x16 patches otherwise.
-// Rows per block in the row mapping (each thread runs that many pixels of its column): 4 and 8
-// measure alike on memory-bound programs, 2 and 16 lower.
-constexpr int kRowsPerBlock = 4;
-
-bool row_mapping(const vdsl_pixel_program& p, int ni) {
-  return !(p.loop && p.test != VDSL_PIX_TEST_NONE) && (ni + kRowsPerBlock - 1) / kRowsPerBlock <= 65535;
+// Rows per block in the row mapping (each thread evaluates that many pixels of its column, then
+// stores them).  Measured on 8192^2 f32: y = 2x + 1 runs best with 4 (1, 2, 8, 16 rows: 61-96%
+// of its rate), a five-point stencil with 8 (its neighbours' rows are then shared within the
+// block; 4 rows: 93%), so programs with gathers take 8.
+int rows_per_block(const vdsl_pixel_program& p) {
+  const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
+  for (int pc = 0; pc < total; ++pc)
+    if (p.code[pc].op == VDSL_PIX_LOAD_AT) return 8;
+  return 4;
 }
 
+// Blocks of rows_per_block rows x 256 pixels for programs whose pixels all do the same work (no
+// escape loop), while the row count fits the grid's y extent; 16x16 patches otherwise.  0 for
+// the patches.
+int row_mapping(const vdsl_pixel_program& p, int ni) {
+  const int rows = rows_per_block(p);
+  return !(p.loop && p.test != VDSL_PIX_TEST_NONE) && (ni + rows - 1) / rows <= 65535 ? rows : 0;
+}
+
+// The program's table as C++ source (opcodes and registers; immediates stay kernel arguments).
+// It names the kernel completely, so it is also the cache key.
 std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni) {
   std::string s = "#include \"pixprog_kern.h\"\nnamespace vdsl {\nstruct PixJit {\n";
   auto c = [&](const char* name, int v) { s += std::string("  static constexpr int ") + name + " = " + std::to_string(v) + ";\n"; };
@@ -92,7 +101,7 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni) {
   c("test_b", p.test_b);
   c("out_kind", p.out_kind);
   c("out_width", p.out_width);
-  c("rows", row_mapping(p, ni) ? kRowsPerBlock : 0);
+  c("rows", row_mapping(p, ni));
   // Entries past out_width / n_inputs are not used: written as 0 / 1, so they do not split the cache.
   auto list = [&](const char* name, const int32_t* v, int n, int fill) {
     s += std::string("  static constexpr int ") + name + "[4] = {";
@@ -150,9 +159,9 @@ extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const
   VDSL_TRY(st);
   void* o = out->ptr;
   void* args[] = {&rt, &in, &o, &ni, &nj};
-  const bool rows = row_mapping(p, ni);
+  const int rows = row_mapping(p, ni);
   const unsigned gx = rows ? static_cast<unsigned>((nj + 255) / 256) : static_cast<unsigned>((nj + 15) / 16);
-  const unsigned gy = rows ? static_cast<unsigned>((ni + kRowsPerBlock - 1) / kRowsPerBlock) : static_cast<unsigned>((ni + 15) / 16);
+  const unsigned gy = rows ? static_cast<unsigned>((ni + rows - 1) / rows) : static_cast<unsigned>((ni + 15) / 16);
   return check_hip(hipModuleLaunchKernel(k->fn[0], gx, gy, 1, 256, 1, 1, 0, q->stream, args, nullptr),
                    "hipModuleLaunchKernel(pixel program)");
 }

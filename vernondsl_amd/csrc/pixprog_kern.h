@@ -193,13 +193,13 @@ __device__ __forceinline__ void pix_trip(const PixRt& rt, const PixIn& in, float
   pix_keep<S::keep_b>(r, old, lk);
 }
 
-// P: the program table (n_pre, n_test, n_body, n_post, loop, test, test_a, test_b, out_kind,
-// out_width, out_regs[], in_widths[], code[]).  out: f32 [ni][nj][out_width] or int32 [ni][nj].
+// Pixel (i, j) of program P (the program table: n_pre, n_test, n_body, n_post, loop, test, test_a,
+// test_b, out_kind, out_width, out_regs[], in_widths[], code[]): its stored registers into res,
+// its trip count into count.
 template <class P>
-__device__ __forceinline__ void pixel_at(const PixRt& rt, const PixIn& in, void* __restrict__ out, int ni, int nj, int i,
-                                         int j) {
+__device__ __forceinline__ void pixel_eval(const PixRt& rt, const PixIn& in, int ni, int nj, int i, int j, float (&res)[4],
+                                           int& count_out) {
   using S = PixSets<P>;
-  const int lane = threadIdx.x & 63;
   const bool inside = i < ni && j < nj;
   // Lanes past the grid run the program on pixel (0, 0), are never live, and store nothing.
   const unsigned long long o = inside ? static_cast<unsigned long long>(i) * static_cast<unsigned>(nj) + j : 0ull;
@@ -262,33 +262,54 @@ __device__ __forceinline__ void pixel_at(const PixRt& rt, const PixIn& in, void*
     }
   }
   pix_run<P, S::q0, P::n_post>(rt, in, r, o, fi, fj, static_cast<float>(count), ni, nj);
-  if (inside) {
-    if constexpr (P::out_kind == VDSL_PIX_OUT_COUNT) {
-      static_cast<int*>(out)[o] = count;
-    } else if constexpr (P::out_kind == VDSL_PIX_OUT_I32) {
-      static_cast<int*>(out)[o] = pix_to_i32(r[P::out_regs[0]]);
-    } else {
 #pragma unroll
-      for (int k = 0; k < P::out_width; ++k) static_cast<float*>(out)[o * P::out_width + k] = r[P::out_regs[k]];
-    }
+  for (int k = 0; k < 4; ++k) res[k] = k < P::out_width ? r[P::out_regs[k]] : 0.0f;
+  count_out = count;
+}
+
+// Stores what pixel_eval gave for pixel (i, j), if it lies in the grid.  out: f32
+// [ni][nj][out_width] or int32 [ni][nj].
+template <class P>
+__device__ __forceinline__ void pixel_store(void* __restrict__ out, int ni, int nj, int i, int j, const float (&res)[4],
+                                            int count) {
+  if (i >= ni || j >= nj) return;
+  const unsigned long long o = static_cast<unsigned long long>(i) * static_cast<unsigned>(nj) + j;
+  if constexpr (P::out_kind == VDSL_PIX_OUT_COUNT) {
+    static_cast<int*>(out)[o] = count;
+  } else if constexpr (P::out_kind == VDSL_PIX_OUT_I32) {
+    static_cast<int*>(out)[o] = pix_to_i32(res[0]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < P::out_width; ++k) static_cast<float*>(out)[o * P::out_width + k] = res[k];
   }
 }
 
 // P::rows > 0: a block takes 256 consecutive pixels of P::rows rows (programs whose pixels all
 // do the same work, where memory access is what counts: every load and store of a wave is 256
-// contiguous bytes, and a thread runs several pixels); otherwise 8x8 tiles per wave and a 16x16
-// patch per block (escape loops, whose lanes leave at different trips).
+// contiguous bytes).  A thread evaluates its P::rows pixels before it stores any of them, so the
+// loads of all of them are in flight together (a store between them would hold every later load
+// back, since the output may be an input).  Pixels read their own inputs before anything is
+// stored, and a read of another pixel's element that the same launch writes has no defined
+// order in any mapping.  Otherwise 8x8 tiles per wave and a 16x16 patch per block (escape loops,
+// whose lanes leave at different trips).
 template <class P>
 __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, void* __restrict__ out, int ni, int nj) {
+  float res[P::rows > 0 ? P::rows : 1][4];
+  int count[P::rows > 0 ? P::rows : 1];
   if constexpr (P::rows > 0) {
     const int j = static_cast<int>(blockIdx.x * 256 + threadIdx.x);
+    const int i0 = static_cast<int>(blockIdx.y) * P::rows;
 #pragma unroll
-    for (int t = 0; t < P::rows; ++t) pixel_at<P>(rt, in, out, ni, nj, static_cast<int>(blockIdx.y) * P::rows + t, j);
+    for (int t = 0; t < P::rows; ++t) pixel_eval<P>(rt, in, ni, nj, i0 + t, j, res[t], count[t]);
+#pragma unroll
+    for (int t = 0; t < P::rows; ++t) pixel_store<P>(out, ni, nj, i0 + t, j, res[t], count[t]);
   } else {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    pixel_at<P>(rt, in, out, ni, nj, static_cast<int>(blockIdx.y * 16 + (wave >> 1) * 8 + (lane >> 3)),
-                static_cast<int>(blockIdx.x * 16 + (wave & 1) * 8 + (lane & 7)));
+    const int i = static_cast<int>(blockIdx.y * 16 + (wave >> 1) * 8 + (lane >> 3));
+    const int j = static_cast<int>(blockIdx.x * 16 + (wave & 1) * 8 + (lane & 7));
+    pixel_eval<P>(rt, in, ni, nj, i, j, res[0], count[0]);
+    pixel_store<P>(out, ni, nj, i, j, res[0], count[0]);
   }
 }
 
