@@ -446,7 +446,58 @@ def bench_pixel_program(dev, q, steps, warmup, do_cpu):
                                              "Gpix-iter/s", "the full 1024x1024 grid")
         res.append(r)
     out.free()
+    res.append(bench_pixel_stencil(dev, q, steps, warmup, do_cpu))
     return res
+
+
+HEAT_N = 8192
+
+
+def heat_program(n=HEAT_N):
+    """examples/heat.py's diffuse kernel (a clamped five-point stencil, k = 0.2) lowered for an n x n
+    plate: the example's W, H set to n."""
+    from vernondsl_amd import taichi_compat as tc
+    text = open(os.path.join(ROOT, "vernondsl_amd", "examples", "heat.py")).read()
+    text = text.replace("W, H = 384, 256", f"W, H = {n}, {n}")
+    return tc.lower_source_kernel(text, "diffuse", {"k": 0.2}).program
+
+
+def bench_pixel_stencil(dev, q, steps, warmup, do_cpu):
+    """A memory-bound struct-for body by the general path: examples/heat.py's diffusion step on an
+    8192 x 8192 f32 plate (one field read through five clamped gathers, one written: 8 B per pixel
+    reach HBM when the neighbours' rows are reused on chip)."""
+    from vernondsl_amd import kernels, rng, spec
+    from vernondsl_amd.rhi import Tensor
+    n = HEAT_N
+    prog = heat_program(n)
+    u = rng.uniform(spec.SEEDS[2] + 7, n * n).reshape(n, n)
+    tu, tv = Tensor.from_numpy(dev, q, u), Tensor(dev, (n, n), "f32")
+    ms, _ = time_replays(q, dev, lambda: kernels.pixel_program(q, prog, [tu], tv), max(10, steps // 5), warmup,
+                         per_graph=10)
+    nbytes = 8 * n * n
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    parity = NOT_CHECKED
+    if do_cpu:  # CPU-baseline leg (timed below); its output is the checker, on the border and middle rows
+        from oracle import oracle
+        got = tv.numpy(q)
+        bad = 0
+        for r0 in (0, n // 2 - 1, n - 3):
+            ref = oracle.pixel_program(prog, n, n, [u], rows=(r0, r0 + 3))
+            bad += int((got[r0:r0 + 3].view(np.uint32) != ref.view(np.uint32)).sum())
+        parity = "ok (rows 0-2, 4095-4097, 8189-8191 bit-exact)" if bad == 0 else f"FAIL {bad} px"
+    r = {"config": "1-general-hbm", "workload": f"heat diffusion step {n}x{n} f32 (examples/heat.py's diffuse "
+                                                "kernel, W = H = 8192), vdsl_op_pixel_program",
+         "metric": "achieved HBM GB/s", "value": gbs, "unit": "GB/s", "ms_per_launch": ms, "parity": parity,
+         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                      "bytes_per_launch": nbytes, "traffic": measured_traffic("pixel_stencil")}}
+    if do_cpu:
+        n1 = 1024
+        r["cpu_baseline"] = cpu_baseline(
+            oracle, lambda: oracle.pixel_program(prog, n, n, [u]), nbytes / 1e9, "GB/s", f"the full {n}x{n} plate",
+            lambda: oracle.pixel_program(prog, n, n, [u], rows=(0, n1)), 8 * n1 * n / 1e9, f"first {n1} of {n} rows")
+    tu.free()
+    tv.free()
+    return r
 
 
 # ---- config 3 ------------------------------------------------------------------------------------
@@ -615,6 +666,8 @@ def _traffic_kernels():
         "vec_transform": ("vec_transform", "vec_transform_kernel", None, (1 << 24) * 40),
         # vec4 [4096][4096] read and written
         "swizzle": ("swizzle", "vdsl_map_jit", None, 2 * 4096 * 4096 * 16),  # the chain compiled at run time
+        # heat.py's stencil on 8192^2 f32: the field read once, the result written once
+        "pixel_stencil": ("pixel_stencil", "vdsl_pix_jit", None, 8 * HEAT_N * HEAT_N),
         # config 4 (2048 x 4096 x 4096 and 4096 x 4096 x 2048 bf16): operands read once, outputs written once
         # X, W1 read; H (bf16) and GELU'(pre) (f32) written
         "c4:linear": ("c4_step", _C4_BPK + "0, true>", None, (16 + 32 + 16 + 32) * _MB),
@@ -736,6 +789,11 @@ def run_kernel_only(dev, q, name, reps):
         tx.buffer.fill_u32(q, 0x3F800000)
         prog = mc.compile(mc.VecInput(0, 4).bgra)
         fn, ts = (lambda: kernels.map_chain_v(q, prog, [tx], ty)), [tx, ty]
+    elif name == "pixel_stencil":
+        prog = heat_program()
+        tu, tv = Tensor(dev, (HEAT_N, HEAT_N), "f32"), Tensor(dev, (HEAT_N, HEAT_N), "f32")
+        tu.buffer.fill_u32(q, 0x3F000000)
+        fn, ts = (lambda: kernels.pixel_program(q, prog, [tu], tv)), [tu, tv]
     elif name == "escape_time":
         p = kernels.escape_time_params(**spec.mandelbrot_params())
         out = Tensor(dev, (1024, 1024), "i32")
@@ -765,7 +823,8 @@ def main():
     ap.add_argument("--only", type=int, default=0, help="run only the headline and one extra config "
                     "(1, 3, 4, 5; 2: the generic map chains; 6: the vector ops)")
     ap.add_argument("--kernel", default="", help="run one kernel --reps times and exit (for rocprofv3 --pmc): "
-                    "map_chain, softmax_f32, softmax_bf16, gemm_bf16, gemm_w8a8, escape_time, copy, c4_step, c5_step")
+                    "map_chain, softmax_f32, softmax_bf16, gemm_bf16, gemm_w8a8, escape_time, pixel_stencil, vec_transform, "
+                    "swizzle, copy, c4_step, c5_step")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--traffic-summary", default="", metavar="DIR",
                     help="write profiles/traffic.json from the counter runs in DIR and exit (no GPU needed)")
