@@ -424,6 +424,37 @@ def test_quantize_rows(dev, q, rows, cols, dt):
         t.free()
 
 
+@pytest.mark.parametrize("cols,dt", [(8192, "bf16"), (16384, "bf16"), (4096, "f32"), (8192, "f32")])
+def test_quantize_rows_ties_and_scales(dev, q, cols, dt):
+    """Rows that exercise the register-resident kernel's IEEE-division fallback: exact rounding ties
+    (amax = 127/64, so s = 1/64 and x / s = 64 x hits k + 1/2), scales below 2^-120 and above 2^120,
+    a zero row, and ordinary rows; bit for bit against the oracle's rintf(x / s)."""
+    rows = 8
+    x = rng.normal(43, rows * cols).reshape(rows, cols)
+    k = np.arange(cols) % 127
+    x[0] = ((2 * k + 1) / 128.0) * np.where(np.arange(cols) % 2, 1.0, -1.0)
+    x[0, 5] = 127.0 / 64.0
+    x[1] *= 2e-35
+    x[2] *= 1e37
+    x[2, 7] = 3e38
+    x[3] = 0
+    x = x.astype(np.float32)
+    xh = rng.f32_to_bf16(x) if dt == "bf16" else x
+    if dt == "bf16":
+        assert rng.bf16_to_f32(xh[0, 5:6])[0] == np.float32(127.0 / 64.0)
+    tx = Tensor.from_numpy(dev, q, xh, dt)
+    tq, ts = Tensor(dev, (rows, cols), "i8"), Tensor(dev, (rows,), "f32")
+    kernels.quantize_rows_i8(q, tx, tq, ts)
+    rq, rs = oracle.quantize_rows_i8(xh)
+    assert rs[0] == np.float32(1.0 / 64.0) and rs[1] < 2.0**-120 and rs[2] > 2.0**120
+    assert np.array_equal(ts.numpy(q), rs)
+    got = tq.numpy(q)
+    bad = np.argwhere(got != rq)
+    assert bad.size == 0, f"{len(bad)} differ, first at {bad[:4].tolist()}"
+    for t in (tx, tq, ts):
+        t.free()
+
+
 @pytest.mark.parametrize("M,N,K,relu,dt", [(512, 8192, 8192, True, "bf16"), (512, 1024, 8192, False, "bf16"),
                                            (100, 70, 48, True, "f32"), (128, 128, 4096, False, "f32"),
                                            (33, 257, 272, True, "bf16")])

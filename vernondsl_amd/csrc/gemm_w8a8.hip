@@ -240,6 +240,30 @@ __global__ __launch_bounds__(BT) void quantize_rows_resident(const void* __restr
   const float s = amax / 127.0f;
   if (threadIdx.x == 0) scale[row] = s;
   int8_t* dst = q + row * COLS;
+  // rint(x / s) without a division per element: q = x * rcp(s) lies within 2.7e-5 of x / s (|x / s|
+  // <= 127, rcp within 1 ulp, one rounding of the product), and fl(x / s) within 3.8e-6 (half an
+  // ulp at 127), so both round to the same integer unless x / s is within 3.1e-5 of a half-integer.
+  // A lane with a quotient within 1.2e-4 of one (or a row whose s is outside [2^-120, 2^120], where
+  // the reciprocal may flush or lose accuracy) takes the IEEE division instead: the same bits as
+  // rintf(x / s) throughout.
+  const float rs = __builtin_amdgcn_rcpf(s);
+  const bool fast = s >= 0x1p-120f && s <= 0x1p120f;
+  float tq[NV][PV];
+  bool near = !fast;
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+#pragma unroll
+    for (int e = 0; e < PV; ++e) {
+      const float qv = elem(k, e) * rs;
+      tq[k][e] = rintf(qv);
+      near |= fabsf(fabsf(qv - tq[k][e]) - 0.5f) < 0x1p-13f;
+    }
+  if (near) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+      for (int e = 0; e < PV; ++e) tq[k][e] = rintf(elem(k, e) / s);
+  }
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     uint32_t packed[PV / 4];
@@ -248,11 +272,7 @@ __global__ __launch_bounds__(BT) void quantize_rows_resident(const void* __restr
 #pragma unroll
     for (int e = 0; e < PV; ++e) {
       int iv = 0;
-      if (s > 0.0f) {
-        float t = rintf(elem(k, e) / s);
-        t = fminf(fmaxf(t, -127.0f), 127.0f);
-        iv = static_cast<int>(t);
-      }
+      if (s > 0.0f) iv = static_cast<int>(fminf(fmaxf(tq[k][e], -127.0f), 127.0f));
       packed[e / 4] |= (static_cast<uint32_t>(iv) & 0xFFu) << (8 * (e % 4));
     }
     const int64_t vi = threadIdx.x + BT * k;
