@@ -61,7 +61,10 @@ typedef enum vdsl_device_kind {
 /* Buffer binding kinds: the vocabulary of the `vernon.semantic` argument attribute that
  * VernonToSPIRVPass maps to SPIR-V storage classes (VernonToSpirv.cpp:43-56; used in
  * color.mlir:4-9,43-45).  Ops may read any kind; UNIFORM_CONSTANT buffers are read-only on the
- * device, and an op that would write one fails with VDSL_ERR_INVALID_ARG. */
+ * device, and an op that would write one fails with VDSL_ERR_INVALID_ARG.  An OUTPUT buffer holds
+ * a result for the host: a bf16 GEMM storing a plain f32 result into one (vdsl_op_gemm_bf16,
+ * vdsl_op_gemm_bf16_packed) uses streaming (non-temporal) stores, so later device work that
+ * reads it right away may run slower than from a STORAGE_BUFFER; the values are the same. */
 typedef enum vdsl_binding {
   VDSL_BIND_STORAGE_BUFFER = 0,  /* "storage_buffer": read-write (default) */
   VDSL_BIND_INPUT = 1,           /* "input" */

@@ -182,3 +182,45 @@ def test_every_w8a8_config_bit_exact(dev, q, forced_config, M, N, K):
     finally:
         for t in ts:
             t.free()
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 256), (300, 512, 256), (256, 768, 192)])
+def test_streamed_f32_output_matches(dev, q, forced_config, M, N, K):
+    """An f32 result bound as VDSL_BIND_OUTPUT leaves the LDS-staged epilogue through streaming
+    stores: the same bits as a storage-buffer result under every configuration, in the NT form,
+    the K-major NN form and the packed-weight form."""
+    A = rng.f32_to_bf16(rng.uniform(91, M * K, -1, 1)).reshape(M, K)
+    B = rng.f32_to_bf16(rng.uniform(92, N * K, -1, 1)).reshape(N, K)
+    tA, tB = Tensor.from_numpy(dev, q, A, "bf16"), Tensor.from_numpy(dev, q, B, "bf16")
+    tBkn = Tensor.from_numpy(dev, q, np.ascontiguousarray(B.T), "bf16")
+    ws = Tensor(dev, (max(1, kernels.gemm_bf16_workspace_bytes(False, False, M, N, K)),), "i8")
+
+    def run(src, tb, binding, packed=False):
+        out = Tensor(dev, (M, N), "f32", binding)
+        out.buffer.fill_u32(q, 0x7FC07FC0)
+        if packed:
+            kernels.gemm_bf16_packed(q, tA, src, out)
+        else:
+            kernels.gemm_bf16(q, tA, src, out, False, tb, _lib.EPI_NONE, None, None if tb else ws)
+        r = out.numpy(q)
+        out.free()
+        return r
+
+    try:
+        for c in [-1] + list(range(N_BF16_CONFIGS)):
+            forced_config(c)
+            for src, tb in ((tB, True), (tBkn, False)):
+                plain = run(src, tb, _lib.BIND_STORAGE_BUFFER)
+                streamed = run(src, tb, _lib.BIND_OUTPUT)
+                assert np.array_equal(plain, streamed), f"config {c} trans_b={tb}: streamed output differs"
+        forced_config(-1)
+        if K % 256 == 0 and N % 32 == 0:
+            tBp = Tensor(dev, (N, K), "bf16")
+            kernels.pack_bf16_weights(q, tB, tBp)
+            plain = run(tBp, True, _lib.BIND_STORAGE_BUFFER, packed=True)
+            assert np.array_equal(plain, run(tBp, True, _lib.BIND_OUTPUT, packed=True)), "packed: streamed output differs"
+            assert np.array_equal(plain, run(tB, True, _lib.BIND_STORAGE_BUFFER)), "packed differs from NT"
+            tBp.free()
+    finally:
+        for t in (tA, tB, tBkn, ws):
+            t.free()

@@ -164,3 +164,15 @@ def test_oracle_w8a8_forward_rows_independent():
     full = oracle.w8a8_forward(x, layers)
     part = oracle.w8a8_forward(x[2:4], layers)
     assert np.array_equal(full[2:4], part)
+
+
+def test_host_outputs_are_the_unread_results():
+    """Buffers bound as VDSL_BIND_OUTPUT (streamed f32 GEMM results): exactly the values the step
+    produces and nothing reads, never op scratch or anything a later op consumes."""
+    g, _ = graph.mlp_train_graph()
+    outs = g.host_outputs()
+    assert {"grad_W1", "grad_W2", "Y", "loss"} <= outs
+    read = {v.name for op in g.ops + g.prepare_ops for v in op.inputs}
+    assert not (outs & read)
+    assert all(g.values[n].kind != "scratch" for n in outs)
+    assert "H" not in outs  # read by the output GEMM and the dW2 GEMM

@@ -77,6 +77,11 @@ constexpr int kFirstDma = 14, kFirstDma128 = 23;
 // Internal epilogue code of vdsl_op_gemm_bf16_gelu_bwd: C (bf16) = v * GELU'(pre) with `pre` an
 // input, and the same values transposed into `ctr` ([N][M], optional).
 constexpr int kEpiGeluBwd = 100;
+// OR-ed into a kernel's `epi` argument when its f32 output is bound as VDSL_BIND_OUTPUT (a result
+// for the host that no later device work reads soon): the LDS-staged epilogue then stores it with
+// non-temporal hints.  In the config-4 step the weight gradients (2 x 64 MB of f32) stored that way
+// no longer leave dirty lines for the next GEMMs to write back: step 372-376 -> 355-358 us.
+constexpr int kEpiStreamOut = 0x1000;
 
 // Backward epilogue modes (template argument BWD): 0 = forward (epi selects it), 1 = C = v *
 // GELU'(pre) (vdsl_op_gemm_bf16_gelu_bwd), 2 = C = v * g with the factor g given in `pre`
@@ -211,6 +216,8 @@ __device__ __forceinline__ void bf16_epilogue_tile_lds(const f32x16 (&acc)[Cfg::
       const size_t o = static_cast<size_t>(row0 + 32 * i + row) * N + col0 + 4 * c4;
       if (VARIANT == 0) {
         *reinterpret_cast<f32x4*>(static_cast<float*>(C) + o) = v;
+      } else if (VARIANT == 3) {  // VARIANT 0 with streaming stores (kEpiStreamOut)
+        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(static_cast<float*>(C) + o));
       } else {
         if (VARIANT == 1) {
           *reinterpret_cast<f32x4*>(pre + o) = v;
@@ -385,6 +392,7 @@ __global__ __launch_bounds__(Cfg::NT, 2) void gemm_bf16_nt(const uint16_t* __res
                                                         void* __restrict__ C, float* __restrict__ pre, int M, int N, int K,
                                                         int epi, int c_dtype, uint16_t* __restrict__ ctr) {
   __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS_BYTES];
+  epi &= ~kEpiStreamOut;  // this kernel's epilogue stores per element, with plain stores
   const int tiles_m = (M + Cfg::BM - 1) / Cfg::BM, tiles_n = (N + Cfg::BN - 1) / Cfg::BN;
   int tm, tn;
   tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
@@ -404,6 +412,8 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_bf16_dma
                                                                                int M, int N, int K, int epi, int c_dtype,
                                                                                uint16_t* __restrict__ ctr) {
   __shared__ __attribute__((aligned(1024))) char smem[Cfg::LDS_BYTES];
+  const bool stream = (epi & kEpiStreamOut) != 0;
+  epi &= ~kEpiStreamOut;
   const int tiles_m = (M + Cfg::BM - 1) / Cfg::BM, tiles_n = (N + Cfg::BN - 1) / Cfg::BN;
   int tm, tn;
   tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
@@ -426,7 +436,8 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_bf16_dma
       const bool v1 = epi == VDSL_EPI_GELU && c_dtype == VDSL_BF16 && pre;
       if (whole && (v0 || v1)) {
         dma_barrier();  // every wave's last fragment reads of the main loop are done
-        if (v0) bf16_epilogue_tile_lds<Cfg, 0>(acc, m0, n0, N, C, pre, smem);
+        if (v0 && stream) bf16_epilogue_tile_lds<Cfg, 3>(acc, m0, n0, N, C, pre, smem);
+        else if (v0) bf16_epilogue_tile_lds<Cfg, 0>(acc, m0, n0, N, C, pre, smem);
         else bf16_epilogue_tile_lds<Cfg, 1>(acc, m0, n0, N, C, pre, smem);
         return;
       }
@@ -441,6 +452,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_nt_simple(const uint16_t* __res
                                                            int K, int epi, int c_dtype, uint16_t* __restrict__ ctr) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (idx >= static_cast<int64_t>(M) * N) return;
+  epi &= ~kEpiStreamOut;
   const int row = static_cast<int>(idx / N), col = static_cast<int>(idx % N);
   float v = 0.0f;
   for (int k = 0; k < K; ++k)
@@ -482,6 +494,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_bpk(const uint16_t* __re
                                                          int epi, int c_dtype, uint16_t* __restrict__ ctr) {
   // The only __shared__ variable (see gemm_bpk.h); after the main loop it stages the epilogue.
   __shared__ __attribute__((aligned(1024))) char smem[bpk_bf16_smem<Cfg, BWD != 0>()];
+  const bool stream = (epi & kEpiStreamOut) != 0;
+  epi &= ~kEpiStreamOut;
   // Tiles in groups of 8 tile-rows, walked column-major (tile_coords): the 32 blocks one XCD runs
   // (congruent ids, made consecutive by xcd_remap) then cover 8 row tiles x 4 column panels, so
   // each XCD's L2 fetches 1/2 of A and 1/4 of B (2048x4096x4096: 128 MB fetched in all, against
@@ -511,7 +525,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_bpk(const uint16_t* __re
     const bool v1 = epi == VDSL_EPI_GELU && c_dtype == VDSL_BF16 && pre;
     if (whole && (v0 || v1)) {
       __syncthreads();  // every wave is past its last read of the main loop's LDS
-      if (v0) bf16_epilogue_tile_lds<Cfg, 0>(acc, m0, n0, N, C, pre, smem);
+      if (v0 && stream) bf16_epilogue_tile_lds<Cfg, 3>(acc, m0, n0, N, C, pre, smem);
+      else if (v0) bf16_epilogue_tile_lds<Cfg, 0>(acc, m0, n0, N, C, pre, smem);
       else bf16_epilogue_tile_lds<Cfg, 1>(acc, m0, n0, N, C, pre, smem);
       return;
     }
@@ -646,6 +661,11 @@ int launch_nt(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, 
   }
 }
 
+// Whether a GEMM's result leaves through streaming stores: a plain f32 output bound as an output.
+bool stream_out(vdsl_buffer C, int epilogue, int c_dtype) {
+  return epilogue == VDSL_EPI_NONE && c_dtype == VDSL_F32 && C->binding == VDSL_BIND_OUTPUT;
+}
+
 // kSizeOverflow when the re-layout copies' size does not fit size_t.
 size_t workspace_bytes(int ta, int tb, int64_t M, int64_t N, int64_t K) {
   const size_t a = ta ? nbytes(M, K, 2) : 0, b = tb ? 0 : nbytes(N, K, 2);
@@ -688,9 +708,10 @@ extern "C" int vdsl_op_gemm_bf16(vdsl_queue q, int32_t trans_a, int32_t trans_b,
   const uint16_t* a = static_cast<const uint16_t*>(A->ptr);
   const uint16_t* b = static_cast<const uint16_t*>(B->ptr);
   float* pre = pre_act ? static_cast<float*>(pre_act->ptr) : nullptr;
+  const int epi = epilogue | (stream_out(C, epilogue, c_dtype) ? kEpiStreamOut : 0);
   if (!ta && !tb && K % 8 == 0) {  // B stored [K][N]: read K-major when a 256-wide configuration runs the shape
     const int rc = launch_dma_kn(choose_config(M, N, K), a, b, C->ptr, pre, static_cast<int>(M), static_cast<int>(N),
-                                 static_cast<int>(K), epilogue, c_dtype, q->stream);
+                                 static_cast<int>(K), epi, c_dtype, q->stream);
     if (rc != 1) return rc;
   }
   char* w = ws ? static_cast<char*>(workspace->ptr) : nullptr;
@@ -703,7 +724,7 @@ extern "C" int vdsl_op_gemm_bf16(vdsl_queue q, int32_t trans_a, int32_t trans_b,
     VDSL_TRY(launch_transpose(b, w, K, N, VDSL_BF16, q->stream));
     b = reinterpret_cast<const uint16_t*>(w);
   }
-  return launch_nt(a, b, C->ptr, pre, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), epilogue, c_dtype,
+  return launch_nt(a, b, C->ptr, pre, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), epi, c_dtype,
                    q->stream);
 }
 
@@ -766,7 +787,7 @@ extern "C" int vdsl_op_gemm_bf16_packed(vdsl_queue q, int64_t M, int64_t N, int6
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles)), dim3(Pb0::NT), 0, q->stream,
                      static_cast<const uint16_t*>(A->ptr), static_cast<const uint16_t*>(Bp->ptr), C->ptr,
                      pre_act ? static_cast<float*>(pre_act->ptr) : nullptr, static_cast<int>(M), static_cast<int>(N),
-                     static_cast<int>(K), epilogue, c_dtype, nullptr);
+                     static_cast<int>(K), epilogue | (stream_out(C, epilogue, c_dtype) ? kEpiStreamOut : 0), c_dtype, nullptr);
   return check_launch("gemm_bf16_bpk");
 }
 

@@ -291,6 +291,13 @@ class Graph:
     def compile(self, dev: Device) -> "Executable":
         return Executable(self, dev)
 
+    def host_outputs(self) -> set:
+        """Values an op produces and no op (step or prepare) reads: results for the host only.  Their
+        buffers are bound as VDSL_BIND_OUTPUT, which lets a GEMM store an f32 result with streaming
+        (non-temporal) stores instead of leaving it dirty in the caches for the next kernels."""
+        read = {v.name for op in self.ops + self.prepare_ops for v in op.inputs}
+        return {v.name for op in self.ops for v in op.outputs if v.kind != "scratch"} - read
+
 
 def _needs(x: Value, g: Graph) -> bool:
     """An activation needs a gradient if some parameter upstream of it requires one."""
@@ -329,9 +336,11 @@ class Executable:
             if op.kind == "w8a8_packed":
                 xq, _, wp, _ = op.inputs
                 ws = max(ws, kernels.gemm_w8a8_packed_workspace_bytes(xq.shape[0], wp.shape[0], xq.shape[1]))
+        outs = g.host_outputs()
         try:
             for v in g.values.values():
-                self.t[v.name] = Tensor(dev, v.shape, v.dtype)
+                bind = _lib.BIND_OUTPUT if v.name in outs else _lib.BIND_STORAGE_BUFFER
+                self.t[v.name] = Tensor(dev, v.shape, v.dtype, bind)
             # One workspace shared by all ops: they run in order on one queue.
             self.workspace = Tensor(dev, (max(ws, 4),), "i8") if ws else None
         except BaseException:
