@@ -84,8 +84,11 @@ def test_mlp_config4_every_element(dev, q):
     bwd = by_kind["gemm_mul_bwd"][0]
     rd = lambda v: exe.read(q, v.name)  # noqa: E731
     dgelu, h = rd(fwd1.attrs["dgelu"]), exe.read(q, "H")
-    y, loss, dy, dy_t = (rd(v) for v in mse.outputs[:4])
-    da, da_t = (rd(v) for v in bwd.outputs[:2])
+    y, loss, dy = (rd(v) for v in mse.outputs[:3])
+    da = rd(bwd.outputs[0])
+    # the weight-gradient GEMMs read dY and dL/dpre as stored (K-major A): their transposes are
+    # neither allocated nor written
+    assert {mse.outputs[3].name, bwd.outputs[1].name} <= g.elided
     X, W1, W2 = _f32(x), _f32(w1), _f32(w2)
     # The step keeps GELU'(pre), not pre: the same forward GEMM with the plain GELU epilogue on the
     # step's own operands gives pre, and its H must equal the step's bit for bit.
@@ -109,10 +112,10 @@ def test_mlp_config4_every_element(dev, q):
     check_gemm(y, H, W2.T, what="Y = H W2^T")
     # the loss and dL/dY from the GPU's Y: dY exact, the loss within f64-sum rounding
     r_loss, r_dy, r_dy_t = oracle.mse_fwd_bwd(y, t)
-    assert np.array_equal(dy, r_dy) and np.array_equal(dy_t, r_dy_t)
+    assert np.array_equal(dy, r_dy)
     assert abs(float(loss[0]) - r_loss) <= 1e-6 * r_loss
     # weight gradient of W2 from the GPU's dY^T and H
-    check_gemm(exe.read(q, "grad_W2"), _f32(dy_t), H, what="dW2 = dY^T H")
+    check_gemm(exe.read(q, "grad_W2"), np.ascontiguousarray(_f32(dy).T), H, what="dW2 = dY^T H")
     # dL/dpre = (dY W2) GELU'(pre): dY W2 from numpy in fp32, GELU' by the oracle; the bound is
     # the GEMM tolerance carried through |GELU'| <= 1.13, plus two bf16 roundings
     DY = _f32(dy)
@@ -121,8 +124,7 @@ def test_mlp_config4_every_element(dev, q):
     mag = (np.abs(DY) @ np.abs(W2)).astype(np.float64) * 1.13
     got, ref = rng.bf16_to_f32(da).astype(np.float64), rng.bf16_to_f32(da_ref).astype(np.float64)
     assert np.all(np.abs(got - ref) <= 1e-2 * mag + 2.0**-7 * np.abs(ref)), "dL/dpre"
-    assert np.array_equal(da_t, np.ascontiguousarray(da.T)), "dL/dpre^T is the transpose of dL/dpre"
     # weight gradient of W1 from the GPU's dL/dpre^T and X
-    check_gemm(exe.read(q, "grad_W1"), _f32(da_t), X, what="dW1 = dA^T X")
+    check_gemm(exe.read(q, "grad_W1"), np.ascontiguousarray(_f32(da).T), X, what="dW1 = dA^T X")
     step.destroy()
     exe.free()

@@ -224,3 +224,41 @@ def test_streamed_f32_output_matches(dev, q, forced_config, M, N, K):
     finally:
         for t in (tA, tB, tBkn, ws):
             t.free()
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 256), (256, 768, 192), (1024, 512, 512), (300, 512, 256)])
+def test_bf16_tn_k_major_a_matches_nt(dev, q, forced_config, M, N, K):
+    """A stored [K][M] (trans_a = 1) and B stored [K][N]: the 256 x 256 direct-to-LDS configuration
+    (15) reads both operands K-major when M and N are multiples of 256, with no transpose into the
+    workspace; every output equals the NT product of the host-transposed operands under the same
+    configuration, bit for bit.  M = 300 takes the transpose path."""
+    A = rng.f32_to_bf16(rng.uniform(95, K * M, -1, 1)).reshape(K, M)   # stored [K][M]
+    B = rng.f32_to_bf16(rng.uniform(96, K * N, -1, 1)).reshape(K, N)   # stored [K][N]
+    tA, tB = Tensor.from_numpy(dev, q, A, "bf16"), Tensor.from_numpy(dev, q, B, "bf16")
+    tAt = Tensor.from_numpy(dev, q, np.ascontiguousarray(A.T), "bf16")
+    tBt = Tensor.from_numpy(dev, q, np.ascontiguousarray(B.T), "bf16")
+    ws = Tensor(dev, (max(1, kernels.gemm_bf16_workspace_bytes(True, False, M, N, K)),), "i8")
+    try:
+        for c in (-1, 15, 14, 23):
+            forced_config(c)
+            ws.buffer.fill_u32(q, 0xA5A5A5A5)
+            out = Tensor(dev, (M, N), "f32")
+            kernels.gemm_bf16(q, tA, tB, out, True, False, _lib.EPI_NONE, None, ws)
+            got = out.numpy(q)
+            if c == 15 and M % 256 == 0 and N % 256 == 0:
+                assert np.all(ws.numpy(q).view(np.uint32) == 0xA5A5A5A5), "K-major A: an operand was transposed"
+            out.buffer.fill_u32(q, 0x7FC07FC0)
+            kernels.gemm_bf16(q, tAt, tBt, out, False, True, _lib.EPI_NONE, None, None)
+            assert np.array_equal(got, out.numpy(q)), f"config {c}: TN output differs from NT"
+            out.free()
+        forced_config(-1)
+        ref = oracle.gemm_bf16(np.ascontiguousarray(A.T), B, False, False)
+        out = Tensor(dev, (M, N), "f32")
+        forced_config(15)
+        kernels.gemm_bf16(q, tA, tB, out, True, False, _lib.EPI_NONE, None, ws)
+        mag = np.abs(rng.bf16_to_f32(A).astype(np.float64)).T @ np.abs(rng.bf16_to_f32(B).astype(np.float64))
+        assert np.all(np.abs(out.numpy(q).astype(np.float64) - ref) <= 1e-2 * mag + 1e-30)
+        out.free()
+    finally:
+        for t in (tA, tB, tAt, tBt, ws):
+            t.free()

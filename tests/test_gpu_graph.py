@@ -112,7 +112,7 @@ def test_mlp_rewritten_weights_reprepared(dev, q):
     W2^T packed): the next step equals the plain graph's step with the new W2, bit for bit."""
     x, w1, w2, t = spec.mlp_inputs(batch=256, d_in=512, hidden=512, d_out=256)
     w2b = np.ascontiguousarray(w2[::-1])
-    plain = {"prepare_transposes": False, "fuse_gelu_backward": False, "pack_weights": False}
+    plain = {"prepare_transposes": False, "fuse_gelu_backward": False, "pack_weights": False, "k_major_grads": False}
     ref = run_mlp(dev, q, x, w1, w2b, t, replays=1, **plain)
     g, _ = graph.mlp_train_graph(256, 512, 512, 256)
     assert len(g.prepare_ops) == 4
@@ -137,7 +137,7 @@ def test_mlp_weights_written_after_capture_reach_the_replay(dev, q):
     graph's step on the new weights bit for bit; then again with the old weights restored."""
     x, w1, w2, t = spec.mlp_inputs(batch=256, d_in=512, hidden=512, d_out=256)
     w1b, w2b = np.ascontiguousarray(w1[:, ::-1]), np.ascontiguousarray(w2[::-1])
-    plain = {"prepare_transposes": False, "fuse_gelu_backward": False, "pack_weights": False}
+    plain = {"prepare_transposes": False, "fuse_gelu_backward": False, "pack_weights": False, "k_major_grads": False}
     ref_new = run_mlp(dev, q, x, w1b, w2b, t, replays=1, **plain)
     ref_old = run_mlp(dev, q, x, w1, w2, t, replays=1, **plain)
     g, _ = graph.mlp_train_graph(256, 512, 512, 256)

@@ -11,7 +11,7 @@ from vernondsl_amd import graph, rng
 
 def test_mlp_backward_op_sequence():
     g, grads = graph.mlp_train_graph(batch=64, d_in=32, hidden=48, d_out=16, prepare_transposes=False,
-                                     fuse_gelu_backward=False)
+                                     fuse_gelu_backward=False, k_major_grads=False)
     kinds = [op.kind for op in g.ops]
     assert kinds == ["linear", "linear", "mse", "gemm", "gemm", "gelu_bwd", "gemm"]
     assert sorted(grads) == ["W1", "W2"]
@@ -36,7 +36,7 @@ def test_mlp_backward_prepared_transpose_and_fused_gelu():
     assert dH.inputs[1].name == "W2.T" and dH.inputs[1].shape == (48, 16) and dH.attrs["trans_b"]
     assert [(op.kind, op.inputs[0].name, op.outputs[0].name) for op in g.prepare_ops] == [("transpose", "W2", "W2.T")]
     g, _ = graph.mlp_train_graph(batch=64, d_in=32, hidden=48, d_out=16, prepare_transposes=True,
-                                 fuse_gelu_backward=True)
+                                 fuse_gelu_backward=True, k_major_grads=False)
     assert [op.kind for op in g.ops] == ["linear", "linear", "mse", "gemm", "gemm_gelu_bwd", "gemm"]
     dA, dW1 = g.ops[4], g.ops[5]
     # dL/dpre = (dY W2) * GELU'(pre) in one op
@@ -176,3 +176,22 @@ def test_host_outputs_are_the_unread_results():
     assert not (outs & read)
     assert all(g.values[n].kind != "scratch" for n in outs)
     assert "H" not in outs  # read by the output GEMM and the dW2 GEMM
+
+
+def test_k_major_grads_elide_transposes():
+    """The config-4 default: the weight-gradient GEMMs take dL/dY and dL/dpre as stored (trans_a),
+    and their transposes, which nothing reads then, are elided; without the option they are read."""
+    g, _ = graph.mlp_train_graph(batch=256, d_in=512, hidden=512, d_out=256)
+    dW2, mul, dW1 = g.ops[2], g.ops[3], g.ops[4]
+    mse = g.ops[1]
+    assert dW2.attrs["trans_a"] and dW2.inputs[0] is mse.outputs[2] and dW2.inputs[0].shape == (256, 256)
+    assert dW1.attrs["trans_a"] and dW1.inputs[0] is mul.outputs[0]
+    assert g.elided == {mse.outputs[3].name, mul.outputs[1].name}
+    assert not (g.elided & g.host_outputs())
+    g2, _ = graph.mlp_train_graph(batch=256, d_in=512, hidden=512, d_out=256, k_major_grads=False)
+    assert not g2.elided and not g2.ops[2].attrs["trans_a"] and g2.ops[2].inputs[0] is g2.ops[1].outputs[3]
+    # the unfused form: the mse op's dY^T and the cast/transpose pair are dropped the same way
+    g3, _ = graph.mlp_train_graph(batch=64, d_in=32, hidden=48, d_out=16, prepare_transposes=False,
+                                  fuse_gelu_backward=False, pack_weights=False, fuse_mse=False, store_gelu_deriv=False)
+    assert len(g3.elided) == 2 and all(n.startswith("dT_") for n in g3.elided)
+    assert all(op.attrs["trans_a"] for op in g3.ops if op.kind == "gemm" and op.outputs[0].name.startswith("grad_"))

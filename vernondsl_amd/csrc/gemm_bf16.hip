@@ -405,7 +405,8 @@ __global__ __launch_bounds__(Cfg::NT, 2) void gemm_bf16_nt(const uint16_t* __res
 
 // Direct-to-LDS kernel (gemm_dma.h).  Blocks of 8 waves are sized for one block per CU, blocks
 // of 4 waves for two.  BKN: B stored [K][N] (the "NN" form, no transpose first; N % 256 == 0).
-template <class Cfg, bool BWD, bool BKN = false>
+// AKM: A stored [K][M] (trans_a; M % 256 == 0), read K-major as well.
+template <class Cfg, bool BWD, bool BKN = false, bool AKM = false>
 __global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_bf16_dma(const uint16_t* __restrict__ A,
                                                                                const uint16_t* __restrict__ B,
                                                                                void* __restrict__ C, float* __restrict__ pre,
@@ -419,8 +420,9 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_bf16_dma
   tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
   const int m0 = tm * Cfg::BM, n0 = tn * Cfg::BN;
   f32x16 acc[Cfg::FM][Cfg::FN];
-  dma_mainloop<MfmaBf16, Cfg, f32x16, Cfg::FM, Cfg::FN, BKN>(reinterpret_cast<const char*>(A), reinterpret_cast<const char*>(B),
-                                                             M, N, K * 2, 0, K * 2, m0, n0, smem, acc, N * 2);
+  dma_mainloop<MfmaBf16, Cfg, f32x16, Cfg::FM, Cfg::FN, BKN, AKM>(reinterpret_cast<const char*>(A),
+                                                                  reinterpret_cast<const char*>(B), M, N, K * 2, 0, K * 2, m0,
+                                                                  n0, smem, acc, N * 2, M * 2);
   if constexpr (kLdsEpilogue<Cfg>) {
     // Block-uniform: the tile is whole, N allows aligned runs, and the variant is one of the two.
     const bool whole = m0 + Cfg::BM <= M && n0 + Cfg::BN <= N && N % 4 == 0;
@@ -583,20 +585,24 @@ int launch_dma(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M,
 }
 
 // The "NN" form (B stored [K][N]) without a transpose: the direct-to-LDS configurations with
-// 256-wide tiles read B K-major (gemm_dma.h) when every tile is whole along N.  Returns 1 (never a
-// status) when the shape needs the transpose path instead.
+// 256-wide tiles read B K-major (gemm_dma.h) when every tile is whole along N.  With akm, the "TN"
+// form (A stored [K][M] as well, e.g. dW = g^T x with g [batch][out] as stored): the 256 x 256
+// configuration reads both operands K-major when M % 256 == 0 too.  Returns 1 (never a status)
+// when the shape needs the transpose path instead.
 int launch_dma_kn(int cfg, const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, int N, int K, int epi, int ct,
-                  hipStream_t s) {
-  if (N % 256 != 0) return 1;
-  auto go = [&](auto cfg_tag) {
+                  hipStream_t s, bool akm = false) {
+  if (N % 256 != 0 || (akm && (M % 256 != 0 || cfg != 15))) return 1;
+  auto go = [&](auto cfg_tag, auto akm_tag) {
     using Cfg = decltype(cfg_tag);
+    constexpr bool kAkm = decltype(akm_tag)::value;
     const int64_t tiles = static_cast<int64_t>((M + Cfg::BM - 1) / Cfg::BM) * (N / Cfg::BN);
-    hipLaunchKernelGGL((gemm_bf16_dma<Cfg, false, true>), dim3(static_cast<unsigned>(tiles)), dim3(Cfg::NT), 0, s, A, B, C, pre,
-                       M, N, K, epi, ct, nullptr);
-    return check_launch("gemm_bf16_dma<K-major B>");
+    hipLaunchKernelGGL((gemm_bf16_dma<Cfg, false, true, kAkm>), dim3(static_cast<unsigned>(tiles)), dim3(Cfg::NT), 0, s, A, B, C,
+                       pre, M, N, K, epi, ct, nullptr);
+    return check_launch(kAkm ? "gemm_bf16_dma<K-major A and B>" : "gemm_bf16_dma<K-major B>");
   };
-  if (cfg == 15) return go(Dm15{});
-  if (cfg == 23) return go(Dm23{});
+  if (akm) return go(Dm15{}, std::true_type{});
+  if (cfg == 15) return go(Dm15{}, std::false_type{});
+  if (cfg == 23) return go(Dm23{}, std::false_type{});
   return 1;
 }
 
@@ -709,9 +715,9 @@ extern "C" int vdsl_op_gemm_bf16(vdsl_queue q, int32_t trans_a, int32_t trans_b,
   const uint16_t* b = static_cast<const uint16_t*>(B->ptr);
   float* pre = pre_act ? static_cast<float*>(pre_act->ptr) : nullptr;
   const int epi = epilogue | (stream_out(C, epilogue, c_dtype) ? kEpiStreamOut : 0);
-  if (!ta && !tb && K % 8 == 0) {  // B stored [K][N]: read K-major when a 256-wide configuration runs the shape
+  if (!tb && K % 8 == 0) {  // B stored [K][N] (and A [K][M] if ta): read K-major when a 256-wide configuration runs it
     const int rc = launch_dma_kn(choose_config(M, N, K), a, b, C->ptr, pre, static_cast<int>(M), static_cast<int>(N),
-                                 static_cast<int>(K), epi, c_dtype, q->stream);
+                                 static_cast<int>(K), epi, c_dtype, q->stream, ta);
     if (rc != 1) return rc;
   }
   char* w = ws ? static_cast<char*>(workspace->ptr) : nullptr;

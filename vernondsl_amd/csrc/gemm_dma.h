@@ -119,13 +119,16 @@ __device__ __forceinline__ void dma_barrier() {
 // K loop over bytes [kb_begin, kb_end) for the tile at (m0, n0).  Requires kb_begin % 16 == 0 and
 // (kb_end - kb_begin) % BKB == 0; Kb = row stride of A and B in bytes.
 // BKN: B is stored [K][N] with row stride Nb bytes (needs BN == 256, bf16, and the tile's N range
-// inside N: the caller launches it only for N % 256 == 0).
-template <class T, class Cfg, class AccT, int FM_, int FN_, bool BKN = false>
+// inside N: the caller launches it only for N % 256 == 0).  AKM: likewise A stored [K][M] with row
+// stride Mb bytes (BM == 256, M % 256 == 0): the same copies and transposing reads as K-major B,
+// since an MFMA A fragment has B's lane layout (lane l: row l % 32, K values 8 (l / 32) .. + 7).
+template <class T, class Cfg, class AccT, int FM_, int FN_, bool BKN = false, bool AKM = false>
 __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const char* __restrict__ B, int M, int N, int Kb,
                                              int kb_begin, int kb_end, int m0, int n0, char* smem, AccT (&acc)[FM_][FN_],
-                                             int Nb = 0) {
+                                             int Nb = 0, int Mb = 0) {
   static_assert(FM_ == Cfg::FM && FN_ == Cfg::FN, "accumulator array must match the configuration");
   static_assert(!BKN || (Cfg::BN == 256 && std::is_same<T, MfmaBf16>::value), "K-major B: bf16, 256-wide tiles");
+  static_assert(!AKM || (Cfg::BM == 256 && std::is_same<T, MfmaBf16>::value), "K-major A: bf16, 256-tall tiles");
   using Frag = typename T::Frag;
   constexpr int FM = Cfg::FM, FN = Cfg::FN, NS = Cfg::NS, BPW = Cfg::BPW, STAGE = Cfg::STAGE, SUB = Cfg::SUB;
   constexpr int KS = Cfg::KS, KSUB = Cfg::KSUB, CPW = Cfg::CPW;
@@ -146,6 +149,13 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
   for (int u = 0; u < BPW; ++u) {
     const int b = wave * BPW + u;
     const bool is_a = b < Cfg::BM / Cfg::RPB;
+    if (AKM && is_a) {  // as K-major B below, over the A area's 16 blocks
+      const int k = 2 * b + (lane >> 5);
+      const int c = (lane & 31) ^ kn_swz(k);
+      src[u] = A + static_cast<size_t>(kb_begin / 2 + k) * Mb + static_cast<size_t>(m0) * 2 + c * 16;
+      kmul[u] = static_cast<size_t>(Mb) / 2;
+      continue;
+    }
     if (BKN && !is_a) {
       // 1 KiB block j holds K rows 2j, 2j+1 of the sub-stage; lane l fills slot l % 32 of row
       // 2j + l / 32 with global chunk (l % 32) ^ kn_swz(row) of that row's 512-byte run.
@@ -183,9 +193,21 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
         tro[r][j] = k * (2 * Cfg::BN) + (((n >> 3) ^ kn_swz(k)) << 4) + ((n >> 2) & 1) * 8;
       }
   }
-  constexpr int NRD = FM + (BKN ? 2 : 1) * FN;  // LDS read instructions per k-step
+  int tra[2][FM];  // K-major A: the same offsets over the A area (row stride 2 BM)
+  if constexpr (AKM) {
+    const int g = lane >> 4, i = lane & 15;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int f = 0; f < FM; ++f) {
+        const int k = 8 * (g >> 1) + 4 * r + (i >> 2);
+        const int m = wm * Cfg::WTM + 32 * f + 16 * (g & 1) + 4 * (i & 3);
+        tra[r][f] = k * (2 * Cfg::BM) + (((m >> 3) ^ kn_swz(k)) << 4) + ((m >> 2) & 1) * 8;
+      }
+  }
+  constexpr int NRD = (AKM ? 2 : 1) * FM + (BKN ? 2 : 1) * FN;  // LDS read instructions per k-step
 
-#define VDSL_DMA_SRC(U, KOFF) (BKN ? src[U] + static_cast<size_t>(KOFF) * kmul[U] : src[U] + (KOFF))
+#define VDSL_DMA_SRC(U, KOFF) ((BKN || AKM) ? src[U] + static_cast<size_t>(KOFF) * kmul[U] : src[U] + (KOFF))
 #define VDSL_DMA_COPY(ST, KB)                                                                     \
   do {                                                                                            \
     _Pragma("unroll") for (int sb = 0; sb < KSUB; ++sb)                                           \
@@ -202,9 +224,17 @@ __device__ __forceinline__ void dma_mainloop(const char* __restrict__ A, const c
 // Fragments of k-step KK (32 K bytes) of stage ST: sub-stage KK / 2, chunks 2 (KK % 2) + hk.
 #define VDSL_DMA_READ(A_, B_, ST, KK)                                                             \
   do {                                                                                            \
-    _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                \
-      A_[i] = *reinterpret_cast<const Frag*>(fa + (ST) * STAGE + ((KK) >> 1) * SUB +              \
-                                             dma_slot(ra + 32 * i, 2 * ((KK) & 1) + hk));          \
+    if constexpr (AKM) {                                                                          \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                            \
+        const char* const ka_ = fa + (ST) * STAGE + ((KK) >> 1) * SUB + ((KK) & 1) * 32 * Cfg::BM; \
+        const i16x4_t lo_ = lds_read_tr16(ka_ + tra[0][i]), hi_ = lds_read_tr16(ka_ + tra[1][i]); \
+        A_[i] = __builtin_bit_cast(Frag, __builtin_shufflevector(lo_, hi_, 0, 1, 2, 3, 4, 5, 6, 7)); \
+      }                                                                                           \
+    } else {                                                                                      \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i)                                              \
+        A_[i] = *reinterpret_cast<const Frag*>(fa + (ST) * STAGE + ((KK) >> 1) * SUB +            \
+                                               dma_slot(ra + 32 * i, 2 * ((KK) & 1) + hk));        \
+    }                                                                                             \
     if constexpr (BKN) {                                                                          \
       _Pragma("unroll") for (int j = 0; j < FN; ++j) {                                            \
         const char* const kb_ = fb + (ST) * STAGE + ((KK) >> 1) * SUB + ((KK) & 1) * 32 * Cfg::BN; \

@@ -51,7 +51,7 @@ class Op:
 class Graph:
     def __init__(self, prepare_transposes: bool = False, fuse_gelu_backward: bool = False,
                  pack_weights: bool = False, fuse_mse: bool = False, keep_y: bool = True,
-                 store_gelu_deriv: bool = False):
+                 store_gelu_deriv: bool = False, k_major_grads: bool = False):
         # prepare_transposes: backward() takes a param's transpose (the NT form's B of dL/dx) from a
         # prepare op instead of transposing the param inside every step's GEMM.
         # fuse_gelu_backward (needs prepare_transposes): GELU' is applied in the epilogue of the GEMM
@@ -76,6 +76,12 @@ class Graph:
         # backward GEMM multiplies by it (vdsl_op_gemm_bf16_mul_packed) instead of evaluating GELU'
         # after its main loop; the same products rounded the same way, bit for bit.
         self.store_gelu_deriv = store_gelu_deriv
+        # k_major_grads: a weight-gradient GEMM dW = g^T x takes g as stored ([batch][out], trans_a,
+        # read K-major by the GEMM) instead of g^T, and the transposed gradients that no op then
+        # reads are elided: not allocated, not written (the epilogues that form g skip them).
+        self.k_major_grads = k_major_grads
+        self.elided: set = set()
+        self._transposed: set = set()
         self.values: dict[str, Value] = {}
         self.ops: list[Op] = []
         # Ops that derive constant operands from params (weight packing): run by
@@ -186,6 +192,7 @@ class Graph:
         y, _ = loss.producer.inputs
         dy = self._value(self._fresh("d_" + y.name), y.shape, "bf16", "grad")
         dy_t = self._value(self._fresh("dT_" + y.name), y.shape[::-1], "bf16", "grad")
+        self._transposed.add(dy_t.name)
         part = self._value(self._fresh("mse_partials"), (max(1, kernels.mse_partials_count(*y.shape)),), "f32", "scratch")
         loss.producer.outputs += [dy, dy_t, part]  # the forward MSE op also emits dL/dy
         grad[y.name] = ("bf16", dy, dy_t)
@@ -221,6 +228,7 @@ class Graph:
                         g = self._to_f32(g[1])
                     da = self._value(self._fresh("d_pre"), y.shape, "bf16", "grad")
                     da_t = self._value(self._fresh("dT_pre"), y.shape[::-1], "bf16", "grad")
+                    self._transposed.add(da_t.name)
                     self._op("gelu_bwd", [g[1], op.attrs["pre"]], [da, da_t])
                     gb, gt = da, da_t
             elif act == "none":
@@ -232,8 +240,12 @@ class Graph:
                 raise NotImplementedError("backward through relu is not implemented (training graphs use gelu)")
             if w.requires_grad:
                 dw = self._value("grad_" + w.name, w.shape, "f32", "grad")
-                # dW[out][in] = sum_b g[b][out] x[b][in]: A = g^T [out][B] (K = B contiguous), B = x [B][in]
-                self._op("gemm", [gt, x], [dw], trans_a=False, trans_b=False, epi=_lib.EPI_NONE)
+                # dW[out][in] = sum_b g[b][out] x[b][in]: A = g^T [out][B] (K = B contiguous), B = x [B][in];
+                # with k_major_grads A is g as stored ([B][out] = [K][M], trans_a)
+                if self.k_major_grads:
+                    self._op("gemm", [gb, x], [dw], trans_a=True, trans_b=False, epi=_lib.EPI_NONE)
+                else:
+                    self._op("gemm", [gt, x], [dw], trans_a=False, trans_b=False, epi=_lib.EPI_NONE)
                 param_grads[w.name] = dw
             if x.requires_grad or (x.producer is not None and x.kind == "activation" and _needs(x, self)):
                 # dx[B][in] = sum_o g[b][o] W[o][in]: A = g [B][out], B = W stored [out][in] = [K][N].
@@ -247,6 +259,7 @@ class Graph:
                     # plus its transpose) without writing dL/dx
                     da = self._value(self._fresh("d_pre"), x.shape, "bf16", "grad")
                     da_t = self._value(self._fresh("dT_pre"), x.shape[::-1], "bf16", "grad")
+                    self._transposed.add(da_t.name)
                     packed = self.pack_weights and wt.shape[0] % 32 == 0 and wt.shape[1] % 256 == 0
                     if packed:  # W^T packed into MFMA fragment order (a second prepare op)
                         wt = self._prepared(wt, "packed", wt.shape, "pack_bf16")
@@ -269,7 +282,21 @@ class Graph:
                     else:
                         self._op("gemm", [gb, w], [dx], trans_a=False, trans_b=False, epi=_lib.EPI_NONE)
                     grad[x.name] = ("f32", dx)
+        if self.k_major_grads:
+            self._elide_unread_transposes()
         return param_grads
+
+    def _elide_unread_transposes(self):
+        """Transposed gradients no op reads: a transpose op that makes one is dropped; one emitted
+        beside its untransposed form by a loss or GEMM epilogue (which accepts no transposed output)
+        is marked elided, so the executable neither allocates nor writes it."""
+        read = {v.name for op in self.ops + self.prepare_ops for v in op.inputs}
+        dead = {n for n in self._transposed if n not in read}
+        for op in list(self.ops):
+            if op.kind == "transpose" and op.outputs[0].name in dead:
+                self.ops.remove(op)
+                del self.values[op.outputs[0].name]
+        self.elided = {n for n in dead if n in self.values}
 
     def _param_transpose(self, w: Value) -> Value:
         """W^T of a param, made by a prepare op (once per write of W, outside the replayed step)."""
@@ -283,6 +310,7 @@ class Graph:
     def _to_bf16_pair(self, v: Value):
         b = self._value(self._fresh(v.name + "_bf16"), v.shape, "bf16", "grad")
         bt = self._value(self._fresh(v.name + "_bf16T"), v.shape[::-1], "bf16", "grad")
+        self._transposed.add(bt.name)
         self._op("cast", [v], [b])
         self._op("transpose", [b], [bt])
         return b, bt
@@ -296,7 +324,7 @@ class Graph:
         buffers are bound as VDSL_BIND_OUTPUT, which lets a GEMM store an f32 result with streaming
         (non-temporal) stores instead of leaving it dirty in the caches for the next kernels."""
         read = {v.name for op in self.ops + self.prepare_ops for v in op.inputs}
-        return {v.name for op in self.ops for v in op.outputs if v.kind != "scratch"} - read
+        return {v.name for op in self.ops for v in op.outputs if v.kind != "scratch"} - read - self.elided
 
 
 def _needs(x: Value, g: Graph) -> bool:
@@ -339,6 +367,9 @@ class Executable:
         outs = g.host_outputs()
         try:
             for v in g.values.values():
+                if v.name in g.elided:
+                    self.t[v.name] = None  # never written: the ops that could emit it are told to skip it
+                    continue
                 bind = _lib.BIND_OUTPUT if v.name in outs else _lib.BIND_STORAGE_BUFFER
                 self.t[v.name] = Tensor(dev, v.shape, v.dtype, bind)
             # One workspace shared by all ops: they run in order on one queue.
@@ -372,6 +403,8 @@ class Executable:
         self._stale.clear()
 
     def read(self, q: Queue, name: str):
+        if self.t.get(name, 0) is None:
+            raise KeyError(f"{name} is elided from this graph (nothing reads it; see Graph.k_major_grads)")
         return self.t[name].numpy(q)
 
     def run(self, q: Queue, events=None):
@@ -485,7 +518,8 @@ class Executable:
 
     def free(self):
         for t in self.t.values():
-            t.free()
+            if t is not None:
+                t.free()
         self.t = {}
         if self.workspace is not None:
             self.workspace.free()
@@ -517,12 +551,13 @@ class Step:
 
 # ---- the two workload graphs ------------------------------------------------------------------------
 def mlp_train_graph(batch=2048, d_in=4096, hidden=4096, d_out=4096, prepare_transposes=True,
-                    fuse_gelu_backward=True, pack_weights=True, fuse_mse=True, keep_y=True, store_gelu_deriv=True):
+                    fuse_gelu_backward=True, pack_weights=True, fuse_mse=True, keep_y=True, store_gelu_deriv=True,
+                    k_major_grads=True):
     """Config 4: X -> GELU(X W1^T) -> (.) W2^T -> MSE(., T), with backward for W1 and W2.
 
     The defaults are the fastest form measured on MI355X (one process, graph replays, same
     gradients bit for bit as the plain graph with none of the options)."""
-    g = Graph(prepare_transposes, fuse_gelu_backward, pack_weights, fuse_mse, keep_y, store_gelu_deriv)
+    g = Graph(prepare_transposes, fuse_gelu_backward, pack_weights, fuse_mse, keep_y, store_gelu_deriv, k_major_grads)
     x = g.input("X", (batch, d_in), "bf16")
     w1 = g.param("W1", (hidden, d_in), "bf16")
     w2 = g.param("W2", (d_out, hidden), "bf16")
