@@ -671,13 +671,13 @@ def _traffic_kernels():
         # config 4 (2048 x 4096 x 4096 and 4096 x 4096 x 2048 bf16): operands read once, outputs written once
         # X, W1 read; H (bf16) and GELU'(pre) (f32) written
         "c4:linear": ("c4_step", _C4_BPK + "0, true>", None, (16 + 32 + 16 + 32) * _MB),
-        # H, W2, T read; Y (f32), dL/dY and its transpose (bf16) written
-        "c4:linear_mse": ("c4_step", "gemm_bf16_bpk_mse", None, (16 + 32 + 32 + 32 + 16 + 16) * _MB),
-        # dL/dY^T (or dL/dpre^T) and H (or X) read; the f32 weight gradient written
-        "c4:gemm": ("c4_step", "gemm_bf16_dma<vdsl::DmaConfig<vdsl::MfmaBf16, 256, 256, 2, 4, 3, 64>, false, true>", None,
-                    (16 + 16 + 64) * _MB),
-        # dL/dY, W2^T, GELU'(pre) read; dL/dpre and its transpose written
-        "c4:gemm_mul_bwd": ("c4_step", _C4_BPK + "2, false>", None, (16 + 32 + 32 + 16 + 16) * _MB),
+        # H, W2, T read; Y (f32) and dL/dY (bf16) written (the weight gradient reads dL/dY as stored)
+        "c4:linear_mse": ("c4_step", "gemm_bf16_bpk_mse", None, (16 + 32 + 32 + 32 + 16) * _MB),
+        # dL/dY (or dL/dpre) and H (or X) read, both K-major; the f32 weight gradient written
+        "c4:gemm": ("c4_step", "gemm_bf16_dma<vdsl::DmaConfig<vdsl::MfmaBf16, 256, 256, 2, 4, 3, 64>, false, true, true>",
+                    None, (16 + 16 + 64) * _MB),
+        # dL/dY, W2^T, GELU'(pre) read; dL/dpre written
+        "c4:gemm_mul_bwd": ("c4_step", _C4_BPK + "2, false>", None, (16 + 32 + 32 + 16) * _MB),
         # config 5 layer 512 x 8192 x 8192 (256 blocks): int8 A, B and both scale vectors read; bf16 Y written
         "c5:w8a8_packed": ("c5_step", "gemm_w8a8_bpk<", 256 * 256,
                            512 * 8192 + 8192 * 8192 + 4 * (512 + 8192) + 2 * 512 * 8192),
@@ -821,7 +821,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline timings")
     ap.add_argument("--only", type=int, default=0, help="run only the headline and one extra config "
-                    "(1, 3, 4, 5; 2: the generic map chains; 6: the vector ops)")
+                    "(1, 3, 4, 5; 2: the generic map chains; 6: the vector ops; 7: the general per-pixel programs)")
+    ap.add_argument("--skip", default="", metavar="IDS",
+                    help="comma-separated config ids (as for --only) to leave out of the run")
     ap.add_argument("--kernel", default="", help="run one kernel --reps times and exit (for rocprofv3 --pmc): "
                     "map_chain, softmax_f32, softmax_bf16, gemm_bf16, gemm_w8a8, escape_time, pixel_stencil, vec_transform, "
                     "swizzle, copy, c4_step, c5_step")
@@ -854,10 +856,11 @@ def main():
     head = bench_map_chain(dev, q, args.steps, args.warmup, do_cpu)
     log("bench: config 2", {k: v for k, v in head.items() if k != "cpu"})
     per_config = []
-    for fn, cid in ((bench_map_chain_generic, 2), (bench_fractal, 1), (bench_pixel_program, 1), (bench_softmax, 3),
+    skip = {int(c) for c in args.skip.split(",") if c.strip()}
+    for fn, cid in ((bench_map_chain_generic, 2), (bench_fractal, 1), (bench_pixel_program, 7), (bench_softmax, 3),
                     (bench_mlp, 4),
                     (bench_w8a8, 5), (bench_vecmat, 6)):
-        if args.only and args.only != cid:
+        if (args.only and args.only != cid) or cid in skip:
             continue
         r = fn(dev, q, args.steps, args.warmup, do_cpu)
         log(f"bench: config {cid}", r)
