@@ -424,7 +424,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_bf16_dma
                                                                   reinterpret_cast<const char*>(B), M, N, K * 2, 0, K * 2, m0,
                                                                   n0, smem, acc, N * 2, M * 2);
   if constexpr (kLdsEpilogue<Cfg>) {
-    // Block-uniform: the tile is whole, N allows aligned runs, and the variant is one of the two.
+    // Block-uniform: the tile is whole, N allows aligned runs, and the epilogue is one the LDS path has.
     const bool whole = m0 + Cfg::BM <= M && n0 + Cfg::BN <= N && N % 4 == 0;
     if constexpr (BWD) {
       if constexpr (Cfg::WTN % 64 == 0 && Cfg::FM * Cfg::WTN / 2 <= 64) {  // pre prefetch: FM * WTN / 2 VGPRs
