@@ -441,6 +441,9 @@ using P2 = BpkConfig<MfmaI8, 2, 2, 4, 7>;  // P1 with loads 7 stages ahead (stag
 // reads (every wave reads all 128 rows of A).  512x8192x8192 with weights rotating through three
 // matrices, same box: 36.6 us against 40.3 us for P2 (4-layer step 162 against 173 us).
 using P3 = BpkConfig<MfmaI8, 4, 1, 4, 3>;
+// 64 x 128 blocks, 4 waves of 64 x 32: a quarter of P0's outputs per block, for narrow outputs
+// split along K over every CU.
+using P4 = BpkConfig<MfmaI8, 2, 1, 4, 3>;
 
 // Whole-tile bf16 epilogue through LDS: each wave writes its dequantised fragments as bf16 into a
 // [BM][EPI_ROW] staging tile (2-byte writes; the row stride 528 = 512 + 16 puts the rows r and
@@ -568,11 +571,12 @@ __global__ __launch_bounds__(256) void w8a8_bpk_reduce(const char* __restrict__ 
 }
 
 // Launch plan of the packed GEMM for a shape: configuration, K split S, tiles.  128 x 256 tiles
-// when they alone give every CU a block; else 128 x 128 when those do; else 64 x 256, with K split
-// only when those are fewer than 256, into about 256 blocks, each a whole number of loop trips
-// (NR stages of 128 bytes).
+// when they alone give every CU a block; else 128 x 128 when those do; else, with M >= 128, 64 x
+// 128 tiles with K split into about 256 blocks; else 64 x 256, with K split only when those are
+// fewer than 256, into about 256 blocks; each split part is a whole number of loop trips (NR
+// stages of 128 bytes).
 struct BpkPlan {
-  int cfg, split;  // cfg: 0 = P0, 1 = P1, 2 = P2, 3 = P3
+  int cfg, split;  // cfg: 0 = P0, 1 = P1, 2 = P2, 3 = P3, 4 = P4
   int64_t tiles;
 };
 std::atomic<int> g_bpk_plan{-1};  // debug override: cfg * 256 + split, or -1
@@ -588,10 +592,13 @@ BpkPlan bpk_plan(int64_t M, int64_t N, int64_t K) {
   if (o >= 0) {  // a forced plan, when its stages split evenly: K % (128 * NR * split) == 0
     const int cfg = o >> 8, split = o & 255;
     const int nr = cfg == 2 ? P2::NR : P0::NR;
-    if (cfg >= 0 && cfg <= 3 && split >= 1 && K % (static_cast<int64_t>(128) * nr * split) == 0) {
+    if (cfg >= 0 && cfg <= 4 && split >= 1 && K % (static_cast<int64_t>(128) * nr * split) == 0) {
       p.cfg = cfg;
       p.split = split;
-      p.tiles = cfg == 0 ? bpk_tiles<P0>(M, N) : cfg == 3 ? bpk_tiles<P3>(M, N) : bpk_tiles<P1>(M, N);
+      p.tiles = cfg == 0   ? bpk_tiles<P0>(M, N)
+                : cfg == 3 ? bpk_tiles<P3>(M, N)
+                : cfg == 4 ? bpk_tiles<P4>(M, N)
+                           : bpk_tiles<P1>(M, N);
       return p;
     }
   }
@@ -605,14 +612,15 @@ BpkPlan bpk_plan(int64_t M, int64_t N, int64_t K) {
   }
   const int64_t trips = K / (128 * P0::NR);
   if (t0 < 256 && M >= 128) {
-    // Narrow outputs: 128 x 128 tiles with K split into about 128 blocks.  The partials' round
-    // trip through memory and the reduce cost more than the extra CUs of a larger split gain:
-    // 512x1024x8192 with weights rotating through 16 copies, same box: split 4 (128 blocks)
-    // 14.4 us, split 8 16.5-16.9, split 2 18.4, unsplit 25.6; 64 x 256 tiles split 8 (the plan
-    // before) 17.3-18.4, split 4 15.0.
-    p.cfg = 3;
-    p.tiles = t3;
-    int64_t s = t3 >= 128 ? 1 : 128 / t3;
+    // Narrow outputs: 64 x 128 tiles with K split into about 256 blocks.  512x1024x8192 with
+    // weights rotating through 16 copies, same box: 64 x 128 split 4 (256 blocks) 13.8 us, split 2
+    // 14.8, split 8 16.6, unsplit 19.1; 128 x 128 split 4 (128 blocks, the plan before) 14.4-14.8,
+    // split 2 18.5, split 8 16.5-16.9; 64 x 256 split 4 15.0.  A larger split costs more in the
+    // partials' round trip through memory and the reduce than its extra blocks gain.
+    const int64_t t4 = bpk_tiles<P4>(M, N);
+    p.cfg = 4;
+    p.tiles = t4;
+    int64_t s = t4 >= 256 ? 1 : 256 / t4;
     if (s > trips) s = trips;
     while (s > 1 && trips % s) --s;
     p.split = static_cast<int>(s < 1 ? 1 : s);
@@ -631,6 +639,7 @@ size_t bpk_workspace_bytes(const BpkPlan& p) {
   if (p.split == 1) return 0;
   const size_t tile_bytes = p.cfg == 0   ? static_cast<size_t>(P0::BM) * P0::BN * 4
                             : p.cfg == 3 ? static_cast<size_t>(P3::BM) * P3::BN * 4
+                            : p.cfg == 4 ? static_cast<size_t>(P4::BM) * P4::BN * 4
                                          : static_cast<size_t>(P1::BM) * P1::BN * 4;
   return static_cast<size_t>(p.tiles) * p.split * tile_bytes;
 }
@@ -803,6 +812,7 @@ static int packed_launch(vdsl_queue q, const BpkPlan& p, int64_t M, int64_t N, i
   const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
   if (p.cfg == 0) return launch_bpk<P0>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
   if (p.cfg == 3) return launch_bpk<P3>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
+  if (p.cfg == 4) return launch_bpk<P4>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
   if (p.cfg == 2) return launch_bpk<P2>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
   return launch_bpk<P1>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
 }
@@ -812,7 +822,7 @@ extern "C" int vdsl_debug_w8a8_packed_plan(int32_t cfg, int32_t split) {
     g_bpk_plan.store(-1, std::memory_order_relaxed);
     return VDSL_OK;
   }
-  if (cfg > 3 || split < 1 || split > 255) return fail(VDSL_ERR_INVALID_ARG, "plan: cfg 0..3, split 1..255");
+  if (cfg > 4 || split < 1 || split > 255) return fail(VDSL_ERR_INVALID_ARG, "plan: cfg 0..4, split 1..255");
   g_bpk_plan.store(cfg * 256 + split, std::memory_order_relaxed);
   return VDSL_OK;
 }
