@@ -69,12 +69,12 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
 
 // Rows per block in the row mapping (each thread evaluates that many pixels of its column, then
 // stores them).  Measured on 8192^2 f32: y = 2x + 1 runs best with 4 (1, 2, 8, 16 rows: 61-96%
-// of its rate), a five-point stencil with 8 (its neighbours' rows are then shared within the
-// block; 4 rows: 93%), so programs with gathers take 8.
+// of its rate), a five-point stencil with 12 (its neighbours' rows are then shared within the
+// block; 8 rows: 98%, 16 rows: 97%, 4 rows: 91%), so programs with gathers take 12.
 int rows_per_block(const vdsl_pixel_program& p) {
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   for (int pc = 0; pc < total; ++pc)
-    if (p.code[pc].op == VDSL_PIX_LOAD_AT) return 8;
+    if (p.code[pc].op == VDSL_PIX_LOAD_AT) return 12;
   return 4;
 }
 
