@@ -679,7 +679,7 @@ def _traffic_kernels():
         # dL/dY, W2^T, GELU'(pre) read; dL/dpre written
         "c4:gemm_mul_bwd": ("c4_step", _C4_BPK + "2, false>", None, (16 + 32 + 32 + 16) * _MB),
         # config 5 layer 512 x 8192 x 8192 (256 blocks): int8 A, B and both scale vectors read; bf16 Y written
-        "c5:w8a8_packed": ("c5_step", "gemm_w8a8_bpk<", 256 * 256,
+        "c5:w8a8_packed": ("c5_step", "gemm_w8a8_bpk<vdsl::BpkConfig<vdsl::MfmaI8, 4, 1, 4, 3>", 256 * 256,
                            512 * 8192 + 8192 * 8192 + 4 * (512 + 8192) + 2 * 512 * 8192),
     }
 
