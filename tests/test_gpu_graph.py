@@ -255,3 +255,19 @@ def test_w8a8_rewritten_weights_are_repacked(dev, q):
     assert np.array_equal(exe.read(q, "Y"), oracle.w8a8_forward(x, layers))
     step.destroy()
     exe.free()
+
+
+def test_elided_values_raise(dev, q):
+    """A transposed gradient the graph elided has no buffer: reading or writing it names the reason."""
+    g, _ = graph.mlp_train_graph(256, 512, 512, 256)
+    exe = g.compile(dev)
+    try:
+        assert g.elided
+        name = sorted(g.elided)[0]
+        assert exe.t[name] is None
+        with pytest.raises(KeyError, match="elided"):
+            exe.read(q, name)
+        with pytest.raises(KeyError, match="elided"):
+            exe.write(q, name, np.zeros((1,), np.uint16))
+    finally:
+        exe.free()

@@ -379,6 +379,8 @@ class Executable:
             raise
 
     def write(self, q: Queue, name: str, host):
+        if self.t.get(name, 0) is None:
+            raise KeyError(f"{name} is elided from this graph (nothing reads it; see Graph.k_major_grads)")
         self.t[name].buffer.write(q, host)
         if any(v.name == name for op in self.graph.prepare_ops for v in op.inputs):
             self._stale.add(name)
