@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define VDSL_ABI_VERSION 2
+#define VDSL_ABI_VERSION 3
 
 typedef enum vdsl_status {
   VDSL_OK = 0,
@@ -224,12 +224,21 @@ typedef enum vdsl_map_opcode {
   VDSL_MAP_MIN = 19,
   VDSL_MAP_FMA = 20,    /* fma(r[a], r[b], r[c]), one rounding */
   VDSL_MAP_MUL_IMM = 21,/* r[a] * imm */
-  VDSL_MAP_ADD_IMM = 22 /* r[a] + imm */
+  VDSL_MAP_ADD_IMM = 22,/* r[a] + imm */
+  /* Matrix-vector products (vdsl_op_map_chain_v only; input a must be a matrix input, n = its
+   * mat_dim): the vector is v = (r[b], r[ext[0]], r[ext[1]], r[ext[2]]) cut to n components and
+   * c selects the output component.  linalg.matvec's accumulation into a zero-initialised
+   * output (color.mlir:29-36), every product and sum rounded to f32, no fused multiply-add:
+   *   MATVEC: r[dst] = ((0 + M[c][0] v0) + M[c][1] v1) + ...   (row c of M times v: M v)
+   *   VECMAT: r[dst] = ((0 + v0 M[0][c]) + v1 M[1][c]) + ...   (v times column c: v^T M)
+   * Every operand register is read before r[dst] is written, so dst may be one of them. */
+  VDSL_MAP_MATVEC = 23,
+  VDSL_MAP_VECMAT = 24
 } vdsl_map_opcode;
 
 typedef struct vdsl_map_instr {
   uint8_t op, dst, a, b, c;
-  uint8_t pad[3];
+  uint8_t ext[3];       /* VDSL_MAP_MATVEC / VECMAT: registers of vector components 1..3; else 0 */
   float imm;
 } vdsl_map_instr;
 
@@ -252,21 +261,27 @@ int vdsl_op_map_chain(vdsl_queue q, int64_t rows, int64_t cols, const vdsl_map_i
                       int32_t n_instr, const vdsl_map_input* inputs, int32_t n_inputs,
                       int32_t out_reg, vdsl_buffer out);
 
-/* ---- vector operands: the vernon dialect's vec2-4 vocabulary (source/README.md:23-55) ------- */
-/* A map-chain input whose elements are f32 vectors of `width` (1..4) components stored AoS
- * (!vernon.vec2-4 element types): element e of a FULL input is the floats [e*width, e*width+width);
- * a ROW input holds [cols][width], a COL input [rows][width], a SCALAR input [width]. */
+/* ---- vector and matrix operands: the vernon dialect's vec2-4 / mat2-4 vocabulary ------------ */
+/* (source/README.md:23-55.)  A map-chain input whose elements are f32 vectors of `width` (1..4)
+ * components (!vernon.vec2-4 element types, mat_dim 0) or f32 mat2 / mat3 / mat4 matrices
+ * (!vernon.mat2-4, mat_dim 2..4, width = mat_dim * mat_dim), stored AoS: element e of a FULL input
+ * is the floats [e*width, e*width+width), a matrix row-major (component r * mat_dim + c is M[r][c]);
+ * a ROW input holds [cols][width], a COL input [rows][width], a SCALAR input [width] (a uniform,
+ * such as the mat4 uniforms of color.mlir:5-7). */
 typedef struct vdsl_map_vinput {
   vdsl_buffer buf;
-  int32_t bcast;        /* vdsl_broadcast (a vector counts as one element) */
+  int32_t bcast;        /* vdsl_broadcast (a vector or matrix counts as one element) */
   int32_t dtype;        /* VDSL_F32 */
-  int32_t width;        /* components per element, 1..4 */
-  int32_t pad;
+  int32_t width;        /* components per element: 1..4 for a vector, mat_dim^2 for a matrix */
+  int32_t mat_dim;      /* 0: a vector; 2, 3, 4: a mat2, mat3, mat4 */
 } vdsl_map_vinput;
 
-/* The map chain over vector operands.  A LOAD (op = VDSL_MAP_LOAD, a = input, c = component)
- * reads one component of its input's element: ExtractComponentOp (README.md:41-45) fused into the
- * load; a swizzle (SwizzleOp, README.md:47-52) is several such loads, or the order of out_regs.
+/* The map chain over vector and matrix operands.  A LOAD (op = VDSL_MAP_LOAD, a = input, c =
+ * component) reads one component of its input's element: ExtractComponentOp (README.md:41-45)
+ * fused into the load, for a matrix component c = row * mat_dim + col; a swizzle (SwizzleOp,
+ * README.md:47-52) is several such loads, or the order of out_regs.  VDSL_MAP_MATVEC / VECMAT
+ * multiply a matrix input's element by a vector held in registers (linalg.matvec of
+ * color.mlir:29-36), one output component per instruction.
  * out: f32 [rows][cols][out_width] (AoS, out_width 1..4); component k of each element is
  * r[out_regs[k]] (tensor.from_elements of color.mlir:21,55).  Components are moved, never
  * rounded: a chain of loads and stores only is an exact permutation. */
@@ -360,6 +375,15 @@ int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const vdsl_pixel
  *   out:  f32 [n][4] (gl_Position);
  *   varying (optional): f32 [n][in_width] = pos (the pass-through result of color.mlir:39). */
 int vdsl_op_vec_transform(vdsl_queue q, int64_t n, int32_t in_width, vdsl_buffer pos, int32_t n_mats,
+                          vdsl_buffer mats, vdsl_buffer out, vdsl_buffer varying);
+
+/* The same chain for any square matrix type (!vernon.mat2 / mat3 / mat4, source/README.md:34-37):
+ * dim 2, 3 or 4; pos f32 [n][in_width] with in_width dim (used as is) or dim - 1 (extended to
+ * vec(pos, 1.0): homogeneous coordinates, as color.mlir:15-21 does for dim 4); mats f32
+ * [n_mats][dim][dim] row-major, n_mats 1..3, applied in order with the accumulation above cut to
+ * dim terms; out f32 [n][dim]; varying (optional) f32 [n][in_width] = pos.
+ * vdsl_op_vec_transform(q, n, w, ...) is vdsl_op_mat_transform(q, n, 4, w, ...). */
+int vdsl_op_mat_transform(vdsl_queue q, int64_t n, int32_t dim, int32_t in_width, vdsl_buffer pos, int32_t n_mats,
                           vdsl_buffer mats, vdsl_buffer out, vdsl_buffer varying);
 
 /* ========================================================================================== */

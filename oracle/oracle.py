@@ -21,6 +21,7 @@ MAP_OPS = {
     "load": 1, "const": 2, "mov": 3, "neg": 4, "abs": 5, "square": 6, "exp": 7, "log": 8,
     "tanh": 9, "sigmoid": 10, "relu": 11, "sqrt": 12, "recip": 13, "add": 14, "sub": 15,
     "mul": 16, "div": 17, "max": 18, "min": 19, "fma": 20, "mul_imm": 21, "add_imm": 22,
+    "matvec": 23, "vecmat": 24,
 }
 
 
@@ -57,7 +58,7 @@ class EscapeTimeParams(C.Structure):
 class MapInstr(C.Structure):
     _fields_ = [
         ("op", C.c_uint8), ("dst", C.c_uint8), ("a", C.c_uint8), ("b", C.c_uint8), ("c", C.c_uint8),
-        ("pad", C.c_uint8 * 3), ("imm", C.c_float),
+        ("ext", C.c_uint8 * 3), ("imm", C.c_float),
     ]
 
 
@@ -67,6 +68,7 @@ _lib.orc_map_chain_rows.argtypes = [_i64, _i64, C.POINTER(MapInstr), C.c_int, C.
 _lib.orc_map_chain_v_rows.argtypes = [_i64, _i64, C.POINTER(MapInstr), C.c_int, C.POINTER(_vp), C.POINTER(C.c_int),
                                       C.POINTER(C.c_int), C.c_int, C.POINTER(C.c_int), C.c_int, _vp, _i64, _i64]
 _lib.orc_vec_transform.argtypes = [_i64, C.c_int, _vp, C.c_int, _vp, _vp]
+_lib.orc_mat_transform.argtypes = [_i64, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp]
 _lib.orc_row_reduce_softmax_rows.argtypes = [_i64, _i64, C.c_int, _vp, _vp, _vp, _vp, _i64, _i64]
 _lib.orc_col_reduce.argtypes = [_i64, _i64, C.c_int, _vp, _vp, _vp]
 _lib.orc_gemm_bf16_rows.argtypes = [C.c_int, C.c_int, _i64, _i64, _i64, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _i64, _i64]
@@ -108,11 +110,21 @@ def escape_time(params: dict, rows=None) -> np.ndarray:
 
 
 # ---- map chain: orc_map_chain -------------------------------------------------------------------
+def _instrs(code_list):
+    """vdsl_map_instr array from (op, dst, a, b, c, imm[, ext]) tuples; ext (three registers) is
+    given only by MATVEC / VECMAT."""
+    code = (MapInstr * max(1, len(code_list)))()
+    for i, ins in enumerate(code_list):
+        op, dst, a, b, c, imm = ins[:6]
+        code[i].op, code[i].dst, code[i].a, code[i].b, code[i].c, code[i].imm = MAP_OPS[op], dst, a, b, c, imm
+        for k, r in enumerate(ins[6] if len(ins) > 6 else ()):
+            code[i].ext[k] = r
+    return code
+
+
 def map_chain(prog, inputs, rows: int, cols: int, row_range=None) -> np.ndarray:
     """prog: vernondsl_amd.mapchain.Program (its code list and broadcasts)."""
-    code = (MapInstr * max(1, len(prog.code)))()
-    for i, (op, dst, a, b, c, imm) in enumerate(prog.code):
-        code[i].op, code[i].dst, code[i].a, code[i].b, code[i].c, code[i].imm = MAP_OPS[op], dst, a, b, c, imm
+    code = _instrs(prog.code)
     arrs = [np.ascontiguousarray(x, dtype=np.float32) for x in inputs]
     ptrs = (_vp * max(1, len(arrs)))(*[a.ctypes.data for a in arrs])
     bc = (C.c_int * max(1, len(arrs)))(*[prog.bcast[k] for k in range(len(arrs))])
@@ -127,9 +139,7 @@ def map_chain(prog, inputs, rows: int, cols: int, row_range=None) -> np.ndarray:
 def map_chain_v(prog, inputs, rows: int, cols: int, row_range=None) -> np.ndarray:
     """Vector-operand chain (orc_map_chain_v_rows): prog carries widths and out_regs; returns
     [rows][cols][len(out_regs)] (or [rows][cols] for one output component) for rows [r0, r1)."""
-    code = (MapInstr * max(1, len(prog.code)))()
-    for i, (op, dst, a, b, c, imm) in enumerate(prog.code):
-        code[i].op, code[i].dst, code[i].a, code[i].b, code[i].c, code[i].imm = MAP_OPS[op], dst, a, b, c, imm
+    code = _instrs(prog.code)
     arrs = [np.ascontiguousarray(x, dtype=np.float32) for x in inputs]
     n = max(1, len(arrs))
     ptrs = (_vp * n)(*[a.ctypes.data for a in arrs])
@@ -160,6 +170,17 @@ def pixel_program(prog, ni: int, nj: int, inputs=(), rows=None) -> np.ndarray:
     out = np.zeros(shape, np.int32 if int_out else np.float32)
     ptrs = (_vp * max(1, len(ins)))(*[a.ctypes.data for a in ins])
     _lib.orc_pixel_program_rows(C.addressof(prog), ni, nj, ptrs, _p(out), r0, r1)
+    return out
+
+
+def mat_transform(pos: np.ndarray, mats: np.ndarray) -> np.ndarray:
+    """orc_mat_transform: mats f32 [k][d][d] (d = 2..4), pos f32 [n][d-1|d] -> f32 [n][d]."""
+    pos = np.ascontiguousarray(pos, np.float32)
+    mats = np.ascontiguousarray(mats, np.float32)
+    n, w = pos.shape
+    d = mats.shape[1]
+    out = np.empty((n, d), np.float32)
+    _lib.orc_mat_transform(n, d, w, _p(pos), mats.shape[0], _p(mats), _p(out))
     return out
 
 

@@ -20,6 +20,7 @@ void orc_map_chain_v_rows(int64_t rows, int64_t cols, const vdsl_map_instr* code
                           const int* bcast, const int* widths, int n_inputs, const int* out_regs, int out_width, float* out,
                           int64_t r0, int64_t r1);
 void orc_vec_transform(int64_t n, int in_width, const float* pos, int n_mats, const float* mats, float* out);
+void orc_mat_transform(int64_t n, int dim, int in_width, const float* pos, int n_mats, const float* mats, float* out);
 void orc_row_reduce_softmax_rows(int64_t rows, int64_t cols, int dtype, const void* x, float* row_sum, float* row_max,
                                  void* softmax, int64_t r0, int64_t r1);
 void orc_col_reduce(int64_t rows, int64_t cols, int dtype, const void* x, float* col_sum, float* col_max);
@@ -121,6 +122,48 @@ static void vec_transform(void) {
         orc_vec_transform(ns[s], w, pos, k, mats, out);
         free(pos); free(mats); free(out);
       }
+  for (int s = 0; s < 4; ++s)
+    for (int d = 2; d <= 4; ++d)
+      for (int w = d - 1; w <= d; ++w)
+        for (int k = 1; k <= 3; ++k) {
+          float* pos = buf((size_t)ns[s] * w * 4, 1);
+          float* mats = buf((size_t)k * d * d * 4, 1);
+          float* out = buf((size_t)ns[s] * d * 4, 0);
+          orc_mat_transform(ns[s], d, w, pos, k, mats, out);
+          free(pos); free(mats); free(out);
+        }
+}
+
+/* Matrix operands of the vector chain: every matrix size and broadcast, both products, and a load
+ * of the last matrix component, each operand buffer at exactly its contract's size. */
+static void map_chain_mat(void) {
+  const int64_t shapes[][2] = {{1, 1}, {3, 5}, {0, 4}, {2, 0}};
+  for (int s = 0; s < 4; ++s) {
+    const int64_t rows = shapes[s][0], cols = shapes[s][1];
+    for (int bc = 0; bc < 4; ++bc)
+      for (int d = 2; d <= 4; ++d) {
+        const int64_t n_in = bc == VDSL_BCAST_FULL ? rows * cols : bc == VDSL_BCAST_ROW ? cols : bc == VDSL_BCAST_COL ? rows : 1;
+        float* vec = buf((size_t)(rows * cols) * 4 * d, 1);
+        float* mat = buf((size_t)n_in * 4 * d * d, 1);
+        const float* ptrs[2] = {vec, mat};
+        const int bcast[2] = {VDSL_BCAST_FULL, bc}, widths[2] = {d, d * d};
+        vdsl_map_instr code[8];
+        memset(code, 0, sizeof code);
+        for (int k = 0; k < d; ++k) {
+          code[k].op = VDSL_MAP_LOAD; code[k].dst = (uint8_t)k; code[k].a = 0; code[k].c = (uint8_t)k;
+        }
+        code[d].op = VDSL_MAP_MATVEC; code[d].dst = 4; code[d].a = 1; code[d].b = 0; code[d].c = (uint8_t)(d - 1);
+        code[d + 1].op = VDSL_MAP_VECMAT; code[d + 1].dst = 5; code[d + 1].a = 1; code[d + 1].b = 0; code[d + 1].c = (uint8_t)(d - 1);
+        for (int k = 1; k < d; ++k) code[d].ext[k - 1] = code[d + 1].ext[k - 1] = (uint8_t)k;
+        code[d + 2].op = VDSL_MAP_LOAD; code[d + 2].dst = 6; code[d + 2].a = 1; code[d + 2].c = (uint8_t)(d * d - 1);
+        const int regs[4] = {4, 5, 6, 0};
+        float* out = buf((size_t)(rows * cols) * 4 * 3, 0);
+        orc_map_chain_v_rows(rows, cols, code, d + 3, ptrs, bcast, widths, 2, regs, 3, out, 0, rows);
+        free(out);
+        free(vec);
+        free(mat);
+      }
+  }
 }
 
 static void reductions(void) {
@@ -251,6 +294,7 @@ int main(void) {
   pixel_programs();
   map_chains();
   vec_transform();
+  map_chain_mat();
   reductions();
   gemms();
   elementwise();

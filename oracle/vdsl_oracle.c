@@ -30,10 +30,18 @@
  *                        program equals numpy fancy indexing of the components, swizzles compose
  *                        as permutations, extract_component after a swizzle picks the permuted
  *                        component, and with width-1 operands it equals orc_map_chain.
- *   orc_vec_transform    the MVP chain of color.mlir:10-39 (vec4(pos, 1) then three linalg.matvec).
- *                        Pinned by identity, permutation, power-of-two scaling and translation
- *                        matrices (exact in f32), small-integer matrices and positions (exact
- *                        integer arithmetic), and numpy f64 within a rounding bound.
+ *                        Matrix operands (mat2-4, extract_component from a matrix, and the
+ *                        MATVEC / VECMAT products of linalg.matvec, color.mlir:29-36): pinned by
+ *                        identity, permutation and power-of-two matrices (exact), small-integer
+ *                        matrices and vectors (exact integer arithmetic), numpy f64 within the
+ *                        n-term rounding bound, VECMAT equal to MATVEC on the transposed matrix,
+ *                        and an explicit numpy restatement of the accumulation order (signed zeros).
+ *   orc_mat_transform / orc_vec_transform
+ *                        the MVP chain of color.mlir:10-39 (vec(pos, 1) then linalg.matvec by up to
+ *                        three matrices; vec_transform is the mat4 case).  Pinned by identity,
+ *                        permutation, power-of-two scaling and translation matrices (exact in
+ *                        f32), small-integer matrices and positions (exact integer arithmetic),
+ *                        and numpy f64 within a rounding bound, for mat2, mat3 and mat4.
  *   orc_row_reduce_softmax / orc_col_reduce
  *                        no reference code.  Pinned by f64 sums, exact max, rows summing to 1,
  *                        constant row -> 1/cols, shift invariance, injected outlier argmax.
@@ -311,10 +319,24 @@ void orc_map_chain_v_rows(int64_t rows, int64_t cols, const vdsl_map_instr* code
       float reg[VDSL_MAP_MAX_REGS] = {0};
       for (int pc = 0; pc < n_instr; ++pc) {
         const vdsl_map_instr* s = &code[pc];
-        if (s->op == VDSL_MAP_LOAD) {
+        if (s->op == VDSL_MAP_LOAD || s->op == VDSL_MAP_MATVEC || s->op == VDSL_MAP_VECMAT) {
           const int bc = bcast[s->a], w = widths[s->a];
           const int64_t e = bc == VDSL_BCAST_FULL ? r * cols + c : bc == VDSL_BCAST_ROW ? c : bc == VDSL_BCAST_COL ? r : 0;
-          reg[s->dst] = in_ptrs[s->a][e * w + s->c];
+          const float* rec = in_ptrs[s->a] + e * w;
+          if (s->op == VDSL_MAP_LOAD) {
+            reg[s->dst] = rec[s->c];
+          } else {
+            /* a matrix input: w = n * n */
+            const int n = w == 16 ? 4 : w == 9 ? 3 : 2;
+            const int vr[4] = {s->b, s->ext[0], s->ext[1], s->ext[2]};
+            float acc = 0.0f;
+            for (int k = 0; k < n; ++k) {
+              const float m = s->op == VDSL_MAP_MATVEC ? rec[s->c * n + k] : rec[k * n + s->c];
+              const float prod = m * reg[vr[k]];
+              acc = acc + prod;
+            }
+            reg[s->dst] = acc;
+          }
         } else {
           reg[s->dst] = map_apply(s->op, reg[s->a], reg[s->b], reg[s->c], s->imm);
         }
@@ -324,30 +346,36 @@ void orc_map_chain_v_rows(int64_t rows, int64_t cols, const vdsl_map_instr* code
   }
 }
 
-/* The MVP chain of color.mlir:10-39 over n vertices: v = vec4(pos, 1) (or pos for in_width 4),
- * then for each of the n_mats row-major mat4s in order, v <- M v with
- * out[i] = (((0 + M[i][0] v0) + M[i][1] v1) + M[i][2] v2) + M[i][3] v3 (f32 products and sums, the
- * mulf/addf accumulation of linalg.matvec into a zero-initialised output). */
-void orc_vec_transform(int64_t n, int in_width, const float* pos, int n_mats, const float* mats, float* out) {
+/* The MVP chain of color.mlir:10-39 over n vertices, for dim x dim matrices (dim 2..4):
+ * v = vec(pos, 1) for in_width dim - 1 (color.mlir:15-21 for dim 4), pos itself for in_width dim;
+ * then for each of the n_mats row-major matrices in order, v <- M v with
+ * out[i] = ((0 + M[i][0] v0) + M[i][1] v1) + ... (f32 products and sums, the mulf/addf
+ * accumulation of linalg.matvec into a zero-initialised output, color.mlir:29-36). */
+void orc_mat_transform(int64_t n, int dim, int in_width, const float* pos, int n_mats, const float* mats, float* out) {
 #pragma omp parallel for schedule(static)
   for (int64_t e = 0; e < n; ++e) {
-    float v[4] = {pos[e * in_width], pos[e * in_width + 1], pos[e * in_width + 2], 1.0f};
-    if (in_width == 4) v[3] = pos[e * in_width + 3];
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < in_width; ++i) v[i] = pos[e * in_width + i];
+    if (in_width == dim - 1) v[dim - 1] = 1.0f;
     for (int t = 0; t < n_mats; ++t) {
-      const float* m = mats + 16 * t;
+      const float* m = mats + dim * dim * t;
       float o[4];
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < dim; ++i) {
         float acc = 0.0f;
-        for (int j = 0; j < 4; ++j) {
-          const float prod = m[4 * i + j] * v[j];
+        for (int j = 0; j < dim; ++j) {
+          const float prod = m[dim * i + j] * v[j];
           acc = acc + prod;
         }
         o[i] = acc;
       }
-      for (int i = 0; i < 4; ++i) v[i] = o[i];
+      for (int i = 0; i < dim; ++i) v[i] = o[i];
     }
-    for (int i = 0; i < 4; ++i) out[e * 4 + i] = v[i];
+    for (int i = 0; i < dim; ++i) out[e * dim + i] = v[i];
   }
+}
+
+void orc_vec_transform(int64_t n, int in_width, const float* pos, int n_mats, const float* mats, float* out) {
+  orc_mat_transform(n, 4, in_width, pos, n_mats, mats, out);
 }
 
 /* ---- row reduce + softmax ---------------------------------------------------------------- */

@@ -32,21 +32,24 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_abi_version():
     from vernondsl_amd import _lib
-    assert _lib.lib.vdsl_abi_version() == 2
+    assert _lib.lib.vdsl_abi_version() == 3
 
 
 def test_struct_layouts_match_header(tmp_path):
     from vernondsl_amd import _lib
     src = tmp_path / "probe.c"
     src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "vdsl.h"\n'
-                   "int main(void){printf(\"%zu %zu %zu %zu %zu %zu\\n\", sizeof(vdsl_escape_time_params),"
+                   "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(vdsl_escape_time_params),"
                    " sizeof(vdsl_map_instr), offsetof(vdsl_map_instr, imm), sizeof(vdsl_map_input),"
-                   " sizeof(vdsl_device_info), offsetof(vdsl_escape_time_params, out_scale));return 0;}\n")
+                   " sizeof(vdsl_device_info), offsetof(vdsl_escape_time_params, out_scale),"
+                   " offsetof(vdsl_map_instr, ext), sizeof(vdsl_map_vinput), offsetof(vdsl_map_vinput, mat_dim));"
+                   "return 0;}\n")
     exe = tmp_path / "probe"
     subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
     got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     want = [C.sizeof(_lib.EscapeTimeParams), C.sizeof(_lib.MapInstr), _lib.MapInstr.imm.offset,
-            C.sizeof(_lib.MapInput), C.sizeof(_lib.DeviceInfo), _lib.EscapeTimeParams.out_scale.offset]
+            C.sizeof(_lib.MapInput), C.sizeof(_lib.DeviceInfo), _lib.EscapeTimeParams.out_scale.offset,
+            _lib.MapInstr.ext.offset, C.sizeof(_lib.MapVInput), _lib.MapVInput.mat_dim.offset]
     assert got == want
 
 

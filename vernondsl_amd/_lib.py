@@ -50,6 +50,7 @@ MAP_OPS = {
     "load": 1, "const": 2, "mov": 3, "neg": 4, "abs": 5, "square": 6, "exp": 7, "log": 8,
     "tanh": 9, "sigmoid": 10, "relu": 11, "sqrt": 12, "recip": 13, "add": 14, "sub": 15,
     "mul": 16, "div": 17, "max": 18, "min": 19, "fma": 20, "mul_imm": 21, "add_imm": 22,
+    "matvec": 23, "vecmat": 24,
 }
 BCAST_FULL, BCAST_ROW, BCAST_COL, BCAST_SCALAR = 0, 1, 2, 3
 
@@ -82,7 +83,7 @@ class EscapeTimeParams(C.Structure):
 class MapInstr(C.Structure):
     _fields_ = [
         ("op", C.c_uint8), ("dst", C.c_uint8), ("a", C.c_uint8), ("b", C.c_uint8), ("c", C.c_uint8),
-        ("pad", C.c_uint8 * 3), ("imm", C.c_float),
+        ("ext", C.c_uint8 * 3), ("imm", C.c_float),
     ]
 
 
@@ -92,7 +93,7 @@ class MapInput(C.Structure):
 
 class MapVInput(C.Structure):
     _fields_ = [("buf", C.c_void_p), ("bcast", C.c_int32), ("dtype", C.c_int32), ("width", C.c_int32),
-                ("pad", C.c_int32)]
+                ("mat_dim", C.c_int32)]
 
 
 _vp = C.c_void_p
@@ -133,6 +134,7 @@ PROTOTYPES = {
     "vdsl_op_map_chain_v": (C.c_int, [_vp, _i64, _i64, C.POINTER(MapInstr), _i32, C.POINTER(MapVInput), _i32,
                                       C.POINTER(_i32), _i32, _vp]),
     "vdsl_op_vec_transform": (C.c_int, [_vp, _i64, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "vdsl_op_mat_transform": (C.c_int, [_vp, _i64, _i32, _i32, _vp, _i32, _vp, _vp, _vp]),
     "vdsl_op_gemm_bf16_mse_packed": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vdsl_debug_map_chain_mode": (C.c_int, [_i32]),
     "vdsl_debug_map_chain_stats": (C.c_int, [C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i64)]),

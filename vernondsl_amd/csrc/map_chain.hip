@@ -123,9 +123,10 @@ int launch(const MapProg& rt, const MapIn& in, float* out, int64_t rows, int64_t
 
 constexpr int kRowsV = 4;  // rows per lane step of the vector kernels
 
-int launch_v(const MapProg& rt, const MapVIn& in, const MapVOut& vo, float* out, int64_t rows, int64_t cols, hipStream_t s) {
+int launch_v(const MapProg& rt, const MapVIn& in, const MapVOut& vo, float* out, int64_t rows, int64_t cols, int comps,
+             hipStream_t s) {
   Geometry g;
-  VDSL_TRY(geometry(1, kRowsV, 4, rows, cols, g));
+  VDSL_TRY(geometry(1, kRowsV, comps, rows, cols, g));
   if (g.idx32)
     hipLaunchKernelGGL((map_chain_v_kernel<GenericProgram, kRowsV, int32_t>), g.grid, dim3(256), 0, s, rt, in, vo, out,
                        static_cast<int32_t>(rows), static_cast<int32_t>(cols));
@@ -181,7 +182,8 @@ std::string program_source(const MapProg& rt, int n_inputs, const int32_t* bcast
   for (int pc = 0; pc < rt.n; ++pc) {
     const vdsl_map_instr& c = rt.code[pc];
     s += "    {" + std::to_string(c.op) + ", " + std::to_string(c.dst) + ", " + std::to_string(c.a) + ", " +
-         std::to_string(c.b) + ", " + std::to_string(c.c) + ", {0, 0, 0}, 0.f},\n";
+         std::to_string(c.b) + ", " + std::to_string(c.c) + ", {" + std::to_string(c.ext[0]) + ", " +
+         std::to_string(c.ext[1]) + ", " + std::to_string(c.ext[2]) + "}, 0.f},\n";
   }
   s += "  };\n};\n}  // namespace vdsl\n";
   if (!vector) {
@@ -214,15 +216,15 @@ bool want_compiled(vdsl_queue q, int64_t elements) {
 // Runs a chain in its compiled form.  VDSL_OK: launched.  VDSL_ERR_UNSUPPORTED with nothing
 // enqueued: not available (not compiled yet while recording a graph, or compilation failed) - the
 // caller runs the interpreter instead.
-int launch_compiled(vdsl_queue q, const std::string& src, bool vector, void* prog_arg, void* in_arg, void* vo_arg, float* out,
-                    int64_t rows, int64_t cols) {
+int launch_compiled(vdsl_queue q, const std::string& src, bool vector, int comps, void* prog_arg, void* in_arg, void* vo_arg,
+                    float* out, int64_t rows, int64_t cols) {
   // Entries with 32- and 64-bit indices.  While recording, only a chain compiled earlier runs.
   const char* const entries[] = {"vdsl_map_jit32", "vdsl_map_jit64"};
   const JitKernels* c = nullptr;
   if (jit_kernels(q->dev->ordinal, src, entries, 2, q->capturing, g_jit, "map chain", &c) != VDSL_OK)
     return VDSL_ERR_UNSUPPORTED;
   Geometry g;
-  VDSL_TRY(geometry(vector ? 1 : 4, vector ? kRowsV : 2, vector ? 4 : 1, rows, cols, g));
+  VDSL_TRY(geometry(vector ? 1 : 4, vector ? kRowsV : 2, comps, rows, cols, g));
   int32_t r32 = static_cast<int32_t>(rows), c32 = static_cast<int32_t>(cols);
   int64_t r64 = rows, c64 = cols;
   void* a32v[] = {prog_arg, in_arg, vo_arg, &out, &r32, &c32};
@@ -238,21 +240,38 @@ int launch_compiled(vdsl_queue q, const std::string& src, bool vector, void* pro
 }
 
 // Shared validation of a chain's instructions.  widths[k]: the component count of input k (1 for
-// the scalar entry point), which bounds a LOAD's component field.
-int load_program(const vdsl_map_instr* code, int32_t n_instr, int32_t n_inputs, const int32_t* widths, MapProg& rt) {
+// the scalar entry point), which bounds a LOAD's component field; dims[k]: its matrix dimension
+// (0 for vectors), which the matrix products require.
+int load_program(const vdsl_map_instr* code, int32_t n_instr, int32_t n_inputs, const int32_t* widths, const int32_t* dims,
+                 MapProg& rt) {
   if (n_instr < 0 || n_instr > VDSL_MAP_MAX_INSTR) return fail(VDSL_ERR_INVALID_ARG, "n_instr out of range [0, 32]");
   if (n_instr && !code) return fail(VDSL_ERR_INVALID_ARG, "code is null");
   rt = MapProg{};
   rt.n = n_instr;
   for (int pc = 0; pc < n_instr; ++pc) {
     const vdsl_map_instr& s = code[pc];
-    if (s.op < VDSL_MAP_LOAD || s.op > VDSL_MAP_ADD_IMM)
-      return fail(VDSL_ERR_INVALID_ARG, "instruction " + std::to_string(pc) + ": unknown opcode " + std::to_string(s.op));
-    if (s.dst >= VDSL_MAP_MAX_REGS || s.b >= VDSL_MAP_MAX_REGS || s.c >= VDSL_MAP_MAX_REGS)
-      return fail(VDSL_ERR_INVALID_ARG, "instruction " + std::to_string(pc) + ": register out of range");
-    if (s.op == VDSL_MAP_LOAD ? (s.a >= n_inputs || s.c >= widths[s.a]) : s.a >= VDSL_MAP_MAX_REGS)
-      return fail(VDSL_ERR_INVALID_ARG, "instruction " + std::to_string(pc) + ": operand out of range");
+    const std::string at = "instruction " + std::to_string(pc) + ": ";
+    if (s.op < VDSL_MAP_LOAD || s.op > VDSL_MAP_VECMAT) return fail(VDSL_ERR_INVALID_ARG, at + "unknown opcode " + std::to_string(s.op));
     rt.code[pc] = s;
+    if (s.op == VDSL_MAP_MATVEC || s.op == VDSL_MAP_VECMAT) {
+      if (s.a >= n_inputs || dims[s.a] == 0)
+        return fail(VDSL_ERR_INVALID_ARG, at + "a matrix product needs a matrix input (vdsl_map_vinput.mat_dim 2..4)");
+      const int n = dims[s.a];
+      if (s.dst >= VDSL_MAP_MAX_REGS || s.b >= VDSL_MAP_MAX_REGS || s.c >= n)
+        return fail(VDSL_ERR_INVALID_ARG, at + "register or matrix row out of range");
+      for (int k = 0; k + 1 < n; ++k)
+        if (s.ext[k] >= VDSL_MAP_MAX_REGS) return fail(VDSL_ERR_INVALID_ARG, at + "vector register out of range");
+      // components past the matrix dimension are not read: keep them 0 so that equal products
+      // compile to one kernel
+      for (int k = n - 1; k < 3; ++k) rt.code[pc].ext[k] = 0;
+      continue;
+    }
+    // a LOAD's c is a component (up to 15 for a mat4), every other opcode's a register
+    if (s.dst >= VDSL_MAP_MAX_REGS || s.b >= VDSL_MAP_MAX_REGS || (s.op != VDSL_MAP_LOAD && s.c >= VDSL_MAP_MAX_REGS))
+      return fail(VDSL_ERR_INVALID_ARG, at + "register out of range");
+    if (s.op == VDSL_MAP_LOAD ? (s.a >= n_inputs || s.c >= widths[s.a]) : s.a >= VDSL_MAP_MAX_REGS)
+      return fail(VDSL_ERR_INVALID_ARG, at + "operand out of range");
+    rt.code[pc].ext[0] = rt.code[pc].ext[1] = rt.code[pc].ext[2] = 0;
   }
   return VDSL_OK;
 }
@@ -271,9 +290,9 @@ extern "C" int vdsl_op_map_chain(vdsl_queue q, int64_t rows, int64_t cols, const
   if (n_inputs && !inputs) return fail(VDSL_ERR_INVALID_ARG, "inputs is null");
   VDSL_TRY(check_buffer(q, out, nbytes(rows, cols, 4), "out", true));
   const int64_t n = rows * cols;  // no overflow: rows * cols * 4 fits size_t (checked above)
-  const int32_t ones[VDSL_MAP_MAX_INPUTS] = {1, 1, 1, 1};
+  const int32_t ones[VDSL_MAP_MAX_INPUTS] = {1, 1, 1, 1}, no_dims[VDSL_MAP_MAX_INPUTS] = {0, 0, 0, 0};
   MapProg rt;
-  VDSL_TRY(load_program(code, n_instr, n_inputs, ones, rt));
+  VDSL_TRY(load_program(code, n_instr, n_inputs, ones, no_dims, rt));
   rt.out_reg = out_reg;
   MapIn in{};
   in.n = n_inputs;
@@ -297,7 +316,7 @@ extern "C" int vdsl_op_map_chain(vdsl_queue q, int64_t rows, int64_t cols, const
   if (vec4 && want_compiled(q, n)) {
     const int32_t regs[4] = {out_reg, 0, 0, 0};
     const std::string src = program_source(rt, n_inputs, in.bcast, ones, regs, 1, false);
-    const int st = launch_compiled(q, src, false, &rt, &in, nullptr, o, rows, cols);
+    const int st = launch_compiled(q, src, false, 1, &rt, &in, nullptr, o, rows, cols);
     if (st != VDSL_ERR_UNSUPPORTED) return st;
   }
   if (vec4) return launch<GenericProgram, 4, 1>(rt, in, o, rows, cols, q->stream);
@@ -336,34 +355,44 @@ extern "C" int vdsl_op_map_chain_v(vdsl_queue q, int64_t rows, int64_t cols, con
   VDSL_TRY(check_buffer(q, out, nbytes(rows, cols, 4 * static_cast<int64_t>(out_width)), "out", true));
   MapVIn in{};
   in.n = n_inputs;
-  int32_t widths[VDSL_MAP_MAX_INPUTS] = {1, 1, 1, 1};
+  int32_t widths[VDSL_MAP_MAX_INPUTS] = {1, 1, 1, 1}, dims[VDSL_MAP_MAX_INPUTS] = {0, 0, 0, 0};
+  int comps = out_width;  // the widest record, which bounds the kernel's element offsets
   for (int k = 0; k < n_inputs; ++k) {
     const vdsl_map_vinput& d = inputs[k];
     if (d.dtype != VDSL_F32) return fail(VDSL_ERR_UNSUPPORTED, "map chain inputs must be f32");
     if (d.bcast < VDSL_BCAST_FULL || d.bcast > VDSL_BCAST_SCALAR) return fail(VDSL_ERR_INVALID_ARG, "unknown broadcast");
-    if (d.width < 1 || d.width > 4) return fail(VDSL_ERR_INVALID_ARG, "input width out of range [1, 4]");
+    if (d.mat_dim == 0) {
+      if (d.width < 1 || d.width > 4) return fail(VDSL_ERR_INVALID_ARG, "vector input width out of range [1, 4]");
+    } else if (d.mat_dim < 2 || d.mat_dim > 4) {
+      return fail(VDSL_ERR_INVALID_ARG, "mat_dim must be 0 (a vector), 2, 3 or 4");
+    } else if (d.width != d.mat_dim * d.mat_dim) {
+      return fail(VDSL_ERR_INVALID_ARG, "a matrix input's width must be mat_dim * mat_dim");
+    }
     const size_t need = d.bcast == VDSL_BCAST_FULL ? nbytes(rows, cols, 4 * static_cast<int64_t>(d.width))
                         : d.bcast == VDSL_BCAST_ROW ? nbytes(cols, 4 * static_cast<int64_t>(d.width))
                         : d.bcast == VDSL_BCAST_COL ? nbytes(rows, 4 * static_cast<int64_t>(d.width))
                                                     : nbytes(1, 4 * static_cast<int64_t>(d.width));
     std::string name = "input" + std::to_string(k);
     VDSL_TRY(check_buffer(q, d.buf, need, name.c_str(), false));
-    // 8- and 16-byte records need their alignment (hipMalloc bases are 256-byte aligned)
-    if ((d.width == 2 || d.width == 4) && (reinterpret_cast<uintptr_t>(d.buf->ptr) % (4 * d.width)))
-      return fail(VDSL_ERR_INVALID_ARG, name + ": base not aligned to its record size");
+    // 8- and 16-byte records (and mat4s, read as 16-byte pieces) need their alignment (hipMalloc
+    // bases are 256-byte aligned)
+    const int align = d.width == 2 ? 8 : (d.width == 4 || d.width == 16) ? 16 : 4;
+    if (reinterpret_cast<uintptr_t>(d.buf->ptr) % align) return fail(VDSL_ERR_INVALID_ARG, name + ": base not aligned to its record size");
     in.p[k] = static_cast<const float*>(d.buf->ptr);
     in.bcast[k] = d.bcast;
     in.width[k] = d.width;
     widths[k] = d.width;
+    dims[k] = d.mat_dim;
+    if (d.width > comps) comps = d.width;
   }
   MapProg rt;
-  VDSL_TRY(load_program(code, n_instr, n_inputs, widths, rt));
+  VDSL_TRY(load_program(code, n_instr, n_inputs, widths, dims, rt));
   if (rows == 0 || cols == 0) return VDSL_OK;
   float* o = static_cast<float*>(out->ptr);
   if (want_compiled(q, rows * cols)) {
     const std::string src = program_source(rt, n_inputs, in.bcast, widths, vo.regs, out_width, true);
-    const int st = launch_compiled(q, src, true, &rt, &in, &vo, o, rows, cols);
+    const int st = launch_compiled(q, src, true, comps, &rt, &in, &vo, o, rows, cols);
     if (st != VDSL_ERR_UNSUPPORTED) return st;
   }
-  return launch_v(rt, in, vo, o, rows, cols, q->stream);
+  return launch_v(rt, in, vo, o, rows, cols, comps, q->stream);
 }

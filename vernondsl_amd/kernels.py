@@ -74,11 +74,14 @@ def map_chain_v(q: Queue, prog: Program, inputs, out: Tensor):
         raise ValueError(f"program reads {prog.n_inputs} inputs, {len(inputs)} given")
     arr = (_lib.MapVInput * max(1, len(inputs)))()
     for k, t in enumerate(inputs):
-        bc, w = prog.bcast[k], prog.widths[k]
+        bc, w, d = prog.bcast[k], prog.widths[k], prog.dims.get(k, 0)
         want = {_lib.BCAST_FULL: (rows, cols), _lib.BCAST_ROW: (cols,), _lib.BCAST_COL: (rows,), _lib.BCAST_SCALAR: ()}[bc]
-        want = want + (w,) if (w > 1 or bc == _lib.BCAST_SCALAR) else want
+        if d:
+            want = want + (d, d)
+        elif w > 1 or bc == _lib.BCAST_SCALAR:
+            want = want + (w,)
         _expect(t, want, "f32", f"input{k}")
-        arr[k].buf, arr[k].bcast, arr[k].dtype, arr[k].width = t.handle.value, bc, _lib.F32, w
+        arr[k].buf, arr[k].bcast, arr[k].dtype, arr[k].width, arr[k].mat_dim = t.handle.value, bc, _lib.F32, w, d
     regs = (C.c_int32 * 4)(*(prog.out_regs + [0] * (4 - ow)))
     call("vdsl_op_map_chain_v", q.handle, rows, cols, prog.instr_array(), len(prog.code), arr, len(inputs), regs, ow,
          out.handle)
@@ -95,6 +98,18 @@ def vec_transform(q: Queue, pos: Tensor, mats: Tensor, out: Tensor, varying: Ten
     _expect(out, (n, 4), "f32", "out")
     _expect(varying, (n, w), "f32", "varying")
     call("vdsl_op_vec_transform", q.handle, n, w, pos.handle, nm, mats.handle, out.handle, _h(varying))
+
+
+def mat_transform(q: Queue, pos: Tensor, mats: Tensor, out: Tensor, varying: Tensor | None = None):
+    """out [n][d] = M_k ... M_1 vec(pos, 1) for pos [n][d-1] (or M... pos for [n][d]); mats [k][d][d]
+    row-major, d = 2, 3 or 4, k = 1..3; varying (optional) [n][d-1|d] = pos."""
+    n, w = pos.shape
+    nm, d = mats.shape[0], mats.shape[1]
+    _expect(pos, (n, w), "f32", "pos")
+    _expect(mats, (nm, d, d), "f32", "mats")
+    _expect(out, (n, d), "f32", "out")
+    _expect(varying, (n, w), "f32", "varying")
+    call("vdsl_op_mat_transform", q.handle, n, d, w, pos.handle, nm, mats.handle, out.handle, _h(varying))
 
 
 # ---- op class 3: row reductions + softmax ------------------------------------------------------

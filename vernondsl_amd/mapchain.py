@@ -19,6 +19,14 @@ Arithmetic on vectors is per component; a scalar operand applies to every compon
     pos = mc.VecInput(0, 3)                       # [rows][cols][3]
     out = mc.vec(pos.zyx * 2.0, 1.0)              # [rows][cols][4], w = 1
     prog = mc.compile(out)                        # prog.out_regs: one register per component
+
+A MatInput holds mat2-mat4 elements (!vernon.mat2-4, row-major AoS; a uniform by default, as the
+mat4 uniforms of color.mlir:5-7).  `M @ v` is linalg.matvec (color.mlir:29-36), `v @ M` the row
+vector times M, `M.T` the transposed view, `M[i, j]` / `M.component(k)` ExtractComponentOp on a
+matrix, `M[i]` / `M.row(i)` / `M.col(j)` vectors of components:
+
+    model, view, proj = (mc.MatInput(k, 4) for k in (1, 2, 3))
+    gl_position = proj @ (view @ (model @ mc.vec(pos, 1.0)))
 """
 from __future__ import annotations
 
@@ -77,7 +85,7 @@ class Expr:
 
 
 class Input(Expr):
-    def __init__(self, index: int, bcast: str = "full", width: int = 1, comp: int = 0):
+    def __init__(self, index: int, bcast: str = "full", width: int = 1, comp: int = 0, mat_dim: int = 0):
         if not 0 <= index < _lib.MAP_MAX_INPUTS:
             raise ValueError("input index out of range")
         super().__init__("load", (), 0.0)
@@ -85,9 +93,12 @@ class Input(Expr):
         self.bcast = _BCAST[bcast] if isinstance(bcast, str) else bcast
         self.width = width
         self.comp = comp
+        self.mat_dim = mat_dim
 
     def key(self):
-        return ("load", self.index) if self.width == 1 else ("load", self.index, self.comp)
+        # the operand's type is part of the key, so that one input read under two types is not
+        # merged into one load (compile() then rejects it)
+        return ("load", self.index, self.comp, self.bcast, self.width, self.mat_dim)
 
 
 _SETS = ("xyzw", "rgba", "stpq")
@@ -182,6 +193,85 @@ class VecInput(Vec):
         self.index = index
 
 
+class MatVec(Expr):
+    """One component of a matrix-vector product: row `row` of matrix input `mat` times the vector
+    (op "matvec", linalg.matvec), or the vector times column `row` (op "vecmat")."""
+
+    def __init__(self, op: str, mat: "MatInput", row: int, comps):
+        super().__init__(op, comps, 0.0)
+        self.mat, self.row = mat, row
+
+    def key(self):
+        return (self.op, self.mat.index, self.row, tuple(a.key() for a in self.args))
+
+
+class MatInput:
+    """Input `index` whose elements are dim x dim matrices (mat2 / mat3 / mat4), row-major AoS:
+    [rows][cols][dim][dim] for a full input, [cols][dim][dim] row-broadcast, [rows][dim][dim]
+    column-broadcast, [dim][dim] for a uniform (bcast "scalar", the default).  `transposed` views
+    the same operand as its transpose (no data moves: products and extraction swap indices)."""
+
+    def __init__(self, index: int, dim: int, bcast: str = "scalar", transposed: bool = False):
+        if dim not in (2, 3, 4):
+            raise ValueError("matrix inputs are mat2, mat3 or mat4")
+        if not 0 <= index < _lib.MAP_MAX_INPUTS:
+            raise ValueError("input index out of range")
+        self.index, self.dim, self.transposed = index, dim, transposed
+        self.bcast = _BCAST[bcast] if isinstance(bcast, str) else bcast
+
+    @property
+    def T(self) -> "MatInput":
+        m = MatInput(self.index, self.dim, "full", not self.transposed)
+        m.bcast = self.bcast
+        return m
+
+    def _flat(self, i: int, j: int) -> int:
+        d = self.dim
+        if not (0 <= i < d and 0 <= j < d):
+            raise IndexError(f"mat{d} index ({i}, {j}) out of range")
+        return j * d + i if self.transposed else i * d + j
+
+    def _load(self, flat: int) -> Input:
+        return Input(self.index, self.bcast, self.dim * self.dim, flat, self.dim)
+
+    def component(self, k) -> Expr:
+        """ExtractComponentOp on a matrix: component k of the row-major view (k = i * dim + j), or
+        k = (i, j)."""
+        i, j = k if isinstance(k, tuple) else divmod(int(k), self.dim)
+        return self._load(self._flat(i, j))
+
+    def row(self, i: int) -> Vec:
+        return Vec([self.component((i, j)) for j in range(self.dim)])
+
+    def col(self, j: int) -> Vec:
+        return Vec([self.component((i, j)) for i in range(self.dim)])
+
+    def __getitem__(self, k):
+        return self.component(k) if isinstance(k, tuple) else self.row(k)
+
+    def _product(self, v, left: bool) -> Vec:
+        v = v if isinstance(v, Vec) else Vec(v)
+        if v.width != self.dim:
+            raise ValueError(f"mat{self.dim} times a vec{v.width}")
+        # M v takes rows of M; v M (= M^T v) takes its columns; the transposed view swaps them.
+        rows_of_stored = left != self.transposed
+        op = "matvec" if rows_of_stored else "vecmat"
+        return Vec([MatVec(op, self, i, v.comps) for i in range(self.dim)])
+
+    def __matmul__(self, v) -> Vec:
+        """M @ v: linalg.matvec, out[i] = ((0 + M[i][0] v0) + M[i][1] v1) + ..."""
+        return self._product(v, True)
+
+    def __rmatmul__(self, v) -> Vec:
+        """v @ M: out[j] = ((0 + v0 M[0][j]) + v1 M[1][j]) + ..."""
+        return self._product(v, False)
+
+
+def matvec(m: MatInput, v) -> Vec:
+    """linalg.matvec (color.mlir:29-36): m @ v."""
+    return m @ v
+
+
 def vec(*parts) -> Vec:
     """tensor.from_elements: a vector from scalars (Expr or numbers) and vectors, in order."""
     comps = []
@@ -226,11 +316,14 @@ def fma(a, b, c):
 
 @dataclass
 class Program:
-    code: list = field(default_factory=list)   # (op, dst, a, b, c, imm); a LOAD's c is its component
+    # (op, dst, a, b, c, imm), plus ext (the registers of vector components 1..3) for MATVEC /
+    # VECMAT; a LOAD's c is its component
+    code: list = field(default_factory=list)
     out_reg: int = 0
     bcast: dict = field(default_factory=dict)  # input index -> broadcast code
-    widths: dict = field(default_factory=dict)  # input index -> components per element (1..4)
+    widths: dict = field(default_factory=dict)  # input index -> components per element (1..4, or dim^2)
     out_regs: list = field(default_factory=list)  # one register per output component
+    dims: dict = field(default_factory=dict)  # input index -> matrix dimension (0: a vector)
 
     @property
     def is_vector(self) -> bool:
@@ -242,8 +335,11 @@ class Program:
 
     def instr_array(self):
         arr = (_lib.MapInstr * max(1, len(self.code)))()
-        for i, (op, dst, a, b, c, imm) in enumerate(self.code):
+        for i, ins in enumerate(self.code):
+            op, dst, a, b, c, imm = ins[:6]
             arr[i].op, arr[i].dst, arr[i].a, arr[i].b, arr[i].c, arr[i].imm = _lib.MAP_OPS[op], dst, a, b, c, imm
+            for k, r in enumerate(ins[6] if len(ins) > 6 else ()):
+                arr[i].ext[k] = r
         return arr
 
 
@@ -284,14 +380,23 @@ def compile(expr) -> Program:  # noqa: A001 - mirrors the DSL verb
             raise ValueError(f"expression needs more than {_lib.MAP_MAX_REGS} live registers")
         dst = free.pop(0)
         reg_of[k] = dst
-        srcs = srcs + [0] * (3 - len(srcs))
+
+        def declare(index, bcast, width, dim):
+            if (prog.bcast.get(index, bcast) != bcast or prog.widths.get(index, width) != width
+                    or prog.dims.get(index, dim) != dim):
+                raise ValueError(f"input {index} is read with two different broadcasts, widths or types")
+            prog.bcast[index], prog.widths[index], prog.dims[index] = bcast, width, dim
+
         if e.op == "load":
-            if prog.bcast.get(e.index, e.bcast) != e.bcast or prog.widths.get(e.index, e.width) != e.width:
-                raise ValueError(f"input {e.index} is read with two different broadcasts or widths")
-            prog.bcast[e.index] = e.bcast
-            prog.widths[e.index] = e.width
+            declare(e.index, e.bcast, e.width, e.mat_dim)
             prog.code.append(("load", dst, e.index, 0, e.comp, 0.0))
+        elif e.op in ("matvec", "vecmat"):
+            m = e.mat
+            declare(m.index, m.bcast, m.dim * m.dim, m.dim)
+            ext = tuple(srcs[1:] + [0] * (4 - len(srcs)))
+            prog.code.append((e.op, dst, m.index, srcs[0], e.row, 0.0, ext))
         else:
+            srcs = srcs + [0] * (3 - len(srcs))
             prog.code.append((e.op, dst, srcs[0], srcs[1], srcs[2], e.imm))
 
     for k in order:
@@ -303,4 +408,5 @@ def compile(expr) -> Program:  # noqa: A001 - mirrors the DSL verb
     for i in range(prog.n_inputs):
         prog.bcast.setdefault(i, _lib.BCAST_FULL)
         prog.widths.setdefault(i, 1)
+        prog.dims.setdefault(i, 0)
     return prog
