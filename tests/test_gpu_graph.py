@@ -271,3 +271,21 @@ def test_elided_values_raise(dev, q):
             exe.write(q, name, np.zeros((1,), np.uint16))
     finally:
         exe.free()
+    # keep_y=False: y is elided, and the step's loss and gradients are those of keep_y=True
+    x, w1, w2, t = spec.mlp_inputs(batch=256, d_in=512, hidden=512, d_out=256)
+    res = []
+    for keep in (True, False):
+        g, _ = graph.mlp_train_graph(256, 512, 512, 256, keep_y=keep)
+        exe = g.compile(dev)
+        try:
+            for nm, arr in (("X", x), ("W1", w1), ("W2", w2), ("T", t)):
+                exe.write(q, nm, arr)
+            exe.run(q)
+            res.append([exe.read(q, n) for n in ("loss", "grad_W1", "grad_W2")])
+            if not keep:
+                with pytest.raises(KeyError, match="keep_y"):
+                    exe.read(q, "Y")
+        finally:
+            exe.free()
+    for a, b in zip(*res):
+        assert np.array_equal(a, b)

@@ -195,3 +195,14 @@ def test_k_major_grads_elide_transposes():
                                   fuse_gelu_backward=False, pack_weights=False, fuse_mse=False, store_gelu_deriv=False)
     assert len(g3.elided) == 2 and all(n.startswith("dT_") for n in g3.elided)
     assert all(op.attrs["trans_a"] for op in g3.ops if op.kind == "gemm" and op.outputs[0].name.startswith("grad_"))
+
+
+def test_fused_loss_without_y_elides_y():
+    """keep_y=False: the fused output GEMM + loss does not store y, so y is elided (no buffer, and
+    reading it raises) instead of an allocated buffer that is never written."""
+    g, _ = graph.mlp_train_graph(batch=256, d_in=512, hidden=512, d_out=256, keep_y=False)
+    lin = g.ops[1]
+    assert lin.kind == "linear_mse"
+    assert lin.outputs[0].name in g.elided and lin.outputs[0].name not in g.host_outputs()
+    g2, _ = graph.mlp_train_graph(batch=256, d_in=512, hidden=512, d_out=256)
+    assert g2.ops[1].outputs[0].name not in g2.elided

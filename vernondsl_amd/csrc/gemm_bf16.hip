@@ -45,8 +45,8 @@ namespace {
 using Bf0 = GemmConfig<MfmaBf16, 128, 128, 128, 2, 2>;  // wave tile 64x64
 using Bf1 = GemmConfig<MfmaBf16, 256, 128, 128, 2, 2>;  // wave tile 128x64
 using Bf2 = GemmConfig<MfmaBf16, 128, 256, 128, 2, 2>;  // wave tile 64x128
-using Bf3 = GemmConfig<MfmaBf16, 256, 256, 128, 2, 2>;  // wave tile 128x128
-using Bf4 = GemmConfig<MfmaBf16, 256, 256, 128, 2, 4>;  // 8 waves, wave tile 128x64
+using Bf3 = GemmConfig<MfmaBf16, 64, 64, 128, 2, 2>;    // wave tile 32x32: small outputs
+using Bf4 = GemmConfig<MfmaBf16, 256, 256, 64, 4, 2>;   // 8 waves, wave tile 64x128
 using Bf5 = GemmConfig<MfmaBf16, 256, 128, 128, 4, 2>;  // 8 waves, wave tile 64x64
 using Bf6 = GemmConfig<MfmaBf16, 128, 128, 256, 2, 2>;  // 128 bf16 of K per stage
 using Bf7 = GemmConfig<MfmaBf16, 128, 64, 128, 2, 2>;   // wave tile 64x32: twice the blocks of 128x128
@@ -388,7 +388,7 @@ __device__ __forceinline__ void bf16_epilogue_mse_lds(const f32x16 (&acc)[Cfg::F
 }
 
 template <class Cfg, bool EDGE, bool BWD>
-__global__ __launch_bounds__(Cfg::NT, 2) void gemm_bf16_nt(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+__global__ __launch_bounds__(Cfg::NT, Cfg::MIN_BLOCKS) void gemm_bf16_nt(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                         void* __restrict__ C, float* __restrict__ pre, int M, int N, int K,
                                                         int epi, int c_dtype, uint16_t* __restrict__ ctr) {
   __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS_BYTES];
@@ -407,7 +407,7 @@ __global__ __launch_bounds__(Cfg::NT, 2) void gemm_bf16_nt(const uint16_t* __res
 // of 4 waves for two.  BKN: B stored [K][N] (the "NN" form, no transpose first; N % 256 == 0).
 // AKM: A stored [K][M] (trans_a; M % 256 == 0), read K-major as well.
 template <class Cfg, bool BWD, bool BKN = false, bool AKM = false>
-__global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_bf16_dma(const uint16_t* __restrict__ A,
+__global__ __launch_bounds__(Cfg::NT, Cfg::MIN_BLOCKS) void gemm_bf16_dma(const uint16_t* __restrict__ A,
                                                                                const uint16_t* __restrict__ B,
                                                                                void* __restrict__ C, float* __restrict__ pre,
                                                                                int M, int N, int K, int epi, int c_dtype,
@@ -589,9 +589,14 @@ int launch_dma(const uint16_t* A, const uint16_t* B, void* C, float* pre, int M,
 // form (A stored [K][M] as well, e.g. dW = g^T x with g [batch][out] as stored): the 256 x 256
 // configuration reads both operands K-major when M % 256 == 0 too.  Returns 1 (never a status)
 // when the shape needs the transpose path instead.
+bool dma_kn_runs(int cfg, int64_t M, int64_t N, bool akm) {
+  if (N % 256 != 0) return false;
+  return akm ? (M % 256 == 0 && cfg == 15) : (cfg == 15 || cfg == 23);
+}
+
 int launch_dma_kn(int cfg, const uint16_t* A, const uint16_t* B, void* C, float* pre, int M, int N, int K, int epi, int ct,
                   hipStream_t s, bool akm = false) {
-  if (N % 256 != 0 || (akm && (M % 256 != 0 || cfg != 15))) return 1;
+  if (!dma_kn_runs(cfg, M, N, akm)) return 1;
   auto go = [&](auto cfg_tag, auto akm_tag) {
     using Cfg = decltype(cfg_tag);
     constexpr bool kAkm = decltype(akm_tag)::value;
@@ -673,7 +678,10 @@ bool stream_out(vdsl_buffer C, int epilogue, int c_dtype) {
 }
 
 // kSizeOverflow when the re-layout copies' size does not fit size_t.
+// Workspace of the transpose path: none when B is stored [K][N] and a configuration that reads the
+// operands K-major runs the shape (vdsl_op_gemm_bf16 then transposes nothing).
 size_t workspace_bytes(int ta, int tb, int64_t M, int64_t N, int64_t K) {
+  if (!tb && K % 8 == 0 && M <= 0x7fffffff && N <= 0x7fffffff && dma_kn_runs(choose_config(M, N, K), M, N, ta)) return 0;
   const size_t a = ta ? nbytes(M, K, 2) : 0, b = tb ? 0 : nbytes(N, K, 2);
   if (a == kSizeOverflow || b == kSizeOverflow || a > kSizeOverflow - 1 - b) return kSizeOverflow;
   return a + b;
@@ -707,7 +715,9 @@ extern "C" int vdsl_op_gemm_bf16(vdsl_queue q, int32_t trans_a, int32_t trans_b,
   VDSL_TRY(check_buffer(q, B, nbytes(N, K, 2), "B", false));
   VDSL_TRY(check_buffer(q, C, nbytes(M, N, dtype_size(c_dtype)), "C", true));
   if (pre_act) VDSL_TRY(check_buffer(q, pre_act, nbytes(M, N, 4), "pre_act", true));
+  // checked here, for the path this call takes (the K-major configurations need none)
   const size_t ws = workspace_bytes(ta, tb, M, N, K);
+  if (ws == kSizeOverflow) return fail(VDSL_ERR_SHAPE, "GEMM workspace size overflows (extents too large)");
   if (ws) VDSL_TRY(check_buffer(q, workspace, ws, "workspace", true));
   if (M == 0 || N == 0) return VDSL_OK;
 
@@ -715,10 +725,9 @@ extern "C" int vdsl_op_gemm_bf16(vdsl_queue q, int32_t trans_a, int32_t trans_b,
   const uint16_t* b = static_cast<const uint16_t*>(B->ptr);
   float* pre = pre_act ? static_cast<float*>(pre_act->ptr) : nullptr;
   const int epi = epilogue | (stream_out(C, epilogue, c_dtype) ? kEpiStreamOut : 0);
-  if (!tb && K % 8 == 0) {  // B stored [K][N] (and A [K][M] if ta): read K-major when a 256-wide configuration runs it
-    const int rc = launch_dma_kn(choose_config(M, N, K), a, b, C->ptr, pre, static_cast<int>(M), static_cast<int>(N),
-                                 static_cast<int>(K), epi, c_dtype, q->stream, ta);
-    if (rc != 1) return rc;
+  if (ws == 0 && !tb) {  // B stored [K][N] (and A [K][M] if ta): read K-major by a 256-wide configuration
+    return launch_dma_kn(choose_config(M, N, K), a, b, C->ptr, pre, static_cast<int>(M), static_cast<int>(N),
+                         static_cast<int>(K), epi, c_dtype, q->stream, ta);
   }
   char* w = ws ? static_cast<char*>(workspace->ptr) : nullptr;
   if (ta) {  // A stored [K][M] -> [M][K]

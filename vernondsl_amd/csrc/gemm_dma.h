@@ -52,6 +52,9 @@ struct DmaConfig {
   static constexpr int SUB = (BM + BN) * 64;         // bytes of one sub-stage
   static constexpr int STAGE = KSUB * SUB;
   static constexpr int LDS_BYTES = NS * STAGE;
+  // blocks per CU the kernel is built for (__launch_bounds__): two 4-wave blocks when their LDS
+  // fits the CU's 160 KiB, else one
+  static constexpr int MIN_BLOCKS = (NT < 512 && 2 * LDS_BYTES <= 160 * 1024) ? 2 : 1;
   static constexpr int NBLK = (BM + BN) / RPB;       // 1 KiB copy blocks per sub-stage
   static constexpr int BPW = NBLK / NW;              // copy instructions per wave per sub-stage
   static constexpr int CPW = KSUB * BPW;             // copy instructions per wave per stage

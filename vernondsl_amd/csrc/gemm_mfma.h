@@ -86,6 +86,9 @@ struct GemmConfig {
   static constexpr int A_PER_T = BM * CPR / NT, B_PER_T = BN * CPR / NT;
   static constexpr int STAGE = (BM + BN) * ROW;
   static constexpr int LDS_BYTES = 2 * STAGE;
+  // blocks per CU the kernel is built for (__launch_bounds__): two when their LDS fits the CU's
+  // 160 KiB, else one (asking for two then only caps the registers for nothing)
+  static constexpr int MIN_BLOCKS = 2 * LDS_BYTES <= 160 * 1024 ? 2 : 1;
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 MFMA tiles");
   static_assert(BKB % 32 == 0, "a stage must hold whole MFMA K steps");
   static_assert((BM * CPR) % NT == 0 && (BN * CPR) % NT == 0, "loads must split evenly over lanes");

@@ -26,8 +26,8 @@ namespace {
 using I0 = GemmConfig<MfmaI8, 128, 128, 128, 2, 2>;
 using I1 = GemmConfig<MfmaI8, 256, 128, 128, 2, 2>;
 using I2 = GemmConfig<MfmaI8, 128, 256, 128, 2, 2>;
-using I3 = GemmConfig<MfmaI8, 256, 256, 128, 2, 2>;
-using I4 = GemmConfig<MfmaI8, 256, 256, 128, 2, 4>;
+using I3 = GemmConfig<MfmaI8, 64, 64, 128, 2, 2>;   // wave tile 32x32: small outputs
+using I4 = GemmConfig<MfmaI8, 256, 256, 64, 4, 2>;  // 8 waves, wave tile 64x128
 using I5 = GemmConfig<MfmaI8, 256, 128, 128, 4, 2>;
 using I6 = GemmConfig<MfmaI8, 128, 128, 256, 2, 2>;
 using I7 = GemmConfig<MfmaI8, 128, 64, 128, 2, 2>;   // wave tile 64x32: twice the blocks of 128x128
@@ -65,7 +65,7 @@ __device__ __forceinline__ float dequant(int32_t acc, float xs, float ws, int re
 
 // SPLIT: block (x, z) covers K range [z*k_per, (z+1)*k_per) and adds its int32 tile into ws_acc.
 template <class Cfg, bool SPLIT, bool EDGE>
-__global__ __launch_bounds__(Cfg::NT, 2) void gemm_w8a8_nt(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
+__global__ __launch_bounds__(Cfg::NT, Cfg::MIN_BLOCKS) void gemm_w8a8_nt(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
                                                         const float* __restrict__ xs, const float* __restrict__ wsc,
                                                         void* __restrict__ y, int out_dtype, int relu,
                                                         int32_t* __restrict__ acc_out, int32_t* __restrict__ ws_acc, int M,
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(Cfg::NT, 2) void gemm_w8a8_nt(const int8_t* __restr
 
 // Direct-to-LDS variant (gemm_dma.h); same epilogue and split-K contract as gemm_w8a8_nt.
 template <class Cfg, bool SPLIT>
-__global__ __launch_bounds__(Cfg::NT, Cfg::NT >= 512 ? 1 : 2) void gemm_w8a8_dma(
+__global__ __launch_bounds__(Cfg::NT, Cfg::MIN_BLOCKS) void gemm_w8a8_dma(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, const float* __restrict__ xs, const float* __restrict__ wsc,
     void* __restrict__ y, int out_dtype, int relu, int32_t* __restrict__ acc_out, int32_t* __restrict__ ws_acc, int M, int N,
     int K, int k_per) {
@@ -327,7 +327,7 @@ int choose_config(int64_t M, int64_t N, int64_t K) {
 }
 
 void config_tile(int c, int& bm, int& bn) {
-  static const int t[kNumConfigs][2] = {{128, 128}, {256, 128}, {128, 256}, {256, 256}, {256, 256}, {256, 128}, {128, 128},
+  static const int t[kNumConfigs][2] = {{128, 128}, {256, 128}, {128, 256}, {64, 64}, {256, 256}, {256, 128}, {128, 128},
                                           {128, 64},  {64, 128},  {128, 128}, {256, 128}, {128, 256}, {256, 256}, {256, 128},
                                           {128, 256}, {256, 256}, {64, 128},  {128, 128}, {128, 128}, {128, 64},
                                           {128, 128}, {128, 128}, {64, 128}};

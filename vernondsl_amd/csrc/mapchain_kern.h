@@ -294,6 +294,13 @@ __device__ __forceinline__ void load_record(const float* __restrict__ p, bool st
   }
 }
 
+// Entry k (< 4) of a kernel-argument array, by compares: indexing the by-value argument struct with
+// a run-time k copies it to scratch memory.
+template <class T>
+__device__ __forceinline__ T pick(const T (&a)[VDSL_MAP_MAX_INPUTS], int k) {
+  return k == 0 ? a[0] : k == 1 ? a[1] : k == 2 ? a[2] : a[3];
+}
+
 // Element index of input k's record at (row, col) under its broadcast.
 template <class IDX>
 __device__ __forceinline__ IDX record_index(int bc, IDX row, IDX col, IDX cols) {
@@ -376,21 +383,26 @@ __device__ __forceinline__ void map_chain_v_rows(const MapProg& rt, const MapVIn
 #pragma unroll 1
         for (int pc = 0; pc < rt.n; ++pc) {
           const vdsl_map_instr s = rt.code[pc];
-          if (s.op == VDSL_MAP_LOAD || s.op == VDSL_MAP_MATVEC || s.op == VDSL_MAP_VECMAT) {
-            const int w = in.width[s.a];
-            // components beyond the register-held slots come from memory
-            const float* rec = in.p[s.a] + record_index<IDX>(in.bcast[s.a], row, col, cols) * w;
+          const bool mem = s.op == VDSL_MAP_MATVEC || s.op == VDSL_MAP_VECMAT || (s.op == VDSL_MAP_LOAD && pick(in.width, s.a) > S);
+          if (s.op == VDSL_MAP_LOAD && !mem) {
+            r[s.dst] = e[S * s.a + s.c];
+          } else if (mem) {
+            // components beyond the register-held slots, and matrix entries, come from memory (the
+            // record is in the cache after its first use); a branch of its own keeps e in registers
+            const int w = pick(in.width, s.a);
+            const float* rec = pick(in.p, s.a) + record_index<IDX>(pick(in.bcast, s.a), row, col, cols) * w;
             if (s.op == VDSL_MAP_LOAD) {
-              r[s.dst] = w <= S ? e[S * s.a + s.c] : rec[s.c];
+              r[s.dst] = rec[s.c];
             } else {
               const int n = mat_dim_of(w);
               const int vr[4] = {s.b, s.ext[0], s.ext[1], s.ext[2]};
               float acc = 0.0f;
-#pragma unroll 1
-              for (int k = 0; k < n; ++k) {
-                const int ci = s.op == VDSL_MAP_MATVEC ? s.c * n + k : k * n + s.c;
-                const float m = w <= S ? e[S * s.a + ci] : rec[ci];
-                acc = acc + m * r[vr[k]];
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                if (k < n) {
+                  const int ci = s.op == VDSL_MAP_MATVEC ? s.c * n + k : k * n + s.c;
+                  acc = acc + rec[ci] * r[vr[k]];
+                }
               }
               r[s.dst] = acc;
             }

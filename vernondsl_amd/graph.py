@@ -208,6 +208,8 @@ class Graph:
             lin.outputs += [loss, dy, dy_t, part]
             for v in (loss, dy, dy_t, part):
                 v.producer = lin
+            if not self.keep_y:  # the fused op does not store y: nothing holds it
+                self.elided.add(y.name)
         param_grads = {}
         for op in reversed(fwd_ops):
             if op.kind == "mse":
@@ -296,7 +298,7 @@ class Graph:
             if op.kind == "transpose" and op.outputs[0].name in dead:
                 self.ops.remove(op)
                 del self.values[op.outputs[0].name]
-        self.elided = {n for n in dead if n in self.values}
+        self.elided |= {n for n in dead if n in self.values}
 
     def _param_transpose(self, w: Value) -> Value:
         """W^T of a param, made by a prepare op (once per write of W, outside the replayed step)."""
@@ -380,7 +382,8 @@ class Executable:
 
     def write(self, q: Queue, name: str, host):
         if self.t.get(name, 0) is None:
-            raise KeyError(f"{name} is elided from this graph (nothing reads it; see Graph.k_major_grads)")
+            raise KeyError(f"{name} is elided from this graph (no op stores it: a transposed gradient nothing reads, "
+                           "see Graph.k_major_grads, or y of a fused loss built with keep_y=False)")
         self.t[name].buffer.write(q, host)
         if any(v.name == name for op in self.graph.prepare_ops for v in op.inputs):
             self._stale.add(name)
@@ -406,7 +409,8 @@ class Executable:
 
     def read(self, q: Queue, name: str):
         if self.t.get(name, 0) is None:
-            raise KeyError(f"{name} is elided from this graph (nothing reads it; see Graph.k_major_grads)")
+            raise KeyError(f"{name} is elided from this graph (no op stores it: a transposed gradient nothing reads, "
+                           "see Graph.k_major_grads, or y of a fused loss built with keep_y=False)")
         return self.t[name].numpy(q)
 
     def run(self, q: Queue, events=None):
