@@ -250,10 +250,9 @@ def bench_map_chain(dev, q, steps, warmup, do_cpu):
 
 
 def bench_map_chain_generic(dev, q, steps, warmup, do_cpu):
-    """The map chain as an op class: config 2's chain (which the library runs as a built-in
-    specialisation by default) in the generic interpreter and compiled at run time, and a second
-    chain of another shape, sigmoid(x) * colvec[row] + x^2 with a per-row operand, which has no
-    built-in specialisation, in both forms.  All on [8192][8192] f32, HBM GB/s from algorithmic
+    """The map chain as an op class: config 2's chain in the generic interpreter (the headline runs
+    it compiled at run time), and a second chain of another shape, sigmoid(x) * colvec[row] + x^2
+    with a per-row operand, in both forms.  All on [8192][8192] f32, HBM GB/s from algorithmic
     bytes."""
     from vernondsl_amd import _lib, kernels, mapchain as mc, spec
     from vernondsl_amd.rhi import Tensor
@@ -269,9 +268,8 @@ def bench_map_chain_generic(dev, q, steps, warmup, do_cpu):
     b1, b2 = spec.map_chain_bytes(rows, cols), 8 * rows * cols + 4 * rows
     c2 = "sigmoid(x) * colvec[row] + x^2"
     cases = (("config-2 chain, generic interpreter", p1, [tx, tb], 1, b1),
-             ("config-2 chain, compiled at run time (instead of the built-in specialisation)", p1, [tx, tb], 2, b1),
              (c2 + ", generic interpreter", p2, [tx, tc], 1, b2),
-             (c2 + ", compiled at run time (the default for it)", p2, [tx, tc], 0, b2))
+             (c2 + ", compiled at run time", p2, [tx, tc], 0, b2))
     for name, prog, ins, mode, nbytes in cases:
         _lib.call("vdsl_debug_map_chain_mode", mode)
         per = 10
@@ -365,6 +363,35 @@ def bench_vecmat(dev, q, steps, warmup, do_cpu):
     out.append(res)
     tx.free()
     ty.free()
+    # a matrix operand per element: mat4 [4096][4096] times vec4 -> vec4 (linalg.matvec per element,
+    # the mat4 records staged through LDS by the compiled kernel)
+    v = r.standard_normal((rows, cols, 4)).astype(np.float32)
+    m = r.standard_normal((rows, cols, 4, 4)).astype(np.float32)
+    prog = mc.compile(mc.MatInput(1, 4, "full") @ mc.VecInput(0, 4))
+    tv, tm, ty = Tensor.from_numpy(dev, q, v), Tensor.from_numpy(dev, q, m), Tensor(dev, (rows, cols, 4), "f32")
+    ms, _ = time_replays(q, dev, lambda: kernels.map_chain_v(q, prog, [tv, tm], ty), max(1, steps // per),
+                         max(1, warmup // per), per_graph=per)
+    nbytes = rows * cols * (64 + 16 + 16)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    res = {"config": "matvec", "workload": f"mat4 @ vec4 per element, [{rows}][{cols}] (vdsl_op_map_chain_v MATVEC)",
+           "metric": "achieved HBM GB/s", "value": gbs, "unit": "GB/s", "ms_per_launch": ms, "parity": NOT_CHECKED,
+           "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                        "bytes_per_launch": nbytes, "traffic": measured_traffic("matvec"), "kernel": "vdsl_map_jit32"}}
+    if do_cpu:
+        from oracle import oracle
+        got = ty.numpy(q)
+        rs = (0, 2049, rows - 1)
+        ok = all(np.array_equal(got[i], oracle.map_chain_v(prog, [v, m], rows, cols, row_range=(i, i + 1))[0]) for i in rs)
+        res["parity"] = "ok (3 rows bit-exact)" if ok else "FAIL"
+        s, s1 = 512, 64
+        res["cpu_baseline"] = cpu_baseline(
+            oracle, lambda: oracle.map_chain_v(prog, [v, m], rows, cols, row_range=(0, s)), nbytes * s / rows / 1e9, "GB/s",
+            f"first {s} of {rows} rows, oracle orc_map_chain_v_rows",
+            lambda: oracle.map_chain_v(prog, [v, m], rows, cols, row_range=(0, s1)), nbytes * s1 / rows / 1e9,
+            f"first {s1} of {rows} rows", reps=3)
+    out.append(res)
+    for t_ in (tv, tm, ty):
+        t_.free()
     return out
 
 
@@ -567,6 +594,8 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
     tflops = flops / (ms * 1e-3) / 1e12
     gemm_ms = sum(r["ms"] for r in rows if "rate" in r)
     loss = float(exe.read(q, "loss")[0])
+    b = 64  # the rows the CPU leg runs; their forward outputs are checked against its oracle run
+    y_rows, h_rows = exe.read(q, "Y")[:b], exe.read(q, "H")[:b]
     step.destroy()
     exe.free()
     gt = dom_flop / (dom_ms * 1e-3) / 1e12
@@ -579,10 +608,19 @@ def bench_mlp(dev, q, steps, warmup, do_cpu):
            "roofline": {"bound": "mfma", "achieved": gt, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                         "frac": gt / PEAK_BF16_TFLOPS, "kernel": f"dominant in-step op: {dom_op}",
                         "kernel_ms": dom_ms, "traffic": measured_traffic("c4:" + dom_kind)},
-           "whole_graph_frac_of_peak": tflops / PEAK_BF16_TFLOPS}
-    if do_cpu:  # CPU-baseline leg
+           "whole_graph_frac_of_peak": tflops / PEAK_BF16_TFLOPS, "parity": NOT_CHECKED}
+    if do_cpu:  # CPU-baseline leg; its oracle run on the first rows is also the checker
         from oracle import oracle
-        b, b1 = 64, 8
+        from vernondsl_amd import rng as vrng
+        b1 = 8
+        ref = oracle.mlp_train_step(x[:b], w1, w2, t[:b])
+
+        def frob(got, want):
+            got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+            return float(np.linalg.norm(got - want) / np.linalg.norm(want))
+        ey, eh = frob(y_rows, ref["Y"]), frob(vrng.bf16_to_f32(h_rows), vrng.bf16_to_f32(ref["H"]))
+        res["parity"] = (f"ok (Y, H of {b} rows: Frobenius-relative {ey:.1e}, {eh:.1e} <= 1e-2)" if max(ey, eh) <= 1e-2
+                         else f"FAIL (Y {ey:.2e}, H {eh:.2e})")
         res["cpu_baseline"] = cpu_baseline(
             oracle, lambda: oracle.mlp_train_step(x[:b], w1, w2, t[:b]), spec.mlp_flops(b, D, Hd, O) / 1e12, "TFLOP/s",
             f"the same step at batch {b} of {B} (every GEMM keeps its 4096x4096 weight shape), f64-accumulating oracle",
@@ -659,13 +697,15 @@ def _traffic_kernels():
     from vernondsl_amd import _lib, spec
     return {
         "copy": ("copy", "copyBuffer", None, 2 * (512 << 20)),
-        "map_chain": ("map_chain", "map_chain_kernel", None, spec.map_chain_bytes(8192, 8192)),
+        "map_chain": ("map_chain", "vdsl_map_jit", None, spec.map_chain_bytes(8192, 8192)),  # compiled at run time
         "softmax_f32": ("softmax_f32", "row_softmax_split<0", None, spec.softmax_bytes(16384, 4096, _lib.F32)),
         "softmax_bf16": ("softmax_bf16", "row_softmax_split<1", None, spec.softmax_bytes(16384, 4096, _lib.BF16)),
         # vec3 positions read, vec4 positions and vec3 varyings written (2^24 vertices)
-        "vec_transform": ("vec_transform", "vec_transform_kernel", None, (1 << 24) * 40),
+        "vec_transform": ("vec_transform", "mat_transform_kernel", None, (1 << 24) * 40),
         # vec4 [4096][4096] read and written
         "swizzle": ("swizzle", "vdsl_map_jit", None, 2 * 4096 * 4096 * 16),  # the chain compiled at run time
+        # mat4 and vec4 [4096][4096] read, vec4 written
+        "matvec": ("matvec", "vdsl_map_jit", None, 4096 * 4096 * 96),
         # heat.py's stencil on 8192^2 f32: the field read once, the result written once
         "pixel_stencil": ("pixel_stencil", "vdsl_pix_jit", None, 8 * HEAT_N * HEAT_N),
         # config 4 (2048 x 4096 x 4096 and 4096 x 4096 x 2048 bf16): operands read once, outputs written once
@@ -789,6 +829,13 @@ def run_kernel_only(dev, q, name, reps):
         tx.buffer.fill_u32(q, 0x3F800000)
         prog = mc.compile(mc.VecInput(0, 4).bgra)
         fn, ts = (lambda: kernels.map_chain_v(q, prog, [tx], ty)), [tx, ty]
+    elif name == "matvec":
+        tv, tm = Tensor(dev, (4096, 4096, 4), "f32"), Tensor(dev, (4096, 4096, 4, 4), "f32")
+        tv.buffer.fill_u32(q, 0x3F800000)
+        tm.buffer.fill_u32(q, 0x3F000000)
+        ty = Tensor(dev, (4096, 4096, 4), "f32")
+        prog = mc.compile(mc.MatInput(1, 4, "full") @ mc.VecInput(0, 4))
+        fn, ts = (lambda: kernels.map_chain_v(q, prog, [tv, tm], ty)), [tv, tm, ty]
     elif name == "pixel_stencil":
         prog = heat_program()
         tu, tv = Tensor(dev, (HEAT_N, HEAT_N), "f32"), Tensor(dev, (HEAT_N, HEAT_N), "f32")
@@ -812,6 +859,38 @@ def run_kernel_only(dev, q, name, reps):
     print(json.dumps({"kernel": name, "reps": reps}), flush=True)
 
 
+def _round(x, sig=4):
+    if isinstance(x, float):
+        return float(f"{x:.{sig}g}")
+    if isinstance(x, dict):
+        return {k: _round(v, sig) for k, v in x.items()}
+    if isinstance(x, list):
+        return [_round(v, sig) for v in x]
+    return x
+
+
+# Fields the one-line summary leaves out (the full records go to stderr as each config finishes):
+# the single-core and median details of a CPU baseline and explanatory notes.
+_CPU_KEEP = ("value", "unit", "cores", "kind", "sample", "single_core_value")
+
+
+def _compact(entry):
+    """A per-config record as it appears in the printed line: values to 4 significant digits, the
+    CPU baseline reduced to its value, unit, cores, kind, sample and single-core value, notes
+    dropped, in-step op lists reduced to (op, ms, frac)."""
+    e = {k: v for k, v in entry.items() if k not in ("note", "metric")}
+    if isinstance(e.get("cpu_baseline"), dict):
+        e["cpu_baseline"] = {k: v for k, v in e["cpu_baseline"].items() if k in _CPU_KEEP}
+    if isinstance(e.get("roofline"), dict):
+        rf = {k: v for k, v in e["roofline"].items() if k != "note"}
+        if isinstance(rf.get("valu_issue"), dict):
+            rf["valu_issue"] = rf["valu_issue"].get("valu_issue_frac")
+        e["roofline"] = rf
+    if isinstance(e.get("in_step"), dict) and isinstance(e["in_step"].get("ops"), list):
+        e["in_step"] = dict(e["in_step"], ops=[{k: o[k] for k in ("op", "ms", "frac") if k in o} for o in e["in_step"]["ops"]])
+    return _round(e)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -826,7 +905,7 @@ def main():
                     help="comma-separated config ids (as for --only) to leave out of the run")
     ap.add_argument("--kernel", default="", help="run one kernel --reps times and exit (for rocprofv3 --pmc): "
                     "map_chain, softmax_f32, softmax_bf16, gemm_bf16, gemm_w8a8, escape_time, pixel_stencil, vec_transform, "
-                    "swizzle, copy, c4_step, c5_step")
+                    "swizzle, matvec, copy, c4_step, c5_step")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--traffic-summary", default="", metavar="DIR",
                     help="write profiles/traffic.json from the counter runs in DIR and exit (no GPU needed)")
@@ -884,10 +963,10 @@ def main():
         "parity": head["parity"],
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(head["gbs"] / PEAK_HBM_GBS, 4), "traffic": measured_traffic("map_chain"),
-                     "kernel": "map_chain_kernel<ProgTanhExpBias,4,2,int32_t>"},
+                     "kernel": "vdsl_map_jit32 (the chain compiled at run time)"},
         "cpu_baseline": head.get("cpu"),
         "device": {"name": info["name"], "arch": info["arch"], "compute_units": info["compute_units"]},
-        "per_config": per_config,
+        "per_config": [_compact(e) for e in per_config],
     }
     q.destroy()
     dev.close()

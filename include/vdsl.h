@@ -559,16 +559,17 @@ int vdsl_debug_gemm_config(int32_t config);
 int vdsl_debug_w8a8_packed_plan(int32_t cfg, int32_t split);
 
 /* ---- map-chain forms (benchmarks and tests, host-side only) ---------------------------------- */
-/* A map chain (vdsl_op_map_chain, vdsl_op_map_chain_v) runs as a specialisation built into the
- * library, as a kernel compiled at run time for the chain (cached per chain and device; the
- * chain's immediates stay arguments), or in the generic interpreter; all three give the same
- * bits.  mode 0 (default): built-in specialisation if one matches, else the compiled form for
- * launches of at least 2^20 elements, else the interpreter; 1: the interpreter for every chain;
- * 2: the compiled form for every chain (built-in specialisations skipped).  A chain not compiled
- * before a queue starts recording a graph is recorded in the interpreter (nothing is compiled
- * while recording); a chain whose compilation fails runs in the interpreter.  Also settable with
- * the environment variable VDSL_MAP_MODE.  No counterpart in the reference; callers are
- * benchmarks and the tests that compare the forms. */
+/* A map chain (vdsl_op_map_chain, vdsl_op_map_chain_v) runs as a kernel compiled at run time for
+ * the chain (hiprtc, for the device's architecture; cached per chain and device, at most 512
+ * programs per device, shared with the per-pixel programs' cache; the chain's immediates stay
+ * arguments) or in the generic interpreter; both give the same bits.  mode 0 (default): the
+ * compiled form for launches of at least 2^20 elements, the interpreter for smaller ones; 1: the
+ * interpreter for every chain; 2: the compiled form for every chain.  Nothing is compiled while a
+ * queue records a graph: a chain that needs its compiled form and was not run before the
+ * recording started fails with VDSL_ERR_CAPTURE.  A failed compilation fails the op (VDSL_ERR_DEVICE,
+ * with the compiler's log), as does a full cache (VDSL_ERR_UNSUPPORTED).  Also settable with the
+ * environment variable VDSL_MAP_MODE.  No counterpart in the reference; callers are benchmarks
+ * and the tests that compare the forms. */
 int vdsl_debug_map_chain_mode(int32_t mode);
 /* Counters since the library was loaded: launches in compiled form, compilations, failed
  * compilations (any pointer may be NULL). */

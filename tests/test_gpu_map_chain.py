@@ -42,24 +42,6 @@ def test_config2_chain_small(dev, q, rows, cols):
     assert np.all(err <= REL * config2_scale(x, bias)), float(np.max(err / config2_scale(x, bias)))
 
 
-def test_config2_full_size_sampled(dev, q):
-    rows = cols = 8192
-    x, bias = spec.map_chain_inputs(rows, cols)
-    prog = mc.compile(spec.map_chain_expr())
-    got = run_chain(dev, q, prog, [x, bias], rows, cols)
-    assert np.isfinite(got).all()
-    # oracle on a seeded sample of rows, including the first and last
-    rr = sorted({0, rows - 1, *np.random.default_rng(11).integers(0, rows, 62).tolist()})
-    for r in rr:
-        ref = oracle.map_chain(prog, [x, bias], rows, cols, row_range=(r, r + 1))[0]
-        sc = config2_scale(x[r:r + 1], bias)[0]
-        assert np.all(np.abs(got[r].astype(np.float64) - ref) <= REL * sc), f"row {r}"
-    # size-independent property: where exp(-x^2) underflows (|x| > ~10) y == bias exactly;
-    # elsewhere y - bias stays within tanh's range
-    d = got.astype(np.float64) - bias[None, :]
-    assert np.all(np.abs(d) <= 1.0 + 1e-6)
-
-
 def test_generic_program_and_broadcasts(dev, q):
     rng = np.random.default_rng(5)
     rows, cols = 67, 1000
@@ -303,7 +285,7 @@ def test_random_exact_programs_end_to_end(dev, q, seed):
         assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32)), prog.code
 
 
-# ---- the three forms of a chain: built-in specialisation, compiled at run time, interpreter ----------
+# ---- the two forms of a chain: compiled at run time, interpreter -----------------------------------
 def _stats():
     import ctypes
     v = [ctypes.c_int64() for _ in range(3)]
@@ -383,37 +365,68 @@ def test_vector_chains_compiled_equal_interpreted(dev, q):
         assert np.array_equal(i, oracle.map_chain_v(prog, ins, rows, cols)) or "tanh" in str(prog.code)
 
 
-def test_recording_uses_compiled_chains_only_if_compiled_before(dev, q):
-    """While a queue records a graph nothing is compiled: a chain first seen there is recorded in
-    the interpreter; one compiled earlier is recorded in compiled form.  Replays equal eager runs."""
-    rows, cols = 64, 1024
+def test_recording_an_uncompiled_chain_is_refused(dev, q):
+    """Nothing is compiled while a queue records a graph: a chain that needs its compiled form and
+    was not run before the recording fails with VDSL_ERR_CAPTURE (no silent interpreter), the
+    recording can be ended and the queue used again; once the chain has run eagerly it records in
+    compiled form, and the replays equal the eager run bit for bit.  A small chain (the
+    interpreter's by the size rule, eagerly too) records as it runs eagerly."""
+    rows, cols = 1024, 1024          # 2^20 elements: the compiled form in the default mode
     x = np.random.default_rng(3200).standard_normal((rows, cols)).astype(np.float32)
     tx, ty = Tensor.from_numpy(dev, q, x), Tensor(dev, (rows, cols), "f32")
-    fresh = mc.compile(mc.sigmoid(mc.Input(0)) * 0.375 + mc.Input(0) * mc.Input(0) * 0.125)
-    seen = mc.compile(mc.relu(mc.Input(0)) * 1.25 - mc.Input(0) * 0.0625)
-    try:
-        _lib.call("vdsl_debug_map_chain_mode", 2)
-        kernels.map_chain(q, seen, [tx], ty)      # compiled eagerly
-        eager_seen = ty.numpy(q)
-        launches0, compiles0, _ = _stats()
-        with q.capture() as rec:
+    fresh = mc.compile(mc.sigmoid(mc.Input(0)) * 0.375 + mc.Input(0) * mc.Input(0) * 0.125 - 0.5)
+    launches0, compiles0, _ = _stats()
+    with pytest.raises(_lib.VdslError) as err:
+        with q.capture():
             kernels.map_chain(q, fresh, [tx], ty)
-        g1 = rec.graph
-        assert _stats()[:2] == [launches0, compiles0]   # interpreter, nothing compiled
-        with q.capture() as rec:
-            kernels.map_chain(q, seen, [tx], ty)
-        g2 = rec.graph
-        assert _stats()[:2] == [launches0 + 1, compiles0]
-    finally:
-        _lib.call("vdsl_debug_map_chain_mode", 0)
+    assert err.value.status == -6 and "run it once before recording" in str(err.value)
+    assert _stats()[:2] == [launches0, compiles0] and not q.capturing
+    kernels.map_chain(q, fresh, [tx], ty)       # compiled here, eagerly
+    eager = ty.numpy(q)
+    assert _stats()[:2] == [launches0 + 1, compiles0 + 1]
+    with q.capture() as rec:
+        kernels.map_chain(q, fresh, [tx], ty)
+    g = rec.graph
+    assert _stats()[:2] == [launches0 + 2, compiles0 + 1]
     for _ in range(3):
         ty.buffer.fill_u32(q, 0x7FC00000)
-        g1.launch(q)
+        g.launch(q)
         q.sync()
-        assert np.array_equal(ty.numpy(q), _in_mode(1, lambda: run_chain(dev, q, fresh, [x], rows, cols)))
-        ty.buffer.fill_u32(q, 0x7FC00000)
-        g2.launch(q)
-        q.sync()
-        assert np.array_equal(ty.numpy(q), eager_seen)
-    for t in (g1, g2, tx, ty):
-        t.destroy() if hasattr(t, "launch") else t.free()
+        assert np.array_equal(ty.numpy(q).view(np.uint32), eager.view(np.uint32))
+    g.destroy()
+    # a small launch of a never-compiled chain: the interpreter, recorded as it runs eagerly
+    small = mc.compile(mc.relu(mc.Input(0)) * 1.25 - mc.Input(0) * 0.0625 + 0.25)
+    ts, tys = Tensor.from_numpy(dev, q, x[:8]), Tensor(dev, (8, cols), "f32")
+    with q.capture() as rec:
+        kernels.map_chain(q, small, [ts], tys)
+    assert _stats()[:2] == [launches0 + 2, compiles0 + 1]
+    rec.graph.launch(q)
+    q.sync()
+    assert np.array_equal(tys.numpy(q), oracle.map_chain(small, [x[:8]], 8, cols))
+    rec.graph.destroy()
+    for t in (tx, ty, ts, tys):
+        t.free()
+
+
+@pytest.mark.parametrize("cols", [8192, 8190])
+def test_full_size_config2_chain_every_element(dev, q, cols):
+    """Config 2's chain at full size ([8192][8192], and a column count that is not a multiple of 4,
+    which the compiled kernel runs with one column per lane): every element against the oracle to
+    the config's 1e-5 bar, in both forms, and the two forms equal bit for bit."""
+    rows = 8192
+    x, bias = spec.map_chain_inputs(rows, cols)
+    prog = mc.compile(spec.map_chain_expr())
+    ref = oracle.map_chain(prog, [x, bias], rows, cols).astype(np.float64)
+    scale = config2_scale(x, bias)
+    forms = {}
+    for mode in (0, 1):   # default (compiled at this size), interpreter
+        before = _stats()[0]
+        forms[mode] = _in_mode(mode, lambda: run_chain(dev, q, prog, [x, bias], rows, cols))
+        assert _stats()[0] == before + (1 if mode == 0 else 0)
+        bad = np.abs(forms[mode].astype(np.float64) - ref) > REL * scale
+        assert not bad.any(), (mode, int(bad.sum()), np.argwhere(bad)[:5])
+    assert np.array_equal(forms[0].view(np.uint32), forms[1].view(np.uint32))
+    # size-independent property: y - bias stays within tanh's range, and y == bias exactly where
+    # exp(-x^2) underflows
+    d = forms[0].astype(np.float64) - bias[None, :]
+    assert np.all(np.abs(d) <= 1.0 + 1e-6)

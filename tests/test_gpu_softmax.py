@@ -59,12 +59,8 @@ def test_config3_full_size(dev, q, bf16):
     xh = rng.f32_to_bf16(x) if bf16 else x
     got = run(dev, q, xh, "bf16" if bf16 else "f32")
     gs, gm, gsm = got
-    rows = x.shape[0]
-    # oracle on a sample of rows (every outlier row among them)
-    sample = np.unique(np.concatenate([orows[:20], np.random.default_rng(1).integers(0, rows, 40), [0, rows - 1]]))
-    for r in sample:
-        ref = oracle.row_reduce_softmax(xh, row_range=(int(r), int(r) + 1))
-        check(xh[r:r + 1], (gs[r:r + 1], gm[r:r + 1], gsm[r:r + 1]), ref, bf16)
+    # every row and element against the oracle (the whole [16384][4096] workload)
+    check(xh, got, oracle.row_reduce_softmax(xh), bf16)
     # size-independent properties on every row
     smf = rng.bf16_to_f32(gsm) if bf16 else gsm
     tol = 3e-2 if bf16 else 1e-4

@@ -6,17 +6,17 @@
 // such as tanh(a*x + b) * exp(-x^2) + bias[col] costs one HBM read of each operand and one
 // write of the result.  The device code is mapchain_kern.h.
 //
-// A chain runs in one of three forms, all from the same source and bit-identical:
-//   - a compile-time specialisation built into the library (ProgTanhExpBias, config 2's chain),
-//     chosen when a runtime chain's opcodes, registers and broadcasts equal its table;
+// A chain runs in one of two forms, from the same source and bit-identical:
 //   - a kernel compiled at run time for the chain (hiprtc, for the device's architecture, with the
 //     library's own compile flags): the chain becomes a compile-time table and the interpreter
 //     unrolls into straight-line code.  Compiled once per distinct chain and device (the
-//     immediates are kernel arguments, not part of the compiled code), for launches of at least
-//     kCompileMinElements elements, never while the queue is recording a graph;
-//   - the generic interpreter, a kernel argument program with uniform dispatch: small launches,
-//     chains first seen while recording, and the fallback if run-time compilation fails.
-// vdsl_debug_map_chain_mode selects the interpreter or the compiled form for every chain.
+//     immediates are kernel arguments, not part of the compiled code), for every launch of at
+//     least kCompileMinElements elements;
+//   - the generic interpreter, a kernel argument program with uniform dispatch, for smaller
+//     launches (microseconds of work, against a fraction of a second to compile).
+// Nothing is compiled while a queue records a graph: a large chain first met there fails with
+// VDSL_ERR_CAPTURE (run it once before recording), and a failed compilation is an error, not a
+// fallback to the interpreter.  vdsl_debug_map_chain_mode selects one form for every chain.
 
 #include <cstdlib>
 #include <string>
@@ -28,28 +28,6 @@
 namespace vdsl {
 namespace {
 
-// Compile-time programs.  Each lists its opcodes/registers, input broadcasts and output register.
-struct ProgTanhExpBias {
-  // y = tanh(x * a + b) * exp(-(x * x)) + bias[col]   (input 0 = x: FULL, input 1 = bias: ROW),
-  // register-allocated exactly as vernondsl_amd.mapchain.compile emits it.
-  static constexpr int n = 10;
-  static constexpr int n_inputs = 2;
-  static constexpr int out_reg = 0;
-  __host__ __device__ static constexpr int bcast_of(int k) { return k == 1 ? VDSL_BCAST_ROW : VDSL_BCAST_FULL; }
-  static constexpr vdsl_map_instr code[VDSL_MAP_MAX_INSTR] = {
-      {VDSL_MAP_LOAD, 0, 0, 0, 0, {0, 0, 0}, 0.f},     // r0 = x
-      {VDSL_MAP_MUL_IMM, 1, 0, 0, 0, {0, 0, 0}, 0.f},  // r1 = r0 * a
-      {VDSL_MAP_ADD_IMM, 1, 1, 0, 0, {0, 0, 0}, 0.f},  // r1 = r1 + b
-      {VDSL_MAP_TANH, 1, 1, 0, 0, {0, 0, 0}, 0.f},     // r1 = tanh(r1)
-      {VDSL_MAP_SQUARE, 0, 0, 0, 0, {0, 0, 0}, 0.f},   // r0 = r0 * r0
-      {VDSL_MAP_NEG, 0, 0, 0, 0, {0, 0, 0}, 0.f},      // r0 = -r0
-      {VDSL_MAP_EXP, 0, 0, 0, 0, {0, 0, 0}, 0.f},      // r0 = exp(r0)
-      {VDSL_MAP_MUL, 0, 1, 0, 0, {0, 0, 0}, 0.f},      // r0 = r1 * r0
-      {VDSL_MAP_LOAD, 1, 1, 0, 0, {0, 0, 0}, 0.f},     // r1 = bias[col]
-      {VDSL_MAP_ADD, 0, 0, 1, 0, {0, 0, 0}, 0.f},      // r0 = r0 + r1
-  };
-};
-
 // The kernels built into the library: thin wrappers around the shared bodies.
 template <class P, int VEC, int R, class IDX>
 __global__ __launch_bounds__(256) void map_chain_kernel(MapProg rt, MapIn in, float* __restrict__ out, IDX rows, IDX cols) {
@@ -60,34 +38,6 @@ template <class P, int R, class IDX>
 __global__ __launch_bounds__(256) void map_chain_v_kernel(MapProg rt, MapVIn in, MapVOut vo, float* __restrict__ out,
                                                           IDX rows, IDX cols) {
   map_chain_v_body<P, R, IDX>(rt, in, vo, out, rows, cols);
-}
-
-template <class P>
-bool matches(const MapProg& rt, const MapIn& in) {
-  if (rt.n != P::n || in.n != P::n_inputs || rt.out_reg != P::out_reg) return false;
-  for (int k = 0; k < P::n_inputs; ++k)
-    if (in.bcast[k] != P::bcast_of(k)) return false;
-  for (int pc = 0; pc < P::n; ++pc) {
-    const vdsl_map_instr& a = rt.code[pc];
-    const vdsl_map_instr& b = P::code[pc];
-    if (a.op != b.op || a.dst != b.dst) return false;
-    // Compare only the operand fields the opcode reads.
-    switch (a.op) {
-      case VDSL_MAP_CONST: break;
-      case VDSL_MAP_LOAD:
-      case VDSL_MAP_MOV: case VDSL_MAP_NEG: case VDSL_MAP_ABS: case VDSL_MAP_SQUARE: case VDSL_MAP_EXP:
-      case VDSL_MAP_LOG: case VDSL_MAP_TANH: case VDSL_MAP_SIGMOID: case VDSL_MAP_RELU: case VDSL_MAP_SQRT:
-      case VDSL_MAP_RECIP: case VDSL_MAP_MUL_IMM: case VDSL_MAP_ADD_IMM:
-        if (a.a != b.a) return false;
-        break;
-      case VDSL_MAP_FMA:
-        if (a.a != b.a || a.b != b.b || a.c != b.c) return false;
-        break;
-      default:
-        if (a.a != b.a || a.b != b.b) return false;
-    }
-  }
-  return true;
 }
 
 // Launch geometry: VEC columns per lane, 256 lanes per block, R rows per step, at most 65535
@@ -161,9 +111,10 @@ JitCounters g_jit;
 std::atomic<int64_t> g_jit_launches{0};
 
 // The fixed-program table of a chain, as C++ source; it names the kernel completely (with the entry
-// points), so it is also the cache key.
+// points), so it is also the cache key.  vec: columns per lane of a scalar chain (4, or 1 when the
+// column count is not a multiple of 4).
 std::string program_source(const MapProg& rt, int n_inputs, const int32_t* bcast, const int32_t* widths,
-                           const int32_t* out_regs, int out_width, bool vector) {
+                           const int32_t* out_regs, int out_width, bool vector, int vec) {
   std::string s = "#include \"mapchain_kern.h\"\nnamespace vdsl {\nstruct JitProg {\n";
   s += "  static constexpr int n = " + std::to_string(rt.n) + ";\n";
   s += "  static constexpr int n_inputs = " + std::to_string(n_inputs) + ";\n";
@@ -187,12 +138,13 @@ std::string program_source(const MapProg& rt, int n_inputs, const int32_t* bcast
   }
   s += "  };\n};\n}  // namespace vdsl\n";
   if (!vector) {
+    const std::string V = std::to_string(vec);
     s += "extern \"C\" __global__ __launch_bounds__(256) void vdsl_map_jit32(vdsl::MapProg rt, vdsl::MapIn in, "
          "float* __restrict__ out, int rows, int cols) {\n"
-         "  vdsl::map_chain_body<vdsl::JitProg, 4, 2, int>(rt, in, out, rows, cols);\n}\n";
+         "  vdsl::map_chain_body<vdsl::JitProg, " + V + ", 2, int>(rt, in, out, rows, cols);\n}\n";
     s += "extern \"C\" __global__ __launch_bounds__(256) void vdsl_map_jit64(vdsl::MapProg rt, vdsl::MapIn in, "
          "float* __restrict__ out, long long rows, long long cols) {\n"
-         "  vdsl::map_chain_body<vdsl::JitProg, 4, 2, long long>(rt, in, out, rows, cols);\n}\n";
+         "  vdsl::map_chain_body<vdsl::JitProg, " + V + ", 2, long long>(rt, in, out, rows, cols);\n}\n";
   } else {
     const std::string R = std::to_string(kRowsV);
     s += "extern \"C\" __global__ __launch_bounds__(256) void vdsl_map_jit32(vdsl::MapProg rt, vdsl::MapVIn in, "
@@ -205,26 +157,28 @@ std::string program_source(const MapProg& rt, int n_inputs, const int32_t* bcast
   return s;
 }
 
-// Whether a launch of `elements` should use (and, if needed, compile) the chain's own kernel.
-bool want_compiled(vdsl_queue q, int64_t elements) {
+// Whether a launch of `elements` runs the chain's own (compiled) kernel.
+bool want_compiled(int64_t elements) {
   const int m = map_mode();
   if (m == kModeInterpret) return false;
-  if (q->capturing) return true;  // only a chain compiled earlier (checked by the caller)
   return m == kModeCompile || elements >= kCompileMinElements;
 }
 
-// Runs a chain in its compiled form.  VDSL_OK: launched.  VDSL_ERR_UNSUPPORTED with nothing
-// enqueued: not available (not compiled yet while recording a graph, or compilation failed) - the
-// caller runs the interpreter instead.
-int launch_compiled(vdsl_queue q, const std::string& src, bool vector, int comps, void* prog_arg, void* in_arg, void* vo_arg,
-                    float* out, int64_t rows, int64_t cols) {
-  // Entries with 32- and 64-bit indices.  While recording, only a chain compiled earlier runs.
+// Runs a chain in its compiled form, compiling it first if needed (never while recording: a chain
+// first met during a recording fails with VDSL_ERR_CAPTURE).  Compilation errors are returned.
+int launch_compiled(vdsl_queue q, const std::string& src, bool vector, int vec, int comps, void* prog_arg, void* in_arg,
+                    void* vo_arg, float* out, int64_t rows, int64_t cols) {
+  // Entries with 32- and 64-bit indices.
   const char* const entries[] = {"vdsl_map_jit32", "vdsl_map_jit64"};
   const JitKernels* c = nullptr;
-  if (jit_kernels(q->dev->ordinal, src, entries, 2, q->capturing, g_jit, "map chain", &c) != VDSL_OK)
-    return VDSL_ERR_UNSUPPORTED;
+  const int st = jit_kernels(q->dev->ordinal, src, entries, 2, q->capturing, g_jit, "map chain", &c);
+  if (st == VDSL_ERR_UNSUPPORTED && q->capturing && !c)
+    return fail(VDSL_ERR_CAPTURE,
+                "map chain: a chain of this size is compiled at run time and was first met while the queue records a "
+                "graph (nothing is compiled during recording); run it once before recording");
+  if (st != VDSL_OK) return st;
   Geometry g;
-  VDSL_TRY(geometry(vector ? 1 : 4, vector ? kRowsV : 2, comps, rows, cols, g));
+  VDSL_TRY(geometry(vec, vector ? kRowsV : 2, comps, rows, cols, g));
   int32_t r32 = static_cast<int32_t>(rows), c32 = static_cast<int32_t>(cols);
   int64_t r64 = rows, c64 = cols;
   void* a32v[] = {prog_arg, in_arg, vo_arg, &out, &r32, &c32};
@@ -310,14 +264,10 @@ extern "C" int vdsl_op_map_chain(vdsl_queue q, int64_t rows, int64_t cols, const
   float* o = static_cast<float*>(out->ptr);
   // 16-byte vectors need cols % 4 == 0 and 16-byte aligned bases (hipMalloc gives 256).
   const bool vec4 = (cols % 4) == 0;
-  const int mode = map_mode();
-  if (vec4 && mode == kModeAuto && matches<ProgTanhExpBias>(rt, in))
-    return launch<ProgTanhExpBias, 4, 2>(rt, in, o, rows, cols, q->stream);
-  if (vec4 && want_compiled(q, n)) {
+  if (want_compiled(n)) {
     const int32_t regs[4] = {out_reg, 0, 0, 0};
-    const std::string src = program_source(rt, n_inputs, in.bcast, ones, regs, 1, false);
-    const int st = launch_compiled(q, src, false, 1, &rt, &in, nullptr, o, rows, cols);
-    if (st != VDSL_ERR_UNSUPPORTED) return st;
+    const std::string src = program_source(rt, n_inputs, in.bcast, ones, regs, 1, false, vec4 ? 4 : 1);
+    return launch_compiled(q, src, false, vec4 ? 4 : 1, 1, &rt, &in, nullptr, o, rows, cols);
   }
   if (vec4) return launch<GenericProgram, 4, 1>(rt, in, o, rows, cols, q->stream);
   return launch<GenericProgram, 1, 1>(rt, in, o, rows, cols, q->stream);
@@ -389,10 +339,9 @@ extern "C" int vdsl_op_map_chain_v(vdsl_queue q, int64_t rows, int64_t cols, con
   VDSL_TRY(load_program(code, n_instr, n_inputs, widths, dims, rt));
   if (rows == 0 || cols == 0) return VDSL_OK;
   float* o = static_cast<float*>(out->ptr);
-  if (want_compiled(q, rows * cols)) {
-    const std::string src = program_source(rt, n_inputs, in.bcast, widths, vo.regs, out_width, true);
-    const int st = launch_compiled(q, src, true, comps, &rt, &in, &vo, o, rows, cols);
-    if (st != VDSL_ERR_UNSUPPORTED) return st;
+  if (want_compiled(rows * cols)) {
+    const std::string src = program_source(rt, n_inputs, in.bcast, widths, vo.regs, out_width, true, 1);
+    return launch_compiled(q, src, true, 1, comps, &rt, &in, &vo, o, rows, cols);
   }
   return launch_v(rt, in, vo, o, rows, cols, comps, q->stream);
 }
