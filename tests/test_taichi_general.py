@@ -451,3 +451,27 @@ def test_gather_clamps_and_int_store_truncates():
     got = oracle.pixel_program(prog, 1, 9, [x])
     assert got.dtype == np.int32
     assert got.tolist() == [[2, -2, 0, 0, 0, 2147483647, -2147483648, 2147483520, -2147483648]]
+
+
+def test_integer_index_arithmetic_within_2_24_is_exact():
+    """(i * j) % 7, (i * 3 - j) // 5 and -(i + j) % 4 on a 1021 x 1023 grid: every intermediate stays
+    below 2^24 in magnitude, so the f32 program gives Taichi's int32 values exactly (numpy int64)."""
+    body = "        f[i, j] = (i * j) % 7 + ((i * 3 - j) // 5) * 10.0 + (-(i + j) % 4) * 1000.0"
+    low = tc.lower_source_kernel(body_kernel(body, shape=(1021, 1023)), "k", {})
+    got = oracle.pixel_program(low.program, 1021, 1023)
+    i = np.arange(1021, dtype=np.int64)[:, None]
+    j = np.arange(1023, dtype=np.int64)[None, :]
+    ref = ((i * j) % 7 + ((i * 3 - j) // 5) * 10 + (-(i + j) % 4) * 1000).astype(np.float32)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("body", ["        f[i, j] = (i * j) % 7",
+                                  "        f[i, j] = (i * j * 3) // 11 + 0.5",
+                                  "        k = i * j\n        f[i, j] = k * 2.0"])
+def test_integer_index_arithmetic_beyond_2_24_is_refused(body):
+    """On an 8192 x 8192 grid i * j reaches 67,092,481 > 2^24: f32 registers cannot hold it exactly
+    while Taichi computes it in int32, so lowering refuses instead of giving other values.  The
+    check is on every integer intermediate, so it also refuses a product that is only used as a
+    float afterwards (k * 2.0, where the two would round alike)."""
+    with pytest.raises(tc.TaichiLoweringError, match="2\\^24"):
+        tc.lower_source_kernel(body_kernel(body, shape=(8192, 8192)), "k", {})

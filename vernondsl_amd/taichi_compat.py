@@ -739,6 +739,11 @@ class _PixInterp:
         self.shape = fld.shape if isinstance(fld, Field) else None  # the struct-for's index space
         self.inputs = []  # Fields read at [i, j], in LOAD order
         self.bools = set()  # ids of Nodes known to hold 1.0 / 0.0 (comparisons and their logic)
+        # ids of Nodes known to hold integers (the indices and +, -, *, %, // of them and of integer
+        # constants) -> a bound on their magnitude.  The program computes in f32 registers, where
+        # integers are exact up to 2^24: an integer expression that may go beyond is refused, since
+        # Taichi evaluates it in int32 and the results would differ.
+        self.ibound = {}
         self.in_loop = False
 
     # -- values
@@ -749,7 +754,31 @@ class _PixInterp:
             return self.b.const(_f32(v))
         raise TaichiLoweringError(f"{v!r} is not a per-pixel scalar")
 
+    _INT_EXACT = 1 << 24
+
+    def _ib(self, v):
+        """Magnitude bound of an integer value (a Python int or a tracked Node), else None."""
+        if isinstance(v, (int, np.integer)) and not isinstance(v, bool):
+            return abs(int(v))
+        return self.ibound.get(id(v)) if isinstance(v, self.pp.Node) else None
+
+    def _int_result(self, r, bound, what):
+        if bound is not None and isinstance(r, self.pp.Node):
+            if bound > self._INT_EXACT:
+                raise TaichiLoweringError(
+                    f"integer expression ({what}) may reach {bound}, beyond 2^24: per-pixel programs compute in f32, "
+                    "where integers are exact only up to 2^24, while Taichi computes it in int32")
+            self.ibound[id(r)] = bound
+        return r
+
     def arith(self, op, x, y):
+        r = self._arith(op, x, y)
+        bx, by = self._ib(x), self._ib(y)
+        if bx is not None and by is not None and op in ("add", "sub", "mul"):
+            return self._int_result(r, bx * by if op == "mul" else bx + by, op)
+        return r
+
+    def _arith(self, op, x, y):
         if isinstance(x, _PVec) or isinstance(y, _PVec):
             xs = x.comps if isinstance(x, _PVec) else None
             ys = y.comps if isinstance(y, _PVec) else None
@@ -780,7 +809,9 @@ class _PixInterp:
             with np.errstate(all="ignore"):
                 return {"neg": -v, "abs": np.abs(v), "sqrt": np.sqrt(v), "exp": np.exp(v), "log": np.log(v), "sin": np.sin(v),
                         "cos": np.cos(v), "tanh": np.tanh(v), "floor": np.floor(v)}[fn]
-        return self.b.op(fn, x)
+        r = self.b.op(fn, x)
+        bx = self._ib(x)
+        return self._int_result(r, bx, fn) if fn in ("neg", "abs", "floor") and bx is not None else r
 
     def dot(self, a, c):
         if not (isinstance(a, _PVec) and isinstance(c, _PVec) and len(a.comps) == len(c.comps)):
@@ -1106,6 +1137,16 @@ class _PixInterp:
             if y == 0:
                 raise TaichiLoweringError("integer division by zero")
             return x % y if mod else x // y
+        bx, by = self._ib(x), self._ib(y)
+        if bx is not None and by is not None:
+            # floor(x / y) of integers below 2^24 in magnitude is exact in f32 (the quotient cannot
+            # round up to the next integer), and so is x - q * y; the results are integers again
+            self._int_result(x, bx, "the dividend of % or //") if isinstance(x, self.pp.Node) else None
+            q = self.b.op("floor", self.node(self._arith("div", x, y)))
+            self.ibound[id(q)] = bx
+            if not mod:
+                return q
+            return self._int_result(self._arith("sub", x, self._arith("mul", q, y)), max(by - 1, 0), "%")
         q = self.unary("floor", self.arith("div", x, y))
         return self.arith("sub", x, self.arith("mul", q, y)) if mod else q
 
@@ -1323,6 +1364,9 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
             raise TaichiLoweringError("the struct-for must iterate a 2-D ti.field or ti.ndrange(W, H)")
         ip = _PixInterp(env, funcs, b, fld, iname, jname)
     local = {iname: b.index(0), jname: b.index(1)}
+    shape = ip.shape if ip.shape is not None else ip.fld.shape
+    for nm, ext in zip((iname, jname), shape):
+        ip.ibound[id(local[nm])] = max(int(ext) - 1, 0)
     stmts = [s for s in loop.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant)) and not isinstance(s, ast.Pass)]
     init, test, new_state, max_iter, has_loop = {}, None, {}, 0, False
     for st in stmts:
