@@ -418,3 +418,34 @@ def test_gather_and_int32_store_bit_exact(dev, q):
     fl = np.array(rng.choice([0.25, -0.75, 2.5, np.nan, 3e9, -3e9, 1e-3], size=(33, 65)), np.float32)
     got = run_prog(dev, q, prog, [ints, fl], 33, 65)
     assert got.dtype == np.int32 and np.array_equal(got, oracle.pixel_program(prog, 33, 65, [ints, fl]))
+
+
+def test_gathers_with_rows_that_vary_across_a_wave_bit_exact(dev, q):
+    """A wave of the row mapping covers 64 pixels of one row, and a gather whose row operand the
+    library finds wave-uniform (computed from i and constants only) forms its row offset once per
+    wave.  These gathers' rows are not wave-uniform, and each must keep its own row: the
+    transpose u[j, i], a row read from data u[v[i, j], j], a row from a fixed-trip loop's state
+    that starts at j, and a row that is uniform before the loop and mixed with j inside it."""
+    rng = np.random.default_rng(41)
+    n = 300
+    u = rng.standard_normal((n, n)).astype(np.float32)
+    v = rng.integers(-5, n + 5, (n, n)).astype(np.float32)
+    progs = []
+    b = pp.Builder()                                        # transpose: row = j
+    progs.append(pp.compile_program(b, out=b.load_at(0, b.index(1), b.index(0)), in_widths=[1, 1]))
+    b = pp.Builder()                                        # row from data
+    progs.append(pp.compile_program(b, out=b.op("add", b.load_at(0, b.load(1), b.index(1)), b.load_at(0, b.index(0), b.load(1))),
+                                    in_widths=[1, 1]))
+    b = pp.Builder()                                        # loop state from j used as a row
+    x = b.state("x")
+    progs.append(pp.compile_program(b, init={"x": b.op("add", b.index(1), 1.0)},
+                                    body={"x": b.op("add", b.op("mul", x, 0.5), b.index(0))},
+                                    max_iter=3, out=b.load_at(0, x, b.index(1)), loop=True, in_widths=[1, 1]))
+    b = pp.Builder()                                        # uniform at entry, mixed with j by the loop
+    y = b.state("y")
+    progs.append(pp.compile_program(b, init={"y": b.op("add", b.index(0), 2.0)},
+                                    body={"y": b.op("add", b.op("mul", y, 0.0), b.index(1))},
+                                    max_iter=2, out=b.op("add", b.load_at(0, y, b.index(0)), b.load_at(0, b.index(0), y)),
+                                    loop=True, in_widths=[1, 1]))
+    for prog in progs:
+        assert np.array_equal(run_prog(dev, q, prog, [u, v], n, n), oracle.pixel_program(prog, n, n, [u, v]))

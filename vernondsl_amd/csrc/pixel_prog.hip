@@ -7,7 +7,9 @@
 // here: the body is a register program (include/vdsl.h), compiled once per program and device into
 // straight-line code around the same check-then-update loop.
 
+#include <cstdlib>
 #include <string>
+#include <vector>
 
 #include "common.h"
 #include "jit.h"
@@ -68,13 +70,18 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
 }
 
 // Rows per block in the row mapping (each thread evaluates that many pixels of its column, then
-// stores them).  Measured on 8192^2 f32: y = 2x + 1 runs best with 4 (1, 2, 8, 16 rows: 61-96%
-// of its rate), a five-point stencil with 12 (its neighbours' rows are then shared within the
-// block; 8 rows: 98%, 16 rows: 97%, 4 rows: 91%), so programs with gathers take 12.
+// stores them).  Measured on 8192^2 f32 (graph replays, one box): y = 2x + 1 runs best with 4
+// (88.2 us; 2, 6, 8, 12, 16 rows: 87-97% of that rate), the clamped five-point stencil of
+// examples/heat.py with 8 (95.7 us; 6: 95.9, 10: 99.1, 12: 99.6-99.9, 4: 103.0, 16: 107.5).
+// VDSL_PIX_ROWS=r (1..16) overrides the choice, for tuning sweeps.
 int rows_per_block(const vdsl_pixel_program& p) {
+  if (const char* e = std::getenv("VDSL_PIX_ROWS")) {  // tuning sweeps: rows per block, 1..16
+    const int r = std::atoi(e);
+    if (r >= 1 && r <= 16) return r;
+  }
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   for (int pc = 0; pc < total; ++pc)
-    if (p.code[pc].op == VDSL_PIX_LOAD_AT) return 12;
+    if (p.code[pc].op == VDSL_PIX_LOAD_AT) return 8;
   return 4;
 }
 
@@ -86,9 +93,68 @@ int row_mapping(const vdsl_pixel_program& p, int ni) {
   return !(p.loop && p.test != VDSL_PIX_TEST_NONE) && (ni + rows - 1) / rows <= 65535 ? rows : 0;
 }
 
+// Registers an instruction reads (a, b, c as the opcode uses them).
+int reads(int op) {
+  switch (op) {
+    case VDSL_MAP_LOAD: case VDSL_MAP_CONST: case VDSL_PIX_INDEX: case VDSL_PIX_COUNT: return 0;
+    case VDSL_PIX_LOAD_AT: return 6;  // b, c
+    case VDSL_MAP_ADD: case VDSL_MAP_SUB: case VDSL_MAP_MUL: case VDSL_MAP_DIV: case VDSL_MAP_MAX: case VDSL_MAP_MIN:
+    case VDSL_PIX_LT: case VDSL_PIX_LE: case VDSL_PIX_EQ: case VDSL_PIX_NE: return 3;  // a, b
+    case VDSL_MAP_FMA: case VDSL_PIX_SELECT: return 7;  // a, b, c
+    default: return 1;  // a
+  }
+}
+
+// Gathers (LOAD_AT) whose row operand is the same on every lane of a wave in the row mapping, where
+// a wave covers 64 pixels of one row: registers computed only from the row index i (INDEX 0),
+// constants and immediates.  Their row offset is then formed once per wave on the scalar unit.
+// A forward pass over the sections (the loop's to a fixed point, joined with the state before it);
+// loads, the column index and the count make a register vary, conservatively.
+std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
+  const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
+  std::vector<char> flag(total, 0);
+  bool uni[VDSL_PIX_MAX_REGS];
+  for (bool& u : uni) u = true;  // registers start at 0
+  auto step = [&](int pc, bool* st) {
+    const vdsl_map_instr& s = p.code[pc];
+    const int rd = reads(s.op);
+    const bool in_uni = (!(rd & 1) || st[s.a]) && (!(rd & 2) || st[s.b]) && (!(rd & 4) || st[s.c]);
+    if (s.op == VDSL_PIX_LOAD_AT) flag[pc] = st[s.b] ? 1 : 0;
+    bool out;
+    if (s.op == VDSL_MAP_CONST) out = true;
+    else if (s.op == VDSL_PIX_INDEX) out = s.a == 0;
+    else if (s.op == VDSL_MAP_LOAD || s.op == VDSL_PIX_LOAD_AT || s.op == VDSL_PIX_COUNT) out = false;
+    else out = in_uni;
+    st[s.dst] = out;
+  };
+  for (int pc = 0; pc < p.n_pre; ++pc) step(pc, uni);
+  if (p.loop) {
+    bool head[VDSL_PIX_MAX_REGS];
+    for (int r = 0; r < VDSL_PIX_MAX_REGS; ++r) head[r] = uni[r];
+    for (int it = 0; it < 2 * VDSL_PIX_MAX_REGS + 2; ++it) {  // each pass can only clear flags
+      bool st[VDSL_PIX_MAX_REGS];
+      for (int r = 0; r < VDSL_PIX_MAX_REGS; ++r) st[r] = head[r];
+      for (int pc = p.n_pre; pc < p.n_pre + p.n_test + p.n_body; ++pc) step(pc, st);
+      bool changed = false;
+      for (int r = 0; r < VDSL_PIX_MAX_REGS; ++r)
+        if (head[r] && !st[r]) head[r] = false, changed = true;
+      if (!changed) break;
+    }
+    bool after_test[VDSL_PIX_MAX_REGS];
+    for (int r = 0; r < VDSL_PIX_MAX_REGS; ++r) after_test[r] = head[r];
+    for (int pc = p.n_pre; pc < p.n_pre + p.n_test; ++pc) step(pc, after_test);
+    bool st[VDSL_PIX_MAX_REGS];
+    for (int r = 0; r < VDSL_PIX_MAX_REGS; ++r) st[r] = head[r];
+    for (int pc = p.n_pre; pc < p.n_pre + p.n_test + p.n_body; ++pc) step(pc, st);  // the loop's flags, at the fixed point
+    for (int r = 0; r < VDSL_PIX_MAX_REGS; ++r) uni[r] = head[r] && after_test[r];  // the loop ends after a test, or at max_iter
+  }
+  for (int pc = p.n_pre + p.n_test + p.n_body; pc < total; ++pc) step(pc, uni);
+  return flag;
+}
+
 // The program's table as C++ source (opcodes and registers; immediates stay kernel arguments).
 // It names the kernel completely, so it is also the cache key.
-std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni) {
+std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni, int nj) {
   std::string s = "#include \"pixprog_kern.h\"\nnamespace vdsl {\nstruct PixJit {\n";
   auto c = [&](const char* name, int v) { s += std::string("  static constexpr int ") + name + " = " + std::to_string(v) + ";\n"; };
   c("n_pre", p.n_pre);
@@ -102,6 +168,10 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni) {
   c("out_kind", p.out_kind);
   c("out_width", p.out_width);
   c("rows", row_mapping(p, ni));
+  // 32-bit element offsets when every field's byte offsets stay below 2^32
+  int maxw = p.out_width;
+  for (int k = 0; k < n_inputs; ++k) maxw = p.in_widths[k] > maxw ? p.in_widths[k] : maxw;
+  c("idx32", static_cast<int64_t>(ni) * nj * maxw * 4 <= int64_t{0xffffffff} ? 1 : 0);
   // Entries past out_width / n_inputs are not used: written as 0 / 1, so they do not split the cache.
   auto list = [&](const char* name, const int32_t* v, int n, int fill) {
     s += std::string("  static constexpr int ") + name + "[4] = {";
@@ -110,12 +180,14 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni) {
   list("out_regs", p.out_regs, p.out_width, 0);
   list("in_widths", p.in_widths, n_inputs, 1);
   list("in_dtypes", p.in_dtypes, n_inputs, VDSL_F32);
+  // ext[0] of a gather: 1 when its row operand is wave-uniform in the row mapping
+  const std::vector<char> ru = row_uniform_gathers(p);
   s += "  static constexpr vdsl_map_instr code[VDSL_PIX_MAX_INSTR] = {\n";
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   for (int pc = 0; pc < total; ++pc) {
     const vdsl_map_instr& k = p.code[pc];
     s += "    {" + std::to_string(k.op) + ", " + std::to_string(k.dst) + ", " + std::to_string(k.a) + ", " + std::to_string(k.b) +
-         ", " + std::to_string(k.c) + ", {0, 0, 0}, 0.f},\n";
+         ", " + std::to_string(k.c) + ", {" + std::to_string(ru[pc]) + ", 0, 0}, 0.f},\n";
   }
   s += "  };\n};\n}  // namespace vdsl\n";
   s += "extern \"C\" __global__ __launch_bounds__(256) void vdsl_pix_jit(vdsl::PixRt rt, vdsl::PixIn in, void* out, int ni, "
@@ -150,7 +222,7 @@ extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   for (int pc = 0; pc < total; ++pc) rt.imm[pc] = p.code[pc].imm;
   rt.max_iter = p.max_iter;
-  const std::string src = program_source(p, n_inputs, ni);
+  const std::string src = program_source(p, n_inputs, ni, nj);
   const char* const entries[] = {"vdsl_pix_jit"};
   const JitKernels* k = nullptr;
   const int st = jit_kernels(q->dev->ordinal, src, entries, 1, q->capturing, g_pix_jit, "pixel program", &k);

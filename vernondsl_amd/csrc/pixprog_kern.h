@@ -34,20 +34,44 @@ struct PixIn {
   const float* p[VDSL_PIX_MAX_INPUTS];
 };
 
+// Element offsets into the fields: 32-bit when every byte offset of the launch's fields is below
+// 2^32 (the host sets P::idx32), so a load is a scalar base plus a 32-bit vector offset and needs
+// no 64-bit address arithmetic; 64-bit otherwise.
+template <bool B>
+struct PixOffT {
+  using type = unsigned long long;
+};
+template <>
+struct PixOffT<true> {
+  using type = unsigned;
+};
+template <class P>
+using PixOff = typename PixOffT<P::idx32 != 0>::type;
+
 // One instruction at program counter PC of the table P.
 // Element e, component c of input a (an int32 input is read as float(v)).
 template <class P, int A>
-__device__ __forceinline__ float pix_load(const PixIn& in, unsigned long long e, int c) {
-  if constexpr (P::in_dtypes[A] == VDSL_I32) return static_cast<float>(reinterpret_cast<const int*>(in.p[A])[e]);
-  else return in.p[A][e * P::in_widths[A] + c];
+__device__ __forceinline__ float pix_load(const PixIn& in, PixOff<P> e, int c) {
+  if constexpr (P::idx32) {
+    // the byte offset formed in 32 bits (the host checked it fits), so the load takes the field's
+    // base in scalar registers and a 32-bit offset
+    const char* base = reinterpret_cast<const char*>(in.p[A]);
+    if constexpr (P::in_dtypes[A] == VDSL_I32) return static_cast<float>(*reinterpret_cast<const int*>(base + e * 4u));
+    else return *reinterpret_cast<const float*>(base + (e * P::in_widths[A] + static_cast<unsigned>(c)) * 4u);
+  } else {
+    if constexpr (P::in_dtypes[A] == VDSL_I32) return static_cast<float>(reinterpret_cast<const int*>(in.p[A])[e]);
+    else return in.p[A][e * P::in_widths[A] + c];
+  }
 }
 
 // A field index from a register: 0 if !(x >= 0) (NaN included), else min((int)min(x, 2^30), n-1).
+// fmaxf(x, 0) is 0 for a NaN or negative x (and either zero for -0), so the conversion is always
+// of a value in [0, 2^30].
 __device__ __forceinline__ unsigned pix_index(float x, int n) {
-  if (!(x >= 0.0f)) return 0u;
-  const int v = static_cast<int>(fminf(x, 1073741824.0f));
+  const int v = static_cast<int>(fminf(fmaxf(x, 0.0f), 1073741824.0f));
   return static_cast<unsigned>(v < n - 1 ? v : n - 1);
 }
+
 
 // A register stored to an int32 field: truncation toward zero, NaN -> 0, saturating.
 __device__ __forceinline__ int pix_to_i32(float x) {
@@ -58,14 +82,17 @@ __device__ __forceinline__ int pix_to_i32(float x) {
 }
 
 template <class P, int PC>
-__device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], unsigned long long o,
+__device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
                                          float fi, float fj, float fcount, int ni, int nj) {
   constexpr vdsl_map_instr s = P::code[PC];
   if constexpr (s.op == VDSL_MAP_LOAD) {
     r[s.dst] = pix_load<P, s.a>(in, o, s.c);
   } else if constexpr (s.op == VDSL_PIX_LOAD_AT) {
-    const unsigned long long e = static_cast<unsigned long long>(pix_index(r[s.b], ni)) * static_cast<unsigned>(nj) +
-                                 pix_index(r[s.c], nj);
+    unsigned ri = pix_index(r[s.b], ni);
+    // a row operand the host found wave-uniform (ext[0]; the row mapping puts one row in each
+    // wave): its offset is formed once per wave on the scalar unit
+    if constexpr (P::rows > 0 && s.ext[0] != 0) ri = __builtin_amdgcn_readfirstlane(ri);
+    const PixOff<P> e = static_cast<PixOff<P>>(ri) * static_cast<unsigned>(nj) + pix_index(r[s.c], nj);
     r[s.dst] = pix_load<P, s.a>(in, e, static_cast<int>(rt.imm[PC]));
   } else if constexpr (s.op == VDSL_PIX_INDEX) {
     r[s.dst] = s.a == 0 ? fi : fj;
@@ -93,7 +120,7 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
 }
 
 template <class P, int BASE, int... K>
-__device__ __forceinline__ void pix_section(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], unsigned long long o,
+__device__ __forceinline__ void pix_section(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
                                             float fi, float fj, float fcount, int ni, int nj, Seq<K...>) {
   (pix_step<P, BASE + K>(rt, in, r, o, fi, fj, fcount, ni, nj), ...);
 }
@@ -156,7 +183,7 @@ struct PixSets {
 };
 
 template <class P, int BASE, int N>
-__device__ __forceinline__ void pix_run(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], unsigned long long o,
+__device__ __forceinline__ void pix_run(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
                                         float fi, float fj, float fcount, int ni, int nj) {
   pix_section<P, BASE>(rt, in, r, o, fi, fj, fcount, ni, nj, typename MakeSeq<N>::type{});
 }
@@ -173,7 +200,7 @@ __device__ __forceinline__ void pix_keep(float (&r)[VDSL_PIX_MAX_REGS], const fl
 // One trip: the test section, the lane's test into the sticky mask `lk`, the body.  Registers in
 // the keep sets hold their values on lanes that are not live.
 template <class P>
-__device__ __forceinline__ void pix_trip(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], unsigned long long o,
+__device__ __forceinline__ void pix_trip(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
                                          float fi, float fj, int ni, int nj, uint64_t& lk) {
   using S = PixSets<P>;
   float old[VDSL_PIX_MAX_REGS];
@@ -202,7 +229,7 @@ __device__ __forceinline__ void pixel_eval(const PixRt& rt, const PixIn& in, int
   using S = PixSets<P>;
   const bool inside = i < ni && j < nj;
   // Lanes past the grid run the program on pixel (0, 0), are never live, and store nothing.
-  const unsigned long long o = inside ? static_cast<unsigned long long>(i) * static_cast<unsigned>(nj) + j : 0ull;
+  const PixOff<P> o = inside ? static_cast<PixOff<P>>(i) * static_cast<unsigned>(nj) + static_cast<unsigned>(j) : PixOff<P>(0);
   const float fi = static_cast<float>(i), fj = static_cast<float>(j);
   float r[VDSL_PIX_MAX_REGS];
 #pragma unroll
@@ -273,14 +300,16 @@ template <class P>
 __device__ __forceinline__ void pixel_store(void* __restrict__ out, int ni, int nj, int i, int j, const float (&res)[4],
                                             int count) {
   if (i >= ni || j >= nj) return;
-  const unsigned long long o = static_cast<unsigned long long>(i) * static_cast<unsigned>(nj) + j;
+  const PixOff<P> o = static_cast<PixOff<P>>(i) * static_cast<unsigned>(nj) + static_cast<unsigned>(j);
+  char* base = static_cast<char*>(out);
   if constexpr (P::out_kind == VDSL_PIX_OUT_COUNT) {
-    static_cast<int*>(out)[o] = count;
+    *reinterpret_cast<int*>(base + o * 4u) = count;
   } else if constexpr (P::out_kind == VDSL_PIX_OUT_I32) {
-    static_cast<int*>(out)[o] = pix_to_i32(res[0]);
+    *reinterpret_cast<int*>(base + o * 4u) = pix_to_i32(res[0]);
   } else {
 #pragma unroll
-    for (int k = 0; k < P::out_width; ++k) static_cast<float*>(out)[o * P::out_width + k] = res[k];
+    for (int k = 0; k < P::out_width; ++k)
+      *reinterpret_cast<float*>(base + (o * P::out_width + static_cast<PixOff<P>>(k)) * 4u) = res[k];
   }
 }
 
@@ -292,13 +321,26 @@ __device__ __forceinline__ void pixel_store(void* __restrict__ out, int ni, int 
 // stored, and a read of another pixel's element that the same launch writes has no defined
 // order in any mapping.  Otherwise 8x8 tiles per wave and a 16x16 patch per block (escape loops,
 // whose lanes leave at different trips).
+//
+// Row blocks are renumbered so that each XCD walks one contiguous band of whole rows: the hardware
+// sends block L (row-major over the grid) to XCD L % 8, so without this the 256-column blocks to
+// the left and right of a block run on other XCDs, and a gather's neighbour columns (j - 1 of the
+// first lane, j + 1 of the last) cost two more 128-byte lines per 1 KiB row in this XCD's L2:
+// +25% of the input fetched for a five-point stencil.  Any bijection is correct; this one keeps
+// neighbouring blocks in one L2.
+__device__ __forceinline__ unsigned xcd_band(unsigned L, unsigned G) {
+  const unsigned x = L % 8, k = L / 8, q = G / 8, r = G % 8;
+  return x * q + (x < r ? x : r) + k;  // XCD x takes logical blocks [x q + min(x, r), + q + (x < r))
+}
+
 template <class P>
 __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, void* __restrict__ out, int ni, int nj) {
   float res[P::rows > 0 ? P::rows : 1][4];
   int count[P::rows > 0 ? P::rows : 1];
   if constexpr (P::rows > 0) {
-    const int j = static_cast<int>(blockIdx.x * 256 + threadIdx.x);
-    const int i0 = static_cast<int>(blockIdx.y) * P::rows;
+    const unsigned T = xcd_band(blockIdx.y * gridDim.x + blockIdx.x, gridDim.x * gridDim.y);
+    const int j = static_cast<int>((T % gridDim.x) * 256 + threadIdx.x);
+    const int i0 = static_cast<int>(T / gridDim.x) * P::rows;
 #pragma unroll
     for (int t = 0; t < P::rows; ++t) pixel_eval<P>(rt, in, ni, nj, i0 + t, j, res[t], count[t]);
 #pragma unroll
