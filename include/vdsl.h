@@ -551,7 +551,7 @@ int vdsl_debug_fail_alloc_after(int64_t n);
 int vdsl_debug_gemm_config(int32_t config);
 /* Forces the launch plan of vdsl_op_gemm_w8a8_packed (and of its _noalloc form): cfg 0 =
  * 128 x 256 blocks, 1 = 64 x 256, 2 = 64 x 256 with loads 7 stages ahead, 3 = 128 x 128,
- * 4 = 64 x 128; K split
+ * 4 = 64 x 128, 5 = 32 x 64, 6 = 32 x 128; K split
  * `split` ways (1..255).  cfg < 0 restores the per-shape plan.  A plan whose stages do not split K
  * evenly (K % (128 * stages per loop trip * split) != 0) is ignored for that call.  Query the
  * workspace size after setting it.  No counterpart in the reference; callers are tuning sweeps and

@@ -147,7 +147,7 @@ def test_packed_shape_errors(dev, q):
 
 
 @pytest.mark.parametrize("cfg,split", [(0, 1), (0, 2), (1, 1), (1, 4), (2, 1), (2, 2), (3, 1), (3, 3), (3, 8), (4, 1),
-                                       (4, 4)])
+                                       (4, 4), (5, 1), (5, 3), (6, 1), (6, 2)])
 def test_every_forced_plan(dev, q, cfg, split):
     """Each tile configuration and K split, forced with vdsl_debug_w8a8_packed_plan on a shape
     ragged in M and N: bit-exact against the oracle (a split whose stages do not divide K is

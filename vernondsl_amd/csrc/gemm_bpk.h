@@ -72,11 +72,13 @@ template <int NM, int D, int V>
 __device__ __forceinline__ void bpk_sched_kstep() {
   __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
   if constexpr (D > 0) __builtin_amdgcn_sched_group_barrier(0x100, D, 0);
+  if constexpr (NM > 1) {
 #pragma unroll
-  for (int i = 0; i < NM - 1; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    for (int i = 0; i < NM - 1; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
 #pragma unroll
-    for (int v = i * V / (NM - 1); v < (i + 1) * V / (NM - 1); ++v) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      for (int v = i * V / (NM - 1); v < (i + 1) * V / (NM - 1); ++v) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
   }
   if constexpr (NM == 1 && V > 0) __builtin_amdgcn_sched_group_barrier(0x020, V, 0);
   __builtin_amdgcn_sched_barrier(0);

@@ -444,6 +444,10 @@ using P3 = BpkConfig<MfmaI8, 4, 1, 4, 3>;
 // 64 x 128 blocks, 4 waves of 64 x 32: a quarter of P0's outputs per block, for narrow outputs
 // split along K over every CU.
 using P4 = BpkConfig<MfmaI8, 2, 1, 4, 3>;
+// 32 x 64 blocks of 2 waves of 32 x 32 and 32 x 128 blocks of 4 waves: narrow outputs without a
+// K split (512 x 1024: 256 and 128 tiles), each block streaming its operands over the whole K.
+using P5 = BpkConfig<MfmaI8, 1, 1, 2, 3>;
+using P6 = BpkConfig<MfmaI8, 1, 1, 4, 3>;
 
 // Whole-tile bf16 epilogue through LDS: each wave writes its dequantised fragments as bf16 into a
 // [BM][EPI_ROW] staging tile (2-byte writes; the row stride 528 = 512 + 16 puts the rows r and
@@ -576,7 +580,7 @@ __global__ __launch_bounds__(256) void w8a8_bpk_reduce(const char* __restrict__ 
 // fewer than 256, into about 256 blocks; each split part is a whole number of loop trips (NR
 // stages of 128 bytes).
 struct BpkPlan {
-  int cfg, split;  // cfg: 0 = P0, 1 = P1, 2 = P2, 3 = P3, 4 = P4
+  int cfg, split;  // cfg: 0 = P0, 1 = P1, 2 = P2, 3 = P3, 4 = P4, 5 = P5, 6 = P6
   int64_t tiles;
 };
 std::atomic<int> g_bpk_plan{-1};  // debug override: cfg * 256 + split, or -1
@@ -592,12 +596,14 @@ BpkPlan bpk_plan(int64_t M, int64_t N, int64_t K) {
   if (o >= 0) {  // a forced plan, when its stages split evenly: K % (128 * NR * split) == 0
     const int cfg = o >> 8, split = o & 255;
     const int nr = cfg == 2 ? P2::NR : P0::NR;
-    if (cfg >= 0 && cfg <= 4 && split >= 1 && K % (static_cast<int64_t>(128) * nr * split) == 0) {
+    if (cfg >= 0 && cfg <= 6 && split >= 1 && K % (static_cast<int64_t>(128) * nr * split) == 0) {
       p.cfg = cfg;
       p.split = split;
       p.tiles = cfg == 0   ? bpk_tiles<P0>(M, N)
                 : cfg == 3 ? bpk_tiles<P3>(M, N)
                 : cfg == 4 ? bpk_tiles<P4>(M, N)
+                : cfg == 5 ? bpk_tiles<P5>(M, N)
+                : cfg == 6 ? bpk_tiles<P6>(M, N)
                            : bpk_tiles<P1>(M, N);
       return p;
     }
@@ -640,6 +646,8 @@ size_t bpk_workspace_bytes(const BpkPlan& p) {
   const size_t tile_bytes = p.cfg == 0   ? static_cast<size_t>(P0::BM) * P0::BN * 4
                             : p.cfg == 3 ? static_cast<size_t>(P3::BM) * P3::BN * 4
                             : p.cfg == 4 ? static_cast<size_t>(P4::BM) * P4::BN * 4
+                            : p.cfg == 5 ? static_cast<size_t>(P5::BM) * P5::BN * 4
+                            : p.cfg == 6 ? static_cast<size_t>(P6::BM) * P6::BN * 4
                                          : static_cast<size_t>(P1::BM) * P1::BN * 4;
   return static_cast<size_t>(p.tiles) * p.split * tile_bytes;
 }
@@ -813,6 +821,8 @@ static int packed_launch(vdsl_queue q, const BpkPlan& p, int64_t M, int64_t N, i
   if (p.cfg == 0) return launch_bpk<P0>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
   if (p.cfg == 3) return launch_bpk<P3>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
   if (p.cfg == 4) return launch_bpk<P4>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
+  if (p.cfg == 5) return launch_bpk<P5>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
+  if (p.cfg == 6) return launch_bpk<P6>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
   if (p.cfg == 2) return launch_bpk<P2>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
   return launch_bpk<P1>(p, a, b, xs, wsc, y->ptr, out_dtype, relu, ao, part, m, n, k, q->stream);
 }
@@ -822,7 +832,7 @@ extern "C" int vdsl_debug_w8a8_packed_plan(int32_t cfg, int32_t split) {
     g_bpk_plan.store(-1, std::memory_order_relaxed);
     return VDSL_OK;
   }
-  if (cfg > 4 || split < 1 || split > 255) return fail(VDSL_ERR_INVALID_ARG, "plan: cfg 0..4, split 1..255");
+  if (cfg > 6 || split < 1 || split > 255) return fail(VDSL_ERR_INVALID_ARG, "plan: cfg 0..6, split 1..255");
   g_bpk_plan.store(cfg * 256 + split, std::memory_order_relaxed);
   return VDSL_OK;
 }
