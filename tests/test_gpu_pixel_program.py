@@ -449,3 +449,27 @@ def test_gathers_with_rows_that_vary_across_a_wave_bit_exact(dev, q):
                                     loop=True, in_widths=[1, 1]))
     for prog in progs:
         assert np.array_equal(run_prog(dev, q, prog, [u, v], n, n), oracle.pixel_program(prog, n, n, [u, v]))
+
+
+def test_reaction_example_sequences_bit_exact(dev, q):
+    """A kernel of two struct-fors, each storing two fields (four programs per step, run in
+    order on one queue): two frames of eight steps equal the oracle run of the same programs and
+    numpy's Gray-Scott update, element for element."""
+    path = os.path.join(EX, "reaction.py")
+    res, img = run_program(path, 2)
+    assert res["frames"] == 2 and img.shape == (256, 256) and img.dtype == np.float32
+    text = open(path).read()
+    kern, funcs, env = tc._parse_source(text, "step", {"dt": 1.0})
+    step = tc.lower_kernel(kern, tc._FuncResolver(env, funcs), env)
+    names = {id(v): k for k, v in env.items() if isinstance(v, tc.Field)}
+    i, j = np.meshgrid(np.arange(256), np.arange(256), indexing="ij")
+    inside = (np.abs(i - 128) < 12) & (np.abs(j - 128) < 12)
+    f = {"u": np.where(inside, np.float32(0.5), np.float32(1.0)).astype(np.float32),
+         "v": np.where(inside, np.float32(0.25) + np.float32(0.01) * ((i * 7 + j * 3) % 5).astype(np.float32),
+                       np.float32(0)).astype(np.float32),
+         "nu": np.zeros((256, 256), np.float32), "nv": np.zeros((256, 256), np.float32)}
+    for _ in range(16):
+        for op in step.ops():
+            f[names[id(op.field)]] = oracle.pixel_program(op.program, 256, 256, [f[names[id(g)]] for g in op.inputs])
+    assert np.array_equal(img, f["v"])
+    assert float(img.max()) > 0.25 and (img > 0.01).sum() > 24 * 24  # the spot has reacted and spread

@@ -475,3 +475,97 @@ def test_integer_index_arithmetic_beyond_2_24_is_refused(body):
     float afterwards (k * 2.0, where the two would round alike)."""
     with pytest.raises(tc.TaichiLoweringError, match="2\\^24"):
         tc.lower_source_kernel(body_kernel(body, shape=(8192, 8192)), "k", {})
+
+
+def lower_named(text, kernel, args):
+    """(the lowered kernel, {id(field): its module-level name})."""
+    kern, funcs, env = tc._parse_source(text, kernel, args)
+    low = tc.lower_kernel(kern, tc._FuncResolver(env, funcs), env)
+    return low, {id(v): k for k, v in env.items() if isinstance(v, tc.Field)}
+
+
+def run_ops(low, names, arrays):
+    """Runs a lowered kernel's programs in order on the oracle over {field name: array}, as the
+    device runs them (each program reads the fields as the programs before it left them)."""
+    for op in low.ops():
+        ni, nj = op.field.shape
+        arrays[names[id(op.field)]] = oracle.pixel_program(op.program, ni, nj, [arrays[names[id(f)]] for f in op.inputs])
+    return arrays
+
+
+def two_fields(body, extra_fields=("c",)):
+    decl = "".join(f"{nm} = ti.field(dtype=float, shape=(24, 40))\n" for nm in ("a", "b") + tuple(extra_fields))
+    return "import taichi as ti\n" + decl + "@ti.kernel\ndef k():\n    for i, j in a:\n" + body + "\n"
+
+
+def test_two_stored_fields_and_reading_one_back_at_the_pixel():
+    low, names = lower_named(two_fields("        a[i, j] = i * 0.5 - j\n        b[i, j] = a[i, j] * a[i, j] + 1.0"), "k", {})
+    assert low.kind == "sequence" and [names[id(o.field)] for o in low.ops()] == ["a", "b"]
+    assert all(o.reads == [] for o in low.ops())  # b's part recomputes a's value, it does not load it
+    out = run_ops(low, names, {"a": None, "b": None})
+    i, j = grid(24, 40)
+    a = i * f32(0.5) - j
+    assert np.array_equal(out["a"], a) and np.array_equal(out["b"], a * a + f32(1.0))
+
+
+def test_a_field_loaded_before_its_store_is_read_by_the_other_part_first():
+    """b reads a's value from before the loop, so b's program must run before a's; c is only read."""
+    body = ("        b[i, j] = a[i, j] * 2.0 + c[(i + 1) % 24, j]\n"
+            "        a[i, j] = a[i, j] + 1.0")
+    low, names = lower_named(two_fields(body), "k", {})
+    assert [names[id(o.field)] for o in low.ops()] == ["b", "a"]
+    rng = np.random.default_rng(12)
+    a0, c = (rng.standard_normal((24, 40)).astype(np.float32) for _ in range(2))
+    out = run_ops(low, names, {"a": a0.copy(), "b": np.zeros((24, 40), np.float32), "c": c})
+    assert np.array_equal(out["b"], a0 * f32(2.0) + np.roll(c, -1, 0))
+    assert np.array_equal(out["a"], a0 + f32(1.0))
+
+
+def test_in_place_updates_of_two_fields_need_no_order():
+    """Each part evaluates the whole body; a load only dead code reads is no dependency."""
+    body = ("        p = a[i, j]\n        q = b[i, j]\n"
+            "        a[i, j] = p * 2.0\n        b[i, j] = q * 3.0 + p")
+    low, names = lower_named(two_fields(body, ()), "k", {})
+    assert [names[id(o.field)] for o in low.ops()] == ["b", "a"]  # b reads a: b first
+    assert [[names[id(f)] for f in o.reads] for o in low.ops()] == [["a", "b"], ["a"]]
+    rng = np.random.default_rng(13)
+    a0, b0 = (rng.standard_normal((24, 40)).astype(np.float32) for _ in range(2))
+    out = run_ops(low, names, {"a": a0.copy(), "b": b0.copy()})
+    assert np.array_equal(out["a"], a0 * f32(2.0)) and np.array_equal(out["b"], b0 * f32(3.0) + a0)
+
+
+def test_fields_that_read_each_other_before_their_stores_are_refused():
+    body = "        t = a[i, j]\n        a[i, j] = b[i, j]\n        b[i, j] = t"
+    with pytest.raises(tc.TaichiLoweringError, match="both ways"):
+        lower_named(two_fields(body, ()), "k", {})
+
+
+def gray_scott_numpy(u, v, dt, Du=0.16, Dv=0.08, feed=0.035, kill=0.065):
+    """examples/reaction.py's step(dt) restated in numpy f32, operations in the program's order."""
+    def lap(x):
+        return (((np.roll(x, -1, 0) + np.roll(x, 1, 0)) + np.roll(x, -1, 1)) + np.roll(x, 1, 1)) - f32(4.0) * x
+    r = (u * v) * v
+    nu = u + f32(dt) * ((f32(Du) * lap(u) - r) + f32(feed) * (f32(1.0) - u))
+    nv = v + f32(dt) * ((f32(Dv) * lap(v) + r) - (f32(feed) + f32(kill)) * v)
+    return nu, nv
+
+
+def test_reaction_example_two_struct_fors_and_two_stores_per_loop():
+    text = ex("reaction.py")
+    seed, names = lower_named(text, "seed", {})
+    assert seed.kind == "sequence" and len(seed.ops()) == 2
+    f = run_ops(seed, names, {})
+    i, j = np.meshgrid(np.arange(256), np.arange(256), indexing="ij")
+    inside = (np.abs(i - 128) < 12) & (np.abs(j - 128) < 12)
+    assert np.array_equal(f["u"], np.where(inside, f32(0.5), f32(1.0)))
+    assert np.array_equal(f["v"], np.where(inside, f32(0.25) + f32(0.01) * ((i * 7 + j * 3) % 5).astype(np.float32), f32(0)))
+    step, names = lower_named(text, "step", {"dt": 1.0})
+    assert [p.kind for p in step.parts] == ["sequence", "sequence"]
+    assert [names[id(o.field)] for o in step.ops()] == ["nu", "nv", "u", "v"]
+    f = {nm: f[nm] if nm in f else np.zeros((256, 256), np.float32) for nm in ("u", "v", "nu", "nv")}
+    u, v = f["u"], f["v"]
+    for _ in range(3):
+        f = run_ops(step, names, f)
+        u, v = gray_scott_numpy(u, v, 1.0)
+        assert np.array_equal(f["u"], u) and np.array_equal(f["v"], v)
+        assert np.array_equal(f["nu"], u) and np.array_equal(f["nv"], v)

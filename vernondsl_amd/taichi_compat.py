@@ -28,8 +28,12 @@ Bodies of any other shape are lowered by the general path to a per-pixel registe
 (vernondsl_amd.pixprog, run by vdsl_op_pixel_program, compiled at run time for the program): any
 expression of the pixel indices, scalar kernel arguments, other 2-D f32 fields read at [i, j]
 and constants, with at most one loop - a `while <test> and <counter> < MAX:` check-then-update
-loop whose body ends with `counter += 1`, or a `for _ in range(N):` loop - and one store
-`F[i, j] = <value>` (an i32 field stores the loop counter).  What neither path lowers raises
+loop whose body ends with `counter += 1`, or a `for _ in range(N):` loop - and stores
+`F[i, j] = <value>` (an i32 field stores the loop counter) into one or more fields of the loop's
+shape: a body storing several fields becomes one program per stored field, run in an order in
+which no program loads a field that an earlier one stored (a load at [i, j] after the body's own
+store reads the stored value, as in Taichi); a kernel of several top-level struct-fors runs their
+lowerings one after another.  What neither path lowers raises
 TaichiLoweringError naming what did not match; there is no CPU fallback.  Accepted complex squares are the ones equal bit for bit to (zr*zr - zi*zi, (zi*zr)*2):
 `z[0]**2 - z[1]**2`, `z[0]*z[0] - z[1]*z[1]`, and `z[1]*z[0]*2` / `z[0]*z[1]*2` / `2*(z[0]*z[1])` /
 `z[0]*z[1] + z[0]*z[1]` for the imaginary part (`(2*z[0])*z[1]` is refused: it rounds differently
@@ -207,10 +211,11 @@ class Kernel:
         low = self.lower(*args)
         from . import kernels
         _, q = _device()
-        if low.kind == "escape_time":
-            kernels.escape_time(q, kernels.escape_time_params(**low.params), low.field.tensor())
-        else:
-            kernels.pixel_program(q, low.program, [f.tensor() for f in low.inputs], low.field.tensor())
+        for op in low.ops():
+            if op.kind == "escape_time":
+                kernels.escape_time(q, kernels.escape_time_params(**op.params), op.field.tensor())
+            else:
+                kernels.pixel_program(q, op.program, [f.tensor() for f in op.inputs], op.field.tensor())
 
 
 def _annotation(node):
@@ -594,9 +599,7 @@ def lower_source_kernel(text: str, kernel_name: str, args: dict, general: bool =
     """As lower_source, by either path (escape-time op, else the general per-pixel program);
     general=True takes the general path even for bodies of the escape-time form."""
     kern, funcs, env = _parse_source(text, kernel_name, args)
-    if general:
-        return lower_pixel_program(kern, _FuncResolver(env, funcs), env)
-    return lower_kernel(kern, _FuncResolver(env, funcs), env)
+    return lower_kernel(kern, _FuncResolver(env, funcs), env, general=general)
 
 
 def _parse_source(text: str, kernel_name: str, args: dict):
@@ -693,16 +696,36 @@ def template():
 
 # ---- the general path: any struct-for body as a per-pixel register program ---------------------------
 class Lowered:
-    """A lowered kernel: kind "escape_time" (field, params for vdsl_op_escape_time) or
-    "pixel_program" (field, program for vdsl_op_pixel_program, input fields it reads)."""
+    """A lowered kernel: kind "escape_time" (field, params for vdsl_op_escape_time),
+    "pixel_program" (field, program for vdsl_op_pixel_program, input fields it reads), or
+    "sequence" (parts: Lowered ops run in order; a kernel of several struct-fors, or a struct-for
+    storing several fields)."""
 
-    def __init__(self, kind, field, params=None, program=None, inputs=()):
+    def __init__(self, kind, field, params=None, program=None, inputs=(), parts=()):
         self.kind, self.field, self.params, self.program, self.inputs = kind, field, params, program, list(inputs)
+        self.parts = list(parts)
+        self.reads = list(inputs)  # the input fields a pixel program loads
+
+    def ops(self):
+        """The escape-time and pixel-program ops this kernel runs, in order."""
+        return [o for p in self.parts for o in p.ops()] if self.kind == "sequence" else [self]
 
 
-def lower_kernel(fdef: ast.FunctionDef, funcs, env) -> Lowered:
-    """The escape-time op for bodies of that form (its hand-tuned kernel), else the general
-    per-pixel program; TaichiLoweringError when neither lowers the body."""
+def lower_kernel(fdef: ast.FunctionDef, funcs, env, general: bool = False) -> Lowered:
+    """Each top-level struct-for of the kernel, in order (a Taichi kernel runs them one after
+    another, each a parallel loop): the escape-time op for bodies of that form (its hand-tuned
+    kernel; not when general), else the general per-pixel program(s); TaichiLoweringError when
+    neither lowers one."""
+    body = [s for s in fdef.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant))]
+    if len(body) > 1 and all(isinstance(s, ast.For) for s in body):
+        parts = []
+        for loop in body:
+            sub = ast.FunctionDef(name=fdef.name, args=fdef.args, body=[loop], decorator_list=[], returns=None,
+                                  type_comment=None)
+            parts.append(lower_kernel(sub, funcs, env, general))
+        return Lowered("sequence", parts[0].field, parts=parts)
+    if general:
+        return lower_pixel_program(fdef, funcs, env)
     try:
         fld, params = lower_escape_time(fdef, funcs, env)
         return Lowered("escape_time", fld, params=params)
@@ -722,7 +745,14 @@ class _PVec:
 
 _UNARY_FUNCS = {"sqrt": "sqrt", "exp": "exp", "log": "log", "sin": "sin", "cos": "cos", "tanh": "tanh", "abs": "abs",
                 "floor": "floor"}
-_STORE = "__store__"  # the value the body stores to the iterated field at [i, j]
+def _skey(fld):
+    """The local-scope key of the value the body has stored to fld[i, j] (read back by a later read
+    of fld[i, j] in the same body)."""
+    return ("__store__", id(fld))
+
+
+def _is_skey(k):
+    return isinstance(k, tuple) and len(k) == 2 and k[0] == "__store__"
 _MATH_FUNCS = ("vec2", "vec3", "vec4", "clamp", "mix", "smoothstep", "length", "normalize", "dot", "cross", "fract",
                "step", "sign")
 
@@ -736,6 +766,8 @@ class _PixInterp:
         self.pp = pixprog
         self.env, self.funcs, self.b = env, funcs, b
         self.fld, self.iname, self.jname = fld, iname, jname
+        self.stored = []  # fields the body stores to at [i, j], in the order of their first store
+        self.fields = {}  # id -> Field, for the store keys
         self.shape = fld.shape if isinstance(fld, Field) else None  # the struct-for's index space
         self.inputs = []  # Fields read at [i, j], in LOAD order
         self.bools = set()  # ids of Nodes known to hold 1.0 / 0.0 (comparisons and their logic)
@@ -892,8 +924,8 @@ class _PixInterp:
         if not (isinstance(idx, ast.Tuple) and len(idx.elts) == 2):
             raise TaichiLoweringError("fields are 2-D: read them as field[i, j]")
         here = [getattr(e, "id", None) for e in idx.elts] == [self.iname, self.jname]
-        if here and fld is self.fld and _STORE in local:
-            return local[_STORE]  # the value this pixel stored earlier in the body
+        if here and _skey(fld) in local:
+            return local[_skey(fld)]  # the value this pixel stored earlier in the body
         if fld.shape != self.shape:
             raise TaichiLoweringError("a field read must be of a field of the struct-for's shape")
         if fld not in self.inputs:
@@ -1176,12 +1208,10 @@ class _PixInterp:
             if vt is vf:
                 local[nm] = vt
                 continue
-            if nm == _STORE:  # the field keeps its value where a branch does not store
-                keep = local.get(_STORE)
-                if self.fld is None:
-                    raise TaichiLoweringError("no output field")
+            if _is_skey(nm):  # the field keeps its value where a branch does not store
+                keep = local.get(nm)
                 if keep is None:
-                    keep = self.field_read(self.fld, ast.Tuple(elts=[ast.Name(id=self.iname), ast.Name(id=self.jname)]), {})
+                    keep = self.field_read(self.fields[nm[1]], ast.Tuple(elts=[ast.Name(id=self.iname), ast.Name(id=self.jname)]), {})
                 vt = keep if vt is _ONE_BRANCH else vt
                 vf = keep if vf is _ONE_BRANCH else vf
             elif vt is _ONE_BRANCH or vf is _ONE_BRANCH or vt is _UNREADABLE or vf is _UNREADABLE:
@@ -1268,10 +1298,8 @@ class _PixInterp:
         if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Subscript):
             tgt = st.targets[0]
             target = self.expr(tgt.value, local)
-            if self.fld is None and isinstance(target, Field) and target.shape == self.shape:
-                self.fld = target  # a loop over ti.ndrange stores to a field of its shape
-            if target is not self.fld:
-                raise TaichiLoweringError("the body may only store to the iterated field (one output field)")
+            if not (isinstance(target, Field) and target.shape == self.shape):
+                raise TaichiLoweringError("the body may only store to fields of the struct-for's shape")
             idx = tgt.slice
             if not (isinstance(idx, ast.Tuple) and [getattr(e, "id", None) for e in idx.elts] == [self.iname, self.jname]):
                 raise TaichiLoweringError("the store must write field[i, j]")
@@ -1280,14 +1308,17 @@ class _PixInterp:
             v = self.expr(st.value, local)
             if isinstance(v, list):
                 v = _PVec(v)
-            if self.fld.width == 1:
+            if target.width == 1:
                 if isinstance(v, _PVec):
                     raise TaichiLoweringError("a field of scalars stores a scalar")
             elif not isinstance(v, _PVec):
-                v = _PVec([v] * self.fld.width)  # a scalar fills every component
-            elif len(v.comps) != self.fld.width:
-                raise TaichiLoweringError(f"a field of {self.fld.width}-vectors stores {self.fld.width} components")
-            local[_STORE] = v
+                v = _PVec([v] * target.width)  # a scalar fills every component
+            elif len(v.comps) != target.width:
+                raise TaichiLoweringError(f"a field of {target.width}-vectors stores {target.width} components")
+            if target not in self.stored:
+                self.stored.append(target)
+                self.fields[id(target)] = target
+            local[_skey(target)] = v
             return True
         if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Name):
             local[st.targets[0].id] = self.expr(st.value, local)
@@ -1339,7 +1370,33 @@ def _assigned_names(stmts):
 
 
 def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
-    """Lowers one @ti.kernel struct-for body to a per-pixel program (vernondsl_amd.pixprog)."""
+    """Lowers one @ti.kernel struct-for body to per-pixel programs (vernondsl_amd.pixprog): one
+    program when the body stores one field; when it stores several, one program per stored field
+    (each evaluates the whole body and stores its field; the other stores stay local, so a later
+    read of such a field at [i, j] sees the stored value), as a "sequence" ordered so that no
+    program reads a field from memory after another program of the sequence has stored it (Taichi
+    reads the values from before the loop there).  A body whose programs need each other's inputs
+    both ways has no such order: TaichiLoweringError."""
+    low, stored = _lower_pixel_one(fdef, funcs, env, None)
+    if low is not None:
+        return low
+    parts = {id(f): _lower_pixel_one(fdef, funcs, env, f)[0] for f in stored}
+    # part T loads field F from memory -> T runs before the part that stores F
+    order, placed = [], set()
+    while len(order) < len(stored):
+        ready = [f for f in stored if id(f) not in placed and
+                 not any(id(g) not in placed and g is not f and f in parts[id(g)].reads for g in stored)]
+        if not ready:
+            raise TaichiLoweringError("the struct-for stores fields that it also reads before storing them, both ways "
+                                      "round: no order of one program per stored field gives Taichi's values")
+        order.append(ready[0])
+        placed.add(id(ready[0]))
+    return Lowered("sequence", stored[0], parts=[parts[id(f)] for f in order])
+
+
+def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target):
+    """(Lowered program storing `target`, the fields the body stores); target None: the only
+    field the body stores (Lowered None when it stores several)."""
     from . import pixprog as pp
     body = [s for s in fdef.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant))]
     if len(body) != 1 or not isinstance(body[0], ast.For):
@@ -1373,7 +1430,7 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
         if isinstance(st, (ast.While, ast.For)) and ip.static_values(st, local) is None:
             if has_loop:
                 raise TaichiLoweringError("at most one loop per struct-for body")
-            if _STORE in local:
+            if any(_is_skey(k) for k in local):
                 raise TaichiLoweringError("the store field[i, j] = ... must come after the loop")
             has_loop = True
             init, test, new_state, max_iter = _lower_loop(st, ip, local, b)
@@ -1381,10 +1438,14 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
         if ip.assign(st, local):
             continue
         raise TaichiLoweringError(f"statement at line {getattr(st, 'lineno', '?')} is not supported")
-    if _STORE not in local:
+    if not ip.stored:
         raise TaichiLoweringError("the struct-for body must store field[i, j] = ...")
-    fld = ip.fld
-    v = local[_STORE]
+    if target is None:
+        if len(ip.stored) > 1:
+            return None, ip.stored
+        target = ip.stored[0]
+    fld = target
+    v = local[_skey(target)]
     out_i32 = False
     if fld.dtype == i32:
         if isinstance(v, pp.Node) and v.kind == "count":
@@ -1401,7 +1462,20 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
                                   in_dtypes=[pp.I32 if f.dtype == i32 else pp.F32 for f in ip.inputs], out_i32=out_i32)
     except pp.ProgramError as e:
         raise TaichiLoweringError(str(e)) from None
-    return Lowered("pixel_program", fld, program=prog, inputs=ip.inputs)
+    # the fields this program loads (an input that only dead code reads is not one)
+    roots = list(init.values()) + list(new_state.values()) + (list(test[1:]) if test else [])
+    roots += out if isinstance(out, list) else [out]
+    todo, seen, live = [n for n in roots if isinstance(n, pp.Node)], set(), set()
+    while todo:
+        n = todo.pop()
+        if id(n) not in seen:
+            seen.add(id(n))
+            if n.kind in ("load", "load_at"):
+                live.add(n.val[0])
+            todo.extend(n.args)
+    low = Lowered("pixel_program", fld, program=prog, inputs=ip.inputs)
+    low.reads = [f for k, f in enumerate(ip.inputs) if k in live]
+    return low, ip.stored
 
 
 def _lower_loop(st, ip: _PixInterp, local: dict, b):
