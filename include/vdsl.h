@@ -449,6 +449,16 @@ int vdsl_op_gelu_fwd(vdsl_queue q, int64_t n, int32_t x_dtype, vdsl_buffer x, in
  * [cols][rows]) receives the transpose of da. */
 int vdsl_op_gelu_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer dh, vdsl_buffer pre,
                      vdsl_buffer da, vdsl_buffer da_t);
+/* ReLU backward, as vdsl_op_gelu_bwd: da = dh where pre > 0, else +0 (pre <= 0 or NaN; a select,
+ * so an infinite dh there gives 0), rounded to bf16; da_t optional. */
+int vdsl_op_relu_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer dh, vdsl_buffer pre,
+                     vdsl_buffer da, vdsl_buffer da_t);
+/* out = a + b elementwise over n elements: each operand F32 or BF16 (widened exactly), one f32
+ * addition, rounded once (RNE) to out's dtype (F32 or BF16).  out may be a or b when it has that
+ * operand's dtype.  The forward of a residual sum and the sum of the gradients of a value that
+ * several ops read. */
+int vdsl_op_add(vdsl_queue q, int64_t n, int32_t a_dtype, vdsl_buffer a, int32_t b_dtype, vdsl_buffer b,
+                int32_t out_dtype, vdsl_buffer out);
 /* The backward of y = GELU(pre) through the GEMM that forms dL/dy, fused: dh = A B^T (f32
  * accumulate, never written), da (bf16 [M][N]) = dh * GELU'(pre), da_t (optional, bf16 [N][M]) =
  * da^T.  A: bf16 [M][K]; B: bf16 [N][K] (the NT form); pre: f32 [M][N].  Bit-identical to

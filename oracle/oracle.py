@@ -76,6 +76,8 @@ _lib.orc_transpose.argtypes = [_i64, _i64, C.c_int, _vp, _vp]
 _lib.orc_cast.argtypes = [_i64, C.c_int, _vp, C.c_int, _vp]
 _lib.orc_gelu_fwd.argtypes = [_i64, C.c_int, _vp, C.c_int, _vp]
 _lib.orc_gelu_bwd.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp]
+_lib.orc_relu_bwd.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp]
+_lib.orc_add.argtypes = [_i64, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp]
 _lib.orc_gelu_grad.argtypes = [_i64, _vp, _vp]
 _lib.orc_pixel_program_rows.argtypes = [_vp, _i64, _i64, C.POINTER(_vp), _vp, _i64, _i64]
 _lib.orc_mse_fwd_bwd.argtypes = [_i64, _i64, _vp, _vp, _vp, _vp, _vp]
@@ -273,6 +275,26 @@ def gelu_bwd(dh: np.ndarray, pre: np.ndarray):
     return da, da_t
 
 
+def relu_bwd(dh: np.ndarray, pre: np.ndarray):
+    dh = np.ascontiguousarray(dh, np.float32)
+    pre = np.ascontiguousarray(pre, np.float32)
+    rows, cols = dh.shape
+    da = np.zeros((rows, cols), np.uint16)
+    da_t = np.zeros((cols, rows), np.uint16)
+    _lib.orc_relu_bwd(rows, cols, _p(dh), _p(pre), _p(da), _p(da_t))
+    return da, da_t
+
+
+def add(a: np.ndarray, b: np.ndarray, out_dtype: int = F32) -> np.ndarray:
+    """a + b elementwise; a, b f32 or uint16 holding bf16; returns f32 or uint16 bf16."""
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    if a.size != b.size:
+        raise ValueError("add: sizes differ")
+    out = np.zeros(a.shape, np.uint16 if out_dtype == BF16 else np.float32)
+    _lib.orc_add(a.size, _dt(a), _p(a), _dt(b), _p(b), out_dtype, _p(out))
+    return out
+
+
 def gelu_grad(x: np.ndarray) -> np.ndarray:
     """GELU'(x) elementwise, f32 in and out."""
     x = np.ascontiguousarray(x, np.float32)
@@ -353,3 +375,58 @@ def w8a8_forward(x, layers):
         xq, xs = quantize_rows_i8(h)
         h = gemm_w8a8(xq, xs, w, s, out_dtype=BF16, relu=li < len(layers) - 1)
     return h
+
+
+def graph_step(g, feeds: dict) -> dict:
+    """Runs an execution graph's prepare ops and step ops (vernondsl_amd.graph.Graph: ops with
+    .kind, .inputs, .outputs, .attrs; values with .name, .dtype) on the routines above, with the
+    roundings the device ops document, and returns {value name: array} (bf16 as uint16).  A
+    packed weight holds the weight itself here (packing only reorders bytes for the device).
+    feeds: the inputs and params by name."""
+    v = dict(feeds)
+    code = {"f32": F32, "bf16": BF16}
+    epi = {"none": 0, "gelu": GELU, "relu": 2}
+
+    def nt(a, b, dtype=F32, e=0, pre=False):
+        return gemm_bf16(v[a.name], v[b.name], False, True, c_dtype=dtype, epilogue=e, want_pre=pre)
+
+    for op in g.prepare_ops:
+        src = v[op.inputs[0].name]
+        v[op.outputs[0].name] = transpose(src) if op.kind == "transpose" else src
+    for op in g.ops:
+        ins, outs, k = op.inputs, op.outputs, op.kind
+        if k == "linear":
+            y, pre = nt(ins[0], ins[1], code[outs[0].dtype], epi[op.attrs["act"]], True)
+            v[outs[0].name] = y
+            if op.attrs.get("pre") is not None:
+                v[op.attrs["pre"].name] = pre
+            if op.attrs.get("dgelu") is not None:
+                v[op.attrs["dgelu"].name] = gelu_grad(pre)
+        elif k == "gemm":
+            v[outs[0].name] = gemm_bf16(v[ins[0].name], v[ins[1].name], op.attrs["trans_a"], op.attrs["trans_b"])
+        elif k in ("mse", "linear_mse"):
+            if k == "linear_mse":
+                v[outs[0].name] = nt(ins[0], ins[1])
+                y, t, outs = v[outs[0].name], v[ins[2].name], outs[1:]
+            else:
+                y, t = v[ins[0].name], v[ins[1].name]
+            loss, dy, dy_t = mse_fwd_bwd(y, t)
+            v[outs[0].name] = np.array([loss], np.float32)
+            if len(outs) > 1:
+                v[outs[1].name], v[outs[2].name] = dy, dy_t
+        elif k in ("gelu_bwd", "relu_bwd"):
+            v[outs[0].name], v[outs[1].name] = (gelu_bwd if k == "gelu_bwd" else relu_bwd)(v[ins[0].name], v[ins[1].name])
+        elif k == "gemm_gelu_bwd":
+            v[outs[0].name], v[outs[1].name] = gelu_bwd(nt(ins[0], ins[1]), v[ins[2].name])
+        elif k == "gemm_mul_bwd":  # dh * GELU'(pre), GELU'(pre) stored by the forward GEMM
+            da = cast((nt(ins[0], ins[1]) * v[ins[2].name]).astype(np.float32), BF16)
+            v[outs[0].name], v[outs[1].name] = da, transpose(da)
+        elif k == "cast":
+            v[outs[0].name] = cast(v[ins[0].name], code[outs[0].dtype])
+        elif k == "transpose":
+            v[outs[0].name] = transpose(v[ins[0].name])
+        elif k == "add":
+            v[outs[0].name] = add(v[ins[0].name], v[ins[1].name], code[outs[0].dtype])
+        else:
+            raise NotImplementedError(k)
+    return v

@@ -49,6 +49,9 @@
  *                        small integers), brute force in Python integers, and numpy f64.
  *   orc_gelu_fwd / orc_gelu_bwd / orc_gelu_grad / orc_mse_fwd_bwd
  *                        no reference code.  Pinned by central finite differences in f64.
+ *   orc_relu_bwd / orc_add
+ *                        no reference code.  Pinned by numpy's f32 select and f32 addition (an
+ *                        IEEE addition has one correct result), bf16 operands widened exactly.
  *   orc_quantize_rows_i8 / orc_gemm_w8a8 / orc_w8a8_dequant
  *                        no reference code.  Pinned by int64 numpy dot products (exact) and a
  *                        numpy restatement of the f32 dequant sequence (orc_w8a8_dequant is the
@@ -540,6 +543,24 @@ void orc_gelu_bwd(int64_t rows, int64_t cols, const float* dh, const float* pre,
       if (da) da[r * cols + c] = h;
       if (da_t) da_t[c * rows + r] = h;
     }
+}
+
+/* ReLU backward: da = dh where pre > 0, else +0 (NaN pre included), RNE to bf16. */
+void orc_relu_bwd(int64_t rows, int64_t cols, const float* dh, const float* pre, uint16_t* da, uint16_t* da_t) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < cols; ++c) {
+      const float p = pre[r * cols + c];
+      const uint16_t h = f32_to_bf16(p > 0.0f ? dh[r * cols + c] : 0.0f);
+      if (da) da[r * cols + c] = h;
+      if (da_t) da_t[c * rows + r] = h;
+    }
+}
+
+/* out = a + b: operands widened to f32, one f32 addition, rounded to out's dtype. */
+void orc_add(int64_t n, int a_dtype, const void* a, int b_dtype, const void* b, int out_dtype, void* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) store_out(out, out_dtype, i, load_elem(a, a_dtype, i) + load_elem(b, b_dtype, i));
 }
 
 /* loss = mean((y - t)^2) (f64 sum, rounded once); dy = (y - t) * (2 / n) in f32, RNE to bf16. */

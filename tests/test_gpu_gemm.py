@@ -179,6 +179,62 @@ def test_gelu_bwd(dev, q, rows, cols):
         t.free()
 
 
+@pytest.mark.parametrize("rows,cols", [(128, 192), (70, 33), (72, 100), (2048, 4096)])
+def test_relu_bwd_bit_exact(dev, q, rows, cols):
+    """A select and one RNE: bit for bit, including pre = +-0, NaN and denormal, infinite dh."""
+    dh = rng.normal(23, rows * cols).reshape(rows, cols)
+    pre = rng.normal(24, rows * cols).reshape(rows, cols)
+    pre[0, :4] = [0.0, -0.0, np.nan, 1e-45]
+    dh[1, :2] = [np.inf, -np.inf]
+    tdh, tpre = Tensor.from_numpy(dev, q, dh), Tensor.from_numpy(dev, q, pre)
+    tda, tdat = Tensor(dev, (rows, cols), "bf16"), Tensor(dev, (cols, rows), "bf16")
+    kernels.gelu_bwd(q, tdh, tpre, tda, tdat, act="relu")
+    rda, rdat = oracle.relu_bwd(dh, pre)
+    assert np.array_equal(tda.numpy(q), rda) and np.array_equal(tdat.numpy(q), rdat)
+    for t in (tdh, tpre, tda, tdat):
+        t.free()
+
+
+# n % 4 == 0 takes the four-element kernel, the others the element-wise one
+@pytest.mark.parametrize("n", [0, 1, 7, 4096, 100003, 2048 * 4096])
+@pytest.mark.parametrize("dts", [("f32", "f32", "f32"), ("bf16", "bf16", "bf16"), ("bf16", "f32", "f32"),
+                                 ("f32", "bf16", "bf16"), ("bf16", "bf16", "f32")])
+def test_add_bit_exact(dev, q, n, dts):
+    r = np.random.default_rng(n + 7)
+    host = []
+    for k, dt in enumerate(dts[:2]):
+        x = r.standard_normal(n).astype(np.float32) * np.float32(10.0 ** -k)
+        host.append(rng.f32_to_bf16(x) if dt == "bf16" else x)
+    ta, tb = (Tensor.from_numpy(dev, q, h, dt) for h, dt in zip(host, dts[:2]))
+    out = Tensor(dev, (n,), dts[2])
+    if out.buffer.nbytes >= 4:  # NaN poison over whole words: every element must be written
+        out.buffer.fill_u32(q, 0x7FC07FC0, 0, out.buffer.nbytes // 4 * 4)
+    kernels.add(q, ta, tb, out)
+    ref = oracle.add(host[0], host[1], oracle.BF16 if dts[2] == "bf16" else oracle.F32)
+    assert np.array_equal(out.numpy(q).view(np.uint16 if dts[2] == "bf16" else np.uint32),
+                          ref.view(np.uint16 if dts[2] == "bf16" else np.uint32))
+    if n and dts[0] == dts[2]:  # in place: out is a
+        kernels.add(q, ta, tb, ta)
+        assert np.array_equal(ta.numpy(q).view(np.uint8), ref.view(np.uint8))
+    for t in (ta, tb, out):
+        t.free()
+
+
+def test_add_rejects_mismatches(dev, q):
+    a, b, short = Tensor(dev, (64,), "f32"), Tensor(dev, (64,), "bf16"), Tensor(dev, (32,), "f32")
+    with pytest.raises(ValueError):
+        kernels.add(q, a, short, a)
+    # out is an operand read as another dtype: refused (a as a, then a as b, stored as bf16)
+    with pytest.raises(_lib.VdslError, match="in-place"):
+        _lib.call("vdsl_op_add", q.handle, 64, F32, a.handle, BF16, b.handle, BF16, a.handle)
+    with pytest.raises(_lib.VdslError, match="in-place"):
+        _lib.call("vdsl_op_add", q.handle, 64, BF16, b.handle, F32, a.handle, BF16, a.handle)
+    with pytest.raises(_lib.VdslError, match="f32 and bf16"):
+        _lib.call("vdsl_op_add", q.handle, 64, 2, a.handle, F32, a.handle, F32, a.handle)
+    for t in (a, b, short):
+        t.free()
+
+
 @pytest.mark.parametrize("rows,cols", [(128, 192), (70, 33), (72, 100), (8, 4), (2048, 4096)])
 def test_mse(dev, q, rows, cols):
     y = rng.normal(31, rows * cols).reshape(rows, cols)

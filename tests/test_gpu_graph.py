@@ -289,3 +289,64 @@ def test_elided_values_raise(dev, q):
             exe.free()
     for a, b in zip(*res):
         assert np.array_equal(a, b)
+
+
+RES = dict(B=256, D=512, Hd=512, O=256)
+FAST = {"prepare_transposes": True, "fuse_gelu_backward": True, "pack_weights": True, "fuse_mse": True,
+        "store_gelu_deriv": True, "k_major_grads": True}
+
+
+def run_residual(dev, q, feeds, replays=2, **flags):
+    """The residual graph of tests/test_graph.py (ReLU, GELU, a residual add, a weight tied across
+    two layers) on the device: eager run, then replays of its capture equal to it bit for bit."""
+    from test_graph import residual_graph
+    g, grads = residual_graph(**RES, **flags)
+    exe = g.compile(dev)
+    names = ["H1", "R", "loss"] + [grads[n].name for n in ("W1", "WR", "W3")]
+    try:
+        for n, a in feeds.items():
+            exe.write(q, n, a)
+        exe.run(q)
+        eager = {n: exe.read(q, n) for n in names}
+        step = exe.capture(q)
+        for _ in range(replays):
+            for n in names:
+                exe.t[n].buffer.fill_u32(q, 0x7FC07FC0)
+            q.sync()
+            step.launch(q)
+            q.sync()
+            for n in names:
+                assert np.array_equal(exe.read(q, n), eager[n]), f"replay differs from eager run in {n}"
+        step.destroy()
+    finally:
+        exe.free()
+    return g, eager
+
+
+def test_residual_graph_against_the_oracle(dev, q):
+    """Plain graph: every op against the oracle's run of the same ops (GEMM tolerances: f32
+    accumulation against the oracle's f64 sums), the residual sum and the gradients summed over
+    two readers included."""
+    from test_graph import residual_inputs
+    feeds = residual_inputs(**RES, w_range=0.08)
+    g, got = run_residual(dev, q, feeds)
+    ref = oracle.graph_step(g, feeds)
+    X, W1 = rng.bf16_to_f32(feeds["X"]), rng.bf16_to_f32(feeds["W1"])
+    bf16_close(got["H1"], ref["H1"], floor=1e-2 * absmm(X, W1.T).max())
+    assert abs(float(got["loss"][0]) - float(ref["loss"][0])) <= 1e-2 * float(ref["loss"][0])
+    for n in ("grad_W1", "grad_WR", "grad_W3"):
+        a, r = got[n].astype(np.float64), ref[n].astype(np.float64)
+        assert np.linalg.norm(a - r) <= 2e-2 * np.linalg.norm(r), n
+
+
+def test_residual_graph_fused_forms_identical(dev, q):
+    """Packed weights, prepared transposes, the fused GELU backward where it applies (H3) and the
+    fused loss give the plain graph's values bit for bit (loss: last bit)."""
+    from test_graph import residual_inputs
+    feeds = residual_inputs(**RES, w_range=0.08)
+    _, base = run_residual(dev, q, feeds, replays=1)
+    for flags in ({"prepare_transposes": True, "fuse_gelu_backward": True}, {"pack_weights": True}, FAST):
+        _, got = run_residual(dev, q, feeds, replays=1, **flags)
+        for n in ("H1", "R", "grad_W1", "grad_WR", "grad_W3"):
+            assert np.array_equal(got[n], base[n]), f"{flags}: {n} differs"
+        assert loss_close(got["loss"], base["loss"]), flags

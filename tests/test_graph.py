@@ -206,3 +206,98 @@ def test_fused_loss_without_y_elides_y():
     assert lin.outputs[0].name in g.elided and lin.outputs[0].name not in g.host_outputs()
     g2, _ = graph.mlp_train_graph(batch=256, d_in=512, hidden=512, d_out=256)
     assert g2.ops[1].outputs[0].name not in g2.elided
+
+
+def residual_graph(B=16, D=8, Hd=8, O=6, **flags):
+    """X -> H1 = relu(X W1^T) -> H2 = GELU(H1 WR^T) -> R = H1 + H2 -> H3 = GELU(R WR^T) -> Y = H3 W3^T
+    -> MSE: H1 is read twice (a residual), WR by two layers (tied weights), ReLU and GELU both."""
+    g = graph.Graph(**flags)
+    x = g.input("X", (B, D), "bf16")
+    w1 = g.param("W1", (Hd, D), "bf16")
+    wr = g.param("WR", (Hd, Hd), "bf16")
+    w3 = g.param("W3", (O, Hd), "bf16")
+    t = g.input("T", (B, O), "f32")
+    h1 = g.linear(x, w1, act="relu", name="H1")
+    h2 = g.linear(h1, wr, act="gelu", name="H2")
+    r = g.add(h1, h2, name="R")
+    h3 = g.linear(r, wr, act="gelu", name="H3")
+    y = g.linear(h3, w3, out_dtype="f32", name="Y")
+    return g, g.backward(g.mse_loss(y, t))
+
+
+def _residual_f64(X, W1, WR, W3, T):
+    def gelu(a):
+        return 0.5 * a * (1 + erf(a / np.sqrt(2)))
+    h1 = np.maximum(X @ W1.T, 0)
+    r = h1 + gelu(h1 @ WR.T)
+    y = gelu(r @ WR.T) @ W3.T
+    return np.mean((y - T) ** 2)
+
+
+def residual_inputs(B=16, D=8, Hd=8, O=6, seed=30, w_range=0.6):
+    x = rng.f32_to_bf16(rng.normal(seed, B * D)).reshape(B, D)
+    w1 = rng.f32_to_bf16(rng.uniform(seed + 1, Hd * D, -w_range, w_range)).reshape(Hd, D)
+    wr = rng.f32_to_bf16(rng.uniform(seed + 2, Hd * Hd, -w_range, w_range)).reshape(Hd, Hd)
+    w3 = rng.f32_to_bf16(rng.uniform(seed + 3, O * Hd, -w_range, w_range)).reshape(O, Hd)
+    t = rng.normal(seed + 4, B * O).reshape(B, O)
+    return {"X": x, "W1": w1, "WR": wr, "W3": w3, "T": t}
+
+
+def test_residual_graph_backward_structure():
+    g, grads = residual_graph()
+    kinds = [op.kind for op in g.ops]
+    assert kinds[:6] == ["linear", "linear", "add", "linear", "linear", "mse"]
+    assert sorted(grads) == ["W1", "W3", "WR"]
+    assert grads["WR"].name == "grad_WR" and grads["WR"].producer.kind == "add"  # the tied weight's two terms
+    terms = grads["WR"].producer.inputs
+    assert all(t.producer.kind == "gemm" and t.name.startswith("dterm_WR") for t in terms)
+    assert kinds.count("relu_bwd") == 1 and kinds.count("gelu_bwd") == 2
+    # dL/dH1: the residual's term (dL/dR) plus the WR layer's dL/dH1, summed in f32 before relu_bwd
+    relu = next(op for op in g.ops if op.kind == "relu_bwd")
+    s = relu.inputs[0]
+    assert s.dtype == "f32" and s.producer.kind == "add" and s.name.startswith("dsum_H1")
+    assert grads["W1"].name == "grad_W1" and grads["W3"].name == "grad_W3"
+
+
+def test_residual_graph_fusions_skip_values_read_twice():
+    """With every fusion on, the GELU backward is fused only where its value has one reader (H3);
+    the values read twice (H1, and R's gradient reaching H1 and H2) take the unfused rules."""
+    flags = dict(prepare_transposes=True, fuse_gelu_backward=True, k_major_grads=True)
+    g, grads = residual_graph(**flags)
+    fused = [op for op in g.ops if op.kind == "gemm_gelu_bwd"]
+    assert len(fused) == 1 and fused[0].inputs[2] is g.ops[3].attrs["pre"]  # H3's pre-activation
+    assert sorted(grads) == ["W1", "W3", "WR"]
+    g2 = graph.Graph(fuse_mse=True, pack_weights=True)
+    x = g2.input("X", (128, 256), "bf16")
+    y = g2.linear(x, g2.param("W", (256, 256), "bf16"), out_dtype="f32", name="Y")
+    z = g2.add(y, y, name="Z")  # Y read by the loss and by another op: the loss stays unfused
+    g2.backward(g2.mse_loss(y, g2.input("T", (128, 256), "f32")))
+    assert [op.kind for op in g2.ops][:3] == ["linear", "add", "mse"] and z.name == "Z"
+
+
+@pytest.mark.parametrize("flags", [{}, {"prepare_transposes": True, "fuse_gelu_backward": True, "k_major_grads": True}])
+def test_residual_graph_gradients_match_finite_differences(flags):
+    """The oracle run of the backward ops the graph emits against central differences of the f64
+    loss: pins the add, relu, fan-out and tied-weight rules (a term dropped or overwritten fails)."""
+    g, grads = residual_graph(**flags)
+    feeds = residual_inputs()
+    v = oracle.graph_step(g, feeds)
+    X, W1, WR, W3 = (rng.bf16_to_f32(feeds[n]).astype(np.float64) for n in ("X", "W1", "WR", "W3"))
+    T = feeds["T"].astype(np.float64)
+    base = _residual_f64(X, W1, WR, W3, T)
+    assert abs(float(v["loss"][0]) - base) <= 2e-2 * base
+    eps = 1e-5
+    for name, W in (("W1", W1), ("WR", WR), ("W3", W3)):
+        fd = np.zeros_like(W)
+        for idx in np.ndindex(W.shape):
+            args = {"W1": W1, "WR": WR, "W3": W3}
+            Wp, Wm = W.copy(), W.copy()
+            Wp[idx] += eps
+            Wm[idx] -= eps
+            fd[idx] = (_residual_f64(X, **{**args, name: Wp}, T=T) - _residual_f64(X, **{**args, name: Wm}, T=T)) / (2 * eps)
+        got = v[grads[name].name].astype(np.float64)
+        assert np.linalg.norm(got - fd) <= 3e-2 * np.linalg.norm(fd), name
+    # a graph that drops the residual's gradient term is caught: H1's gradient without it
+    relu = next(op for op in g.ops if op.kind == "relu_bwd")
+    terms = relu.inputs[0].producer.inputs
+    assert len(terms) == 2 and not np.array_equal(v[terms[0].name], v[relu.inputs[0].name])

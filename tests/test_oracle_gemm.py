@@ -124,6 +124,28 @@ def test_gelu_grad_keeps_relative_accuracy_for_negative_pre():
     assert np.all(np.abs(rng.bf16_to_f32(da) - exact) <= 2 ** -8 * np.abs(exact))
 
 
+def test_relu_bwd_is_a_select_and_add_is_one_f32_addition():
+    """orc_relu_bwd against numpy's select (pre <= 0 and NaN give +0, infinities pass where pre >
+    0), orc_add against numpy's f32 addition (one correctly rounded result), bf16 widened exactly."""
+    r = np.random.default_rng(21)
+    dh = r.standard_normal((9, 13)).astype(np.float32)
+    pre = r.standard_normal((9, 13)).astype(np.float32)
+    pre[0, :4] = [0.0, -0.0, np.nan, 1e-45]
+    dh[1, :2] = [np.inf, -np.inf]
+    pre[1, :2] = [-1.0, 2.0]
+    da, da_t = oracle.relu_bwd(dh, pre)
+    ref = oracle.cast(np.where(pre > 0, dh, np.float32(0)).astype(np.float32), oracle.BF16)
+    assert np.array_equal(da, ref) and np.array_equal(da_t, ref.T)
+    assert da[0, 0] == da[0, 1] == da[0, 2] == 0 and da[1, 0] == 0 and da[1, 1] == 0xFF80  # +0s, -inf kept
+    a = r.standard_normal(1000).astype(np.float32)
+    b = (r.standard_normal(1000) * 1e-3).astype(np.float32)
+    assert np.array_equal(oracle.add(a, b), a + b)
+    ab, bb = oracle.cast(a, oracle.BF16), oracle.cast(b, oracle.BF16)
+    wide = rng.bf16_to_f32(ab) + rng.bf16_to_f32(bb)
+    assert np.array_equal(oracle.add(ab, bb), wide)
+    assert np.array_equal(oracle.add(ab, b, oracle.BF16), oracle.cast(rng.bf16_to_f32(ab) + b, oracle.BF16))
+
+
 def test_mse_matches_finite_differences():
     y = rng.normal(7, 32 * 40).reshape(32, 40)
     t = rng.normal(8, 32 * 40).reshape(32, 40)

@@ -148,6 +148,8 @@ PROTOTYPES = {
     "vdsl_op_cast": (C.c_int, [_vp, _i64, _i32, _vp, _i32, _vp]),
     "vdsl_op_gelu_fwd": (C.c_int, [_vp, _i64, _i32, _vp, _i32, _vp]),
     "vdsl_op_gelu_bwd": (C.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "vdsl_op_relu_bwd": (C.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "vdsl_op_add": (C.c_int, [_vp, _i64, C.c_int32, _vp, C.c_int32, _vp, C.c_int32, _vp]),
     "vdsl_op_gemm_bf16_gelu_bwd": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
     "vdsl_op_gemm_bf16_gelu_bwd_packed": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
     "vdsl_op_gemm_bf16_mul_packed": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),

@@ -201,6 +201,13 @@ int main(void) {
     vdsl_buffer da = alloc(d, (size_t)(M * N * 2)), dat = alloc(d, (size_t)(M * N * 2));
     EXPECT_OK(vdsl_op_gelu_bwd(q, M, N, C, pre, da, dat));
     EXPECT_ERR(vdsl_op_gelu_bwd(q, M, 2 * N, C, pre, da, dat));
+    EXPECT_OK(vdsl_op_relu_bwd(q, M, N, C, pre, da, NULL));
+    EXPECT_ERR(vdsl_op_relu_bwd(q, kHuge, N, C, pre, da, dat));
+    EXPECT_OK(vdsl_op_add(q, M * N, VDSL_F32, C, VDSL_F32, pre, VDSL_F32, C));
+    EXPECT_OK(vdsl_op_add(q, M * N - 3, VDSL_BF16, da, VDSL_F32, pre, VDSL_BF16, dat));
+    EXPECT_ERR(vdsl_op_add(q, M * N, VDSL_F32, C, VDSL_F32, pre, VDSL_BF16, C));
+    EXPECT_ERR(vdsl_op_add(q, 2 * M * N, VDSL_F32, C, VDSL_F32, pre, VDSL_F32, C));
+    EXPECT_ERR(vdsl_op_add(q, M * N, VDSL_I8, C, VDSL_F32, pre, VDSL_F32, C));
     const int64_t parts = vdsl_mse_partials_count(M, N);
     vdsl_buffer loss = alloc(d, 4), part = alloc(d, (size_t)(parts > 0 ? parts : 1) * 8);
     EXPECT_OK(vdsl_op_mse_fwd_bwd(q, M, N, C, pre, loss, da, dat, part));

@@ -1,4 +1,5 @@
-// Autodiff building blocks of the MLP graph on gfx950: GELU backward and MSE forward+backward.
+// Autodiff building blocks of the execution graph on gfx950: GELU and ReLU backward, MSE
+// forward+backward, and the elementwise sum (residual adds, gradients of a value read twice).
 //
 // No reference code (north-star op class: "compiler-generated backward").  Both kernels are
 // elementwise over [rows][cols] and also emit the transposed gradient, because the weight
@@ -45,9 +46,20 @@ __device__ __forceinline__ void pack_unit(const float (&v)[2][4], uint32_t (&row
   }
 }
 
-__global__ __launch_bounds__(256) void gelu_bwd_vec(const float* __restrict__ dh, const float* __restrict__ pre,
-                                                    uint16_t* __restrict__ da, uint16_t* __restrict__ da_t,
-                                                    int64_t rows, int64_t cols) {
+// The activation backward of y = act(pre): dL/dpre = dL/dy * act'(pre).  ACT 0: GELU' (the erfc
+// form of gelu_grad_f); ACT 1: ReLU', dL/dy where pre > 0, else +0 (pre <= 0 and NaN: 0, as
+// torch's threshold backward; a select, so an infinite dL/dy at pre <= 0 gives 0, not NaN).
+enum { kActGelu = 0, kActRelu = 1 };
+template <int ACT>
+__device__ __forceinline__ float act_bwd(float g, float pre) {
+  if constexpr (ACT == kActGelu) return g * gelu_grad_f(pre);
+  else return pre > 0.0f ? g : 0.0f;
+}
+
+template <int ACT>
+__global__ __launch_bounds__(256) void act_bwd_vec(const float* __restrict__ dh, const float* __restrict__ pre,
+                                                   uint16_t* __restrict__ da, uint16_t* __restrict__ da_t,
+                                                   int64_t rows, int64_t cols) {
   __shared__ __align__(16) uint32_t tile[kPairTileWords];
   const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
   f32x4 g[2][2], x[2][2];
@@ -75,7 +87,7 @@ __global__ __launch_bounds__(256) void gelu_bwd_vec(const float* __restrict__ dh
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[i][j] = g[k][i][j] * gelu_grad_f(x[k][i][j]);
+      for (int j = 0; j < 4; ++j) v[i][j] = act_bwd<ACT>(g[k][i][j], x[k][i][j]);
     uint32_t row[2][2], pair[4];
     pack_unit(v, row, pair);
     const int64_t o = (r0 + 2 * q) * cols + c0 + 4 * t;
@@ -157,9 +169,10 @@ __global__ __launch_bounds__(256) void mse_tile_vec(const float* __restrict__ y,
   store_pair_tile_transposed(tile, dy_t, rows, cols, r0, c0);
 }
 
-__global__ __launch_bounds__(256) void gelu_bwd_kernel(const float* __restrict__ dh, const float* __restrict__ pre,
-                                                       uint16_t* __restrict__ da, uint16_t* __restrict__ da_t,
-                                                       int64_t rows, int64_t cols) {
+template <int ACT>
+__global__ __launch_bounds__(256) void act_bwd_kernel(const float* __restrict__ dh, const float* __restrict__ pre,
+                                                      uint16_t* __restrict__ da, uint16_t* __restrict__ da_t,
+                                                      int64_t rows, int64_t cols) {
   __shared__ uint16_t tile[64][66];
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
@@ -168,7 +181,7 @@ __global__ __launch_bounds__(256) void gelu_bwd_kernel(const float* __restrict__
     const int64_t r = r0 + ty + 4 * p, c = c0 + tx;
     if (r < rows && c < cols) {
       const int64_t o = r * cols + c;
-      const uint16_t h = f32_to_bf16(dh[o] * gelu_grad_f(pre[o]));
+      const uint16_t h = f32_to_bf16(act_bwd<ACT>(dh[o], pre[o]));
       da[o] = h;
       tile[ty + 4 * p][tx] = h;
     }
@@ -243,8 +256,11 @@ int launch_mse_finish(const double* partials, int64_t n_partials, float* loss, d
 
 using namespace vdsl;
 
-extern "C" int vdsl_op_gelu_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer dh, vdsl_buffer pre, vdsl_buffer da,
-                                vdsl_buffer da_t) {
+namespace vdsl {
+namespace {
+template <int ACT>
+int launch_act_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer dh, vdsl_buffer pre, vdsl_buffer da,
+                   vdsl_buffer da_t, const char* name) {
   VDSL_TRY(enter_queue(q));
   if (rows < 0 || cols < 0) return fail(VDSL_ERR_INVALID_ARG, "negative shape");
   VDSL_TRY(check_buffer(q, dh, nbytes(rows, cols, 4), "dh", false));
@@ -254,18 +270,30 @@ extern "C" int vdsl_op_gelu_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_b
   const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols);  // fits: checked above
   if (n == 0) return VDSL_OK;
   const int64_t gx = (cols + 63) / 64, gy = (rows + 63) / 64;
-  if (gy > 65535 || gx > 0x7fffffff) return fail(VDSL_ERR_UNSUPPORTED, "gelu_bwd: tensor too large");
+  if (gy > 65535 || gx > 0x7fffffff) return fail(VDSL_ERR_UNSUPPORTED, std::string(name) + ": tensor too large");
   const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+  const float* g = static_cast<const float*>(dh->ptr);
+  const float* x = static_cast<const float*>(pre->ptr);
+  uint16_t* a = static_cast<uint16_t*>(da->ptr);
+  uint16_t* at = da_t ? static_cast<uint16_t*>(da_t->ptr) : nullptr;
   if (rows % 8 == 0 && cols % 4 == 0) {
-    hipLaunchKernelGGL(gelu_bwd_vec, grid, dim3(256), 0, q->stream, static_cast<const float*>(dh->ptr),
-                       static_cast<const float*>(pre->ptr), static_cast<uint16_t*>(da->ptr),
-                       da_t ? static_cast<uint16_t*>(da_t->ptr) : nullptr, rows, cols);
-    return check_launch("gelu_bwd_vec");
+    hipLaunchKernelGGL(act_bwd_vec<ACT>, grid, dim3(256), 0, q->stream, g, x, a, at, rows, cols);
+    return check_launch("act_bwd_vec");
   }
-  hipLaunchKernelGGL(gelu_bwd_kernel, grid, dim3(256), 0, q->stream,
-                     static_cast<const float*>(dh->ptr), static_cast<const float*>(pre->ptr), static_cast<uint16_t*>(da->ptr),
-                     da_t ? static_cast<uint16_t*>(da_t->ptr) : nullptr, rows, cols);
-  return check_launch("gelu_bwd_kernel");
+  hipLaunchKernelGGL(act_bwd_kernel<ACT>, grid, dim3(256), 0, q->stream, g, x, a, at, rows, cols);
+  return check_launch("act_bwd_kernel");
+}
+}  // namespace
+}  // namespace vdsl
+
+extern "C" int vdsl_op_gelu_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer dh, vdsl_buffer pre, vdsl_buffer da,
+                                vdsl_buffer da_t) {
+  return launch_act_bwd<kActGelu>(q, rows, cols, dh, pre, da, da_t, "gelu_bwd");
+}
+
+extern "C" int vdsl_op_relu_bwd(vdsl_queue q, int64_t rows, int64_t cols, vdsl_buffer dh, vdsl_buffer pre, vdsl_buffer da,
+                                vdsl_buffer da_t) {
+  return launch_act_bwd<kActRelu>(q, rows, cols, dh, pre, da, da_t, "relu_bwd");
 }
 
 extern "C" int64_t vdsl_mse_partials_count(int64_t rows, int64_t cols) {
@@ -337,4 +365,104 @@ extern "C" int vdsl_op_mse_fwd_bwd(vdsl_queue q, int64_t rows, int64_t cols, vds
   hipLaunchKernelGGL(mse_finish_kernel, dim3(1), dim3(256), 0, q->stream, part, np, static_cast<float*>(loss->ptr),
                      1.0 / static_cast<double>(n));
   return check_launch("mse_finish_kernel");
+}
+
+namespace vdsl {
+namespace {
+// Four consecutive elements of an F32 or BF16 array, widened to f32 (exact), from one 16- or
+// 8-byte load; and their store, rounded once (RNE) to the output dtype.
+template <int T>
+__device__ __forceinline__ void load4(const void* __restrict__ p, int64_t i, float (&v)[4]) {
+  if constexpr (T == VDSL_F32) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = x[j];
+  } else {
+    const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+    v[0] = __uint_as_float(w.x << 16);
+    v[1] = __uint_as_float(w.x & 0xFFFF0000u);
+    v[2] = __uint_as_float(w.y << 16);
+    v[3] = __uint_as_float(w.y & 0xFFFF0000u);
+  }
+}
+
+template <int T>
+__device__ __forceinline__ void store4(void* __restrict__ p, int64_t i, const float (&v)[4]) {
+  if constexpr (T == VDSL_F32) {
+    const f32x4 x = {v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(static_cast<float*>(p) + i) = x;
+  } else {
+    uint2 w;
+    w.x = pack_bf16x2(v[0], v[1]);
+    w.y = pack_bf16x2(v[2], v[3]);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i) = w;
+  }
+}
+
+template <int T>
+__device__ __forceinline__ float load1(const void* __restrict__ p, int64_t i) {
+  if constexpr (T == VDSL_F32) return static_cast<const float*>(p)[i];
+  else return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+// out = a + b elementwise: one f32 addition per element, rounded once to out's dtype.  VEC (n %
+// 4 == 0; every buffer is a whole 256-byte-aligned allocation): four elements per lane and trip.
+// A lane reads its elements before it writes them, so out may be a or b (same dtype).
+template <int AT, int BT, int OT, bool VEC>
+__global__ __launch_bounds__(256) void add_kernel(const void* a, const void* b, void* out, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if constexpr (VEC) {
+    for (int64_t u = first; u < n / 4; u += stride) {
+      float x[4], y[4], z[4];
+      load4<AT>(a, 4 * u, x);
+      load4<BT>(b, 4 * u, y);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) z[j] = x[j] + y[j];
+      store4<OT>(out, 4 * u, z);
+    }
+  } else {
+    for (int64_t i = first; i < n; i += stride) {
+      const float z = load1<AT>(a, i) + load1<BT>(b, i);
+      if constexpr (OT == VDSL_F32) static_cast<float*>(out)[i] = z;
+      else static_cast<uint16_t*>(out)[i] = f32_to_bf16(z);
+    }
+  }
+}
+
+typedef void (*AddKernel)(const void*, const void*, void*, int64_t);
+template <int AT, int BT, int OT>
+AddKernel add_pick(bool vec) {
+  return vec ? add_kernel<AT, BT, OT, true> : add_kernel<AT, BT, OT, false>;
+}
+template <int AT, int BT>
+AddKernel add_pick(int ot, bool vec) {
+  return ot == VDSL_F32 ? add_pick<AT, BT, VDSL_F32>(vec) : add_pick<AT, BT, VDSL_BF16>(vec);
+}
+template <int AT>
+AddKernel add_pick(int bt, int ot, bool vec) {
+  return bt == VDSL_F32 ? add_pick<AT, VDSL_F32>(ot, vec) : add_pick<AT, VDSL_BF16>(ot, vec);
+}
+}  // namespace
+}  // namespace vdsl
+
+extern "C" int vdsl_op_add(vdsl_queue q, int64_t n, int32_t a_dtype, vdsl_buffer a, int32_t b_dtype, vdsl_buffer b,
+                           int32_t out_dtype, vdsl_buffer out) {
+  VDSL_TRY(enter_queue(q));
+  if (n < 0) return fail(VDSL_ERR_INVALID_ARG, "negative element count");
+  auto fb = [](int32_t t) { return t == VDSL_F32 || t == VDSL_BF16; };
+  if (!fb(a_dtype) || !fb(b_dtype) || !fb(out_dtype)) return fail(VDSL_ERR_UNSUPPORTED, "add supports f32 and bf16");
+  VDSL_TRY(check_buffer(q, a, nbytes(n, dtype_size(a_dtype)), "a", false));
+  VDSL_TRY(check_buffer(q, b, nbytes(n, dtype_size(b_dtype)), "b", false));
+  VDSL_TRY(check_buffer(q, out, nbytes(n, dtype_size(out_dtype)), "out", true));
+  if ((out == a && a_dtype != out_dtype) || (out == b && b_dtype != out_dtype))
+    return fail(VDSL_ERR_INVALID_ARG, "in-place add needs the output's dtype on the operand it overwrites");
+  if (n == 0) return VDSL_OK;
+  const bool vec = n % 4 == 0;
+  const int64_t units = vec ? n / 4 : n;
+  const int64_t blocks = std::min<int64_t>((units + 255) / 256, 256 * 16);
+  const AddKernel k = a_dtype == VDSL_F32 ? add_pick<VDSL_F32>(b_dtype, out_dtype, vec)
+                                          : add_pick<VDSL_BF16>(b_dtype, out_dtype, vec);
+  hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, q->stream, a->ptr, b->ptr, out->ptr, n);
+  return check_launch("add_kernel");
 }

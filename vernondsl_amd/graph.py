@@ -17,10 +17,15 @@ recorded on one queue and replayed as a single hipGraph (no host work or allocat
     exe.write(q, "W1", w1_new); step.launch(q)       # re-packs W1 first, then replays
 
 Backward rules (y = act(x W^T), W stored [out][in]):
-    g    = dL/dy (+ its transpose g^T), bf16; for act = gelu: g = gelu_bwd(dL/dh, pre)
+    g    = dL/dy (+ its transpose g^T), bf16; for act = gelu / relu: g = gelu_bwd / relu_bwd(dL/dh, pre)
     dW   = g^T x        -> vdsl_op_gemm_bf16(A = g^T [out][B], B = x [B][in], trans_b = 0)
     dx   = g W          -> vdsl_op_gemm_bf16(A = g [B][out], B = W [out][in], trans_b = 0)
     MSE: loss and dL/dy = 2 (y - t) / n (bf16, plus transpose) from one fused op.
+    y = a + b: dL/da = dL/db = dL/dy.
+    A value read by several ops (a residual input, a weight tied across layers): dL/dv is the f32
+    sum of the terms its readers give (an add op per extra term); fusions that would apply a term
+    before the sum is complete (GELU' in the dL/dx GEMM, the loss in the last GEMM) are skipped
+    for such values.
 """
 from __future__ import annotations
 
@@ -146,6 +151,20 @@ class Graph:
         self.prepare_ops.append(op)
         return v
 
+    def add(self, a: Value, b: Value, out_dtype: str | None = None, name=None) -> Value:
+        """a + b elementwise (a residual sum): f32 or bf16 operands of one shape, one f32 addition,
+        rounded to out_dtype (default f32 when either operand is f32, else bf16)."""
+        if a.shape != b.shape:
+            raise ValueError(f"add: shapes {a.shape} and {b.shape} differ")
+        if a.dtype not in ("f32", "bf16") or b.dtype not in ("f32", "bf16"):
+            raise TypeError("add takes f32 and bf16 tensors")
+        out_dtype = out_dtype or ("f32" if "f32" in (a.dtype, b.dtype) else "bf16")
+        if out_dtype not in ("f32", "bf16"):
+            raise TypeError("add stores f32 or bf16")
+        y = self._value(name or self._fresh("add"), a.shape, out_dtype, requires_grad=a.requires_grad or b.requires_grad)
+        self._op("add", [a, b], [y])
+        return y
+
     def mse_loss(self, y: Value, t: Value, name="loss") -> Value:
         if y.dtype != "f32" or t.dtype != "f32" or y.shape != t.shape:
             raise TypeError("mse_loss takes two f32 tensors of one shape")
@@ -187,6 +206,10 @@ class Graph:
         if loss.producer is None or loss.producer.kind != "mse":
             raise ValueError("backward() starts from an mse_loss value")
         fwd_ops = list(self.ops)
+        uses: dict[str, int] = {}  # forward reads of each value: more than one means summed gradients
+        for op in fwd_ops:
+            for v in op.inputs:
+                uses[v.name] = uses.get(v.name, 0) + 1
         # gradient of each activation: ("bf16", g, g_t) or ("f32", g)
         grad: dict[str, tuple] = {}
         y, _ = loss.producer.inputs
@@ -198,7 +221,7 @@ class Graph:
         grad[y.name] = ("bf16", dy, dy_t)
         lin = y.producer
         if (self.fuse_mse and lin is not None and lin.kind == "linear" and lin.attrs["act"] == "none"
-                and lin.attrs.get("packed") is not None and y.dtype == "f32"
+                and uses[y.name] == 1 and lin.attrs.get("packed") is not None and y.dtype == "f32"
                 and y.shape[0] % 128 == 0 and y.shape[1] % 256 == 0):
             # the linear op and the loss become one op: the GEMM's epilogue forms the loss and dL/dy
             mse_op = loss.producer
@@ -210,14 +233,19 @@ class Graph:
                 v.producer = lin
             if not self.keep_y:  # the fused op does not store y: nothing holds it
                 self.elided.add(y.name)
-        param_grads = {}
+        contrib: dict[str, list] = {}  # param name -> its gradient's terms, one per linear op reading it
         for op in reversed(fwd_ops):
             if op.kind == "mse":
                 continue
-            if op.kind not in ("linear", "linear_mse"):
+            if op.kind not in ("linear", "linear_mse", "add"):
                 raise NotImplementedError(f"no backward rule for {op.kind}")
             y = op.outputs[0]
             if y.name not in grad:
+                continue
+            if op.kind == "add":  # d(a + b) passes dL/dy to both operands
+                for x in op.inputs:
+                    if x.requires_grad or (x.producer is not None and x.kind == "activation" and _needs(x, self)):
+                        self._accumulate(grad, x, grad[y.name])
                 continue
             x, w = op.inputs[:2]
             g = grad[y.name]
@@ -238,17 +266,24 @@ class Graph:
                     gb, gt = self._to_bf16_pair(g[1])
                 else:
                     gb, gt = g[1], g[2]
-            else:
-                raise NotImplementedError("backward through relu is not implemented (training graphs use gelu)")
+            else:  # relu: dL/dpre = dL/dy where pre > 0
+                if g[0] != "f32":
+                    g = self._to_f32(g[1])
+                da = self._value(self._fresh("d_pre"), y.shape, "bf16", "grad")
+                da_t = self._value(self._fresh("dT_pre"), y.shape[::-1], "bf16", "grad")
+                self._transposed.add(da_t.name)
+                self._op("relu_bwd", [g[1], op.attrs["pre"]], [da, da_t])
+                gb, gt = da, da_t
             if w.requires_grad:
-                dw = self._value("grad_" + w.name, w.shape, "f32", "grad")
+                single = uses[w.name] == 1
+                dw = self._value("grad_" + w.name if single else self._fresh("dterm_" + w.name), w.shape, "f32", "grad")
                 # dW[out][in] = sum_b g[b][out] x[b][in]: A = g^T [out][B] (K = B contiguous), B = x [B][in];
                 # with k_major_grads A is g as stored ([B][out] = [K][M], trans_a)
                 if self.k_major_grads:
                     self._op("gemm", [gb, x], [dw], trans_a=True, trans_b=False, epi=_lib.EPI_NONE)
                 else:
                     self._op("gemm", [gt, x], [dw], trans_a=False, trans_b=False, epi=_lib.EPI_NONE)
-                param_grads[w.name] = dw
+                contrib.setdefault(w.name, []).append(dw)
             if x.requires_grad or (x.producer is not None and x.kind == "activation" and _needs(x, self)):
                 # dx[B][in] = sum_o g[b][o] W[o][in]: A = g [B][out], B = W stored [out][in] = [K][N].
                 # A param's transpose W^T [in][out] (the NT form's B) is made once by a prepare op
@@ -256,7 +291,7 @@ class Graph:
                 wt = self._param_transpose(w) if self.prepare_transposes and w.kind == "param" else None
                 xp = x.producer
                 if (self.fuse_gelu_backward and wt is not None and xp is not None and xp.kind == "linear"
-                        and xp.attrs["act"] == "gelu"):
+                        and xp.attrs["act"] == "gelu" and uses[x.name] == 1):
                     # x = GELU(pre): the GEMM's epilogue applies GELU'(pre) and emits dL/dpre (bf16,
                     # plus its transpose) without writing dL/dx
                     da = self._value(self._fresh("d_pre"), x.shape, "bf16", "grad")
@@ -283,10 +318,36 @@ class Graph:
                         self._op("gemm", [gb, wt], [dx], trans_a=False, trans_b=True, epi=_lib.EPI_NONE)
                     else:
                         self._op("gemm", [gb, w], [dx], trans_a=False, trans_b=False, epi=_lib.EPI_NONE)
-                    grad[x.name] = ("f32", dx)
+                    self._accumulate(grad, x, ("f32", dx))
+        param_grads = {}
+        for name, terms in contrib.items():
+            # a param read by several linear ops (tied weights): the sum of its terms, in the order
+            # backward formed them (the last forward use first), named grad_<param> at the end
+            acc = terms[0]
+            for k, t in enumerate(terms[1:], 2):
+                last = k == len(terms)
+                s = self._value("grad_" + name if last else self._fresh("dsum_" + name), acc.shape, "f32", "grad")
+                self._op("add", [acc, t], [s])
+                acc = s
+            param_grads[name] = acc
         if self.k_major_grads:
             self._elide_unread_transposes()
         return param_grads
+
+    def _accumulate(self, grad: dict, x: Value, g: tuple):
+        """Adds the gradient term g to dL/dx: the first term is kept as it is; a second one (x read
+        by several ops) makes dL/dx their f32 sum, formed by an add op."""
+        prev = grad.get(x.name)
+        if prev is None:
+            grad[x.name] = g
+            return
+        if "gelu_da" in (prev[0], g[0]):
+            raise AssertionError("a GELU backward was fused for a value with several readers")
+        a = prev[1] if prev[0] == "f32" else self._to_f32(prev[1])
+        b = g[1] if g[0] == "f32" else self._to_f32(g[1])
+        s = self._value(self._fresh("dsum_" + x.name), x.shape, "f32", "grad")
+        self._op("add", [a, b], [s])
+        grad[x.name] = ("f32", s)
 
     def _elide_unread_transposes(self):
         """Transposed gradients no op reads: a transpose op that makes one is dropped; one emitted
@@ -495,6 +556,10 @@ class Executable:
                 raise RuntimeError("mse without backward: call Graph.backward() or use the loss op's fused form")
         elif op.kind == "gelu_bwd":
             kernels.gelu_bwd(q, ins[0], ins[1], outs[0], outs[1])
+        elif op.kind == "relu_bwd":
+            kernels.gelu_bwd(q, ins[0], ins[1], outs[0], outs[1], act="relu")
+        elif op.kind == "add":
+            kernels.add(q, ins[0], ins[1], outs[0])
         elif op.kind == "gemm_gelu_bwd":
             kernels.gemm_bf16_gelu_bwd(q, ins[0], ins[1], ins[2], outs[0], outs[1], op.attrs.get("packed", False))
         elif op.kind == "gemm_mul_bwd":

@@ -216,13 +216,22 @@ def gelu_fwd(q: Queue, x: Tensor, y: Tensor):
     call("vdsl_op_gelu_fwd", q.handle, x.numel, x.dtype, x.handle, y.dtype, y.handle)
 
 
-def gelu_bwd(q: Queue, dh: Tensor, pre: Tensor, da: Tensor, da_t=None):
+def gelu_bwd(q: Queue, dh: Tensor, pre: Tensor, da: Tensor, da_t=None, act: str = "gelu"):
+    """da = bf16(dh * act'(pre)) (+ its transpose da_t); act "gelu" or "relu"."""
     rows, cols = dh.shape
     _expect(dh, (rows, cols), "f32", "dh")
     _expect(pre, (rows, cols), "f32", "pre")
     _expect(da, (rows, cols), "bf16", "da")
     _expect(da_t, (cols, rows), "bf16", "da_t")
-    call("vdsl_op_gelu_bwd", q.handle, rows, cols, dh.handle, pre.handle, da.handle, _h(da_t))
+    fn = {"gelu": "vdsl_op_gelu_bwd", "relu": "vdsl_op_relu_bwd"}[act]
+    call(fn, q.handle, rows, cols, dh.handle, pre.handle, da.handle, _h(da_t))
+
+
+def add(q: Queue, a: Tensor, b: Tensor, out: Tensor):
+    """out = a + b elementwise (f32 or bf16 each; one f32 addition rounded to out's dtype)."""
+    if not (a.numel == b.numel == out.numel):
+        raise ValueError(f"add: {a.numel}, {b.numel} and {out.numel} elements")
+    call("vdsl_op_add", q.handle, out.numel, a.dtype, a.handle, b.dtype, b.handle, out.dtype, out.handle)
 
 
 def gemm_bf16_gelu_bwd(q: Queue, A: Tensor, B: Tensor, pre: Tensor, da: Tensor, da_t=None, packed=False):
