@@ -473,3 +473,16 @@ def test_reaction_example_sequences_bit_exact(dev, q):
             f[names[id(op.field)]] = oracle.pixel_program(op.program, 256, 256, [f[names[id(g)]] for g in op.inputs])
     assert np.array_equal(img, f["v"])
     assert float(img.max()) > 0.25 and (img > 0.01).sum() > 24 * 24  # the spot has reacted and spread
+
+
+def test_particles_example_one_d_fields_bit_exact(dev, q):
+    """1-D struct-fors over fields of 2-vectors, one program per stored field with a snapshot copy
+    (x and v load each other), an augmented store: 30 frames of 10 steps on the device equal
+    numpy's restatement of the update, particle for particle, bounces included."""
+    from test_taichi_general import particles_numpy, particles_seed
+    res, img = run_program(os.path.join(EX, "particles.py"), 30)
+    assert res["frames"] == 30 and img.shape == (16384, 2) and img.dtype == np.float32
+    x0, v0 = particles_seed()
+    x, v, _ = particles_numpy(x0, v0, np.zeros(16384, np.float32), 300)
+    assert np.array_equal(img, x)
+    assert (v[:, 1] > 0).any() and (x[:, 1] >= 0).all()  # some have bounced off the floor

@@ -486,10 +486,20 @@ def lower_named(text, kernel, args):
 
 def run_ops(low, names, arrays):
     """Runs a lowered kernel's programs in order on the oracle over {field name: array}, as the
-    device runs them (each program reads the fields as the programs before it left them)."""
+    device runs them (each program reads the fields as the programs before it left them; a
+    snapshot copy is named after its field with a trailing ').  1-D fields run as one row."""
     for op in low.ops():
-        ni, nj = op.field.shape
-        arrays[names[id(op.field)]] = oracle.pixel_program(op.program, ni, nj, [arrays[names[id(f)]] for f in op.inputs])
+        if op.kind == "copy":
+            names[id(op.field)] = names[id(op.inputs[0])] + "'"
+            arrays[names[id(op.field)]] = arrays[names[id(op.inputs[0])]].copy()
+            continue
+        shape = op.field.shape
+        ni, nj = shape if len(shape) == 2 else (1, shape[0])
+
+        def grid(a):
+            return a if len(shape) == 2 else a.reshape((1,) + a.shape)
+        out = oracle.pixel_program(op.program, ni, nj, [grid(arrays[names[id(f)]]) for f in op.inputs])
+        arrays[names[id(op.field)]] = out if len(shape) == 2 else out.reshape(out.shape[1:])
     return arrays
 
 
@@ -534,10 +544,17 @@ def test_in_place_updates_of_two_fields_need_no_order():
     assert np.array_equal(out["a"], a0 * f32(2.0)) and np.array_equal(out["b"], b0 * f32(3.0) + a0)
 
 
-def test_fields_that_read_each_other_before_their_stores_are_refused():
+def test_fields_that_load_each_other_are_read_from_a_snapshot():
+    """a, b = b, a through a temporary: each program loads the field the other stores, so one of
+    them is first copied to a snapshot, which the other program loads."""
     body = "        t = a[i, j]\n        a[i, j] = b[i, j]\n        b[i, j] = t"
-    with pytest.raises(tc.TaichiLoweringError, match="both ways"):
-        lower_named(two_fields(body, ()), "k", {})
+    low, names = lower_named(two_fields(body, ()), "k", {})
+    kinds = [op.kind for op in low.ops()]
+    assert kinds == ["copy", "pixel_program", "pixel_program"]
+    rng_ = np.random.default_rng(14)
+    a0, b0 = (rng_.standard_normal((24, 40)).astype(np.float32) for _ in range(2))
+    out = run_ops(low, names, {"a": a0.copy(), "b": b0.copy()})
+    assert np.array_equal(out["a"], b0) and np.array_equal(out["b"], a0)
 
 
 def gray_scott_numpy(u, v, dt, Du=0.16, Dv=0.08, feed=0.035, kill=0.065):
@@ -569,3 +586,105 @@ def test_reaction_example_two_struct_fors_and_two_stores_per_loop():
         u, v = gray_scott_numpy(u, v, 1.0)
         assert np.array_equal(f["u"], u) and np.array_equal(f["v"], v)
         assert np.array_equal(f["nu"], u) and np.array_equal(f["nv"], v)
+
+
+ONE_D = '''import taichi as ti
+N = 1000
+x = ti.field(dtype=float, shape=N)
+y = ti.field(dtype=float, shape=N)
+p = ti.Vector.field(2, dtype=float, shape=N)
+
+@ti.kernel
+def fill():
+    for i in x:
+        x[i] = i * 0.5 - 7.0
+
+@ti.kernel
+def smooth():
+    for i in y:
+        y[i] = (x[(i + 1) % N] + x[(i + N - 1) % N]) * 0.5 + x[ti.min(i + 3, N - 1)]
+
+@ti.kernel
+def pairs():
+    for k in range(N):
+        p[k] = [k * 0.25, x[k] * x[k]]
+
+@ti.kernel
+def bump():
+    for i in ti.ndrange(N):
+        x[i] += 1.5
+        x[i] *= 2.0
+'''
+
+
+def test_one_d_struct_fors_gathers_range_and_augmented_stores():
+    low, names = lower_named(ONE_D, "fill", {})
+    f = run_ops(low, names, {})
+    i = np.arange(1000, dtype=np.float32)
+    x = i * f32(0.5) - f32(7.0)
+    assert np.array_equal(f["x"], x)
+    low, names = lower_named(ONE_D, "smooth", {})
+    assert [fl.shape for fl in low.inputs] == [(1000,)]
+    f = run_ops(low, names, {"x": x})
+    assert np.array_equal(f["y"], (np.roll(x, -1) + np.roll(x, 1)) * f32(0.5) + x[np.minimum(np.arange(1000) + 3, 999)])
+    low, names = lower_named(ONE_D, "pairs", {})
+    f = run_ops(low, names, {"x": x})
+    assert f["p"].shape == (1000, 2) and np.array_equal(f["p"], np.stack([i * f32(0.25), x * x], -1))
+    low, names = lower_named(ONE_D, "bump", {})
+    f = run_ops(low, names, {"x": x})
+    assert np.array_equal(f["x"], (x + f32(1.5)) * f32(2.0))
+
+
+@pytest.mark.parametrize("kernel,msg", [
+    ("    for i in x:\n        x[i, 0] = 1.0", "1-D"),
+    ("    for i, j in ti.ndrange(N):\n        x[i] = 1.0", "2 non-negative"),
+    ("    for i in range(N, 2):\n        x[i] = 1.0", "extent"),
+    ("    for i in x:\n        x[i + 1] = 1.0", "store must write field"),
+])
+def test_one_d_errors(kernel, msg):
+    text = "import taichi as ti\nN = 8\nx = ti.field(dtype=float, shape=N)\n@ti.kernel\ndef k():\n" + kernel + "\n"
+    with pytest.raises(tc.TaichiLoweringError, match=msg):
+        tc.lower_source_kernel(text, "k", {})
+
+
+def particles_numpy(x, v, age, steps, g=-9.8, dt=0.002, damping=0.8):
+    """examples/particles.py's step() restated in numpy f32, operations in the program's order."""
+    x, v, age = x.copy(), v.copy(), age.copy()
+    gdt = f32(g) * f32(dt)
+    for _ in range(steps):
+        vel = v.copy()
+        vel[:, 1] = vel[:, 1] + gdt
+        pos = x + vel * f32(dt)
+        lo = pos[:, 1] < 0
+        pos[lo, 1] = -pos[lo, 1]
+        vel[lo, 1] = (-vel[lo, 1]) * f32(damping)
+        side = (pos[:, 0] < 0) | (pos[:, 0] > 1)
+        pos[side, 0] = np.minimum(np.maximum(pos[side, 0], f32(0)), f32(1))
+        vel[side, 0] = (-vel[side, 0]) * f32(damping)
+        x, v = pos, vel
+        age = age + f32(dt)
+    return x, v, age
+
+
+def particles_seed(n=16384):
+    i = np.arange(n)
+    x = np.stack([((i * 37 % 1009).astype(np.float32) / f32(1009.0)),
+                  f32(0.5) + (i * 59 % 997).astype(np.float32) / f32(1994.0)], -1)
+    v = np.stack([((i * 13 % 17) - 8).astype(np.float32) * f32(0.25), np.zeros(n, np.float32)], -1)
+    return x, v
+
+
+def test_particles_example_one_d_vector_fields_and_snapshot():
+    text = ex("particles.py")
+    seed, names = lower_named(text, "seed", {})
+    f = run_ops(seed, names, {})
+    x0, v0 = particles_seed()
+    assert np.array_equal(f["x"], x0) and np.array_equal(f["v"], v0)
+    step, names = lower_named(text, "step", {})
+    assert [op.kind for op in step.ops()] == ["copy", "pixel_program", "pixel_program", "pixel_program"]
+    f["age"] = np.zeros(16384, np.float32)
+    for _ in range(30):
+        f = run_ops(step, names, f)
+    x, v, age = particles_numpy(x0, v0, np.zeros(16384, np.float32), 30)
+    assert np.array_equal(f["x"], x) and np.array_equal(f["v"], v) and np.array_equal(f["age"], age)
+    assert (v0[:, 1] != v[:, 1]).all()

@@ -88,6 +88,11 @@ class Buffer:
         call("vdsl_buffer_read", queue.handle, self.handle, offset, host.ctypes.data_as(C.c_void_p), host.nbytes)
         return host
 
+    def copy_from(self, queue: "Queue", src: "Buffer", nbytes: int | None = None, dst_offset: int = 0, src_offset: int = 0):
+        """Device-to-device copy of nbytes (default: all of src) on the queue."""
+        n = src.nbytes - src_offset if nbytes is None else nbytes
+        call("vdsl_buffer_copy", queue.handle, self.handle, dst_offset, src.handle, src_offset, n)
+
     def fill_u32(self, queue: "Queue", pattern: int = 0, offset: int = 0, nbytes: int | None = None):
         n = self.nbytes - offset if nbytes is None else nbytes
         call("vdsl_buffer_fill_u32", queue.handle, self.handle, offset, n, pattern & 0xFFFFFFFF)
@@ -137,8 +142,20 @@ class Tensor:
         out = np.empty(self.shape, dtype=np_dtype(self.dtype))
         return self.buffer.read_into(queue, out)
 
+    def view(self, shape) -> "Tensor":
+        """The same buffer as a tensor of another shape with the same element count (row-major
+        data is unchanged); the view never frees the buffer, its owner does."""
+        shape = tuple(int(s) for s in shape)
+        if (int(np.prod(shape)) if shape else 1) != self.numel:
+            raise ValueError(f"view: shape {shape} does not hold {self.numel} elements")
+        v = object.__new__(Tensor)
+        v.shape, v.dtype, v.numel, v.buffer, v.device = shape, self.dtype, self.numel, self.buffer, self.device
+        v._view = True
+        return v
+
     def free(self):
-        self.buffer.free()
+        if not getattr(self, "_view", False):
+            self.buffer.free()
 
 
 class Graph:

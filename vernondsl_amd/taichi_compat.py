@@ -31,9 +31,10 @@ and constants, with at most one loop - a `while <test> and <counter> < MAX:` che
 loop whose body ends with `counter += 1`, or a `for _ in range(N):` loop - and stores
 `F[i, j] = <value>` (an i32 field stores the loop counter) into one or more fields of the loop's
 shape: a body storing several fields becomes one program per stored field, run in an order in
-which no program loads a field that an earlier one stored (a load at [i, j] after the body's own
-store reads the stored value, as in Taichi); a kernel of several top-level struct-fors runs their
-lowerings one after another.  What neither path lowers raises
+which no program loads a field that an earlier one stored (a snapshot copy where the programs
+load each other's fields; a load at [i, j] after the body's own store reads the stored value, as
+in Taichi); a kernel of several top-level struct-fors runs their lowerings one after another.
+1-D fields and struct-fors (`for i in x:`, `for i in range(N):`) run as one row of the grid.  What neither path lowers raises
 TaichiLoweringError naming what did not match; there is no CPU fallback.  Accepted complex squares are the ones equal bit for bit to (zr*zr - zi*zi, (zi*zr)*2):
 `z[0]**2 - z[1]**2`, `z[0]*z[0] - z[1]*z[1]`, and `z[1]*z[0]*2` / `z[0]*z[1]*2` / `2*(z[0]*z[1])` /
 `z[0]*z[1] + z[0]*z[1]` for the imaginary part (`(2*z[0])*z[1]` is refused: it rounds differently
@@ -90,9 +91,9 @@ def _device():
 
 
 class Field:
-    """A dense 2-D field (fractal.py:8) of scalars, or of vectors of `width` f32 components
-    (ti.Vector.field).  Storage is a device tensor ([W][H] or [W][H][width]), allocated and zeroed
-    on first use."""
+    """A dense 2-D field (fractal.py:8), or a 1-D one, of scalars or of vectors of `width` f32
+    components (ti.Vector.field).  Storage is a device tensor ([W][H], [N], plus [width] for
+    vectors), allocated and zeroed on first use."""
 
     def __init__(self, dtype, shape, width=1):
         if dtype in (float, f32, None):
@@ -108,6 +109,14 @@ class Field:
         if not 1 <= self.width <= 4 or (self.width > 1 and self.dtype != f32):
             raise TaichiLoweringError("vector fields hold 1 to 4 f32 components")
         self._tensor = None
+        self._snap = None
+
+    def snapshot(self):
+        """A hidden field of this one's type and shape, made once: the copy of its values taken
+        before a struct-for's programs when one of them stores it and another loads it."""
+        if self._snap is None:
+            self._snap = Field(self.dtype, self.shape, self.width)
+        return self._snap
 
     def tensor(self):
         if self._tensor is None:
@@ -117,6 +126,11 @@ class Field:
             t.buffer.fill_u32(q, 0)  # a Taichi field starts zeroed
             self._tensor = t
         return self._tensor
+
+    def grid_tensor(self):
+        """The tensor as a per-pixel program grid: a 1-D field of n elements is one row, [1][n]."""
+        t = self.tensor()
+        return t.view((1,) + t.shape) if len(self.shape) == 1 else t
 
     def to_numpy(self):
         _, q = _device()
@@ -173,6 +187,11 @@ class GUI:
     def set_image(self, img):
         self.last_image = img.to_numpy() if isinstance(img, Field) else np.asarray(img)
 
+    def circles(self, pos, radius=1, color=0xFFFFFF, **_kw):
+        """Headless: the frame's content is the positions drawn (an [N][2] array, or a field of
+        2-vectors read back)."""
+        self.last_image = pos.to_numpy() if isinstance(pos, Field) else np.asarray(pos)
+
     def show(self, *_a):
         self.frames += 1
         _state["frames"] += 1
@@ -212,10 +231,12 @@ class Kernel:
         from . import kernels
         _, q = _device()
         for op in low.ops():
-            if op.kind == "escape_time":
+            if op.kind == "copy":
+                op.field.tensor().buffer.copy_from(q, op.inputs[0].tensor().buffer)
+            elif op.kind == "escape_time":
                 kernels.escape_time(q, kernels.escape_time_params(**op.params), op.field.tensor())
             else:
-                kernels.pixel_program(q, op.program, [f.tensor() for f in op.inputs], op.field.tensor())
+                kernels.pixel_program(q, op.program, [f.grid_tensor() for f in op.inputs], op.field.grid_tensor())
 
 
 def _annotation(node):
@@ -697,9 +718,9 @@ def template():
 # ---- the general path: any struct-for body as a per-pixel register program ---------------------------
 class Lowered:
     """A lowered kernel: kind "escape_time" (field, params for vdsl_op_escape_time),
-    "pixel_program" (field, program for vdsl_op_pixel_program, input fields it reads), or
-    "sequence" (parts: Lowered ops run in order; a kernel of several struct-fors, or a struct-for
-    storing several fields)."""
+    "pixel_program" (field, program for vdsl_op_pixel_program, input fields it reads), "copy"
+    (field = a copy of inputs[0]), or "sequence" (parts: Lowered ops run in order; a kernel of
+    several struct-fors, or a struct-for storing several fields)."""
 
     def __init__(self, kind, field, params=None, program=None, inputs=(), parts=()):
         self.kind, self.field, self.params, self.program, self.inputs = kind, field, params, program, list(inputs)
@@ -709,6 +730,11 @@ class Lowered:
     def ops(self):
         """The escape-time and pixel-program ops this kernel runs, in order."""
         return [o for p in self.parts for o in p.ops()] if self.kind == "sequence" else [self]
+
+    def substitute(self, old, new):
+        """Reads field `new` wherever this program read `old` (same type and shape)."""
+        self.inputs = [new if f is old else f for f in self.inputs]
+        self.reads = [new if f is old else f for f in self.reads]
 
 
 def lower_kernel(fdef: ast.FunctionDef, funcs, env, general: bool = False) -> Lowered:
@@ -766,6 +792,7 @@ class _PixInterp:
         self.pp = pixprog
         self.env, self.funcs, self.b = env, funcs, b
         self.fld, self.iname, self.jname = fld, iname, jname
+        self.names = [iname] if jname is None else [iname, jname]  # a 1-D struct-for binds one index
         self.stored = []  # fields the body stores to at [i, j], in the order of their first store
         self.fields = {}  # id -> Field, for the store keys
         self.shape = fld.shape if isinstance(fld, Field) else None  # the struct-for's index space
@@ -918,12 +945,29 @@ class _PixInterp:
             return self.call(n, local)
         raise TaichiLoweringError(f"expression {ast.dump(n)[:60]} is not supported")
 
+    def _elts(self, idx):
+        """The index expressions of a subscript: field[i, j] of a 2-D struct-for, field[i] of a 1-D one."""
+        elts = list(idx.elts) if isinstance(idx, ast.Tuple) else [idx]
+        if len(elts) != len(self.names):
+            raise TaichiLoweringError(f"fields of this struct-for are {len(self.names)}-D: index them as "
+                                      f"field[{', '.join(self.names)}]")
+        return elts
+
+    def _is_here(self, idx):
+        return [getattr(e, "id", None) for e in self._elts(idx)] == self.names
+
+    def _here(self):
+        """The subscript of this pixel: (i, j), or i."""
+        if len(self.names) == 1:
+            return ast.Name(id=self.iname)
+        return ast.Tuple(elts=[ast.Name(id=self.iname), ast.Name(id=self.jname)])
+
     def field_read(self, fld, idx, local):
         """fld[i, j] (this pixel), or fld[e1, e2] at per-pixel indices (a stencil or gather read,
-        clamped to the field, whose shape must be the struct-for's)."""
-        if not (isinstance(idx, ast.Tuple) and len(idx.elts) == 2):
-            raise TaichiLoweringError("fields are 2-D: read them as field[i, j]")
-        here = [getattr(e, "id", None) for e in idx.elts] == [self.iname, self.jname]
+        clamped to the field, whose shape must be the struct-for's); fld[i] / fld[e] in a 1-D
+        struct-for, which runs as one row (row index 0)."""
+        elts = self._elts(idx)
+        here = self._is_here(idx)
         if here and _skey(fld) in local:
             return local[_skey(fld)]  # the value this pixel stored earlier in the body
         if fld.shape != self.shape:
@@ -937,7 +981,10 @@ class _PixInterp:
             if fld.width == 1:
                 return self.b.load(k)
             return _PVec([self.b.load(k, c) for c in range(fld.width)])
-        row, col = (self.expr(e, local) for e in idx.elts)
+        if len(elts) == 1:
+            row, col = 0.0, self.expr(elts[0], local)
+        else:
+            row, col = (self.expr(e, local) for e in elts)
         if isinstance(row, _PVec) or isinstance(col, _PVec):
             raise TaichiLoweringError("field indices are scalars")
         row, col = self.node(row), self.node(col)
@@ -1211,7 +1258,7 @@ class _PixInterp:
             if _is_skey(nm):  # the field keeps its value where a branch does not store
                 keep = local.get(nm)
                 if keep is None:
-                    keep = self.field_read(self.fields[nm[1]], ast.Tuple(elts=[ast.Name(id=self.iname), ast.Name(id=self.jname)]), {})
+                    keep = self.field_read(self.fields[nm[1]], self._here(), {})
                 vt = keep if vt is _ONE_BRANCH else vt
                 vf = keep if vf is _ONE_BRANCH else vf
             elif vt is _ONE_BRANCH or vf is _ONE_BRANCH or vt is _UNREADABLE or vf is _UNREADABLE:
@@ -1295,14 +1342,18 @@ class _PixInterp:
             tgt = st.target if isinstance(st, ast.AugAssign) else st.targets[0]
             if isinstance(tgt.value, ast.Name) and isinstance(local.get(tgt.value.id), _PVec):
                 return self.component_assign(st, tgt, local)
+        if isinstance(st, ast.AugAssign) and isinstance(st.target, ast.Subscript):
+            # field[i, j] op= v is field[i, j] = field[i, j] op v (the read sees an earlier store)
+            return self.assign(ast.Assign(targets=[st.target], value=ast.BinOp(
+                left=ast.Subscript(value=st.target.value, slice=st.target.slice, ctx=ast.Load()), op=st.op,
+                right=st.value), lineno=getattr(st, "lineno", 0)), local)
         if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Subscript):
             tgt = st.targets[0]
             target = self.expr(tgt.value, local)
             if not (isinstance(target, Field) and target.shape == self.shape):
                 raise TaichiLoweringError("the body may only store to fields of the struct-for's shape")
-            idx = tgt.slice
-            if not (isinstance(idx, ast.Tuple) and [getattr(e, "id", None) for e in idx.elts] == [self.iname, self.jname]):
-                raise TaichiLoweringError("the store must write field[i, j]")
+            if not self._is_here(tgt.slice):
+                raise TaichiLoweringError(f"the store must write field[{', '.join(self.names)}]")
             if self.in_loop:
                 raise TaichiLoweringError("a store inside the loop is not supported (store after it)")
             v = self.expr(st.value, local)
@@ -1373,25 +1424,34 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
     """Lowers one @ti.kernel struct-for body to per-pixel programs (vernondsl_amd.pixprog): one
     program when the body stores one field; when it stores several, one program per stored field
     (each evaluates the whole body and stores its field; the other stores stay local, so a later
-    read of such a field at [i, j] sees the stored value), as a "sequence" ordered so that no
-    program reads a field from memory after another program of the sequence has stored it (Taichi
-    reads the values from before the loop there).  A body whose programs need each other's inputs
-    both ways has no such order: TaichiLoweringError."""
+    read of such a field at [i, j] sees the stored value), as a "sequence" in which no program
+    loads a field from memory after another program of the sequence has stored it (the loads see
+    the values from before the loop, as Taichi's do at [i, j]).  The programs are ordered so that
+    a program loading a field runs before the one storing it; where they load each other's fields
+    (x from v and v from x, as a particle update does), one such field is first copied to a
+    snapshot (Field.snapshot) that the other programs load instead."""
     low, stored = _lower_pixel_one(fdef, funcs, env, None)
     if low is not None:
         return low
     parts = {id(f): _lower_pixel_one(fdef, funcs, env, f)[0] for f in stored}
-    # part T loads field F from memory -> T runs before the part that stores F
-    order, placed = [], set()
-    while len(order) < len(stored):
-        ready = [f for f in stored if id(f) not in placed and
-                 not any(id(g) not in placed and g is not f and f in parts[id(g)].reads for g in stored)]
-        if not ready:
-            raise TaichiLoweringError("the struct-for stores fields that it also reads before storing them, both ways "
-                                      "round: no order of one program per stored field gives Taichi's values")
-        order.append(ready[0])
-        placed.add(id(ready[0]))
-    return Lowered("sequence", stored[0], parts=[parts[id(f)] for f in order])
+
+    def loaded_by_other(f, among):  # some other program still to run loads f
+        return any(g is not f and f in parts[id(g)].reads for g in among)
+
+    order, copies, pending = [], [], list(stored)
+    while pending:
+        ready = [f for f in pending if not loaded_by_other(f, pending)]
+        if ready:
+            order.append(ready[0])
+            pending.remove(ready[0])
+            continue
+        f = next(f for f in pending if loaded_by_other(f, pending))
+        snap = f.snapshot()
+        copies.append(Lowered("copy", snap, inputs=[f]))
+        for g in pending:
+            if g is not f:
+                parts[id(g)].substitute(f, snap)
+    return Lowered("sequence", stored[0], parts=copies + [parts[id(f)] for f in order])
 
 
 def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target):
@@ -1400,29 +1460,38 @@ def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target):
     from . import pixprog as pp
     body = [s for s in fdef.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant))]
     if len(body) != 1 or not isinstance(body[0], ast.For):
-        raise TaichiLoweringError("the kernel body must be one struct-for `for i, j in field:`")
+        raise TaichiLoweringError("the kernel body must be one struct-for `for i, j in field:` (or `for i in field:`)")
     loop = body[0]
-    if not (isinstance(loop.target, ast.Tuple) and len(loop.target.elts) == 2):
-        raise TaichiLoweringError("the struct-for must bind two indices (a 2-D field)")
-    iname, jname = (e.id for e in loop.target.elts)
+    if isinstance(loop.target, ast.Tuple) and len(loop.target.elts) == 2:
+        iname, jname = (e.id for e in loop.target.elts)
+    elif isinstance(loop.target, ast.Name):
+        iname, jname = loop.target.id, None  # a 1-D struct-for
+    else:
+        raise TaichiLoweringError("the struct-for must bind one index (a 1-D field) or two (a 2-D field)")
+    dims = 1 if jname is None else 2
     b = pp.Builder()
     it0 = _PixInterp(env, funcs, b, None, iname, jname)
     it = loop.iter
-    if (isinstance(it, ast.Call) and ((isinstance(it.func, ast.Attribute) and it.func.attr == "ndrange") or
-                                      (isinstance(it.func, ast.Name) and it.func.id == "ndrange"))):
+    fname = it.func.attr if isinstance(it, ast.Call) and isinstance(it.func, ast.Attribute) else \
+        it.func.id if isinstance(it, ast.Call) and isinstance(it.func, ast.Name) else None
+    if fname in ("ndrange", "range"):  # ti.ndrange(W, H) / ti.ndrange(N), or a top-level range(N)
         shape = tuple(it0.expr(a, {}) for a in it.args)
-        if len(shape) != 2 or not all(isinstance(v, (int, np.integer)) and v >= 0 for v in shape):
-            raise TaichiLoweringError("ti.ndrange needs two non-negative integer extents")
+        if (fname == "range" and len(it.args) != 1) or len(shape) != dims or \
+                not all(isinstance(v, (int, np.integer)) and v >= 0 for v in shape):
+            raise TaichiLoweringError(f"the loop needs {dims} non-negative integer extent(s) for its {dims} "
+                                      "index(es): ti.ndrange(W, H), ti.ndrange(N) or range(N)")
         ip = _PixInterp(env, funcs, b, None, iname, jname)
         ip.shape = tuple(int(v) for v in shape)
     else:
         fld = it0.expr(it, {})
-        if not isinstance(fld, Field) or len(fld.shape) != 2:
-            raise TaichiLoweringError("the struct-for must iterate a 2-D ti.field or ti.ndrange(W, H)")
+        if not isinstance(fld, Field) or len(fld.shape) != dims:
+            raise TaichiLoweringError(f"the struct-for binds {dims} index(es): it must iterate a {dims}-D ti.field, "
+                                      "ti.ndrange or range")
         ip = _PixInterp(env, funcs, b, fld, iname, jname)
-    local = {iname: b.index(0), jname: b.index(1)}
+    # a 1-D struct-for runs as one row of the program grid: its index is the column index
+    local = {iname: b.index(0), jname: b.index(1)} if dims == 2 else {iname: b.index(1)}
     shape = ip.shape if ip.shape is not None else ip.fld.shape
-    for nm, ext in zip((iname, jname), shape):
+    for nm, ext in zip(ip.names, shape):
         ip.ibound[id(local[nm])] = max(int(ext) - 1, 0)
     stmts = [s for s in loop.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant)) and not isinstance(s, ast.Pass)]
     init, test, new_state, max_iter, has_loop = {}, None, {}, 0, False
