@@ -326,7 +326,12 @@ typedef enum vdsl_pix_opcode {
   /* Component (int)imm of input a's pixel [row][col], row = index(r[b], ni), col = index(r[c], nj)
    * with index(x, n) = 0 if !(x >= 0), n - 1 if x >= n - 1, else (int)x: a stencil or gather read,
    * clamped to the field (Taichi leaves reads outside a field undefined). */
-  VDSL_PIX_LOAD_AT = 42
+  VDSL_PIX_LOAD_AT = 42,
+  /* r[dst] = float(the loop's trip: the updates made before it, 0 on the first), test and body
+   * sections only.  Every lane still in the loop is on the same trip, so this is the loop
+   * variable of `for k in range(N)` and the counter of a while loop (an index: gathers at it
+   * read one element per wave). */
+  VDSL_PIX_TRIP = 43
 } vdsl_pix_opcode;
 
 typedef enum vdsl_pix_test {

@@ -220,7 +220,7 @@ static float pix_apply(const vdsl_pixel_program* p, const vdsl_map_instr* s, con
     case VDSL_PIX_LOAD_AT:
       return pix_load(p, inputs, s->a, pix_index(reg[s->b], ni) * nj + pix_index(reg[s->c], nj), (int)s->imm);
     case VDSL_PIX_INDEX: return s->a == 0 ? (float)i : (float)j;
-    case VDSL_PIX_COUNT: return (float)count;
+    case VDSL_PIX_COUNT: case VDSL_PIX_TRIP: return (float)count;  /* the trip, in the loop's sections */
     case VDSL_PIX_COS: return cosf(reg[s->a]);
     case VDSL_PIX_SIN: return sinf(reg[s->a]);
     case VDSL_PIX_LT: return reg[s->a] < reg[s->b] ? 1.0f : 0.0f;
@@ -261,9 +261,9 @@ void orc_pixel_program_rows(const vdsl_pixel_program* p, int64_t ni, int64_t nj,
       for (int pc = 0; pc < t0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, 0, ni, nj);
       if (p->loop) {
         while (count < p->max_iter) {
-          for (int pc = t0; pc < b0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, 0, ni, nj);
+          for (int pc = t0; pc < b0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, count, ni, nj);
           if (!pix_test(p->test, reg[p->test_a], reg[p->test_b])) break;
-          for (int pc = b0; pc < q0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, 0, ni, nj);
+          for (int pc = b0; pc < q0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, count, ni, nj);
           ++count;
         }
       }

@@ -136,3 +136,13 @@ def test_semantic_vocabulary_covers_pass_table():
     for s in ("input", "output", "uniform", "uniform_constant", "storage_buffer", "image", "varying"):
         assert s in _lib.SEMANTIC_TO_BINDING
     assert len(set(_lib.SEMANTIC_TO_BINDING.values())) == 7
+
+
+def test_opcode_tables_match_the_header():
+    """pixprog.OP and the map-chain opcodes name the values include/vdsl.h gives them."""
+    from vernondsl_amd import pixprog
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    enum = {m.group(1).lower(): int(m.group(2)) for m in re.finditer(r"VDSL_(?:MAP|PIX)_(\w+)\s*=\s*(\d+)", text)}
+    for name, code in pixprog.OP.items():
+        assert enum.get(name) == code, name
+    assert enum["trip"] == 43 and pixprog.OP["trip"] == 43

@@ -486,3 +486,38 @@ def test_particles_example_one_d_fields_bit_exact(dev, q):
     x, v, _ = particles_numpy(x0, v0, np.zeros(16384, np.float32), 300)
     assert np.array_equal(img, x)
     assert (v[:, 1] > 0).any() and (x[:, 1] >= 0).all()  # some have bounced off the floor
+
+
+def test_loops_reading_their_trip_bit_exact(dev, q):
+    """Runtime loops whose variable is read (the trip, the same on every live lane): prefix sums
+    over 300 trips, a window over range(-40, 41), a while loop whose test reads its counter, and
+    gathers at the trip, on grids of rows and of 16x16 patches (the search loop has a test)."""
+    from test_taichi_general import ROW_LOOPS
+    rng_ = np.random.default_rng(16)
+    u = rng_.random((37, 300)).astype(np.float32)
+    for kernel, args in (("prefix", {}), ("window", {"r": 5}), ("search", {})):
+        low = tc.lower_source_kernel(ROW_LOOPS, kernel, args)
+        got = run_prog(dev, q, low.program, [u], 37, 300)
+        ref = oracle.pixel_program(low.program, 37, 300, [u])
+        assert np.array_equal(got, ref), kernel
+
+
+def test_nbody_example_bit_exact(dev, q):
+    """O(N^2) forces by a 4096-trip loop gathering x[j] at the trip, then the kick-drift update
+    (x's program first: it loads v before v's program stores it): two steps on the device from a
+    random state equal the oracle's from the same state, program by program; the example runs."""
+    from test_taichi_general import lower_named
+    text = open(os.path.join(EX, "nbody.py")).read()
+    rng_ = np.random.default_rng(17)
+    f = {"x": (rng_.random((4096, 2)) * 2 - 1).astype(np.float32), "v": (rng_.random((4096, 2)) - 0.5).astype(np.float32)}
+    for _ in range(2):
+        for kernel in ("forces", "advance"):
+            low, names = lower_named(text, kernel, {})
+            for op in low.ops():
+                src = [f[names[id(g)]].reshape(1, 4096, 2) for g in op.inputs]
+                got = run_prog(dev, q, op.program, src, 1, 4096).reshape(4096, 2)
+                assert np.array_equal(got, oracle.pixel_program(op.program, 1, 4096, src).reshape(4096, 2)), kernel
+                f[names[id(op.field)]] = got
+    assert np.isfinite(f["x"]).all() and not np.array_equal(f["a"], np.zeros_like(f["a"]))
+    res, img = run_program(os.path.join(EX, "nbody.py"), 2)
+    assert res["frames"] == 2 and img.shape == (4096, 2) and np.isfinite(img).all()

@@ -158,9 +158,24 @@ def k():
     assert np.array_equal(got, ref)
 
 
+def test_while_body_reads_its_counter():
+    """x = 0 + 1 + ... + 9 in a while loop whose body reads the counter (the trip)."""
+    text = ("import taichi as ti\nf = ti.field(dtype=float, shape=(8, 8))\n@ti.kernel\ndef k():\n    for i, j in f:\n"
+            "        x = 0.0\n        k = 0\n        while k < 10 and x < i * 4.0:\n            x = x + k\n            k += 1\n"
+            "        f[i, j] = x + k * 0.01\n")
+    low = tc.lower_source_kernel(text, "k", {})
+    got = oracle.pixel_program(low.program, 8, 8)
+    ref = np.zeros((8, 8), np.float32)
+    for i in range(8):
+        x, k = f32(0), 0
+        while k < 10 and x < f32(i) * f32(4.0):
+            x, k = x + f32(k), k + 1
+        ref[i, :] = x + f32(k) * f32(0.01)
+    assert np.array_equal(got, ref) and len(np.unique(ref)) > 4
+
+
 @pytest.mark.parametrize("body,msg", [
     ("        k = 0\n        while k < 10:\n            k += 1\n            k += 1\n        f[i, j] = k", "counter|loop"),
-    ("        x = 0.0\n        k = 0\n        while k < 10:\n            x = x + k\n            k += 1\n        f[i, j] = x", "counter"),
     ("        f[i, j] = 1.0\n        for _ in range(3):\n            x = 2.0", "after the loop"),
     ("        x = 0.0\n        for _ in range(3):\n            for _ in range(2):\n                x = x + 1.0\n        f[i, j] = x", "statement"),
     ("        x = 0.0\n        for _ in range(3):\n            f[i, j] = x", "store inside the loop"),
@@ -688,3 +703,108 @@ def test_particles_example_one_d_vector_fields_and_snapshot():
     x, v, age = particles_numpy(x0, v0, np.zeros(16384, np.float32), 30)
     assert np.array_equal(f["x"], x) and np.array_equal(f["v"], v) and np.array_equal(f["age"], age)
     assert (v0[:, 1] != v[:, 1]).all()
+
+
+ROW_LOOPS = '''import taichi as ti
+W, H = 37, 300
+u = ti.field(dtype=float, shape=(W, H))
+s = ti.field(dtype=float, shape=(W, H))
+c = ti.field(dtype=ti.i32, shape=(W, H))
+
+@ti.kernel
+def prefix():
+    for i, j in s:
+        acc = 0.0
+        for k in range(H):
+            acc += ti.select(k <= j, u[i, k], 0.0)
+        s[i, j] = acc
+
+@ti.kernel
+def window(r: int):
+    for i, j in s:
+        acc = 0.0
+        for k in range(-40, 41):
+            acc += u[i, ti.min(ti.max(j + k, 0), H - 1)] * (1.0 if abs(k) <= r else 0.0)
+        s[i, j] = acc
+
+@ti.kernel
+def search():
+    for i, j in c:
+        k = 0
+        while k < H and u[i, (j + k) % H] < 0.97:
+            k += 1
+        c[i, j] = k
+'''
+
+
+def test_loop_index_read_in_the_body_and_the_test():
+    """The variable of a runtime `for k in range(...)` and the counter of a while loop are the
+    loop's trip: prefix sums by a 300-trip loop, a window by range(-40, 41), a search whose test
+    reads the counter (check-then-update: the count is the first k that fails)."""
+    g = np.random.default_rng(15).random((37, 300)).astype(np.float32)
+    low, names = lower_named(ROW_LOOPS, "prefix", {})
+    assert low.program.loop and low.program.max_iter == 300
+    f = run_ops(low, names, {"u": g})
+    ref = np.zeros_like(g)
+    acc = np.zeros(37, np.float32)
+    for j in range(300):  # the same f32 additions in the same order: acc_j = u[:, 0] + ... + u[:, j]
+        acc = acc + g[:, j]
+        ref[:, j] = acc
+    # each pixel adds u[i, k] for k <= j, then zeros: its sum is the running sum to j, plus +0s
+    assert np.array_equal(f["s"], ref)
+    low, names = lower_named(ROW_LOOPS, "window", {"r": 5})
+    f = run_ops(low, names, {"u": g})
+    ref = np.zeros_like(g)
+    for k in range(-40, 41):
+        ref = ref + g[:, np.clip(np.arange(300) + k, 0, 299)] * (f32(1.0) if abs(k) <= 5 else f32(0.0))
+    assert np.array_equal(f["s"], ref)
+    low, names = lower_named(ROW_LOOPS, "search", {})
+    f = run_ops(low, names, {"u": g})
+    ref = np.full((37, 300), 300, np.int32)
+    for i in range(37):
+        for j in range(300):
+            for k in range(300):
+                if not g[i, (j + k) % 300] < f32(0.97):
+                    ref[i, j] = k
+                    break
+    assert np.array_equal(f["c"], ref) and ref.min() == 0 and 0 < np.median(ref) < 300
+
+
+def test_trip_is_refused_after_the_loop_and_in_initial_values():
+    b = pp.Builder()
+    with pytest.raises(pp.ProgramError, match="trip"):
+        pp.compile_program(b, body={"x": b.op("add", b.state("x"), b.trip())}, init={"x": 0.0}, max_iter=4,
+                           out=b.op("add", b.trip(), 1.0), loop=True)
+    with pytest.raises(pp.ProgramError, match="trip"):
+        pp.compile_program(b, init={"x": b.trip()}, body={"x": b.state("x")}, max_iter=4, out=b.state("x"), loop=True)
+
+
+def nbody_forces_numpy(x, n, soft=0.001):
+    """examples/nbody.py's forces() in numpy f32, the program's operations in its order:
+    acc += d / (r2 sqrt(r2)), r2 = (d0 d0 + d1 d1) + soft, over j in order, then acc / N."""
+    acc = np.zeros_like(x)
+    for j in range(n):
+        d = x[j] - x
+        r2 = (d[:, 0] * d[:, 0] + d[:, 1] * d[:, 1]) + f32(soft)
+        den = r2 * np.sqrt(r2)
+        acc = acc + d / den[:, None]
+    return acc / f32(n)
+
+
+def test_nbody_example_loop_over_all_particles():
+    text = ex("nbody.py").replace("N = 4096", "N = 512")
+    seed, names = lower_named(text, "seed", {})
+    f = run_ops(seed, names, {})
+    forces, fn = lower_named(text, "forces", {})
+    p = forces.program
+    assert p.loop and p.max_iter == 512 and p.test == pp.TESTS["none"]
+    advance, an = lower_named(text, "advance", {})
+    x, v = f["x"], f["v"]
+    for _ in range(3):
+        f = run_ops(forces, fn, {"x": x})
+        a = nbody_forces_numpy(x, 512)
+        assert np.array_equal(f["a"], a)
+        g = run_ops(advance, an, {"x": x, "v": v, "a": a})
+        v = v + a * f32(0.0005)
+        x = x + v * f32(0.0005)
+        assert np.array_equal(g["v"], v) and np.array_equal(g["x"], x)

@@ -48,7 +48,7 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
     const vdsl_map_instr& s = p.code[pc];
     const std::string at = "pixel program: instruction " + std::to_string(pc);
     const bool map_op = s.op >= VDSL_MAP_LOAD && s.op <= VDSL_MAP_ADD_IMM;
-    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_LOAD_AT;
+    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_TRIP;
     if (!map_op && !pix_op) return fail(VDSL_ERR_INVALID_ARG, at + ": unknown opcode " + std::to_string(s.op));
     if (s.dst >= VDSL_PIX_MAX_REGS || s.b >= VDSL_PIX_MAX_REGS || s.c >= VDSL_PIX_MAX_REGS)
       return fail(VDSL_ERR_INVALID_ARG, at + ": register out of range");
@@ -65,6 +65,8 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
       return fail(VDSL_ERR_INVALID_ARG, at + ": register out of range");
     }
     if (s.op == VDSL_PIX_COUNT && pc < post0) return fail(VDSL_ERR_INVALID_ARG, at + ": COUNT outside the post section");
+    if (s.op == VDSL_PIX_TRIP && (pc < p.n_pre || pc >= post0))
+      return fail(VDSL_ERR_INVALID_ARG, at + ": TRIP outside the loop's test and body sections");
   }
   return VDSL_OK;
 }
@@ -96,7 +98,7 @@ int row_mapping(const vdsl_pixel_program& p, int ni) {
 // Registers an instruction reads (a, b, c as the opcode uses them).
 int reads(int op) {
   switch (op) {
-    case VDSL_MAP_LOAD: case VDSL_MAP_CONST: case VDSL_PIX_INDEX: case VDSL_PIX_COUNT: return 0;
+    case VDSL_MAP_LOAD: case VDSL_MAP_CONST: case VDSL_PIX_INDEX: case VDSL_PIX_COUNT: case VDSL_PIX_TRIP: return 0;
     case VDSL_PIX_LOAD_AT: return 6;  // b, c
     case VDSL_MAP_ADD: case VDSL_MAP_SUB: case VDSL_MAP_MUL: case VDSL_MAP_DIV: case VDSL_MAP_MAX: case VDSL_MAP_MIN:
     case VDSL_PIX_LT: case VDSL_PIX_LE: case VDSL_PIX_EQ: case VDSL_PIX_NE: return 3;  // a, b
@@ -106,8 +108,8 @@ int reads(int op) {
 }
 
 // Gathers (LOAD_AT) whose row operand is the same on every lane of a wave in the row mapping, where
-// a wave covers 64 pixels of one row: registers computed only from the row index i (INDEX 0),
-// constants and immediates.  Their row offset is then formed once per wave on the scalar unit.
+// a wave covers 64 pixels of one row: registers computed only from the row index i (INDEX 0), the
+// loop's trip, constants and immediates.  Their row offset is then formed once per wave on the scalar unit.
 // A forward pass over the sections (the loop's to a fixed point, joined with the state before it);
 // loads, the column index and the count make a register vary, conservatively.
 std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
@@ -121,7 +123,7 @@ std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
     const bool in_uni = (!(rd & 1) || st[s.a]) && (!(rd & 2) || st[s.b]) && (!(rd & 4) || st[s.c]);
     if (s.op == VDSL_PIX_LOAD_AT) flag[pc] = st[s.b] ? 1 : 0;
     bool out;
-    if (s.op == VDSL_MAP_CONST) out = true;
+    if (s.op == VDSL_MAP_CONST || s.op == VDSL_PIX_TRIP) out = true;  // the trip is the same on every lane
     else if (s.op == VDSL_PIX_INDEX) out = s.a == 0;
     else if (s.op == VDSL_MAP_LOAD || s.op == VDSL_PIX_LOAD_AT || s.op == VDSL_PIX_COUNT) out = false;
     else out = in_uni;

@@ -96,8 +96,8 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
     r[s.dst] = pix_load<P, s.a>(in, e, static_cast<int>(rt.imm[PC]));
   } else if constexpr (s.op == VDSL_PIX_INDEX) {
     r[s.dst] = s.a == 0 ? fi : fj;
-  } else if constexpr (s.op == VDSL_PIX_COUNT) {
-    r[s.dst] = fcount;
+  } else if constexpr (s.op == VDSL_PIX_COUNT || s.op == VDSL_PIX_TRIP) {
+    r[s.dst] = fcount;  // the count in the post section, the trip in the loop's sections
   } else if constexpr (s.op == VDSL_PIX_COS) {
     r[s.dst] = cosf(r[s.a]);
   } else if constexpr (s.op == VDSL_PIX_SIN) {
@@ -180,6 +180,13 @@ struct PixSets {
   static constexpr uint32_t keep_b = body_w & post_r;   // kept from the lane's last counted trip
   static constexpr bool free_running = (loop_w & post_r) == 0u;
   static constexpr uint32_t carried = rbw(t0, q0) & loop_w;  // the loop's state from trip to trip
+  static constexpr bool reads_trip() {
+    for (int pc = t0; pc < q0; ++pc)
+      if (P::code[pc].op == VDSL_PIX_TRIP) return true;
+    return false;
+  }
+  // a loop that reads its trip is not a function of its state alone: no periodicity exit
+  static constexpr bool periodic = free_running && carried != 0u && !reads_trip();
 };
 
 template <class P, int BASE, int N>
@@ -201,7 +208,7 @@ __device__ __forceinline__ void pix_keep(float (&r)[VDSL_PIX_MAX_REGS], const fl
 // the keep sets hold their values on lanes that are not live.
 template <class P>
 __device__ __forceinline__ void pix_trip(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
-                                         float fi, float fj, int ni, int nj, uint64_t& lk) {
+                                         float fi, float fj, int ni, int nj, uint64_t& lk, float trip) {
   using S = PixSets<P>;
   float old[VDSL_PIX_MAX_REGS];
   if constexpr (S::keep_t != 0u) {
@@ -209,14 +216,14 @@ __device__ __forceinline__ void pix_trip(const PixRt& rt, const PixIn& in, float
     for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) old[k] = r[k];
   }
   const uint64_t start = lk;
-  pix_run<P, S::t0, P::n_test>(rt, in, r, o, fi, fj, 0.0f, ni, nj);
+  pix_run<P, S::t0, P::n_test>(rt, in, r, o, fi, fj, trip, ni, nj);
   pix_keep<S::keep_t>(r, old, start);
   lk &= __builtin_amdgcn_ballot_w64(pix_test<P::test>(r[P::test_a], r[P::test_b]));
   if constexpr (S::keep_b != 0u) {
 #pragma unroll
     for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) old[k] = r[k];
   }
-  pix_run<P, S::b0, P::n_body>(rt, in, r, o, fi, fj, 0.0f, ni, nj);
+  pix_run<P, S::b0, P::n_body>(rt, in, r, o, fi, fj, trip, ni, nj);
   pix_keep<S::keep_b>(r, old, lk);
 }
 
@@ -242,8 +249,9 @@ __device__ __forceinline__ void pixel_eval(const PixRt& rt, const PixIn& in, int
     const int max_iter = rt.max_iter;
     if constexpr (!S::free_running) {
       for (int t = 0; t < max_iter; ++t) {
-        pix_run<P, S::t0, P::n_test>(rt, in, r, o, fi, fj, 0.0f, ni, nj);
-        pix_run<P, S::b0, P::n_body>(rt, in, r, o, fi, fj, 0.0f, ni, nj);
+        const float trip = static_cast<float>(t);
+        pix_run<P, S::t0, P::n_test>(rt, in, r, o, fi, fj, trip, ni, nj);
+        pix_run<P, S::b0, P::n_body>(rt, in, r, o, fi, fj, trip, ni, nj);
       }
     }
     count = max_iter;
@@ -260,12 +268,12 @@ __device__ __forceinline__ void pixel_eval(const PixRt& rt, const PixIn& in, int
       uint64_t lk = live;
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        pix_trip<P>(rt, in, r, o, fi, fj, ni, nj, lk);
+        pix_trip<P>(rt, in, r, o, fi, fj, ni, nj, lk, static_cast<float>(t + u));
         m[u] = lk;
       }
       count += block_trips16(m, live);
       live = lk;
-      if constexpr (S::free_running && S::carried != 0u) {
+      if constexpr (S::periodic) {
         uint64_t same = live;
 #pragma unroll
         for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k)
@@ -283,7 +291,7 @@ __device__ __forceinline__ void pixel_eval(const PixRt& rt, const PixIn& in, int
     }
     if (t > max_iter - kUnroll && live != 0ull) {
       for (; t < max_iter; ++t) {  // the last max_iter % 16 trips, counted one by one
-        pix_trip<P>(rt, in, r, o, fi, fj, ni, nj, live);
+        pix_trip<P>(rt, in, r, o, fi, fj, ni, nj, live, static_cast<float>(t));
         count += lane_select(live, 1, 0);
       }
     }

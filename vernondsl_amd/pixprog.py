@@ -26,7 +26,7 @@ from . import _lib
 MAX_INSTR, MAX_REGS, MAX_INPUTS = 128, 32, 4
 OP = dict(_lib.MAP_OPS)
 OP.update({"index": 32, "cos": 33, "sin": 34, "count": 35, "lt": 36, "le": 37, "eq": 38, "ne": 39, "select": 40,
-           "floor": 41, "load_at": 42})
+           "floor": 41, "load_at": 42, "trip": 43})
 TESTS = {"none": 0, "lt": 1, "le": 2, "gt": 3, "ge": 4}
 OUT_REG, OUT_COUNT, OUT_I32 = 0, 1, 2
 F32, I32 = _lib.F32, _lib.I32  # input dtypes (vdsl_dtype)
@@ -59,8 +59,8 @@ class Node:
             return repr(float(self.val))
         if self.kind in ("index", "load", "state"):
             return f"{self.kind}({self.val})"
-        if self.kind == "count":
-            return "count"
+        if self.kind in ("count", "trip"):
+            return self.kind
         return f"{self.kind}({', '.join(map(repr, self.args))})"
 
 
@@ -77,7 +77,7 @@ class Builder:
             n = Node()
             n.kind, n.args, n.val, n.key = kind, tuple(args), val, key
             deps = set()
-            if kind in ("state", "count"):
+            if kind in ("state", "count", "trip"):
                 deps.add(kind)
             for a in args:
                 deps |= a.deps
@@ -112,6 +112,11 @@ class Builder:
 
     def count(self) -> Node:
         return self._node("count")
+
+    def trip(self) -> Node:
+        """The loop's trip (updates made before it, as a float): the same on every lane still in
+        the loop; the test and the body may read it."""
+        return self._node("trip")
 
     def op(self, kind: str, *args) -> Node:
         args = tuple(a if isinstance(a, Node) else self.const(a) for a in args)
@@ -209,6 +214,8 @@ class _Emitter:
             op, a, b, c, imm = OP["load_at"], n.val[0], srcs[0], srcs[1], float(n.val[1])
         elif k == "count":
             op = OP["count"]
+        elif k == "trip":
+            op = OP["trip"]
         elif k == "state":
             raise ProgramError(f"state {n.val!r} read outside the loop's registers")
         elif k in ("add", "mul") and n.args[1].kind == "const" and n.args[1] not in self.pinned:
@@ -267,7 +274,9 @@ def compile_program(b: Builder, init: dict | None = None, test=None, body: dict 
             raise ProgramError("the loop count can only be read after the loop")
     for n in init_nodes:
         if n.deps:
-            raise ProgramError("an initial value reads loop state or the count")
+            raise ProgramError("an initial value reads loop state, the trip or the count")
+    if any("trip" in n.deps for n in outs):
+        raise ProgramError("the trip can only be read inside the loop")
     if not loop and (out is COUNT or any("count" in n.deps for n in outs)):
         raise ProgramError("the count needs a loop")
     # Registers pinned for the whole program: one per state, then each maximal loop-invariant

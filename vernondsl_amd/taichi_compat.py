@@ -28,7 +28,8 @@ Bodies of any other shape are lowered by the general path to a per-pixel registe
 (vernondsl_amd.pixprog, run by vdsl_op_pixel_program, compiled at run time for the program): any
 expression of the pixel indices, scalar kernel arguments, other 2-D f32 fields read at [i, j]
 and constants, with at most one loop - a `while <test> and <counter> < MAX:` check-then-update
-loop whose body ends with `counter += 1`, or a `for _ in range(N):` loop - and stores
+loop whose body ends with `counter += 1`, or a `for k in range(N)` / `range(A, B)` loop, whose
+test and body may read the counter or k (the loop's trip) - and stores
 `F[i, j] = <value>` (an i32 field stores the loop counter) into one or more fields of the loop's
 shape: a body storing several fields becomes one program per stored field, run in an order in
 which no program loads a field that an earlier one stored (a snapshot copy where the programs
@@ -1551,14 +1552,16 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
     """One loop of the body: (initial states, test, new states, max_iter); rebinds `local` to the
     values after the loop (states, and the counter as the loop's count)."""
     from . import pixprog as pp
-    counter = None
+    counter, first = None, 0
     if isinstance(st, ast.For):
         it = st.iter
-        if not (isinstance(it, ast.Call) and isinstance(it.func, ast.Name) and it.func.id == "range" and len(it.args) == 1):
-            raise TaichiLoweringError("the inner loop must be `for _ in range(N)` or a while loop")
-        max_iter = ip.expr(it.args[0], local)
-        if not isinstance(max_iter, (int, np.integer)) or max_iter < 0:
-            raise TaichiLoweringError("range(N) needs a non-negative integer constant N")
+        if not (isinstance(it, ast.Call) and isinstance(it.func, ast.Name) and it.func.id == "range" and len(it.args) in (1, 2)):
+            raise TaichiLoweringError("the inner loop must be `for k in range(N)`, `for k in range(A, B)` or a while loop")
+        bounds = [ip.expr(a, local) for a in it.args]
+        if not all(isinstance(v, (int, np.integer)) for v in bounds):
+            raise TaichiLoweringError("range(...) of a loop needs integer constants")
+        first = int(bounds[0]) if len(bounds) == 2 else 0
+        max_iter = max(int(bounds[-1]) - first, 0)
         loop_var = st.target.id if isinstance(st.target, ast.Name) else None
         loop_body = list(st.body)
         test = None
@@ -1592,13 +1595,22 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
         max_iter = max(0, max_iter)
     # loop-carried state: names assigned in the body that exist before the loop
     assigned = _assigned_names(loop_body)
+    for nm in (counter, loop_var):
+        if nm is not None and nm in assigned:
+            raise TaichiLoweringError(f"the loop variable {nm!r} is assigned in the loop: the counter of a while loop "
+                                      "changes only by its final `+= 1`, a range loop's variable not at all")
     state = [nm for nm in assigned if nm in local and nm != counter]
     init, names = {}, {}
     body_local = dict(local)
+    # inside the loop the counter of a while loop and the variable of `for k in range(N)` are the
+    # loop's trip (the same on every lane still in the loop), exact while N - 1 <= 2^24
+    trip = b.trip() if max_iter - 1 <= _PixInterp._INT_EXACT else _UNREADABLE
+    if trip is not _UNREADABLE:
+        ip.ibound[id(trip)] = max(int(max_iter) - 1, 0)
     if counter is not None:
-        body_local[counter] = _UNREADABLE
+        body_local[counter] = trip
     if loop_var is not None:
-        body_local[loop_var] = _UNREADABLE
+        body_local[loop_var] = trip if (trip is _UNREADABLE or first == 0) else ip.arith("add", trip, first)
     for nm in state:
         v = local[nm]
         if isinstance(v, _PVec):
