@@ -177,7 +177,7 @@ def test_while_body_reads_its_counter():
 @pytest.mark.parametrize("body,msg", [
     ("        k = 0\n        while k < 10:\n            k += 1\n            k += 1\n        f[i, j] = k", "counter|loop"),
     ("        f[i, j] = 1.0\n        for _ in range(3):\n            x = 2.0", "after the loop"),
-    ("        x = 0.0\n        for _ in range(3):\n            for _ in range(2):\n                x = x + 1.0\n        f[i, j] = x", "statement"),
+    ("        x = 0.0\n        for _ in range(3):\n            y = 1.0\n            for _ in range(2):\n                x = x + y\n        f[i, j] = x", "statement"),
     ("        x = 0.0\n        for _ in range(3):\n            f[i, j] = x", "store inside the loop"),
     ("        f[i, j] = i << 3", "LShift"),
     ("        if i > j:\n            y = 1.0\n        f[i, j] = y", "one branch"),
@@ -808,3 +808,67 @@ def test_nbody_example_loop_over_all_particles():
         v = v + a * f32(0.0005)
         x = x + v * f32(0.0005)
         assert np.array_equal(g["v"], v) and np.array_equal(g["x"], x)
+
+
+NESTS = '''import taichi as ti
+W, H, R = 40, 56, 20
+u = ti.field(dtype=float, shape=(W, H))
+s = ti.field(dtype=float, shape=(W, H))
+
+@ti.kernel
+def count3():
+    for i, j in s:
+        x = 0.0
+        for _ in range(3):
+            for _ in range(2):
+                x = x + 1.0
+        s[i, j] = x
+
+@ti.kernel
+def window():
+    for i, j in s:
+        acc = 0.0
+        for di in range(-R, R + 1):
+            for dj in range(-R, R + 1):
+                w = 1.0 / (1.0 + di * di + dj * dj)
+                acc += w * u[ti.min(ti.max(i + di, 0), W - 1), ti.min(ti.max(j + dj, 0), H - 1)]
+        s[i, j] = acc
+
+@ti.kernel
+def triple():
+    for i, j in s:
+        acc = 0.0
+        for a in range(2, 5):
+            for b in range(7):
+                for c in range(-3, 2):
+                    acc += a * 100.0 + b * 10.0 + c + u[i, j] * 0.0
+        s[i, j] = acc
+'''
+
+
+def test_perfect_nests_of_range_loops_run_as_one_loop():
+    """Nested range loops become one loop over the product of their extents, each variable
+    recovered from the trip (innermost fastest, exact integer // and %): the counting nest, a
+    41 x 41 window (too large to unroll) against numpy in the same order, a triple nest."""
+    g = np.random.default_rng(18).random((40, 56)).astype(np.float32)
+    low, names = lower_named(NESTS, "count3", {})
+    assert low.program.max_iter == 6
+    assert np.array_equal(run_ops(low, names, {"u": g})["s"], np.full((40, 56), 6.0, np.float32))
+    low, names = lower_named(NESTS, "window", {})
+    assert low.program.max_iter == 41 * 41
+    got = run_ops(low, names, {"u": g})["s"]
+    ref = np.zeros_like(g)
+    ii, jj = np.meshgrid(np.arange(40), np.arange(56), indexing="ij")
+    for di in range(-20, 21):
+        for dj in range(-20, 21):
+            w = f32(1.0) / ((f32(1.0) + f32(di * di)) + f32(dj * dj))
+            ref = ref + w * g[np.clip(ii + di, 0, 39), np.clip(jj + dj, 0, 55)]
+    assert np.array_equal(got, ref)
+    low, names = lower_named(NESTS, "triple", {})
+    got = run_ops(low, names, {"u": g})["s"]
+    acc = f32(0)
+    for a in range(2, 5):
+        for b in range(7):
+            for c in range(-3, 2):
+                acc = acc + (((f32(a) * f32(100.0)) + f32(b) * f32(10.0)) + f32(c) + f32(0.0))
+    assert np.array_equal(got, np.full((40, 56), acc, np.float32))

@@ -28,8 +28,9 @@ Bodies of any other shape are lowered by the general path to a per-pixel registe
 (vernondsl_amd.pixprog, run by vdsl_op_pixel_program, compiled at run time for the program): any
 expression of the pixel indices, scalar kernel arguments, other 2-D f32 fields read at [i, j]
 and constants, with at most one loop - a `while <test> and <counter> < MAX:` check-then-update
-loop whose body ends with `counter += 1`, or a `for k in range(N)` / `range(A, B)` loop, whose
-test and body may read the counter or k (the loop's trip) - and stores
+loop whose body ends with `counter += 1`, or a `for k in range(N)` / `range(A, B)` loop (a
+perfect nest of them runs as one loop over its trips), whose test and body may read the counter
+or k (from the loop's trip) - and stores
 `F[i, j] = <value>` (an i32 field stores the loop counter) into one or more fields of the loop's
 shape: a body storing several fields becomes one program per stored field, run in an order in
 which no program loads a field that an earlier one stored (a snapshot copy where the programs
@@ -1276,10 +1277,13 @@ class _PixInterp:
         if not (isinstance(it, ast.Call) and len(it.args) == 1 and
                 ((isinstance(it.func, ast.Attribute) and it.func.attr == "static") or
                  (isinstance(it.func, ast.Name) and it.func.id == "static"))):
-            # `for k in range(N)` whose body reads k (a component index, say): unrolled as well,
-            # which runs the same statements in the same order; N is bounded by the program size
+            # `for k in range(N)` whose body reads k (a component index, say) and holds no other
+            # loop: unrolled as well, which runs the same statements in the same order; N is
+            # bounded by the program size.  A loop around another loop stays a loop (a nest of
+            # range loops runs as one loop over its trips), so nests do not multiply the program.
             if (isinstance(it, ast.Call) and isinstance(it.func, ast.Name) and it.func.id == "range"
                     and isinstance(st.target, ast.Name)
+                    and not any(isinstance(nd, (ast.For, ast.While)) for s2 in st.body for nd in ast.walk(s2))
                     and any(isinstance(nd, ast.Name) and nd.id == st.target.id and isinstance(nd.ctx, ast.Load)
                             for s2 in st.body for nd in ast.walk(s2))):
                 bounds = [self.expr(a, local) for a in it.args]
@@ -1548,22 +1552,50 @@ def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target):
     return low, ip.stored
 
 
+def _is_range(it) -> bool:
+    return (isinstance(it, ast.Call) and isinstance(it.func, ast.Name) and it.func.id == "range"
+            and len(it.args) in (1, 2))
+
+
+def _range_bounds(it, ip, local):
+    """(first, end) of range(N) / range(A, B) with integer constant arguments, else None."""
+    try:
+        vals = [ip.expr(a, local) for a in it.args]
+    except TaichiLoweringError:
+        return None
+    if not all(isinstance(v, (int, np.integer)) and not isinstance(v, bool) for v in vals):
+        return None
+    return (int(vals[0]), int(vals[1])) if len(vals) == 2 else (0, int(vals[0]))
+
+
 def _lower_loop(st, ip: _PixInterp, local: dict, b):
     """One loop of the body: (initial states, test, new states, max_iter); rebinds `local` to the
     values after the loop (states, and the counter as the loop's count)."""
     from . import pixprog as pp
-    counter, first = None, 0
+    counter, nest = None, []
     if isinstance(st, ast.For):
-        it = st.iter
-        if not (isinstance(it, ast.Call) and isinstance(it.func, ast.Name) and it.func.id == "range" and len(it.args) in (1, 2)):
-            raise TaichiLoweringError("the inner loop must be `for k in range(N)`, `for k in range(A, B)` or a while loop")
-        bounds = [ip.expr(a, local) for a in it.args]
-        if not all(isinstance(v, (int, np.integer)) for v in bounds):
-            raise TaichiLoweringError("range(...) of a loop needs integer constants")
-        first = int(bounds[0]) if len(bounds) == 2 else 0
-        max_iter = max(int(bounds[-1]) - first, 0)
-        loop_var = st.target.id if isinstance(st.target, ast.Name) else None
-        loop_body = list(st.body)
+        # a perfect nest of range loops (each body is just the next loop) runs as one loop over
+        # the product of the extents, its variables recovered from the trip, the innermost fastest
+        loops = [st]
+        while True:
+            inner = [s for s in loops[-1].body
+                     if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant)) and not isinstance(s, ast.Pass)]
+            if not (len(inner) == 1 and isinstance(inner[0], ast.For) and _is_range(inner[0].iter)
+                    and _range_bounds(inner[0].iter, ip, local) is not None
+                    and ip.static_values(inner[0], local) is None):
+                break
+            loops.append(inner[0])
+        for lp in loops:
+            if not _is_range(lp.iter):
+                raise TaichiLoweringError("the inner loop must be `for k in range(N)`, `for k in range(A, B)` or a while loop")
+            bounds = _range_bounds(lp.iter, ip, local)
+            if bounds is None:
+                raise TaichiLoweringError("range(...) of a loop needs integer constants")
+            nest.append((lp.target.id if isinstance(lp.target, ast.Name) else None, bounds[0], max(bounds[1] - bounds[0], 0)))
+        max_iter = 1
+        for _, _, ext in nest:
+            max_iter *= ext
+        loop_body = list(loops[-1].body)
         test = None
     else:
         tests = st.test.values if isinstance(st.test, ast.BoolOp) and isinstance(st.test.op, ast.And) else [st.test]
@@ -1591,11 +1623,10 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
         if max_iter is None:
             raise TaichiLoweringError("the while condition needs a bound `counter < MAX`")
         test = test_cmp or None
-        loop_var = None
         max_iter = max(0, max_iter)
     # loop-carried state: names assigned in the body that exist before the loop
     assigned = _assigned_names(loop_body)
-    for nm in (counter, loop_var):
+    for nm in [counter] + [v for v, _, _ in nest]:
         if nm is not None and nm in assigned:
             raise TaichiLoweringError(f"the loop variable {nm!r} is assigned in the loop: the counter of a while loop "
                                       "changes only by its final `+= 1`, a range loop's variable not at all")
@@ -1609,8 +1640,18 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
         ip.ibound[id(trip)] = max(int(max_iter) - 1, 0)
     if counter is not None:
         body_local[counter] = trip
-    if loop_var is not None:
-        body_local[loop_var] = trip if (trip is _UNREADABLE or first == 0) else ip.arith("add", trip, first)
+    rest = trip  # the trips of the loops not yet given their variables
+    for k in range(len(nest) - 1, -1, -1):
+        nm, first, ext = nest[k]
+        if trip is _UNREADABLE:
+            idx = _UNREADABLE
+        elif k == 0:
+            idx = rest
+        else:
+            idx = ip.floor_op(True, rest, ext)
+            rest = ip.floor_op(False, rest, ext)
+        if nm is not None:
+            body_local[nm] = idx if (idx is _UNREADABLE or first == 0) else ip.arith("add", idx, first)
     for nm in state:
         v = local[nm]
         if isinstance(v, _PVec):
