@@ -7,6 +7,7 @@
 // here: the body is a register program (include/vdsl.h), compiled once per program and device into
 // straight-line code around the same check-then-update loop.
 
+#include <algorithm>
 #include <cstdlib>
 #include <string>
 #include <vector>
@@ -91,7 +92,9 @@ int rows_per_block(const vdsl_pixel_program& p) {
 // escape loop), while the row count fits the grid's y extent; 16x16 patches otherwise.  0 for
 // the patches.
 int row_mapping(const vdsl_pixel_program& p, int ni) {
-  const int rows = rows_per_block(p);
+  // never more rows per block than the grid has: a 1-D field is a grid of one row, whose blocks
+  // would otherwise run their loops for rows that do not exist
+  const int rows = std::min(rows_per_block(p), std::max(ni, 1));
   return !(p.loop && p.test != VDSL_PIX_TEST_NONE) && (ni + rows - 1) / rows <= 65535 ? rows : 0;
 }
 
@@ -107,9 +110,10 @@ int reads(int op) {
   }
 }
 
-// Gathers (LOAD_AT) whose row operand is the same on every lane of a wave in the row mapping, where
-// a wave covers 64 pixels of one row: registers computed only from the row index i (INDEX 0), the
-// loop's trip, constants and immediates.  Their row offset is then formed once per wave on the scalar unit.
+// Gathers (LOAD_AT) whose row operand (bit 0 of the flag) or column operand (bit 1) is the same on
+// every lane of a wave in the row mapping, where a wave covers 64 pixels of one row and every lane
+// makes every trip of a loop (the mapping has no escape loops): registers computed only from the
+// row index i (INDEX 0), the loop's trip, constants and immediates.  Their row offset is then formed once per wave on the scalar unit.
 // A forward pass over the sections (the loop's to a fixed point, joined with the state before it);
 // loads, the column index and the count make a register vary, conservatively.
 std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
@@ -121,7 +125,7 @@ std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
     const vdsl_map_instr& s = p.code[pc];
     const int rd = reads(s.op);
     const bool in_uni = (!(rd & 1) || st[s.a]) && (!(rd & 2) || st[s.b]) && (!(rd & 4) || st[s.c]);
-    if (s.op == VDSL_PIX_LOAD_AT) flag[pc] = st[s.b] ? 1 : 0;
+    if (s.op == VDSL_PIX_LOAD_AT) flag[pc] = static_cast<char>((st[s.b] ? 1 : 0) | (st[s.c] ? 2 : 0));
     bool out;
     if (s.op == VDSL_MAP_CONST || s.op == VDSL_PIX_TRIP) out = true;  // the trip is the same on every lane
     else if (s.op == VDSL_PIX_INDEX) out = s.a == 0;
@@ -182,14 +186,15 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni, in
   list("out_regs", p.out_regs, p.out_width, 0);
   list("in_widths", p.in_widths, n_inputs, 1);
   list("in_dtypes", p.in_dtypes, n_inputs, VDSL_F32);
-  // ext[0] of a gather: 1 when its row operand is wave-uniform in the row mapping
+  // ext[0] / ext[1] of a gather: 1 when its row / column operand is wave-uniform in the row mapping
   const std::vector<char> ru = row_uniform_gathers(p);
   s += "  static constexpr vdsl_map_instr code[VDSL_PIX_MAX_INSTR] = {\n";
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   for (int pc = 0; pc < total; ++pc) {
     const vdsl_map_instr& k = p.code[pc];
     s += "    {" + std::to_string(k.op) + ", " + std::to_string(k.dst) + ", " + std::to_string(k.a) + ", " + std::to_string(k.b) +
-         ", " + std::to_string(k.c) + ", {" + std::to_string(ru[pc]) + ", 0, 0}, 0.f},\n";
+         ", " + std::to_string(k.c) + ", {" + std::to_string(ru[pc] & 1) + ", " + std::to_string((ru[pc] >> 1) & 1) +
+         ", 0}, 0.f},\n";
   }
   s += "  };\n};\n}  // namespace vdsl\n";
   s += "extern \"C\" __global__ __launch_bounds__(256) void vdsl_pix_jit(vdsl::PixRt rt, vdsl::PixIn in, void* out, int ni, "

@@ -88,11 +88,13 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
   if constexpr (s.op == VDSL_MAP_LOAD) {
     r[s.dst] = pix_load<P, s.a>(in, o, s.c);
   } else if constexpr (s.op == VDSL_PIX_LOAD_AT) {
-    unsigned ri = pix_index(r[s.b], ni);
-    // a row operand the host found wave-uniform (ext[0]; the row mapping puts one row in each
-    // wave): its offset is formed once per wave on the scalar unit
+    unsigned ri = pix_index(r[s.b], ni), ci = pix_index(r[s.c], nj);
+    // a row / column operand the host found wave-uniform (ext[0] / ext[1]; the row mapping puts
+    // one row in each wave and runs no escape loops): its index is taken once per wave, into a
+    // scalar register
     if constexpr (P::rows > 0 && s.ext[0] != 0) ri = __builtin_amdgcn_readfirstlane(ri);
-    const PixOff<P> e = static_cast<PixOff<P>>(ri) * static_cast<unsigned>(nj) + pix_index(r[s.c], nj);
+    if constexpr (P::rows > 0 && s.ext[1] != 0) ci = __builtin_amdgcn_readfirstlane(ci);
+    const PixOff<P> e = static_cast<PixOff<P>>(ri) * static_cast<unsigned>(nj) + ci;
     r[s.dst] = pix_load<P, s.a>(in, e, static_cast<int>(rt.imm[PC]));
   } else if constexpr (s.op == VDSL_PIX_INDEX) {
     r[s.dst] = s.a == 0 ? fi : fj;
@@ -248,7 +250,18 @@ __device__ __forceinline__ void pixel_eval(const PixRt& rt, const PixIn& in, int
     // what they compute.
     const int max_iter = rt.max_iter;
     if constexpr (!S::free_running) {
-      for (int t = 0; t < max_iter; ++t) {
+      // four trips per iteration: loads that depend only on the trip (gathers at it) can be
+      // issued for all four before the arithmetic of the first
+      int t = 0;
+      for (; t + 4 <= max_iter; t += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float trip = static_cast<float>(t + u);
+          pix_run<P, S::t0, P::n_test>(rt, in, r, o, fi, fj, trip, ni, nj);
+          pix_run<P, S::b0, P::n_body>(rt, in, r, o, fi, fj, trip, ni, nj);
+        }
+      }
+      for (; t < max_iter; ++t) {
         const float trip = static_cast<float>(t);
         pix_run<P, S::t0, P::n_test>(rt, in, r, o, fi, fj, trip, ni, nj);
         pix_run<P, S::b0, P::n_body>(rt, in, r, o, fi, fj, trip, ni, nj);
@@ -350,7 +363,10 @@ __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, voi
     const int j = static_cast<int>((T % gridDim.x) * 256 + threadIdx.x);
     const int i0 = static_cast<int>(T / gridDim.x) * P::rows;
 #pragma unroll
-    for (int t = 0; t < P::rows; ++t) pixel_eval<P>(rt, in, ni, nj, i0 + t, j, res[t], count[t]);
+    for (int t = 0; t < P::rows; ++t) {
+      if (i0 + t >= ni) break;  // the last band's rows past the grid (the same for the whole block)
+      pixel_eval<P>(rt, in, ni, nj, i0 + t, j, res[t], count[t]);
+    }
 #pragma unroll
     for (int t = 0; t < P::rows; ++t) pixel_store<P>(out, ni, nj, i0 + t, j, res[t], count[t]);
   } else {
