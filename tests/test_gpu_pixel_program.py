@@ -532,3 +532,76 @@ def test_nested_range_loops_bit_exact(dev, q):
         low = tc.lower_source_kernel(NESTS, kernel, {})
         got = run_prog(dev, q, low.program, [u][:len(low.inputs)], 40, 56)
         assert np.array_equal(got, oracle.pixel_program(low.program, 40, 56, [u][:len(low.inputs)])), kernel
+
+
+# ---- seeded random programs against the oracle -----------------------------------------------------
+EXACT_UNARY = ("neg", "abs", "sqrt", "floor", "square")
+EXACT_BINARY = ("add", "sub", "mul", "div", "max", "min", "lt", "le", "eq", "ne")
+
+
+def random_program(seed):
+    """A random program of exactly rounded operations: pixel indices, constants, loads and clamped
+    gathers of one or two inputs of 1-2 components, selects; half of them with a loop (with or
+    without a test) over two states that reads the trip and gathers at state-derived indices,
+    the output reading the states and the count."""
+    r = np.random.default_rng(seed)
+    b = pp.Builder()
+    widths = [int(r.integers(1, 3)) for _ in range(int(r.integers(1, 3)))]
+    pool = [b.index(0), b.index(1), b.const(float(np.float32(r.uniform(-3, 3))))]
+    pool += [b.load(k, int(r.integers(0, w))) for k, w in enumerate(widths)]
+
+    def grow(pool, n, extra=()):
+        vals = list(pool) + list(extra)
+        for _ in range(n):
+            pick = lambda: vals[int(r.integers(len(vals)))]
+            u = r.random()
+            if u < 0.25:
+                v = b.op(EXACT_UNARY[int(r.integers(len(EXACT_UNARY)))], pick())
+            elif u < 0.8:
+                v = b.op(EXACT_BINARY[int(r.integers(len(EXACT_BINARY)))], pick(), pick())
+            elif u < 0.9:
+                v = b.op("select", pick(), pick(), pick())
+            else:
+                k = int(r.integers(len(widths)))
+                v = b.load_at(k, b.op("mul", pick(), 3.0), pick(), int(r.integers(0, widths[k])))
+            vals.append(v)
+        return vals
+
+    vals = grow(pool, int(r.integers(3, 9)))
+    if r.random() < 0.5:
+        return pp.compile_program(b, out=vals[-1], in_widths=widths), widths
+    x, y = b.state("x"), b.state("y")
+    body = grow([x, y, b.trip()], int(r.integers(3, 8)), extra=vals[:4])
+    test = None
+    if r.random() < 0.6:
+        test = (("lt", "le", "gt", "ge")[int(r.integers(4))], body[int(r.integers(3, len(body)))], 4.0)
+    out = b.op("add", b.op("mul", x, 0.5), b.op("sub", y, b.op("mul", b.count(), 0.125)))
+    prog = pp.compile_program(b, init={"x": vals[-1], "y": vals[int(r.integers(len(vals)))]}, test=test,
+                              body={"x": body[-1], "y": body[int(r.integers(2, len(body)))]},
+                              max_iter=int(r.integers(0, 40)), out=out, loop=True, in_widths=widths)
+    return prog, widths
+
+
+def same_values(a, b):
+    """The same bits wherever the oracle has a number (signed zeros included), NaN where it has NaN."""
+    nan = np.isnan(b)
+    return bool(np.array_equal(np.isnan(a), nan) and np.array_equal(a.view(np.uint32)[~nan], b.view(np.uint32)[~nan]))
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_programs_bit_exact(dev, q, seed):
+    """Seeded random programs (every exactly rounded opcode, gathers, loops with and without a
+    test, the trip, the count) on a grid of 16x16 patches and on row grids, against the oracle:
+    the same bits (NaN where the oracle has NaN)."""
+    try:
+        prog, widths = random_program(seed)
+    except pp.ProgramError:
+        pytest.skip("the random program does not fit the device form")
+    rng_ = np.random.default_rng(1000 + seed)
+    for ni, nj in ((37, 53), (1, 300), (9, 260)):
+        ins = [np.where(rng_.random((ni, nj, w)) < 0.05, np.float32(np.nan),
+                        rng_.standard_normal((ni, nj, w)) * 4).astype(np.float32).reshape((ni, nj) if w == 1 else (ni, nj, w))
+               for w in widths]
+        got = run_prog(dev, q, prog, ins, ni, nj)
+        ref = oracle.pixel_program(prog, ni, nj, ins)
+        assert same_values(got, ref), (seed, ni, nj, pp.describe(prog))
