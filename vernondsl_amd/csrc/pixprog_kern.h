@@ -364,7 +364,11 @@ __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, voi
     const int i0 = static_cast<int>(T / gridDim.x) * P::rows;
 #pragma unroll
     for (int t = 0; t < P::rows; ++t) {
-      if (i0 + t >= ni) break;  // the last band's rows past the grid (the same for the whole block)
+      // a loop is not run for the last band's rows past the grid (the same for the whole block);
+      // a program without one evaluates them unconditionally, so the loads of all its rows are
+      // issued together (a branch between them would order them)
+      if constexpr (P::loop)
+        if (i0 + t >= ni) break;
       pixel_eval<P>(rt, in, ni, nj, i0 + t, j, res[t], count[t]);
     }
 #pragma unroll
