@@ -872,3 +872,35 @@ def test_perfect_nests_of_range_loops_run_as_one_loop():
             for c in range(-3, 2):
                 acc = acc + (((f32(a) * f32(100.0)) + f32(b) * f32(10.0)) + f32(c) + f32(0.0))
     assert np.array_equal(got, np.full((40, 56), acc, np.float32))
+
+
+CACHED_F = tc.field(dtype=float, shape=(8, 8))
+CACHED_SCALE = 2.0
+
+
+@tc.kernel
+def _cached_kernel(a: float):
+    for i, j in CACHED_F:
+        CACHED_F[i, j] = i * a + CACHED_SCALE
+
+
+def test_kernel_lowerings_are_cached_per_argument_values():
+    """A kernel is lowered once per argument tuple (the last 64 kept); module-level values are
+    taken at that first lowering, as Taichi takes Python globals as compile-time constants."""
+    global CACHED_SCALE
+    k = _cached_kernel
+    first = k.lower(1.5)
+    assert k.lower(1.5) is first and k.lower(2.5) is not first
+    assert k.lower(1) is k.lower(1.0)  # an int argument to a float parameter is coerced first
+    CACHED_SCALE = 5.0
+    try:
+        assert k.lower(1.5) is first
+        fresh = k.lower(3.5)
+        got = oracle.pixel_program(fresh.program, 8, 8)
+        i, _ = grid(8, 8)
+        assert np.array_equal(got, i * f32(3.5) + f32(5.0))
+    finally:
+        CACHED_SCALE = 2.0
+    for v in range(70):
+        k.lower(float(v) + 0.25)
+    assert len(k._cache) == tc.Kernel.CACHE_SIZE and k.lower(1.5) is not first

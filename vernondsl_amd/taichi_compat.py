@@ -45,6 +45,7 @@ when the product is subnormal).
 from __future__ import annotations
 
 import ast
+import collections
 import inspect
 import math as _pymath
 import textwrap
@@ -221,12 +222,32 @@ class Kernel:
         self.fdef = next(n for n in mod.body if isinstance(n, ast.FunctionDef))
         self.arg_names = [a.arg for a in self.fdef.args.args]
         self.arg_types = [_annotation(a.annotation) for a in self.fdef.args.args]
+        self._cache = collections.OrderedDict()  # argument values -> Lowered, most recent last
+
+    CACHE_SIZE = 64
 
     def lower(self, *args) -> "Lowered":
+        """The kernel lowered for these argument values, from a per-kernel cache of the last
+        CACHE_SIZE argument tuples.  Module-level values the body reads are taken at the first
+        lowering for given arguments, as Taichi takes Python globals as compile-time constants."""
+        vals = tuple(_coerce(typ, val) for typ, val in zip(self.arg_types, args))
+        try:
+            key = (len(args),) + tuple((type(v).__name__, v) for v in vals)
+            hit = self._cache.get(key)
+        except TypeError:  # an unhashable argument: lowered every call
+            key, hit = None, None
+        if hit is not None:
+            self._cache.move_to_end(key)
+            return hit
         env = dict(self.fn.__globals__)
-        for name, typ, val in zip(self.arg_names, self.arg_types, args):
-            env[name] = _coerce(typ, val)
-        return lower_kernel(self.fdef, _FuncResolver(env), env)
+        for name, val in zip(self.arg_names, vals):
+            env[name] = val
+        low = lower_kernel(self.fdef, _FuncResolver(env), env)
+        if key is not None:
+            self._cache[key] = low
+            while len(self._cache) > self.CACHE_SIZE:
+                self._cache.popitem(last=False)
+        return low
 
     def __call__(self, *args):
         low = self.lower(*args)
