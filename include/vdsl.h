@@ -37,7 +37,9 @@
 extern "C" {
 #endif
 
-#define VDSL_ABI_VERSION 3
+/* 3: vdsl_map_instr.ext and vdsl_map_vinput.mat_dim (matrix operands); 4: VDSL_PIX_TRIP,
+ * vdsl_op_relu_bwd, vdsl_op_add (struct layouts unchanged since 3). */
+#define VDSL_ABI_VERSION 4
 
 typedef enum vdsl_status {
   VDSL_OK = 0,
