@@ -605,3 +605,21 @@ def test_random_programs_bit_exact(dev, q, seed):
         got = run_prog(dev, q, prog, ins, ni, nj)
         ref = oracle.pixel_program(prog, ni, nj, ins)
         assert same_values(got, ref), (seed, ni, nj, pp.describe(prog))
+
+
+def test_body_with_three_loops_split_into_parts_bit_exact(dev, q):
+    """A body of three runtime loops (a while loop, a range loop of a per-pixel trip count, another
+    while loop) runs as parts passing values through hidden fields: every program of the sequence
+    on the device equals the oracle's on the same inputs, and the stored fields equal the oracle's
+    run of the whole sequence."""
+    from test_taichi_general import TWO_LOOPS, lower_named
+    u = np.random.default_rng(21).random((48, 40)).astype(np.float32)
+    low, names = lower_named(TWO_LOOPS, "march", {})
+    dev_f, ref_f = {"u": u}, {"u": u}
+    for op in low.ops():
+        names.setdefault(id(op.field), f"hidden{len(names)}")
+        got = run_prog(dev, q, op.program, [dev_f[names[id(g)]] for g in op.inputs], 48, 40)
+        ref = oracle.pixel_program(op.program, 48, 40, [ref_f[names[id(g)]] for g in op.inputs])
+        assert np.array_equal(got, ref), names[id(op.field)]
+        dev_f[names[id(op.field)]], ref_f[names[id(op.field)]] = got, ref
+    assert len(low.ops()) >= 4 and np.array_equal(dev_f["f"], ref_f["f"]) and np.array_equal(dev_f["g"], ref_f["g"])

@@ -502,7 +502,8 @@ def lower_named(text, kernel, args):
 def run_ops(low, names, arrays):
     """Runs a lowered kernel's programs in order on the oracle over {field name: array}, as the
     device runs them (each program reads the fields as the programs before it left them; a
-    snapshot copy is named after its field with a trailing ').  1-D fields run as one row."""
+    snapshot copy is named after its field with a trailing ', a field the lowering made between
+    the parts of a body is named hidden<n>).  1-D fields run as one row."""
     for op in low.ops():
         if op.kind == "copy":
             names[id(op.field)] = names[id(op.inputs[0])] + "'"
@@ -514,6 +515,7 @@ def run_ops(low, names, arrays):
         def grid(a):
             return a if len(shape) == 2 else a.reshape((1,) + a.shape)
         out = oracle.pixel_program(op.program, ni, nj, [grid(arrays[names[id(f)]]) for f in op.inputs])
+        names.setdefault(id(op.field), f"hidden{len(names)}")  # a field the lowering made (between parts)
         arrays[names[id(op.field)]] = out if len(shape) == 2 else out.reshape(out.shape[1:])
     return arrays
 
@@ -904,3 +906,78 @@ def test_kernel_lowerings_are_cached_per_argument_values():
     for v in range(70):
         k.lower(float(v) + 0.25)
     assert len(k._cache) == tc.Kernel.CACHE_SIZE and k.lower(1.5) is not first
+
+
+TWO_LOOPS = '''import taichi as ti
+W, H = 48, 40
+u = ti.field(dtype=float, shape=(W, H))
+f = ti.field(dtype=float, shape=(W, H))
+g = ti.Vector.field(2, dtype=float, shape=(W, H))
+
+@ti.kernel
+def march():
+    for i, j in f:
+        t = 0.0
+        k = 0
+        while k < 60 and t < i * 0.5 + u[i, j]:
+            t += 0.75
+            k += 1
+        p = ti.Vector([t, k * 1.0])
+        s = 0.0
+        for m in range(j % 7 + 20):
+            s += p[0] * 0.125 + m
+        shade = 1.0
+        n = 0
+        while n < 30 and shade > 0.2 + u[i, j] * 0.1:
+            shade *= 0.9
+            n += 1
+        f[i, j] = s + shade + k + n * 0.01
+        g[i, j] = [p[1], s]
+'''
+
+
+def test_struct_for_with_three_runtime_loops():
+    """Three runtime loops in one body run as three parts, each passing the values the next one
+    reads (t, k, p, s) through hidden per-pixel fields; the stores at the end read all of them."""
+    u = np.random.default_rng(20).random((48, 40)).astype(np.float32)
+    low, names = lower_named(TWO_LOOPS, "march", {})
+    assert low.kind == "sequence"
+    f = run_ops(low, names, {"u": u})
+    ref_f = np.zeros((48, 40), np.float32)
+    ref_g = np.zeros((48, 40, 2), np.float32)
+    for i in range(48):
+        for j in range(40):
+            t, k = f32(0), 0
+            while k < 60 and t < f32(i) * f32(0.5) + u[i, j]:
+                t, k = t + f32(0.75), k + 1
+            p = (t, f32(k) * f32(1.0))
+            s = f32(0)
+            for m in range(j % 7 + 20):
+                s = s + (p[0] * f32(0.125) + f32(m))
+            shade, n = f32(1), 0
+            while n < 30 and shade > f32(0.2) + u[i, j] * f32(0.1):
+                shade, n = shade * f32(0.9), n + 1
+            ref_f[i, j] = ((s + shade) + f32(k)) + f32(n) * f32(0.01)
+            ref_g[i, j] = (p[1], s)
+    assert np.array_equal(f["f"], ref_f) and np.array_equal(f["g"], ref_g)
+
+
+def test_range_of_a_per_pixel_integer_and_its_errors():
+    """range(N) with N an integer expression of the indices runs as a loop of at most N's bound
+    trips with the test k < N; a float N is refused."""
+    text = ("import taichi as ti\nf = ti.field(dtype=float, shape=(12, 9))\n@ti.kernel\ndef k():\n    for i, j in f:\n"
+            "        s = 0.0\n        for m in range(i * 2 - j):\n            s += m * 0.5 + 1.0\n        f[i, j] = s\n"
+            "@ti.kernel\ndef bad():\n    for i, j in f:\n        s = 0.0\n        for m in range(i * 0.5):\n"
+            "            s += 1.0\n        f[i, j] = s\n")
+    low = tc.lower_source_kernel(text, "k", {})
+    assert low.program.max_iter == 11 * 2 + 8 and low.program.test == pp.TESTS["lt"]
+    ref = np.zeros((12, 9), np.float32)
+    for i in range(12):
+        for j in range(9):
+            s = f32(0)
+            for m in range(i * 2 - j):
+                s = s + (f32(m) * f32(0.5) + f32(1.0))
+            ref[i, j] = s
+    assert np.array_equal(oracle.pixel_program(low.program, 12, 9), ref)
+    with pytest.raises(tc.TaichiLoweringError, match="range"):
+        tc.lower_source_kernel(text, "bad", {})

@@ -27,10 +27,11 @@ f32 (Taichi's default float type), and the body must have the escape-time shape
 Bodies of any other shape are lowered by the general path to a per-pixel register program
 (vernondsl_amd.pixprog, run by vdsl_op_pixel_program, compiled at run time for the program): any
 expression of the pixel indices, scalar kernel arguments, other 2-D f32 fields read at [i, j]
-and constants, with at most one loop - a `while <test> and <counter> < MAX:` check-then-update
+and constants, with loops - a `while <test> and <counter> < MAX:` check-then-update
 loop whose body ends with `counter += 1`, or a `for k in range(N)` / `range(A, B)` loop (a
-perfect nest of them runs as one loop over its trips), whose test and body may read the counter
-or k (from the loop's trip) - and stores
+perfect nest of them runs as one loop over its trips; N may be an integer expression of the
+pixel), whose test and body may read the counter or k (from the loop's trip); a body of several
+loops runs as parts joined by hidden per-pixel fields - and stores
 `F[i, j] = <value>` (an i32 field stores the loop counter) into one or more fields of the loop's
 shape: a body storing several fields becomes one program per stored field, run in an order in
 which no program loads a field that an earlier one stored (a snapshot copy where the programs
@@ -48,6 +49,7 @@ import ast
 import collections
 import inspect
 import math as _pymath
+import sys
 import textwrap
 import types
 
@@ -1456,6 +1458,9 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
     a program loading a field runs before the one storing it; where they load each other's fields
     (x from v and v from x, as a particle update does), one such field is first copied to a
     snapshot (Field.snapshot) that the other programs load instead."""
+    split = _split_at_second_loop(fdef, funcs, env)
+    if split is not None:
+        return split
     low, stored = _lower_pixel_one(fdef, funcs, env, None)
     if low is not None:
         return low
@@ -1480,9 +1485,9 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
     return Lowered("sequence", stored[0], parts=copies + [parts[id(f)] for f in order])
 
 
-def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target):
-    """(Lowered program storing `target`, the fields the body stores); target None: the only
-    field the body stores (Lowered None when it stores several)."""
+def _struct_for(fdef: ast.FunctionDef, funcs, env):
+    """The struct-for of a kernel body set up for interpretation: (the loop, the interpreter, its
+    Builder, the locals holding the indices, the body's statements)."""
     from . import pixprog as pp
     body = [s for s in fdef.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant))]
     if len(body) != 1 or not isinstance(body[0], ast.For):
@@ -1520,9 +1525,24 @@ def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target):
     for nm, ext in zip(ip.names, shape):
         ip.ibound[id(local[nm])] = max(int(ext) - 1, 0)
     stmts = [s for s in loop.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant)) and not isinstance(s, ast.Pass)]
+    return loop, ip, b, local, stmts
+
+
+def _is_runtime_loop(st, ip, local) -> bool:
+    if not isinstance(st, (ast.While, ast.For)):
+        return False
+    try:
+        return ip.static_values(st, local) is None
+    except TaichiLoweringError:
+        return True
+
+
+def _run_stmts(ip, b, local, stmts):
+    """Interprets a struct-for body (at most one runtime loop): (initial states, test, new states,
+    max_iter, whether there is a loop)."""
     init, test, new_state, max_iter, has_loop = {}, None, {}, 0, False
     for st in stmts:
-        if isinstance(st, (ast.While, ast.For)) and ip.static_values(st, local) is None:
+        if _is_runtime_loop(st, ip, local):
             if has_loop:
                 raise TaichiLoweringError("at most one loop per struct-for body")
             if any(_is_skey(k) for k in local):
@@ -1533,6 +1553,100 @@ def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target):
         if ip.assign(st, local):
             continue
         raise TaichiLoweringError(f"statement at line {getattr(st, 'lineno', '?')} is not supported")
+    return init, test, new_state, max_iter, has_loop
+
+
+def _split_at_second_loop(fdef: ast.FunctionDef, funcs, env):
+    """A struct-for body with two or more runtime loops, as two parts run one after the other: the
+    statements before the second loop, then the rest.  The values the second part reads from the
+    first go through hidden per-pixel fields of the struct-for's shape (their components packed
+    four to a field; plain numbers are passed as constants), which the first part stores and the
+    second reads at the pixel.  None for a body with at most one runtime loop."""
+    loop, ip, b, local, stmts = _struct_for(fdef, funcs, env)
+    loops = [k for k, st in enumerate(stmts) if _is_runtime_loop(st, ip, local)]
+    if len(loops) < 2:
+        return None
+    part1, part2 = stmts[:loops[1]], stmts[loops[1]:]
+    _run_stmts(ip, b, local, part1)  # a dry run: the kinds of the values the second part reads
+    reads2 = {nd.id for st in part2 for nd in ast.walk(st) if isinstance(nd, ast.Name) and isinstance(nd.ctx, ast.Load)}
+    consts, comps = [], []  # (name, value) passed as constants; (name, width) through fields
+    for nm, v in local.items():
+        if not (isinstance(nm, str) and nm in reads2 and nm not in ip.names):
+            continue
+        if v is _UNREADABLE or v is _ONE_BRANCH:
+            continue
+        if isinstance(v, _PVec):
+            if all(_is_num(c) for c in v.comps):
+                consts.append((nm, [float(_f32(c)) for c in v.comps]))
+            else:
+                comps.append((nm, len(v.comps)))
+        elif _is_num(v):
+            consts.append((nm, v if isinstance(v, (int, np.integer)) and not isinstance(v, bool) else float(_f32(v))))
+        else:
+            comps.append((nm, 0))
+    shape = ip.shape if ip.shape is not None else ip.fld.shape
+    env2 = dict(env)
+    env2["__vdsl_ti"] = sys.modules[__name__]
+    flat = [(nm, c) for nm, w in comps for c in range(max(w, 1))]  # every component to pass, in order
+    fields, stores, slot = [], [], {}
+    serial = sum(1 for nm in env2 if str(nm).startswith("__vdsl_tmp"))  # names of earlier splits stay bound
+    for k in range(0, len(flat), 4):
+        group = flat[k:k + 4]
+        name = f"__vdsl_tmp{serial + k // 4}"
+        env2[name] = Field(f32, shape, len(group))
+        fields.append(name)
+        for q, (nm, c) in enumerate(group):
+            slot[(nm, c)] = (name, q, len(group))
+    here = ast.Name(id=ip.iname) if len(ip.names) == 1 else ast.Tuple(elts=[ast.Name(id=n) for n in ip.names])
+
+    def comp_src(nm, c):  # the value component nm[c] in the first part
+        base = ast.Name(id=nm, ctx=ast.Load())
+        return base if dict(comps)[nm] == 0 else ast.Subscript(value=base, slice=ast.Constant(value=c), ctx=ast.Load())
+
+    for name in fields:
+        members = sorted((q, nm, c) for (nm, c), (fn, q, _) in slot.items() if fn == name)
+        vals = [comp_src(nm, c) for _, nm, c in members]
+        value = vals[0] if len(vals) == 1 else ast.Call(func=ast.Attribute(value=ast.Name(id="__vdsl_ti"), attr="Vector"),
+                                                         args=[ast.List(elts=vals, ctx=ast.Load())], keywords=[])
+        stores.append(ast.Assign(targets=[ast.Subscript(value=ast.Name(id=name), slice=here, ctx=ast.Store())],
+                                 value=value, lineno=0))
+    prelude = []
+    for nm, v in consts:
+        val = ast.Call(func=ast.Attribute(value=ast.Name(id="__vdsl_ti"), attr="Vector"),
+                       args=[ast.List(elts=[ast.Constant(value=c) for c in v], ctx=ast.Load())], keywords=[]) \
+            if isinstance(v, list) else ast.Constant(value=v)
+        prelude.append(ast.Assign(targets=[ast.Name(id=nm, ctx=ast.Store())], value=val, lineno=0))
+
+    def read(nm, c):
+        fn, q, width = slot[(nm, c)]
+        whole = ast.Subscript(value=ast.Name(id=fn), slice=here, ctx=ast.Load())
+        return whole if width == 1 else ast.Subscript(value=whole, slice=ast.Constant(value=q), ctx=ast.Load())
+
+    for nm, w in comps:
+        val = read(nm, 0) if w == 0 else ast.Call(
+            func=ast.Attribute(value=ast.Name(id="__vdsl_ti"), attr="Vector"),
+            args=[ast.List(elts=[read(nm, c) for c in range(w)], ctx=ast.Load())], keywords=[])
+        prelude.append(ast.Assign(targets=[ast.Name(id=nm, ctx=ast.Store())], value=val, lineno=0))
+
+    def kernel_of(body):
+        f = ast.For(target=loop.target, iter=loop.iter, body=body, orelse=[], lineno=getattr(loop, "lineno", 0))
+        return ast.FunctionDef(name=fdef.name, args=fdef.args, body=[f], decorator_list=[], returns=None, type_comment=None)
+
+    if not stores and not any(isinstance(nd, ast.Subscript) and isinstance(nd.ctx, ast.Store)
+                              for st in part1 for nd in ast.walk(st)):
+        # the first part passes nothing on and stores nothing: only its loop's cost would remain
+        return lower_pixel_program(kernel_of(prelude + part2), funcs, env2)
+    first = lower_pixel_program(kernel_of(part1 + stores), funcs, env2)
+    second = lower_pixel_program(kernel_of(prelude + part2), funcs, env2)
+    return Lowered("sequence", second.field, parts=[first, second])
+
+
+def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target):
+    """(Lowered program storing `target`, the fields the body stores); target None: the only
+    field the body stores (Lowered None when it stores several)."""
+    from . import pixprog as pp
+    loop, ip, b, local, stmts = _struct_for(fdef, funcs, env)
+    init, test, new_state, max_iter, has_loop = _run_stmts(ip, b, local, stmts)
     if not ip.stored:
         raise TaichiLoweringError("the struct-for body must store field[i, j] = ...")
     if target is None:
@@ -1593,7 +1707,7 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
     """One loop of the body: (initial states, test, new states, max_iter); rebinds `local` to the
     values after the loop (states, and the counter as the loop's count)."""
     from . import pixprog as pp
-    counter, nest = None, []
+    counter, nest, dyn_n = None, [], None
     if isinstance(st, ast.For):
         # a perfect nest of range loops (each body is just the next loop) runs as one loop over
         # the product of the extents, its variables recovered from the trip, the innermost fastest
@@ -1610,8 +1724,16 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
             if not _is_range(lp.iter):
                 raise TaichiLoweringError("the inner loop must be `for k in range(N)`, `for k in range(A, B)` or a while loop")
             bounds = _range_bounds(lp.iter, ip, local)
+            if bounds is None and len(loops) == 1 and len(lp.iter.args) == 1:
+                # range(N) with N an integer expression of the pixel: a loop of at most N's bound
+                # trips whose test is `k < N` (lanes leave it at their own N)
+                n = ip.expr(lp.iter.args[0], local)
+                bnd = ip._ib(n) if isinstance(n, pp.Node) else None
+                if bnd is not None:
+                    dyn_n, bounds = n, (0, bnd)
             if bounds is None:
-                raise TaichiLoweringError("range(...) of a loop needs integer constants")
+                raise TaichiLoweringError("range(...) of a loop needs integer constants, or range(N) an integer expression "
+                                          "of the indices and constants")
             nest.append((lp.target.id if isinstance(lp.target, ast.Name) else None, bounds[0], max(bounds[1] - bounds[0], 0)))
         max_iter = 1
         for _, _, ext in nest:
@@ -1693,6 +1815,10 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
         if nm not in state and nm != counter:
             body_local.pop(nm, None)  # defined inside the loop: read before assignment is an error
     test_out = None
+    if dyn_n is not None:
+        if trip is _UNREADABLE:
+            raise TaichiLoweringError("range(N) of a per-pixel N needs N below 2^24")
+        test_out = ("lt", trip, dyn_n)
     if test is not None:
         ops = {ast.Lt: "lt", ast.LtE: "le", ast.Gt: "gt", ast.GtE: "ge"}
         one = test[0]
