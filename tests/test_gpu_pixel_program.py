@@ -623,3 +623,18 @@ def test_body_with_three_loops_split_into_parts_bit_exact(dev, q):
         assert np.array_equal(got, ref), names[id(op.field)]
         dev_f[names[id(op.field)]], ref_f[names[id(op.field)]] = got, ref
     assert len(low.ops()) >= 4 and np.array_equal(dev_f["f"], ref_f["f"]) and np.array_equal(dev_f["g"], ref_f["g"])
+
+
+def test_body_too_large_for_one_program_bit_exact(dev, q):
+    """A body beyond one program's 128 instructions runs as several programs joined by hidden
+    fields; each program on the device equals the oracle's on the same inputs."""
+    from test_taichi_general import BIG_BODY, lower_named
+    low, names = lower_named(BIG_BODY, "k", {})
+    dev_f, ref_f = {}, {}
+    for op in low.ops():
+        names.setdefault(id(op.field), f"hidden{len(names)}")
+        got = run_prog(dev, q, op.program, [dev_f[names[id(g)]] for g in op.inputs], 20, 30)
+        ref = oracle.pixel_program(op.program, 20, 30, [ref_f[names[id(g)]] for g in op.inputs])
+        assert np.array_equal(got, ref), names[id(op.field)]
+        dev_f[names[id(op.field)]], ref_f[names[id(op.field)]] = got, ref
+    assert len(low.ops()) >= 2 and np.array_equal(dev_f["f"], ref_f["f"])

@@ -981,3 +981,24 @@ def test_range_of_a_per_pixel_integer_and_its_errors():
     assert np.array_equal(oracle.pixel_program(low.program, 12, 9), ref)
     with pytest.raises(tc.TaichiLoweringError, match="range"):
         tc.lower_source_kernel(text, "bad", {})
+
+
+BIG_BODY = ("import taichi as ti\nf = ti.field(dtype=float, shape=(20, 30))\n@ti.kernel\ndef k():\n    for i, j in f:\n"
+            "        a = i * 0.5\n        b = j * 0.25\n" +
+            "".join(f"        a = a * {1 + (k % 7) * 0.001:.3f} + b * {0.01 * (k % 5 + 1):.2f}\n"
+                    f"        b = b - a * 0.0625\n" for k in range(60)) + "        f[i, j] = a + b\n")
+
+
+def test_bodies_too_large_for_one_program_are_split():
+    """A straight-line body of 120 dependent statements (about 240 instructions, beyond the 128 of
+    one program) runs as several programs passing their state through hidden fields: the same
+    values as one pass in numpy, operation for operation."""
+    low, names = lower_named(BIG_BODY, "k", {})
+    assert low.kind == "sequence" and len(low.ops()) >= 2
+    got = run_ops(low, names, {})["f"]
+    i, j = grid(20, 30)
+    a, b = i * f32(0.5), j * f32(0.25)
+    for k in range(60):
+        a = a * f32(float(f"{1 + (k % 7) * 0.001:.3f}")) + b * f32(float(f"{0.01 * (k % 5 + 1):.2f}"))
+        b = b - a * f32(0.0625)
+    assert np.array_equal(got, a + b)

@@ -55,13 +55,20 @@ class Node:
     __slots__ = ("kind", "args", "val", "key", "deps")
 
     def __repr__(self):
+        return self.text(4)
+
+    def text(self, depth):
+        """The expression as text, subexpressions below `depth` levels written as `...` (nodes are
+        shared, so written out in full the text can grow exponentially)."""
         if self.kind == "const":
             return repr(float(self.val))
         if self.kind in ("index", "load", "state"):
             return f"{self.kind}({self.val})"
         if self.kind in ("count", "trip"):
             return self.kind
-        return f"{self.kind}({', '.join(map(repr, self.args))})"
+        if depth <= 0:
+            return "..."
+        return f"{self.kind}({', '.join(a.text(depth - 1) for a in self.args)})"
 
 
 class Builder:

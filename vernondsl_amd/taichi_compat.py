@@ -308,7 +308,14 @@ class Sym:
         self.op, self.args = op, args
 
     def __repr__(self):
-        return f"{self.op}({', '.join(map(repr, self.args))})"
+        return self.text(4)
+
+    def text(self, depth):
+        """The expression as text, subexpressions below `depth` levels written as `...` (the tree
+        shares subexpressions, so written out in full it can grow exponentially)."""
+        if depth <= 0:
+            return "..."
+        return f"{self.op}({', '.join(a.text(depth - 1) if isinstance(a, Sym) else repr(a) for a in self.args)})"
 
 
 class Vec:
@@ -984,8 +991,9 @@ class _PixInterp:
     def _here(self):
         """The subscript of this pixel: (i, j), or i."""
         if len(self.names) == 1:
-            return ast.Name(id=self.iname)
-        return ast.Tuple(elts=[ast.Name(id=self.iname), ast.Name(id=self.jname)])
+            return ast.Name(id=self.iname, ctx=ast.Load())
+        return ast.Tuple(elts=[ast.Name(id=self.iname, ctx=ast.Load()), ast.Name(id=self.jname, ctx=ast.Load())],
+                         ctx=ast.Load())
 
     def field_read(self, fld, idx, local):
         """fld[i, j] (this pixel), or fld[e1, e2] at per-pixel indices (a stencil or gather read,
@@ -1448,7 +1456,7 @@ def _assigned_names(stmts):
     return out
 
 
-def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
+def lower_pixel_program(fdef: ast.FunctionDef, funcs, env, depth=0) -> Lowered:
     """Lowers one @ti.kernel struct-for body to per-pixel programs (vernondsl_amd.pixprog): one
     program when the body stores one field; when it stores several, one program per stored field
     (each evaluates the whole body and stores its field; the other stores stay local, so a later
@@ -1458,13 +1466,21 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env) -> Lowered:
     a program loading a field runs before the one storing it; where they load each other's fields
     (x from v and v from x, as a particle update does), one such field is first copied to a
     snapshot (Field.snapshot) that the other programs load instead."""
-    split = _split_at_second_loop(fdef, funcs, env)
+    split = _split_at_second_loop(fdef, funcs, env, depth)
     if split is not None:
         return split
-    low, stored = _lower_pixel_one(fdef, funcs, env, None)
-    if low is not None:
-        return low
-    parts = {id(f): _lower_pixel_one(fdef, funcs, env, f)[0] for f in stored}
+    try:
+        low, stored = _lower_pixel_one(fdef, funcs, env, None)
+        if low is not None:
+            return low
+        parts = {id(f): _lower_pixel_one(fdef, funcs, env, f)[0] for f in stored}
+    except TaichiLoweringError as e:
+        # a program too large for the device form (instructions or registers): the body in two
+        # parts, split at a statement in its middle
+        stmts = _struct_for(fdef, funcs, env)[4]
+        if not str(e).startswith("the program needs more than") or len(stmts) < 2:
+            raise
+        return _split_body(fdef, funcs, env, len(stmts) // 2, depth)
 
     def loaded_by_other(f, among):  # some other program still to run loads f
         return any(g is not f and f in parts[id(g)].reads for g in among)
@@ -1556,19 +1572,28 @@ def _run_stmts(ip, b, local, stmts):
     return init, test, new_state, max_iter, has_loop
 
 
-def _split_at_second_loop(fdef: ast.FunctionDef, funcs, env):
-    """A struct-for body with two or more runtime loops, as two parts run one after the other: the
-    statements before the second loop, then the rest.  The values the second part reads from the
-    first go through hidden per-pixel fields of the struct-for's shape (their components packed
-    four to a field; plain numbers are passed as constants), which the first part stores and the
-    second reads at the pixel.  None for a body with at most one runtime loop."""
+def _split_at_second_loop(fdef: ast.FunctionDef, funcs, env, depth=0):
+    """A struct-for body with two or more runtime loops, split before the second loop
+    (_split_body); None for a body with at most one runtime loop."""
     loop, ip, b, local, stmts = _struct_for(fdef, funcs, env)
     loops = [k for k, st in enumerate(stmts) if _is_runtime_loop(st, ip, local)]
     if len(loops) < 2:
         return None
-    part1, part2 = stmts[:loops[1]], stmts[loops[1]:]
+    return _split_body(fdef, funcs, env, loops[1], depth)
+
+
+def _split_body(fdef: ast.FunctionDef, funcs, env, at, depth):
+    """The struct-for body as two parts run one after the other: its statements before `at`, then
+    the rest.  The values the second part reads from the first go through hidden per-pixel fields
+    of the struct-for's shape (their components packed four to a field; plain numbers are passed
+    as constants), which the first part stores and the second reads at the pixel."""
+    if depth > 8:
+        raise TaichiLoweringError("the struct-for body does not split into programs that fit the device form")
+    loop, ip, b, local, stmts = _struct_for(fdef, funcs, env)
+    part1, part2 = stmts[:at], stmts[at:]
     _run_stmts(ip, b, local, part1)  # a dry run: the kinds of the values the second part reads
-    reads2 = {nd.id for st in part2 for nd in ast.walk(st) if isinstance(nd, ast.Name) and isinstance(nd.ctx, ast.Load)}
+    reads2 = {nd.id for st in part2 for nd in ast.walk(st)
+              if isinstance(nd, ast.Name) and isinstance(getattr(nd, "ctx", ast.Load()), ast.Load)}
     consts, comps = [], []  # (name, value) passed as constants; (name, width) through fields
     for nm, v in local.items():
         if not (isinstance(nm, str) and nm in reads2 and nm not in ip.names):
@@ -1597,7 +1622,8 @@ def _split_at_second_loop(fdef: ast.FunctionDef, funcs, env):
         fields.append(name)
         for q, (nm, c) in enumerate(group):
             slot[(nm, c)] = (name, q, len(group))
-    here = ast.Name(id=ip.iname) if len(ip.names) == 1 else ast.Tuple(elts=[ast.Name(id=n) for n in ip.names])
+    here = ast.Name(id=ip.iname, ctx=ast.Load()) if len(ip.names) == 1 else \
+        ast.Tuple(elts=[ast.Name(id=n, ctx=ast.Load()) for n in ip.names], ctx=ast.Load())
 
     def comp_src(nm, c):  # the value component nm[c] in the first part
         base = ast.Name(id=nm, ctx=ast.Load())
@@ -1606,25 +1632,25 @@ def _split_at_second_loop(fdef: ast.FunctionDef, funcs, env):
     for name in fields:
         members = sorted((q, nm, c) for (nm, c), (fn, q, _) in slot.items() if fn == name)
         vals = [comp_src(nm, c) for _, nm, c in members]
-        value = vals[0] if len(vals) == 1 else ast.Call(func=ast.Attribute(value=ast.Name(id="__vdsl_ti"), attr="Vector"),
+        value = vals[0] if len(vals) == 1 else ast.Call(func=ast.Attribute(value=ast.Name(id="__vdsl_ti", ctx=ast.Load()), attr="Vector"),
                                                          args=[ast.List(elts=vals, ctx=ast.Load())], keywords=[])
-        stores.append(ast.Assign(targets=[ast.Subscript(value=ast.Name(id=name), slice=here, ctx=ast.Store())],
+        stores.append(ast.Assign(targets=[ast.Subscript(value=ast.Name(id=name, ctx=ast.Load()), slice=here, ctx=ast.Store())],
                                  value=value, lineno=0))
     prelude = []
     for nm, v in consts:
-        val = ast.Call(func=ast.Attribute(value=ast.Name(id="__vdsl_ti"), attr="Vector"),
+        val = ast.Call(func=ast.Attribute(value=ast.Name(id="__vdsl_ti", ctx=ast.Load()), attr="Vector"),
                        args=[ast.List(elts=[ast.Constant(value=c) for c in v], ctx=ast.Load())], keywords=[]) \
             if isinstance(v, list) else ast.Constant(value=v)
         prelude.append(ast.Assign(targets=[ast.Name(id=nm, ctx=ast.Store())], value=val, lineno=0))
 
     def read(nm, c):
         fn, q, width = slot[(nm, c)]
-        whole = ast.Subscript(value=ast.Name(id=fn), slice=here, ctx=ast.Load())
+        whole = ast.Subscript(value=ast.Name(id=fn, ctx=ast.Load()), slice=here, ctx=ast.Load())
         return whole if width == 1 else ast.Subscript(value=whole, slice=ast.Constant(value=q), ctx=ast.Load())
 
     for nm, w in comps:
         val = read(nm, 0) if w == 0 else ast.Call(
-            func=ast.Attribute(value=ast.Name(id="__vdsl_ti"), attr="Vector"),
+            func=ast.Attribute(value=ast.Name(id="__vdsl_ti", ctx=ast.Load()), attr="Vector"),
             args=[ast.List(elts=[read(nm, c) for c in range(w)], ctx=ast.Load())], keywords=[])
         prelude.append(ast.Assign(targets=[ast.Name(id=nm, ctx=ast.Store())], value=val, lineno=0))
 
@@ -1635,9 +1661,9 @@ def _split_at_second_loop(fdef: ast.FunctionDef, funcs, env):
     if not stores and not any(isinstance(nd, ast.Subscript) and isinstance(nd.ctx, ast.Store)
                               for st in part1 for nd in ast.walk(st)):
         # the first part passes nothing on and stores nothing: only its loop's cost would remain
-        return lower_pixel_program(kernel_of(prelude + part2), funcs, env2)
-    first = lower_pixel_program(kernel_of(part1 + stores), funcs, env2)
-    second = lower_pixel_program(kernel_of(prelude + part2), funcs, env2)
+        return lower_pixel_program(kernel_of(prelude + part2), funcs, env2, depth + 1)
+    first = lower_pixel_program(kernel_of(part1 + stores), funcs, env2, depth + 1)
+    second = lower_pixel_program(kernel_of(prelude + part2), funcs, env2, depth + 1)
     return Lowered("sequence", second.field, parts=[first, second])
 
 
