@@ -638,3 +638,31 @@ def test_body_too_large_for_one_program_bit_exact(dev, q):
         assert np.array_equal(got, ref), names[id(op.field)]
         dev_f[names[id(op.field)]], ref_f[names[id(op.field)]] = got, ref
     assert len(low.ops()) >= 2 and np.array_equal(dev_f["f"], ref_f["f"])
+
+
+def test_three_d_fields_bit_exact(dev, q):
+    """3-D fields as [A B][C] grids: init, a clamped seven-point stencil and gathers one past each
+    axis on the device equal the oracle; the volume example's frames equal the oracle's run of
+    the same kernels (the middle slice)."""
+    from test_taichi_general import VOLUME, lower_named
+    f_dev, f_ref = {}, {}
+    for kernel, args in (("init", {}), ("diffuse", {"c": 0.1}), ("grad", {})):
+        low, names = lower_named(VOLUME, kernel, args)
+        for op in low.ops():
+            src = [f_dev[names[id(g)]].reshape((120, 36) + ((g.width,) if g.width > 1 else ())) for g in op.inputs]
+            got = run_prog(dev, q, op.program, src, 120, 36)
+            ref = oracle.pixel_program(op.program, 120, 36, src)
+            assert np.array_equal(got, ref), kernel
+            f_dev[names[id(op.field)]] = got.reshape((12, 10, 36) + got.shape[2:])
+    path = os.path.join(EX, "volume.py")
+    res, img = run_program(path, 2)
+    assert res["frames"] == 2 and img.shape == (96, 96)
+    text = open(path).read()
+    shape = (96 * 96, 96)
+    u0 = oracle.pixel_program(tc.lower_source_kernel(text, "init", {}).program, *shape)
+    diff = tc.lower_source_kernel(text, "diffuse", {"c": 0.15}).program
+    u = u0
+    for _ in range(10):
+        u = oracle.pixel_program(diff, *shape, [u])
+    assert np.array_equal(img, u.reshape(96, 96, 96)[:, :, 48])
+    assert (img > 0).sum() > (u0.reshape(96, 96, 96)[:, :, 48] > 0).sum()  # the heat has spread

@@ -510,13 +510,13 @@ def run_ops(low, names, arrays):
             arrays[names[id(op.field)]] = arrays[names[id(op.inputs[0])]].copy()
             continue
         shape = op.field.shape
-        ni, nj = shape if len(shape) == 2 else (1, shape[0])
+        ni, nj = (1, shape[0]) if len(shape) == 1 else tuple(shape) if len(shape) == 2 else (shape[0] * shape[1], shape[2])
 
-        def grid(a):
-            return a if len(shape) == 2 else a.reshape((1,) + a.shape)
+        def grid(a):  # the field's array as the program grid [ni][nj] (+ components)
+            return a.reshape((ni, nj) + a.shape[len(shape):])
         out = oracle.pixel_program(op.program, ni, nj, [grid(arrays[names[id(f)]]) for f in op.inputs])
         names.setdefault(id(op.field), f"hidden{len(names)}")  # a field the lowering made (between parts)
-        arrays[names[id(op.field)]] = out if len(shape) == 2 else out.reshape(out.shape[1:])
+        arrays[names[id(op.field)]] = out.reshape(tuple(shape) + out.shape[2:])
     return arrays
 
 
@@ -1002,3 +1002,50 @@ def test_bodies_too_large_for_one_program_are_split():
         a = a * f32(float(f"{1 + (k % 7) * 0.001:.3f}")) + b * f32(float(f"{0.01 * (k % 5 + 1):.2f}"))
         b = b - a * f32(0.0625)
     assert np.array_equal(got, a + b)
+
+
+VOLUME = '''import taichi as ti
+A, B, C = 12, 10, 36
+u = ti.field(dtype=float, shape=(A, B, C))
+v = ti.field(dtype=float, shape=(A, B, C))
+g = ti.Vector.field(3, dtype=float, shape=(A, B, C))
+
+@ti.kernel
+def init():
+    for i, j, k in u:
+        u[i, j, k] = ((i * 7 + j * 3 + k) % 11) * 0.125
+
+@ti.kernel
+def diffuse(c: float):
+    for i, j, k in v:
+        s = (u[ti.max(i - 1, 0), j, k] + u[ti.min(i + 1, A - 1), j, k] + u[i, ti.max(j - 1, 0), k]
+             + u[i, ti.min(j + 1, B - 1), k] + u[i, j, ti.max(k - 1, 0)] + u[i, j, ti.min(k + 1, C - 1)])
+        v[i, j, k] = u[i, j, k] + c * (s - 6.0 * u[i, j, k])
+
+@ti.kernel
+def grad():
+    for i, j, k in ti.ndrange(A, B, C):
+        g[i, j, k] = [u[i + 1, j, k] - u[i, j, k], u[i, j + 1, k] - u[i, j, k], u[i, j, k + 1] - u[i, j, k]]
+'''
+
+
+def test_three_d_fields_stencils_and_gathers_past_an_axis():
+    """3-D fields run as [A B][C] grids with i, j from the row by exact integer // and %: an init
+    from the indices, a clamped seven-point stencil, and gathers one past the last index of each
+    axis (clamped to that axis, not run into the next row)."""
+    low, names = lower_named(VOLUME, "init", {})
+    f = run_ops(low, names, {})
+    i, j, k = np.meshgrid(np.arange(12), np.arange(10), np.arange(36), indexing="ij")
+    u = (((i * 7 + j * 3 + k) % 11).astype(np.float32) * f32(0.125))
+    assert f["u"].shape == (12, 10, 36) and np.array_equal(f["u"], u)
+    low, names = lower_named(VOLUME, "diffuse", {"c": 0.1})
+    f = run_ops(low, names, {"u": u})
+    def sh(a, ax, d):
+        idx = np.clip(np.arange(a.shape[ax]) + d, 0, a.shape[ax] - 1)
+        return np.take(a, idx, axis=ax)
+    s = ((((sh(u, 0, -1) + sh(u, 0, 1)) + sh(u, 1, -1)) + sh(u, 1, 1)) + sh(u, 2, -1)) + sh(u, 2, 1)
+    assert np.array_equal(f["v"], u + f32(0.1) * (s - f32(6.0) * u))
+    low, names = lower_named(VOLUME, "grad", {})
+    f = run_ops(low, names, {"u": u})
+    ref = np.stack([sh(u, 0, 1) - u, sh(u, 1, 1) - u, sh(u, 2, 1) - u], -1)
+    assert f["g"].shape == (12, 10, 36, 3) and np.array_equal(f["g"], ref)

@@ -37,7 +37,8 @@ shape: a body storing several fields becomes one program per stored field, run i
 which no program loads a field that an earlier one stored (a snapshot copy where the programs
 load each other's fields; a load at [i, j] after the body's own store reads the stored value, as
 in Taichi); a kernel of several top-level struct-fors runs their lowerings one after another.
-1-D fields and struct-fors (`for i in x:`, `for i in range(N):`) run as one row of the grid.  What neither path lowers raises
+1-D fields and struct-fors (`for i in x:`, `for i in range(N):`) run as one row of the grid, 3-D
+ones ([A][B][C], `for i, j, k in u:`) as the grid [A B][C].  What neither path lowers raises
 TaichiLoweringError naming what did not match; there is no CPU fallback.  Accepted complex squares are the ones equal bit for bit to (zr*zr - zi*zi, (zi*zr)*2):
 `z[0]**2 - z[1]**2`, `z[0]*z[0] - z[1]*z[1]`, and `z[1]*z[0]*2` / `z[0]*z[1]*2` / `2*(z[0]*z[1])` /
 `z[0]*z[1] + z[0]*z[1]` for the imaginary part (`(2*z[0])*z[1]` is refused: it rounds differently
@@ -133,9 +134,14 @@ class Field:
         return self._tensor
 
     def grid_tensor(self):
-        """The tensor as a per-pixel program grid: a 1-D field of n elements is one row, [1][n]."""
+        """The tensor as a per-pixel program grid: a 1-D field of n elements is one row, [1][n]; a
+        3-D field [A][B][C] is [A B][C] (the same bytes)."""
         t = self.tensor()
-        return t.view((1,) + t.shape) if len(self.shape) == 1 else t
+        if len(self.shape) == 1:
+            return t.view((1,) + t.shape)
+        if len(self.shape) == 3:
+            return t.view((self.shape[0] * self.shape[1],) + t.shape[2:])
+        return t
 
     def to_numpy(self):
         _, q = _device()
@@ -819,12 +825,13 @@ class _PixInterp:
     """Evaluates a struct-for body over numbers (folded in f32 as Taichi's default float, ints
     kept exact), pixprog Nodes and _PVec vectors."""
 
-    def __init__(self, env, funcs, b, fld, iname, jname):
+    def __init__(self, env, funcs, b, fld, iname, jname, kname=None):
         from . import pixprog
         self.pp = pixprog
         self.env, self.funcs, self.b = env, funcs, b
         self.fld, self.iname, self.jname = fld, iname, jname
-        self.names = [iname] if jname is None else [iname, jname]  # a 1-D struct-for binds one index
+        # the struct-for's indices: one (1-D), two (2-D) or three (3-D)
+        self.names = [iname] if jname is None else [iname, jname] if kname is None else [iname, jname, kname]
         self.stored = []  # fields the body stores to at [i, j], in the order of their first store
         self.fields = {}  # id -> Field, for the store keys
         self.shape = fld.shape if isinstance(fld, Field) else None  # the struct-for's index space
@@ -989,11 +996,10 @@ class _PixInterp:
         return [getattr(e, "id", None) for e in self._elts(idx)] == self.names
 
     def _here(self):
-        """The subscript of this pixel: (i, j), or i."""
+        """The subscript of this pixel: (i, j), i, or (i, j, k)."""
         if len(self.names) == 1:
             return ast.Name(id=self.iname, ctx=ast.Load())
-        return ast.Tuple(elts=[ast.Name(id=self.iname, ctx=ast.Load()), ast.Name(id=self.jname, ctx=ast.Load())],
-                         ctx=ast.Load())
+        return ast.Tuple(elts=[ast.Name(id=n, ctx=ast.Load()) for n in self.names], ctx=ast.Load())
 
     def field_read(self, fld, idx, local):
         """fld[i, j] (this pixel), or fld[e1, e2] at per-pixel indices (a stencil or gather read,
@@ -1016,6 +1022,16 @@ class _PixInterp:
             return _PVec([self.b.load(k, c) for c in range(fld.width)])
         if len(elts) == 1:
             row, col = 0.0, self.expr(elts[0], local)
+        elif len(elts) == 3:
+            # [A][B][C] runs as [A B][C]: the row A-index * B + B-index, each clamped to its own
+            # axis and truncated first (so an index past one axis does not run into the next)
+            a, b2, col = (self.expr(e, local) for e in elts)
+            if any(isinstance(v, _PVec) for v in (a, b2, col)):
+                raise TaichiLoweringError("field indices are scalars")
+
+            def axis(v, n):
+                return self.unary("floor", self.minmax("min", [self.minmax("max", [v, 0.0]), float(n - 1)]))
+            row = self.arith("add", self.arith("mul", axis(a, fld.shape[0]), float(fld.shape[1])), axis(b2, fld.shape[1]))
         else:
             row, col = (self.expr(e, local) for e in elts)
         if isinstance(row, _PVec) or isinstance(col, _PVec):
@@ -1509,15 +1525,18 @@ def _struct_for(fdef: ast.FunctionDef, funcs, env):
     if len(body) != 1 or not isinstance(body[0], ast.For):
         raise TaichiLoweringError("the kernel body must be one struct-for `for i, j in field:` (or `for i in field:`)")
     loop = body[0]
+    kname = None
     if isinstance(loop.target, ast.Tuple) and len(loop.target.elts) == 2:
         iname, jname = (e.id for e in loop.target.elts)
+    elif isinstance(loop.target, ast.Tuple) and len(loop.target.elts) == 3:
+        iname, jname, kname = (e.id for e in loop.target.elts)  # a 3-D struct-for
     elif isinstance(loop.target, ast.Name):
         iname, jname = loop.target.id, None  # a 1-D struct-for
     else:
-        raise TaichiLoweringError("the struct-for must bind one index (a 1-D field) or two (a 2-D field)")
-    dims = 1 if jname is None else 2
+        raise TaichiLoweringError("the struct-for must bind one, two or three indices (a 1-D, 2-D or 3-D field)")
+    dims = 1 if jname is None else 2 if kname is None else 3
     b = pp.Builder()
-    it0 = _PixInterp(env, funcs, b, None, iname, jname)
+    it0 = _PixInterp(env, funcs, b, None, iname, jname, kname)
     it = loop.iter
     fname = it.func.attr if isinstance(it, ast.Call) and isinstance(it.func, ast.Attribute) else \
         it.func.id if isinstance(it, ast.Call) and isinstance(it.func, ast.Name) else None
@@ -1527,19 +1546,29 @@ def _struct_for(fdef: ast.FunctionDef, funcs, env):
                 not all(isinstance(v, (int, np.integer)) and v >= 0 for v in shape):
             raise TaichiLoweringError(f"the loop needs {dims} non-negative integer extent(s) for its {dims} "
                                       "index(es): ti.ndrange(W, H), ti.ndrange(N) or range(N)")
-        ip = _PixInterp(env, funcs, b, None, iname, jname)
+        ip = _PixInterp(env, funcs, b, None, iname, jname, kname)
         ip.shape = tuple(int(v) for v in shape)
     else:
         fld = it0.expr(it, {})
         if not isinstance(fld, Field) or len(fld.shape) != dims:
             raise TaichiLoweringError(f"the struct-for binds {dims} index(es): it must iterate a {dims}-D ti.field, "
                                       "ti.ndrange or range")
-        ip = _PixInterp(env, funcs, b, fld, iname, jname)
-    # a 1-D struct-for runs as one row of the program grid: its index is the column index
-    local = {iname: b.index(0), jname: b.index(1)} if dims == 2 else {iname: b.index(1)}
+        ip = _PixInterp(env, funcs, b, fld, iname, jname, kname)
+    # a 1-D struct-for runs as one row of the program grid: its index is the column index; a 3-D
+    # one [A][B][C] as the grid [A B][C]: i = row // B, j = row % B (exact integer operations), k
+    # the column
     shape = ip.shape if ip.shape is not None else ip.fld.shape
-    for nm, ext in zip(ip.names, shape):
-        ip.ibound[id(local[nm])] = max(int(ext) - 1, 0)
+    if dims == 3:
+        if shape[0] * shape[1] > _PixInterp._INT_EXACT:
+            raise TaichiLoweringError("a 3-D struct-for needs A * B <= 2^24 for its [A][B][C] extents")
+        row = b.index(0)
+        ip.ibound[id(row)] = max(shape[0] * shape[1] - 1, 0)
+        local = {iname: ip.floor_op(False, row, shape[1]), jname: ip.floor_op(True, row, shape[1]), kname: b.index(1)}
+        ip.ibound[id(local[kname])] = max(int(shape[2]) - 1, 0)
+    else:
+        local = {iname: b.index(0), jname: b.index(1)} if dims == 2 else {iname: b.index(1)}
+        for nm, ext in zip(ip.names, shape):
+            ip.ibound[id(local[nm])] = max(int(ext) - 1, 0)
     stmts = [s for s in loop.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant)) and not isinstance(s, ast.Pass)]
     return loop, ip, b, local, stmts
 
