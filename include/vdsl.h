@@ -38,8 +38,9 @@ extern "C" {
 #endif
 
 /* 3: vdsl_map_instr.ext and vdsl_map_vinput.mat_dim (matrix operands); 4: VDSL_PIX_TRIP,
- * vdsl_op_relu_bwd, vdsl_op_add (struct layouts unchanged since 3). */
-#define VDSL_ABI_VERSION 4
+ * vdsl_op_relu_bwd, vdsl_op_add (struct layouts unchanged since 3); 5: vdsl_pixel_program.in_rows
+ * and in_cols (inputs of another shape than the grid). */
+#define VDSL_ABI_VERSION 5
 
 typedef enum vdsl_status {
   VDSL_OK = 0,
@@ -360,11 +361,16 @@ typedef struct vdsl_pixel_program {
   int32_t out_regs[4];                     /* their registers, in component order */
   int32_t in_widths[VDSL_PIX_MAX_INPUTS];  /* components per pixel of input k, 1..4 */
   int32_t in_dtypes[VDSL_PIX_MAX_INPUTS];  /* VDSL_F32, or VDSL_I32 (one component, read as float(v)) */
+  /* Extents [in_rows[k]][in_cols[k]] of input k when it is not of the program's grid (a field of
+   * another shape, read only by VDSL_PIX_LOAD_AT, whose indices it clamps to these extents); both
+   * 0: the grid's [ni][nj]. */
+  int32_t in_rows[VDSL_PIX_MAX_INPUTS];
+  int32_t in_cols[VDSL_PIX_MAX_INPUTS];
   vdsl_map_instr code[VDSL_PIX_MAX_INSTR];
 } vdsl_pixel_program;
 
 /* Runs `prog` for every pixel of an [ni][nj] grid.  inputs: f32 [ni][nj][in_widths[k]] or int32
- * [ni][nj] fields (n_inputs <= 4); out: f32 [ni][nj][out_width] (VDSL_PIX_OUT_REG) or int32
+ * [ni][nj] fields (n_inputs <= 4; [in_rows[k]][in_cols[k]] for an input of its own extents); out: f32 [ni][nj][out_width] (VDSL_PIX_OUT_REG) or int32
  * [ni][nj] (VDSL_PIX_OUT_COUNT, VDSL_PIX_OUT_I32).  A program may read its output buffer as an
  * input: at [i][j] that is the pixel's value before the store; elsewhere (LOAD_AT) the result
  * depends on the order pixels run in, as for a Taichi kernel reading the field it writes. */

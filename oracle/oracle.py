@@ -164,8 +164,9 @@ def pixel_program(prog, ni: int, nj: int, inputs=(), rows=None) -> np.ndarray:
     ins = [np.ascontiguousarray(a, np.int32 if prog.in_dtypes[k] == 3 else np.float32) for k, a in enumerate(inputs)]
     for k, a in enumerate(ins):
         w = prog.in_widths[k]
-        if a.shape != ((ni, nj) if w == 1 else (ni, nj, w)) and a.shape != (ni, nj, w):
-            raise ValueError(f"input {k} of shape {a.shape}, expected {(ni, nj, w)}")
+        rk, ck = (prog.in_rows[k], prog.in_cols[k]) if prog.in_rows[k] else (ni, nj)  # an input of its own extents
+        if a.shape != ((rk, ck) if w == 1 else (rk, ck, w)) and a.shape != (rk, ck, w):
+            raise ValueError(f"input {k} of shape {a.shape}, expected {(rk, ck, w)}")
     r0, r1 = rows if rows else (0, ni)
     int_out = prog.out_kind in (1, 2)  # the loop count, or a value stored to an int32 field
     shape = (r1 - r0, nj) if int_out or prog.out_width == 1 else (r1 - r0, nj, prog.out_width)

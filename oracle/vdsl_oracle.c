@@ -217,8 +217,10 @@ static float pix_apply(const vdsl_pixel_program* p, const vdsl_map_instr* s, con
                        int64_t o, int64_t i, int64_t j, int count, int64_t ni, int64_t nj) {
   switch (s->op) {
     case VDSL_MAP_LOAD: return pix_load(p, inputs, s->a, o, s->c);
-    case VDSL_PIX_LOAD_AT:
-      return pix_load(p, inputs, s->a, pix_index(reg[s->b], ni) * nj + pix_index(reg[s->c], nj), (int)s->imm);
+    case VDSL_PIX_LOAD_AT: {  /* clamped to the input's own extents (the grid's unless in_rows/in_cols) */
+      const int64_t rn = p->in_rows[s->a] ? p->in_rows[s->a] : ni, cn = p->in_cols[s->a] ? p->in_cols[s->a] : nj;
+      return pix_load(p, inputs, s->a, pix_index(reg[s->b], rn) * cn + pix_index(reg[s->c], cn), (int)s->imm);
+    }
     case VDSL_PIX_INDEX: return s->a == 0 ? (float)i : (float)j;
     case VDSL_PIX_COUNT: case VDSL_PIX_TRIP: return (float)count;  /* the trip, in the loop's sections */
     case VDSL_PIX_COS: return cosf(reg[s->a]);

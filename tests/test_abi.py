@@ -32,7 +32,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_abi_version():
     from vernondsl_amd import _lib
-    assert _lib.lib.vdsl_abi_version() == 4
+    assert _lib.lib.vdsl_abi_version() == 5
 
 
 def test_struct_layouts_match_header(tmp_path):
@@ -43,6 +43,7 @@ def test_struct_layouts_match_header(tmp_path):
                    " sizeof(vdsl_map_instr), offsetof(vdsl_map_instr, imm), sizeof(vdsl_map_input),"
                    " sizeof(vdsl_device_info), offsetof(vdsl_escape_time_params, out_scale),"
                    " offsetof(vdsl_map_instr, ext), sizeof(vdsl_map_vinput), offsetof(vdsl_map_vinput, mat_dim));"
+                   "printf(\"%zu %zu\\n\", sizeof(vdsl_pixel_program), offsetof(vdsl_pixel_program, code));"
                    "return 0;}\n")
     exe = tmp_path / "probe"
     subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
@@ -50,6 +51,8 @@ def test_struct_layouts_match_header(tmp_path):
     want = [C.sizeof(_lib.EscapeTimeParams), C.sizeof(_lib.MapInstr), _lib.MapInstr.imm.offset,
             C.sizeof(_lib.MapInput), C.sizeof(_lib.DeviceInfo), _lib.EscapeTimeParams.out_scale.offset,
             _lib.MapInstr.ext.offset, C.sizeof(_lib.MapVInput), _lib.MapVInput.mat_dim.offset]
+    from vernondsl_amd import pixprog
+    want += [C.sizeof(pixprog.PixelProgram), pixprog.PixelProgram.code.offset]
     assert got == want
 
 

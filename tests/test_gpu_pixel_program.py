@@ -666,3 +666,29 @@ def test_three_d_fields_bit_exact(dev, q):
         u = oracle.pixel_program(diff, *shape, [u])
     assert np.array_equal(img, u.reshape(96, 96, 96)[:, :, 48])
     assert (img > 0).sum() > (u0.reshape(96, 96, 96)[:, :, 48] > 0).sum()  # the heat has spread
+
+
+def test_fields_of_other_shapes_bit_exact(dev, q):
+    """Gathers from fields of other shapes than the loop's (a 1-D field at the trip, a smaller 2-D
+    field past its last row, a 3-D field past its last k), each clamped to its own extents: the
+    device equals the oracle; the metaballs example runs and equals the oracle's frames."""
+    from test_taichi_general import OTHER_SHAPES, lower_named
+    rng_ = np.random.default_rng(23)
+    data = {"pos": (rng_.random((1, 24, 2)) * np.array([40, 30])).astype(np.float32),
+            "small": rng_.random((20, 10)).astype(np.float32), "vol": rng_.random((1200, 5)).astype(np.float32)}
+    for kernel in ("blobs", "upsample", "project"):
+        low, names = lower_named(OTHER_SHAPES, kernel, {})
+        for op in low.ops():
+            src = [data[names[id(g)]] for g in op.inputs]
+            got = run_prog(dev, q, op.program, src, 40, 30)
+            assert np.array_equal(got, oracle.pixel_program(op.program, 40, 30, src)), kernel
+    path = os.path.join(EX, "metaballs.py")
+    res, img = run_program(path, 3)
+    assert res["frames"] == 3 and img.shape == (640, 480) and 0.0 < img.mean() < 1.0
+    low, names = lower_named(open(path).read(), "render", {})
+    p = np.zeros((1, 48, 2), np.float32)
+    k = np.arange(48)
+    p[0, :, 0], p[0, :, 1] = (k * 97 % 613) + 10.0, (k * 53 % 457) + 10.0
+    assert low.program.in_rows[0] == 1 and low.program.in_cols[0] == 48
+    got = run_prog(dev, q, low.program, [p], 640, 480)
+    assert np.array_equal(got, oracle.pixel_program(low.program, 640, 480, [p]))

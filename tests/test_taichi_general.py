@@ -514,7 +514,12 @@ def run_ops(low, names, arrays):
 
         def grid(a):  # the field's array as the program grid [ni][nj] (+ components)
             return a.reshape((ni, nj) + a.shape[len(shape):])
-        out = oracle.pixel_program(op.program, ni, nj, [grid(arrays[names[id(f)]]) for f in op.inputs])
+        def as_input(f):  # an input of the loop's shape in the grid, one of its own in its own grid
+            a = arrays[names[id(f)]]
+            if tuple(f.shape) == tuple(shape):
+                return grid(a)
+            return a.reshape(tc._grid_of(f.shape) + a.shape[len(f.shape):])
+        out = oracle.pixel_program(op.program, ni, nj, [as_input(f) for f in op.inputs])
         names.setdefault(id(op.field), f"hidden{len(names)}")  # a field the lowering made (between parts)
         arrays[names[id(op.field)]] = out.reshape(tuple(shape) + out.shape[2:])
     return arrays
@@ -1049,3 +1054,63 @@ def test_three_d_fields_stencils_and_gathers_past_an_axis():
     f = run_ops(low, names, {"u": u})
     ref = np.stack([sh(u, 0, 1) - u, sh(u, 1, 1) - u, sh(u, 2, 1) - u], -1)
     assert f["g"].shape == (12, 10, 36, 3) and np.array_equal(f["g"], ref)
+
+
+OTHER_SHAPES = '''import taichi as ti
+W, H, N = 40, 30, 24
+img = ti.field(dtype=float, shape=(W, H))
+small = ti.field(dtype=float, shape=(W // 2, H // 3))
+pos = ti.Vector.field(2, dtype=float, shape=N)
+vol = ti.field(dtype=float, shape=(W, H, 5))
+
+@ti.kernel
+def blobs():
+    for i, j in img:
+        s = 0.0
+        for k in range(N):
+            d = pos[k] - ti.Vector([i * 1.0, j * 1.0])
+            s += 20.0 / (d.dot(d) + 1.0)
+        img[i, j] = ti.min(s, 1.0)
+
+@ti.kernel
+def upsample():
+    for i, j in img:
+        img[i, j] = small[i // 2, j // 3] + small[i // 2 + 1, j // 3] * 0.5
+
+@ti.kernel
+def project():
+    for i, j in img:
+        s = 0.0
+        for k in range(5):
+            s += vol[i, j, k] * (k + 1.0)
+        img[i, j] = s + vol[i, j, 9]
+'''
+
+
+def test_fields_of_other_shapes_are_gathered_in_their_own_extents():
+    """A 2-D struct-for reads a 1-D field of 2-vectors at the loop's trip, a smaller 2-D field
+    (indices clamped to its own extents: i // 2 + 1 runs past its last row) and a 3-D field (its
+    last index 9 clamped to 4): equal to numpy."""
+    rng_ = np.random.default_rng(22)
+    P = (rng_.random((24, 2)) * np.array([40, 30])).astype(np.float32)
+    low, names = lower_named(OTHER_SHAPES, "blobs", {})
+    assert [(low.program.in_rows[0], low.program.in_cols[0])] == [(1, 24)]
+    got = run_ops(low, names, {"pos": P})["img"]
+    i, j = grid(40, 30)
+    s = np.zeros((40, 30), np.float32)
+    for k in range(24):
+        dx, dy = P[k, 0] - i * f32(1.0), P[k, 1] - j * f32(1.0)
+        s = s + f32(20.0) / ((dx * dx + dy * dy) + f32(1.0))
+    assert np.array_equal(got, np.minimum(s, f32(1.0)))
+    sm = rng_.random((20, 10)).astype(np.float32)
+    low, names = lower_named(OTHER_SHAPES, "upsample", {})
+    got = run_ops(low, names, {"small": sm})["img"]
+    ii, jj = np.meshgrid(np.arange(40), np.arange(30), indexing="ij")
+    assert np.array_equal(got, sm[ii // 2, jj // 3] + sm[np.minimum(ii // 2 + 1, 19), jj // 3] * f32(0.5))
+    v = rng_.random((40, 30, 5)).astype(np.float32)
+    low, names = lower_named(OTHER_SHAPES, "project", {})
+    got = run_ops(low, names, {"vol": v})["img"]
+    ref = np.zeros((40, 30), np.float32)
+    for k in range(5):
+        ref = ref + v[:, :, k] * f32(k + 1.0)
+    assert np.array_equal(got, ref + v[:, :, 4])

@@ -40,6 +40,8 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
       return fail(VDSL_ERR_INVALID_ARG, "pixel program: out_regs out of range");
   for (int k = 0; k < n_inputs; ++k) {
     if (p.in_widths[k] < 1 || p.in_widths[k] > 4) return fail(VDSL_ERR_INVALID_ARG, "pixel program: in_widths must be 1..4");
+    if ((p.in_rows[k] == 0) != (p.in_cols[k] == 0) || p.in_rows[k] < 0 || p.in_cols[k] < 0)
+      return fail(VDSL_ERR_INVALID_ARG, "pixel program: in_rows / in_cols must both be 0 or both positive");
     if (p.in_dtypes[k] != VDSL_F32 && !(p.in_dtypes[k] == VDSL_I32 && p.in_widths[k] == 1))
       return fail(VDSL_ERR_INVALID_ARG, "pixel program: in_dtypes must be VDSL_F32 or VDSL_I32 (one component)");
   }
@@ -56,6 +58,8 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
     if (s.op == VDSL_MAP_LOAD) {
       if (s.a >= n_inputs || s.c >= p.in_widths[s.a])
         return fail(VDSL_ERR_INVALID_ARG, at + ": LOAD of an input or component that is not there");
+      if (p.in_rows[s.a] || p.in_cols[s.a])
+        return fail(VDSL_ERR_INVALID_ARG, at + ": LOAD (at the pixel) of an input of its own extents; use LOAD_AT");
     } else if (s.op == VDSL_PIX_LOAD_AT) {
       const bool comp_ok = s.a < n_inputs && s.imm >= 0.0f && s.imm < static_cast<float>(p.in_widths[s.a]) &&
                            s.imm == static_cast<float>(static_cast<int>(s.imm));
@@ -177,7 +181,10 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni, in
   // 32-bit element offsets when every field's byte offsets stay below 2^32
   int maxw = p.out_width;
   for (int k = 0; k < n_inputs; ++k) maxw = p.in_widths[k] > maxw ? p.in_widths[k] : maxw;
-  c("idx32", static_cast<int64_t>(ni) * nj * maxw * 4 <= int64_t{0xffffffff} ? 1 : 0);
+  int64_t elems = static_cast<int64_t>(ni) * nj;  // the largest field of the launch, in elements
+  for (int k = 0; k < n_inputs; ++k)
+    if (p.in_rows[k]) elems = std::max(elems, static_cast<int64_t>(p.in_rows[k]) * p.in_cols[k]);
+  c("idx32", elems * maxw * 4 <= int64_t{0xffffffff} ? 1 : 0);
   // Entries past out_width / n_inputs are not used: written as 0 / 1, so they do not split the cache.
   auto list = [&](const char* name, const int32_t* v, int n, int fill) {
     s += std::string("  static constexpr int ") + name + "[4] = {";
@@ -220,7 +227,9 @@ extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const
   PixIn in{};
   for (int k = 0; k < n_inputs; ++k) {
     const std::string name = "input" + std::to_string(k);
-    VDSL_TRY(check_buffer(q, inputs[k], nbytes(ni, nj, 4 * p.in_widths[k]), name.c_str(), false));
+    in.rows[k] = p.in_rows[k] ? p.in_rows[k] : ni;
+    in.cols[k] = p.in_cols[k] ? p.in_cols[k] : nj;
+    VDSL_TRY(check_buffer(q, inputs[k], nbytes(in.rows[k], in.cols[k], 4 * p.in_widths[k]), name.c_str(), false));
     in.p[k] = static_cast<const float*>(inputs[k]->ptr);
   }
   if (ni == 0 || nj == 0) return VDSL_OK;

@@ -32,6 +32,7 @@ struct PixRt {
 
 struct PixIn {
   const float* p[VDSL_PIX_MAX_INPUTS];
+  int rows[VDSL_PIX_MAX_INPUTS], cols[VDSL_PIX_MAX_INPUTS];  // each input's extents (the grid's for most)
 };
 
 // Element offsets into the fields: 32-bit when every byte offset of the launch's fields is below
@@ -88,13 +89,14 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
   if constexpr (s.op == VDSL_MAP_LOAD) {
     r[s.dst] = pix_load<P, s.a>(in, o, s.c);
   } else if constexpr (s.op == VDSL_PIX_LOAD_AT) {
-    unsigned ri = pix_index(r[s.b], ni), ci = pix_index(r[s.c], nj);
+    // indices clamped to the input's own extents (the grid's, unless it is a field of another shape)
+    unsigned ri = pix_index(r[s.b], in.rows[s.a]), ci = pix_index(r[s.c], in.cols[s.a]);
     // a row / column operand the host found wave-uniform (ext[0] / ext[1]; the row mapping puts
     // one row in each wave and runs no escape loops): its index is taken once per wave, into a
     // scalar register
     if constexpr (P::rows > 0 && s.ext[0] != 0) ri = __builtin_amdgcn_readfirstlane(ri);
     if constexpr (P::rows > 0 && s.ext[1] != 0) ci = __builtin_amdgcn_readfirstlane(ci);
-    const PixOff<P> e = static_cast<PixOff<P>>(ri) * static_cast<unsigned>(nj) + ci;
+    const PixOff<P> e = static_cast<PixOff<P>>(ri) * static_cast<unsigned>(in.cols[s.a]) + ci;
     r[s.dst] = pix_load<P, s.a>(in, e, static_cast<int>(rt.imm[PC]));
   } else if constexpr (s.op == VDSL_PIX_INDEX) {
     r[s.dst] = s.a == 0 ? fi : fj;

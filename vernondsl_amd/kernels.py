@@ -271,20 +271,21 @@ def pixel_program(q: Queue, prog, inputs, out: Tensor):
     """Runs a compiled per-pixel program (vernondsl_amd.pixprog.PixelProgram) over out's [ni][nj]
     grid: out f32 [ni][nj] or [ni][nj][out_width] (the program stores registers) or i32 [ni][nj]
     (it stores its loop count); inputs: f32 fields [ni][nj] or [ni][nj][in_widths[k]], read at
-    each pixel."""
+    each pixel, or of their own extents [in_rows[k]][in_cols[k]] (gathered)."""
     if len(out.shape) not in (2, 3):
         raise ValueError("out must be a 2-D field of scalars or vectors")
     ni, nj = out.shape[:2]
 
-    def field_shape(w):
-        return (ni, nj) if w == 1 else (ni, nj, w)
+    def field_shape(w, r=ni, c=nj):
+        return (r, c) if w == 1 else (r, c, w)
 
     if prog.out_kind in (1, 2):  # the loop count, or an int32 field
         _expect(out, (ni, nj), "i32", "out")
     else:
         _expect(out, field_shape(prog.out_width), "f32", "out")
     for k, t in enumerate(inputs):
-        _expect(t, field_shape(prog.in_widths[k]), "i32" if prog.in_dtypes[k] == _lib.I32 else "f32", f"input{k}")
+        r, c = (prog.in_rows[k], prog.in_cols[k]) if prog.in_rows[k] else (ni, nj)  # an input of its own extents
+        _expect(t, field_shape(prog.in_widths[k], r, c), "i32" if prog.in_dtypes[k] == _lib.I32 else "f32", f"input{k}")
     hs = (C.c_void_p * max(1, len(inputs)))(*[t.handle for t in inputs])
     call("vdsl_op_pixel_program", q.handle, ni, nj, C.byref(prog), hs, len(inputs), out.handle)
 

@@ -43,6 +43,7 @@ class PixelProgram(C.Structure):
                 ("loop", C.c_int32), ("max_iter", C.c_int32), ("test", C.c_int32), ("test_a", C.c_int32),
                 ("test_b", C.c_int32), ("out_kind", C.c_int32), ("out_width", C.c_int32), ("out_regs", C.c_int32 * 4),
                 ("in_widths", C.c_int32 * MAX_INPUTS), ("in_dtypes", C.c_int32 * MAX_INPUTS),
+                ("in_rows", C.c_int32 * MAX_INPUTS), ("in_cols", C.c_int32 * MAX_INPUTS),
                 ("code", _lib.MapInstr * MAX_INSTR)]
 
 
@@ -251,7 +252,8 @@ def _node_of(b: Builder, v) -> Node:
 
 
 def compile_program(b: Builder, init: dict | None = None, test=None, body: dict | None = None, max_iter: int = 0,
-                    out=None, loop: bool | None = None, in_widths=(), in_dtypes=(), out_i32: bool = False) -> PixelProgram:
+                    out=None, loop: bool | None = None, in_widths=(), in_dtypes=(), out_i32: bool = False,
+                    in_extents=()) -> PixelProgram:
     """init: {state name: initial Node or number}; test: (op, lhs, rhs) with op in lt/le/gt/ge (None:
     no test), both sides per-pixel values; body: {state name: new value} (the parallel update of
     one loop trip; names not listed keep their value); max_iter: most updates; out: the stored
@@ -259,7 +261,8 @@ def compile_program(b: Builder, init: dict | None = None, test=None, body: dict 
     field of vectors) or COUNT.  loop defaults to whether a body or test is given.  in_widths:
     components per pixel of each input field (default 1); in_dtypes: F32 or I32 per input (an
     int32 field of one component, read as float); out_i32: store the (single) value into an int32
-    field, truncating as a Taichi int field assignment does."""
+    field, truncating as a Taichi int field assignment does.  in_extents: (rows, cols) per input of
+    another shape than the grid (read only by load_at, clamped to those extents), or None."""
     init = dict(init or {})
     body = dict(body or {})
     loop = bool(body or test) if loop is None else bool(loop)
@@ -382,6 +385,9 @@ def compile_program(b: Builder, init: dict | None = None, test=None, body: dict 
             raise ProgramError("an input field is f32, or int32 of one component")
         p.in_widths[k] = widths[k]
         p.in_dtypes[k] = dtypes[k]
+    for k, ext in enumerate(in_extents):
+        if ext is not None:
+            p.in_rows[k], p.in_cols[k] = int(ext[0]), int(ext[1])
     for k, ins in enumerate(code):
         p.code[k] = ins
     return p

@@ -374,6 +374,11 @@ class _Interp:
             raise TaichiLoweringError(f"unknown name {n.id!r}")
         if isinstance(n, ast.BinOp):
             ops = {ast.Add: "add", ast.Sub: "sub", ast.Mult: "mul", ast.Div: "div", ast.Pow: "pow"}
+            if isinstance(n.op, (ast.FloorDiv, ast.Mod)):  # of integers (extents, module constants)
+                x, y = self.expr(n.left, local), self.expr(n.right, local)
+                if not all(isinstance(v, (int, np.integer)) and not isinstance(v, bool) for v in (x, y)) or y == 0:
+                    raise TaichiLoweringError(f"{type(n.op).__name__} is supported here for integer constants only")
+                return x // y if isinstance(n.op, ast.FloorDiv) else x % y
             if type(n.op) not in ops:
                 raise TaichiLoweringError(f"operator {type(n.op).__name__} is not supported")
             return _binop(ops[type(n.op)], self.expr(n.left, local), self.expr(n.right, local))
@@ -836,6 +841,7 @@ class _PixInterp:
         self.fields = {}  # id -> Field, for the store keys
         self.shape = fld.shape if isinstance(fld, Field) else None  # the struct-for's index space
         self.inputs = []  # Fields read at [i, j], in LOAD order
+        self.in_extents = []  # per input: None (the struct-for's grid), or its own grid (rows, cols)
         self.bools = set()  # ids of Nodes known to hold 1.0 / 0.0 (comparisons and their logic)
         # ids of Nodes known to hold integers (the indices and +, -, *, %, // of them and of integer
         # constants) -> a bound on their magnitude.  The program computes in f32 registers, where
@@ -843,6 +849,7 @@ class _PixInterp:
         # Taichi evaluates it in int32 and the results would differ.
         self.ibound = {}
         self.in_loop = False
+        self.unroll = True  # unroll short range loops whose variable is read (False: keep them loops)
 
     # -- values
     def node(self, v):
@@ -1005,16 +1012,22 @@ class _PixInterp:
         """fld[i, j] (this pixel), or fld[e1, e2] at per-pixel indices (a stencil or gather read,
         clamped to the field, whose shape must be the struct-for's); fld[i] / fld[e] in a 1-D
         struct-for, which runs as one row (row index 0)."""
-        elts = self._elts(idx)
-        here = self._is_here(idx)
+        own = tuple(fld.shape) != tuple(self.shape)  # a field of another shape: gathered in its own grid
+        if own:
+            elts = list(idx.elts) if isinstance(idx, ast.Tuple) else [idx]
+            if len(elts) != len(fld.shape):
+                raise TaichiLoweringError(f"a field of shape {fld.shape} is indexed with {len(fld.shape)} indices")
+            here = False
+        else:
+            elts = self._elts(idx)
+            here = self._is_here(idx)
         if here and _skey(fld) in local:
             return local[_skey(fld)]  # the value this pixel stored earlier in the body
-        if fld.shape != self.shape:
-            raise TaichiLoweringError("a field read must be of a field of the struct-for's shape")
         if fld not in self.inputs:
             if len(self.inputs) == self.pp.MAX_INPUTS:
                 raise TaichiLoweringError(f"at most {self.pp.MAX_INPUTS} fields can be read")
             self.inputs.append(fld)
+            self.in_extents.append(_grid_of(fld.shape) if own else None)
         k = self.inputs.index(fld)
         if here:
             if fld.width == 1:
@@ -1328,7 +1341,7 @@ class _PixInterp:
             # loop: unrolled as well, which runs the same statements in the same order; N is
             # bounded by the program size.  A loop around another loop stays a loop (a nest of
             # range loops runs as one loop over its trips), so nests do not multiply the program.
-            if (isinstance(it, ast.Call) and isinstance(it.func, ast.Name) and it.func.id == "range"
+            if (self.unroll and isinstance(it, ast.Call) and isinstance(it.func, ast.Name) and it.func.id == "range"
                     and isinstance(st.target, ast.Name)
                     and not any(isinstance(nd, (ast.For, ast.While)) for s2 in st.body for nd in ast.walk(s2))
                     and any(isinstance(nd, ast.Name) and nd.id == st.target.id and isinstance(nd.ctx, ast.Load)
@@ -1472,7 +1485,7 @@ def _assigned_names(stmts):
     return out
 
 
-def lower_pixel_program(fdef: ast.FunctionDef, funcs, env, depth=0) -> Lowered:
+def lower_pixel_program(fdef: ast.FunctionDef, funcs, env, depth=0, unroll=True) -> Lowered:
     """Lowers one @ti.kernel struct-for body to per-pixel programs (vernondsl_amd.pixprog): one
     program when the body stores one field; when it stores several, one program per stored field
     (each evaluates the whole body and stores its field; the other stores stay local, so a later
@@ -1482,19 +1495,28 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env, depth=0) -> Lowered:
     a program loading a field runs before the one storing it; where they load each other's fields
     (x from v and v from x, as a particle update does), one such field is first copied to a
     snapshot (Field.snapshot) that the other programs load instead."""
-    split = _split_at_second_loop(fdef, funcs, env, depth)
+    split = _split_at_second_loop(fdef, funcs, env, depth, unroll)
     if split is not None:
         return split
     try:
-        low, stored = _lower_pixel_one(fdef, funcs, env, None)
+        low, stored = _lower_pixel_one(fdef, funcs, env, None, unroll)
         if low is not None:
             return low
-        parts = {id(f): _lower_pixel_one(fdef, funcs, env, f)[0] for f in stored}
+        parts = {id(f): _lower_pixel_one(fdef, funcs, env, f, unroll)[0] for f in stored}
     except TaichiLoweringError as e:
-        # a program too large for the device form (instructions or registers): the body in two
-        # parts, split at a statement in its middle
+        if not str(e).startswith("the program needs more than"):
+            raise
+        # a program too large for the device form (instructions or registers): first with short
+        # range loops kept as loops rather than unrolled, then as two parts split at a statement
+        # in the middle of the body
+        if unroll:
+            try:
+                return lower_pixel_program(fdef, funcs, env, depth, unroll=False)
+            except TaichiLoweringError as e2:
+                if not str(e2).startswith("the program needs more than") and "does not split" not in str(e2):
+                    raise
         stmts = _struct_for(fdef, funcs, env)[4]
-        if not str(e).startswith("the program needs more than") or len(stmts) < 2:
+        if len(stmts) < 2:
             raise
         return _split_body(fdef, funcs, env, len(stmts) // 2, depth)
 
@@ -1517,7 +1539,7 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env, depth=0) -> Lowered:
     return Lowered("sequence", stored[0], parts=copies + [parts[id(f)] for f in order])
 
 
-def _struct_for(fdef: ast.FunctionDef, funcs, env):
+def _struct_for(fdef: ast.FunctionDef, funcs, env, unroll=True):
     """The struct-for of a kernel body set up for interpretation: (the loop, the interpreter, its
     Builder, the locals holding the indices, the body's statements)."""
     from . import pixprog as pp
@@ -1554,6 +1576,7 @@ def _struct_for(fdef: ast.FunctionDef, funcs, env):
             raise TaichiLoweringError(f"the struct-for binds {dims} index(es): it must iterate a {dims}-D ti.field, "
                                       "ti.ndrange or range")
         ip = _PixInterp(env, funcs, b, fld, iname, jname, kname)
+    ip.unroll = unroll
     # a 1-D struct-for runs as one row of the program grid: its index is the column index; a 3-D
     # one [A][B][C] as the grid [A B][C]: i = row // B, j = row % B (exact integer operations), k
     # the column
@@ -1571,6 +1594,15 @@ def _struct_for(fdef: ast.FunctionDef, funcs, env):
             ip.ibound[id(local[nm])] = max(int(ext) - 1, 0)
     stmts = [s for s in loop.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant)) and not isinstance(s, ast.Pass)]
     return loop, ip, b, local, stmts
+
+
+def _grid_of(shape):
+    """The per-pixel program grid of a field of `shape`: [1][N], [R][C], or [A B][C]."""
+    if len(shape) == 1:
+        return (1, shape[0])
+    if len(shape) == 3:
+        return (shape[0] * shape[1], shape[2])
+    return tuple(shape)
 
 
 def _is_runtime_loop(st, ip, local) -> bool:
@@ -1601,24 +1633,24 @@ def _run_stmts(ip, b, local, stmts):
     return init, test, new_state, max_iter, has_loop
 
 
-def _split_at_second_loop(fdef: ast.FunctionDef, funcs, env, depth=0):
+def _split_at_second_loop(fdef: ast.FunctionDef, funcs, env, depth=0, unroll=True):
     """A struct-for body with two or more runtime loops, split before the second loop
     (_split_body); None for a body with at most one runtime loop."""
-    loop, ip, b, local, stmts = _struct_for(fdef, funcs, env)
+    loop, ip, b, local, stmts = _struct_for(fdef, funcs, env, unroll)
     loops = [k for k, st in enumerate(stmts) if _is_runtime_loop(st, ip, local)]
     if len(loops) < 2:
         return None
-    return _split_body(fdef, funcs, env, loops[1], depth)
+    return _split_body(fdef, funcs, env, loops[1], depth, unroll)
 
 
-def _split_body(fdef: ast.FunctionDef, funcs, env, at, depth):
+def _split_body(fdef: ast.FunctionDef, funcs, env, at, depth, unroll=True):
     """The struct-for body as two parts run one after the other: its statements before `at`, then
     the rest.  The values the second part reads from the first go through hidden per-pixel fields
     of the struct-for's shape (their components packed four to a field; plain numbers are passed
     as constants), which the first part stores and the second reads at the pixel."""
     if depth > 8:
         raise TaichiLoweringError("the struct-for body does not split into programs that fit the device form")
-    loop, ip, b, local, stmts = _struct_for(fdef, funcs, env)
+    loop, ip, b, local, stmts = _struct_for(fdef, funcs, env, unroll)
     part1, part2 = stmts[:at], stmts[at:]
     _run_stmts(ip, b, local, part1)  # a dry run: the kinds of the values the second part reads
     reads2 = {nd.id for st in part2 for nd in ast.walk(st)
@@ -1690,17 +1722,17 @@ def _split_body(fdef: ast.FunctionDef, funcs, env, at, depth):
     if not stores and not any(isinstance(nd, ast.Subscript) and isinstance(nd.ctx, ast.Store)
                               for st in part1 for nd in ast.walk(st)):
         # the first part passes nothing on and stores nothing: only its loop's cost would remain
-        return lower_pixel_program(kernel_of(prelude + part2), funcs, env2, depth + 1)
-    first = lower_pixel_program(kernel_of(part1 + stores), funcs, env2, depth + 1)
-    second = lower_pixel_program(kernel_of(prelude + part2), funcs, env2, depth + 1)
+        return lower_pixel_program(kernel_of(prelude + part2), funcs, env2, depth + 1, unroll)
+    first = lower_pixel_program(kernel_of(part1 + stores), funcs, env2, depth + 1, unroll)
+    second = lower_pixel_program(kernel_of(prelude + part2), funcs, env2, depth + 1, unroll)
     return Lowered("sequence", second.field, parts=[first, second])
 
 
-def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target):
+def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target, unroll=True):
     """(Lowered program storing `target`, the fields the body stores); target None: the only
     field the body stores (Lowered None when it stores several)."""
     from . import pixprog as pp
-    loop, ip, b, local, stmts = _struct_for(fdef, funcs, env)
+    loop, ip, b, local, stmts = _struct_for(fdef, funcs, env, unroll)
     init, test, new_state, max_iter, has_loop = _run_stmts(ip, b, local, stmts)
     if not ip.stored:
         raise TaichiLoweringError("the struct-for body must store field[i, j] = ...")
@@ -1723,7 +1755,8 @@ def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target):
     try:
         prog = pp.compile_program(b, init=init, test=test, body=new_state, max_iter=max_iter, out=out, loop=has_loop,
                                   in_widths=[f.width for f in ip.inputs],
-                                  in_dtypes=[pp.I32 if f.dtype == i32 else pp.F32 for f in ip.inputs], out_i32=out_i32)
+                                  in_dtypes=[pp.I32 if f.dtype == i32 else pp.F32 for f in ip.inputs], out_i32=out_i32,
+                                  in_extents=ip.in_extents)
     except pp.ProgramError as e:
         raise TaichiLoweringError(str(e)) from None
     # the fields this program loads (an input that only dead code reads is not one)
