@@ -891,6 +891,20 @@ def _compact(entry):
     return _round(e)
 
 
+def _summary_row(entry):
+    """[config, value, unit, roofline frac, ms] of one per-config record, with the kernel or
+    example named where several records share a config id."""
+    cid = entry.get("config")
+    wl = str(entry.get("workload", ""))
+    tag = {"Burning": "ship", "heat": "heat", "bf16": "bf16", "generic interpreter": "interp",
+           "compiled at run time": "jit", "sigmoid": "sigmoid"}
+    names = [v for k, v in tag.items() if k in wl]
+    label = str(cid) + ("/" + "/".join(names) if names else "")
+    rf = entry.get("roofline") or {}
+    ms = entry.get("ms_per_launch", entry.get("ms_per_step"))
+    return [label, _round(entry.get("value")), entry.get("unit"), rf.get("frac"), _round(ms)]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -967,6 +981,9 @@ def main():
         "cpu_baseline": head.get("cpu"),
         "device": {"name": info["name"], "arch": info["arch"], "compute_units": info["compute_units"]},
         "per_config": [_compact(e) for e in per_config],
+        # last, so that a reader keeping only the line's final ~2000 characters still sees every
+        # config's figure: [config, value, unit, roofline fraction, ms per launch or step]
+        "summary": [_summary_row(e) for e in per_config],
     }
     q.destroy()
     dev.close()
