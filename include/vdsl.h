@@ -39,8 +39,9 @@ extern "C" {
 
 /* 3: vdsl_map_instr.ext and vdsl_map_vinput.mat_dim (matrix operands); 4: VDSL_PIX_TRIP,
  * vdsl_op_relu_bwd, vdsl_op_add (struct layouts unchanged since 3); 5: vdsl_pixel_program.in_rows
- * and in_cols (inputs of another shape than the grid). */
-#define VDSL_ABI_VERSION 5
+ * and in_cols (inputs of another shape than the grid); 6: VDSL_PIX_ATOMIC_ADD,
+ * VDSL_PIX_OUT_NONE (scatter-adds) and VDSL_PIX_TRUNC (struct layouts unchanged since 5). */
+#define VDSL_ABI_VERSION 6
 
 typedef enum vdsl_status {
   VDSL_OK = 0,
@@ -334,7 +335,20 @@ typedef enum vdsl_pix_opcode {
    * sections only.  Every lane still in the loop is on the same trip, so this is the loop
    * variable of `for k in range(N)` and the counter of a while loop (an index: gathers at it
    * read one element per wave). */
-  VDSL_PIX_TRIP = 43
+  VDSL_PIX_TRIP = 43,
+  /* Scatter-add (Taichi's `f[idx] += v` at an index other than the pixel's, an atomic add):
+   * component (int)imm of input a at [(int)r[b]][(int)r[c]] += r[dst], when 0 <= r[b] < rows
+   * and 0 <= r[c] < cols of input a (its own extents or the grid's).  Otherwise (an index
+   * negative, NaN or too large: nothing is clamped) the add is dropped, as it is on lanes past
+   * the grid.  r[dst] is read, no register is written.  Pre and post sections only.  Input a is
+   * then written: its buffer must be writable, must not be `out`, and no LOAD / LOAD_AT of the
+   * program may read it.  An int32 input adds r[dst] converted as VDSL_PIX_OUT_I32 stores it,
+   * wrapping on overflow: exact in any order.  An f32 input adds in f32 with the hardware's
+   * atomic float add; the adds of one launch to one element happen in no fixed order, so the
+   * sum's rounding may differ between runs (as Taichi's atomic adds).  Where both indices are
+   * the same for every lane of a wave, the wave's values are summed first and added once. */
+  VDSL_PIX_ATOMIC_ADD = 44,
+  VDSL_PIX_TRUNC = 45   /* truncf(r[a]): toward zero (Taichi's float -> int conversion, kept in f32) */
 } vdsl_pix_opcode;
 
 typedef enum vdsl_pix_test {
@@ -347,7 +361,10 @@ typedef enum vdsl_pix_output {
   VDSL_PIX_OUT_COUNT = 1,  /* int32 field: the count of loop updates (out_width 1) */
   /* int32 field: r[out_regs[0]] converted as a Taichi int field assignment does, truncating
    * toward zero (NaN gives 0, values beyond the int32 range saturate); out_width 1 */
-  VDSL_PIX_OUT_I32 = 2
+  VDSL_PIX_OUT_I32 = 2,
+  /* no per-pixel store: a program whose effects are its VDSL_PIX_ATOMIC_ADDs (out may be null;
+   * out_width 1) */
+  VDSL_PIX_OUT_NONE = 3
 } vdsl_pix_output;
 
 typedef struct vdsl_pixel_program {
@@ -371,7 +388,7 @@ typedef struct vdsl_pixel_program {
 
 /* Runs `prog` for every pixel of an [ni][nj] grid.  inputs: f32 [ni][nj][in_widths[k]] or int32
  * [ni][nj] fields (n_inputs <= 4; [in_rows[k]][in_cols[k]] for an input of its own extents); out: f32 [ni][nj][out_width] (VDSL_PIX_OUT_REG) or int32
- * [ni][nj] (VDSL_PIX_OUT_COUNT, VDSL_PIX_OUT_I32).  A program may read its output buffer as an
+ * [ni][nj] (VDSL_PIX_OUT_COUNT, VDSL_PIX_OUT_I32), unused for VDSL_PIX_OUT_NONE.  A program may read its output buffer as an
  * input: at [i][j] that is the pixel's value before the store; elsewhere (LOAD_AT) the result
  * depends on the order pixels run in, as for a Taichi kernel reading the field it writes. */
 int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const vdsl_pixel_program* prog,

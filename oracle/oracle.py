@@ -160,7 +160,16 @@ def pixel_program(prog, ni: int, nj: int, inputs=(), rows=None) -> np.ndarray:
     """orc_pixel_program_rows: prog is a vernondsl_amd.pixprog.PixelProgram (the C struct);
     inputs: f32 [ni][nj] (one component) or [ni][nj][w] arrays, w = prog.in_widths[k], or int32
     [ni][nj] (prog.in_dtypes[k] = VDSL_I32); returns f32 [rows][nj] or [rows][nj][out_width], or
-    int32 [rows][nj] (the count or an int32 field; rows: (r0, r1), default all)."""
+    int32 [rows][nj] (the count or an int32 field; rows: (r0, r1), default all), or None for a
+    program that stores nothing.  An input the program scatter-adds into is updated in place: it
+    must be a C-contiguous array of its dtype (float32 / int32)."""
+    total = prog.n_pre + prog.n_test + prog.n_body + prog.n_post
+    targets = {prog.code[pc].a for pc in range(total) if prog.code[pc].op == 44}
+    for k in targets:
+        want = np.int32 if prog.in_dtypes[k] == 3 else np.float32
+        a = inputs[k]
+        if not (isinstance(a, np.ndarray) and a.dtype == want and a.flags.c_contiguous and a.flags.writeable):
+            raise ValueError(f"input {k} is scatter-added into: pass a writable C-contiguous {np.dtype(want).name} array")
     ins = [np.ascontiguousarray(a, np.int32 if prog.in_dtypes[k] == 3 else np.float32) for k, a in enumerate(inputs)]
     for k, a in enumerate(ins):
         w = prog.in_widths[k]
@@ -173,7 +182,7 @@ def pixel_program(prog, ni: int, nj: int, inputs=(), rows=None) -> np.ndarray:
     out = np.zeros(shape, np.int32 if int_out else np.float32)
     ptrs = (_vp * max(1, len(ins)))(*[a.ctypes.data for a in ins])
     _lib.orc_pixel_program_rows(C.addressof(prog), ni, nj, ptrs, _p(out), r0, r1)
-    return out
+    return None if prog.out_kind == 3 else out
 
 
 def mat_transform(pos: np.ndarray, mats: np.ndarray) -> np.ndarray:

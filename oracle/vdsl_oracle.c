@@ -231,6 +231,7 @@ static float pix_apply(const vdsl_pixel_program* p, const vdsl_map_instr* s, con
     case VDSL_PIX_NE: return reg[s->a] != reg[s->b] ? 1.0f : 0.0f;
     case VDSL_PIX_SELECT: return reg[s->a] != 0.0f ? reg[s->b] : reg[s->c];
     case VDSL_PIX_FLOOR: return floorf(reg[s->a]);
+    case VDSL_PIX_TRUNC: return truncf(reg[s->a]);
     default: return map_apply(s->op, reg[s->a], reg[s->b], reg[s->c], s->imm);
   }
 }
@@ -245,32 +246,66 @@ static int pix_test(int test, float a, float b) {
   }
 }
 
+/* VDSL_PIX_ATOMIC_ADD: component imm of input a at [(int)r[b]][(int)r[c]] += r[dst] when
+ * 0 <= r[b] < rows and 0 <= r[c] < cols of input a, else nothing.  f32: one f32 addition; int32:
+ * the value converted as an int32 store converts it, added modulo 2^32. */
+static void pix_scatter_add(const vdsl_pixel_program* p, const vdsl_map_instr* s, const float* reg, const void* const* inputs,
+                            int64_t ni, int64_t nj) {
+  const int64_t rn = p->in_rows[s->a] ? p->in_rows[s->a] : ni, cn = p->in_cols[s->a] ? p->in_cols[s->a] : nj;
+  const float x = reg[s->b], y = reg[s->c];
+  if (!(x >= 0.0f && y >= 0.0f && x < 1073741824.0f && y < 1073741824.0f)) return;
+  const int64_t xi = (int64_t)x, yi = (int64_t)y;
+  if (xi >= rn || yi >= cn) return;
+  const int64_t e = xi * cn + yi;
+  if (p->in_dtypes[s->a] == VDSL_I32) {
+    uint32_t* t = (uint32_t*)inputs[s->a] + e;
+    *t = *t + (uint32_t)pix_to_i32(reg[s->dst]);
+  } else {
+    float* t = (float*)inputs[s->a] + e * p->in_widths[s->a] + (int)s->imm;
+    *t = *t + reg[s->dst];
+  }
+}
+
+/* One instruction: its register, or a scatter-add's effect. */
+static void pix_exec(const vdsl_pixel_program* p, int pc, float* reg, const void* const* inputs, int64_t o, int64_t i,
+                     int64_t j, int count, int64_t ni, int64_t nj) {
+  const vdsl_map_instr* s = &p->code[pc];
+  if (s->op == VDSL_PIX_ATOMIC_ADD) pix_scatter_add(p, s, reg, inputs, ni, nj);
+  else reg[s->dst] = pix_apply(p, s, reg, inputs, o, i, j, count, ni, nj);
+}
+
 /* Rows [r0, r1) of vdsl_op_pixel_program: per pixel, VDSL_PIX_MAX_REGS registers at 0, the pre section, the
  * check-then-update loop (fractal.py:22-24: test, stop unless it holds and fewer than max_iter
  * updates were made, body, count), the post section, then out[i][j][k] = r[out_regs[k]] (f32,
- * out_width components) or the count (int32).  A LOAD reads component c of input a's pixel
- * (in_widths[a] components each).  The program is taken as validated by the caller. */
+ * out_width components) or the count (int32), nothing for VDSL_PIX_OUT_NONE.  A LOAD reads
+ * component c of input a's pixel (in_widths[a] components each).  A program with scatter-adds
+ * runs its pixels one after another in row-major order (so an f32 target gets its adds in that
+ * order); others run rows in parallel.  The program is taken as validated by the caller. */
 void orc_pixel_program_rows(const vdsl_pixel_program* p, int64_t ni, int64_t nj, const void* const* inputs, void* out,
                             int64_t r0, int64_t r1) {
   const int t0 = p->n_pre, b0 = t0 + p->n_test, q0 = b0 + p->n_body, end = q0 + p->n_post;
-#pragma omp parallel for schedule(dynamic, 4)
+  int scatters = 0;
+  for (int pc = 0; pc < end; ++pc) scatters |= p->code[pc].op == VDSL_PIX_ATOMIC_ADD;
+#pragma omp parallel for schedule(dynamic, 4) if (!scatters)
   for (int64_t i = r0; i < r1; ++i)
     for (int64_t j = 0; j < nj; ++j) {
       const int64_t o = i * nj + j;
       float reg[VDSL_PIX_MAX_REGS];
       for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) reg[k] = 0.0f;
       int count = 0;
-      for (int pc = 0; pc < t0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, 0, ni, nj);
+      for (int pc = 0; pc < t0; ++pc) pix_exec(p, pc, reg, inputs, o, i, j, 0, ni, nj);
       if (p->loop) {
         while (count < p->max_iter) {
-          for (int pc = t0; pc < b0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, count, ni, nj);
+          for (int pc = t0; pc < b0; ++pc) pix_exec(p, pc, reg, inputs, o, i, j, count, ni, nj);
           if (!pix_test(p->test, reg[p->test_a], reg[p->test_b])) break;
-          for (int pc = b0; pc < q0; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, count, ni, nj);
+          for (int pc = b0; pc < q0; ++pc) pix_exec(p, pc, reg, inputs, o, i, j, count, ni, nj);
           ++count;
         }
       }
-      for (int pc = q0; pc < end; ++pc) reg[p->code[pc].dst] = pix_apply(p, &p->code[pc], reg, inputs, o, i, j, count, ni, nj);
-      if (p->out_kind == VDSL_PIX_OUT_COUNT) {
+      for (int pc = q0; pc < end; ++pc) pix_exec(p, pc, reg, inputs, o, i, j, count, ni, nj);
+      if (p->out_kind == VDSL_PIX_OUT_NONE) {
+        continue;
+      } else if (p->out_kind == VDSL_PIX_OUT_COUNT) {
         ((int32_t*)out)[o - r0 * nj] = count;
       } else if (p->out_kind == VDSL_PIX_OUT_I32) {
         ((int32_t*)out)[o - r0 * nj] = pix_to_i32(reg[p->out_regs[0]]);

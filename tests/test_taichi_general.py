@@ -503,23 +503,24 @@ def run_ops(low, names, arrays):
     """Runs a lowered kernel's programs in order on the oracle over {field name: array}, as the
     device runs them (each program reads the fields as the programs before it left them; a
     snapshot copy is named after its field with a trailing ', a field the lowering made between
-    the parts of a body is named hidden<n>).  1-D fields run as one row."""
+    the parts of a body is named hidden<n>).  1-D fields run as one row.  A field scatter-added
+    into is updated in its array (which must be float32 / int32 and C-contiguous)."""
     for op in low.ops():
         if op.kind == "copy":
             names[id(op.field)] = names[id(op.inputs[0])] + "'"
             arrays[names[id(op.field)]] = arrays[names[id(op.inputs[0])]].copy()
             continue
-        shape = op.field.shape
-        ni, nj = (1, shape[0]) if len(shape) == 1 else tuple(shape) if len(shape) == 2 else (shape[0] * shape[1], shape[2])
+        ni, nj = op.grid
 
-        def grid(a):  # the field's array as the program grid [ni][nj] (+ components)
-            return a.reshape((ni, nj) + a.shape[len(shape):])
-        def as_input(f):  # an input of the loop's shape in the grid, one of its own in its own grid
+        def as_input(k, f):  # an input of the loop's shape in the grid, one of its own in its own grid
             a = arrays[names[id(f)]]
-            if tuple(f.shape) == tuple(shape):
-                return grid(a)
-            return a.reshape(tc._grid_of(f.shape) + a.shape[len(f.shape):])
-        out = oracle.pixel_program(op.program, ni, nj, [as_input(f) for f in op.inputs])
+            p = op.program
+            r, c = (p.in_rows[k], p.in_cols[k]) if p.in_rows[k] else (ni, nj)
+            return a.reshape((r, c) + a.shape[len(f.shape):])
+        out = oracle.pixel_program(op.program, ni, nj, [as_input(k, f) for k, f in enumerate(op.inputs)])
+        if op.field is None:  # scatter-adds only
+            continue
+        shape = op.field.shape
         names.setdefault(id(op.field), f"hidden{len(names)}")  # a field the lowering made (between parts)
         arrays[names[id(op.field)]] = out.reshape(tuple(shape) + out.shape[2:])
     return arrays

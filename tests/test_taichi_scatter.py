@@ -1,0 +1,285 @@
+"""Scatter-adds (Taichi's `field[index] += v` at an index other than the loop's, an atomic add)
+on the CPU: the oracle's VDSL_PIX_ATOMIC_ADD is pinned by numpy's `np.add.at` (unbuffered adds
+in index order, the order the oracle runs pixels in) and by the drop rule written out per index;
+the front end's lowering of scatter-adds (histograms, 0-D totals, vector indices base + offset,
+adds in if branches, 3-D targets, bodies that also store) is pinned by numpy restatements run in
+the same order, so bit for bit."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from vernondsl_amd import pixprog as pp, taichi_compat as tc
+from test_taichi_general import lower_named, run_ops
+
+EX = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "vernondsl_amd", "examples")
+f32 = np.float32
+
+
+def scatter_program(b, effects, dtypes, widths, extents, out=None):
+    return pp.compile_program(b, out=out, effects=effects, in_dtypes=dtypes, in_widths=widths, in_extents=extents)
+
+
+# ---- the oracle's scatter-add ---------------------------------------------------------------------
+def test_oracle_scatter_add_equals_numpy_add_at():
+    """f32 (a vector field's component 1) and int32 targets of their own extents, indices from an
+    input field: the oracle adds in row-major pixel order, as np.add.at does over raveled
+    indices, so the f32 sums agree bit for bit."""
+    ni, nj, R, C = 23, 31, 5, 7
+    rng = np.random.default_rng(5)
+    rows = rng.integers(0, R, (ni, nj)).astype(f32)
+    cols = rng.integers(0, C, (ni, nj)).astype(f32)
+    val = rng.standard_normal((ni, nj)).astype(f32)
+    b = pp.Builder()
+    r, c, v = b.load(0, 0), b.load(0, 1), b.load(0, 2)  # one input of three components
+    effects = [b.scatter_add(1, r, c, v, 1), b.scatter_add(2, r, c, b.op("mul", v, 100.0))]
+    prog = scatter_program(b, effects, [pp.F32, pp.F32, pp.I32], [3, 2, 1], [None, (R, C), (R, C)])
+    assert prog.out_kind == pp.OUT_NONE
+    t_f = rng.standard_normal((R, C, 2)).astype(f32)
+    t_i = rng.integers(-50, 50, (R, C)).astype(np.int32)
+    want_f, want_i = t_f.copy(), t_i.astype(np.int64)
+    assert oracle.pixel_program(prog, ni, nj, [np.stack([rows, cols, val], -1), t_f, t_i]) is None
+    idx = (rows.astype(int).ravel(), cols.astype(int).ravel())
+    np.add.at(want_f[:, :, 1], idx, val.ravel())
+    np.add.at(want_i, idx, np.trunc(val * f32(100.0)).astype(np.int64).ravel())
+    assert np.array_equal(t_f, want_f)  # component 0 untouched, component 1 summed in order
+    assert np.array_equal(t_i, want_i.astype(np.int32))
+
+
+def test_oracle_scatter_add_drops_indices_outside_the_target():
+    """An add happens only where 0 <= row < R and 0 <= col < C (NaN, negative and too large
+    indices are dropped, not clamped); fractional indices truncate; int32 adds wrap."""
+    specials = np.array([-1.0, -0.5, 0.0, 0.75, 2.0, 2.999, 3.0, 4.0, np.nan, np.inf, -np.inf, 1e30], f32)
+    n = specials.size
+    rows, cols = np.meshgrid(specials, specials, indexing="ij")
+    b = pp.Builder()
+    effects = [b.scatter_add(2, b.load(0), b.load(1), 1.0), b.scatter_add(3, b.load(0), b.load(1), 2.0e9)]
+    prog = scatter_program(b, effects, [pp.F32, pp.F32, pp.F32, pp.I32], [1] * 4, [None, None, (3, 3), (3, 3)])
+    cnt = np.zeros((3, 3), f32)
+    wrap = np.zeros((3, 3), np.int32)
+    oracle.pixel_program(prog, n, n, [rows.astype(f32), cols.astype(f32), cnt, wrap])
+    want = np.zeros((3, 3), np.int64)
+    for x in specials:
+        for y in specials:
+            if 0 <= x < 3 and 0 <= y < 3:  # False for NaN
+                want[int(x), int(y)] += 1
+    assert np.array_equal(cnt, want.astype(f32))
+    assert np.array_equal(wrap, ((want * 2_000_000_000 + 2**31) % 2**32 - 2**31).astype(np.int32))
+
+
+def test_oracle_scatter_add_skips_nothing_it_should_run():
+    """A program that stores and scatter-adds: the store is the plain program's, and the adds
+    follow the loop (here the escape count of each pixel, binned)."""
+    b = pp.Builder()
+    x0 = b.op("mul", b.index(0), 0.25)
+    x = b.state("x")
+    count_bin = b.scatter_add(0, 0.0, b.count(), 1.0)
+    prog = pp.compile_program(b, init={"x": x0}, test=("lt", x, 3.0), body={"x": b.op("add", b.op("mul", x, x), 0.5)},
+                              max_iter=9, out=pp.COUNT, effects=[count_bin], in_dtypes=[pp.I32], in_extents=[(1, 10)])
+    hist = np.zeros((1, 10), np.int32)
+    counts = oracle.pixel_program(prog, 12, 3, [hist])
+    assert np.array_equal(hist[0], np.bincount(counts.ravel(), minlength=10))
+
+
+# ---- the front end ----------------------------------------------------------------------------------
+def escape_counts(W, H, MAX, cx, cy, scale):
+    """The histogram example's escape loop in numpy f32 (the same operations in the same order)."""
+    i, j = np.meshgrid(np.arange(W), np.arange(H), indexing="ij")
+    x0 = f32(cx) + (i.astype(f32) - f32(W / 2)) * f32(scale)
+    y0 = f32(cy) + (j.astype(f32) - f32(H / 2)) * f32(scale)
+    x = np.zeros((W, H), f32)
+    y = np.zeros((W, H), f32)
+    k = np.zeros((W, H), np.int32)
+    live = np.ones((W, H), bool)
+    for _ in range(MAX):
+        live &= (x * x + y * y) <= f32(4.0)
+        if not live.any():
+            break
+        nx, ny = x * x - y * y + x0, f32(2.0) * x * y + y0
+        x, y = np.where(live, nx, x), np.where(live, ny, y)
+        k += live
+    return k
+
+
+def test_histogram_example_lowers_to_one_program_with_its_adds():
+    text = open(os.path.join(EX, "histogram.py")).read()
+    args = {"cx": -0.745, "cy": 0.11, "scale": 0.004}
+    low, names = lower_named(text, "escape", args)
+    assert low.kind == "pixel_program" and names[id(low.field)] == "counts"
+    assert low.program.out_kind == pp.OUT_COUNT and [names[id(f)] for f in low.inputs] == ["hist", "total"]
+    arrays = {"counts": None, "hist": np.zeros(201, np.int32), "total": np.zeros((), np.int32)}
+    run_ops(low, names, arrays)
+    counts = arrays["counts"]
+    assert np.array_equal(counts, escape_counts(640, 480, 200, *args.values()))
+    assert np.array_equal(arrays["hist"], np.bincount(counts.ravel(), minlength=201))
+    assert int(arrays["total"]) == int(counts.sum())
+    shade, names2 = lower_named(text, "shade", {})
+    k = [names2[id(f)] for f in shade.inputs].index("cdf")  # cdf[counts[i, j]]: a gather in cdf's own grid
+    assert shade.program.in_rows[k] == 1 and shade.program.in_cols[k] == 201
+
+
+def weights(fx):
+    """The quadratic B-spline weights of the splat example, per axis (f32, its operation order)."""
+    return [f32(0.5) * ((f32(1.5) - fx) * (f32(1.5) - fx)), f32(0.75) - (fx - f32(1.0)) * (fx - f32(1.0)),
+            f32(0.5) * ((fx - f32(0.5)) * (fx - f32(0.5)))]
+
+
+def splat_nodes(x, G):
+    """Per particle and node (i, j) of ti.ndrange(3, 3): row, column and weight, [N][3][3]."""
+    xs = x * f32(G)
+    base = np.trunc(xs - f32(0.5))
+    w = weights(xs - base)
+    i, j = np.meshgrid(np.arange(3), np.arange(3), indexing="ij")
+    rows = base[:, 0, None, None].astype(np.int64) + i
+    cols = base[:, 1, None, None].astype(np.int64) + j
+    wt = np.stack([np.stack([w[a][:, 0] * w[b][:, 1] for b in range(3)], -1) for a in range(3)], -2)
+    return rows, cols, wt
+
+
+def test_splat_p2g_equals_sequential_numpy_adds():
+    """The splat example's particle-to-grid kernel (quadratic B-spline weights, base + offset
+    vector indices, a scalar and a vector target) against its numpy restatement, adding in the
+    oracle's order: particle by particle, the nine nodes in ti.ndrange order (np.add.at over the
+    [N][3][3] arrays raveled in C order adds in that order)."""
+    text = open(os.path.join(EX, "splat.py")).read()
+    low, names = lower_named(text, "p2g", {})
+    assert low.kind == "pixel_program" and low.field is None and low.program.out_kind == pp.OUT_NONE
+    N, G = 8192, 128
+    rng = np.random.default_rng(9)
+    x = (rng.random((N, 2)) * 0.9 + 0.05).astype(f32)  # every node inside the grid
+    v = rng.standard_normal((N, 2)).astype(f32)
+    arrays = {"x": x, "v": v, "grid_m": np.zeros((G, G), f32), "grid_v": np.zeros((G, G, 2), f32)}
+    run_ops(low, names, arrays)
+    rows, cols, wt = splat_nodes(x, G)
+    gm, gv = np.zeros((G, G), f32), np.zeros((G, G, 2), f32)
+    idx = (rows.ravel(), cols.ravel())
+    np.add.at(gm, idx, wt.ravel())
+    for c in range(2):
+        np.add.at(gv[:, :, c], idx, (wt * v[:, c, None, None]).ravel())
+    assert np.array_equal(arrays["grid_m"], gm) and np.array_equal(arrays["grid_v"], gv)
+    assert abs(float(gm.sum(dtype=np.float64)) - N) < 1e-2  # the weights of a particle sum to 1
+
+
+def test_splat_g2p_gathers_at_vector_indices():
+    text = open(os.path.join(EX, "splat.py")).read()
+    low, names = lower_named(text, "g2p", {})
+    assert [names[id(o.field)] for o in low.ops()] == ["v", "x"]
+    N, G = 8192, 128
+    rng = np.random.default_rng(10)
+    x = (rng.random((N, 2)) * 0.9 + 0.05).astype(f32)  # every node inside the grid
+    gv = rng.standard_normal((G, G, 2)).astype(f32)
+    arrays = {"x": x.copy(), "v": np.zeros((N, 2), f32), "grid_v": gv}
+    run_ops(low, names, arrays)
+    rows, cols, wt = splat_nodes(x, G)
+    want = np.zeros((N, 2), f32)
+    for i in range(3):
+        for j in range(3):  # new_v += w * grid_v[...], node by node
+            want = want + wt[:, i, j, None] * gv[rows[:, i, j], cols[:, i, j]]
+    assert np.array_equal(arrays["v"], want)
+    assert np.array_equal(arrays["x"], x + f32(2e-4) * want)
+
+
+KERNELS = """import taichi as ti
+a = ti.field(dtype=float, shape=(16, 12))
+cnt = ti.field(dtype=int, shape=(4, 3))
+acc = ti.field(dtype=float, shape=8)
+vol = ti.field(dtype=int, shape=(3, 4, 5))
+s = ti.field(dtype=float, shape=())
+out = ti.field(dtype=float, shape=(16, 12))
+
+@ti.kernel
+def branchy():
+    for i, j in a:
+        if a[i, j] > 0.5:
+            cnt[i % 4, j % 3] += 1
+        else:
+            ti.atomic_sub(acc[i % 8], a[i, j])
+        ti.atomic_add(s[None], 1.0)
+
+@ti.kernel
+def three_d():
+    for i, j in a:
+        vol[i - 2, j - 3, (i + j) % 7] += 1
+
+@ti.kernel
+def store_and_add():
+    for i, j in a:
+        out[i, j] = a[i, j] * 2.0
+        a[i, j] = a[i, j] + 1.0
+        acc[j % 8] += out[i, j]
+
+@ti.kernel
+def read_total():
+    for i, j in out:
+        out[i, j] = s[None] + i
+"""
+
+
+def test_adds_in_branches_happen_where_the_branch_runs():
+    low, names = lower_named(KERNELS, "branchy", {})
+    rng = np.random.default_rng(11)
+    a = rng.random((16, 12)).astype(f32)
+    arrays = {"a": a, "cnt": np.zeros((4, 3), np.int32), "acc": np.zeros(8, f32), "s": np.zeros((), f32)}
+    run_ops(low, names, arrays)
+    i, j = np.meshgrid(np.arange(16), np.arange(12), indexing="ij")
+    hi = a > f32(0.5)
+    want_cnt = np.zeros((4, 3), np.int64)
+    np.add.at(want_cnt, ((i % 4)[hi], (j % 3)[hi]), 1)
+    want_acc = np.zeros(8, f32)
+    np.add.at(want_acc, (i % 8)[~hi], -a[~hi])  # row-major order, as the oracle adds
+    assert np.array_equal(arrays["cnt"], want_cnt.astype(np.int32))
+    assert np.array_equal(arrays["acc"], want_acc)
+    assert float(arrays["s"]) == 16 * 12
+
+
+def test_three_d_target_drops_each_axis_on_its_own():
+    """vol[i - 2, j - 3, (i + j) % 7] of a [3][4][5] field: an index past one axis is dropped,
+    not carried into the next (as flattening [A B][C] alone would do)."""
+    low, names = lower_named(KERNELS, "three_d", {})
+    arrays = {"a": np.zeros((16, 12), f32), "vol": np.zeros((3, 4, 5), np.int32)}
+    run_ops(low, names, arrays)
+    want = np.zeros((3, 4, 5), np.int64)
+    for i in range(16):
+        for j in range(12):
+            a_, b_, c_ = i - 2, j - 3, (i + j) % 7
+            if 0 <= a_ < 3 and 0 <= b_ < 4 and 0 <= c_ < 5:
+                want[a_, b_, c_] += 1
+    assert np.array_equal(arrays["vol"], want.astype(np.int32))
+
+
+def test_a_body_that_stores_two_fields_runs_its_adds_once():
+    low, names = lower_named(KERNELS, "store_and_add", {})
+    ops = low.ops()
+    assert sum(o.field is None for o in ops) == 1  # one program of the adds, beside the stores
+    rng = np.random.default_rng(12)
+    a0 = rng.random((16, 12)).astype(f32)
+    arrays = {"a": a0.copy(), "out": np.zeros((16, 12), f32), "acc": np.zeros(8, f32)}
+    run_ops(low, names, arrays)
+    assert np.array_equal(arrays["out"], a0 * f32(2.0)) and np.array_equal(arrays["a"], a0 + f32(1.0))
+    want = np.zeros(8, f32)
+    j = np.broadcast_to(np.arange(12), (16, 12))
+    np.add.at(want, (j % 8).ravel(), (a0 * f32(2.0)).ravel())  # the adds read a before its store
+    assert np.array_equal(arrays["acc"], want)
+
+
+def test_zero_d_field_read_in_a_kernel():
+    low, names = lower_named(KERNELS, "read_total", {})
+    assert low.program.in_rows[0] == 1 and low.program.in_cols[0] == 1
+    arrays = {"out": np.zeros((16, 12), f32), "s": np.array(2.5, f32)}
+    run_ops(low, names, arrays)
+    assert np.array_equal(arrays["out"], f32(2.5) + np.arange(16, dtype=f32)[:, None] + np.zeros((1, 12), f32))
+
+
+@pytest.mark.parametrize("body, msg", [
+    ("        cnt[i % 4, j % 3] += 1\n        a[i, j] = cnt[0, 0] * 1.0", "also read"),
+    ("        a[i, j] = 1.0\n        a[i + 1, j] += 1.0", "both stored"),
+    ("        k = 0\n        while k < 3:\n            acc[k] += 1.0\n            k += 1", "inside a runtime loop"),
+    ("        acc[i % 8] *= 2.0", "only += and -="),
+    ("        x = ti.atomic_add(acc[0], 1.0)", "as a statement"),
+])
+def test_scatter_forms_refused(body, msg):
+    text = KERNELS.split("@ti.kernel")[0] + "@ti.kernel\ndef bad():\n    for i, j in a:\n" + body + "\n"
+    with pytest.raises(tc.TaichiLoweringError, match=re.escape(msg)):
+        lower_named(text, "bad", {})

@@ -31,7 +31,8 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
   if (p.test < VDSL_PIX_TEST_NONE || p.test > VDSL_PIX_TEST_GE) return fail(VDSL_ERR_INVALID_ARG, "pixel program: unknown test");
   if (p.test_a < 0 || p.test_a >= VDSL_PIX_MAX_REGS || p.test_b < 0 || p.test_b >= VDSL_PIX_MAX_REGS)
     return fail(VDSL_ERR_INVALID_ARG, "pixel program: test register out of range");
-  if (p.out_kind != VDSL_PIX_OUT_REG && p.out_kind != VDSL_PIX_OUT_COUNT && p.out_kind != VDSL_PIX_OUT_I32)
+  if (p.out_kind != VDSL_PIX_OUT_REG && p.out_kind != VDSL_PIX_OUT_COUNT && p.out_kind != VDSL_PIX_OUT_I32 &&
+      p.out_kind != VDSL_PIX_OUT_NONE)
     return fail(VDSL_ERR_INVALID_ARG, "pixel program: unknown out_kind");
   if (p.out_width < 1 || p.out_width > 4 || (p.out_kind != VDSL_PIX_OUT_REG && p.out_width != 1))
     return fail(VDSL_ERR_INVALID_ARG, "pixel program: out_width must be 1..4 (1 for an int32 field)");
@@ -51,7 +52,7 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
     const vdsl_map_instr& s = p.code[pc];
     const std::string at = "pixel program: instruction " + std::to_string(pc);
     const bool map_op = s.op >= VDSL_MAP_LOAD && s.op <= VDSL_MAP_ADD_IMM;
-    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_TRIP;
+    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_TRUNC;
     if (!map_op && !pix_op) return fail(VDSL_ERR_INVALID_ARG, at + ": unknown opcode " + std::to_string(s.op));
     if (s.dst >= VDSL_PIX_MAX_REGS || s.b >= VDSL_PIX_MAX_REGS || s.c >= VDSL_PIX_MAX_REGS)
       return fail(VDSL_ERR_INVALID_ARG, at + ": register out of range");
@@ -64,6 +65,18 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
       const bool comp_ok = s.a < n_inputs && s.imm >= 0.0f && s.imm < static_cast<float>(p.in_widths[s.a]) &&
                            s.imm == static_cast<float>(static_cast<int>(s.imm));
       if (!comp_ok) return fail(VDSL_ERR_INVALID_ARG, at + ": LOAD_AT of an input or component that is not there");
+    } else if (s.op == VDSL_PIX_ATOMIC_ADD) {
+      const bool comp_ok = s.a < n_inputs && s.imm >= 0.0f && s.imm < static_cast<float>(p.in_widths[s.a]) &&
+                           s.imm == static_cast<float>(static_cast<int>(s.imm));
+      if (!comp_ok) return fail(VDSL_ERR_INVALID_ARG, at + ": ATOMIC_ADD to an input or component that is not there");
+      if (pc >= p.n_pre && pc < post0)
+        return fail(VDSL_ERR_INVALID_ARG, at + ": ATOMIC_ADD in the loop's sections (pre and post only)");
+      for (int q = 0; q < total; ++q) {
+        const vdsl_map_instr& l = p.code[q];
+        if ((l.op == VDSL_MAP_LOAD || l.op == VDSL_PIX_LOAD_AT) && l.a == s.a)
+          return fail(VDSL_ERR_INVALID_ARG, at + ": ATOMIC_ADD to an input the program also reads (instruction " +
+                                                std::to_string(q) + ")");
+      }
     } else if (s.op == VDSL_PIX_INDEX) {
       if (s.a > 1) return fail(VDSL_ERR_INVALID_ARG, at + ": INDEX axis must be 0 (i) or 1 (j)");
     } else if (s.a >= VDSL_PIX_MAX_REGS) {
@@ -110,26 +123,46 @@ int reads(int op) {
     case VDSL_MAP_ADD: case VDSL_MAP_SUB: case VDSL_MAP_MUL: case VDSL_MAP_DIV: case VDSL_MAP_MAX: case VDSL_MAP_MIN:
     case VDSL_PIX_LT: case VDSL_PIX_LE: case VDSL_PIX_EQ: case VDSL_PIX_NE: return 3;  // a, b
     case VDSL_MAP_FMA: case VDSL_PIX_SELECT: return 7;  // a, b, c
+    case VDSL_PIX_ATOMIC_ADD: return 6;  // b, c (and the value r[dst]; no register written)
     default: return 1;  // a
   }
 }
 
-// Gathers (LOAD_AT) whose row operand (bit 0 of the flag) or column operand (bit 1) is the same on
+// Gathers (LOAD_AT) and scatter-adds (ATOMIC_ADD) whose row operand (bit 0 of the flag) or column operand (bit 1) is the same on
 // every lane of a wave in the row mapping, where a wave covers 64 pixels of one row and every lane
 // makes every trip of a loop (the mapping has no escape loops): registers computed only from the
 // row index i (INDEX 0), the loop's trip, constants and immediates.  Their row offset is then formed once per wave on the scalar unit.
 // A forward pass over the sections (the loop's to a fixed point, joined with the state before it);
 // loads, the column index and the count make a register vary, conservatively.
+//
+// Bit 2 marks a scatter-add whose row and column are both constants (computed from constants and
+// immediates alone, in the pre or post section), the same on every lane in any mapping.
 std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   std::vector<char> flag(total, 0);
   bool uni[VDSL_PIX_MAX_REGS];
   for (bool& u : uni) u = true;  // registers start at 0
+  bool cst[VDSL_PIX_MAX_REGS];     // constants, pre and post sections
+  for (bool& c : cst) c = true;
+  auto const_step = [&](int pc) {
+    const vdsl_map_instr& s = p.code[pc];
+    const int rd = reads(s.op);
+    if (s.op == VDSL_PIX_ATOMIC_ADD) {
+      if (cst[s.b] && cst[s.c]) flag[pc] = static_cast<char>(flag[pc] | 4);
+      return;
+    }
+    const bool in_cst = (!(rd & 1) || cst[s.a]) && (!(rd & 2) || cst[s.b]) && (!(rd & 4) || cst[s.c]);
+    const bool var = s.op == VDSL_MAP_LOAD || s.op == VDSL_PIX_LOAD_AT || s.op == VDSL_PIX_INDEX ||
+                     s.op == VDSL_PIX_COUNT || s.op == VDSL_PIX_TRIP;
+    cst[s.dst] = !var && in_cst;
+  };
   auto step = [&](int pc, bool* st) {
     const vdsl_map_instr& s = p.code[pc];
     const int rd = reads(s.op);
     const bool in_uni = (!(rd & 1) || st[s.a]) && (!(rd & 2) || st[s.b]) && (!(rd & 4) || st[s.c]);
-    if (s.op == VDSL_PIX_LOAD_AT) flag[pc] = static_cast<char>((st[s.b] ? 1 : 0) | (st[s.c] ? 2 : 0));
+    if (s.op == VDSL_PIX_LOAD_AT || s.op == VDSL_PIX_ATOMIC_ADD)
+      flag[pc] = static_cast<char>((st[s.b] ? 1 : 0) | (st[s.c] ? 2 : 0));
+    if (s.op == VDSL_PIX_ATOMIC_ADD) return;  // writes no register
     bool out;
     if (s.op == VDSL_MAP_CONST || s.op == VDSL_PIX_TRIP) out = true;  // the trip is the same on every lane
     else if (s.op == VDSL_PIX_INDEX) out = s.a == 0;
@@ -137,7 +170,10 @@ std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
     else out = in_uni;
     st[s.dst] = out;
   };
-  for (int pc = 0; pc < p.n_pre; ++pc) step(pc, uni);
+  for (int pc = 0; pc < p.n_pre; ++pc) step(pc, uni), const_step(pc);
+  // after the loop, a register it writes is no constant
+  for (int pc = p.n_pre; pc < p.n_pre + p.n_test + p.n_body; ++pc)
+    if (p.code[pc].op != VDSL_PIX_ATOMIC_ADD) cst[p.code[pc].dst] = false;
   if (p.loop) {
     bool head[VDSL_PIX_MAX_REGS];
     for (int r = 0; r < VDSL_PIX_MAX_REGS; ++r) head[r] = uni[r];
@@ -158,7 +194,7 @@ std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
     for (int pc = p.n_pre; pc < p.n_pre + p.n_test + p.n_body; ++pc) step(pc, st);  // the loop's flags, at the fixed point
     for (int r = 0; r < VDSL_PIX_MAX_REGS; ++r) uni[r] = head[r] && after_test[r];  // the loop ends after a test, or at max_iter
   }
-  for (int pc = p.n_pre + p.n_test + p.n_body; pc < total; ++pc) step(pc, uni);
+  for (int pc = p.n_pre + p.n_test + p.n_body; pc < total; ++pc) step(pc, uni), const_step(pc);
   return flag;
 }
 
@@ -193,7 +229,8 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni, in
   list("out_regs", p.out_regs, p.out_width, 0);
   list("in_widths", p.in_widths, n_inputs, 1);
   list("in_dtypes", p.in_dtypes, n_inputs, VDSL_F32);
-  // ext[0] / ext[1] of a gather: 1 when its row / column operand is wave-uniform in the row mapping
+  // ext[0] / ext[1] of a gather or scatter-add: 1 when its row / column operand is wave-uniform in
+  // the row mapping; ext[2] of a scatter-add: 1 when both are constants
   const std::vector<char> ru = row_uniform_gathers(p);
   s += "  static constexpr vdsl_map_instr code[VDSL_PIX_MAX_INSTR] = {\n";
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
@@ -201,7 +238,7 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni, in
     const vdsl_map_instr& k = p.code[pc];
     s += "    {" + std::to_string(k.op) + ", " + std::to_string(k.dst) + ", " + std::to_string(k.a) + ", " + std::to_string(k.b) +
          ", " + std::to_string(k.c) + ", {" + std::to_string(ru[pc] & 1) + ", " + std::to_string((ru[pc] >> 1) & 1) +
-         ", 0}, 0.f},\n";
+         ", " + std::to_string((ru[pc] >> 2) & 1) + "}, 0.f},\n";
   }
   s += "  };\n};\n}  // namespace vdsl\n";
   s += "extern \"C\" __global__ __launch_bounds__(256) void vdsl_pix_jit(vdsl::PixRt rt, vdsl::PixIn in, void* out, int ni, "
@@ -223,19 +260,24 @@ extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const
   if (n_inputs && !inputs) return fail(VDSL_ERR_INVALID_ARG, "inputs is null");
   const vdsl_pixel_program& p = *prog;
   VDSL_TRY(check_program(p, n_inputs));
-  VDSL_TRY(check_buffer(q, out, nbytes(ni, nj, 4 * p.out_width), "out", true));
+  if (p.out_kind != VDSL_PIX_OUT_NONE) VDSL_TRY(check_buffer(q, out, nbytes(ni, nj, 4 * p.out_width), "out", true));
+  bool target[VDSL_PIX_MAX_INPUTS] = {};  // inputs the program scatter-adds into (written)
+  const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
+  for (int pc = 0; pc < total; ++pc)
+    if (p.code[pc].op == VDSL_PIX_ATOMIC_ADD) target[p.code[pc].a] = true;
   PixIn in{};
   for (int k = 0; k < n_inputs; ++k) {
     const std::string name = "input" + std::to_string(k);
     in.rows[k] = p.in_rows[k] ? p.in_rows[k] : ni;
     in.cols[k] = p.in_cols[k] ? p.in_cols[k] : nj;
-    VDSL_TRY(check_buffer(q, inputs[k], nbytes(in.rows[k], in.cols[k], 4 * p.in_widths[k]), name.c_str(), false));
+    VDSL_TRY(check_buffer(q, inputs[k], nbytes(in.rows[k], in.cols[k], 4 * p.in_widths[k]), name.c_str(), target[k]));
+    if (target[k] && p.out_kind != VDSL_PIX_OUT_NONE && inputs[k] == out)
+      return fail(VDSL_ERR_INVALID_ARG, "pixel program: " + name + " is scatter-added into and is also the output");
     in.p[k] = static_cast<const float*>(inputs[k]->ptr);
   }
   if (ni == 0 || nj == 0) return VDSL_OK;
   if ((ni + 15) / 16 > 65535) return fail(VDSL_ERR_UNSUPPORTED, "pixel program: ni too large");
   PixRt rt{};
-  const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   for (int pc = 0; pc < total; ++pc) rt.imm[pc] = p.code[pc].imm;
   rt.max_iter = p.max_iter;
   const std::string src = program_source(p, n_inputs, ni, nj);
@@ -245,7 +287,7 @@ extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const
   if (st == VDSL_ERR_UNSUPPORTED && q->capturing)
     return fail(VDSL_ERR_CAPTURE, "pixel program: not compiled yet; run it once before recording a graph");
   VDSL_TRY(st);
-  void* o = out->ptr;
+  void* o = p.out_kind == VDSL_PIX_OUT_NONE ? nullptr : out->ptr;
   void* args[] = {&rt, &in, &o, &ni, &nj};
   const int rows = row_mapping(p, ni);
   const unsigned gx = rows ? static_cast<unsigned>((nj + 255) / 256) : static_cast<unsigned>((nj + 15) / 16);

@@ -82,11 +82,74 @@ __device__ __forceinline__ int pix_to_i32(float x) {
   return static_cast<int>(x);
 }
 
+// Wave sums for scatter-adds at wave-uniform indices (every lane of the wave takes part; lanes
+// that add nothing hold 0).  Lane l adds lane l ^ m's value, m = 32, 16, ..., 1.
+__device__ __forceinline__ int pix_lane() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+__device__ __forceinline__ float pix_wave_sum(float v) {
+  const int lane = pix_lane();
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1)
+    v += __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ m) << 2, __float_as_int(v)));
+  return v;
+}
+
+__device__ __forceinline__ int pix_wave_sum(int v) {
+  const int lane = pix_lane();
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1)  // wrapping, as the atomic adds themselves
+    v = static_cast<int>(static_cast<unsigned>(v) + static_cast<unsigned>(__builtin_amdgcn_ds_bpermute((lane ^ m) << 2, v)));
+  return v;
+}
+
+// VDSL_PIX_ATOMIC_ADD into input A: component c of [x][y] += v where 0 <= x < rows and
+// 0 <= y < cols (A's extents) on lanes with act set.  UNI: x and y are the same on every lane of
+// the wave (host dataflow, row mapping), so the wave's values are summed and one lane adds.
+template <class P, int A, bool UNI>
+__device__ __forceinline__ void pix_scatter_add(const PixIn& in, float x, float y, float v, int c, bool act) {
+  // NaN fails every comparison; below 2^30 the conversion is exact truncation, and the row and
+  // column are then checked as integers (float(rows) may round above 2^24)
+  const bool num = x >= 0.0f && x < 1073741824.0f && y >= 0.0f && y < 1073741824.0f;
+  const int xi = num ? static_cast<int>(x) : 0, yi = num ? static_cast<int>(y) : 0;
+  const bool ok = act && num && xi < in.rows[A] && yi < in.cols[A];
+  const PixOff<P> e = static_cast<PixOff<P>>(static_cast<unsigned>(xi)) * static_cast<unsigned>(in.cols[A]) +
+                      static_cast<unsigned>(yi);
+  char* base = const_cast<char*>(reinterpret_cast<const char*>(in.p[A]));
+  if constexpr (P::in_dtypes[A] == VDSL_I32) {
+    int* t = reinterpret_cast<int*>(base) + e;
+    int add = ok ? pix_to_i32(v) : 0;
+    if constexpr (UNI) {
+      const uint64_t any = __builtin_amdgcn_ballot_w64(ok);
+      if (any == 0ull) return;
+      add = pix_wave_sum(add);
+      if (pix_lane() == __builtin_ctzll(any)) atomicAdd(t, add);
+    } else {
+      if (ok) atomicAdd(t, add);
+    }
+  } else {
+    float* t = reinterpret_cast<float*>(base) + (e * static_cast<PixOff<P>>(P::in_widths[A]) + static_cast<PixOff<P>>(c));
+    float add = ok ? v : 0.0f;
+    if constexpr (UNI) {
+      const uint64_t any = __builtin_amdgcn_ballot_w64(ok);
+      if (any == 0ull) return;
+      add = pix_wave_sum(add);
+      if (pix_lane() == __builtin_ctzll(any)) unsafeAtomicAdd(t, add);
+    } else {
+      if (ok) unsafeAtomicAdd(t, add);
+    }
+  }
+}
+
 template <class P, int PC>
 __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
-                                         float fi, float fj, float fcount, int ni, int nj) {
+                                         float fi, float fj, float fcount, int ni, int nj, bool act) {
   constexpr vdsl_map_instr s = P::code[PC];
-  if constexpr (s.op == VDSL_MAP_LOAD) {
+  if constexpr (s.op == VDSL_PIX_ATOMIC_ADD) {
+    // one add per wave where both indices are the same on every lane: found wave-uniform by the
+    // host in the row mapping (ext[0], ext[1]), or constants in any mapping (ext[2])
+    constexpr bool uni = (P::rows > 0 && s.ext[0] != 0 && s.ext[1] != 0) || s.ext[2] != 0;
+    pix_scatter_add<P, s.a, uni>(in, r[s.b], r[s.c], r[s.dst], static_cast<int>(rt.imm[PC]), act);
+  } else if constexpr (s.op == VDSL_MAP_LOAD) {
     r[s.dst] = pix_load<P, s.a>(in, o, s.c);
   } else if constexpr (s.op == VDSL_PIX_LOAD_AT) {
     // indices clamped to the input's own extents (the grid's, unless it is a field of another shape)
@@ -118,6 +181,8 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
     r[s.dst] = r[s.a] != 0.0f ? r[s.b] : r[s.c];
   } else if constexpr (s.op == VDSL_PIX_FLOOR) {
     r[s.dst] = floorf(r[s.a]);
+  } else if constexpr (s.op == VDSL_PIX_TRUNC) {
+    r[s.dst] = truncf(r[s.a]);
   } else {
     r[s.dst] = apply_op(s.op, r[s.a], r[s.b], r[s.c], rt.imm[PC]);
   }
@@ -125,8 +190,8 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
 
 template <class P, int BASE, int... K>
 __device__ __forceinline__ void pix_section(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
-                                            float fi, float fj, float fcount, int ni, int nj, Seq<K...>) {
-  (pix_step<P, BASE + K>(rt, in, r, o, fi, fj, fcount, ni, nj), ...);
+                                            float fi, float fj, float fcount, int ni, int nj, bool act, Seq<K...>) {
+  (pix_step<P, BASE + K>(rt, in, r, o, fi, fj, fcount, ni, nj, act), ...);
 }
 
 template <int TEST>
@@ -147,8 +212,14 @@ __device__ constexpr uint32_t pix_reads(const vdsl_map_instr& s) {
       return (1u << s.a) | (1u << s.b);
     case VDSL_PIX_LOAD_AT: return (1u << s.b) | (1u << s.c);
     case VDSL_MAP_FMA: case VDSL_PIX_SELECT: return (1u << s.a) | (1u << s.b) | (1u << s.c);
+    case VDSL_PIX_ATOMIC_ADD: return (1u << s.dst) | (1u << s.b) | (1u << s.c);  // the value is r[dst]
     default: return 1u << s.a;
   }
+}
+
+// Register an instruction writes (a bit); a scatter-add writes none.
+__device__ constexpr uint32_t pix_writes(const vdsl_map_instr& s) {
+  return s.op == VDSL_PIX_ATOMIC_ADD ? 0u : 1u << s.dst;
 }
 
 // Register sets of program P (instructions [lo, hi) of its table): written, and read before
@@ -158,14 +229,14 @@ struct PixSets {
   static constexpr int t0 = P::n_pre, b0 = t0 + P::n_test, q0 = b0 + P::n_body, end = q0 + P::n_post;
   static constexpr uint32_t writes(int lo, int hi) {
     uint32_t w = 0u;
-    for (int pc = lo; pc < hi; ++pc) w |= 1u << P::code[pc].dst;
+    for (int pc = lo; pc < hi; ++pc) w |= pix_writes(P::code[pc]);
     return w;
   }
   static constexpr uint32_t rbw(int lo, int hi) {
     uint32_t w = 0u, r = 0u;
     for (int pc = lo; pc < hi; ++pc) {
       r |= pix_reads(P::code[pc]) & ~w;
-      w |= 1u << P::code[pc].dst;
+      w |= pix_writes(P::code[pc]);
     }
     return r;
   }
@@ -174,7 +245,7 @@ struct PixSets {
   static constexpr uint32_t loop_w = test_w | body_w;
   static constexpr uint32_t stored() {
     uint32_t m = 0u;
-    if (P::out_kind != VDSL_PIX_OUT_COUNT)
+    if (P::out_kind != VDSL_PIX_OUT_COUNT && P::out_kind != VDSL_PIX_OUT_NONE)
       for (int k = 0; k < P::out_width; ++k) m |= 1u << P::out_regs[k];
     return m;
   }
@@ -193,10 +264,11 @@ struct PixSets {
   static constexpr bool periodic = free_running && carried != 0u && !reads_trip();
 };
 
+// act: the pixel lies in the grid (its scatter-adds happen); the loop's sections have none.
 template <class P, int BASE, int N>
 __device__ __forceinline__ void pix_run(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
-                                        float fi, float fj, float fcount, int ni, int nj) {
-  pix_section<P, BASE>(rt, in, r, o, fi, fj, fcount, ni, nj, typename MakeSeq<N>::type{});
+                                        float fi, float fj, float fcount, int ni, int nj, bool act = false) {
+  pix_section<P, BASE>(rt, in, r, o, fi, fj, fcount, ni, nj, act, typename MakeSeq<N>::type{});
 }
 
 // r[k] <- r[k] where the lane's bit of `mask` is set, else old[k], for the registers in KEEP.
@@ -245,7 +317,7 @@ __device__ __forceinline__ void pixel_eval(const PixRt& rt, const PixIn& in, int
   float r[VDSL_PIX_MAX_REGS];
 #pragma unroll
   for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) r[k] = 0.0f;
-  pix_run<P, 0, P::n_pre>(rt, in, r, o, fi, fj, 0.0f, ni, nj);
+  pix_run<P, 0, P::n_pre>(rt, in, r, o, fi, fj, 0.0f, ni, nj, inside);
   int count = 0;
   if constexpr (P::loop && P::test == VDSL_PIX_TEST_NONE) {
     // No test: every lane makes max_iter trips; they run only if something after the loop reads
@@ -311,7 +383,7 @@ __device__ __forceinline__ void pixel_eval(const PixRt& rt, const PixIn& in, int
       }
     }
   }
-  pix_run<P, S::q0, P::n_post>(rt, in, r, o, fi, fj, static_cast<float>(count), ni, nj);
+  pix_run<P, S::q0, P::n_post>(rt, in, r, o, fi, fj, static_cast<float>(count), ni, nj, inside);
 #pragma unroll
   for (int k = 0; k < 4; ++k) res[k] = k < P::out_width ? r[P::out_regs[k]] : 0.0f;
   count_out = count;
@@ -322,6 +394,7 @@ __device__ __forceinline__ void pixel_eval(const PixRt& rt, const PixIn& in, int
 template <class P>
 __device__ __forceinline__ void pixel_store(void* __restrict__ out, int ni, int nj, int i, int j, const float (&res)[4],
                                             int count) {
+  if constexpr (P::out_kind == VDSL_PIX_OUT_NONE) return;
   if (i >= ni || j >= nj) return;
   const PixOff<P> o = static_cast<PixOff<P>>(i) * static_cast<unsigned>(nj) + static_cast<unsigned>(j);
   char* base = static_cast<char*>(out);

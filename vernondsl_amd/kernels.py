@@ -267,27 +267,35 @@ def gemm_bf16_mul_packed(q: Queue, A: Tensor, Bp: Tensor, g: Tensor, c: Tensor, 
     call("vdsl_op_gemm_bf16_mul_packed", q.handle, M, N, K, A.handle, Bp.handle, g.handle, c.handle, _h(c_t))
 
 
-def pixel_program(q: Queue, prog, inputs, out: Tensor):
+def pixel_program(q: Queue, prog, inputs, out: Tensor | None, grid=None):
     """Runs a compiled per-pixel program (vernondsl_amd.pixprog.PixelProgram) over out's [ni][nj]
     grid: out f32 [ni][nj] or [ni][nj][out_width] (the program stores registers) or i32 [ni][nj]
     (it stores its loop count); inputs: f32 fields [ni][nj] or [ni][nj][in_widths[k]], read at
-    each pixel, or of their own extents [in_rows[k]][in_cols[k]] (gathered)."""
-    if len(out.shape) not in (2, 3):
-        raise ValueError("out must be a 2-D field of scalars or vectors")
-    ni, nj = out.shape[:2]
+    each pixel, or of their own extents [in_rows[k]][in_cols[k]] (gathered, or scatter-added
+    into).  A program that stores nothing (pixprog.OUT_NONE) takes out None and grid (ni, nj)."""
+    if prog.out_kind == 3:
+        if out is not None or grid is None or len(grid) != 2:
+            raise ValueError("a program that stores nothing takes out=None and grid=(ni, nj)")
+        ni, nj = (int(v) for v in grid)
+    else:
+        if out is None or len(out.shape) not in (2, 3):
+            raise ValueError("out must be a 2-D field of scalars or vectors")
+        ni, nj = out.shape[:2]
+        if grid is not None and tuple(grid) != (ni, nj):
+            raise ValueError(f"grid {tuple(grid)} is not out's [{ni}][{nj}]")
 
     def field_shape(w, r=ni, c=nj):
         return (r, c) if w == 1 else (r, c, w)
 
     if prog.out_kind in (1, 2):  # the loop count, or an int32 field
         _expect(out, (ni, nj), "i32", "out")
-    else:
+    elif prog.out_kind != 3:
         _expect(out, field_shape(prog.out_width), "f32", "out")
     for k, t in enumerate(inputs):
         r, c = (prog.in_rows[k], prog.in_cols[k]) if prog.in_rows[k] else (ni, nj)  # an input of its own extents
         _expect(t, field_shape(prog.in_widths[k], r, c), "i32" if prog.in_dtypes[k] == _lib.I32 else "f32", f"input{k}")
     hs = (C.c_void_p * max(1, len(inputs)))(*[t.handle for t in inputs])
-    call("vdsl_op_pixel_program", q.handle, ni, nj, C.byref(prog), hs, len(inputs), out.handle)
+    call("vdsl_op_pixel_program", q.handle, ni, nj, C.byref(prog), hs, len(inputs), _h(out))
 
 
 def mse_partials_count(rows, cols) -> int:

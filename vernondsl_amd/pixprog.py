@@ -26,13 +26,13 @@ from . import _lib
 MAX_INSTR, MAX_REGS, MAX_INPUTS = 128, 32, 4
 OP = dict(_lib.MAP_OPS)
 OP.update({"index": 32, "cos": 33, "sin": 34, "count": 35, "lt": 36, "le": 37, "eq": 38, "ne": 39, "select": 40,
-           "floor": 41, "load_at": 42, "trip": 43})
+           "floor": 41, "load_at": 42, "trip": 43, "atomic_add": 44, "trunc": 45})
 TESTS = {"none": 0, "lt": 1, "le": 2, "gt": 3, "ge": 4}
-OUT_REG, OUT_COUNT, OUT_I32 = 0, 1, 2
+OUT_REG, OUT_COUNT, OUT_I32, OUT_NONE = 0, 1, 2, 3
 F32, I32 = _lib.F32, _lib.I32  # input dtypes (vdsl_dtype)
 COUNT = "count"  # compile_program(out=COUNT): store the loop's update count (an int32 field)
 
-UNARY = ("neg", "abs", "sqrt", "exp", "log", "tanh", "sigmoid", "cos", "sin", "recip", "square", "floor")
+UNARY = ("neg", "abs", "sqrt", "exp", "log", "tanh", "sigmoid", "cos", "sin", "recip", "square", "floor", "trunc")
 BINARY = ("add", "sub", "mul", "div", "max", "min", "lt", "le", "eq", "ne")  # comparisons give 1.0 / 0.0
 TERNARY = ("fma", "select")  # select(c, a, b): a where c != 0 (NaN included), else b
 
@@ -115,6 +115,18 @@ class Builder:
         args = tuple(a if isinstance(a, Node) else self.const(a) for a in (row, col))
         return self._node("load_at", args, val=(int(k), int(component)))
 
+    def scatter_add(self, k: int, row, col, value, component: int = 0) -> Node:
+        """The effect `input k [row][col] (component) += value` (an atomic add; dropped where the
+        indices fall outside field k), for compile_program(effects=...)."""
+        if not 0 <= k < MAX_INPUTS:
+            raise ProgramError(f"at most {MAX_INPUTS} input fields")
+        if not 0 <= component < 4:
+            raise ProgramError("a field has at most 4 components")
+        args = tuple(a if isinstance(a, Node) else self.const(a) for a in (row, col, value))
+        # never merged with an equal one: two equal adds in a body are two adds
+        self._effects = getattr(self, "_effects", 0) + 1
+        return self._node("atomic_add", args, val=(int(k), int(component), self._effects))
+
     def state(self, name: str) -> Node:
         return self._node("state", val=name)
 
@@ -188,6 +200,9 @@ class _Emitter:
                 if a not in self.pinned and id(a) not in root_ids and last.get(id(a)) == pos and reg.get(id(a)) is not None:
                     free.append(reg[id(a)])
                     reg[id(a)] = None
+            if n.kind == "atomic_add":  # an effect: reads its operands, writes no register
+                self._instr(n, None, srcs)
+                continue
             if not free:
                 raise ProgramError(f"the program needs more than {MAX_REGS} registers")
             dst = min(free)
@@ -196,7 +211,7 @@ class _Emitter:
             self._instr(n, dst, srcs)
         out = {}
         for r in roots:
-            out[r] = self.pinned[r] if r in self.pinned else reg[id(r)]
+            out[r] = self.pinned[r] if r in self.pinned else reg.get(id(r))
         return out
 
     def _imm_arg(self, n):
@@ -220,6 +235,8 @@ class _Emitter:
             op, a, c = OP["load"], n.val[0], n.val[1]
         elif k == "load_at":
             op, a, b, c, imm = OP["load_at"], n.val[0], srcs[0], srcs[1], float(n.val[1])
+        elif k == "atomic_add":  # dst names the register of the value added
+            op, dst, a, b, c, imm = OP["atomic_add"], srcs[2], n.val[0], srcs[0], srcs[1], float(n.val[1])
         elif k == "count":
             op = OP["count"]
         elif k == "trip":
@@ -253,7 +270,7 @@ def _node_of(b: Builder, v) -> Node:
 
 def compile_program(b: Builder, init: dict | None = None, test=None, body: dict | None = None, max_iter: int = 0,
                     out=None, loop: bool | None = None, in_widths=(), in_dtypes=(), out_i32: bool = False,
-                    in_extents=()) -> PixelProgram:
+                    in_extents=(), effects=()) -> PixelProgram:
     """init: {state name: initial Node or number}; test: (op, lhs, rhs) with op in lt/le/gt/ge (None:
     no test), both sides per-pixel values; body: {state name: new value} (the parallel update of
     one loop trip; names not listed keep their value); max_iter: most updates; out: the stored
@@ -262,20 +279,30 @@ def compile_program(b: Builder, init: dict | None = None, test=None, body: dict 
     components per pixel of each input field (default 1); in_dtypes: F32 or I32 per input (an
     int32 field of one component, read as float); out_i32: store the (single) value into an int32
     field, truncating as a Taichi int field assignment does.  in_extents: (rows, cols) per input of
-    another shape than the grid (read only by load_at, clamped to those extents), or None."""
+    another shape than the grid (read only by load_at, clamped to those extents), or None.
+    effects: Builder.scatter_add nodes, run after the loop (their order is that of the list);
+    out may then be None (a program that stores nothing per pixel)."""
     init = dict(init or {})
     body = dict(body or {})
+    effects = list(effects)
     loop = bool(body or test) if loop is None else bool(loop)
-    if out is None:
+    if out is None and not effects:
         raise ProgramError("no output")
+    for e in effects:
+        if not isinstance(e, Node) or e.kind != "atomic_add":
+            raise ProgramError("effects are scatter_add nodes")
+        if "trip" in e.deps:
+            raise ProgramError("a scatter-add inside a runtime loop is not supported (only before or after it)")
+        if not loop and "count" in e.deps:
+            raise ProgramError("the count needs a loop")
     for name in body:
         if name not in init:
             raise ProgramError(f"loop state {name!r} has no initial value")
     state_names = list(init)
     nodes_test = [] if test is None else [_node_of(b, v) for v in test[1:]]
     nodes_body = [_node_of(b, body[nm]) for nm in body]
-    outs = [] if out is COUNT else [_node_of(b, v) for v in (out if isinstance(out, (list, tuple)) else [out])]
-    if out is not COUNT and not 1 <= len(outs) <= 4:
+    outs = [] if out is COUNT or out is None else [_node_of(b, v) for v in (out if isinstance(out, (list, tuple)) else [out])]
+    if out is not COUNT and out is not None and not 1 <= len(outs) <= 4:
         raise ProgramError("a pixel stores 1 to 4 components")
     out_node = outs[0] if outs else None
     init_nodes = [_node_of(b, init[nm]) for nm in state_names]
@@ -359,10 +386,14 @@ def compile_program(b: Builder, init: dict | None = None, test=None, body: dict 
             _move(code, r, pinned[b.state(nm)])
         n_body = len(code) - n_pre - n_test
     out_kind, out_regs = OUT_REG, [0]
+    # the post section: the stored value(s), and the effects (whose operands stay live only
+    # until their add; the stored registers are held to the end)
+    regs = _Emitter(code, pinned, reserved).emit(outs + effects)
     if out is COUNT:
         out_kind = OUT_COUNT
+    elif out is None:
+        out_kind = OUT_NONE
     else:
-        regs = _Emitter(code, pinned, reserved).emit(outs)
         out_regs = [regs[n] for n in outs]
         if out_i32:
             if len(outs) != 1:
@@ -411,5 +442,8 @@ def describe(p: PixelProgram) -> str:
     for k in range(total):
         s = p.code[k]
         sec = "pre" if k < p.n_pre else "test" if k < p.n_pre + p.n_test else "body" if k < p.n_pre + p.n_test + p.n_body else "post"
+        if s.op == OP["atomic_add"]:
+            lines.append(f"{sec:4s} input{s.a}[r{s.b}][r{s.c}].{int(s.imm)} += r{s.dst}")
+            continue
         lines.append(f"{sec:4s} r{s.dst} = {names.get(s.op, s.op)} a={s.a} b={s.b} c={s.c} imm={s.imm:g}")
     return "\n".join(lines)

@@ -49,6 +49,7 @@ from __future__ import annotations
 import ast
 import collections
 import inspect
+import itertools
 import math as _pymath
 import sys
 import textwrap
@@ -97,9 +98,9 @@ def _device():
 
 
 class Field:
-    """A dense 2-D field (fractal.py:8), or a 1-D one, of scalars or of vectors of `width` f32
-    components (ti.Vector.field).  Storage is a device tensor ([W][H], [N], plus [width] for
-    vectors), allocated and zeroed on first use."""
+    """A dense 2-D field (fractal.py:8), or a 0-D (shape ()), 1-D or 3-D one, of scalars or of
+    vectors of `width` f32 components (ti.Vector.field).  Storage is a device tensor ([W][H],
+    [N], [1] for 0-D, plus [width] for vectors), allocated and zeroed on first use."""
 
     def __init__(self, dtype, shape, width=1):
         if dtype in (float, f32, None):
@@ -110,7 +111,7 @@ class Field:
             raise TaichiLoweringError(f"field dtype {dtype!r}: only f32 and i32 fields are supported")
         if isinstance(shape, int):
             shape = (shape,)
-        self.shape = tuple(int(s) for s in shape)
+        self.shape = tuple(int(s) for s in (shape if shape is not None else ()))
         self.width = int(width)
         if not 1 <= self.width <= 4 or (self.width > 1 and self.dtype != f32):
             raise TaichiLoweringError("vector fields hold 1 to 4 f32 components")
@@ -128,16 +129,17 @@ class Field:
         if self._tensor is None:
             from .rhi import Tensor
             dev, q = _device()
-            t = Tensor(dev, self.shape if self.width == 1 else self.shape + (self.width,), self.dtype)
+            shape = self.shape or (1,)  # a 0-D field holds one element
+            t = Tensor(dev, shape if self.width == 1 else shape + (self.width,), self.dtype)
             t.buffer.fill_u32(q, 0)  # a Taichi field starts zeroed
             self._tensor = t
         return self._tensor
 
     def grid_tensor(self):
         """The tensor as a per-pixel program grid: a 1-D field of n elements is one row, [1][n]; a
-        3-D field [A][B][C] is [A B][C] (the same bytes)."""
+        3-D field [A][B][C] is [A B][C] (the same bytes); a 0-D field is [1][1]."""
         t = self.tensor()
-        if len(self.shape) == 1:
+        if len(self.shape) <= 1:
             return t.view((1,) + t.shape)
         if len(self.shape) == 3:
             return t.view((self.shape[0] * self.shape[1],) + t.shape[2:])
@@ -145,10 +147,31 @@ class Field:
 
     def to_numpy(self):
         _, q = _device()
-        return self.tensor().numpy(q)
+        a = self.tensor().numpy(q)
+        return a.reshape(a.shape[1:]) if not self.shape else a
+
+    def from_numpy(self, arr):
+        """Sets every element from an array of the field's shape (and component count)."""
+        want = self.shape if self.width == 1 else self.shape + (self.width,)
+        a = np.array(arr, np.int32 if self.dtype == i32 else np.float32, order="C")  # keeps a 0-D shape
+        if a.shape != want:
+            raise ValueError(f"from_numpy: array of shape {a.shape}, the field is {want}")
+        _, q = _device()
+        self.tensor().buffer.write(q, a.reshape(-1))
+
+    def fill(self, value):
+        """Sets every element (every component) to value."""
+        bits = np.array([value], np.int32 if self.dtype == i32 else np.float32).view(np.uint32)[0]
+        _, q = _device()
+        self.tensor().buffer.fill_u32(q, int(bits))
 
     def __getitem__(self, idx):
-        return self.to_numpy()[idx]
+        return self.to_numpy()[() if idx is None else idx]
+
+    def __setitem__(self, idx, value):
+        a = self.to_numpy()
+        a[() if idx is None else idx] = value
+        self.from_numpy(a)
 
 
 def field(dtype=float, shape=None, **_kw):
@@ -267,7 +290,8 @@ class Kernel:
             elif op.kind == "escape_time":
                 kernels.escape_time(q, kernels.escape_time_params(**op.params), op.field.tensor())
             else:
-                kernels.pixel_program(q, op.program, [f.grid_tensor() for f in op.inputs], op.field.grid_tensor())
+                out = op.field.grid_tensor() if op.field is not None else None  # None: scatter-adds only
+                kernels.pixel_program(q, op.program, [f.grid_tensor() for f in op.inputs], out, grid=op.grid)
 
 
 def _annotation(node):
@@ -761,7 +785,8 @@ def template():
 # ---- the general path: any struct-for body as a per-pixel register program ---------------------------
 class Lowered:
     """A lowered kernel: kind "escape_time" (field, params for vdsl_op_escape_time),
-    "pixel_program" (field, program for vdsl_op_pixel_program, input fields it reads), "copy"
+    "pixel_program" (field, program for vdsl_op_pixel_program, input fields it reads or
+    scatter-adds into, grid: its [ni][nj]; field None for a program of scatter-adds alone), "copy"
     (field = a copy of inputs[0]), or "sequence" (parts: Lowered ops run in order; a kernel of
     several struct-fors, or a struct-for storing several fields)."""
 
@@ -769,6 +794,7 @@ class Lowered:
         self.kind, self.field, self.params, self.program, self.inputs = kind, field, params, program, list(inputs)
         self.parts = list(parts)
         self.reads = list(inputs)  # the input fields a pixel program loads
+        self.grid = None
 
     def ops(self):
         """The escape-time and pixel-program ops this kernel runs, in order."""
@@ -850,6 +876,9 @@ class _PixInterp:
         self.ibound = {}
         self.in_loop = False
         self.unroll = True  # unroll short range loops whose variable is read (False: keep them loops)
+        self.targets = []  # fields the body scatter-adds into (also in inputs, never read)
+        self.scatters = []  # their adds (pixprog scatter_add effects), in program order
+        self.pred = None  # inside if branches: the condition under which a statement runs
 
     # -- values
     def node(self, v):
@@ -913,7 +942,7 @@ class _PixInterp:
             v = np.float32(x)
             with np.errstate(all="ignore"):
                 return {"neg": -v, "abs": np.abs(v), "sqrt": np.sqrt(v), "exp": np.exp(v), "log": np.log(v), "sin": np.sin(v),
-                        "cos": np.cos(v), "tanh": np.tanh(v), "floor": np.floor(v)}[fn]
+                        "cos": np.cos(v), "tanh": np.tanh(v), "floor": np.floor(v), "trunc": np.trunc(v)}[fn]
         r = self.b.op(fn, x)
         bx = self._ib(x)
         return self._int_result(r, bx, fn) if fn in ("neg", "abs", "floor") and bx is not None else r
@@ -942,6 +971,8 @@ class _PixInterp:
                 return v
             if n.id in self.env:
                 return self.env[n.id]
+            if n.id in _BUILTINS:  # int / float as values (a .cast(int) argument)
+                return _BUILTINS[n.id]
             raise TaichiLoweringError(f"unknown name {n.id!r}")
         if isinstance(n, ast.BinOp):
             ops = {ast.Add: "add", ast.Sub: "sub", ast.Mult: "mul", ast.Div: "div", ast.Pow: "pow"}
@@ -974,6 +1005,8 @@ class _PixInterp:
             idx = self.expr(n.slice, local)
             if isinstance(base, _PVec) and isinstance(idx, (int, np.integer)) and -len(base.comps) <= idx < len(base.comps):
                 return base.comps[int(idx)]
+            if isinstance(base, list) and isinstance(idx, (int, np.integer)) and -len(base) <= idx < len(base):
+                return base[int(idx)]  # a Python list of values (w[i] of a list of weight vectors)
             raise TaichiLoweringError("only constant vector indexing and field[i, j] reads are supported")
         if isinstance(n, ast.Attribute):
             base = self.expr(n.value, local)
@@ -1002,6 +1035,11 @@ class _PixInterp:
     def _is_here(self, idx):
         return [getattr(e, "id", None) for e in self._elts(idx)] == self.names
 
+    def _at_here(self, fld, idx):
+        """fld[idx] is this pixel's element of a field of the struct-for's shape."""
+        elts = list(idx.elts) if isinstance(idx, ast.Tuple) else [idx]
+        return tuple(fld.shape) == tuple(self.shape) and [getattr(e, "id", None) for e in elts] == self.names
+
     def _here(self):
         """The subscript of this pixel: (i, j), i, or (i, j, k)."""
         if len(self.names) == 1:
@@ -1012,15 +1050,11 @@ class _PixInterp:
         """fld[i, j] (this pixel), or fld[e1, e2] at per-pixel indices (a stencil or gather read,
         clamped to the field, whose shape must be the struct-for's); fld[i] / fld[e] in a 1-D
         struct-for, which runs as one row (row index 0)."""
+        if fld in self.targets:
+            raise TaichiLoweringError("a field scatter-added into is also read in the same struct-for")
         own = tuple(fld.shape) != tuple(self.shape)  # a field of another shape: gathered in its own grid
-        if own:
-            elts = list(idx.elts) if isinstance(idx, ast.Tuple) else [idx]
-            if len(elts) != len(fld.shape):
-                raise TaichiLoweringError(f"a field of shape {fld.shape} is indexed with {len(fld.shape)} indices")
-            here = False
-        else:
-            elts = self._elts(idx)
-            here = self._is_here(idx)
+        elts = list(idx.elts) if isinstance(idx, ast.Tuple) else [idx]
+        here = not own and [getattr(e, "id", None) for e in elts] == self.names
         if here and _skey(fld) in local:
             return local[_skey(fld)]  # the value this pixel stored earlier in the body
         if fld not in self.inputs:
@@ -1033,22 +1067,21 @@ class _PixInterp:
             if fld.width == 1:
                 return self.b.load(k)
             return _PVec([self.b.load(k, c) for c in range(fld.width)])
-        if len(elts) == 1:
-            row, col = 0.0, self.expr(elts[0], local)
-        elif len(elts) == 3:
+        vals = self._index_values(fld, idx, local)
+        if len(vals) == 0:  # a 0-D field
+            row, col = 0.0, 0.0
+        elif len(vals) == 1:
+            row, col = 0.0, vals[0]
+        elif len(vals) == 3:
             # [A][B][C] runs as [A B][C]: the row A-index * B + B-index, each clamped to its own
             # axis and truncated first (so an index past one axis does not run into the next)
-            a, b2, col = (self.expr(e, local) for e in elts)
-            if any(isinstance(v, _PVec) for v in (a, b2, col)):
-                raise TaichiLoweringError("field indices are scalars")
+            a, b2, col = vals
 
             def axis(v, n):
                 return self.unary("floor", self.minmax("min", [self.minmax("max", [v, 0.0]), float(n - 1)]))
             row = self.arith("add", self.arith("mul", axis(a, fld.shape[0]), float(fld.shape[1])), axis(b2, fld.shape[1]))
         else:
-            row, col = (self.expr(e, local) for e in elts)
-        if isinstance(row, _PVec) or isinstance(col, _PVec):
-            raise TaichiLoweringError("field indices are scalars")
+            row, col = vals
         row, col = self.node(row), self.node(col)
         if fld.width == 1:
             return self.b.load_at(k, row, col)
@@ -1069,6 +1102,8 @@ class _PixInterp:
                     return self.normalize(base)
                 if f.attr == "cross":
                     return self.cross(base, self.expr(n.args[0], local))
+                if f.attr == "cast":
+                    return self.cast(base, self.expr(n.args[0], local))
                 raise TaichiLoweringError(f"vector method {f.attr!r} is not supported")
             if f.attr == "Vector":
                 comps = self.expr(n.args[0], local)
@@ -1087,6 +1122,12 @@ class _PixInterp:
                 return self.unary("neg", self.unary("floor", self.unary("neg", self.expr(n.args[0], local))))
             if f.attr in ("max", "min"):
                 return self.minmax(f.attr, [self.expr(a, local) for a in n.args])
+            if f.attr == "cast":
+                if len(n.args) != 2:
+                    raise TaichiLoweringError("ti.cast takes (value, dtype)")
+                return self.cast(self.expr(n.args[0], local), self.expr(n.args[1], local))
+            if f.attr in ("atomic_add", "atomic_sub"):
+                raise TaichiLoweringError(f"ti.{f.attr} is supported as a statement (its old value is not returned)")
             raise TaichiLoweringError(f"call {f.attr!r} is not supported")
         if isinstance(f, ast.Name):
             fdef = self.funcs.get(f.id)
@@ -1099,6 +1140,8 @@ class _PixInterp:
                 if obj is float:
                     v = self.expr(n.args[0], local)
                     return _f32(v) if _is_num(v) else v
+                if obj is int:
+                    return self.cast(self.expr(n.args[0], local), int)
                 raise TaichiLoweringError(f"call of {f.id!r}: only @ti.func functions are inlined")
             args = [self.expr(a, local) for a in n.args]
             sub = dict(zip([a.arg for a in fdef.args.args], args))
@@ -1113,6 +1156,97 @@ class _PixInterp:
                 raise TaichiLoweringError(f"statement in @ti.func {f.id!r} is not supported")
             raise TaichiLoweringError(f"@ti.func {f.id!r} returns nothing")
         raise TaichiLoweringError("unsupported call")
+
+    def cast(self, v, dtype):
+        """ti.cast / .cast / int(): to an integer type truncates toward zero (Taichi's float ->
+        int conversion), to a float type keeps the value."""
+        if isinstance(v, _PVec):
+            return _PVec([self.cast(c, dtype) for c in v.comps])
+        if dtype in (float, f32, f64):
+            return _f32(v) if _is_num(v) and not isinstance(v, (int, np.integer)) else v
+        if dtype not in (int, i32):
+            raise TaichiLoweringError(f"cast to {dtype!r}: only int / ti.i32 and float / ti.f32")
+        if isinstance(v, (int, np.integer)) and not isinstance(v, bool):
+            return int(v)
+        if _is_num(v):
+            x = float(_f32(v))
+            if x != x or abs(x) >= 2.0 ** 31:
+                raise TaichiLoweringError(f"int({x}) is outside int32")
+            return int(x)
+        if self._ib(v) is not None:
+            return v  # already an integer
+        return self.unary("trunc", v)
+
+    def _index_values(self, fld, idx, local):
+        """The index values of fld[idx]: one per axis of fld (a tuple of expressions, one
+        expression, or one vector expression such as base + offset); () for a 0-D field."""
+        if not fld.shape:
+            if not ((isinstance(idx, ast.Constant) and idx.value is None) or (isinstance(idx, ast.Tuple) and not idx.elts)):
+                raise TaichiLoweringError("a 0-D field is indexed as field[None]")
+            return []
+        elts = list(idx.elts) if isinstance(idx, ast.Tuple) else [idx]
+        vals = [self.expr(e, local) for e in elts]
+        if len(vals) == 1 and isinstance(vals[0], _PVec):
+            vals = list(vals[0].comps)
+        if len(vals) != len(fld.shape):
+            raise TaichiLoweringError(f"a field of shape {fld.shape} is indexed with {len(vals)} indices")
+        if any(isinstance(v, (_PVec, list)) for v in vals):
+            raise TaichiLoweringError("field indices are scalars")
+        return vals
+
+    def scatter(self, fld, idx, value, local, negate=False):
+        """fld[idx] += value (-= with negate) at an index other than this pixel's: Taichi's atomic
+        add, an effect of the program (pixprog scatter_add), dropped where an index falls outside
+        fld.  The field must be neither stored nor read in the same struct-for (its reads would
+        race with the adds)."""
+        if self.in_loop:
+            raise TaichiLoweringError("a scatter-add (field[...] += v at another index) inside a runtime loop is not supported")
+        if fld in self.stored:
+            raise TaichiLoweringError("a field is both stored at the loop index and scatter-added into in one struct-for")
+        if fld in self.inputs and fld not in self.targets:
+            raise TaichiLoweringError("a field scatter-added into is also read in the same struct-for")
+        vals = self._index_values(fld, idx, local)
+        if len(vals) == 0:
+            row, col = 0.0, 0.0
+        elif len(vals) == 1:
+            row, col = 0.0, vals[0]
+        elif len(vals) == 2:
+            row, col = vals
+        else:
+            # [A][B][C] as [A B][C]: the row a * B + b where 0 <= a < A and 0 <= b < B, else -1 (the
+            # add is dropped); each axis truncated first, so b past B does not reach the next a
+            a, b2, col = vals
+            A, B = fld.shape[0], fld.shape[1]
+            a, b2 = self.cast(a, int), self.cast(b2, int)
+            ok = self.logic("and", [self.cmp_value("le", 0.0, a), self.cmp_value("lt", a, float(A)),
+                                    self.cmp_value("le", 0.0, b2), self.cmp_value("lt", b2, float(B))])
+            row = self.select(ok, self.arith("add", self.arith("mul", a, float(B)), b2), -1.0)
+        v = _PVec(value) if isinstance(value, list) else value
+        if fld.width == 1:
+            if isinstance(v, _PVec):
+                raise TaichiLoweringError("a field of scalars takes a scalar")
+            comps = [v]
+        elif isinstance(v, _PVec):
+            if len(v.comps) != fld.width:
+                raise TaichiLoweringError(f"a field of {fld.width}-vectors takes {fld.width} components")
+            comps = v.comps
+        else:
+            comps = [v] * fld.width
+        if fld not in self.inputs:
+            if len(self.inputs) == self.pp.MAX_INPUTS:
+                raise TaichiLoweringError(f"at most {self.pp.MAX_INPUTS} fields can be read or scatter-added into")
+            self.inputs.append(fld)
+            self.in_extents.append(_grid_of(fld.shape) if tuple(fld.shape) != tuple(self.shape) else None)
+        if fld not in self.targets:
+            self.targets.append(fld)
+        k = self.inputs.index(fld)
+        if self.pred is not None:  # in an if branch: a row of -1 drops the add where it does not run
+            row = self.select(self.pred, row, -1.0)
+        r, c = self.node(row), self.node(col)
+        for q, x in enumerate(comps):
+            if negate:
+                x = self.unary("neg", x)
+            self.scatters.append(self.b.scatter_add(k, r, c, self.node(x), q))
 
     def minmax(self, which, vals):
         if len(vals) < 2:
@@ -1305,11 +1439,17 @@ class _PixInterp:
                     raise TaichiLoweringError(f"statement at line {getattr(s2, 'lineno', '?')} is not supported")
             return
         branches = []
-        for stmts in (st.body, st.orelse):
+        outer = self.pred
+        for stmts, cond in ((st.body, self.truth(c)), (st.orelse, self.logic_not(c))):
             loc = dict(local)
-            for s2 in stmts:
-                if not self.assign(s2, loc):
-                    raise TaichiLoweringError(f"statement at line {getattr(s2, 'lineno', '?')} in an if is not supported")
+            # scatter-adds in a branch happen only where its condition holds
+            self.pred = cond if outer is None else self.logic("and", [outer, cond])
+            try:
+                for s2 in stmts:
+                    if not self.assign(s2, loc):
+                        raise TaichiLoweringError(f"statement at line {getattr(s2, 'lineno', '?')} in an if is not supported")
+            finally:
+                self.pred = outer
             branches.append(loc)
         lt, lf = branches
         for nm in list(dict.fromkeys(list(lt) + list(lf))):
@@ -1356,6 +1496,20 @@ class _PixInterp:
             if not all(isinstance(v, (int, np.integer)) for v in bounds):
                 raise TaichiLoweringError("ti.static(range(...)) needs integer constants")
             return list(range(*[int(v) for v in bounds]))
+        if isinstance(inner, ast.Call) and ((isinstance(inner.func, ast.Attribute) and inner.func.attr == "ndrange") or
+                                            (isinstance(inner.func, ast.Name) and inner.func.id == "ndrange")):
+            # ti.static(ti.ndrange(A, B, ...)): every index tuple, the last index fastest; an
+            # extent is n (0 .. n-1) or a pair (lo, hi)
+            axes = []
+            for a in inner.args:
+                v = self.expr(a, local)
+                if isinstance(v, (int, np.integer)) and not isinstance(v, bool):
+                    axes.append(range(int(v)))
+                elif isinstance(v, list) and len(v) == 2 and all(isinstance(x, (int, np.integer)) for x in v):
+                    axes.append(range(int(v[0]), int(v[1])))
+                else:
+                    raise TaichiLoweringError("ti.static(ti.ndrange(...)) needs integer extents")
+            return [tuple(t) for t in itertools.product(*axes)]
         vals = self.expr(inner, local)
         if isinstance(vals, _PVec):
             return list(vals.comps)
@@ -1394,10 +1548,18 @@ class _PixInterp:
             return True
         vals = self.static_values(st, local)
         if vals is not None:
-            if not isinstance(st.target, ast.Name) or st.orelse:
-                raise TaichiLoweringError("a ti.static loop binds one name and has no else")
+            tnames = [st.target.id] if isinstance(st.target, ast.Name) else \
+                [e.id for e in st.target.elts] if isinstance(st.target, ast.Tuple) and \
+                all(isinstance(e, ast.Name) for e in st.target.elts) else None
+            if tnames is None or st.orelse:
+                raise TaichiLoweringError("a ti.static loop binds names and has no else")
             for v in vals:
-                local[st.target.id] = v
+                if len(tnames) == 1:
+                    local[tnames[0]] = v
+                else:
+                    if not isinstance(v, tuple) or len(v) != len(tnames):
+                        raise TaichiLoweringError(f"a ti.static loop over {len(tnames)} names needs tuples of that many values")
+                    local.update(zip(tnames, v))
                 for s2 in st.body:
                     if not self.assign(s2, local):
                         raise TaichiLoweringError(f"statement at line {getattr(s2, 'lineno', '?')} is not supported")
@@ -1407,7 +1569,26 @@ class _PixInterp:
             tgt = st.target if isinstance(st, ast.AugAssign) else st.targets[0]
             if isinstance(tgt.value, ast.Name) and isinstance(local.get(tgt.value.id), _PVec):
                 return self.component_assign(st, tgt, local)
+        if isinstance(st, ast.Expr) and isinstance(st.value, ast.Call):
+            # ti.atomic_add(field[idx], v) / ti.atomic_sub as a statement: field[idx] += v / -= v
+            fn = st.value.func
+            name = fn.attr if isinstance(fn, ast.Attribute) else fn.id if isinstance(fn, ast.Name) else None
+            if name in ("atomic_add", "atomic_sub"):
+                args = st.value.args
+                if len(args) != 2 or not isinstance(args[0], ast.Subscript):
+                    raise TaichiLoweringError(f"ti.{name} takes (field[index], value)")
+                op = ast.Add() if name == "atomic_add" else ast.Sub()
+                return self.assign(ast.AugAssign(target=args[0], op=op, value=args[1], lineno=getattr(st, "lineno", 0)), local)
+            return False
         if isinstance(st, ast.AugAssign) and isinstance(st.target, ast.Subscript):
+            base = self.expr(st.target.value, local)
+            if isinstance(base, Field) and not self._at_here(base, st.target.slice):
+                # at another index: Taichi's atomic add
+                if not isinstance(st.op, (ast.Add, ast.Sub)):
+                    raise TaichiLoweringError(f"augmented {type(st.op).__name__} at another index than the loop's "
+                                              "(only += and -=, Taichi's atomic adds)")
+                self.scatter(base, st.target.slice, self.expr(st.value, local), local, negate=isinstance(st.op, ast.Sub))
+                return True
             # field[i, j] op= v is field[i, j] = field[i, j] op v (the read sees an earlier store)
             return self.assign(ast.Assign(targets=[st.target], value=ast.BinOp(
                 left=ast.Subscript(value=st.target.value, slice=st.target.slice, ctx=ast.Load()), op=st.op,
@@ -1464,14 +1645,16 @@ _UNREADABLE = object()  # the loop counter inside the loop
 _ONE_BRANCH = object()  # a name an if statement assigns in one branch only
 
 
-_BUILTINS = {"abs": abs, "max": max, "min": min, "float": float}
+_BUILTINS = {"abs": abs, "max": max, "min": min, "float": float, "int": int}
 
 
 def _assigned_names(stmts):
     out = []
     for st in stmts:
         if isinstance(st, (ast.If, ast.For)):  # if branches; unrolled loops (their variable too)
-            names = [st.target.id] if isinstance(st, ast.For) and isinstance(st.target, ast.Name) else []
+            names = [st.target.id] if isinstance(st, ast.For) and isinstance(st.target, ast.Name) else \
+                [e.id for e in st.target.elts if isinstance(e, ast.Name)] if isinstance(st, ast.For) and \
+                isinstance(st.target, ast.Tuple) else []
             for nm in names + _assigned_names(st.body) + _assigned_names(st.orelse):
                 if nm not in out:
                     out.append(nm)
@@ -1499,10 +1682,13 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env, depth=0, unroll=True)
     if split is not None:
         return split
     try:
-        low, stored = _lower_pixel_one(fdef, funcs, env, None, unroll)
+        low, stored, scatters = _lower_pixel_one(fdef, funcs, env, None, unroll)
         if low is not None:
             return low
         parts = {id(f): _lower_pixel_one(fdef, funcs, env, f, unroll)[0] for f in stored}
+        if scatters:  # the body's scatter-adds run once, as a program of their own
+            parts[id(_SCATTERS)] = _lower_pixel_one(fdef, funcs, env, _SCATTERS, unroll)[0]
+            stored = stored + [_SCATTERS]
     except TaichiLoweringError as e:
         if not str(e).startswith("the program needs more than"):
             raise
@@ -1531,7 +1717,7 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env, depth=0, unroll=True)
             pending.remove(ready[0])
             continue
         f = next(f for f in pending if loaded_by_other(f, pending))
-        snap = f.snapshot()
+        snap = f.snapshot()  # (never the scatter-adds' entry: no program loads it)
         copies.append(Lowered("copy", snap, inputs=[f]))
         for g in pending:
             if g is not f:
@@ -1597,7 +1783,9 @@ def _struct_for(fdef: ast.FunctionDef, funcs, env, unroll=True):
 
 
 def _grid_of(shape):
-    """The per-pixel program grid of a field of `shape`: [1][N], [R][C], or [A B][C]."""
+    """The per-pixel program grid of a field of `shape`: [1][1] (0-D), [1][N], [R][C], or [A B][C]."""
+    if len(shape) == 0:
+        return (1, 1)
     if len(shape) == 1:
         return (1, shape[0])
     if len(shape) == 3:
@@ -1719,7 +1907,7 @@ def _split_body(fdef: ast.FunctionDef, funcs, env, at, depth, unroll=True):
         f = ast.For(target=loop.target, iter=loop.iter, body=body, orelse=[], lineno=getattr(loop, "lineno", 0))
         return ast.FunctionDef(name=fdef.name, args=fdef.args, body=[f], decorator_list=[], returns=None, type_comment=None)
 
-    if not stores and not any(isinstance(nd, ast.Subscript) and isinstance(nd.ctx, ast.Store)
+    if not stores and not any((isinstance(nd, ast.Subscript) and isinstance(nd.ctx, ast.Store)) or _is_atomic_call(nd)
                               for st in part1 for nd in ast.walk(st)):
         # the first part passes nothing on and stores nothing: only its loop's cost would remain
         return lower_pixel_program(kernel_of(prelude + part2), funcs, env2, depth + 1, unroll)
@@ -1728,22 +1916,42 @@ def _split_body(fdef: ast.FunctionDef, funcs, env, at, depth, unroll=True):
     return Lowered("sequence", second.field, parts=[first, second])
 
 
+_SCATTERS = object()  # the target of the program that runs a body's scatter-adds on their own
+
+
+def _is_atomic_call(nd) -> bool:
+    """ti.atomic_add(...) / ti.atomic_sub(...) (a scatter-add statement)."""
+    if not isinstance(nd, ast.Call):
+        return False
+    f = nd.func
+    return (f.attr if isinstance(f, ast.Attribute) else f.id if isinstance(f, ast.Name) else None) in ("atomic_add",
+                                                                                                       "atomic_sub")
+
+
 def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target, unroll=True):
-    """(Lowered program storing `target`, the fields the body stores); target None: the only
-    field the body stores (Lowered None when it stores several)."""
+    """(Lowered program storing `target`, the fields the body stores, whether the body
+    scatter-adds); target None: the only field the body stores, with the body's scatter-adds
+    (Lowered None when it stores several); target _SCATTERS: a program of the scatter-adds alone,
+    storing nothing."""
     from . import pixprog as pp
     loop, ip, b, local, stmts = _struct_for(fdef, funcs, env, unroll)
     init, test, new_state, max_iter, has_loop = _run_stmts(ip, b, local, stmts)
-    if not ip.stored:
-        raise TaichiLoweringError("the struct-for body must store field[i, j] = ...")
+    if not ip.stored and not ip.scatters:
+        raise TaichiLoweringError("the struct-for body must store field[i, j] = ... or scatter-add (field[...] += v)")
+    effects = []
     if target is None:
         if len(ip.stored) > 1:
-            return None, ip.stored
-        target = ip.stored[0]
-    fld = target
-    v = local[_skey(target)]
+            return None, ip.stored, bool(ip.scatters)
+        target = ip.stored[0] if ip.stored else _SCATTERS
+        effects = ip.scatters
+    elif target is _SCATTERS:
+        effects = ip.scatters
+    fld = None if target is _SCATTERS else target
+    v = None if fld is None else local[_skey(target)]
     out_i32 = False
-    if fld.dtype == i32:
+    if fld is None:
+        out = None
+    elif fld.dtype == i32:
         if isinstance(v, pp.Node) and v.kind == "count":
             out = pp.COUNT
         else:  # any value, truncated as Taichi's int field assignment does
@@ -1756,12 +1964,13 @@ def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target, unroll=True):
         prog = pp.compile_program(b, init=init, test=test, body=new_state, max_iter=max_iter, out=out, loop=has_loop,
                                   in_widths=[f.width for f in ip.inputs],
                                   in_dtypes=[pp.I32 if f.dtype == i32 else pp.F32 for f in ip.inputs], out_i32=out_i32,
-                                  in_extents=ip.in_extents)
+                                  in_extents=ip.in_extents, effects=effects)
     except pp.ProgramError as e:
         raise TaichiLoweringError(str(e)) from None
     # the fields this program loads (an input that only dead code reads is not one)
     roots = list(init.values()) + list(new_state.values()) + (list(test[1:]) if test else [])
     roots += out if isinstance(out, list) else [out]
+    roots += effects
     todo, seen, live = [n for n in roots if isinstance(n, pp.Node)], set(), set()
     while todo:
         n = todo.pop()
@@ -1772,7 +1981,8 @@ def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target, unroll=True):
             todo.extend(n.args)
     low = Lowered("pixel_program", fld, program=prog, inputs=ip.inputs)
     low.reads = [f for k, f in enumerate(ip.inputs) if k in live]
-    return low, ip.stored
+    low.grid = _grid_of(ip.shape if ip.shape is not None else ip.fld.shape)
+    return low, ip.stored, bool(ip.scatters)
 
 
 def _is_range(it) -> bool:
