@@ -24,7 +24,12 @@
  *                        expressions, field reads, if / else and compound loop tests), by
  *                        equality with orc_escape_time on the programs both express, by closed
  *                        forms (a loop with no test runs max_iter times), and the comparison,
- *                        select and floor opcodes by numpy on every pair of special values.
+ *                        select, floor and trunc opcodes by numpy on every pair of special values.
+ *                        Scatter-adds (VDSL_PIX_ATOMIC_ADD, run pixel by pixel in row-major
+ *                        order): by numpy's np.add.at over the same indices in the same order
+ *                        (f32 bit for bit, int32 exactly with wrap-around) and by the drop rule
+ *                        written out index by index over negative, fractional, too large,
+ *                        infinite and NaN indices; histograms by np.bincount.
  *   orc_map_chain_v_rows vector operands (the vec2-4 / extract_component / swizzle vocabulary of
  *                        source/README.md:23-55).  Pinned by permutation closed forms: a swizzle
  *                        program equals numpy fancy indexing of the components, swizzles compose

@@ -276,7 +276,7 @@ def test_compare_select_floor_opcodes_bit_exact(dev, q):
     b = pp.Builder()
     la, lc = b.load(0), b.load(1)
     for node in (b.op("lt", la, lc), b.op("le", la, lc), b.op("eq", la, lc), b.op("ne", la, lc),
-                 b.op("select", la, lc, b.op("neg", lc)), b.op("floor", la),
+                 b.op("select", la, lc, b.op("neg", lc)), b.op("floor", la), b.op("trunc", la),
                  b.op("select", b.op("lt", la, lc), b.op("floor", lc), b.op("max", la, lc))):
         prog = pp.compile_program(b, out=node)
         got = run_prog(dev, q, prog, [a, c], n, n)
@@ -535,7 +535,7 @@ def test_nested_range_loops_bit_exact(dev, q):
 
 
 # ---- seeded random programs against the oracle -----------------------------------------------------
-EXACT_UNARY = ("neg", "abs", "sqrt", "floor", "square")
+EXACT_UNARY = ("neg", "abs", "sqrt", "floor", "square", "trunc")
 EXACT_BINARY = ("add", "sub", "mul", "div", "max", "min", "lt", "le", "eq", "ne")
 
 

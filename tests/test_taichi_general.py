@@ -287,7 +287,8 @@ SPECIALS = np.array([0.0, -0.0, 1.0, -1.0, 0.5, -0.5, 2.5, -2.5, 1e-40, -1e-40, 
 
 def test_compare_select_floor_opcodes_against_numpy():
     """The new opcodes on every pair of special values (signed zeros, subnormals, infinities,
-    NaN): comparisons as IEEE predicates, select on `!= 0` (NaN true, -0 false), floor as np.floor."""
+    NaN): comparisons as IEEE predicates, select on `!= 0` (NaN true, -0 false), floor as
+    np.floor, trunc as np.trunc (toward zero; -0.5 -> -0)."""
     n = len(SPECIALS)
     a = np.repeat(SPECIALS[:, None], n, axis=1)
     c = np.repeat(SPECIALS[None, :], n, axis=0)
@@ -304,6 +305,9 @@ def test_compare_select_floor_opcodes_against_numpy():
     prog = pp.compile_program(b, out=b.op("floor", la))
     fl = oracle.pixel_program(prog, n, n, [a, c])
     assert np.array_equal(fl.view(np.uint32), np.floor(a).view(np.uint32))
+    prog = pp.compile_program(b, out=b.op("trunc", la))
+    tr = oracle.pixel_program(prog, n, n, [a, c])
+    assert np.array_equal(tr.view(np.uint32), np.trunc(a).view(np.uint32))
 
 
 def palette_numpy(shift, W=800, H=600, limit=120):

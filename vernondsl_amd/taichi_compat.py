@@ -38,7 +38,12 @@ which no program loads a field that an earlier one stored (a snapshot copy where
 load each other's fields; a load at [i, j] after the body's own store reads the stored value, as
 in Taichi); a kernel of several top-level struct-fors runs their lowerings one after another.
 1-D fields and struct-fors (`for i in x:`, `for i in range(N):`) run as one row of the grid, 3-D
-ones ([A][B][C], `for i, j, k in u:`) as the grid [A B][C].  What neither path lowers raises
+ones ([A][B][C], `for i, j, k in u:`) as the grid [A B][C]; 0-D fields (`shape=()`) are read and
+added into as `s[None]`.  `F[idx] += v` / `-= v` at an index other than the loop's (and
+`ti.atomic_add(F[idx], v)` as a statement) is Taichi's atomic add: a scatter-add of the program,
+dropped where an index falls outside F, with idx a tuple or a vector expression such as
+`base + offset` (`.cast(int)` / `int()` truncate); a field added into is neither read nor stored
+by the same struct-for, and adds inside an if happen only where the branch runs.  What neither path lowers raises
 TaichiLoweringError naming what did not match; there is no CPU fallback.  Accepted complex squares are the ones equal bit for bit to (zr*zr - zi*zi, (zi*zr)*2):
 `z[0]**2 - z[1]**2`, `z[0]*z[0] - z[1]*z[1]`, and `z[1]*z[0]*2` / `z[0]*z[1]*2` / `2*(z[0]*z[1])` /
 `z[0]*z[1] + z[0]*z[1]` for the imaginary part (`(2*z[0])*z[1]` is refused: it rounds differently
