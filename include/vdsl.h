@@ -344,9 +344,10 @@ typedef enum vdsl_pix_opcode {
    * then written: its buffer must be writable, must not be `out`, and no LOAD / LOAD_AT of the
    * program may read it.  An int32 input adds r[dst] converted as VDSL_PIX_OUT_I32 stores it,
    * wrapping on overflow: exact in any order.  An f32 input adds in f32 with the hardware's
-   * atomic float add; the adds of one launch to one element happen in no fixed order, so the
-   * sum's rounding may differ between runs (as Taichi's atomic adds).  Where both indices are
-   * the same for every lane of a wave, the wave's values are summed first and added once. */
+   * atomic float add; the adds of one launch to one element happen in no fixed order, and
+   * several may be summed before they reach it (per wave or per block where the indices are
+   * the same on every lane or constant, and in a per-block copy of a target of at most 8192
+   * elements), so the sum's rounding may differ between runs (as Taichi's atomic adds). */
   VDSL_PIX_ATOMIC_ADD = 44,
   VDSL_PIX_TRUNC = 45   /* truncf(r[a]): toward zero (Taichi's float -> int conversion, kept in f32) */
 } vdsl_pix_opcode;

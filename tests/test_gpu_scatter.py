@@ -60,12 +60,15 @@ def hist_program(bins, scale, dtype=pp.I32, value=1.0):
     return pp.compile_program(b, out=None, effects=[e], in_dtypes=[pp.F32, dtype], in_extents=[None, (1, bins)])
 
 
-@pytest.mark.parametrize("ni, nj", [(37, 53), (1, 1000), (300, 1), (256, 256), (1, 1)])
-def test_histogram_bins_per_lane_bit_exact(dev, q, ni, nj):
-    rng = np.random.default_rng(ni * 1000 + nj)
+@pytest.mark.parametrize("ni, nj, bins", [(37, 53, 16), (1, 1000, 16), (300, 1, 16), (256, 256, 16), (1, 1, 16),
+                                          (256, 256, 8192), (256, 256, 8193), (97, 301, 5000), (97, 301, 20000)])
+def test_histogram_bins_per_lane_bit_exact(dev, q, ni, nj, bins):
+    """Up to 8192 bins each block adds into its own copy in LDS and then adds the copy's non-zero
+    bins; above, every lane adds into memory."""
+    rng = np.random.default_rng(ni * 1000 + nj + bins)
     x = rng.random((ni, nj)).astype(f32)
-    prog = hist_program(16, 16.0)
-    h0 = rng.integers(-5, 5, (1, 16)).astype(np.int32)
+    prog = hist_program(bins, float(bins))
+    h0 = rng.integers(-5, 5, (1, bins)).astype(np.int32)
     _, (_, got) = run_scatter(dev, q, prog, [x, h0], ni, nj)
     want = h0.copy()
     oracle.pixel_program(prog, ni, nj, [x, want])
@@ -127,18 +130,25 @@ def test_indices_outside_the_target_are_dropped(dev, q):
     assert np.array_equal(gc, c) and np.array_equal(gw, w) and int(c.sum()) == 25  # 5 x 5 in-range pairs (-0.0 is one)
 
 
-@pytest.mark.parametrize("uniform", [False, True])
-def test_f32_dyadic_sums_bit_exact(dev, q, uniform):
-    """Values k / 64 with |k| < 256 into 8 bins (per lane) or one element (per wave): every partial
-    sum of at most 2^13 of them is exact in f32, so any order gives the oracle's bits."""
+@pytest.mark.parametrize("uniform, bins", [(False, 8), (True, 1), (False, 9000)])
+def test_f32_dyadic_sums_bit_exact(dev, q, uniform, bins):
+    """Values k / 64 with |k| < 256 into 8 bins (per lane, into LDS copies), one element (summed
+    per thread and block) or 9000 bins (per lane, into memory): every partial sum of at most 2^13
+    of them is exact in f32, so any order gives the oracle's bits."""
     ni, nj = 48, 160
-    rng = np.random.default_rng(31 + uniform)
+    rng = np.random.default_rng(31 + uniform + bins)
     v = (rng.integers(-255, 256, (ni, nj)) / 64.0).astype(f32)
     b = pp.Builder()
-    col = 0.0 if uniform else b.op("floor", b.op("mul", b.index(1), 0.05))  # j // 20: 8 bins
+    if uniform:
+        col = 0.0
+    elif bins == 8:
+        col = b.op("floor", b.op("mul", b.index(1), 0.05))  # j // 20: 8 bins
+    else:
+        col = b.op("floor", b.op("mul", b.load(0), 4.0))  # floor(4 v) in -16 .. 15, + 64: columns 48 .. 79
+        col = b.op("add", col, 64.0)
     e = b.scatter_add(1, 0.0, col, b.load(0))
-    prog = pp.compile_program(b, out=None, effects=[e], in_dtypes=[pp.F32, pp.F32], in_extents=[None, (1, 8)])
-    t = np.zeros((1, 8), f32)
+    prog = pp.compile_program(b, out=None, effects=[e], in_dtypes=[pp.F32, pp.F32], in_extents=[None, (1, bins)])
+    t = np.zeros((1, bins), f32)
     _, (_, got) = run_scatter(dev, q, prog, [v, t], ni, nj)
     oracle.pixel_program(prog, ni, nj, [v, t])
     assert np.array_equal(got, t)

@@ -136,6 +136,24 @@ int main(void) {
   pp.code[2].c = VDSL_PIX_MAX_REGS;
   EXPECT_ERR(vdsl_op_pixel_program(q, 8, 16, &pp, NULL, 0, a));  /* register out of range */
 
+  /* scatter-adds: total[0][0] += j for every pixel, into an f32 [1][1] input; no output */
+  vdsl_pixel_program sp;
+  memset(&sp, 0, sizeof sp);
+  sp.n_post = 2; sp.out_kind = VDSL_PIX_OUT_NONE; sp.out_width = 1;
+  sp.in_widths[0] = 1; sp.in_dtypes[0] = VDSL_F32; sp.in_rows[0] = 1; sp.in_cols[0] = 1;
+  sp.code[0].op = VDSL_PIX_INDEX; sp.code[0].dst = 1; sp.code[0].a = 1;
+  sp.code[1].op = VDSL_PIX_ATOMIC_ADD; sp.code[1].dst = 1; sp.code[1].a = 0; sp.code[1].b = 0; sp.code[1].c = 0;
+  vdsl_buffer tot = alloc(d, 4);
+  fill_f32(q, tot, 1, 0.0f);
+  EXPECT_OK(vdsl_op_pixel_program(q, 8, 16, &sp, &tot, 1, NULL));
+  sp.code[1].imm = 1.0f;  /* component 1 of a field of scalars */
+  EXPECT_ERR(vdsl_op_pixel_program(q, 8, 16, &sp, &tot, 1, NULL));
+  sp.code[1].imm = 0.0f;
+  EXPECT_ERR(vdsl_op_pixel_program(q, 8, 16, &sp, &tot, 0, NULL));  /* no input 0 */
+  sp.out_kind = VDSL_PIX_OUT_REG;
+  EXPECT_ERR(vdsl_op_pixel_program(q, 8, 16, &sp, &tot, 1, NULL));  /* a stored output needs its buffer */
+  EXPECT_OK(vdsl_buffer_free(tot));
+
   /* ---- op class 2: map chains ---- */
   vdsl_map_instr code[3];
   memset(code, 0, sizeof code);

@@ -89,29 +89,55 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
   return VDSL_OK;
 }
 
+std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p);
+
+// Elements (x components) of input k when its scatter-adds go to a copy in LDS per block
+// (pixprog_kern.h), else 0: a target of at most kPrivMax elements that some add reaches at
+// per-pixel indices (a histogram).  Adds at constant indices are summed in registers instead.
+constexpr int kPrivMax = 8192;
+int privatized(const vdsl_pixel_program& p, int k, int ni, int nj) {
+  const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
+  const std::vector<char> flags = row_uniform_gathers(p);
+  bool per_pixel = false;
+  for (int pc = 0; pc < total; ++pc)
+    per_pixel |= p.code[pc].op == VDSL_PIX_ATOMIC_ADD && p.code[pc].a == k && !(flags[pc] & 4);
+  const int64_t elems = static_cast<int64_t>(p.in_rows[k] ? p.in_rows[k] : ni) * (p.in_cols[k] ? p.in_cols[k] : nj) *
+                        p.in_widths[k];
+  return per_pixel && elems <= kPrivMax ? static_cast<int>(elems) : 0;
+}
+
 // Rows per block in the row mapping (each thread evaluates that many pixels of its column, then
 // stores them).  Measured on 8192^2 f32 (graph replays, one box): y = 2x + 1 runs best with 4
 // (88.2 us; 2, 6, 8, 12, 16 rows: 87-97% of that rate), the clamped five-point stencil of
-// examples/heat.py with 8 (95.7 us; 6: 95.9, 10: 99.1, 12: 99.6-99.9, 4: 103.0, 16: 107.5).
-// VDSL_PIX_ROWS=r (1..16) overrides the choice, for tuning sweeps.
-int rows_per_block(const vdsl_pixel_program& p) {
-  if (const char* e = std::getenv("VDSL_PIX_ROWS")) {  // tuning sweeps: rows per block, 1..16
+// examples/heat.py with 8 (95.7 us; 6: 95.9, 10: 99.1, 12: 99.6-99.9, 4: 103.0, 16: 107.5).  A
+// program that stores nothing and adds only at constant indices (a reduction such as
+// `total[None] += x[i, j]`) adds once per block, and those adds to one element are serialised
+// (~13 ns each): 64 rows (the sum of an 8192^2 field: 834 / 420 / 214 us with 4 / 8 / 16 rows);
+// so does one whose other adds go to per-block copies in LDS (their flush is per block too).
+// VDSL_PIX_ROWS=r (1..64) overrides the choice, for tuning sweeps.
+int rows_per_block(const vdsl_pixel_program& p, int ni, int nj) {
+  if (const char* e = std::getenv("VDSL_PIX_ROWS")) {  // tuning sweeps: rows per block, 1..64
     const int r = std::atoi(e);
-    if (r >= 1 && r <= 16) return r;
+    if (r >= 1 && r <= 64) return r;
   }
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
-  for (int pc = 0; pc < total; ++pc)
-    if (p.code[pc].op == VDSL_PIX_LOAD_AT) return 8;
-  return 4;
+  bool gathers = false, reduction = p.out_kind == VDSL_PIX_OUT_NONE;
+  const std::vector<char> flags = row_uniform_gathers(p);
+  for (int pc = 0; pc < total; ++pc) {
+    gathers |= p.code[pc].op == VDSL_PIX_LOAD_AT;
+    if (p.code[pc].op == VDSL_PIX_ATOMIC_ADD && !(flags[pc] & 4) && !privatized(p, p.code[pc].a, ni, nj))
+      reduction = false;
+  }
+  return reduction ? 64 : gathers ? 8 : 4;
 }
 
 // Blocks of rows_per_block rows x 256 pixels for programs whose pixels all do the same work (no
 // escape loop), while the row count fits the grid's y extent; 16x16 patches otherwise.  0 for
 // the patches.
-int row_mapping(const vdsl_pixel_program& p, int ni) {
+int row_mapping(const vdsl_pixel_program& p, int ni, int nj) {
   // never more rows per block than the grid has: a 1-D field is a grid of one row, whose blocks
   // would otherwise run their loops for rows that do not exist
-  const int rows = std::min(rows_per_block(p), std::max(ni, 1));
+  const int rows = std::min(rows_per_block(p, ni, nj), std::max(ni, 1));
   return !(p.loop && p.test != VDSL_PIX_TEST_NONE) && (ni + rows - 1) / rows <= 65535 ? rows : 0;
 }
 
@@ -213,7 +239,7 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni, in
   c("test_b", p.test_b);
   c("out_kind", p.out_kind);
   c("out_width", p.out_width);
-  c("rows", row_mapping(p, ni));
+  c("rows", row_mapping(p, ni, nj));
   // 32-bit element offsets when every field's byte offsets stay below 2^32
   int maxw = p.out_width;
   for (int k = 0; k < n_inputs; ++k) maxw = p.in_widths[k] > maxw ? p.in_widths[k] : maxw;
@@ -229,6 +255,9 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni, in
   list("out_regs", p.out_regs, p.out_width, 0);
   list("in_widths", p.in_widths, n_inputs, 1);
   list("in_dtypes", p.in_dtypes, n_inputs, VDSL_F32);
+  int32_t priv[VDSL_PIX_MAX_INPUTS] = {};
+  for (int k = 0; k < n_inputs; ++k) priv[k] = privatized(p, k, ni, nj);
+  list("priv", priv, n_inputs, 0);
   // ext[0] / ext[1] of a gather or scatter-add: 1 when its row / column operand is wave-uniform in
   // the row mapping; ext[2] of a scatter-add: 1 when both are constants
   const std::vector<char> ru = row_uniform_gathers(p);
@@ -289,7 +318,7 @@ extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const
   VDSL_TRY(st);
   void* o = p.out_kind == VDSL_PIX_OUT_NONE ? nullptr : out->ptr;
   void* args[] = {&rt, &in, &o, &ni, &nj};
-  const int rows = row_mapping(p, ni);
+  const int rows = row_mapping(p, ni, nj);
   const unsigned gx = rows ? static_cast<unsigned>((nj + 255) / 256) : static_cast<unsigned>((nj + 15) / 16);
   const unsigned gy = rows ? static_cast<unsigned>((ni + rows - 1) / rows) : static_cast<unsigned>((ni + 15) / 16);
   return check_hip(hipModuleLaunchKernel(k->fn[0], gx, gy, 1, 256, 1, 1, 0, q->stream, args, nullptr),

@@ -102,53 +102,158 @@ __device__ __forceinline__ int pix_wave_sum(int v) {
   return v;
 }
 
-// VDSL_PIX_ATOMIC_ADD into input A: component c of [x][y] += v where 0 <= x < rows and
-// 0 <= y < cols (A's extents) on lanes with act set.  UNI: x and y are the same on every lane of
-// the wave (host dataflow, row mapping), so the wave's values are summed and one lane adds.
-template <class P, int A, bool UNI>
-__device__ __forceinline__ void pix_scatter_add(const PixIn& in, float x, float y, float v, int c, bool act) {
-  // NaN fails every comparison; below 2^30 the conversion is exact truncation, and the row and
-  // column are then checked as integers (float(rows) may round above 2^24)
+// The element a scatter-add into input A at [x][y] reaches: ok is false where x or y is outside
+// A's extents (NaN fails every comparison; below 2^30 the conversion is exact truncation, and the
+// row and column are then checked as integers, since float(rows) may round above 2^24).
+template <class P, int A>
+__device__ __forceinline__ PixOff<P> pix_target(const PixIn& in, float x, float y, bool& ok) {
   const bool num = x >= 0.0f && x < 1073741824.0f && y >= 0.0f && y < 1073741824.0f;
   const int xi = num ? static_cast<int>(x) : 0, yi = num ? static_cast<int>(y) : 0;
-  const bool ok = act && num && xi < in.rows[A] && yi < in.cols[A];
-  const PixOff<P> e = static_cast<PixOff<P>>(static_cast<unsigned>(xi)) * static_cast<unsigned>(in.cols[A]) +
-                      static_cast<unsigned>(yi);
+  ok = num && xi < in.rows[A] && yi < in.cols[A];
+  return static_cast<PixOff<P>>(static_cast<unsigned>(xi)) * static_cast<unsigned>(in.cols[A]) + static_cast<unsigned>(yi);
+}
+
+template <class P, int A>
+__device__ __forceinline__ void pix_atomic(const PixIn& in, PixOff<P> e, int c, float vf, int vi) {
   char* base = const_cast<char*>(reinterpret_cast<const char*>(in.p[A]));
-  if constexpr (P::in_dtypes[A] == VDSL_I32) {
-    int* t = reinterpret_cast<int*>(base) + e;
-    int add = ok ? pix_to_i32(v) : 0;
-    if constexpr (UNI) {
-      const uint64_t any = __builtin_amdgcn_ballot_w64(ok);
-      if (any == 0ull) return;
-      add = pix_wave_sum(add);
-      if (pix_lane() == __builtin_ctzll(any)) atomicAdd(t, add);
-    } else {
-      if (ok) atomicAdd(t, add);
-    }
+  if constexpr (P::in_dtypes[A] == VDSL_I32)
+    atomicAdd(reinterpret_cast<int*>(base) + e, vi);
+  else
+    unsafeAtomicAdd(reinterpret_cast<float*>(base) + (e * static_cast<PixOff<P>>(P::in_widths[A]) + static_cast<PixOff<P>>(c)), vf);
+}
+
+// Scatter-adds at constant indices (ext[2]: the same element for every pixel, such as
+// `total[None] += v`) are not added where they run: each thread sums its pixels' values
+// (PixAcc), and at the end of the block the sums of its four waves are added once (pix_flush).
+template <class P>
+struct PixConstAdds {
+  static constexpr int end = P::n_pre + P::n_test + P::n_body + P::n_post;
+  static constexpr bool at(int pc) { return P::code[pc].op == VDSL_PIX_ATOMIC_ADD && P::code[pc].ext[2] != 0; }
+  static constexpr int slot(int pc) {
+    int n = 0;
+    for (int q = 0; q < pc; ++q) n += at(q) ? 1 : 0;
+    return n;
+  }
+  static constexpr int N = slot(end);
+};
+
+
+template <class P>
+struct PixAcc {
+  static constexpr int N = PixConstAdds<P>::N > 0 ? PixConstAdds<P>::N : 1;
+  float f[N];        // f32 targets: this thread's sum
+  int i[N];          // int32 targets: this thread's sum, wrapping
+  int n[N];          // adds made (none: nothing to add)
+  float x[N], y[N];  // the indices (constants)
+  unsigned* sh[VDSL_PIX_MAX_INPUTS];  // the block's LDS copy of input k where P::priv[k] > 0
+};
+
+// An add into input A's element e, component c: into the block's LDS copy where A has one
+// (P::priv[A] > 0), else into memory.
+template <class P, int A>
+__device__ __forceinline__ void pix_add(const PixIn& in, PixAcc<P>& acc, PixOff<P> e, int c, float vf, int vi) {
+  if constexpr (P::priv[A] > 0) {
+    const unsigned k = static_cast<unsigned>(e) * static_cast<unsigned>(P::in_widths[A]) + static_cast<unsigned>(c);
+    if constexpr (P::in_dtypes[A] == VDSL_I32) atomicAdd(reinterpret_cast<int*>(acc.sh[A]) + k, vi);
+    else atomicAdd(reinterpret_cast<float*>(acc.sh[A]) + k, vf);
   } else {
-    float* t = reinterpret_cast<float*>(base) + (e * static_cast<PixOff<P>>(P::in_widths[A]) + static_cast<PixOff<P>>(c));
-    float add = ok ? v : 0.0f;
-    if constexpr (UNI) {
-      const uint64_t any = __builtin_amdgcn_ballot_w64(ok);
-      if (any == 0ull) return;
-      add = pix_wave_sum(add);
-      if (pix_lane() == __builtin_ctzll(any)) unsafeAtomicAdd(t, add);
-    } else {
-      if (ok) unsafeAtomicAdd(t, add);
+    pix_atomic<P, A>(in, e, c, vf, vi);
+  }
+}
+
+// VDSL_PIX_ATOMIC_ADD into input A: component c of [x][y] += v on lanes with act set, where the
+// element is in A.  UNI: x and y are the same on every lane of the wave (host dataflow, row
+// mapping), so the wave's values are summed and one lane adds.
+template <class P, int A, bool UNI>
+__device__ __forceinline__ void pix_scatter_add(const PixIn& in, PixAcc<P>& acc, float x, float y, float v, int c, bool act) {
+  bool in_a;
+  const PixOff<P> e = pix_target<P, A>(in, x, y, in_a);
+  const bool ok = act && in_a;
+  constexpr bool i32 = P::in_dtypes[A] == VDSL_I32;
+  float vf = ok && !i32 ? v : 0.0f;
+  int vi = ok && i32 ? pix_to_i32(v) : 0;
+  if constexpr (UNI) {
+    const uint64_t any = __builtin_amdgcn_ballot_w64(ok);
+    if (any == 0ull) return;
+    if constexpr (i32) vi = pix_wave_sum(vi);
+    else vf = pix_wave_sum(vf);
+    if (pix_lane() == __builtin_ctzll(any)) pix_add<P, A>(in, acc, e, c, vf, vi);
+  } else {
+    if (ok) pix_add<P, A>(in, acc, e, c, vf, vi);
+  }
+}
+
+template <class P, int PC>
+__device__ __forceinline__ void pix_accumulate(PixAcc<P>& acc, float x, float y, float v, bool act) {
+  constexpr vdsl_map_instr s = P::code[PC];
+  constexpr int k = PixConstAdds<P>::slot(PC);
+  if constexpr (P::in_dtypes[s.a] == VDSL_I32)
+    acc.i[k] = static_cast<int>(static_cast<unsigned>(acc.i[k]) + static_cast<unsigned>(act ? pix_to_i32(v) : 0));
+  else
+    acc.f[k] += act ? v : 0.0f;
+  acc.n[k] += act ? 1 : 0;
+  acc.x[k] = x;
+  acc.y[k] = y;
+}
+
+// Wave sums of every constant-index add into LDS, then thread k adds the block's sum of add k.
+// Every thread of the 256-thread block (4 waves) calls this once, after all its pixels.
+template <class P, int PC>
+__device__ __forceinline__ void pix_flush_wave(PixAcc<P>& acc, float (*sf)[PixAcc<P>::N], int (*si)[PixAcc<P>::N],
+                                               int (*sn)[PixAcc<P>::N]) {
+  if constexpr (PixConstAdds<P>::at(PC)) {
+    constexpr int k = PixConstAdds<P>::slot(PC);
+    const float f = pix_wave_sum(acc.f[k]);
+    const int iv = pix_wave_sum(acc.i[k]), n = pix_wave_sum(acc.n[k]);
+    if (pix_lane() == 0) {
+      sf[threadIdx.x >> 6][k] = f;
+      si[threadIdx.x >> 6][k] = iv;
+      sn[threadIdx.x >> 6][k] = n;
     }
   }
 }
 
 template <class P, int PC>
+__device__ __forceinline__ void pix_flush_add(const PixRt& rt, const PixIn& in, const PixAcc<P>& acc,
+                                              float (*sf)[PixAcc<P>::N], int (*si)[PixAcc<P>::N], int (*sn)[PixAcc<P>::N]) {
+  if constexpr (PixConstAdds<P>::at(PC)) {
+    constexpr vdsl_map_instr s = P::code[PC];
+    constexpr int k = PixConstAdds<P>::slot(PC);
+    if (threadIdx.x == k) {
+      const float f = ((sf[0][k] + sf[1][k]) + sf[2][k]) + sf[3][k];
+      const int iv = static_cast<int>(static_cast<unsigned>(si[0][k]) + static_cast<unsigned>(si[1][k]) +
+                                      static_cast<unsigned>(si[2][k]) + static_cast<unsigned>(si[3][k]));
+      bool ok;
+      const PixOff<P> e = pix_target<P, s.a>(in, acc.x[k], acc.y[k], ok);
+      if (ok && sn[0][k] + sn[1][k] + sn[2][k] + sn[3][k] > 0)
+        pix_atomic<P, s.a>(in, e, static_cast<int>(rt.imm[PC]), f, iv);
+    }
+  }
+}
+
+template <class P, int... K>
+__device__ __forceinline__ void pix_flush(const PixRt& rt, const PixIn& in, PixAcc<P>& acc, Seq<K...>) {
+  if constexpr (PixConstAdds<P>::N > 0) {
+    constexpr int N = PixAcc<P>::N;
+    __shared__ float sf[4][N];
+    __shared__ int si[4][N], sn[4][N];
+    (pix_flush_wave<P, K>(acc, sf, si, sn), ...);
+    __syncthreads();
+    (pix_flush_add<P, K>(rt, in, acc, sf, si, sn), ...);
+  }
+}
+
+template <class P, int PC>
 __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
-                                         float fi, float fj, float fcount, int ni, int nj, bool act) {
+                                         float fi, float fj, float fcount, int ni, int nj, bool act, PixAcc<P>& acc) {
   constexpr vdsl_map_instr s = P::code[PC];
-  if constexpr (s.op == VDSL_PIX_ATOMIC_ADD) {
-    // one add per wave where both indices are the same on every lane: found wave-uniform by the
-    // host in the row mapping (ext[0], ext[1]), or constants in any mapping (ext[2])
-    constexpr bool uni = (P::rows > 0 && s.ext[0] != 0 && s.ext[1] != 0) || s.ext[2] != 0;
-    pix_scatter_add<P, s.a, uni>(in, r[s.b], r[s.c], r[s.dst], static_cast<int>(rt.imm[PC]), act);
+  if constexpr (s.op == VDSL_PIX_ATOMIC_ADD && s.ext[2] != 0) {
+    pix_accumulate<P, PC>(acc, r[s.b], r[s.c], r[s.dst], act);  // constant indices: added per block
+  } else if constexpr (s.op == VDSL_PIX_ATOMIC_ADD) {
+    // one add per wave where both indices are the same on every lane (found wave-uniform by the
+    // host in the row mapping: ext[0], ext[1]), else one per lane
+    constexpr bool uni = P::rows > 0 && s.ext[0] != 0 && s.ext[1] != 0;
+    pix_scatter_add<P, s.a, uni>(in, acc, r[s.b], r[s.c], r[s.dst], static_cast<int>(rt.imm[PC]), act);
   } else if constexpr (s.op == VDSL_MAP_LOAD) {
     r[s.dst] = pix_load<P, s.a>(in, o, s.c);
   } else if constexpr (s.op == VDSL_PIX_LOAD_AT) {
@@ -190,8 +295,9 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
 
 template <class P, int BASE, int... K>
 __device__ __forceinline__ void pix_section(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
-                                            float fi, float fj, float fcount, int ni, int nj, bool act, Seq<K...>) {
-  (pix_step<P, BASE + K>(rt, in, r, o, fi, fj, fcount, ni, nj, act), ...);
+                                            float fi, float fj, float fcount, int ni, int nj, bool act, PixAcc<P>& acc,
+                                            Seq<K...>) {
+  (pix_step<P, BASE + K>(rt, in, r, o, fi, fj, fcount, ni, nj, act, acc), ...);
 }
 
 template <int TEST>
@@ -264,11 +370,20 @@ struct PixSets {
   static constexpr bool periodic = free_running && carried != 0u && !reads_trip();
 };
 
-// act: the pixel lies in the grid (its scatter-adds happen); the loop's sections have none.
+// act: the pixel lies in the grid (its scatter-adds happen); acc: the thread's sums of its
+// constant-index adds.
 template <class P, int BASE, int N>
 __device__ __forceinline__ void pix_run(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
-                                        float fi, float fj, float fcount, int ni, int nj, bool act = false) {
-  pix_section<P, BASE>(rt, in, r, o, fi, fj, fcount, ni, nj, act, typename MakeSeq<N>::type{});
+                                        float fi, float fj, float fcount, int ni, int nj, bool act, PixAcc<P>& acc) {
+  pix_section<P, BASE>(rt, in, r, o, fi, fj, fcount, ni, nj, act, acc, typename MakeSeq<N>::type{});
+}
+
+// The loop's sections, which hold no scatter-adds.
+template <class P, int BASE, int N>
+__device__ __forceinline__ void pix_run(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
+                                        float fi, float fj, float fcount, int ni, int nj) {
+  PixAcc<P> none;
+  pix_section<P, BASE>(rt, in, r, o, fi, fj, fcount, ni, nj, false, none, typename MakeSeq<N>::type{});
 }
 
 // r[k] <- r[k] where the lane's bit of `mask` is set, else old[k], for the registers in KEEP.
@@ -308,7 +423,7 @@ __device__ __forceinline__ void pix_trip(const PixRt& rt, const PixIn& in, float
 // its trip count into count.
 template <class P>
 __device__ __forceinline__ void pixel_eval(const PixRt& rt, const PixIn& in, int ni, int nj, int i, int j, float (&res)[4],
-                                           int& count_out) {
+                                           int& count_out, PixAcc<P>& acc) {
   using S = PixSets<P>;
   const bool inside = i < ni && j < nj;
   // Lanes past the grid run the program on pixel (0, 0), are never live, and store nothing.
@@ -317,7 +432,7 @@ __device__ __forceinline__ void pixel_eval(const PixRt& rt, const PixIn& in, int
   float r[VDSL_PIX_MAX_REGS];
 #pragma unroll
   for (int k = 0; k < VDSL_PIX_MAX_REGS; ++k) r[k] = 0.0f;
-  pix_run<P, 0, P::n_pre>(rt, in, r, o, fi, fj, 0.0f, ni, nj, inside);
+  pix_run<P, 0, P::n_pre>(rt, in, r, o, fi, fj, 0.0f, ni, nj, inside, acc);
   int count = 0;
   if constexpr (P::loop && P::test == VDSL_PIX_TEST_NONE) {
     // No test: every lane makes max_iter trips; they run only if something after the loop reads
@@ -383,7 +498,7 @@ __device__ __forceinline__ void pixel_eval(const PixRt& rt, const PixIn& in, int
       }
     }
   }
-  pix_run<P, S::q0, P::n_post>(rt, in, r, o, fi, fj, static_cast<float>(count), ni, nj, inside);
+  pix_run<P, S::q0, P::n_post>(rt, in, r, o, fi, fj, static_cast<float>(count), ni, nj, inside, acc);
 #pragma unroll
   for (int k = 0; k < 4; ++k) res[k] = k < P::out_width ? r[P::out_regs[k]] : 0.0f;
   count_out = count;
@@ -424,6 +539,27 @@ __device__ __forceinline__ void pixel_store(void* __restrict__ out, int ni, int 
 // first lane, j + 1 of the last) cost two more 128-byte lines per 1 KiB row in this XCD's L2:
 // +25% of the input fetched for a five-point stencil.  Any bijection is correct; this one keeps
 // neighbouring blocks in one L2.
+template <int E>
+__device__ __forceinline__ void pix_priv_zero(unsigned* sh) {
+  if constexpr (E > 0)
+    for (int e = threadIdx.x; e < E; e += 256) sh[e] = 0u;
+}
+
+// The block's sums in an LDS copy added to input A, element by element (only those not +0 /
+// 0: adding them would change nothing, beyond turning a -0 target into +0).
+template <class P, int A>
+__device__ __forceinline__ void pix_priv_flush(const PixIn& in, const unsigned* sh) {
+  if constexpr (P::priv[A] > 0) {
+    char* base = const_cast<char*>(reinterpret_cast<const char*>(in.p[A]));
+    for (int e = threadIdx.x; e < P::priv[A]; e += 256) {
+      const unsigned v = sh[e];
+      if (v == 0u) continue;
+      if constexpr (P::in_dtypes[A] == VDSL_I32) atomicAdd(reinterpret_cast<int*>(base) + e, static_cast<int>(v));
+      else unsafeAtomicAdd(reinterpret_cast<float*>(base) + e, __uint_as_float(v));
+    }
+  }
+}
+
 __device__ __forceinline__ unsigned xcd_band(unsigned L, unsigned G) {
   const unsigned x = L % 8, k = L / 8, q = G / 8, r = G % 8;
   return x * q + (x < r ? x : r) + k;  // XCD x takes logical blocks [x q + min(x, r), + q + (x < r))
@@ -433,28 +569,58 @@ template <class P>
 __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, void* __restrict__ out, int ni, int nj) {
   float res[P::rows > 0 ? P::rows : 1][4];
   int count[P::rows > 0 ? P::rows : 1];
+  PixAcc<P> acc{};
+  // per-block LDS copies of the small scatter targets (a histogram's bins), zeroed first
+  __shared__ unsigned sh0[P::priv[0] > 0 ? P::priv[0] : 1], sh1[P::priv[1] > 0 ? P::priv[1] : 1],
+      sh2[P::priv[2] > 0 ? P::priv[2] : 1], sh3[P::priv[3] > 0 ? P::priv[3] : 1];
+  constexpr bool priv = P::priv[0] + P::priv[1] + P::priv[2] + P::priv[3] > 0;
+  if constexpr (priv) {
+    acc.sh[0] = sh0, acc.sh[1] = sh1, acc.sh[2] = sh2, acc.sh[3] = sh3;
+    pix_priv_zero<P::priv[0]>(sh0), pix_priv_zero<P::priv[1]>(sh1), pix_priv_zero<P::priv[2]>(sh2),
+        pix_priv_zero<P::priv[3]>(sh3);
+    __syncthreads();
+  }
   if constexpr (P::rows > 0) {
     const unsigned T = xcd_band(blockIdx.y * gridDim.x + blockIdx.x, gridDim.x * gridDim.y);
     const int j = static_cast<int>((T % gridDim.x) * 256 + threadIdx.x);
     const int i0 = static_cast<int>(T / gridDim.x) * P::rows;
+    if constexpr (P::out_kind == VDSL_PIX_OUT_NONE) {
+      // nothing stored (a reduction into a few elements, whose blocks cover many rows so that
+      // few adds reach memory): the rows in a loop, eight at a time
+#pragma unroll 8
+      for (int t = 0; t < P::rows; ++t) {
+        if constexpr (P::loop)
+          if (i0 + t >= ni) break;
+        float unused[4];
+        int unused_count;
+        pixel_eval<P>(rt, in, ni, nj, i0 + t, j, unused, unused_count, acc);
+      }
+    } else {
 #pragma unroll
-    for (int t = 0; t < P::rows; ++t) {
-      // a loop is not run for the last band's rows past the grid (the same for the whole block);
-      // a program without one evaluates them unconditionally, so the loads of all its rows are
-      // issued together (a branch between them would order them)
-      if constexpr (P::loop)
-        if (i0 + t >= ni) break;
-      pixel_eval<P>(rt, in, ni, nj, i0 + t, j, res[t], count[t]);
+      for (int t = 0; t < P::rows; ++t) {
+        // a loop is not run for the last band's rows past the grid (the same for the whole
+        // block); a program without one evaluates them unconditionally, so the loads of all its
+        // rows are issued together (a branch between them would order them)
+        if constexpr (P::loop)
+          if (i0 + t >= ni) break;
+        pixel_eval<P>(rt, in, ni, nj, i0 + t, j, res[t], count[t], acc);
+      }
+#pragma unroll
+      for (int t = 0; t < P::rows; ++t) pixel_store<P>(out, ni, nj, i0 + t, j, res[t], count[t]);
     }
-#pragma unroll
-    for (int t = 0; t < P::rows; ++t) pixel_store<P>(out, ni, nj, i0 + t, j, res[t], count[t]);
   } else {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int i = static_cast<int>(blockIdx.y * 16 + (wave >> 1) * 8 + (lane >> 3));
     const int j = static_cast<int>(blockIdx.x * 16 + (wave & 1) * 8 + (lane & 7));
-    pixel_eval<P>(rt, in, ni, nj, i, j, res[0], count[0]);
+    pixel_eval<P>(rt, in, ni, nj, i, j, res[0], count[0], acc);
     pixel_store<P>(out, ni, nj, i, j, res[0], count[0]);
+  }
+  pix_flush<P>(rt, in, acc, typename MakeSeq<PixConstAdds<P>::end>::type{});
+  if constexpr (priv) {
+    __syncthreads();
+    pix_priv_flush<P, 0>(in, sh0), pix_priv_flush<P, 1>(in, sh1), pix_priv_flush<P, 2>(in, sh2),
+        pix_priv_flush<P, 3>(in, sh3);
   }
 }
 
