@@ -40,8 +40,9 @@ extern "C" {
 /* 3: vdsl_map_instr.ext and vdsl_map_vinput.mat_dim (matrix operands); 4: VDSL_PIX_TRIP,
  * vdsl_op_relu_bwd, vdsl_op_add (struct layouts unchanged since 3); 5: vdsl_pixel_program.in_rows
  * and in_cols (inputs of another shape than the grid); 6: VDSL_PIX_ATOMIC_ADD,
- * VDSL_PIX_OUT_NONE (scatter-adds) and VDSL_PIX_TRUNC (struct layouts unchanged since 5). */
-#define VDSL_ABI_VERSION 6
+ * VDSL_PIX_OUT_NONE (scatter-adds) and VDSL_PIX_TRUNC (struct layouts unchanged since 5); 7:
+ * VDSL_PIX_MAX_INSTR 256 and VDSL_PIX_MAX_INPUTS 8 (vdsl_pixel_program's arrays grow). */
+#define VDSL_ABI_VERSION 7
 
 typedef enum vdsl_status {
   VDSL_OK = 0,
@@ -312,9 +313,9 @@ int vdsl_op_map_chain_v(vdsl_queue q, int64_t rows, int64_t cols, const vdsl_map
  * recording.  No counterpart in the reference beyond the program surface it runs; the caller is
  * the Taichi-subset front end for kernel bodies other than the escape-time form of
  * vdsl_op_escape_time. */
-#define VDSL_PIX_MAX_INSTR 128
+#define VDSL_PIX_MAX_INSTR 256
 #define VDSL_PIX_MAX_REGS 32
-#define VDSL_PIX_MAX_INPUTS 4
+#define VDSL_PIX_MAX_INPUTS 8
 
 typedef enum vdsl_pix_opcode {
   VDSL_PIX_INDEX = 32,  /* r[dst] = float(i) (a = 0, the outer axis) or float(j) (a = 1) */
@@ -388,7 +389,8 @@ typedef struct vdsl_pixel_program {
 } vdsl_pixel_program;
 
 /* Runs `prog` for every pixel of an [ni][nj] grid.  inputs: f32 [ni][nj][in_widths[k]] or int32
- * [ni][nj] fields (n_inputs <= 4; [in_rows[k]][in_cols[k]] for an input of its own extents); out: f32 [ni][nj][out_width] (VDSL_PIX_OUT_REG) or int32
+ * [ni][nj] fields (n_inputs <= VDSL_PIX_MAX_INPUTS; [in_rows[k]][in_cols[k]] for an input of its own
+ * extents); out: f32 [ni][nj][out_width] (VDSL_PIX_OUT_REG) or int32
  * [ni][nj] (VDSL_PIX_OUT_COUNT, VDSL_PIX_OUT_I32), unused for VDSL_PIX_OUT_NONE.  A program may read its output buffer as an
  * input: at [i][j] that is the pixel's value before the store; elsewhere (LOAD_AT) the result
  * depends on the order pixels run in, as for a Taichi kernel reading the field it writes. */

@@ -32,7 +32,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_abi_version():
     from vernondsl_amd import _lib
-    assert _lib.lib.vdsl_abi_version() == 6
+    assert _lib.lib.vdsl_abi_version() == 7
 
 
 def test_struct_layouts_match_header(tmp_path):

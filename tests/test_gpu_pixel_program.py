@@ -183,7 +183,7 @@ def test_invalid_programs_rejected(dev, q):
         return p
 
     assert "LOAD" in call(good, n_inputs=0, ins=[])
-    assert "at most 128" in call(mutate(n_post=124))
+    assert "at most 256" in call(mutate(n_post=252))
     assert "unknown test" in call(mutate(test=9))
     p = mutate()
     p.code[0].dst = 32  # registers are 0..31
@@ -192,7 +192,7 @@ def test_invalid_programs_rejected(dev, q):
     p.code[0].op = 99
     assert "unknown opcode" in call(p)
     assert "count needs a loop" in call(mutate(loop=0, n_body=0, out_kind=1))
-    assert "n_inputs" in call(good, n_inputs=5, ins=[Tensor(dev, (8, 8), "f32") for _ in range(5)])
+    assert "n_inputs" in call(good, n_inputs=9, ins=[Tensor(dev, (8, 8), "f32") for _ in range(9)])
     small = Tensor(dev, (4, 8), "f32")
     hs = (ctypes.c_void_p * 1)(small.handle)
     with pytest.raises(_lib.VdslError):

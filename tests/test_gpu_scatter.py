@@ -20,8 +20,8 @@ import pytest
 from oracle import oracle
 from vernondsl_amd import _lib, kernels, pixprog as pp, run, taichi_compat as tc
 from vernondsl_amd.rhi import Tensor
-from test_taichi_general import lower_named
-from test_taichi_scatter import escape_counts
+from test_taichi_general import lower_named, run_ops
+from test_taichi_scatter import escape_counts, mpm88_p2g_terms
 
 pytestmark = pytest.mark.gpu
 EX = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "vernondsl_amd", "examples")
@@ -324,3 +324,76 @@ def test_field_host_operations(dev, q):
     assert np.array_equal(vf.to_numpy(), np.full((3, 4, 2), -1.5, f32))
     with pytest.raises(ValueError):
         vf.from_numpy(np.zeros((4, 3, 2), f32))
+
+
+def elem_shape(fld):
+    return fld.mat or ((fld.width,) if fld.width > 1 else ())
+
+
+def test_mpm88_substeps_on_the_device(dev, q):
+    """Two substeps of the mpm88 example, each of its 12 programs run on the device beside the
+    oracle from the same inputs: the particle-to-grid adds (f32, in no fixed order on the device)
+    within the any-order bound per node (and the device's grid carried on), every other program
+    (grid update, the grid-to-particle parts joined by hidden fields, the particle stores) bit for
+    bit."""
+    text = open(os.path.join(EX, "mpm88.py")).read()
+    n, G = 8192, 128
+    init, names_i = lower_named(text, "init", {})
+    sub, names = lower_named(text, "substep", {})
+    host = {"x": np.zeros((n, 2), f32), "v": np.zeros((n, 2), f32), "C": np.zeros((n, 2, 2), f32),
+            "J": np.zeros(n, f32), "grid_v": np.zeros((G, G, 2), f32), "grid_m": np.zeros((G, G), f32)}
+    run_ops(init, names_i, host)
+    fields = {}
+    for op in sub.ops():
+        for f in op.inputs + ([op.field] if op.field is not None else []):
+            fields.setdefault(id(f), f)
+    ts = {}
+
+    def tensor(f):
+        nm = names[id(f)]
+        if nm not in ts:
+            a = host.get(nm)
+            a = np.zeros(f.shape + elem_shape(f), f32) if a is None else a
+            ts[nm] = Tensor.from_numpy(dev, q, np.ascontiguousarray(
+                a.reshape(tc._grid_of(f.shape) + ((f.width,) if f.width > 1 else ())), f32))
+        return ts[nm]
+
+    def read(f):
+        return ts[names[id(f)]].numpy(q).reshape(f.shape + elem_shape(f))
+
+    try:
+        for step in range(2):
+            for k, op in enumerate(sub.ops()):
+                before = {nm: host[nm].copy() for nm in ("x", "v", "C", "J")}
+                run_ops(op, names, host)  # the oracle (names the hidden fields it makes)
+                ins = [tensor(f) for f in op.inputs]
+                out = tensor(op.field) if op.field is not None else None
+                if out is not None and op.field not in op.inputs:
+                    out.buffer.fill_u32(q, 0x7FC00000)  # NaN: every element must be written
+                kernels.pixel_program(q, op.program, ins, out, grid=op.grid)
+                if op.field is not None:
+                    assert np.array_equal(read(op.field), host[names[id(op.field)]]), (step, k, names[id(op.field)])
+                    continue
+                # the particle-to-grid adds: within the bound, then the device's grid is the state
+                idx, terms = mpm88_p2g_terms(before["x"], before["v"], before["C"], before["J"])
+                n_terms = np.ones((G, G))
+                np.add.at(n_terms, idx, 1)
+                gv_d = read(fields[next(i for i, nm in names.items() if nm == "grid_v")])
+                gm_d = read(fields[next(i for i, nm in names.items() if nm == "grid_m")])
+                for got, want, t in ((gv_d[:, :, 0], host["grid_v"][:, :, 0], terms[0]),
+                                     (gv_d[:, :, 1], host["grid_v"][:, :, 1], terms[1]), (gm_d, host["grid_m"], terms[2])):
+                    abs_sum = np.zeros((G, G))
+                    np.add.at(abs_sum, idx, np.abs(t).astype(np.float64))
+                    assert bound_ok(got, want, n_terms, abs_sum), (step, k)
+                host["grid_v"], host["grid_m"] = gv_d.copy(), gm_d.copy()
+        assert abs(float(host["grid_m"].sum(dtype=np.float64)) - n * (1.0 / 256) ** 2) < 1e-6
+    finally:
+        for t in ts.values():
+            t.free()
+
+
+def test_mpm88_example_runs(dev, q):
+    res, pos = run_program(os.path.join(EX, "mpm88.py"), 2)
+    assert res["frames"] == 2 and pos.shape == (8192, 2) and np.isfinite(pos).all()
+    assert 0.0 < float(pos.min()) and float(pos.max()) < 1.0
+    assert float(pos[:, 1].mean()) < 0.4  # the block has fallen (it starts at 0.2 - 0.6)

@@ -191,14 +191,14 @@ def test_rejected_general_bodies(body, msg):
 
 def test_register_pressure_is_reported():
     b = pp.Builder()
-    vals = [b.op("sin", b.op("mul", b.index(0), float(k + 1))) for k in range(40)]
+    vals = [b.op("sin", b.op("mul", b.index(0), float(k + 1))) for k in range(80)]
     acc = vals[0]
     for v in vals[1:]:
         acc = b.op("add", acc, v)
     pp.compile_program(b, out=acc)  # a chain: few registers live at once
     wide = b.op("add", vals[0], vals[1])
-    for k in range(2, 40):
-        wide = b.op("add", wide, b.op("mul", vals[k], vals[(k + 7) % 40]))
+    for k in range(2, 80):
+        wide = b.op("add", wide, b.op("mul", vals[k], vals[(k + 37) % 80]))
     with pytest.raises(pp.ProgramError, match="registers|instructions"):
         pp.compile_program(b, out=wide)
 
@@ -520,12 +520,14 @@ def run_ops(low, names, arrays):
             a = arrays[names[id(f)]]
             p = op.program
             r, c = (p.in_rows[k], p.in_cols[k]) if p.in_rows[k] else (ni, nj)
-            return a.reshape((r, c) + a.shape[len(f.shape):])
+            return a.reshape((r, c) + ((f.width,) if f.width > 1 else ()))  # a matrix field: its components flat
         out = oracle.pixel_program(op.program, ni, nj, [as_input(k, f) for k, f in enumerate(op.inputs)])
         if op.field is None:  # scatter-adds only
             continue
         shape = op.field.shape
         names.setdefault(id(op.field), f"hidden{len(names)}")  # a field the lowering made (between parts)
+        if op.field.mat:
+            out = out.reshape(out.shape[:2] + op.field.mat)
         arrays[names[id(op.field)]] = out.reshape(tuple(shape) + out.shape[2:])
     return arrays
 

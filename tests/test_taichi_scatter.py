@@ -283,3 +283,123 @@ def test_scatter_forms_refused(body, msg):
     text = KERNELS.split("@ti.kernel")[0] + "@ti.kernel\ndef bad():\n    for i, j in a:\n" + body + "\n"
     with pytest.raises(tc.TaichiLoweringError, match=re.escape(msg)):
         lower_named(text, "bad", {})
+
+
+# ---- MPM88: matrices, matrix fields, field-element components, splits between static iterations
+def mpm88_constants(G=128):
+    dx = f32(1.0 / G)
+    dt, E = f32(2e-4), f32(400.0)
+    p_vol = f32((1.0 / G * 0.5) ** 2)
+    p_mass = f32(p_vol * 1.0)
+    return dx, dt, dx * dx, ((-dt * f32(4.0)) * E) * p_vol, p_mass
+
+
+def bspline(Xp):
+    base = np.trunc(Xp - f32(0.5))
+    fx = Xp - base
+    w = [f32(0.5) * ((f32(1.5) - fx) * (f32(1.5) - fx)), f32(0.75) - (fx - f32(1.0)) * (fx - f32(1.0)),
+         f32(0.5) * ((fx - f32(0.5)) * (fx - f32(0.5)))]
+    return base, fx, w
+
+
+def mpm88_p2g_terms(x, v, C, J, G=128):
+    """The particle-to-grid adds of the mpm88 example: (rows, columns) and the momentum (two
+    components) and mass terms, particle by particle and node by node (np.add.at's order)."""
+    dx, dt, inv_dx2, k_stress, p_mass = mpm88_constants(G)
+    base, fx, w = bspline(x / dx)
+    stress = (k_stress * (J - f32(1.0))) / inv_dx2
+    a00 = stress + p_mass * C[:, 0, 0]
+    a01 = f32(0.0) + p_mass * C[:, 0, 1]
+    a10 = f32(0.0) + p_mass * C[:, 1, 0]
+    a11 = stress + p_mass * C[:, 1, 1]
+    rows, cols, vals_v0, vals_v1, vals_m = [], [], [], [], []
+    for i in range(3):
+        for j in range(3):
+            d0 = (f32(i) - fx[:, 0]) * dx
+            d1 = (f32(j) - fx[:, 1]) * dx
+            wt = w[i][:, 0] * w[j][:, 1]
+            m0 = p_mass * v[:, 0] + (a00 * d0 + a01 * d1)
+            m1 = p_mass * v[:, 1] + (a10 * d0 + a11 * d1)
+            rows.append(base[:, 0].astype(np.int64) + i)
+            cols.append(base[:, 1].astype(np.int64) + j)
+            vals_v0.append(wt * m0)
+            vals_v1.append(wt * m1)
+            vals_m.append(wt * p_mass)
+    order = lambda lst: np.stack(lst, 1).ravel()  # particle by particle, node by node
+    return (order(rows), order(cols)), (order(vals_v0), order(vals_v1), order(vals_m))
+
+
+def mpm88_numpy_substep(x, v, C, J, G=128):
+    """One substep of the mpm88 example in numpy f32, the same operations in the same order
+    (constants folded in f32 as the front end folds them); the particle-to-grid adds in the
+    oracle's order (particle by particle, node by node)."""
+    n = x.shape[0]
+    dx, dt, inv_dx2, k_stress, p_mass = mpm88_constants(G)  # dx ** 2 and the stress constant folded in f32
+    gravity = f32(9.8)
+    gv = np.zeros((G, G, 2), f32)
+    gm = np.zeros((G, G), f32)
+    idx, terms = mpm88_p2g_terms(x, v, C, J, G)
+    np.add.at(gv[:, :, 0], idx, terms[0])
+    np.add.at(gv[:, :, 1], idx, terms[1])
+    np.add.at(gm, idx, terms[2])
+    Xp = x / dx
+    base, fx, w = bspline(Xp)
+    # grid update
+    i, j = np.meshgrid(np.arange(G), np.arange(G), indexing="ij")
+    has = gm > f32(0.0)
+    with np.errstate(all="ignore"):
+        vx = np.where(has, gv[:, :, 0] / gm, gv[:, :, 0])
+        vy = np.where(has, gv[:, :, 1] / gm, gv[:, :, 1])
+    vy = vy - dt * gravity
+    vx = np.where((i < 3) & (vx < 0), f32(0.0), vx)
+    vx = np.where((i > G - 3) & (vx > 0), f32(0.0), vx)
+    vy = np.where((j < 3) & (vy < 0), f32(0.0), vy)
+    vy = np.where((j > G - 3) & (vy > 0), f32(0.0), vy)
+    gv = np.stack([vx, vy], -1).astype(f32)
+    # grid to particles
+    nv = [np.zeros(n, f32), np.zeros(n, f32)]
+    nC = [[np.zeros(n, f32), np.zeros(n, f32)], [np.zeros(n, f32), np.zeros(n, f32)]]
+    for a in range(3):
+        for c in range(3):
+            d = [(f32(a) - fx[:, 0]) * dx, (f32(c) - fx[:, 1]) * dx]
+            wt = w[a][:, 0] * w[c][:, 1]
+            g = gv[base[:, 0].astype(np.int64) + a, base[:, 1].astype(np.int64) + c]
+            for k in range(2):
+                nv[k] = nv[k] + wt * g[:, k]
+            s = f32(4.0) * wt
+            for r in range(2):
+                for q in range(2):
+                    nC[r][q] = nC[r][q] + (s * (g[:, r] * d[q])) / inv_dx2
+    v2 = np.stack(nv, -1)
+    x2 = x + dt * v2
+    J2 = J * (f32(1.0) + dt * (nC[0][0] + nC[1][1]))
+    C2 = np.stack([np.stack(nC[0], -1), np.stack(nC[1], -1)], -2)
+    return x2, v2, C2, J2, gv, gm
+
+
+def test_mpm88_substeps_on_the_oracle_equal_numpy():
+    """The example's init and two substeps (12 programs each: the grid-to-particle loop runs as
+    parts joined by hidden fields, split between static iterations) against the numpy
+    restatement, bit for bit: matrices (ti.Matrix, @, outer_product, trace, matrix fields), the
+    grid-velocity component updates and the scatter-adds."""
+    text = open(os.path.join(EX, "mpm88.py")).read()
+    init, names_i = lower_named(text, "init", {})
+    sub, names = lower_named(text, "substep", {})
+    n, G = 8192, 128
+    arrays = {"x": np.zeros((n, 2), f32), "v": np.zeros((n, 2), f32), "C": np.zeros((n, 2, 2), f32),
+              "J": np.zeros(n, f32), "grid_v": np.zeros((G, G, 2), f32), "grid_m": np.zeros((G, G), f32)}
+    run_ops(init, names_i, arrays)
+    p = np.arange(n)
+    x0 = np.stack([((p * 37 % 1009).astype(f32) / f32(1009.0)) * f32(0.4) + f32(0.2),
+                   ((p * 59 % 997).astype(f32) / f32(997.0)) * f32(0.4) + f32(0.2)], -1)
+    assert np.array_equal(arrays["x"], x0) and np.all(arrays["J"] == 1.0)
+    ref = (arrays["x"].copy(), arrays["v"].copy(), arrays["C"].copy(), arrays["J"].copy())
+    for _ in range(2):
+        run_ops(sub, names, arrays)
+        x2, v2, C2, J2, gv, gm = mpm88_numpy_substep(*ref)
+        assert np.array_equal(arrays["grid_m"], gm)
+        assert np.array_equal(arrays["grid_v"], gv)
+        for k, want in (("v", v2), ("x", x2), ("C", C2), ("J", J2)):
+            assert np.array_equal(arrays[k], want), k
+        ref = (x2, v2, C2, J2)
+    assert abs(float(arrays["grid_m"].sum(dtype=np.float64)) - n * (1.0 / 256) ** 2) < 1e-6  # mass is conserved

@@ -126,7 +126,7 @@ int main(void) {
   pp.code[2].op = VDSL_PIX_SELECT; pp.code[2].dst = 2; pp.code[2].a = 0; pp.code[2].b = 1; pp.code[2].c = 0;
   EXPECT_OK(vdsl_op_pixel_program(q, 8, 16, &pp, NULL, 0, a));
   EXPECT_ERR(vdsl_op_pixel_program(q, 64, 64, &pp, NULL, 0, a)); /* out too small */
-  EXPECT_ERR(vdsl_op_pixel_program(q, 8, 16, &pp, NULL, 5, a));  /* too many inputs */
+  EXPECT_ERR(vdsl_op_pixel_program(q, 8, 16, &pp, NULL, VDSL_PIX_MAX_INPUTS + 1, a));  /* too many inputs */
   pp.out_width = 5;
   EXPECT_ERR(vdsl_op_pixel_program(q, 8, 16, &pp, NULL, 0, a));  /* at most 4 components */
   pp.out_width = 4;

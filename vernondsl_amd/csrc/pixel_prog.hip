@@ -93,17 +93,24 @@ std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p);
 
 // Elements (x components) of input k when its scatter-adds go to a copy in LDS per block
 // (pixprog_kern.h), else 0: a target of at most kPrivMax elements that some add reaches at
-// per-pixel indices (a histogram).  Adds at constant indices are summed in registers instead.
+// per-pixel indices (a histogram), while the copies of the targets before it and its own take
+// at most kPrivMax elements in all (32 KiB of a block's LDS).  Adds at constant indices are
+// summed in registers instead.
 constexpr int kPrivMax = 8192;
 int privatized(const vdsl_pixel_program& p, int k, int ni, int nj) {
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   const std::vector<char> flags = row_uniform_gathers(p);
-  bool per_pixel = false;
-  for (int pc = 0; pc < total; ++pc)
-    per_pixel |= p.code[pc].op == VDSL_PIX_ATOMIC_ADD && p.code[pc].a == k && !(flags[pc] & 4);
-  const int64_t elems = static_cast<int64_t>(p.in_rows[k] ? p.in_rows[k] : ni) * (p.in_cols[k] ? p.in_cols[k] : nj) *
-                        p.in_widths[k];
-  return per_pixel && elems <= kPrivMax ? static_cast<int>(elems) : 0;
+  int64_t used = 0, own = 0;
+  for (int t = 0; t <= k; ++t) {
+    bool per_pixel = false;
+    for (int pc = 0; pc < total; ++pc)
+      per_pixel |= p.code[pc].op == VDSL_PIX_ATOMIC_ADD && p.code[pc].a == t && !(flags[pc] & 4);
+    const int64_t elems = static_cast<int64_t>(p.in_rows[t] ? p.in_rows[t] : ni) * (p.in_cols[t] ? p.in_cols[t] : nj) *
+                          p.in_widths[t];
+    own = per_pixel && used + elems <= kPrivMax ? elems : 0;
+    used += own;
+  }
+  return static_cast<int>(own);
 }
 
 // Rows per block in the row mapping (each thread evaluates that many pixels of its column, then
@@ -248,16 +255,24 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni, in
     if (p.in_rows[k]) elems = std::max(elems, static_cast<int64_t>(p.in_rows[k]) * p.in_cols[k]);
   c("idx32", elems * maxw * 4 <= int64_t{0xffffffff} ? 1 : 0);
   // Entries past out_width / n_inputs are not used: written as 0 / 1, so they do not split the cache.
-  auto list = [&](const char* name, const int32_t* v, int n, int fill) {
-    s += std::string("  static constexpr int ") + name + "[4] = {";
-    for (int k = 0; k < 4; ++k) s += std::to_string(k < n ? v[k] : fill) + (k < 3 ? ", " : "};\n");
+  auto list = [&](const char* name, const int32_t* v, int n, int fill, int size) {
+    s += std::string("  static constexpr int ") + name + "[" + std::to_string(size) + "] = {";
+    for (int k = 0; k < size; ++k) s += std::to_string(k < n ? v[k] : fill) + (k < size - 1 ? ", " : "};\n");
   };
-  list("out_regs", p.out_regs, p.out_width, 0);
-  list("in_widths", p.in_widths, n_inputs, 1);
-  list("in_dtypes", p.in_dtypes, n_inputs, VDSL_F32);
-  int32_t priv[VDSL_PIX_MAX_INPUTS] = {};
-  for (int k = 0; k < n_inputs; ++k) priv[k] = privatized(p, k, ni, nj);
-  list("priv", priv, n_inputs, 0);
+  list("out_regs", p.out_regs, p.out_width, 0, 4);
+  list("in_widths", p.in_widths, n_inputs, 1, VDSL_PIX_MAX_INPUTS);
+  list("in_dtypes", p.in_dtypes, n_inputs, VDSL_F32, VDSL_PIX_MAX_INPUTS);
+  // per-block LDS copies of small scatter targets: sizes and offsets in one array
+  int32_t priv[VDSL_PIX_MAX_INPUTS] = {}, priv_off[VDSL_PIX_MAX_INPUTS] = {};
+  int32_t priv_total = 0;
+  for (int k = 0; k < n_inputs; ++k) {
+    priv[k] = privatized(p, k, ni, nj);
+    priv_off[k] = priv_total;
+    priv_total += priv[k];
+  }
+  list("priv", priv, n_inputs, 0, VDSL_PIX_MAX_INPUTS);
+  list("priv_off", priv_off, n_inputs, 0, VDSL_PIX_MAX_INPUTS);
+  c("priv_total", priv_total);
   // ext[0] / ext[1] of a gather or scatter-add: 1 when its row / column operand is wave-uniform in
   // the row mapping; ext[2] of a scatter-add: 1 when both are constants
   const std::vector<char> ru = row_uniform_gathers(p);
@@ -285,7 +300,8 @@ extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const
   VDSL_TRY(enter_queue(q));
   if (!prog) return fail(VDSL_ERR_INVALID_ARG, "prog is null");
   if (ni < 0 || nj < 0) return fail(VDSL_ERR_INVALID_ARG, "negative grid extent");
-  if (n_inputs < 0 || n_inputs > VDSL_PIX_MAX_INPUTS) return fail(VDSL_ERR_INVALID_ARG, "n_inputs out of range [0, 4]");
+  if (n_inputs < 0 || n_inputs > VDSL_PIX_MAX_INPUTS)
+    return fail(VDSL_ERR_INVALID_ARG, "n_inputs out of range [0, " + std::to_string(VDSL_PIX_MAX_INPUTS) + "]");
   if (n_inputs && !inputs) return fail(VDSL_ERR_INVALID_ARG, "inputs is null");
   const vdsl_pixel_program& p = *prog;
   VDSL_TRY(check_program(p, n_inputs));

@@ -539,12 +539,6 @@ __device__ __forceinline__ void pixel_store(void* __restrict__ out, int ni, int 
 // first lane, j + 1 of the last) cost two more 128-byte lines per 1 KiB row in this XCD's L2:
 // +25% of the input fetched for a five-point stencil.  Any bijection is correct; this one keeps
 // neighbouring blocks in one L2.
-template <int E>
-__device__ __forceinline__ void pix_priv_zero(unsigned* sh) {
-  if constexpr (E > 0)
-    for (int e = threadIdx.x; e < E; e += 256) sh[e] = 0u;
-}
-
 // The block's sums in an LDS copy added to input A, element by element (only those not +0 /
 // 0: adding them would change nothing, beyond turning a -0 target into +0).
 template <class P, int A>
@@ -552,12 +546,17 @@ __device__ __forceinline__ void pix_priv_flush(const PixIn& in, const unsigned* 
   if constexpr (P::priv[A] > 0) {
     char* base = const_cast<char*>(reinterpret_cast<const char*>(in.p[A]));
     for (int e = threadIdx.x; e < P::priv[A]; e += 256) {
-      const unsigned v = sh[e];
+      const unsigned v = sh[P::priv_off[A] + e];
       if (v == 0u) continue;
       if constexpr (P::in_dtypes[A] == VDSL_I32) atomicAdd(reinterpret_cast<int*>(base) + e, static_cast<int>(v));
       else unsafeAtomicAdd(reinterpret_cast<float*>(base) + e, __uint_as_float(v));
     }
   }
+}
+
+template <class P, int... A>
+__device__ __forceinline__ void pix_priv_flush_all(const PixIn& in, const unsigned* sh, Seq<A...>) {
+  (pix_priv_flush<P, A>(in, sh), ...);
 }
 
 __device__ __forceinline__ unsigned xcd_band(unsigned L, unsigned G) {
@@ -570,14 +569,14 @@ __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, voi
   float res[P::rows > 0 ? P::rows : 1][4];
   int count[P::rows > 0 ? P::rows : 1];
   PixAcc<P> acc{};
-  // per-block LDS copies of the small scatter targets (a histogram's bins), zeroed first
-  __shared__ unsigned sh0[P::priv[0] > 0 ? P::priv[0] : 1], sh1[P::priv[1] > 0 ? P::priv[1] : 1],
-      sh2[P::priv[2] > 0 ? P::priv[2] : 1], sh3[P::priv[3] > 0 ? P::priv[3] : 1];
-  constexpr bool priv = P::priv[0] + P::priv[1] + P::priv[2] + P::priv[3] > 0;
+  // per-block LDS copies of the small scatter targets (a histogram's bins), in one array at the
+  // offsets the host chose, zeroed first
+  __shared__ unsigned sh[P::priv_total > 0 ? P::priv_total : 1];
+  constexpr bool priv = P::priv_total > 0;
   if constexpr (priv) {
-    acc.sh[0] = sh0, acc.sh[1] = sh1, acc.sh[2] = sh2, acc.sh[3] = sh3;
-    pix_priv_zero<P::priv[0]>(sh0), pix_priv_zero<P::priv[1]>(sh1), pix_priv_zero<P::priv[2]>(sh2),
-        pix_priv_zero<P::priv[3]>(sh3);
+#pragma unroll
+    for (int k = 0; k < VDSL_PIX_MAX_INPUTS; ++k) acc.sh[k] = sh + P::priv_off[k];
+    for (int e = threadIdx.x; e < P::priv_total; e += 256) sh[e] = 0u;
     __syncthreads();
   }
   if constexpr (P::rows > 0) {
@@ -619,8 +618,7 @@ __device__ __forceinline__ void pixel_body(const PixRt& rt, const PixIn& in, voi
   pix_flush<P>(rt, in, acc, typename MakeSeq<PixConstAdds<P>::end>::type{});
   if constexpr (priv) {
     __syncthreads();
-    pix_priv_flush<P, 0>(in, sh0), pix_priv_flush<P, 1>(in, sh1), pix_priv_flush<P, 2>(in, sh2),
-        pix_priv_flush<P, 3>(in, sh3);
+    pix_priv_flush_all<P>(in, sh, typename MakeSeq<VDSL_PIX_MAX_INPUTS>::type{});
   }
 }
 

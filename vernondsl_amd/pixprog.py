@@ -23,7 +23,7 @@ import numpy as np
 
 from . import _lib
 
-MAX_INSTR, MAX_REGS, MAX_INPUTS = 128, 32, 4
+MAX_INSTR, MAX_REGS, MAX_INPUTS = 256, 32, 8
 OP = dict(_lib.MAP_OPS)
 OP.update({"index": 32, "cos": 33, "sin": 34, "count": 35, "lt": 36, "le": 37, "eq": 38, "ne": 39, "select": 40,
            "floor": 41, "load_at": 42, "trip": 43, "atomic_add": 44, "trunc": 45})

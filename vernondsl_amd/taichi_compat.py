@@ -53,6 +53,7 @@ from __future__ import annotations
 
 import ast
 import collections
+import copy
 import inspect
 import itertools
 import math as _pymath
@@ -107,7 +108,8 @@ class Field:
     vectors of `width` f32 components (ti.Vector.field).  Storage is a device tensor ([W][H],
     [N], [1] for 0-D, plus [width] for vectors), allocated and zeroed on first use."""
 
-    def __init__(self, dtype, shape, width=1):
+    def __init__(self, dtype, shape, width=1, mat=None):
+        self.mat = tuple(mat) if mat else None  # (n, m) for a field of n x m matrices (row-major components)
         if dtype in (float, f32, None):
             self.dtype = f32
         elif dtype in (int, i32):
@@ -127,7 +129,7 @@ class Field:
         """A hidden field of this one's type and shape, made once: the copy of its values taken
         before a struct-for's programs when one of them stores it and another loads it."""
         if self._snap is None:
-            self._snap = Field(self.dtype, self.shape, self.width)
+            self._snap = Field(self.dtype, self.shape, self.width, self.mat)
         return self._snap
 
     def tensor(self):
@@ -200,6 +202,19 @@ class Vector:  # only meaningful inside kernels, where the lowering interprets i
     def field(n, dtype=float, shape=None, **_kw):
         """ti.Vector.field(n, dtype, shape): a 2-D field of n-component f32 vectors."""
         return Field(dtype, shape, width=n)
+
+
+class Matrix:  # only meaningful inside kernels, where the lowering interprets it
+    def __init__(self, *_a, **_k):
+        raise TaichiLoweringError("ti.Matrix is only available inside @ti.kernel / @ti.func code")
+
+    @staticmethod
+    def field(n, m, dtype=float, shape=None, **_kw):
+        """ti.Matrix.field(n, m, dtype, shape): a field of n x m f32 matrices (n m <= 4), stored
+        row-major as n m components per element."""
+        if n * m > 4:
+            raise TaichiLoweringError("matrix fields hold at most 4 components (2 x 2)")
+        return Field(dtype, shape, width=n * m, mat=(n, m))
 
 
 def cos(x):
@@ -731,10 +746,15 @@ def _parse_source(text: str, kernel_name: str, args: dict):
             if isinstance(v, ast.Call) and isinstance(v.func, ast.Attribute) and v.func.attr == "field":
                 kw = {k.arg: k.value for k in v.keywords}
                 is_vec = isinstance(v.func.value, ast.Attribute) and v.func.value.attr == "Vector"
+                is_mat = isinstance(v.func.value, ast.Attribute) and v.func.value.attr == "Matrix"
                 pos = list(v.args)
-                width = 1
+                width, mat = 1, None
                 if is_vec:  # ti.Vector.field(n, dtype, shape)
                     width = interp.expr(kw["n"] if "n" in kw else pos.pop(0), {})
+                elif is_mat:  # ti.Matrix.field(n, m, dtype, shape)
+                    mat = (interp.expr(kw["n"] if "n" in kw else pos.pop(0), {}),
+                           interp.expr(kw["m"] if "m" in kw else pos.pop(0), {}))
+                    width = mat[0] * mat[1]
                 elif "n" in kw:
                     raise TaichiLoweringError("ti.field takes no component count")
                 if "dtype" not in kw and pos:  # ti.field(dtype, shape)
@@ -745,7 +765,7 @@ def _parse_source(text: str, kernel_name: str, args: dict):
                 dt = kw.get("dtype")
                 dtype = f32 if dt is None or (isinstance(dt, ast.Name) and dt.id == "float") else (
                     i32 if (isinstance(dt, ast.Name) and dt.id == "int") or getattr(dt, "attr", "") in ("i32", "int32") else f32)
-                env[st.targets[0].id] = Field(dtype, shape, width=int(width))
+                env[st.targets[0].id] = Field(dtype, shape, width=int(width), mat=mat)
             else:
                 try:
                     env[st.targets[0].id] = interp.expr(v, {})
@@ -843,6 +863,26 @@ class _PVec:
         self.comps = list(comps)
 
 
+class _PMat:
+    """A small matrix (ti.Matrix) of per-pixel values, as rows of numbers or pixprog Nodes."""
+
+    def __init__(self, rows):
+        self.rows = [list(r) for r in rows]
+        if not self.rows or any(len(r) != len(self.rows[0]) for r in self.rows) or not self.rows[0]:
+            raise TaichiLoweringError("a matrix has rows of one length")
+
+    @property
+    def shape(self):
+        return len(self.rows), len(self.rows[0])
+
+    def flat(self):
+        return [x for r in self.rows for x in r]
+
+    @staticmethod
+    def of(flat, n, m):
+        return _PMat([flat[i * m:(i + 1) * m] for i in range(n)])
+
+
 _UNARY_FUNCS = {"sqrt": "sqrt", "exp": "exp", "log": "log", "sin": "sin", "cos": "cos", "tanh": "tanh", "abs": "abs",
                 "floor": "floor"}
 def _skey(fld):
@@ -918,6 +958,16 @@ class _PixInterp:
         return r
 
     def _arith(self, op, x, y):
+        if isinstance(x, _PMat) or isinstance(y, _PMat):
+            # element by element (Taichi's * of two matrices is too; @ is the product)
+            if isinstance(x, _PVec) or isinstance(y, _PVec):
+                raise TaichiLoweringError("a matrix and a vector combine with @, not element by element")
+            if isinstance(x, _PMat) and isinstance(y, _PMat) and x.shape != y.shape:
+                raise TaichiLoweringError(f"matrix shapes {x.shape} and {y.shape} differ")
+            n, m = (x if isinstance(x, _PMat) else y).shape
+            xf = x.flat() if isinstance(x, _PMat) else [x] * (n * m)
+            yf = y.flat() if isinstance(y, _PMat) else [y] * (n * m)
+            return _PMat.of([self.arith(op, a, c) for a, c in zip(xf, yf)], n, m)
         if isinstance(x, _PVec) or isinstance(y, _PVec):
             xs = x.comps if isinstance(x, _PVec) else None
             ys = y.comps if isinstance(y, _PVec) else None
@@ -941,6 +991,8 @@ class _PixInterp:
     def unary(self, fn, x):
         if isinstance(x, _PVec):
             return _PVec([self.unary(fn, c) for c in x.comps])
+        if isinstance(x, _PMat):
+            return _PMat.of([self.unary(fn, c) for c in x.flat()], *x.shape)
         if isinstance(x, (int, np.integer)) and not isinstance(x, bool) and fn in ("neg", "abs"):
             return -int(x) if fn == "neg" else abs(int(x))  # integers stay exact integers
         if _is_num(x):
@@ -951,6 +1003,63 @@ class _PixInterp:
         r = self.b.op(fn, x)
         bx = self._ib(x)
         return self._int_result(r, bx, fn) if fn in ("neg", "abs", "floor") and bx is not None else r
+
+    def matmul(self, a, c):
+        """a @ c for matrices and vectors (a vector is a column, or a row on the left): each
+        element a[i][0] c[0][j] + a[i][1] c[1][j] + ..., summed in that order."""
+        def rows(v, left):
+            if isinstance(v, _PMat):
+                return v.rows
+            if isinstance(v, _PVec):
+                return [list(v.comps)] if left else [[x] for x in v.comps]
+            raise TaichiLoweringError("@ takes matrices and vectors")
+        ra, rc = rows(a, True), rows(c, False)
+        if len(ra[0]) != len(rc):
+            raise TaichiLoweringError(f"@ of a {len(ra)} x {len(ra[0])} and a {len(rc)} x {len(rc[0])} operand")
+        out = []
+        for i in range(len(ra)):
+            row = []
+            for j in range(len(rc[0])):
+                acc = self.arith("mul", ra[i][0], rc[0][j])
+                for k in range(1, len(rc)):
+                    acc = self.arith("add", acc, self.arith("mul", ra[i][k], rc[k][j]))
+                row.append(acc)
+            out.append(row)
+        if isinstance(c, _PVec):
+            return _PVec([r[0] for r in out])
+        if isinstance(a, _PVec):
+            return _PVec(out[0])
+        return _PMat(out)
+
+    def mat_method(self, mat, name, args):
+        n, m = mat.shape
+        if name == "transpose":
+            return _PMat([[mat.rows[i][j] for i in range(n)] for j in range(m)])
+        if name == "trace":
+            if n != m:
+                raise TaichiLoweringError("trace of a square matrix")
+            acc = mat.rows[0][0]
+            for i in range(1, n):
+                acc = self.arith("add", acc, mat.rows[i][i])
+            return acc
+        if name == "determinant":
+            r = mat.rows
+            if (n, m) == (1, 1):
+                return r[0][0]
+            if (n, m) == (2, 2):
+                return self.arith("sub", self.arith("mul", r[0][0], r[1][1]), self.arith("mul", r[0][1], r[1][0]))
+            if (n, m) == (3, 3):
+                def minor(a, b, c, d):
+                    return self.arith("sub", self.arith("mul", a, d), self.arith("mul", b, c))
+                t0 = self.arith("mul", r[0][0], minor(r[1][1], r[1][2], r[2][1], r[2][2]))
+                t1 = self.arith("mul", r[0][1], minor(r[1][0], r[1][2], r[2][0], r[2][2]))
+                t2 = self.arith("mul", r[0][2], minor(r[1][0], r[1][1], r[2][0], r[2][1]))
+                return self.arith("add", self.arith("sub", t0, t1), t2)
+            raise TaichiLoweringError("determinant of a 1 x 1, 2 x 2 or 3 x 3 matrix")
+        if name in ("norm", "norm_sqr"):
+            f = _PVec(mat.flat())
+            return self.dot(f, f) if name == "norm_sqr" else self.unary("sqrt", self.dot(f, f))
+        raise TaichiLoweringError(f"matrix method {name!r} is not supported")
 
     def dot(self, a, c):
         if not (isinstance(a, _PVec) and isinstance(c, _PVec) and len(a.comps) == len(c.comps)):
@@ -984,6 +1093,8 @@ class _PixInterp:
             x, y = self.expr(n.left, local), self.expr(n.right, local)
             if isinstance(n.op, (ast.Mod, ast.FloorDiv)):
                 return self.floor_op(type(n.op) is ast.Mod, x, y)
+            if isinstance(n.op, ast.MatMult):
+                return self.matmul(x, y)
             if type(n.op) not in ops:
                 raise TaichiLoweringError(f"operator {type(n.op).__name__} is not supported")
             return self.arith(ops[type(n.op)], x, y)
@@ -1012,6 +1123,9 @@ class _PixInterp:
                 return base.comps[int(idx)]
             if isinstance(base, list) and isinstance(idx, (int, np.integer)) and -len(base) <= idx < len(base):
                 return base[int(idx)]  # a Python list of values (w[i] of a list of weight vectors)
+            if isinstance(base, _PMat) and isinstance(idx, list) and len(idx) == 2 and \
+                    all(isinstance(k, (int, np.integer)) for k in idx):
+                return base.rows[int(idx[0])][int(idx[1])]
             raise TaichiLoweringError("only constant vector indexing and field[i, j] reads are supported")
         if isinstance(n, ast.Attribute):
             base = self.expr(n.value, local)
@@ -1052,6 +1166,13 @@ class _PixInterp:
         return ast.Tuple(elts=[ast.Name(id=n, ctx=ast.Load()) for n in self.names], ctx=ast.Load())
 
     def field_read(self, fld, idx, local):
+        """fld[idx] as _field_read gives it; a field of matrices as a matrix."""
+        v = self._field_read(fld, idx, local)
+        if fld.mat and isinstance(v, _PVec):
+            return _PMat.of(v.comps, *fld.mat)
+        return v
+
+    def _field_read(self, fld, idx, local):
         """fld[i, j] (this pixel), or fld[e1, e2] at per-pixel indices (a stencil or gather read,
         clamped to the field, whose shape must be the struct-for's); fld[i] / fld[e] in a 1-D
         struct-for, which runs as one row (row index 0)."""
@@ -1109,7 +1230,33 @@ class _PixInterp:
                     return self.cross(base, self.expr(n.args[0], local))
                 if f.attr == "cast":
                     return self.cast(base, self.expr(n.args[0], local))
+                if f.attr == "outer_product":
+                    c = self.expr(n.args[0], local)
+                    if not isinstance(c, _PVec):
+                        raise TaichiLoweringError("outer_product takes a vector")
+                    return _PMat([[self.arith("mul", a, d) for d in c.comps] for a in base.comps])
                 raise TaichiLoweringError(f"vector method {f.attr!r} is not supported")
+            if isinstance(base, _PMat):
+                if f.attr == "cast":
+                    return self.cast(base, self.expr(n.args[0], local))
+                return self.mat_method(base, f.attr, [self.expr(a, local) for a in n.args])
+            if base is Matrix or base is Vector:  # ti.Matrix.zero / identity, ti.Vector.zero / one
+                vals = [self.expr(a, local) for a in n.args[1:]]
+                if not all(isinstance(v, (int, np.integer)) for v in vals):
+                    raise TaichiLoweringError(f"ti.{base.__name__}.{f.attr} takes (dtype, sizes)")
+                if base is Vector and f.attr in ("zero", "one") and len(vals) == 1:
+                    return _PVec([0.0 if f.attr == "zero" else 1.0] * int(vals[0]))
+                if base is Matrix and f.attr == "zero" and len(vals) == 2:
+                    return _PMat([[0.0] * int(vals[1]) for _ in range(int(vals[0]))])
+                if base is Matrix and f.attr == "identity" and len(vals) == 1:
+                    k = int(vals[0])
+                    return _PMat([[1.0 if i == j else 0.0 for j in range(k)] for i in range(k)])
+                raise TaichiLoweringError(f"ti.{base.__name__}.{f.attr} is not supported")
+            if f.attr == "Matrix":
+                rows = self.expr(n.args[0], local)
+                if not isinstance(rows, list) or not all(isinstance(r, (list, _PVec)) for r in rows):
+                    raise TaichiLoweringError("ti.Matrix takes a list of rows")
+                return _PMat([r.comps if isinstance(r, _PVec) else r for r in rows])
             if f.attr == "Vector":
                 comps = self.expr(n.args[0], local)
                 if not isinstance(comps, list) or any(isinstance(c, _PVec) for c in comps):
@@ -1167,6 +1314,8 @@ class _PixInterp:
         int conversion), to a float type keeps the value."""
         if isinstance(v, _PVec):
             return _PVec([self.cast(c, dtype) for c in v.comps])
+        if isinstance(v, _PMat):
+            return _PMat.of([self.cast(c, dtype) for c in v.flat()], *v.shape)
         if dtype in (float, f32, f64):
             return _f32(v) if _is_num(v) and not isinstance(v, (int, np.integer)) else v
         if dtype not in (int, i32):
@@ -1227,6 +1376,10 @@ class _PixInterp:
                                     self.cmp_value("le", 0.0, b2), self.cmp_value("lt", b2, float(B))])
             row = self.select(ok, self.arith("add", self.arith("mul", a, float(B)), b2), -1.0)
         v = _PVec(value) if isinstance(value, list) else value
+        if isinstance(v, _PMat):
+            if fld.mat != v.shape:
+                raise TaichiLoweringError("a matrix is added into a field of matrices of its shape")
+            v = _PVec(v.flat())
         if fld.width == 1:
             if isinstance(v, _PVec):
                 raise TaichiLoweringError("a field of scalars takes a scalar")
@@ -1394,6 +1547,10 @@ class _PixInterp:
         return self._bool(self.b.op("eq", t, 0.0))
 
     def select(self, c, x, y):
+        if isinstance(x, _PMat) or isinstance(y, _PMat):
+            if not (isinstance(x, _PMat) and isinstance(y, _PMat) and x.shape == y.shape):
+                raise TaichiLoweringError("a conditional picks between two matrices of one shape")
+            return _PMat.of([self.select(c, a, d) for a, d in zip(x.flat(), y.flat())], *x.shape)
         if isinstance(x, _PVec) or isinstance(y, _PVec):
             if not (isinstance(x, _PVec) and isinstance(y, _PVec) and len(x.comps) == len(y.comps)):
                 raise TaichiLoweringError("a conditional picks between two vectors of one length or two scalars")
@@ -1465,7 +1622,7 @@ class _PixInterp:
             if _is_skey(nm):  # the field keeps its value where a branch does not store
                 keep = local.get(nm)
                 if keep is None:
-                    keep = self.field_read(self.fields[nm[1]], self._here(), {})
+                    keep = self._field_read(self.fields[nm[1]], self._here(), {})
                 vt = keep if vt is _ONE_BRANCH else vt
                 vf = keep if vf is _ONE_BRANCH else vf
             elif vt is _ONE_BRANCH or vf is _ONE_BRANCH or vt is _UNREADABLE or vf is _UNREADABLE:
@@ -1522,10 +1679,84 @@ class _PixInterp:
             return list(vals)
         raise TaichiLoweringError("ti.static loops over range(...) or a list of values")
 
+    def store_here(self, target, v, local):
+        """target[i, j] = v (this pixel's element; kept as the stored value, components flat)."""
+        if self.in_loop:
+            raise TaichiLoweringError("a store inside the loop is not supported (store after it)")
+        if isinstance(v, list):
+            v = _PVec(v)
+        if isinstance(v, _PMat):
+            if target.mat != v.shape:
+                raise TaichiLoweringError(f"a {v.shape[0]} x {v.shape[1]} matrix stored to a field of "
+                                          f"{'matrices ' + str(target.mat) if target.mat else 'vectors or scalars'}")
+            v = _PVec(v.flat())
+        if target.width == 1:
+            if isinstance(v, _PVec):
+                raise TaichiLoweringError("a field of scalars stores a scalar")
+        elif not isinstance(v, _PVec):
+            v = _PVec([v] * target.width)  # a scalar fills every component
+        elif len(v.comps) != target.width:
+            raise TaichiLoweringError(f"a field of {target.width}-vectors stores {target.width} components")
+        if target in self.targets:
+            raise TaichiLoweringError("a field is both stored at the loop index and scatter-added into in one struct-for")
+        if target not in self.stored:
+            self.stored.append(target)
+            self.fields[id(target)] = target
+        local[_skey(target)] = v
+
+    def element_component_assign(self, st, tgt, local):
+        """field[i, j].y op= v, field[i, j][k] op= v, field[i, j][a, b] = v (a matrix field): this
+        pixel's element with one component replaced, stored again."""
+        sub = tgt.value
+        fld = self.expr(sub.value, local)
+        if not (isinstance(fld, Field) and self._at_here(fld, sub.slice)):
+            raise TaichiLoweringError("a component is assigned in this pixel's element of a field (field[i, j].x = v)")
+        cur = self._field_read(fld, sub.slice, local)
+        comps = list(cur.comps) if isinstance(cur, _PVec) else [cur]
+        if isinstance(tgt, ast.Attribute):
+            if tgt.attr not in ("x", "y", "z", "w") or "xyzw".index(tgt.attr) >= len(comps):
+                raise TaichiLoweringError(f"the field's elements have no component {tgt.attr!r}")
+            k = "xyzw".index(tgt.attr)
+        else:
+            idx = self.expr(tgt.slice, local)
+            if fld.mat and isinstance(idx, list) and len(idx) == 2 and all(isinstance(x, (int, np.integer)) for x in idx):
+                k = int(idx[0]) * fld.mat[1] + int(idx[1])
+            elif isinstance(idx, (int, np.integer)) and 0 <= idx < len(comps):
+                k = int(idx)
+            else:
+                raise TaichiLoweringError("a field element's component is set at a constant index")
+        val = self.expr(st.value, local)
+        if isinstance(st, ast.AugAssign):
+            ops = {ast.Add: "add", ast.Sub: "sub", ast.Mult: "mul", ast.Div: "div"}
+            if type(st.op) not in ops:
+                raise TaichiLoweringError(f"augmented {type(st.op).__name__} is not supported")
+            val = self.arith(ops[type(st.op)], comps[k], val)
+        if isinstance(val, (_PVec, _PMat)):
+            raise TaichiLoweringError("a component takes a scalar")
+        comps[k] = val
+        self.store_here(fld, _PVec(comps) if len(comps) > 1 else comps[0], local)
+        return True
+
     def component_assign(self, st, tgt, local):
-        """v[k] = x, v.x = x, v[k] += x on a local vector: a new vector with component k replaced."""
+        """v[k] = x, v.x = x, v[k] += x on a local vector (M[a, b] on a local matrix): a new value
+        with that component replaced."""
         name = tgt.value.id
         vec = local[name]
+        if isinstance(vec, _PMat):
+            idx = self.expr(tgt.slice, local) if isinstance(tgt, ast.Subscript) else None
+            if not (isinstance(idx, list) and len(idx) == 2 and all(isinstance(x, (int, np.integer)) for x in idx)):
+                raise TaichiLoweringError("a matrix component is set as M[a, b] at constant indices")
+            a, c = int(idx[0]), int(idx[1])
+            val = self.expr(st.value, local)
+            if isinstance(st, ast.AugAssign):
+                ops = {ast.Add: "add", ast.Sub: "sub", ast.Mult: "mul", ast.Div: "div"}
+                if type(st.op) not in ops:
+                    raise TaichiLoweringError(f"augmented {type(st.op).__name__} is not supported")
+                val = self.arith(ops[type(st.op)], vec.rows[a][c], val)
+            rows = [list(r) for r in vec.rows]
+            rows[a][c] = val
+            local[name] = _PMat(rows)
+            return True
         if isinstance(tgt, ast.Attribute):
             if tgt.attr not in ("x", "y", "z", "w"):
                 raise TaichiLoweringError(f"vector has no component {tgt.attr!r}")
@@ -1572,8 +1803,10 @@ class _PixInterp:
         if (isinstance(st, (ast.Assign, ast.AugAssign)) and isinstance(getattr(st, "target", None) or st.targets[0],
                                                                        (ast.Subscript, ast.Attribute))):
             tgt = st.target if isinstance(st, ast.AugAssign) else st.targets[0]
-            if isinstance(tgt.value, ast.Name) and isinstance(local.get(tgt.value.id), _PVec):
+            if isinstance(tgt.value, ast.Name) and isinstance(local.get(tgt.value.id), (_PVec, _PMat)):
                 return self.component_assign(st, tgt, local)
+            if isinstance(tgt.value, ast.Subscript) and isinstance(self.expr(tgt.value.value, local), Field):
+                return self.element_component_assign(st, tgt, local)
         if isinstance(st, ast.Expr) and isinstance(st.value, ast.Call):
             # ti.atomic_add(field[idx], v) / ti.atomic_sub as a statement: field[idx] += v / -= v
             fn = st.value.func
@@ -1605,22 +1838,7 @@ class _PixInterp:
                 raise TaichiLoweringError("the body may only store to fields of the struct-for's shape")
             if not self._is_here(tgt.slice):
                 raise TaichiLoweringError(f"the store must write field[{', '.join(self.names)}]")
-            if self.in_loop:
-                raise TaichiLoweringError("a store inside the loop is not supported (store after it)")
-            v = self.expr(st.value, local)
-            if isinstance(v, list):
-                v = _PVec(v)
-            if target.width == 1:
-                if isinstance(v, _PVec):
-                    raise TaichiLoweringError("a field of scalars stores a scalar")
-            elif not isinstance(v, _PVec):
-                v = _PVec([v] * target.width)  # a scalar fills every component
-            elif len(v.comps) != target.width:
-                raise TaichiLoweringError(f"a field of {target.width}-vectors stores {target.width} components")
-            if target not in self.stored:
-                self.stored.append(target)
-                self.fields[id(target)] = target
-            local[_skey(target)] = v
+            self.store_here(target, self.expr(st.value, local), local)
             return True
         if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Name):
             local[st.targets[0].id] = self.expr(st.value, local)
@@ -1706,6 +1924,9 @@ def lower_pixel_program(fdef: ast.FunctionDef, funcs, env, depth=0, unroll=True)
             except TaichiLoweringError as e2:
                 if not str(e2).startswith("the program needs more than") and "does not split" not in str(e2):
                     raise
+        expanded = _expand_static_loops(fdef, funcs, env)  # so that the split can fall between iterations
+        if expanded is not None:
+            fdef = expanded
         stmts = _struct_for(fdef, funcs, env)[4]
         if len(stmts) < 2:
             raise
@@ -1846,27 +2067,21 @@ def _split_body(fdef: ast.FunctionDef, funcs, env, at, depth, unroll=True):
     loop, ip, b, local, stmts = _struct_for(fdef, funcs, env, unroll)
     part1, part2 = stmts[:at], stmts[at:]
     _run_stmts(ip, b, local, part1)  # a dry run: the kinds of the values the second part reads
-    reads2 = {nd.id for st in part2 for nd in ast.walk(st)
-              if isinstance(nd, ast.Name) and isinstance(getattr(nd, "ctx", ast.Load()), ast.Load)}
-    consts, comps = [], []  # (name, value) passed as constants; (name, width) through fields
+    reads2 = _reads_before_writes(part2)
+    passed = []  # (name, value) of the locals the second part reads
     for nm, v in local.items():
         if not (isinstance(nm, str) and nm in reads2 and nm not in ip.names):
             continue
         if v is _UNREADABLE or v is _ONE_BRANCH:
             continue
-        if isinstance(v, _PVec):
-            if all(_is_num(c) for c in v.comps):
-                consts.append((nm, [float(_f32(c)) for c in v.comps]))
-            else:
-                comps.append((nm, len(v.comps)))
-        elif _is_num(v):
-            consts.append((nm, v if isinstance(v, (int, np.integer)) and not isinstance(v, bool) else float(_f32(v))))
-        else:
-            comps.append((nm, 0))
+        if _leaves(v) is None:
+            raise TaichiLoweringError(f"{nm!r} holds a value that cannot pass between the parts of a split body")
+        passed.append((nm, v))
     shape = ip.shape if ip.shape is not None else ip.fld.shape
     env2 = dict(env)
     env2["__vdsl_ti"] = sys.modules[__name__]
-    flat = [(nm, c) for nm, w in comps for c in range(max(w, 1))]  # every component to pass, in order
+    # every per-pixel scalar to pass, in order (numbers are written into the second part)
+    flat = [(nm, path) for nm, v in passed for path, x in _leaves(v) if not _is_num(x)]
     fields, stores, slot = [], [], {}
     serial = sum(1 for nm in env2 if str(nm).startswith("__vdsl_tmp"))  # names of earlier splits stay bound
     for k in range(0, len(flat), 4):
@@ -1874,39 +2089,35 @@ def _split_body(fdef: ast.FunctionDef, funcs, env, at, depth, unroll=True):
         name = f"__vdsl_tmp{serial + k // 4}"
         env2[name] = Field(f32, shape, len(group))
         fields.append(name)
-        for q, (nm, c) in enumerate(group):
-            slot[(nm, c)] = (name, q, len(group))
+        for q, key in enumerate(group):
+            slot[key] = (name, q, len(group))
     here = ast.Name(id=ip.iname, ctx=ast.Load()) if len(ip.names) == 1 else \
         ast.Tuple(elts=[ast.Name(id=n, ctx=ast.Load()) for n in ip.names], ctx=ast.Load())
 
-    def comp_src(nm, c):  # the value component nm[c] in the first part
-        base = ast.Name(id=nm, ctx=ast.Load())
-        return base if dict(comps)[nm] == 0 else ast.Subscript(value=base, slice=ast.Constant(value=c), ctx=ast.Load())
-
     for name in fields:
-        members = sorted((q, nm, c) for (nm, c), (fn, q, _) in slot.items() if fn == name)
-        vals = [comp_src(nm, c) for _, nm, c in members]
+        members = sorted((q, key) for key, (fn, q, _) in slot.items() if fn == name)
+        vals = [_access(nm, path) for _, (nm, path) in members]
         value = vals[0] if len(vals) == 1 else ast.Call(func=ast.Attribute(value=ast.Name(id="__vdsl_ti", ctx=ast.Load()), attr="Vector"),
                                                          args=[ast.List(elts=vals, ctx=ast.Load())], keywords=[])
         stores.append(ast.Assign(targets=[ast.Subscript(value=ast.Name(id=name, ctx=ast.Load()), slice=here, ctx=ast.Store())],
                                  value=value, lineno=0))
-    prelude = []
-    for nm, v in consts:
-        val = ast.Call(func=ast.Attribute(value=ast.Name(id="__vdsl_ti", ctx=ast.Load()), attr="Vector"),
-                       args=[ast.List(elts=[ast.Constant(value=c) for c in v], ctx=ast.Load())], keywords=[]) \
-            if isinstance(v, list) else ast.Constant(value=v)
-        prelude.append(ast.Assign(targets=[ast.Name(id=nm, ctx=ast.Store())], value=val, lineno=0))
 
-    def read(nm, c):
-        fn, q, width = slot[(nm, c)]
+    def read(nm, path):
+        fn, q, width = slot[(nm, path)]
         whole = ast.Subscript(value=ast.Name(id=fn, ctx=ast.Load()), slice=here, ctx=ast.Load())
         return whole if width == 1 else ast.Subscript(value=whole, slice=ast.Constant(value=q), ctx=ast.Load())
 
-    for nm, w in comps:
-        val = read(nm, 0) if w == 0 else ast.Call(
-            func=ast.Attribute(value=ast.Name(id="__vdsl_ti", ctx=ast.Load()), attr="Vector"),
-            args=[ast.List(elts=[read(nm, c) for c in range(w)], ctx=ast.Load())], keywords=[])
-        prelude.append(ast.Assign(targets=[ast.Name(id=nm, ctx=ast.Store())], value=val, lineno=0))
+    prelude = []
+    for nm, v in passed:
+        leaf = dict(_leaves(v))
+
+        def leaf_ast(path, nm=nm, leaf=leaf):
+            x = leaf[path]
+            if _is_num(x):
+                return ast.Constant(value=int(x) if isinstance(x, (int, np.integer)) and not isinstance(x, bool)
+                                    else float(_f32(x)))
+            return read(nm, path)
+        prelude.append(ast.Assign(targets=[ast.Name(id=nm, ctx=ast.Store())], value=_rebuild(v, leaf_ast), lineno=0))
 
     def kernel_of(body):
         f = ast.For(target=loop.target, iter=loop.iter, body=body, orelse=[], lineno=getattr(loop, "lineno", 0))
@@ -1919,6 +2130,112 @@ def _split_body(fdef: ast.FunctionDef, funcs, env, at, depth, unroll=True):
     first = lower_pixel_program(kernel_of(part1 + stores), funcs, env2, depth + 1, unroll)
     second = lower_pixel_program(kernel_of(prelude + part2), funcs, env2, depth + 1, unroll)
     return Lowered("sequence", second.field, parts=[first, second])
+
+
+def _reads_before_writes(stmts):
+    """The names a statement list reads before it assigns them (a statement's own reads count
+    before its assignments; a compound statement's reads all count)."""
+    assigned, reads = set(), set()
+    for st in stmts:
+        for nd in ast.walk(st):
+            if isinstance(nd, ast.Name) and isinstance(getattr(nd, "ctx", ast.Load()), ast.Load) and nd.id not in assigned:
+                reads.add(nd.id)
+        if isinstance(st, ast.AugAssign) and isinstance(st.target, ast.Name):
+            reads.add(st.target.id) if st.target.id not in assigned else None
+        if isinstance(st, (ast.Assign, ast.AugAssign)):
+            for t in (st.targets if isinstance(st, ast.Assign) else [st.target]):
+                for e in (t.elts if isinstance(t, ast.Tuple) else [t]):
+                    if isinstance(e, ast.Name):
+                        assigned.add(e.id)
+    return reads
+
+
+def _leaves(v, path=()):
+    """The scalar leaves of a value one part of a split body passes to the next: [(path, value)],
+    a path step being an index (a list or vector component) or a pair (a matrix element); None
+    for a value not made of scalars, vectors, matrices and lists of them."""
+    if isinstance(v, _PMat):
+        n, m = v.shape
+        return [(path + ((a, c),), v.rows[a][c]) for a in range(n) for c in range(m)]
+    if isinstance(v, _PVec):
+        return [(path + (k,), c) for k, c in enumerate(v.comps)]
+    if isinstance(v, list):
+        out = []
+        for k, e in enumerate(v):
+            sub = _leaves(e, path + (k,))
+            if sub is None:
+                return None
+            out += sub
+        return out
+    from . import pixprog
+    if _is_num(v) or isinstance(v, pixprog.Node):
+        return [(path, v)]
+    return None
+
+
+def _access(name, path):
+    """The expression name[...] along a leaf path (a matrix element as M[a, b])."""
+    node = ast.Name(id=name, ctx=ast.Load())
+    for step in path:
+        idx = ast.Tuple(elts=[ast.Constant(value=step[0]), ast.Constant(value=step[1])], ctx=ast.Load()) \
+            if isinstance(step, tuple) else ast.Constant(value=step)
+        node = ast.Subscript(value=node, slice=idx, ctx=ast.Load())
+    return node
+
+
+def _rebuild(v, leaf_ast, path=()):
+    """An expression of v's structure (ti.Matrix, ti.Vector, lists) with leaf_ast(path) at each
+    scalar."""
+    ti_ = ast.Name(id="__vdsl_ti", ctx=ast.Load())
+    if isinstance(v, _PMat):
+        n, m = v.shape
+        rows = [ast.List(elts=[leaf_ast(path + ((a, c),)) for c in range(m)], ctx=ast.Load()) for a in range(n)]
+        return ast.Call(func=ast.Attribute(value=ti_, attr="Matrix"), args=[ast.List(elts=rows, ctx=ast.Load())], keywords=[])
+    if isinstance(v, _PVec):
+        return ast.Call(func=ast.Attribute(value=ti_, attr="Vector"),
+                        args=[ast.List(elts=[leaf_ast(path + (k,)) for k in range(len(v.comps))], ctx=ast.Load())],
+                        keywords=[])
+    if isinstance(v, list):
+        return ast.List(elts=[_rebuild(e, leaf_ast, path + (k,)) for k, e in enumerate(v)], ctx=ast.Load())
+    return leaf_ast(path)
+
+
+def _expand_static_loops(fdef: ast.FunctionDef, funcs, env):
+    """fdef with each top-level static loop of its struct-for body (ti.static, or a short range
+    loop that is unrolled anyway) over constant values written out iteration by iteration (the
+    loop's names bound by assignments, then a copy of its body), so that a body too large for one
+    program can be split between iterations; None if there is no such loop."""
+    loop, ip, b, local, stmts = _struct_for(fdef, funcs, env)
+    out, changed = [], False
+    for st in stmts:
+        vals = None
+        if isinstance(st, ast.For) and not st.orelse:
+            try:
+                vals = ip.static_values(st, local)
+            except TaichiLoweringError:
+                vals = None
+        names = [st.target.id] if isinstance(getattr(st, "target", None), ast.Name) else \
+            [e.id for e in st.target.elts] if isinstance(getattr(st, "target", None), ast.Tuple) and \
+            all(isinstance(e, ast.Name) for e in st.target.elts) else None
+
+        def const(x):
+            return isinstance(x, (int, float, np.integer, np.floating)) and not isinstance(x, bool)
+        ok = vals is not None and names is not None and all(
+            (len(names) == 1 and const(v)) or (isinstance(v, tuple) and len(v) == len(names) and all(map(const, v)))
+            for v in vals)
+        if not ok:
+            out.append(st)
+            continue
+        for v in vals:
+            for nm, x in zip(names, v if isinstance(v, tuple) else (v,)):
+                out.append(ast.Assign(targets=[ast.Name(id=nm, ctx=ast.Store())], lineno=0,
+                                      value=ast.Constant(value=int(x) if isinstance(x, (int, np.integer)) else float(x))))
+            out.extend(copy.deepcopy(st.body))
+        changed = True
+    if not changed:
+        return None
+    f = ast.For(target=loop.target, iter=loop.iter, body=out, orelse=[], lineno=getattr(loop, "lineno", 0))
+    return ast.FunctionDef(name=fdef.name, args=fdef.args, body=[f], decorator_list=[], returns=None, type_comment=None)
 
 
 _SCATTERS = object()  # the target of the program that runs a body's scatter-adds on their own
