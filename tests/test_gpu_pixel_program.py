@@ -391,6 +391,30 @@ def test_life_example_against_numpy(dev, q):
     assert np.array_equal(img, st) and 0 < st.sum() < st.size
 
 
+_GRAPH_F = tc.field(dtype=float, shape=(64, 48))
+
+
+@tc.kernel
+def _graph_step(k: float):
+    for i, j in _GRAPH_F:
+        _GRAPH_F[i, j] = _GRAPH_F[i, j] * 0.5 + i * k - j
+
+
+def test_repeated_kernel_calls_replay_a_graph(dev, q):
+    """From its second call with the same arguments a kernel's launches are recorded as one
+    hipGraph and replayed: every call still advances the field once, bit for bit as the oracle."""
+    tc.init(arch=tc.gpu)
+    prog = _graph_step.lower(0.25).program
+    want = np.zeros((64, 48), np.float32)
+    for n in range(1, 7):
+        _graph_step(0.25)
+        want = oracle.pixel_program(prog, 64, 48, [want])
+        assert np.array_equal(_GRAPH_F.to_numpy(), want), n
+    assert _graph_step.lower(0.25).graph  # recorded after the second call, replayed since
+    _graph_step(0.5)  # other arguments: a lowering of their own, eager at first
+    assert not getattr(_graph_step.lower(0.5), "graph", None)
+
+
 def test_heat_example_bit_exact(dev, q):
     path = os.path.join(EX, "heat.py")
     res, img = run_program(path, 2)

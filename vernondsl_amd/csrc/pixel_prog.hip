@@ -8,8 +8,11 @@
 // straight-line code around the same check-then-update loop.
 
 #include <algorithm>
+#include <cstddef>
 #include <cstdlib>
+#include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "common.h"
@@ -97,9 +100,8 @@ std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p);
 // at most kPrivMax elements in all (32 KiB of a block's LDS).  Adds at constant indices are
 // summed in registers instead.
 constexpr int kPrivMax = 8192;
-int privatized(const vdsl_pixel_program& p, int k, int ni, int nj) {
+int privatized(const vdsl_pixel_program& p, const std::vector<char>& flags, int k, int ni, int nj) {
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
-  const std::vector<char> flags = row_uniform_gathers(p);
   int64_t used = 0, own = 0;
   for (int t = 0; t <= k; ++t) {
     bool per_pixel = false;
@@ -122,18 +124,16 @@ int privatized(const vdsl_pixel_program& p, int k, int ni, int nj) {
 // (~13 ns each): 64 rows (the sum of an 8192^2 field: 834 / 420 / 214 us with 4 / 8 / 16 rows);
 // so does one whose other adds go to per-block copies in LDS (their flush is per block too).
 // VDSL_PIX_ROWS=r (1..64) overrides the choice, for tuning sweeps.
-int rows_per_block(const vdsl_pixel_program& p, int ni, int nj) {
+int rows_per_block(const vdsl_pixel_program& p, const std::vector<char>& flags, const int32_t* priv) {
   if (const char* e = std::getenv("VDSL_PIX_ROWS")) {  // tuning sweeps: rows per block, 1..64
     const int r = std::atoi(e);
     if (r >= 1 && r <= 64) return r;
   }
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   bool gathers = false, reduction = p.out_kind == VDSL_PIX_OUT_NONE;
-  const std::vector<char> flags = row_uniform_gathers(p);
   for (int pc = 0; pc < total; ++pc) {
     gathers |= p.code[pc].op == VDSL_PIX_LOAD_AT;
-    if (p.code[pc].op == VDSL_PIX_ATOMIC_ADD && !(flags[pc] & 4) && !privatized(p, p.code[pc].a, ni, nj))
-      reduction = false;
+    if (p.code[pc].op == VDSL_PIX_ATOMIC_ADD && !(flags[pc] & 4) && !priv[p.code[pc].a]) reduction = false;
   }
   return reduction ? 64 : gathers ? 8 : 4;
 }
@@ -141,10 +141,10 @@ int rows_per_block(const vdsl_pixel_program& p, int ni, int nj) {
 // Blocks of rows_per_block rows x 256 pixels for programs whose pixels all do the same work (no
 // escape loop), while the row count fits the grid's y extent; 16x16 patches otherwise.  0 for
 // the patches.
-int row_mapping(const vdsl_pixel_program& p, int ni, int nj) {
+int row_mapping(const vdsl_pixel_program& p, const std::vector<char>& flags, const int32_t* priv, int ni) {
   // never more rows per block than the grid has: a 1-D field is a grid of one row, whose blocks
   // would otherwise run their loops for rows that do not exist
-  const int rows = std::min(rows_per_block(p, ni, nj), std::max(ni, 1));
+  const int rows = std::min(rows_per_block(p, flags, priv), std::max(ni, 1));
   return !(p.loop && p.test != VDSL_PIX_TEST_NONE) && (ni + rows - 1) / rows <= 65535 ? rows : 0;
 }
 
@@ -231,9 +231,30 @@ std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
   return flag;
 }
 
+// What the launch of a program over an [ni][nj] grid is worked out to: the dataflow flags of its
+// gathers and scatter-adds, the LDS copies of its small scatter targets, the rows per block.
+struct Plan {
+  std::vector<char> flags;
+  int32_t priv[VDSL_PIX_MAX_INPUTS] = {}, priv_off[VDSL_PIX_MAX_INPUTS] = {};
+  int32_t priv_total = 0;
+  int rows = 0;
+};
+
+Plan make_plan(const vdsl_pixel_program& p, int n_inputs, int ni, int nj) {
+  Plan pl;
+  pl.flags = row_uniform_gathers(p);
+  for (int k = 0; k < n_inputs; ++k) {
+    pl.priv[k] = privatized(p, pl.flags, k, ni, nj);
+    pl.priv_off[k] = pl.priv_total;
+    pl.priv_total += pl.priv[k];
+  }
+  pl.rows = row_mapping(p, pl.flags, pl.priv, ni);
+  return pl;
+}
+
 // The program's table as C++ source (opcodes and registers; immediates stay kernel arguments).
 // It names the kernel completely, so it is also the cache key.
-std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni, int nj) {
+std::string program_source(const vdsl_pixel_program& p, const Plan& pl, int n_inputs, int ni, int nj) {
   std::string s = "#include \"pixprog_kern.h\"\nnamespace vdsl {\nstruct PixJit {\n";
   auto c = [&](const char* name, int v) { s += std::string("  static constexpr int ") + name + " = " + std::to_string(v) + ";\n"; };
   c("n_pre", p.n_pre);
@@ -246,7 +267,7 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni, in
   c("test_b", p.test_b);
   c("out_kind", p.out_kind);
   c("out_width", p.out_width);
-  c("rows", row_mapping(p, ni, nj));
+  c("rows", pl.rows);
   // 32-bit element offsets when every field's byte offsets stay below 2^32
   int maxw = p.out_width;
   for (int k = 0; k < n_inputs; ++k) maxw = p.in_widths[k] > maxw ? p.in_widths[k] : maxw;
@@ -263,19 +284,12 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni, in
   list("in_widths", p.in_widths, n_inputs, 1, VDSL_PIX_MAX_INPUTS);
   list("in_dtypes", p.in_dtypes, n_inputs, VDSL_F32, VDSL_PIX_MAX_INPUTS);
   // per-block LDS copies of small scatter targets: sizes and offsets in one array
-  int32_t priv[VDSL_PIX_MAX_INPUTS] = {}, priv_off[VDSL_PIX_MAX_INPUTS] = {};
-  int32_t priv_total = 0;
-  for (int k = 0; k < n_inputs; ++k) {
-    priv[k] = privatized(p, k, ni, nj);
-    priv_off[k] = priv_total;
-    priv_total += priv[k];
-  }
-  list("priv", priv, n_inputs, 0, VDSL_PIX_MAX_INPUTS);
-  list("priv_off", priv_off, n_inputs, 0, VDSL_PIX_MAX_INPUTS);
-  c("priv_total", priv_total);
+  list("priv", pl.priv, n_inputs, 0, VDSL_PIX_MAX_INPUTS);
+  list("priv_off", pl.priv_off, n_inputs, 0, VDSL_PIX_MAX_INPUTS);
+  c("priv_total", pl.priv_total);
   // ext[0] / ext[1] of a gather or scatter-add: 1 when its row / column operand is wave-uniform in
   // the row mapping; ext[2] of a scatter-add: 1 when both are constants
-  const std::vector<char> ru = row_uniform_gathers(p);
+  const std::vector<char>& ru = pl.flags;
   s += "  static constexpr vdsl_map_instr code[VDSL_PIX_MAX_INSTR] = {\n";
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   for (int pc = 0; pc < total; ++pc) {
@@ -288,6 +302,49 @@ std::string program_source(const vdsl_pixel_program& p, int n_inputs, int ni, in
   s += "extern \"C\" __global__ __launch_bounds__(256) void vdsl_pix_jit(vdsl::PixRt rt, vdsl::PixIn in, void* out, int ni, "
        "int nj) {\n  vdsl::pixel_body<vdsl::PixJit>(rt, in, out, ni, nj);\n}\n";
   return s;
+}
+
+// Launches already worked out, keyed by the program's bytes without its immediates and max_iter
+// (everything its source depends on) with the device and the grid: the source, its dataflow
+// analysis and the cache lookup by source text cost more host time than the kernels of small
+// programs (MPM88's 12 programs per substep: 57 us each from Python before).  Entries point into
+// the compiled-program cache, whose entries stay for the process.
+struct Launch {
+  const JitKernels* k = nullptr;
+  int rows = 0;
+};
+std::mutex g_launch_mu;
+std::unordered_map<std::string, Launch> g_launches;
+constexpr size_t kMaxLaunches = 4096;
+
+std::string launch_key(const vdsl_pixel_program& p, int ordinal, int n_inputs, int ni, int nj) {
+  const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
+  vdsl_pixel_program head = p;  // the fields before the code, without max_iter
+  head.max_iter = 0;
+  const int32_t ext[4] = {ordinal, n_inputs, ni, nj};
+  std::string key(reinterpret_cast<const char*>(ext), sizeof ext);
+  key.append(reinterpret_cast<const char*>(&head), offsetof(vdsl_pixel_program, code));
+  for (int pc = 0; pc < total; ++pc) {
+    vdsl_map_instr s = p.code[pc];
+    s.imm = 0.0f;
+    key.append(reinterpret_cast<const char*>(&s), sizeof s);
+  }
+  if (const char* e = std::getenv("VDSL_PIX_ROWS")) key.append(e);  // a tuning override changes the plan
+  return key;
+}
+
+bool find_launch(const std::string& key, Launch& out) {
+  std::lock_guard<std::mutex> lk(g_launch_mu);
+  const auto it = g_launches.find(key);
+  if (it == g_launches.end()) return false;
+  out = it->second;
+  return true;
+}
+
+void keep_launch(const std::string& key, const Launch& ln) {
+  std::lock_guard<std::mutex> lk(g_launch_mu);
+  if (g_launches.size() >= kMaxLaunches) g_launches.clear();  // a bound; entries are cheap to work out again
+  g_launches[key] = ln;
 }
 
 }  // namespace
@@ -325,16 +382,26 @@ extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const
   PixRt rt{};
   for (int pc = 0; pc < total; ++pc) rt.imm[pc] = p.code[pc].imm;
   rt.max_iter = p.max_iter;
-  const std::string src = program_source(p, n_inputs, ni, nj);
-  const char* const entries[] = {"vdsl_pix_jit"};
-  const JitKernels* k = nullptr;
-  const int st = jit_kernels(q->dev->ordinal, src, entries, 1, q->capturing, g_pix_jit, "pixel program", &k);
-  if (st == VDSL_ERR_UNSUPPORTED && q->capturing)
-    return fail(VDSL_ERR_CAPTURE, "pixel program: not compiled yet; run it once before recording a graph");
-  VDSL_TRY(st);
+  // The kernel and its rows per block, from the launches seen before when this program (but for
+  // its immediates and max_iter, which are arguments) ran on a grid of these extents on this
+  // device; else from its source (compiled on first use).
+  const std::string key = launch_key(p, q->dev->ordinal, n_inputs, ni, nj);
+  Launch ln;
+  if (!find_launch(key, ln)) {
+    const Plan pl = make_plan(p, n_inputs, ni, nj);
+    const std::string src = program_source(p, pl, n_inputs, ni, nj);
+    const char* const entries[] = {"vdsl_pix_jit"};
+    const int st = jit_kernels(q->dev->ordinal, src, entries, 1, q->capturing, g_pix_jit, "pixel program", &ln.k);
+    if (st == VDSL_ERR_UNSUPPORTED && q->capturing)
+      return fail(VDSL_ERR_CAPTURE, "pixel program: not compiled yet; run it once before recording a graph");
+    VDSL_TRY(st);
+    ln.rows = pl.rows;
+    keep_launch(key, ln);
+  }
+  const JitKernels* k = ln.k;
   void* o = p.out_kind == VDSL_PIX_OUT_NONE ? nullptr : out->ptr;
   void* args[] = {&rt, &in, &o, &ni, &nj};
-  const int rows = row_mapping(p, ni, nj);
+  const int rows = ln.rows;
   const unsigned gx = rows ? static_cast<unsigned>((nj + 255) / 256) : static_cast<unsigned>((nj + 15) / 16);
   const unsigned gy = rows ? static_cast<unsigned>((ni + rows - 1) / rows) : static_cast<unsigned>((ni + 15) / 16);
   return check_hip(hipModuleLaunchKernel(k->fn[0], gx, gy, 1, 256, 1, 1, 0, q->stream, args, nullptr),

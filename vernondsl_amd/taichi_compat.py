@@ -56,6 +56,7 @@ import collections
 import copy
 import inspect
 import itertools
+import os
 import math as _pymath
 import sys
 import textwrap
@@ -124,6 +125,7 @@ class Field:
             raise TaichiLoweringError("vector fields hold 1 to 4 f32 components")
         self._tensor = None
         self._snap = None
+        self._grid = None
 
     def snapshot(self):
         """A hidden field of this one's type and shape, made once: the copy of its values taken
@@ -146,11 +148,15 @@ class Field:
         """The tensor as a per-pixel program grid: a 1-D field of n elements is one row, [1][n]; a
         3-D field [A][B][C] is [A B][C] (the same bytes); a 0-D field is [1][1]."""
         t = self.tensor()
-        if len(self.shape) <= 1:
-            return t.view((1,) + t.shape)
-        if len(self.shape) == 3:
-            return t.view((self.shape[0] * self.shape[1],) + t.shape[2:])
-        return t
+        if self._grid is None or self._grid[0] is not t:
+            if len(self.shape) <= 1:
+                g = t.view((1,) + t.shape)
+            elif len(self.shape) == 3:
+                g = t.view((self.shape[0] * self.shape[1],) + t.shape[2:])
+            else:
+                g = t
+            self._grid = (t, g)  # made once: kernels launch many times
+        return self._grid[1]
 
     def to_numpy(self):
         _, q = _device()
@@ -300,10 +306,33 @@ class Kernel:
                 self._cache.popitem(last=False)
         return low
 
+    # Calls of one lowering (one argument tuple) made eagerly before its launches are recorded as
+    # one hipGraph, replayed by the calls after (VDSL_TI_GRAPHS=0: always eager).  A kernel called
+    # every frame or substep then costs one graph launch instead of one launch per program (the
+    # mpm88 example's substep: 12 programs, 32 us of device time, ~325 us launched one by one).
+    GRAPH_AFTER = 2
+
     def __call__(self, *args):
         low = self.lower(*args)
-        from . import kernels
         _, q = _device()
+        graph = getattr(low, "graph", None)
+        if graph:
+            graph.launch(q)
+            return
+        self._launch(low, q)
+        low.calls = getattr(low, "calls", 0) + 1
+        if graph is None and low.calls >= self.GRAPH_AFTER and os.environ.get("VDSL_TI_GRAPHS", "1") != "0":
+            # record (not run) the same launches; every program is compiled by now
+            try:
+                with q.capture() as rec:
+                    self._launch(low, q)
+                low.graph = rec.graph
+            except Exception:  # an op that cannot be recorded: this lowering stays eager
+                low.graph = False
+
+    @staticmethod
+    def _launch(low, q):
+        from . import kernels
         for op in low.ops():
             if op.kind == "copy":
                 op.field.tensor().buffer.copy_from(q, op.inputs[0].tensor().buffer)
