@@ -43,7 +43,10 @@ added into as `s[None]`.  `F[idx] += v` / `-= v` at an index other than the loop
 `ti.atomic_add(F[idx], v)` as a statement) is Taichi's atomic add: a scatter-add of the program,
 dropped where an index falls outside F, with idx a tuple or a vector expression such as
 `base + offset` (`.cast(int)` / `int()` truncate); a field added into is neither read nor stored
-by the same struct-for, and adds inside an if happen only where the branch runs.  What neither path lowers raises
+by the same struct-for, and adds inside an if happen only where the branch runs.  `ti.Matrix`
+values (`@`, `outer_product`, `trace`, `determinant`, `transpose`) and 2 x 2 matrix fields lower
+to their scalar operations.  A lowering called again with the same arguments is replayed as one
+recorded hipGraph.  What neither path lowers raises
 TaichiLoweringError naming what did not match; there is no CPU fallback.  Accepted complex squares are the ones equal bit for bit to (zr*zr - zi*zi, (zi*zr)*2):
 `z[0]**2 - z[1]**2`, `z[0]*z[0] - z[1]*z[1]`, and `z[1]*z[0]*2` / `z[0]*z[1]*2` / `2*(z[0]*z[1])` /
 `z[0]*z[1] + z[0]*z[1]` for the imaginary part (`(2*z[0])*z[1]` is refused: it rounds differently
