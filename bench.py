@@ -902,7 +902,9 @@ def _summary_row(entry):
     label = str(cid) + ("/" + "/".join(names) if names else "")
     rf = entry.get("roofline") or {}
     ms = entry.get("ms_per_launch", entry.get("ms_per_step"))
-    return [label, _round(entry.get("value")), entry.get("unit"), rf.get("frac"), _round(ms)]
+    frac = rf.get("frac")
+    return [label, _round(entry.get("value")), entry.get("unit"), round(frac, 4) if isinstance(frac, float) else frac,
+            _round(ms)]
 
 
 def main():
