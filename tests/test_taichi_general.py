@@ -1121,3 +1121,32 @@ def test_fields_of_other_shapes_are_gathered_in_their_own_extents():
     for k in range(5):
         ref = ref + v[:, :, k] * f32(k + 1.0)
     assert np.array_equal(got, ref + v[:, :, 4])
+
+
+GROUPED = """import taichi as ti
+a = ti.field(dtype=float, shape=(12, 9))
+b = ti.Vector.field(2, dtype=float, shape=(12, 9))
+c = ti.field(dtype=float, shape=20)
+@ti.kernel
+def k():
+    for I in ti.grouped(a):
+        a[I] = I[0] * 2.0 + I[1] + b[I].x
+        b[I] = ti.Vector([I.x, a[I]])
+    for I in ti.grouped(c):
+        c[I] = I[0] * 0.5
+"""
+
+
+def test_grouped_struct_fors():
+    """`for I in ti.grouped(F)`: I is the index vector, F[I] this pixel's element (a load at the
+    pixel, not a gather), for 2-D and 1-D fields."""
+    low, names = lower_named(GROUPED, "k", {})
+    assert [names[id(o.field)] for o in low.ops()] == ["a", "b", "c"]
+    assert all(ins.op != pp.OP["load_at"] for o in low.ops() for ins in o.program.code[:o.program.n_post])
+    b0 = np.random.default_rng(1).random((12, 9, 2)).astype(np.float32)
+    arr = {"a": np.zeros((12, 9), np.float32), "b": b0.copy(), "c": np.zeros(20, np.float32)}
+    run_ops(low, names, arr)
+    i, j = grid(12, 9)
+    a = (i * f32(2.0) + j) + b0[:, :, 0]
+    assert np.array_equal(arr["a"], a) and np.array_equal(arr["b"][:, :, 1], a) and np.array_equal(arr["b"][:, :, 0], i)
+    assert np.array_equal(arr["c"], np.arange(20, dtype=np.float32) * f32(0.5))

@@ -45,7 +45,7 @@ dropped where an index falls outside F, with idx a tuple or a vector expression 
 `base + offset` (`.cast(int)` / `int()` truncate); a field added into is neither read nor stored
 by the same struct-for, and adds inside an if happen only where the branch runs.  `ti.Matrix`
 values (`@`, `outer_product`, `trace`, `determinant`, `transpose`) and 2 x 2 matrix fields lower
-to their scalar operations.  A lowering called again with the same arguments is replayed as one
+to their scalar operations; `for I in ti.grouped(F)` binds I to the index vector.  A lowering called again with the same arguments is replayed as one
 recorded hipGraph.  What neither path lowers raises
 TaichiLoweringError naming what did not match; there is no CPU fallback.  Accepted complex squares are the ones equal bit for bit to (zr*zr - zi*zi, (zi*zr)*2):
 `z[0]**2 - z[1]**2`, `z[0]*z[0] - z[1]*z[1]`, and `z[1]*z[0]*2` / `z[0]*z[1]*2` / `2*(z[0]*z[1])` /
@@ -1990,7 +1990,7 @@ def _struct_for(fdef: ast.FunctionDef, funcs, env, unroll=True):
     body = [s for s in fdef.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant))]
     if len(body) != 1 or not isinstance(body[0], ast.For):
         raise TaichiLoweringError("the kernel body must be one struct-for `for i, j in field:` (or `for i in field:`)")
-    loop = body[0]
+    loop = _ungroup(body[0], env, funcs)
     kname = None
     if isinstance(loop.target, ast.Tuple) and len(loop.target.elts) == 2:
         iname, jname = (e.id for e in loop.target.elts)
@@ -2038,6 +2038,38 @@ def _struct_for(fdef: ast.FunctionDef, funcs, env, unroll=True):
             ip.ibound[id(local[nm])] = max(int(ext) - 1, 0)
     stmts = [s for s in loop.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant)) and not isinstance(s, ast.Pass)]
     return loop, ip, b, local, stmts
+
+
+def _ungroup(loop, env, funcs):
+    """`for I in ti.grouped(F): ...` as `for i0, i1 in F: I = ti.Vector([i0, i1]); ...`, with
+    F[I] written F[i0, i1] (so it is this pixel's element); other loops unchanged."""
+    it = loop.iter
+    if not (isinstance(it, ast.Call) and len(it.args) == 1 and isinstance(loop.target, ast.Name) and (
+            (isinstance(it.func, ast.Attribute) and it.func.attr == "grouped") or
+            (isinstance(it.func, ast.Name) and it.func.id == "grouped"))):
+        return loop
+    fld = _PixInterp(env, funcs, None, None, "_", None).expr(it.args[0], {})
+    shape = fld.shape if isinstance(fld, Field) else tuple(fld) if isinstance(fld, (list, tuple)) else None
+    if not shape or not 1 <= len(shape) <= 3:
+        raise TaichiLoweringError("ti.grouped takes a 1-D, 2-D or 3-D field or ti.ndrange")
+    grp = loop.target.id
+    names = [f"__vdsl_{grp}{k}" for k in range(len(shape))]
+
+    class Sub(ast.NodeTransformer):
+        def visit_Subscript(self, nd):
+            self.generic_visit(nd)
+            if isinstance(nd.slice, ast.Name) and nd.slice.id == grp:
+                nd.slice = ast.Tuple(elts=[ast.Name(id=n, ctx=ast.Load()) for n in names], ctx=ast.Load()) \
+                    if len(names) > 1 else ast.Name(id=names[0], ctx=ast.Load())
+            return nd
+    body = [Sub().visit(copy.deepcopy(st)) for st in loop.body]
+    bind = ast.Assign(targets=[ast.Name(id=grp, ctx=ast.Store())], lineno=0, value=ast.Call(
+        func=ast.Attribute(value=ast.Name(id="__vdsl_ti", ctx=ast.Load()), attr="Vector"),
+        args=[ast.List(elts=[ast.Name(id=n, ctx=ast.Load()) for n in names], ctx=ast.Load())], keywords=[]))
+    env.setdefault("__vdsl_ti", sys.modules[__name__])
+    target = ast.Tuple(elts=[ast.Name(id=n, ctx=ast.Store()) for n in names], ctx=ast.Store()) if len(names) > 1 \
+        else ast.Name(id=names[0], ctx=ast.Store())
+    return ast.For(target=target, iter=it.args[0], body=[bind] + body, orelse=[], lineno=getattr(loop, "lineno", 0))
 
 
 def _grid_of(shape):
