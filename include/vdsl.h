@@ -41,7 +41,8 @@ extern "C" {
  * vdsl_op_relu_bwd, vdsl_op_add (struct layouts unchanged since 3); 5: vdsl_pixel_program.in_rows
  * and in_cols (inputs of another shape than the grid); 6: VDSL_PIX_ATOMIC_ADD,
  * VDSL_PIX_OUT_NONE (scatter-adds) and VDSL_PIX_TRUNC (struct layouts unchanged since 5); 7:
- * VDSL_PIX_MAX_INSTR 256 and VDSL_PIX_MAX_INPUTS 8 (vdsl_pixel_program's arrays grow). */
+ * VDSL_PIX_MAX_INSTR 256 and VDSL_PIX_MAX_INPUTS 8 (vdsl_pixel_program's arrays grow),
+ * VDSL_PIX_ATOMIC_MAX / MIN. */
 #define VDSL_ABI_VERSION 7
 
 typedef enum vdsl_status {
@@ -350,7 +351,13 @@ typedef enum vdsl_pix_opcode {
    * the same on every lane or constant, and in a per-block copy of a target of at most 8192
    * elements), so the sum's rounding may differ between runs (as Taichi's atomic adds). */
   VDSL_PIX_ATOMIC_ADD = 44,
-  VDSL_PIX_TRUNC = 45   /* truncf(r[a]): toward zero (Taichi's float -> int conversion, kept in f32) */
+  VDSL_PIX_TRUNC = 45,  /* truncf(r[a]): toward zero (Taichi's float -> int conversion, kept in f32) */
+  /* Taichi's atomic_max / atomic_min: as VDSL_PIX_ATOMIC_ADD (operands, extents, drops,
+   * refusals), the element becoming max / min(element, r[dst]): int32 exactly (the value
+   * converted as VDSL_PIX_OUT_I32 stores it); f32 as fmaxf / fminf (a NaN operand is ignored), in
+   * any order the same value except that the sign of a zero result may depend on the order. */
+  VDSL_PIX_ATOMIC_MAX = 46,
+  VDSL_PIX_ATOMIC_MIN = 47
 } vdsl_pix_opcode;
 
 typedef enum vdsl_pix_test {

@@ -251,9 +251,10 @@ static int pix_test(int test, float a, float b) {
   }
 }
 
-/* VDSL_PIX_ATOMIC_ADD: component imm of input a at [(int)r[b]][(int)r[c]] += r[dst] when
- * 0 <= r[b] < rows and 0 <= r[c] < cols of input a, else nothing.  f32: one f32 addition; int32:
- * the value converted as an int32 store converts it, added modulo 2^32. */
+/* VDSL_PIX_ATOMIC_ADD / MAX / MIN: component imm of input a at [(int)r[b]][(int)r[c]] += r[dst]
+ * (or becomes the max / min of it and r[dst]) when 0 <= r[b] < rows and 0 <= r[c] < cols of
+ * input a, else nothing.  f32: one f32 addition, fmaxf, fminf; int32: the value converted as an
+ * int32 store converts it, added modulo 2^32, or compared. */
 static void pix_scatter_add(const vdsl_pixel_program* p, const vdsl_map_instr* s, const float* reg, const void* const* inputs,
                             int64_t ni, int64_t nj) {
   const int64_t rn = p->in_rows[s->a] ? p->in_rows[s->a] : ni, cn = p->in_cols[s->a] ? p->in_cols[s->a] : nj;
@@ -263,19 +264,28 @@ static void pix_scatter_add(const vdsl_pixel_program* p, const vdsl_map_instr* s
   if (xi >= rn || yi >= cn) return;
   const int64_t e = xi * cn + yi;
   if (p->in_dtypes[s->a] == VDSL_I32) {
-    uint32_t* t = (uint32_t*)inputs[s->a] + e;
-    *t = *t + (uint32_t)pix_to_i32(reg[s->dst]);
+    int32_t* t = (int32_t*)inputs[s->a] + e;
+    const int32_t v = pix_to_i32(reg[s->dst]);
+    if (s->op == VDSL_PIX_ATOMIC_ADD) *t = (int32_t)((uint32_t)*t + (uint32_t)v);
+    else if (s->op == VDSL_PIX_ATOMIC_MAX) *t = v > *t ? v : *t;
+    else *t = v < *t ? v : *t;
   } else {
     float* t = (float*)inputs[s->a] + e * p->in_widths[s->a] + (int)s->imm;
-    *t = *t + reg[s->dst];
+    if (s->op == VDSL_PIX_ATOMIC_ADD) *t = *t + reg[s->dst];
+    else if (s->op == VDSL_PIX_ATOMIC_MAX) *t = fmaxf(*t, reg[s->dst]);
+    else *t = fminf(*t, reg[s->dst]);
   }
+}
+
+static int pix_scatter_op(int op) {
+  return op == VDSL_PIX_ATOMIC_ADD || op == VDSL_PIX_ATOMIC_MAX || op == VDSL_PIX_ATOMIC_MIN;
 }
 
 /* One instruction: its register, or a scatter-add's effect. */
 static void pix_exec(const vdsl_pixel_program* p, int pc, float* reg, const void* const* inputs, int64_t o, int64_t i,
                      int64_t j, int count, int64_t ni, int64_t nj) {
   const vdsl_map_instr* s = &p->code[pc];
-  if (s->op == VDSL_PIX_ATOMIC_ADD) pix_scatter_add(p, s, reg, inputs, ni, nj);
+  if (pix_scatter_op(s->op)) pix_scatter_add(p, s, reg, inputs, ni, nj);
   else reg[s->dst] = pix_apply(p, s, reg, inputs, o, i, j, count, ni, nj);
 }
 
@@ -290,7 +300,7 @@ void orc_pixel_program_rows(const vdsl_pixel_program* p, int64_t ni, int64_t nj,
                             int64_t r0, int64_t r1) {
   const int t0 = p->n_pre, b0 = t0 + p->n_test, q0 = b0 + p->n_body, end = q0 + p->n_post;
   int scatters = 0;
-  for (int pc = 0; pc < end; ++pc) scatters |= p->code[pc].op == VDSL_PIX_ATOMIC_ADD;
+  for (int pc = 0; pc < end; ++pc) scatters |= pix_scatter_op(p->code[pc].op);
 #pragma omp parallel for schedule(dynamic, 4) if (!scatters)
   for (int64_t i = r0; i < r1; ++i)
     for (int64_t j = 0; j < nj; ++j) {

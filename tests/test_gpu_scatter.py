@@ -397,3 +397,39 @@ def test_mpm88_example_runs(dev, q):
     assert res["frames"] == 2 and pos.shape == (8192, 2) and np.isfinite(pos).all()
     assert 0.0 < float(pos.min()) and float(pos.max()) < 1.0
     assert float(pos[:, 1].mean()) < 0.4  # the block has fallen (it starts at 0.2 - 0.6)
+
+
+@pytest.mark.parametrize("where", ["lane", "row", "const", "escape"])
+def test_scatter_max_min_bit_exact(dev, q, where):
+    """ti.atomic_max / atomic_min on every device path (one per lane into memory, row-uniform
+    per wave, constant per block, constant after an escape loop in 16 x 16 patches), f32 with NaN,
+    signed zeros and infinities among the values, and int32: equal to the oracle (fmaxf / fminf
+    give one value in any order; a zero result may differ in sign only)."""
+    ni, nj = 70, 333
+    rng = np.random.default_rng(50 + len(where))
+    v = rng.standard_normal((ni, nj)).astype(f32)
+    v.ravel()[rng.choice(v.size, 300, replace=False)] = rng.choice(np.array([np.nan, 0.0, -0.0, np.inf, -np.inf], f32), 300)
+    b = pp.Builder()
+    x = b.load(0)
+    if where == "lane":
+        row, col, R, C = 0.0, b.op("floor", b.op("mul", b.op("abs", x), 3.0)), 1, 12
+    elif where == "row":
+        row, col, R, C = b.op("sub", b.index(0), b.op("mul", b.op("floor", b.op("mul", b.index(0), 0.125)), 8.0)), 0.0, 8, 1
+    else:
+        row, col, R, C = 0.0, 0.0, 1, 1
+    eff = [b.scatter_add(1, row, col, x, op="max"), b.scatter_add(2, row, col, x, op="min"),
+           b.scatter_add(3, row, col, b.op("mul", x, 100.0), op="max")]
+    kw = dict(out=None)
+    if where == "escape":  # a test loop first: the patch mapping
+        s = b.state("s")
+        kw = dict(init={"s": 0.0}, test=("lt", s, b.op("abs", x)), body={"s": b.op("add", s, 0.5)}, max_iter=9, out=pp.COUNT)
+    prog = pp.compile_program(b, effects=eff, in_dtypes=[pp.F32, pp.F32, pp.F32, pp.I32],
+                              in_extents=[None, (R, C), (R, C), (R, C)], **kw)
+    t = [np.full((R, C), -7.0, f32), np.full((R, C), 7.0, f32), np.full((R, C), -5, np.int32)]
+    got_out, back = run_scatter(dev, q, prog, [v] + [a.copy() for a in t], ni, nj)
+    want_out = oracle.pixel_program(prog, ni, nj, [v] + t)
+    if where == "escape":
+        assert np.array_equal(got_out, want_out)
+    assert np.array_equal(back[1], t[0], equal_nan=True) and np.array_equal(back[2], t[1], equal_nan=True)
+    assert np.array_equal(back[3], t[2])
+    assert np.isinf(t[0]).any() or where == "lane"  # the infinities reached the maxima

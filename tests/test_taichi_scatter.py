@@ -403,3 +403,64 @@ def test_mpm88_substeps_on_the_oracle_equal_numpy():
             assert np.array_equal(arrays[k], want), k
         ref = (x2, v2, C2, J2)
     assert abs(float(arrays["grid_m"].sum(dtype=np.float64)) - n * (1.0 / 256) ** 2) < 1e-6  # mass is conserved
+
+
+# ---- scatter max / min (ti.atomic_max / atomic_min) -------------------------------------------------
+def test_oracle_scatter_max_min_equal_numpy():
+    """f32 max / min as fmaxf / fminf (np.fmax.at / np.fmin.at: a NaN value is ignored), int32
+    exactly (np.maximum.at / np.minimum.at), over NaN, signed zeros and infinities."""
+    ni, nj, bins = 19, 23, 6
+    rng = np.random.default_rng(15)
+    v = rng.standard_normal((ni, nj)).astype(f32)
+    v.ravel()[rng.choice(v.size, 40, replace=False)] = rng.choice(np.array([np.nan, 0.0, -0.0, np.inf, -np.inf], f32), 40)
+    col = rng.integers(0, bins, (ni, nj)).astype(f32)
+    b = pp.Builder()
+    x, c = b.load(0, 0), b.load(0, 1)
+    eff = [b.scatter_add(1, 0.0, c, x, op="max"), b.scatter_add(2, 0.0, c, x, op="min"),
+           b.scatter_add(3, 0.0, c, b.op("mul", x, 1000.0), op="max"), b.scatter_add(3, 0.0, c, 1.0, op="add")]
+    prog = pp.compile_program(b, out=None, effects=eff, in_widths=[2, 1, 1, 1], in_dtypes=[pp.F32, pp.F32, pp.F32, pp.I32],
+                              in_extents=[None, (1, bins), (1, bins), (1, bins)])
+    mx = np.full((1, bins), -5.0, f32)
+    mn = np.full((1, bins), np.nan, f32)  # a NaN element takes the first value
+    im = np.zeros((1, bins), np.int32)
+    oracle.pixel_program(prog, ni, nj, [np.stack([v, col], -1), mx, mn, im])
+    idx = (np.zeros(v.size, np.int64), col.astype(np.int64).ravel())
+    want_mx, want_mn = np.full((1, bins), -5.0, f32), np.full((1, bins), np.nan, f32)
+    np.fmax.at(want_mx, idx, v.ravel())
+    np.fmin.at(want_mn, idx, v.ravel())
+    assert np.array_equal(mx, want_mx, equal_nan=True) and np.array_equal(mn, want_mn, equal_nan=True)
+    # the int32 target takes max(trunc(1000 v)) (NaN -> 0, infinities saturate) and then + 1 per
+    # pixel (wrapping), in program order pixel by pixel
+    want_i = np.zeros(bins, np.int64)
+    for val, k in zip(v.ravel(), col.astype(np.int64).ravel()):
+        t = 0 if np.isnan(val) else int(np.clip(np.trunc(np.float64(np.float32(val * np.float32(1000.0)))), -2**31, 2**31 - 1))
+        want_i[k] = (max(want_i[k], t) + 1 + 2**31) % 2**32 - 2**31  # the add wraps in int32
+    assert np.array_equal(im[0], want_i.astype(np.int32))
+
+
+ATOMIC_EXT = """import taichi as ti
+x = ti.field(dtype=float, shape=(30, 20))
+mx = ti.field(dtype=float, shape=())
+mn = ti.field(dtype=float, shape=4)
+peak = ti.field(dtype=float, shape=(30, 20))
+
+@ti.kernel
+def k():
+    for i, j in x:
+        ti.atomic_max(mx[None], x[i, j])
+        ti.atomic_min(mn[j % 4], x[i, j] * 2.0)
+        ti.atomic_max(peak[i, j], x[i, j] - 0.5)
+"""
+
+
+def test_front_end_atomic_max_min():
+    low, names = lower_named(ATOMIC_EXT, "k", {})
+    rng = np.random.default_rng(16)
+    x = rng.standard_normal((30, 20)).astype(f32)
+    p0 = rng.standard_normal((30, 20)).astype(f32)
+    arr = {"x": x, "mx": np.array(-100.0, f32), "mn": np.full(4, 100.0, f32), "peak": p0.copy()}
+    run_ops(low, names, arr)
+    assert float(arr["mx"]) == float(x.max())
+    j = np.broadcast_to(np.arange(20), (30, 20))
+    assert np.array_equal(arr["mn"], np.array([(x * f32(2.0))[j % 4 == k].min() for k in range(4)], f32))
+    assert np.array_equal(arr["peak"], np.maximum(p0, x - f32(0.5)))  # the pixel's own element: a plain max

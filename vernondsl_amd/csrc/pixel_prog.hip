@@ -24,6 +24,10 @@ namespace {
 
 JitCounters g_pix_jit;
 
+bool scatter_op(int op) {
+  return op == VDSL_PIX_ATOMIC_ADD || op == VDSL_PIX_ATOMIC_MAX || op == VDSL_PIX_ATOMIC_MIN;
+}
+
 int check_program(const vdsl_pixel_program& p, int n_inputs) {
   const int64_t total = int64_t{p.n_pre} + p.n_test + p.n_body + p.n_post;
   if (p.n_pre < 0 || p.n_test < 0 || p.n_body < 0 || p.n_post < 0 || total > VDSL_PIX_MAX_INSTR)
@@ -55,7 +59,7 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
     const vdsl_map_instr& s = p.code[pc];
     const std::string at = "pixel program: instruction " + std::to_string(pc);
     const bool map_op = s.op >= VDSL_MAP_LOAD && s.op <= VDSL_MAP_ADD_IMM;
-    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_TRUNC;
+    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_ATOMIC_MIN;
     if (!map_op && !pix_op) return fail(VDSL_ERR_INVALID_ARG, at + ": unknown opcode " + std::to_string(s.op));
     if (s.dst >= VDSL_PIX_MAX_REGS || s.b >= VDSL_PIX_MAX_REGS || s.c >= VDSL_PIX_MAX_REGS)
       return fail(VDSL_ERR_INVALID_ARG, at + ": register out of range");
@@ -68,7 +72,7 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
       const bool comp_ok = s.a < n_inputs && s.imm >= 0.0f && s.imm < static_cast<float>(p.in_widths[s.a]) &&
                            s.imm == static_cast<float>(static_cast<int>(s.imm));
       if (!comp_ok) return fail(VDSL_ERR_INVALID_ARG, at + ": LOAD_AT of an input or component that is not there");
-    } else if (s.op == VDSL_PIX_ATOMIC_ADD) {
+    } else if (scatter_op(s.op)) {
       const bool comp_ok = s.a < n_inputs && s.imm >= 0.0f && s.imm < static_cast<float>(p.in_widths[s.a]) &&
                            s.imm == static_cast<float>(static_cast<int>(s.imm));
       if (!comp_ok) return fail(VDSL_ERR_INVALID_ARG, at + ": ATOMIC_ADD to an input or component that is not there");
@@ -104,9 +108,13 @@ int privatized(const vdsl_pixel_program& p, const std::vector<char>& flags, int 
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   int64_t used = 0, own = 0;
   for (int t = 0; t <= k; ++t) {
-    bool per_pixel = false;
-    for (int pc = 0; pc < total; ++pc)
-      per_pixel |= p.code[pc].op == VDSL_PIX_ATOMIC_ADD && p.code[pc].a == t && !(flags[pc] & 4);
+    bool per_pixel = false, other = false;  // adds at per-pixel indices; a max or min into it
+    for (int pc = 0; pc < total; ++pc) {
+      if (p.code[pc].a != t) continue;
+      per_pixel |= p.code[pc].op == VDSL_PIX_ATOMIC_ADD && !(flags[pc] & 4);
+      other |= p.code[pc].op == VDSL_PIX_ATOMIC_MAX || p.code[pc].op == VDSL_PIX_ATOMIC_MIN;
+    }
+    per_pixel &= !other;
     const int64_t elems = static_cast<int64_t>(p.in_rows[t] ? p.in_rows[t] : ni) * (p.in_cols[t] ? p.in_cols[t] : nj) *
                           p.in_widths[t];
     own = per_pixel && used + elems <= kPrivMax ? elems : 0;
@@ -133,7 +141,7 @@ int rows_per_block(const vdsl_pixel_program& p, const std::vector<char>& flags, 
   bool gathers = false, reduction = p.out_kind == VDSL_PIX_OUT_NONE;
   for (int pc = 0; pc < total; ++pc) {
     gathers |= p.code[pc].op == VDSL_PIX_LOAD_AT;
-    if (p.code[pc].op == VDSL_PIX_ATOMIC_ADD && !(flags[pc] & 4) && !priv[p.code[pc].a]) reduction = false;
+    if (scatter_op(p.code[pc].op) && !(flags[pc] & 4) && !priv[p.code[pc].a]) reduction = false;
   }
   return reduction ? 64 : gathers ? 8 : 4;
 }
@@ -156,7 +164,8 @@ int reads(int op) {
     case VDSL_MAP_ADD: case VDSL_MAP_SUB: case VDSL_MAP_MUL: case VDSL_MAP_DIV: case VDSL_MAP_MAX: case VDSL_MAP_MIN:
     case VDSL_PIX_LT: case VDSL_PIX_LE: case VDSL_PIX_EQ: case VDSL_PIX_NE: return 3;  // a, b
     case VDSL_MAP_FMA: case VDSL_PIX_SELECT: return 7;  // a, b, c
-    case VDSL_PIX_ATOMIC_ADD: return 6;  // b, c (and the value r[dst]; no register written)
+    case VDSL_PIX_ATOMIC_ADD: case VDSL_PIX_ATOMIC_MAX: case VDSL_PIX_ATOMIC_MIN:
+      return 6;  // b, c (and the value r[dst]; no register written)
     default: return 1;  // a
   }
 }
@@ -180,7 +189,7 @@ std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
   auto const_step = [&](int pc) {
     const vdsl_map_instr& s = p.code[pc];
     const int rd = reads(s.op);
-    if (s.op == VDSL_PIX_ATOMIC_ADD) {
+    if (scatter_op(s.op)) {
       if (cst[s.b] && cst[s.c]) flag[pc] = static_cast<char>(flag[pc] | 4);
       return;
     }
@@ -193,9 +202,9 @@ std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
     const vdsl_map_instr& s = p.code[pc];
     const int rd = reads(s.op);
     const bool in_uni = (!(rd & 1) || st[s.a]) && (!(rd & 2) || st[s.b]) && (!(rd & 4) || st[s.c]);
-    if (s.op == VDSL_PIX_LOAD_AT || s.op == VDSL_PIX_ATOMIC_ADD)
+    if (s.op == VDSL_PIX_LOAD_AT || scatter_op(s.op))
       flag[pc] = static_cast<char>((st[s.b] ? 1 : 0) | (st[s.c] ? 2 : 0));
-    if (s.op == VDSL_PIX_ATOMIC_ADD) return;  // writes no register
+    if (scatter_op(s.op)) return;  // writes no register
     bool out;
     if (s.op == VDSL_MAP_CONST || s.op == VDSL_PIX_TRIP) out = true;  // the trip is the same on every lane
     else if (s.op == VDSL_PIX_INDEX) out = s.a == 0;
@@ -206,7 +215,7 @@ std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
   for (int pc = 0; pc < p.n_pre; ++pc) step(pc, uni), const_step(pc);
   // after the loop, a register it writes is no constant
   for (int pc = p.n_pre; pc < p.n_pre + p.n_test + p.n_body; ++pc)
-    if (p.code[pc].op != VDSL_PIX_ATOMIC_ADD) cst[p.code[pc].dst] = false;
+    if (!scatter_op(p.code[pc].op)) cst[p.code[pc].dst] = false;
   if (p.loop) {
     bool head[VDSL_PIX_MAX_REGS];
     for (int r = 0; r < VDSL_PIX_MAX_REGS; ++r) head[r] = uni[r];
@@ -366,7 +375,7 @@ extern "C" int vdsl_op_pixel_program(vdsl_queue q, int32_t ni, int32_t nj, const
   bool target[VDSL_PIX_MAX_INPUTS] = {};  // inputs the program scatter-adds into (written)
   const int total = p.n_pre + p.n_test + p.n_body + p.n_post;
   for (int pc = 0; pc < total; ++pc)
-    if (p.code[pc].op == VDSL_PIX_ATOMIC_ADD) target[p.code[pc].a] = true;
+    if (scatter_op(p.code[pc].op)) target[p.code[pc].a] = true;
   PixIn in{};
   for (int k = 0; k < n_inputs; ++k) {
     const std::string name = "input" + std::to_string(k);

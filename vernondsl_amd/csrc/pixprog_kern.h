@@ -74,6 +74,11 @@ __device__ __forceinline__ unsigned pix_index(float x, int n) {
 }
 
 
+// Scatter-adds and their max / min forms: instructions with an effect and no result register.
+__device__ constexpr bool pix_scatter_op(int op) {
+  return op == VDSL_PIX_ATOMIC_ADD || op == VDSL_PIX_ATOMIC_MAX || op == VDSL_PIX_ATOMIC_MIN;
+}
+
 // A register stored to an int32 field: truncation toward zero, NaN -> 0, saturating.
 __device__ __forceinline__ int pix_to_i32(float x) {
   if (x != x) return 0;
@@ -102,6 +107,50 @@ __device__ __forceinline__ int pix_wave_sum(int v) {
   return v;
 }
 
+// Wave maximum / minimum (OP VDSL_PIX_ATOMIC_MAX / MIN) of v: f32 as fmaxf / fminf (a lane with
+// nothing to give holds NaN, which they ignore), int32 exactly.
+template <int OP>
+__device__ __forceinline__ float pix_wave_ext(float v) {
+  const int lane = pix_lane();
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float o = __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ m) << 2, __float_as_int(v)));
+    v = OP == VDSL_PIX_ATOMIC_MAX ? fmaxf(v, o) : fminf(v, o);
+  }
+  return v;
+}
+
+template <int OP>
+__device__ __forceinline__ int pix_wave_ext(int v) {
+  const int lane = pix_lane();
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const int o = __builtin_amdgcn_ds_bpermute((lane ^ m) << 2, v);
+    v = OP == VDSL_PIX_ATOMIC_MAX ? (o > v ? o : v) : (o < v ? o : v);
+  }
+  return v;
+}
+
+// The combination of two values by scatter op OP (sum, max, min), and its identity.
+template <int OP>
+__device__ __forceinline__ float pix_combine(float a, float b) {
+  return OP == VDSL_PIX_ATOMIC_ADD ? a + b : OP == VDSL_PIX_ATOMIC_MAX ? fmaxf(a, b) : fminf(a, b);
+}
+template <int OP>
+__device__ __forceinline__ int pix_combine(int a, int b) {
+  if constexpr (OP == VDSL_PIX_ATOMIC_ADD) return static_cast<int>(static_cast<unsigned>(a) + static_cast<unsigned>(b));
+  else if constexpr (OP == VDSL_PIX_ATOMIC_MAX) return a > b ? a : b;
+  else return a < b ? a : b;
+}
+template <int OP>
+__device__ __forceinline__ float pix_none_f() {
+  return OP == VDSL_PIX_ATOMIC_ADD ? 0.0f : __int_as_float(0x7FC00000);  // NaN: ignored by fmaxf / fminf
+}
+template <int OP>
+__device__ __forceinline__ int pix_none_i() {
+  return OP == VDSL_PIX_ATOMIC_ADD ? 0 : OP == VDSL_PIX_ATOMIC_MAX ? -2147483647 - 1 : 2147483647;
+}
+
 // The element a scatter-add into input A at [x][y] reaches: ok is false where x or y is outside
 // A's extents (NaN fails every comparison; below 2^30 the conversion is exact truncation, and the
 // row and column are then checked as integers, since float(rows) may round above 2^24).
@@ -113,13 +162,31 @@ __device__ __forceinline__ PixOff<P> pix_target(const PixIn& in, float x, float 
   return static_cast<PixOff<P>>(static_cast<unsigned>(xi)) * static_cast<unsigned>(in.cols[A]) + static_cast<unsigned>(yi);
 }
 
-template <class P, int A>
+template <class P, int A, int OP = VDSL_PIX_ATOMIC_ADD>
 __device__ __forceinline__ void pix_atomic(const PixIn& in, PixOff<P> e, int c, float vf, int vi) {
   char* base = const_cast<char*>(reinterpret_cast<const char*>(in.p[A]));
-  if constexpr (P::in_dtypes[A] == VDSL_I32)
-    atomicAdd(reinterpret_cast<int*>(base) + e, vi);
-  else
-    unsafeAtomicAdd(reinterpret_cast<float*>(base) + (e * static_cast<PixOff<P>>(P::in_widths[A]) + static_cast<PixOff<P>>(c)), vf);
+  if constexpr (P::in_dtypes[A] == VDSL_I32) {
+    int* t = reinterpret_cast<int*>(base) + e;
+    if constexpr (OP == VDSL_PIX_ATOMIC_ADD) atomicAdd(t, vi);
+    else if constexpr (OP == VDSL_PIX_ATOMIC_MAX) atomicMax(t, vi);
+    else atomicMin(t, vi);
+  } else {
+    float* t = reinterpret_cast<float*>(base) + (e * static_cast<PixOff<P>>(P::in_widths[A]) + static_cast<PixOff<P>>(c));
+    if constexpr (OP == VDSL_PIX_ATOMIC_ADD) {
+      unsafeAtomicAdd(t, vf);
+    } else {
+      // compare and swap until the element holds fmaxf / fminf(element, vf) (or already did)
+      unsigned* u = reinterpret_cast<unsigned*>(t);
+      unsigned old = __hip_atomic_load(u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (;;) {
+        const unsigned want = __float_as_uint(pix_combine<OP>(__uint_as_float(old), vf));
+        if (want == old) break;
+        const unsigned seen = atomicCAS(u, old, want);
+        if (seen == old) break;
+        old = seen;
+      }
+    }
+  }
 }
 
 // Scatter-adds at constant indices (ext[2]: the same element for every pixel, such as
@@ -128,7 +195,7 @@ __device__ __forceinline__ void pix_atomic(const PixIn& in, PixOff<P> e, int c, 
 template <class P>
 struct PixConstAdds {
   static constexpr int end = P::n_pre + P::n_test + P::n_body + P::n_post;
-  static constexpr bool at(int pc) { return P::code[pc].op == VDSL_PIX_ATOMIC_ADD && P::code[pc].ext[2] != 0; }
+  static constexpr bool at(int pc) { return pix_scatter_op(P::code[pc].op) && P::code[pc].ext[2] != 0; }
   static constexpr int slot(int pc) {
     int n = 0;
     for (int q = 0; q < pc; ++q) n += at(q) ? 1 : 0;
@@ -164,22 +231,31 @@ __device__ __forceinline__ void pix_add(const PixIn& in, PixAcc<P>& acc, PixOff<
 // VDSL_PIX_ATOMIC_ADD into input A: component c of [x][y] += v on lanes with act set, where the
 // element is in A.  UNI: x and y are the same on every lane of the wave (host dataflow, row
 // mapping), so the wave's values are summed and one lane adds.
-template <class P, int A, bool UNI>
+template <class P, int A, bool UNI, int OP>
 __device__ __forceinline__ void pix_scatter_add(const PixIn& in, PixAcc<P>& acc, float x, float y, float v, int c, bool act) {
   bool in_a;
   const PixOff<P> e = pix_target<P, A>(in, x, y, in_a);
   const bool ok = act && in_a;
   constexpr bool i32 = P::in_dtypes[A] == VDSL_I32;
-  float vf = ok && !i32 ? v : 0.0f;
-  int vi = ok && i32 ? pix_to_i32(v) : 0;
+  float vf = ok && !i32 ? v : pix_none_f<OP>();
+  int vi = ok && i32 ? pix_to_i32(v) : pix_none_i<OP>();
   if constexpr (UNI) {
     const uint64_t any = __builtin_amdgcn_ballot_w64(ok);
     if (any == 0ull) return;
-    if constexpr (i32) vi = pix_wave_sum(vi);
-    else vf = pix_wave_sum(vf);
-    if (pix_lane() == __builtin_ctzll(any)) pix_add<P, A>(in, acc, e, c, vf, vi);
-  } else {
-    if (ok) pix_add<P, A>(in, acc, e, c, vf, vi);
+    if constexpr (OP == VDSL_PIX_ATOMIC_ADD) {
+      if constexpr (i32) vi = pix_wave_sum(vi);
+      else vf = pix_wave_sum(vf);
+    } else {
+      if constexpr (i32) vi = pix_wave_ext<OP>(vi);
+      else vf = pix_wave_ext<OP>(vf);
+    }
+    if (pix_lane() == __builtin_ctzll(any)) {
+      if constexpr (OP == VDSL_PIX_ATOMIC_ADD) pix_add<P, A>(in, acc, e, c, vf, vi);
+      else pix_atomic<P, A, OP>(in, e, c, vf, vi);
+    }
+  } else if (ok) {
+    if constexpr (OP == VDSL_PIX_ATOMIC_ADD) pix_add<P, A>(in, acc, e, c, vf, vi);
+    else pix_atomic<P, A, OP>(in, e, c, vf, vi);
   }
 }
 
@@ -187,11 +263,15 @@ template <class P, int PC>
 __device__ __forceinline__ void pix_accumulate(PixAcc<P>& acc, float x, float y, float v, bool act) {
   constexpr vdsl_map_instr s = P::code[PC];
   constexpr int k = PixConstAdds<P>::slot(PC);
-  if constexpr (P::in_dtypes[s.a] == VDSL_I32)
-    acc.i[k] = static_cast<int>(static_cast<unsigned>(acc.i[k]) + static_cast<unsigned>(act ? pix_to_i32(v) : 0));
-  else
-    acc.f[k] += act ? v : 0.0f;
-  acc.n[k] += act ? 1 : 0;
+  constexpr int OP = s.op;
+  if (act) {
+    // the first value as it is (the accumulators start at 0, which is no identity of max / min)
+    if constexpr (P::in_dtypes[s.a] == VDSL_I32)
+      acc.i[k] = acc.n[k] ? pix_combine<OP>(acc.i[k], pix_to_i32(v)) : pix_to_i32(v);
+    else
+      acc.f[k] = acc.n[k] ? pix_combine<OP>(acc.f[k], v) : v;
+    acc.n[k] += 1;
+  }
   acc.x[k] = x;
   acc.y[k] = y;
 }
@@ -203,8 +283,15 @@ __device__ __forceinline__ void pix_flush_wave(PixAcc<P>& acc, float (*sf)[PixAc
                                                int (*sn)[PixAcc<P>::N]) {
   if constexpr (PixConstAdds<P>::at(PC)) {
     constexpr int k = PixConstAdds<P>::slot(PC);
-    const float f = pix_wave_sum(acc.f[k]);
-    const int iv = pix_wave_sum(acc.i[k]), n = pix_wave_sum(acc.n[k]);
+    constexpr int OP = P::code[PC].op;
+    // lanes without a value give the identity (0 for sums; for max / min NaN, or the extreme int)
+    const float f0 = acc.n[k] ? acc.f[k] : pix_none_f<OP>();
+    const int i0 = acc.n[k] ? acc.i[k] : pix_none_i<OP>();
+    float f;
+    int iv;
+    if constexpr (OP == VDSL_PIX_ATOMIC_ADD) f = pix_wave_sum(f0), iv = pix_wave_sum(i0);
+    else f = pix_wave_ext<OP>(f0), iv = pix_wave_ext<OP>(i0);
+    const int n = pix_wave_sum(acc.n[k]);
     if (pix_lane() == 0) {
       sf[threadIdx.x >> 6][k] = f;
       si[threadIdx.x >> 6][k] = iv;
@@ -220,13 +307,13 @@ __device__ __forceinline__ void pix_flush_add(const PixRt& rt, const PixIn& in, 
     constexpr vdsl_map_instr s = P::code[PC];
     constexpr int k = PixConstAdds<P>::slot(PC);
     if (threadIdx.x == k) {
-      const float f = ((sf[0][k] + sf[1][k]) + sf[2][k]) + sf[3][k];
-      const int iv = static_cast<int>(static_cast<unsigned>(si[0][k]) + static_cast<unsigned>(si[1][k]) +
-                                      static_cast<unsigned>(si[2][k]) + static_cast<unsigned>(si[3][k]));
+      constexpr int OP = s.op;
+      const float f = pix_combine<OP>(pix_combine<OP>(pix_combine<OP>(sf[0][k], sf[1][k]), sf[2][k]), sf[3][k]);
+      const int iv = pix_combine<OP>(pix_combine<OP>(pix_combine<OP>(si[0][k], si[1][k]), si[2][k]), si[3][k]);
       bool ok;
       const PixOff<P> e = pix_target<P, s.a>(in, acc.x[k], acc.y[k], ok);
       if (ok && sn[0][k] + sn[1][k] + sn[2][k] + sn[3][k] > 0)
-        pix_atomic<P, s.a>(in, e, static_cast<int>(rt.imm[PC]), f, iv);
+        pix_atomic<P, s.a, OP>(in, e, static_cast<int>(rt.imm[PC]), f, iv);
     }
   }
 }
@@ -247,13 +334,13 @@ template <class P, int PC>
 __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
                                          float fi, float fj, float fcount, int ni, int nj, bool act, PixAcc<P>& acc) {
   constexpr vdsl_map_instr s = P::code[PC];
-  if constexpr (s.op == VDSL_PIX_ATOMIC_ADD && s.ext[2] != 0) {
-    pix_accumulate<P, PC>(acc, r[s.b], r[s.c], r[s.dst], act);  // constant indices: added per block
-  } else if constexpr (s.op == VDSL_PIX_ATOMIC_ADD) {
-    // one add per wave where both indices are the same on every lane (found wave-uniform by the
-    // host in the row mapping: ext[0], ext[1]), else one per lane
+  if constexpr (pix_scatter_op(s.op) && s.ext[2] != 0) {
+    pix_accumulate<P, PC>(acc, r[s.b], r[s.c], r[s.dst], act);  // constant indices: combined per block
+  } else if constexpr (pix_scatter_op(s.op)) {
+    // one add (max, min) per wave where both indices are the same on every lane (found
+    // wave-uniform by the host in the row mapping: ext[0], ext[1]), else one per lane
     constexpr bool uni = P::rows > 0 && s.ext[0] != 0 && s.ext[1] != 0;
-    pix_scatter_add<P, s.a, uni>(in, acc, r[s.b], r[s.c], r[s.dst], static_cast<int>(rt.imm[PC]), act);
+    pix_scatter_add<P, s.a, uni, s.op>(in, acc, r[s.b], r[s.c], r[s.dst], static_cast<int>(rt.imm[PC]), act);
   } else if constexpr (s.op == VDSL_MAP_LOAD) {
     r[s.dst] = pix_load<P, s.a>(in, o, s.c);
   } else if constexpr (s.op == VDSL_PIX_LOAD_AT) {
@@ -318,14 +405,15 @@ __device__ constexpr uint32_t pix_reads(const vdsl_map_instr& s) {
       return (1u << s.a) | (1u << s.b);
     case VDSL_PIX_LOAD_AT: return (1u << s.b) | (1u << s.c);
     case VDSL_MAP_FMA: case VDSL_PIX_SELECT: return (1u << s.a) | (1u << s.b) | (1u << s.c);
-    case VDSL_PIX_ATOMIC_ADD: return (1u << s.dst) | (1u << s.b) | (1u << s.c);  // the value is r[dst]
+    case VDSL_PIX_ATOMIC_ADD: case VDSL_PIX_ATOMIC_MAX: case VDSL_PIX_ATOMIC_MIN:
+      return (1u << s.dst) | (1u << s.b) | (1u << s.c);  // the value is r[dst]
     default: return 1u << s.a;
   }
 }
 
-// Register an instruction writes (a bit); a scatter-add writes none.
+// Register an instruction writes (a bit); a scatter-add (or max, min) writes none.
 __device__ constexpr uint32_t pix_writes(const vdsl_map_instr& s) {
-  return s.op == VDSL_PIX_ATOMIC_ADD ? 0u : 1u << s.dst;
+  return pix_scatter_op(s.op) ? 0u : 1u << s.dst;
 }
 
 // Register sets of program P (instructions [lo, hi) of its table): written, and read before

@@ -26,7 +26,8 @@ from . import _lib
 MAX_INSTR, MAX_REGS, MAX_INPUTS = 256, 32, 8
 OP = dict(_lib.MAP_OPS)
 OP.update({"index": 32, "cos": 33, "sin": 34, "count": 35, "lt": 36, "le": 37, "eq": 38, "ne": 39, "select": 40,
-           "floor": 41, "load_at": 42, "trip": 43, "atomic_add": 44, "trunc": 45})
+           "floor": 41, "load_at": 42, "trip": 43, "atomic_add": 44, "trunc": 45, "atomic_max": 46, "atomic_min": 47})
+SCATTERS = ("atomic_add", "atomic_max", "atomic_min")  # effect nodes: no result register
 TESTS = {"none": 0, "lt": 1, "le": 2, "gt": 3, "ge": 4}
 OUT_REG, OUT_COUNT, OUT_I32, OUT_NONE = 0, 1, 2, 3
 F32, I32 = _lib.F32, _lib.I32  # input dtypes (vdsl_dtype)
@@ -115,9 +116,12 @@ class Builder:
         args = tuple(a if isinstance(a, Node) else self.const(a) for a in (row, col))
         return self._node("load_at", args, val=(int(k), int(component)))
 
-    def scatter_add(self, k: int, row, col, value, component: int = 0) -> Node:
-        """The effect `input k [row][col] (component) += value` (an atomic add; dropped where the
-        indices fall outside field k), for compile_program(effects=...)."""
+    def scatter_add(self, k: int, row, col, value, component: int = 0, op: str = "add") -> Node:
+        """The effect `input k [row][col] (component) += value` (an atomic add; op "max" / "min":
+        the element becomes the max / min of itself and value; dropped where the indices fall
+        outside field k), for compile_program(effects=...)."""
+        if op not in ("add", "max", "min"):
+            raise ProgramError(f"unknown scatter op {op!r}")
         if not 0 <= k < MAX_INPUTS:
             raise ProgramError(f"at most {MAX_INPUTS} input fields")
         if not 0 <= component < 4:
@@ -125,7 +129,7 @@ class Builder:
         args = tuple(a if isinstance(a, Node) else self.const(a) for a in (row, col, value))
         # never merged with an equal one: two equal adds in a body are two adds
         self._effects = getattr(self, "_effects", 0) + 1
-        return self._node("atomic_add", args, val=(int(k), int(component), self._effects))
+        return self._node("atomic_" + op, args, val=(int(k), int(component), self._effects))
 
     def state(self, name: str) -> Node:
         return self._node("state", val=name)
@@ -200,7 +204,7 @@ class _Emitter:
                 if a not in self.pinned and id(a) not in root_ids and last.get(id(a)) == pos and reg.get(id(a)) is not None:
                     free.append(reg[id(a)])
                     reg[id(a)] = None
-            if n.kind == "atomic_add":  # an effect: reads its operands, writes no register
+            if n.kind in SCATTERS:  # an effect: reads its operands, writes no register
                 self._instr(n, None, srcs)
                 continue
             if not free:
@@ -235,8 +239,8 @@ class _Emitter:
             op, a, c = OP["load"], n.val[0], n.val[1]
         elif k == "load_at":
             op, a, b, c, imm = OP["load_at"], n.val[0], srcs[0], srcs[1], float(n.val[1])
-        elif k == "atomic_add":  # dst names the register of the value added
-            op, dst, a, b, c, imm = OP["atomic_add"], srcs[2], n.val[0], srcs[0], srcs[1], float(n.val[1])
+        elif k in SCATTERS:  # dst names the register of the value added (or compared)
+            op, dst, a, b, c, imm = OP[k], srcs[2], n.val[0], srcs[0], srcs[1], float(n.val[1])
         elif k == "count":
             op = OP["count"]
         elif k == "trip":
@@ -289,7 +293,7 @@ def compile_program(b: Builder, init: dict | None = None, test=None, body: dict 
     if out is None and not effects:
         raise ProgramError("no output")
     for e in effects:
-        if not isinstance(e, Node) or e.kind != "atomic_add":
+        if not isinstance(e, Node) or e.kind not in SCATTERS:
             raise ProgramError("effects are scatter_add nodes")
         if "trip" in e.deps:
             raise ProgramError("a scatter-add inside a runtime loop is not supported (only before or after it)")
@@ -442,8 +446,9 @@ def describe(p: PixelProgram) -> str:
     for k in range(total):
         s = p.code[k]
         sec = "pre" if k < p.n_pre else "test" if k < p.n_pre + p.n_test else "body" if k < p.n_pre + p.n_test + p.n_body else "post"
-        if s.op == OP["atomic_add"]:
-            lines.append(f"{sec:4s} input{s.a}[r{s.b}][r{s.c}].{int(s.imm)} += r{s.dst}")
+        if s.op in (OP["atomic_add"], OP["atomic_max"], OP["atomic_min"]):
+            sym = {OP["atomic_add"]: "+=", OP["atomic_max"]: "max=", OP["atomic_min"]: "min="}[s.op]
+            lines.append(f"{sec:4s} input{s.a}[r{s.b}][r{s.c}].{int(s.imm)} {sym} r{s.dst}")
             continue
         lines.append(f"{sec:4s} r{s.dst} = {names.get(s.op, s.op)} a={s.a} b={s.b} c={s.c} imm={s.imm:g}")
     return "\n".join(lines)

@@ -40,7 +40,8 @@ in Taichi); a kernel of several top-level struct-fors runs their lowerings one a
 1-D fields and struct-fors (`for i in x:`, `for i in range(N):`) run as one row of the grid, 3-D
 ones ([A][B][C], `for i, j, k in u:`) as the grid [A B][C]; 0-D fields (`shape=()`) are read and
 added into as `s[None]`.  `F[idx] += v` / `-= v` at an index other than the loop's (and
-`ti.atomic_add(F[idx], v)` as a statement) is Taichi's atomic add: a scatter-add of the program,
+`ti.atomic_add(F[idx], v)` as a statement; `ti.atomic_max` / `atomic_min` alike) is Taichi's atomic
+add: a scatter-add of the program,
 dropped where an index falls outside F, with idx a tuple or a vector expression such as
 `base + offset` (`.cast(int)` / `int()` truncate); a field added into is neither read nor stored
 by the same struct-for, and adds inside an if happen only where the branch runs.  `ti.Matrix`
@@ -1310,7 +1311,7 @@ class _PixInterp:
                 if len(n.args) != 2:
                     raise TaichiLoweringError("ti.cast takes (value, dtype)")
                 return self.cast(self.expr(n.args[0], local), self.expr(n.args[1], local))
-            if f.attr in ("atomic_add", "atomic_sub"):
+            if f.attr in ("atomic_add", "atomic_sub", "atomic_max", "atomic_min"):
                 raise TaichiLoweringError(f"ti.{f.attr} is supported as a statement (its old value is not returned)")
             raise TaichiLoweringError(f"call {f.attr!r} is not supported")
         if isinstance(f, ast.Name):
@@ -1380,7 +1381,7 @@ class _PixInterp:
             raise TaichiLoweringError("field indices are scalars")
         return vals
 
-    def scatter(self, fld, idx, value, local, negate=False):
+    def scatter(self, fld, idx, value, local, negate=False, op="add"):
         """fld[idx] += value (-= with negate) at an index other than this pixel's: Taichi's atomic
         add, an effect of the program (pixprog scatter_add), dropped where an index falls outside
         fld.  The field must be neither stored nor read in the same struct-for (its reads would
@@ -1436,7 +1437,7 @@ class _PixInterp:
         for q, x in enumerate(comps):
             if negate:
                 x = self.unary("neg", x)
-            self.scatters.append(self.b.scatter_add(k, r, c, self.node(x), q))
+            self.scatters.append(self.b.scatter_add(k, r, c, self.node(x), q, op=op))
 
     def minmax(self, which, vals):
         if len(vals) < 2:
@@ -1843,12 +1844,27 @@ class _PixInterp:
             # ti.atomic_add(field[idx], v) / ti.atomic_sub as a statement: field[idx] += v / -= v
             fn = st.value.func
             name = fn.attr if isinstance(fn, ast.Attribute) else fn.id if isinstance(fn, ast.Name) else None
-            if name in ("atomic_add", "atomic_sub"):
+            if name in ("atomic_add", "atomic_sub", "atomic_max", "atomic_min"):
                 args = st.value.args
                 if len(args) != 2 or not isinstance(args[0], ast.Subscript):
                     raise TaichiLoweringError(f"ti.{name} takes (field[index], value)")
-                op = ast.Add() if name == "atomic_add" else ast.Sub()
-                return self.assign(ast.AugAssign(target=args[0], op=op, value=args[1], lineno=getattr(st, "lineno", 0)), local)
+                if name in ("atomic_add", "atomic_sub"):
+                    op = ast.Add() if name == "atomic_add" else ast.Sub()
+                    return self.assign(ast.AugAssign(target=args[0], op=op, value=args[1],
+                                                     lineno=getattr(st, "lineno", 0)), local)
+                which = name[len("atomic_"):]
+                fld = self.expr(args[0].value, local)
+                if not isinstance(fld, Field):
+                    raise TaichiLoweringError(f"ti.{name} takes a field element")
+                val = self.expr(args[1], local)
+                if self._at_here(fld, args[0].slice):  # this pixel's element: a plain max / min and store
+                    cur = self._field_read(fld, args[0].slice, local)
+                    if isinstance(val, list):
+                        val = _PVec(val)
+                    self.store_here(fld, self.elementwise(lambda a, c: self.minmax(which, [a, c]), cur, val), local)
+                else:
+                    self.scatter(fld, args[0].slice, val, local, op=which)
+                return True
             return False
         if isinstance(st, ast.AugAssign) and isinstance(st.target, ast.Subscript):
             base = self.expr(st.target.value, local)
@@ -2310,8 +2326,8 @@ def _is_atomic_call(nd) -> bool:
     if not isinstance(nd, ast.Call):
         return False
     f = nd.func
-    return (f.attr if isinstance(f, ast.Attribute) else f.id if isinstance(f, ast.Name) else None) in ("atomic_add",
-                                                                                                       "atomic_sub")
+    return (f.attr if isinstance(f, ast.Attribute) else f.id if isinstance(f, ast.Name) else None) in (
+        "atomic_add", "atomic_sub", "atomic_max", "atomic_min")
 
 
 def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target, unroll=True):
