@@ -42,7 +42,7 @@ extern "C" {
  * and in_cols (inputs of another shape than the grid); 6: VDSL_PIX_ATOMIC_ADD,
  * VDSL_PIX_OUT_NONE (scatter-adds) and VDSL_PIX_TRUNC (struct layouts unchanged since 5); 7:
  * VDSL_PIX_MAX_INSTR 256 and VDSL_PIX_MAX_INPUTS 8 (vdsl_pixel_program's arrays grow),
- * VDSL_PIX_ATOMIC_MAX / MIN. */
+ * VDSL_PIX_ATOMIC_MAX / MIN and VDSL_PIX_STORE_AT. */
 #define VDSL_ABI_VERSION 7
 
 typedef enum vdsl_status {
@@ -357,7 +357,12 @@ typedef enum vdsl_pix_opcode {
    * converted as VDSL_PIX_OUT_I32 stores it); f32 as fmaxf / fminf (a NaN operand is ignored), in
    * any order the same value except that the sign of a zero result may depend on the order. */
   VDSL_PIX_ATOMIC_MAX = 46,
-  VDSL_PIX_ATOMIC_MIN = 47
+  VDSL_PIX_ATOMIC_MIN = 47,
+  /* Taichi's `F[idx] = v` at an index other than the pixel's: a plain store of r[dst] (int32:
+   * converted as VDSL_PIX_OUT_I32 stores it) with the operands, extents, drops and refusals of
+   * VDSL_PIX_ATOMIC_ADD; where several pixels store to one element, one of them wins, in no fixed
+   * order (a race in Taichi too). */
+  VDSL_PIX_STORE_AT = 48
 } vdsl_pix_opcode;
 
 typedef enum vdsl_pix_test {

@@ -164,7 +164,7 @@ def pixel_program(prog, ni: int, nj: int, inputs=(), rows=None) -> np.ndarray:
     program that stores nothing.  An input the program scatter-adds into is updated in place: it
     must be a C-contiguous array of its dtype (float32 / int32)."""
     total = prog.n_pre + prog.n_test + prog.n_body + prog.n_post
-    targets = {prog.code[pc].a for pc in range(total) if prog.code[pc].op in (44, 46, 47)}  # scatter add / max / min
+    targets = {prog.code[pc].a for pc in range(total) if prog.code[pc].op in (44, 46, 47, 48)}  # scatter add / max / min, store
     for k in targets:
         want = np.int32 if prog.in_dtypes[k] == 3 else np.float32
         a = inputs[k]

@@ -251,8 +251,8 @@ static int pix_test(int test, float a, float b) {
   }
 }
 
-/* VDSL_PIX_ATOMIC_ADD / MAX / MIN: component imm of input a at [(int)r[b]][(int)r[c]] += r[dst]
- * (or becomes the max / min of it and r[dst]) when 0 <= r[b] < rows and 0 <= r[c] < cols of
+/* VDSL_PIX_ATOMIC_ADD / MAX / MIN / STORE_AT: component imm of input a at [(int)r[b]][(int)r[c]]
+ * += r[dst] (or becomes the max / min of it and r[dst], or r[dst]) when 0 <= r[b] < rows and 0 <= r[c] < cols of
  * input a, else nothing.  f32: one f32 addition, fmaxf, fminf; int32: the value converted as an
  * int32 store converts it, added modulo 2^32, or compared. */
 static void pix_scatter_add(const vdsl_pixel_program* p, const vdsl_map_instr* s, const float* reg, const void* const* inputs,
@@ -266,19 +266,21 @@ static void pix_scatter_add(const vdsl_pixel_program* p, const vdsl_map_instr* s
   if (p->in_dtypes[s->a] == VDSL_I32) {
     int32_t* t = (int32_t*)inputs[s->a] + e;
     const int32_t v = pix_to_i32(reg[s->dst]);
-    if (s->op == VDSL_PIX_ATOMIC_ADD) *t = (int32_t)((uint32_t)*t + (uint32_t)v);
+    if (s->op == VDSL_PIX_STORE_AT) *t = v;
+    else if (s->op == VDSL_PIX_ATOMIC_ADD) *t = (int32_t)((uint32_t)*t + (uint32_t)v);
     else if (s->op == VDSL_PIX_ATOMIC_MAX) *t = v > *t ? v : *t;
     else *t = v < *t ? v : *t;
   } else {
     float* t = (float*)inputs[s->a] + e * p->in_widths[s->a] + (int)s->imm;
-    if (s->op == VDSL_PIX_ATOMIC_ADD) *t = *t + reg[s->dst];
+    if (s->op == VDSL_PIX_STORE_AT) *t = reg[s->dst];
+    else if (s->op == VDSL_PIX_ATOMIC_ADD) *t = *t + reg[s->dst];
     else if (s->op == VDSL_PIX_ATOMIC_MAX) *t = fmaxf(*t, reg[s->dst]);
     else *t = fminf(*t, reg[s->dst]);
   }
 }
 
-static int pix_scatter_op(int op) {
-  return op == VDSL_PIX_ATOMIC_ADD || op == VDSL_PIX_ATOMIC_MAX || op == VDSL_PIX_ATOMIC_MIN;
+static int pix_scatter_op(int op) {  /* the instructions with an effect: scatter add / max / min, store at */
+  return op == VDSL_PIX_ATOMIC_ADD || op == VDSL_PIX_ATOMIC_MAX || op == VDSL_PIX_ATOMIC_MIN || op == VDSL_PIX_STORE_AT;
 }
 
 /* One instruction: its register, or a scatter-add's effect. */

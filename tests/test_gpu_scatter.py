@@ -433,3 +433,25 @@ def test_scatter_max_min_bit_exact(dev, q, where):
     assert np.array_equal(back[1], t[0], equal_nan=True) and np.array_equal(back[2], t[1], equal_nan=True)
     assert np.array_equal(back[3], t[2])
     assert np.isinf(t[0]).any() or where == "lane"  # the infinities reached the maxima
+
+
+def test_stores_at_computed_indices_on_the_device(dev, q):
+    """The interior stencil, boundary and transposed-store kernels of the front-end test, each
+    program run on the device beside the oracle from the same fields: bit for bit (no two pixels
+    store to one element)."""
+    from test_taichi_scatter import STORES
+    rng = np.random.default_rng(22)
+    host = {"u": rng.random((40, 30)).astype(f32), "v": rng.random((40, 30)).astype(f32),
+            "code": rng.integers(-9, 9, (40, 30)).astype(np.int32)}
+    ts = {k: Tensor.from_numpy(dev, q, a) for k, a in host.items()}
+    try:
+        for kern in ("interior", "boundary", "transpose_into"):
+            low, names = lower_named(STORES, kern, {})
+            for op in low.ops():
+                kernels.pixel_program(q, op.program, [ts[names[id(f)]] for f in op.inputs], None, grid=op.grid)
+                run_ops(op, names, host)
+            for k in ("v", "code"):
+                assert np.array_equal(ts[k].numpy(q), host[k]), (kern, k)
+    finally:
+        for t in ts.values():
+            t.free()

@@ -665,10 +665,10 @@ def test_one_d_struct_fors_gathers_range_and_augmented_stores():
 
 
 @pytest.mark.parametrize("kernel,msg", [
-    ("    for i in x:\n        x[i, 0] = 1.0", "1-D"),
-    ("    for i, j in ti.ndrange(N):\n        x[i] = 1.0", "2 non-negative"),
-    ("    for i in range(N, 2):\n        x[i] = 1.0", "extent"),
-    ("    for i in x:\n        x[i + 1] = 1.0", "store must write field"),
+    ("    for i in x:\n        x[i, 0] = 1.0", "indexed with 2 indices"),
+    ("    for i, j in ti.ndrange(N):\n        x[i] = 1.0", "2 integer extent"),
+    ("    for i in range(N, 2, 1):\n        x[i] = 1.0", "extent"),
+    ("    for i in x:\n        x[i + 1] = 1.0\n        x[i] = 2.0", "both stored"),
 ])
 def test_one_d_errors(kernel, msg):
     text = "import taichi as ti\nN = 8\nx = ti.field(dtype=float, shape=N)\n@ti.kernel\ndef k():\n" + kernel + "\n"

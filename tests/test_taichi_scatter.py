@@ -464,3 +464,68 @@ def test_front_end_atomic_max_min():
     j = np.broadcast_to(np.arange(20), (30, 20))
     assert np.array_equal(arr["mn"], np.array([(x * f32(2.0))[j % 4 == k].min() for k in range(4)], f32))
     assert np.array_equal(arr["peak"], np.maximum(p0, x - f32(0.5)))  # the pixel's own element: a plain max
+
+
+# ---- stores at computed indices (VDSL_PIX_STORE_AT) --------------------------------------------------
+STORES = """import taichi as ti
+W, H = 40, 30
+u = ti.field(dtype=float, shape=(W, H))
+v = ti.field(dtype=float, shape=(W, H))
+code = ti.field(dtype=int, shape=(W, H))
+@ti.kernel
+def interior():
+    for i, j in ti.ndrange((1, W - 1), (1, H - 1)):
+        v[i, j] = 0.25 * (u[i - 1, j] + u[i + 1, j] + u[i, j - 1] + u[i, j + 1])
+@ti.kernel
+def boundary():
+    for i in range(W):
+        v[i, 0] = 1.0
+        v[i, H - 1] = -1.0
+        code[i, (i * 7) % H] = i * 2.5
+@ti.kernel
+def transpose_into():
+    for i, j in ti.ndrange(30, 40):
+        v[j, i] = u[j, i] * 2.0
+        if u[j, i] > 0.5:
+            code[j, i] = -3
+"""
+
+
+def test_stores_at_computed_indices():
+    """An interior ti.ndrange((1, W - 1), ...) stencil, boundary rows written from a 1-D loop (an
+    int field storing a truncated float), and a transposed loop with a store inside an if: every
+    store lands where numpy's assignment puts it, nothing else changes."""
+    rng = np.random.default_rng(21)
+    u = rng.random((40, 30)).astype(f32)
+    v0 = rng.random((40, 30)).astype(f32)
+    c0 = rng.integers(-9, 9, (40, 30)).astype(np.int32)
+    arr = {"u": u, "v": v0.copy(), "code": c0.copy()}
+    want_v, want_c = v0.copy(), c0.copy()
+    low, names = lower_named(STORES, "interior", {})
+    assert low.field is None and low.grid == (38, 28)
+    run_ops(low, names, arr)
+    want_v[1:-1, 1:-1] = f32(0.25) * (((u[:-2, 1:-1] + u[2:, 1:-1]) + u[1:-1, :-2]) + u[1:-1, 2:])
+    assert np.array_equal(arr["v"], want_v)
+    low, names = lower_named(STORES, "boundary", {})
+    run_ops(low, names, arr)
+    i = np.arange(40)
+    want_v[:, 0], want_v[:, -1] = 1.0, -1.0
+    want_c[i, (i * 7) % 30] = np.trunc(i * 2.5).astype(np.int32)
+    assert np.array_equal(arr["v"], want_v) and np.array_equal(arr["code"], want_c)
+    low, names = lower_named(STORES, "transpose_into", {})
+    run_ops(low, names, arr)
+    want_v = u * f32(2.0)
+    want_c = np.where(u > f32(0.5), np.int32(-3), want_c)
+    assert np.array_equal(arr["v"], want_v) and np.array_equal(arr["code"], want_c)
+
+
+def test_oracle_store_at_drops_outside_and_keeps_the_rest():
+    b = pp.Builder()
+    e = b.scatter_add(1, b.load(0, 0), b.load(0, 1), b.load(0, 2), op="store")
+    prog = pp.compile_program(b, out=None, effects=[e], in_widths=[3, 1], in_extents=[None, (4, 5)])
+    pts = np.array([[[0, 0, 1.5], [3, 4, 2.5], [4, 0, 9.0], [-1, 2, 9.0], [2, np.nan, 9.0], [1.7, 2.2, 3.5]]], f32)
+    t = np.full((4, 5), -1.0, f32)
+    oracle.pixel_program(prog, 1, 6, [pts, t])
+    want = np.full((4, 5), -1.0, f32)
+    want[0, 0], want[3, 4], want[1, 2] = 1.5, 2.5, 3.5
+    assert np.array_equal(t, want)

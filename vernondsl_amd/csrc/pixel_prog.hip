@@ -24,8 +24,8 @@ namespace {
 
 JitCounters g_pix_jit;
 
-bool scatter_op(int op) {
-  return op == VDSL_PIX_ATOMIC_ADD || op == VDSL_PIX_ATOMIC_MAX || op == VDSL_PIX_ATOMIC_MIN;
+bool scatter_op(int op) {  // an instruction with an effect and no result register
+  return op == VDSL_PIX_ATOMIC_ADD || op == VDSL_PIX_ATOMIC_MAX || op == VDSL_PIX_ATOMIC_MIN || op == VDSL_PIX_STORE_AT;
 }
 
 int check_program(const vdsl_pixel_program& p, int n_inputs) {
@@ -59,7 +59,7 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
     const vdsl_map_instr& s = p.code[pc];
     const std::string at = "pixel program: instruction " + std::to_string(pc);
     const bool map_op = s.op >= VDSL_MAP_LOAD && s.op <= VDSL_MAP_ADD_IMM;
-    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_ATOMIC_MIN;
+    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_STORE_AT;
     if (!map_op && !pix_op) return fail(VDSL_ERR_INVALID_ARG, at + ": unknown opcode " + std::to_string(s.op));
     if (s.dst >= VDSL_PIX_MAX_REGS || s.b >= VDSL_PIX_MAX_REGS || s.c >= VDSL_PIX_MAX_REGS)
       return fail(VDSL_ERR_INVALID_ARG, at + ": register out of range");
@@ -112,7 +112,8 @@ int privatized(const vdsl_pixel_program& p, const std::vector<char>& flags, int 
     for (int pc = 0; pc < total; ++pc) {
       if (p.code[pc].a != t) continue;
       per_pixel |= p.code[pc].op == VDSL_PIX_ATOMIC_ADD && !(flags[pc] & 4);
-      other |= p.code[pc].op == VDSL_PIX_ATOMIC_MAX || p.code[pc].op == VDSL_PIX_ATOMIC_MIN;
+      other |= p.code[pc].op == VDSL_PIX_ATOMIC_MAX || p.code[pc].op == VDSL_PIX_ATOMIC_MIN ||
+               p.code[pc].op == VDSL_PIX_STORE_AT;
     }
     per_pixel &= !other;
     const int64_t elems = static_cast<int64_t>(p.in_rows[t] ? p.in_rows[t] : ni) * (p.in_cols[t] ? p.in_cols[t] : nj) *
@@ -141,7 +142,8 @@ int rows_per_block(const vdsl_pixel_program& p, const std::vector<char>& flags, 
   bool gathers = false, reduction = p.out_kind == VDSL_PIX_OUT_NONE;
   for (int pc = 0; pc < total; ++pc) {
     gathers |= p.code[pc].op == VDSL_PIX_LOAD_AT;
-    if (scatter_op(p.code[pc].op) && !(flags[pc] & 4) && !priv[p.code[pc].a]) reduction = false;
+    if (scatter_op(p.code[pc].op) && ((!(flags[pc] & 4) && !priv[p.code[pc].a]) || p.code[pc].op == VDSL_PIX_STORE_AT))
+      reduction = false;
   }
   return reduction ? 64 : gathers ? 8 : 4;
 }
@@ -164,7 +166,7 @@ int reads(int op) {
     case VDSL_MAP_ADD: case VDSL_MAP_SUB: case VDSL_MAP_MUL: case VDSL_MAP_DIV: case VDSL_MAP_MAX: case VDSL_MAP_MIN:
     case VDSL_PIX_LT: case VDSL_PIX_LE: case VDSL_PIX_EQ: case VDSL_PIX_NE: return 3;  // a, b
     case VDSL_MAP_FMA: case VDSL_PIX_SELECT: return 7;  // a, b, c
-    case VDSL_PIX_ATOMIC_ADD: case VDSL_PIX_ATOMIC_MAX: case VDSL_PIX_ATOMIC_MIN:
+    case VDSL_PIX_ATOMIC_ADD: case VDSL_PIX_ATOMIC_MAX: case VDSL_PIX_ATOMIC_MIN: case VDSL_PIX_STORE_AT:
       return 6;  // b, c (and the value r[dst]; no register written)
     default: return 1;  // a
   }

@@ -74,10 +74,12 @@ __device__ __forceinline__ unsigned pix_index(float x, int n) {
 }
 
 
-// Scatter-adds and their max / min forms: instructions with an effect and no result register.
+// Scatter-adds and their max / min forms, combined where indices agree; with the stores at
+// computed indices, the instructions that have an effect and no result register.
 __device__ constexpr bool pix_scatter_op(int op) {
   return op == VDSL_PIX_ATOMIC_ADD || op == VDSL_PIX_ATOMIC_MAX || op == VDSL_PIX_ATOMIC_MIN;
 }
+__device__ constexpr bool pix_effect_op(int op) { return pix_scatter_op(op) || op == VDSL_PIX_STORE_AT; }
 
 // A register stored to an int32 field: truncation toward zero, NaN -> 0, saturating.
 __device__ __forceinline__ int pix_to_i32(float x) {
@@ -334,7 +336,17 @@ template <class P, int PC>
 __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
                                          float fi, float fj, float fcount, int ni, int nj, bool act, PixAcc<P>& acc) {
   constexpr vdsl_map_instr s = P::code[PC];
-  if constexpr (pix_scatter_op(s.op) && s.ext[2] != 0) {
+  if constexpr (s.op == VDSL_PIX_STORE_AT) {
+    bool ok;
+    const PixOff<P> e = pix_target<P, s.a>(in, r[s.b], r[s.c], ok);
+    if (act && ok) {
+      char* base = const_cast<char*>(reinterpret_cast<const char*>(in.p[s.a]));
+      if constexpr (P::in_dtypes[s.a] == VDSL_I32)
+        reinterpret_cast<int*>(base)[e] = pix_to_i32(r[s.dst]);
+      else
+        reinterpret_cast<float*>(base)[e * static_cast<PixOff<P>>(P::in_widths[s.a]) + static_cast<PixOff<P>>(rt.imm[PC])] = r[s.dst];
+    }
+  } else if constexpr (pix_scatter_op(s.op) && s.ext[2] != 0) {
     pix_accumulate<P, PC>(acc, r[s.b], r[s.c], r[s.dst], act);  // constant indices: combined per block
   } else if constexpr (pix_scatter_op(s.op)) {
     // one add (max, min) per wave where both indices are the same on every lane (found
@@ -405,15 +417,15 @@ __device__ constexpr uint32_t pix_reads(const vdsl_map_instr& s) {
       return (1u << s.a) | (1u << s.b);
     case VDSL_PIX_LOAD_AT: return (1u << s.b) | (1u << s.c);
     case VDSL_MAP_FMA: case VDSL_PIX_SELECT: return (1u << s.a) | (1u << s.b) | (1u << s.c);
-    case VDSL_PIX_ATOMIC_ADD: case VDSL_PIX_ATOMIC_MAX: case VDSL_PIX_ATOMIC_MIN:
+    case VDSL_PIX_ATOMIC_ADD: case VDSL_PIX_ATOMIC_MAX: case VDSL_PIX_ATOMIC_MIN: case VDSL_PIX_STORE_AT:
       return (1u << s.dst) | (1u << s.b) | (1u << s.c);  // the value is r[dst]
     default: return 1u << s.a;
   }
 }
 
-// Register an instruction writes (a bit); a scatter-add (or max, min) writes none.
+// Register an instruction writes (a bit); an effect (scatter-add, max, min, store) writes none.
 __device__ constexpr uint32_t pix_writes(const vdsl_map_instr& s) {
-  return pix_scatter_op(s.op) ? 0u : 1u << s.dst;
+  return pix_effect_op(s.op) ? 0u : 1u << s.dst;
 }
 
 // Register sets of program P (instructions [lo, hi) of its table): written, and read before

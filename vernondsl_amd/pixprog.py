@@ -26,8 +26,9 @@ from . import _lib
 MAX_INSTR, MAX_REGS, MAX_INPUTS = 256, 32, 8
 OP = dict(_lib.MAP_OPS)
 OP.update({"index": 32, "cos": 33, "sin": 34, "count": 35, "lt": 36, "le": 37, "eq": 38, "ne": 39, "select": 40,
-           "floor": 41, "load_at": 42, "trip": 43, "atomic_add": 44, "trunc": 45, "atomic_max": 46, "atomic_min": 47})
-SCATTERS = ("atomic_add", "atomic_max", "atomic_min")  # effect nodes: no result register
+           "floor": 41, "load_at": 42, "trip": 43, "atomic_add": 44, "trunc": 45, "atomic_max": 46, "atomic_min": 47,
+           "store_at": 48})
+SCATTERS = ("atomic_add", "atomic_max", "atomic_min", "store_at")  # effect nodes: no result register
 TESTS = {"none": 0, "lt": 1, "le": 2, "gt": 3, "ge": 4}
 OUT_REG, OUT_COUNT, OUT_I32, OUT_NONE = 0, 1, 2, 3
 F32, I32 = _lib.F32, _lib.I32  # input dtypes (vdsl_dtype)
@@ -120,7 +121,7 @@ class Builder:
         """The effect `input k [row][col] (component) += value` (an atomic add; op "max" / "min":
         the element becomes the max / min of itself and value; dropped where the indices fall
         outside field k), for compile_program(effects=...)."""
-        if op not in ("add", "max", "min"):
+        if op not in ("add", "max", "min", "store"):
             raise ProgramError(f"unknown scatter op {op!r}")
         if not 0 <= k < MAX_INPUTS:
             raise ProgramError(f"at most {MAX_INPUTS} input fields")
@@ -129,7 +130,7 @@ class Builder:
         args = tuple(a if isinstance(a, Node) else self.const(a) for a in (row, col, value))
         # never merged with an equal one: two equal adds in a body are two adds
         self._effects = getattr(self, "_effects", 0) + 1
-        return self._node("atomic_" + op, args, val=(int(k), int(component), self._effects))
+        return self._node("store_at" if op == "store" else "atomic_" + op, args, val=(int(k), int(component), self._effects))
 
     def state(self, name: str) -> Node:
         return self._node("state", val=name)
@@ -446,8 +447,8 @@ def describe(p: PixelProgram) -> str:
     for k in range(total):
         s = p.code[k]
         sec = "pre" if k < p.n_pre else "test" if k < p.n_pre + p.n_test else "body" if k < p.n_pre + p.n_test + p.n_body else "post"
-        if s.op in (OP["atomic_add"], OP["atomic_max"], OP["atomic_min"]):
-            sym = {OP["atomic_add"]: "+=", OP["atomic_max"]: "max=", OP["atomic_min"]: "min="}[s.op]
+        if s.op in (OP["atomic_add"], OP["atomic_max"], OP["atomic_min"], OP["store_at"]):
+            sym = {OP["atomic_add"]: "+=", OP["atomic_max"]: "max=", OP["atomic_min"]: "min=", OP["store_at"]: "="}[s.op]
             lines.append(f"{sec:4s} input{s.a}[r{s.b}][r{s.c}].{int(s.imm)} {sym} r{s.dst}")
             continue
         lines.append(f"{sec:4s} r{s.dst} = {names.get(s.op, s.op)} a={s.a} b={s.b} c={s.c} imm={s.imm:g}")

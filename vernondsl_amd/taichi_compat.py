@@ -44,7 +44,8 @@ added into as `s[None]`.  `F[idx] += v` / `-= v` at an index other than the loop
 add: a scatter-add of the program,
 dropped where an index falls outside F, with idx a tuple or a vector expression such as
 `base + offset` (`.cast(int)` / `int()` truncate); a field added into is neither read nor stored
-by the same struct-for, and adds inside an if happen only where the branch runs.  `ti.Matrix`
+by the same struct-for, and adds inside an if happen only where the branch runs.  `F[idx] = v` at
+another index is a plain store there (with ti.ndrange((a, b), ...) interiors and boundary loops).  `ti.Matrix`
 values (`@`, `outer_product`, `trace`, `determinant`, `transpose`) and 2 x 2 matrix fields lower
 to their scalar operations; `for I in ti.grouped(F)` binds I to the index vector.  A lowering called again with the same arguments is replayed as one
 recorded hipGraph.  What neither path lowers raises
@@ -1882,10 +1883,11 @@ class _PixInterp:
         if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Subscript):
             tgt = st.targets[0]
             target = self.expr(tgt.value, local)
-            if not (isinstance(target, Field) and target.shape == self.shape):
-                raise TaichiLoweringError("the body may only store to fields of the struct-for's shape")
-            if not self._is_here(tgt.slice):
-                raise TaichiLoweringError(f"the store must write field[{', '.join(self.names)}]")
+            if not isinstance(target, Field):
+                raise TaichiLoweringError("the body stores to fields (field[...] = v)")
+            if not self._at_here(target, tgt.slice):  # another element: a store at computed indices
+                self.scatter(target, tgt.slice, self.expr(st.value, local), local, op="store")
+                return True
             self.store_here(target, self.expr(st.value, local), local)
             return True
         if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Name):
@@ -2022,14 +2024,26 @@ def _struct_for(fdef: ast.FunctionDef, funcs, env, unroll=True):
     it = loop.iter
     fname = it.func.attr if isinstance(it, ast.Call) and isinstance(it.func, ast.Attribute) else \
         it.func.id if isinstance(it, ast.Call) and isinstance(it.func, ast.Name) else None
-    if fname in ("ndrange", "range"):  # ti.ndrange(W, H) / ti.ndrange(N), or a top-level range(N)
-        shape = tuple(it0.expr(a, {}) for a in it.args)
-        if (fname == "range" and len(it.args) != 1) or len(shape) != dims or \
-                not all(isinstance(v, (int, np.integer)) and v >= 0 for v in shape):
-            raise TaichiLoweringError(f"the loop needs {dims} non-negative integer extent(s) for its {dims} "
-                                      "index(es): ti.ndrange(W, H), ti.ndrange(N) or range(N)")
+    offsets = (0,) * dims
+    if fname in ("ndrange", "range"):  # ti.ndrange(W, H) / ti.ndrange((a, b), ...) / range(N) / range(A, B)
+        vals = [it0.expr(a, {}) for a in it.args]
+        if fname == "range":
+            vals = [vals] if len(vals) == 2 else vals
+        bounds = []
+        for v in vals:
+            if isinstance(v, (int, np.integer)) and not isinstance(v, bool):
+                bounds.append((0, int(v)))
+            elif isinstance(v, (list, tuple)) and len(v) == 2 and all(isinstance(x, (int, np.integer)) for x in v):
+                bounds.append((int(v[0]), int(v[1])))
+            else:
+                bounds = None
+                break
+        if bounds is None or len(bounds) != dims or (fname == "range" and len(it.args) not in (1, 2)):
+            raise TaichiLoweringError(f"the loop needs {dims} integer extent(s) for its {dims} index(es): "
+                                      "ti.ndrange(W, H), ti.ndrange((a, b), (c, d)), range(N) or range(A, B)")
         ip = _PixInterp(env, funcs, b, None, iname, jname, kname)
-        ip.shape = tuple(int(v) for v in shape)
+        ip.shape = tuple(max(hi - lo, 0) for lo, hi in bounds)
+        offsets = tuple(lo for lo, _ in bounds)
     else:
         fld = it0.expr(it, {})
         if not isinstance(fld, Field) or len(fld.shape) != dims:
@@ -2052,6 +2066,9 @@ def _struct_for(fdef: ast.FunctionDef, funcs, env, unroll=True):
         local = {iname: b.index(0), jname: b.index(1)} if dims == 2 else {iname: b.index(1)}
         for nm, ext in zip(ip.names, shape):
             ip.ibound[id(local[nm])] = max(int(ext) - 1, 0)
+    for nm, lo in zip(ip.names, offsets):  # ti.ndrange((a, b), ...): the index runs from a
+        if lo:
+            local[nm] = ip.arith("add", local[nm], lo)
     stmts = [s for s in loop.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant)) and not isinstance(s, ast.Pass)]
     return loop, ip, b, local, stmts
 
