@@ -455,3 +455,46 @@ def test_stores_at_computed_indices_on_the_device(dev, q):
     finally:
         for t in ts.values():
             t.free()
+
+
+_RX = tc.field(dtype=float, shape=(64, 48))
+_RV = tc.Vector.field(2, dtype=float, shape=1000)
+
+
+@tc.kernel
+def _energy() -> float:
+    e = 0.0
+    for i in _RV:
+        e += 0.5 * _RV[i].norm_sqr()
+    for i, j in _RX:
+        e -= _RX[i, j]
+    return e
+
+
+@tc.kernel
+def _count(t: float) -> int:
+    n = 0
+    for i, j in _RX:
+        if _RX[i, j] > t:
+            n += 1
+    return n
+
+
+def test_kernel_scope_reductions_return_values(dev, q):
+    """A kernel returning a kernel-scope sum: the device's value within the any-order bound of
+    the f32 sum, an int32 count exactly; called again (the graph-replayed form from the second
+    call) the accumulators start from their initial values each time."""
+    tc.init(arch=tc.gpu)
+    rng = np.random.default_rng(23)
+    X = rng.random((64, 48)).astype(f32)
+    V = rng.standard_normal((1000, 2)).astype(f32)
+    _RX.from_numpy(X)
+    _RV.from_numpy(V)
+    terms = np.concatenate([(f32(0.5) * (V[:, 0] * V[:, 0] + V[:, 1] * V[:, 1])).astype(np.float64), -X.ravel().astype(np.float64)])
+    exact = float(terms.sum())
+    for _ in range(4):
+        e = _energy()
+        assert isinstance(e, float) and abs(e - exact) <= 2 * terms.size * U * float(np.abs(terms).sum())
+        n = _count(0.25)
+        assert n == int((X > f32(0.25)).sum())
+    assert _energy.lower().graph and _count.lower(0.25).graph

@@ -529,3 +529,54 @@ def test_oracle_store_at_drops_outside_and_keeps_the_rest():
     want = np.full((4, 5), -1.0, f32)
     want[0, 0], want[3, 4], want[1, 2] = 1.5, 2.5, 3.5
     assert np.array_equal(t, want)
+
+
+# ---- kernel-scope reductions: `e = 0.0; for ...: e += ...; return e` --------------------------------
+REDUCE = """import taichi as ti
+x = ti.field(dtype=float, shape=(50, 40))
+v = ti.Vector.field(2, dtype=float, shape=300)
+@ti.kernel
+def energy() -> float:
+    e = 0.0
+    n = 0
+    for i in v:
+        e += 0.5 * v[i].norm_sqr()
+    for i, j in x:
+        if x[i, j] > 0.5:
+            n += 1
+        e -= x[i, j]
+    return e
+"""
+
+
+def test_kernel_scope_reductions_on_the_oracle():
+    """Each kernel-scope scalar is a hidden 0-D field: its initial value stored, the loops' += / -=
+    added at a constant index, the returned one named by Lowered.ret; the oracle's sums (pixel by
+    pixel) equal numpy's sequential f32 sums."""
+    low, names = lower_named(REDUCE, "energy", {})
+    assert low.ret is not None and low.ret.shape == () and low.ret.dtype == tc.f32
+    rng = np.random.default_rng(2)
+    X = rng.random((50, 40)).astype(f32)
+    V = rng.standard_normal((300, 2)).astype(f32)
+    arrays = {"x": X, "v": V}
+    for op in low.ops():
+        for f in op.inputs + ([op.field] if op.field is not None else []):
+            if id(f) not in names:  # the hidden accumulators
+                names[id(f)] = f"acc{len(names)}"
+                arrays[names[id(f)]] = np.zeros((), np.int32 if f.dtype == tc.i32 else f32)
+    run_ops(low, names, arrays)
+    e = f32(0.0)
+    for a, c in V:
+        e = e + f32(0.5) * (a * a + c * c)
+    for xv in X.ravel():
+        e = e + (-xv)
+    got = {a.dtype.kind: a for k, a in arrays.items() if k.startswith("acc")}
+    assert float(got["f"]) == float(e) and int(got["i"]) == int((X > f32(0.5)).sum())
+
+
+def test_kernel_scope_forms_refused():
+    for body, msg in (("    e = 0.0\n    for i in v:\n        e += 1.0\n    e = e * 2.0\n    return e", "kernel body"),
+                      ("    e = x[0, 0]\n    for i in v:\n        e += 1.0\n    return e", "constant")):
+        text = REDUCE.split("@ti.kernel")[0] + "@ti.kernel\ndef bad() -> float:\n" + body + "\n"
+        with pytest.raises(tc.TaichiLoweringError, match=msg):
+            lower_named(text, "bad", {})

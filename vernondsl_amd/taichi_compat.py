@@ -45,7 +45,9 @@ add: a scatter-add of the program,
 dropped where an index falls outside F, with idx a tuple or a vector expression such as
 `base + offset` (`.cast(int)` / `int()` truncate); a field added into is neither read nor stored
 by the same struct-for, and adds inside an if happen only where the branch runs.  `F[idx] = v` at
-another index is a plain store there (with ti.ndrange((a, b), ...) interiors and boundary loops).  `ti.Matrix`
+another index is a plain store there (with ti.ndrange((a, b), ...) interiors and boundary loops).
+Kernel-scope scalars set to constants before the struct-fors and `+=` / `-=` in them are Taichi's
+reductions; `return name` returns one from the call.  `ti.Matrix`
 values (`@`, `outer_product`, `trace`, `determinant`, `transpose`) and 2 x 2 matrix fields lower
 to their scalar operations; `for I in ti.grouped(F)` binds I to the index vector.  A lowering called again with the same arguments is replayed as one
 recorded hipGraph.  What neither path lowers raises
@@ -323,7 +325,7 @@ class Kernel:
         graph = getattr(low, "graph", None)
         if graph:
             graph.launch(q)
-            return
+            return self._result(low)
         self._launch(low, q)
         low.calls = getattr(low, "calls", 0) + 1
         if graph is None and low.calls >= self.GRAPH_AFTER and os.environ.get("VDSL_TI_GRAPHS", "1") != "0":
@@ -334,6 +336,16 @@ class Kernel:
                 low.graph = rec.graph
             except Exception:  # an op that cannot be recorded: this lowering stays eager
                 low.graph = False
+        return self._result(low)
+
+    @staticmethod
+    def _result(low):
+        """The value `return name` names (its hidden 0-D field, read back), or None."""
+        ret = getattr(low, "ret", None)
+        if ret is None:
+            return None
+        v = ret.to_numpy()[()]
+        return int(v) if ret.dtype == i32 else float(v)
 
     @staticmethod
     def _launch(low, q):
@@ -871,6 +883,8 @@ def lower_kernel(fdef: ast.FunctionDef, funcs, env, general: bool = False) -> Lo
     kernel; not when general), else the general per-pixel program(s); TaichiLoweringError when
     neither lowers one."""
     body = [s for s in fdef.body if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant))]
+    if any(not isinstance(s, ast.For) for s in body) and len(body) > 1:
+        return _lower_with_reducers(fdef, body, funcs, env, general)
     if len(body) > 1 and all(isinstance(s, ast.For) for s in body):
         parts = []
         for loop in body:
@@ -888,6 +902,66 @@ def lower_kernel(fdef: ast.FunctionDef, funcs, env, general: bool = False) -> Lo
             return lower_pixel_program(fdef, funcs, env)
         except TaichiLoweringError as e2:
             raise TaichiLoweringError(f"{e2} (and not of the escape-time form: {e1})") from None
+
+
+def _lower_with_reducers(fdef, body, funcs, env, general):
+    """A kernel body with kernel-scope scalars around its struct-fors, Taichi's reduction idiom:
+
+        e = 0.0
+        for i in x:
+            e += f(x[i])          (+= / -= only: Taichi makes them atomic adds)
+        return e
+
+    Each such scalar becomes a hidden 0-D field: one store of its initial value, then
+    scatter-adds at a constant index (summed per block), and `return` names the field whose
+    value the call returns (Lowered.ret)."""
+    env2 = dict(env)
+    fields, loops, ret = {}, [], None
+    interp = _PixInterp(env, funcs, None, None, "_", None)
+
+    class Use(ast.NodeTransformer):  # a kernel-scope name inside a loop: its hidden field's element
+        def visit_Name(self, nd):
+            if nd.id in fields:
+                return ast.copy_location(ast.Subscript(value=ast.Name(id=fields[nd.id][0], ctx=ast.Load()),
+                                                       slice=ast.Constant(value=None), ctx=nd.ctx), nd)
+            return nd
+
+    for k, st in enumerate(body):
+        if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Name) \
+                and not any(isinstance(s2, ast.For) for s2 in body[:k]):
+            try:
+                v = interp.expr(st.value, {})
+            except (TaichiLoweringError, TypeError, AttributeError):
+                v = None
+            if not _is_num(v):
+                raise TaichiLoweringError("a kernel-scope variable starts from a constant")
+            nm = st.targets[0].id
+            hidden = f"__vdsl_red_{nm}"
+            fld = Field(i32 if isinstance(v, (int, np.integer)) and not isinstance(v, bool) else f32, ())
+            env2[hidden] = fld
+            fields[nm] = (hidden, fld)
+            init = ast.For(target=ast.Name(id="__vdsl_r", ctx=ast.Store()), iter=ast.Call(
+                func=ast.Name(id="range", ctx=ast.Load()), args=[ast.Constant(value=1)], keywords=[]), orelse=[],
+                lineno=0, body=[ast.Assign(targets=[ast.Subscript(value=ast.Name(id=hidden, ctx=ast.Load()),
+                                                                  slice=ast.Constant(value=None), ctx=ast.Store())],
+                                           value=ast.Constant(value=v.item() if hasattr(v, "item") else v), lineno=0)])
+            loops.append(init)
+        elif isinstance(st, ast.For):
+            loops.append(Use().visit(copy.deepcopy(st)))
+        elif isinstance(st, ast.Return) and st is body[-1] and isinstance(st.value, ast.Name) and st.value.id in fields:
+            ret = fields[st.value.id][1]
+        else:
+            raise TaichiLoweringError(f"statement at line {getattr(st, 'lineno', '?')} of the kernel body: a kernel holds "
+                                      "struct-fors, kernel-scope scalars set to constants before them, and `return name`")
+    if not loops:
+        raise TaichiLoweringError("the kernel has no struct-for")
+    parts = []
+    for loop in loops:
+        sub = ast.FunctionDef(name=fdef.name, args=fdef.args, body=[loop], decorator_list=[], returns=None, type_comment=None)
+        parts.append(lower_kernel(sub, funcs, env2, general))
+    low = Lowered("sequence", parts[0].field, parts=parts)
+    low.ret = ret
+    return low
 
 
 class _PVec:
