@@ -42,7 +42,7 @@ extern "C" {
  * and in_cols (inputs of another shape than the grid); 6: VDSL_PIX_ATOMIC_ADD,
  * VDSL_PIX_OUT_NONE (scatter-adds) and VDSL_PIX_TRUNC (struct layouts unchanged since 5); 7:
  * VDSL_PIX_MAX_INSTR 256 and VDSL_PIX_MAX_INPUTS 8 (vdsl_pixel_program's arrays grow),
- * VDSL_PIX_ATOMIC_MAX / MIN and VDSL_PIX_STORE_AT. */
+ * VDSL_PIX_ATOMIC_MAX / MIN, VDSL_PIX_STORE_AT and VDSL_PIX_RANDOM. */
 #define VDSL_ABI_VERSION 7
 
 typedef enum vdsl_status {
@@ -362,7 +362,12 @@ typedef enum vdsl_pix_opcode {
    * converted as VDSL_PIX_OUT_I32 stores it) with the operands, extents, drops and refusals of
    * VDSL_PIX_ATOMIC_ADD; where several pixels store to one element, one of them wins, in no fixed
    * order (a race in Taichi too). */
-  VDSL_PIX_STORE_AT = 48
+  VDSL_PIX_STORE_AT = 48,
+  /* r[dst] = a uniform number in [0, 1) (Taichi's ti.random()): h = H(H(H(s) ^ d) ^ (i nj + j)), with
+   * s = (uint32)r[a] (a seed, an integer below 2^24 held as a float), d = (uint32)imm (which
+   * draw of the pixel), H Chris Wellons' lowbias32 integer hash (x ^= x >> 16; x *= 0x7feb352d;
+   * x ^= x >> 15; x *= 0x846ca68b; x ^= x >> 16), and the result (h >> 8) * 2^-24, exact in f32. */
+  VDSL_PIX_RANDOM = 49
 } vdsl_pix_opcode;
 
 typedef enum vdsl_pix_test {

@@ -218,6 +218,21 @@ static int32_t pix_to_i32(float x) {
   return (int32_t)x;
 }
 
+/* VDSL_PIX_RANDOM: Chris Wellons' lowbias32 hash of the seed, the draw and the pixel. */
+static uint32_t pix_hash(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+static float pix_random(float seed, uint32_t draw, uint32_t pixel) {
+  const uint32_t s = seed >= 0.0f && seed < 16777216.0f ? (uint32_t)seed : 0u;
+  return (float)(pix_hash(pix_hash(pix_hash(s) ^ draw) ^ pixel) >> 8) * 0x1p-24f;
+}
+
 static float pix_apply(const vdsl_pixel_program* p, const vdsl_map_instr* s, const float* reg, const void* const* inputs,
                        int64_t o, int64_t i, int64_t j, int count, int64_t ni, int64_t nj) {
   switch (s->op) {
@@ -236,6 +251,7 @@ static float pix_apply(const vdsl_pixel_program* p, const vdsl_map_instr* s, con
     case VDSL_PIX_NE: return reg[s->a] != reg[s->b] ? 1.0f : 0.0f;
     case VDSL_PIX_SELECT: return reg[s->a] != 0.0f ? reg[s->b] : reg[s->c];
     case VDSL_PIX_FLOOR: return floorf(reg[s->a]);
+    case VDSL_PIX_RANDOM: return pix_random(reg[s->a], (uint32_t)s->imm, (uint32_t)(i * nj + j));
     case VDSL_PIX_TRUNC: return truncf(reg[s->a]);
     default: return map_apply(s->op, reg[s->a], reg[s->b], reg[s->c], s->imm);
   }

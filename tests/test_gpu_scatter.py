@@ -498,3 +498,37 @@ def test_kernel_scope_reductions_return_values(dev, q):
         n = _count(0.25)
         assert n == int((X > f32(0.25)).sum())
     assert _energy.lower().graph and _count.lower(0.25).graph
+
+
+_RP = tc.Vector.field(2, dtype=float, shape=4096)
+
+
+@tc.kernel
+def _scatter_points():
+    for i in _RP:
+        _RP[i] = [ti_random_pair() * 2.0, tc.random()]
+
+
+@tc.func
+def ti_random_pair():
+    return tc.random()
+
+
+def test_random_numbers_on_the_device(dev, q):
+    """ti.random on the device equals the oracle's numbers for the same generator state, bit for
+    bit; every call (eager, then graph replays) advances the state, so the numbers change."""
+    from test_taichi_scatter import RANDOM
+    low, names = lower_named(RANDOM, "seed", {})
+    prog = low.program
+    state = np.array([[123]], np.int32)
+    got, _ = run_scatter(dev, q, prog, [state], 1, 5000, out_shape=(1, 5000, 2))
+    assert np.array_equal(got.reshape(5000, 2), oracle.pixel_program(prog, 1, 5000, [state]).reshape(5000, 2))
+    tc.init(arch=tc.gpu)
+    seen = []
+    for _ in range(4):
+        _scatter_points()
+        a = _RP.to_numpy()
+        assert 0.0 <= a[:, 1].min() and a[:, 1].max() < 1.0 and 0.0 <= a[:, 0].min() and a[:, 0].max() < 2.0
+        assert all(not np.array_equal(a, b) for b in seen)
+        seen.append(a)
+    assert _scatter_points.lower().graph

@@ -580,3 +580,44 @@ def test_kernel_scope_forms_refused():
         text = REDUCE.split("@ti.kernel")[0] + "@ti.kernel\ndef bad() -> float:\n" + body + "\n"
         with pytest.raises(tc.TaichiLoweringError, match=msg):
             lower_named(text, "bad", {})
+
+
+# ---- ti.random ----------------------------------------------------------------------------------
+def lowbias32(x):
+    """Chris Wellons' lowbias32 integer hash, in numpy uint32 arithmetic."""
+    x = np.atleast_1d(np.asarray(x, np.uint32))
+    with np.errstate(over="ignore"):  # the multiplies wrap modulo 2^32, as the hash means them to
+        x = x ^ (x >> np.uint32(16))
+        x = x * np.uint32(0x7feb352d)
+        x = x ^ (x >> np.uint32(15))
+        x = x * np.uint32(0x846ca68b)
+        x = x ^ (x >> np.uint32(16))
+    return x
+
+
+RANDOM = """import taichi as ti
+p = ti.Vector.field(2, dtype=float, shape=5000)
+@ti.kernel
+def seed():
+    for i in p:
+        p[i] = [ti.random() * 0.4 + 0.2, ti.random(float)]
+"""
+
+
+def test_random_numbers_on_the_oracle():
+    """Each ti.random() call site is a draw of its own: the oracle's numbers equal the hash
+    restated in numpy (seed, draw, pixel), lie in [0, 1), and look uniform and independent."""
+    low, names = lower_named(RANDOM, "seed", {})
+    prog = low.program
+    draws = [int(prog.code[k].imm) for k in range(prog.n_pre + prog.n_post) if prog.code[k].op == pp.OP["random"]]
+    assert len(draws) == 2 and draws[0] != draws[1]
+    names[id(tc._rng_state())] = "rng"
+    for seed in (0, 7):
+        arr = {"p": np.zeros((5000, 2), f32), "rng": np.array(seed, np.int32)}
+        run_ops(low, names, arr)
+        pix = np.arange(5000, dtype=np.uint32)
+        u = [(lowbias32(lowbias32(lowbias32(seed) ^ np.uint32(d)) ^ pix) >> np.uint32(8)).astype(f32) * f32(2.0 ** -24)
+             for d in draws]
+        assert np.array_equal(arr["p"][:, 0], u[0] * f32(0.4) + f32(0.2)) and np.array_equal(arr["p"][:, 1], u[1])
+        assert 0.0 <= u[1].min() and u[1].max() < 1.0 and abs(float(u[1].mean()) - 0.5) < 0.02
+        assert abs(float(np.corrcoef(u[0], u[1])[0, 1])) < 0.05

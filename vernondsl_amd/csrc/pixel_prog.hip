@@ -59,7 +59,7 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
     const vdsl_map_instr& s = p.code[pc];
     const std::string at = "pixel program: instruction " + std::to_string(pc);
     const bool map_op = s.op >= VDSL_MAP_LOAD && s.op <= VDSL_MAP_ADD_IMM;
-    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_STORE_AT;
+    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_RANDOM;
     if (!map_op && !pix_op) return fail(VDSL_ERR_INVALID_ARG, at + ": unknown opcode " + std::to_string(s.op));
     if (s.dst >= VDSL_PIX_MAX_REGS || s.b >= VDSL_PIX_MAX_REGS || s.c >= VDSL_PIX_MAX_REGS)
       return fail(VDSL_ERR_INVALID_ARG, at + ": register out of range");
@@ -197,7 +197,7 @@ std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
     }
     const bool in_cst = (!(rd & 1) || cst[s.a]) && (!(rd & 2) || cst[s.b]) && (!(rd & 4) || cst[s.c]);
     const bool var = s.op == VDSL_MAP_LOAD || s.op == VDSL_PIX_LOAD_AT || s.op == VDSL_PIX_INDEX ||
-                     s.op == VDSL_PIX_COUNT || s.op == VDSL_PIX_TRIP;
+                     s.op == VDSL_PIX_COUNT || s.op == VDSL_PIX_TRIP || s.op == VDSL_PIX_RANDOM;
     cst[s.dst] = !var && in_cst;
   };
   auto step = [&](int pc, bool* st) {
@@ -210,7 +210,7 @@ std::vector<char> row_uniform_gathers(const vdsl_pixel_program& p) {
     bool out;
     if (s.op == VDSL_MAP_CONST || s.op == VDSL_PIX_TRIP) out = true;  // the trip is the same on every lane
     else if (s.op == VDSL_PIX_INDEX) out = s.a == 0;
-    else if (s.op == VDSL_MAP_LOAD || s.op == VDSL_PIX_LOAD_AT || s.op == VDSL_PIX_COUNT) out = false;
+    else if (s.op == VDSL_MAP_LOAD || s.op == VDSL_PIX_LOAD_AT || s.op == VDSL_PIX_COUNT || s.op == VDSL_PIX_RANDOM) out = false;
     else out = in_uni;
     st[s.dst] = out;
   };

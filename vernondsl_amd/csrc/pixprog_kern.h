@@ -332,6 +332,22 @@ __device__ __forceinline__ void pix_flush(const PixRt& rt, const PixIn& in, PixA
   }
 }
 
+// Chris Wellons' lowbias32 integer hash (a published 32-bit mixer) and VDSL_PIX_RANDOM's number.
+__device__ __forceinline__ unsigned pix_hash(unsigned x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+__device__ __forceinline__ float pix_random(float seed, unsigned draw, unsigned pixel) {
+  const unsigned s = seed >= 0.0f && seed < 16777216.0f ? static_cast<unsigned>(seed) : 0u;
+  const unsigned h = pix_hash(pix_hash(pix_hash(s) ^ draw) ^ pixel);
+  return static_cast<float>(h >> 8) * 0x1p-24f;
+}
+
 template <class P, int PC>
 __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float (&r)[VDSL_PIX_MAX_REGS], PixOff<P> o,
                                          float fi, float fj, float fcount, int ni, int nj, bool act, PixAcc<P>& acc) {
@@ -383,6 +399,9 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
     r[s.dst] = r[s.a] != r[s.b] ? 1.0f : 0.0f;
   } else if constexpr (s.op == VDSL_PIX_SELECT) {
     r[s.dst] = r[s.a] != 0.0f ? r[s.b] : r[s.c];
+  } else if constexpr (s.op == VDSL_PIX_RANDOM) {
+    const unsigned pixel = static_cast<unsigned>(fi) * static_cast<unsigned>(nj) + static_cast<unsigned>(fj);
+    r[s.dst] = pix_random(r[s.a], static_cast<unsigned>(rt.imm[PC]), pixel);
   } else if constexpr (s.op == VDSL_PIX_FLOOR) {
     r[s.dst] = floorf(r[s.a]);
   } else if constexpr (s.op == VDSL_PIX_TRUNC) {

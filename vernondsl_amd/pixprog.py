@@ -27,7 +27,7 @@ MAX_INSTR, MAX_REGS, MAX_INPUTS = 256, 32, 8
 OP = dict(_lib.MAP_OPS)
 OP.update({"index": 32, "cos": 33, "sin": 34, "count": 35, "lt": 36, "le": 37, "eq": 38, "ne": 39, "select": 40,
            "floor": 41, "load_at": 42, "trip": 43, "atomic_add": 44, "trunc": 45, "atomic_max": 46, "atomic_min": 47,
-           "store_at": 48})
+           "store_at": 48, "random": 49})
 SCATTERS = ("atomic_add", "atomic_max", "atomic_min", "store_at")  # effect nodes: no result register
 TESTS = {"none": 0, "lt": 1, "le": 2, "gt": 3, "ge": 4}
 OUT_REG, OUT_COUNT, OUT_I32, OUT_NONE = 0, 1, 2, 3
@@ -131,6 +131,11 @@ class Builder:
         # never merged with an equal one: two equal adds in a body are two adds
         self._effects = getattr(self, "_effects", 0) + 1
         return self._node("store_at" if op == "store" else "atomic_" + op, args, val=(int(k), int(component), self._effects))
+
+    def random(self, seed, draw: int) -> Node:
+        """A uniform number in [0, 1) for this pixel, from seed (a per-pixel value holding an
+        integer below 2^24) and the draw index (distinct draws give unrelated numbers)."""
+        return self._node("random", (seed if isinstance(seed, Node) else self.const(seed),), val=int(draw))
 
     def state(self, name: str) -> Node:
         return self._node("state", val=name)
@@ -242,6 +247,8 @@ class _Emitter:
             op, a, b, c, imm = OP["load_at"], n.val[0], srcs[0], srcs[1], float(n.val[1])
         elif k in SCATTERS:  # dst names the register of the value added (or compared)
             op, dst, a, b, c, imm = OP[k], srcs[2], n.val[0], srcs[0], srcs[1], float(n.val[1])
+        elif k == "random":
+            op, a, imm = OP["random"], srcs[0], float(n.val)
         elif k == "count":
             op = OP["count"]
         elif k == "trip":

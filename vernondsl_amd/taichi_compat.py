@@ -47,7 +47,8 @@ dropped where an index falls outside F, with idx a tuple or a vector expression 
 by the same struct-for, and adds inside an if happen only where the branch runs.  `F[idx] = v` at
 another index is a plain store there (with ti.ndrange((a, b), ...) interiors and boundary loops).
 Kernel-scope scalars set to constants before the struct-fors and `+=` / `-=` in them are Taichi's
-reductions; `return name` returns one from the call.  `ti.Matrix`
+reductions; `return name` returns one from the call.  `ti.random()` draws from a counter-based
+generator whose state advances once per kernel call.  `ti.Matrix`
 values (`@`, `outer_product`, `trace`, `determinant`, `transpose`) and 2 x 2 matrix fields lower
 to their scalar operations; `for I in ti.grouped(F)` binds I to the index vector.  A lowering called again with the same arguments is replayed as one
 recorded hipGraph.  What neither path lowers raises
@@ -306,7 +307,8 @@ class Kernel:
         env = dict(self.fn.__globals__)
         for name, val in zip(self.arg_names, vals):
             env[name] = val
-        low = lower_kernel(self.fdef, _FuncResolver(env), env)
+        funcs = _FuncResolver(env)
+        low = _with_rng_advance(lower_kernel(self.fdef, funcs, env), self.fdef, funcs, env)
         if key is not None:
             self._cache[key] = low
             while len(self._cache) > self.CACHE_SIZE:
@@ -358,6 +360,34 @@ class Kernel:
             else:
                 out = op.field.grid_tensor() if op.field is not None else None  # None: scatter-adds only
                 kernels.pixel_program(q, op.program, [f.grid_tensor() for f in op.inputs], out, grid=op.grid)
+
+
+_RNG = {}
+
+
+def _rng_state():
+    """The global generator state of ti.random (an int32 0-D field, made once)."""
+    if "field" not in _RNG:
+        _RNG["field"] = Field(i32, ())
+    return _RNG["field"]
+
+
+def _with_rng_advance(low, fdef, funcs, env):
+    """low, followed (when one of its programs draws ti.random numbers) by a program adding 1 to
+    the generator state, so that the next call draws other numbers."""
+    if not any(getattr(op, "uses_rng", False) for op in low.ops()):
+        return low
+    env2 = dict(env)
+    env2["__vdsl_rng"] = _rng_state()
+    body = [ast.AugAssign(target=ast.Subscript(value=ast.Name(id="__vdsl_rng", ctx=ast.Load()), slice=ast.Constant(value=None),
+                                               ctx=ast.Store()), op=ast.Add(), value=ast.Constant(value=1), lineno=0)]
+    loop = ast.For(target=ast.Name(id="__vdsl_r", ctx=ast.Store()), iter=ast.Call(func=ast.Name(id="range", ctx=ast.Load()),
+                   args=[ast.Constant(value=1)], keywords=[]), body=body, orelse=[], lineno=0)
+    inc = lower_pixel_program(ast.FunctionDef(name=fdef.name, args=fdef.args, body=[loop], decorator_list=[], returns=None,
+                                              type_comment=None), funcs, env2)
+    out = Lowered("sequence", low.field, parts=[low, inc])
+    out.ret = getattr(low, "ret", None)
+    return out
 
 
 def _annotation(node):
@@ -1032,6 +1062,7 @@ class _PixInterp:
         self.targets = []  # fields the body scatter-adds into (also in inputs, never read)
         self.scatters = []  # their adds (pixprog scatter_add effects), in program order
         self.pred = None  # inside if branches: the condition under which a statement runs
+        self.rng, self.draws = False, {}  # ti.random: used; draws met per call site
 
     # -- values
     def node(self, v):
@@ -1388,6 +1419,8 @@ class _PixInterp:
                 return self.cast(self.expr(n.args[0], local), self.expr(n.args[1], local))
             if f.attr in ("atomic_add", "atomic_sub", "atomic_max", "atomic_min"):
                 raise TaichiLoweringError(f"ti.{f.attr} is supported as a statement (its old value is not returned)")
+            if f.attr == "random":
+                return self.random(n, local)
             raise TaichiLoweringError(f"call {f.attr!r} is not supported")
         if isinstance(f, ast.Name):
             fdef = self.funcs.get(f.id)
@@ -1416,6 +1449,22 @@ class _PixInterp:
                 raise TaichiLoweringError(f"statement in @ti.func {f.id!r} is not supported")
             raise TaichiLoweringError(f"@ti.func {f.id!r} returns nothing")
         raise TaichiLoweringError("unsupported call")
+
+    def random(self, n, local):
+        """ti.random() / ti.random(float): a uniform number in [0, 1), a function of the global
+        generator state (a hidden 0-D field, advanced once per kernel call), this pixel and the
+        draw: the call's place in the source and how often the lowering has met it (static loops
+        unroll one call into several draws)."""
+        if n.args:
+            dt = self.expr(n.args[0], local)
+            if dt not in (float, f32):
+                raise TaichiLoweringError("ti.random gives f32 numbers here (ti.random() or ti.random(float))")
+        site = (getattr(n, "lineno", 0) % 4096) * 64 + getattr(n, "col_offset", 0) % 64
+        occ = self.draws.get(site, 0)
+        self.draws[site] = occ + 1
+        seed = self._field_read(_rng_state(), ast.Constant(value=None), local)
+        self.rng = True
+        return self.b.random(seed, site * 64 + occ % 64)
 
     def cast(self, v, dtype):
         """ti.cast / .cast / int(): to an integer type truncates toward zero (Taichi's float ->
@@ -2475,6 +2524,7 @@ def _lower_pixel_one(fdef: ast.FunctionDef, funcs, env, target, unroll=True):
     low = Lowered("pixel_program", fld, program=prog, inputs=ip.inputs)
     low.reads = [f for k, f in enumerate(ip.inputs) if k in live]
     low.grid = _grid_of(ip.shape if ip.shape is not None else ip.fld.shape)
+    low.uses_rng = ip.rng
     return low, ip.stored, bool(ip.scatters)
 
 
