@@ -42,7 +42,7 @@ extern "C" {
  * and in_cols (inputs of another shape than the grid); 6: VDSL_PIX_ATOMIC_ADD,
  * VDSL_PIX_OUT_NONE (scatter-adds) and VDSL_PIX_TRUNC (struct layouts unchanged since 5); 7:
  * VDSL_PIX_MAX_INSTR 256 and VDSL_PIX_MAX_INPUTS 8 (vdsl_pixel_program's arrays grow),
- * VDSL_PIX_ATOMIC_MAX / MIN, VDSL_PIX_STORE_AT and VDSL_PIX_RANDOM. */
+ * VDSL_PIX_ATOMIC_MAX / MIN, VDSL_PIX_STORE_AT, VDSL_PIX_RANDOM, VDSL_PIX_ATAN2 ... POW. */
 #define VDSL_ABI_VERSION 7
 
 typedef enum vdsl_status {
@@ -367,7 +367,15 @@ typedef enum vdsl_pix_opcode {
    * s = (uint32)r[a] (a seed, an integer below 2^24 held as a float), d = (uint32)imm (which
    * draw of the pixel), H Chris Wellons' lowbias32 integer hash (x ^= x >> 16; x *= 0x7feb352d;
    * x ^= x >> 15; x *= 0x846ca68b; x ^= x >> 16), and the result (h >> 8) * 2^-24, exact in f32. */
-  VDSL_PIX_RANDOM = 49
+  VDSL_PIX_RANDOM = 49,
+  /* the device math library's float functions (a few ulp from the correctly rounded value):
+   * atan2f(r[a], r[b]), asinf, acosf, atanf, tanf of r[a], powf(r[a], r[b]) */
+  VDSL_PIX_ATAN2 = 50,
+  VDSL_PIX_ASIN = 51,
+  VDSL_PIX_ACOS = 52,
+  VDSL_PIX_ATAN = 53,
+  VDSL_PIX_TAN = 54,
+  VDSL_PIX_POWF = 55
 } vdsl_pix_opcode;
 
 typedef enum vdsl_pix_test {

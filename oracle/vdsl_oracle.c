@@ -24,7 +24,10 @@
  *                        expressions, field reads, if / else and compound loop tests), by
  *                        equality with orc_escape_time on the programs both express, by closed
  *                        forms (a loop with no test runs max_iter times), and the comparison,
- *                        select, floor and trunc opcodes by numpy on every pair of special values.
+ *                        select, floor and trunc opcodes by numpy on every pair of special values;
+ *                        asin, acos, atan, tan, atan2 and powf (the C library's float functions)
+ *                        within 2 ulp of numpy's double-precision results, with atan2's signed-
+ *                        zero quadrants and pow's IEEE special cases exactly.
  *                        Scatter-adds (VDSL_PIX_ATOMIC_ADD, run pixel by pixel in row-major
  *                        order): by numpy's np.add.at over the same indices in the same order
  *                        (f32 bit for bit, int32 exactly with wrap-around) and by the drop rule
@@ -243,6 +246,12 @@ static float pix_apply(const vdsl_pixel_program* p, const vdsl_map_instr* s, con
     }
     case VDSL_PIX_INDEX: return s->a == 0 ? (float)i : (float)j;
     case VDSL_PIX_COUNT: case VDSL_PIX_TRIP: return (float)count;  /* the trip, in the loop's sections */
+    case VDSL_PIX_ATAN2: return atan2f(reg[s->a], reg[s->b]);
+    case VDSL_PIX_ASIN: return asinf(reg[s->a]);
+    case VDSL_PIX_ACOS: return acosf(reg[s->a]);
+    case VDSL_PIX_ATAN: return atanf(reg[s->a]);
+    case VDSL_PIX_TAN: return tanf(reg[s->a]);
+    case VDSL_PIX_POWF: return powf(reg[s->a], reg[s->b]);
     case VDSL_PIX_COS: return cosf(reg[s->a]);
     case VDSL_PIX_SIN: return sinf(reg[s->a]);
     case VDSL_PIX_LT: return reg[s->a] < reg[s->b] ? 1.0f : 0.0f;

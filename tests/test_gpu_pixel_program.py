@@ -159,6 +159,34 @@ def test_transcendentals_within_bounds(dev, q):
             assert np.all(np.abs(got - ref) <= REL * np.abs(ref) + 1e-37), name
 
 
+def test_inverse_trig_tan_atan2_pow_within_ulp_of_oracle(dev, q):
+    """asin, acos, atan, tan, atan2 and powf from the device math library against the C library's
+    (the oracle) over a domain crossing every branch (|x| > 1, signed zeros, infinities, NaN,
+    tiny and huge values): within 4 ulp, NaN exactly where the oracle has NaN; and the kernel
+    using them through the Taichi front end within a few f32 ulp of the oracle."""
+    from test_taichi_general import MATH_DOMAIN, MATH_KERNELS, ulp_distance
+    x = MATH_DOMAIN[None]
+    b = pp.Builder()
+    la, lc = b.load(0), b.load(1)
+    worst = {}
+    for name in ("asin", "acos", "atan", "tan"):
+        prog = pp.compile_program(b, out=b.op(name, la))
+        got = run_prog(dev, q, prog, [x, x], 1, x.shape[1])
+        worst[name] = int(ulp_distance(got, oracle.pixel_program(prog, 1, x.shape[1], [x, x])).max())
+    y = MATH_DOMAIN[::7]
+    a = np.repeat(y[:, None], len(y), axis=1)
+    c = np.repeat(y[None, :], len(y), axis=0)
+    for name in ("atan2", "powf"):
+        prog = pp.compile_program(b, out=b.op(name, la, lc))
+        got = run_prog(dev, q, prog, [a, c], len(y), len(y))
+        worst[name] = int(ulp_distance(got, oracle.pixel_program(prog, len(y), len(y), [a, c])).max())
+    print("ulp against the oracle:", worst)
+    assert max(worst.values()) <= 4, worst
+    low = tc.lower_source_kernel(MATH_KERNELS, "polar", {})
+    u = np.random.default_rng(5).uniform(-2, 2, (16, 32)).astype(np.float32)
+    got = run_prog(dev, q, low.program, [u], 16, 32)
+    assert np.allclose(got, oracle.pixel_program(low.program, 16, 32, [u]), rtol=2e-6, atol=1e-6)
+
 def test_invalid_programs_rejected(dev, q):
     import ctypes
     out = Tensor(dev, (8, 8), "f32")

@@ -310,6 +310,97 @@ def test_compare_select_floor_opcodes_against_numpy():
     assert np.array_equal(tr.view(np.uint32), np.trunc(a).view(np.uint32))
 
 
+def ulp_distance(got, want):
+    """Distance in units in the last place between two f32 arrays (the gap in the ordered bit
+    patterns), 0 where both are NaN, a huge value where only one is."""
+    def ordered(x):
+        i = np.asarray(x, np.float32).view(np.int32).astype(np.int64)
+        return np.where(i < 0, -(i & 0x7FFFFFFF), i)
+    g, w = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    d = np.abs(ordered(g) - ordered(w))
+    both = np.isnan(g) & np.isnan(w)
+    one = np.isnan(g) ^ np.isnan(w)
+    return np.where(both, 0, np.where(one, 1 << 40, d))
+
+
+MATH_DOMAIN = np.concatenate([np.linspace(-1.2, 1.2, 301), np.linspace(-40, 40, 257), np.geomspace(1e-6, 1e6, 97),
+                              -np.geomspace(1e-6, 1e6, 97), [0.0, -0.0, 1.0, -1.0, np.inf, -np.inf, np.nan]]).astype(np.float32)
+MATH_UNARY = {"asin": np.arcsin, "acos": np.arccos, "atan": np.arctan, "tan": np.tan}
+
+
+def test_inverse_trig_tan_atan2_pow_opcodes_against_numpy():
+    """asin, acos, atan, tan, atan2 and powf take the C library's float functions in the oracle:
+    within 2 ulp of numpy's double-precision result rounded to f32 on a domain crossing every
+    branch (|x| > 1 gives NaN for asin/acos; signed zeros, infinities, NaN), and the IEEE special
+    cases of atan2 (quadrants, signed zeros) and pow (x^0 = 1, 1^y = 1, negative base with a
+    fractional exponent = NaN, 0^-1 = inf) exactly."""
+    x = MATH_DOMAIN
+    n = len(x)
+    b = pp.Builder()
+    la, lc = b.load(0), b.load(1)
+    for name, fn in MATH_UNARY.items():
+        got = oracle.pixel_program(pp.compile_program(b, out=b.op(name, la)), 1, n, [x[None], x[None]])[0]
+        with np.errstate(all="ignore"):
+            want = fn(x.astype(np.float64)).astype(np.float32)
+        assert ulp_distance(got, want).max() <= 2, name
+    y = MATH_DOMAIN[::7]
+    a = np.repeat(y[:, None], len(y), axis=1)
+    c = np.repeat(y[None, :], len(y), axis=0)
+    for name, fn in (("atan2", np.arctan2), ("powf", np.power)):
+        got = oracle.pixel_program(pp.compile_program(b, out=b.op(name, la, lc)), len(y), len(y), [a, c])
+        with np.errstate(all="ignore"):
+            want = fn(a.astype(np.float64), c.astype(np.float64)).astype(np.float32)
+        assert ulp_distance(got, want).max() <= 2, name
+    sp = np.array([[0.0, 0.0], [-0.0, 0.0], [0.0, -0.0], [-0.0, -0.0], [0.0, -1.0], [-0.0, -1.0], [1.0, 0.0], [-1.0, -0.0], [1.0, 1.0],
+                   [-1.0, 1.0]], np.float32)
+    got = oracle.pixel_program(pp.compile_program(b, out=b.op("atan2", la, lc)), 1, len(sp), [sp[None, :, 0], sp[None, :, 1]])[0]
+    pi = np.float32(np.pi)
+    want = np.array([0.0, -0.0, pi, -pi, pi, -pi, pi / 2, -pi / 2, pi / 4, -pi / 4], np.float32)
+    assert np.array_equal(np.signbit(got), np.signbit(want)) and ulp_distance(got, want).max() <= 1
+    pw = np.array([[5.0, 0.0], [np.nan, 0.0], [1.0, np.nan], [-8.0, 1.0 / 3.0], [0.0, -1.0], [-2.0, 3.0], [4.0, 0.5]],
+                  np.float32)
+    got = oracle.pixel_program(pp.compile_program(b, out=b.op("powf", la, lc)), 1, len(pw), [pw[None, :, 0], pw[None, :, 1]])[0]
+    assert np.array_equal(got, np.array([1.0, 1.0, 1.0, np.nan, np.inf, -8.0, 2.0], np.float32), equal_nan=True)
+
+
+MATH_KERNELS = """
+import taichi as ti
+import taichi.math as tm
+ti.init(arch=ti.gpu)
+u = ti.field(dtype=float, shape=(16, 32))
+out = ti.Vector.field(4, dtype=float, shape=(16, 32))
+
+@ti.kernel
+def polar():
+    for i, j in out:
+        x = u[i, j]
+        r = ti.sqrt(x * x + 1.0) ** 1.5
+        out[i, j] = [ti.atan2(x, i - 7.5), ti.asin(ti.min(ti.max(x, -1.0), 1.0)) + ti.acos(0.25), ti.atan(x) * ti.tan(0.1 * j), r]
+"""
+
+
+def test_taichi_atan2_asin_pow_lower_to_math_opcodes():
+    """ti.atan2 / ti.asin / ti.acos / ti.atan / ti.tan and x ** y with a fractional exponent lower
+    to the math opcodes (a constant argument folds in f32 on the host): the oracle's result is
+    within a few f32 ulp of numpy's double-precision restatement of the kernel."""
+    low = tc.lower_source_kernel(MATH_KERNELS, "polar", {})
+    names = {v: k for k, v in pp.OP.items()}
+    prog = low.program
+    count = prog.n_pre + prog.n_test + prog.n_body + prog.n_post
+    ops = {names.get(prog.code[k].op) for k in range(count)}
+    u = np.random.default_rng(5).uniform(-2, 2, (16, 32)).astype(np.float32)
+    got = oracle.pixel_program(low.program, 16, 32, [u])
+    i = np.arange(16, dtype=np.float64)[:, None] * np.ones((1, 32))
+    j = np.ones((16, 1)) * np.arange(32, dtype=np.float64)[None, :]
+    x = u.astype(np.float64)
+    want = np.stack([np.arctan2(x, i - 7.5), np.arcsin(np.clip(x, -1, 1)) + np.arccos(0.25),
+                     np.arctan(x) * np.tan(np.float32(0.1) * j.astype(np.float32)),
+                     np.sqrt(x * x + 1.0) ** 1.5], axis=-1).astype(np.float32)
+    # the kernel's f32 roundings (x * x + 1, the sum asin + acos near its zero) against double
+    # precision: within a few f32 ulp of the terms' magnitude (|terms| < 3)
+    assert np.allclose(got, want, rtol=2e-6, atol=1e-6)
+    assert {"atan2", "asin", "atan", "tan", "powf"} <= ops
+
 def palette_numpy(shift, W=800, H=600, limit=120):
     x, y = grid(W, H)
     c0 = (x / f32(W)) * f32(3.0) + f32(-1.5)

@@ -385,6 +385,18 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
     r[s.dst] = s.a == 0 ? fi : fj;
   } else if constexpr (s.op == VDSL_PIX_COUNT || s.op == VDSL_PIX_TRIP) {
     r[s.dst] = fcount;  // the count in the post section, the trip in the loop's sections
+  } else if constexpr (s.op == VDSL_PIX_ATAN2) {
+    r[s.dst] = atan2f(r[s.a], r[s.b]);
+  } else if constexpr (s.op == VDSL_PIX_ASIN) {
+    r[s.dst] = asinf(r[s.a]);
+  } else if constexpr (s.op == VDSL_PIX_ACOS) {
+    r[s.dst] = acosf(r[s.a]);
+  } else if constexpr (s.op == VDSL_PIX_ATAN) {
+    r[s.dst] = atanf(r[s.a]);
+  } else if constexpr (s.op == VDSL_PIX_TAN) {
+    r[s.dst] = tanf(r[s.a]);
+  } else if constexpr (s.op == VDSL_PIX_POWF) {
+    r[s.dst] = powf(r[s.a], r[s.b]);
   } else if constexpr (s.op == VDSL_PIX_COS) {
     r[s.dst] = cosf(r[s.a]);
   } else if constexpr (s.op == VDSL_PIX_SIN) {
@@ -432,7 +444,7 @@ __device__ constexpr uint32_t pix_reads(const vdsl_map_instr& s) {
   switch (s.op) {
     case VDSL_MAP_LOAD: case VDSL_MAP_CONST: case VDSL_PIX_INDEX: case VDSL_PIX_COUNT: return 0u;
     case VDSL_MAP_ADD: case VDSL_MAP_SUB: case VDSL_MAP_MUL: case VDSL_MAP_DIV: case VDSL_MAP_MAX: case VDSL_MAP_MIN:
-    case VDSL_PIX_LT: case VDSL_PIX_LE: case VDSL_PIX_EQ: case VDSL_PIX_NE:
+    case VDSL_PIX_LT: case VDSL_PIX_LE: case VDSL_PIX_EQ: case VDSL_PIX_NE: case VDSL_PIX_ATAN2: case VDSL_PIX_POWF:
       return (1u << s.a) | (1u << s.b);
     case VDSL_PIX_LOAD_AT: return (1u << s.b) | (1u << s.c);
     case VDSL_MAP_FMA: case VDSL_PIX_SELECT: return (1u << s.a) | (1u << s.b) | (1u << s.c);

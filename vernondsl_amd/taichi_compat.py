@@ -1022,7 +1022,7 @@ class _PMat:
 
 
 _UNARY_FUNCS = {"sqrt": "sqrt", "exp": "exp", "log": "log", "sin": "sin", "cos": "cos", "tanh": "tanh", "abs": "abs",
-                "floor": "floor"}
+                "floor": "floor", "asin": "asin", "acos": "acos", "atan": "atan", "tan": "tan"}
 def _skey(fld):
     """The local-scope key of the value the body has stored to fld[i, j] (read back by a later read
     of fld[i, j] in the same body)."""
@@ -1120,7 +1120,7 @@ class _PixInterp:
             return _binop(op, x, y)
         if op == "pow":
             if not (isinstance(y, (int, np.integer)) and 1 <= int(y) <= 8):
-                raise TaichiLoweringError("only small positive integer powers (x ** n, n <= 8) are supported")
+                return self.b.op("powf", self.node(x), self.node(y))  # the math library's powf
             r = x
             for _ in range(int(y) - 1):
                 r = self.b.op("mul", self.node(r), self.node(x))
@@ -1138,7 +1138,8 @@ class _PixInterp:
             v = np.float32(x)
             with np.errstate(all="ignore"):
                 return {"neg": -v, "abs": np.abs(v), "sqrt": np.sqrt(v), "exp": np.exp(v), "log": np.log(v), "sin": np.sin(v),
-                        "cos": np.cos(v), "tanh": np.tanh(v), "floor": np.floor(v), "trunc": np.trunc(v)}[fn]
+                        "cos": np.cos(v), "tanh": np.tanh(v), "floor": np.floor(v), "trunc": np.trunc(v),
+                        "asin": np.arcsin(v), "acos": np.arccos(v), "atan": np.arctan(v), "tan": np.tan(v)}[fn]
         r = self.b.op(fn, x)
         bx = self._ib(x)
         return self._int_result(r, bx, fn) if fn in ("neg", "abs", "floor") and bx is not None else r
@@ -1421,6 +1422,18 @@ class _PixInterp:
                 raise TaichiLoweringError(f"ti.{f.attr} is supported as a statement (its old value is not returned)")
             if f.attr == "random":
                 return self.random(n, local)
+            if f.attr in ("atan2", "pow"):
+                if len(n.args) != 2:
+                    raise TaichiLoweringError(f"ti.{f.attr} takes two values")
+                kind = "atan2" if f.attr == "atan2" else "powf"
+                x, y = (self.expr(a, local) for a in n.args)
+
+                def fn2(a, c):
+                    if _is_num(a) and _is_num(c):
+                        with np.errstate(all="ignore"):
+                            return (np.arctan2 if kind == "atan2" else np.power)(_f32(a), _f32(c))
+                    return self.b.op(kind, self.node(a), self.node(c))
+                return self.elementwise(fn2, x, y)
             raise TaichiLoweringError(f"call {f.attr!r} is not supported")
         if isinstance(f, ast.Name):
             fdef = self.funcs.get(f.id)
