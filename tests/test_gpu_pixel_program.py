@@ -744,3 +744,21 @@ def test_fields_of_other_shapes_bit_exact(dev, q):
     assert low.program.in_rows[0] == 1 and low.program.in_cols[0] == 48
     got = run_prog(dev, q, low.program, [p], 640, 480)
     assert np.array_equal(got, oracle.pixel_program(low.program, 640, 480, [p]))
+
+
+@pytest.mark.parametrize("kernel", ["first_over", "skip_parity", "escape_break", "own_trips", "misc"])
+def test_break_continue_and_small_math_bit_exact(dev, q, kernel):
+    """Loops with break / continue (flags read by the loop's test and guarding the statements
+    after a jump), a while counter read after a break, rsqrt, taichi.math.mod and static
+    conditions: every program of the kernel on the device equals the oracle bit for bit."""
+    from test_taichi_general import JUMPS, SMALL_MATH, lower_named
+    text = SMALL_MATH if kernel == "misc" else JUMPS
+    low, names = lower_named(text, kernel, {})
+    r = np.random.default_rng(3)
+    fields = {"u": r.uniform(-0.5, 2.5, (12, 20)).astype(np.float32) if kernel != "misc"
+              else r.uniform(-2, 2, (8, 16)).astype(np.float32)}
+    for op in low.ops():
+        ni, nj = op.grid
+        src = [fields[names[id(f)]] for f in op.inputs]
+        got = run_prog(dev, q, op.program, src, ni, nj)
+        assert np.array_equal(got, oracle.pixel_program(op.program, ni, nj, src)), kernel

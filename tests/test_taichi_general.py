@@ -1241,3 +1241,158 @@ def test_grouped_struct_fors():
     a = (i * f32(2.0) + j) + b0[:, :, 0]
     assert np.array_equal(arr["a"], a) and np.array_equal(arr["b"][:, :, 1], a) and np.array_equal(arr["b"][:, :, 0], i)
     assert np.array_equal(arr["c"], np.arange(20, dtype=np.float32) * f32(0.5))
+
+
+JUMPS = """
+import taichi as ti
+ti.init(arch=ti.gpu)
+u = ti.field(dtype=float, shape=(12, 20))
+k = ti.field(dtype=ti.i32, shape=(12, 20))
+out = ti.field(dtype=float, shape=(12, 20))
+cnt = ti.field(dtype=ti.i32, shape=(12, 20))
+
+@ti.kernel
+def first_over():
+    for i, j in out:
+        s = 0.0
+        for t in range(40):
+            if s > u[i, j]:
+                break
+            s += 0.1
+        out[i, j] = s
+
+@ti.kernel
+def skip_parity():
+    for i, j in out:
+        s = 0.0
+        for t in range(9):
+            if t % 2 == i % 2:
+                continue
+            s += t * u[i, j]
+        out[i, j] = s
+
+@ti.kernel
+def escape_break():
+    for i, j in cnt:
+        x = u[i, j]
+        n = 0
+        while n < 30:
+            x = x * x - 1.5
+            if ti.abs(x) > 4.0:
+                break
+            n += 1
+        cnt[i, j] = n
+
+@ti.kernel
+def own_trips():
+    for i, j in out:
+        s = 0.0
+        for t in range((i * 7 + j) % 12):
+            if t * 0.25 > u[i, j]:
+                break
+            elif t == 3:
+                continue
+            else:
+                s += 1.0
+            s *= 1.5
+        out[i, j] = s
+"""
+
+
+def _jump_reference(kernel, u, kk):
+    """The kernels above as plain Python loops, every value an f32 rounded where Taichi's is."""
+    out = np.zeros(u.shape, np.float32)
+    cnt = np.zeros(u.shape, np.int32)
+    for i in range(u.shape[0]):
+        for j in range(u.shape[1]):
+            uv = u[i, j]
+            s = f32(0.0)
+            if kernel == "first_over":
+                for _ in range(40):
+                    if s > uv:
+                        break
+                    s = f32(s + f32(0.1))
+            elif kernel == "skip_parity":
+                for t in range(9):
+                    if t % 2 == i % 2:
+                        continue
+                    s = f32(s + f32(f32(t) * uv))
+            elif kernel == "escape_break":
+                x, n = uv, 0
+                while n < 30:
+                    x = f32(f32(x * x) - f32(1.5))
+                    if abs(x) > 4.0:
+                        break
+                    n += 1
+                cnt[i, j] = n
+            else:
+                for t in range((i * 7 + j) % 12):
+                    if f32(t) * f32(0.25) > uv:
+                        break
+                    elif t == 3:
+                        continue
+                    else:
+                        s = f32(s + f32(1.0))
+                    s = f32(s * f32(1.5))
+            out[i, j] = s
+    return cnt if kernel == "escape_break" else out
+
+
+@pytest.mark.parametrize("kernel", ["first_over", "skip_parity", "escape_break", "own_trips"])
+def test_break_and_continue_bit_exact(kernel):
+    """break and continue in runtime loops (range loops, a while loop whose counter is read after
+    it, a loop of a per-pixel trip count, break / continue in if / elif / else with statements
+    after them): a break sets a flag the loop's test reads before the next trip, statements
+    after a possible jump run only where none happened, and the while counter misses the
+    increment of the trip that broke out.  Bit for bit against plain Python loops."""
+    r = np.random.default_rng(3)
+    u = r.uniform(-0.5, 2.5, (12, 20)).astype(np.float32)
+    kk = r.integers(0, 12, (12, 20)).astype(np.int32)
+    low, names = lower_named(JUMPS, kernel, {})
+    arrays = {"u": u, "k": kk, "out": np.zeros((12, 20), np.float32), "cnt": np.zeros((12, 20), np.int32)}
+    run_ops(low, names, arrays)
+    got = arrays["cnt" if kernel == "escape_break" else "out"]
+    want = _jump_reference(kernel, u, kk)
+    assert np.array_equal(got, want), kernel
+    assert len(np.unique(want)) > 3  # the jumps happen at different trips on different pixels
+
+
+def test_continue_in_a_while_loop_is_refused():
+    text = JUMPS.replace("            if ti.abs(x) > 4.0:\n                break", "            if ti.abs(x) > 4.0:\n                continue")
+    with pytest.raises(tc.TaichiLoweringError, match="continue in a while loop"):
+        tc.lower_source_kernel(text, "escape_break", {})
+
+
+SMALL_MATH = """
+import taichi as ti
+import taichi.math as tm
+ti.init(arch=ti.gpu)
+u = ti.field(dtype=float, shape=(8, 16))
+out = ti.Vector.field(3, dtype=float, shape=(8, 16))
+
+@ti.kernel
+def misc():
+    for i, j in out:
+        x = u[i, j]
+        out[i, j] = [ti.rsqrt(x * x + 1.0), tm.mod(x, 0.3), 0.0]
+        if ti.static(True):
+            out[i, j].z = 2.0 * x
+        if ti.static(False):
+            out[i, j].z = 5.0
+"""
+
+
+def test_rsqrt_mod_and_static_conditions():
+    """ti.rsqrt as 1 / sqrt (each exactly rounded), taichi.math.mod as x - y floor(x / y) (GLSL's
+    mod: the sign of y), and `if ti.static(c)` decided when the kernel is lowered: bit for bit
+    against numpy's f32 restatement."""
+    low, names = lower_named(SMALL_MATH, "misc", {})
+    u = np.random.default_rng(8).uniform(-2, 2, (8, 16)).astype(np.float32)
+    arrays = {"u": u, "out": np.zeros((8, 16, 3), np.float32)}
+    run_ops(low, names, arrays)
+    got = arrays["out"]
+    assert np.array_equal(got[..., 0], f32(1.0) / np.sqrt(u * u + f32(1.0)))
+    y = f32(0.3)
+    assert np.array_equal(got[..., 1], u - y * np.floor(u / y))
+    assert np.array_equal(got[..., 2], f32(2.0) * u)
+    assert (got[..., 1] >= 0).all()  # GLSL's mod takes the sign of the divisor

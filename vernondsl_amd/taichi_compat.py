@@ -30,8 +30,9 @@ expression of the pixel indices, scalar kernel arguments, other 2-D f32 fields r
 and constants, with loops - a `while <test> and <counter> < MAX:` check-then-update
 loop whose body ends with `counter += 1`, or a `for k in range(N)` / `range(A, B)` loop (a
 perfect nest of them runs as one loop over its trips; N may be an integer expression of the
-pixel), whose test and body may read the counter or k (from the loop's trip); a body of several
-loops runs as parts joined by hidden per-pixel fields - and stores
+pixel), whose test and body may read the counter or k (from the loop's trip), with `break` and
+`continue` in the body or its ifs (`continue` not in a while loop, where it would skip the
+increment); a body of several loops runs as parts joined by hidden per-pixel fields - and stores
 `F[i, j] = <value>` (an i32 field stores the loop counter) into one or more fields of the loop's
 shape: a body storing several fields becomes one program per stored field, run in an order in
 which no program loads a field that an earlier one stored (a snapshot copy where the programs
@@ -865,7 +866,8 @@ math = types.ModuleType("taichi.math")
 math.pi = _pymath.pi
 math.e = _pymath.e
 for _name in ("vec2", "vec3", "vec4", "clamp", "mix", "smoothstep", "length", "normalize", "dot", "cross", "fract",
-              "sign", "step", "sqrt", "exp", "log", "sin", "cos", "tanh", "floor", "ceil", "min", "max"):
+              "sign", "step", "sqrt", "exp", "log", "sin", "cos", "tanh", "floor", "ceil", "min", "max", "mod", "log2",
+              "atan2", "asin", "acos", "atan", "tan", "pow"):
     setattr(math, _name, _name)  # placeholders: only meaningful inside kernels
 
 
@@ -1139,7 +1141,8 @@ class _PixInterp:
             with np.errstate(all="ignore"):
                 return {"neg": -v, "abs": np.abs(v), "sqrt": np.sqrt(v), "exp": np.exp(v), "log": np.log(v), "sin": np.sin(v),
                         "cos": np.cos(v), "tanh": np.tanh(v), "floor": np.floor(v), "trunc": np.trunc(v),
-                        "asin": np.arcsin(v), "acos": np.arccos(v), "atan": np.arctan(v), "tan": np.tan(v)}[fn]
+                        "asin": np.arcsin(v), "acos": np.arccos(v), "atan": np.arctan(v), "tan": np.tan(v),
+                        "recip": np.float32(1.0) / v}[fn]
         r = self.b.op(fn, x)
         bx = self._ib(x)
         return self._int_result(r, bx, fn) if fn in ("neg", "abs", "floor") and bx is not None else r
@@ -1212,7 +1215,9 @@ class _PixInterp:
     # -- expressions
     def expr(self, n, local):
         if isinstance(n, ast.Constant):
-            if isinstance(n.value, bool) or not isinstance(n.value, (int, float)):
+            if isinstance(n.value, bool):  # True / False are the integers 1 / 0, as in Taichi
+                return int(n.value)
+            if not isinstance(n.value, (int, float)):
                 raise TaichiLoweringError(f"constant {n.value!r} is not a number")
             return n.value
         if isinstance(n, ast.Name):
@@ -1422,6 +1427,15 @@ class _PixInterp:
                 raise TaichiLoweringError(f"ti.{f.attr} is supported as a statement (its old value is not returned)")
             if f.attr == "random":
                 return self.random(n, local)
+            if f.attr == "static" and len(n.args) == 1:  # `if ti.static(cond):` decided when lowering
+                return self.expr(n.args[0], local)
+            if f.attr == "rsqrt" and len(n.args) == 1:  # 1 / sqrt(x), both exactly rounded
+                return self.unary("recip", self.unary("sqrt", self.expr(n.args[0], local)))
+            if f.attr == "log2" and len(n.args) == 1:  # log(x) / ln 2
+                return self.arith("mul", self.unary("log", self.expr(n.args[0], local)), _f32(1.0 / _pymath.log(2.0)))
+            if f.attr == "mod" and len(n.args) == 2:  # taichi.math.mod: x - y floor(x / y), GLSL's mod
+                x, y = (self.expr(a, local) for a in n.args)
+                return self.arith("sub", x, self.arith("mul", y, self.unary("floor", self.arith("div", x, y))))
             if f.attr in ("atan2", "pow"):
                 if len(n.args) != 2:
                     raise TaichiLoweringError(f"ti.{f.attr} takes two values")
@@ -1816,6 +1830,7 @@ class _PixInterp:
             if (self.unroll and isinstance(it, ast.Call) and isinstance(it.func, ast.Name) and it.func.id == "range"
                     and isinstance(st.target, ast.Name)
                     and not any(isinstance(nd, (ast.For, ast.While)) for s2 in st.body for nd in ast.walk(s2))
+                    and not any(_jumps(st.body))
                     and any(isinstance(nd, ast.Name) and nd.id == st.target.id and isinstance(nd.ctx, ast.Load)
                             for s2 in st.body for nd in ast.walk(s2))):
                 bounds = [self.expr(a, local) for a in it.args]
@@ -2557,6 +2572,51 @@ def _range_bounds(it, ip, local):
     return (int(vals[0]), int(vals[1])) if len(vals) == 2 else (0, int(vals[0]))
 
 
+_BRK, _SKIP = "__vdsl_break", "__vdsl_skip"  # hidden locals of a loop with break / continue
+
+
+def _jumps(stmts):
+    """(break, continue) among the statements at this loop's level: in if branches, not in the
+    bodies of inner loops (which they leave instead)."""
+    brk = cont = False
+    for st in stmts:
+        if isinstance(st, ast.Break):
+            brk = True
+        elif isinstance(st, ast.Continue):
+            cont = True
+        elif isinstance(st, ast.If):
+            b2, c2 = _jumps(st.body + st.orelse)
+            brk, cont = brk or b2, cont or c2
+    return brk, cont
+
+
+def _without_jumps(stmts):
+    """The loop body with break / continue as assignments to flags: a jump sets the trip's skip
+    flag (break also the loop's break flag, which the loop's test reads before the next trip),
+    and the statements after one that may jump run under `if skip == 0`, so they take effect
+    only on lanes that did not jump."""
+    def flag(name):
+        return ast.Assign(targets=[ast.Name(id=name, ctx=ast.Store())], value=ast.Constant(value=1), lineno=0)
+    out = []
+    for k, st in enumerate(stmts):
+        if isinstance(st, (ast.Break, ast.Continue)):
+            out.append(flag(_SKIP))
+            if isinstance(st, ast.Break):
+                out.append(flag(_BRK))
+            return out  # what follows an unconditional jump never runs
+        if isinstance(st, ast.If) and any(_jumps([st])):
+            out.append(ast.If(test=st.test, body=_without_jumps(st.body), orelse=_without_jumps(st.orelse),
+                              lineno=getattr(st, "lineno", 0)))
+            rest = _without_jumps(stmts[k + 1:])
+            if rest:
+                live = ast.Compare(left=ast.Name(id=_SKIP, ctx=ast.Load()), ops=[ast.Eq()],
+                                   comparators=[ast.Constant(value=0)])
+                out.append(ast.If(test=live, body=rest, orelse=[], lineno=getattr(st, "lineno", 0)))
+            return out
+        out.append(st)
+    return out
+
+
 def _lower_loop(st, ip: _PixInterp, local: dict, b):
     """One loop of the body: (initial states, test, new states, max_iter); rebinds `local` to the
     values after the loop (states, and the counter as the loop's count)."""
@@ -2570,6 +2630,7 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
             inner = [s for s in loops[-1].body
                      if not (isinstance(s, ast.Expr) and isinstance(s.value, ast.Constant)) and not isinstance(s, ast.Pass)]
             if not (len(inner) == 1 and isinstance(inner[0], ast.For) and _is_range(inner[0].iter)
+                    and not _jumps(inner[0].body)[0]  # a break leaves the inner loop only
                     and _range_bounds(inner[0].iter, ip, local) is not None
                     and ip.static_values(inner[0], local) is None):
                 break
@@ -2619,8 +2680,20 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
                 test_cmp.append(t)
         if max_iter is None:
             raise TaichiLoweringError("the while condition needs a bound `counter < MAX`")
+        if _jumps(loop_body)[1]:
+            raise TaichiLoweringError("continue in a while loop would skip its `counter += 1`")
         test = test_cmp or None
         max_iter = max(0, max_iter)
+    # break / continue: flags (a loop state and a per-trip value); the loop runs while the break
+    # flag is clear, the check made before each trip as the loop's other tests are
+    brk, cont = _jumps(loop_body)
+    if brk or cont:
+        loop_body = [ast.Assign(targets=[ast.Name(id=_SKIP, ctx=ast.Store())], value=ast.Constant(value=0), lineno=0)] \
+            + _without_jumps(loop_body)
+    if brk:
+        local[_BRK] = 0
+        clear = ast.Compare(left=ast.Name(id=_BRK, ctx=ast.Load()), ops=[ast.Eq()], comparators=[ast.Constant(value=0)])
+        test = (test or []) + [clear]
     # loop-carried state: names assigned in the body that exist before the loop
     assigned = _assigned_names(loop_body)
     for nm in [counter] + [v for v, _, _ in nest]:
@@ -2676,13 +2749,17 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
     if test is not None:
         ops = {ast.Lt: "lt", ast.LtE: "le", ast.Gt: "gt", ast.GtE: "ge"}
         one = test[0]
-        if len(test) == 1 and isinstance(one, ast.Compare) and len(one.ops) == 1 and type(one.ops[0]) in ops:
+        if (len(test) == 1 and dyn_n is None and isinstance(one, ast.Compare) and len(one.ops) == 1
+                and type(one.ops[0]) in ops):
             lhs, rhs = ip.expr(one.left, body_local), ip.expr(one.comparators[0], body_local)
             if isinstance(lhs, _PVec) or isinstance(rhs, _PVec):
                 raise TaichiLoweringError("the loop test compares scalars")
             test_out = (ops[type(one.ops[0])], lhs, rhs)
         else:  # any other condition: its truth value (1 / 0) against 0.5
-            t = ip.logic("and", [ip.expr(e, body_local) for e in test])
+            terms = [ip.expr(e, body_local) for e in test]
+            if dyn_n is not None:
+                terms = [b.op("lt", trip, dyn_n)] + terms
+            t = ip.logic("and", terms)
             test_out = ("gt", t, 0.5)
     ip.in_loop = True
     try:
@@ -2707,7 +2784,8 @@ def _lower_loop(st, ip: _PixInterp, local: dict, b):
     for nm, shape in names.items():
         local[nm] = _PVec([b.state(f"{nm}.{c}") for c in range(shape[0])]) if shape else b.state(nm)
     if counter is not None:
-        local[counter] = b.count()
+        # a trip that broke out did not reach its `counter += 1`
+        local[counter] = ip.arith("sub", b.count(), b.state(_BRK)) if brk else b.count()
     for nm in assigned:
         if nm not in state and nm != counter:
             local.pop(nm, None)
