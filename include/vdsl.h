@@ -42,7 +42,8 @@ extern "C" {
  * and in_cols (inputs of another shape than the grid); 6: VDSL_PIX_ATOMIC_ADD,
  * VDSL_PIX_OUT_NONE (scatter-adds) and VDSL_PIX_TRUNC (struct layouts unchanged since 5); 7:
  * VDSL_PIX_MAX_INSTR 256 and VDSL_PIX_MAX_INPUTS 8 (vdsl_pixel_program's arrays grow),
- * VDSL_PIX_ATOMIC_MAX / MIN, VDSL_PIX_STORE_AT, VDSL_PIX_RANDOM, VDSL_PIX_ATAN2 ... POW. */
+ * VDSL_PIX_ATOMIC_MAX / MIN, VDSL_PIX_STORE_AT, VDSL_PIX_RANDOM, VDSL_PIX_ATAN2 ... POWF and
+ * the bit operations VDSL_PIX_BAND ... SHR. */
 #define VDSL_ABI_VERSION 7
 
 typedef enum vdsl_status {
@@ -375,7 +376,16 @@ typedef enum vdsl_pix_opcode {
   VDSL_PIX_ACOS = 52,
   VDSL_PIX_ATAN = 53,
   VDSL_PIX_TAN = 54,
-  VDSL_PIX_POWF = 55
+  VDSL_PIX_POWF = 55,
+  /* integer bit operations: both registers converted to int32 as VDSL_PIX_OUT_I32 stores them
+   * (toward zero, NaN -> 0, saturating), the int32 operation, the result back to f32 (exact
+   * below 2^24 in magnitude): r[a] & r[b], |, ^, r[a] << (r[b] & 31), and r[a] >> (r[b] & 31)
+   * arithmetic (the sign copied in) */
+  VDSL_PIX_BAND = 56,
+  VDSL_PIX_BOR = 57,
+  VDSL_PIX_BXOR = 58,
+  VDSL_PIX_SHL = 59,
+  VDSL_PIX_SHR = 60
 } vdsl_pix_opcode;
 
 typedef enum vdsl_pix_test {

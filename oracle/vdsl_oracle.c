@@ -27,7 +27,9 @@
  *                        select, floor and trunc opcodes by numpy on every pair of special values;
  *                        asin, acos, atan, tan, atan2 and powf (the C library's float functions)
  *                        within 2 ulp of numpy's double-precision results, with atan2's signed-
- *                        zero quadrants and pow's IEEE special cases exactly.
+ *                        zero quadrants and pow's IEEE special cases exactly; the bit operations
+ *                        (and, or, xor, shifts) by numpy's int32 operations on every pair of a
+ *                        set of values (negatives, fractions, NaN, past int32, counts past 31).
  *                        Scatter-adds (VDSL_PIX_ATOMIC_ADD, run pixel by pixel in row-major
  *                        order): by numpy's np.add.at over the same indices in the same order
  *                        (f32 bit for bit, int32 exactly with wrap-around) and by the drop rule
@@ -252,6 +254,11 @@ static float pix_apply(const vdsl_pixel_program* p, const vdsl_map_instr* s, con
     case VDSL_PIX_ATAN: return atanf(reg[s->a]);
     case VDSL_PIX_TAN: return tanf(reg[s->a]);
     case VDSL_PIX_POWF: return powf(reg[s->a], reg[s->b]);
+    case VDSL_PIX_BAND: return (float)(pix_to_i32(reg[s->a]) & pix_to_i32(reg[s->b]));
+    case VDSL_PIX_BOR: return (float)(pix_to_i32(reg[s->a]) | pix_to_i32(reg[s->b]));
+    case VDSL_PIX_BXOR: return (float)(pix_to_i32(reg[s->a]) ^ pix_to_i32(reg[s->b]));
+    case VDSL_PIX_SHL: return (float)(int32_t)((uint32_t)pix_to_i32(reg[s->a]) << (pix_to_i32(reg[s->b]) & 31));
+    case VDSL_PIX_SHR: return (float)(pix_to_i32(reg[s->a]) >> (pix_to_i32(reg[s->b]) & 31));
     case VDSL_PIX_COS: return cosf(reg[s->a]);
     case VDSL_PIX_SIN: return sinf(reg[s->a]);
     case VDSL_PIX_LT: return reg[s->a] < reg[s->b] ? 1.0f : 0.0f;

@@ -762,3 +762,25 @@ def test_break_continue_and_small_math_bit_exact(dev, q, kernel):
         src = [fields[names[id(f)]] for f in op.inputs]
         got = run_prog(dev, q, op.program, src, ni, nj)
         assert np.array_equal(got, oracle.pixel_program(op.program, ni, nj, src)), kernel
+
+
+def test_bit_opcodes_and_operators_bit_exact(dev, q):
+    """The bit opcodes on every pair of a set of values (negatives, fractions, NaN, values past
+    int32, shift counts past 31) and the Taichi kernel using &, |, ^, <<, >> of indices: the
+    device equals the oracle bit for bit."""
+    from test_taichi_general import BITS, lower_named
+    vals = np.array([0, 1, -1, 5, -6, 255, 256, -256, 1 << 23, -(1 << 23), 7.9, -7.9, np.nan, 3e9, -3e9, 31, 32, 33],
+                    np.float32)
+    n = len(vals)
+    a = np.repeat(vals[:, None], n, axis=1)
+    c = np.repeat(vals[None, :], n, axis=0)
+    b = pp.Builder()
+    la, lc = b.load(0), b.load(1)
+    for name in ("band", "bor", "bxor", "shl", "shr"):
+        prog = pp.compile_program(b, out=b.op(name, la, lc))
+        assert np.array_equal(run_prog(dev, q, prog, [a, c], n, n), oracle.pixel_program(prog, n, n, [a, c])), name
+    low, names = lower_named(BITS, "bits", {})
+    for op in low.ops():
+        ni, nj = op.grid
+        assert not op.inputs
+        assert np.array_equal(run_prog(dev, q, op.program, [], ni, nj), oracle.pixel_program(op.program, ni, nj, []))

@@ -179,7 +179,7 @@ def test_while_body_reads_its_counter():
     ("        f[i, j] = 1.0\n        for _ in range(3):\n            x = 2.0", "after the loop"),
     ("        x = 0.0\n        for _ in range(3):\n            y = 1.0\n            for _ in range(2):\n                x = x + y\n        f[i, j] = x", "statement"),
     ("        x = 0.0\n        for _ in range(3):\n            f[i, j] = x", "store inside the loop"),
-    ("        f[i, j] = i << 3", "LShift"),
+    ("        f[i, j] = i << j", "known when"),
     ("        if i > j:\n            y = 1.0\n        f[i, j] = y", "one branch"),
     ("        x = 1.0", "must store"),
 ])
@@ -1396,3 +1396,73 @@ def test_rsqrt_mod_and_static_conditions():
     assert np.array_equal(got[..., 1], u - y * np.floor(u / y))
     assert np.array_equal(got[..., 2], f32(2.0) * u)
     assert (got[..., 1] >= 0).all()  # GLSL's mod takes the sign of the divisor
+
+
+def test_bit_opcodes_against_numpy_int32():
+    """band / bor / bxor / shl / shr: the registers converted to int32 as an int32 store converts
+    them (toward zero, NaN -> 0, saturating), numpy's int32 operation (shift counts taken mod
+    32, >> arithmetic), the result back to f32."""
+    vals = np.array([0, 1, -1, 5, -6, 255, 256, -256, 1 << 23, -(1 << 23), 7.9, -7.9, np.nan, 3e9, -3e9, 31, 32, 33],
+                    np.float32)
+    n = len(vals)
+    a = np.repeat(vals[:, None], n, axis=1)
+    c = np.repeat(vals[None, :], n, axis=0)
+
+    def to_i32(x):
+        with np.errstate(invalid="ignore"):
+            return np.where(np.isnan(x), 0, np.clip(np.trunc(x.astype(np.float64)), -2**31, 2**31 - 1)).astype(np.int32)
+    ia, ic = to_i32(a), to_i32(c)
+    sh = (ic & 31).astype(np.uint32)
+    want = {"band": ia & ic, "bor": ia | ic, "bxor": ia ^ ic,
+            "shl": (ia.astype(np.uint32) << sh).astype(np.int32), "shr": ia >> sh.astype(np.int32)}
+    b = pp.Builder()
+    la, lc = b.load(0), b.load(1)
+    for name, w in want.items():
+        got = oracle.pixel_program(pp.compile_program(b, out=b.op(name, la, lc)), n, n, [a, c])
+        assert np.array_equal(got, w.astype(np.float32)), name
+
+
+BITS = """
+import taichi as ti
+ti.init(arch=ti.gpu)
+u = ti.field(dtype=float, shape=(24, 40))
+out = ti.field(dtype=float, shape=(24, 40))
+
+@ti.kernel
+def bits():
+    for i, j in out:
+        h = (i * 40 + j) ^ ((i << 3) | (j >> 2))
+        out[i, j] = float((i & 3) + (j | 1) + (i ^ j) + (i << 1) + (j >> 1) + ((i - 12) >> 1) + (h & 255))
+
+@ti.kernel
+def float_bits():
+    for i, j in out:
+        out[i, j] = float(int(u[i, j]) & 1)
+
+@ti.kernel
+def var_shift():
+    for i, j in out:
+        out[i, j] = float(1 << j)
+
+@ti.kernel
+def wide_shift():
+    for i, j in out:
+        out[i, j] = float((i * j) << 20)
+"""
+
+
+def test_taichi_bit_operators():
+    """&, |, ^, << and >> of indices and integer arithmetic of them lower to the bit opcodes (>>
+    arithmetic on negatives): equal to numpy's int32 restatement.  Operands of no known integer
+    bound (a value from a float field), shifts by a per-pixel count, and results that may pass
+    2^24 are refused."""
+    low, names = lower_named(BITS, "bits", {})
+    arrays = {"u": np.zeros((24, 40), np.float32), "out": np.zeros((24, 40), np.float32)}
+    run_ops(low, names, arrays)
+    i, j = np.meshgrid(np.arange(24, dtype=np.int32), np.arange(40, dtype=np.int32), indexing="ij")
+    h = (i * 40 + j) ^ ((i << 3) | (j >> 2))
+    want = (i & 3) + (j | 1) + (i ^ j) + (i << 1) + (j >> 1) + ((i - 12) >> 1) + (h & 255)
+    assert np.array_equal(arrays["out"], want.astype(np.float32))
+    for kern, msg in (("float_bits", "known bound"), ("var_shift", "known when"), ("wide_shift", "beyond 2\\^24")):
+        with pytest.raises(tc.TaichiLoweringError, match=msg):
+            tc.lower_source_kernel(BITS, kern, {})

@@ -59,7 +59,7 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
     const vdsl_map_instr& s = p.code[pc];
     const std::string at = "pixel program: instruction " + std::to_string(pc);
     const bool map_op = s.op >= VDSL_MAP_LOAD && s.op <= VDSL_MAP_ADD_IMM;
-    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_POWF;
+    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_SHR;
     if (!map_op && !pix_op) return fail(VDSL_ERR_INVALID_ARG, at + ": unknown opcode " + std::to_string(s.op));
     if (s.dst >= VDSL_PIX_MAX_REGS || s.b >= VDSL_PIX_MAX_REGS || s.c >= VDSL_PIX_MAX_REGS)
       return fail(VDSL_ERR_INVALID_ARG, at + ": register out of range");
@@ -165,6 +165,7 @@ int reads(int op) {
     case VDSL_PIX_LOAD_AT: return 6;  // b, c
     case VDSL_MAP_ADD: case VDSL_MAP_SUB: case VDSL_MAP_MUL: case VDSL_MAP_DIV: case VDSL_MAP_MAX: case VDSL_MAP_MIN:
     case VDSL_PIX_LT: case VDSL_PIX_LE: case VDSL_PIX_EQ: case VDSL_PIX_NE: case VDSL_PIX_ATAN2: case VDSL_PIX_POWF:
+    case VDSL_PIX_BAND: case VDSL_PIX_BOR: case VDSL_PIX_BXOR: case VDSL_PIX_SHL: case VDSL_PIX_SHR:
       return 3;  // a, b
     case VDSL_MAP_FMA: case VDSL_PIX_SELECT: return 7;  // a, b, c
     case VDSL_PIX_ATOMIC_ADD: case VDSL_PIX_ATOMIC_MAX: case VDSL_PIX_ATOMIC_MIN: case VDSL_PIX_STORE_AT:

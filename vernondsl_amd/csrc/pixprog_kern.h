@@ -397,6 +397,15 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
     r[s.dst] = tanf(r[s.a]);
   } else if constexpr (s.op == VDSL_PIX_POWF) {
     r[s.dst] = powf(r[s.a], r[s.b]);
+  } else if constexpr (s.op >= VDSL_PIX_BAND && s.op <= VDSL_PIX_SHR) {
+    const int x = pix_to_i32(r[s.a]), y = pix_to_i32(r[s.b]);
+    int v;
+    if constexpr (s.op == VDSL_PIX_BAND) v = x & y;
+    else if constexpr (s.op == VDSL_PIX_BOR) v = x | y;
+    else if constexpr (s.op == VDSL_PIX_BXOR) v = x ^ y;
+    else if constexpr (s.op == VDSL_PIX_SHL) v = static_cast<int>(static_cast<unsigned>(x) << (y & 31));
+    else v = x >> (y & 31);
+    r[s.dst] = static_cast<float>(v);
   } else if constexpr (s.op == VDSL_PIX_COS) {
     r[s.dst] = cosf(r[s.a]);
   } else if constexpr (s.op == VDSL_PIX_SIN) {
@@ -445,6 +454,7 @@ __device__ constexpr uint32_t pix_reads(const vdsl_map_instr& s) {
     case VDSL_MAP_LOAD: case VDSL_MAP_CONST: case VDSL_PIX_INDEX: case VDSL_PIX_COUNT: return 0u;
     case VDSL_MAP_ADD: case VDSL_MAP_SUB: case VDSL_MAP_MUL: case VDSL_MAP_DIV: case VDSL_MAP_MAX: case VDSL_MAP_MIN:
     case VDSL_PIX_LT: case VDSL_PIX_LE: case VDSL_PIX_EQ: case VDSL_PIX_NE: case VDSL_PIX_ATAN2: case VDSL_PIX_POWF:
+    case VDSL_PIX_BAND: case VDSL_PIX_BOR: case VDSL_PIX_BXOR: case VDSL_PIX_SHL: case VDSL_PIX_SHR:
       return (1u << s.a) | (1u << s.b);
     case VDSL_PIX_LOAD_AT: return (1u << s.b) | (1u << s.c);
     case VDSL_MAP_FMA: case VDSL_PIX_SELECT: return (1u << s.a) | (1u << s.b) | (1u << s.c);

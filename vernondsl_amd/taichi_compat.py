@@ -1023,6 +1023,7 @@ class _PMat:
         return _PMat([flat[i * m:(i + 1) * m] for i in range(n)])
 
 
+_BIT_OPS = {ast.BitAnd: "band", ast.BitOr: "bor", ast.BitXor: "bxor", ast.LShift: "shl", ast.RShift: "shr"}
 _UNARY_FUNCS = {"sqrt": "sqrt", "exp": "exp", "log": "log", "sin": "sin", "cos": "cos", "tanh": "tanh", "abs": "abs",
                 "floor": "floor", "asin": "asin", "acos": "acos", "atan": "atan", "tan": "tan"}
 def _skey(fld):
@@ -1240,6 +1241,8 @@ class _PixInterp:
                 return self.floor_op(type(n.op) is ast.Mod, x, y)
             if isinstance(n.op, ast.MatMult):
                 return self.matmul(x, y)
+            if type(n.op) in _BIT_OPS:
+                return self.bit_op(_BIT_OPS[type(n.op)], x, y)
             if type(n.op) not in ops:
                 raise TaichiLoweringError(f"operator {type(n.op).__name__} is not supported")
             return self.arith(ops[type(n.op)], x, y)
@@ -1749,6 +1752,30 @@ class _PixInterp:
         if id(self.node(x)) in self.bools and id(self.node(y)) in self.bools:
             self.bools.add(id(r))
         return r
+
+    def bit_op(self, op, x, y):
+        """&, |, ^, << and >> of integers (int32 operations, >> arithmetic): folded when both are
+        known, else the bit opcodes on values whose bound keeps them exact in f32 registers."""
+        if isinstance(x, _PVec) or isinstance(y, _PVec):
+            return self.elementwise(lambda a, c: self.bit_op(op, a, c), x, y)
+        ints = all(isinstance(v, (int, np.integer)) and not isinstance(v, bool) for v in (x, y))
+        if ints:
+            a, c = int(x), int(y)
+            return {"band": a & c, "bor": a | c, "bxor": a ^ c, "shl": a << (c & 31), "shr": a >> (c & 31)}[op]
+        bx, by = self._ib(x), self._ib(y)
+        if bx is None or by is None:
+            raise TaichiLoweringError("bit operations take integers of a known bound below 2^24 (indices, loop variables, "
+                                      "constants and integer arithmetic of them)")
+        if op == "shl":
+            if not isinstance(y, (int, np.integer)):
+                raise TaichiLoweringError("x << n needs n known when the kernel is lowered")
+            bound = bx << (int(y) & 31)
+        elif op == "shr":
+            bound = bx
+        else:  # two's complement operands in [-2^k, 2^k) give results in the same range
+            bound = 1 << max(bx, by).bit_length()
+        r = self.b.op(op, self.node(x), self.node(y))
+        return self._int_result(r, bound, {"band": "&", "bor": "|", "bxor": "^", "shl": "<<", "shr": ">>"}[op])
 
     def floor_op(self, mod, x, y):
         """x % y (floored, the sign of y) and x // y, as x - floor(x / y) * y and floor(x / y)."""
