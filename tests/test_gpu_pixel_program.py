@@ -784,3 +784,17 @@ def test_bit_opcodes_and_operators_bit_exact(dev, q):
         ni, nj = op.grid
         assert not op.inputs
         assert np.array_equal(run_prog(dev, q, op.program, [], ni, nj), oracle.pixel_program(op.program, ni, nj, []))
+
+
+def test_taichi_surface_additions_on_the_device(dev, q):
+    """The kernel of @ti.func ifs, ti.types.vector, swizzles, vector reductions, reflect, isnan,
+    casts and ~: every program on the device equals the oracle bit for bit."""
+    from test_taichi_general import SURFACE, lower_named
+    low, names = lower_named(SURFACE, "surface", {})
+    r = np.random.default_rng(12)
+    fields = {"u": r.uniform(-2, 2, (10, 14)).astype(np.float32), "v3": r.uniform(-1, 1, (10, 14, 3)).astype(np.float32)}
+    fields["u"][2, 3] = 0.0
+    for op in low.ops():
+        ni, nj = op.grid
+        src = [fields[names[id(f)]] for f in op.inputs]
+        assert np.array_equal(run_prog(dev, q, op.program, src, ni, nj), oracle.pixel_program(op.program, ni, nj, src))

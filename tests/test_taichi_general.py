@@ -1466,3 +1466,68 @@ def test_taichi_bit_operators():
     for kern, msg in (("float_bits", "known bound"), ("var_shift", "known when"), ("wide_shift", "beyond 2\\^24")):
         with pytest.raises(tc.TaichiLoweringError, match=msg):
             tc.lower_source_kernel(BITS, kern, {})
+
+
+SURFACE = """
+import taichi as ti
+import taichi.math as tm
+ti.init(arch=ti.gpu)
+vec3 = ti.types.vector(3, float)
+u = ti.field(dtype=float, shape=(10, 14))
+v3 = ti.Vector.field(3, dtype=float, shape=(10, 14))
+out = ti.Vector.field(4, dtype=float, shape=(10, 14))
+
+@ti.func
+def bent(x):
+    a = x + 1.0
+    if a > 0.5:
+        a = a * 2.0
+    else:
+        a -= 3.0
+    return a
+
+@ti.kernel
+def surface():
+    for i, j in out:
+        p = vec3(u[i, j], 1.0, 2.0)
+        q = v3[i, j]
+        r = tm.reflect(q, tm.normalize(p))
+        a = b = q.zy.norm_sqr() + q.bgr.x
+        nan = 1.0 if tm.isnan(u[i, j] / u[i, j]) else 0.0
+        out[i, j] = [bent(u[i, j]) + q.sum() + q.max() - q.min(), r.y + ti.f32(q.n),
+                     a + b + float(ti.i32(u[i, j] * 4.0)), nan + float(~i)]
+"""
+
+
+def test_taichi_surface_additions_bit_exact():
+    """@ti.func bodies with ifs before their final return, ti.types.vector constructors, swizzles
+    of 2-3 components (xyzw and rgba) and .n, vector sum / max / min, taichi.math.reflect and
+    isnan, ti.f32 / ti.i32 casts, chained assignment and ~ of an index: bit for bit against
+    numpy's f32 restatement."""
+    low, names = lower_named(SURFACE, "surface", {})
+    r = np.random.default_rng(12)
+    u = r.uniform(-2, 2, (10, 14)).astype(np.float32)
+    u[2, 3] = 0.0  # 0 / 0: NaN
+    v3 = r.uniform(-1, 1, (10, 14, 3)).astype(np.float32)
+    arrays = {"u": u, "v3": v3, "out": np.zeros((10, 14, 4), np.float32)}
+    run_ops(low, names, arrays)
+    got = arrays["out"]
+    i = np.arange(10)[:, None] * np.ones((1, 14), np.int64)
+    qx, qy, qz = v3[..., 0], v3[..., 1], v3[..., 2]
+    a1 = u + f32(1.0)
+    bent = np.where(a1 > f32(0.5), a1 * f32(2.0), a1 - f32(3.0))
+    s = (qx + qy) + qz
+    mx, mn = np.maximum(np.maximum(qx, qy), qz), np.minimum(np.minimum(qx, qy), qz)
+    want0 = ((bent + s) + mx) - mn
+    # the reflection through normalize(p): within f32 rounding of x - 2 dot(n, x) n
+    pl = np.sqrt((u * u + f32(1.0)) + f32(4.0))
+    px, py, pz = u / pl, f32(1.0) / pl, f32(2.0) / pl
+    assert np.allclose(got[..., 1], (qy - f32(2.0) * ((px * qx + py * qy) + pz * qz) * py) + f32(3.0), atol=1e-6)
+    ab = (qz * qz + qy * qy) + qz
+    with np.errstate(invalid="ignore"):
+        nan = np.isnan(u / u).astype(np.float32)
+    want2 = (ab + ab) + np.trunc(u * f32(4.0))
+    assert np.array_equal(got[..., 0], want0)
+    assert np.array_equal(got[..., 2], want2)
+    assert np.array_equal(got[..., 3], nan + (-i - 1).astype(np.float32))
+    assert got[2, 3, 3] == 1.0 - 3.0

@@ -32,7 +32,8 @@ loop whose body ends with `counter += 1`, or a `for k in range(N)` / `range(A, B
 perfect nest of them runs as one loop over its trips; N may be an integer expression of the
 pixel), whose test and body may read the counter or k (from the loop's trip), with `break` and
 `continue` in the body or its ifs (`continue` not in a while loop, where it would skip the
-increment); a body of several loops runs as parts joined by hidden per-pixel fields - and stores
+increment), `@ti.func` calls (statements before a final return), `ti.types.vector` values,
+swizzles, integer bit operations (`& | ^ << >> ~`) of bounded integers; a body of several loops runs as parts joined by hidden per-pixel fields - and stores
 `F[i, j] = <value>` (an i32 field stores the loop counter) into one or more fields of the loop's
 shape: a body storing several fields becomes one program per stored field, run in an order in
 which no program loads a field that an earlier one stored (a snapshot copy where the programs
@@ -69,7 +70,7 @@ import os
 import math as _pymath
 import sys
 import textwrap
-import types
+import types as _pytypes
 
 import numpy as np
 
@@ -843,6 +844,9 @@ def _parse_source(text: str, kernel_name: str, args: dict):
                 dtype = f32 if dt is None or (isinstance(dt, ast.Name) and dt.id == "float") else (
                     i32 if (isinstance(dt, ast.Name) and dt.id == "int") or getattr(dt, "attr", "") in ("i32", "int32") else f32)
                 env[st.targets[0].id] = Field(dtype, shape, width=int(width), mat=mat)
+            elif (isinstance(v, ast.Call) and isinstance(v.func, ast.Attribute) and v.func.attr == "vector"
+                  and isinstance(v.func.value, ast.Attribute) and v.func.value.attr == "types" and v.args):
+                env[st.targets[0].id] = _VectorType(interp.expr(v.args[0], {}))  # vec3 = ti.types.vector(3, float)
             else:
                 try:
                     env[st.targets[0].id] = interp.expr(v, {})
@@ -862,13 +866,31 @@ pi = _pymath.pi
 # ti.math (also importable as taichi.math under the runner): names only; inside kernels the
 # lowering interprets the calls (vec2-4, clamp, mix, smoothstep, length, normalize, dot, cross,
 # fract, sign, step and the scalar functions).
-math = types.ModuleType("taichi.math")
+math = _pytypes.ModuleType("taichi.math")
 math.pi = _pymath.pi
 math.e = _pymath.e
 for _name in ("vec2", "vec3", "vec4", "clamp", "mix", "smoothstep", "length", "normalize", "dot", "cross", "fract",
               "sign", "step", "sqrt", "exp", "log", "sin", "cos", "tanh", "floor", "ceil", "min", "max", "mod", "log2",
               "atan2", "asin", "acos", "atan", "tan", "pow"):
     setattr(math, _name, _name)  # placeholders: only meaningful inside kernels
+
+
+class _VectorType:
+    """ti.types.vector(n, dtype) / ti.math.vec2-4: inside kernels a constructor of n-vectors
+    (one scalar fills every component; vectors and scalars are laid out in order)."""
+    def __init__(self, n, dtype=float):
+        self.n, self.dtype = int(n), dtype
+
+
+def _matrix_type(n, m, dtype=float):
+    raise TaichiLoweringError("ti.types.matrix is not supported; use ti.Matrix values")
+
+
+types = _pytypes.ModuleType("taichi.types")  # ti.types
+types.vector = _VectorType
+types.matrix = _matrix_type
+for _name in ("reflect", "isnan", "isinf"):
+    setattr(math, _name, _name)
 
 
 def ndrange(*extents):
@@ -1250,6 +1272,12 @@ class _PixInterp:
             v = self.expr(n.operand, local)
             if isinstance(n.op, ast.USub):
                 return self.unary("neg", v)
+            if isinstance(n.op, ast.Invert):  # ~x = -x - 1 of an integer
+                if isinstance(v, (int, np.integer)) and not isinstance(v, bool):
+                    return ~int(v)
+                if self._ib(v) is None:
+                    raise TaichiLoweringError("~ takes integers of a known bound")
+                return self.arith("sub", self.unary("neg", v), 1)
             if isinstance(n.op, ast.UAdd):
                 return v
             if isinstance(n.op, ast.Not):
@@ -1277,11 +1305,15 @@ class _PixInterp:
             raise TaichiLoweringError("only constant vector indexing and field[i, j] reads are supported")
         if isinstance(n, ast.Attribute):
             base = self.expr(n.value, local)
-            if isinstance(base, _PVec) and n.attr in ("x", "y", "z", "w"):
-                k = "xyzw".index(n.attr)
-                if k >= len(base.comps):
+            if isinstance(base, _PVec) and n.attr == "n":
+                return len(base.comps)
+            if isinstance(base, _PVec) and 1 <= len(n.attr) <= 4 and \
+                    (set(n.attr) <= set("xyzw") or set(n.attr) <= set("rgba")):
+                names = "xyzw" if set(n.attr) <= set("xyzw") else "rgba"
+                ks = [names.index(ch) for ch in n.attr]
+                if max(ks) >= len(base.comps):
                     raise TaichiLoweringError(f"vector has no component {n.attr!r}")
-                return base.comps[k]
+                return base.comps[ks[0]] if len(ks) == 1 else _PVec([base.comps[k] for k in ks])
             if isinstance(base, (_PVec, self.pp.Node)):
                 return (base, n.attr)
             return getattr(base, n.attr)
@@ -1374,6 +1406,13 @@ class _PixInterp:
                     return self.dot(base, self.expr(n.args[0], local))
                 if f.attr == "normalized":
                     return self.normalize(base)
+                if f.attr == "sum":  # ((c0 + c1) + c2) + ...
+                    acc = base.comps[0]
+                    for c in base.comps[1:]:
+                        acc = self.arith("add", acc, c)
+                    return acc
+                if f.attr in ("max", "min"):
+                    return self.minmax(f.attr, list(base.comps))
                 if f.attr == "cross":
                     return self.cross(base, self.expr(n.args[0], local))
                 if f.attr == "cast":
@@ -1430,6 +1469,22 @@ class _PixInterp:
                 raise TaichiLoweringError(f"ti.{f.attr} is supported as a statement (its old value is not returned)")
             if f.attr == "random":
                 return self.random(n, local)
+            if f.attr in ("f32", "float32") and len(n.args) == 1:
+                v = self.expr(n.args[0], local)
+                return _f32(v) if _is_num(v) else v
+            if f.attr in ("i32", "int32") and len(n.args) == 1:
+                return self.cast(self.expr(n.args[0], local), int)
+            if f.attr == "reflect" and len(n.args) == 2:  # x - 2 dot(n, x) n
+                x, nn = (self.expr(a, local) for a in n.args)
+                return self.arith("sub", x, self.arith("mul", self.arith("mul", 2.0, self.dot(nn, x)), nn))
+            if f.attr in ("isnan", "isinf") and len(n.args) == 1:
+                def test(v):
+                    if _is_num(v):
+                        return int(np.isnan(_f32(v)) if f.attr == "isnan" else np.isinf(_f32(v)))
+                    if f.attr == "isnan":
+                        return self.b.op("ne", v, v)
+                    return self.b.op("eq", self.b.op("abs", v), float("inf"))
+                return self.elementwise(test, self.expr(n.args[0], local))
             if f.attr == "static" and len(n.args) == 1:  # `if ti.static(cond):` decided when lowering
                 return self.expr(n.args[0], local)
             if f.attr == "rsqrt" and len(n.args) == 1:  # 1 / sqrt(x), both exactly rounded
@@ -1465,19 +1520,36 @@ class _PixInterp:
                     return _f32(v) if _is_num(v) else v
                 if obj is int:
                     return self.cast(self.expr(n.args[0], local), int)
+                if isinstance(obj, _VectorType):
+                    vals = [self.expr(a, local) for a in n.args]
+                    if len(vals) == 1 and not isinstance(vals[0], (_PVec, list)):
+                        return _PVec([vals[0]] * obj.n)
+                    comps = [c for v in vals for c in (v.comps if isinstance(v, _PVec) else v if isinstance(v, list) else [v])]
+                    if len(comps) != obj.n:
+                        raise TaichiLoweringError(f"a {obj.n}-vector made of {len(comps)} components")
+                    return _PVec(comps)
                 raise TaichiLoweringError(f"call of {f.id!r}: only @ti.func functions are inlined")
             args = [self.expr(a, local) for a in n.args]
-            sub = dict(zip([a.arg for a in fdef.args.args], args))
-            for st in fdef.body:
+            # the function's own scope, sharing the caller's view of the fields it has stored
+            sub = {k: v for k, v in local.items() if _is_skey(k)}
+            sub.update(zip([a.arg for a in fdef.args.args], args))
+            body = [st for st in fdef.body if not (isinstance(st, ast.Expr) and isinstance(st.value, ast.Constant))]
+            if any(isinstance(nd, ast.Return) for st in body[:-1] for nd in ast.walk(st)) or \
+                    any(isinstance(nd, ast.Return) for st in body[-1:] if not isinstance(st, ast.Return) for nd in ast.walk(st)):
+                raise TaichiLoweringError(f"@ti.func {f.id!r}: a return must be its last statement")
+            for st in body:
                 if isinstance(st, ast.Return):
-                    return self.expr(st.value, sub)
-                if isinstance(st, ast.Assign) and len(st.targets) == 1 and isinstance(st.targets[0], ast.Name):
-                    sub[st.targets[0].id] = self.expr(st.value, sub)
-                    continue
-                if isinstance(st, ast.Expr) and isinstance(st.value, ast.Constant):
-                    continue
-                raise TaichiLoweringError(f"statement in @ti.func {f.id!r} is not supported")
-            raise TaichiLoweringError(f"@ti.func {f.id!r} returns nothing")
+                    for k, v in sub.items():
+                        if _is_skey(k):
+                            local[k] = v
+                    return self.expr(st.value, sub) if st.value is not None else None
+                if not self.assign(st, sub):
+                    raise TaichiLoweringError(f"statement at line {getattr(st, 'lineno', '?')} in @ti.func {f.id!r} "
+                                              "is not supported")
+            for k, v in sub.items():
+                if _is_skey(k):
+                    local[k] = v
+            return None
         raise TaichiLoweringError("unsupported call")
 
     def random(self, n, local):
@@ -1991,6 +2063,9 @@ class _PixInterp:
         return True
 
     def assign(self, st, local):
+        if isinstance(st, ast.Assign) and len(st.targets) > 1:  # a = b = value
+            return all(self.assign(ast.Assign(targets=[t], value=st.value, lineno=getattr(st, "lineno", 0)), local)
+                       for t in st.targets)
         if isinstance(st, ast.If):
             self.if_stmt(st, local)
             return True
