@@ -591,8 +591,9 @@ EXACT_UNARY = ("neg", "abs", "sqrt", "floor", "square", "trunc")
 EXACT_BINARY = ("add", "sub", "mul", "div", "max", "min", "lt", "le", "eq", "ne")
 
 
-def random_program(seed):
-    """A random program of exactly rounded operations: pixel indices, constants, loads and clamped
+def random_program(seed, binary=EXACT_BINARY):
+    """A random program of exactly rounded operations (binary: the two-operand opcodes drawn
+    from): pixel indices, constants, loads and clamped
     gathers of one or two inputs of 1-2 components, selects; half of them with a loop (with or
     without a test) over two states that reads the trip and gathers at state-derived indices,
     the output reading the states and the count."""
@@ -610,7 +611,7 @@ def random_program(seed):
             if u < 0.25:
                 v = b.op(EXACT_UNARY[int(r.integers(len(EXACT_UNARY)))], pick())
             elif u < 0.8:
-                v = b.op(EXACT_BINARY[int(r.integers(len(EXACT_BINARY)))], pick(), pick())
+                v = b.op(binary[int(r.integers(len(binary)))], pick(), pick())
             elif u < 0.9:
                 v = b.op("select", pick(), pick(), pick())
             else:
@@ -653,6 +654,25 @@ def test_random_programs_bit_exact(dev, q, seed):
     for ni, nj in ((37, 53), (1, 300), (9, 260)):
         ins = [np.where(rng_.random((ni, nj, w)) < 0.05, np.float32(np.nan),
                         rng_.standard_normal((ni, nj, w)) * 4).astype(np.float32).reshape((ni, nj) if w == 1 else (ni, nj, w))
+               for w in widths]
+        got = run_prog(dev, q, prog, ins, ni, nj)
+        ref = oracle.pixel_program(prog, ni, nj, ins)
+        assert same_values(got, ref), (seed, ni, nj, pp.describe(prog))
+
+
+@pytest.mark.parametrize("seed", range(100, 112))
+def test_random_programs_with_bit_operations_bit_exact(dev, q, seed):
+    """Seeded random programs that also draw the bit opcodes (int32 conversions of arbitrary
+    values: fractions, NaN, values past int32, results past 2^24 rounded back to f32): the same
+    bits as the oracle."""
+    try:
+        prog, widths = random_program(seed, EXACT_BINARY + ("band", "bor", "bxor", "shl", "shr"))
+    except pp.ProgramError:
+        pytest.skip("the random program does not fit the device form")
+    rng_ = np.random.default_rng(1000 + seed)
+    for ni, nj in ((37, 53), (1, 300)):
+        ins = [np.where(rng_.random((ni, nj, w)) < 0.05, np.float32(np.nan),
+                        rng_.standard_normal((ni, nj, w)) * 300).astype(np.float32).reshape((ni, nj) if w == 1 else (ni, nj, w))
                for w in widths]
         got = run_prog(dev, q, prog, ins, ni, nj)
         ref = oracle.pixel_program(prog, ni, nj, ins)
