@@ -43,7 +43,7 @@ extern "C" {
  * VDSL_PIX_OUT_NONE (scatter-adds) and VDSL_PIX_TRUNC (struct layouts unchanged since 5); 7:
  * VDSL_PIX_MAX_INSTR 256 and VDSL_PIX_MAX_INPUTS 8 (vdsl_pixel_program's arrays grow),
  * VDSL_PIX_ATOMIC_MAX / MIN, VDSL_PIX_STORE_AT, VDSL_PIX_RANDOM, VDSL_PIX_ATAN2 ... POWF and
- * the bit operations VDSL_PIX_BAND ... SHR. */
+ * the bit operations VDSL_PIX_BAND ... SHR, VDSL_PIX_ROUND. */
 #define VDSL_ABI_VERSION 7
 
 typedef enum vdsl_status {
@@ -385,7 +385,9 @@ typedef enum vdsl_pix_opcode {
   VDSL_PIX_BOR = 57,
   VDSL_PIX_BXOR = 58,
   VDSL_PIX_SHL = 59,
-  VDSL_PIX_SHR = 60
+  VDSL_PIX_SHR = 60,
+  /* roundf(r[a]): to the nearest integer, halfway cases away from zero (exact) */
+  VDSL_PIX_ROUND = 61
 } vdsl_pix_opcode;
 
 typedef enum vdsl_pix_test {

@@ -254,6 +254,7 @@ static float pix_apply(const vdsl_pixel_program* p, const vdsl_map_instr* s, con
     case VDSL_PIX_ATAN: return atanf(reg[s->a]);
     case VDSL_PIX_TAN: return tanf(reg[s->a]);
     case VDSL_PIX_POWF: return powf(reg[s->a], reg[s->b]);
+    case VDSL_PIX_ROUND: return roundf(reg[s->a]);
     case VDSL_PIX_BAND: return (float)(pix_to_i32(reg[s->a]) & pix_to_i32(reg[s->b]));
     case VDSL_PIX_BOR: return (float)(pix_to_i32(reg[s->a]) | pix_to_i32(reg[s->b]));
     case VDSL_PIX_BXOR: return (float)(pix_to_i32(reg[s->a]) ^ pix_to_i32(reg[s->b]));

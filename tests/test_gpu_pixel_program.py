@@ -818,3 +818,13 @@ def test_taichi_surface_additions_on_the_device(dev, q):
         ni, nj = op.grid
         src = [fields[names[id(f)]] for f in op.inputs]
         assert np.array_equal(run_prog(dev, q, op.program, src, ni, nj), oracle.pixel_program(op.program, ni, nj, src))
+
+
+def test_round_opcode_bit_exact(dev, q):
+    """VDSL_PIX_ROUND on halfway cases, signed zeros, values past 2^23, infinities and NaN: the
+    device's roundf equals the oracle's bit for bit."""
+    from test_taichi_general import ROUND_VALUES
+    x = np.tile(ROUND_VALUES, 7)[None]
+    b = pp.Builder()
+    prog = pp.compile_program(b, out=b.op("round", b.load(0)))
+    assert same_values(run_prog(dev, q, prog, [x], 1, x.shape[1]), oracle.pixel_program(prog, 1, x.shape[1], [x]))

@@ -1531,3 +1531,34 @@ def test_taichi_surface_additions_bit_exact():
     assert np.array_equal(got[..., 2], want2)
     assert np.array_equal(got[..., 3], nan + (-i - 1).astype(np.float32))
     assert got[2, 3, 3] == 1.0 - 3.0
+
+
+ROUND_VALUES = np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 0.49999997, -0.49999997, 8388609.0, 4194304.5, -0.3, -0.0,
+                         0.0, 3.7, -3.7, 1e-40, np.inf, -np.inf, np.nan, 3.4e38], np.float32)
+
+
+def round_half_away(x):
+    """Nearest integer, halfway cases away from zero, computed in f64 (|x| + 0.5 is exact there)."""
+    with np.errstate(invalid="ignore"):
+        return np.copysign(np.floor(np.abs(x.astype(np.float64)) + 0.5), x).astype(np.float32)
+
+
+def test_round_opcode_and_ti_round():
+    """VDSL_PIX_ROUND (C's roundf: halfway cases away from zero, signed zeros kept) against an f64
+    restatement on halfway cases, the largest float below 0.5, values past 2^23, infinities and
+    NaN; ti.round lowers to it (Taichi's own rounding of halfway cases is parity unpinned: Taichi
+    is not importable here)."""
+    x = ROUND_VALUES[None]
+    b = pp.Builder()
+    got = oracle.pixel_program(pp.compile_program(b, out=b.op("round", b.load(0))), 1, x.shape[1], [x])
+    want = round_half_away(x)
+    assert np.array_equal(got.view(np.uint32)[~np.isnan(want)], want.view(np.uint32)[~np.isnan(want)])
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    text = SMALL_MATH.replace("out[i, j] = [ti.rsqrt(x * x + 1.0), tm.mod(x, 0.3), 0.0]",
+                              "out[i, j] = [ti.round(x * 2.0), tm.round(x), 0.0]")
+    low, names = lower_named(text, "misc", {})
+    u = np.random.default_rng(8).uniform(-2, 2, (8, 16)).astype(np.float32)
+    arrays = {"u": u, "out": np.zeros((8, 16, 3), np.float32)}
+    run_ops(low, names, arrays)
+    assert np.array_equal(arrays["out"][..., 0], round_half_away(u * f32(2.0)))
+    assert np.array_equal(arrays["out"][..., 1], round_half_away(u))

@@ -59,7 +59,7 @@ int check_program(const vdsl_pixel_program& p, int n_inputs) {
     const vdsl_map_instr& s = p.code[pc];
     const std::string at = "pixel program: instruction " + std::to_string(pc);
     const bool map_op = s.op >= VDSL_MAP_LOAD && s.op <= VDSL_MAP_ADD_IMM;
-    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_SHR;
+    const bool pix_op = s.op >= VDSL_PIX_INDEX && s.op <= VDSL_PIX_ROUND;
     if (!map_op && !pix_op) return fail(VDSL_ERR_INVALID_ARG, at + ": unknown opcode " + std::to_string(s.op));
     if (s.dst >= VDSL_PIX_MAX_REGS || s.b >= VDSL_PIX_MAX_REGS || s.c >= VDSL_PIX_MAX_REGS)
       return fail(VDSL_ERR_INVALID_ARG, at + ": register out of range");

@@ -397,6 +397,8 @@ __device__ __forceinline__ void pix_step(const PixRt& rt, const PixIn& in, float
     r[s.dst] = tanf(r[s.a]);
   } else if constexpr (s.op == VDSL_PIX_POWF) {
     r[s.dst] = powf(r[s.a], r[s.b]);
+  } else if constexpr (s.op == VDSL_PIX_ROUND) {
+    r[s.dst] = roundf(r[s.a]);
   } else if constexpr (s.op >= VDSL_PIX_BAND && s.op <= VDSL_PIX_SHR) {
     const int x = pix_to_i32(r[s.a]), y = pix_to_i32(r[s.b]);
     int v;

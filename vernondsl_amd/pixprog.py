@@ -28,7 +28,7 @@ OP = dict(_lib.MAP_OPS)
 OP.update({"index": 32, "cos": 33, "sin": 34, "count": 35, "lt": 36, "le": 37, "eq": 38, "ne": 39, "select": 40,
            "floor": 41, "load_at": 42, "trip": 43, "atomic_add": 44, "trunc": 45, "atomic_max": 46, "atomic_min": 47,
            "store_at": 48, "random": 49, "atan2": 50, "asin": 51, "acos": 52, "atan": 53, "tan": 54, "powf": 55,
-           "band": 56, "bor": 57, "bxor": 58, "shl": 59, "shr": 60})
+           "band": 56, "bor": 57, "bxor": 58, "shl": 59, "shr": 60, "round": 61})
 SCATTERS = ("atomic_add", "atomic_max", "atomic_min", "store_at")  # effect nodes: no result register
 TESTS = {"none": 0, "lt": 1, "le": 2, "gt": 3, "ge": 4}
 OUT_REG, OUT_COUNT, OUT_I32, OUT_NONE = 0, 1, 2, 3
@@ -36,7 +36,7 @@ F32, I32 = _lib.F32, _lib.I32  # input dtypes (vdsl_dtype)
 COUNT = "count"  # compile_program(out=COUNT): store the loop's update count (an int32 field)
 
 UNARY = ("neg", "abs", "sqrt", "exp", "log", "tanh", "sigmoid", "cos", "sin", "recip", "square", "floor", "trunc",
-         "asin", "acos", "atan", "tan")
+         "asin", "acos", "atan", "tan", "round")
 BINARY = ("add", "sub", "mul", "div", "max", "min", "lt", "le", "eq", "ne", "atan2", "powf",
           "band", "bor", "bxor", "shl", "shr")  # comparisons give 1.0 / 0.0; bit operations of int32 values
 TERNARY = ("fma", "select")  # select(c, a, b): a where c != 0 (NaN included), else b

@@ -871,7 +871,7 @@ math.pi = _pymath.pi
 math.e = _pymath.e
 for _name in ("vec2", "vec3", "vec4", "clamp", "mix", "smoothstep", "length", "normalize", "dot", "cross", "fract",
               "sign", "step", "sqrt", "exp", "log", "sin", "cos", "tanh", "floor", "ceil", "min", "max", "mod", "log2",
-              "atan2", "asin", "acos", "atan", "tan", "pow"):
+              "atan2", "asin", "acos", "atan", "tan", "pow", "round"):
     setattr(math, _name, _name)  # placeholders: only meaningful inside kernels
 
 
@@ -1047,7 +1047,7 @@ class _PMat:
 
 _BIT_OPS = {ast.BitAnd: "band", ast.BitOr: "bor", ast.BitXor: "bxor", ast.LShift: "shl", ast.RShift: "shr"}
 _UNARY_FUNCS = {"sqrt": "sqrt", "exp": "exp", "log": "log", "sin": "sin", "cos": "cos", "tanh": "tanh", "abs": "abs",
-                "floor": "floor", "asin": "asin", "acos": "acos", "atan": "atan", "tan": "tan"}
+                "floor": "floor", "asin": "asin", "acos": "acos", "atan": "atan", "tan": "tan", "round": "round"}
 def _skey(fld):
     """The local-scope key of the value the body has stored to fld[i, j] (read back by a later read
     of fld[i, j] in the same body)."""
@@ -1165,10 +1165,11 @@ class _PixInterp:
                 return {"neg": -v, "abs": np.abs(v), "sqrt": np.sqrt(v), "exp": np.exp(v), "log": np.log(v), "sin": np.sin(v),
                         "cos": np.cos(v), "tanh": np.tanh(v), "floor": np.floor(v), "trunc": np.trunc(v),
                         "asin": np.arcsin(v), "acos": np.arccos(v), "atan": np.arctan(v), "tan": np.tan(v),
-                        "recip": np.float32(1.0) / v}[fn]
+                        "recip": np.float32(1.0) / v,
+                        "round": np.float32(np.copysign(np.floor(np.abs(np.float64(v)) + 0.5), v))}[fn]
         r = self.b.op(fn, x)
         bx = self._ib(x)
-        return self._int_result(r, bx, fn) if fn in ("neg", "abs", "floor") and bx is not None else r
+        return self._int_result(r, bx, fn) if fn in ("neg", "abs", "floor", "round") and bx is not None else r
 
     def matmul(self, a, c):
         """a @ c for matrices and vectors (a vector is a column, or a row on the left): each
