@@ -29,7 +29,8 @@
  *                        within 2 ulp of numpy's double-precision results, with atan2's signed-
  *                        zero quadrants and pow's IEEE special cases exactly; the bit operations
  *                        (and, or, xor, shifts) by numpy's int32 operations on every pair of a
- *                        set of values (negatives, fractions, NaN, past int32, counts past 31).
+ *                        set of values (negatives, fractions, NaN, past int32, counts past 31);
+ *                        round (roundf) by an f64 restatement of halfway-away-from-zero rounding.
  *                        Scatter-adds (VDSL_PIX_ATOMIC_ADD, run pixel by pixel in row-major
  *                        order): by numpy's np.add.at over the same indices in the same order
  *                        (f32 bit for bit, int32 exactly with wrap-around) and by the drop rule
